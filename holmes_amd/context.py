@@ -1,0 +1,352 @@
+"""Device-resident CKKS context and ciphertext containers.
+
+Mirrors the EasyFHE native context and cipher objects that Holmes' operators touch
+(attributes L, N, M, K, alpha, max_slots, device, logN, scale_at, rescale_divisor_at, primes,
+get_rotation_key_for_limbs: llama3fhe/parallel/prefill/keys.py:39-47; cipher fields cv, state,
+is_ext, slots, batch_size, cipher_like, deep_copy: bench/cmp/holmes_multi_mac.py:61-89).
+Every arithmetic operation runs in libholmes_ckks (HIP, gfx950); tensors are PyTorch-ROCm
+buffers used only as device memory.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass, replace
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .params import CKKSContextSpec
+
+N_LOG = 16
+
+
+@dataclass(frozen=True)
+class CipherState:
+    """Ciphertext metadata (easyfhe.fhe.CipherState: cur_limbs, scale_degree, scaling_factor)."""
+
+    cur_limbs: int
+    scale_degree: int = 1
+    scaling_factor: float = float(2**40)
+
+    def replace(self, **changes) -> "CipherState":
+        return replace(self, **changes)
+
+
+class Cipher:
+    """A batch of CKKS ciphertexts: ``cv = [c0, c1]``, each ``[batch][limbs][N]`` uint64.
+
+    Limb l of every polynomial is a residue modulo prime l of the Q chain (or, with
+    ``is_ext``, Q limbs 0..cur_limbs-1 followed by the K special primes).
+    """
+
+    __slots__ = ("cv", "state", "slots", "is_ext", "batch_size", "_released")
+
+    def __init__(self, cv, state: CipherState, *, slots: int, is_ext: bool = False, batch_size: int | None = None):
+        self.cv = list(cv)
+        self.state = state
+        self.slots = int(slots)
+        self.is_ext = bool(is_ext)
+        self.batch_size = int(batch_size if batch_size is not None else self.cv[0].shape[0])
+        self._released = False
+
+    @property
+    def device(self):
+        return self.cv[0].device
+
+    def cipher_like(self, cv, *, state=None, slots=None, is_ext=None, batch_size=None) -> "Cipher":
+        return Cipher(
+            cv,
+            self.state if state is None else state,
+            slots=self.slots if slots is None else slots,
+            is_ext=self.is_ext if is_ext is None else is_ext,
+            batch_size=batch_size,
+        )
+
+    def deep_copy(self) -> "Cipher":
+        return self.cipher_like([c.clone() for c in self.cv])
+
+    def release(self) -> None:
+        self.cv = []
+        self._released = True
+
+    def __repr__(self) -> str:
+        return (f"Cipher(batch={self.batch_size}, limbs={self.state.cur_limbs}, "
+                f"scale_degree={self.state.scale_degree}, ext={self.is_ext})")
+
+
+def _stream_ptr(device) -> int:
+    return int(torch.cuda.current_stream(device).cuda_stream)
+
+
+class CKKSContext:
+    """Prime chain + device tables (libholmes_ckks context) + evaluation keys in HBM."""
+
+    def __init__(self, spec: CKKSContextSpec, device: str = "cuda"):
+        spec.validate()
+        if not torch.cuda.is_available():
+            raise RuntimeError("holmes_amd needs a ROCm GPU: no device is visible (no CPU fallback)")
+        self.spec = spec
+        self.device = torch.device(device if device != "cuda" else "cuda:0")
+        self.logN = N_LOG
+        self.N = 1 << N_LOG
+        self.M = 2 * self.N
+        self.max_slots = self.N // 2
+        q, p = spec.prime_chain()
+        self.q_primes, self.p_primes = q, p
+        self.primes = q + p
+        self.L = len(q)
+        self.K = len(p)
+        self.alpha = spec.alpha
+        self.dnum = int(spec.dnum)
+        self.beta_max = -(-self.L // self.alpha)
+        self._scale = float(2 ** int(spec.scale_bits))
+        L = nat.lib()
+        h = ctypes.c_void_p()
+        with torch.cuda.device(self.device):
+            nat.check(
+                L.hck_context_create(ctypes.byref(h), N_LOG, self.L, self.K, self.alpha,
+                                     nat.u64_array(self.primes)),
+                "hck_context_create",
+            )
+        self._h = h
+        self._ws: torch.Tensor | None = None
+        self.rotation_keys: dict[int, torch.Tensor] = {}
+        self.relin_key: torch.Tensor | None = None
+
+    # ------------------------------------------------------------------ lifetime
+    def close(self) -> None:
+        if getattr(self, "_h", None) and self._h.value:
+            nat.lib().hck_context_destroy(self._h)
+            self._h = ctypes.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    @property
+    def handle(self):
+        return self._h
+
+    # ------------------------------------------------------------------ parameters
+    def scale_at(self, cur_limbs: int) -> float:
+        """Default encoding scale at a limb count (fixed scale mode)."""
+
+        return self._scale
+
+    def rescale_divisor_at(self, limbs: int) -> int:
+        """The prime a rescale from ``limbs`` limbs divides by (q_{limbs-1})."""
+
+        return int(self.q_primes[int(limbs) - 1])
+
+    def q_prime_idx(self, limbs: int) -> list[int]:
+        return list(range(int(limbs)))
+
+    def ext_prime_idx(self, limbs: int) -> list[int]:
+        return list(range(int(limbs))) + [self.L + k for k in range(self.K)]
+
+    def galois_element(self, rotation: int) -> int:
+        """5^r mod 2N for a left rotation by r slots (r taken mod N/2); 2N - 1 for conjugation."""
+
+        r = int(rotation) % self.max_slots
+        return pow(5, r, self.M)
+
+    # ------------------------------------------------------------------ memory
+    def workspace(self, nbytes: int) -> torch.Tensor:
+        nbytes = max(int(nbytes), 256)
+        if self._ws is None or self._ws.numel() < nbytes:
+            self._ws = None
+            self._ws = torch.empty(nbytes, dtype=torch.uint8, device=self.device)
+        return self._ws
+
+    def empty(self, *shape) -> torch.Tensor:
+        return torch.empty(shape, dtype=torch.uint64, device=self.device)
+
+    def zeros(self, *shape) -> torch.Tensor:
+        return torch.zeros(shape, dtype=torch.uint64, device=self.device)
+
+    # ------------------------------------------------------------------ kernels
+    @staticmethod
+    def _check_poly(t: torch.Tensor, limbs: int, n: int) -> None:
+        if t.dtype != torch.uint64 or t.dim() != 3:
+            raise ValueError("expected a [batch][limbs][N] uint64 tensor")
+        if t.shape[1] < limbs or t.shape[2] != n or t.stride(2) != 1 or t.stride(1) != n:
+            raise ValueError("limb-major [batch][>=limbs][N] layout with contiguous limbs required")
+        if t.device.type != "cuda":
+            raise ValueError("tensors must live on the GPU")
+
+    def ntt(self, src: torch.Tensor, dst: torch.Tensor | None = None, *, prime_idx, inverse: bool = False) -> torch.Tensor:
+        limbs = len(prime_idx)
+        self._check_poly(src, limbs, self.N)
+        dst = src if dst is None else dst
+        self._check_poly(dst, limbs, self.N)
+        fn = nat.lib().hck_ntt_inverse if inverse else nat.lib().hck_ntt_forward
+        nat.check(fn(self._h, src.data_ptr(), dst.data_ptr(), src.shape[0], src.stride(0), dst.stride(0),
+                     limbs, nat.int_array(prime_idx), _stream_ptr(self.device)),
+                  "hck_ntt_inverse" if inverse else "hck_ntt_forward")
+        return dst
+
+    def automorphism(self, src: torch.Tensor, galois: int, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        self._check_poly(src, limbs, self.N)
+        if out is None:
+            out = self.empty(src.shape[0], limbs, self.N)
+        self._check_poly(out, limbs, self.N)
+        nat.check(nat.lib().hck_automorphism(self._h, src.data_ptr(), out.data_ptr(), src.shape[0],
+                                             src.stride(0), out.stride(0), limbs, int(galois),
+                                             _stream_ptr(self.device)), "hck_automorphism")
+        return out
+
+    def poly_op(self, op: int, out: torch.Tensor, a: torch.Tensor, b: torch.Tensor | None = None, *,
+                prime_idx, scalar=None) -> torch.Tensor:
+        limbs = len(prime_idx)
+        for t in (out, a) + ((b,) if b is not None else ()):
+            self._check_poly(t, limbs, self.N)
+        bb = b if b is not None else a
+        sc = nat.u64_array(scalar) if scalar is not None else None
+        nat.check(nat.lib().hck_poly_op(self._h, int(op), out.data_ptr(), a.data_ptr(), bb.data_ptr(),
+                                        a.shape[0], out.stride(0), a.stride(0), bb.stride(0), limbs,
+                                        nat.int_array(prime_idx), sc, _stream_ptr(self.device)),
+                  "hck_poly_op")
+        return out
+
+    def from_signed(self, coeffs: torch.Tensor, prime_idx) -> torch.Tensor:
+        """int64 coefficient vectors [batch][N] -> residues [batch][limbs][N] (coefficient domain)."""
+
+        if coeffs.dtype != torch.int64 or coeffs.dim() != 2 or coeffs.shape[1] != self.N:
+            raise ValueError("expected [batch][N] int64 coefficients")
+        coeffs = coeffs.contiguous()
+        out = self.empty(coeffs.shape[0], len(prime_idx), self.N)
+        nat.check(nat.lib().hck_poly_from_signed(self._h, coeffs.data_ptr(), out.data_ptr(), coeffs.shape[0],
+                                                 coeffs.stride(0), out.stride(0), len(prime_idx),
+                                                 nat.int_array(prime_idx), _stream_ptr(self.device)),
+                  "hck_poly_from_signed")
+        return out
+
+    def keyswitch(self, d: torch.Tensor, limbs: int, keys, *, add: torch.Tensor | None = None,
+                  out_b: torch.Tensor | None = None, out_a: torch.Tensor | None = None):
+        """Batched hybrid key switch; ``keys`` is one key tensor per batch item (or one for all)."""
+
+        self._check_poly(d, limbs, self.N)
+        B = d.shape[0]
+        if isinstance(keys, torch.Tensor):
+            keys = [keys] * B
+        if len(keys) != B:
+            raise ValueError("one key per batch item")
+        for k in keys:
+            self._check_key(k)
+        out_b = self.empty(B, limbs, self.N) if out_b is None else out_b
+        out_a = self.empty(B, limbs, self.N) if out_a is None else out_a
+        if out_b.stride(0) != out_a.stride(0):
+            raise ValueError("out_b and out_a need the same batch stride")
+        if add is not None:
+            self._check_poly(add, limbs, self.N)
+        L = nat.lib()
+        ws_bytes = L.hck_keyswitch_workspace_bytes(self._h, limbs, B)
+        ws = self.workspace(ws_bytes)
+        nat.check(L.hck_keyswitch(self._h, limbs, B, d.data_ptr(), d.stride(0),
+                                  nat.ptr_array([k.data_ptr() for k in keys]),
+                                  add.data_ptr() if add is not None else None,
+                                  add.stride(0) if add is not None else 0,
+                                  out_b.data_ptr(), out_a.data_ptr(), out_b.stride(0),
+                                  ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_keyswitch")
+        return out_b, out_a
+
+    def rotate_raw(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois: int, keys,
+                   out0: torch.Tensor | None = None, out1: torch.Tensor | None = None):
+        self._check_poly(c0, limbs, self.N)
+        self._check_poly(c1, limbs, self.N)
+        if c0.stride(0) != c1.stride(0):
+            raise ValueError("c0 and c1 need the same batch stride")
+        B = c0.shape[0]
+        if isinstance(keys, torch.Tensor):
+            keys = [keys] * B
+        for k in keys:
+            self._check_key(k)
+        out0 = self.empty(B, limbs, self.N) if out0 is None else out0
+        out1 = self.empty(B, limbs, self.N) if out1 is None else out1
+        L = nat.lib()
+        ws = self.workspace(L.hck_rotate_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_rotate(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), c0.stride(0),
+                               nat.ptr_array([k.data_ptr() for k in keys]), out0.data_ptr(), out1.data_ptr(),
+                               out0.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                  "hck_rotate")
+        return out0, out1
+
+    def rescale_raw(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        self._check_poly(x, limbs, self.N)
+        if limbs < 2:
+            raise ValueError("rescale needs at least two limbs")
+        out = self.empty(x.shape[0], limbs - 1, self.N) if out is None else out
+        L = nat.lib()
+        ws = self.workspace(L.hck_rescale_workspace_bytes(self._h, limbs, x.shape[0]))
+        nat.check(L.hck_rescale(self._h, limbs, x.shape[0], x.data_ptr(), x.stride(0), out.data_ptr(),
+                                out.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                  "hck_rescale")
+        return out
+
+    def _check_key(self, k: torch.Tensor) -> None:
+        shape = (2, self.beta_max, self.L + self.K, self.N)
+        if k.dtype != torch.uint64 or tuple(k.shape) != shape or not k.is_contiguous():
+            raise ValueError(f"key must be a contiguous uint64 tensor of shape {shape}")
+
+    # ------------------------------------------------------------------ keys
+    def make_switching_key(self, s_from: np.ndarray, s_to: np.ndarray, a: np.ndarray, e: np.ndarray) -> torch.Tensor:
+        """Key switching s_from -> s_to (coefficient int64 vectors) on the GPU:
+        b_j = -a_j s_to + e_j + [P]_{q_i} s_from on digit j's Q limbs, a_j as given
+        (a: [beta_max][L+K][N] uniform residues, NTT domain; e: [beta_max][N] int64)."""
+
+        np_ = self.L + self.K
+        idx = list(range(np_))
+        dev = self.device
+        sf = self.from_signed(torch.from_numpy(np.ascontiguousarray(s_from, dtype=np.int64)).reshape(1, -1).to(dev), idx)
+        st = self.from_signed(torch.from_numpy(np.ascontiguousarray(s_to, dtype=np.int64)).reshape(1, -1).to(dev), idx)
+        self.ntt(sf, prime_idx=idx)
+        self.ntt(st, prime_idx=idx)
+        key = self.empty(2, self.beta_max, np_, self.N)
+        a_t = torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint64)).to(dev)
+        key[1].copy_(a_t)
+        e_t = torch.from_numpy(np.ascontiguousarray(e, dtype=np.int64)).to(dev)
+        ee = self.from_signed(e_t, idx)                      # [beta][np][N]
+        self.ntt(ee, prime_idx=idx)
+        pmod = []
+        for i in range(np_):
+            v = 1
+            for pk in self.p_primes:
+                v = v * pk % self.primes[i]
+            pmod.append(v if i < self.L else 0)
+        ps = self.empty(1, np_, self.N)
+        self.poly_op(nat.HCK_OP_MUL_SCALAR, ps, sf, prime_idx=idx, scalar=pmod)
+        for j in range(self.beta_max):
+            b = key[0, j].unsqueeze(0)
+            self.poly_op(nat.HCK_OP_MUL, b, a_t[j].unsqueeze(0), st, prime_idx=idx)
+            self.poly_op(nat.HCK_OP_SUB, b, ee[j].unsqueeze(0), b, prime_idx=idx)
+            lo, hi = j * self.alpha, min((j + 1) * self.alpha, self.L)
+            sub = list(range(lo, hi))
+            bv = key[0, j, lo:hi].unsqueeze(0)
+            self.poly_op(nat.HCK_OP_ADD, bv, bv, ps[:, lo:hi], prime_idx=sub)
+        return key
+
+    def get_rotation_key_for_limbs(self, rotation: int, cur_limbs: int) -> torch.Tensor:
+        g = self.galois_element(rotation) if int(rotation) != self.M - 1 else self.M - 1
+        key = self.rotation_keys.get(g)
+        if key is None:
+            raise KeyError(f"no rotation key for rotation {rotation} (galois element {g})")
+        return key
+
+    def key_for_galois(self, g: int) -> torch.Tensor:
+        key = self.rotation_keys.get(int(g))
+        if key is None:
+            raise KeyError(f"no key for galois element {g}")
+        return key
+
+    def clear_cuda_rotation_cache(self, keep_rotations=()) -> None:
+        keep = {self.galois_element(r) for r in keep_rotations}
+        for g in list(self.rotation_keys):
+            if g not in keep:
+                del self.rotation_keys[g]
+
+
+__all__ = ["CKKSContext", "Cipher", "CipherState"]

@@ -1,0 +1,261 @@
+// CKKS context: prime tables, NTT twiddles and key-switching constants, resident in HBM.
+//
+// Replaces the native-context tables that Holmes reads through EasyFHE
+// (`primes`, `barret_ratio`, `power_of_roots(_shoup)`, `PModq`, `QplusP_map`:
+// bench/cmp/holmes_fast_stage2.py:74-82, bench/cmp/holmes_fast_encode.py:70-75), re-laid out for
+// the FP64 arithmetic of modarith.hpp: every constant w is stored with its companion fl(w/p).
+#include <hip/hip_runtime.h>
+
+#include <cstring>
+#include <new>
+#include <vector>
+
+#include "../../include/holmes_ckks.h"
+#include "internal.hpp"
+
+using u64 = uint64_t;
+using u128 = unsigned __int128;
+
+namespace {
+
+u64 mulmod(u64 a, u64 b, u64 q) { return (u64)((u128)a * b % q); }
+u64 powmod(u64 b, u64 e, u64 q) {
+  u64 r = 1;
+  b %= q;
+  while (e) {
+    if (e & 1) r = mulmod(r, b, q);
+    b = mulmod(b, b, q);
+    e >>= 1;
+  }
+  return r;
+}
+u64 invmod(u64 a, u64 q) { return powmod(a, q - 2, q); }
+
+bool probable_prime(u64 n) {
+  if (n < 4) return n >= 2;
+  if (n % 2 == 0) return false;
+  u64 d = n - 1;
+  int s = 0;
+  while (!(d & 1)) { d >>= 1; ++s; }
+  for (u64 a : {2ULL, 325ULL, 9375ULL, 28178ULL, 450775ULL, 9780504ULL, 1795265022ULL}) {
+    u64 x = powmod(a % n, d, n);
+    if (a % n == 0 || x == 1 || x == n - 1) continue;
+    bool composite = true;
+    for (int r = 1; r < s && composite; ++r) {
+      x = mulmod(x, x, n);
+      if (x == n - 1) composite = false;
+    }
+    if (composite) return false;
+  }
+  return true;
+}
+
+// A primitive 2N-th root of unity: g^((q-1)/2N) for the smallest quadratic non-residue g.
+u64 primitive_root_2n(u64 q, int log_n) {
+  const u64 two_n = (u64)2 << log_n;
+  for (u64 g = 2;; ++g)
+    if (powmod(g, (q - 1) / 2, q) == q - 1) return powmod(g, (q - 1) / two_n, q);
+}
+
+hck::TwPair pair_of(u64 w, u64 q) { return hck::TwPair{(double)w, (double)w / (double)q}; }
+
+u64 brv(u64 x, int bits) {
+  u64 r = 0;
+  for (int i = 0; i < bits; ++i) { r = (r << 1) | (x & 1); x >>= 1; }
+  return r;
+}
+
+// Base-conversion constants from primes src[] to primes dst[] (hmod[s][t] = prod_{r != s} b_r mod t).
+void fill_conv(hck::ConvConsts& cc, const std::vector<u64>& P, const std::vector<int>& src,
+               const std::vector<int>& dst, const std::vector<int>& dst_slot) {
+  std::memset(&cc, 0, sizeof(cc));
+  cc.ns = (int)src.size();
+  cc.nt = (int)dst.size();
+  for (int s = 0; s < cc.ns; ++s) {
+    const u64 bs = P[src[s]];
+    u64 h = 1;
+    for (int r = 0; r < cc.ns; ++r) if (r != s) h = mulmod(h, P[src[r]] % bs, bs);
+    cc.src_prime[s] = src[s];
+    cc.hinv[s] = pair_of(invmod(h, bs), bs);
+    for (int t = 0; t < cc.nt; ++t) {
+      const u64 qt = P[dst[t]];
+      u64 v = 1;
+      for (int r = 0; r < cc.ns; ++r) if (r != s) v = mulmod(v, P[src[r]] % qt, qt);
+      cc.hmod[s][t] = pair_of(v, qt);
+    }
+  }
+  for (int t = 0; t < cc.nt; ++t) { cc.dst_prime[t] = dst[t]; cc.dst_slot[t] = dst_slot[t]; }
+}
+
+}  // namespace
+
+extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int num_p, int alpha,
+                                  const uint64_t* primes) {
+  if (!out || !primes) return HCK_ERR_ARG;
+  *out = nullptr;
+  if (log_n != hck::kLogN) return HCK_ERR_UNSUPPORTED;
+  if (num_q < 1 || num_p < 1 || num_p > hck::kMaxSpecial || alpha < 1 || alpha > hck::kMaxAlpha)
+    return HCK_ERR_ARG;
+  if (num_q + num_p > hck::kMaxPrimes) return HCK_ERR_ARG;
+  const int np = num_q + num_p;
+  const u64 two_n = (u64)2 << log_n;
+  std::vector<u64> P(primes, primes + np);
+  for (int i = 0; i < np; ++i) {
+    // The FP64 path needs p < 2^50 (exactness bounds of modarith.hpp) and p = 1 mod 2N.
+    if (P[i] >= (1ULL << 50) || P[i] % two_n != 1 || !probable_prime(P[i])) return HCK_ERR_PRIME;
+    for (int j = 0; j < i; ++j) if (P[j] == P[i]) return HCK_ERR_PRIME;
+  }
+  // Rescale reduces a [0, q_last) coefficient modulo q_i with one conditional subtraction.
+  for (int i = 0; i < np; ++i)
+    for (int j = 0; j < np; ++j)
+      if (P[i] >= 2 * P[j]) return HCK_ERR_PRIME;
+
+  hck_context* c = new (std::nothrow) hck_context();
+  if (!c) return HCK_ERR_ALLOC;
+  c->log_n = log_n; c->L = num_q; c->K = num_p; c->alpha = alpha; c->np = np;
+  c->primes = P;
+  c->beta_max = (num_q + alpha - 1) / alpha;
+  const size_t n = (size_t)1 << log_n;
+
+  // host tables
+  std::vector<double> hp(np), hpinv(np);
+  std::vector<hck::TwPair> fwd((size_t)np * n), inv((size_t)np * n), ninv(np), ninv_w1(np), zeta4(np);
+  for (int i = 0; i < np; ++i) {
+    const u64 q = P[i];
+    hp[i] = (double)q;
+    hpinv[i] = 1.0 / (double)q;
+    const u64 psi = primitive_root_2n(q, log_n), ipsi = invmod(psi, q);
+    u64 a = 1, b = 1;
+    for (size_t k = 0; k < n; ++k) {
+      const size_t r = brv(k, log_n);
+      fwd[(size_t)i * n + r] = pair_of(a, q);
+      inv[(size_t)i * n + r] = pair_of(b, q);
+      a = mulmod(a, psi, q);
+      b = mulmod(b, ipsi, q);
+    }
+    const u64 ni = invmod(n % q, q);
+    ninv[i] = pair_of(ni, q);
+    // the inverse transform's last stage uses psi_rev_inv[1]; folding N^-1 into it saves a pass
+    ninv_w1[i] = pair_of(mulmod(ni, (u64)inv[(size_t)i * n + 1].w, q), q);
+    zeta4[i] = pair_of(powmod(psi, n / 2, q), q);
+  }
+
+  // key-switching constants for every level ell in [1, L] and digit j
+  c->h_modup.assign((size_t)(num_q + 1) * c->beta_max, hck::ConvConsts{});
+  c->h_moddown.assign((size_t)(num_q + 1), hck::ConvConsts{});
+  c->h_level.assign((size_t)(num_q + 1), hck::LevelConsts{});
+  for (int ell = 1; ell <= num_q; ++ell) {
+    const int beta = (ell + alpha - 1) / alpha;
+    for (int j = 0; j < beta; ++j) {
+      const int lo = j * alpha, hi = std::min(lo + alpha, ell);
+      std::vector<int> src, dst, slot;
+      for (int i = lo; i < hi; ++i) src.push_back(i);
+      for (int e = 0; e < ell + num_p; ++e) {
+        if (e >= lo && e < hi) continue;
+        dst.push_back(e < ell ? e : num_q + (e - ell));
+        slot.push_back(e);
+      }
+      fill_conv(c->h_modup[(size_t)ell * c->beta_max + j], P, src, dst, slot);
+    }
+    std::vector<int> src, dst, slot;
+    for (int k = 0; k < num_p; ++k) src.push_back(num_q + k);
+    for (int i = 0; i < ell; ++i) { dst.push_back(i); slot.push_back(i); }
+    fill_conv(c->h_moddown[ell], P, src, dst, slot);
+    hck::LevelConsts& lc = c->h_level[ell];
+    for (int i = 0; i < ell; ++i) {
+      u64 pm = 1;
+      for (int k = 0; k < num_p; ++k) pm = mulmod(pm, P[num_q + k] % P[i], P[i]);
+      lc.p_inv[i] = pair_of(invmod(pm, P[i]), P[i]);
+      if (i < ell - 1) lc.qlast_inv[i] = pair_of(invmod(P[ell - 1] % P[i], P[i]), P[i]);
+    }
+  }
+
+  // one device block: [p | pinv | fwd | inv | ninv | ninv_w1 | zeta4 | modup | moddown | level]
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  size_t off = 0;
+  const size_t o_p = off; off = align(off + np * sizeof(double));
+  const size_t o_pinv = off; off = align(off + np * sizeof(double));
+  const size_t o_fwd = off; off = align(off + fwd.size() * sizeof(hck::TwPair));
+  const size_t o_inv = off; off = align(off + inv.size() * sizeof(hck::TwPair));
+  const size_t o_ninv = off; off = align(off + np * sizeof(hck::TwPair));
+  const size_t o_nw1 = off; off = align(off + np * sizeof(hck::TwPair));
+  const size_t o_z4 = off; off = align(off + np * sizeof(hck::TwPair));
+  const size_t o_mu = off; off = align(off + c->h_modup.size() * sizeof(hck::ConvConsts));
+  const size_t o_md = off; off = align(off + c->h_moddown.size() * sizeof(hck::ConvConsts));
+  const size_t o_lv = off; off = align(off + c->h_level.size() * sizeof(hck::LevelConsts));
+  const size_t o_pu = off; off = align(off + np * sizeof(u64));
+  void* blk = nullptr;
+  hipError_t e = hipMalloc(&blk, off);
+  if (e != hipSuccess) { delete c; return (int)e; }
+  char* base = (char*)blk;
+  struct Up { size_t o; const void* src; size_t bytes; } ups[] = {
+      {o_p, hp.data(), np * sizeof(double)},
+      {o_pinv, hpinv.data(), np * sizeof(double)},
+      {o_fwd, fwd.data(), fwd.size() * sizeof(hck::TwPair)},
+      {o_inv, inv.data(), inv.size() * sizeof(hck::TwPair)},
+      {o_ninv, ninv.data(), np * sizeof(hck::TwPair)},
+      {o_nw1, ninv_w1.data(), np * sizeof(hck::TwPair)},
+      {o_z4, zeta4.data(), np * sizeof(hck::TwPair)},
+      {o_mu, c->h_modup.data(), c->h_modup.size() * sizeof(hck::ConvConsts)},
+      {o_md, c->h_moddown.data(), c->h_moddown.size() * sizeof(hck::ConvConsts)},
+      {o_lv, c->h_level.data(), c->h_level.size() * sizeof(hck::LevelConsts)},
+      {o_pu, P.data(), np * sizeof(u64)},
+  };
+  for (const Up& u : ups) {
+    e = hipMemcpy(base + u.o, u.src, u.bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) { (void)hipFree(blk); delete c; return (int)e; }
+  }
+  c->d_block = blk;
+  c->dev.L = num_q; c->dev.K = num_p; c->dev.alpha = alpha; c->dev.np = np;
+  c->dev.p = (const double*)(base + o_p);
+  c->dev.pinv = (const double*)(base + o_pinv);
+  c->dev.tw_fwd = (const hck::TwPair*)(base + o_fwd);
+  c->dev.tw_inv = (const hck::TwPair*)(base + o_inv);
+  c->dev.ninv = (const hck::TwPair*)(base + o_ninv);
+  c->dev.ninv_w1 = (const hck::TwPair*)(base + o_nw1);
+  c->dev.zeta4 = (const hck::TwPair*)(base + o_z4);
+  c->d_modup = (hck::ConvConsts*)(base + o_mu);
+  c->d_moddown = (hck::ConvConsts*)(base + o_md);
+  c->d_level = (hck::LevelConsts*)(base + o_lv);
+  c->d_primes_u64 = (const u64*)(base + o_pu);
+  *out = c;
+  return HCK_OK;
+}
+
+extern "C" void hck_context_destroy(hck_context* ctx) {
+  if (!ctx) return;
+  if (ctx->d_block) (void)hipFree(ctx->d_block);
+  delete ctx;
+}
+
+extern "C" int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uint64_t* out) {
+  if (!ctx || !out || prime_idx < 0 || prime_idx >= ctx->np) return HCK_ERR_ARG;
+  const size_t n = (size_t)1 << ctx->log_n;
+  std::vector<hck::TwPair> tmp(n);
+  const hck::TwPair* src = (inverse ? ctx->dev.tw_inv : ctx->dev.tw_fwd) + (size_t)prime_idx * n;
+  hipError_t e = hipMemcpy(tmp.data(), src, n * sizeof(hck::TwPair), hipMemcpyDeviceToHost);
+  if (e != hipSuccess) return (int)e;
+  for (size_t k = 0; k < n; ++k) out[k] = (uint64_t)tmp[k].w;
+  return HCK_OK;
+}
+
+extern "C" int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, int* num_p, int* alpha) {
+  if (!ctx) return HCK_ERR_ARG;
+  if (log_n) *log_n = ctx->log_n;
+  if (num_q) *num_q = ctx->L;
+  if (num_p) *num_p = ctx->K;
+  if (alpha) *alpha = ctx->alpha;
+  return HCK_OK;
+}
+
+extern "C" const char* hck_error_string(int code) {
+  switch (code) {
+    case HCK_OK: return "ok";
+    case HCK_ERR_ARG: return "invalid argument";
+    case HCK_ERR_UNSUPPORTED: return "unsupported parameter";
+    case HCK_ERR_PRIME: return "prime rejected (needs p < 2^50, p = 1 mod 2N, prime, distinct, within a factor 2 of the others)";
+    case HCK_ERR_ALLOC: return "host allocation failed";
+    case HCK_ERR_WORKSPACE: return "workspace too small";
+    default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
+  }
+}

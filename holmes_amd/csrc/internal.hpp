@@ -1,0 +1,91 @@
+// Device-resident CKKS context shared by every kernel translation unit of libholmes_ckks.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <vector>
+
+#include "modarith.hpp"
+
+namespace hck {
+
+constexpr int kMaxPrimes = 64;  // Q + P primes
+constexpr int kMaxAlpha = 16;   // limbs per key-switching digit
+constexpr int kMaxSpecial = 16; // P primes
+
+// Base conversion constants from a source basis {b_s} to target primes {t}:
+//   y_s = [x_s * hinv_s]_{b_s} (canonical),   out_t = sum_s y_s * hmod[s][t]  mod t.
+struct ConvConsts {
+  int ns, nt;
+  int src_prime[kMaxAlpha];  // prime indices of the source limbs
+  int dst_prime[kMaxPrimes]; // prime index of target t
+  int dst_slot[kMaxPrimes];  // position of target t in the destination buffer (limb index)
+  TwPair hinv[kMaxAlpha];
+  TwPair hmod[kMaxAlpha][kMaxPrimes];
+};
+
+// Per-level ModDown / rescale constants.
+struct LevelConsts {
+  TwPair p_inv[kMaxPrimes];     // P^-1 mod q_i (i < ell)
+  TwPair qlast_inv[kMaxPrimes]; // q_{ell-1}^-1 mod q_i (i < ell - 1)
+};
+
+struct DevTables {
+  int L, K, alpha, np;
+  const double* p;      // [np]
+  const double* pinv;   // [np]
+  const TwPair* tw_fwd; // [np][N]: psi^brv(k) with its w/p companion
+  const TwPair* tw_inv; // [np][N]: psi^-brv(k)
+  const TwPair* ninv;   // [np]: N^-1
+  const TwPair* ninv_w1;// [np]: N^-1 * psi_rev_inv[1] (last inverse stage folded with N^-1)
+  const TwPair* zeta4;  // [np]: psi^(N/2), a primitive 4th root of unity (multiplication by X^(N/2))
+};
+
+}  // namespace hck
+
+struct hck_context {
+  int log_n, L, K, alpha, np;
+  std::vector<uint64_t> primes;
+  hck::DevTables dev;
+  // device allocations
+  void* d_block = nullptr;            // one allocation holding all tables
+  hck::ConvConsts* d_modup = nullptr; // [(L + 1) * beta_max]: index ell * beta_max + digit
+  hck::ConvConsts* d_moddown = nullptr; // [L + 1]
+  hck::LevelConsts* d_level = nullptr;  // [L + 1]
+  const uint64_t* d_primes_u64 = nullptr; // [np]
+  std::vector<hck::ConvConsts> h_modup, h_moddown;
+  std::vector<hck::LevelConsts> h_level;
+  int beta_max;
+};
+
+namespace hck {
+
+// A list of limbs inside one polynomial group: limb i sits at element offset off[i] * N from the
+// group base and uses prime prime[i].  Passed by value as a kernel argument.
+constexpr int kMaxList = 192;
+struct LimbList {
+  int n;
+  uint16_t off[kMaxList];
+  uint8_t prime[kMaxList];
+};
+
+enum Fmt { kU64 = 0, kF64 = 1 };  // canonical uint64 residues, or signed-lazy exact doubles
+
+// Two-pass NTT launchers shared by every translation unit (ntt.hip).  Group g of `groups` starts at
+// src + g * src_stride (elements); dst likewise.  Passing src == dst transforms in place.
+int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
+                   long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
+int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
+                   long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
+
+inline int beta_of(const hck_context* c, int ell) { return (ell + c->alpha - 1) / c->alpha; }
+inline const ConvConsts* modup_consts(const hck_context* c, int ell, int j) {
+  return c->d_modup + (size_t)ell * c->beta_max + j;
+}
+inline int prime_of_ext(const hck_context* c, int ell, int e) { return e < ell ? e : c->L + (e - ell); }
+}  // namespace hck
+
+#define HCK_CHECK_LAUNCH()                         \
+  do {                                             \
+    hipError_t _e = hipGetLastError();             \
+    if (_e != hipSuccess) return (int)_e;          \
+  } while (0)

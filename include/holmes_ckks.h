@@ -1,0 +1,121 @@
+/*
+ * holmes_ckks.h -- C ABI of the MI355X-native CKKS evaluation backend (libholmes_ckks.so).
+ *
+ * Every entry point takes device pointers that the caller allocated (the Python host side uses
+ * PyTorch-ROCm tensors) and a HIP stream passed as void*.  The library never frees caller memory.
+ * Residues are uint64 in [0, q), laid out limb-major [poly][limb][N] with N = 2^16, NTT
+ * (evaluation) domain unless a function says otherwise.  Return codes: 0 = success, negative =
+ * argument error (HCK_ERR_*), positive = a hipError_t from the launch.
+ *
+ * Reference interfaces replaced (EasyFHE is not vendored in the reference; its kernel names are
+ * listed in bench/cmp/report.py:26-48 and the sidecar C ABIs in bench/cmp/kernels/):
+ *   hck_context_*          native context tables (`primes`, `power_of_roots(_shoup)`, `PModq`,
+ *                          `QplusP_map`) read by bench/cmp/holmes_fast_stage2.py:74-82
+ *   hck_ntt_forward/inverse  EasyFHE NttImpl (spec: bench/cmp/kernels/holmes_encode.cu:75-78,200-226)
+ *   hck_automorphism       F.cv_hrot's NTT-domain permutation (bench/cmp/report.py:26-30)
+ *   hck_keyswitch          F.cv_modup + F.cv_innerproduct_* + F.cv_moddown (report.py:26-30),
+ *                          batched like giant_step_batched (bench/cmp/holmes_multi_mac.py:180-186)
+ *   hck_rotate             fhe.homo_rotate (llama3fhe/operators/linear/operator.py:446-453)
+ *   hck_rescale            fhe.rescale / F.cv_rescale_one_level (operator.py:387-394)
+ *   hck_poly_op            F.cv_add / cv_sub / cv_neg / cv_mul / cv_mul_by_monomial (report.py:26-48)
+ *   hck_poly_from_signed   the encoder's signed-integer reduction (holmes_encode.cu:108-111,133-159)
+ */
+#ifndef HOLMES_CKKS_H
+#define HOLMES_CKKS_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HCK_OK 0
+#define HCK_ERR_ARG (-1)
+#define HCK_ERR_UNSUPPORTED (-2)
+#define HCK_ERR_PRIME (-3)
+#define HCK_ERR_ALLOC (-4)
+#define HCK_ERR_WORKSPACE (-5)
+
+typedef struct hck_context hck_context;
+
+/* Context over primes[0..num_q) (Q chain) followed by primes[num_q..num_q+num_p) (special
+ * primes P); key-switching digits of `alpha` Q limbs.  Uploads all tables to the current device. */
+int hck_context_create(hck_context** out, int log_n, int num_q, int num_p, int alpha,
+                       const uint64_t* primes);
+void hck_context_destroy(hck_context* ctx);
+int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, int* num_p, int* alpha);
+/* Host copy of the root table psi^brv(k) (inverse: psi^-brv(k)) of prime `prime_idx` (N words). */
+int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uint64_t* out);
+const char* hck_error_string(int code);
+
+/* In-place (src == dst allowed) negacyclic NTT of `polys` x `limbs` limbs: limb l of poly b is at
+ * base + b * stride + l * N and uses prime prime_idx[l] (host array).  Forward: natural-order
+ * coefficients in, bit-reversed evaluation order out (out[k] = a(psi^(2 brv(k) + 1))). */
+int hck_ntt_forward(const hck_context* ctx, const uint64_t* src, uint64_t* dst, int polys,
+                    int64_t src_stride, int64_t dst_stride, int limbs, const int* prime_idx,
+                    void* stream);
+int hck_ntt_inverse(const hck_context* ctx, const uint64_t* src, uint64_t* dst, int polys,
+                    int64_t src_stride, int64_t dst_stride, int limbs, const int* prime_idx,
+                    void* stream);
+
+/* sigma_g on NTT-domain limbs: out[k] = in[k'] with 2 brv(k') + 1 = g (2 brv(k) + 1) mod 2N.
+ * Out-of-place only (out must not alias in). */
+int hck_automorphism(const hck_context* ctx, const uint64_t* in, uint64_t* out, int polys,
+                     int64_t in_stride, int64_t out_stride, int limbs, uint32_t galois,
+                     void* stream);
+
+/* Device workspace (bytes) hck_keyswitch / hck_rotate need for `batch` inputs at `level_limbs`. */
+size_t hck_keyswitch_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
+
+/* Hybrid key switch of `batch` polynomials d[b] (level_limbs limbs, stride d_stride):
+ * (out_b[b], out_a[b]) = ModDown(sum_j ModUp_j(d[b]) * ksk[b]_j) (+ add_b[b] when add_b != NULL).
+ * ksk[b] (host array of device pointers) is laid out [2][beta_max][num_q + num_p][N]
+ * (Q limbs, then P limbs; beta_max = ceil(num_q / alpha)).  Outputs must not alias d. */
+int hck_keyswitch(const hck_context* ctx, int level_limbs, int batch, const uint64_t* d,
+                  int64_t d_stride, const uint64_t* const* ksk, const uint64_t* add_b,
+                  int64_t add_stride, uint64_t* out_b, uint64_t* out_a, int64_t out_stride,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* Rotation of `batch` ciphertexts (c0[b], c1[b]) by galois element g with keys ksk[b]:
+ * out0 = sigma(c0) + KS_b(sigma(c1)), out1 = KS_a(sigma(c1)).  Same workspace as hck_keyswitch
+ * plus 2 * batch * level_limbs * N words (hck_rotate_workspace_bytes). */
+size_t hck_rotate_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
+int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
+               const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+               const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* Rescale `polys` polynomials from level_limbs to level_limbs - 1 limbs:
+ * out_i = (in_i - NTT([INTT(in_last)]_{q_i})) * q_last^-1 mod q_i. */
+size_t hck_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int polys);
+int hck_rescale(const hck_context* ctx, int level_limbs, int polys, const uint64_t* in,
+                int64_t in_stride, uint64_t* out, int64_t out_stride, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* Elementwise limb ops on [polys][limbs][N] (limb l uses prime prime_idx[l]).
+ * HCK_OP_ADD/SUB/MUL: out = a op b; NEG: out = -a; MUL_SCALAR: out = a * scalar[l];
+ * MUL_XHALF: out = a * X^(N/2) (NTT domain; times i on the slots); MAC: out = out + a * b. */
+#define HCK_OP_ADD 0
+#define HCK_OP_SUB 1
+#define HCK_OP_MUL 2
+#define HCK_OP_NEG 3
+#define HCK_OP_MUL_SCALAR 4
+#define HCK_OP_MUL_XHALF 5
+#define HCK_OP_MAC 6
+int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const uint64_t* a,
+                const uint64_t* b, int polys, int64_t out_stride, int64_t a_stride,
+                int64_t b_stride, int limbs, const int* prime_idx, const uint64_t* scalar,
+                void* stream);
+
+/* Signed 64-bit integers (coefficient domain, N per poly) reduced to residues for each limb:
+ * out[b][l][n] = in[b][n] mod q_{prime_idx[l]} in [0, q). */
+int hck_poly_from_signed(const hck_context* ctx, const int64_t* in, uint64_t* out, int polys,
+                         int64_t in_stride, int64_t out_stride, int limbs, const int* prime_idx,
+                         void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HOLMES_CKKS_H */

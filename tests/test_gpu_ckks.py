@@ -1,0 +1,103 @@
+"""End-to-end CKKS semantics on the GPU: encrypt -> op -> decrypt against NumPy float64.
+
+Pins the slot conventions of llama3fhe: rotate(v, r)[s] = v[(s + r) mod slots]
+(llama3fhe/layouts/shifted_lane.py:24-37), conjugation through galois element 2N - 1
+(operators/linear/complex.py:63-67), multiplication by i through homo_mul_i, and rescale
+dividing the scale by q_last.  Tolerance: 2^-16 relative to the slot scale (the bar of the
+decrypted-output parity).
+"""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+TOL = 2.0**-16
+
+
+@pytest.fixture(scope="module")
+def env():
+    from holmes_amd import fhe
+
+    spec = fhe.CKKSContextSpec(depth=23, dnum=3, seed=7, rotations=(1, 5, -3, 64, (1 << 17) - 1))
+    client, ctx = fhe.generate_client_context(spec)
+    return fhe, client, ctx
+
+
+def test_encrypt_decrypt_roundtrip(env):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(1)
+    v = rng.normal(size=ctx.max_slots)
+    ct = client.encrypt(v, cur_limbs=20)
+    out = client.decrypt(ct)
+    assert np.max(np.abs(out.real - v)) < TOL
+
+
+@pytest.mark.parametrize("r", [1, 5, -3, 64])
+def test_rotation_semantics(env, r):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(r + 100)
+    v = rng.normal(size=ctx.max_slots) + 1j * rng.normal(size=ctx.max_slots)
+    ct = client.encrypt(v, cur_limbs=24)
+    rot = fhe.homo_rotate(ct, r, ctx)
+    out = client.decrypt(rot)
+    assert np.max(np.abs(out - np.roll(v, -r))) < TOL
+
+
+def test_conjugation(env):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(2)
+    v = rng.normal(size=ctx.max_slots) + 1j * rng.normal(size=ctx.max_slots)
+    ct = client.encrypt(v, cur_limbs=12)
+    out = client.decrypt(fhe.homo_rotate(ct, ctx.M - 1, ctx))
+    assert np.max(np.abs(out - np.conj(v))) < TOL
+
+
+def test_mul_i_add_sub(env):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(3)
+    a = rng.normal(size=ctx.max_slots)
+    b = rng.normal(size=ctx.max_slots)
+    ca, cb = client.encrypt(a, cur_limbs=10), client.encrypt(b, cur_limbs=10)
+    out = client.decrypt(fhe.homo_add(fhe.homo_mul_i(ca, ctx), cb, ctx))
+    assert np.max(np.abs(out - (1j * a + b))) < TOL
+    out = client.decrypt(fhe.homo_sub(fhe.homo_mul_i(ca, ctx, negative=True), cb, ctx))
+    assert np.max(np.abs(out - (-1j * a - b))) < TOL
+
+
+def test_plain_multiply_and_rescale(env):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(4)
+    a = rng.normal(size=ctx.max_slots)
+    w = rng.normal(scale=0.5, size=ctx.max_slots)
+    ct = client.encrypt(a, cur_limbs=20)
+    # plaintext at scale q_last so the rescaled product returns to the input scale
+    st = fhe.CipherState(cur_limbs=20, scale_degree=1, scaling_factor=float(ctx.rescale_divisor_at(20)))
+    pt = fhe.encode_plaintext(w, st, ctx.max_slots, ctx)
+    prod = fhe.rescale(fhe.homo_mul_pt(ct, pt, ctx), ctx)
+    assert prod.state.cur_limbs == 19
+    assert abs(prod.state.scaling_factor - ct.state.scaling_factor) < 1e-6 * ct.state.scaling_factor
+    out = client.decrypt(prod)
+    assert np.max(np.abs(out.real - a * w)) < TOL
+
+
+def test_batched_rotation_one_key_per_item(env):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(5)
+    v = rng.normal(size=(3, ctx.max_slots))
+    ct = client.encrypt(v, cur_limbs=16)
+    rots = [1, 5, -3]
+    out = client.decrypt(fhe.homo_rotate_batch(ct, rots, ctx))
+    for b, r in enumerate(rots):
+        assert np.max(np.abs(out[b].real - np.roll(v[b], -r))) < TOL
+
+
+def test_align_to_drops_limbs_only(env):
+    fhe, client, ctx = env
+    rng = np.random.default_rng(6)
+    v = rng.normal(size=ctx.max_slots)
+    ct = client.encrypt(v, cur_limbs=18)
+    low = fhe.align_to(ct, ct.state.replace(cur_limbs=9), ctx)
+    assert low.state.cur_limbs == 9
+    assert np.max(np.abs(client.decrypt(low).real - v)) < TOL
