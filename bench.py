@@ -40,6 +40,7 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--seed", type=int, default=20261202)
+    ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -73,8 +74,15 @@ def main() -> int:
     torch.cuda.synchronize()
     _log(f"setup {time.perf_counter() - t0:.1f}s (context, 16 keys of {keys[0].numel() * 8 / 2**20:.0f} MiB)")
 
+    chunk = max(1, min(CTS, args.chunk))
+
+    def step():
+        for c0 in range(0, CTS, chunk):
+            c1 = min(CTS, c0 + chunk)
+            ctx.keyswitch(d[c0:c1], LIMBS, keys[c0:c1], out_b=out_b[c0:c1], out_a=out_a[c0:c1])
+
     for _ in range(args.warmup):
-        ctx.keyswitch(d, LIMBS, keys, out_b=out_b, out_a=out_a)
+        step()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -83,7 +91,7 @@ def main() -> int:
     w0 = time.perf_counter()
     ev0.record(stream)
     for _ in range(args.steps):
-        ctx.keyswitch(d, LIMBS, keys, out_b=out_b, out_a=out_a)
+        step()
     ev1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
@@ -139,6 +147,7 @@ def main() -> int:
             "special_primes": ctx.K,
             "batch": CTS,
             "algorithmic_bytes_per_step": step_bytes,
+            "cts_per_launch": chunk,
         },
         "roofline": {
             "bound": "hbm",

@@ -3,7 +3,8 @@
 // Replaces the native-context tables that Holmes reads through EasyFHE
 // (`primes`, `barret_ratio`, `power_of_roots(_shoup)`, `PModq`, `QplusP_map`:
 // bench/cmp/holmes_fast_stage2.py:74-82, bench/cmp/holmes_fast_encode.py:70-75), re-laid out for
-// the FP64 arithmetic of modarith.hpp: every constant w is stored with its companion fl(w/p).
+// the FP64 arithmetic of modarith.hpp: NTT roots as exact doubles, every other constant w with its
+// companion fl(w/p).
 #include <hip/hip_runtime.h>
 
 #include <cstring>
@@ -119,7 +120,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
 
   // host tables
   std::vector<double> hp(np), hpinv(np);
-  std::vector<hck::TwPair> fwd((size_t)np * n), inv((size_t)np * n), ninv(np), ninv_w1(np), zeta4(np);
+  std::vector<double> fwd((size_t)np * n), inv((size_t)np * n);
+  std::vector<hck::TwPair> ninv(np), ninv_w1(np), zeta4(np);
   for (int i = 0; i < np; ++i) {
     const u64 q = P[i];
     hp[i] = (double)q;
@@ -128,15 +130,15 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     u64 a = 1, b = 1;
     for (size_t k = 0; k < n; ++k) {
       const size_t r = brv(k, log_n);
-      fwd[(size_t)i * n + r] = pair_of(a, q);
-      inv[(size_t)i * n + r] = pair_of(b, q);
+      fwd[(size_t)i * n + r] = (double)a;
+      inv[(size_t)i * n + r] = (double)b;
       a = mulmod(a, psi, q);
       b = mulmod(b, ipsi, q);
     }
     const u64 ni = invmod(n % q, q);
     ninv[i] = pair_of(ni, q);
     // the inverse transform's last stage uses psi_rev_inv[1]; folding N^-1 into it saves a pass
-    ninv_w1[i] = pair_of(mulmod(ni, (u64)inv[(size_t)i * n + 1].w, q), q);
+    ninv_w1[i] = pair_of(mulmod(ni, (u64)inv[(size_t)i * n + 1], q), q);
     zeta4[i] = pair_of(powmod(psi, n / 2, q), q);
   }
 
@@ -175,8 +177,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   size_t off = 0;
   const size_t o_p = off; off = align(off + np * sizeof(double));
   const size_t o_pinv = off; off = align(off + np * sizeof(double));
-  const size_t o_fwd = off; off = align(off + fwd.size() * sizeof(hck::TwPair));
-  const size_t o_inv = off; off = align(off + inv.size() * sizeof(hck::TwPair));
+  const size_t o_fwd = off; off = align(off + fwd.size() * sizeof(double));
+  const size_t o_inv = off; off = align(off + inv.size() * sizeof(double));
   const size_t o_ninv = off; off = align(off + np * sizeof(hck::TwPair));
   const size_t o_nw1 = off; off = align(off + np * sizeof(hck::TwPair));
   const size_t o_z4 = off; off = align(off + np * sizeof(hck::TwPair));
@@ -191,8 +193,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   struct Up { size_t o; const void* src; size_t bytes; } ups[] = {
       {o_p, hp.data(), np * sizeof(double)},
       {o_pinv, hpinv.data(), np * sizeof(double)},
-      {o_fwd, fwd.data(), fwd.size() * sizeof(hck::TwPair)},
-      {o_inv, inv.data(), inv.size() * sizeof(hck::TwPair)},
+      {o_fwd, fwd.data(), fwd.size() * sizeof(double)},
+      {o_inv, inv.data(), inv.size() * sizeof(double)},
       {o_ninv, ninv.data(), np * sizeof(hck::TwPair)},
       {o_nw1, ninv_w1.data(), np * sizeof(hck::TwPair)},
       {o_z4, zeta4.data(), np * sizeof(hck::TwPair)},
@@ -209,8 +211,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->dev.L = num_q; c->dev.K = num_p; c->dev.alpha = alpha; c->dev.np = np;
   c->dev.p = (const double*)(base + o_p);
   c->dev.pinv = (const double*)(base + o_pinv);
-  c->dev.tw_fwd = (const hck::TwPair*)(base + o_fwd);
-  c->dev.tw_inv = (const hck::TwPair*)(base + o_inv);
+  c->dev.tw_fwd = (const double*)(base + o_fwd);
+  c->dev.tw_inv = (const double*)(base + o_inv);
   c->dev.ninv = (const hck::TwPair*)(base + o_ninv);
   c->dev.ninv_w1 = (const hck::TwPair*)(base + o_nw1);
   c->dev.zeta4 = (const hck::TwPair*)(base + o_z4);
@@ -231,11 +233,11 @@ extern "C" void hck_context_destroy(hck_context* ctx) {
 extern "C" int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uint64_t* out) {
   if (!ctx || !out || prime_idx < 0 || prime_idx >= ctx->np) return HCK_ERR_ARG;
   const size_t n = (size_t)1 << ctx->log_n;
-  std::vector<hck::TwPair> tmp(n);
-  const hck::TwPair* src = (inverse ? ctx->dev.tw_inv : ctx->dev.tw_fwd) + (size_t)prime_idx * n;
-  hipError_t e = hipMemcpy(tmp.data(), src, n * sizeof(hck::TwPair), hipMemcpyDeviceToHost);
+  std::vector<double> tmp(n);
+  const double* src = (inverse ? ctx->dev.tw_inv : ctx->dev.tw_fwd) + (size_t)prime_idx * n;
+  hipError_t e = hipMemcpy(tmp.data(), src, n * sizeof(double), hipMemcpyDeviceToHost);
   if (e != hipSuccess) return (int)e;
-  for (size_t k = 0; k < n; ++k) out[k] = (uint64_t)tmp[k].w;
+  for (size_t k = 0; k < n; ++k) out[k] = (uint64_t)tmp[k];
   return HCK_OK;
 }
 

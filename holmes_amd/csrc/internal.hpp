@@ -9,8 +9,8 @@
 namespace hck {
 
 constexpr int kMaxPrimes = 64;  // Q + P primes
-constexpr int kMaxAlpha = 16;   // limbs per key-switching digit
-constexpr int kMaxSpecial = 16; // P primes
+constexpr int kMaxAlpha = 8;    // limbs per key-switching digit (fused ModUp holds them in LDS)
+constexpr int kMaxSpecial = 8;  // P primes (fused ModDown holds them in LDS)
 
 // Base conversion constants from a source basis {b_s} to target primes {t}:
 //   y_s = [x_s * hinv_s]_{b_s} (canonical),   out_t = sum_s y_s * hmod[s][t]  mod t.
@@ -33,8 +33,8 @@ struct DevTables {
   int L, K, alpha, np;
   const double* p;      // [np]
   const double* pinv;   // [np]
-  const TwPair* tw_fwd; // [np][N]: psi^brv(k) with its w/p companion
-  const TwPair* tw_inv; // [np][N]: psi^-brv(k)
+  const double* tw_fwd; // [np][N]: psi^brv(k) (companion recomputed in mulv)
+  const double* tw_inv; // [np][N]: psi^-brv(k)
   const TwPair* ninv;   // [np]: N^-1
   const TwPair* ninv_w1;// [np]: N^-1 * psi_rev_inv[1] (last inverse stage folded with N^-1)
   const TwPair* zeta4;  // [np]: psi^(N/2), a primitive 4th root of unity (multiplication by X^(N/2))
@@ -76,6 +76,11 @@ int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
 int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
+
+size_t ks_fused_bytes(const hck_context* c, int ell, int batch);
+int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
+             const uint64_t* const* ksk, const uint64_t* add, long long add_stride, uint64_t* out_b,
+             uint64_t* out_a, long long out_stride, char* ws, hipStream_t s);
 
 inline int beta_of(const hck_context* c, int ell) { return (ell + c->alpha - 1) / c->alpha; }
 inline const ConvConsts* modup_consts(const hck_context* c, int ell, int j) {

@@ -1,0 +1,490 @@
+// Fused hybrid key switch: five kernels per batch, extended-basis limbs cross HBM once.
+//
+// A limb (N = 2^16 words) is a 256 x 256 matrix, n = 256 r + c.  The forward NTT runs stages
+// 0..7 inside columns ("cols" pass) and 8..15 inside rows ("rows" pass); the inverse runs rows
+// (15..8) then cols (7..0).  Workspace buffers keep limbs in a transposed layout (element (r, c)
+// at c * 256 + r) so a column is 2 KiB contiguous: the cols kernels read and write whole columns,
+// the rows kernels read 16 rows at once as 128-byte runs.
+//
+//   K1 ks_intt_rows   d (natural, u64) --INTT rows-->                         T1 (transposed)
+//   K2 ks_cols_conv   T1 --INTT cols--> coefficients --ModUp conversion (LDS)--> NTT cols --> T2
+//   K3 ks_rows_ip     T2 --NTT rows--> x_j;  acc = sum_j x_j * key_j  (d for the digit's own limbs)
+//                     Q limbs: acc --> ACCQ (natural);  P limbs: acc --INTT rows--> ACCP (transposed)
+//   K4 ks_cols_conv   ACCP --INTT cols--> ModDown conversion P -> Q --NTT cols--> T4
+//   K5 ks_rows_finish T4 --NTT rows--> v;  out = (ACCQ - v) * P^-1 (+ addend), canonical u64
+//
+// Per ciphertext at ell = 24, K = 8, dnum 3 this moves 352 MiB (key 96 MiB) instead of the
+// 648 MiB of separate transform / conversion / product kernels.  Arithmetic: modarith.hpp.
+// Algorithm: the key-switch EasyFHE runs for fhe.homo_rotate (F.cv_modup, F.cv_innerproduct_*,
+// F.cv_moddown; bench/cmp/report.py:26-30); key layout llama3fhe/parallel/prefill/keys.py:105-117.
+#include <hip/hip_runtime.h>
+
+#include "../../include/holmes_ckks.h"
+#include "internal.hpp"
+
+namespace hck {
+namespace {
+
+constexpr int kT = 256;          // threads per workgroup
+constexpr int kMaxBatchF = 64;   // ciphertexts per launch (key pointers passed by value)
+constexpr int kSrcMax = 8;       // source limbs of one conversion held in LDS
+constexpr int kYStride = 272;    // LDS stride of one (source, column) run of 256 values
+
+struct KeyPtrsF {
+  const uint64_t* k[kMaxBatchF];
+};
+
+template <bool RED>
+__device__ __forceinline__ void ct_bf(double& u, double& v, const double w, double p, double pinv) {
+  const double m = mulv(v, w, p, pinv);
+  const double a = RED ? reduce(u, p, pinv) : u;
+  u = a + m;
+  v = a - m;
+}
+
+__device__ __forceinline__ void gs_bf(double& u, double& v, const double w, double p, double pinv) {
+  const double s = u + v, d = u - v;
+  u = reduce(s, p, pinv);
+  v = mulv(d, w, p, pinv);
+}
+
+// ----------------------------------------------------------------- column transforms (16 threads)
+// A "slot" of 16 threads owns one 256-point column; thread j holds 16 values, either rows
+// j + 16k (layout A) or rows 16j + k (layout B).  R is the slot's LDS run of 272 doubles.
+__device__ __forceinline__ int cpad(int r) { return r + (r >> 4); }
+
+__device__ __forceinline__ void col_a_to_b(double (&x)[16], double* R, int j) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) R[cpad(j + 16 * k)] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = R[cpad(16 * j + k)];
+  __syncthreads();
+}
+
+__device__ __forceinline__ void col_b_to_a(double (&x)[16], double* R, int j) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) R[cpad(16 * j + k)] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = R[cpad(j + 16 * k)];
+  __syncthreads();
+}
+
+// forward stages 0..3 on layout A
+__device__ __forceinline__ void col_fwd_lo(double (&x)[16], const double* __restrict__ tw, double p, double pinv) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const int h = 8 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const double w = tw[(1 << l) + (k >> (4 - l))];
+      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      else ct_bf<true>(x[k], x[k + h], w, p, pinv);
+    }
+  }
+}
+
+// forward stages 4..7 on layout B
+__device__ __forceinline__ void col_fwd_hi(double (&x)[16], int j, const double* __restrict__ tw, double p,
+                                           double pinv) {
+#pragma unroll
+  for (int l = 4; l < 8; ++l) {
+    const int h = 128 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const double w = tw[(1 << l) + (j << (l - 4)) + (k >> (8 - l))];
+      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      else ct_bf<true>(x[k], x[k + h], w, p, pinv);
+    }
+  }
+}
+
+// inverse stages 7..4 on layout B
+__device__ __forceinline__ void col_inv_hi(double (&x)[16], int j, const double* __restrict__ tw, double p,
+                                           double pinv) {
+#pragma unroll
+  for (int l = 7; l >= 4; --l) {
+    const int h = 128 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      gs_bf(x[k], x[k + h], tw[(1 << l) + (j << (l - 4)) + (k >> (8 - l))], p, pinv);
+    }
+  }
+}
+
+// inverse stages 3..0 on layout A, N^-1 folded into stage 0
+__device__ __forceinline__ void col_inv_lo(double (&x)[16], const double* __restrict__ tw, TwPair n0, TwPair n1,
+                                           double p, double pinv) {
+#pragma unroll
+  for (int l = 3; l >= 1; --l) {
+    const int h = 8 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      gs_bf(x[k], x[k + h], tw[(1 << l) + (k >> (4 - l))], p, pinv);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {
+    const double s = x[k] + x[k + 8], d = x[k] - x[k + 8];
+    x[k] = mulc(s, n0, p);
+    x[k + 8] = mulc(d, n1, p);
+  }
+}
+
+// ----------------------------------------------------------------- row transforms (256 threads)
+// The block owns 16 rows (b = r0 + rb).  Two thread mappings: "N" (rb = t >> 4, j = t & 15) makes
+// 16 consecutive lanes touch 16 consecutive words of a natural-layout row; "T" (rb = t & 15,
+// j = t >> 4) makes them touch 16 consecutive rows of a transposed-layout column.
+__device__ __forceinline__ int ridx(int rb, int c) { return rb * 273 + c + (c >> 4); }
+constexpr int kRowLds = 16 * 273 + 16;
+
+struct RowMap {
+  int rb, j;
+};
+__device__ __forceinline__ RowMap map_n() { return RowMap{(int)threadIdx.x >> 4, (int)threadIdx.x & 15}; }
+__device__ __forceinline__ RowMap map_t() { return RowMap{(int)threadIdx.x & 15, (int)threadIdx.x >> 4}; }
+
+// x in layout (from, A or B) -> layout (to, A or B) under mapping `to_map`
+template <bool FROM_A, bool TO_A>
+__device__ __forceinline__ void row_xchg(double (&x)[16], double* S, RowMap fm, RowMap tm) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) S[ridx(fm.rb, FROM_A ? fm.j + 16 * k : 16 * fm.j + k)] = x[k];
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = S[ridx(tm.rb, TO_A ? tm.j + 16 * k : 16 * tm.j + k)];
+  __syncthreads();
+}
+
+// forward stages 8..11 on layout A for row b
+__device__ __forceinline__ void row_fwd_lo(double (&x)[16], int b, const double* __restrict__ tw, double p,
+                                           double pinv) {
+#pragma unroll
+  for (int l = 8; l < 12; ++l) {
+    const int h = 2048 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const double w = tw[(1 << l) + (b << (l - 8)) + (k >> (12 - l))];
+      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      else ct_bf<true>(x[k], x[k + h], w, p, pinv);
+    }
+  }
+}
+
+// forward stages 12..15 on layout B
+__device__ __forceinline__ void row_fwd_hi(double (&x)[16], int b, int j, const double* __restrict__ tw, double p,
+                                           double pinv) {
+#pragma unroll
+  for (int l = 12; l < 16; ++l) {
+    const int h = 32768 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const double w = tw[(1 << l) + (b << (l - 8)) + (j << (l - 12)) + (k >> (16 - l))];
+      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      else ct_bf<true>(x[k], x[k + h], w, p, pinv);
+    }
+  }
+}
+
+// inverse stages 15..12 on layout B
+__device__ __forceinline__ void row_inv_hi(double (&x)[16], int b, int j, const double* __restrict__ tw, double p,
+                                           double pinv) {
+#pragma unroll
+  for (int l = 15; l >= 12; --l) {
+    const int h = 32768 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      gs_bf(x[k], x[k + h], tw[(1 << l) + (b << (l - 8)) + (j << (l - 12)) + (k >> (16 - l))], p, pinv);
+    }
+  }
+}
+
+// inverse stages 11..8 on layout A
+__device__ __forceinline__ void row_inv_lo(double (&x)[16], int b, const double* __restrict__ tw, double p,
+                                           double pinv) {
+#pragma unroll
+  for (int l = 11; l >= 8; --l) {
+    const int h = 2048 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      gs_bf(x[k], x[k + h], tw[(1 << l) + (b << (l - 8)) + (k >> (12 - l))], p, pinv);
+    }
+  }
+}
+
+// Natural-layout access in layout A under map N: thread (rb, j) owns words j + 16k of row r0 + rb;
+// 16 consecutive lanes touch 128 consecutive bytes.
+__device__ __forceinline__ long long nat_a(int r0) {
+  const RowMap mn = map_n();
+  return (long long)(r0 + mn.rb) * 256 + mn.j;
+}
+
+// NTT rows pass of 16 transposed-layout rows: loads under map T (layout A), returns layout A under
+// map N (thread owns natural words nat_a(r0) + 16k).
+__device__ __forceinline__ void rows_fwd_from_t(double (&x)[16], const double* __restrict__ src_t, int r0,
+                                                double* S, const double* __restrict__ tw, double p, double pinv) {
+  const RowMap mt = map_t(), mn = map_n();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = src_t[(long long)(mt.j + 16 * k) * 256 + r0 + mt.rb];
+  row_fwd_lo(x, r0 + mt.rb, tw, p, pinv);
+  row_xchg<true, false>(x, S, mt, mn);
+  row_fwd_hi(x, r0 + mn.rb, mn.j, tw, p, pinv);
+  row_xchg<false, true>(x, S, mn, mn);
+}
+
+// INTT rows pass of 16 rows held in layout A under map N; stores the result transposed.
+__device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restrict__ dst_t, int r0, double* S,
+                                              const double* __restrict__ tw, double p, double pinv) {
+  const RowMap mt = map_t(), mn = map_n();
+  row_xchg<true, false>(x, S, mn, mn);
+  row_inv_hi(x, r0 + mn.rb, mn.j, tw, p, pinv);
+  row_xchg<false, true>(x, S, mn, mt);
+  row_inv_lo(x, r0 + mt.rb, tw, p, pinv);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) dst_t[(long long)(mt.j + 16 * k) * 256 + r0 + mt.rb] = x[k];
+}
+
+// ----------------------------------------------------------------- K1: INTT rows of d
+__global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
+                                                     double* __restrict__ t1, int ell, DevTables T) {
+  __shared__ double S[kRowLds];
+  const int i = blockIdx.z, b = blockIdx.x, r0 = blockIdx.y * 16;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const double* __restrict__ tw = T.tw_inv + (size_t)i * kN;
+  const uint64_t* src = d + (long long)b * d_stride + (long long)i * kN + nat_a(r0);
+  double x[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = u2d(src[16 * k]);
+  rows_inv_to_t(x, t1 + ((long long)b * ell + i) * kN, r0, S, tw, p, pinv);
+}
+
+// ----------------------------------------------------------------- K2 / K4: cols + conversion
+// Block: two columns (c0, c0 + 1) of one conversion group.  Phase 1: INTT cols of each source limb,
+// y_s = centered [x_s * hinv_s] into LDS.  Phase 2: per target t, sum_s y_s * hmod[s][t], NTT cols,
+// store.  16 slots of 16 threads; slot sigma handles (limb = pi >> 1, column = pi & 1), pi = 16 r + sigma.
+__global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ src, long long src_zs,
+                                                     long long src_ys, int src_off_y, double* __restrict__ dst,
+                                                     long long dst_zs, long long dst_ys,
+                                                     const ConvConsts* __restrict__ cc_base, int cc_y,
+                                                     DevTables T) {
+  __shared__ double X[16 * 272];              // per-slot exchange runs
+  __shared__ double Y[kSrcMax * 2 * kYStride];  // y_s for both columns
+  const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
+  const int c0 = blockIdx.x * 2;
+  const int y = blockIdx.y;
+  const long long z = blockIdx.z;
+  const ConvConsts& C = cc_base[y * cc_y];
+  const int ns = C.ns, nt = C.nt;
+  double* R = X + sigma * 272;
+  const double* sbase = src + z * src_zs + y * src_ys + (long long)y * src_off_y * kN;
+  double x[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = 0.0;
+  // phase 1
+  for (int r = 0; r < (2 * ns + 15) / 16; ++r) {
+    const int pi = 16 * r + sigma, s = pi >> 1, cl = pi & 1;
+    const bool act = s < ns;
+    const int sp = C.src_prime[act ? s : 0];
+    const double p = T.p[sp], pinv = T.pinv[sp];
+    const double* __restrict__ tw = T.tw_inv + (size_t)sp * kN;
+    if (act) {
+      const double* col = sbase + (long long)s * kN + (long long)(c0 + cl) * 256;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = col[j + 16 * k];
+    }
+    col_a_to_b(x, R, j);
+    if (act) col_inv_hi(x, j, tw, p, pinv);
+    col_b_to_a(x, R, j);
+    if (act) {
+      col_inv_lo(x, tw, T.ninv[sp], T.ninv_w1[sp], p, pinv);
+      const TwPair hi = C.hinv[s];
+      double* Yr = Y + (s * 2 + cl) * kYStride;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const double v = canon(mulc(x[k], hi, p), p, pinv);
+        Yr[j + 16 * k] = v > 0.5 * p ? v - p : v;  // centered lift: zero-mean
+      }
+    }
+  }
+  __syncthreads();
+  // phase 2
+  double* dbase = dst + z * dst_zs + y * dst_ys;
+  for (int r = 0; r < (2 * nt + 15) / 16; ++r) {
+    const int pi = 16 * r + sigma, tg = pi >> 1, cl = pi & 1;
+    const bool act = tg < nt;
+    const int tp = C.dst_prime[act ? tg : 0];
+    const double p = T.p[tp], pinv = T.pinv[tp];
+    const double* __restrict__ tw = T.tw_fwd + (size_t)tp * kN;
+    if (act) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = 0.0;
+      for (int s = 0; s < ns; ++s) {
+        const TwPair h = C.hmod[s][tg];
+        const double* Yr = Y + (s * 2 + cl) * kYStride;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) x[k] += mulc(Yr[j + 16 * k], h, p);  // |term| <= 0.625 p
+      }
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = reduce(x[k], p, pinv);
+      col_fwd_lo(x, tw, p, pinv);
+    }
+    col_a_to_b(x, R, j);
+    if (act) col_fwd_hi(x, j, tw, p, pinv);
+    col_b_to_a(x, R, j);
+    if (act) {
+      double* col = dbase + (long long)C.dst_slot[tg] * kN + (long long)(c0 + cl) * 256;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) col[j + 16 * k] = x[k];
+    }
+  }
+}
+
+// ----------------------------------------------------------------- K3: NTT rows + inner product
+__global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride,
+                                                   const double* __restrict__ t2, KeyPtrsF keys, int ell,
+                                                   int beta, double* __restrict__ accq, double* __restrict__ accp,
+                                                   DevTables T) {
+  __shared__ double S[kRowLds];
+  const int e = blockIdx.z, b = blockIdx.x, r0 = blockIdx.y * 16;
+  const int L = T.L, K = T.K, alpha = T.alpha;
+  const int ext_l = ell + K;
+  const int pi = e < ell ? e : L + (e - ell);
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  const double* __restrict__ twf = T.tw_fwd + (size_t)pi * kN;
+  const int beta_max = (L + alpha - 1) / alpha;
+  const long long comp_stride = (long long)beta_max * (L + K) * kN;
+  const uint64_t* key = keys.k[b];
+  const int own = e < ell ? e / alpha : -1;
+  const long long na = nat_a(r0);
+  double sb[16], sa[16], x[16];
+  uint64_t kb[16], ka[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
+  for (int jd = 0; jd < beta; ++jd) {
+    // issue this digit's key loads first: they land while the NTT below computes
+    const uint64_t* kp = key + ((long long)jd * (L + K) + pi) * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { kb[k] = kp[16 * k]; ka[k] = kp[comp_stride + 16 * k]; }
+    if (jd == own) {
+      const uint64_t* src = d + (long long)b * d_stride + (long long)e * kN + na;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = u2d(src[16 * k]);
+    } else {
+      rows_fwd_from_t(x, t2 + (((long long)b * beta + jd) * ext_l + e) * kN, r0, S, twf, p, pinv);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);  // |x| <= 3.9p: |term| <= 2p
+      sa[k] += mulv(x[k], u2d(ka[k]), p, pinv);
+    }
+    if ((jd & 3) == 3) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+  if (e < ell) {
+    double* ob = accq + ((long long)b * 2 * ell + e) * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { ob[16 * k] = sb[k]; ob[(long long)ell * kN + 16 * k] = sa[k]; }
+    return;
+  }
+  // P limb: INTT rows of both components, stored transposed for the ModDown cols kernel
+  const double* __restrict__ twi = T.tw_inv + (size_t)pi * kN;
+  double* o = accp + ((long long)b * 2 * K + (e - ell)) * kN;
+  rows_inv_to_t(sb, o, r0, S, twi, p, pinv);
+  rows_inv_to_t(sa, o + (long long)K * kN, r0, S, twi, p, pinv);
+}
+
+// ----------------------------------------------------------------- K5: NTT rows + ModDown combine
+__global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const double* __restrict__ accq,
+                                                       const uint64_t* __restrict__ add, long long add_stride,
+                                                       uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
+                                                       long long out_stride, int ell,
+                                                       const LevelConsts* __restrict__ lc, DevTables T) {
+  __shared__ double S[kRowLds];
+  const int i = blockIdx.z, r0 = blockIdx.y * 16;
+  const int b = blockIdx.x >> 1, comp = blockIdx.x & 1;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const double* __restrict__ tw = T.tw_fwd + (size_t)i * kN;
+  const long long na = nat_a(r0);
+  // prefetch the accumulator (and the rotation addend) before the transform
+  double a[16];
+  const double* ap = accq + (((long long)b * 2 + comp) * ell + i) * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) a[k] = ap[16 * k];
+  uint64_t ad[16];
+  const bool has_add = comp == 0 && add;
+  if (has_add) {
+    const uint64_t* pp = add + (long long)b * add_stride + (long long)i * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ad[k] = pp[16 * k];
+  }
+  double x[16];
+  rows_fwd_from_t(x, t4 + (((long long)b * 2 + comp) * ell + i) * kN, r0, S, tw, p, pinv);
+  const TwPair pi_ = lc->p_inv[i];
+  uint64_t* o = (comp == 0 ? out_b : out_a) + (long long)b * out_stride + (long long)i * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    double r = mulc(a[k] - x[k], pi_, p);  // |acc - v| <= 4.5 p: |r| <= 2.2 p
+    if (has_add) r += u2d(ad[k]);
+    o[16 * k] = d2u(canon(r, p, pinv));
+  }
+}
+
+}  // namespace
+
+// Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)],
+// ACCQ [2 ell], ACCP [2 K].
+size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
+  const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
+  return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * ell + 2 * c->K);
+}
+
+int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
+             const uint64_t* const* ksk, const uint64_t* add, long long add_stride, uint64_t* out_b,
+             uint64_t* out_a, long long out_stride, char* ws, hipStream_t s) {
+  if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
+  if (batch > kMaxBatchF) return HCK_ERR_ARG;
+  const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
+  const long long n = kN;
+  double* r1 = (double*)ws;
+  double* t2 = r1 + (long long)batch * 2 * ell * n;
+  double* accq = t2 + (long long)batch * beta * ext_l * n;
+  double* accp = accq + (long long)batch * 2 * ell * n;
+  // K1
+  // row kernels: ciphertext index fastest, so the blocks in flight share one prime's twiddles
+  k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, r1, ell, c->dev);
+  HCK_CHECK_LAUNCH();
+  // K2: ModUp, one block per (column pair, digit, ciphertext)
+  k_ks_cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
+                                                       (long long)beta * ext_l * n, (long long)ext_l * n,
+                                                       modup_consts(c, ell, 0), 1, c->dev);
+  HCK_CHECK_LAUNCH();
+  // K3
+  KeyPtrsF kp{};
+  for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
+  k_ks_rows_ip<<<dim3(batch, 16, ext_l), kT, 0, s>>>(d, d_stride, t2, kp, ell, beta, accq, accp, c->dev);
+  HCK_CHECK_LAUNCH();
+  // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
+  double* t4 = r1;
+  k_ks_cols_conv<<<dim3(128, 2, batch), kT, 0, s>>>(accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n,
+                                                    (long long)ell * n, c->d_moddown + ell, 0, c->dev);
+  HCK_CHECK_LAUNCH();
+  // K5
+  k_ks_rows_finish<<<dim3(2 * batch, 16, ell), kT, 0, s>>>(t4, accq, add, add_stride, out_b, out_a, out_stride,
+                                                           ell, c->d_level + ell, c->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+}  // namespace hck

@@ -66,8 +66,11 @@ __device__ __forceinline__ double canon(double x, double p, double pinv) {
   return r;
 }
 
-// a * b mod p for two variables a, b (|a| <= 2^51, 0 <= b < p): the quotient estimate uses
-// b * pinv instead of a precomputed w / p; same bounds as mulc with one extra multiply.
+// a * b mod p for a residue b in [0, p) without a stored companion: the quotient estimate uses
+// fl(b * pinv) (two roundings, relative error <= 1.5 * 2^-52), so for |a| = A p,
+//   |r| <= (0.5 + 0.375 A) p   (p < 2^50),
+// and the FMA stays exact while |a| < 2^53.  Twiddle tables store only w (8 bytes); their
+// companion is recomputed here, halving the table traffic of the NTT passes.
 __device__ __forceinline__ double mulv(double a, double b, double p, double pinv) {
   return mulc(a, b, b * pinv, p);
 }

@@ -15,9 +15,10 @@
 // consecutive words.  Between the passes the limb is kept in HBM as signed-lazy doubles
 // (modarith.hpp), so only the final pass canonicalises.
 //
-// Lazy-reduction bounds (p < 2^50): forward stages reduce the sum operand on even stages only, so
-// values stay below 2p after even and 3p after odd stages (< 2^52, the mulc input bound);
-// inverse stages reduce every sum, values stay below 1.5 p.
+// Lazy-reduction bounds (p < 2^50, mulv error model of modarith.hpp): forward stages reduce the
+// sum operand on even stages only; with B_e, B_o the bounds (in units of p) after even and odd
+// stages, B_e = 1 + 0.375 B_o and B_o = 0.5 + 1.375 B_e, so values stay below 2.45 p and 3.9 p
+// (< 2^52).  Inverse stages reduce every sum: values stay below 2 p.
 #include <hip/hip_runtime.h>
 
 #include "../../include/holmes_ckks.h"
@@ -35,17 +36,17 @@ __device__ __forceinline__ int cidx(int r, int cl) { return (r + (r >> 4)) * 16 
 __device__ __forceinline__ int ridx(int rb, int c) { return rb * 272 + c + (c >> 4); }
 
 template <bool RED>
-__device__ __forceinline__ void ct(double& u, double& v, const TwPair w, double p, double pinv) {
-  const double m = mulc(v, w, p);
+__device__ __forceinline__ void ct(double& u, double& v, const double w, double p, double pinv) {
+  const double m = mulv(v, w, p, pinv);
   const double a = RED ? reduce(u, p, pinv) : u;
   u = a + m;
   v = a - m;
 }
 
-__device__ __forceinline__ void gs(double& u, double& v, const TwPair w, double p, double pinv) {
+__device__ __forceinline__ void gs(double& u, double& v, const double w, double p, double pinv) {
   const double s = u + v, d = u - v;
   u = reduce(s, p, pinv);
-  v = mulc(d, w, p);
+  v = mulv(d, w, p, pinv);
 }
 
 template <Fmt F>
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_cols(const void* __restrict__ 
   const int e = blockIdx.y;
   const int pi = list.prime[e];
   const double p = T.p[pi], pinv = T.pinv[pi];
-  const TwPair* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
+  const double* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
   const long long lo = (long long)list.off[e] * kN;
   const char* s = (const char*)src + ((long long)blockIdx.z * src_stride + lo) * 8;
   char* d = (char*)dst + ((long long)blockIdx.z * dst_stride + lo) * 8;
@@ -84,7 +85,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_cols(const void* __restrict__ 
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (k & h) continue;
-      const TwPair w = tw[(1 << l) + (k >> (4 - l))];
+      const double w = tw[(1 << l) + (k >> (4 - l))];
       if (l & 1) ct<false>(x[k], x[k + h], w, p, pinv);
       else ct<true>(x[k], x[k + h], w, p, pinv);
     }
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_cols(const void* __restrict__ 
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (k & h) continue;
-      const TwPair w = tw[(1 << l) + (j << (l - 4)) + (k >> (8 - l))];
+      const double w = tw[(1 << l) + (j << (l - 4)) + (k >> (8 - l))];
       if (l & 1) ct<false>(x[k], x[k + h], w, p, pinv);
       else ct<true>(x[k], x[k + h], w, p, pinv);
     }
@@ -118,7 +119,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_rows(void* data, long long str
   const int e = blockIdx.y;
   const int pi = list.prime[e];
   const double p = T.p[pi], pinv = T.pinv[pi];
-  const TwPair* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
+  const double* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
   char* base = (char*)data + ((long long)blockIdx.z * stride + (long long)list.off[e] * kN) * 8;
   const int tid = threadIdx.x, j = tid & 15, rb = tid >> 4, b = blockIdx.x * 16 + rb;
   double* row = (double*)base + (long long)b * 256;
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_rows(void* data, long long str
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (k & h) continue;
-      const TwPair w = tw[(1 << l) + (b << (l - 8)) + (k >> (12 - l))];
+      const double w = tw[(1 << l) + (b << (l - 8)) + (k >> (12 - l))];
       if (l & 1) ct<false>(x[k], x[k + h], w, p, pinv);
       else ct<true>(x[k], x[k + h], w, p, pinv);
     }
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(kThreads) void k_fwd_rows(void* data, long long str
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       if (k & h) continue;
-      const TwPair w = tw[(1 << l) + (b << (l - 8)) + (j << (l - 12)) + (k >> (16 - l))];
+      const double w = tw[(1 << l) + (b << (l - 8)) + (j << (l - 12)) + (k >> (16 - l))];
       if (l & 1) ct<false>(x[k], x[k + h], w, p, pinv);
       else ct<true>(x[k], x[k + h], w, p, pinv);
     }
@@ -171,7 +172,7 @@ __global__ __launch_bounds__(kThreads) void k_inv_rows(const void* __restrict__ 
   const int e = blockIdx.y;
   const int pi = list.prime[e];
   const double p = T.p[pi], pinv = T.pinv[pi];
-  const TwPair* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
+  const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   const long long lo = (long long)list.off[e] * kN;
   const char* s = (const char*)src + ((long long)blockIdx.z * src_stride + lo) * 8;
   char* d = (char*)dst + ((long long)blockIdx.z * dst_stride + lo) * 8;
@@ -221,7 +222,7 @@ __global__ __launch_bounds__(kThreads) void k_inv_cols(void* data, long long str
   const int e = blockIdx.y;
   const int pi = list.prime[e];
   const double p = T.p[pi], pinv = T.pinv[pi];
-  const TwPair* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
+  const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   char* base = (char*)data + ((long long)blockIdx.z * stride + (long long)list.off[e] * kN) * 8;
   double* m = (double*)base;
   const int tid = threadIdx.x, cl = tid & 15, j = tid >> 4, c = blockIdx.x * 16 + cl;
