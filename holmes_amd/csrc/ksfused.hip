@@ -53,22 +53,31 @@ __device__ __forceinline__ void gs_bf(double& u, double& v, const double w, doub
 // j + 16k (layout A) or rows 16j + k (layout B).  R is the slot's LDS run of 272 doubles.
 __device__ __forceinline__ int cpad(int r) { return r + (r >> 4); }
 
+// The 16 threads of a slot are 16 consecutive lanes of one wave and R is private to the slot, so
+// an exchange needs only wave-level ordering of its LDS accesses, not a workgroup barrier: waves
+// of the block run through their transforms independently.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ void col_a_to_b(double (&x)[16], double* R, int j) {
 #pragma unroll
   for (int k = 0; k < 16; ++k) R[cpad(j + 16 * k)] = x[k];
-  __syncthreads();
+  wave_sync();
 #pragma unroll
   for (int k = 0; k < 16; ++k) x[k] = R[cpad(16 * j + k)];
-  __syncthreads();
+  wave_sync();
 }
 
 __device__ __forceinline__ void col_b_to_a(double (&x)[16], double* R, int j) {
 #pragma unroll
   for (int k = 0; k < 16; ++k) R[cpad(16 * j + k)] = x[k];
-  __syncthreads();
+  wave_sync();
 #pragma unroll
   for (int k = 0; k < 16; ++k) x[k] = R[cpad(j + 16 * k)];
-  __syncthreads();
+  wave_sync();
 }
 
 // forward stages 0..3 on layout A
@@ -277,12 +286,14 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
                                                      DevTables T) {
   __shared__ double X[16 * 272];              // per-slot exchange runs
   __shared__ double Y[kSrcMax * 2 * kYStride];  // y_s for both columns
+  __shared__ TwPair H[kSrcMax * kMaxPrimes];    // hmod[s][t] of this conversion group
   const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
   const int c0 = blockIdx.x * 2;
   const int y = blockIdx.y;
   const long long z = blockIdx.z;
   const ConvConsts& C = cc_base[y * cc_y];
   const int ns = C.ns, nt = C.nt;
+  for (int q = t; q < ns * nt; q += kT) H[(q / nt) * kMaxPrimes + q % nt] = C.hmod[q / nt][q % nt];
   double* R = X + sigma * 272;
   const double* sbase = src + z * src_zs + y * src_ys + (long long)y * src_off_y * kN;
   double x[16];
@@ -326,11 +337,14 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
     if (act) {
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = 0.0;
-      for (int s = 0; s < ns; ++s) {
-        const TwPair h = C.hmod[s][tg];
-        const double* Yr = Y + (s * 2 + cl) * kYStride;
 #pragma unroll
-        for (int k = 0; k < 16; ++k) x[k] += mulc(Yr[j + 16 * k], h, p);  // |term| <= 0.625 p
+      for (int s = 0; s < kSrcMax; ++s) {
+        if (s < ns) {
+          const TwPair h = H[s * kMaxPrimes + tg];
+          const double* Yr = Y + (s * 2 + cl) * kYStride;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) x[k] += mulc(Yr[j + 16 * k], h, p);  // |term| <= 0.69 p
+        }
       }
 #pragma unroll
       for (int k = 0; k < 16; ++k) x[k] = reduce(x[k], p, pinv);

@@ -36,6 +36,8 @@ __all__ = [
     "homo_mul_i",
     "homo_mul_pt",
     "encode_plaintext",
+    "PackedRaw",
+    "ConstantBundle",
 ]
 
 
@@ -239,3 +241,48 @@ def homo_mul_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
         scaling_factor=float(st.scaling_factor) * float(pt.state.scaling_factor),
     )
     return ct.cipher_like(out, state=state)
+
+
+class PackedRaw:
+    """Raw slot values of one constant (a float/complex vector or a [rows][slots] array)."""
+
+    def __init__(self, values):
+        self.values = values
+
+    def numpy(self) -> np.ndarray:
+        v = self.values
+        if hasattr(v, "detach"):
+            v = v.detach().cpu().numpy()
+        return np.asarray(v)
+
+
+class ConstantBundle:
+    """Named constants encoded on demand (``bundle.plaintext(name, state, slots, context, ...)``,
+    llama3fhe/backend.py:346-356, operators/linear/weight.py:458-469).  ``cache_mode="plain"``
+    keeps each encoded plaintext for reuse; ``"none"`` encodes every call."""
+
+    def __init__(self, vectors: dict, cache_mode: str = "none"):
+        self.vectors = dict(vectors)
+        self.cache_mode = str(cache_mode)
+        self._cache: dict = {}
+
+    def plaintext(self, name: str, state: CipherState, slots: int, context: CKKSContext,
+                  is_ext: bool = False, cache: bool | None = None) -> Plaintext:
+        if is_ext:
+            raise ValueError("extended-basis plaintexts are not supported by this backend")
+        key = (str(name), int(state.cur_limbs), float(state.scaling_factor), int(slots))
+        keep = self.cache_mode in ("plain", "both") if cache is None else bool(cache)
+        hit = self._cache.get(key)
+        if hit is not None:
+            return hit
+        pt = encode_plaintext(self.vectors[str(name)].numpy(), state, int(slots), context)
+        if keep:
+            self._cache[key] = pt
+        return pt
+
+    def cache_info(self) -> dict:
+        total = sum(int(pt.cv[0].numel()) * 8 for pt in self._cache.values())
+        return {"entries": len(self._cache), "total_bytes": total}
+
+    def clear_cache(self) -> None:
+        self._cache.clear()

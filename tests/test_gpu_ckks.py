@@ -101,3 +101,29 @@ def test_align_to_drops_limbs_only(env):
     low = fhe.align_to(ct, ct.state.replace(cur_limbs=9), ctx)
     assert low.state.cur_limbs == 9
     assert np.max(np.abs(client.decrypt(low).real - v)) < TOL
+
+
+def test_easyfhe_context_session_roundtrip():
+    """The llama3fhe/backend.py session surface: create_sim_context, encrypt at a level,
+    plaintext at a level, homo_mul_pt + rescale, decrypt."""
+
+    from holmes_amd import backend
+    from holmes_amd.config import SimulatorConfig
+
+    cfg = SimulatorConfig(maxLevelsRemaining=5, dnum=2)
+    sess = backend.create_sim_context(cfg, input_dim=16, block_out=8, rotations=(3,))
+    assert sess.max_slots == 32768 and sess.context.L == 6
+    rng = np.random.default_rng(11)
+    v = rng.normal(size=sess.max_slots)
+    w = rng.normal(size=sess.max_slots)
+    ct = sess.encrypt(v, level=1)
+    assert sess.level_for_cipher(ct) == 1 and ct.state.cur_limbs == 5
+    pt = sess.plaintext(w, name="model.layers.3.w", level=1)
+    prod = sess.fhe.rescale(sess.fhe.homo_mul_pt(ct, pt, sess.context), sess.context)
+    assert sess.level_for_cipher(prod) == 2
+    out = sess.decrypt(prod)
+    assert np.max(np.abs(out.real - v * w)) < 2.0**-10  # scale 2^40 * 2^40 / q (~2^50) = 2^30
+    rot = sess.decrypt(sess.fhe.homo_rotate(ct, 3, sess.context))
+    assert np.max(np.abs(rot.real - np.roll(v, -3))) < TOL
+    backend.release_if_supported(prod)
+    assert prod.cv == []

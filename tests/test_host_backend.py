@@ -1,0 +1,85 @@
+"""CPU tests of the host-side boundary logic (no GPU): name normalisation, plaintext cache policy,
+default rotation sets, configuration, the prime-chain rule and the encoder."""
+
+import numpy as np
+import pytest
+
+from holmes_amd import backend, encoding
+from holmes_amd.config import SimulatorConfig
+from holmes_amd.params import CKKSContextSpec, ntt_primes
+from oracle import oracle as O
+
+
+def test_constant_names_normalise_layer_and_rank_prefixes():
+    n = backend._normalized_constant_name
+    assert n("model.layers.7.attn.mask") == n("model.layers.31.attn.mask")
+    assert n("t2l.r3.i9.mask") == n("t2l.r0.i1.mask")
+    assert n(("a", ["model.layers.1.x"])) == ("a", ("model.layers.*.x",))
+
+
+def test_plaintext_cache_is_first_fit_and_capped():
+    cache = backend.SessionPlaintextCache(limit_bytes=100, max_source_bytes=60)
+    made = []
+
+    def factory(admit):
+        made.append(admit)
+        return object()
+
+    a = cache.get("a", factory, source_bytes=50)
+    assert cache.get("a", factory, source_bytes=50) is a
+    cache.get("b", factory, source_bytes=60)  # would cross 100: transient, not admitted
+    assert made == [True, False]
+    assert cache.info()["entries"] == 1 and cache.info()["hits"] == 1 and cache.info()["skips"] == 1
+    assert not cache.accepts_source(61)
+    cache.clear()
+    with pytest.raises(RuntimeError):
+        cache.get("c", factory, source_bytes=1)
+
+
+def test_default_rotations_match_reference_rule():
+    # block_out * 2^i for i < log2(input_dim), plus 2^i for i < log2(block_out)
+    assert backend.default_rotations(16, 4) == {4, 8, 16, 32, 1, 2}
+    with pytest.raises(ValueError):
+        backend.default_rotations(12, 4)
+
+
+def test_simulator_config_validation():
+    cfg = SimulatorConfig()
+    cfg.validate()
+    assert cfg.rescale_policy() == "manual"
+    with pytest.raises(ValueError):
+        SimulatorConfig(rescaleTech="BOGUS").rescale_policy()
+
+
+def test_spec_prime_chain_follows_oracle_rule():
+    spec = CKKSContextSpec(depth=23, dnum=3)
+    q, p = spec.prime_chain()
+    assert len(q) == 24 and len(p) == 8 and spec.alpha == 8
+    assert p == O.gen_primes(16, 50, 8)
+    assert q == O.gen_primes(16, 50, 24, exclude=p)
+    assert ntt_primes(16, 50, 3) == O.gen_primes(16, 50, 3)
+    with pytest.raises(ValueError):
+        CKKSContextSpec(dcrt_bits=59).validate()
+
+
+@pytest.mark.parametrize("slots", [32768, 4096])
+def test_encode_decode_roundtrip_and_rotation_group(slots):
+    rng = np.random.default_rng(slots)
+    z = rng.normal(size=slots) + 1j * rng.normal(size=slots)
+    m = encoding.encode(z, 2.0**40, 16, slots)
+    back = encoding.decode(m, 2.0**40, 16, slots)
+    assert np.max(np.abs(back - z)) < 2.0**-30
+    # X -> X^5 on the coefficients rotates the slots left by one
+    n = 1 << 16
+    idx = (np.arange(n) * 5) % (2 * n)
+    m5 = np.zeros(n)
+    wrap = idx >= n
+    m5[idx[~wrap]] = m[~wrap]
+    m5[idx[wrap] - n] = -m[wrap]
+    rot = encoding.decode(m5, 2.0**40, 16, slots)
+    assert np.max(np.abs(rot - np.roll(z, -1))) < 2.0**-30
+
+
+def test_encoder_cap():
+    with pytest.raises(ValueError):
+        encoding.encode(np.full(8, 1e9), 2.0**40, 16, 8)
