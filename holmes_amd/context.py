@@ -287,6 +287,70 @@ class CKKSContext:
                   "hck_rescale")
         return out
 
+    def bsgs_mac(self, babies_c0, babies_c1, pts: torch.Tensor, limbs: int, giants: int,
+                 out: torch.Tensor | None = None) -> torch.Tensor:
+        """Baby-step partial sums res[c][g][i] = sum_b pts[g*nb + b] * baby_b[i][c] (exact residues).
+        babies_c0/c1: one [inputs][>=limbs][N] tensor per baby step (same batch stride)."""
+
+        nb = len(babies_c0)
+        if nb != len(babies_c1) or nb < 1:
+            raise ValueError("one (c0, c1) pair per baby step")
+        ni = int(babies_c0[0].shape[0])
+        stride = babies_c0[0].stride(0)
+        for t in list(babies_c0) + list(babies_c1):
+            self._check_poly(t, limbs, self.N)
+            if t.shape[0] != ni or t.stride(0) != stride:
+                raise ValueError("baby tensors need one shape and batch stride")
+        self._check_poly(pts, limbs, self.N)
+        if pts.shape[0] != giants * nb:
+            raise ValueError(f"expected {giants * nb} plaintext rows, got {pts.shape[0]}")
+        if out is None:
+            out = self.empty(2, giants, ni, limbs, self.N)
+        if tuple(out.shape) != (2, giants, ni, limbs, self.N) or not out.is_contiguous():
+            raise ValueError("out must be a contiguous [2][giants][inputs][limbs][N] tensor")
+        nat.check(nat.lib().hck_bsgs_mac(self._h, limbs, ni, nb, giants,
+                                         nat.ptr_array([t.data_ptr() for t in babies_c0]),
+                                         nat.ptr_array([t.data_ptr() for t in babies_c1]), stride,
+                                         pts.data_ptr(), pts.stride(0), out.data_ptr(),
+                                         _stream_ptr(self.device)), "hck_bsgs_mac")
+        return out
+
+    def pack_diagonals(self, weight: torch.Tensor, *, lanes: int, lane_shift: int, baby_steps: int,
+                       giant_base: int, giant_count: int) -> torch.Tensor:
+        """Diagonal rows [giant_count * baby_steps][N/2] (float64) of one BSGS chunk."""
+
+        if weight.dtype != torch.float64 or weight.dim() != 2 or weight.shape[0] != weight.shape[1]:
+            raise ValueError("weight must be a square float64 matrix")
+        weight = weight.contiguous()
+        out = torch.empty((giant_count * baby_steps, self.max_slots), dtype=torch.float64, device=self.device)
+        nat.check(nat.lib().hck_pack_diagonals(self._h, weight.data_ptr(), int(weight.shape[0]), int(lanes),
+                                               int(lane_shift), int(baby_steps), int(giant_base),
+                                               int(giant_count), out.data_ptr(), _stream_ptr(self.device)),
+                  "hck_pack_diagonals")
+        return out
+
+    def encode_real(self, values: torch.Tensor, scale: float, limbs: int,
+                    out: torch.Tensor | None = None, check: bool = True) -> torch.Tensor:
+        """Encode real slot rows [rows][N/2] (float64, device) into NTT-domain residues
+        [rows][limbs][N].  With ``check`` the overflow flags are read back (one host sync)."""
+
+        if values.dtype != torch.float64 or values.dim() != 2 or values.shape[1] != self.max_slots:
+            raise ValueError("values must be [rows][N/2] float64")
+        values = values.contiguous()
+        rows = int(values.shape[0])
+        if out is None:
+            out = self.empty(rows, limbs, self.N)
+        self._check_poly(out, limbs, self.N)
+        L = nat.lib()
+        ws = torch.empty(L.hck_encode_workspace_bytes(self._h, rows), dtype=torch.uint8, device=self.device)
+        flags = torch.zeros(max(rows, 1), dtype=torch.int32, device=self.device)
+        nat.check(L.hck_encode_real(self._h, values.data_ptr(), rows, float(scale), int(limbs),
+                                    nat.int_array(range(limbs)), out.data_ptr(), out.stride(0), ws.data_ptr(),
+                                    ws.numel(), flags.data_ptr(), _stream_ptr(self.device)), "hck_encode_real")
+        if check and bool(flags.any().item()):
+            raise ValueError("encoded coefficient reached 2^52: lower the scale or the value range")
+        return out
+
     def _check_key(self, k: torch.Tensor) -> None:
         shape = (2, self.beta_max, self.L + self.K, self.N)
         if k.dtype != torch.uint64 or tuple(k.shape) != shape or not k.is_contiguous():

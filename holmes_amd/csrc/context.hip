@@ -7,6 +7,7 @@
 // companion fl(w/p).
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstring>
 #include <new>
 #include <vector>
@@ -142,6 +143,29 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     zeta4[i] = pair_of(powmod(psi, n / 2, q), q);
   }
 
+  // encoder roots: stage of half-width h (1 <= h < N/2) at [h - 1, 2h - 1), entry j =
+  // exp(2 pi i idx / M) with idx = (lenq - (5^j mod lenq)) * (M / lenq), lenq = 8h, M = 2N
+  const size_t nslots = n / 2;
+  std::vector<double> etr(nslots, 0.0), eti(nslots, 0.0);
+  {
+    // separate cos / sin calls (a fused sincos() differs from them in the last bit for some
+    // arguments); the volatile pointers keep any compiler from fusing them
+    double (*volatile vcos)(double) = std::cos;
+    double (*volatile vsin)(double) = std::sin;
+    const u64 M = 2 * (u64)n;
+    for (u64 h = 1; h < nslots; h <<= 1) {
+      const u64 lenq = 8 * h, gap = M / lenq;
+      u64 r = 1;
+      for (u64 j = 0; j < h; ++j) {
+        const u64 idx = (lenq - (r % lenq)) * gap;
+        const double ang = 2.0 * M_PI * (double)idx / (double)M;
+        etr[h - 1 + j] = vcos(ang);
+        eti[h - 1 + j] = vsin(ang);
+        r = (r * 5) % M;
+      }
+    }
+  }
+
   // key-switching constants for every level ell in [1, L] and digit j
   c->h_modup.assign((size_t)(num_q + 1) * c->beta_max, hck::ConvConsts{});
   c->h_moddown.assign((size_t)(num_q + 1), hck::ConvConsts{});
@@ -186,6 +210,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   const size_t o_md = off; off = align(off + c->h_moddown.size() * sizeof(hck::ConvConsts));
   const size_t o_lv = off; off = align(off + c->h_level.size() * sizeof(hck::LevelConsts));
   const size_t o_pu = off; off = align(off + np * sizeof(u64));
+  const size_t o_etr = off; off = align(off + nslots * sizeof(double));
+  const size_t o_eti = off; off = align(off + nslots * sizeof(double));
   void* blk = nullptr;
   hipError_t e = hipMalloc(&blk, off);
   if (e != hipSuccess) { delete c; return (int)e; }
@@ -202,6 +228,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       {o_md, c->h_moddown.data(), c->h_moddown.size() * sizeof(hck::ConvConsts)},
       {o_lv, c->h_level.data(), c->h_level.size() * sizeof(hck::LevelConsts)},
       {o_pu, P.data(), np * sizeof(u64)},
+      {o_etr, etr.data(), nslots * sizeof(double)},
+      {o_eti, eti.data(), nslots * sizeof(double)},
   };
   for (const Up& u : ups) {
     e = hipMemcpy(base + u.o, u.src, u.bytes, hipMemcpyHostToDevice);
@@ -220,6 +248,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->d_moddown = (hck::ConvConsts*)(base + o_md);
   c->d_level = (hck::LevelConsts*)(base + o_lv);
   c->d_primes_u64 = (const u64*)(base + o_pu);
+  c->d_enc_twr = (const double*)(base + o_etr);
+  c->d_enc_twi = (const double*)(base + o_eti);
   *out = c;
   return HCK_OK;
 }

@@ -52,6 +52,8 @@ struct hck_context {
   hck::ConvConsts* d_moddown = nullptr; // [L + 1]
   hck::LevelConsts* d_level = nullptr;  // [L + 1]
   const uint64_t* d_primes_u64 = nullptr; // [np]
+  const double* d_enc_twr = nullptr;      // [N/2]: special-IFFT roots, stage h at [h-1, 2h-1)
+  const double* d_enc_twi = nullptr;
   std::vector<hck::ConvConsts> h_modup, h_moddown;
   std::vector<hck::LevelConsts> h_level;
   int beta_max;

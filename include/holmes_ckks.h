@@ -19,6 +19,11 @@
  *   hck_rescale            fhe.rescale / F.cv_rescale_one_level (operator.py:387-394)
  *   hck_poly_op            F.cv_add / cv_sub / cv_neg / cv_mul / cv_mul_by_monomial (report.py:26-48)
  *   hck_poly_from_signed   the encoder's signed-integer reduction (holmes_encode.cu:108-111,133-159)
+ *   hck_bsgs_mac           holmes_mac_multi, the multi-input BSGS baby-step MAC (holmes_mac.cu:359-402)
+ *   hck_pack_diagonals     the BSGS weight diagonal packers (llama3fhe/operators/linear/weight.py:122-154,
+ *                          gpu_packer.py:156-198)
+ *   hck_encode_real        EasyFHE encode: special IFFT (cv_pre_encode_stage1) + holmes_encode_stage2
+ *                          (round, reduce, NTT; holmes_encode.cu:240-285)
  */
 #ifndef HOLMES_CKKS_H
 #define HOLMES_CKKS_H
@@ -113,6 +118,30 @@ int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const uint64_t* a
 int hck_poly_from_signed(const hck_context* ctx, const int64_t* in, uint64_t* out, int polys,
                          int64_t in_stride, int64_t out_stride, int limbs, const int* prime_idx,
                          void* stream);
+
+/* BSGS baby-step MAC over `inputs` ciphertexts and `giants` giant groups:
+ *   res[c][g][i][l][n] = sum_{b < babies} pts[g * babies + b][l][n] * baby_b[i][c][l][n]  (mod q_l)
+ * baby_c0[b] / baby_c1[b] (host arrays of `babies` device pointers): components of baby rotation b,
+ * [inputs][>= limbs][N] with batch stride baby_stride; pts rows [giants * babies][>= limbs][N] with
+ * row stride pt_stride; res [2][giants][inputs][limbs][N] contiguous. */
+int hck_bsgs_mac(const hck_context* ctx, int limbs, int inputs, int babies, int giants,
+                 const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, int64_t baby_stride,
+                 const uint64_t* pts, int64_t pt_stride, uint64_t* res, void* stream);
+
+/* Diagonal rows of one BSGS chunk from a row-major float64 weight [dimension][dimension]:
+ * out[gr * baby_steps + b][s] = W[(f - (giant_base + gr) baby_steps) mod D][(f + b + lane_shift lane) mod D],
+ * f = s / lanes, lane = s % lanes, s < N/2. */
+int hck_pack_diagonals(const hck_context* ctx, const double* weight, int dimension, int lanes,
+                       int lane_shift, int baby_steps, int giant_base, int giant_count, double* out,
+                       void* stream);
+
+/* Encode `rows` real slot vectors (float64 [rows][N/2]) at `scale` into NTT-domain residues
+ * out[row][l] (row stride out_row_stride words, limb l modulo prime prime_idx[l]).  A coefficient
+ * of magnitude >= 2^52 sets overflow_flags[row] (device int array, caller-zeroed). */
+size_t hck_encode_workspace_bytes(const hck_context* ctx, int rows);
+int hck_encode_real(const hck_context* ctx, const double* values, int rows, double scale, int limbs,
+                    const int* prime_idx, uint64_t* out, int64_t out_row_stride, void* workspace,
+                    size_t workspace_bytes, int* overflow_flags, void* stream);
 
 #ifdef __cplusplus
 }

@@ -486,3 +486,124 @@ int or_num_threads(void) {
   return 1;
 #endif
 }
+
+/* ------------------------------------------------------------------ CKKS encode (stage 1 + 2)
+ * Special inverse FFT of the slot vector over the rotation group (the textbook CKKS encoder; the
+ * reference's encode stage 1 feeds holmes_encode.cu:108-111, whose stage 2 rounds
+ * Re(w_n) * scale into coefficient n and Im(w_n) * scale into coefficient n + slots).  Every
+ * floating-point operation is written out so that the GPU encoder can perform the identical IEEE
+ * sequence (this file is compiled with -ffp-contract=off):
+ *   for lenh = n/2, n/4, ..., 1:  for each block i and j < lenh:
+ *     u = v[i+j] + v[i+j+lenh];  d = v[i+j] - v[i+j+lenh];  v[i+j] = u;  v[i+j+lenh] = d * zeta
+ *     zeta = exp(2 pi i idx / M),  idx = (lenq - (5^j mod lenq)) * (M / lenq),  lenq = 8 lenh
+ *   complex product (a + bi)(c + di) = (a c - b d) + (a d + b c) i
+ *   then w[k] = v[brv(k)] * (1/n);  coefficient = round-half-away(w * scale).
+ * n = slots = N/2 (full packing). */
+#include <math.h>
+
+/* round half away from zero (llround semantics, holmes_encode.cu:133-159), via trunc */
+static double round_away(double x) {
+  double r = trunc(x);
+  const double d = x - r;
+  if (d >= 0.5) r += 1.0;
+  else if (d <= -0.5) r -= 1.0;
+  return r;
+}
+
+/* cos and sin are called through volatile pointers so that no compiler fuses them into sincos(),
+ * whose results differ from separate cos/sin calls in the last bit for some arguments. */
+static double (*volatile or_cos)(double) = cos;
+static double (*volatile or_sin)(double) = sin;
+
+void or_encode_twiddles(int log_n, double* tw_re, double* tw_im) {
+  /* concatenated per-stage tables: stage with half-width h occupies [h - 1, 2h - 1) */
+  const u64 n = (u64)1 << (log_n - 1), M = (u64)4 << (log_n - 1);
+  for (u64 h = 1; h < n; h <<= 1) {
+    const u64 lenq = 8 * h, gap = M / lenq;
+    u64 r = 1;  /* 5^j mod M, reduced mod lenq below */
+    for (u64 j = 0; j < h; ++j) {
+      const u64 idx = (lenq - (r % lenq)) * gap;
+      const double ang = 2.0 * M_PI * (double)idx / (double)M;
+      tw_re[h - 1 + j] = or_cos(ang);
+      tw_im[h - 1 + j] = or_sin(ang);
+      r = (r * 5) % M;
+    }
+  }
+}
+
+void or_special_ifft(int log_n, double* re, double* im, const double* tw_re, const double* tw_im) {
+  const u64 n = (u64)1 << (log_n - 1);
+  for (u64 h = n >> 1; h >= 1; h >>= 1) {
+    for (u64 i = 0; i < n; i += 2 * h) {
+      for (u64 j = 0; j < h; ++j) {
+        const double ar = re[i + j], ai = im[i + j], br = re[i + j + h], bi = im[i + j + h];
+        const double ur = ar + br, ui = ai + bi;
+        const double dr = ar - br, di = ai - bi;
+        const double wr = tw_re[h - 1 + j], wi = tw_im[h - 1 + j];
+        re[i + j] = ur;
+        im[i + j] = ui;
+        re[i + j + h] = dr * wr - di * wi;
+        im[i + j + h] = dr * wi + di * wr;
+      }
+    }
+    if (h == 1) break;
+  }
+}
+
+/* values: real slot vector (n doubles).  out: [limbs][N] residues (NTT domain when ntt != 0),
+ * limb l modulo the oracle context's prime prime_idx[l].  Returns -1 if a rounded coefficient is
+ * 2^52 or more in magnitude (outside the exact-double range the GPU encoder supports), else 0. */
+int or_encode_real(const or_ctx* c, const double* values, double scale, int limbs, const int* prime_idx,
+                   int ntt, u64* out) {
+  const int log_n = c->log_n;
+  const u64 n = c->n >> 1, N = c->n;
+  double* re = (double*)malloc(sizeof(double) * n);
+  double* im = (double*)calloc(n, sizeof(double));
+  double* twr = (double*)malloc(sizeof(double) * n);
+  double* twi = (double*)malloc(sizeof(double) * n);
+  double* coef = (double*)malloc(sizeof(double) * N);
+  memcpy(re, values, sizeof(double) * n);
+  or_encode_twiddles(log_n, twr, twi);
+  or_special_ifft(log_n, re, im, twr, twi);
+  const double inv_n = 1.0 / (double)n;
+  int rc = 0;
+  for (u64 k = 0; k < n; ++k) {
+    const u64 s = bitrev(k, log_n - 1);
+    const double wr = re[s] * inv_n, wi = im[s] * inv_n;
+    coef[k] = round_away(wr * scale);
+    coef[k + n] = round_away(wi * scale);
+  }
+  for (u64 k = 0; k < N; ++k) if (fabs(coef[k]) >= 4503599627370496.0) rc = -1;
+  for (int l = 0; l < limbs; ++l) {
+    const u64 q = c->primes[prime_idx[l]];
+    u64* o = out + (size_t)l * N;
+    for (u64 k = 0; k < N; ++k) {
+      const double v = coef[k];
+      const u64 mag = (u64)fabs(v) % q;
+      o[k] = v < 0 ? (mag ? q - mag : 0) : mag;
+    }
+    if (ntt) ntt_f(c, o, prime_idx[l]);
+  }
+  free(re); free(im); free(twr); free(twi); free(coef);
+  return rc;
+}
+
+/* Diagonal packing of the BSGS weight rows (llama3fhe/operators/linear/weight.py:122-154):
+ * row (g, b) of a chunk, g = giant_base + gr, gr < giant_count, b < baby_steps:
+ *   row[s] = W[(f - g B) mod D][(f + b + lane_shift * lane) mod D],  f = s / lanes, lane = s % lanes. */
+void or_pack_diagonals(const double* W, int D, int lanes, int lane_shift, int baby_steps, int giant_base,
+                       int giant_count, int slots, double* out) {
+  for (int gr = 0; gr < giant_count; ++gr) {
+    const int g = giant_base + gr;
+    for (int b = 0; b < baby_steps; ++b) {
+      double* row = out + ((size_t)gr * baby_steps + b) * slots;
+      for (int s = 0; s < slots; ++s) {
+        const long f = s / lanes, lane = s % lanes;
+        long o = (f - (long)g * baby_steps) % D;
+        if (o < 0) o += D;
+        const long in = (f + b + (long)lane_shift * lane) % D;
+        row[s] = W[(size_t)o * D + in];
+      }
+    }
+  }
+}

@@ -21,6 +21,7 @@ _u64p = ctypes.POINTER(ctypes.c_uint64)
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _i32p = ctypes.POINTER(ctypes.c_int)
 _vp = ctypes.c_void_p
+_f64p = ctypes.POINTER(ctypes.c_double)
 _lib = None
 
 
@@ -62,6 +63,10 @@ def lib():
         "or_bsgs_mac": (None, [_vp, i, i, i, _u64p, _u64p, _u64p]),
         "or_mul_limbs": (None, [_vp, i, _u64p, _u64p, _u64p]),
         "or_num_threads": (i, []),
+        "or_encode_twiddles": (None, [i, _f64p, _f64p]),
+        "or_special_ifft": (None, [i, _f64p, _f64p, _f64p, _f64p]),
+        "or_encode_real": (i, [_vp, _f64p, ctypes.c_double, i, _i32p, i, _u64p]),
+        "or_pack_diagonals": (None, [_f64p, i, i, i, i, i, i, i, _f64p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -79,6 +84,8 @@ def _p(a: np.ndarray):
         return a.ctypes.data_as(_i64p)
     if a.dtype == np.int32:
         return a.ctypes.data_as(_i32p)
+    if a.dtype == np.float64:
+        return a.ctypes.data_as(_f64p)
     raise TypeError(a.dtype)
 
 
@@ -231,12 +238,39 @@ class OracleContext:
         lib().or_make_ksk(self._h, _p(s_from), _p(s_to), _p(a), _p(e), _p(out))
         return out
 
+    def encode_real(self, values: np.ndarray, scale: float, prime_idx, ntt: bool = True):
+        """Encode one real slot vector (N/2 values): (residues [limbs][N], ok)."""
+
+        values = np.ascontiguousarray(values, dtype=np.float64)
+        idx = np.ascontiguousarray(np.asarray(prime_idx, dtype=np.int32))
+        out = np.zeros((idx.size, self.n), dtype=np.uint64)
+        rc = lib().or_encode_real(self._h, _p(values), float(scale), int(idx.size), _p(idx), int(bool(ntt)), _p(out))
+        return out, rc == 0
+
     def bsgs_mac(self, limbs: int, nb: int, G: int, pt: np.ndarray, baby: np.ndarray) -> np.ndarray:
         pt = np.ascontiguousarray(pt, dtype=np.uint64)
         baby = np.ascontiguousarray(baby, dtype=np.uint64)
         res = np.zeros((2, G, limbs, self.n), dtype=np.uint64)
         lib().or_bsgs_mac(self._h, int(limbs), int(nb), int(G), _p(pt), _p(baby), _p(res))
         return res
+
+
+def encode_twiddles(log_n: int):
+    n = 1 << (log_n - 1)
+    re = np.zeros(n, dtype=np.float64)
+    im = np.zeros(n, dtype=np.float64)
+    lib().or_encode_twiddles(int(log_n), _p(re), _p(im))
+    return re, im
+
+
+def pack_diagonals(W: np.ndarray, lanes: int, lane_shift: int, baby_steps: int, giant_base: int,
+                   giant_count: int, slots: int) -> np.ndarray:
+    W = np.ascontiguousarray(W, dtype=np.float64)
+    D = int(W.shape[0])
+    out = np.zeros((giant_count * baby_steps, slots), dtype=np.float64)
+    lib().or_pack_diagonals(_p(W), D, int(lanes), int(lane_shift), int(baby_steps), int(giant_base),
+                            int(giant_count), int(slots), _p(out))
+    return out
 
 
 def num_threads() -> int:
