@@ -1,0 +1,361 @@
+"""Diagonal (BSGS) linear layers on the GPU: plan, weight, operator.
+
+Restates the schedule of llama3fhe/operators/linear/config.py:47-380 (``LinearOperatorConfig``,
+``LinearPlan``, ``LinearChunk``, ``linear_rotations``) and the execution of
+llama3fhe/operators/linear/operator.py:203-467 (chunk loop, per-chunk giant steps, chunk-base
+alignment rotation, accumulate, final rescale), re-organised for one GPU:
+
+* the baby rotations of all inputs are computed once (one batched rotation per baby offset:
+  every input shares that offset's key) and kept in HBM;
+* a chunk's diagonals are packed and encoded on the GPU (``hck_pack_diagonals``,
+  ``hck_encode_real``) and multiplied into every input at once by ``hck_bsgs_mac``
+  (partial sums ``[2][G][inputs]``);
+* each Horner giant step rotates all inputs' accumulators in one batched key switch with the
+  shared giant key, as the batched giant step of bench/cmp/holmes_multi_mac.py:180-186.
+
+Residues are exact: the result equals the oracle composition of the same rotations, MACs and
+rescale bit for bit (tests/test_gpu_linear.py).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from . import _native as nat
+from .context import Cipher, CipherState, CKKSContext
+
+_HOIST_STRATEGIES = {"normal", "ext_normal", "ext_double_hoist"}
+
+
+@dataclass(frozen=True)
+class LinearChunk:
+    index: int
+    giant_base: int
+    giant_count: int
+
+    @property
+    def name(self) -> str:
+        return f"chunk.{int(self.index)}"
+
+
+@dataclass(frozen=True)
+class BabyBlock:
+    start: int
+    width: int
+
+
+@dataclass(frozen=True)
+class LinearPlan:
+    """Physical BSGS schedule of one square block (llama3fhe/operators/linear/config.py:172-331)."""
+
+    dimension: int
+    token_lanes: int
+    baby_steps: int
+    baby_anchor_step: int
+    max_plaintext_rows: int
+    lane_shift: int = 0
+
+    def __post_init__(self) -> None:
+        if int(self.dimension) <= 0 or int(self.token_lanes) <= 0 or int(self.baby_steps) <= 0:
+            raise ValueError("dimension, token_lanes and baby_steps must be positive.")
+        if int(self.lane_shift) < 0:
+            raise ValueError("lane_shift must be zero or positive.")
+        if int(self.lane_shift) and int(self.lane_shift) * int(self.token_lanes) != int(self.dimension):
+            raise ValueError("shifted-lane packing requires lane_shift * token_lanes == dimension.")
+        if int(self.diagonals) % int(self.baby_steps):
+            raise ValueError(f"baby_steps={self.baby_steps} must divide diagonals={self.diagonals}.")
+        if int(self.baby_anchor_step) in (0, 1) or int(self.baby_anchor_step) < -1:
+            raise ValueError("baby_anchor_step must be at least two or -1.")
+        if int(self.max_plaintext_rows) < int(self.baby_steps):
+            raise ValueError("max_plaintext_rows must hold one baby-step group.")
+
+    @property
+    def shifted_lanes(self) -> bool:
+        return bool(int(self.lane_shift))
+
+    @property
+    def diagonals(self) -> int:
+        return int(self.lane_shift) if self.shifted_lanes else int(self.dimension)
+
+    @property
+    def giant_steps(self) -> int:
+        return int(self.diagonals) // int(self.baby_steps)
+
+    @property
+    def chunk_giants(self) -> int:
+        return max(1, int(self.max_plaintext_rows) // int(self.baby_steps))
+
+    @property
+    def giant_offset(self) -> int:
+        return int(self.baby_steps) * int(self.token_lanes)
+
+    @property
+    def baby_offsets(self) -> tuple[int, ...]:
+        return tuple(b * int(self.token_lanes) for b in range(int(self.baby_steps)))
+
+    @property
+    def anchor_enabled(self) -> bool:
+        return bool(int(self.baby_anchor_step) >= 2 and int(self.baby_steps) > int(self.baby_anchor_step))
+
+    @property
+    def baby_blocks(self) -> tuple[BabyBlock, ...]:
+        width = int(self.baby_anchor_step) if self.anchor_enabled else int(self.baby_steps)
+        return tuple(BabyBlock(start=s, width=min(width, int(self.baby_steps) - s))
+                     for s in range(0, int(self.baby_steps), width))
+
+    @property
+    def baby_rotation_count(self) -> int:
+        return max(0, int(self.baby_steps) - 1)
+
+    @property
+    def baby_key_offsets(self) -> tuple[int, ...]:
+        width = int(self.baby_blocks[0].width)
+        offsets = {s * int(self.token_lanes) for s in range(1, width)}
+        if len(self.baby_blocks) > 1:
+            offsets.add(int(self.baby_anchor_step) * int(self.token_lanes))
+        return tuple(sorted(offsets))
+
+    @property
+    def fold_offsets(self) -> tuple[int, ...]:
+        if not self.shifted_lanes:
+            return ()
+        return tuple(1 << i for i in range(int(self.token_lanes).bit_length() - 1))
+
+    @property
+    def lane_expand_offsets(self) -> tuple[int, ...]:
+        if not self.shifted_lanes:
+            return ()
+        return tuple((int(self.dimension) - 1) * lane for lane in range(1, int(self.token_lanes)))
+
+    @property
+    def chunks(self) -> tuple[LinearChunk, ...]:
+        return tuple(
+            LinearChunk(index=i, giant_base=base, giant_count=min(self.chunk_giants, self.giant_steps - base))
+            for i, base in enumerate(range(0, self.giant_steps, self.chunk_giants))
+        )
+
+    @property
+    def chunk_sizes(self) -> tuple[int, ...]:
+        return tuple(c.giant_count for c in self.chunks)
+
+    @property
+    def plaintext_chunks(self) -> int:
+        return len(self.chunks)
+
+    @property
+    def cache_key(self) -> tuple[int, ...]:
+        return (int(self.dimension), int(self.token_lanes), int(self.baby_steps), int(self.max_plaintext_rows),
+                int(self.lane_shift))
+
+
+@dataclass(frozen=True)
+class LinearOperatorConfig:
+    """Schedule knobs of one linear (llama3fhe/operators/linear/config.py:47-117)."""
+
+    baby_steps: int = 32
+    baby_anchor_step: int = 32
+    max_plaintext_rows: int = 512
+    reuse_baby_rotations: bool = True
+    hoist_strategy: str = "normal"
+    lane_shift: int = 0
+
+    def __post_init__(self) -> None:
+        if int(self.baby_steps) <= 0:
+            raise ValueError("baby_steps must be positive.")
+        if int(self.baby_anchor_step) in (0, 1) or int(self.baby_anchor_step) < -1:
+            raise ValueError("baby_anchor_step must be at least two or -1.")
+        if int(self.max_plaintext_rows) < int(self.baby_steps):
+            raise ValueError("max_plaintext_rows must hold one baby-step group.")
+        if str(self.hoist_strategy).lower() not in _HOIST_STRATEGIES:
+            raise ValueError("hoist_strategy must be 'normal', 'ext_normal', or 'ext_double_hoist'.")
+
+    def plan(self, *, dimension: int, token_lanes: int) -> LinearPlan:
+        return LinearPlan(dimension=int(dimension), token_lanes=int(token_lanes), baby_steps=int(self.baby_steps),
+                          baby_anchor_step=int(self.baby_anchor_step),
+                          max_plaintext_rows=int(self.max_plaintext_rows), lane_shift=int(self.lane_shift))
+
+
+def linear_rotations(*, dimension: int, token_lanes: int, slots: int | None = None,
+                     include_conjugation: bool = False,
+                     operator_config: LinearOperatorConfig | None = None) -> tuple[int, ...]:
+    """Evaluation-key union of one schedule (llama3fhe/operators/linear/config.py:333-380)."""
+
+    cfg = LinearOperatorConfig() if operator_config is None else operator_config
+    plan = cfg.plan(dimension=int(dimension), token_lanes=int(token_lanes))
+    rot = set(plan.baby_key_offsets)
+    max_chunk = max(c.giant_count for c in plan.chunks)
+    if max_chunk > 1:
+        if str(cfg.hoist_strategy).lower() == "ext_double_hoist":
+            rot.update(s * plan.giant_offset for s in range(1, int(max_chunk)))
+        else:
+            rot.add(plan.giant_offset)
+    rot.update(int(c.giant_base) * plan.giant_offset for c in plan.chunks if int(c.giant_base))
+    rot.update(plan.fold_offsets)
+    rot.update(plan.lane_expand_offsets)
+    if include_conjugation:
+        if slots is None:
+            raise ValueError("slots are required when conjugation is requested.")
+        rot.add(4 * int(slots) - 1)
+    return tuple(sorted(int(v) for v in rot if int(v)))
+
+
+def bsgs_rotations(plan: LinearPlan) -> tuple[int, ...]:
+    """Keys this GPU schedule uses: every baby offset, the giant offset, the chunk bases."""
+
+    rot = {o for o in plan.baby_offsets if o}
+    if max(plan.chunk_sizes) > 1:
+        rot.add(plan.giant_offset)
+    rot.update(int(c.giant_base) * plan.giant_offset for c in plan.chunks if int(c.giant_base))
+    return tuple(sorted(rot))
+
+
+class LinearWeight:
+    """A square weight held on the device; packs and encodes one chunk's diagonals on demand."""
+
+    def __init__(self, weight: np.ndarray, *, crypto_context: CKKSContext):
+        w = np.asarray(weight)
+        if w.ndim != 2 or w.shape[0] != w.shape[1]:
+            raise ValueError("LinearWeight expects a square matrix.")
+        self.crypto_context = crypto_context
+        self.dimension = int(w.shape[0])
+        self._w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float64)).to(crypto_context.device)
+        self._closed = False
+
+    @property
+    def closed(self) -> bool:
+        return self._closed
+
+    def plaintext(self, plan: LinearPlan, chunk: LinearChunk, *, limbs: int, scale: float) -> torch.Tensor:
+        """Encoded diagonals [giant_count * baby_steps][limbs][N] of ``chunk`` (NTT domain)."""
+
+        if self._closed:
+            raise RuntimeError("linear weight is closed")
+        ctx = self.crypto_context
+        rows = ctx.pack_diagonals(self._w, lanes=plan.token_lanes, lane_shift=plan.lane_shift,
+                                  baby_steps=plan.baby_steps, giant_base=chunk.giant_base,
+                                  giant_count=chunk.giant_count)
+        return ctx.encode_real(rows, scale, limbs)
+
+    def close(self) -> None:
+        self._w = None
+        self._closed = True
+
+
+def _stack(ciphers) -> tuple[torch.Tensor, torch.Tensor, CipherState]:
+    ciphers = tuple(ciphers)
+    states = {(int(c.state.cur_limbs), int(c.state.scale_degree), float(c.state.scaling_factor)) for c in ciphers}
+    if len(states) != 1:
+        raise ValueError("linear inputs must enter at one common level and scale.")
+    limbs = ciphers[0].state.cur_limbs
+    c0 = torch.cat([c.cv[0][:, :limbs] for c in ciphers], 0).contiguous()
+    c1 = torch.cat([c.cv[1][:, :limbs] for c in ciphers], 0).contiguous()
+    return c0, c1, ciphers[0].state
+
+
+class LinearOperator:
+    """A reusable BSGS schedule over the ``token_lanes`` feature-major layout."""
+
+    def __init__(self, *, crypto_context, token_lanes: int, config: LinearOperatorConfig | None = None):
+        self.crypto_context = crypto_context
+        self.token_lanes = int(token_lanes)
+        if self.token_lanes <= 0:
+            raise ValueError("token_lanes must be positive.")
+        self.config = LinearOperatorConfig() if config is None else config
+        if int(self.config.lane_shift):
+            raise NotImplementedError("shifted-lane packing is not built in this backend yet")
+        self._closed = False
+
+    @property
+    def closed(self) -> bool:
+        return self._closed
+
+    def plan(self, dimension: int) -> LinearPlan:
+        return self.config.plan(dimension=int(dimension), token_lanes=self.token_lanes)
+
+    def _ctx(self) -> CKKSContext:
+        cc = self.crypto_context
+        return getattr(cc, "context", cc)
+
+    def _rotate_all(self, c0, c1, rotation: int, limbs: int):
+        ctx = self._ctx()
+        g = ctx.galois_element(rotation)
+        return ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g))
+
+    def apply(self, input_ciphers, weight: LinearWeight, *, chunk_indices=None, rescale: bool = True,
+              weight_scale: float | None = None):
+        """BSGS projection of every input; returns (outputs, stage_seconds).
+
+        Weights are encoded at ``weight_scale`` (default: the prime the final rescale divides by,
+        so the output returns to the input scale)."""
+
+        if self._closed:
+            raise RuntimeError("linear operator is closed.")
+        inputs = tuple(input_ciphers)
+        if not inputs:
+            return (), {}
+        if weight.closed:
+            raise RuntimeError("cannot apply a closed linear weight.")
+        ctx = self._ctx()
+        plan = self.plan(weight.dimension)
+        chunks = plan.chunks if chunk_indices is None else tuple(plan.chunks[int(i)] for i in chunk_indices)
+        x0, x1, state = _stack(inputs)
+        limbs = int(state.cur_limbs)
+        if rescale and limbs < 2:
+            raise ValueError("rescale needs at least two limbs")
+        wscale = float(ctx.rescale_divisor_at(limbs)) if weight_scale is None else float(weight_scale)
+        idx = ctx.q_prime_idx(limbs)
+        # baby rotations, each batched over all inputs with that offset's key
+        babies0, babies1 = [x0], [x1]
+        for off in plan.baby_offsets[1:]:
+            b0, b1 = self._rotate_all(x0, x1, off, limbs)
+            babies0.append(b0)
+            babies1.append(b1)
+        total0 = total1 = None
+        for chunk in chunks:
+            pts = weight.plaintext(plan, chunk, limbs=limbs, scale=wscale)
+            part = ctx.bsgs_mac(babies0, babies1, pts, limbs, int(chunk.giant_count))  # [2][G][I][l][N]
+            del pts
+            acc0, acc1 = part[0, -1], part[1, -1]
+            for g in range(int(chunk.giant_count) - 2, -1, -1):
+                r0, r1 = self._rotate_all(acc0, acc1, plan.giant_offset, limbs)
+                ctx.poly_op(nat.HCK_OP_ADD, r0, r0, part[0, g], prime_idx=idx)
+                ctx.poly_op(nat.HCK_OP_ADD, r1, r1, part[1, g], prime_idx=idx)
+                acc0, acc1 = r0, r1
+            if int(chunk.giant_base):
+                acc0, acc1 = self._rotate_all(acc0, acc1, int(chunk.giant_base) * plan.giant_offset, limbs)
+            if total0 is None:
+                total0, total1 = acc0.clone(), acc1.clone()
+            else:
+                ctx.poly_op(nat.HCK_OP_ADD, total0, total0, acc0, prime_idx=idx)
+                ctx.poly_op(nat.HCK_OP_ADD, total1, total1, acc1, prime_idx=idx)
+            del part
+        out_state = state.replace(scale_degree=int(state.scale_degree) + 1,
+                                  scaling_factor=float(state.scaling_factor) * wscale)
+        slots = inputs[0].slots
+        if rescale:
+            both = ctx.rescale_raw(torch.cat([total0, total1], 0), limbs)
+            n_in = total0.shape[0]
+            total0, total1 = both[:n_in], both[n_in:]
+            out_state = out_state.replace(cur_limbs=limbs - 1, scale_degree=int(state.scale_degree),
+                                          scaling_factor=out_state.scaling_factor / float(ctx.rescale_divisor_at(limbs)))
+        outputs = []
+        start = 0
+        for c in inputs:
+            B = c.batch_size
+            outputs.append(Cipher([total0[start:start + B], total1[start:start + B]], out_state, slots=slots))
+            start += B
+        return tuple(outputs), {}
+
+    def project(self, input_ciphers, weight: LinearWeight, **kwargs):
+        outputs, _ = self.apply(input_ciphers, weight, **kwargs)
+        return outputs
+
+    def close(self) -> None:
+        self._closed = True
+
+
+__all__ = ["LinearChunk", "BabyBlock", "LinearPlan", "LinearOperatorConfig", "linear_rotations",
+           "bsgs_rotations", "LinearWeight", "LinearOperator"]

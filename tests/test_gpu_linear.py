@@ -1,0 +1,91 @@
+"""GPU BSGS linear layer: bit-exact against the oracle composition of the same schedule, and the
+decrypted result against W @ X (float64) within 2^-16 of the slot scale."""
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+torch = pytest.importorskip("torch")
+
+from oracle import oracle as O  # noqa: E402
+
+D, LANES, B, ROWS = 256, 8, 16, 128
+LIMBS = 4
+
+
+@pytest.fixture(scope="module")
+def env():
+    from holmes_amd import fhe, linear
+
+    cfg = linear.LinearOperatorConfig(baby_steps=B, baby_anchor_step=-1, max_plaintext_rows=ROWS)
+    plan = cfg.plan(dimension=D, token_lanes=LANES)
+    spec = fhe.CKKSContextSpec(depth=23, dnum=3, seed=4242, rotations=linear.bsgs_rotations(plan))
+    client, ctx = fhe.generate_client_context(spec)
+    rng = np.random.default_rng(5)
+    W = rng.normal(scale=1.0 / np.sqrt(D), size=(D, D))
+    X = [rng.normal(size=(D, LANES)) for _ in range(2)]
+    return fhe, linear, client, ctx, cfg, plan, W, X
+
+
+def _slots(X, slots):
+    s = np.arange(slots)
+    return X[(s // LANES) % D, s % LANES]
+
+
+def test_linear_decrypts_to_matvec(env):
+    fhe, linear, client, ctx, cfg, plan, W, X = env
+    cts = [client.encrypt(_slots(x, ctx.max_slots), cur_limbs=LIMBS) for x in X]
+    op = linear.LinearOperator(crypto_context=ctx, token_lanes=LANES, config=cfg)
+    weight = linear.LinearWeight(W, crypto_context=ctx)
+    outs = op.project(cts, weight)
+    assert plan.plaintext_chunks == 2
+    for x, out in zip(X, outs):
+        assert out.state.cur_limbs == LIMBS - 1
+        assert abs(out.state.scaling_factor - cts[0].state.scaling_factor) < 1e-6 * cts[0].state.scaling_factor
+        got = client.decrypt(out).real
+        want = _slots(W @ x, ctx.max_slots)
+        assert np.max(np.abs(got - want)) < 2.0**-16
+
+
+def test_linear_residues_match_oracle_composition(env):
+    fhe, linear, client, ctx, cfg, plan, W, X = env
+    orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+    keys = {}
+    for r in linear.bsgs_rotations(plan):
+        g = ctx.galois_element(r)
+        keys[r] = (g, orc.make_ksk(*client.key_inputs(g)))
+    ct = client.encrypt(_slots(X[0], ctx.max_slots), cur_limbs=LIMBS)
+    op = linear.LinearOperator(crypto_context=ctx, token_lanes=LANES, config=cfg)
+    out = op.project([ct], linear.LinearWeight(W, crypto_context=ctx))[0]
+    torch.cuda.synchronize()
+    g0, g1 = out.cv[0].cpu().numpy()[0], out.cv[1].cpu().numpy()[0]
+
+    q = np.array(ctx.primes[:LIMBS], dtype=object).reshape(LIMBS, 1)
+    c0, c1 = ct.cv[0].cpu().numpy()[0], ct.cv[1].cpu().numpy()[0]
+
+    def rot(a0, a1, r):
+        g, k = keys[r]
+        return orc.rotate(LIMBS, g, a0, a1, k)
+
+    babies = [(c0, c1)] + [rot(c0, c1, off) for off in plan.baby_offsets[1:]]
+    baby_arr = np.stack([np.stack(bb) for bb in babies])  # [nb][2][limbs][N]
+    scale = float(ctx.rescale_divisor_at(LIMBS))
+    tot0 = tot1 = None
+    for chunk in plan.chunks:
+        rows = O.pack_diagonals(W, LANES, 0, B, chunk.giant_base, chunk.giant_count, ctx.max_slots)
+        pts = np.stack([orc.encode_real(r, scale, list(range(LIMBS)))[0] for r in rows])
+        part = orc.bsgs_mac(LIMBS, B, chunk.giant_count, pts, baby_arr)  # [2][G][limbs][N]
+        a0, a1 = part[0, -1], part[1, -1]
+        for g in range(chunk.giant_count - 2, -1, -1):
+            r0, r1 = rot(a0, a1, plan.giant_offset)
+            a0 = ((r0.astype(object) + part[0, g].astype(object)) % q).astype(np.uint64)
+            a1 = ((r1.astype(object) + part[1, g].astype(object)) % q).astype(np.uint64)
+        if chunk.giant_base:
+            a0, a1 = rot(a0, a1, chunk.giant_base * plan.giant_offset)
+        if tot0 is None:
+            tot0, tot1 = a0, a1
+        else:
+            tot0 = ((tot0.astype(object) + a0.astype(object)) % q).astype(np.uint64)
+            tot1 = ((tot1.astype(object) + a1.astype(object)) % q).astype(np.uint64)
+    w0, w1 = orc.rescale(LIMBS, tot0), orc.rescale(LIMBS, tot1)
+    assert np.array_equal(g0[: LIMBS - 1], w0) and np.array_equal(g1[: LIMBS - 1], w1)
