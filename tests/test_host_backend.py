@@ -83,3 +83,21 @@ def test_encode_decode_roundtrip_and_rotation_group(slots):
 def test_encoder_cap():
     with pytest.raises(ValueError):
         encoding.encode(np.full(8, 1e9), 2.0**40, 16, 8)
+
+
+def test_feature_major_layout_roundtrip_and_slot_rule():
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+
+    lay = FeatureMajorPrefillLayout()
+    assert lay.tokens_per_cipher == 8 and lay.cipher_count == 16
+    rng = np.random.default_rng(1)
+    rows = rng.normal(size=(128, 4096))
+    packed = lay.pack(rows)
+    assert packed.shape == (16, 32768)
+    assert packed[3, lay.slot(17, 5)] == rows[3 * 8 + 5, 17]
+    assert np.array_equal(lay.unpack(packed), rows)
+    small = FeatureMajorPrefillLayout(seq_len=5, hidden_dim=16, slots=64)
+    r = rng.normal(size=(5, 16))
+    assert np.array_equal(small.unpack(small.pack(r)), r)
+    with pytest.raises(ValueError):
+        FeatureMajorPrefillLayout(hidden_dim=12)
