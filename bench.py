@@ -1,4 +1,6 @@
-"""Benchmark: batched hybrid key switching on one MI355X.
+"""Benchmark on one MI355X.
+
+Default (``--workload c2``, the headline line): batched hybrid key switching.
 
 Workload (one "step"): 16 ciphertext polynomials d at 24 limbs of 50-bit primes, N = 2^16, each
 key-switched with its own rotation key (rotations 1..16), dnum 3 (8-limb digits), 8 special
@@ -10,6 +12,13 @@ per ciphertext d 12 MiB + key 96 MiB + (b, a) out 24 MiB = 138,412,032 B; 16 per
 
 cpu_baseline: this repository's CPU oracle (oracle/ckks_oracle.c, exact 128-bit integer
 arithmetic, OpenMP over ciphertexts) runs the same 16 key switches once on the host.
+
+``--workload c3``: one Llama-3-8B q_proj projection (4096 x 4096, Gaussian std 0.02 weights
+right-multiplied by a seeded randomized Hadamard) applied by the BSGS diagonal method (baby step
+16, 512 plaintext rows per chunk) to 128 tokens x 4096 features encrypted feature-major into 16
+ciphertexts at 20 limbs, scale 2^40.  A step is one whole projection, pack + encode of every
+diagonal included (the reference encodes per chunk per call,
+llama3fhe/operators/linear/operator.py:296-312).  Its line reports seconds per projection.
 """
 
 from __future__ import annotations
@@ -26,6 +35,11 @@ BYTES_PER_CT = (12 + 96 + 24) * 2**20  # 138,412,032
 CTS = 16
 LIMBS = 24
 HBM_PEAK_GBS = 8000.0
+# C3: 4096 plaintexts x 20 limbs + keys + inputs + outputs, the algorithmic figure of the config
+C3_BYTES = 45_629_833_216
+C3_LIMBS = 20
+C3_DIM = 4096
+C3_TOKENS = 128
 METRIC = "s per encrypted Llama-3-8B layer (128-tok prefill, 1 GPU); key-switch HBM GB/s"
 
 
@@ -41,6 +55,10 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
+    ap.add_argument("--workload", choices=("c2", "c3", "stream"), default="c2",
+                    help="c2: batched key switch (headline); c3: q_proj BSGS projection; stream: the "
+                         "residue negation kernel over 16 x 24 limbs, a plain read-once/write-once "
+                         "stream of known size (HBM ceiling and counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(
@@ -57,6 +75,10 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("no GPU visible", file=sys.stderr)
         return 1
+    if args.workload == "c3":
+        return run_c3(args)
+    if args.workload == "stream":
+        return run_stream(args)
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
@@ -163,6 +185,198 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def run_stream(args) -> int:
+    import torch
+
+    from holmes_amd import _native as nat
+    from holmes_amd import fhe
+
+    spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
+    ctx = fhe.CKKSContext(spec)
+    idx = ctx.q_prime_idx(LIMBS)
+    a = ctx.zeros(CTS, LIMBS, ctx.N)
+    out = ctx.empty(CTS, LIMBS, ctx.N)
+    nbytes = 2 * a.numel() * 8
+    for _ in range(args.warmup):
+        ctx.poly_op(nat.HCK_OP_NEG, out, a, prime_idx=idx)
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        ctx.poly_op(nat.HCK_OP_NEG, out, a, prime_idx=idx)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    print(json.dumps({"workload": "stream: k_poly_op<NEG> over 16 x 24 limbs", "bytes_per_launch": nbytes,
+                      "read_bytes": nbytes // 2, "write_bytes": nbytes // 2, "launches": args.steps,
+                      "ms_per_launch": round(ms, 5), "GB/s": round(nbytes / (ms * 1e-3) / 1e9, 2)}), flush=True)
+    return 0
+
+
+def randomized_hadamard_right(w: np.ndarray, seed: int) -> np.ndarray:
+    """w @ (diag(s) H / sqrt(n)) with s a seeded +-1 vector and H the Sylvester Hadamard matrix,
+    by an in-place fast Walsh-Hadamard transform over the last axis (the QuaRot-style rotation
+    of tools/convert/hadamard/numpy.py:1-40, restated)."""
+
+    n = w.shape[-1]
+    if n & (n - 1):
+        raise ValueError("Hadamard size must be a power of two")
+    s = np.random.default_rng(seed).choice(np.array([-1.0, 1.0]), size=n)
+    x = (np.asarray(w, dtype=np.float64) * s).copy()
+    h = 1
+    while h < n:
+        x = x.reshape(*x.shape[:-1], n // (2 * h), 2, h)
+        a, b = x[..., 0, :].copy(), x[..., 1, :].copy()
+        x[..., 0, :], x[..., 1, :] = a + b, a - b
+        x = x.reshape(*x.shape[:-3], n)
+        h *= 2
+    return x / np.sqrt(n)
+
+
+def run_c3(args) -> int:
+    import torch
+
+    from holmes_amd import fhe, linear
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+
+    seed = int(args.seed)
+    steps = int(args.steps) if args.steps != 20 else 3
+    warmup = int(args.warmup) if args.warmup != 3 else 1
+    t0 = time.perf_counter()
+    cfg = linear.LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512)
+    layout = FeatureMajorPrefillLayout(seq_len=C3_TOKENS, hidden_dim=C3_DIM, slots=32768)
+    lanes = layout.tokens_per_cipher
+    plan = cfg.plan(dimension=C3_DIM, token_lanes=lanes)
+    spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=seed,
+                               rotations=linear.bsgs_rotations(plan))
+    client, ctx = fhe.generate_client_context(spec)
+    rng = np.random.default_rng(seed)
+    w = randomized_hadamard_right(rng.normal(scale=0.02, size=(C3_DIM, C3_DIM)), seed + 1)
+    x = rng.normal(size=(C3_TOKENS, C3_DIM))
+    packed = layout.pack(x)
+    cts = [client.encrypt(packed[c], cur_limbs=C3_LIMBS, scaling_factor=2.0**40) for c in range(layout.cipher_count)]
+    op = linear.LinearOperator(crypto_context=ctx, token_lanes=lanes, config=cfg)
+    weight = linear.LinearWeight(w, crypto_context=ctx)
+    torch.cuda.synchronize()
+    _log(f"c3 setup {time.perf_counter() - t0:.1f}s: {len(spec.rotations)} keys, {len(cts)} cts at "
+         f"{C3_LIMBS} limbs, {plan.plaintext_chunks} chunks x {plan.chunk_giants} giants x {plan.baby_steps} babies")
+
+    outs = None
+    for _ in range(warmup):
+        outs = op.project(cts, weight)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(steps):
+        outs = op.project(cts, weight)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    s_wall = (time.perf_counter() - w0) / steps
+    s_events = ev0.elapsed_time(ev1) * 1e-3 / steps
+    _log(f"{steps} projections: {s_wall:.4f} s wall, {s_events:.4f} s events")
+
+    # decrypted spot check of two ciphertexts against float64 W' x
+    want = layout.pack(x @ w.T)
+    err = 0.0
+    for c in (0, layout.cipher_count - 1):
+        got = client.decrypt(outs[c]).real
+        err = max(err, float(np.max(np.abs(got - want[c]))))
+    _log(f"decrypted max abs error {err:.3e} (bound 2^-16 = {2.0**-16:.3e})")
+
+    ks_per_projection = len(cts) * (plan.baby_rotation_count + sum(c.giant_count - 1 for c in plan.chunks)
+                                    + sum(1 for c in plan.chunks if c.giant_base))
+    cpu = None
+    if not args.no_cpu:
+        cpu = _c3_cpu_sample(ctx, client, plan, w, cts, ks_per_projection)
+
+    achieved = C3_BYTES / s_events / 1e9
+    line = {
+        "metric": "s per q_proj projection (C3: 4096x4096 BSGS, 16 cts x 20 limbs)",
+        "value": round(s_wall, 5),
+        "unit": "s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": warmup,
+        "ms_per_step": round(s_wall * 1e3, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "u64",
+        "data": "synthetic",
+        "config": {
+            "workload": "C3 q_proj BSGS: 4096x4096 Hadamard-rotated N(0, 0.02^2) weight, 128 tokens "
+                        "feature-major in 16 cts x 20 limbs, baby 16, 512 plaintext rows per chunk",
+            "N": ctx.N,
+            "limbs": C3_LIMBS,
+            "chunks": plan.plaintext_chunks,
+            "key_switches": ks_per_projection,
+            "algorithmic_bytes_per_step": C3_BYTES,
+            "decrypted_max_abs_error": err,
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "kernel": "whole projection (babies, pack + encode, MAC, Horner giant key switches, rescale)",
+            "ms_per_launch": round(s_events * 1e3, 3),
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def _c3_cpu_sample(ctx, client, plan, w, cts, ks_count):
+    """Times the oracle on a bounded sample and extrapolates to one projection: one rotation at
+    20 limbs (x key switches per projection), one chunk's MAC for one input (x chunks x inputs)
+    and the encode of 8 diagonal rows (x 4096 / 8)."""
+
+    from oracle import oracle as O
+
+    threads = O.num_threads()
+    orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+    g = ctx.galois_element(plan.giant_offset)
+    key = orc.make_ksk(*client.key_inputs(g))
+    c0 = cts[0].cv[0].cpu().numpy()[0, :C3_LIMBS]
+    c1 = cts[0].cv[1].cpu().numpy()[0, :C3_LIMBS]
+    t = time.perf_counter()
+    orc.rotate(C3_LIMBS, g, c0, c1, key)
+    t_ks = time.perf_counter() - t
+    chunk = plan.chunks[0]
+    scale = float(ctx.rescale_divisor_at(C3_LIMBS))
+    rows = O.pack_diagonals(w, plan.token_lanes, 0, plan.baby_steps, chunk.giant_base, chunk.giant_count,
+                            ctx.max_slots)
+    idx = list(range(C3_LIMBS))
+    t = time.perf_counter()
+    enc = [orc.encode_real(rows[i], scale, idx)[0] for i in range(8)]
+    t_enc8 = time.perf_counter() - t
+    pts = np.stack(enc * (rows.shape[0] // 8))
+    babies = np.stack([np.stack([c0, c1])] * plan.baby_steps)
+    t = time.perf_counter()
+    orc.bsgs_mac(C3_LIMBS, plan.baby_steps, chunk.giant_count, pts, babies)
+    t_mac = time.perf_counter() - t
+    total = ks_count * t_ks + plan.plaintext_chunks * len(cts) * t_mac + (C3_DIM // 8) * t_enc8
+    _log(f"cpu sample: rotation {t_ks:.3f}s, chunk MAC {t_mac:.2f}s, 8 encodes {t_enc8:.3f}s -> "
+         f"{total:.1f} s per projection")
+    return {
+        "value": round(total, 2),
+        "unit": "s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"extrapolated: 1 rotation at 20 limbs ({t_ks:.3f} s) x {ks_count}, one chunk MAC for "
+                  f"one input ({t_mac:.2f} s) x {plan.plaintext_chunks * len(cts)}, 8 row encodes "
+                  f"({t_enc8:.3f} s) x {C3_DIM // 8}",
+    }
 
 
 if __name__ == "__main__":

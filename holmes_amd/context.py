@@ -255,7 +255,11 @@ class CKKSContext:
         return out_b, out_a
 
     def rotate_raw(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois: int, keys,
-                   out0: torch.Tensor | None = None, out1: torch.Tensor | None = None):
+                   out0: torch.Tensor | None = None, out1: torch.Tensor | None = None,
+                   acc: tuple[torch.Tensor, torch.Tensor] | None = None):
+        """(sigma(c0) + KS_b(sigma(c1)), KS_a(sigma(c1))), plus ``acc`` = (acc0, acc1) when given.
+        Outputs may be the ``acc`` tensors themselves, never c0 / c1."""
+
         self._check_poly(c0, limbs, self.N)
         self._check_poly(c1, limbs, self.N)
         if c0.stride(0) != c1.stride(0):
@@ -263,15 +267,37 @@ class CKKSContext:
         B = c0.shape[0]
         if isinstance(keys, torch.Tensor):
             keys = [keys] * B
+        if len(keys) != B:
+            raise ValueError("one key per batch item")
         for k in keys:
             self._check_key(k)
         out0 = self.empty(B, limbs, self.N) if out0 is None else out0
         out1 = self.empty(B, limbs, self.N) if out1 is None else out1
+        for o in (out0, out1):
+            self._check_poly(o, limbs, self.N)
+            if o.shape[0] != B:
+                raise ValueError("outputs need one row per input")
+        if out0.stride(0) != out1.stride(0):
+            raise ValueError("out0 and out1 need the same batch stride")
+        a0 = a1 = None
+        a_stride = 0
+        if acc is not None:
+            a0, a1 = acc
+            for a in (a0, a1):
+                self._check_poly(a, limbs, self.N)
+                if a.shape[0] != B:
+                    raise ValueError("accumulators need one row per input")
+            if a0.stride(0) != a1.stride(0):
+                raise ValueError("acc0 and acc1 need the same batch stride")
+            a_stride = a0.stride(0)
         L = nat.lib()
         ws = self.workspace(L.hck_rotate_workspace_bytes(self._h, limbs, B))
         nat.check(L.hck_rotate(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), c0.stride(0),
-                               nat.ptr_array([k.data_ptr() for k in keys]), out0.data_ptr(), out1.data_ptr(),
-                               out0.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                               nat.ptr_array([k.data_ptr() for k in keys]),
+                               a0.data_ptr() if a0 is not None else None,
+                               a1.data_ptr() if a1 is not None else None, a_stride,
+                               out0.data_ptr(), out1.data_ptr(), out0.stride(0), ws.data_ptr(), ws.numel(),
+                               _stream_ptr(self.device)),
                   "hck_rotate")
         return out0, out1
 

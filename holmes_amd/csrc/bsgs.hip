@@ -24,7 +24,6 @@ constexpr int kMacThreads = 128;
 constexpr int kTI = 4;          // inputs per thread
 constexpr int kTG = 4;          // giants per thread
 constexpr int kMaxBabies = 64;
-constexpr int kXcds = 8;
 
 struct BabyPtrs {
   const uint64_t* c0[kMaxBabies];

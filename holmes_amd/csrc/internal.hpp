@@ -80,9 +80,15 @@ int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
 
 size_t ks_fused_bytes(const hck_context* c, int ell, int batch);
-int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
-             const uint64_t* const* ksk, const uint64_t* add, long long add_stride, uint64_t* out_b,
-             uint64_t* out_a, long long out_stride, char* ws, hipStream_t s);
+// d and add are read through sigma_galois (galois == 1: unpermuted); acc_b / acc_a (nullable,
+// unpermuted) are added to out_b / out_a.
+int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+             const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+             const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
+             char* ws, hipStream_t s);
+
+// MI355X deals consecutive workgroups to its 8 XCDs (each with its own L2) round-robin.
+constexpr int kXcds = 8;
 
 inline int beta_of(const hck_context* c, int ell) { return (ell + c->alpha - 1) / c->alpha; }
 inline const ConvConsts* modup_consts(const hck_context* c, int ell, int j) {

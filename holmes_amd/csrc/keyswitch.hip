@@ -56,38 +56,44 @@ extern "C" int hck_keyswitch(const hck_context* ctx, int level_limbs, int batch,
   if (!workspace || workspace_bytes < hck::ks_fused_bytes(ctx, level_limbs, chunk)) return HCK_ERR_WORKSPACE;
   for (int b0 = 0; b0 < batch; b0 += chunk) {
     const int nb = batch - b0 < chunk ? batch - b0 : chunk;
-    int rc = hck::ks_fused(ctx, level_limbs, nb, d + (long long)b0 * d_stride, d_stride, ksk + b0,
-                                  add_b ? add_b + (long long)b0 * add_stride : nullptr, add_stride,
-                                  out_b + (long long)b0 * out_stride, out_a + (long long)b0 * out_stride,
-                                  out_stride, (char*)workspace, (hipStream_t)stream);
+    int rc = hck::ks_fused(ctx, level_limbs, nb, d + (long long)b0 * d_stride, d_stride, 1u, ksk + b0,
+                           add_b ? add_b + (long long)b0 * add_stride : nullptr, add_stride, nullptr, nullptr, 0,
+                           out_b + (long long)b0 * out_stride, out_a + (long long)b0 * out_stride, out_stride,
+                           (char*)workspace, (hipStream_t)stream);
     if (rc) return rc;
   }
   return HCK_OK;
 }
 
 extern "C" size_t hck_rotate_workspace_bytes(const hck_context* ctx, int level_limbs, int batch) {
-  if (!ctx || level_limbs < 1 || level_limbs > ctx->L || batch < 0) return 0;
-  const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
-  return hck::ks_fused_bytes(ctx, level_limbs, chunk) + (size_t)2 * batch * level_limbs * hck::kN * 8;
+  return hck_keyswitch_workspace_bytes(ctx, level_limbs, batch);
 }
 
 extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
                           const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
-                          const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                          const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                          int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                           void* workspace, size_t workspace_bytes, void* stream) {
   if (!ctx || !c0 || !c1 || !ksk || !out0 || !out1 || batch < 0) return HCK_ERR_ARG;
   if (level_limbs < 1 || level_limbs > ctx->L) return HCK_ERR_ARG;
+  if ((galois & 1u) == 0 || galois >= 2u * hck::kN) return HCK_ERR_ARG;
+  if ((acc0 == nullptr) != (acc1 == nullptr)) return HCK_ERR_ARG;
+  // the inputs are gathered through sigma while the outputs are written: no aliasing
+  if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1) return HCK_ERR_ARG;
   if (batch == 0) return HCK_OK;
-  if (!workspace || workspace_bytes < hck_rotate_workspace_bytes(ctx, level_limbs, batch)) return HCK_ERR_WORKSPACE;
-  const long long ln = (long long)level_limbs * hck::kN;
-  uint64_t* r0 = (uint64_t*)workspace;
-  uint64_t* r1 = r0 + (long long)batch * ln;
-  char* ks_ws = (char*)(r1 + (long long)batch * ln);
-  int rc = hck_automorphism(ctx, c0, r0, batch, in_stride, ln, level_limbs, galois, stream);
-  if (rc) return rc;
-  if ((rc = hck_automorphism(ctx, c1, r1, batch, in_stride, ln, level_limbs, galois, stream))) return rc;
-  return hck_keyswitch(ctx, level_limbs, batch, r1, ln, ksk, r0, ln, out0, out1, out_stride, ks_ws,
-                       workspace_bytes - (size_t)((char*)ks_ws - (char*)workspace), stream);
+  for (int b = 0; b < batch; ++b) if (!ksk[b]) return HCK_ERR_ARG;
+  const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
+  if (!workspace || workspace_bytes < hck::ks_fused_bytes(ctx, level_limbs, chunk)) return HCK_ERR_WORKSPACE;
+  for (int b0 = 0; b0 < batch; b0 += chunk) {
+    const int nb = batch - b0 < chunk ? batch - b0 : chunk;
+    const long long ai = (long long)b0 * acc_stride;
+    int rc = hck::ks_fused(ctx, level_limbs, nb, c1 + (long long)b0 * in_stride, in_stride, galois, ksk + b0,
+                           c0 + (long long)b0 * in_stride, in_stride, acc0 ? acc0 + ai : nullptr,
+                           acc1 ? acc1 + ai : nullptr, acc_stride, out0 + (long long)b0 * out_stride,
+                           out1 + (long long)b0 * out_stride, out_stride, (char*)workspace, (hipStream_t)stream);
+    if (rc) return rc;
+  }
+  return HCK_OK;
 }
 
 extern "C" size_t hck_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int polys) {

@@ -6,13 +6,19 @@
 // at c * 256 + r) so a column is 2 KiB contiguous: the cols kernels read and write whole columns,
 // the rows kernels read 16 rows at once as 128-byte runs.
 //
-//   K1 ks_intt_rows   d (natural, u64) --INTT rows-->                         T1 (transposed)
+//   K1 ks_intt_rows   sigma_g(d) (natural, u64) --INTT rows-->                T1 (transposed)
 //   K2 ks_cols_conv   T1 --INTT cols--> coefficients --ModUp conversion (LDS)--> NTT cols --> T2
 //   K3 ks_rows_ip     T2 --NTT rows--> x_j;  acc = sum_j x_j * key_j  (d for the digit's own limbs)
 //                     Q limbs: acc --> ACCQ (natural);  P limbs: acc --INTT rows--> ACCP (transposed)
 //   K4 ks_cols_conv   ACCP --INTT cols--> ModDown conversion P -> Q --NTT cols--> T4
-//   K5 ks_rows_finish T4 --NTT rows--> v;  out = (ACCQ - v) * P^-1 (+ addend), canonical u64
+//   K5 ks_rows_finish T4 --NTT rows--> v;  out = (ACCQ - v) * P^-1 (+ sigma_g(addend)) (+ acc),
+//                     canonical u64
 //
+// A rotation passes its Galois element g: the NTT-domain automorphism sigma_g is a permutation of
+// each limb, so K1 (and K3 for a digit's own limbs) read d = c1 and K5 reads the addend c0 through
+// it, and no permuted copy of the input is written.  The optional per-component accumulators
+// (acc_b, acc_a) fold a following ciphertext addition (the Horner giant step of a BSGS product)
+// into the same store.
 // Per ciphertext at ell = 24, K = 8, dnum 3 this moves 352 MiB (key 96 MiB) instead of the
 // 648 MiB of separate transform / conversion / product kernels.  Arithmetic: modarith.hpp.
 // Algorithm: the key-switch EasyFHE runs for fhe.homo_rotate (F.cv_modup, F.cv_innerproduct_*,
@@ -229,6 +235,26 @@ __device__ __forceinline__ void row_inv_lo(double (&x)[16], int b, const double*
   }
 }
 
+// Natural position that lands in slot n under sigma_g: slot n holds the evaluation at
+// psi^(2 brv(n) + 1), and sigma_g moves the evaluation at psi^(g (2 brv(n) + 1)) there.
+__device__ __forceinline__ long long gal_src(long long n, uint32_t g) {
+  const uint32_t e = ((2u * (__brev((uint32_t)n) >> 16) + 1u) * g) & (2u * kN - 1u);
+  return (long long)(__brev((e - 1u) >> 1) >> 16);
+}
+
+// 16 words of one natural-layout limb for the thread at natural offset na (+16k), read through
+// sigma_g (g == 1: the identity, plain coalesced loads).
+__device__ __forceinline__ void load_gal(double (&x)[16], const uint64_t* __restrict__ limb, long long na,
+                                         uint32_t g) {
+  if (g == 1u) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = u2d(limb[na + 16 * k]);
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = u2d(limb[gal_src(na + 16 * k, g)]);
+  }
+}
+
 // Natural-layout access in layout A under map N: thread (rb, j) owns words j + 16k of row r0 + rb;
 // 16 consecutive lanes touch 128 consecutive bytes.
 __device__ __forceinline__ long long nat_a(int r0) {
@@ -263,15 +289,13 @@ __device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restric
 
 // ----------------------------------------------------------------- K1: INTT rows of d
 __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
-                                                     double* __restrict__ t1, int ell, DevTables T) {
+                                                     uint32_t g, double* __restrict__ t1, int ell, DevTables T) {
   __shared__ double S[kRowLds];
   const int i = blockIdx.z, b = blockIdx.x, r0 = blockIdx.y * 16;
   const double p = T.p[i], pinv = T.pinv[i];
   const double* __restrict__ tw = T.tw_inv + (size_t)i * kN;
-  const uint64_t* src = d + (long long)b * d_stride + (long long)i * kN + nat_a(r0);
   double x[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) x[k] = u2d(src[16 * k]);
+  load_gal(x, d + (long long)b * d_stride + (long long)i * kN, nat_a(r0), g);
   rows_inv_to_t(x, t1 + ((long long)b * ell + i) * kN, r0, S, tw, p, pinv);
 }
 
@@ -362,12 +386,19 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
 }
 
 // ----------------------------------------------------------------- K3: NTT rows + inner product
-__global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride,
+// Grid: one linear id per (ciphertext, tile), tile = (row group, extended limb).  Workgroups are
+// dealt to the 8 XCDs round-robin; the decode keeps every ciphertext of one tile on one XCD, one
+// after another, so a key shared by the batch (a giant step) is read from HBM once per tile and
+// served from that XCD's L2 to the other ciphertexts.
+__global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
                                                    const double* __restrict__ t2, KeyPtrsF keys, int ell,
-                                                   int beta, double* __restrict__ accq, double* __restrict__ accp,
-                                                   DevTables T) {
+                                                   int beta, int batch, int tiles, double* __restrict__ accq,
+                                                   double* __restrict__ accp, DevTables T) {
   __shared__ double S[kRowLds];
-  const int e = blockIdx.z, b = blockIdx.x, r0 = blockIdx.y * 16;
+  const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
+  const int tile = (q / batch) * kXcds + xcd, b = q % batch;
+  if (tile >= tiles) return;
+  const int e = tile >> 4, r0 = (tile & 15) * 16;
   const int L = T.L, K = T.K, alpha = T.alpha;
   const int ext_l = ell + K;
   const int pi = e < ell ? e : L + (e - ell);
@@ -388,9 +419,7 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
 #pragma unroll
     for (int k = 0; k < 16; ++k) { kb[k] = kp[16 * k]; ka[k] = kp[comp_stride + 16 * k]; }
     if (jd == own) {
-      const uint64_t* src = d + (long long)b * d_stride + (long long)e * kN + na;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = u2d(src[16 * k]);
+      load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
     } else {
       rows_fwd_from_t(x, t2 + (((long long)b * beta + jd) * ext_l + e) * kN, r0, S, twf, p, pinv);
     }
@@ -422,6 +451,8 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
 // ----------------------------------------------------------------- K5: NTT rows + ModDown combine
 __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const double* __restrict__ accq,
                                                        const uint64_t* __restrict__ add, long long add_stride,
+                                                       uint32_t g, const uint64_t* __restrict__ acc_b,
+                                                       const uint64_t* __restrict__ acc_a, long long acc_stride,
                                                        uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
                                                        long long out_stride, int ell,
                                                        const LevelConsts* __restrict__ lc, DevTables T) {
@@ -436,13 +467,11 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
   const double* ap = accq + (((long long)b * 2 + comp) * ell + i) * kN + na;
 #pragma unroll
   for (int k = 0; k < 16; ++k) a[k] = ap[16 * k];
-  uint64_t ad[16];
+  double ad[16], ac[16];
   const bool has_add = comp == 0 && add;
-  if (has_add) {
-    const uint64_t* pp = add + (long long)b * add_stride + (long long)i * kN + na;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) ad[k] = pp[16 * k];
-  }
+  if (has_add) load_gal(ad, add + (long long)b * add_stride + (long long)i * kN, na, g);
+  const uint64_t* accp_ = comp == 0 ? acc_b : acc_a;
+  if (accp_) load_gal(ac, accp_ + (long long)b * acc_stride + (long long)i * kN, na, 1u);
   double x[16];
   rows_fwd_from_t(x, t4 + (((long long)b * 2 + comp) * ell + i) * kN, r0, S, tw, p, pinv);
   const TwPair pi_ = lc->p_inv[i];
@@ -450,7 +479,8 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
     double r = mulc(a[k] - x[k], pi_, p);  // |acc - v| <= 4.5 p: |r| <= 2.2 p
-    if (has_add) r += u2d(ad[k]);
+    if (has_add) r += ad[k];
+    if (accp_) r += ac[k];                 // |r| <= 4.2 p
     o[16 * k] = d2u(canon(r, p, pinv));
   }
 }
@@ -464,9 +494,10 @@ size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
   return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * ell + 2 * c->K);
 }
 
-int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
-             const uint64_t* const* ksk, const uint64_t* add, long long add_stride, uint64_t* out_b,
-             uint64_t* out_a, long long out_stride, char* ws, hipStream_t s) {
+int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+             const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+             const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
+             char* ws, hipStream_t s) {
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch > kMaxBatchF) return HCK_ERR_ARG;
   const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
@@ -477,7 +508,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   double* accp = accq + (long long)batch * 2 * ell * n;
   // K1
   // row kernels: ciphertext index fastest, so the blocks in flight share one prime's twiddles
-  k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, r1, ell, c->dev);
+  k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, galois, r1, ell, c->dev);
   HCK_CHECK_LAUNCH();
   // K2: ModUp, one block per (column pair, digit, ciphertext)
   k_ks_cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
@@ -487,7 +518,10 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   // K3
   KeyPtrsF kp{};
   for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
-  k_ks_rows_ip<<<dim3(batch, 16, ext_l), kT, 0, s>>>(d, d_stride, t2, kp, ell, beta, accq, accp, c->dev);
+  const int tiles = 16 * ext_l;
+  const int groups = (tiles + kXcds - 1) / kXcds;
+  k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
+                                                          accq, accp, c->dev);
   HCK_CHECK_LAUNCH();
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
   double* t4 = r1;
@@ -495,8 +529,9 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
                                                     (long long)ell * n, c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
   // K5
-  k_ks_rows_finish<<<dim3(2 * batch, 16, ell), kT, 0, s>>>(t4, accq, add, add_stride, out_b, out_a, out_stride,
-                                                           ell, c->d_level + ell, c->dev);
+  k_ks_rows_finish<<<dim3(2 * batch, 16, ell), kT, 0, s>>>(t4, accq, add, add_stride, galois, acc_b, acc_a,
+                                                           acc_stride, out_b, out_a, out_stride, ell,
+                                                           c->d_level + ell, c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }

@@ -279,10 +279,13 @@ class LinearOperator:
         cc = self.crypto_context
         return getattr(cc, "context", cc)
 
-    def _rotate_all(self, c0, c1, rotation: int, limbs: int):
+    def _rotate_all(self, c0, c1, rotation: int, limbs: int, acc=None):
         ctx = self._ctx()
         g = ctx.galois_element(rotation)
-        return ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g))
+        if acc is None:
+            return ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g))
+        # rotate-and-add in one pass, written over the addend
+        return ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g), out0=acc[0], out1=acc[1], acc=acc)
 
     def apply(self, input_ciphers, weight: LinearWeight, *, chunk_indices=None, rescale: bool = True,
               weight_scale: float | None = None):
@@ -320,14 +323,17 @@ class LinearOperator:
             del pts
             acc0, acc1 = part[0, -1], part[1, -1]
             for g in range(int(chunk.giant_count) - 2, -1, -1):
-                r0, r1 = self._rotate_all(acc0, acc1, plan.giant_offset, limbs)
-                ctx.poly_op(nat.HCK_OP_ADD, r0, r0, part[0, g], prime_idx=idx)
-                ctx.poly_op(nat.HCK_OP_ADD, r1, r1, part[1, g], prime_idx=idx)
-                acc0, acc1 = r0, r1
-            if int(chunk.giant_base):
-                acc0, acc1 = self._rotate_all(acc0, acc1, int(chunk.giant_base) * plan.giant_offset, limbs)
+                # Horner: acc <- rot(acc) + partial_g, stored over partial_g
+                acc0, acc1 = self._rotate_all(acc0, acc1, plan.giant_offset, limbs, acc=(part[0, g], part[1, g]))
+            base = int(chunk.giant_base) * plan.giant_offset
             if total0 is None:
-                total0, total1 = acc0.clone(), acc1.clone()
+                if base:
+                    total0, total1 = self._rotate_all(acc0, acc1, base, limbs)
+                else:
+                    total0, total1 = acc0.clone(), acc1.clone()
+            elif base:
+                # chunk alignment rotation, accumulated into the running total in the same pass
+                self._rotate_all(acc0, acc1, base, limbs, acc=(total0, total1))
             else:
                 ctx.poly_op(nat.HCK_OP_ADD, total0, total0, acc0, prime_idx=idx)
                 ctx.poly_op(nat.HCK_OP_ADD, total1, total1, acc1, prime_idx=idx)

@@ -83,12 +83,15 @@ int hck_keyswitch(const hck_context* ctx, int level_limbs, int batch, const uint
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /* Rotation of `batch` ciphertexts (c0[b], c1[b]) by galois element g with keys ksk[b]:
- * out0 = sigma(c0) + KS_b(sigma(c1)), out1 = KS_a(sigma(c1)).  Same workspace as hck_keyswitch
- * plus 2 * batch * level_limbs * N words (hck_rotate_workspace_bytes). */
+ * out0 = sigma(c0) + KS_b(sigma(c1)) (+ acc0[b]), out1 = KS_a(sigma(c1)) (+ acc1[b]).
+ * acc0 / acc1 are both NULL or both given (the Horner giant step of a BSGS product,
+ * operator.py:446-453 followed by fhe.homo_add).  Outputs may alias acc but not c0 / c1.
+ * Same workspace as hck_keyswitch (hck_rotate_workspace_bytes). */
 size_t hck_rotate_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
 int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
                const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
-               const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+               const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+               int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                void* workspace, size_t workspace_bytes, void* stream);
 
 /* Rescale `polys` polynomials from level_limbs to level_limbs - 1 limbs:

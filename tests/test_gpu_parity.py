@@ -203,6 +203,46 @@ def test_rotate_matches_oracle(env):
     assert np.array_equal(_host(r0)[0], orc.rescale(ell, w0))
 
 
+@pytest.mark.parametrize("ell,rot", [(20, 128), (9, -3), (3, 4096)])
+def test_rotate_accumulate_batch_matches_oracle(env, ell, rot):
+    """Batched rotation with a shared key and the fused addends: out = rot(c) + acc, written over
+    acc (the BSGS Horner step), against the oracle rotation followed by exact addition."""
+    _, client, ctx, orc = env
+    g = ctx.galois_element(rot)
+    gk, ok = _key_pair(client, ctx, orc, g)
+    rng = np.random.default_rng(700 + ell)
+    B = 5
+    c0, c1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
+    a0, a1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
+    acc0, acc1 = _dev(a0), _dev(a1)
+    o0, o1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, g, gk, out0=acc0, out1=acc1, acc=(acc0, acc1))
+    assert o0.data_ptr() == acc0.data_ptr()
+    h0, h1 = _host(o0), _host(o1)
+    q = np.array(ctx.primes[:ell], dtype=object).reshape(ell, 1)
+    for b in range(B):
+        w0, w1 = orc.rotate(ell, g, c0[b], c1[b], ok)
+        e0 = ((w0.astype(object) + a0[b].astype(object)) % q).astype(np.uint64)
+        e1 = ((w1.astype(object) + a1[b].astype(object)) % q).astype(np.uint64)
+        assert np.array_equal(h0[b], e0), f"b component, item {b}"
+        assert np.array_equal(h1[b], e1), f"a component, item {b}"
+    # plain batched rotation with the same key, no addends
+    p0, p1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, g, gk)
+    w0, w1 = orc.rotate(ell, g, c0[B - 1], c1[B - 1], ok)
+    assert np.array_equal(_host(p0)[B - 1], w0) and np.array_equal(_host(p1)[B - 1], w1)
+
+
+def test_rotate_rejects_aliased_output(env):
+    _, client, ctx, orc = env
+    from holmes_amd import _native as nat
+
+    g = ctx.galois_element(1)
+    gk, _ = _key_pair(client, ctx, orc, g)
+    rng = np.random.default_rng(9)
+    c0, c1 = _dev(_rand(ctx, rng, 1, 4)), _dev(_rand(ctx, rng, 1, 4))
+    with pytest.raises(nat.NativeError):
+        ctx.rotate_raw(c0, c1, 4, g, gk, out0=c0)
+
+
 @pytest.mark.parametrize("ell", [24, 2])
 def test_rescale(env, ell):
     _, _, ctx, orc = env
