@@ -55,8 +55,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
-    ap.add_argument("--workload", choices=("c2", "c3", "stream"), default="c2",
-                    help="c2: batched key switch (headline); c3: q_proj BSGS projection; stream: the "
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "stream"), default="c2",
+                    help="c2: batched key switch (headline); c1: one rotation + rescale (latency); "
+                         "c3: q_proj BSGS projection; stream: the "
                          "residue negation kernel over 16 x 24 limbs, a plain read-once/write-once "
                          "stream of known size (HBM ceiling and counter calibration)")
     args = ap.parse_args()
@@ -77,6 +78,8 @@ def main() -> int:
         return 1
     if args.workload == "c3":
         return run_c3(args)
+    if args.workload == "c1":
+        return run_c1(args)
     if args.workload == "stream":
         return run_stream(args)
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
@@ -184,6 +187,74 @@ def main() -> int:
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+    return 0
+
+
+C1_BYTES = 149_946_368  # ct(24) in + KSK(24) + ct(23) out
+
+
+def run_c1(args) -> int:
+    """One rotation by 5^1 of one ciphertext at 24 limbs (fused automorphism + key switch), then
+    rescale to 23 limbs: the latency case, with the oracle's result as the parity check."""
+
+    import torch
+
+    from holmes_amd import fhe
+
+    seed = 20261201
+    spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=seed)
+    client, ctx = fhe.generate_client_context(spec)
+    g = ctx.galois_element(1)
+    key = client.rotation_key(g)
+    rng = np.random.default_rng(seed)
+    c = [np.stack([rng.integers(0, ctx.primes[i], ctx.N, dtype=np.uint64) for i in range(LIMBS)])[None]
+         for _ in range(2)]
+    c0, c1 = (torch.from_numpy(x).to(ctx.device) for x in c)
+    o0, o1 = ctx.empty(1, LIMBS, ctx.N), ctx.empty(1, LIMBS, ctx.N)
+    r0 = ctx.empty(2, LIMBS - 1, ctx.N)
+    both = ctx.empty(2, LIMBS, ctx.N)
+
+    def step():
+        ctx.rotate_raw(c0, c1, LIMBS, g, key, out0=both[0:1], out1=both[1:2])
+        ctx.rescale_raw(both, LIMBS, out=r0)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        step()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_wall = (time.perf_counter() - w0) * 1e3 / args.steps
+    ms = ev0.elapsed_time(ev1) / args.steps
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+        ok_key = orc.make_ksk(*client.key_inputs(g))
+        t = time.perf_counter()
+        w0_, w1_ = orc.rotate(LIMBS, g, c[0][0], c[1][0], ok_key)
+        want = np.stack([orc.rescale(LIMBS, w0_), orc.rescale(LIMBS, w1_)])
+        csec = time.perf_counter() - t
+        ok = bool(np.array_equal(r0.cpu().numpy(), want))
+        cpu = {"value": round(csec * 1e3, 3), "unit": "ms", "cores": int(O.num_threads()), "kind": "port",
+               "sample": f"the whole unit (rotation + rescale of both components) once; bit-exact vs GPU: {ok}"}
+    achieved = C1_BYTES / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "ms per rotation + rescale (C1: 1 ct x 24 limbs)", "value": round(ms_wall, 4), "unit": "ms",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_wall, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+        "config": {"workload": "C1 single rotation by 5^1 + rescale, 24 -> 23 limbs, dnum 3, K 8",
+                   "algorithmic_bytes_per_step": C1_BYTES},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "rotation (5 fused key-switch kernels) + rescale", "ms_per_launch": round(ms, 4)},
+        "cpu_baseline": cpu}), flush=True)
     return 0
 
 
