@@ -46,10 +46,14 @@ SIGNATURES = {
     "hck_rescale": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_poly_op": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i64, _i64, _i64, _i, _ip, _u64p, _vp]),
     "hck_poly_from_signed": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _i, _ip, _vp]),
-    "hck_bsgs_mac": (_i, [_vp, _i, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64, _vp, _i64, _vp, _vp]),
+    "hck_bsgs_mac": (_i, [_vp, _i, _ip, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64, _vp, _i64, _vp,
+                          _vp]),
+    "hck_rotate_ext": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _sz, _vp]),
+    "hck_moddown_workspace_bytes": (_sz, [_vp, _i, _i]),
+    "hck_moddown": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_pack_diagonals": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "hck_encode_workspace_bytes": (_sz, [_vp, _i]),
-    "hck_encode_real": (_i, [_vp, _vp, _i, ctypes.c_double, _i, _ip, _vp, _i64, _vp, _sz, _vp, _vp]),
+    "hck_encode": (_i, [_vp, _vp, _vp, _i, ctypes.c_double, _i, _ip, _vp, _i64, _vp, _sz, _vp, _vp]),
 }
 
 _lib = None

@@ -107,13 +107,23 @@ class Client:
 
         ctx = self.context
         m = np.atleast_2d(np.asarray(m, dtype=np.int64))
-        B = m.shape[0]
+        idx = ctx.q_prime_idx(cur_limbs)
+        pt = ctx.from_signed(torch.from_numpy(m).to(ctx.device), idx)
+        ctx.ntt(pt, prime_idx=idx)
+        return self.encrypt_ntt(pt, cur_limbs, state, slots)
+
+    def encrypt_ntt(self, pt: torch.Tensor, cur_limbs: int, state: CipherState, slots: int) -> Cipher:
+        """Encrypt NTT-domain plaintexts pt ([batch][>= cur_limbs][N]): (pt + e - a s, a)."""
+
+        ctx = self.context
+        B = int(pt.shape[0])
         self._enc_counter += 1
         rng = _rng(ctx.spec.seed, "encrypt", self._enc_counter)
-        e = sample_gaussian(rng, m.shape, ctx.spec.error_sigma)
+        e = sample_gaussian(rng, (B, ctx.N), ctx.spec.error_sigma)
         idx = ctx.q_prime_idx(cur_limbs)
-        mpe = ctx.from_signed(torch.from_numpy(m + e).to(ctx.device), idx)
+        mpe = ctx.from_signed(torch.from_numpy(e).to(ctx.device), idx)
         ctx.ntt(mpe, prime_idx=idx)
+        ctx.poly_op(nat.HCK_OP_ADD, mpe, mpe, pt[:, :cur_limbs], prime_idx=idx)
         a = torch.from_numpy(sample_uniform(rng, ctx.primes[:cur_limbs], (B,), ctx.N)).to(ctx.device)
         s = self._s_ntt[:, :cur_limbs].expand(B, -1, -1)
         as_ = ctx.empty(B, cur_limbs, ctx.N)
@@ -130,11 +140,10 @@ class Client:
         slots = ctx.max_slots if slots is None else int(slots)
         cur_limbs = ctx.L if cur_limbs is None else int(cur_limbs)
         scale = ctx.scale_at(cur_limbs) if scaling_factor is None else float(scaling_factor)
-        vals = np.asarray(values)
-        rows = vals.reshape(1, -1) if vals.ndim <= 1 else vals.reshape(vals.shape[0], -1)
-        m = np.stack([encoding.encode(r, scale, ctx.logN, slots) for r in rows])
+        re, im = ctx.slot_rows(values, slots)
+        pt = ctx.encode(re, scale, cur_limbs, values_im=im)
         state = CipherState(cur_limbs=cur_limbs, scale_degree=1, scaling_factor=scale)
-        return self.encrypt_coeffs(m, cur_limbs, state, slots)
+        return self.encrypt_ntt(pt, cur_limbs, state, slots)
 
     def decrypt_coeffs(self, cipher: Cipher) -> np.ndarray:
         """Centered integer coefficients of c0 + c1 s (object array of Python ints, [batch][N])."""

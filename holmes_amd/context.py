@@ -301,6 +301,53 @@ class CKKSContext:
                   "hck_rotate")
         return out0, out1
 
+    def rotate_ext(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois: int, keys,
+                   out0: torch.Tensor | None = None, out1: torch.Tensor | None = None):
+        """Hoisted-form rotation ending in the extended basis: (P sigma(c0) + IP_b, IP_a) as
+        [batch][limbs + K][N] tensors (Q limbs, then the special primes); ``moddown`` of each
+        component gives ``rotate_raw``'s result bit for bit."""
+
+        self._check_poly(c0, limbs, self.N)
+        self._check_poly(c1, limbs, self.N)
+        if c0.stride(0) != c1.stride(0):
+            raise ValueError("c0 and c1 need the same batch stride")
+        B = c0.shape[0]
+        if isinstance(keys, torch.Tensor):
+            keys = [keys] * B
+        if len(keys) != B:
+            raise ValueError("one key per batch item")
+        for k in keys:
+            self._check_key(k)
+        ext = limbs + self.K
+        out0 = self.empty(B, ext, self.N) if out0 is None else out0
+        out1 = self.empty(B, ext, self.N) if out1 is None else out1
+        for o in (out0, out1):
+            self._check_poly(o, ext, self.N)
+            if o.shape[0] != B:
+                raise ValueError("outputs need one row per input")
+        if out0.stride(0) != out1.stride(0):
+            raise ValueError("out0 and out1 need the same batch stride")
+        L = nat.lib()
+        ws = self.workspace(L.hck_keyswitch_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_rotate_ext(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), c0.stride(0),
+                                   nat.ptr_array([k.data_ptr() for k in keys]), out0.data_ptr(), out1.data_ptr(),
+                                   out0.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                  "hck_rotate_ext")
+        return out0, out1
+
+    def moddown(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Extended-basis polys [polys][limbs + K][N] -> [polys][limbs][N] (divide by P, round)."""
+
+        self._check_poly(x, limbs + self.K, self.N)
+        out = self.empty(x.shape[0], limbs, self.N) if out is None else out
+        self._check_poly(out, limbs, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_moddown_workspace_bytes(self._h, limbs, x.shape[0]))
+        nat.check(L.hck_moddown(self._h, limbs, x.shape[0], x.data_ptr(), x.stride(0), out.data_ptr(),
+                                out.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                  "hck_moddown")
+        return out
+
     def rescale_raw(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
         self._check_poly(x, limbs, self.N)
         if limbs < 2:
@@ -314,9 +361,14 @@ class CKKSContext:
         return out
 
     def bsgs_mac(self, babies_c0, babies_c1, pts: torch.Tensor, limbs: int, giants: int,
-                 out: torch.Tensor | None = None) -> torch.Tensor:
+                 out: torch.Tensor | None = None, prime_idx=None) -> torch.Tensor:
         """Baby-step partial sums res[c][g][i] = sum_b pts[g*nb + b] * baby_b[i][c] (exact residues).
-        babies_c0/c1: one [inputs][>=limbs][N] tensor per baby step (same batch stride)."""
+        babies_c0/c1: one [inputs][>=limbs][N] tensor per baby step (same batch stride); limb l
+        uses prime prime_idx[l] (default: the first ``limbs`` Q primes)."""
+
+        prime_idx = self.q_prime_idx(limbs) if prime_idx is None else list(prime_idx)
+        if len(prime_idx) != limbs:
+            raise ValueError("one prime index per limb")
 
         nb = len(babies_c0)
         if nb != len(babies_c1) or nb < 1:
@@ -334,7 +386,7 @@ class CKKSContext:
             out = self.empty(2, giants, ni, limbs, self.N)
         if tuple(out.shape) != (2, giants, ni, limbs, self.N) or not out.is_contiguous():
             raise ValueError("out must be a contiguous [2][giants][inputs][limbs][N] tensor")
-        nat.check(nat.lib().hck_bsgs_mac(self._h, limbs, ni, nb, giants,
+        nat.check(nat.lib().hck_bsgs_mac(self._h, limbs, nat.int_array(prime_idx), ni, nb, giants,
                                          nat.ptr_array([t.data_ptr() for t in babies_c0]),
                                          nat.ptr_array([t.data_ptr() for t in babies_c1]), stride,
                                          pts.data_ptr(), pts.stride(0), out.data_ptr(),
@@ -355,27 +407,86 @@ class CKKSContext:
                   "hck_pack_diagonals")
         return out
 
-    def encode_real(self, values: torch.Tensor, scale: float, limbs: int,
-                    out: torch.Tensor | None = None, check: bool = True) -> torch.Tensor:
-        """Encode real slot rows [rows][N/2] (float64, device) into NTT-domain residues
-        [rows][limbs][N].  With ``check`` the overflow flags are read back (one host sync)."""
+    def slot_rows(self, values, slots: int):
+        """Values (one vector or [rows][slots]; numpy or torch, real or complex) -> device float64
+        (re, im or None) rows of N/2 slots: a sparse vector (slots < N/2) is tiled, which is its
+        encoding in the subring X^(N / 2 slots)."""
 
-        if values.dtype != torch.float64 or values.dim() != 2 or values.shape[1] != self.max_slots:
-            raise ValueError("values must be [rows][N/2] float64")
+        v = values
+        if isinstance(v, torch.Tensor):
+            v = v.detach().to(self.device)
+        else:
+            v = torch.from_numpy(np.asarray(v)).to(self.device)
+        if v.dim() <= 1:
+            v = v.reshape(1, -1)
+        else:
+            v = v.reshape(v.shape[0], -1)
+        n = int(v.shape[1])
+        slots = int(slots)
+        if n > slots or slots > self.max_slots or self.max_slots % slots or slots & (slots - 1):
+            raise ValueError(f"{n} values do not fit {slots} slots (a power of two up to {self.max_slots})")
+        if n < slots:
+            v = torch.nn.functional.pad(v, (0, slots - n))
+        reps = self.max_slots // slots
+        if torch.is_complex(v):
+            re = v.real.to(torch.float64).repeat(1, reps).contiguous()
+            im = v.imag.to(torch.float64).repeat(1, reps).contiguous()
+            return re, (im if bool(torch.any(im != 0)) else None)
+        return v.to(torch.float64).repeat(1, reps).contiguous(), None
+
+    def encode(self, values: torch.Tensor, scale: float, limbs: int, *, values_im: torch.Tensor | None = None,
+               prime_idx=None, out: torch.Tensor | None = None, flags: torch.Tensor | None = None) -> torch.Tensor:
+        """Encode slot rows [rows][N/2] (float64 on the device: real parts, optional imaginary parts)
+        into NTT-domain residues [rows][limbs][N], limb l modulo prime prime_idx[l] (default: the
+        first ``limbs`` Q primes; ``ext_prime_idx`` gives an extended-basis plaintext).
+
+        Overflow (a coefficient reaching 2^52) sets an int32 device flag per row.  Without
+        ``flags`` they are read back here (one host sync) and raise; with a caller-owned
+        ``flags`` tensor ([>= rows] int32, zeroed once) the flags accumulate there for one check
+        at the caller's next synchronisation point (``check_encode_flags``)."""
+
+        for v in (values,) + ((values_im,) if values_im is not None else ()):
+            if v.dtype != torch.float64 or v.dim() != 2 or v.shape[1] != self.max_slots:
+                raise ValueError("values must be [rows][N/2] float64")
+            if v.device.type != "cuda":
+                raise ValueError("values must live on the GPU")
         values = values.contiguous()
         rows = int(values.shape[0])
+        if values_im is not None:
+            if values_im.shape[0] != rows:
+                raise ValueError("values_im needs one row per values row")
+            values_im = values_im.contiguous()
+        prime_idx = self.q_prime_idx(limbs) if prime_idx is None else list(prime_idx)
+        if len(prime_idx) != int(limbs):
+            raise ValueError("one prime index per limb")
         if out is None:
             out = self.empty(rows, limbs, self.N)
         self._check_poly(out, limbs, self.N)
+        own = flags is None
+        if own:
+            flags = torch.zeros(max(rows, 1), dtype=torch.int32, device=self.device)
+        elif flags.dtype != torch.int32 or flags.numel() < rows or not flags.is_contiguous():
+            raise ValueError("flags must be a contiguous int32 tensor with one entry per row")
         L = nat.lib()
-        ws = torch.empty(L.hck_encode_workspace_bytes(self._h, rows), dtype=torch.uint8, device=self.device)
-        flags = torch.zeros(max(rows, 1), dtype=torch.int32, device=self.device)
-        nat.check(L.hck_encode_real(self._h, values.data_ptr(), rows, float(scale), int(limbs),
-                                    nat.int_array(range(limbs)), out.data_ptr(), out.stride(0), ws.data_ptr(),
-                                    ws.numel(), flags.data_ptr(), _stream_ptr(self.device)), "hck_encode_real")
-        if check and bool(flags.any().item()):
-            raise ValueError("encoded coefficient reached 2^52: lower the scale or the value range")
+        ws = self.workspace(L.hck_encode_workspace_bytes(self._h, rows))
+        nat.check(L.hck_encode(self._h, values.data_ptr(), values_im.data_ptr() if values_im is not None else None,
+                               rows, float(scale), int(limbs), nat.int_array(prime_idx), out.data_ptr(),
+                               out.stride(0), ws.data_ptr(), ws.numel(), flags.data_ptr(),
+                               _stream_ptr(self.device)), "hck_encode")
+        if own:
+            self.check_encode_flags(flags)
         return out
+
+    @staticmethod
+    def check_encode_flags(flags: torch.Tensor) -> None:
+        if bool(flags.any().item()):
+            raise ValueError("encoded coefficient reached 2^52: lower the scale or the value range")
+
+    def encode_real(self, values: torch.Tensor, scale: float, limbs: int, out: torch.Tensor | None = None,
+                    flags: torch.Tensor | None = None) -> torch.Tensor:
+        """Real slot rows [rows][N/2] -> NTT-domain residues over the first ``limbs`` Q primes."""
+
+        return self.encode(values, scale, limbs, out=out, flags=flags)
 
     def _check_key(self, k: torch.Tensor) -> None:
         shape = (2, self.beta_max, self.L + self.K, self.N)

@@ -8,7 +8,8 @@
 //
 // A thread owns one coefficient of one limb and a TI x TG tile of (input, giant) accumulators for
 // both components: per baby step it reads TG plaintext words and 2 TI baby words for 2 TI TG
-// products, so plaintexts stream once per input tile and babies once per giant tile.  All tiles
+// products (the next step's words are loaded while the current step computes), so plaintexts
+// stream once per input tile and babies once per giant tile.  All tiles
 // of one (limb, 128-coefficient) unit are dispatched to the same XCD (workgroups are handed to
 // the 8 XCDs round-robin by linear id), so the unit's plaintext and baby data is fetched from HBM
 // once and then served from that XCD's L2.
@@ -21,20 +22,53 @@ namespace hck {
 namespace {
 
 constexpr int kMacThreads = 128;
-constexpr int kTI = 4;          // inputs per thread
-constexpr int kTG = 4;          // giants per thread
+// Register tile: inputs x giants per thread (both components).  Tunable at build time.
+#ifndef HCK_MAC_TI
+#define HCK_MAC_TI 4
+#endif
+#ifndef HCK_MAC_TG
+#define HCK_MAC_TG 8
+#endif
+constexpr int kTI = HCK_MAC_TI;
+constexpr int kTG = HCK_MAC_TG;
 constexpr int kMaxBabies = 64;
 
 struct BabyPtrs {
   const uint64_t* c0[kMaxBabies];
   const uint64_t* c1[kMaxBabies];
 };
+struct MacPrimes {
+  uint8_t prime[kMaxPrimes];
+};
+
+// One baby step's operands for a thread: TG plaintext words, TI words of each component.
+struct MacOps {
+  uint64_t w[kTG], x0[kTI], x1[kTI];
+};
+
+__device__ __forceinline__ void mac_load(MacOps& o, const BabyPtrs& babies, int b, int nb, int G, int ni,
+                                         int g0, int i0, const uint64_t* __restrict__ pts, long long pt_stride,
+                                         long long baby_stride, long long ln) {
+#pragma unroll
+  for (int g = 0; g < kTG; ++g) {
+    const int gg = g0 + g < G ? g0 + g : g0;  // clamp: duplicates are never stored
+    o.w[g] = pts[((long long)gg * nb + b) * pt_stride + ln];
+  }
+  const uint64_t* b0 = babies.c0[b];
+  const uint64_t* b1 = babies.c1[b];
+#pragma unroll
+  for (int t = 0; t < kTI; ++t) {
+    const int ii = i0 + t < ni ? i0 + t : i0;
+    o.x0[t] = b0[(long long)ii * baby_stride + ln];
+    o.x1[t] = b1[(long long)ii * baby_stride + ln];
+  }
+}
 
 __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__ res, BabyPtrs babies,
                                                           long long baby_stride, int nb, int ni, int G,
                                                           const uint64_t* __restrict__ pts, long long pt_stride,
-                                                          int limbs, int units_per_limb, int tiles_i, int tiles_g,
-                                                          int total_units, DevTables T) {
+                                                          int limbs, MacPrimes mp, int units_per_limb,
+                                                          int tiles_i, int tiles_g, int total_units, DevTables T) {
   // XCD-aware decode of the linear workgroup id into (unit, tile)
   const int tiles = tiles_i * tiles_g;
   const int lin = blockIdx.x;
@@ -45,7 +79,8 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
   const int l = unit / units_per_limb;
   const int n = (unit % units_per_limb) * kMacThreads + threadIdx.x;
   const int i0 = (tile % tiles_i) * kTI, g0 = (tile / tiles_i) * kTG;
-  const double p = T.p[l], pinv = T.pinv[l];
+  const int pi = mp.prime[l];
+  const double p = T.p[pi], pinv = T.pinv[pi];
   const long long ln = (long long)l * kN + n;
   double acc[kTI][2][kTG];
 #pragma unroll
@@ -54,21 +89,20 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int g = 0; g < kTG; ++g) acc[t][c][g] = 0.0;
+  // two-stage software pipeline: baby step b + 1's loads are in flight while b computes
+  MacOps cur, nxt;
+  mac_load(cur, babies, 0, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
   for (int b = 0; b < nb; ++b) {
+    if (b + 1 < nb) mac_load(nxt, babies, b + 1, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
     double w[kTG], wp[kTG];
 #pragma unroll
     for (int g = 0; g < kTG; ++g) {
-      const int gg = g0 + g < G ? g0 + g : g0;  // clamp: duplicates are never stored
-      w[g] = u2d(pts[((long long)gg * nb + b) * pt_stride + ln]);
+      w[g] = u2d(cur.w[g]);
       wp[g] = w[g] * pinv;
     }
-    const uint64_t* b0 = babies.c0[b];
-    const uint64_t* b1 = babies.c1[b];
 #pragma unroll
     for (int t = 0; t < kTI; ++t) {
-      const int ii = i0 + t < ni ? i0 + t : i0;
-      const double x0 = u2d(b0[(long long)ii * baby_stride + ln]);
-      const double x1 = u2d(b1[(long long)ii * baby_stride + ln]);
+      const double x0 = u2d(cur.x0[t]), x1 = u2d(cur.x1[t]);
 #pragma unroll
       for (int g = 0; g < kTG; ++g) {
         acc[t][0][g] += mulc(x0, w[g], wp[g], p);  // canonical operands: |term| <= 0.875 p
@@ -83,6 +117,7 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
 #pragma unroll
           for (int g = 0; g < kTG; ++g) acc[t][c][g] = reduce(acc[t][c][g], p, pinv);
     }
+    cur = nxt;
   }
   const long long is = (long long)limbs * kN, gs = (long long)ni * is, cs = (long long)G * gs;
 #pragma unroll
@@ -100,13 +135,18 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
 }  // namespace
 }  // namespace hck
 
-extern "C" int hck_bsgs_mac(const hck_context* ctx, int limbs, int inputs, int babies, int giants,
-                            const uint64_t* const* baby_c0, const uint64_t* const* baby_c1,
+extern "C" int hck_bsgs_mac(const hck_context* ctx, int limbs, const int* prime_idx, int inputs, int babies,
+                            int giants, const uint64_t* const* baby_c0, const uint64_t* const* baby_c1,
                             int64_t baby_stride, const uint64_t* pts, int64_t pt_stride, uint64_t* res,
                             void* stream) {
-  if (!ctx || !baby_c0 || !baby_c1 || !pts || !res) return HCK_ERR_ARG;
-  if (limbs < 1 || limbs > ctx->L || inputs < 1 || babies < 1 || babies > hck::kMaxBabies || giants < 1)
+  if (!ctx || !prime_idx || !baby_c0 || !baby_c1 || !pts || !res) return HCK_ERR_ARG;
+  if (limbs < 1 || limbs > hck::kMaxPrimes || inputs < 1 || babies < 1 || babies > hck::kMaxBabies || giants < 1)
     return HCK_ERR_ARG;
+  hck::MacPrimes mp{};
+  for (int l = 0; l < limbs; ++l) {
+    if (prime_idx[l] < 0 || prime_idx[l] >= ctx->np) return HCK_ERR_ARG;
+    mp.prime[l] = (uint8_t)prime_idx[l];
+  }
   hck::BabyPtrs bp{};
   for (int b = 0; b < babies; ++b) {
     if (!baby_c0[b] || !baby_c1[b]) return HCK_ERR_ARG;
@@ -121,7 +161,7 @@ extern "C" int hck_bsgs_mac(const hck_context* ctx, int limbs, int inputs, int b
   const long long blocks = units_padded * tiles;
   if (blocks > 0x7fffffffLL) return HCK_ERR_ARG;
   hck::k_bsgs_mac<<<dim3((unsigned)blocks), hck::kMacThreads, 0, (hipStream_t)stream>>>(
-      res, bp, baby_stride, babies, inputs, giants, pts, pt_stride, limbs, units_per_limb, tiles_i, tiles_g,
+      res, bp, baby_stride, babies, inputs, giants, pts, pt_stride, limbs, mp, units_per_limb, tiles_i, tiles_g,
       total_units, ctx->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;

@@ -122,7 +122,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   // host tables
   std::vector<double> hp(np), hpinv(np);
   std::vector<double> fwd((size_t)np * n), inv((size_t)np * n);
-  std::vector<hck::TwPair> ninv(np), ninv_w1(np), zeta4(np);
+  std::vector<hck::TwPair> ninv(np), ninv_w1(np), zeta4(np), pmodq(np);
   for (int i = 0; i < np; ++i) {
     const u64 q = P[i];
     hp[i] = (double)q;
@@ -141,6 +141,9 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     // the inverse transform's last stage uses psi_rev_inv[1]; folding N^-1 into it saves a pass
     ninv_w1[i] = pair_of(mulmod(ni, (u64)inv[(size_t)i * n + 1], q), q);
     zeta4[i] = pair_of(powmod(psi, n / 2, q), q);
+    u64 pm = 1;
+    for (int k = 0; k < num_p; ++k) pm = mulmod(pm, P[num_q + k] % q, q);
+    pmodq[i] = pair_of(pm, q);
   }
 
   // encoder roots: stage of half-width h (1 <= h < N/2) at [h - 1, 2h - 1), entry j =
@@ -206,6 +209,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   const size_t o_ninv = off; off = align(off + np * sizeof(hck::TwPair));
   const size_t o_nw1 = off; off = align(off + np * sizeof(hck::TwPair));
   const size_t o_z4 = off; off = align(off + np * sizeof(hck::TwPair));
+  const size_t o_pmq = off; off = align(off + np * sizeof(hck::TwPair));
   const size_t o_mu = off; off = align(off + c->h_modup.size() * sizeof(hck::ConvConsts));
   const size_t o_md = off; off = align(off + c->h_moddown.size() * sizeof(hck::ConvConsts));
   const size_t o_lv = off; off = align(off + c->h_level.size() * sizeof(hck::LevelConsts));
@@ -224,6 +228,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       {o_ninv, ninv.data(), np * sizeof(hck::TwPair)},
       {o_nw1, ninv_w1.data(), np * sizeof(hck::TwPair)},
       {o_z4, zeta4.data(), np * sizeof(hck::TwPair)},
+      {o_pmq, pmodq.data(), np * sizeof(hck::TwPair)},
       {o_mu, c->h_modup.data(), c->h_modup.size() * sizeof(hck::ConvConsts)},
       {o_md, c->h_moddown.data(), c->h_moddown.size() * sizeof(hck::ConvConsts)},
       {o_lv, c->h_level.data(), c->h_level.size() * sizeof(hck::LevelConsts)},
@@ -244,6 +249,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->dev.ninv = (const hck::TwPair*)(base + o_ninv);
   c->dev.ninv_w1 = (const hck::TwPair*)(base + o_nw1);
   c->dev.zeta4 = (const hck::TwPair*)(base + o_z4);
+  c->dev.pmodq = (const hck::TwPair*)(base + o_pmq);
   c->d_modup = (hck::ConvConsts*)(base + o_mu);
   c->d_moddown = (hck::ConvConsts*)(base + o_md);
   c->d_level = (hck::LevelConsts*)(base + o_lv);

@@ -54,17 +54,23 @@ __global__ __launch_bounds__(256) void k_pack_diagonals(const double* __restrict
 }
 
 // Column pass: block = 16 columns x 256 rows of one row-vector; thread (cl, j) holds rows j + 16k
-// (stages 16384 .. 2048) then rows 16j + k (stages 1024 .. 128).  Input: real values (imag 0).
-__global__ __launch_bounds__(256) void k_sifft_cols(const double* __restrict__ vals, double* __restrict__ vre,
+// (stages 16384 .. 2048) then rows 16j + k (stages 1024 .. 128).  Input: real parts, and
+// imaginary parts when vals_im is given (else 0).
+__global__ __launch_bounds__(256) void k_sifft_cols(const double* __restrict__ vals,
+                                                    const double* __restrict__ vals_im, double* __restrict__ vre,
                                                     double* __restrict__ vim, const double* __restrict__ twr,
                                                     const double* __restrict__ twi) {
   __shared__ double S[16 * 272];
   const long long row = blockIdx.y;
   const double* v = vals + row * kSlots;
+  const double* vi = vals_im ? vals_im + row * kSlots : nullptr;
   const int t = threadIdx.x, cl = t & 15, j = t >> 4, c = blockIdx.x * 16 + cl;
   Cx x[16];
 #pragma unroll
-  for (int k = 0; k < 16; ++k) x[k] = Cx{v[(j + 16 * k) * 128 + c], 0.0};
+  for (int k = 0; k < 16; ++k) {
+    const int at = (j + 16 * k) * 128 + c;
+    x[k] = Cx{v[at], vi ? vi[at] : 0.0};
+  }
   // rows r = j + 16k: half-width 128 * 2^tt pairs r and r + 2^tt, tt = 7 .. 4 (k bits 3 .. 0)
 #pragma unroll
   for (int tt = 7; tt >= 4; --tt) {
@@ -227,9 +233,9 @@ extern "C" size_t hck_encode_workspace_bytes(const hck_context* ctx, int rows) {
   return (size_t)rows * hck::kSlots * 2 * sizeof(double) + (size_t)rows * sizeof(int) + 256;
 }
 
-extern "C" int hck_encode_real(const hck_context* ctx, const double* values, int rows, double scale, int limbs,
-                               const int* prime_idx, uint64_t* out, int64_t out_row_stride, void* workspace,
-                               size_t workspace_bytes, int* overflow_flags, void* stream) {
+extern "C" int hck_encode(const hck_context* ctx, const double* values, const double* values_im, int rows,
+                          double scale, int limbs, const int* prime_idx, uint64_t* out, int64_t out_row_stride,
+                          void* workspace, size_t workspace_bytes, int* overflow_flags, void* stream) {
   if (!ctx || !values || !out || !prime_idx || !overflow_flags || rows < 0 || rows > 65535) return HCK_ERR_ARG;
   if (limbs < 1 || limbs > hck::kMaxPrimes || !(scale > 0.0)) return HCK_ERR_ARG;
   if (rows == 0) return HCK_OK;
@@ -246,7 +252,8 @@ extern "C" int hck_encode_real(const hck_context* ctx, const double* values, int
   hipStream_t s = (hipStream_t)stream;
   double* vre = (double*)workspace;
   double* vim = vre + (size_t)rows * hck::kSlots;
-  hck::k_sifft_cols<<<dim3(128 / 16, rows), 256, 0, s>>>(values, vre, vim, ctx->d_enc_twr, ctx->d_enc_twi);
+  hck::k_sifft_cols<<<dim3(128 / 16, rows), 256, 0, s>>>(values, values_im, vre, vim, ctx->d_enc_twr,
+                                                          ctx->d_enc_twi);
   HCK_CHECK_LAUNCH();
   hck::k_sifft_rows<<<dim3(256 / 32, rows), 256, 0, s>>>(vre, vim, ctx->d_enc_twr, ctx->d_enc_twi);
   HCK_CHECK_LAUNCH();

@@ -38,6 +38,7 @@ struct DevTables {
   const TwPair* ninv;   // [np]: N^-1
   const TwPair* ninv_w1;// [np]: N^-1 * psi_rev_inv[1] (last inverse stage folded with N^-1)
   const TwPair* zeta4;  // [np]: psi^(N/2), a primitive 4th root of unity (multiplication by X^(N/2))
+  const TwPair* pmodq;  // [np]: P = prod of the special primes, mod each prime (0 for the special ones)
 };
 
 }  // namespace hck
@@ -85,7 +86,12 @@ size_t ks_fused_bytes(const hck_context* c, int ell, int batch);
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
-             char* ws, hipStream_t s);
+             char* ws, hipStream_t s, uint64_t* ext_b = nullptr, uint64_t* ext_a = nullptr,
+             long long ext_stride = 0);
+// ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
+size_t moddown_bytes(const hck_context* c, int ell, int polys);
+int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                long long out_stride, char* ws, hipStream_t s);
 
 // MI355X deals consecutive workgroups to its 8 XCDs (each with its own L2) round-robin.
 constexpr int kXcds = 8;

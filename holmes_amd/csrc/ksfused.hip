@@ -25,6 +25,8 @@
 // F.cv_moddown; bench/cmp/report.py:26-30); key layout llama3fhe/parallel/prefill/keys.py:105-117.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
 
@@ -288,15 +290,19 @@ __device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restric
 }
 
 // ----------------------------------------------------------------- K1: INTT rows of d
+// Limb i (< gridDim.z) of poly b reads input limb limb0 + i under prime prime0 + i and writes
+// output limb i of a gridDim.z-limb transposed poly.
 __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
-                                                     uint32_t g, double* __restrict__ t1, int ell, DevTables T) {
+                                                     uint32_t g, int limb0, int prime0, double* __restrict__ t1,
+                                                     DevTables T) {
   __shared__ double S[kRowLds];
   const int i = blockIdx.z, b = blockIdx.x, r0 = blockIdx.y * 16;
-  const double p = T.p[i], pinv = T.pinv[i];
-  const double* __restrict__ tw = T.tw_inv + (size_t)i * kN;
+  const int pi = prime0 + i;
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   double x[16];
-  load_gal(x, d + (long long)b * d_stride + (long long)i * kN, nat_a(r0), g);
-  rows_inv_to_t(x, t1 + ((long long)b * ell + i) * kN, r0, S, tw, p, pinv);
+  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(r0), g);
+  rows_inv_to_t(x, t1 + ((long long)b * gridDim.z + i) * kN, r0, S, tw, p, pinv);
 }
 
 // ----------------------------------------------------------------- K2 / K4: cols + conversion
@@ -390,10 +396,15 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
 // dealt to the 8 XCDs round-robin; the decode keeps every ciphertext of one tile on one XCD, one
 // after another, so a key shared by the batch (a giant step) is read from HBM once per tile and
 // served from that XCD's L2 to the other ciphertexts.
+// With ext_b set the kernel ends the key switch in the extended basis: it writes (P * sigma(add) +
+// IP_b, IP_a) over Q u P as canonical NTT-domain residues to ext_b / ext_a ([ell + K] limbs per
+// ciphertext, Q limbs first) and skips the ModDown inputs.
 __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
                                                    const double* __restrict__ t2, KeyPtrsF keys, int ell,
                                                    int beta, int batch, int tiles, double* __restrict__ accq,
-                                                   double* __restrict__ accp, DevTables T) {
+                                                   double* __restrict__ accp, const uint64_t* __restrict__ add,
+                                                   long long add_stride, uint64_t* __restrict__ ext_b,
+                                                   uint64_t* __restrict__ ext_a, long long ext_stride, DevTables T) {
   __shared__ double S[kRowLds];
   const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
   const int tile = (q / batch) * kXcds + xcd, b = q % batch;
@@ -435,6 +446,23 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
   }
 #pragma unroll
   for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+  if (ext_b) {
+    if (e < ell && add) {
+      double ad[16];
+      load_gal(ad, add + (long long)b * add_stride + (long long)e * kN, na, g);
+      const TwPair pm = T.pmodq[pi];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sb[k] += mulc(ad[k], pm, p);  // |sb| <= 1.5 p
+    }
+    uint64_t* ob = ext_b + (long long)b * ext_stride + (long long)e * kN + na;
+    uint64_t* oa = ext_a + (long long)b * ext_stride + (long long)e * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      ob[16 * k] = d2u(canon(sb[k], p, pinv));
+      oa[16 * k] = d2u(canon(sa[k], p, pinv));
+    }
+    return;
+  }
   if (e < ell) {
     double* ob = accq + ((long long)b * 2 * ell + e) * kN + na;
 #pragma unroll
@@ -449,7 +477,12 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
 }
 
 // ----------------------------------------------------------------- K5: NTT rows + ModDown combine
-__global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const double* __restrict__ accq,
+// Poly p = blockIdx.x (= 2 b + comp): v = NTT rows of T4[p]; out = (ACCQ[p] - v) * P^-1 (+ addends).
+// ACCQ is the inner product's lazy FP64 output (key switch) or canonical u64 residues (ModDown of
+// an extended-basis ciphertext); accq_pstride is its per-poly stride in elements.
+template <typename AccT>
+__global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const AccT* __restrict__ accq,
+                                                       long long accq_pstride,
                                                        const uint64_t* __restrict__ add, long long add_stride,
                                                        uint32_t g, const uint64_t* __restrict__ acc_b,
                                                        const uint64_t* __restrict__ acc_a, long long acc_stride,
@@ -464,9 +497,12 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
   const long long na = nat_a(r0);
   // prefetch the accumulator (and the rotation addend) before the transform
   double a[16];
-  const double* ap = accq + (((long long)b * 2 + comp) * ell + i) * kN + na;
+  const AccT* ap = accq + (long long)blockIdx.x * accq_pstride + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) a[k] = ap[16 * k];
+  for (int k = 0; k < 16; ++k) {
+    if constexpr (std::is_same<AccT, uint64_t>::value) a[k] = u2d(ap[16 * k]);
+    else a[k] = ap[16 * k];
+  }
   double ad[16], ac[16];
   const bool has_add = comp == 0 && add;
   if (has_add) load_gal(ad, add + (long long)b * add_stride + (long long)i * kN, na, g);
@@ -497,7 +533,7 @@ size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
-             char* ws, hipStream_t s) {
+             char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride) {
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch > kMaxBatchF) return HCK_ERR_ARG;
   const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
@@ -508,7 +544,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   double* accp = accq + (long long)batch * 2 * ell * n;
   // K1
   // row kernels: ciphertext index fastest, so the blocks in flight share one prime's twiddles
-  k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, galois, r1, ell, c->dev);
+  k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, galois, 0, 0, r1, c->dev);
   HCK_CHECK_LAUNCH();
   // K2: ModUp, one block per (column pair, digit, ciphertext)
   k_ks_cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
@@ -521,17 +557,45 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   const int tiles = 16 * ext_l;
   const int groups = (tiles + kXcds - 1) / kXcds;
   k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
-                                                          accq, accp, c->dev);
+                                                          accq, accp, add, add_stride, ext_b, ext_a, ext_stride,
+                                                          c->dev);
   HCK_CHECK_LAUNCH();
+  if (ext_b) return HCK_OK;
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
   double* t4 = r1;
   k_ks_cols_conv<<<dim3(128, 2, batch), kT, 0, s>>>(accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n,
                                                     (long long)ell * n, c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
   // K5
-  k_ks_rows_finish<<<dim3(2 * batch, 16, ell), kT, 0, s>>>(t4, accq, add, add_stride, galois, acc_b, acc_a,
-                                                           acc_stride, out_b, out_a, out_stride, ell,
-                                                           c->d_level + ell, c->dev);
+  k_ks_rows_finish<double><<<dim3(2 * batch, 16, ell), kT, 0, s>>>(t4, accq, (long long)ell * n, add, add_stride,
+                                                                   galois, acc_b, acc_a, acc_stride, out_b, out_a,
+                                                                   out_stride, ell, c->d_level + ell, c->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+size_t moddown_bytes(const hck_context* c, int ell, int polys) {
+  return (size_t)polys * kN * 8 * (size_t)(c->K + ell);
+}
+
+// ModDown of extended-basis polys in[p] ([ell + K] canonical NTT-domain limbs, Q first):
+// out[p] = (x_Q - NTT(conv(INTT(x_P)))) * P^-1 over the ell Q primes.
+int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                long long out_stride, char* ws, hipStream_t s) {
+  if (c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
+  const int K = c->K;
+  const long long n = kN;
+  double* tp = (double*)ws;                       // [polys][K] transposed
+  double* t4 = tp + (long long)polys * K * n;     // [polys][ell] transposed
+  k_ks_intt_rows<<<dim3(polys, 16, K), kT, 0, s>>>(in, in_stride, 1u, ell, c->L, tp, c->dev);
+  HCK_CHECK_LAUNCH();
+  k_ks_cols_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
+                                                    c->d_moddown + ell, 0, c->dev);
+  HCK_CHECK_LAUNCH();
+  // poly p = 2 b + comp: out_b / out_a interleave at out_stride, so p lands at out + p * out_stride
+  k_ks_rows_finish<uint64_t><<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, nullptr, 0, 1u, nullptr, nullptr,
+                                                                 0, out, out + out_stride, 2 * out_stride, ell,
+                                                                 c->d_level + ell, c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }

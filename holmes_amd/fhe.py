@@ -14,7 +14,6 @@ import numpy as np
 import torch
 
 from . import _native as nat
-from . import encoding
 from .client import Client
 from .context import Cipher, CipherState, CKKSContext
 from .params import CKKSContextSpec
@@ -38,6 +37,13 @@ __all__ = [
     "encode_plaintext",
     "PackedRaw",
     "ConstantBundle",
+    "pack_cipher_batch",
+    "unpack_cipher_batch",
+    "fast_rotate",
+    "moddown_from_ext",
+    "grouped_pairwise_mac",
+    "prepare_hoisted_baby_rotations",
+    "hoisted_mac_sum",
 ]
 
 
@@ -205,17 +211,16 @@ def homo_mul_i(ct: Cipher, ctx: CKKSContext, negative: bool = False) -> Cipher:
     return ct.cipher_like(out)
 
 
-def encode_plaintext(values, state: CipherState, slots: int, ctx: CKKSContext) -> Plaintext:
-    """Encode real/complex ``values`` at ``state`` (limbs, scale) into the NTT domain."""
+def encode_plaintext(values, state: CipherState, slots: int, ctx: CKKSContext, is_ext: bool = False) -> Plaintext:
+    """Encode real/complex ``values`` at ``state`` (limbs, scale) into the NTT domain on the GPU
+    (special IFFT, rounding and per-limb reduction, forward NTT); ``is_ext`` adds the special
+    primes (a plaintext for extended-basis products)."""
 
-    vals = np.asarray(values)
-    rows = vals.reshape(1, -1) if vals.ndim <= 1 else vals.reshape(vals.shape[0], -1)
-    m = np.stack([encoding.encode(r, float(state.scaling_factor), ctx.logN, slots) for r in rows])
+    re, im = ctx.slot_rows(values, slots)
     limbs = int(state.cur_limbs)
-    idx = ctx.q_prime_idx(limbs)
-    poly = ctx.from_signed(torch.from_numpy(m).to(ctx.device), idx)
-    ctx.ntt(poly, prime_idx=idx)
-    return Plaintext(poly, state, slots=slots)
+    idx = ctx.ext_prime_idx(limbs) if is_ext else ctx.q_prime_idx(limbs)
+    poly = ctx.encode(re, float(state.scaling_factor), len(idx), values_im=im, prime_idx=idx)
+    return Plaintext(poly, state, slots=slots, is_ext=is_ext)
 
 
 def homo_mul_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
@@ -268,14 +273,14 @@ class ConstantBundle:
 
     def plaintext(self, name: str, state: CipherState, slots: int, context: CKKSContext,
                   is_ext: bool = False, cache: bool | None = None) -> Plaintext:
-        if is_ext:
-            raise ValueError("extended-basis plaintexts are not supported by this backend")
-        key = (str(name), int(state.cur_limbs), float(state.scaling_factor), int(slots))
+        key = (str(name), int(state.cur_limbs), float(state.scaling_factor), int(slots), bool(is_ext))
         keep = self.cache_mode in ("plain", "both") if cache is None else bool(cache)
         hit = self._cache.get(key)
         if hit is not None:
             return hit
-        pt = encode_plaintext(self.vectors[str(name)].numpy(), state, int(slots), context)
+        v = self.vectors[str(name)]
+        v = v.values if isinstance(v, PackedRaw) else v
+        pt = encode_plaintext(v, state, int(slots), context, is_ext=bool(is_ext))
         if keep:
             self._cache[key] = pt
         return pt
@@ -286,3 +291,213 @@ class ConstantBundle:
 
     def clear_cache(self) -> None:
         self._cache.clear()
+
+
+# ---------------------------------------------------------------------- hoisted / batched surface
+def pack_cipher_batch(ciphers) -> Cipher:
+    """Stack ciphertexts (same level, scale and basis) into one batch cipher, rows in order."""
+
+    ciphers = tuple(ciphers)
+    if not ciphers:
+        raise ValueError("pack_cipher_batch needs at least one ciphertext")
+    first = ciphers[0]
+    for c in ciphers[1:]:
+        if (c.is_ext != first.is_ext or int(c.state.cur_limbs) != int(first.state.cur_limbs)
+                or int(c.state.scale_degree) != int(first.state.scale_degree)):
+            raise ValueError("pack_cipher_batch: ciphertexts differ in level, scale degree or basis")
+    rows = int(first.cv[0].shape[1]) if first.is_ext else _limbs(first)
+    cv = [torch.cat([c.cv[i][:, :rows] for c in ciphers], 0).contiguous() for i in range(2)]
+    return first.cipher_like(cv, batch_size=int(cv[0].shape[0]))
+
+
+def unpack_cipher_batch(batch: Cipher) -> tuple:
+    """One cipher per batch row (views of the batch tensors: no copy)."""
+
+    return tuple(batch.cipher_like([c[i:i + 1] for c in batch.cv], batch_size=1) for i in range(batch.batch_size))
+
+
+def _lift_ext(x: torch.Tensor, limbs: int, ctx: CKKSContext) -> torch.Tensor:
+    """[B][limbs][N] -> its extended-basis form P * x: [B][limbs + K][N], zero on the special
+    primes (ModDown returns x exactly)."""
+
+    P = 1
+    for p in ctx.primes[ctx.L:ctx.L + ctx.K]:
+        P *= int(p)
+    out = ctx.zeros(x.shape[0], limbs + ctx.K, ctx.N)
+    ctx.poly_op(nat.HCK_OP_MUL_SCALAR, out[:, :limbs], _view(x, limbs), prime_idx=ctx.q_prime_idx(limbs),
+                scalar=[P % int(q) for q in ctx.primes[:limbs]])
+    return out
+
+
+def fast_rotate(ct: Cipher, offsets, ctx: CKKSContext, output_ext: bool = False) -> Cipher:
+    """Rotations of ``ct`` by each offset as one batch cipher (row o * B + b = item b rotated by
+    offsets[o]).  ``output_ext`` stops every rotation in the extended basis (no ModDown): the
+    rows are then summed or multiplied there and closed by one ``moddown_from_ext``
+    (llama3fhe/operators/attention/prefill/input.py:1669-1687, shifted_lane.py:76)."""
+
+    if ct.is_ext:
+        raise ValueError("fast_rotate expects a non-extended ciphertext")
+    offsets = [int(o) for o in offsets]
+    if not offsets:
+        raise ValueError("fast_rotate needs at least one offset")
+    limbs = _limbs(ct)
+    c0, c1 = _view(ct.cv[0], limbs), _view(ct.cv[1], limbs)
+    B = ct.batch_size
+    rows = limbs + (ctx.K if output_ext else 0)
+    out0 = ctx.empty(len(offsets) * B, rows, ctx.N)
+    out1 = ctx.empty(len(offsets) * B, rows, ctx.N)
+    for i, off in enumerate(offsets):
+        o0, o1 = out0[i * B:(i + 1) * B], out1[i * B:(i + 1) * B]
+        if off % ctx.max_slots == 0 and off != ctx.M - 1:
+            if output_ext:
+                o0.copy_(_lift_ext(c0, limbs, ctx))
+                o1.copy_(_lift_ext(c1, limbs, ctx))
+            else:
+                o0.copy_(c0)
+                o1.copy_(c1)
+            continue
+        g = _galois(off, ctx)
+        key = ctx.key_for_galois(g)
+        if output_ext:
+            ctx.rotate_ext(c0, c1, limbs, g, key, out0=o0, out1=o1)
+        else:
+            ctx.rotate_raw(c0, c1, limbs, g, key, out0=o0, out1=o1)
+    return ct.cipher_like([out0, out1], is_ext=bool(output_ext), batch_size=len(offsets) * B)
+
+
+def moddown_from_ext(ct: Cipher, ctx: CKKSContext) -> Cipher:
+    """Close an extended-basis cipher: divide by P (rounded) back to its Q limbs."""
+
+    if not ct.is_ext:
+        raise ValueError("moddown_from_ext expects an extended-basis ciphertext")
+    limbs = _limbs(ct)
+    out = [ctx.moddown(c, limbs) for c in ct.cv]
+    return ct.cipher_like(out, is_ext=False)
+
+
+def grouped_pairwise_mac(batch: Cipher, pts: Plaintext, groups: int, ctx: CKKSContext) -> Cipher:
+    """Row-wise products summed within ``groups`` equal consecutive groups of rows:
+    out[g] = sum_{r in group g} pts[r] * batch[r] (exact residues; extended-basis rows need an
+    extended-basis plaintext).  Scale degrees and factors multiply."""
+
+    groups = int(groups)
+    R = batch.batch_size
+    if groups < 1 or R % groups:
+        raise ValueError(f"{R} rows do not split into {groups} groups")
+    if bool(pts.is_ext) != bool(batch.is_ext):
+        raise ValueError("plaintext and ciphertext bases differ (extended vs not)")
+    if pts.batch_size != R:
+        raise ValueError(f"expected {R} plaintext rows, got {pts.batch_size}")
+    limbs = _limbs(batch)
+    idx = ctx.ext_prime_idx(limbs) if batch.is_ext else ctx.q_prime_idx(limbs)
+    n = len(idx)
+    m = R // groups
+    if pts.state.cur_limbs < limbs:
+        raise ValueError("plaintext has fewer limbs than the ciphertext")
+    p = pts.cv[0]
+    if batch.is_ext and pts.state.cur_limbs != limbs:
+        raise ValueError("an extended-basis plaintext must match the ciphertext level exactly")
+    out0 = ctx.empty(groups, n, ctx.N)
+    out1 = ctx.empty(groups, n, ctx.N)
+    for g in range(groups):
+        b0 = [batch.cv[0][g * m + b:g * m + b + 1] for b in range(m)]
+        b1 = [batch.cv[1][g * m + b:g * m + b + 1] for b in range(m)]
+        res = ctx.bsgs_mac(b0, b1, p[g * m:(g + 1) * m], n, 1, prime_idx=idx)
+        out0[g].copy_(res[0, 0, 0])
+        out1[g].copy_(res[1, 0, 0])
+    st = batch.state
+    state = st.replace(scale_degree=int(st.scale_degree) + int(pts.state.scale_degree),
+                       scaling_factor=float(st.scaling_factor) * float(pts.state.scaling_factor))
+    return batch.cipher_like([out0, out1], state=state, batch_size=groups)
+
+
+def _has_key(ctx: CKKSContext, offset: int) -> bool:
+    return _galois(offset, ctx) in ctx.rotation_keys
+
+
+def prepare_hoisted_baby_rotations(ct: Cipher, offsets, ctx: CKKSContext, strategy: str = "normal",
+                                   baby_anchor_step: int = -1) -> tuple:
+    """The baby basis of a BSGS product: one cipher per offset (the input batch rotated by it),
+    offset 0 sharing the input's tensors.  An offset without its own key is reached from the
+    largest smaller offset already built whose difference has a key (the anchor blocks of
+    llama3fhe/operators/linear/config.py:235-268)."""
+
+    if ct.is_ext:
+        raise ValueError("baby rotations start from a non-extended ciphertext")
+    limbs = _limbs(ct)
+    c0, c1 = _view(ct.cv[0], limbs), _view(ct.cv[1], limbs)
+    if c0.stride(0) != limbs * ctx.N or c1.stride(0) != limbs * ctx.N:
+        # the MAC needs one batch stride across the basis: drop the stored limbs above the level
+        c0, c1 = c0.contiguous(), c1.contiguous()
+    built: dict[int, tuple] = {}
+    out = []
+    for off in [int(o) for o in offsets]:
+        if off % ctx.max_slots == 0:
+            pair = (c0, c1)
+        elif _has_key(ctx, off):
+            g = _galois(off, ctx)
+            pair = ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g))
+        else:
+            base = max((b for b in built if b < off and _has_key(ctx, off - b)), default=None)
+            if base is None:
+                raise KeyError(f"no rotation key reaches baby offset {off}")
+            g = _galois(off - base, ctx)
+            pair = ctx.rotate_raw(built[base][0], built[base][1], limbs, g, ctx.key_for_galois(g))
+        built[off] = pair
+        out.append(ct.cipher_like(list(pair)))
+    return tuple(out)
+
+
+def hoisted_mac_sum(ct: Cipher, baby_offsets, plaintexts: Plaintext, giant_offset: int, giant_count: int,
+                    ctx: CKKSContext, strategy: str = "normal", baby_anchor_step: int = -1,
+                    baby_rotations=None) -> Cipher:
+    """One BSGS chunk: sum_g rot(sum_b pt[g B + b] * baby_b, g * giant_offset) for every batch row
+    of ``ct`` (llama3fhe/operators/linear/operator.py:434-444).  The baby MAC runs over all rows
+    and giants at once (hck_bsgs_mac).  ``strategy="normal"`` closes the giants by Horner steps
+    acc <- rot(acc, giant_offset) + partial_g, each one fused rotate-and-add; with
+    ``"ext_double_hoist"`` every partial is rotated by its own multiple of giant_offset in the
+    extended basis and the sum is closed by one ModDown.  The result keeps the input level with
+    the plaintext's scale multiplied in (not rescaled)."""
+
+    strategy = str(strategy).lower()
+    if strategy not in ("normal", "ext_normal", "ext_double_hoist"):
+        raise ValueError("strategy must be 'normal', 'ext_normal' or 'ext_double_hoist'")
+    limbs = _limbs(ct)
+    offsets = [int(o) for o in baby_offsets]
+    nb, G = len(offsets), int(giant_count)
+    if baby_rotations is None:
+        baby_rotations = prepare_hoisted_baby_rotations(ct, offsets, ctx, strategy=strategy,
+                                                        baby_anchor_step=baby_anchor_step)
+    babies = tuple(baby_rotations)
+    if len(babies) != nb:
+        raise ValueError(f"expected {nb} baby rotations, got {len(babies)}")
+    pts = plaintexts.cv[0] if isinstance(plaintexts, Plaintext) else plaintexts
+    pt_state = plaintexts.state if isinstance(plaintexts, Plaintext) else None
+    if pts.shape[0] != nb * G:
+        raise ValueError(f"expected {nb * G} plaintext rows, got {pts.shape[0]}")
+    part = ctx.bsgs_mac([_view(b.cv[0], limbs) for b in babies], [_view(b.cv[1], limbs) for b in babies],
+                        pts, limbs, G)  # [2][G][B][limbs][N]
+    idx = ctx.q_prime_idx(limbs)
+    if strategy == "ext_double_hoist" and G > 1:
+        ext0 = _lift_ext(part[0, 0], limbs, ctx)
+        ext1 = _lift_ext(part[1, 0], limbs, ctx)
+        eidx = ctx.ext_prime_idx(limbs)
+        for g in range(1, G):
+            gg = _galois(g * int(giant_offset), ctx)
+            r0, r1 = ctx.rotate_ext(part[0, g], part[1, g], limbs, gg, ctx.key_for_galois(gg))
+            ctx.poly_op(nat.HCK_OP_ADD, ext0, ext0, r0, prime_idx=eidx)
+            ctx.poly_op(nat.HCK_OP_ADD, ext1, ext1, r1, prime_idx=eidx)
+        acc0, acc1 = ctx.moddown(ext0, limbs), ctx.moddown(ext1, limbs)
+    else:
+        acc0, acc1 = part[0, G - 1], part[1, G - 1]
+        gk = _galois(int(giant_offset), ctx) if G > 1 else None
+        for g in range(G - 2, -1, -1):
+            acc0, acc1 = ctx.rotate_raw(acc0, acc1, limbs, gk, ctx.key_for_galois(gk), out0=part[0, g],
+                                        out1=part[1, g], acc=(part[0, g], part[1, g]))
+        acc0, acc1 = acc0.clone(), acc1.clone()
+    del part
+    st = ct.state
+    deg = int(pt_state.scale_degree) if pt_state is not None else 1
+    fac = float(pt_state.scaling_factor) if pt_state is not None else 1.0
+    state = st.replace(scale_degree=int(st.scale_degree) + deg, scaling_factor=float(st.scaling_factor) * fac)
+    return ct.cipher_like([acc0, acc1], state=state)

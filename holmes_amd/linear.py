@@ -8,7 +8,7 @@ alignment rotation, accumulate, final rescale), re-organised for one GPU:
 * the baby rotations of all inputs are computed once (one batched rotation per baby offset:
   every input shares that offset's key) and kept in HBM;
 * a chunk's diagonals are packed and encoded on the GPU (``hck_pack_diagonals``,
-  ``hck_encode_real``) and multiplied into every input at once by ``hck_bsgs_mac``
+  ``hck_encode``) and multiplied into every input at once by ``hck_bsgs_mac``
   (partial sums ``[2][G][inputs]``);
 * each Horner giant step rotates all inputs' accumulators in one batched key switch with the
   shared giant key, as the batched giant step of bench/cmp/holmes_multi_mac.py:180-186.
@@ -25,6 +25,7 @@ import numpy as np
 import torch
 
 from . import _native as nat
+from . import fhe
 from .context import Cipher, CipherState, CKKSContext
 
 _HOIST_STRATEGIES = {"normal", "ext_normal", "ext_double_hoist"}
@@ -202,12 +203,16 @@ def linear_rotations(*, dimension: int, token_lanes: int, slots: int | None = No
     return tuple(sorted(int(v) for v in rot if int(v)))
 
 
-def bsgs_rotations(plan: LinearPlan) -> tuple[int, ...]:
-    """Keys this GPU schedule uses: every baby offset, the giant offset, the chunk bases."""
+def bsgs_rotations(plan: LinearPlan, strategy: str = "normal") -> tuple[int, ...]:
+    """Keys this GPU schedule uses: every baby offset, the giant offset (Horner) or every multiple
+    of it inside a chunk (``ext_double_hoist``), the chunk bases."""
 
     rot = {o for o in plan.baby_offsets if o}
     if max(plan.chunk_sizes) > 1:
-        rot.add(plan.giant_offset)
+        if str(strategy).lower() == "ext_double_hoist":
+            rot.update(s * plan.giant_offset for s in range(1, max(plan.chunk_sizes)))
+        else:
+            rot.add(plan.giant_offset)
     rot.update(int(c.giant_base) * plan.giant_offset for c in plan.chunks if int(c.giant_base))
     return tuple(sorted(rot))
 
@@ -228,8 +233,10 @@ class LinearWeight:
     def closed(self) -> bool:
         return self._closed
 
-    def plaintext(self, plan: LinearPlan, chunk: LinearChunk, *, limbs: int, scale: float) -> torch.Tensor:
-        """Encoded diagonals [giant_count * baby_steps][limbs][N] of ``chunk`` (NTT domain)."""
+    def plaintext(self, plan: LinearPlan, chunk: LinearChunk, *, limbs: int, scale: float,
+                  flags: torch.Tensor | None = None) -> torch.Tensor:
+        """Encoded diagonals [giant_count * baby_steps][limbs][N] of ``chunk`` (NTT domain).
+        ``flags`` (int32, one per row) defers the overflow check to the caller."""
 
         if self._closed:
             raise RuntimeError("linear weight is closed")
@@ -237,7 +244,7 @@ class LinearWeight:
         rows = ctx.pack_diagonals(self._w, lanes=plan.token_lanes, lane_shift=plan.lane_shift,
                                   baby_steps=plan.baby_steps, giant_base=chunk.giant_base,
                                   giant_count=chunk.giant_count)
-        return ctx.encode_real(rows, scale, limbs)
+        return ctx.encode_real(rows, scale, limbs, flags=flags)
 
     def close(self) -> None:
         self._w = None
@@ -310,34 +317,37 @@ class LinearOperator:
             raise ValueError("rescale needs at least two limbs")
         wscale = float(ctx.rescale_divisor_at(limbs)) if weight_scale is None else float(weight_scale)
         idx = ctx.q_prime_idx(limbs)
+        strategy = str(self.config.hoist_strategy).lower()
+        xc = Cipher([x0, x1], state, slots=inputs[0].slots)
         # baby rotations, each batched over all inputs with that offset's key
-        babies0, babies1 = [x0], [x1]
-        for off in plan.baby_offsets[1:]:
-            b0, b1 = self._rotate_all(x0, x1, off, limbs)
-            babies0.append(b0)
-            babies1.append(b1)
+        babies = fhe.prepare_hoisted_baby_rotations(xc, plan.baby_offsets, ctx, strategy=strategy,
+                                                    baby_anchor_step=int(plan.baby_anchor_step))
         total0 = total1 = None
+        # encode overflow flags of every chunk, read back once after the last chunk
+        flags = torch.zeros(int(plan.max_plaintext_rows), dtype=torch.int32, device=x0.device)
+        pt_state = CipherState(cur_limbs=limbs, scale_degree=1, scaling_factor=wscale)
         for chunk in chunks:
-            pts = weight.plaintext(plan, chunk, limbs=limbs, scale=wscale)
-            part = ctx.bsgs_mac(babies0, babies1, pts, limbs, int(chunk.giant_count))  # [2][G][I][l][N]
+            pts = fhe.Plaintext(weight.plaintext(plan, chunk, limbs=limbs, scale=wscale, flags=flags), pt_state,
+                                slots=xc.slots)
+            res = fhe.hoisted_mac_sum(xc, plan.baby_offsets, pts, plan.giant_offset, int(chunk.giant_count), ctx,
+                                      strategy=strategy, baby_anchor_step=int(plan.baby_anchor_step),
+                                      baby_rotations=babies)
             del pts
-            acc0, acc1 = part[0, -1], part[1, -1]
-            for g in range(int(chunk.giant_count) - 2, -1, -1):
-                # Horner: acc <- rot(acc) + partial_g, stored over partial_g
-                acc0, acc1 = self._rotate_all(acc0, acc1, plan.giant_offset, limbs, acc=(part[0, g], part[1, g]))
+            acc0, acc1 = res.cv
             base = int(chunk.giant_base) * plan.giant_offset
             if total0 is None:
                 if base:
                     total0, total1 = self._rotate_all(acc0, acc1, base, limbs)
                 else:
-                    total0, total1 = acc0.clone(), acc1.clone()
+                    total0, total1 = acc0, acc1
             elif base:
                 # chunk alignment rotation, accumulated into the running total in the same pass
                 self._rotate_all(acc0, acc1, base, limbs, acc=(total0, total1))
             else:
                 ctx.poly_op(nat.HCK_OP_ADD, total0, total0, acc0, prime_idx=idx)
                 ctx.poly_op(nat.HCK_OP_ADD, total1, total1, acc1, prime_idx=idx)
-            del part
+            del res
+        ctx.check_encode_flags(flags)
         out_state = state.replace(scale_degree=int(state.scale_degree) + 1,
                                   scaling_factor=float(state.scaling_factor) * wscale)
         slots = inputs[0].slots

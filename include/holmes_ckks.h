@@ -22,7 +22,7 @@
  *   hck_bsgs_mac           holmes_mac_multi, the multi-input BSGS baby-step MAC (holmes_mac.cu:359-402)
  *   hck_pack_diagonals     the BSGS weight diagonal packers (llama3fhe/operators/linear/weight.py:122-154,
  *                          gpu_packer.py:156-198)
- *   hck_encode_real        EasyFHE encode: special IFFT (cv_pre_encode_stage1) + holmes_encode_stage2
+ *   hck_encode             EasyFHE encode: special IFFT (cv_pre_encode_stage1) + holmes_encode_stage2
  *                          (round, reduce, NTT; holmes_encode.cu:240-285)
  */
 #ifndef HOLMES_CKKS_H
@@ -94,6 +94,23 @@ int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galo
                int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                void* workspace, size_t workspace_bytes, void* stream);
 
+/* Rotation ending in the extended basis (hoisted form; no ModDown), fhe.fast_rotate(...,
+ * output_ext=True) (llama3fhe/operators/attention/prefill/input.py:1669-1687):
+ * out0 = P * sigma(c0) + IP_b(sigma(c1)), out1 = IP_a(sigma(c1)) over the level_limbs Q primes
+ * then the K special primes (out_stride >= (level_limbs + K) * N words per item).  hck_moddown of
+ * the pair equals hck_rotate bit for bit.  Same workspace as hck_keyswitch. */
+int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
+                   const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                   const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+/* ModDown of `polys` extended-basis polynomials (level_limbs + K canonical NTT-domain limbs, Q
+ * first) to level_limbs limbs: out = (x_Q - conv_{P->Q}(x_P)) * P^-1, fhe.moddown_from_ext
+ * (input.py:1023-1029; F.cv_moddown, report.py:26-30). */
+size_t hck_moddown_workspace_bytes(const hck_context* ctx, int level_limbs, int polys);
+int hck_moddown(const hck_context* ctx, int level_limbs, int polys, const uint64_t* in, int64_t in_stride,
+                uint64_t* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Rescale `polys` polynomials from level_limbs to level_limbs - 1 limbs:
  * out_i = (in_i - NTT([INTT(in_last)]_{q_i})) * q_last^-1 mod q_i. */
 size_t hck_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int polys);
@@ -124,10 +141,11 @@ int hck_poly_from_signed(const hck_context* ctx, const int64_t* in, uint64_t* ou
 
 /* BSGS baby-step MAC over `inputs` ciphertexts and `giants` giant groups:
  *   res[c][g][i][l][n] = sum_{b < babies} pts[g * babies + b][l][n] * baby_b[i][c][l][n]  (mod q_l)
+ * limb l uses prime prime_idx[l] (Q limbs, or Q then P limbs for extended-basis operands).
  * baby_c0[b] / baby_c1[b] (host arrays of `babies` device pointers): components of baby rotation b,
  * [inputs][>= limbs][N] with batch stride baby_stride; pts rows [giants * babies][>= limbs][N] with
  * row stride pt_stride; res [2][giants][inputs][limbs][N] contiguous. */
-int hck_bsgs_mac(const hck_context* ctx, int limbs, int inputs, int babies, int giants,
+int hck_bsgs_mac(const hck_context* ctx, int limbs, const int* prime_idx, int inputs, int babies, int giants,
                  const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, int64_t baby_stride,
                  const uint64_t* pts, int64_t pt_stride, uint64_t* res, void* stream);
 
@@ -138,13 +156,15 @@ int hck_pack_diagonals(const hck_context* ctx, const double* weight, int dimensi
                        int lane_shift, int baby_steps, int giant_base, int giant_count, double* out,
                        void* stream);
 
-/* Encode `rows` real slot vectors (float64 [rows][N/2]) at `scale` into NTT-domain residues
- * out[row][l] (row stride out_row_stride words, limb l modulo prime prime_idx[l]).  A coefficient
- * of magnitude >= 2^52 sets overflow_flags[row] (device int array, caller-zeroed). */
+/* Encode `rows` slot vectors at `scale` into NTT-domain residues out[row][l] (row stride
+ * out_row_stride words, limb l modulo prime prime_idx[l]; Q then P primes gives an
+ * extended-basis plaintext).  values / values_im: float64 [rows][N/2] real and imaginary parts
+ * (values_im NULL: real input).  A coefficient of magnitude >= 2^52 sets overflow_flags[row]
+ * (device int array, caller-zeroed). */
 size_t hck_encode_workspace_bytes(const hck_context* ctx, int rows);
-int hck_encode_real(const hck_context* ctx, const double* values, int rows, double scale, int limbs,
-                    const int* prime_idx, uint64_t* out, int64_t out_row_stride, void* workspace,
-                    size_t workspace_bytes, int* overflow_flags, void* stream);
+int hck_encode(const hck_context* ctx, const double* values, const double* values_im, int rows, double scale,
+               int limbs, const int* prime_idx, uint64_t* out, int64_t out_row_stride, void* workspace,
+               size_t workspace_bytes, int* overflow_flags, void* stream);
 
 #ifdef __cplusplus
 }
