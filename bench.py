@@ -55,6 +55,9 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
+    ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
+                    help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
+                         "(both are hoist strategies of the reference's LinearOperatorConfig)")
     ap.add_argument("--workload", choices=("c1", "c2", "c3", "stream"), default="c2",
                     help="c2: batched key switch (headline); c1: one rotation + rescale (latency); "
                          "c3: q_proj BSGS projection; stream: the "
@@ -318,12 +321,13 @@ def run_c3(args) -> int:
     steps = int(args.steps) if args.steps != 20 else 3
     warmup = int(args.warmup) if args.warmup != 3 else 1
     t0 = time.perf_counter()
-    cfg = linear.LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512)
+    cfg = linear.LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512,
+                                      hoist_strategy=args.strategy)
     layout = FeatureMajorPrefillLayout(seq_len=C3_TOKENS, hidden_dim=C3_DIM, slots=32768)
     lanes = layout.tokens_per_cipher
     plan = cfg.plan(dimension=C3_DIM, token_lanes=lanes)
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=seed,
-                               rotations=linear.bsgs_rotations(plan))
+                               rotations=linear.bsgs_rotations(plan, args.strategy))
     client, ctx = fhe.generate_client_context(spec)
     rng = np.random.default_rng(seed)
     w = randomized_hadamard_right(rng.normal(scale=0.02, size=(C3_DIM, C3_DIM)), seed + 1)
@@ -388,6 +392,7 @@ def run_c3(args) -> int:
             "limbs": C3_LIMBS,
             "chunks": plan.plaintext_chunks,
             "key_switches": ks_per_projection,
+            "hoist_strategy": args.strategy,
             "algorithmic_bytes_per_step": C3_BYTES,
             "decrypted_max_abs_error": err,
         },

@@ -48,7 +48,8 @@ SIGNATURES = {
     "hck_poly_from_signed": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _i, _ip, _vp]),
     "hck_bsgs_mac": (_i, [_vp, _i, _ip, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64, _vp, _i64, _vp,
                           _vp]),
-    "hck_rotate_ext": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _sz, _vp]),
+    "hck_rotate_ext": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp, _i64,
+                            _vp, _sz, _vp]),
     "hck_moddown_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_moddown": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_pack_diagonals": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),

@@ -76,6 +76,13 @@ class Cipher:
                 f"scale_degree={self.state.scale_degree}, ext={self.is_ext})")
 
 
+def _bstride(t: torch.Tensor) -> int:
+    """Batch stride passed to the kernels: a single-item batch may carry any stride (a size-1
+    axis from numpy has stride 0), so it is reported as the dense item size."""
+
+    return int(t.stride(0)) if t.shape[0] > 1 else int(t[0].numel())
+
+
 def _stream_ptr(device) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
 
@@ -184,7 +191,7 @@ class CKKSContext:
         dst = src if dst is None else dst
         self._check_poly(dst, limbs, self.N)
         fn = nat.lib().hck_ntt_inverse if inverse else nat.lib().hck_ntt_forward
-        nat.check(fn(self._h, src.data_ptr(), dst.data_ptr(), src.shape[0], src.stride(0), dst.stride(0),
+        nat.check(fn(self._h, src.data_ptr(), dst.data_ptr(), src.shape[0], _bstride(src), _bstride(dst),
                      limbs, nat.int_array(prime_idx), _stream_ptr(self.device)),
                   "hck_ntt_inverse" if inverse else "hck_ntt_forward")
         return dst
@@ -195,7 +202,7 @@ class CKKSContext:
             out = self.empty(src.shape[0], limbs, self.N)
         self._check_poly(out, limbs, self.N)
         nat.check(nat.lib().hck_automorphism(self._h, src.data_ptr(), out.data_ptr(), src.shape[0],
-                                             src.stride(0), out.stride(0), limbs, int(galois),
+                                             _bstride(src), _bstride(out), limbs, int(galois),
                                              _stream_ptr(self.device)), "hck_automorphism")
         return out
 
@@ -207,7 +214,7 @@ class CKKSContext:
         bb = b if b is not None else a
         sc = nat.u64_array(scalar) if scalar is not None else None
         nat.check(nat.lib().hck_poly_op(self._h, int(op), out.data_ptr(), a.data_ptr(), bb.data_ptr(),
-                                        a.shape[0], out.stride(0), a.stride(0), bb.stride(0), limbs,
+                                        a.shape[0], _bstride(out), _bstride(a), _bstride(bb), limbs,
                                         nat.int_array(prime_idx), sc, _stream_ptr(self.device)),
                   "hck_poly_op")
         return out
@@ -220,7 +227,7 @@ class CKKSContext:
         coeffs = coeffs.contiguous()
         out = self.empty(coeffs.shape[0], len(prime_idx), self.N)
         nat.check(nat.lib().hck_poly_from_signed(self._h, coeffs.data_ptr(), out.data_ptr(), coeffs.shape[0],
-                                                 coeffs.stride(0), out.stride(0), len(prime_idx),
+                                                 _bstride(coeffs), _bstride(out), len(prime_idx),
                                                  nat.int_array(prime_idx), _stream_ptr(self.device)),
                   "hck_poly_from_signed")
         return out
@@ -239,18 +246,18 @@ class CKKSContext:
             self._check_key(k)
         out_b = self.empty(B, limbs, self.N) if out_b is None else out_b
         out_a = self.empty(B, limbs, self.N) if out_a is None else out_a
-        if out_b.stride(0) != out_a.stride(0):
+        if _bstride(out_b) != _bstride(out_a):
             raise ValueError("out_b and out_a need the same batch stride")
         if add is not None:
             self._check_poly(add, limbs, self.N)
         L = nat.lib()
         ws_bytes = L.hck_keyswitch_workspace_bytes(self._h, limbs, B)
         ws = self.workspace(ws_bytes)
-        nat.check(L.hck_keyswitch(self._h, limbs, B, d.data_ptr(), d.stride(0),
+        nat.check(L.hck_keyswitch(self._h, limbs, B, d.data_ptr(), _bstride(d),
                                   nat.ptr_array([k.data_ptr() for k in keys]),
                                   add.data_ptr() if add is not None else None,
-                                  add.stride(0) if add is not None else 0,
-                                  out_b.data_ptr(), out_a.data_ptr(), out_b.stride(0),
+                                  _bstride(add) if add is not None else 0,
+                                  out_b.data_ptr(), out_a.data_ptr(), _bstride(out_b),
                                   ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_keyswitch")
         return out_b, out_a
 
@@ -262,7 +269,7 @@ class CKKSContext:
 
         self._check_poly(c0, limbs, self.N)
         self._check_poly(c1, limbs, self.N)
-        if c0.stride(0) != c1.stride(0):
+        if _bstride(c0) != _bstride(c1):
             raise ValueError("c0 and c1 need the same batch stride")
         B = c0.shape[0]
         if isinstance(keys, torch.Tensor):
@@ -277,7 +284,7 @@ class CKKSContext:
             self._check_poly(o, limbs, self.N)
             if o.shape[0] != B:
                 raise ValueError("outputs need one row per input")
-        if out0.stride(0) != out1.stride(0):
+        if _bstride(out0) != _bstride(out1):
             raise ValueError("out0 and out1 need the same batch stride")
         a0 = a1 = None
         a_stride = 0
@@ -287,29 +294,31 @@ class CKKSContext:
                 self._check_poly(a, limbs, self.N)
                 if a.shape[0] != B:
                     raise ValueError("accumulators need one row per input")
-            if a0.stride(0) != a1.stride(0):
+            if _bstride(a0) != _bstride(a1):
                 raise ValueError("acc0 and acc1 need the same batch stride")
-            a_stride = a0.stride(0)
+            a_stride = _bstride(a0)
         L = nat.lib()
         ws = self.workspace(L.hck_rotate_workspace_bytes(self._h, limbs, B))
-        nat.check(L.hck_rotate(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), c0.stride(0),
+        nat.check(L.hck_rotate(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), _bstride(c0),
                                nat.ptr_array([k.data_ptr() for k in keys]),
                                a0.data_ptr() if a0 is not None else None,
                                a1.data_ptr() if a1 is not None else None, a_stride,
-                               out0.data_ptr(), out1.data_ptr(), out0.stride(0), ws.data_ptr(), ws.numel(),
+                               out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
                                _stream_ptr(self.device)),
                   "hck_rotate")
         return out0, out1
 
     def rotate_ext(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois: int, keys,
-                   out0: torch.Tensor | None = None, out1: torch.Tensor | None = None):
+                   out0: torch.Tensor | None = None, out1: torch.Tensor | None = None,
+                   acc: tuple[torch.Tensor, torch.Tensor] | None = None):
         """Hoisted-form rotation ending in the extended basis: (P sigma(c0) + IP_b, IP_a) as
-        [batch][limbs + K][N] tensors (Q limbs, then the special primes); ``moddown`` of each
+        [batch][limbs + K][N] tensors (Q limbs, then the special primes), plus the extended-basis
+        ``acc`` pair when given (the outputs may be the ``acc`` tensors); ``moddown`` of each
         component gives ``rotate_raw``'s result bit for bit."""
 
         self._check_poly(c0, limbs, self.N)
         self._check_poly(c1, limbs, self.N)
-        if c0.stride(0) != c1.stride(0):
+        if _bstride(c0) != _bstride(c1):
             raise ValueError("c0 and c1 need the same batch stride")
         B = c0.shape[0]
         if isinstance(keys, torch.Tensor):
@@ -325,13 +334,27 @@ class CKKSContext:
             self._check_poly(o, ext, self.N)
             if o.shape[0] != B:
                 raise ValueError("outputs need one row per input")
-        if out0.stride(0) != out1.stride(0):
+        if _bstride(out0) != _bstride(out1):
             raise ValueError("out0 and out1 need the same batch stride")
+        a0 = a1 = None
+        a_stride = 0
+        if acc is not None:
+            a0, a1 = acc
+            for a in (a0, a1):
+                self._check_poly(a, ext, self.N)
+                if a.shape[0] != B:
+                    raise ValueError("accumulators need one row per input")
+            if _bstride(a0) != _bstride(a1):
+                raise ValueError("acc0 and acc1 need the same batch stride")
+            a_stride = _bstride(a0)
         L = nat.lib()
         ws = self.workspace(L.hck_keyswitch_workspace_bytes(self._h, limbs, B))
-        nat.check(L.hck_rotate_ext(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), c0.stride(0),
-                                   nat.ptr_array([k.data_ptr() for k in keys]), out0.data_ptr(), out1.data_ptr(),
-                                   out0.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+        nat.check(L.hck_rotate_ext(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), _bstride(c0),
+                                   nat.ptr_array([k.data_ptr() for k in keys]),
+                                   a0.data_ptr() if a0 is not None else None,
+                                   a1.data_ptr() if a1 is not None else None, a_stride,
+                                   out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
+                                   _stream_ptr(self.device)),
                   "hck_rotate_ext")
         return out0, out1
 
@@ -343,8 +366,8 @@ class CKKSContext:
         self._check_poly(out, limbs, self.N)
         L = nat.lib()
         ws = self.workspace(L.hck_moddown_workspace_bytes(self._h, limbs, x.shape[0]))
-        nat.check(L.hck_moddown(self._h, limbs, x.shape[0], x.data_ptr(), x.stride(0), out.data_ptr(),
-                                out.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+        nat.check(L.hck_moddown(self._h, limbs, x.shape[0], x.data_ptr(), _bstride(x), out.data_ptr(),
+                                _bstride(out), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
                   "hck_moddown")
         return out
 
@@ -355,8 +378,8 @@ class CKKSContext:
         out = self.empty(x.shape[0], limbs - 1, self.N) if out is None else out
         L = nat.lib()
         ws = self.workspace(L.hck_rescale_workspace_bytes(self._h, limbs, x.shape[0]))
-        nat.check(L.hck_rescale(self._h, limbs, x.shape[0], x.data_ptr(), x.stride(0), out.data_ptr(),
-                                out.stride(0), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+        nat.check(L.hck_rescale(self._h, limbs, x.shape[0], x.data_ptr(), _bstride(x), out.data_ptr(),
+                                _bstride(out), ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
                   "hck_rescale")
         return out
 
@@ -377,7 +400,7 @@ class CKKSContext:
         stride = babies_c0[0].stride(0)
         for t in list(babies_c0) + list(babies_c1):
             self._check_poly(t, limbs, self.N)
-            if t.shape[0] != ni or t.stride(0) != stride:
+            if t.shape[0] != ni or _bstride(t) != stride:
                 raise ValueError("baby tensors need one shape and batch stride")
         self._check_poly(pts, limbs, self.N)
         if pts.shape[0] != giants * nb:
@@ -389,7 +412,7 @@ class CKKSContext:
         nat.check(nat.lib().hck_bsgs_mac(self._h, limbs, nat.int_array(prime_idx), ni, nb, giants,
                                          nat.ptr_array([t.data_ptr() for t in babies_c0]),
                                          nat.ptr_array([t.data_ptr() for t in babies_c1]), stride,
-                                         pts.data_ptr(), pts.stride(0), out.data_ptr(),
+                                         pts.data_ptr(), _bstride(pts), out.data_ptr(),
                                          _stream_ptr(self.device)), "hck_bsgs_mac")
         return out
 
@@ -471,7 +494,7 @@ class CKKSContext:
         ws = self.workspace(L.hck_encode_workspace_bytes(self._h, rows))
         nat.check(L.hck_encode(self._h, values.data_ptr(), values_im.data_ptr() if values_im is not None else None,
                                rows, float(scale), int(limbs), nat.int_array(prime_idx), out.data_ptr(),
-                               out.stride(0), ws.data_ptr(), ws.numel(), flags.data_ptr(),
+                               _bstride(out), ws.data_ptr(), ws.numel(), flags.data_ptr(),
                                _stream_ptr(self.device)), "hck_encode")
         if own:
             self.check_encode_flags(flags)

@@ -82,7 +82,8 @@ int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
 
 size_t ks_fused_bytes(const hck_context* c, int ell, int batch);
 // d and add are read through sigma_galois (galois == 1: unpermuted); acc_b / acc_a (nullable,
-// unpermuted) are added to out_b / out_a.
+// unpermuted) are added to out_b / out_a, or, with ext_b / ext_a set (the key switch stops in the
+// extended basis), to the extended-basis outputs.
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,

@@ -98,23 +98,29 @@ extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, ui
 
 extern "C" int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
                               const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
-                              const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                              const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                              int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                               void* workspace, size_t workspace_bytes, void* stream) {
   if (!ctx || !c0 || !c1 || !ksk || !out0 || !out1 || batch < 0) return HCK_ERR_ARG;
+  if ((acc0 == nullptr) != (acc1 == nullptr)) return HCK_ERR_ARG;
+  // item strides only matter between items: a single item may carry any stride (numpy views of
+  // size-1 axes have stride 0)
+  if (acc0 && batch > 1 && acc_stride < (int64_t)(level_limbs + ctx->K) * hck::kN) return HCK_ERR_ARG;
   if (level_limbs < 1 || level_limbs > ctx->L) return HCK_ERR_ARG;
   if ((galois & 1u) == 0 || galois >= 2u * hck::kN) return HCK_ERR_ARG;
   if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1 || out0 == out1) return HCK_ERR_ARG;
-  if (out_stride < (int64_t)(level_limbs + ctx->K) * hck::kN) return HCK_ERR_ARG;
+  if (batch > 1 && out_stride < (int64_t)(level_limbs + ctx->K) * hck::kN) return HCK_ERR_ARG;
   if (batch == 0) return HCK_OK;
   for (int b = 0; b < batch; ++b) if (!ksk[b]) return HCK_ERR_ARG;
   const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
   if (!workspace || workspace_bytes < hck::ks_fused_bytes(ctx, level_limbs, chunk)) return HCK_ERR_WORKSPACE;
   for (int b0 = 0; b0 < batch; b0 += chunk) {
     const int nb = batch - b0 < chunk ? batch - b0 : chunk;
-    const long long oi = (long long)b0 * out_stride;
+    const long long oi = (long long)b0 * out_stride, ai = (long long)b0 * acc_stride;
     int rc = hck::ks_fused(ctx, level_limbs, nb, c1 + (long long)b0 * in_stride, in_stride, galois, ksk + b0,
-                           c0 + (long long)b0 * in_stride, in_stride, nullptr, nullptr, 0, nullptr, nullptr, 0,
-                           (char*)workspace, (hipStream_t)stream, out0 + oi, out1 + oi, out_stride);
+                           c0 + (long long)b0 * in_stride, in_stride, acc0 ? acc0 + ai : nullptr,
+                           acc1 ? acc1 + ai : nullptr, acc_stride, nullptr, nullptr, 0, (char*)workspace,
+                           (hipStream_t)stream, out0 + oi, out1 + oi, out_stride);
     if (rc) return rc;
   }
   return HCK_OK;
@@ -131,7 +137,8 @@ extern "C" int hck_moddown(const hck_context* ctx, int level_limbs, int polys, c
                            size_t workspace_bytes, void* stream) {
   if (!ctx || !in || !out || polys < 0 || polys > 65535) return HCK_ERR_ARG;
   if (level_limbs < 1 || level_limbs > ctx->L) return HCK_ERR_ARG;
-  if (in_stride < (int64_t)(level_limbs + ctx->K) * hck::kN || out_stride < (int64_t)level_limbs * hck::kN)
+  if (polys > 1 && (in_stride < (int64_t)(level_limbs + ctx->K) * hck::kN ||
+                    out_stride < (int64_t)level_limbs * hck::kN))
     return HCK_ERR_ARG;
   if (polys == 0) return HCK_OK;
   if (!workspace || workspace_bytes < hck::moddown_bytes(ctx, level_limbs, polys)) return HCK_ERR_WORKSPACE;

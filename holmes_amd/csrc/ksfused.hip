@@ -398,13 +398,15 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
 // served from that XCD's L2 to the other ciphertexts.
 // With ext_b set the kernel ends the key switch in the extended basis: it writes (P * sigma(add) +
 // IP_b, IP_a) over Q u P as canonical NTT-domain residues to ext_b / ext_a ([ell + K] limbs per
-// ciphertext, Q limbs first) and skips the ModDown inputs.
+// ciphertext, Q limbs first), plus the extended-basis accumulators acc_b / acc_a when given (which
+// ext_b / ext_a may alias), and skips the ModDown inputs.
 __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
                                                    const double* __restrict__ t2, KeyPtrsF keys, int ell,
                                                    int beta, int batch, int tiles, double* __restrict__ accq,
                                                    double* __restrict__ accp, const uint64_t* __restrict__ add,
-                                                   long long add_stride, uint64_t* __restrict__ ext_b,
-                                                   uint64_t* __restrict__ ext_a, long long ext_stride, DevTables T) {
+                                                   long long add_stride, uint64_t* ext_b, uint64_t* ext_a,
+                                                   long long ext_stride, const uint64_t* acc_b,
+                                                   const uint64_t* acc_a, long long acc_stride, DevTables T) {
   __shared__ double S[kRowLds];
   const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
   const int tile = (q / batch) * kXcds + xcd, b = q % batch;
@@ -453,6 +455,13 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
       const TwPair pm = T.pmodq[pi];
 #pragma unroll
       for (int k = 0; k < 16; ++k) sb[k] += mulc(ad[k], pm, p);  // |sb| <= 1.5 p
+    }
+    if (acc_b) {
+      double ab[16], aa[16];
+      load_gal(ab, acc_b + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+      load_gal(aa, acc_a + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) { sb[k] += ab[k]; sa[k] += aa[k]; }  // |sb| <= 2.5 p
     }
     uint64_t* ob = ext_b + (long long)b * ext_stride + (long long)e * kN + na;
     uint64_t* oa = ext_a + (long long)b * ext_stride + (long long)e * kN + na;
@@ -558,7 +567,8 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   const int groups = (tiles + kXcds - 1) / kXcds;
   k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
                                                           accq, accp, add, add_stride, ext_b, ext_a, ext_stride,
-                                                          c->dev);
+                                                          ext_b ? acc_b : nullptr, ext_b ? acc_a : nullptr,
+                                                          acc_stride, c->dev);
   HCK_CHECK_LAUNCH();
   if (ext_b) return HCK_OK;
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1

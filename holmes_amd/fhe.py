@@ -426,7 +426,7 @@ def prepare_hoisted_baby_rotations(ct: Cipher, offsets, ctx: CKKSContext, strate
         raise ValueError("baby rotations start from a non-extended ciphertext")
     limbs = _limbs(ct)
     c0, c1 = _view(ct.cv[0], limbs), _view(ct.cv[1], limbs)
-    if c0.stride(0) != limbs * ctx.N or c1.stride(0) != limbs * ctx.N:
+    if c0.shape[0] > 1 and (c0.stride(0) != limbs * ctx.N or c1.stride(0) != limbs * ctx.N):
         # the MAC needs one batch stride across the basis: drop the stored limbs above the level
         c0, c1 = c0.contiguous(), c1.contiguous()
     built: dict[int, tuple] = {}
@@ -481,12 +481,11 @@ def hoisted_mac_sum(ct: Cipher, baby_offsets, plaintexts: Plaintext, giant_offse
     if strategy == "ext_double_hoist" and G > 1:
         ext0 = _lift_ext(part[0, 0], limbs, ctx)
         ext1 = _lift_ext(part[1, 0], limbs, ctx)
-        eidx = ctx.ext_prime_idx(limbs)
         for g in range(1, G):
+            # each partial rotated by its own giant multiple, summed in the extended basis
             gg = _galois(g * int(giant_offset), ctx)
-            r0, r1 = ctx.rotate_ext(part[0, g], part[1, g], limbs, gg, ctx.key_for_galois(gg))
-            ctx.poly_op(nat.HCK_OP_ADD, ext0, ext0, r0, prime_idx=eidx)
-            ctx.poly_op(nat.HCK_OP_ADD, ext1, ext1, r1, prime_idx=eidx)
+            ctx.rotate_ext(part[0, g], part[1, g], limbs, gg, ctx.key_for_galois(gg), out0=ext0, out1=ext1,
+                           acc=(ext0, ext1))
         acc0, acc1 = ctx.moddown(ext0, limbs), ctx.moddown(ext1, limbs)
     else:
         acc0, acc1 = part[0, G - 1], part[1, G - 1]

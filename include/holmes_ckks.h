@@ -96,12 +96,16 @@ int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galo
 
 /* Rotation ending in the extended basis (hoisted form; no ModDown), fhe.fast_rotate(...,
  * output_ext=True) (llama3fhe/operators/attention/prefill/input.py:1669-1687):
- * out0 = P * sigma(c0) + IP_b(sigma(c1)), out1 = IP_a(sigma(c1)) over the level_limbs Q primes
- * then the K special primes (out_stride >= (level_limbs + K) * N words per item).  hck_moddown of
- * the pair equals hck_rotate bit for bit.  Same workspace as hck_keyswitch. */
+ * out0 = P * sigma(c0) + IP_b(sigma(c1)) (+ acc0), out1 = IP_a(sigma(c1)) (+ acc1) over the
+ * level_limbs Q primes then the K special primes (out / acc strides >= (level_limbs + K) * N words
+ * per item; acc0 / acc1 both NULL or both given, and may be out0 / out1: the double-hoisted
+ * giant-step sum of a BSGS product, hoist_strategy "ext_double_hoist",
+ * llama3fhe/operators/linear/config.py:353-360).  hck_moddown of the pair equals hck_rotate bit
+ * for bit.  Same workspace as hck_keyswitch. */
 int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
                    const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
-                   const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                   const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                   int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 /* ModDown of `polys` extended-basis polynomials (level_limbs + K canonical NTT-domain limbs, Q

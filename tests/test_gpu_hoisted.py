@@ -53,6 +53,23 @@ def test_fast_rotate_ext_then_moddown_is_exact(env):
     assert np.array_equal(_h(back.cv[1]), _h(plain.cv[1]))
 
 
+def test_rotate_ext_accumulates(env):
+    fhe, client, ctx, x, ct = env
+    g = ctx.galois_element(5)
+    key = ctx.key_for_galois(g)
+    c0, c1 = ct.cv[0][:, :LIMBS], ct.cv[1][:, :LIMBS]
+    e0, e1 = ctx.rotate_ext(c0, c1, LIMBS, g, key)
+    rng = np.random.default_rng(4)
+    idx = ctx.ext_prime_idx(LIMBS)
+    acc = [np.stack([rng.integers(0, ctx.primes[i], ctx.N, dtype=np.uint64) for i in idx])[None] for _ in range(2)]
+    a0, a1 = (torch.from_numpy(a).cuda() for a in acc)
+    s0, s1 = ctx.rotate_ext(c0, c1, LIMBS, g, key, out0=a0, out1=a1, acc=(a0, a1))
+    q = np.array([ctx.primes[i] for i in idx], dtype=object).reshape(-1, 1)
+    for got, base, add in ((s0, e0, acc[0]), (s1, e1, acc[1])):
+        want = ((_h(base)[0].astype(object) + add[0].astype(object)) % q).astype(np.uint64)
+        assert np.array_equal(_h(got)[0], want)
+
+
 def test_moddown_matches_oracle(env):
     fhe, client, ctx, x, ct = env
     orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
