@@ -32,6 +32,10 @@ import time
 import numpy as np
 
 BYTES_PER_CT = (12 + 96 + 24) * 2**20  # 138,412,032
+# HBM bytes one C2 step actually moves (all five kernels), from two rocprofv3 --pmc runs of this
+# workload: FETCH_SIZE (x 2.0, the factor the stream workload's known 192 MiB read calibrates) +
+# WRITE_SIZE (x 1.0): 3817 MiB + 2048 MiB.
+C2_TRAFFIC_BYTES = 5865 * 2**20
 CTS = 16
 LIMBS = 24
 HBM_PEAK_GBS = 8000.0
@@ -183,7 +187,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": C2_TRAFFIC_BYTES,
             "kernel": "hck_keyswitch (whole ModUp -> inner product -> ModDown launch sequence per step)",
             "ms_per_launch": round(ms_events, 4),
         },

@@ -101,3 +101,24 @@ def test_feature_major_layout_roundtrip_and_slot_rule():
     assert np.array_equal(small.unpack(small.pack(r)), r)
     with pytest.raises(ValueError):
         FeatureMajorPrefillLayout(hidden_dim=12)
+
+
+def test_easyfhe_alias_binds_the_hot_path_surface():
+    from holmes_amd import easyfhe_compat
+
+    easyfhe_compat.install()
+    try:
+        from easyfhe import fhe  # noqa: F401  (the import llama3fhe's operators make)
+        import easyfhe
+
+        import holmes_amd.fhe as ours
+
+        assert fhe is ours and easyfhe.fhe is ours
+        for name in ("CKKSContextSpec", "generate_client_context", "CipherState", "ConstantBundle", "PackedRaw",
+                     "homo_rotate", "prepare_hoisted_baby_rotations", "hoisted_mac_sum", "rescale", "align_to",
+                     "homo_add", "homo_sub", "homo_mul_i", "homo_mul_pt", "fast_rotate", "grouped_pairwise_mac",
+                     "moddown_from_ext", "pack_cipher_batch", "unpack_cipher_batch"):
+            assert callable(getattr(fhe, name)), name
+        assert easyfhe.uint64 is not None and easyfhe.get_device_module("cuda") is not None
+    finally:
+        easyfhe_compat.uninstall()
