@@ -68,8 +68,10 @@ u64 brv(u64 x, int bits) {
 }
 
 // Base-conversion constants from primes src[] to primes dst[] (hmod[s][t] = prod_{r != s} b_r mod t).
+// ninv[i] = N^-1 and ninv_w1[i] = N^-1 psi_rev_inv[1] mod P[i] (the inverse NTT's last-stage factors).
 void fill_conv(hck::ConvConsts& cc, const std::vector<u64>& P, const std::vector<int>& src,
-               const std::vector<int>& dst, const std::vector<int>& dst_slot) {
+               const std::vector<int>& dst, const std::vector<int>& dst_slot, const std::vector<u64>& ninv,
+               const std::vector<u64>& ninv_w1) {
   std::memset(&cc, 0, sizeof(cc));
   cc.ns = (int)src.size();
   cc.nt = (int)dst.size();
@@ -78,7 +80,10 @@ void fill_conv(hck::ConvConsts& cc, const std::vector<u64>& P, const std::vector
     u64 h = 1;
     for (int r = 0; r < cc.ns; ++r) if (r != s) h = mulmod(h, P[src[r]] % bs, bs);
     cc.src_prime[s] = src[s];
-    cc.hinv[s] = pair_of(invmod(h, bs), bs);
+    const u64 hi = invmod(h, bs);
+    cc.hinv[s] = pair_of(hi, bs);
+    cc.inv_n0[s] = pair_of(mulmod(ninv[src[s]], hi, bs), bs);
+    cc.inv_n1[s] = pair_of(mulmod(ninv_w1[src[s]], hi, bs), bs);
     for (int t = 0; t < cc.nt; ++t) {
       const u64 qt = P[dst[t]];
       u64 v = 1;
@@ -123,6 +128,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   std::vector<double> hp(np), hpinv(np);
   std::vector<double> fwd((size_t)np * n), inv((size_t)np * n);
   std::vector<hck::TwPair> ninv(np), ninv_w1(np), zeta4(np), pmodq(np);
+  std::vector<u64> ninv_u(np), ninv_w1_u(np);
   for (int i = 0; i < np; ++i) {
     const u64 q = P[i];
     hp[i] = (double)q;
@@ -139,7 +145,9 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     const u64 ni = invmod(n % q, q);
     ninv[i] = pair_of(ni, q);
     // the inverse transform's last stage uses psi_rev_inv[1]; folding N^-1 into it saves a pass
-    ninv_w1[i] = pair_of(mulmod(ni, (u64)inv[(size_t)i * n + 1], q), q);
+    ninv_u[i] = ni;
+    ninv_w1_u[i] = mulmod(ni, (u64)inv[(size_t)i * n + 1], q);
+    ninv_w1[i] = pair_of(ninv_w1_u[i], q);
     zeta4[i] = pair_of(powmod(psi, n / 2, q), q);
     u64 pm = 1;
     for (int k = 0; k < num_p; ++k) pm = mulmod(pm, P[num_q + k] % q, q);
@@ -184,12 +192,12 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
         dst.push_back(e < ell ? e : num_q + (e - ell));
         slot.push_back(e);
       }
-      fill_conv(c->h_modup[(size_t)ell * c->beta_max + j], P, src, dst, slot);
+      fill_conv(c->h_modup[(size_t)ell * c->beta_max + j], P, src, dst, slot, ninv_u, ninv_w1_u);
     }
     std::vector<int> src, dst, slot;
     for (int k = 0; k < num_p; ++k) src.push_back(num_q + k);
     for (int i = 0; i < ell; ++i) { dst.push_back(i); slot.push_back(i); }
-    fill_conv(c->h_moddown[ell], P, src, dst, slot);
+    fill_conv(c->h_moddown[ell], P, src, dst, slot, ninv_u, ninv_w1_u);
     hck::LevelConsts& lc = c->h_level[ell];
     for (int i = 0; i < ell; ++i) {
       u64 pm = 1;

@@ -14,12 +14,16 @@ constexpr int kMaxSpecial = 8;  // P primes (fused ModDown holds them in LDS)
 
 // Base conversion constants from a source basis {b_s} to target primes {t}:
 //   y_s = [x_s * hinv_s]_{b_s} (canonical),   out_t = sum_s y_s * hmod[s][t]  mod t.
+// When x_s comes out of an inverse NTT, the multiplication by hinv_s rides on the transform's
+// last stage: inv_n0[s] = N^-1 hinv_s and inv_n1[s] = N^-1 psi_rev_inv[1] hinv_s (mod b_s).
 struct ConvConsts {
   int ns, nt;
   int src_prime[kMaxAlpha];  // prime indices of the source limbs
   int dst_prime[kMaxPrimes]; // prime index of target t
   int dst_slot[kMaxPrimes];  // position of target t in the destination buffer (limb index)
   TwPair hinv[kMaxAlpha];
+  TwPair inv_n0[kMaxAlpha];
+  TwPair inv_n1[kMaxAlpha];
   TwPair hmod[kMaxAlpha][kMaxPrimes];
 };
 

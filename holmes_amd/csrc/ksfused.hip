@@ -2,9 +2,11 @@
 //
 // A limb (N = 2^16 words) is a 256 x 256 matrix, n = 256 r + c.  The forward NTT runs stages
 // 0..7 inside columns ("cols" pass) and 8..15 inside rows ("rows" pass); the inverse runs rows
-// (15..8) then cols (7..0).  Workspace buffers keep limbs in a transposed layout (element (r, c)
-// at c * 256 + r) so a column is 2 KiB contiguous: the cols kernels read and write whole columns,
-// the rows kernels read 16 rows at once as 128-byte runs.
+// (15..8) then cols (7..0).  Workspace buffers keep limbs column-major, a column 2 KiB contiguous,
+// with row r of a column at position tpos(r) = 16 (r mod 16) + r / 16 (the two nibbles of r
+// swapped).  A rows-kernel block owns the 16 rows g + 16 m (row group g), which sit at positions
+// 16 g .. 16 g + 15 of every column (128-byte runs); a cols-kernel thread holding rows 16 j + k
+// (k = 0..15) finds them at positions 16 k + j, so 16 lanes touch 128 consecutive bytes.
 //
 //   K1 ks_intt_rows   sigma_g(d) (natural, u64) --INTT rows-->                T1 (transposed)
 //   K2 ks_cols_conv   T1 --INTT cols--> coefficients --ModUp conversion (LDS)--> NTT cols --> T2
@@ -154,9 +156,10 @@ __device__ __forceinline__ void col_inv_lo(double (&x)[16], const double* __rest
 }
 
 // ----------------------------------------------------------------- row transforms (256 threads)
-// The block owns 16 rows (b = r0 + rb).  Two thread mappings: "N" (rb = t >> 4, j = t & 15) makes
-// 16 consecutive lanes touch 16 consecutive words of a natural-layout row; "T" (rb = t & 15,
-// j = t >> 4) makes them touch 16 consecutive rows of a transposed-layout column.
+// The block owns row group g: rows b = g + 16 rb, rb = 0..15.  Two thread mappings: "N"
+// (rb = t >> 4, j = t & 15) makes 16 consecutive lanes touch 16 consecutive words of a
+// natural-layout row; "T" (rb = t & 15, j = t >> 4) makes them touch the 16 consecutive positions
+// 16 g + rb of a workspace column.
 __device__ __forceinline__ int ridx(int rb, int c) { return rb * 273 + c + (c >> 4); }
 constexpr int kRowLds = 16 * 273 + 16;
 
@@ -257,36 +260,46 @@ __device__ __forceinline__ void load_gal(double (&x)[16], const uint64_t* __rest
   }
 }
 
-// Natural-layout access in layout A under map N: thread (rb, j) owns words j + 16k of row r0 + rb;
+// Natural-layout access in layout A under map N: thread (rb, j) owns words j + 16k of row g + 16 rb;
 // 16 consecutive lanes touch 128 consecutive bytes.
-__device__ __forceinline__ long long nat_a(int r0) {
+__device__ __forceinline__ long long nat_a(int g) {
   const RowMap mn = map_n();
-  return (long long)(r0 + mn.rb) * 256 + mn.j;
+  return (long long)(g + 16 * mn.rb) * 256 + mn.j;
 }
 
-// NTT rows pass of 16 transposed-layout rows: loads under map T (layout A), returns layout A under
-// map N (thread owns natural words nat_a(r0) + 16k).
-__device__ __forceinline__ void rows_fwd_from_t(double (&x)[16], const double* __restrict__ src_t, int r0,
-                                                double* S, const double* __restrict__ tw, double p, double pinv) {
-  const RowMap mt = map_t(), mn = map_n();
+// Workspace element of row g + 16 rb (map T, layout A: columns j + 16 k) at column-major position
+// 16 g + rb.
+__device__ __forceinline__ long long ws_a(int g, int k) {
+  const RowMap mt = map_t();
+  return (long long)(mt.j + 16 * k) * 256 + 16 * g + mt.rb;
+}
+
+__device__ __forceinline__ void load_t(double (&x)[16], const double* __restrict__ src_t, int g) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) x[k] = src_t[(long long)(mt.j + 16 * k) * 256 + r0 + mt.rb];
-  row_fwd_lo(x, r0 + mt.rb, tw, p, pinv);
+  for (int k = 0; k < 16; ++k) x[k] = src_t[ws_a(g, k)];
+}
+
+// NTT rows pass of row group g, x loaded by load_t (map T, layout A); returns layout A under map N
+// (thread owns natural words nat_a(g) + 16k).
+__device__ __forceinline__ void rows_fwd_t(double (&x)[16], int g, double* S, const double* __restrict__ tw,
+                                           double p, double pinv) {
+  const RowMap mt = map_t(), mn = map_n();
+  row_fwd_lo(x, g + 16 * mt.rb, tw, p, pinv);
   row_xchg<true, false>(x, S, mt, mn);
-  row_fwd_hi(x, r0 + mn.rb, mn.j, tw, p, pinv);
+  row_fwd_hi(x, g + 16 * mn.rb, mn.j, tw, p, pinv);
   row_xchg<false, true>(x, S, mn, mn);
 }
 
-// INTT rows pass of 16 rows held in layout A under map N; stores the result transposed.
-__device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restrict__ dst_t, int r0, double* S,
+// INTT rows pass of row group g held in layout A under map N; stores the result to the workspace.
+__device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restrict__ dst_t, int g, double* S,
                                               const double* __restrict__ tw, double p, double pinv) {
   const RowMap mt = map_t(), mn = map_n();
   row_xchg<true, false>(x, S, mn, mn);
-  row_inv_hi(x, r0 + mn.rb, mn.j, tw, p, pinv);
+  row_inv_hi(x, g + 16 * mn.rb, mn.j, tw, p, pinv);
   row_xchg<false, true>(x, S, mn, mt);
-  row_inv_lo(x, r0 + mt.rb, tw, p, pinv);
+  row_inv_lo(x, g + 16 * mt.rb, tw, p, pinv);
 #pragma unroll
-  for (int k = 0; k < 16; ++k) dst_t[(long long)(mt.j + 16 * k) * 256 + r0 + mt.rb] = x[k];
+  for (int k = 0; k < 16; ++k) dst_t[ws_a(g, k)] = x[k];
 }
 
 // ----------------------------------------------------------------- K1: INTT rows of d
@@ -296,97 +309,124 @@ __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict_
                                                      uint32_t g, int limb0, int prime0, double* __restrict__ t1,
                                                      DevTables T) {
   __shared__ double S[kRowLds];
-  const int i = blockIdx.z, b = blockIdx.x, r0 = blockIdx.y * 16;
+  const int i = blockIdx.z, b = blockIdx.x, rg = blockIdx.y;
   const int pi = prime0 + i;
   const double p = T.p[pi], pinv = T.pinv[pi];
   const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   double x[16];
-  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(r0), g);
-  rows_inv_to_t(x, t1 + ((long long)b * gridDim.z + i) * kN, r0, S, tw, p, pinv);
+  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), g);
+  rows_inv_to_t(x, t1 + ((long long)b * gridDim.z + i) * kN, rg, S, tw, p, pinv);
 }
 
 // ----------------------------------------------------------------- K2 / K4: cols + conversion
-// Block: two columns (c0, c0 + 1) of one conversion group.  Phase 1: INTT cols of each source limb,
-// y_s = centered [x_s * hinv_s] into LDS.  Phase 2: per target t, sum_s y_s * hmod[s][t], NTT cols,
-// store.  16 slots of 16 threads; slot sigma handles (limb = pi >> 1, column = pi & 1), pi = 16 r + sigma.
+// Block: two columns (c0, c0 + 1) of one conversion group; 16 slots of 16 threads.  LDS holds 16 runs
+// of kYStride doubles (Y).
+// Phase 1: slot sigma owns (source s = sigma >> 1, column sigma & 1): it loads the column straight
+// into layout B, runs the INTT col stages with run sigma as its exchange buffer (the last stage also
+// multiplies by hinv_s, folded into N^-1), and leaves y_s = centered [x_s * hinv_s] in run sigma.
+// Phase 2: thread j of slot sigma owns rows j + 16k of column sigma & 1 for the targets
+// tg = 8 r + (sigma >> 1), r = 0 .. rounds - 1: they share that column, so each y value read from LDS
+// feeds up to kRoundsFused targets at once.  Then NTT col stages per target, stored straight from
+// layout B.  Without SEPX (at most kRoundsFused rounds) the exchanges reuse the Y runs after a
+// barrier that follows the last read of Y; SEPX keeps separate exchange runs for more targets.
+constexpr int kRoundsFused = 3;                 // targets per thread held in registers
+constexpr int kTgtFused = 8 * kRoundsFused;     // targets a conversion group may have without SEPX
+
+template <bool SEPX>
 __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ src, long long src_zs,
                                                      long long src_ys, int src_off_y, double* __restrict__ dst,
                                                      long long dst_zs, long long dst_ys,
                                                      const ConvConsts* __restrict__ cc_base, int cc_y,
                                                      DevTables T) {
-  __shared__ double X[16 * 272];              // per-slot exchange runs
-  __shared__ double Y[kSrcMax * 2 * kYStride];  // y_s for both columns
-  __shared__ TwPair H[kSrcMax * kMaxPrimes];    // hmod[s][t] of this conversion group
+  __shared__ double Y[16 * kYStride];
+  __shared__ double X[SEPX ? 16 * kYStride : 1];
+  __shared__ TwPair H[kSrcMax * (SEPX ? kMaxPrimes : kTgtFused)];  // H[s * nt + tg] = hmod[s][tg]
   const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
   const int c0 = blockIdx.x * 2;
   const int y = blockIdx.y;
   const long long z = blockIdx.z;
   const ConvConsts& C = cc_base[y * cc_y];
   const int ns = C.ns, nt = C.nt;
-  for (int q = t; q < ns * nt; q += kT) H[(q / nt) * kMaxPrimes + q % nt] = C.hmod[q / nt][q % nt];
-  double* R = X + sigma * 272;
-  const double* sbase = src + z * src_zs + y * src_ys + (long long)y * src_off_y * kN;
-  double x[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) x[k] = 0.0;
-  // phase 1
-  for (int r = 0; r < (2 * ns + 15) / 16; ++r) {
-    const int pi = 16 * r + sigma, s = pi >> 1, cl = pi & 1;
+  for (int q = t; q < ns * nt; q += kT) H[q] = C.hmod[q / nt][q % nt];
+  const int cl = sigma & 1;
+  double* R = Y + sigma * kYStride;
+  // phase 1 (ns <= 8: one task per slot)
+  {
+    const int s = sigma >> 1;
     const bool act = s < ns;
     const int sp = C.src_prime[act ? s : 0];
     const double p = T.p[sp], pinv = T.pinv[sp];
     const double* __restrict__ tw = T.tw_inv + (size_t)sp * kN;
-    if (act) {
-      const double* col = sbase + (long long)s * kN + (long long)(c0 + cl) * 256;
+    double x[16];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = col[j + 16 * k];
+    for (int k = 0; k < 16; ++k) x[k] = 0.0;
+    if (act) {
+      const double* col = src + z * src_zs + y * src_ys + (long long)(y * src_off_y + s) * kN +
+                          (long long)(c0 + cl) * 256;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = col[16 * k + j];
+      col_inv_hi(x, j, tw, p, pinv);
     }
-    col_a_to_b(x, R, j);
-    if (act) col_inv_hi(x, j, tw, p, pinv);
     col_b_to_a(x, R, j);
     if (act) {
-      col_inv_lo(x, tw, T.ninv[sp], T.ninv_w1[sp], p, pinv);
-      const TwPair hi = C.hinv[s];
-      double* Yr = Y + (s * 2 + cl) * kYStride;
+      col_inv_lo(x, tw, C.inv_n0[s], C.inv_n1[s], p, pinv);
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        const double v = canon(mulc(x[k], hi, p), p, pinv);
-        Yr[j + 16 * k] = v > 0.5 * p ? v - p : v;  // centered lift: zero-mean
+        const double v = canon(x[k], p, pinv);
+        R[j + 16 * k] = v > 0.5 * p ? v - p : v;  // centered lift: zero-mean
       }
     }
   }
   __syncthreads();
   // phase 2
-  double* dbase = dst + z * dst_zs + y * dst_ys;
-  for (int r = 0; r < (2 * nt + 15) / 16; ++r) {
-    const int pi = 16 * r + sigma, tg = pi >> 1, cl = pi & 1;
-    const bool act = tg < nt;
-    const int tp = C.dst_prime[act ? tg : 0];
-    const double p = T.p[tp], pinv = T.pinv[tp];
-    const double* __restrict__ tw = T.tw_fwd + (size_t)tp * kN;
-    if (act) {
+  const int rounds = (nt + 7) / 8;
+  double* dbase = dst + z * dst_zs + y * dst_ys + (long long)(c0 + cl) * 256;
+  double* RX = SEPX ? X + sigma * kYStride : R;
+  for (int r0 = 0; r0 < rounds; r0 += kRoundsFused) {
+    double x[kRoundsFused][16];
+    int tg[kRoundsFused];
+    double p[kRoundsFused], pinv[kRoundsFused];
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = 0.0;
+    for (int u = 0; u < kRoundsFused; ++u) {
+      const int tt = 8 * (r0 + u) + (sigma >> 1);
+      tg[u] = tt < nt ? tt : -1;
+      const int tp = C.dst_prime[tt < nt ? tt : 0];
+      p[u] = T.p[tp];
+      pinv[u] = T.pinv[tp];
 #pragma unroll
-      for (int s = 0; s < kSrcMax; ++s) {
-        if (s < ns) {
-          const TwPair h = H[s * kMaxPrimes + tg];
-          const double* Yr = Y + (s * 2 + cl) * kYStride;
+      for (int k = 0; k < 16; ++k) x[u][k] = 0.0;
+    }
+    for (int s = 0; s < ns; ++s) {
+      const double* Yr = Y + (s * 2 + cl) * kYStride;
+      TwPair h[kRoundsFused];
 #pragma unroll
-          for (int k = 0; k < 16; ++k) x[k] += mulc(Yr[j + 16 * k], h, p);  // |term| <= 0.69 p
+      for (int u = 0; u < kRoundsFused; ++u) h[u] = H[s * nt + (tg[u] < 0 ? 0 : tg[u])];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const double v = Yr[j + 16 * k];
+#pragma unroll
+        for (int u = 0; u < kRoundsFused; ++u) x[u][k] += mulc(v, h[u], p[u]);  // |term| <= 0.69 p
+      }
+    }
+    if (!SEPX) __syncthreads();  // every slot is done reading Y before the runs become exchange buffers
+#pragma unroll
+    for (int u = 0; u < kRoundsFused; ++u) {
+      if (r0 + u < rounds) {  // uniform across the block
+        const bool act = tg[u] >= 0;
+        const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? tg[u] : 0] * kN;
+        if (act) {
+#pragma unroll
+          for (int k = 0; k < 16; ++k) x[u][k] = reduce(x[u][k], p[u], pinv[u]);
+          col_fwd_lo(x[u], tw, p[u], pinv[u]);
+        }
+        col_a_to_b(x[u], RX, j);
+        if (act) {
+          col_fwd_hi(x[u], j, tw, p[u], pinv[u]);
+          double* col = dbase + (long long)C.dst_slot[tg[u]] * kN;
+#pragma unroll
+          for (int k = 0; k < 16; ++k) col[16 * k + j] = x[u][k];
         }
       }
-#pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = reduce(x[k], p, pinv);
-      col_fwd_lo(x, tw, p, pinv);
-    }
-    col_a_to_b(x, R, j);
-    if (act) col_fwd_hi(x, j, tw, p, pinv);
-    col_b_to_a(x, R, j);
-    if (act) {
-      double* col = dbase + (long long)C.dst_slot[tg] * kN + (long long)(c0 + cl) * 256;
-#pragma unroll
-      for (int k = 0; k < 16; ++k) col[j + 16 * k] = x[k];
     }
   }
 }
@@ -411,7 +451,7 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
   const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
   const int tile = (q / batch) * kXcds + xcd, b = q % batch;
   if (tile >= tiles) return;
-  const int e = tile >> 4, r0 = (tile & 15) * 16;
+  const int e = tile >> 4, rg = tile & 15;
   const int L = T.L, K = T.K, alpha = T.alpha;
   const int ext_l = ell + K;
   const int pi = e < ell ? e : L + (e - ell);
@@ -421,21 +461,21 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
   const long long comp_stride = (long long)beta_max * (L + K) * kN;
   const uint64_t* key = keys.k[b];
   const int own = e < ell ? e / alpha : -1;
-  const long long na = nat_a(r0);
+  const long long na = nat_a(rg);
   double sb[16], sa[16], x[16];
   uint64_t kb[16], ka[16];
 #pragma unroll
   for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
   for (int jd = 0; jd < beta; ++jd) {
-    // issue this digit's key loads first: they land while the NTT below computes
+    // the digit's loads go first and the key's after them, so the NTT below waits only for the
+    // digit while the key lands
+    const bool mine = jd == own;
+    if (mine) load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
+    else load_t(x, t2 + (((long long)b * beta + jd) * ext_l + e) * kN, rg);
     const uint64_t* kp = key + ((long long)jd * (L + K) + pi) * kN + na;
 #pragma unroll
     for (int k = 0; k < 16; ++k) { kb[k] = kp[16 * k]; ka[k] = kp[comp_stride + 16 * k]; }
-    if (jd == own) {
-      load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
-    } else {
-      rows_fwd_from_t(x, t2 + (((long long)b * beta + jd) * ext_l + e) * kN, r0, S, twf, p, pinv);
-    }
+    if (!mine) rows_fwd_t(x, rg, S, twf, p, pinv);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);  // |x| <= 3.9p: |term| <= 2p
@@ -481,8 +521,8 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
   // P limb: INTT rows of both components, stored transposed for the ModDown cols kernel
   const double* __restrict__ twi = T.tw_inv + (size_t)pi * kN;
   double* o = accp + ((long long)b * 2 * K + (e - ell)) * kN;
-  rows_inv_to_t(sb, o, r0, S, twi, p, pinv);
-  rows_inv_to_t(sa, o + (long long)K * kN, r0, S, twi, p, pinv);
+  rows_inv_to_t(sb, o, rg, S, twi, p, pinv);
+  rows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, p, pinv);
 }
 
 // ----------------------------------------------------------------- K5: NTT rows + ModDown combine
@@ -499,11 +539,11 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
                                                        long long out_stride, int ell,
                                                        const LevelConsts* __restrict__ lc, DevTables T) {
   __shared__ double S[kRowLds];
-  const int i = blockIdx.z, r0 = blockIdx.y * 16;
+  const int i = blockIdx.z, rg = blockIdx.y;
   const int b = blockIdx.x >> 1, comp = blockIdx.x & 1;
   const double p = T.p[i], pinv = T.pinv[i];
   const double* __restrict__ tw = T.tw_fwd + (size_t)i * kN;
-  const long long na = nat_a(r0);
+  const long long na = nat_a(rg);
   // prefetch the accumulator (and the rotation addend) before the transform
   double a[16];
   const AccT* ap = accq + (long long)blockIdx.x * accq_pstride + (long long)i * kN + na;
@@ -518,7 +558,8 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
   const uint64_t* accp_ = comp == 0 ? acc_b : acc_a;
   if (accp_) load_gal(ac, accp_ + (long long)b * acc_stride + (long long)i * kN, na, 1u);
   double x[16];
-  rows_fwd_from_t(x, t4 + (((long long)b * 2 + comp) * ell + i) * kN, r0, S, tw, p, pinv);
+  load_t(x, t4 + (((long long)b * 2 + comp) * ell + i) * kN, rg);
+  rows_fwd_t(x, rg, S, tw, p, pinv);
   const TwPair pi_ = lc->p_inv[i];
   uint64_t* o = (comp == 0 ? out_b : out_a) + (long long)b * out_stride + (long long)i * kN + na;
 #pragma unroll
@@ -556,7 +597,10 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, galois, 0, 0, r1, c->dev);
   HCK_CHECK_LAUNCH();
   // K2: ModUp, one block per (column pair, digit, ciphertext)
-  k_ks_cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
+  // ModUp targets of digit j: ext_l minus the digit's own limbs; the last digit is the smallest
+  const int last_digit = ell - c->alpha * (beta - 1);
+  auto cols_conv = ext_l - last_digit <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
                                                        (long long)beta * ext_l * n, (long long)ext_l * n,
                                                        modup_consts(c, ell, 0), 1, c->dev);
   HCK_CHECK_LAUNCH();
@@ -573,7 +617,8 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   if (ext_b) return HCK_OK;
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
   double* t4 = r1;
-  k_ks_cols_conv<<<dim3(128, 2, batch), kT, 0, s>>>(accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n,
+  auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  md_conv<<<dim3(128, 2, batch), kT, 0, s>>>(accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n,
                                                     (long long)ell * n, c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
   // K5
@@ -599,7 +644,8 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   double* t4 = tp + (long long)polys * K * n;     // [polys][ell] transposed
   k_ks_intt_rows<<<dim3(polys, 16, K), kT, 0, s>>>(in, in_stride, 1u, ell, c->L, tp, c->dev);
   HCK_CHECK_LAUNCH();
-  k_ks_cols_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
+  auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
                                                     c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
   // poly p = 2 b + comp: out_b / out_a interleave at out_stride, so p lands at out + p * out_stride
