@@ -431,38 +431,22 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
   }
 }
 
-// ----------------------------------------------------------------- K3: NTT rows + inner product
-// Grid: one linear id per (ciphertext, tile), tile = (row group, extended limb).  Workgroups are
-// dealt to the 8 XCDs round-robin; the decode keeps every ciphertext of one tile on one XCD, one
-// after another, so a key shared by the batch (a giant step) is read from HBM once per tile and
-// served from that XCD's L2 to the other ciphertexts.
-// With ext_b set the kernel ends the key switch in the extended basis: it writes (P * sigma(add) +
-// IP_b, IP_a) over Q u P as canonical NTT-domain residues to ext_b / ext_a ([ell + K] limbs per
-// ciphertext, Q limbs first), plus the extended-basis accumulators acc_b / acc_a when given (which
-// ext_b / ext_a may alias), and skips the ModDown inputs.
-__global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
-                                                   const double* __restrict__ t2, KeyPtrsF keys, int ell,
-                                                   int beta, int batch, int tiles, double* __restrict__ accq,
-                                                   double* __restrict__ accp, const uint64_t* __restrict__ add,
-                                                   long long add_stride, uint64_t* ext_b, uint64_t* ext_a,
-                                                   long long ext_stride, const uint64_t* acc_b,
-                                                   const uint64_t* acc_a, long long acc_stride, DevTables T) {
-  __shared__ double S[kRowLds];
-  const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
-  const int tile = (q / batch) * kXcds + xcd, b = q % batch;
-  if (tile >= tiles) return;
-  const int e = tile >> 4, rg = tile & 15;
+// ----------------------------------------------------------------- inner product of one tile
+// sb / sa = sum_j x_j * key_j[comp] over the digits j of ciphertext b, extended limb e (prime pi),
+// row group rg: x_j is the NTT rows pass of the ModUp output T2 (or, for the digit that contains
+// limb e, d itself read through sigma_g).  Returns |sb|, |sa| <= p/2 + 1.
+__device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], const uint64_t* __restrict__ d,
+                                        long long d_stride, uint32_t g, const double* __restrict__ t2,
+                                        const uint64_t* __restrict__ key, int b, int e, int pi, int rg, int ell,
+                                        int beta, double* S, const double* __restrict__ twf, double p, double pinv,
+                                        const DevTables& T) {
   const int L = T.L, K = T.K, alpha = T.alpha;
   const int ext_l = ell + K;
-  const int pi = e < ell ? e : L + (e - ell);
-  const double p = T.p[pi], pinv = T.pinv[pi];
-  const double* __restrict__ twf = T.tw_fwd + (size_t)pi * kN;
   const int beta_max = (L + alpha - 1) / alpha;
   const long long comp_stride = (long long)beta_max * (L + K) * kN;
-  const uint64_t* key = keys.k[b];
   const int own = e < ell ? e / alpha : -1;
   const long long na = nat_a(rg);
-  double sb[16], sa[16], x[16];
+  double x[16];
   uint64_t kb[16], ka[16];
 #pragma unroll
   for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
@@ -488,6 +472,45 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
   }
 #pragma unroll
   for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+}
+
+// Grids of the tile kernels: one linear id per (ciphertext, tile).  Workgroups are dealt to the 8
+// XCDs round-robin; the decode keeps every ciphertext of one tile on one XCD, one after another, so
+// a key shared by the batch (a giant step) is read from HBM once per tile and served from that
+// XCD's L2 to the other ciphertexts.
+struct TileId {
+  int tile, b;
+};
+__device__ __forceinline__ TileId decode_tile(int batch) {
+  const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
+  return TileId{(q / batch) * kXcds + xcd, q % batch};
+}
+
+// ----------------------------------------------------------------- K3: inner product, P limbs / ext
+// Tile = (row group, extended limb e0 + tile / 16).  Without ext_b the kernel covers the K special
+// limbs (e0 = ell): the inner product's INTT rows pass goes to ACCP (workspace layout) for the
+// ModDown conversion.  With ext_b it covers all ell + K limbs (e0 = 0) and ends the key switch in the
+// extended basis: it writes (P * sigma(add) + IP_b, IP_a) over Q u P as canonical NTT-domain residues
+// to ext_b / ext_a ([ell + K] limbs per ciphertext, Q limbs first), plus the extended-basis
+// accumulators acc_b / acc_a when given (which ext_b / ext_a may alias).
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
+                                                   const double* __restrict__ t2, KeyPtrsF keys, int ell,
+                                                   int beta, int batch, int tiles, int e0, double* __restrict__ accp,
+                                                   const uint64_t* __restrict__ add, long long add_stride,
+                                                   uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
+                                                   const uint64_t* acc_b, const uint64_t* acc_a,
+                                                   long long acc_stride, DevTables T) {
+  __shared__ double S[kRowLds];
+  const TileId id = decode_tile(batch);
+  if (id.tile >= tiles) return;
+  const int b = id.b, e = e0 + (id.tile >> 4), rg = id.tile & 15;
+  const int L = T.L, K = T.K;
+  const int pi = e < ell ? e : L + (e - ell);
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  const double* __restrict__ twf = T.tw_fwd + (size_t)pi * kN;
+  double sb[16], sa[16];
+  tile_ip(sb, sa, d, d_stride, g, t2, keys.k[b], b, e, pi, rg, ell, beta, S, twf, p, pinv, T);
+  const long long na = nat_a(rg);
   if (ext_b) {
     if (e < ell && add) {
       double ad[16];
@@ -512,72 +535,100 @@ __global__ __launch_bounds__(kT) void k_ks_rows_ip(const uint64_t* __restrict__ 
     }
     return;
   }
-  if (e < ell) {
-    double* ob = accq + ((long long)b * 2 * ell + e) * kN + na;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) { ob[16 * k] = sb[k]; ob[(long long)ell * kN + 16 * k] = sa[k]; }
-    return;
-  }
-  // P limb: INTT rows of both components, stored transposed for the ModDown cols kernel
+  // P limb: INTT rows of both components, stored to the workspace for the ModDown cols kernel
   const double* __restrict__ twi = T.tw_inv + (size_t)pi * kN;
   double* o = accp + ((long long)b * 2 * K + (e - ell)) * kN;
   rows_inv_to_t(sb, o, rg, S, twi, p, pinv);
   rows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, p, pinv);
 }
 
-// ----------------------------------------------------------------- K5: NTT rows + ModDown combine
-// Poly p = blockIdx.x (= 2 b + comp): v = NTT rows of T4[p]; out = (ACCQ[p] - v) * P^-1 (+ addends).
-// ACCQ is the inner product's lazy FP64 output (key switch) or canonical u64 residues (ModDown of
-// an extended-basis ciphertext); accq_pstride is its per-poly stride in elements.
-template <typename AccT>
-__global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const AccT* __restrict__ accq,
-                                                       long long accq_pstride,
-                                                       const uint64_t* __restrict__ add, long long add_stride,
-                                                       uint32_t g, const uint64_t* __restrict__ acc_b,
-                                                       const uint64_t* __restrict__ acc_a, long long acc_stride,
-                                                       uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
-                                                       long long out_stride, int ell,
+// One component of the ModDown finish: ip <- (ip - NTT rows(v_t)) * P^-1, then the addends (read after
+// the transform, so only ip, its sibling and the transform are live at once), canonical store.
+__device__ __forceinline__ void ipq_finish(double (&ip)[16], const double* __restrict__ v_t,
+                                           const uint64_t* __restrict__ add_limb, uint32_t g,
+                                           const uint64_t* __restrict__ acc_limb, uint64_t* __restrict__ o,
+                                           long long na, int rg, double* S, const double* __restrict__ twf,
+                                           TwPair pinv_P, double p, double pinv) {
+  double x[16];
+  load_t(x, v_t, rg);
+  rows_fwd_t(x, rg, S, twf, p, pinv);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) ip[k] = mulc(ip[k] - x[k], pinv_P, p);  // |ip - v| <= 4.5 p: |r| <= 2.2 p
+  if (add_limb) {
+    load_gal(x, add_limb, na, g);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ip[k] += x[k];
+  }
+  if (acc_limb) {
+    load_gal(x, acc_limb, na, 1u);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ip[k] += x[k];  // |r| <= 4.2 p
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
+}
+
+// ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
+// Tile = (row group, Q limb i): the inner product of limb i (as in K3) is combined with the NTT rows
+// pass v of the ModDown conversion T4 right away, so the Q-limb inner product never goes to HBM:
+//   out_b = (IP_b - v_b) * P^-1 + sigma_g(add) (+ acc_b),   out_a = (IP_a - v_a) * P^-1 (+ acc_a),
+// canonical u64.
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
+                                                    const double* __restrict__ t2, KeyPtrsF keys, int ell, int beta,
+                                                    int batch, const double* __restrict__ t4,
+                                                    const uint64_t* __restrict__ add, long long add_stride,
+                                                    const uint64_t* __restrict__ acc_b,
+                                                    const uint64_t* __restrict__ acc_a, long long acc_stride,
+                                                    uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
+                                                    long long out_stride, const LevelConsts* __restrict__ lc,
+                                                    DevTables T) {
+  __shared__ double S[kRowLds];
+  const TileId id = decode_tile(batch);
+  if (id.tile >= 16 * ell) return;
+  const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const double* __restrict__ twf = T.tw_fwd + (size_t)i * kN;
+  double sb[16], sa[16];
+  tile_ip(sb, sa, d, d_stride, g, t2, keys.k[b], b, i, i, rg, ell, beta, S, twf, p, pinv, T);
+  const long long na = nat_a(rg);
+  const TwPair pinv_P = lc->p_inv[i];
+  ipq_finish(sb, t4 + ((long long)b * 2 * ell + i) * kN, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr,
+             g, acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
+             out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, twf, pinv_P, p, pinv);
+  ipq_finish(sa, t4 + ((long long)b * 2 * ell + ell + i) * kN, nullptr, 1u,
+             acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
+             out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, twf, pinv_P, p, pinv);
+}
+
+// ----------------------------------------------------------------- ModDown finish of ext-basis input
+// Poly p = blockIdx.x: v = NTT rows of T4[p]; out = (x_Q[p] - v) * P^-1 with x_Q canonical u64.
+__global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const uint64_t* __restrict__ xq,
+                                                       long long xq_pstride, uint64_t* __restrict__ out,
+                                                       long long out_pstride, int ell,
                                                        const LevelConsts* __restrict__ lc, DevTables T) {
   __shared__ double S[kRowLds];
-  const int i = blockIdx.z, rg = blockIdx.y;
-  const int b = blockIdx.x >> 1, comp = blockIdx.x & 1;
+  const int i = blockIdx.z, rg = blockIdx.y, pl = blockIdx.x;
   const double p = T.p[i], pinv = T.pinv[i];
   const double* __restrict__ tw = T.tw_fwd + (size_t)i * kN;
   const long long na = nat_a(rg);
-  // prefetch the accumulator (and the rotation addend) before the transform
-  double a[16];
-  const AccT* ap = accq + (long long)blockIdx.x * accq_pstride + (long long)i * kN + na;
+  double a[16], x[16];
+  const uint64_t* ap = xq + (long long)pl * xq_pstride + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    if constexpr (std::is_same<AccT, uint64_t>::value) a[k] = u2d(ap[16 * k]);
-    else a[k] = ap[16 * k];
-  }
-  double ad[16], ac[16];
-  const bool has_add = comp == 0 && add;
-  if (has_add) load_gal(ad, add + (long long)b * add_stride + (long long)i * kN, na, g);
-  const uint64_t* accp_ = comp == 0 ? acc_b : acc_a;
-  if (accp_) load_gal(ac, accp_ + (long long)b * acc_stride + (long long)i * kN, na, 1u);
-  double x[16];
-  load_t(x, t4 + (((long long)b * 2 + comp) * ell + i) * kN, rg);
+  for (int k = 0; k < 16; ++k) a[k] = u2d(ap[16 * k]);
+  load_t(x, t4 + ((long long)pl * ell + i) * kN, rg);
   rows_fwd_t(x, rg, S, tw, p, pinv);
   const TwPair pi_ = lc->p_inv[i];
-  uint64_t* o = (comp == 0 ? out_b : out_a) + (long long)b * out_stride + (long long)i * kN + na;
+  uint64_t* o = out + (long long)pl * out_pstride + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    double r = mulc(a[k] - x[k], pi_, p);  // |acc - v| <= 4.5 p: |r| <= 2.2 p
-    if (has_add) r += ad[k];
-    if (accp_) r += ac[k];                 // |r| <= 4.2 p
-    o[16 * k] = d2u(canon(r, p, pinv));
-  }
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(a[k] - x[k], pi_, p), p, pinv));
 }
 
 }  // namespace
 
-// Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)],
-// ACCQ [2 ell], ACCP [2 K].
+// Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)], ACCP [2 K].
 size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
   const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
-  return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * ell + 2 * c->K);
+  return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * c->K);
 }
 
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
@@ -590,42 +641,52 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   const long long n = kN;
   double* r1 = (double*)ws;
   double* t2 = r1 + (long long)batch * 2 * ell * n;
-  double* accq = t2 + (long long)batch * beta * ext_l * n;
-  double* accp = accq + (long long)batch * 2 * ell * n;
+  double* accp = t2 + (long long)batch * beta * ext_l * n;
   // K1
   // row kernels: ciphertext index fastest, so the blocks in flight share one prime's twiddles
   k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, galois, 0, 0, r1, c->dev);
   HCK_CHECK_LAUNCH();
-  // K2: ModUp, one block per (column pair, digit, ciphertext)
-  // ModUp targets of digit j: ext_l minus the digit's own limbs; the last digit is the smallest
+  // K2: ModUp, one block per (column pair, digit, ciphertext).  Targets of digit j: ext_l minus the
+  // digit's own limbs; the last digit is the smallest.
   const int last_digit = ell - c->alpha * (beta - 1);
   auto cols_conv = ext_l - last_digit <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
   cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
-                                                       (long long)beta * ext_l * n, (long long)ext_l * n,
-                                                       modup_consts(c, ell, 0), 1, c->dev);
+                                                  (long long)beta * ext_l * n, (long long)ext_l * n,
+                                                  modup_consts(c, ell, 0), 1, c->dev);
   HCK_CHECK_LAUNCH();
-  // K3
   KeyPtrsF kp{};
   for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
-  const int tiles = 16 * ext_l;
-  const int groups = (tiles + kXcds - 1) / kXcds;
-  k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
-                                                          accq, accp, add, add_stride, ext_b, ext_a, ext_stride,
-                                                          ext_b ? acc_b : nullptr, ext_b ? acc_a : nullptr,
-                                                          acc_stride, c->dev);
-  HCK_CHECK_LAUNCH();
-  if (ext_b) return HCK_OK;
+  if (ext_b) {
+    // K3 over every extended limb, ending in the extended basis
+    const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
+    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
+                                                            0, nullptr, add, add_stride, ext_b, ext_a, ext_stride,
+                                                            acc_b, acc_a, acc_stride, c->dev);
+    HCK_CHECK_LAUNCH();
+    return HCK_OK;
+  }
+  // K3 over the K special limbs
+  {
+    const int tiles = 16 * K, groups = (tiles + kXcds - 1) / kXcds;
+    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
+                                                            ell, accp, nullptr, 0, nullptr, nullptr, 0, nullptr,
+                                                            nullptr, 0, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
   double* t4 = r1;
   auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
   md_conv<<<dim3(128, 2, batch), kT, 0, s>>>(accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n,
-                                                    (long long)ell * n, c->d_moddown + ell, 0, c->dev);
+                                             (long long)ell * n, c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
-  // K5
-  k_ks_rows_finish<double><<<dim3(2 * batch, 16, ell), kT, 0, s>>>(t4, accq, (long long)ell * n, add, add_stride,
-                                                                   galois, acc_b, acc_a, acc_stride, out_b, out_a,
-                                                                   out_stride, ell, c->d_level + ell, c->dev);
-  HCK_CHECK_LAUNCH();
+  // K5: Q limbs
+  {
+    const int tiles = 16 * ell, groups = (tiles + kXcds - 1) / kXcds;
+    k_ks_rows_ipq<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, t4,
+                                                             add, add_stride, acc_b, acc_a, acc_stride, out_b,
+                                                             out_a, out_stride, c->d_level + ell, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
   return HCK_OK;
 }
 
@@ -640,18 +701,16 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   if (c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   const int K = c->K;
   const long long n = kN;
-  double* tp = (double*)ws;                       // [polys][K] transposed
-  double* t4 = tp + (long long)polys * K * n;     // [polys][ell] transposed
+  double* tp = (double*)ws;                       // [polys][K] workspace layout
+  double* t4 = tp + (long long)polys * K * n;     // [polys][ell] workspace layout
   k_ks_intt_rows<<<dim3(polys, 16, K), kT, 0, s>>>(in, in_stride, 1u, ell, c->L, tp, c->dev);
   HCK_CHECK_LAUNCH();
   auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
   md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
-                                                    c->d_moddown + ell, 0, c->dev);
+                                             c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
-  // poly p = 2 b + comp: out_b / out_a interleave at out_stride, so p lands at out + p * out_stride
-  k_ks_rows_finish<uint64_t><<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, nullptr, 0, 1u, nullptr, nullptr,
-                                                                 0, out, out + out_stride, 2 * out_stride, ell,
-                                                                 c->d_level + ell, c->dev);
+  k_ks_rows_finish<<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, out, out_stride, ell, c->d_level + ell,
+                                                       c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }

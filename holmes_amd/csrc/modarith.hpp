@@ -66,13 +66,18 @@ __device__ __forceinline__ double canon(double x, double p, double pinv) {
   return r;
 }
 
-// a * b mod p for a residue b in [0, p) without a stored companion: the quotient estimate uses
-// fl(b * pinv) (two roundings, relative error <= 1.5 * 2^-52), so for |a| = A p,
+// a * b mod p for a residue b in [0, p) without a stored companion: the quotient is estimated
+// from the product itself, q = rint(fl(a * b) * pinv).  fl(fl(a b) pinv) is within three
+// roundings of X = a b / p, so |q - X| <= 0.5 + |X| 3 2^-53, and with |X| < |a| = A p,
 //   |r| <= (0.5 + 0.375 A) p   (p < 2^50),
-// and the FMA stays exact while |a| < 2^53.  Twiddle tables store only w (8 bytes); their
-// companion is recomputed here, halving the table traffic of the NTT passes.
+// the bound of mulc.  For |a| <= 2^52 (A <= 4): |h - q p| <= 2p + 2^49 < 2^53, so the FMA is
+// exact and r == a b (mod p).  Twiddle tables store only w (8 bytes), and the product doubles as
+// the quotient's input: 6 FP64 operations.
 __device__ __forceinline__ double mulv(double a, double b, double p, double pinv) {
-  return mulc(a, b, b * pinv, p);
+  const double h = a * b;
+  const double q = __builtin_rint(h * pinv);
+  const double l = __builtin_fma(a, b, -h);
+  return __builtin_fma(-q, p, h) + l;
 }
 
 }  // namespace hck
