@@ -2,19 +2,21 @@
 //
 // A limb (N = 2^16 words) is a 256 x 256 matrix, n = 256 r + c.  The forward NTT runs stages
 // 0..7 inside columns ("cols" pass) and 8..15 inside rows ("rows" pass); the inverse runs rows
-// (15..8) then cols (7..0).  Workspace buffers keep limbs column-major, a column 2 KiB contiguous,
-// with row r of a column at position tpos(r) = 16 (r mod 16) + r / 16 (the two nibbles of r
-// swapped).  A rows-kernel block owns the 16 rows g + 16 m (row group g), which sit at positions
-// 16 g .. 16 g + 15 of every column (128-byte runs); a cols-kernel thread holding rows 16 j + k
-// (k = 0..15) finds them at positions 16 k + j, so 16 lanes touch 128 consecutive bytes.
+// (15..8) then cols (7..0).  A rows-kernel block owns row group g: the 16 rows g + 16 m.
+// Workspace buffers keep limbs tile-major: element (r, c) at wpos(r, c) = 4096 (r mod 16) +
+// 16 c + r / 16, so each row group is one contiguous 32 KiB run ([column][m]) that the rows
+// kernels read and write whole, while a cols-kernel thread holding rows 16 j + k (k = 0..15) of
+// column c finds them at 4096 k + 16 c + j: 16 lanes touch 128 consecutive bytes (256 per column
+// pair).  The memory-bound rows kernels get the contiguous side; the VALU-bound cols kernels the
+// strided one.
 //
-//   K1 ks_intt_rows   sigma_g(d) (natural, u64) --INTT rows-->                T1 (transposed)
+//   K1 ks_intt_rows   sigma_g(d) (natural, u64) --INTT rows-->                T1 (workspace)
 //   K2 ks_cols_conv   T1 --INTT cols--> coefficients --ModUp conversion (LDS)--> NTT cols --> T2
-//   K3 ks_rows_ip     T2 --NTT rows--> x_j;  acc = sum_j x_j * key_j  (d for the digit's own limbs)
-//                     Q limbs: acc --> ACCQ (natural);  P limbs: acc --INTT rows--> ACCP (transposed)
+//   K3 ks_rows_ip     P limbs: T2 --NTT rows--> x_j;  acc = sum_j x_j * key_j --INTT rows--> ACCP
 //   K4 ks_cols_conv   ACCP --INTT cols--> ModDown conversion P -> Q --NTT cols--> T4
-//   K5 ks_rows_finish T4 --NTT rows--> v;  out = (ACCQ - v) * P^-1 (+ sigma_g(addend)) (+ acc),
-//                     canonical u64
+//   K5 ks_rows_ipq    Q limbs: acc = sum_j x_j * key_j as in K3 (d itself for the digit's own limbs);
+//                     T4 --NTT rows--> v;  out = (acc - v) * P^-1 (+ sigma_g(addend)) (+ acc_in),
+//                     canonical u64.  The Q-limb inner product never goes to HBM.
 //
 // A rotation passes its Galois element g: the NTT-domain automorphism sigma_g is a permutation of
 // each limb, so K1 (and K3 for a digit's own limbs) read d = c1 and K5 reads the addend c0 through
@@ -90,7 +92,9 @@ __device__ __forceinline__ void col_b_to_a(double (&x)[16], double* R, int j) {
   wave_sync();
 }
 
-// forward stages 0..3 on layout A
+// forward stages 0..3 on layout A.  Inputs already within p/2 + 1 (REDUCED) skip the reduction
+// of stage 0; the bounds after stage 1 are then those of the reducing schedule (<= 2.15 p).
+template <bool REDUCED = false>
 __device__ __forceinline__ void col_fwd_lo(double (&x)[16], const double* __restrict__ tw, double p, double pinv) {
 #pragma unroll
   for (int l = 0; l < 4; ++l) {
@@ -99,7 +103,7 @@ __device__ __forceinline__ void col_fwd_lo(double (&x)[16], const double* __rest
     for (int k = 0; k < 16; ++k) {
       if (k & h) continue;
       const double w = tw[(1 << l) + (k >> (4 - l))];
-      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      if ((l & 1) || (REDUCED && l == 0)) ct_bf<false>(x[k], x[k + h], w, p, pinv);
       else ct_bf<true>(x[k], x[k + h], w, p, pinv);
     }
   }
@@ -267,16 +271,23 @@ __device__ __forceinline__ long long nat_a(int g) {
   return (long long)(g + 16 * mn.rb) * 256 + mn.j;
 }
 
-// Workspace element of row g + 16 rb (map T, layout A: columns j + 16 k) at column-major position
-// 16 g + rb.
+// Workspace element of row g + 16 rb (map T, layout A: columns j + 16 k): wpos = 4096 g + 16 (j + 16 k) + rb.
 __device__ __forceinline__ long long ws_a(int g, int k) {
   const RowMap mt = map_t();
-  return (long long)(mt.j + 16 * k) * 256 + 16 * g + mt.rb;
+  return 4096LL * g + 16 * (mt.j + 16 * k) + mt.rb;
 }
 
+// Loads of one workspace tile go through a buffer descriptor: the 16 loads of a thread are 2 KiB
+// apart, and as buffer loads they share one VGPR offset (the per-load part is a scalar) instead of
+// 16 live 64-bit addresses.
+constexpr int kBufWord3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
+
 __device__ __forceinline__ void load_t(double (&x)[16], const double* __restrict__ src_t, int g) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)src_t, 0, kN * 8, kBufWord3);
+  const int off = (int)ws_a(g, 0) * 8;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) x[k] = src_t[ws_a(g, k)];
+  for (int k = 0; k < 16; ++k)
+    x[k] = __builtin_bit_cast(double, __builtin_amdgcn_raw_buffer_load_b64(r, off, k * 16 * 16 * 8, 0));
 }
 
 // NTT rows pass of row group g, x loaded by load_t (map T, layout A); returns layout A under map N
@@ -304,7 +315,7 @@ __device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restric
 
 // ----------------------------------------------------------------- K1: INTT rows of d
 // Limb i (< gridDim.z) of poly b reads input limb limb0 + i under prime prime0 + i and writes
-// output limb i of a gridDim.z-limb transposed poly.
+// output limb i of a gridDim.z-limb workspace poly.
 __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
                                                      uint32_t g, int limb0, int prime0, double* __restrict__ t1,
                                                      DevTables T) {
@@ -362,25 +373,26 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
     for (int k = 0; k < 16; ++k) x[k] = 0.0;
     if (act) {
       const double* col = src + z * src_zs + y * src_ys + (long long)(y * src_off_y + s) * kN +
-                          (long long)(c0 + cl) * 256;
+                          (long long)(c0 + cl) * 16;
 #pragma unroll
-      for (int k = 0; k < 16; ++k) x[k] = col[16 * k + j];
+      for (int k = 0; k < 16; ++k) x[k] = col[4096 * k + j];  // rows 16 j + k: wpos = 4096 k + 16 c + j
       col_inv_hi(x, j, tw, p, pinv);
     }
     col_b_to_a(x, R, j);
     if (act) {
       col_inv_lo(x, tw, C.inv_n0[s], C.inv_n1[s], p, pinv);
+      // centered lift (zero-mean): |x| <= 1.5 p, so fl(x pinv) is within 3 2^-53 of x / p while
+      // x / p is at least 1 / (2p) > 4 2^-53 away from a half-integer (p odd, p < 2^50): the
+      // rounding picks the nearest multiple of p and the result is the unique representative in
+      // [-(p-1)/2, (p-1)/2]
 #pragma unroll
-      for (int k = 0; k < 16; ++k) {
-        const double v = canon(x[k], p, pinv);
-        R[j + 16 * k] = v > 0.5 * p ? v - p : v;  // centered lift: zero-mean
-      }
+      for (int k = 0; k < 16; ++k) R[j + 16 * k] = reduce(x[k], p, pinv);
     }
   }
   __syncthreads();
   // phase 2
   const int rounds = (nt + 7) / 8;
-  double* dbase = dst + z * dst_zs + y * dst_ys + (long long)(c0 + cl) * 256;
+  double* dbase = dst + z * dst_zs + y * dst_ys + (long long)(c0 + cl) * 16;
   double* RX = SEPX ? X + sigma * kYStride : R;
   for (int r0 = 0; r0 < rounds; r0 += kRoundsFused) {
     double x[kRoundsFused][16];
@@ -417,28 +429,124 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
         if (act) {
 #pragma unroll
           for (int k = 0; k < 16; ++k) x[u][k] = reduce(x[u][k], p[u], pinv[u]);
-          col_fwd_lo(x[u], tw, p[u], pinv[u]);
+          col_fwd_lo<true>(x[u], tw, p[u], pinv[u]);
         }
         col_a_to_b(x[u], RX, j);
         if (act) {
           col_fwd_hi(x[u], j, tw, p[u], pinv[u]);
           double* col = dbase + (long long)C.dst_slot[tg[u]] * kN;
 #pragma unroll
-          for (int k = 0; k < 16; ++k) col[16 * k + j] = x[u][k];
+          for (int k = 0; k < 16; ++k) col[4096 * k + j] = x[u][k];
         }
       }
     }
   }
 }
 
+// ----------------------------------------------------------------- forward row twiddles in LDS
+// The tile kernels keep the forward twiddles of their 16 rows in LDS, so that no global load sits
+// between a tile's data loads and its transform (loads retire in order: a twiddle load issued
+// behind a key load would wait for it).  Row rb (row b = g + 16 rb) owns a 256-entry run at
+// TW + rb * kTwRow; stage l (8..15) uses entries [2^(l-8), 2^(l-7)) of the run:
+//   stages 8..11 (map T, index uniform per row): entry 2^(l-8) + t holds tw[2^l + (b << (l-8)) + t];
+//   stages 12..15 (map N, lane j): entry 2^(l-8) + 16 k' + j holds tw[2^l + (b << (l-8)) + (j << (l-12)) + k'],
+// so the 16 lanes of a row read 16 consecutive entries.  The odd run stride spreads the 16 rows of
+// map T over distinct banks.
+constexpr int kTwRow = 257;
+constexpr int kTwLds = 16 * kTwRow;
+
+__device__ __forceinline__ int tw_heap_src(int b, int m) {
+  // m in [1, 256): stage l = 8 + floor(log2 m), t = m - 2^(l-8); returns the table index for entry m
+  const int lv = 31 - __clz(m);  // l - 8
+  int t = m - (1 << lv);
+  if (lv >= 4) {                 // stored transposed: t = 16 k' + j  <->  (j << (lv-4)) + k'
+    const int j = t & 15, kk = t >> 4;
+    t = (j << (lv - 4)) + kk;
+  }
+  return (1 << (lv + 8)) + (b << lv) + t;
+}
+
+// Loads the forward twiddles of row group rg (prime table tw) into TW: issue (registers), then store.
+struct TwStage {
+  double v[16];
+};
+__device__ __forceinline__ void tw_issue(TwStage& st, const double* __restrict__ tw, int rg) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int idx = threadIdx.x + kT * i, rb = idx >> 8, m = idx & 255;
+    st.v[i] = m ? tw[tw_heap_src(rg + 16 * rb, m)] : 0.0;
+  }
+}
+__device__ __forceinline__ void tw_store(const TwStage& st, double* TW) {
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int idx = threadIdx.x + kT * i;
+    TW[(idx >> 8) * kTwRow + (idx & 255)] = st.v[i];
+  }
+}
+
+// forward stages 8..11 on layout A (map T) with the row's twiddle run R
+__device__ __forceinline__ void row_fwd_lo_lds(double (&x)[16], const double* R, double p, double pinv) {
+#pragma unroll
+  for (int l = 8; l < 12; ++l) {
+    const int h = 2048 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const double w = R[(1 << (l - 8)) + (k >> (12 - l))];
+      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      else ct_bf<true>(x[k], x[k + h], w, p, pinv);
+    }
+  }
+}
+
+// forward stages 12..15 on layout B (map N, lane j) with the row's twiddle run R
+__device__ __forceinline__ void row_fwd_hi_lds(double (&x)[16], const double* R, int j, double p, double pinv) {
+#pragma unroll
+  for (int l = 12; l < 16; ++l) {
+    const int h = 32768 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const double w = R[(1 << (l - 8)) + 16 * (k >> (16 - l)) + j];
+      if (l & 1) ct_bf<false>(x[k], x[k + h], w, p, pinv);
+      else ct_bf<true>(x[k], x[k + h], w, p, pinv);
+    }
+  }
+}
+
+// NTT rows pass of x (map T, layout A, as load_t returns it).  The result stays in S: thread (map N)
+// finds its natural words nat_a(g) + 16 k at S[s_out(k)].  S may be read until the next rows_fwd_lds,
+// which starts with a barrier.
+__device__ __forceinline__ int s_out(int k) {
+  const RowMap mn = map_n();
+  return ridx(mn.rb, mn.j + 16 * k);
+}
+__device__ __forceinline__ void rows_fwd_lds(double (&x)[16], double* S, const double* TW, double p, double pinv) {
+  const RowMap mt = map_t(), mn = map_n();
+  row_fwd_lo_lds(x, TW + mt.rb * kTwRow, p, pinv);
+  __syncthreads();  // earlier readers of S are done
+  row_xchg<true, false>(x, S, mt, mn);
+  row_fwd_hi_lds(x, TW + mn.rb * kTwRow, mn.j, p, pinv);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) S[ridx(mn.rb, 16 * mn.j + k)] = x[k];
+  __syncthreads();
+}
+
 // ----------------------------------------------------------------- inner product of one tile
 // sb / sa = sum_j x_j * key_j[comp] over the digits j of ciphertext b, extended limb e (prime pi),
 // row group rg: x_j is the NTT rows pass of the ModUp output T2 (or, for the digit that contains
-// limb e, d itself read through sigma_g).  Returns |sb|, |sa| <= p/2 + 1.
-__device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], const uint64_t* __restrict__ d,
-                                        long long d_stride, uint32_t g, const double* __restrict__ t2,
-                                        const uint64_t* __restrict__ key, int b, int e, int pi, int rg, int ell,
-                                        int beta, double* S, const double* __restrict__ twf, double p, double pinv,
+// limb e, d itself read through sigma_g).  Loads are software-pipelined: a digit's tile load is
+// issued as soon as the previous transform has left its result in S, its key loads right after the
+// previous inner product, so each transform runs while the next tile and the current keys are in
+// flight.  The digit containing e goes first; after the last digit, `after` (a workspace limb, or
+// null) is loaded into x for the caller.  TW must hold the forward twiddles (visible).  Returns
+// |sb|, |sa| <= p/2 + 1.
+__device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], double (&x)[16],
+                                        const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
+                                        const double* __restrict__ t2, const uint64_t* __restrict__ key, int b,
+                                        int e, int pi, int rg, int ell, int beta, double* S, const double* TW,
+                                        const double* __restrict__ after, double p, double pinv,
                                         const DevTables& T) {
   const int L = T.L, K = T.K, alpha = T.alpha;
   const int ext_l = ell + K;
@@ -446,26 +554,44 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], cons
   const long long comp_stride = (long long)beta_max * (L + K) * kN;
   const int own = e < ell ? e / alpha : -1;
   const long long na = nat_a(rg);
-  double x[16];
-  uint64_t kb[16], ka[16];
-#pragma unroll
-  for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
-  for (int jd = 0; jd < beta; ++jd) {
-    // the digit's loads go first and the key's after them, so the NTT below waits only for the
-    // digit while the key lands
-    const bool mine = jd == own;
-    if (mine) load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
-    else load_t(x, t2 + (((long long)b * beta + jd) * ext_l + e) * kN, rg);
+  const double* t2b = t2 + ((long long)b * beta * ext_l + e) * kN;  // digit j at t2b + j * ext_l * kN
+  auto load_keys = [&](uint64_t (&kb)[16], uint64_t (&ka)[16], int jd) {
     const uint64_t* kp = key + ((long long)jd * (L + K) + pi) * kN + na;
 #pragma unroll
     for (int k = 0; k < 16; ++k) { kb[k] = kp[16 * k]; ka[k] = kp[comp_stride + 16 * k]; }
-    if (!mine) rows_fwd_t(x, rg, S, twf, p, pinv);
+  };
+  // the T2 digits: every digit but the own one, ascending
+  const int nt2 = beta - (own >= 0 ? 1 : 0);
+  auto t2digit = [&](int n) { return (own >= 0 && n >= own) ? n + 1 : n; };
+  uint64_t kb[16], ka[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
+  if (own >= 0) {
+    load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
+    load_keys(kb, ka, own);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);  // |x| <= 3.9p: |term| <= 2p
+      sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);  // |x| < p: |term| <= 0.9p
       sa[k] += mulv(x[k], u2d(ka[k]), p, pinv);
     }
-    if ((jd & 3) == 3) {
+  }
+  {
+    const double* first = nt2 > 0 ? t2b + (long long)t2digit(0) * ext_l * kN : after;
+    if (first) load_t(x, first, rg);
+    if (nt2 > 0) load_keys(kb, ka, t2digit(0));
+  }
+  for (int n = 0; n < nt2; ++n) {
+    rows_fwd_lds(x, S, TW, p, pinv);
+    const double* next = n + 1 < nt2 ? t2b + (long long)t2digit(n + 1) * ext_l * kN : after;
+    if (next) load_t(x, next, rg);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const double v = S[s_out(k)];
+      sb[k] += mulv(v, u2d(kb[k]), p, pinv);  // |v| <= 3.9p: |term| <= 2p
+      sa[k] += mulv(v, u2d(ka[k]), p, pinv);
+    }
+    if (n + 1 < nt2) load_keys(kb, ka, t2digit(n + 1));
+    if (n % 3 == 2) {  // <= p/2 + 3 * 2p (+ 0.9p for the own digit) < 8p <= 2^53 between reductions
 #pragma unroll
       for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
     }
@@ -501,15 +627,21 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict
                                                    const uint64_t* acc_b, const uint64_t* acc_a,
                                                    long long acc_stride, DevTables T) {
   __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
   const TileId id = decode_tile(batch);
   if (id.tile >= tiles) return;
   const int b = id.b, e = e0 + (id.tile >> 4), rg = id.tile & 15;
   const int L = T.L, K = T.K;
   const int pi = e < ell ? e : L + (e - ell);
   const double p = T.p[pi], pinv = T.pinv[pi];
-  const double* __restrict__ twf = T.tw_fwd + (size_t)pi * kN;
-  double sb[16], sa[16];
-  tile_ip(sb, sa, d, d_stride, g, t2, keys.k[b], b, e, pi, rg, ell, beta, S, twf, p, pinv, T);
+  {
+    TwStage st;
+    tw_issue(st, T.tw_fwd + (size_t)pi * kN, rg);
+    tw_store(st, TW);
+    __syncthreads();
+  }
+  double sb[16], sa[16], x[16];
+  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T);
   const long long na = nat_a(rg);
   if (ext_b) {
     if (e < ell && add) {
@@ -538,31 +670,32 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict
   // P limb: INTT rows of both components, stored to the workspace for the ModDown cols kernel
   const double* __restrict__ twi = T.tw_inv + (size_t)pi * kN;
   double* o = accp + ((long long)b * 2 * K + (e - ell)) * kN;
+  __syncthreads();  // the inner product's reads of S are done before the exchanges rewrite it
   rows_inv_to_t(sb, o, rg, S, twi, p, pinv);
   rows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, p, pinv);
 }
 
-// One component of the ModDown finish: ip <- (ip - NTT rows(v_t)) * P^-1, then the addends (read after
-// the transform, so only ip, its sibling and the transform are live at once), canonical store.
-__device__ __forceinline__ void ipq_finish(double (&ip)[16], const double* __restrict__ v_t,
+// One component of the ModDown finish, its T4 tile loaded in x (map T): ip <- (ip - NTT rows(v)) * P^-1,
+// plus the addends, canonical store.  `next` (or nothing) is loaded into x once the transform is done.
+__device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], const double* __restrict__ next,
                                            const uint64_t* __restrict__ add_limb, uint32_t g,
                                            const uint64_t* __restrict__ acc_limb, uint64_t* __restrict__ o,
-                                           long long na, int rg, double* S, const double* __restrict__ twf,
-                                           TwPair pinv_P, double p, double pinv) {
-  double x[16];
-  load_t(x, v_t, rg);
-  rows_fwd_t(x, rg, S, twf, p, pinv);
+                                           long long na, int rg, double* S, const double* TW, TwPair pinv_P,
+                                           double p, double pinv) {
+  rows_fwd_lds(x, S, TW, p, pinv);
+  if (next) load_t(x, next, rg);
+  double ad[16];
+  if (add_limb) load_gal(ad, add_limb, na, g);
 #pragma unroll
-  for (int k = 0; k < 16; ++k) ip[k] = mulc(ip[k] - x[k], pinv_P, p);  // |ip - v| <= 4.5 p: |r| <= 2.2 p
+  for (int k = 0; k < 16; ++k) ip[k] = mulc(ip[k] - S[s_out(k)], pinv_P, p);  // |ip - v| <= 4.5 p: |r| <= 2.2 p
   if (add_limb) {
-    load_gal(x, add_limb, na, g);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) ip[k] += x[k];
+    for (int k = 0; k < 16; ++k) ip[k] += ad[k];
   }
   if (acc_limb) {
-    load_gal(x, acc_limb, na, 1u);
+    load_gal(ad, acc_limb, na, 1u);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) ip[k] += x[k];  // |r| <= 4.2 p
+    for (int k = 0; k < 16; ++k) ip[k] += ad[k];  // |r| <= 4.2 p
   }
 #pragma unroll
   for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
@@ -583,21 +716,28 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restric
                                                     long long out_stride, const LevelConsts* __restrict__ lc,
                                                     DevTables T) {
   __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
   const TileId id = decode_tile(batch);
   if (id.tile >= 16 * ell) return;
   const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
   const double p = T.p[i], pinv = T.pinv[i];
-  const double* __restrict__ twf = T.tw_fwd + (size_t)i * kN;
-  double sb[16], sa[16];
-  tile_ip(sb, sa, d, d_stride, g, t2, keys.k[b], b, i, i, rg, ell, beta, S, twf, p, pinv, T);
+  {
+    TwStage st;
+    tw_issue(st, T.tw_fwd + (size_t)i * kN, rg);
+    tw_store(st, TW);
+    __syncthreads();
+  }
+  const double* v_b = t4 + ((long long)b * 2 * ell + i) * kN;
+  const double* v_a = v_b + (long long)ell * kN;
+  double sb[16], sa[16], x[16];
+  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T);
   const long long na = nat_a(rg);
   const TwPair pinv_P = lc->p_inv[i];
-  ipq_finish(sb, t4 + ((long long)b * 2 * ell + i) * kN, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr,
-             g, acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
-             out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, twf, pinv_P, p, pinv);
-  ipq_finish(sa, t4 + ((long long)b * 2 * ell + ell + i) * kN, nullptr, 1u,
-             acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
-             out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, twf, pinv_P, p, pinv);
+  ipq_finish(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
+             acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
+             out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
+  ipq_finish(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
+             out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
 }
 
 // ----------------------------------------------------------------- ModDown finish of ext-basis input
