@@ -314,19 +314,24 @@ __device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restric
 }
 
 // ----------------------------------------------------------------- K1: INTT rows of d
-// Limb i (< gridDim.z) of poly b reads input limb limb0 + i under prime prime0 + i and writes
-// output limb i of a gridDim.z-limb workspace poly.
+// Limb i (< limbs) of poly b reads input limb limb0 + i under prime prime0 + i and writes output
+// limb i of a `limbs`-limb workspace poly.  1-D grid over (poly, limb, row group) tiles, decoded so
+// that the polys of one tile run on one XCD back to back (the XCDs take workgroups round-robin):
+// each row group's twiddles are then fetched into one XCD's L2, not into all eight.
 __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
                                                      uint32_t g, int limb0, int prime0, double* __restrict__ t1,
-                                                     DevTables T) {
+                                                     int limbs, int batch, DevTables T) {
   __shared__ double S[kRowLds];
-  const int i = blockIdx.z, b = blockIdx.x, rg = blockIdx.y;
+  const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
+  const int tile = (q / batch) * kXcds + xcd, b = q % batch;
+  if (tile >= 16 * limbs) return;
+  const int i = tile >> 4, rg = tile & 15;
   const int pi = prime0 + i;
   const double p = T.p[pi], pinv = T.pinv[pi];
   const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   double x[16];
   load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), g);
-  rows_inv_to_t(x, t1 + ((long long)b * gridDim.z + i) * kN, rg, S, tw, p, pinv);
+  rows_inv_to_t(x, t1 + ((long long)b * limbs + i) * kN, rg, S, tw, p, pinv);
 }
 
 // ----------------------------------------------------------------- K2 / K4: cols + conversion
@@ -536,12 +541,11 @@ __device__ __forceinline__ void rows_fwd_lds(double (&x)[16], double* S, const d
 // ----------------------------------------------------------------- inner product of one tile
 // sb / sa = sum_j x_j * key_j[comp] over the digits j of ciphertext b, extended limb e (prime pi),
 // row group rg: x_j is the NTT rows pass of the ModUp output T2 (or, for the digit that contains
-// limb e, d itself read through sigma_g).  Loads are software-pipelined: a digit's tile load is
-// issued as soon as the previous transform has left its result in S, its key loads right after the
-// previous inner product, so each transform runs while the next tile and the current keys are in
-// flight.  The digit containing e goes first; after the last digit, `after` (a workspace limb, or
-// null) is loaded into x for the caller.  TW must hold the forward twiddles (visible).  Returns
-// |sb|, |sa| <= p/2 + 1.
+// limb e, d itself read through sigma_g).  The digit containing e goes first; each later digit's
+// tile load is issued as soon as the previous transform has left its result in S, behind that
+// digit's key loads, so the tile lands while the inner product runs.  After the last digit, `after`
+// (a workspace limb, or null) is loaded into x for the caller.  TW must hold the forward twiddles
+// (visible).  Returns |sb|, |sa| <= p/2 + 1.
 __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], double (&x)[16],
                                         const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
                                         const double* __restrict__ t2, const uint64_t* __restrict__ key, int b,
@@ -578,10 +582,13 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
   {
     const double* first = nt2 > 0 ? t2b + (long long)t2digit(0) * ext_l * kN : after;
     if (first) load_t(x, first, rg);
-    if (nt2 > 0) load_keys(kb, ka, t2digit(0));
   }
   for (int n = 0; n < nt2; ++n) {
     rows_fwd_lds(x, S, TW, p, pinv);
+    // the keys, then the next tile: the inner product waits for the keys only, the tile lands
+    // behind it.  (Keys issued before the transform would overlap it too, but with the tile, both
+    // accumulators and the transform live they do not fit in 256 VGPRs.)
+    load_keys(kb, ka, t2digit(n));
     const double* next = n + 1 < nt2 ? t2b + (long long)t2digit(n + 1) * ext_l * kN : after;
     if (next) load_t(x, next, rg);
 #pragma unroll
@@ -590,7 +597,6 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
       sb[k] += mulv(v, u2d(kb[k]), p, pinv);  // |v| <= 3.9p: |term| <= 2p
       sa[k] += mulv(v, u2d(ka[k]), p, pinv);
     }
-    if (n + 1 < nt2) load_keys(kb, ka, t2digit(n + 1));
     if (n % 3 == 2) {  // <= p/2 + 3 * 2p (+ 0.9p for the own digit) < 8p <= 2^53 between reductions
 #pragma unroll
       for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
@@ -783,8 +789,8 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   double* t2 = r1 + (long long)batch * 2 * ell * n;
   double* accp = t2 + (long long)batch * beta * ext_l * n;
   // K1
-  // row kernels: ciphertext index fastest, so the blocks in flight share one prime's twiddles
-  k_ks_intt_rows<<<dim3(batch, 16, ell), kT, 0, s>>>(d, d_stride, galois, 0, 0, r1, c->dev);
+  k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, 0, 0,
+                                                                                    r1, ell, batch, c->dev);
   HCK_CHECK_LAUNCH();
   // K2: ModUp, one block per (column pair, digit, ciphertext).  Targets of digit j: ext_l minus the
   // digit's own limbs; the last digit is the smallest.
@@ -843,7 +849,8 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   const long long n = kN;
   double* tp = (double*)ws;                       // [polys][K] workspace layout
   double* t4 = tp + (long long)polys * K * n;     // [polys][ell] workspace layout
-  k_ks_intt_rows<<<dim3(polys, 16, K), kT, 0, s>>>(in, in_stride, 1u, ell, c->L, tp, c->dev);
+  k_ks_intt_rows<<<dim3(((16 * K + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, 1u, ell, c->L,
+                                                                                   tp, K, polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
   md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
