@@ -34,8 +34,8 @@ import numpy as np
 BYTES_PER_CT = (12 + 96 + 24) * 2**20  # 138,412,032
 # HBM bytes one C2 step actually moves (all five kernels), from two rocprofv3 --pmc runs of this
 # workload: FETCH_SIZE (x 2.0, the factor the stream workload's known 192 MiB read calibrates) +
-# WRITE_SIZE (x 1.0): 3817 MiB + 2048 MiB.
-C2_TRAFFIC_BYTES = 5865 * 2**20
+# WRITE_SIZE (x 1.0): 2 x 1,662,281 KiB + 1,703,936 KiB (= 3246.6 MiB read + 1664.0 MiB written).
+C2_TRAFFIC_BYTES = 5_149_181_760
 CTS = 16
 LIMBS = 24
 HBM_PEAK_GBS = 8000.0
