@@ -18,6 +18,7 @@ HCK_OP_NEG = 3
 HCK_OP_MUL_SCALAR = 4
 HCK_OP_MUL_XHALF = 5
 HCK_OP_MAC = 6
+HCK_OP_ADD_SCALAR = 7
 
 # Every symbol include/holmes_ckks.h declares, with (restype, argtypes).
 _vp = ctypes.c_void_p
@@ -55,6 +56,12 @@ SIGNATURES = {
     "hck_pack_diagonals": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),
     "hck_encode_workspace_bytes": (_sz, [_vp, _i]),
     "hck_encode": (_i, [_vp, _vp, _vp, _i, ctypes.c_double, _i, _ip, _vp, _i64, _vp, _sz, _vp, _vp]),
+    "hck_tensor": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp]),
+    "hck_relinearize_workspace_bytes": (_sz, [_vp, _i, _i]),
+    "hck_relinearize": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "hck_mul_relin_workspace_bytes": (_sz, [_vp, _i, _i]),
+    "hck_mul_relin": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "hck_weighted_sum": (_i, [_vp, _i, _i, _i, _vp, _i64, _vp, _vp, _i64, _vp]),
 }
 
 _lib = None

@@ -94,6 +94,35 @@ class Client:
         e = sample_gaussian(rng, (ctx.beta_max, ctx.N), spec.error_sigma)
         return automorph_coeff_signed(self.secret, galois), self.secret.copy(), a, e
 
+    def secret_square(self) -> np.ndarray:
+        """Coefficients of s^2 in Z[X]/(X^N + 1), int64: the NTT-domain square over q_0, inverse
+        transformed and centered (exact, since every coefficient of s^2 is at most the number of
+        nonzero coefficients of s, far below q_0 / 2)."""
+
+        ctx = self.context
+        s0 = self._s_ntt[:, :1].contiguous()
+        sq = ctx.empty(1, 1, ctx.N)
+        ctx.poly_op(nat.HCK_OP_MUL, sq, s0, s0, prime_idx=[0])
+        ctx.ntt(sq, prime_idx=[0], inverse=True)
+        r = sq[0, 0].cpu().numpy().astype(np.int64)
+        q0 = int(ctx.primes[0])
+        return np.where(r > q0 // 2, r - q0, r).astype(np.int64)
+
+    def relin_key_inputs(self):
+        """(s_from = s^2, s_to = s, a, e) of the relinearisation key (for checkers)."""
+
+        ctx = self.context
+        spec = ctx.spec
+        rng = _rng(spec.seed, "relin-key")
+        a = sample_uniform(rng, ctx.primes, (ctx.beta_max,), ctx.N)
+        e = sample_gaussian(rng, (ctx.beta_max, ctx.N), spec.error_sigma)
+        return self.secret_square(), self.secret.copy(), a, e
+
+    def relin_key(self) -> torch.Tensor:
+        """The s^2 -> s key-switching key that relinearises a ciphertext product."""
+
+        return self.context.make_switching_key(*self.relin_key_inputs())
+
     def generate_rotation_keys(self, rotations) -> None:
         ctx = self.context
         for r in rotations:

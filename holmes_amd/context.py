@@ -358,6 +358,77 @@ class CKKSContext:
                   "hck_rotate_ext")
         return out0, out1
 
+    def _pair(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, what: str) -> int:
+        self._check_poly(c0, limbs, self.N)
+        self._check_poly(c1, limbs, self.N)
+        if c0.shape[0] != c1.shape[0] or _bstride(c0) != _bstride(c1):
+            raise ValueError(f"{what}: both components need one shape and batch stride")
+        return _bstride(c0)
+
+    def tensor(self, a0, a1, b0, b1, limbs: int):
+        """(a0 b0, a0 b1 + a1 b0, a1 b1) over ``limbs`` Q limbs, as [batch][limbs][N] tensors."""
+
+        sa = self._pair(a0, a1, limbs, "tensor lhs")
+        sb = self._pair(b0, b1, limbs, "tensor rhs")
+        B = a0.shape[0]
+        if b0.shape[0] != B:
+            raise ValueError("tensor operands need the same batch")
+        d = self.empty(3, B, limbs, self.N)
+        nat.check(nat.lib().hck_tensor(self._h, limbs, B, a0.data_ptr(), a1.data_ptr(), sa, b0.data_ptr(),
+                                       b1.data_ptr(), sb, d[0].data_ptr(), d[1].data_ptr(), d[2].data_ptr(),
+                                       limbs * self.N, _stream_ptr(self.device)), "hck_tensor")
+        return d[0], d[1], d[2]
+
+    def relinearize_raw(self, d0, d1, d2, limbs: int, key: torch.Tensor):
+        """(d0, d1) + KeySwitch(d2) with the s^2 -> s key."""
+
+        self._check_key(key)
+        s01 = self._pair(d0, d1, limbs, "relinearize")
+        self._check_poly(d2, limbs, self.N)
+        if d2.shape[0] != d0.shape[0] or _bstride(d2) != s01:
+            raise ValueError("relinearize: d2 needs the shape and batch stride of d0 / d1")
+        B = d0.shape[0]
+        out = self.empty(2, B, limbs, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_relinearize_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_relinearize(self._h, limbs, B, d0.data_ptr(), d1.data_ptr(), d2.data_ptr(), s01,
+                                    key.data_ptr(), out[0].data_ptr(), out[1].data_ptr(), limbs * self.N,
+                                    ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_relinearize")
+        return out[0], out[1]
+
+    def mul_relin_raw(self, a0, a1, b0, b1, limbs: int, key: torch.Tensor):
+        """Tensor product followed by relinearisation: a two-component [batch][limbs][N] pair."""
+
+        self._check_key(key)
+        sa = self._pair(a0, a1, limbs, "mul lhs")
+        sb = self._pair(b0, b1, limbs, "mul rhs")
+        B = a0.shape[0]
+        if b0.shape[0] != B:
+            raise ValueError("mul operands need the same batch")
+        out = self.empty(2, B, limbs, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_mul_relin_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_mul_relin(self._h, limbs, B, a0.data_ptr(), a1.data_ptr(), sa, b0.data_ptr(), b1.data_ptr(),
+                                  sb, key.data_ptr(), out[0].data_ptr(), out[1].data_ptr(), limbs * self.N,
+                                  ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_mul_relin")
+        return out[0], out[1]
+
+    def weighted_sum(self, x: torch.Tensor, weights: torch.Tensor, limbs: int) -> torch.Tensor:
+        """out[g] = sum_j weights[g][j][l] x[j] per limb l: x [n][>= limbs][N], weights a uint64
+        tensor [groups][n][limbs] of residues (moved to the device here)."""
+
+        self._check_poly(x, limbs, self.N)
+        n = int(x.shape[0])
+        w = weights.to(self.device, torch.uint64).contiguous()
+        if w.dim() != 3 or int(w.shape[1]) != n or int(w.shape[2]) != limbs:
+            raise ValueError(f"weights must be [groups][{n}][{limbs}]")
+        G = int(w.shape[0])
+        out = self.empty(G, limbs, self.N)
+        nat.check(nat.lib().hck_weighted_sum(self._h, limbs, n, G, x.data_ptr(), _bstride(x), w.data_ptr(),
+                                             out.data_ptr(), limbs * self.N, _stream_ptr(self.device)),
+                  "hck_weighted_sum")
+        return out
+
     def moddown(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
         """Extended-basis polys [polys][limbs + K][N] -> [polys][limbs][N] (divide by P, round)."""
 

@@ -1,0 +1,155 @@
+// Ciphertext x ciphertext multiplication: tensor product, relinearisation (a key switch of the
+// degree-2 component with the s^2 -> s key, its result added to the degree-0/1 components inside
+// the key switch's last kernel), and the grouped scalar-weighted sum the polynomial evaluators use.
+// Algorithm: the CKKS multiply EasyFHE runs for fhe.homo_mul_no_relin / homo_relinearize /
+// homo_mul_relin (llama3fhe/operators/attention/prefill/qk.py:460-464,
+// llama3fhe/operators/attention/kernel_helpers.py:146-152,
+// llama3fhe/operators/nonlinear/polynomial.py:140-190) and grouped_scalar_weighted_acc
+// (polynomial.py:256-300).
+#include <hip/hip_runtime.h>
+
+#include "../../include/holmes_ckks.h"
+#include "internal.hpp"
+
+namespace hck {
+namespace {
+
+constexpr int kMaxBatchM = 64;  // items per key-switch launch sequence
+
+// d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1 (mod q_limb), canonical.  Grid (N / 256, limbs, batch).
+__global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a0, const uint64_t* __restrict__ a1,
+                                                long long a_stride, const uint64_t* __restrict__ b0,
+                                                const uint64_t* __restrict__ b1, long long b_stride,
+                                                uint64_t* __restrict__ d0, uint64_t* __restrict__ d1,
+                                                uint64_t* __restrict__ d2, long long d_stride, DevTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  const long long z = blockIdx.z;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const long long lo = (long long)i * kN + k;
+  const double x0 = u2d(a0[z * a_stride + lo]), x1 = u2d(a1[z * a_stride + lo]);
+  const double y0 = u2d(b0[z * b_stride + lo]), y1 = u2d(b1[z * b_stride + lo]);
+  // canonical operands: each product is within 0.875 p, the cross sum within 1.75 p
+  d0[z * d_stride + lo] = d2u(canon(mulv(x0, y0, p, pinv), p, pinv));
+  d1[z * d_stride + lo] = d2u(canon(mulv(x0, y1, p, pinv) + mulv(x1, y0, p, pinv), p, pinv));
+  d2[z * d_stride + lo] = d2u(canon(mulv(x1, y1, p, pinv), p, pinv));
+}
+
+// out[g][l][k] = sum_j w[g][j][l] * in[j][l][k] (mod q_l), canonical.  Grid (N / 256, limbs, groups).
+__global__ __launch_bounds__(256) void k_weighted_sum(const uint64_t* __restrict__ in, long long in_stride, int n,
+                                                      const uint64_t* __restrict__ w, uint64_t* __restrict__ out,
+                                                      long long out_stride, int limbs, DevTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  const long long g = blockIdx.z;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const uint64_t* wg = w + g * (long long)n * limbs + i;
+  const uint64_t* x = in + (long long)i * kN + k;
+  double acc = 0.0;
+  for (int j = 0; j < n; ++j) {
+    acc += mulv(u2d(x[(long long)j * in_stride]), u2d(wg[(long long)j * limbs]), p, pinv);  // |term| <= 0.875 p
+    if ((j & 7) == 7) acc = reduce(acc, p, pinv);  // <= p/2 + 8 * 0.875 p < 8 p between reductions
+  }
+  out[g * out_stride + (long long)i * kN + k] = d2u(canon(acc, p, pinv));
+}
+
+int launch_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
+                  const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1,
+                  uint64_t* d2, long long d_stride, hipStream_t s) {
+  k_tensor<<<dim3(kN / 256, ell, batch), 256, 0, s>>>(a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride,
+                                                      c->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+bool valid_level(const hck_context* c, int ell) { return c && ell >= 1 && ell <= c->L; }
+
+}  // namespace
+}  // namespace hck
+
+extern "C" int hck_tensor(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0, const uint64_t* a1,
+                          int64_t a_stride, const uint64_t* b0, const uint64_t* b1, int64_t b_stride, uint64_t* d0,
+                          uint64_t* d1, uint64_t* d2, int64_t d_stride, void* stream) {
+  if (!hck::valid_level(ctx, level_limbs) || batch < 0 || batch > 65535) return HCK_ERR_ARG;
+  if (!a0 || !a1 || !b0 || !b1 || !d0 || !d1 || !d2) return HCK_ERR_ARG;
+  if (batch == 0) return HCK_OK;
+  return hck::launch_tensor(ctx, level_limbs, batch, a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride,
+                            (hipStream_t)stream);
+}
+
+extern "C" size_t hck_relinearize_workspace_bytes(const hck_context* ctx, int level_limbs, int batch) {
+  return hck_keyswitch_workspace_bytes(ctx, level_limbs, batch);
+}
+
+extern "C" int hck_relinearize(const hck_context* ctx, int level_limbs, int batch, const uint64_t* d0,
+                               const uint64_t* d1, const uint64_t* d2, int64_t in_stride, const uint64_t* relin_ksk,
+                               uint64_t* out0, uint64_t* out1, int64_t out_stride, void* workspace,
+                               size_t workspace_bytes, void* stream) {
+  if (!hck::valid_level(ctx, level_limbs) || batch < 0) return HCK_ERR_ARG;
+  if (!d0 || !d1 || !d2 || !relin_ksk || !out0 || !out1) return HCK_ERR_ARG;
+  // d2 is read by two kernels while the outputs are written; d0 / d1 are read where they are written
+  if (out0 == d2 || out1 == d2 || out0 == out1) return HCK_ERR_ARG;
+  if (batch == 0) return HCK_OK;
+  const int chunk = batch < hck::kMaxBatchM ? batch : hck::kMaxBatchM;
+  if (!workspace || workspace_bytes < hck::ks_fused_bytes(ctx, level_limbs, chunk)) return HCK_ERR_WORKSPACE;
+  const uint64_t* keys[hck::kMaxBatchM];
+  for (int b = 0; b < chunk; ++b) keys[b] = relin_ksk;
+  for (int i0 = 0; i0 < batch; i0 += chunk) {
+    const int nb = batch - i0 < chunk ? batch - i0 : chunk;
+    const long long ii = (long long)i0 * in_stride, oi = (long long)i0 * out_stride;
+    int rc = hck::ks_fused(ctx, level_limbs, nb, d2 + ii, in_stride, 1u, keys, nullptr, 0, d0 + ii, d1 + ii,
+                           in_stride, out0 + oi, out1 + oi, out_stride, (char*)workspace, (hipStream_t)stream);
+    if (rc) return rc;
+  }
+  return HCK_OK;
+}
+
+extern "C" size_t hck_mul_relin_workspace_bytes(const hck_context* ctx, int level_limbs, int batch) {
+  if (!hck::valid_level(ctx, level_limbs) || batch < 0) return 0;
+  const int chunk = batch < hck::kMaxBatchM ? batch : hck::kMaxBatchM;
+  return hck::ks_fused_bytes(ctx, level_limbs, chunk) + (size_t)3 * chunk * level_limbs * hck::kN * 8;
+}
+
+extern "C" int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                             const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
+                             int64_t b_stride, const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1,
+                             int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!hck::valid_level(ctx, level_limbs) || batch < 0) return HCK_ERR_ARG;
+  if (!a0 || !a1 || !b0 || !b1 || !relin_ksk || !out0 || !out1 || out0 == out1) return HCK_ERR_ARG;
+  if (batch == 0) return HCK_OK;
+  if (!workspace || workspace_bytes < hck_mul_relin_workspace_bytes(ctx, level_limbs, batch)) return HCK_ERR_WORKSPACE;
+  const int chunk = batch < hck::kMaxBatchM ? batch : hck::kMaxBatchM;
+  const long long poly = (long long)level_limbs * hck::kN;
+  char* ks_ws = (char*)workspace;
+  uint64_t* d = (uint64_t*)(ks_ws + hck::ks_fused_bytes(ctx, level_limbs, chunk));  // [3][chunk][limbs][N]
+  const uint64_t* keys[hck::kMaxBatchM];
+  for (int b = 0; b < chunk; ++b) keys[b] = relin_ksk;
+  hipStream_t s = (hipStream_t)stream;
+  for (int i0 = 0; i0 < batch; i0 += chunk) {
+    const int nb = batch - i0 < chunk ? batch - i0 : chunk;
+    uint64_t* d0 = d;
+    uint64_t* d1 = d + (long long)chunk * poly;
+    uint64_t* d2 = d + 2LL * chunk * poly;
+    int rc = hck::launch_tensor(ctx, level_limbs, nb, a0 + (long long)i0 * a_stride, a1 + (long long)i0 * a_stride,
+                                a_stride, b0 + (long long)i0 * b_stride, b1 + (long long)i0 * b_stride, b_stride, d0,
+                                d1, d2, poly, s);
+    if (rc) return rc;
+    const long long oi = (long long)i0 * out_stride;
+    rc = hck::ks_fused(ctx, level_limbs, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, out0 + oi, out1 + oi,
+                       out_stride, ks_ws, s);
+    if (rc) return rc;
+  }
+  return HCK_OK;
+}
+
+extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int groups, const uint64_t* in,
+                                int64_t in_stride, const uint64_t* weights, uint64_t* out, int64_t out_stride,
+                                void* stream) {
+  if (!ctx || !in || !weights || !out || limbs < 1 || limbs > ctx->L || n < 1 || groups < 0 || groups > 65535)
+    return HCK_ERR_ARG;
+  if (groups == 0) return HCK_OK;
+  hck::k_weighted_sum<<<dim3(hck::kN / 256, limbs, groups), 256, 0, (hipStream_t)stream>>>(
+      in, in_stride, n, weights, out, out_stride, limbs, ctx->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}

@@ -1,5 +1,5 @@
-// Elementwise limb kernels: automorphism (NTT-domain permutation), add/sub/mul/neg, scalar and
-// X^(N/2) multiplication, signed-integer reduction.  All are HBM-streaming kernels: one thread per
+// Elementwise limb kernels: automorphism (NTT-domain permutation), add/sub/mul/neg, scalar
+// multiplication and addition, X^(N/2) multiplication, signed-integer reduction.  All are HBM-streaming kernels: one thread per
 // coefficient, 256 threads per workgroup, grid (N / 256, limbs, polys).
 #include <hip/hip_runtime.h>
 
@@ -58,6 +58,9 @@ __global__ __launch_bounds__(256) void k_poly_op(uint64_t* out, const uint64_t* 
     r = canon(acc + mulv(x, u2d(b[z * b_stride + lo]), p, pinv), p, pinv);
   } else if constexpr (OP == HCK_OP_MUL_SCALAR) {
     r = canon(mulc(x, sm.s[limb], p), p, pinv);
+  } else if constexpr (OP == HCK_OP_ADD_SCALAR) {
+    r = x + sm.s[limb].w;  // a constant polynomial is the same value at every evaluation point
+    r = r >= p ? r - p : r;
   } else {  // HCK_OP_MUL_XHALF: X^(N/2) evaluates to zeta4 at slots k < N/2 and -zeta4 above
     const double m = mulc(x, T.zeta4[pi], p);
     r = canon(k < kN / 2 ? m : -m, p, pinv);
@@ -103,13 +106,14 @@ extern "C" int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const 
   if (limbs < 0 || limbs > hck::kMaxPrimes) return HCK_ERR_ARG;
   const bool binary = op == HCK_OP_ADD || op == HCK_OP_SUB || op == HCK_OP_MUL || op == HCK_OP_MAC;
   if (binary && !b) return HCK_ERR_ARG;
-  if (op == HCK_OP_MUL_SCALAR && !scalar) return HCK_ERR_ARG;
+  const bool with_scalar = op == HCK_OP_MUL_SCALAR || op == HCK_OP_ADD_SCALAR;
+  if (with_scalar && !scalar) return HCK_ERR_ARG;
   hck::PrimeMap pm{};
   hck::ScalarMap sm{};
   for (int i = 0; i < limbs; ++i) {
     if (prime_idx[i] < 0 || prime_idx[i] >= ctx->np) return HCK_ERR_ARG;
     pm.prime[i] = (uint8_t)prime_idx[i];
-    if (op == HCK_OP_MUL_SCALAR) {
+    if (with_scalar) {
       const uint64_t q = ctx->primes[prime_idx[i]];
       if (scalar[i] >= q) return HCK_ERR_ARG;
       sm.s[i] = hck::TwPair{(double)scalar[i], (double)scalar[i] / (double)q};
@@ -126,6 +130,7 @@ extern "C" int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const 
     case HCK_OP_MUL_SCALAR: hck::k_poly_op<HCK_OP_MUL_SCALAR><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sm, ctx->dev); break;
     case HCK_OP_MUL_XHALF: hck::k_poly_op<HCK_OP_MUL_XHALF><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sm, ctx->dev); break;
     case HCK_OP_MAC: hck::k_poly_op<HCK_OP_MAC><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sm, ctx->dev); break;
+    case HCK_OP_ADD_SCALAR: hck::k_poly_op<HCK_OP_ADD_SCALAR><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sm, ctx->dev); break;
     default: return HCK_ERR_ARG;
   }
   HCK_CHECK_LAUNCH();

@@ -44,7 +44,26 @@ __all__ = [
     "grouped_pairwise_mac",
     "prepare_hoisted_baby_rotations",
     "hoisted_mac_sum",
+    "EncodedScalar",
+    "encode_scalar",
+    "homo_mul_scalar",
+    "homo_mul_scalar_rescale",
+    "homo_add_scalar",
+    "homo_add_pt",
+    "homo_mul_no_relin",
+    "homo_relinearize",
+    "homo_mul_relin",
+    "homo_mul_relin_rescale_postop",
+    "grouped_scalar_weighted_acc",
+    "cipher_batch_item",
 ]
+
+# Fixed-scale mode (scale_mode "fixed"): a product rescaled by a prime q_l carries the exact scale
+# s_a s_b / q_l, which differs from the nominal scale by |q_l / 2^bits - 1| (below 2^-32 for the
+# chain's NTT primes when the scale matches the prime size).  Additions accept scales equal to
+# this relative tolerance and keep the left operand's scale, as the reference's Chebyshev
+# recurrence requires (T_k = 2 T_a T_b - T_1, llama3fhe/operators/nonlinear/polynomial.py:140-160).
+SCALE_RTOL = 2.0**-20
 
 
 class Plaintext:
@@ -64,11 +83,13 @@ class Plaintext:
 
 
 def generate_client_context(spec: CKKSContextSpec, device: str = "cuda"):
-    """Build the context (device tables) and the client (secret key); generate the requested
-    rotation keys when ``spec.auto_load_keys``.  Returns ``(client, context)``."""
+    """Build the context (device tables) and the client (secret key) with the relinearisation key;
+    generate the requested rotation keys when ``spec.auto_load_keys``.  Returns
+    ``(client, context)``."""
 
     ctx = CKKSContext(spec, device=device)
     client = Client(ctx)
+    ctx.relin_key = client.relin_key()
     if spec.auto_load_keys and spec.rotations:
         client.generate_rotation_keys(spec.rotations)
     return client, ctx
@@ -159,20 +180,36 @@ def align_to(ct: Cipher, state: CipherState, ctx: CKKSContext) -> Cipher:
     return ct.cipher_like([_view(c, target).clone() for c in ct.cv], state=ct.state.replace(cur_limbs=target))
 
 
+def _same_scale(fa: float, fb: float) -> bool:
+    return abs(fa - fb) <= SCALE_RTOL * max(abs(fa), abs(fb))
+
+
 def _binary(a: Cipher, b: Cipher, ctx: CKKSContext, op: int) -> Cipher:
+    """a op b componentwise; a two-component operand meets a three-component one (a product before
+    relinearisation) with a zero third component."""
+
     if a.is_ext or b.is_ext:
         raise ValueError("add/sub expect non-extended ciphertexts")
     if int(a.state.scale_degree) != int(b.state.scale_degree):
         raise ValueError("scale degrees differ")
     fa, fb = float(a.state.scaling_factor), float(b.state.scaling_factor)
-    if abs(fa - fb) > 1e-9 * max(fa, fb):
+    if not _same_scale(fa, fb):
         raise ValueError(f"scaling factors differ ({fa} vs {fb})")
+    if a.batch_size != b.batch_size:
+        raise ValueError("batch sizes differ")
     limbs = min(_limbs(a), _limbs(b))
     idx = ctx.q_prime_idx(limbs)
     out = []
-    for x, y in zip(a.cv, b.cv):
-        o = ctx.empty(x.shape[0], limbs, ctx.N)
-        ctx.poly_op(op, o, _view(x, limbs), _view(y, limbs), prime_idx=idx)
+    for c in range(max(len(a.cv), len(b.cv))):
+        o = ctx.empty(a.batch_size, limbs, ctx.N)
+        if c < len(a.cv) and c < len(b.cv):
+            ctx.poly_op(op, o, _view(a.cv[c], limbs), _view(b.cv[c], limbs), prime_idx=idx)
+        elif c < len(a.cv):
+            o.copy_(_view(a.cv[c], limbs))
+        elif op == nat.HCK_OP_SUB:
+            ctx.poly_op(nat.HCK_OP_NEG, o, _view(b.cv[c], limbs), prime_idx=idx)
+        else:
+            o.copy_(_view(b.cv[c], limbs))
         out.append(o)
     return a.cipher_like(out, state=a.state.replace(cur_limbs=limbs))
 
@@ -500,3 +537,248 @@ def hoisted_mac_sum(ct: Cipher, baby_offsets, plaintexts: Plaintext, giant_offse
     fac = float(pt_state.scaling_factor) if pt_state is not None else 1.0
     state = st.replace(scale_degree=int(st.scale_degree) + deg, scaling_factor=float(st.scaling_factor) * fac)
     return ct.cipher_like([acc0, acc1], state=state)
+
+
+# ---------------------------------------------------------------------------- scalars
+MAX_ENCODED_BITS = 61  # |value * scale| must stay below 2^61 (llama3fhe/operators/attention/prefill/softmax.py:559)
+
+
+class EncodedScalar:
+    """A constant encoded for one level: ``residues`` holds round(value * scaling_factor) (or the
+    integer itself) modulo each of the ``cur_limbs`` Q primes, last axis = limb; the leading axes
+    index groups / entries of a table (fhe.EncodedScalar, llama3fhe/operators/nonlinear/
+    polynomial.py:286-291).  A constant polynomial takes the same value at every NTT evaluation
+    point, so these residues act on every coefficient of an NTT-domain limb."""
+
+    __slots__ = ("residues", "cur_limbs", "scale_degree", "scaling_factor")
+
+    def __init__(self, residues, cur_limbs: int, scale_degree: int, scaling_factor: float):
+        self.residues = residues
+        self.cur_limbs = int(cur_limbs)
+        self.scale_degree = int(scale_degree)
+        self.scaling_factor = float(scaling_factor)
+
+
+def _scaled_int(value, scaling_factor: float, integer: bool) -> int:
+    if integer:
+        if float(value) != int(value):
+            raise ValueError(f"integer mode needs an integral value, got {value!r}")
+        m = int(value)
+    else:
+        x = float(value) * float(scaling_factor)
+        if not np.isfinite(x):
+            raise ValueError("scalar * scale is not finite")
+        m = int(np.sign(x) * np.floor(abs(x) + 0.5))  # round half away from zero, as the encoder
+    if abs(m) >= 1 << MAX_ENCODED_BITS:
+        raise ValueError(f"encoded scalar {value!r} x {scaling_factor} exceeds 2^{MAX_ENCODED_BITS}")
+    return m
+
+
+def _scalar_residues(values, cur_limbs: int, scaling_factor: float, integer: bool, ctx: CKKSContext) -> np.ndarray:
+    vals = np.atleast_1d(np.asarray(values, dtype=np.float64 if not integer else object))
+    primes = ctx.q_primes[: int(cur_limbs)]
+    out = np.empty(vals.shape + (len(primes),), dtype=np.uint64)
+    for pos in np.ndindex(vals.shape):
+        m = _scaled_int(vals[pos], scaling_factor, integer)
+        out[pos] = [m % q for q in primes]
+    return out
+
+
+def encode_scalar(value, cur_limbs: int, scale_degree: int = 1, scaling_factor: float | None = None,
+                  context: CKKSContext | None = None, mode: str = "double") -> EncodedScalar:
+    """Encode a constant for a ciphertext at ``cur_limbs`` limbs.  ``mode="double"`` (scale_degree
+    >= 1): round(value * scaling_factor), the scaling factor defaulting to the level's scale;
+    ``mode="integer"`` or scale_degree 0: the integer itself (scale 1).  Keywords as
+    llama3fhe/operators/nonlinear/polynomial.py:72-97, bootstrap.py:604-623."""
+
+    ctx = context
+    if ctx is None:
+        raise ValueError("encode_scalar needs the context")
+    integer = str(mode) == "integer" or int(scale_degree) == 0
+    sf = 1.0 if integer else (ctx.scale_at(int(cur_limbs)) if scaling_factor is None else float(scaling_factor))
+    res = _scalar_residues(value, int(cur_limbs), sf, integer, ctx)
+    if np.ndim(value) == 0:
+        res = res[0]
+    return EncodedScalar(torch.from_numpy(res), int(cur_limbs), 0 if integer else int(scale_degree), sf)
+
+
+def _scalar_list(enc: EncodedScalar, limbs: int):
+    r = enc.residues.cpu().numpy() if hasattr(enc.residues, "cpu") else np.asarray(enc.residues)
+    r = np.asarray(r, dtype=np.uint64).reshape(-1)
+    if r.size < limbs:
+        raise ValueError(f"encoded scalar has {r.size} limbs, need {limbs}")
+    return [int(v) for v in r[:limbs]]
+
+
+def homo_mul_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
+    """Multiply every slot by the encoded constant (exact residue products); scale degrees add and
+    scaling factors multiply."""
+
+    limbs = min(_limbs(ct), enc.cur_limbs)
+    idx = ctx.q_prime_idx(limbs)
+    sc = _scalar_list(enc, limbs)
+    out = []
+    for x in ct.cv:
+        o = ctx.empty(x.shape[0], limbs, ctx.N)
+        ctx.poly_op(nat.HCK_OP_MUL_SCALAR, o, _view(x, limbs), prime_idx=idx, scalar=sc)
+        out.append(o)
+    st = ct.state
+    state = st.replace(cur_limbs=limbs, scale_degree=int(st.scale_degree) + enc.scale_degree,
+                       scaling_factor=float(st.scaling_factor) * enc.scaling_factor)
+    return ct.cipher_like(out, state=state)
+
+
+def homo_mul_scalar_rescale(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
+    """homo_mul_scalar followed by rescale (softmax.py:720-729, norm/refresh.py:21-31)."""
+
+    tmp = homo_mul_scalar(ct, enc, ctx)
+    out = rescale(tmp, ctx)
+    tmp.release()
+    return out
+
+
+def homo_add_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
+    """Add the encoded constant to every slot (to c0 only); the constant must carry the
+    ciphertext's scale (softmax.py:1053-1064)."""
+
+    if not _same_scale(float(ct.state.scaling_factor), enc.scaling_factor):
+        raise ValueError(f"scalar scale {enc.scaling_factor} != ciphertext scale {ct.state.scaling_factor}")
+    limbs = min(_limbs(ct), enc.cur_limbs)
+    idx = ctx.q_prime_idx(limbs)
+    c0 = ctx.empty(ct.batch_size, limbs, ctx.N)
+    ctx.poly_op(nat.HCK_OP_ADD_SCALAR, c0, _view(ct.cv[0], limbs), prime_idx=idx, scalar=_scalar_list(enc, limbs))
+    rest = [_view(x, limbs).clone() for x in ct.cv[1:]]
+    return ct.cipher_like([c0] + rest, state=ct.state.replace(cur_limbs=limbs))
+
+
+def homo_add_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
+    """Add a plaintext (same scale) to every slot: c0 + pt (softmax.py:290-298, rmsnorm.py:793)."""
+
+    if not _same_scale(float(ct.state.scaling_factor), float(pt.state.scaling_factor)):
+        raise ValueError(f"plaintext scale {pt.state.scaling_factor} != ciphertext scale {ct.state.scaling_factor}")
+    limbs = min(_limbs(ct), int(pt.state.cur_limbs))
+    idx = ctx.q_prime_idx(limbs)
+    p = _view(pt.cv[0], limbs)
+    if p.shape[0] not in (1, ct.batch_size):
+        raise ValueError("plaintext batch must be 1 or the ciphertext batch")
+    if p.shape[0] == 1 and ct.batch_size > 1:
+        p = p.expand(ct.batch_size, -1, -1)
+    c0 = ctx.empty(ct.batch_size, limbs, ctx.N)
+    ctx.poly_op(nat.HCK_OP_ADD, c0, _view(ct.cv[0], limbs), p.contiguous(), prime_idx=idx)
+    rest = [_view(x, limbs).clone() for x in ct.cv[1:]]
+    return ct.cipher_like([c0] + rest, state=ct.state.replace(cur_limbs=limbs))
+
+
+# ---------------------------------------------------------------------------- ciphertext products
+def _product_state(a: Cipher, b: Cipher, limbs: int) -> CipherState:
+    return a.state.replace(cur_limbs=limbs,
+                           scale_degree=int(a.state.scale_degree) + int(b.state.scale_degree),
+                           scaling_factor=float(a.state.scaling_factor) * float(b.state.scaling_factor))
+
+
+def _mul_operands(a: Cipher, b: Cipher):
+    if a.is_ext or b.is_ext or len(a.cv) != 2 or len(b.cv) != 2:
+        raise ValueError("products take two-component, non-extended ciphertexts")
+    if a.batch_size != b.batch_size:
+        raise ValueError("batch sizes differ")
+    limbs = min(_limbs(a), _limbs(b))
+    return limbs, [_view(x, limbs) for x in a.cv], [_view(x, limbs) for x in b.cv]
+
+
+def homo_mul_no_relin(a: Cipher, b: Cipher, ctx: CKKSContext) -> Cipher:
+    """Tensor product: the three-component ciphertext (a0 b0, a0 b1 + a1 b0, a1 b1) decrypting
+    under (1, s, s^2) (qk.py:460-464, pv.py:544-548)."""
+
+    limbs, (a0, a1), (b0, b1) = _mul_operands(a, b)
+    d0, d1, d2 = ctx.tensor(a0, a1, b0, b1, limbs)
+    return a.cipher_like([d0, d1, d2], state=_product_state(a, b, limbs))
+
+
+def _relin_key(ctx: CKKSContext) -> torch.Tensor:
+    if ctx.relin_key is None:
+        raise RuntimeError("the context holds no relinearisation key (generate_client_context makes one)")
+    return ctx.relin_key
+
+
+def homo_relinearize(ct: Cipher, ctx: CKKSContext) -> Cipher:
+    """Three components back to two: (d0, d1) + KeySwitch_{s^2 -> s}(d2) (kernel_helpers.py:146-152)."""
+
+    if len(ct.cv) == 2:
+        return ct.cipher_like([x.clone() for x in ct.cv])
+    if len(ct.cv) != 3 or ct.is_ext:
+        raise ValueError("relinearize takes a three-component, non-extended ciphertext")
+    limbs = _limbs(ct)
+    d0, d1, d2 = (_view(x, limbs) for x in ct.cv)
+    o0, o1 = ctx.relinearize_raw(d0, d1, d2, limbs, _relin_key(ctx))
+    return ct.cipher_like([o0, o1])
+
+
+def homo_mul_relin(a: Cipher, b: Cipher, ctx: CKKSContext) -> Cipher:
+    """Product with relinearisation (tensor product and key switch, the tensor components kept in
+    the workspace)."""
+
+    limbs, (a0, a1), (b0, b1) = _mul_operands(a, b)
+    o0, o1 = ctx.mul_relin_raw(a0, a1, b0, b1, limbs, _relin_key(ctx))
+    return a.cipher_like([o0, o1], state=_product_state(a, b, limbs))
+
+
+def homo_mul_relin_rescale_postop(lhs: Cipher, rhs: Cipher, ctx: CKKSContext, apply_double: bool = False,
+                                  sub: Cipher | None = None, scalar: EncodedScalar | None = None) -> Cipher:
+    """rescale(lhs * rhs) (relinearised), then x 2 when ``apply_double``, minus ``sub`` (dropped to
+    the result's level), plus the encoded ``scalar``: the Chebyshev step T_{a+b} = 2 T_a T_b -
+    T_{|a-b|} (llama3fhe/operators/nonlinear/polynomial.py:140-190)."""
+
+    prod = homo_mul_relin(lhs, rhs, ctx)
+    out = rescale(prod, ctx)
+    prod.release()
+    if apply_double:
+        doubled = homo_add(out, out, ctx)
+        out.release()
+        out = doubled
+    if sub is not None:
+        s_al = align_to(sub, out.state, ctx) if _limbs(sub) > _limbs(out) else sub
+        sub_state = s_al.state.replace(scale_degree=out.state.scale_degree)
+        diff = homo_sub(out, s_al.cipher_like(s_al.cv, state=sub_state), ctx)
+        if s_al is not sub:
+            s_al.release()
+        out.release()
+        out = diff
+    if scalar is not None:
+        added = homo_add_scalar(out, scalar, ctx)
+        out.release()
+        out = added
+    return out
+
+
+def grouped_scalar_weighted_acc(batch: Cipher, table: EncodedScalar, ctx: CKKSContext) -> Cipher:
+    """out[g] = sum_j table[g][j] * batch[j] over the items of a cipher batch (one kernel per
+    component); ``table.residues`` is [groups][items][limbs] (or [items][limbs] for one group).
+    Scale degrees add and scaling factors multiply, as for homo_mul_scalar; the caller rescales
+    (polynomial.py:256-300)."""
+
+    if batch.is_ext:
+        raise ValueError("weighted sums take non-extended ciphertexts")
+    limbs = min(_limbs(batch), table.cur_limbs)
+    r = table.residues if isinstance(table.residues, torch.Tensor) else torch.from_numpy(np.asarray(table.residues))
+    r = r.to(torch.uint64)
+    if r.dim() == 2:
+        r = r.unsqueeze(0)
+    n = batch.batch_size
+    if r.dim() != 3 or int(r.shape[1]) != n:
+        raise ValueError(f"weight table must be [groups][{n}][limbs]")
+    w = r[:, :, :limbs].contiguous()
+    out = [ctx.weighted_sum(_view(x, limbs), w, limbs) for x in batch.cv]
+    st = batch.state
+    state = st.replace(cur_limbs=limbs, scale_degree=int(st.scale_degree) + table.scale_degree,
+                       scaling_factor=float(st.scaling_factor) * table.scaling_factor)
+    return batch.cipher_like(out, state=state, batch_size=int(w.shape[0]))
+
+
+def cipher_batch_item(batch: Cipher, index: int) -> Cipher:
+    """Item ``index`` of a cipher batch as a one-item cipher (views; easyfhe.fhe.ops.layout,
+    polynomial.py:293-296)."""
+
+    i = int(index)
+    if not 0 <= i < batch.batch_size:
+        raise IndexError(f"item {i} of a batch of {batch.batch_size}")
+    return batch.cipher_like([x[i:i + 1] for x in batch.cv], batch_size=1)

@@ -24,6 +24,11 @@
  *                          gpu_packer.py:156-198)
  *   hck_encode             EasyFHE encode: special IFFT (cv_pre_encode_stage1) + holmes_encode_stage2
  *                          (round, reduce, NTT; holmes_encode.cu:240-285)
+ *   hck_tensor / hck_relinearize / hck_mul_relin
+ *                          fhe.homo_mul_no_relin / homo_relinearize / homo_mul_relin
+ *                          (llama3fhe/operators/attention/prefill/qk.py:460-464,
+ *                          attention/kernel_helpers.py:146-152, nonlinear/polynomial.py:140-190)
+ *   hck_weighted_sum       fhe.grouped_scalar_weighted_acc (nonlinear/polynomial.py:256-300)
  */
 #ifndef HOLMES_CKKS_H
 #define HOLMES_CKKS_H
@@ -124,6 +129,7 @@ int hck_rescale(const hck_context* ctx, int level_limbs, int polys, const uint64
 
 /* Elementwise limb ops on [polys][limbs][N] (limb l uses prime prime_idx[l]).
  * HCK_OP_ADD/SUB/MUL: out = a op b; NEG: out = -a; MUL_SCALAR: out = a * scalar[l];
+ * ADD_SCALAR: out = a + scalar[l] (a constant polynomial added in the NTT domain);
  * MUL_XHALF: out = a * X^(N/2) (NTT domain; times i on the slots); MAC: out = out + a * b. */
 #define HCK_OP_ADD 0
 #define HCK_OP_SUB 1
@@ -132,6 +138,7 @@ int hck_rescale(const hck_context* ctx, int level_limbs, int polys, const uint64
 #define HCK_OP_MUL_SCALAR 4
 #define HCK_OP_MUL_XHALF 5
 #define HCK_OP_MAC 6
+#define HCK_OP_ADD_SCALAR 7
 int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const uint64_t* a,
                 const uint64_t* b, int polys, int64_t out_stride, int64_t a_stride,
                 int64_t b_stride, int limbs, const int* prime_idx, const uint64_t* scalar,
@@ -169,6 +176,37 @@ size_t hck_encode_workspace_bytes(const hck_context* ctx, int rows);
 int hck_encode(const hck_context* ctx, const double* values, const double* values_im, int rows, double scale,
                int limbs, const int* prime_idx, uint64_t* out, int64_t out_row_stride, void* workspace,
                size_t workspace_bytes, int* overflow_flags, void* stream);
+
+/* Tensor product of `batch` ciphertext pairs at level_limbs limbs (a = (a0, a1), b = (b0, b1), item
+ * strides a_stride / b_stride): d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1 — the three-component
+ * product fhe.homo_mul_no_relin returns (llama3fhe/operators/attention/prefill/qk.py:460-464). */
+int hck_tensor(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0, const uint64_t* a1,
+               int64_t a_stride, const uint64_t* b0, const uint64_t* b1, int64_t b_stride, uint64_t* d0,
+               uint64_t* d1, uint64_t* d2, int64_t d_stride, void* stream);
+
+/* Relinearisation of three-component ciphertexts (d0, d1, d2) with the s^2 -> s key relin_ksk
+ * (layout as for hck_keyswitch): out = (d0, d1) + KeySwitch(d2), fhe.homo_relinearize
+ * (llama3fhe/operators/attention/kernel_helpers.py:146-152).  out0 / out1 may be d0 / d1, not d2. */
+size_t hck_relinearize_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
+int hck_relinearize(const hck_context* ctx, int level_limbs, int batch, const uint64_t* d0, const uint64_t* d1,
+                    const uint64_t* d2, int64_t in_stride, const uint64_t* relin_ksk, uint64_t* out0,
+                    uint64_t* out1, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Ciphertext x ciphertext product with relinearisation: hck_tensor followed by hck_relinearize
+ * (the tensor components stay in the workspace), fhe.homo_mul_relin
+ * (llama3fhe/operators/nonlinear/polynomial.py:140-190, before its rescale / post-ops). */
+size_t hck_mul_relin_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
+int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0, const uint64_t* a1,
+                  int64_t a_stride, const uint64_t* b0, const uint64_t* b1, int64_t b_stride,
+                  const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/* Grouped scalar-weighted sum over one component of n inputs (item stride in_stride, [limbs][N]
+ * each): out[g] = sum_j weights[g][j][l] * in[j] (mod q_l); weights is a device array
+ * [groups][n][limbs] of residues, out items at out_stride.  fhe.grouped_scalar_weighted_acc
+ * (llama3fhe/operators/nonlinear/polynomial.py:256-300). */
+int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int groups, const uint64_t* in, int64_t in_stride,
+                     const uint64_t* weights, uint64_t* out, int64_t out_stride, void* stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,9 @@
  *    llama3fhe/operators/linear/complex.py:63-67.
  *  - Exact-residue BSGS MAC res[g] = sum_b pt[g*B+b] * baby[b] mod q:
  *    bench/cmp/kernels/holmes_mac.cu:8-12.
+ *  - Ciphertext product (tensor, then relinearisation = key switch of d2 added to (d0, d1)) and the
+ *    grouped scalar-weighted sum: the call sites qk.py:460-464, kernel_helpers.py:146-152 and
+ *    nonlinear/polynomial.py:140-300 under llama3fhe/operators/.
  *
  * Parity pins for every function here live in tests/test_oracle_*.py (closed forms,
  * brute-force DFT, Python big-integer CRT, round trips).
@@ -477,6 +480,37 @@ void or_bsgs_mac(const or_ctx* c, int limbs, int nb, int G, const u64* pt, const
 void or_mul_limbs(const or_ctx* c, int limbs, const u64* a, const u64* b, u64* out) {
   for (int l = 0; l < limbs; ++l)
     for (u64 j = 0; j < c->n; ++j) out[l * c->n + j] = mulmod(a[l * c->n + j], b[l * c->n + j], c->primes[l]);
+}
+
+/* Ciphertext product before relinearisation (the textbook CKKS tensor: (a0 + a1 s)(b0 + b1 s) =
+ * d0 + d1 s + d2 s^2 slotwise in the NTT domain), as fhe.homo_mul_no_relin returns it
+ * (llama3fhe/operators/attention/prefill/qk.py:460-464): d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1. */
+void or_tensor(const or_ctx* c, int limbs, const u64* a0, const u64* a1, const u64* b0, const u64* b1, u64* d0,
+               u64* d1, u64* d2) {
+  for (int l = 0; l < limbs; ++l) {
+    const u64 q = c->primes[l];
+    for (u64 j = 0; j < c->n; ++j) {
+      const u64 k = l * c->n + j;
+      d0[k] = mulmod(a0[k], b0[k], q);
+      d1[k] = addmod(mulmod(a0[k], b1[k], q), mulmod(a1[k], b0[k], q), q);
+      d2[k] = mulmod(a1[k], b1[k], q);
+    }
+  }
+}
+
+/* out[g][l] = sum_j w[g][j][l] * x[j][l] mod q_l (fhe.grouped_scalar_weighted_acc,
+ * llama3fhe/operators/nonlinear/polynomial.py:256-300). */
+void or_weighted_sum(const or_ctx* c, int limbs, int n, int groups, const u64* x, const u64* w, u64* out) {
+  for (int g = 0; g < groups; ++g)
+    for (int l = 0; l < limbs; ++l) {
+      const u64 q = c->primes[l];
+      for (u64 j = 0; j < c->n; ++j) {
+        u128 acc = 0;
+        for (int t = 0; t < n; ++t)
+          acc += (u128)w[((u64)g * n + t) * limbs + l] * x[((u64)t * limbs + l) * c->n + j] % q;
+        out[((u64)g * limbs + l) * c->n + j] = (u64)(acc % q);
+      }
+    }
 }
 
 int or_num_threads(void) {

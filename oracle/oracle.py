@@ -62,6 +62,8 @@ def lib():
         "or_make_ksk": (None, [_vp, _i64p, _i64p, _u64p, _i64p, _u64p]),
         "or_bsgs_mac": (None, [_vp, i, i, i, _u64p, _u64p, _u64p]),
         "or_mul_limbs": (None, [_vp, i, _u64p, _u64p, _u64p]),
+        "or_tensor": (None, [_vp, i, _u64p, _u64p, _u64p, _u64p, _u64p, _u64p, _u64p]),
+        "or_weighted_sum": (None, [_vp, i, i, i, _u64p, _u64p, _u64p]),
         "or_num_threads": (i, []),
         "or_encode_twiddles": (None, [i, _f64p, _f64p]),
         "or_special_ifft": (None, [i, _f64p, _f64p, _f64p, _f64p]),
@@ -246,6 +248,35 @@ class OracleContext:
         out = np.zeros((idx.size, self.n), dtype=np.uint64)
         rc = lib().or_encode_real(self._h, _p(values), float(scale), int(idx.size), _p(idx), int(bool(ntt)), _p(out))
         return out, rc == 0
+
+    def tensor(self, limbs: int, a0, a1, b0, b1):
+        """(a0 b0, a0 b1 + a1 b0, a1 b1) over the first ``limbs`` Q primes ([limbs][N] each)."""
+
+        ins = [np.ascontiguousarray(np.asarray(v)[:limbs], dtype=np.uint64) for v in (a0, a1, b0, b1)]
+        outs = [np.zeros((limbs, self.n), dtype=np.uint64) for _ in range(3)]
+        lib().or_tensor(self._h, int(limbs), *[_p(v) for v in ins], *[_p(v) for v in outs])
+        return tuple(outs)
+
+    def relinearize(self, limbs: int, d0, d1, d2, rlk: np.ndarray):
+        """(d0, d1) + KeySwitch(d2) with the s^2 -> s key ``rlk`` (the oracle's key switch)."""
+
+        kb, ka = self.keyswitch(limbs, d2, rlk)
+        q = np.asarray(self.primes[:limbs], dtype=np.uint64)[:, None]
+        return (np.asarray(d0[:limbs], dtype=np.uint64) + kb) % q, (np.asarray(d1[:limbs], dtype=np.uint64) + ka) % q
+
+    def mul_relin(self, limbs: int, a0, a1, b0, b1, rlk: np.ndarray):
+        d0, d1, d2 = self.tensor(limbs, a0, a1, b0, b1)
+        return self.relinearize(limbs, d0, d1, d2, rlk)
+
+    def weighted_sum(self, limbs: int, x: np.ndarray, w: np.ndarray) -> np.ndarray:
+        """out[g] = sum_j w[g][j][l] x[j][l]: x [n][limbs][N], w [groups][n][limbs]."""
+
+        x = np.ascontiguousarray(np.asarray(x)[:, :limbs], dtype=np.uint64)
+        w = np.ascontiguousarray(w, dtype=np.uint64)
+        G, n = int(w.shape[0]), int(w.shape[1])
+        out = np.zeros((G, limbs, self.n), dtype=np.uint64)
+        lib().or_weighted_sum(self._h, int(limbs), n, G, _p(x), _p(w), _p(out))
+        return out
 
     def bsgs_mac(self, limbs: int, nb: int, G: int, pt: np.ndarray, baby: np.ndarray) -> np.ndarray:
         pt = np.ascontiguousarray(pt, dtype=np.uint64)

@@ -122,3 +122,26 @@ def test_easyfhe_alias_binds_the_hot_path_surface():
         assert easyfhe.uint64 is not None and easyfhe.get_device_module("cuda") is not None
     finally:
         easyfhe_compat.uninstall()
+
+
+def test_scalar_encoding_residues_and_rounding():
+    from types import SimpleNamespace
+
+    from holmes_amd import fhe
+
+    primes = [1125899906826241, 1125899906629633, 1125899906301953]
+    ctx = SimpleNamespace(q_primes=primes)
+    sf = 2.0**40
+    r = fhe._scalar_residues(0.5, 3, sf, False, ctx)
+    assert [int(v) for v in r[0]] == [2**39 % q for q in primes]
+    r = fhe._scalar_residues(-1.5, 2, sf, False, ctx)
+    assert [int(v) for v in r[0]] == [(-3 * 2**39) % q for q in primes[:2]]
+    # round half away from zero, as the encoder
+    assert fhe._scaled_int(2.5, 1.0, False) == 3 and fhe._scaled_int(-2.5, 1.0, False) == -3
+    assert fhe._scaled_int(7, 1.0, True) == 7
+    with pytest.raises(ValueError):
+        fhe._scaled_int(2.5, 1.0, True)  # integer mode needs an integral value
+    with pytest.raises(ValueError):
+        fhe._scaled_int(1.0, 2.0**61, False)  # beyond the 2^61 encoding cap
+    tab = fhe._scalar_residues(np.array([1.0, -1.0]), 3, 4.0, False, ctx)
+    assert tab.shape == (2, 3) and int(tab[1, 0]) == primes[0] - 4
