@@ -396,8 +396,9 @@ class CKKSContext:
                                     ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_relinearize")
         return out[0], out[1]
 
-    def mul_relin_raw(self, a0, a1, b0, b1, limbs: int, key: torch.Tensor):
-        """Tensor product followed by relinearisation: a two-component [batch][limbs][N] pair."""
+    def mul_relin_raw(self, a0, a1, b0, b1, limbs: int, key: torch.Tensor, stacked: bool = False):
+        """Tensor product followed by relinearisation: a two-component [batch][limbs][N] pair (or,
+        with ``stacked``, the one [2][batch][limbs][N] tensor holding both)."""
 
         self._check_key(key)
         sa = self._pair(a0, a1, limbs, "mul lhs")
@@ -411,7 +412,7 @@ class CKKSContext:
         nat.check(L.hck_mul_relin(self._h, limbs, B, a0.data_ptr(), a1.data_ptr(), sa, b0.data_ptr(), b1.data_ptr(),
                                   sb, key.data_ptr(), out[0].data_ptr(), out[1].data_ptr(), limbs * self.N,
                                   ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_mul_relin")
-        return out[0], out[1]
+        return out if stacked else (out[0], out[1])
 
     def weighted_sum(self, x: torch.Tensor, weights: torch.Tensor, limbs: int) -> torch.Tensor:
         """out[g] = sum_j weights[g][j][l] x[j] per limb l: x [n][>= limbs][N], weights a uint64

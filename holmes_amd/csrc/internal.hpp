@@ -55,11 +55,12 @@ struct hck_context {
   void* d_block = nullptr;            // one allocation holding all tables
   hck::ConvConsts* d_modup = nullptr; // [(L + 1) * beta_max]: index ell * beta_max + digit
   hck::ConvConsts* d_moddown = nullptr; // [L + 1]
+  hck::ConvConsts* d_rescale = nullptr; // [L + 1]: level ell converts limb ell - 1 to limbs 0 .. ell - 2
   hck::LevelConsts* d_level = nullptr;  // [L + 1]
   const uint64_t* d_primes_u64 = nullptr; // [np]
   const double* d_enc_twr = nullptr;      // [N/2]: special-IFFT roots, stage h at [h-1, 2h-1)
   const double* d_enc_twi = nullptr;
-  std::vector<hck::ConvConsts> h_modup, h_moddown;
+  std::vector<hck::ConvConsts> h_modup, h_moddown, h_rescale;
   std::vector<hck::LevelConsts> h_level;
   int beta_max;
 };
@@ -97,6 +98,11 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                 long long out_stride, char* ws, hipStream_t s);
+// Rescale of polys from ell to ell - 1 limbs on the ModDown kernels (q_{ell-1} as the one special
+// prime): out_i = (x_i - [centered x_{ell-1}]_{q_i}) * q_{ell-1}^-1.  Workspace: polys * ell limbs.
+size_t rescale_bytes(const hck_context* c, int ell, int polys);
+int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                  long long out_stride, char* ws, hipStream_t s);
 
 // MI355X deals consecutive workgroups to its 8 XCDs (each with its own L2) round-robin.
 constexpr int kXcds = 8;

@@ -1,4 +1,4 @@
-// Key-switch C ABI (the fused kernels live in ksfused.hip), rotation and rescale.
+// Key-switch C ABI (the fused kernels live in ksfused.hip), rotation, ModDown and rescale.
 #include <hip/hip_runtime.h>
 
 #include "../../include/holmes_ckks.h"
@@ -8,32 +8,6 @@ namespace hck {
 namespace {
 
 constexpr int kMaxBatch = 64;
-
-// Rescale helpers: spread the last limb's coefficients, as centered (-q_last/2, q_last/2]
-// values, to every lower prime, then combine (x_i - NTT(spread_i)) * q_last^-1 = round(X / q_last).
-__global__ __launch_bounds__(256) void k_rescale_spread(const uint64_t* __restrict__ last, double* __restrict__ spread,
-                                                        int ell, DevTables T) {
-  const int k = blockIdx.x * 256 + threadIdx.x;
-  const int i = blockIdx.y;
-  const long long z = blockIdx.z;
-  const double x = u2d(last[z * kN + k]);
-  const double p = T.p[i], ql = T.p[ell - 1];
-  // x in (q_last/2, q_last) stands for x - q_last; q_last < 2 q_i keeps both cases in [0, q_i)
-  spread[(z * (ell - 1) + i) * kN + k] = x > 0.5 * ql ? x - ql + p : (x >= p ? x - p : x);
-}
-
-__global__ __launch_bounds__(256) void k_rescale_combine(const uint64_t* __restrict__ in, long long in_stride,
-                                                         const double* __restrict__ spread, uint64_t* __restrict__ out,
-                                                         long long out_stride, int ell,
-                                                         const LevelConsts* __restrict__ lc, DevTables T) {
-  const int k = blockIdx.x * 256 + threadIdx.x;
-  const int i = blockIdx.y;
-  const long long z = blockIdx.z;
-  const double p = T.p[i], pinv = T.pinv[i];
-  const double x = u2d(in[z * in_stride + (long long)i * kN + k]);
-  const double v = spread[(z * (ell - 1) + i) * kN + k];
-  out[z * out_stride + (long long)i * kN + k] = d2u(canon(mulc(x - v, lc->qlast_inv[i], p), p, pinv));
-}
 
 }  // namespace
 }  // namespace hck
@@ -148,7 +122,7 @@ extern "C" int hck_moddown(const hck_context* ctx, int level_limbs, int polys, c
 
 extern "C" size_t hck_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int polys) {
   if (!ctx || level_limbs < 2 || level_limbs > ctx->L || polys < 0) return 0;
-  return (size_t)polys * hck::kN * 8 * (1 + (size_t)(level_limbs - 1));
+  return hck::rescale_bytes(ctx, level_limbs, polys);
 }
 
 extern "C" int hck_rescale(const hck_context* ctx, int level_limbs, int polys, const uint64_t* in,
@@ -157,28 +131,7 @@ extern "C" int hck_rescale(const hck_context* ctx, int level_limbs, int polys, c
   if (!ctx || !in || !out || polys < 0 || polys > 65535) return HCK_ERR_ARG;
   if (level_limbs < 2 || level_limbs > ctx->L) return HCK_ERR_ARG;
   if (polys == 0) return HCK_OK;
-  if (!workspace || workspace_bytes < hck_rescale_workspace_bytes(ctx, level_limbs, polys)) return HCK_ERR_WORKSPACE;
-  hipStream_t s = (hipStream_t)stream;
-  const int ell = level_limbs;
-  uint64_t* last = (uint64_t*)workspace;                    // [polys][N]
-  double* spread = (double*)(last + (size_t)polys * hck::kN);  // [polys][ell-1][N]
-  hck::LimbList l1;
-  l1.n = 1;
-  l1.off[0] = 0;
-  l1.prime[0] = (uint8_t)(ell - 1);
-  int rc = hck::launch_ntt_inv(ctx, in + (long long)(ell - 1) * hck::kN, hck::kU64, last, hck::kU64, polys,
-                               in_stride, hck::kN, l1, s);
-  if (rc) return rc;
-  hck::k_rescale_spread<<<dim3(hck::kN / 256, ell - 1, polys), 256, 0, s>>>(last, spread, ell, ctx->dev);
-  HCK_CHECK_LAUNCH();
-  hck::LimbList lq;
-  lq.n = ell - 1;
-  for (int i = 0; i < ell - 1; ++i) { lq.off[i] = (uint16_t)i; lq.prime[i] = (uint8_t)i; }
-  if ((rc = hck::launch_ntt_fwd(ctx, spread, hck::kF64, spread, hck::kF64, polys, (long long)(ell - 1) * hck::kN,
-                                (long long)(ell - 1) * hck::kN, lq, s)))
-    return rc;
-  hck::k_rescale_combine<<<dim3(hck::kN / 256, ell - 1, polys), 256, 0, s>>>(
-      in, in_stride, spread, out, out_stride, ell, ctx->d_level + ell, ctx->dev);
-  HCK_CHECK_LAUNCH();
-  return HCK_OK;
+  if (!workspace || workspace_bytes < hck::rescale_bytes(ctx, level_limbs, polys)) return HCK_ERR_WORKSPACE;
+  return hck::rescale_fused(ctx, level_limbs, polys, in, in_stride, out, out_stride, (char*)workspace,
+                            (hipStream_t)stream);
 }

@@ -746,12 +746,13 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restric
              out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
 }
 
-// ----------------------------------------------------------------- ModDown finish of ext-basis input
-// Poly p = blockIdx.x: v = NTT rows of T4[p]; out = (x_Q[p] - v) * P^-1 with x_Q canonical u64.
+// ----------------------------------------------------------------- ModDown / rescale finish
+// Poly p = blockIdx.x: v = NTT rows of T4[p] (ell limbs); out = (x[p] - v) * inv[i] with x canonical
+// u64: inv = P^-1 (ModDown of an extended-basis input) or q_last^-1 (rescale).
 __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict__ t4, const uint64_t* __restrict__ xq,
                                                        long long xq_pstride, uint64_t* __restrict__ out,
                                                        long long out_pstride, int ell,
-                                                       const LevelConsts* __restrict__ lc, DevTables T) {
+                                                       const TwPair* __restrict__ inv, DevTables T) {
   __shared__ double S[kRowLds];
   const int i = blockIdx.z, rg = blockIdx.y, pl = blockIdx.x;
   const double p = T.p[i], pinv = T.pinv[i];
@@ -763,10 +764,10 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
   for (int k = 0; k < 16; ++k) a[k] = u2d(ap[16 * k]);
   load_t(x, t4 + ((long long)pl * ell + i) * kN, rg);
   rows_fwd_t(x, rg, S, tw, p, pinv);
-  const TwPair pi_ = lc->p_inv[i];
+  const TwPair pi_ = inv[i];
   uint64_t* o = out + (long long)pl * out_pstride + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(a[k] - x[k], pi_, p), p, pinv));
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(a[k] - x[k], pi_, p), p, pinv));  // |a - x| <= 4.9 p
 }
 
 }  // namespace
@@ -856,8 +857,32 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
                                              c->d_moddown + ell, 0, c->dev);
   HCK_CHECK_LAUNCH();
-  k_ks_rows_finish<<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, out, out_stride, ell, c->d_level + ell,
-                                                       c->dev);
+  k_ks_rows_finish<<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, out, out_stride, ell,
+                                                       (c->d_level + ell)->p_inv, c->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+size_t rescale_bytes(const hck_context* c, int ell, int polys) { return (size_t)polys * kN * 8 * (size_t)ell; }
+
+// Rescale = ModDown with q_{ell-1} as the one special prime: INTT rows of the last limb, then the
+// cols kernel (INTT cols, centered lift, spread to the ell - 1 lower primes, NTT cols), then the
+// finish kernel with q_{ell-1}^-1.  The spread limbs cross HBM once (the two-pass NTT of a separate
+// spread would move them three times).
+int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                  long long out_stride, char* ws, hipStream_t s) {
+  const long long n = kN;
+  const int nt = ell - 1;
+  double* tl = (double*)ws;                       // [polys][1] workspace layout
+  double* t4 = tl + (long long)polys * n;         // [polys][ell - 1] workspace layout
+  k_ks_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, 1u, ell - 1,
+                                                                                ell - 1, tl, 1, polys, c->dev);
+  HCK_CHECK_LAUNCH();
+  auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  conv<<<dim3(128, 1, polys), kT, 0, s>>>(tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_rescale + ell, 0, c->dev);
+  HCK_CHECK_LAUNCH();
+  k_ks_rows_finish<<<dim3(polys, 16, nt), kT, 0, s>>>(t4, in, in_stride, out, out_stride, nt,
+                                                      (c->d_level + ell)->qlast_inv, c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }
