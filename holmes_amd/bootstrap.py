@@ -1,0 +1,685 @@
+"""CKKS bootstrapping of full-slot ciphertexts on the GPU kernels (the ``easyfhe.bs.openfhe``
+surface Holmes drives: ``BootstrapSpec``, ``generate(context, spec)``, ``bootstrap(cipher, context,
+program)``, ``requirements(specs, log_n).rotations``; llama3fhe/operators/nonlinear/
+bootstrap.py:119-160,260-348,626-640).
+
+Pipeline ("modraise_first"), every step a sequence of this package's HIP-backed operations:
+
+1. Pre-scale: multiply by 2^-r (r message-ratio bits, rescaled) and drop to one limb, so the
+   message m(X) is small against q_0 (sin(2 pi m / q_0) ~ 2 pi m / q_0).
+2. ModRaise to ``raise_to_limbs`` limbs: the ciphertext now decrypts to M = m + q_0 I(X) with a
+   small integer polynomial I (|I| bounded through the sparse secret).
+3. CoeffToSlot: the slot vector of M is U0 (M_lo + i M_hi) (U0 the n x n special DFT, n = N / 2,
+   slot j = m(zeta_j), zeta_j = exp(2 pi i 5^j / 2N)); U0^-1 = (bit reversal) x 15 inverse butterfly
+   layers, applied as ``level_budget[0]`` merged layers, each a BSGS plaintext product of its
+   diagonals.  Output: (M_lo + i M_hi) / (2 q_0 K') in bit-reversed slot order.
+4. Real / imaginary split with the conjugation key: R = x + conj(x), J = -i (x - conj(x)), slots
+   t / K' with t = m / q_0 + I.
+5. EvalMod on R and J (one batch): a Chebyshev interpolant of cos(2 pi (K' u - 1/4) / 2^d) on
+   [-1, 1], then d double-angle steps cos(2a) = 2 cos^2(a) - 1: sin(2 pi t) = sin(2 pi m / q_0).
+6. Recombine R + i J and SlotToCoeff: U0 (the forward butterflies, bit-reversed input) times
+   q_0 / (2 pi S) in the plaintexts, then the integer 2^r; the output decrypts to the input message.
+
+Scales: every plaintext and scalar multiplied in is encoded at exactly the prime the following
+rescale drops, so the working scale never drifts; after ModRaise the ciphertext is read at the
+context's nominal scale S = 2^scale_bits (only the decryption M matters), and the output state
+carries the exact factor that makes its slots equal the input message.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import numpy as np
+import torch
+
+from . import fhe
+from .context import Cipher, CKKSContext
+
+__all__ = ["BootstrapSpec", "BootstrapProgram", "Requirements", "Stage", "requirements", "generate", "bootstrap",
+           "special_fft_layers", "merge_layers", "chebyshev_divide", "canonical_scales", "evalmod_levels",
+           "evalmod_coefficients", "make_stage", "plan_stages", "plan_program", "stage_rows", "apply_stage",
+           "apply_stages", "bootstrap_with_correction"]
+
+
+# ---------------------------------------------------------------------------- spec / requirements
+@dataclass(frozen=True)
+class BootstrapSpec:
+    """Keywords of easyfhe.bs.openfhe.BootstrapSpec as Holmes builds it (bootstrap.py:119-160);
+    the EvalMod fields are this backend's.  ``output_levels`` 0 means all that remain."""
+
+    log_slots: int = 15
+    level_budget: tuple = (3, 3)
+    output_levels: int = 0
+    strategy: str = "normal_bsgs"
+    mode: str = "modraise_first"
+    dim1: tuple | None = None
+    baby_step: tuple | None = None
+    message_ratio_bits: int = 8  # message <= 2^-8 q_0 at one limb: sine error <= 2^-13.3 relative
+    mod_bound: int = 24          # |I| <= mod_bound on every coefficient (sparse secret)
+    double_angle: int = 3
+    cheb_degree: int = 48
+
+    def validate(self, log_n: int) -> None:
+        if int(self.log_slots) != int(log_n) - 1:
+            raise ValueError("this bootstrap handles full-slot ciphertexts (log_slots = log_n - 1)")
+        if str(self.mode) != "modraise_first":
+            raise ValueError("only mode='modraise_first' is supported")
+        if len(tuple(self.level_budget)) != 2 or min(int(b) for b in self.level_budget) < 1:
+            raise ValueError("level_budget needs two positive entries (CoeffToSlot, SlotToCoeff)")
+
+
+@dataclass(frozen=True)
+class Requirements:
+    rotations: tuple
+    depth: int
+
+
+def _split(count: int, parts: int) -> list[int]:
+    """Sizes of ``parts`` contiguous groups covering ``count`` layers, the larger groups first."""
+
+    parts = max(1, min(int(parts), count))
+    base, extra = divmod(count, parts)
+    return [base + (1 if i < extra else 0) for i in range(parts)]
+
+
+def _stage_layers(log_slots: int, budget: int, inverse: bool) -> list[list[int]]:
+    """Layer indices t (1..log_slots, layer t has block size n >> (t - 1)) per stage, in the order
+    the stages are applied: CoeffToSlot applies L_1^-1 first, SlotToCoeff L_logn first."""
+
+    order = list(range(1, log_slots + 1)) if inverse else list(range(log_slots, 0, -1))
+    out, i = [], 0
+    for size in _split(log_slots, budget):
+        out.append(order[i:i + size])
+        i += size
+    return out
+
+
+def _bsgs_shape(layers: list[int], n: int) -> tuple[int, int, int]:
+    """(h_min, n1, kmax): the stage's diagonals sit at k h_min, |k| <= kmax; babies 0..n1-1."""
+
+    hs = [n >> t for t in layers]
+    h_min = min(hs)
+    kmax = sum(h // h_min for h in hs)
+    n1 = 1 << max(1, math.ceil(math.log2(2 * kmax + 1) / 2))
+    return h_min, n1, kmax
+
+
+def _stage_rotations(layers: list[int], n: int) -> set[int]:
+    h_min, n1, kmax = _bsgs_shape(layers, n)
+    rots = {(k1 * h_min) % n for k1 in range(1, n1)}
+    for k2 in range(-((kmax + n1 - 1) // n1) - 1, kmax // n1 + 2):
+        if k2:
+            rots.add((k2 * n1 * h_min) % n)
+    rots.discard(0)
+    return rots
+
+
+def requirements(specs, log_n: int) -> Requirements:
+    """Rotation amounts (slot rotations, plus the conjugation 2N - 1) and depth of the programs."""
+
+    specs = (specs,) if isinstance(specs, BootstrapSpec) else tuple(specs)
+    n = 1 << (int(log_n) - 1)
+    rots: set[int] = set()
+    depth = 0
+    for spec in specs:
+        spec.validate(log_n)
+        b1, b2 = (int(b) for b in spec.level_budget)
+        for layers in _stage_layers(spec.log_slots, b1, True) + _stage_layers(spec.log_slots, b2, False):
+            rots |= _stage_rotations(layers, n)
+        depth = max(depth, b1 + b2 + evalmod_levels(spec, 1024, [2] * 1025))
+    rots.add(4 * n - 1)  # conjugation
+    return Requirements(rotations=tuple(sorted(rots)), depth=depth)
+
+
+# ---------------------------------------------------------------------------- special FFT
+def _pow5(count: int, mod: int) -> np.ndarray:
+    out = np.empty(count, dtype=np.int64)
+    v = 1
+    for j in range(count):
+        out[j] = v
+        v = v * 5 % mod
+    return out
+
+
+def special_fft_layers(log_slots: int, inverse: bool = False) -> list[dict]:
+    """Diagonals of the butterfly layers L_t = I_(2^(t-1)) (x) B_m, m = n >> (t - 1), of the special
+    DFT U0 = L_1 L_2 ... L_logn (bit reversal):  B_m = [[I, D], [I, -D]], D = diag(exp(2 pi i 5^p /
+    4m)), p < m / 2.  With ``inverse`` the layers of U0^-1 (B_m^-1 = [[I, I], [D^-1, -D^-1]] / 2).
+    Layer t as {rotation d in [0, n): slot vector diag_d}, (A x)_j = sum_d diag_d[j] x[(j + d) mod n]."""
+
+    n = 1 << int(log_slots)
+    p5 = _pow5(n // 2, 4 * n)
+    layers = []
+    for t in range(1, int(log_slots) + 1):
+        m = n >> (t - 1)
+        h = m // 2
+        p = np.arange(n) % m
+        lo = p < h
+        pp = np.where(lo, p, p - h)
+        D = np.exp(2j * np.pi * (p5[pp] % (4 * m)) / (4 * m))
+        if not inverse:
+            d0 = np.where(lo, 1.0, -D)
+            dp = np.where(lo, D, 0.0)
+            dm = np.where(lo, 0.0, 1.0)
+        else:
+            d0 = np.where(lo, 0.5, -0.5 / D)
+            dp = np.where(lo, 0.5, 0.0)
+            dm = np.where(lo, 0.0, 0.5 / D)
+        diags: dict[int, np.ndarray] = {}
+        for d, v in ((0, d0), (h % n, dp), ((n - h) % n, dm)):
+            diags[d] = diags.get(d, 0) + v.astype(np.complex128)
+        layers.append(diags)
+    return layers
+
+
+def merge_layers(layers: list[dict], n: int) -> dict:
+    """Diagonals of A_r ... A_2 A_1 (A_1 applied first): (A B)_(d+e) += a_d rot(b_e, d)."""
+
+    acc = {d: v.copy() for d, v in layers[0].items()}
+    for a in layers[1:]:
+        out: dict[int, np.ndarray] = {}
+        for d, ad in a.items():
+            for e, be in acc.items():
+                k = (d + e) % n
+                out[k] = out.get(k, 0) + ad * np.roll(be, -d)
+        acc = out
+    return {d: v for d, v in acc.items() if np.max(np.abs(v)) > 1e-13}
+
+
+def bit_reverse_order(values: np.ndarray) -> np.ndarray:
+    n = values.shape[-1]
+    bits = n.bit_length() - 1
+    idx = np.array([int(format(i, f"0{bits}b")[::-1], 2) for i in range(n)])
+    return values[..., idx]
+
+
+# ---------------------------------------------------------------------------- Chebyshev evaluation
+def chebyshev_divide(coeffs: np.ndarray, M: int) -> tuple[np.ndarray, np.ndarray]:
+    """p = q T_M + r for a Chebyshev series p of length <= 2M: T_(M+a) = 2 T_M T_a - T_(M-a)."""
+
+    c = np.asarray(coeffs, dtype=np.float64)
+    if len(c) <= M:
+        return np.zeros(1), c.copy()
+    if len(c) > 2 * M:
+        raise ValueError("chebyshev_divide needs len(coeffs) <= 2 M")
+    q = np.zeros(len(c) - M)
+    r = c[:M].copy()
+    q[0] = c[M]
+    for a in range(1, len(c) - M):
+        q[a] = 2.0 * c[M + a]
+        r[M - a] -= c[M + a]
+    return q, r
+
+
+def _baby_size(degree: int) -> int:
+    return 1 << max(1, math.ceil(math.log2(math.sqrt(degree + 1))))
+
+
+def canonical_scales(primes, top_limbs: int, top_scale: float) -> dict:
+    """Scale of a ciphertext at each level below ``top_limbs`` when every product multiplies two
+    operands of one level and rescales: S_(l) = S_(l+1)^2 / q_l (q_l the prime the rescale from
+    l + 1 limbs drops)."""
+
+    out = {int(top_limbs): float(top_scale)}
+    for l in range(int(top_limbs) - 1, 0, -1):
+        out[l] = out[l + 1] * out[l + 1] / float(primes[l])
+    return out
+
+
+class _PSEval:
+    """Chebyshev series on a cipher batch with slots in [-1, 1], every scale exact.
+
+    Paterson-Stockmeyer over the Chebyshev basis (the split of the reference's evaluator,
+    llama3fhe/operators/nonlinear/polynomial.py:140-330): baby basis T_1 .. T_k, giants T_k, T_2k,
+    ..., p = q T_M + r (``chebyshev_divide``) recursively.  Every ciphertext at l limbs carries the
+    canonical scale S_(l) (``canonical_scales``): a product of two operands at one level lands on
+    the next level's scale, a linear combination encodes each coefficient at the ratio that lands
+    its term on the target scale (so it changes level and scale for free), and ``adjust`` (one
+    scalar product and rescale) brings any other operand down to a level.  Additions therefore
+    never mix scales.  With ``sim`` the operands are plain limb counts: the same schedule run for
+    its levels only (the program's depth)."""
+
+    def __init__(self, ctx: CKKSContext | None, x, limbs: int, scale: float, degree: int, primes,
+                 sim: bool = False):
+        self.ctx = ctx
+        self.sim = bool(sim)
+        self.primes = [int(p) for p in primes]
+        self.canon = canonical_scales(self.primes, limbs, scale)
+        self.k = _baby_size(degree)
+        self._adj: dict = {}
+        T = {1: (limbs if self.sim else self._fix(x, limbs))}
+        for j in range(2, self.k + 1):
+            a, b = j // 2, j - j // 2
+            T[j] = self.double_minus(T[a], T[b], sub=None if a == b else T[1])
+        M = 2 * self.k
+        while M <= degree:
+            T[M] = self.double_minus(T[M // 2], T[M // 2])
+            M *= 2
+        self.T = T
+
+    # -- primitives (ciphertexts, or limb counts when simulating)
+    def lv(self, x) -> int:
+        return int(x) if self.sim else int(x.state.cur_limbs)
+
+    def _fix(self, ct: Cipher, l: int) -> Cipher:
+        want = self.canon[l]
+        got = float(ct.state.scaling_factor)
+        if abs(got - want) > 2.0**-40 * want:
+            raise AssertionError(f"scale {got} at {l} limbs drifted from {want}")
+        return ct.cipher_like(ct.cv, state=ct.state.replace(scaling_factor=want, scale_degree=1))
+
+    def adjust(self, x, l: int):
+        lx = self.lv(x)
+        if lx == l:
+            return x
+        if lx < l:
+            raise AssertionError(f"cannot raise an operand from {lx} to {l} limbs")
+        if self.sim:
+            return l
+        key = (id(x), l)
+        hit = self._adj.get(key)
+        if hit is not None and hit[0] is x:
+            return hit[1]
+        ctx = self.ctx
+        t = fhe.align_to(x, x.state.replace(cur_limbs=l + 1), ctx) if lx > l + 1 else x
+        ratio = self.canon[l] * float(self.primes[l]) / self.canon[lx]
+        enc = fhe.encode_scalar(1.0, cur_limbs=l + 1, scale_degree=1, scaling_factor=ratio, context=ctx)
+        y = self._fix(fhe.rescale(fhe.homo_mul_scalar(t, enc, ctx), ctx), l)
+        self._adj[key] = (x, y)
+        return y
+
+    def mul(self, a, b):
+        l = min(self.lv(a), self.lv(b))
+        if l < 2:
+            raise ValueError("EvalMod ran out of levels")
+        a, b = self.adjust(a, l), self.adjust(b, l)
+        if self.sim:
+            return l - 1
+        return self._fix(fhe.rescale(fhe.homo_mul_relin(a, b, self.ctx), self.ctx), l - 1)
+
+    def add(self, a, b):
+        l = min(self.lv(a), self.lv(b))
+        a, b = self.adjust(a, l), self.adjust(b, l)
+        return l if self.sim else fhe.homo_add(a, b, self.ctx)
+
+    def add_const(self, x, c: float):
+        if self.sim or c == 0.0:
+            return x
+        l = self.lv(x)
+        enc = fhe.encode_scalar(float(c), cur_limbs=l, scale_degree=1, scaling_factor=self.canon[l], context=self.ctx)
+        return fhe.homo_add_scalar(x, enc, self.ctx)
+
+    def double_minus(self, a, b, sub=None):
+        """2 a b - sub (sub = None: - 1)."""
+
+        p = self.mul(a, b)
+        if self.sim:
+            return p
+        p2 = fhe.homo_add(p, p, self.ctx)
+        if sub is None:
+            return self.add_const(p2, -1.0)
+        return fhe.homo_sub(p2, self.adjust(sub, self.lv(p2)), self.ctx)
+
+    def lincomb(self, terms, c0: float, cap: int | None):
+        """c0 + sum c_j x_j over ``terms`` = [(c_j, x_j)], rescaled once, at min(level) - 1 or ``cap``."""
+
+        l = min(self.lv(x) for _, x in terms) - 1
+        if cap is not None:
+            l = min(l, int(cap))
+        if l < 1:
+            raise ValueError("EvalMod ran out of levels")
+        if self.sim:
+            return l
+        ctx = self.ctx
+        target = self.canon[l] * float(self.primes[l])
+        acc = None
+        for c, x in terms:
+            lx = self.lv(x)
+            t = fhe.align_to(x, x.state.replace(cur_limbs=l + 1), ctx) if lx > l + 1 else x
+            enc = fhe.encode_scalar(float(c), cur_limbs=l + 1, scale_degree=1,
+                                    scaling_factor=target / self.canon[lx], context=ctx)
+            term = fhe.homo_mul_scalar(t, enc, ctx)
+            term = term.cipher_like(term.cv, state=term.state.replace(scaling_factor=target))
+            acc = term if acc is None else fhe.homo_add(acc, term, ctx)
+        return self.add_const(self._fix(fhe.rescale(acc, ctx), l), c0)
+
+    # -- the series
+    def evaluate(self, coeffs, cap: int | None = None):
+        c = np.asarray(coeffs, dtype=np.float64)
+        if len(c) <= self.k:
+            terms = [(c[j], self.T[j]) for j in range(1, len(c)) if c[j] != 0.0] or [(0.0, self.T[1])]
+            return self.lincomb(terms, float(c[0]), cap)
+        M = self.k
+        while 2 * M < len(c):
+            M *= 2
+        q, r = chebyshev_divide(c, M)
+        TM = self.T[M]
+        if len(q) == 1:
+            prod = self.lincomb([(q[0], TM)], 0.0, cap)
+        else:
+            qe = self.evaluate(q, self.lv(TM) if cap is None else min(self.lv(TM), cap + 1))
+            prod = self.mul(qe, TM)
+            if cap is not None and self.lv(prod) > cap:
+                prod = self.adjust(prod, cap)
+        re = self.evaluate(r, self.lv(prod))
+        return self.add(prod, re)
+
+
+def evalmod_levels(spec: BootstrapSpec, limbs: int, primes) -> int:
+    """Levels the EvalMod of ``spec`` consumes from ``limbs`` limbs (Chebyshev series and the
+    double-angle steps)."""
+
+    ev = _PSEval(None, None, limbs, 1.0, int(spec.cheb_degree), primes, sim=True)
+    y = ev.evaluate(np.ones(int(spec.cheb_degree) + 1))
+    for _ in range(int(spec.double_angle)):
+        y = ev.double_minus(y, y)
+    return limbs - int(y)
+
+
+# ---------------------------------------------------------------------------- program
+@dataclass
+class Stage:
+    """One merged linear-transform stage: sum_k diags[k] (.) rot(x, k h_min), |k| <= kmax, by
+    ``n1`` baby rotations (k1 h_min, k1 < n1) and one giant rotation per k2 (k2 n1 h_min)."""
+
+    layers: list
+    h_min: int
+    n1: int
+    giants: list            # giant indices k2, ascending
+    diags: dict             # k -> slot vector (complex128, length n)
+    cache: dict = field(default_factory=dict)  # limbs -> encoded rows [giants * n1][limbs][N]
+
+
+def make_stage(layers: list[int], all_layers: list[dict], n: int, factor: float = 1.0) -> Stage:
+    """Merge ``layers`` (applied in list order) into one stage, every diagonal times ``factor``."""
+
+    h_min, n1, kmax = _bsgs_shape(layers, n)
+    merged = merge_layers([all_layers[t - 1] for t in layers], n)
+    diags: dict[int, np.ndarray] = {}
+    for d, v in merged.items():
+        s = d - n if d > n // 2 else d
+        if s % h_min or abs(s // h_min) > kmax:
+            raise AssertionError("merged diagonal off the stage's grid")
+        diags[s // h_min] = v * factor
+    giants = sorted({k // n1 for k in diags})
+    return Stage(layers=list(layers), h_min=h_min, n1=n1, giants=giants, diags=diags)
+
+
+def stage_rows(st: Stage, n: int) -> np.ndarray:
+    """Plaintext rows [giant][baby] of a stage: diags[k1 + k2 n1] rotated right by k2 n1 h_min, so
+    that sum_k2 rot(sum_k1 row[k2][k1] (.) rot(x, k1 h_min), k2 n1 h_min) = sum_k diags[k] (.)
+    rot(x, k h_min) (the giant rotation lines each row up again)."""
+
+    rows = np.zeros((len(st.giants) * st.n1, n), dtype=np.complex128)
+    for gi, k2 in enumerate(st.giants):
+        for k1 in range(st.n1):
+            v = st.diags.get(k1 + k2 * st.n1)
+            if v is not None:
+                rows[gi * st.n1 + k1] = np.roll(v, k2 * st.n1 * st.h_min)
+    return rows
+
+
+def plan_stages(log_slots: int, budget: int, inverse: bool, factor: float) -> list[Stage]:
+    """CoeffToSlot (``inverse``: U0^-1 up to the bit reversal) or SlotToCoeff (U0 of a bit-reversed
+    input) as ``budget`` merged stages, ``factor`` folded into the first."""
+
+    n = 1 << int(log_slots)
+    layers = special_fft_layers(log_slots, inverse=inverse)
+    groups = _stage_layers(log_slots, budget, inverse)
+    return [make_stage(g, layers, n, factor if i == 0 else 1.0) for i, g in enumerate(groups)]
+
+
+class _Constants:
+    """Program constants view with the reference's cache-mode call (bootstrap.py:264-275): the
+    encoded diagonals are kept per level unless the mode is "none"."""
+
+    def __init__(self, program: "BootstrapProgram"):
+        self._program = program
+        self.mode = "plain"
+
+    def set_cache_mode(self, mode: str, clear: bool = False) -> None:
+        self.mode = str(mode)
+        if clear:
+            self._program.release()
+
+
+@dataclass
+class BootstrapProgram:
+    spec: BootstrapSpec
+    raise_to_limbs: int
+    evalmod_limbs: int        # limbs entering EvalMod
+    output_limbs: int         # limbs the refreshed ciphertext leaves with
+    q0: int
+    nominal_scale: float      # S: ModRaise output read at this scale
+    evalmod_out_scale: float  # canonical scale at EvalMod's output level
+    mod_scale: float          # K' = mod_bound + 1
+    cheb: np.ndarray          # Chebyshev coefficients of cos(2 pi (K' u - 1/4) / 2^d) on [-1, 1]
+    cts: list
+    stc: list
+    cts_rho: float            # per-stage share of the CoeffToSlot constant S / (2 q_0 K')
+    stc_rho: float            # per-stage share of the SlotToCoeff constant q_0 / (2 pi S_out)
+    constants: _Constants = None
+
+    def release(self) -> None:
+        for st in self.cts + self.stc:
+            st.cache.clear()
+
+
+def evalmod_coefficients(spec: BootstrapSpec) -> np.ndarray:
+    Kp = float(int(spec.mod_bound) + 1)
+    d = float(1 << int(spec.double_angle))
+    return np.polynomial.chebyshev.chebinterpolate(
+        lambda u: np.cos(2.0 * np.pi * (Kp * u - 0.25) / d), int(spec.cheb_degree))
+
+
+def generate(context: CKKSContext, spec: BootstrapSpec) -> BootstrapProgram:
+    """Plan a bootstrap for ``context``: merged CoeffToSlot / SlotToCoeff diagonals (encoded per
+    level on first use), the EvalMod interpolant and the level schedule.  The context must hold
+    the rotation keys of ``requirements(spec, log_n).rotations`` and its relinearisation key."""
+
+    ctx = context
+    spec.validate(ctx.logN)
+    req = requirements(spec, ctx.logN)
+    missing = [r for r in req.rotations if fhe._galois(r, ctx) not in ctx.rotation_keys]
+    if missing:
+        raise ValueError(f"the context lacks {len(missing)} bootstrap rotation keys (e.g. {missing[:4]}); "
+                         "generate them from requirements(spec, log_n).rotations")
+    if ctx.relin_key is None:
+        raise ValueError("bootstrap needs the relinearisation key")
+    return plan_program(spec, ctx.q_primes, float(ctx.scale_at(ctx.L)), ctx.L)
+
+
+def plan_program(spec: BootstrapSpec, q_primes, scale: float, raise_to: int) -> BootstrapProgram:
+    """The host half of ``generate``: level schedule, stage diagonals and interpolant for a chain
+    of Q primes, the nominal scale S and the ModRaise target."""
+
+    b1, b2 = (int(b) for b in spec.level_budget)
+    raise_to = int(raise_to)
+    em_in = raise_to - b1
+    primes = [int(p) for p in q_primes]
+    em_out = em_in - evalmod_levels(spec, em_in, primes)
+    out = em_out - b2
+    if out < 1:
+        raise ValueError(f"the bootstrap needs {raise_to - out + 1} limbs; the context has {raise_to}")
+    if int(spec.output_levels) and int(spec.output_levels) > out:
+        raise ValueError(f"output_levels {spec.output_levels} exceeds the {out} limbs the program leaves")
+    q0 = primes[0]
+    S = float(scale)
+    S_out = canonical_scales(primes, em_in, S)[em_out]
+    Kp = float(int(spec.mod_bound) + 1)
+    prog = BootstrapProgram(spec=spec, raise_to_limbs=raise_to, evalmod_limbs=em_in, output_limbs=out, q0=q0,
+                            nominal_scale=S, evalmod_out_scale=S_out, mod_scale=Kp,
+                            cheb=evalmod_coefficients(spec),
+                            cts=plan_stages(spec.log_slots, b1, True, 1.0),
+                            stc=plan_stages(spec.log_slots, b2, False, 1.0),
+                            cts_rho=(S / (2.0 * q0 * Kp)) ** (1.0 / b1),
+                            stc_rho=(q0 / (2.0 * math.pi * S_out)) ** (1.0 / b2))
+    prog.constants = _Constants(prog)
+    return prog
+
+
+# ---------------------------------------------------------------------------- evaluation
+def _stage_plaintexts(st: Stage, limbs: int, pt_scale: float, ctx: CKKSContext, keep: bool) -> torch.Tensor:
+    key = (int(limbs), float(pt_scale))
+    pts = st.cache.get(key)
+    if pts is not None:
+        return pts
+    rows = stage_rows(st, ctx.max_slots)
+    re = torch.from_numpy(np.ascontiguousarray(rows.real)).to(ctx.device)
+    im = torch.from_numpy(np.ascontiguousarray(rows.imag)).to(ctx.device)
+    pts = ctx.encode(re, float(pt_scale), int(limbs), values_im=im)
+    if keep:
+        st.cache[key] = pts
+    return pts
+
+
+def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: bool = True) -> Cipher:
+    """One stage on a one-item cipher, without a rescale: baby rotations, the baby-step MAC of
+    every giant row with the diagonals encoded at ``pt_scale``, the giant rotations accumulated in
+    place.  The slots become the stage applied to the slots; the scaling factor is multiplied by
+    ``pt_scale`` (the caller rescales, possibly after further stages: the key-switch noise of a
+    rotation is then small against the still unrescaled message)."""
+
+    limbs = int(x.state.cur_limbs)
+    babies = fhe.fast_rotate(x, [k1 * st.h_min for k1 in range(st.n1)], ctx)
+    pts = _stage_plaintexts(st, limbs, pt_scale, ctx, keep)
+    res = ctx.bsgs_mac([babies.cv[0][i:i + 1] for i in range(st.n1)],
+                       [babies.cv[1][i:i + 1] for i in range(st.n1)], pts, limbs, len(st.giants))
+    babies.release()
+    n = ctx.max_slots
+    order = sorted(range(len(st.giants)), key=lambda gi: st.giants[gi] != 0)  # the unrotated row first
+    acc0 = acc1 = None
+    for gi in order:
+        k2 = st.giants[gi]
+        c0, c1 = res[0, gi], res[1, gi]
+        if k2 == 0:
+            acc0, acc1 = c0, c1
+            continue
+        g = ctx.galois_element((k2 * st.n1 * st.h_min) % n)
+        key = ctx.key_for_galois(g)
+        if acc0 is None:
+            acc0, acc1 = ctx.rotate_raw(c0, c1, limbs, g, key)
+        else:
+            ctx.rotate_raw(c0, c1, limbs, g, key, out0=acc0, out1=acc1, acc=(acc0, acc1))
+    s = x.state
+    return x.cipher_like([acc0, acc1], batch_size=1,
+                         state=s.replace(scale_degree=int(s.scale_degree) + 1,
+                                         scaling_factor=float(s.scaling_factor) * float(pt_scale)))
+
+
+def apply_stages(x: Cipher, stages: list, rho: float, ctx: CKKSContext, keep: bool = True) -> Cipher:
+    """All ``stages`` at the input's level (stage i's plaintexts at q_(l-1-i) rho, the prime the
+    i-th of the later rescales drops), no rescale: ``len(stages)`` rescales return the scale to
+    the input's times rho^len(stages)."""
+
+    limbs = int(x.state.cur_limbs)
+    if limbs <= len(stages):
+        raise ValueError(f"{len(stages)} stages need more than {limbs} limbs")
+    for i, st in enumerate(stages):
+        x = apply_stage(x, st, ctx, float(ctx.rescale_divisor_at(limbs - i)) * rho, keep)
+    return x
+
+
+def _rescale_times(ct: Cipher, times: int, scale: float, ctx: CKKSContext) -> Cipher:
+    for _ in range(int(times)):
+        ct = fhe.rescale(ct, ctx)
+    return ct.cipher_like(ct.cv, state=ct.state.replace(scaling_factor=float(scale), scale_degree=1))
+
+
+def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram) -> Cipher:
+    """Refresh ``cipher`` (one item, two components, >= 2 limbs, full slots, |slot| <= 1) to
+    ``spec.output_levels`` limbs (0: all the program leaves).  The result keeps the input's
+    scaling factor; the input is not consumed."""
+
+    ctx = context
+    spec = program.spec
+    if cipher.is_ext or len(cipher.cv) != 2 or cipher.batch_size != 1:
+        raise ValueError("bootstrap takes one two-component, non-extended ciphertext")
+    if int(cipher.state.cur_limbs) < 2:
+        raise ValueError("bootstrap needs at least two limbs (one is spent scaling the message down)")
+    if int(cipher.slots) != ctx.max_slots:
+        raise ValueError("bootstrap handles full-slot ciphertexts")
+    keep = program.constants is None or program.constants.mode != "none"
+    S_in = float(cipher.state.scaling_factor)
+    limbs = int(cipher.state.cur_limbs)
+    b1, b2 = len(program.cts), len(program.stc)
+    # 1. message down to 2^-bits of q_0, then one limb
+    bits = max(0, int(round(math.log2(S_in / program.q0))) + int(spec.message_ratio_bits))
+    x = cipher
+    if bits:
+        enc = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
+                                scaling_factor=float(ctx.rescale_divisor_at(limbs)) * 2.0**-bits, context=ctx)
+        x = fhe.rescale(fhe.homo_mul_scalar(x, enc, ctx), ctx)
+    # 2. ModRaise: decrypts to M = m + q_0 I over the raised modulus; read at the nominal scale S
+    raised = [ctx.modraise(c[:, :1].contiguous(), program.raise_to_limbs) for c in x.cv]
+    S = program.nominal_scale
+    ct = x.cipher_like(raised, state=x.state.replace(cur_limbs=program.raise_to_limbs, scale_degree=1,
+                                                     scaling_factor=S))
+    # 3. CoeffToSlot at the raised level: (M_lo + i M_hi) / (2 q_0 K') up to the shares rho
+    ct = apply_stages(ct, program.cts, program.cts_rho, ctx, keep)
+    # 4. real and imaginary parts before the rescales (t / K' with t = M / q_0), then b1 rescales
+    conj = fhe.homo_rotate(ct, ctx.M - 1, ctx)
+    re = fhe.homo_add(ct, conj, ctx)
+    im = fhe.homo_mul_i(fhe.homo_sub(ct, conj, ctx), ctx, negative=True)
+    both = _rescale_times(fhe.pack_cipher_batch([re, im]), b1, S, ctx)
+    # 5. EvalMod: sin(2 pi t) = cos(2 pi (K' u - 1/4)) by the interpolant and double angles
+    ev = _PSEval(ctx, both, program.evalmod_limbs, S, int(spec.cheb_degree), ctx.q_primes)
+    y = ev.evaluate(program.cheb)
+    for _ in range(int(spec.double_angle)):
+        y = ev.double_minus(y, y)
+    yr, yi = fhe.cipher_batch_item(y, 0), fhe.cipher_batch_item(y, 1)
+    z = fhe.homo_add(yr, fhe.homo_mul_i(yi, ctx), ctx)
+    # 6. SlotToCoeff (q_0 / (2 pi S_out) in the shares), b2 rescales, the integer 2^bits
+    z = _rescale_times(apply_stages(z, program.stc, program.stc_rho, ctx, keep), b2, S_in * 2.0**-bits, ctx)
+    if bits:
+        z = fhe.homo_mul_scalar(z, fhe.encode_scalar(1 << bits, cur_limbs=int(z.state.cur_limbs), scale_degree=0,
+                                                     mode="integer", context=ctx), ctx)
+    # the decryption is now S_in * (encoding of the input slots)
+    z = z.cipher_like(z.cv, state=z.state.replace(scaling_factor=S_in, scale_degree=1))
+    target = int(spec.output_levels) or program.output_limbs
+    if int(z.state.cur_limbs) > target:
+        z = fhe.align_to(z, z.state.replace(cur_limbs=target), ctx)
+    return z
+
+
+def _times_integer(ct: Cipher, value: int, ctx: CKKSContext) -> Cipher:
+    enc = fhe.encode_scalar(int(value), cur_limbs=int(ct.state.cur_limbs), scale_degree=0, mode="integer",
+                            context=ctx)
+    return fhe.homo_mul_scalar(ct, enc, ctx)
+
+
+def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *,
+                              iterations: int = 2, precision_bits: int = 12) -> Cipher:
+    """One bootstrap, or the two-pass correction of llama3fhe/operators/nonlinear/bootstrap.py:
+    626-720: first = BTS(x); the scaled error 2^p (first - x) at x's level is bootstrapped too and
+    subtracted from 2^p first, then 2^-p multiplies the result back (encoded at the prime the
+    rescale drops, so the scale is the input's exactly).  The second pass's own error is divided
+    by 2^p.  A ValueError in the second pass (too few levels) returns the first result, as the
+    reference does."""
+
+    ctx = context
+    iterations = int(iterations)
+    if iterations not in (1, 2):
+        raise ValueError("bootstrap iterations must be one or two")
+    first = bootstrap(cipher, ctx, program)
+    if iterations == 1 or int(first.state.cur_limbs) <= int(cipher.state.cur_limbs):
+        return first
+    p = int(precision_bits)
+    try:
+        scale = 1 << max(p, 0)
+        first_scaled = _times_integer(first, scale, ctx) if p > 0 else first
+        first_down = fhe.align_to(first_scaled, cipher.state, ctx)
+        orig_scaled = _times_integer(cipher, scale, ctx) if p > 0 else cipher
+        error = bootstrap(fhe.homo_sub(first_down, orig_scaled, ctx), ctx, program)
+        corrected = fhe.homo_sub(fhe.align_to(first_scaled, error.state, ctx), error, ctx)
+        if p <= 0:
+            return corrected
+        limbs = int(corrected.state.cur_limbs)
+        back = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
+                                 scaling_factor=float(ctx.rescale_divisor_at(limbs)) * 2.0**-p, context=ctx)
+        out = fhe.rescale(fhe.homo_mul_scalar(corrected, back, ctx), ctx)
+        return out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(cipher.state.scaling_factor)))
+    except ValueError:
+        return first

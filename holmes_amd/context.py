@@ -443,6 +443,21 @@ class CKKSContext:
                   "hck_moddown")
         return out
 
+    def modraise(self, x: torch.Tensor, to_limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
+        """Lift one-limb polys x[p][0] (modulo q_0, NTT domain) to ``to_limbs`` limbs: the centered
+        coefficients of limb 0 reduced modulo every q_i (the first step of a bootstrap)."""
+
+        self._check_poly(x, 1, self.N)
+        to_limbs = int(to_limbs)
+        P = int(x.shape[0])
+        out = self.empty(P, to_limbs, self.N) if out is None else out
+        self._check_poly(out, to_limbs, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_modraise_workspace_bytes(self._h, to_limbs, P))
+        nat.check(L.hck_modraise(self._h, to_limbs, P, x.data_ptr(), _bstride(x), out.data_ptr(), _bstride(out),
+                                 ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_modraise")
+        return out
+
     def rescale_raw(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
         self._check_poly(x, limbs, self.N)
         if limbs < 2:

@@ -182,6 +182,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->h_moddown.assign((size_t)(num_q + 1), hck::ConvConsts{});
   c->h_level.assign((size_t)(num_q + 1), hck::LevelConsts{});
   c->h_rescale.assign((size_t)(num_q + 1), hck::ConvConsts{});
+  c->h_raise.assign((size_t)(num_q + 1), hck::ConvConsts{});
   for (int ell = 1; ell <= num_q; ++ell) {
     const int beta = (ell + alpha - 1) / alpha;
     for (int j = 0; j < beta; ++j) {
@@ -203,6 +204,10 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       std::vector<int> rsrc{ell - 1}, rdst, rslot;
       for (int i = 0; i < ell - 1; ++i) { rdst.push_back(i); rslot.push_back(i); }
       fill_conv(c->h_rescale[ell], P, rsrc, rdst, rslot, ninv_u, ninv_w1_u);
+      // ModRaise to ell limbs: limb 0 is the one source, limbs 1 .. ell - 1 the targets
+      std::vector<int> usrc{0}, udst, uslot;
+      for (int i = 1; i < ell; ++i) { udst.push_back(i); uslot.push_back(i - 1); }
+      fill_conv(c->h_raise[ell], P, usrc, udst, uslot, ninv_u, ninv_w1_u);
     }
     hck::LevelConsts& lc = c->h_level[ell];
     for (int i = 0; i < ell; ++i) {
@@ -214,7 +219,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   }
 
   // one device block: [p | pinv | fwd | inv | ninv | ninv_w1 | zeta4 | pmodq | modup | moddown | level |
-  // rescale | primes | encoder roots]
+  // rescale | raise | primes | encoder roots]
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   size_t off = 0;
   const size_t o_p = off; off = align(off + np * sizeof(double));
@@ -229,6 +234,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   const size_t o_md = off; off = align(off + c->h_moddown.size() * sizeof(hck::ConvConsts));
   const size_t o_lv = off; off = align(off + c->h_level.size() * sizeof(hck::LevelConsts));
   const size_t o_rs = off; off = align(off + c->h_rescale.size() * sizeof(hck::ConvConsts));
+  const size_t o_ra = off; off = align(off + c->h_raise.size() * sizeof(hck::ConvConsts));
   const size_t o_pu = off; off = align(off + np * sizeof(u64));
   const size_t o_etr = off; off = align(off + nslots * sizeof(double));
   const size_t o_eti = off; off = align(off + nslots * sizeof(double));
@@ -249,6 +255,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       {o_md, c->h_moddown.data(), c->h_moddown.size() * sizeof(hck::ConvConsts)},
       {o_lv, c->h_level.data(), c->h_level.size() * sizeof(hck::LevelConsts)},
       {o_rs, c->h_rescale.data(), c->h_rescale.size() * sizeof(hck::ConvConsts)},
+      {o_ra, c->h_raise.data(), c->h_raise.size() * sizeof(hck::ConvConsts)},
       {o_pu, P.data(), np * sizeof(u64)},
       {o_etr, etr.data(), nslots * sizeof(double)},
       {o_eti, eti.data(), nslots * sizeof(double)},
@@ -271,6 +278,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->d_moddown = (hck::ConvConsts*)(base + o_md);
   c->d_level = (hck::LevelConsts*)(base + o_lv);
   c->d_rescale = (hck::ConvConsts*)(base + o_rs);
+  c->d_raise = (hck::ConvConsts*)(base + o_ra);
   c->d_primes_u64 = (const u64*)(base + o_pu);
   c->d_enc_twr = (const double*)(base + o_etr);
   c->d_enc_twi = (const double*)(base + o_eti);

@@ -56,11 +56,12 @@ struct hck_context {
   hck::ConvConsts* d_modup = nullptr; // [(L + 1) * beta_max]: index ell * beta_max + digit
   hck::ConvConsts* d_moddown = nullptr; // [L + 1]
   hck::ConvConsts* d_rescale = nullptr; // [L + 1]: level ell converts limb ell - 1 to limbs 0 .. ell - 2
+  hck::ConvConsts* d_raise = nullptr;   // [L + 1]: target count t converts limb 0 to limbs 1 .. t - 1
   hck::LevelConsts* d_level = nullptr;  // [L + 1]
   const uint64_t* d_primes_u64 = nullptr; // [np]
   const double* d_enc_twr = nullptr;      // [N/2]: special-IFFT roots, stage h at [h-1, 2h-1)
   const double* d_enc_twi = nullptr;
-  std::vector<hck::ConvConsts> h_modup, h_moddown, h_rescale;
+  std::vector<hck::ConvConsts> h_modup, h_moddown, h_rescale, h_raise;
   std::vector<hck::LevelConsts> h_level;
   int beta_max;
 };
@@ -103,6 +104,11 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
 size_t rescale_bytes(const hck_context* c, int ell, int polys);
 int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                   long long out_stride, char* ws, hipStream_t s);
+// ModRaise of polys from one limb (q_0) to `to` limbs: the centered lift of limb 0's coefficients,
+// reduced modulo q_1 .. q_{to-1} and transformed; limb 0 is copied.  Workspace: polys * to limbs.
+size_t modraise_bytes(const hck_context* c, int to, int polys);
+int modraise_fused(const hck_context* c, int to, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                   long long out_stride, char* ws, hipStream_t s);
 
 // MI355X deals consecutive workgroups to its 8 XCDs (each with its own L2) round-robin.
 constexpr int kXcds = 8;

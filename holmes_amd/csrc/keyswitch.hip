@@ -135,3 +135,20 @@ extern "C" int hck_rescale(const hck_context* ctx, int level_limbs, int polys, c
   return hck::rescale_fused(ctx, level_limbs, polys, in, in_stride, out, out_stride, (char*)workspace,
                             (hipStream_t)stream);
 }
+
+extern "C" size_t hck_modraise_workspace_bytes(const hck_context* ctx, int to_limbs, int polys) {
+  if (!ctx || to_limbs < 2 || to_limbs > ctx->L || polys < 0) return 0;
+  return hck::modraise_bytes(ctx, to_limbs, polys);
+}
+
+extern "C" int hck_modraise(const hck_context* ctx, int to_limbs, int polys, const uint64_t* in, int64_t in_stride,
+                            uint64_t* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!ctx || !in || !out || polys < 0 || polys > 65535) return HCK_ERR_ARG;
+  if (to_limbs < 2 || to_limbs > ctx->L) return HCK_ERR_ARG;
+  if (polys > 1 && (in_stride < hck::kN || out_stride < (int64_t)to_limbs * hck::kN)) return HCK_ERR_ARG;
+  if (in == out) return HCK_ERR_ARG;
+  if (polys == 0) return HCK_OK;
+  if (!workspace || workspace_bytes < hck::modraise_bytes(ctx, to_limbs, polys)) return HCK_ERR_WORKSPACE;
+  return hck::modraise_fused(ctx, to_limbs, polys, in, in_stride, out, out_stride, (char*)workspace,
+                             (hipStream_t)stream);
+}

@@ -770,6 +770,26 @@ __global__ __launch_bounds__(kT) void k_ks_rows_finish(const double* __restrict_
   for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(a[k] - x[k], pi_, p), p, pinv));  // |a - x| <= 4.9 p
 }
 
+// ----------------------------------------------------------------- NTT rows + canonical store
+// Poly p = blockIdx.x, limb i = blockIdx.z of an ell-limb workspace poly: out limb (limb0 + i) of
+// poly p = canonical NTT rows pass of T4[p][i] under prime prime0 + i.
+__global__ __launch_bounds__(kT) void k_ks_rows_store(const double* __restrict__ t4, int ell,
+                                                      uint64_t* __restrict__ out, long long out_pstride, int limb0,
+                                                      int prime0, DevTables T) {
+  __shared__ double S[kRowLds];
+  const int i = blockIdx.z, rg = blockIdx.y, pl = blockIdx.x;
+  const int pi = prime0 + i;
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  const double* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
+  const long long na = nat_a(rg);
+  double x[16];
+  load_t(x, t4 + ((long long)pl * ell + i) * kN, rg);
+  rows_fwd_t(x, rg, S, tw, p, pinv);
+  uint64_t* o = out + (long long)pl * out_pstride + (long long)(limb0 + i) * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(x[k], p, pinv));
+}
+
 }  // namespace
 
 // Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)], ACCP [2 K].
@@ -885,6 +905,32 @@ int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, 
                                                       (c->d_level + ell)->qlast_inv, c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
+}
+
+size_t modraise_bytes(const hck_context* c, int to, int polys) { return (size_t)polys * kN * 8 * (size_t)to; }
+
+// ModRaise on the conversion kernels: INTT rows of limb 0, the cols kernel (INTT cols, centered
+// lift, spread to q_1 .. q_{to-1}, NTT cols), NTT rows with a canonical store; limb 0 itself is
+// unchanged (the lift is congruent to it modulo q_0) and copied.
+int modraise_fused(const hck_context* c, int to, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                   long long out_stride, char* ws, hipStream_t s) {
+  const long long n = kN;
+  const int nt = to - 1;
+  double* tl = (double*)ws;                       // [polys][1] workspace layout
+  double* t4 = tl + (long long)polys * n;         // [polys][to - 1] workspace layout
+  k_ks_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, 1u, 0, 0, tl, 1,
+                                                                                polys, c->dev);
+  HCK_CHECK_LAUNCH();
+  auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  conv<<<dim3(128, 1, polys), kT, 0, s>>>(tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_raise + to, 0, c->dev);
+  HCK_CHECK_LAUNCH();
+  k_ks_rows_store<<<dim3(polys, 16, nt), kT, 0, s>>>(t4, nt, out, out_stride, 1, 1, c->dev);
+  HCK_CHECK_LAUNCH();
+  // a single poly may come with any item stride (0 included): its pitch is then the row itself
+  const size_t row = (size_t)n * 8;
+  const size_t dp = polys > 1 ? (size_t)out_stride * 8 : row, sp = polys > 1 ? (size_t)in_stride * 8 : row;
+  hipError_t e = hipMemcpy2DAsync(out, dp, in, sp, row, polys, hipMemcpyDeviceToDevice, s);
+  return e == hipSuccess ? HCK_OK : (int)e;
 }
 
 }  // namespace hck

@@ -127,6 +127,14 @@ int hck_rescale(const hck_context* ctx, int level_limbs, int polys, const uint64
                 int64_t in_stride, uint64_t* out, int64_t out_stride, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* ModRaise (the first step of a bootstrap, easyfhe.bs.openfhe bootstrap with
+ * mode "modraise_first", llama3fhe/operators/nonlinear/bootstrap.py:119-160,626-640): `polys`
+ * one-limb polynomials (limb 0 modulo q_0, NTT domain, at in + p * in_stride) lifted to to_limbs
+ * limbs: out limb i = NTT_{q_i}(centered coefficients of limb 0 reduced modulo q_i). */
+size_t hck_modraise_workspace_bytes(const hck_context* ctx, int to_limbs, int polys);
+int hck_modraise(const hck_context* ctx, int to_limbs, int polys, const uint64_t* in, int64_t in_stride,
+                 uint64_t* out, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 /* Elementwise limb ops on [polys][limbs][N] (limb l uses prime prime_idx[l]).
  * HCK_OP_ADD/SUB/MUL: out = a op b; NEG: out = -a; MUL_SCALAR: out = a * scalar[l];
  * ADD_SCALAR: out = a + scalar[l] (a constant polynomial added in the NTT domain);

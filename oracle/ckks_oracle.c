@@ -513,6 +513,26 @@ void or_weighted_sum(const or_ctx* c, int limbs, int n, int groups, const u64* x
     }
 }
 
+/* ModRaise of one NTT-domain limb modulo q_0 to `to` limbs: the centered lift c in (-q_0/2, q_0/2] of
+ * its coefficients, reduced modulo q_i and transformed (the first step of a CKKS bootstrap; the
+ * reference drives EasyFHE's, llama3fhe/operators/nonlinear/bootstrap.py:626-640). */
+void or_modraise(const or_ctx* c, int to, const u64* in, u64* out) {
+  const u64 q0 = c->primes[0];
+  u64* coef = (u64*)malloc(c->n * sizeof(u64));
+  memcpy(coef, in, c->n * sizeof(u64));
+  ntt_i(c, coef, 0);
+  for (int i = 0; i < to; ++i) {
+    const u64 q = c->primes[i];
+    u64* o = out + (u64)i * c->n;
+    for (u64 j = 0; j < c->n; ++j) {
+      const u64 v = coef[j];
+      o[j] = v > q0 / 2 ? (q - (q0 - v) % q) % q : v % q;  /* v - q0 when v > q0 / 2 */
+    }
+    ntt_f(c, o, i);
+  }
+  free(coef);
+}
+
 int or_num_threads(void) {
 #ifdef _OPENMP
   return omp_get_max_threads();

@@ -64,6 +64,7 @@ def lib():
         "or_mul_limbs": (None, [_vp, i, _u64p, _u64p, _u64p]),
         "or_tensor": (None, [_vp, i, _u64p, _u64p, _u64p, _u64p, _u64p, _u64p, _u64p]),
         "or_weighted_sum": (None, [_vp, i, i, i, _u64p, _u64p, _u64p]),
+        "or_modraise": (None, [_vp, i, _u64p, _u64p]),
         "or_num_threads": (i, []),
         "or_encode_twiddles": (None, [i, _f64p, _f64p]),
         "or_special_ifft": (None, [i, _f64p, _f64p, _f64p, _f64p]),
@@ -267,6 +268,14 @@ class OracleContext:
     def mul_relin(self, limbs: int, a0, a1, b0, b1, rlk: np.ndarray):
         d0, d1, d2 = self.tensor(limbs, a0, a1, b0, b1)
         return self.relinearize(limbs, d0, d1, d2, rlk)
+
+    def modraise(self, to: int, x: np.ndarray) -> np.ndarray:
+        """One NTT-domain limb modulo q_0 lifted (centered) to ``to`` limbs."""
+
+        x = np.ascontiguousarray(np.asarray(x).reshape(-1)[: self.n], dtype=np.uint64)
+        out = np.zeros((to, self.n), dtype=np.uint64)
+        lib().or_modraise(self._h, int(to), _p(x), _p(out))
+        return out
 
     def weighted_sum(self, limbs: int, x: np.ndarray, w: np.ndarray) -> np.ndarray:
         """out[g] = sum_j w[g][j][l] x[j][l]: x [n][limbs][N], w [groups][n][limbs]."""

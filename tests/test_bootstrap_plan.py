@@ -1,0 +1,228 @@
+"""CPU pins of the bootstrap's host plan (no GPU).
+
+* The butterfly layers factor the decoder: U0 w = L_1 ... L_logn (bit-reversed w), U0 the
+  slot map of the host decoder (holmes_amd.encoding.decode, an FFT evaluation at the 5^j-th
+  roots), and the inverse layers undo it; a wrong twiddle, block size or sign fails.
+* Merged stages equal their layers applied one by one, and the BSGS rows (pre-rotated diagonals,
+  then giant rotations) equal the merged stage, for both directions at several budgets.
+* The rotation list of ``requirements`` holds every baby and giant rotation the stages use.
+* The Chebyshev division identity, the canonical-scale recursion, and the EvalMod interpolant
+  against sin(2 pi t) through the double angles.
+* An end-to-end numeric run of the whole pipeline on slot values (no encryption): coefficients
+  with a q_0 I overflow, CoeffToSlot, the real / imaginary split, EvalMod, SlotToCoeff, the
+  integer 2^bits, with the program's own constants; it must return the input slots.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+from holmes_amd import bootstrap as B
+from holmes_amd import encoding
+
+
+def _apply(diags, x):
+    n = x.shape[-1]
+    out = np.zeros_like(x)
+    for d, v in diags.items():
+        out += v * np.roll(x, -(d % n))
+    return out
+
+
+def _rot(x, r):
+    return np.roll(x, -(int(r) % x.shape[-1]))
+
+
+def _bsgs(st, x):
+    n = x.shape[-1]
+    rows = B.stage_rows(st, n)
+    babies = [_rot(x, k1 * st.h_min) for k1 in range(st.n1)]
+    out = np.zeros_like(x)
+    for gi, k2 in enumerate(st.giants):
+        inner = sum(rows[gi * st.n1 + k1] * babies[k1] for k1 in range(st.n1))
+        out += _rot(inner, k2 * st.n1 * st.h_min)
+    return out
+
+
+def _slots_of(coeffs, log_n):
+    return encoding.decode(coeffs, 1.0, log_n)
+
+
+@pytest.mark.parametrize("log_n", [4, 6, 9])
+def test_butterflies_factor_the_decoder(log_n):
+    rng = np.random.default_rng(log_n)
+    N = 1 << log_n
+    n = N // 2
+    c = rng.normal(size=N)
+    w = c[:n] + 1j * c[n:]
+    want = _slots_of(c, log_n)
+    fwd = B.special_fft_layers(log_n - 1)
+    y = B.bit_reverse_order(w)
+    for t in range(log_n - 1, 0, -1):     # L_logn first, L_1 last
+        y = _apply(fwd[t - 1], y)
+    assert np.allclose(y, want, atol=1e-9 * n)
+    inv = B.special_fft_layers(log_n - 1, inverse=True)
+    z = want.copy()
+    for t in range(1, log_n):             # L_1^-1 first
+        z = _apply(inv[t - 1], z)
+    assert np.allclose(z, B.bit_reverse_order(w), atol=1e-9)
+
+
+def test_butterflies_reject_a_wrong_twiddle():
+    # the pin above is sensitive: conjugating one layer's twiddles breaks the factorisation
+    log_n = 6
+    rng = np.random.default_rng(1)
+    c = rng.normal(size=1 << log_n)
+    n = (1 << log_n) // 2
+    w = c[:n] + 1j * c[n:]
+    fwd = B.special_fft_layers(log_n - 1)
+    bad = {d: np.conj(v) for d, v in fwd[2].items()}
+    y = B.bit_reverse_order(w)
+    for t in range(log_n - 1, 0, -1):
+        y = _apply(bad if t == 3 else fwd[t - 1], y)
+    assert not np.allclose(y, _slots_of(c, log_n), atol=1e-6)
+
+
+@pytest.mark.parametrize("budget", [1, 2, 3, 4])
+@pytest.mark.parametrize("inverse", [True, False])
+def test_merged_stages_and_bsgs_rows(budget, inverse):
+    log_slots = 8
+    n = 1 << log_slots
+    rng = np.random.default_rng(budget + 10 * inverse)
+    x = rng.normal(size=n) + 1j * rng.normal(size=n)
+    layers = B.special_fft_layers(log_slots, inverse=inverse)
+    stages = B.plan_stages(log_slots, budget, inverse, 0.75)
+    seq = x.copy()
+    got = x.copy()
+    order = []
+    for i, st in enumerate(stages):
+        for t in st.layers:
+            seq = _apply(layers[t - 1], seq)
+            order.append(t)
+        if i == 0:
+            seq = seq * 0.75
+        assert np.allclose(_apply({(k * st.h_min) % n: v for k, v in st.diags.items()}, got), seq, atol=1e-9)
+        got = _bsgs(st, got)
+        assert np.allclose(got, seq, atol=1e-9)
+        _, _, kmax = B._bsgs_shape(st.layers, n)
+        assert max(abs(k) for k in st.diags) <= kmax
+    assert sorted(order) == list(range(1, log_slots + 1))
+    assert order == (list(range(1, log_slots + 1)) if inverse else list(range(log_slots, 0, -1)))
+
+
+def test_requirements_cover_every_stage_rotation():
+    spec = B.BootstrapSpec(log_slots=9, level_budget=(3, 2), cheb_degree=32)
+    req = B.requirements(spec, 10)
+    n = 1 << 9
+    rots = set(req.rotations)
+    assert 4 * n - 1 in rots  # conjugation
+    for st in B.plan_stages(9, 3, True, 1.0) + B.plan_stages(9, 2, False, 1.0):
+        for k1 in range(1, st.n1):
+            assert (k1 * st.h_min) % n in rots
+        for k2 in st.giants:
+            if k2:
+                assert (k2 * st.n1 * st.h_min) % n in rots
+    assert req.depth == 3 + 2 + B.evalmod_levels(spec, 40, [2] * 41)
+
+
+def test_full_slot_spec_is_required():
+    with pytest.raises(ValueError):
+        B.requirements(B.BootstrapSpec(log_slots=14), 16)
+    with pytest.raises(ValueError):
+        B.requirements(B.BootstrapSpec(mode="slots_first"), 16)
+
+
+def test_chebyshev_division_identity():
+    rng = np.random.default_rng(3)
+    C = np.polynomial.chebyshev
+    for M, ln in ((8, 13), (16, 32), (32, 49)):
+        c = rng.normal(size=ln)
+        q, r = B.chebyshev_divide(c, M)
+        u = np.linspace(-1, 1, 101)
+        TM = C.chebval(u, np.eye(M + 1)[M])
+        assert np.allclose(C.chebval(u, c), C.chebval(u, q) * TM + C.chebval(u, r), atol=1e-12)
+        assert len(r) <= M
+
+
+def test_canonical_scales_close_under_products():
+    primes = [2**50 - 2**26 * k + 1 for k in range(1, 12)]
+    sc = B.canonical_scales(primes, 10, 2.0**50)
+    for l in range(2, 11):
+        assert sc[l - 1] == pytest.approx(sc[l] * sc[l] / primes[l - 1], rel=1e-15)
+    assert abs(math.log2(sc[1]) - 50) < 0.01
+
+
+def test_evalmod_interpolant_gives_sine():
+    spec = B.BootstrapSpec()
+    c = B.evalmod_coefficients(spec)
+    Kp = spec.mod_bound + 1
+    t = np.concatenate([np.linspace(-Kp + 0.5, Kp - 0.5, 4001), np.arange(-spec.mod_bound, spec.mod_bound + 1) + 1e-4])
+    y = np.polynomial.chebyshev.chebval(t / Kp, c)
+    for _ in range(spec.double_angle):
+        y = 2 * y * y - 1
+    assert np.max(np.abs(y - np.sin(2 * np.pi * t))) < 2.0**-30
+
+
+def test_evalmod_levels_match_schedule():
+    spec = B.BootstrapSpec()
+    # baby basis T_1..T_8 (3), giants T_16 (4), T_32 (5), the top product (6), 3 double angles
+    assert B.evalmod_levels(spec, 21, [2] * 30) == 9
+
+
+def _simulate(prog, v, q0, I, S_in, log_n, bits):
+    """The bootstrap on slot values: what the GPU path computes, less the encryption noise."""
+
+    S = prog.nominal_scale
+    m = encoding.encode_real_coeffs(v, S_in * 2.0**-bits, log_n)     # message at one limb
+    M = m + float(q0) * I                                             # after ModRaise
+    z = encoding.decode(M, S, log_n)
+    for st in prog.cts:
+        z = _bsgs(st, z)
+    z = z * prog.cts_rho ** len(prog.cts)
+    R, J = 2 * z.real, 2 * z.imag                                     # x + conj(x), -i (x - conj(x))
+    ys = []
+    for u in (R, J):
+        assert np.max(np.abs(u)) <= 1.0
+        y = np.polynomial.chebyshev.chebval(u, prog.cheb)
+        for _ in range(prog.spec.double_angle):
+            y = 2 * y * y - 1
+        ys.append(y)
+    w = ys[0] + 1j * ys[1]
+    for st in prog.stc:
+        w = _bsgs(st, w)
+    w = w * prog.stc_rho ** len(prog.stc) * float(1 << bits)
+    return w * prog.evalmod_out_scale / S_in                          # decryption / S_in
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_numeric_pipeline_returns_the_input(seed):
+    log_n = 10
+    spec = B.BootstrapSpec(log_slots=log_n - 1, level_budget=(3, 3))
+    rng = np.random.default_rng(seed)
+    primes = [2**50 - 2**27 * k + 1 for k in range(1, 31)]
+    prog = B.plan_program(spec, primes, 2.0**50, 30)
+    n = 1 << (log_n - 1)
+    v = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)) / math.sqrt(2)
+    I = rng.integers(-spec.mod_bound + 1, spec.mod_bound, 1 << log_n).astype(np.float64)
+    S_in = 2.0**50
+    bits = int(round(math.log2(S_in / primes[0]))) + spec.message_ratio_bits
+    got = _simulate(prog, v, primes[0], I, S_in, log_n, bits)
+    err = np.max(np.abs(got - v))
+    assert err < 2.0**-20, err
+
+
+def test_numeric_pipeline_catches_a_wrong_constant():
+    log_n = 8
+    spec = B.BootstrapSpec(log_slots=log_n - 1, level_budget=(2, 2))
+    primes = [2**50 - 2**27 * k + 1 for k in range(1, 31)]
+    prog = B.plan_program(spec, primes, 2.0**50, 30)
+    rng = np.random.default_rng(5)
+    n = 1 << (log_n - 1)
+    v = rng.uniform(-1, 1, n) + 0j
+    I = rng.integers(-5, 6, 1 << log_n).astype(np.float64)
+    good = _simulate(prog, v, primes[0], I, 2.0**50, log_n, 12)
+    assert np.max(np.abs(good - v)) < 2.0**-20
+    prog.stc[0].diags = {k: d * (1 + 2.0**-10) for k, d in prog.stc[0].diags.items()}
+    bad = _simulate(prog, v, primes[0], I, 2.0**50, log_n, 12)
+    assert np.max(np.abs(bad - v)) > 2.0**-12

@@ -270,3 +270,13 @@ def test_batched_keyswitch_sixteen_keys(env):
     wb, wa = orc.keyswitch_batch(ell, d, keys_orc)
     assert np.array_equal(_host(ob), wb)
     assert np.array_equal(_host(oa), wa)
+
+
+@pytest.mark.parametrize("to", [24, 2])
+def test_modraise(env, to):
+    _, _, ctx, orc = env
+    rng = np.random.default_rng(60 + to)
+    x = _rand(ctx, rng, 3, 1)
+    out = _host(ctx.modraise(_dev(x), to))
+    for b in range(3):
+        assert np.array_equal(out[b], orc.modraise(to, x[b]))

@@ -204,3 +204,20 @@ def test_bsgs_mac_matches_big_integer_sum():
                 for j in range(ctx.n):
                     want = sum(int(pt[g * nb + b][l][j]) * int(baby[b][c][l][j]) for b in range(nb)) % q
                     assert int(res[c][g][l][j]) == want
+
+
+@pytest.mark.parametrize("to", [2, 5])
+def test_modraise_is_the_centered_lift(to):
+    # every output limb holds the centered representative of limb 0's coefficient (|x| < q_0 / 2)
+    # reduced modulo its own prime; limb 0 is unchanged
+    ctx = _ctx(4, 5, 1, 2)
+    rng = np.random.default_rng(200 + to)
+    x = _rand_ntt(ctx, rng, 1)
+    out = ctx.modraise(to, x[0])
+    assert np.array_equal(out[0], x[0])
+    c0 = ctx.ntt_inv_limbs(x, [0])[0]
+    co = ctx.ntt_inv_limbs(out, list(range(to)))
+    q0 = ctx.primes[0]
+    for t in range(ctx.n):
+        v = centered(int(c0[t]), q0)
+        assert [int(co[i][t]) for i in range(to)] == [v % ctx.primes[i] for i in range(to)]
