@@ -19,6 +19,10 @@ right-multiplied by a seeded randomized Hadamard) applied by the BSGS diagonal m
 ciphertexts at 20 limbs, scale 2^40.  A step is one whole projection, pack + encode of every
 diagonal included (the reference encodes per chunk per call,
 llama3fhe/operators/linear/operator.py:296-312).  Its line reports seconds per projection.
+
+``--workload bootstrap``: one full-slot bootstrap (N = 2^16, 24 x 50-bit primes, dnum 3, scale
+2^50, sparse ternary secret h = 192, level budget (3, 3)) of a ciphertext at 3 limbs; its line
+reports ms per bootstrap and the precision of the refreshed slots.
 """
 
 from __future__ import annotations
@@ -62,10 +66,11 @@ def main() -> int:
     ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
                     help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
                          "(both are hoist strategies of the reference's LinearOperatorConfig)")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "mul", "stream"), default="c2",
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "mul", "bootstrap", "stream"), default="c2",
                     help="c2: batched key switch (headline); c1: one rotation + rescale (latency); "
                          "c3: q_proj BSGS projection; mul: 16 ciphertext products with "
-                         "relinearisation and rescale at 24 limbs; stream: the "
+                         "relinearisation and rescale at 24 limbs; bootstrap: one full-slot bootstrap "
+                         "at 24 limbs; stream: the "
                          "residue negation kernel over 16 x 24 limbs, a plain read-once/write-once "
                          "stream of known size (HBM ceiling and counter calibration)")
     args = ap.parse_args()
@@ -92,6 +97,8 @@ def main() -> int:
         return run_stream(args)
     if args.workload == "mul":
         return run_mul(args)
+    if args.workload == "bootstrap":
+        return run_bootstrap(args)
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
@@ -338,6 +345,163 @@ def run_mul(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "tensor + 5 key-switch kernels + rescale per step", "ms_per_launch": round(ms, 4)},
+        "cpu_baseline": cpu}), flush=True)
+    return 0
+
+
+# bootstrap: the bytes of one refresh are the HBM floors of the library calls it makes, summed
+# from the call log of one run (limb = N x 8 bytes): key switch per item d + add + out (b, a) +
+# its key 2 beta (limbs + K); product with relinearisation 4 in + 2 out per item + the shared key;
+# MAC babies + plaintext rows + partial sums; rescale / ModRaise / weighted sums / elementwise
+# ops and automorphisms their inputs and outputs.
+class _CallLog:
+    NAMES = ("keyswitch", "rotate_raw", "mul_relin_raw", "relinearize_raw", "bsgs_mac", "rescale_raw",
+             "modraise", "weighted_sum", "poly_op", "automorphism")
+
+    def __init__(self, ctx):
+        self.ctx = ctx
+        self.calls = []
+
+    def __enter__(self):
+        for name in self.NAMES:
+            orig = getattr(self.ctx, name)
+
+            def wrap(*a, _orig=orig, _name=name, **k):
+                self.calls.append((_name, a, k))
+                return _orig(*a, **k)
+
+            setattr(self.ctx, name, wrap)
+        return self
+
+    def __exit__(self, *exc):
+        for name in self.NAMES:
+            delattr(self.ctx, name)
+
+    def limbs_bytes(self):
+        """(algorithmic limbs moved, [(kind, items, limbs)] of the key switches)."""
+
+        ctx = self.ctx
+        K = ctx.K
+        beta = lambda l: (l + ctx.alpha - 1) // ctx.alpha  # noqa: E731
+        total = 0
+        ks = []
+        for name, a, k in self.calls:
+            if name == "keyswitch":
+                d, l = a[0], int(a[1])
+                B = int(d.shape[0])
+                total += B * (l * (3 + (k.get("add") is not None)) + 2 * beta(l) * (l + K))
+                ks.append(("rotation", B, l))
+            elif name == "rotate_raw":
+                l, B = int(a[2]), int(a[0].shape[0])
+                total += B * (l * (4 + 2 * (k.get("acc") is not None)) + 2 * beta(l) * (l + K))
+                ks.append(("rotation", B, l))
+            elif name == "mul_relin_raw":
+                l, B = int(a[4]), int(a[0].shape[0])
+                total += B * 6 * l + 2 * beta(l) * (l + K)
+                ks.append(("product", B, l))
+            elif name == "relinearize_raw":
+                l, B = int(a[3]), int(a[0].shape[0])
+                total += B * 5 * l + 2 * beta(l) * (l + K)
+                ks.append(("product", B, l))
+            elif name == "bsgs_mac":
+                b0, pts, l, G = a[0], a[2], int(a[3]), int(a[4])
+                ni = int(b0[0].shape[0])
+                total += len(b0) * ni * 2 * l + int(pts.shape[0]) * l + 2 * G * ni * l
+            elif name == "rescale_raw":
+                x, l = a[0], int(a[1])
+                total += int(x.shape[0]) * (2 * l - 1)
+            elif name == "modraise":
+                total += int(a[0].shape[0]) * (1 + int(a[1]))
+            elif name == "weighted_sum":
+                x, w, l = a[0], a[1], int(a[2])
+                total += (int(x.shape[0]) + int(w.shape[0])) * l
+            elif name == "poly_op":
+                out, l = a[1], len(k["prime_idx"])
+                total += int(out.shape[0]) * l * (3 if len(a) > 3 and a[3] is not None else 2)
+            elif name == "automorphism":
+                total += int(a[0].shape[0]) * 2 * int(a[2])
+        return total, ks
+
+
+def run_bootstrap(args) -> int:
+    """Full-slot bootstrap of one ciphertext at 3 limbs (holmes_amd.bootstrap, the
+    easyfhe.bs.openfhe surface): ModRaise, CoeffToSlot (3 merged BSGS stages), EvalMod (degree-48
+    Chebyshev + 3 double angles on the real and imaginary parts), SlotToCoeff (3 stages)."""
+
+    import math
+
+    import torch
+
+    from holmes_amd import bootstrap as B
+    from holmes_amd import fhe
+
+    seed = 20261230
+    spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, scale_bits=50,
+                               secret_key_dist="SPARSE_TERNARY", hamming_weight=192, seed=seed)
+    t0 = time.perf_counter()
+    client, ctx = fhe.generate_client_context(spec)
+    bspec = B.BootstrapSpec(log_slots=ctx.logN - 1, level_budget=(3, 3))
+    req = B.requirements(bspec, ctx.logN)
+    client.generate_rotation_keys(req.rotations)
+    prog = B.generate(ctx, bspec)
+    rng = np.random.default_rng(seed)
+    v = (rng.uniform(-1, 1, ctx.max_slots) + 1j * rng.uniform(-1, 1, ctx.max_slots)) / math.sqrt(2)
+    ct = client.encrypt(v, cur_limbs=3)
+    _log(f"context, {len(req.rotations)} keys, program: {time.perf_counter() - t0:.1f} s")
+    out = B.bootstrap(ct, ctx, prog)  # encodes and caches the stage diagonals
+    with _CallLog(ctx) as log:
+        out = B.bootstrap(ct, ctx, prog)
+    limbs_moved, ks = log.limbs_bytes()
+    bs_bytes = limbs_moved * ctx.N * 8
+    for _ in range(args.warmup):
+        out = B.bootstrap(ct, ctx, prog)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    ev0.record(stream)
+    for _ in range(args.steps):
+        out = B.bootstrap(ct, ctx, prog)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_wall = (time.perf_counter() - w0) * 1e3 / args.steps
+    ms = ev0.elapsed_time(ev1) / args.steps
+    err = float(np.max(np.abs(client.decrypt(out) - v)))
+    ks_items = sum(b for _, b, _ in ks)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+        g = ctx.galois_element(1)
+        okey = orc.make_ksk(*client.key_inputs(g))
+        rlk = orc.make_ksk(*client.relin_key_inputs())
+        x = [np.stack([rng.integers(0, ctx.primes[i], ctx.N, dtype=np.uint64) for i in range(LIMBS)])
+             for _ in range(4)]
+        t = time.perf_counter()
+        orc.rotate(LIMBS, g, x[0], x[1], okey)
+        t_rot = time.perf_counter() - t
+        t = time.perf_counter()
+        orc.mul_relin(21, x[0][:21], x[1][:21], x[2][:21], x[3][:21], rlk)
+        t_mul = time.perf_counter() - t
+        total = sum(b * (t_rot * l / LIMBS if kind == "rotation" else t_mul * l / 21) for kind, b, l in ks)
+        cpu = {"value": round(total * 1e3, 1), "unit": "ms", "cores": int(O.num_threads()), "kind": "port",
+               "sample": f"extrapolated from the key switches alone: one rotation at 24 limbs ({t_rot:.3f} s) "
+                         f"and one product + relinearisation at 21 limbs ({t_mul:.3f} s), scaled by limbs, "
+                         f"over the {ks_items} key-switched items of one bootstrap"}
+    achieved = bs_bytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "ms per full-slot CKKS bootstrap (N=2^16, 24 x 50-bit limbs, dnum 3)", "value": round(ms_wall, 3),
+        "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_wall, 3),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+        "config": {"workload": "bootstrap of 1 ct at 3 limbs -> %d limbs; level budget (3, 3), EvalMod deg %d + "
+                               "%d double angles, message ratio 2^-%d, sparse ternary h=192"
+                               % (prog.output_limbs, bspec.cheb_degree, bspec.double_angle, bspec.message_ratio_bits),
+                   "max_error_bits": round(-math.log2(err), 2), "key_switched_items": ks_items,
+                   "algorithmic_bytes_per_step": bs_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole bootstrap (key switches, MACs, rescales, elementwise)", "ms_per_launch": round(ms, 3)},
         "cpu_baseline": cpu}), flush=True)
     return 0
 

@@ -28,6 +28,7 @@ _u32 = ctypes.c_uint32
 _sz = ctypes.c_size_t
 _ip = ctypes.POINTER(ctypes.c_int)
 _u64p = ctypes.POINTER(ctypes.c_uint64)
+_u32p = ctypes.POINTER(ctypes.c_uint32)
 
 SIGNATURES = {
     "hck_context_create": (_i, [ctypes.POINTER(_vp), _i, _i, _i, _i, _u64p]),
@@ -51,6 +52,10 @@ SIGNATURES = {
                           _vp]),
     "hck_rotate_ext": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp, _i64,
                             _vp, _sz, _vp]),
+    "hck_rotate_many": (_i, [_vp, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp,
+                             _i64, _vp, _sz, _vp]),
+    "hck_rotate_ext_many": (_i, [_vp, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp,
+                                 _i64, _vp, _sz, _vp]),
     "hck_moddown_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_moddown": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_pack_diagonals": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),
@@ -107,6 +112,11 @@ def int_array(values) -> ctypes.Array:
 def u64_array(values) -> ctypes.Array:
     values = [int(v) for v in values]
     return (ctypes.c_uint64 * max(1, len(values)))(*values)
+
+
+def u32_array(values) -> ctypes.Array:
+    values = [int(v) for v in values]
+    return (ctypes.c_uint32 * max(1, len(values)))(*values)
 
 
 def ptr_array(ptrs) -> ctypes.Array:

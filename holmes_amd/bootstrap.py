@@ -34,6 +34,7 @@ from dataclasses import dataclass, field
 import numpy as np
 import torch
 
+from . import _native as _nat
 from . import fhe
 from .context import Cipher, CKKSContext
 
@@ -387,7 +388,7 @@ class Stage:
     layers: list
     h_min: int
     n1: int
-    giants: list            # giant indices k2, ascending
+    giants: list            # giant indices k2: 0 (when present) first, then ascending
     diags: dict             # k -> slot vector (complex128, length n)
     cache: dict = field(default_factory=dict)  # limbs -> encoded rows [giants * n1][limbs][N]
 
@@ -403,7 +404,7 @@ def make_stage(layers: list[int], all_layers: list[dict], n: int, factor: float 
         if s % h_min or abs(s // h_min) > kmax:
             raise AssertionError("merged diagonal off the stage's grid")
         diags[s // h_min] = v * factor
-    giants = sorted({k // n1 for k in diags})
+    giants = sorted({k // n1 for k in diags}, key=lambda k2: (k2 != 0, k2))  # the unrotated row first
     return Stage(layers=list(layers), h_min=h_min, n1=n1, giants=giants, diags=diags)
 
 
@@ -535,36 +536,47 @@ def _stage_plaintexts(st: Stage, limbs: int, pt_scale: float, ctx: CKKSContext, 
     return pts
 
 
+def _rotate_many(c0: torch.Tensor, c1: torch.Tensor, offsets, limbs: int, ctx: CKKSContext):
+    """Item i of (c0, c1) ([items][limbs][N]; batch stride 0: one input) rotated by offsets[i],
+    each with its own key, in one batched key switch with a Galois element per item."""
+
+    gs = [ctx.galois_element(int(off) % ctx.max_slots) for off in offsets]
+    return ctx.rotate_raw(c0, c1, limbs, gs, [ctx.key_for_galois(g) for g in gs])
+
+
 def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: bool = True) -> Cipher:
-    """One stage on a one-item cipher, without a rescale: baby rotations, the baby-step MAC of
-    every giant row with the diagonals encoded at ``pt_scale``, the giant rotations accumulated in
-    place.  The slots become the stage applied to the slots; the scaling factor is multiplied by
-    ``pt_scale`` (the caller rescales, possibly after further stages: the key-switch noise of a
-    rotation is then small against the still unrescaled message)."""
+    """One stage on a one-item cipher, without a rescale: the baby rotations as one batched key
+    switch, the baby-step MAC of every giant row with the diagonals encoded at ``pt_scale``, the
+    giant rotations as a second batched key switch and their sum.  The slots become the stage
+    applied to the slots; the scaling factor is multiplied by ``pt_scale`` (the caller rescales,
+    possibly after further stages: a rotation's key-switch noise is then small against the still
+    unrescaled message)."""
 
     limbs = int(x.state.cur_limbs)
-    babies = fhe.fast_rotate(x, [k1 * st.h_min for k1 in range(st.n1)], ctx)
-    pts = _stage_plaintexts(st, limbs, pt_scale, ctx, keep)
-    res = ctx.bsgs_mac([babies.cv[0][i:i + 1] for i in range(st.n1)],
-                       [babies.cv[1][i:i + 1] for i in range(st.n1)], pts, limbs, len(st.giants))
-    babies.release()
     n = ctx.max_slots
-    order = sorted(range(len(st.giants)), key=lambda gi: st.giants[gi] != 0)  # the unrotated row first
-    acc0 = acc1 = None
-    for gi in order:
-        k2 = st.giants[gi]
-        c0, c1 = res[0, gi], res[1, gi]
-        if k2 == 0:
-            acc0, acc1 = c0, c1
-            continue
-        g = ctx.galois_element((k2 * st.n1 * st.h_min) % n)
-        key = ctx.key_for_galois(g)
-        if acc0 is None:
-            acc0, acc1 = ctx.rotate_raw(c0, c1, limbs, g, key)
-        else:
-            ctx.rotate_raw(c0, c1, limbs, g, key, out0=acc0, out1=acc1, acc=(acc0, acc1))
+    c0, c1 = x.cv[0][:, :limbs].contiguous(), x.cv[1][:, :limbs].contiguous()
+    nb = st.n1 - 1
+    b0, b1 = _rotate_many(c0.expand(nb, -1, -1), c1.expand(nb, -1, -1),
+                          [k1 * st.h_min for k1 in range(1, st.n1)], limbs, ctx)
+    pts = _stage_plaintexts(st, limbs, pt_scale, ctx, keep)
+    res = ctx.bsgs_mac([c0] + [b0[i:i + 1] for i in range(nb)], [c1] + [b1[i:i + 1] for i in range(nb)],
+                       pts, limbs, len(st.giants))  # [2][G][1][limbs][N]
+    del b0, b1
+    first = 1 if st.giants[0] == 0 else 0
+    rot = st.giants[first:]
+    if not rot:
+        acc = [res[0, 0].clone(), res[1, 0].clone()]
+    else:
+        g0, g1 = _rotate_many(res[0, first:, 0], res[1, first:, 0], [k2 * st.n1 * st.h_min for k2 in rot],
+                              limbs, ctx)
+        ones = torch.ones((1, len(rot), limbs), dtype=torch.uint64, device=ctx.device)
+        acc = [ctx.weighted_sum(g0, ones, limbs), ctx.weighted_sum(g1, ones, limbs)]
+        if first:
+            idx = ctx.q_prime_idx(limbs)
+            for c in range(2):
+                ctx.poly_op(_nat.HCK_OP_ADD, acc[c], acc[c], res[c, 0], prime_idx=idx)
     s = x.state
-    return x.cipher_like([acc0, acc1], batch_size=1,
+    return x.cipher_like(acc, batch_size=1,
                          state=s.replace(scale_degree=int(s.scale_degree) + 1,
                                          scaling_factor=float(s.scaling_factor) * float(pt_scale)))
 

@@ -265,7 +265,9 @@ class CKKSContext:
                    out0: torch.Tensor | None = None, out1: torch.Tensor | None = None,
                    acc: tuple[torch.Tensor, torch.Tensor] | None = None):
         """(sigma(c0) + KS_b(sigma(c1)), KS_a(sigma(c1))), plus ``acc`` = (acc0, acc1) when given.
-        Outputs may be the ``acc`` tensors themselves, never c0 / c1."""
+        Outputs may be the ``acc`` tensors themselves, never c0 / c1.  ``galois`` is one element
+        for every item or a sequence of one per item (then one key per item too); c0 / c1 with
+        batch stride 0 (an expanded view) rotate one input by every element."""
 
         self._check_poly(c0, limbs, self.N)
         self._check_poly(c1, limbs, self.N)
@@ -299,14 +301,24 @@ class CKKSContext:
             a_stride = _bstride(a0)
         L = nat.lib()
         ws = self.workspace(L.hck_rotate_workspace_bytes(self._h, limbs, B))
-        nat.check(L.hck_rotate(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), _bstride(c0),
-                               nat.ptr_array([k.data_ptr() for k in keys]),
-                               a0.data_ptr() if a0 is not None else None,
-                               a1.data_ptr() if a1 is not None else None, a_stride,
-                               out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
-                               _stream_ptr(self.device)),
-                  "hck_rotate")
+        fn, gal, name = self._galois_arg(L, galois, B, "hck_rotate")
+        nat.check(fn(self._h, limbs, B, gal, c0.data_ptr(), c1.data_ptr(), _bstride(c0),
+                     nat.ptr_array([k.data_ptr() for k in keys]),
+                     a0.data_ptr() if a0 is not None else None,
+                     a1.data_ptr() if a1 is not None else None, a_stride,
+                     out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
+                     _stream_ptr(self.device)), name)
         return out0, out1
+
+    @staticmethod
+    def _galois_arg(L, galois, batch: int, base: str):
+        """(entry point, galois argument, name): the per-item variant for a sequence."""
+
+        if isinstance(galois, (list, tuple, np.ndarray)):
+            if len(galois) != batch:
+                raise ValueError("one Galois element per item")
+            return getattr(L, base + "_many"), nat.u32_array(galois), base + "_many"
+        return getattr(L, base), int(galois), base
 
     def rotate_ext(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois: int, keys,
                    out0: torch.Tensor | None = None, out1: torch.Tensor | None = None,
@@ -349,13 +361,13 @@ class CKKSContext:
             a_stride = _bstride(a0)
         L = nat.lib()
         ws = self.workspace(L.hck_keyswitch_workspace_bytes(self._h, limbs, B))
-        nat.check(L.hck_rotate_ext(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), _bstride(c0),
-                                   nat.ptr_array([k.data_ptr() for k in keys]),
-                                   a0.data_ptr() if a0 is not None else None,
-                                   a1.data_ptr() if a1 is not None else None, a_stride,
-                                   out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
-                                   _stream_ptr(self.device)),
-                  "hck_rotate_ext")
+        fn, gal, name = self._galois_arg(L, galois, B, "hck_rotate_ext")
+        nat.check(fn(self._h, limbs, B, gal, c0.data_ptr(), c1.data_ptr(), _bstride(c0),
+                     nat.ptr_array([k.data_ptr() for k in keys]),
+                     a0.data_ptr() if a0 is not None else None,
+                     a1.data_ptr() if a1 is not None else None, a_stride,
+                     out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
+                     _stream_ptr(self.device)), name)
         return out0, out1
 
     def _pair(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, what: str) -> int:

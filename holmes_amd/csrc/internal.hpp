@@ -87,14 +87,15 @@ int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
 
 size_t ks_fused_bytes(const hck_context* c, int ell, int batch);
-// d and add are read through sigma_galois (galois == 1: unpermuted); acc_b / acc_a (nullable,
+// d and add are read through sigma_galois (galois == 1: unpermuted), or through sigma of
+// galois_items[b] for ciphertext b when that host array is given; acc_b / acc_a (nullable,
 // unpermuted) are added to out_b / out_a, or, with ext_b / ext_a set (the key switch stops in the
 // extended basis), to the extended-basis outputs.
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
              char* ws, hipStream_t s, uint64_t* ext_b = nullptr, uint64_t* ext_a = nullptr,
-             long long ext_stride = 0);
+             long long ext_stride = 0, const uint32_t* galois_items = nullptr);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

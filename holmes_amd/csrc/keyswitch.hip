@@ -43,47 +43,34 @@ extern "C" size_t hck_rotate_workspace_bytes(const hck_context* ctx, int level_l
   return hck_keyswitch_workspace_bytes(ctx, level_limbs, batch);
 }
 
-extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
-                          const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
-                          const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
-                          int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
-                          void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+bool galois_ok(uint32_t g) { return (g & 1u) != 0 && g < 2u * hck::kN; }
+
+// Rotation of every item b by galois (or galois_items[b]), plain or ending in the extended basis.
+int rotate_impl(const hck_context* ctx, int level_limbs, int batch, uint32_t galois, const uint32_t* galois_items,
+                const uint64_t* c0, const uint64_t* c1, int64_t in_stride, const uint64_t* const* ksk,
+                const uint64_t* acc0, const uint64_t* acc1, int64_t acc_stride, uint64_t* out0, uint64_t* out1,
+                int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream, bool ext) {
   if (!ctx || !c0 || !c1 || !ksk || !out0 || !out1 || batch < 0) return HCK_ERR_ARG;
   if (level_limbs < 1 || level_limbs > ctx->L) return HCK_ERR_ARG;
-  if ((galois & 1u) == 0 || galois >= 2u * hck::kN) return HCK_ERR_ARG;
   if ((acc0 == nullptr) != (acc1 == nullptr)) return HCK_ERR_ARG;
   // the inputs are gathered through sigma while the outputs are written: no aliasing
   if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1) return HCK_ERR_ARG;
-  if (batch == 0) return HCK_OK;
-  for (int b = 0; b < batch; ++b) if (!ksk[b]) return HCK_ERR_ARG;
-  const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
-  if (!workspace || workspace_bytes < hck::ks_fused_bytes(ctx, level_limbs, chunk)) return HCK_ERR_WORKSPACE;
-  for (int b0 = 0; b0 < batch; b0 += chunk) {
-    const int nb = batch - b0 < chunk ? batch - b0 : chunk;
-    const long long ai = (long long)b0 * acc_stride;
-    int rc = hck::ks_fused(ctx, level_limbs, nb, c1 + (long long)b0 * in_stride, in_stride, galois, ksk + b0,
-                           c0 + (long long)b0 * in_stride, in_stride, acc0 ? acc0 + ai : nullptr,
-                           acc1 ? acc1 + ai : nullptr, acc_stride, out0 + (long long)b0 * out_stride,
-                           out1 + (long long)b0 * out_stride, out_stride, (char*)workspace, (hipStream_t)stream);
-    if (rc) return rc;
+  if (ext) {
+    // item strides only matter between items: a single item may carry any stride (numpy views of
+    // size-1 axes have stride 0)
+    const int64_t ext_limb_words = (int64_t)(level_limbs + ctx->K) * hck::kN;
+    if (acc0 && batch > 1 && acc_stride < ext_limb_words) return HCK_ERR_ARG;
+    if (out0 == out1) return HCK_ERR_ARG;
+    if (batch > 1 && out_stride < ext_limb_words) return HCK_ERR_ARG;
   }
-  return HCK_OK;
-}
-
-extern "C" int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
-                              const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
-                              const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
-                              int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
-                              void* workspace, size_t workspace_bytes, void* stream) {
-  if (!ctx || !c0 || !c1 || !ksk || !out0 || !out1 || batch < 0) return HCK_ERR_ARG;
-  if ((acc0 == nullptr) != (acc1 == nullptr)) return HCK_ERR_ARG;
-  // item strides only matter between items: a single item may carry any stride (numpy views of
-  // size-1 axes have stride 0)
-  if (acc0 && batch > 1 && acc_stride < (int64_t)(level_limbs + ctx->K) * hck::kN) return HCK_ERR_ARG;
-  if (level_limbs < 1 || level_limbs > ctx->L) return HCK_ERR_ARG;
-  if ((galois & 1u) == 0 || galois >= 2u * hck::kN) return HCK_ERR_ARG;
-  if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1 || out0 == out1) return HCK_ERR_ARG;
-  if (batch > 1 && out_stride < (int64_t)(level_limbs + ctx->K) * hck::kN) return HCK_ERR_ARG;
+  if (galois_items) {
+    for (int b = 0; b < batch; ++b)
+      if (!galois_ok(galois_items[b])) return HCK_ERR_ARG;
+  } else if (!galois_ok(galois)) {
+    return HCK_ERR_ARG;
+  }
   if (batch == 0) return HCK_OK;
   for (int b = 0; b < batch; ++b) if (!ksk[b]) return HCK_ERR_ARG;
   const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
@@ -91,13 +78,62 @@ extern "C" int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch
   for (int b0 = 0; b0 < batch; b0 += chunk) {
     const int nb = batch - b0 < chunk ? batch - b0 : chunk;
     const long long oi = (long long)b0 * out_stride, ai = (long long)b0 * acc_stride;
-    int rc = hck::ks_fused(ctx, level_limbs, nb, c1 + (long long)b0 * in_stride, in_stride, galois, ksk + b0,
-                           c0 + (long long)b0 * in_stride, in_stride, acc0 ? acc0 + ai : nullptr,
-                           acc1 ? acc1 + ai : nullptr, acc_stride, nullptr, nullptr, 0, (char*)workspace,
-                           (hipStream_t)stream, out0 + oi, out1 + oi, out_stride);
+    const uint32_t* gi = galois_items ? galois_items + b0 : nullptr;
+    int rc;
+    if (ext) {
+      rc = hck::ks_fused(ctx, level_limbs, nb, c1 + (long long)b0 * in_stride, in_stride, galois, ksk + b0,
+                         c0 + (long long)b0 * in_stride, in_stride, acc0 ? acc0 + ai : nullptr,
+                         acc1 ? acc1 + ai : nullptr, acc_stride, nullptr, nullptr, 0, (char*)workspace,
+                         (hipStream_t)stream, out0 + oi, out1 + oi, out_stride, gi);
+    } else {
+      rc = hck::ks_fused(ctx, level_limbs, nb, c1 + (long long)b0 * in_stride, in_stride, galois, ksk + b0,
+                         c0 + (long long)b0 * in_stride, in_stride, acc0 ? acc0 + ai : nullptr,
+                         acc1 ? acc1 + ai : nullptr, acc_stride, out0 + oi, out1 + oi, out_stride,
+                         (char*)workspace, (hipStream_t)stream, nullptr, nullptr, 0, gi);
+    }
     if (rc) return rc;
   }
   return HCK_OK;
+}
+
+}  // namespace
+
+extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
+                          const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                          const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                          int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+  return rotate_impl(ctx, level_limbs, batch, galois, nullptr, c0, c1, in_stride, ksk, acc0, acc1, acc_stride,
+                     out0, out1, out_stride, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int hck_rotate_many(const hck_context* ctx, int level_limbs, int batch, const uint32_t* galois,
+                               const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                               const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                               int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  if (!galois) return HCK_ERR_ARG;
+  return rotate_impl(ctx, level_limbs, batch, 1u, galois, c0, c1, in_stride, ksk, acc0, acc1, acc_stride,
+                     out0, out1, out_stride, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
+                              const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                              const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                              int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  return rotate_impl(ctx, level_limbs, batch, galois, nullptr, c0, c1, in_stride, ksk, acc0, acc1, acc_stride,
+                     out0, out1, out_stride, workspace, workspace_bytes, stream, true);
+}
+
+extern "C" int hck_rotate_ext_many(const hck_context* ctx, int level_limbs, int batch, const uint32_t* galois,
+                                   const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                                   const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                                   int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                                   void* workspace, size_t workspace_bytes, void* stream) {
+  if (!galois) return HCK_ERR_ARG;
+  return rotate_impl(ctx, level_limbs, batch, 1u, galois, c0, c1, in_stride, ksk, acc0, acc1, acc_stride,
+                     out0, out1, out_stride, workspace, workspace_bytes, stream, true);
 }
 
 extern "C" size_t hck_moddown_workspace_bytes(const hck_context* ctx, int level_limbs, int polys) {

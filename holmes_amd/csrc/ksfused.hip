@@ -46,6 +46,21 @@ struct KeyPtrsF {
   const uint64_t* k[kMaxBatchF];
 };
 
+// Galois element per ciphertext of a launch (a batch of rotations by different amounts), or one for
+// all (then the batch may exceed kMaxBatchF).  The value is uniform over a workgroup.
+struct GalF {
+  int per_item;
+  uint32_t uniform;
+  uint32_t g[kMaxBatchF];
+};
+__device__ __forceinline__ uint32_t gal_of(const GalF& G, int b) { return G.per_item ? G.g[b] : G.uniform; }
+inline GalF gal_uniform(uint32_t g) {
+  GalF G{};
+  G.per_item = 0;
+  G.uniform = g;
+  return G;
+}
+
 template <bool RED>
 __device__ __forceinline__ void ct_bf(double& u, double& v, const double w, double p, double pinv) {
   const double m = mulv(v, w, p, pinv);
@@ -319,7 +334,7 @@ __device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restric
 // that the polys of one tile run on one XCD back to back (the XCDs take workgroups round-robin):
 // each row group's twiddles are then fetched into one XCD's L2, not into all eight.
 __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
-                                                     uint32_t g, int limb0, int prime0, double* __restrict__ t1,
+                                                     const GalF G, int limb0, int prime0, double* __restrict__ t1,
                                                      int limbs, int batch, DevTables T) {
   __shared__ double S[kRowLds];
   const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
@@ -330,7 +345,7 @@ __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict_
   const double p = T.p[pi], pinv = T.pinv[pi];
   const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   double x[16];
-  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), g);
+  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), gal_of(G, b));
   rows_inv_to_t(x, t1 + ((long long)b * limbs + i) * kN, rg, S, tw, p, pinv);
 }
 
@@ -625,7 +640,7 @@ __device__ __forceinline__ TileId decode_tile(int batch) {
 // extended basis: it writes (P * sigma(add) + IP_b, IP_a) over Q u P as canonical NTT-domain residues
 // to ext_b / ext_a ([ell + K] limbs per ciphertext, Q limbs first), plus the extended-basis
 // accumulators acc_b / acc_a when given (which ext_b / ext_a may alias).
-__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
                                                    const double* __restrict__ t2, KeyPtrsF keys, int ell,
                                                    int beta, int batch, int tiles, int e0, double* __restrict__ accp,
                                                    const uint64_t* __restrict__ add, long long add_stride,
@@ -637,6 +652,7 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict
   const TileId id = decode_tile(batch);
   if (id.tile >= tiles) return;
   const int b = id.b, e = e0 + (id.tile >> 4), rg = id.tile & 15;
+  const uint32_t g = gal_of(G, b);
   const int L = T.L, K = T.K;
   const int pi = e < ell ? e : L + (e - ell);
   const double p = T.p[pi], pinv = T.pinv[pi];
@@ -712,7 +728,7 @@ __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], co
 // pass v of the ModDown conversion T4 right away, so the Q-limb inner product never goes to HBM:
 //   out_b = (IP_b - v_b) * P^-1 + sigma_g(add) (+ acc_b),   out_a = (IP_a - v_a) * P^-1 (+ acc_a),
 // canonical u64.
-__global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
                                                     const double* __restrict__ t2, KeyPtrsF keys, int ell, int beta,
                                                     int batch, const double* __restrict__ t4,
                                                     const uint64_t* __restrict__ add, long long add_stride,
@@ -726,6 +742,7 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restric
   const TileId id = decode_tile(batch);
   if (id.tile >= 16 * ell) return;
   const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
+  const uint32_t g = gal_of(G, b);
   const double p = T.p[i], pinv = T.pinv[i];
   {
     TwStage st;
@@ -801,16 +818,22 @@ size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
-             char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride) {
+             char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
+             const uint32_t* galois_items) {
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch > kMaxBatchF) return HCK_ERR_ARG;
+  GalF G = gal_uniform(galois);
+  if (galois_items) {
+    G.per_item = 1;
+    for (int b = 0; b < batch; ++b) G.g[b] = galois_items[b];
+  }
   const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
   const long long n = kN;
   double* r1 = (double*)ws;
   double* t2 = r1 + (long long)batch * 2 * ell * n;
   double* accp = t2 + (long long)batch * beta * ext_l * n;
   // K1
-  k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, 0, 0,
+  k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0,
                                                                                     r1, ell, batch, c->dev);
   HCK_CHECK_LAUNCH();
   // K2: ModUp, one block per (column pair, digit, ciphertext).  Targets of digit j: ext_l minus the
@@ -826,7 +849,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   if (ext_b) {
     // K3 over every extended limb, ending in the extended basis
     const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
-    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
+    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, tiles,
                                                             0, nullptr, add, add_stride, ext_b, ext_a, ext_stride,
                                                             acc_b, acc_a, acc_stride, c->dev);
     HCK_CHECK_LAUNCH();
@@ -835,7 +858,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   // K3 over the K special limbs
   {
     const int tiles = 16 * K, groups = (tiles + kXcds - 1) / kXcds;
-    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, tiles,
+    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, tiles,
                                                             ell, accp, nullptr, 0, nullptr, nullptr, 0, nullptr,
                                                             nullptr, 0, c->dev);
     HCK_CHECK_LAUNCH();
@@ -849,7 +872,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   // K5: Q limbs
   {
     const int tiles = 16 * ell, groups = (tiles + kXcds - 1) / kXcds;
-    k_ks_rows_ipq<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, galois, t2, kp, ell, beta, batch, t4,
+    k_ks_rows_ipq<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, t4,
                                                              add, add_stride, acc_b, acc_a, acc_stride, out_b,
                                                              out_a, out_stride, c->d_level + ell, c->dev);
     HCK_CHECK_LAUNCH();
@@ -870,7 +893,7 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   const long long n = kN;
   double* tp = (double*)ws;                       // [polys][K] workspace layout
   double* t4 = tp + (long long)polys * K * n;     // [polys][ell] workspace layout
-  k_ks_intt_rows<<<dim3(((16 * K + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, 1u, ell, c->L,
+  k_ks_intt_rows<<<dim3(((16 * K + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, gal_uniform(1u), ell, c->L,
                                                                                    tp, K, polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
@@ -895,7 +918,7 @@ int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, 
   const int nt = ell - 1;
   double* tl = (double*)ws;                       // [polys][1] workspace layout
   double* t4 = tl + (long long)polys * n;         // [polys][ell - 1] workspace layout
-  k_ks_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, 1u, ell - 1,
+  k_ks_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, gal_uniform(1u), ell - 1,
                                                                                 ell - 1, tl, 1, polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
@@ -918,7 +941,7 @@ int modraise_fused(const hck_context* c, int to, int polys, const uint64_t* in, 
   const int nt = to - 1;
   double* tl = (double*)ws;                       // [polys][1] workspace layout
   double* t4 = tl + (long long)polys * n;         // [polys][to - 1] workspace layout
-  k_ks_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, 1u, 0, 0, tl, 1,
+  k_ks_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, gal_uniform(1u), 0, 0, tl, 1,
                                                                                 polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;

@@ -103,6 +103,36 @@ def _view(t: torch.Tensor, limbs: int) -> torch.Tensor:
     return t[:, :limbs]
 
 
+def _alloc(ctx: CKKSContext, comps: int, batch: int, limbs: int) -> list:
+    """Output components as views of one [comps][batch][limbs][N] buffer: back to back, so a later
+    rescale (or any per-poly kernel) takes them as one batch without a copy."""
+
+    buf = ctx.empty(comps, batch, limbs, ctx.N)
+    return [buf[c] for c in range(comps)]
+
+
+def _joined(cv, limbs: int, n: int):
+    """The components as one [comps * batch][limbs][N] view when they sit back to back in one buffer
+    with one item stride (as ``_alloc`` leaves them); None otherwise."""
+
+    t0 = cv[0]
+    B = int(t0.shape[0])
+    if len(cv) == 1:
+        return t0[:, :limbs]
+    gap = (cv[1].data_ptr() - t0.data_ptr()) // 8
+    if gap <= 0 or gap % B:
+        return None
+    s = gap // B  # item stride in elements
+    if s < limbs * n:
+        return None
+    for i, t in enumerate(cv):
+        if (t.shape != t0.shape or t.dtype != t0.dtype or t.stride(1) != n or t.stride(2) != 1
+                or (B > 1 and t.stride(0) != s) or t.data_ptr() != t0.data_ptr() + i * gap * 8
+                or t.untyped_storage().data_ptr() != t0.untyped_storage().data_ptr()):
+            return None
+    return torch.as_strided(t0, (len(cv) * B, limbs, n), (s, n, 1))
+
+
 def _galois(rotation: int, ctx: CKKSContext) -> int:
     r = int(rotation)
     if r == ctx.M - 1:
@@ -157,8 +187,10 @@ def rescale(ct: Cipher, ctx: CKKSContext) -> Cipher:
     limbs = _limbs(ct)
     if ct.is_ext or limbs < 2:
         raise ValueError("rescale needs a non-extended ciphertext with at least two limbs")
-    both = torch.cat([_view(c, limbs) for c in ct.cv], 0) if len(ct.cv) > 1 else _view(ct.cv[0], limbs)
-    out = ctx.rescale_raw(both.contiguous(), limbs)
+    both = _joined(ct.cv, limbs, ctx.N)
+    if both is None:
+        both = torch.cat([_view(c, limbs) for c in ct.cv], 0)
+    out = ctx.rescale_raw(both, limbs)
     B = ct.batch_size
     parts = [out[i * B:(i + 1) * B] for i in range(len(ct.cv))]
     st = ct.state
@@ -177,7 +209,10 @@ def align_to(ct: Cipher, state: CipherState, ctx: CKKSContext) -> Cipher:
     target = int(state.cur_limbs)
     if target > limbs:
         raise ValueError(f"cannot raise a ciphertext from {limbs} to {target} limbs")
-    return ct.cipher_like([_view(c, target).clone() for c in ct.cv], state=ct.state.replace(cur_limbs=target))
+    out = _alloc(ctx, len(ct.cv), ct.batch_size if not ct.is_ext else int(ct.cv[0].shape[0]), target)
+    for o, c in zip(out, ct.cv):
+        o.copy_(_view(c, target))
+    return ct.cipher_like(out, state=ct.state.replace(cur_limbs=target))
 
 
 def _same_scale(fa: float, fb: float) -> bool:
@@ -199,9 +234,11 @@ def _binary(a: Cipher, b: Cipher, ctx: CKKSContext, op: int) -> Cipher:
         raise ValueError("batch sizes differ")
     limbs = min(_limbs(a), _limbs(b))
     idx = ctx.q_prime_idx(limbs)
+    comps = max(len(a.cv), len(b.cv))
+    bufs = _alloc(ctx, comps, a.batch_size, limbs)
     out = []
-    for c in range(max(len(a.cv), len(b.cv))):
-        o = ctx.empty(a.batch_size, limbs, ctx.N)
+    for c in range(comps):
+        o = bufs[c]
         if c < len(a.cv) and c < len(b.cv):
             ctx.poly_op(op, o, _view(a.cv[c], limbs), _view(b.cv[c], limbs), prime_idx=idx)
         elif c < len(a.cv):
@@ -225,11 +262,9 @@ def homo_sub(a: Cipher, b: Cipher, ctx: CKKSContext) -> Cipher:
 def homo_neg(a: Cipher, ctx: CKKSContext) -> Cipher:
     limbs = _limbs(a)
     idx = ctx.q_prime_idx(limbs)
-    out = []
-    for x in a.cv:
-        o = ctx.empty(x.shape[0], limbs, ctx.N)
+    out = _alloc(ctx, len(a.cv), int(a.cv[0].shape[0]), limbs)
+    for o, x in zip(out, a.cv):
         ctx.poly_op(nat.HCK_OP_NEG, o, _view(x, limbs), prime_idx=idx)
-        out.append(o)
     return a.cipher_like(out)
 
 
@@ -238,13 +273,11 @@ def homo_mul_i(ct: Cipher, ctx: CKKSContext, negative: bool = False) -> Cipher:
 
     limbs = _limbs(ct)
     idx = ctx.q_prime_idx(limbs)
-    out = []
-    for x in ct.cv:
-        o = ctx.empty(x.shape[0], limbs, ctx.N)
+    out = _alloc(ctx, len(ct.cv), int(ct.cv[0].shape[0]), limbs)
+    for o, x in zip(out, ct.cv):
         ctx.poly_op(nat.HCK_OP_MUL_XHALF, o, _view(x, limbs), prime_idx=idx)
         if negative:
             ctx.poly_op(nat.HCK_OP_NEG, o, o, prime_idx=idx)
-        out.append(o)
     return ct.cipher_like(out)
 
 
@@ -343,8 +376,11 @@ def pack_cipher_batch(ciphers) -> Cipher:
                 or int(c.state.scale_degree) != int(first.state.scale_degree)):
             raise ValueError("pack_cipher_batch: ciphertexts differ in level, scale degree or basis")
     rows = int(first.cv[0].shape[1]) if first.is_ext else _limbs(first)
-    cv = [torch.cat([c.cv[i][:, :rows] for c in ciphers], 0).contiguous() for i in range(2)]
-    return first.cipher_like(cv, batch_size=int(cv[0].shape[0]))
+    total = sum(int(c.cv[0].shape[0]) for c in ciphers)
+    buf = first.cv[0].new_empty((2, total, rows, first.cv[0].shape[2]))
+    for i in range(2):
+        torch.cat([c.cv[i][:, :rows] for c in ciphers], 0, out=buf[i])
+    return first.cipher_like([buf[0], buf[1]], batch_size=total)
 
 
 def unpack_cipher_batch(batch: Cipher) -> tuple:
@@ -617,11 +653,9 @@ def homo_mul_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
     limbs = min(_limbs(ct), enc.cur_limbs)
     idx = ctx.q_prime_idx(limbs)
     sc = _scalar_list(enc, limbs)
-    out = []
-    for x in ct.cv:
-        o = ctx.empty(x.shape[0], limbs, ctx.N)
+    out = _alloc(ctx, len(ct.cv), int(ct.cv[0].shape[0]), limbs)
+    for o, x in zip(out, ct.cv):
         ctx.poly_op(nat.HCK_OP_MUL_SCALAR, o, _view(x, limbs), prime_idx=idx, scalar=sc)
-        out.append(o)
     st = ct.state
     state = st.replace(cur_limbs=limbs, scale_degree=int(st.scale_degree) + enc.scale_degree,
                        scaling_factor=float(st.scaling_factor) * enc.scaling_factor)
@@ -645,10 +679,12 @@ def homo_add_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
         raise ValueError(f"scalar scale {enc.scaling_factor} != ciphertext scale {ct.state.scaling_factor}")
     limbs = min(_limbs(ct), enc.cur_limbs)
     idx = ctx.q_prime_idx(limbs)
-    c0 = ctx.empty(ct.batch_size, limbs, ctx.N)
-    ctx.poly_op(nat.HCK_OP_ADD_SCALAR, c0, _view(ct.cv[0], limbs), prime_idx=idx, scalar=_scalar_list(enc, limbs))
-    rest = [_view(x, limbs).clone() for x in ct.cv[1:]]
-    return ct.cipher_like([c0] + rest, state=ct.state.replace(cur_limbs=limbs))
+    out = _alloc(ctx, len(ct.cv), ct.batch_size, limbs)
+    ctx.poly_op(nat.HCK_OP_ADD_SCALAR, out[0], _view(ct.cv[0], limbs), prime_idx=idx,
+                scalar=_scalar_list(enc, limbs))
+    for o, x in zip(out[1:], ct.cv[1:]):
+        o.copy_(_view(x, limbs))
+    return ct.cipher_like(out, state=ct.state.replace(cur_limbs=limbs))
 
 
 def homo_add_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
@@ -718,8 +754,8 @@ def homo_mul_relin(a: Cipher, b: Cipher, ctx: CKKSContext) -> Cipher:
     the workspace)."""
 
     limbs, (a0, a1), (b0, b1) = _mul_operands(a, b)
-    o0, o1 = ctx.mul_relin_raw(a0, a1, b0, b1, limbs, _relin_key(ctx))
-    return a.cipher_like([o0, o1], state=_product_state(a, b, limbs))
+    both = ctx.mul_relin_raw(a0, a1, b0, b1, limbs, _relin_key(ctx), stacked=True)
+    return a.cipher_like([both[0], both[1]], state=_product_state(a, b, limbs))
 
 
 def homo_mul_relin_rescale_postop(lhs: Cipher, rhs: Cipher, ctx: CKKSContext, apply_double: bool = False,

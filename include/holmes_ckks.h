@@ -113,6 +113,23 @@ int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t 
                    int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* hck_rotate / hck_rotate_ext with a Galois element per item (galois[b], host array of `batch`):
+ * one launch sequence for rotations by different amounts, each with its own key -- the batched
+ * giant step of bench/cmp/holmes_multi_mac.py:180-186 (fhe.homo_rotate_batch) and the baby and
+ * giant rotations of a bootstrap's linear transforms (easyfhe.bs.openfhe, "double_hoist",
+ * llama3fhe/operators/nonlinear/bootstrap.py:119-160).  in_stride 0 rotates one input by every
+ * element.  Same workspace as hck_keyswitch. */
+int hck_rotate_many(const hck_context* ctx, int level_limbs, int batch, const uint32_t* galois,
+                    const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                    const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                    int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                    void* workspace, size_t workspace_bytes, void* stream);
+int hck_rotate_ext_many(const hck_context* ctx, int level_limbs, int batch, const uint32_t* galois,
+                        const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                        const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                        int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
 /* ModDown of `polys` extended-basis polynomials (level_limbs + K canonical NTT-domain limbs, Q
  * first) to level_limbs limbs: out = (x_Q - conv_{P->Q}(x_P)) * P^-1, fhe.moddown_from_ext
  * (input.py:1023-1029; F.cv_moddown, report.py:26-30). */

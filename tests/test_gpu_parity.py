@@ -280,3 +280,55 @@ def test_modraise(env, to):
     out = _host(ctx.modraise(_dev(x), to))
     for b in range(3):
         assert np.array_equal(out[b], orc.modraise(to, x[b]))
+
+
+@pytest.mark.parametrize("ell", [24, 7])
+def test_rotate_many_matches_oracle(env, ell):
+    """Rotations by different amounts in one launch (a Galois element and a key per item), with and
+    without the fused addends, against the oracle's rotation of each item; then one input rotated by
+    every element (batch stride 0)."""
+    _, client, ctx, orc = env
+    gs = [ctx.galois_element(1), ctx.galois_element(-512), ctx.M - 1, ctx.galois_element(4096)]
+    pairs = [_key_pair(client, ctx, orc, g) for g in gs]
+    rng = np.random.default_rng(900 + ell)
+    B = len(gs)
+    c0, c1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
+    a0, a1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
+    o0, o1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, gs, [p[0] for p in pairs])
+    h0, h1 = _host(o0), _host(o1)
+    q = np.array(ctx.primes[:ell], dtype=object).reshape(ell, 1)
+    want = [orc.rotate(ell, g, c0[b], c1[b], pairs[b][1]) for b, g in enumerate(gs)]
+    for b in range(B):
+        assert np.array_equal(h0[b], want[b][0]) and np.array_equal(h1[b], want[b][1]), f"item {b}"
+    acc0, acc1 = _dev(a0), _dev(a1)
+    ctx.rotate_raw(_dev(c0), _dev(c1), ell, gs, [p[0] for p in pairs], out0=acc0, out1=acc1, acc=(acc0, acc1))
+    h0, h1 = _host(acc0), _host(acc1)
+    for b in range(B):
+        e0 = ((want[b][0].astype(object) + a0[b].astype(object)) % q).astype(np.uint64)
+        e1 = ((want[b][1].astype(object) + a1[b].astype(object)) % q).astype(np.uint64)
+        assert np.array_equal(h0[b], e0) and np.array_equal(h1[b], e1), f"accumulated item {b}"
+    one0, one1 = _dev(c0[:1]), _dev(c1[:1])
+    s0, s1 = ctx.rotate_raw(one0.expand(B, -1, -1), one1.expand(B, -1, -1), ell, gs, [p[0] for p in pairs])
+    h0, h1 = _host(s0), _host(s1)
+    for b, g in enumerate(gs):
+        w0, w1 = orc.rotate(ell, g, c0[0], c1[0], pairs[b][1])
+        assert np.array_equal(h0[b], w0) and np.array_equal(h1[b], w1), f"broadcast item {b}"
+
+
+def test_rotate_ext_many_equals_single_rotations(env):
+    _, client, ctx, orc = env
+    ell = 10
+    gs = [ctx.galois_element(3), ctx.galois_element(-1), ctx.galois_element(77)]
+    keys = [_key_pair(client, ctx, orc, g)[0] for g in gs]
+    rng = np.random.default_rng(31)
+    c0, c1 = _dev(_rand(ctx, rng, 3, ell)), _dev(_rand(ctx, rng, 3, ell))
+    m0, m1 = ctx.rotate_ext(c0, c1, ell, gs, keys)
+    for b, g in enumerate(gs):
+        s0, s1 = ctx.rotate_ext(c0[b:b + 1], c1[b:b + 1], ell, g, keys[b])
+        assert torch.equal(m0[b:b + 1], s0) and torch.equal(m1[b:b + 1], s1), f"item {b}"
+    from holmes_amd import _native as nat
+
+    with pytest.raises(ValueError):
+        ctx.rotate_raw(c0, c1, ell, gs[:2], keys)
+    with pytest.raises(nat.NativeError):
+        ctx.rotate_raw(c0, c1, ell, [gs[0], 4, gs[2]], keys)  # an even Galois element

@@ -145,3 +145,24 @@ def test_scalar_encoding_residues_and_rounding():
         fhe._scaled_int(1.0, 2.0**61, False)  # beyond the 2^61 encoding cap
     tab = fhe._scalar_residues(np.array([1.0, -1.0]), 3, 4.0, False, ctx)
     assert tab.shape == (2, 3) and int(tab[1, 0]) == primes[0] - 4
+
+
+def test_joined_components_view_without_copy():
+    # components allocated back to back are rescaled as one batch through a strided view; anything
+    # else is refused (and the caller falls back to a concatenation)
+    import torch
+
+    from holmes_amd.fhe import _joined
+
+    n = 8
+    buf = torch.arange(2 * 3 * 5 * n, dtype=torch.int64).reshape(2, 3, 5, n)
+    v = _joined([buf[0], buf[1]], 4, n)
+    assert v is not None and v.shape == (6, 4, n)
+    assert torch.equal(v, torch.cat([buf[0, :, :4], buf[1, :, :4]], 0))
+    one = torch.arange(2 * 1 * 5 * n, dtype=torch.int64).reshape(2, 1, 5, n)
+    assert torch.equal(_joined([one[0], one[1]], 5, n), one.reshape(2, 5, n))
+    other = torch.zeros(3, 5, n, dtype=torch.int64)
+    assert _joined([buf[0], other], 4, n) is None
+    assert _joined([buf[1], buf[0]], 4, n) is None
+    gapped = torch.zeros(3, 3, 5, n, dtype=torch.int64)
+    assert _joined([gapped[0], gapped[2]], 4, n) is None
