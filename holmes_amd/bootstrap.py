@@ -251,9 +251,14 @@ class _PSEval:
         self.k = _baby_size(degree)
         self._adj: dict = {}
         T = {1: (limbs if self.sim else self._fix(x, limbs))}
-        for j in range(2, self.k + 1):
-            a, b = j // 2, j - j // 2
-            T[j] = self.double_minus(T[a], T[b], sub=None if a == b else T[1])
+        j0 = 1
+        while j0 < self.k:  # T_(j0+1) .. T_(2 j0) from T_(j/2) T_(j - j/2): one batched product per depth
+            js = list(range(j0 + 1, min(2 * j0, self.k) + 1))
+            prods = self.mul_many([(T[j // 2], T[j - j // 2]) for j in js])
+            for j, p in zip(js, prods):
+                a, b = j // 2, j - j // 2
+                T[j] = self._finish_double(p, None if a == b else T[b - a])
+            j0 *= 2
         M = 2 * self.k
         while M <= degree:
             T[M] = self.double_minus(T[M // 2], T[M // 2])
@@ -271,6 +276,21 @@ class _PSEval:
             raise AssertionError(f"scale {got} at {l} limbs drifted from {want}")
         return ct.cipher_like(ct.cv, state=ct.state.replace(scaling_factor=want, scale_degree=1))
 
+    def _combine(self, terms, limbs: int, weights: np.ndarray) -> list:
+        """sum_t weights[t] * terms[t] (residue tables [terms][limbs]) for every component and item,
+        each term read at its own level: one hck_lincomb launch."""
+
+        ctx = self.ctx
+        B = terms[0].batch_size
+        out = fhe._alloc(ctx, 2, B, limbs)
+        xs = [[x.cv[c][b] for x in terms] for c in range(2) for b in range(B)]
+        ctx.lincomb(xs, limbs, [out[c][b] for c in range(2) for b in range(B)],
+                    torch.from_numpy(np.ascontiguousarray(weights, dtype=np.uint64)).to(ctx.device))
+        return out
+
+    def _residues(self, value: float, limbs: int, scaling_factor: float, integer: bool = False) -> np.ndarray:
+        return fhe._scalar_residues(value, limbs, scaling_factor, integer, self.ctx)[0]
+
     def adjust(self, x, l: int):
         lx = self.lv(x)
         if lx == l:
@@ -283,11 +303,11 @@ class _PSEval:
         hit = self._adj.get(key)
         if hit is not None and hit[0] is x:
             return hit[1]
-        ctx = self.ctx
-        t = fhe.align_to(x, x.state.replace(cur_limbs=l + 1), ctx) if lx > l + 1 else x
         ratio = self.canon[l] * float(self.primes[l]) / self.canon[lx]
-        enc = fhe.encode_scalar(1.0, cur_limbs=l + 1, scale_degree=1, scaling_factor=ratio, context=ctx)
-        y = self._fix(fhe.rescale(fhe.homo_mul_scalar(t, enc, ctx), ctx), l)
+        out = self._combine([x], l + 1, self._residues(1.0, l + 1, ratio)[None])
+        t = x.cipher_like(out, state=x.state.replace(cur_limbs=l + 1, scale_degree=2,
+                                                     scaling_factor=self.canon[l] * float(self.primes[l])))
+        y = self._fix(fhe.rescale(t, self.ctx), l)
         self._adj[key] = (x, y)
         return y
 
@@ -305,26 +325,59 @@ class _PSEval:
         a, b = self.adjust(a, l), self.adjust(b, l)
         return l if self.sim else fhe.homo_add(a, b, self.ctx)
 
-    def add_const(self, x, c: float):
+    def _add_const_inplace(self, x, c: float):
+        """c added to every slot of ``x`` (a temporary this evaluator owns), in place on c0."""
+
         if self.sim or c == 0.0:
             return x
         l = self.lv(x)
-        enc = fhe.encode_scalar(float(c), cur_limbs=l, scale_degree=1, scaling_factor=self.canon[l], context=self.ctx)
-        return fhe.homo_add_scalar(x, enc, self.ctx)
+        res = self._residues(float(c), l, self.canon[l])
+        self.ctx.poly_op(_nat.HCK_OP_ADD_SCALAR, x.cv[0], x.cv[0], prime_idx=self.ctx.q_prime_idx(l),
+                         scalar=[int(v) for v in res])
+        return x
+
+    def mul_many(self, pairs) -> list:
+        """Products of several operand pairs as one batched product + relinearisation and one
+        rescale, every operand first brought to the lowest level among them."""
+
+        if len(pairs) == 1 or self.sim:
+            return [self.mul(a, b) for a, b in pairs]
+        l = min(self.lv(x) for pr in pairs for x in pr)
+        if l < 2:
+            raise ValueError("EvalMod ran out of levels")
+        ops = [(self.adjust(a, l), self.adjust(b, l)) for a, b in pairs]
+        B = ops[0][0].batch_size
+        side = [[torch.cat([pr[k].cv[c][:, :l] for pr in ops], 0) for c in range(2)] for k in range(2)]
+        both = self.ctx.mul_relin_raw(side[0][0], side[0][1], side[1][0], side[1][1], l, self.ctx.relin_key,
+                                      stacked=True)
+        x0 = ops[0][0]
+        n = len(ops) * B
+        prod = x0.cipher_like([both[0], both[1]], batch_size=n,
+                              state=x0.state.replace(cur_limbs=l, scale_degree=2,
+                                                     scaling_factor=self.canon[l] * self.canon[l]))
+        r = self._fix(fhe.rescale(prod, self.ctx), l - 1)
+        return [r.cipher_like([c[i * B:(i + 1) * B] for c in r.cv], batch_size=B) for i in range(len(ops))]
+
+    def _finish_double(self, p, sub=None):
+        """2 p - sub (sub = None: - 1) for a product p on its canonical scale."""
+
+        if self.sim:
+            return p
+        l = self.lv(p)
+        terms = [p] if sub is None else [p, self.adjust(sub, l)]
+        w = np.stack([self._residues(v, l, 1.0, integer=True) for v in ((2,) if sub is None else (2, -1))])
+        out = p.cipher_like(self._combine(terms, l, w))
+        return self._add_const_inplace(out, -1.0) if sub is None else out
 
     def double_minus(self, a, b, sub=None):
         """2 a b - sub (sub = None: - 1)."""
 
-        p = self.mul(a, b)
-        if self.sim:
-            return p
-        p2 = fhe.homo_add(p, p, self.ctx)
-        if sub is None:
-            return self.add_const(p2, -1.0)
-        return fhe.homo_sub(p2, self.adjust(sub, self.lv(p2)), self.ctx)
+        return self._finish_double(self.mul(a, b), sub)
 
     def lincomb(self, terms, c0: float, cap: int | None):
-        """c0 + sum c_j x_j over ``terms`` = [(c_j, x_j)], rescaled once, at min(level) - 1 or ``cap``."""
+        """c0 + sum c_j x_j over ``terms`` = [(c_j, x_j)], rescaled once, at min(level) - 1 or ``cap``:
+        each coefficient is encoded at the ratio that lands its term on the target scale, and the
+        terms are read at their own levels by one hck_lincomb launch."""
 
         l = min(self.lv(x) for _, x in terms) - 1
         if cap is not None:
@@ -333,18 +386,12 @@ class _PSEval:
             raise ValueError("EvalMod ran out of levels")
         if self.sim:
             return l
-        ctx = self.ctx
         target = self.canon[l] * float(self.primes[l])
-        acc = None
-        for c, x in terms:
-            lx = self.lv(x)
-            t = fhe.align_to(x, x.state.replace(cur_limbs=l + 1), ctx) if lx > l + 1 else x
-            enc = fhe.encode_scalar(float(c), cur_limbs=l + 1, scale_degree=1,
-                                    scaling_factor=target / self.canon[lx], context=ctx)
-            term = fhe.homo_mul_scalar(t, enc, ctx)
-            term = term.cipher_like(term.cv, state=term.state.replace(scaling_factor=target))
-            acc = term if acc is None else fhe.homo_add(acc, term, ctx)
-        return self.add_const(self._fix(fhe.rescale(acc, ctx), l), c0)
+        w = np.stack([self._residues(float(c), l + 1, target / self.canon[self.lv(x)]) for c, x in terms])
+        x0 = terms[0][1]
+        acc = x0.cipher_like(self._combine([x for _, x in terms], l + 1, w),
+                             state=x0.state.replace(cur_limbs=l + 1, scale_degree=2, scaling_factor=target))
+        return self._add_const_inplace(self._fix(fhe.rescale(acc, self.ctx), l), c0)
 
     # -- the series
     def evaluate(self, coeffs, cap: int | None = None):
@@ -564,17 +611,14 @@ def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: b
     del b0, b1
     first = 1 if st.giants[0] == 0 else 0
     rot = st.giants[first:]
-    if not rot:
-        acc = [res[0, 0].clone(), res[1, 0].clone()]
-    else:
+    acc = fhe._alloc(ctx, 2, 1, limbs)
+    xs = [[res[c, 0, 0]] if first else [] for c in range(2)]
+    if rot:
         g0, g1 = _rotate_many(res[0, first:, 0], res[1, first:, 0], [k2 * st.n1 * st.h_min for k2 in rot],
                               limbs, ctx)
-        ones = torch.ones((1, len(rot), limbs), dtype=torch.uint64, device=ctx.device)
-        acc = [ctx.weighted_sum(g0, ones, limbs), ctx.weighted_sum(g1, ones, limbs)]
-        if first:
-            idx = ctx.q_prime_idx(limbs)
-            for c in range(2):
-                ctx.poly_op(_nat.HCK_OP_ADD, acc[c], acc[c], res[c, 0], prime_idx=idx)
+        xs[0] += [g0[i] for i in range(len(rot))]
+        xs[1] += [g1[i] for i in range(len(rot))]
+    ctx.lincomb(xs, limbs, [acc[0][0], acc[1][0]])
     s = x.state
     return x.cipher_like(acc, batch_size=1,
                          state=s.replace(scale_degree=int(s.scale_degree) + 1,

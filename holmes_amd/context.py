@@ -442,6 +442,43 @@ class CKKSContext:
                   "hck_weighted_sum")
         return out
 
+    def _check_single(self, t: torch.Tensor, limbs: int, what: str) -> None:
+        if t.dim() == 3 and t.shape[0] == 1:
+            t = t[0]
+        if (t.dtype != torch.uint64 or t.dim() != 2 or t.shape[0] < limbs or t.shape[1] != self.N
+                or t.stride(1) != 1 or t.stride(0) != self.N or t.device.type != "cuda"):
+            raise ValueError(f"{what}: expected one [>= {limbs}][N] uint64 GPU polynomial with contiguous limbs")
+
+    def lincomb(self, xs, limbs: int, outs, weights: torch.Tensor | None = None):
+        """out[g] = sum_t w[t] * xs[g][t] over the first ``limbs`` Q primes: ``xs`` is [groups][terms]
+        single polynomials ([limbs'][N] or [1][limbs'][N] views, limbs' >= limbs, any allocation),
+        ``outs`` one polynomial per group, ``weights`` a [terms][limbs] uint64 GPU table of residues
+        (None: unit weights).  One launch (hck_lincomb)."""
+
+        G = len(xs)
+        if G != len(outs) or G < 1:
+            raise ValueError("one output per group")
+        T = len(xs[0])
+        ptrs = []
+        for row in xs:
+            if len(row) != T:
+                raise ValueError("every group needs the same number of terms")
+            for t in row:
+                self._check_single(t, limbs, "lincomb input")
+                ptrs.append(t.data_ptr())
+        for o in outs:
+            self._check_single(o, limbs, "lincomb output")
+        wp = None
+        if weights is not None:
+            if (weights.dtype != torch.uint64 or tuple(weights.shape) != (T, limbs) or not weights.is_contiguous()
+                    or weights.device.type != "cuda"):
+                raise ValueError(f"weights must be a contiguous [{T}][{limbs}] uint64 GPU table")
+            wp = weights.data_ptr()
+        nat.check(nat.lib().hck_lincomb(self._h, int(limbs), G, T, nat.ptr_array(ptrs), wp,
+                                        nat.ptr_array([o.data_ptr() for o in outs]), _stream_ptr(self.device)),
+                  "hck_lincomb")
+        return outs
+
     def moddown(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
         """Extended-basis polys [polys][limbs + K][N] -> [polys][limbs][N] (divide by P, round)."""
 

@@ -53,6 +53,32 @@ __global__ __launch_bounds__(256) void k_weighted_sum(const uint64_t* __restrict
   out[g * out_stride + (long long)i * kN + k] = d2u(canon(acc, p, pinv));
 }
 
+// Linear combinations over pointer lists: out[g][l][k] = sum_t w[t][l] * x[g * terms + t][l][k] (mod q_l),
+// canonical; w == null: unit weights (canonical inputs).  Each operand is one [limbs][N] polynomial at
+// its own address, so ciphertexts of different levels and allocations combine without copies.
+// Grid (N / 256, limbs, groups).  Reduced every 7 terms: |acc| <= p/2 + 7 p < 2^53 stays exact.
+constexpr int kLcMaxPtrs = 256;
+constexpr int kLcMaxGroups = 64;
+struct LcPtrs {
+  const uint64_t* x[kLcMaxPtrs];
+  uint64_t* out[kLcMaxGroups];
+};
+
+__global__ __launch_bounds__(256) void k_lincomb(const LcPtrs P, int terms, const uint64_t* __restrict__ w, int limbs,
+                                                DevTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y, g = blockIdx.z;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const long long off = (long long)i * kN + k;
+  double acc = 0.0;
+  for (int t = 0; t < terms; ++t) {
+    const double x = u2d(P.x[g * terms + t][off]);
+    acc += w ? mulv(x, u2d(w[(long long)t * limbs + i]), p, pinv) : x;  // |term| < p
+    if (t % 7 == 6) acc = reduce(acc, p, pinv);
+  }
+  P.out[g][off] = d2u(canon(acc, p, pinv));
+}
+
 int launch_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
                   const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1,
                   uint64_t* d2, long long d_stride, hipStream_t s) {
@@ -150,6 +176,26 @@ extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int gr
   if (groups == 0) return HCK_OK;
   hck::k_weighted_sum<<<dim3(hck::kN / 256, limbs, groups), 256, 0, (hipStream_t)stream>>>(
       in, in_stride, n, weights, out, out_stride, limbs, ctx->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+extern "C" int hck_lincomb(const hck_context* ctx, int limbs, int groups, int terms, const uint64_t* const* x,
+                           const uint64_t* weights, uint64_t* const* out, void* stream) {
+  if (!ctx || !x || !out || limbs < 1 || limbs > ctx->L || groups < 0 || terms < 1) return HCK_ERR_ARG;
+  if (groups > hck::kLcMaxGroups || (long long)groups * terms > hck::kLcMaxPtrs) return HCK_ERR_ARG;
+  if (groups == 0) return HCK_OK;
+  hck::LcPtrs P{};
+  for (int j = 0; j < groups * terms; ++j) {
+    if (!x[j]) return HCK_ERR_ARG;
+    P.x[j] = x[j];
+  }
+  for (int g = 0; g < groups; ++g) {
+    if (!out[g]) return HCK_ERR_ARG;
+    P.out[g] = out[g];
+  }
+  hck::k_lincomb<<<dim3(hck::kN / 256, limbs, groups), 256, 0, (hipStream_t)stream>>>(P, terms, weights, limbs,
+                                                                                     ctx->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }

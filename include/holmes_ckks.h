@@ -233,6 +233,17 @@ int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch, const uint
 int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int groups, const uint64_t* in, int64_t in_stride,
                      const uint64_t* weights, uint64_t* out, int64_t out_stride, void* stream);
 
+/* Linear combinations over pointer lists: out[g] = sum_t w[t] * x[g * terms + t] over the first `limbs`
+ * Q primes (limb l of every operand and output at element offset l * N from its pointer), canonical.
+ * `weights` is a device [terms][limbs] table of residues shared by every group, or NULL for unit
+ * weights (then the inputs must be canonical).  groups <= 64, groups * terms <= 256; an output may
+ * be one of its own group's inputs.  The reference's linear combinations of ciphertexts of
+ * different levels (fhe.homo_mul_scalar + homo_add chains, llama3fhe/operators/nonlinear/
+ * polynomial.py:256-300) and the PairFold page append (four ciphertext sums committed together,
+ * llama3fhe/operators/pairfold_kv_cache.py:400-450) in one launch. */
+int hck_lincomb(const hck_context* ctx, int limbs, int groups, int terms, const uint64_t* const* x,
+                const uint64_t* weights, uint64_t* const* out, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -239,3 +239,29 @@ def test_product_arguments_are_checked(env):
                              ctx.relin_key.data_ptr(), t.data_ptr(), ctx.empty(1, 4, ctx.N).data_ptr(), 4 * ctx.N,
                              ws.data_ptr(), ws.numel(), None)
     assert rc == -1
+
+
+def test_lincomb_matches_oracle(env):
+    """Pointer-list linear combinations (hck_lincomb): operands at different levels in separate
+    allocations, weighted (against the oracle's weighted sum per group) and unit weights (against
+    exact sums), an output aliasing its group's first input."""
+    fhe, client, ctx, orc = env
+    rng = np.random.default_rng(41)
+    limbs, G, T = 6, 3, 9
+    srcs = [[_dev(_rand(ctx, rng, 1, limbs + int(rng.integers(0, 5)))[0]) for _ in range(T)] for _ in range(G)]
+    w = np.stack([[rng.integers(0, ctx.primes[l], dtype=np.uint64) for l in range(limbs)] for _ in range(T)])
+    outs = [ctx.empty(limbs, ctx.N) for _ in range(G)]
+    ctx.lincomb(srcs, limbs, outs, torch.from_numpy(w).cuda())
+    for g in range(G):
+        x = np.stack([_host(t)[:limbs] for t in srcs[g]])
+        assert np.array_equal(_host(outs[g]), orc.weighted_sum(limbs, x, w[None])[0]), f"group {g}"
+    q = np.array(ctx.primes[:limbs], dtype=object).reshape(limbs, 1)
+    want = [sum(_host(t)[:limbs].astype(object) for t in srcs[g]) % q for g in range(G)]
+    first = [_host(srcs[g][0]).copy() for g in range(G)]
+    ctx.lincomb(srcs, limbs, [srcs[g][0] for g in range(G)])  # unit weights, in place
+    for g in range(G):
+        got = _host(srcs[g][0])
+        assert np.array_equal(got[:limbs], want[g].astype(np.uint64)), f"unit group {g}"
+        assert np.array_equal(got[limbs:], first[g][limbs:])  # limbs above the count untouched
+    with pytest.raises(ValueError):
+        ctx.lincomb(srcs, limbs, outs[:2])
