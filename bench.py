@@ -20,6 +20,11 @@ ciphertexts at 20 limbs, scale 2^40.  A step is one whole projection, pack + enc
 diagonal included (the reference encodes per chunk per call,
 llama3fhe/operators/linear/operator.py:296-312).  Its line reports seconds per projection.
 
+``--workload kv``: 128 PairFold token writes (4 ciphertexts each, 12 limbs) appended into one
+HBM-pooled page: each append is one fused launch of eight polynomial sums into a fresh slot.
+``--workload wire``: 16 ciphertexts at 24 limbs packed into one device buffer in the wire layout,
+copied to pinned host memory and unpacked again.
+
 ``--workload bootstrap``: one full-slot bootstrap (N = 2^16, 24 x 50-bit primes, dnum 3, scale
 2^50, sparse ternary secret h = 192, level budget (3, 3)) of a ciphertext at 3 limbs; its line
 reports ms per bootstrap and the precision of the refreshed slots.
@@ -66,11 +71,14 @@ def main() -> int:
     ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
                     help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
                          "(both are hoist strategies of the reference's LinearOperatorConfig)")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "mul", "bootstrap", "stream"), default="c2",
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "mul", "bootstrap", "kv", "wire", "stream"),
+                    default="c2",
                     help="c2: batched key switch (headline); c1: one rotation + rescale (latency); "
                          "c3: q_proj BSGS projection; mul: 16 ciphertext products with "
                          "relinearisation and rescale at 24 limbs; bootstrap: one full-slot bootstrap "
-                         "at 24 limbs; stream: the "
+                         "at 24 limbs; kv: 128 token appends into an HBM-pooled KV page; wire: 16 "
+                         "ciphertexts packed into one device buffer and round-tripped through pinned "
+                         "host memory; stream: the "
                          "residue negation kernel over 16 x 24 limbs, a plain read-once/write-once "
                          "stream of known size (HBM ceiling and counter calibration)")
     args = ap.parse_args()
@@ -99,6 +107,10 @@ def main() -> int:
         return run_mul(args)
     if args.workload == "bootstrap":
         return run_bootstrap(args)
+    if args.workload == "kv":
+        return run_kv(args)
+    if args.workload == "wire":
+        return run_wire(args)
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
@@ -503,6 +515,191 @@ def run_bootstrap(args) -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole bootstrap (key switches, MACs, rescales, elementwise)", "ms_per_launch": round(ms, 3)},
         "cpu_baseline": cpu}), flush=True)
+    return 0
+
+
+KV_LIMBS = 12
+KV_TOKENS = 128
+
+
+def run_kv(args) -> int:
+    """A step = 128 token writes appended into one page of an HBM-pooled PairFold layer cache
+    (holmes_amd.kv_pages): the first opens the page by move, the others are fused four-ciphertext
+    sums into a fresh pool slot.  Algorithmic bytes per fused append: the tail page and the token
+    read, the new page written (3 x 8 polys x 12 limbs x 512 KiB)."""
+
+    import torch
+
+    from holmes_amd import backend, fhe
+    from holmes_amd.context import Cipher, CipherState
+    from holmes_amd.kv_pages import KVPagePool, PairFoldLayerCache, PairFoldTokenWrite
+
+    seed = 20261241
+    spec = fhe.CKKSContextSpec(depth=KV_LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=seed)
+    client, ctx = fhe.generate_client_context(spec)
+    session = backend.EasyFHEContext(tensor=torch, fhe=fhe, client=client, context=ctx, max_slots=ctx.max_slots)
+    rng = np.random.default_rng(seed)
+    st = CipherState(cur_limbs=KV_LIMBS, scale_degree=1, scaling_factor=2.0**40)
+    hi = np.array(ctx.primes[:KV_LIMBS], dtype=np.uint64)[None, None, :, None]
+    src = torch.from_numpy(rng.integers(0, hi, (4, 2, KV_LIMBS, ctx.N), dtype=np.uint64)).cuda()
+    pool = KVPagePool(ctx, KV_LIMBS, capacity=4)
+
+    def tokens():
+        # distinct handles per token (views of one resident source: the inputs are in HBM)
+        return [PairFoldTokenWrite([Cipher([src[h, 0][None], src[h, 1][None]], st, slots=ctx.max_slots)
+                                    for h in (0, 1)],
+                                   [Cipher([src[h, 0][None], src[h, 1][None]], st, slots=ctx.max_slots)
+                                    for h in (2, 3)], t) for t in range(KV_TOKENS)]
+
+    def step(toks):
+        cache = PairFoldLayerCache(pool=pool)
+        for t in toks:
+            cache.append(t, crypto_context=session)
+        return cache
+
+    for _ in range(args.warmup):
+        step(tokens()).release()
+    torch.cuda.synchronize()
+    batches = [tokens() for _ in range(args.steps)]
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    w0 = time.perf_counter()
+    ev0.record(stream)
+    caches = []
+    for b in batches:
+        c = step(b)
+        caches.append(c)
+        c.release()
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ms_wall = (time.perf_counter() - w0) * 1e3 / args.steps
+    ms = ev0.elapsed_time(ev1) / args.steps
+    # parity: the page of the last step is 128 x the source, modulo each prime
+    q = hi.astype(object)
+    c = step(tokens())
+    got = np.stack([np.stack([h.cv[k][0].cpu().numpy() for k in range(2)]) for h in c.pages[0].handles])
+    want = (src.cpu().numpy().astype(object) * KV_TOKENS % q).astype(np.uint64)
+    ok = bool(np.array_equal(got, want))
+    c.release()
+    per_append = 3 * 8 * KV_LIMBS * ctx.N * 8
+    step_bytes = (KV_TOKENS - 1) * per_append
+    # the fused append kernel alone: the same launch (tail slot + token -> fresh slot), back to back
+    xs = [[pool.buf[0, h, c, 0], src[h, c]] for h in range(4) for c in range(2)]
+    outs = [pool.buf[1, h, c, 0] for h in range(4) for c in range(2)]
+    ctx.lincomb(xs, KV_LIMBS, outs)
+    torch.cuda.synchronize()
+    ev0.record(stream)
+    for _ in range(KV_TOKENS - 1):
+        ctx.lincomb(xs, KV_LIMBS, outs)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    k_ms = ev0.elapsed_time(ev1) / (KV_TOKENS - 1)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+        x = src.cpu().numpy()
+        ones = np.ones((1, 2, KV_LIMBS), dtype=np.uint64)
+        t = time.perf_counter()
+        for h in range(4):
+            for k in range(2):
+                orc.weighted_sum(KV_LIMBS, np.stack([x[h, k], x[h, k]]), ones)
+        csec = time.perf_counter() - t
+        cpu = {"value": round(per_append / csec / 1e9, 3), "unit": "GB/s", "cores": int(O.num_threads()),
+               "kind": "port", "sample": f"one append's eight sums with the oracle's weighted sum ({csec * 1e3:.1f} ms)"}
+    achieved = per_append / (k_ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "PairFold KV page appends (HBM pool, 12 limbs), algorithmic GB/s", "value": round(
+            step_bytes / (ms_wall * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_wall, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+        "config": {"workload": "128 token writes (4 cts x 12 limbs) into one pooled page; 127 fused appends",
+                   "us_per_append": round(ms * 1e3 / (KV_TOKENS - 1), 2), "algorithmic_bytes_per_step": step_bytes,
+                   "page_exact": ok, "note": "value includes the host-side ownership bookkeeping of each append; "
+                                             "roofline is the fused append kernel alone"},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_lincomb (8 groups x 2 terms per append)", "ms_per_launch": round(k_ms, 5)},
+        "cpu_baseline": cpu}), flush=True)
+    return 0
+
+
+def run_wire(args) -> int:
+    """A step = 16 ciphertexts at 24 limbs packed into one device buffer (wire layout), copied to
+    pinned host memory and back, and unpacked: the bytes of the 16 ciphertexts cross HBM (gather),
+    PCIe twice and HBM again (unpack)."""
+
+    import torch
+
+    from holmes_amd import fhe, wire
+    from holmes_amd.context import Cipher, CipherState
+
+    seed = 20261242
+    spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=seed)
+    client, ctx = fhe.generate_client_context(spec)
+    rng = np.random.default_rng(seed)
+    st = CipherState(cur_limbs=LIMBS, scale_degree=1, scaling_factor=2.0**40)
+    hi = np.array(ctx.primes[:LIMBS], dtype=np.uint64)[None, :, None]
+    cts = [Cipher([torch.from_numpy(rng.integers(0, hi, (1, LIMBS, ctx.N), dtype=np.uint64)).cuda() for _ in range(2)],
+                  st, slots=ctx.max_slots) for _ in range(CTS)]
+    buf = wire.device_pack(cts, primes=ctx.q_primes)
+    nbytes = int(buf.numel())
+    pinned = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    back = torch.empty_like(buf)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        wire.device_pack(cts, primes=ctx.q_primes, out=buf)
+        pinned.copy_(buf, non_blocking=True)
+        back.copy_(pinned, non_blocking=True)
+        return wire.device_unpack(back, count=CTS)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t_pack = t_d2h = 0.0
+    for _ in range(args.steps):
+        torch.cuda.synchronize()
+        a = time.perf_counter()
+        wire.device_pack(cts, primes=ctx.q_primes, out=buf)
+        torch.cuda.synchronize()
+        b = time.perf_counter()
+        pinned.copy_(buf, non_blocking=True)
+        torch.cuda.synchronize()
+        t_pack += (b - a) * 1e3
+        t_d2h += (time.perf_counter() - b) * 1e3
+    w0 = time.perf_counter()
+    for _ in range(args.steps):
+        out = step()
+    torch.cuda.synchronize()
+    ms_wall = (time.perf_counter() - w0) * 1e3 / args.steps
+    ok = all(torch.equal(a, b) for x, y in zip(out, cts) for a, b in zip(x.cv, y.cv))
+    host = pinned.numpy().tobytes()
+    t = time.perf_counter()
+    serial = [wire.serialize(c, primes=ctx.q_primes) for c in cts[:4]]
+    t_ser = (time.perf_counter() - t) / 4
+    t = time.perf_counter()
+    for s_ in serial:
+        wire.deserialize(s_, device="cpu", primes=ctx.q_primes)
+    t_de = (time.perf_counter() - t) / 4
+    ct_bytes = 2 * LIMBS * ctx.N * 8
+    pack_gbs = 2 * nbytes / (t_pack / args.steps * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "ciphertext wire round trip (16 cts x 24 limbs: pack, D2H + H2D pinned, unpack), GB/s of ciphertext",
+        "value": round(nbytes / (ms_wall * 1e-3) / 1e9, 2), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_wall, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "u64", "data": "synthetic",
+        "config": {"workload": "16 ciphertexts at 24 limbs through the wire layout", "bytes": nbytes,
+                   "device_pack_ms": round(t_pack / args.steps, 4), "d2h_pinned_GBs": round(
+                       nbytes / (t_d2h / args.steps * 1e-3) / 1e9, 2), "round_trip_exact": ok,
+                   "host_serialize_GBs": round(ct_bytes / t_ser / 1e9, 3),
+                   "host_deserialize_GBs": round(ct_bytes / t_de / 1e9, 3), "pinned_bytes": len(host)},
+        "roofline": {"bound": "hbm", "achieved": round(pack_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(pack_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "device_pack (headers + one strided copy per component, host time included)",
+                     "ms_per_launch": round(t_pack / args.steps, 4)},
+        "cpu_baseline": None}), flush=True)
     return 0
 
 

@@ -36,7 +36,7 @@ import torch
 
 from . import _native as _nat
 from . import fhe
-from .context import Cipher, CKKSContext
+from .context import Cipher, CKKSContext, u64_cat
 
 __all__ = ["BootstrapSpec", "BootstrapProgram", "Requirements", "Stage", "requirements", "generate", "bootstrap",
            "special_fft_layers", "merge_layers", "chebyshev_divide", "canonical_scales", "evalmod_levels",
@@ -347,7 +347,7 @@ class _PSEval:
             raise ValueError("EvalMod ran out of levels")
         ops = [(self.adjust(a, l), self.adjust(b, l)) for a, b in pairs]
         B = ops[0][0].batch_size
-        side = [[torch.cat([pr[k].cv[c][:, :l] for pr in ops], 0) for c in range(2)] for k in range(2)]
+        side = [[u64_cat([pr[k].cv[c][:, :l] for pr in ops]) for c in range(2)] for k in range(2)]
         both = self.ctx.mul_relin_raw(side[0][0], side[0][1], side[1][0], side[1][1], l, self.ctx.relin_key,
                                       stacked=True)
         x0 = ops[0][0]

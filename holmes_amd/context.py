@@ -65,7 +65,7 @@ class Cipher:
         )
 
     def deep_copy(self) -> "Cipher":
-        return self.cipher_like([c.clone() for c in self.cv])
+        return self.cipher_like([u64_clone(c) for c in self.cv])
 
     def release(self) -> None:
         self.cv = []
@@ -74,6 +74,25 @@ class Cipher:
     def __repr__(self) -> str:
         return (f"Cipher(batch={self.batch_size}, limbs={self.state.cur_limbs}, "
                 f"scale_degree={self.state.scale_degree}, ext={self.is_ext})")
+
+
+def u64_copy(dst: torch.Tensor, src: torch.Tensor) -> torch.Tensor:
+    """dst <- src for uint64 tensors through int64 views: torch's vectorised copy kernels (its
+    uint64 copies take a slow generic path)."""
+
+    dst.view(torch.int64).copy_(src.view(torch.int64))
+    return dst
+
+
+def u64_clone(t: torch.Tensor) -> torch.Tensor:
+    return t.view(torch.int64).clone().view(torch.uint64)
+
+
+def u64_cat(parts, dim: int = 0, out: torch.Tensor | None = None) -> torch.Tensor:
+    if out is not None:
+        torch.cat([x.view(torch.int64) for x in parts], dim, out=out.view(torch.int64))
+        return out
+    return torch.cat([x.view(torch.int64) for x in parts], dim).view(torch.uint64)
 
 
 def _bstride(t: torch.Tensor) -> int:

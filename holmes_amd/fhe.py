@@ -15,7 +15,7 @@ import torch
 
 from . import _native as nat
 from .client import Client
-from .context import Cipher, CipherState, CKKSContext
+from .context import Cipher, CipherState, CKKSContext, u64_cat, u64_clone, u64_copy
 from .params import CKKSContextSpec
 
 __all__ = [
@@ -189,7 +189,7 @@ def rescale(ct: Cipher, ctx: CKKSContext) -> Cipher:
         raise ValueError("rescale needs a non-extended ciphertext with at least two limbs")
     both = _joined(ct.cv, limbs, ctx.N)
     if both is None:
-        both = torch.cat([_view(c, limbs) for c in ct.cv], 0)
+        both = u64_cat([_view(c, limbs) for c in ct.cv])
     out = ctx.rescale_raw(both, limbs)
     B = ct.batch_size
     parts = [out[i * B:(i + 1) * B] for i in range(len(ct.cv))]
@@ -211,7 +211,7 @@ def align_to(ct: Cipher, state: CipherState, ctx: CKKSContext) -> Cipher:
         raise ValueError(f"cannot raise a ciphertext from {limbs} to {target} limbs")
     out = _alloc(ctx, len(ct.cv), ct.batch_size if not ct.is_ext else int(ct.cv[0].shape[0]), target)
     for o, c in zip(out, ct.cv):
-        o.copy_(_view(c, target))
+        u64_copy(o, _view(c, target))
     return ct.cipher_like(out, state=ct.state.replace(cur_limbs=target))
 
 
@@ -242,11 +242,11 @@ def _binary(a: Cipher, b: Cipher, ctx: CKKSContext, op: int) -> Cipher:
         if c < len(a.cv) and c < len(b.cv):
             ctx.poly_op(op, o, _view(a.cv[c], limbs), _view(b.cv[c], limbs), prime_idx=idx)
         elif c < len(a.cv):
-            o.copy_(_view(a.cv[c], limbs))
+            u64_copy(o, _view(a.cv[c], limbs))
         elif op == nat.HCK_OP_SUB:
             ctx.poly_op(nat.HCK_OP_NEG, o, _view(b.cv[c], limbs), prime_idx=idx)
         else:
-            o.copy_(_view(b.cv[c], limbs))
+            u64_copy(o, _view(b.cv[c], limbs))
         out.append(o)
     return a.cipher_like(out, state=a.state.replace(cur_limbs=limbs))
 
@@ -379,7 +379,7 @@ def pack_cipher_batch(ciphers) -> Cipher:
     total = sum(int(c.cv[0].shape[0]) for c in ciphers)
     buf = first.cv[0].new_empty((2, total, rows, first.cv[0].shape[2]))
     for i in range(2):
-        torch.cat([c.cv[i][:, :rows] for c in ciphers], 0, out=buf[i])
+        u64_cat([c.cv[i][:, :rows] for c in ciphers], 0, out=buf[i])
     return first.cipher_like([buf[0], buf[1]], batch_size=total)
 
 
@@ -423,11 +423,11 @@ def fast_rotate(ct: Cipher, offsets, ctx: CKKSContext, output_ext: bool = False)
         o0, o1 = out0[i * B:(i + 1) * B], out1[i * B:(i + 1) * B]
         if off % ctx.max_slots == 0 and off != ctx.M - 1:
             if output_ext:
-                o0.copy_(_lift_ext(c0, limbs, ctx))
-                o1.copy_(_lift_ext(c1, limbs, ctx))
+                u64_copy(o0, _lift_ext(c0, limbs, ctx))
+                u64_copy(o1, _lift_ext(c1, limbs, ctx))
             else:
-                o0.copy_(c0)
-                o1.copy_(c1)
+                u64_copy(o0, c0)
+                u64_copy(o1, c1)
             continue
         g = _galois(off, ctx)
         key = ctx.key_for_galois(g)
@@ -476,8 +476,8 @@ def grouped_pairwise_mac(batch: Cipher, pts: Plaintext, groups: int, ctx: CKKSCo
         b0 = [batch.cv[0][g * m + b:g * m + b + 1] for b in range(m)]
         b1 = [batch.cv[1][g * m + b:g * m + b + 1] for b in range(m)]
         res = ctx.bsgs_mac(b0, b1, p[g * m:(g + 1) * m], n, 1, prime_idx=idx)
-        out0[g].copy_(res[0, 0, 0])
-        out1[g].copy_(res[1, 0, 0])
+        u64_copy(out0[g], res[0, 0, 0])
+        u64_copy(out1[g], res[1, 0, 0])
     st = batch.state
     state = st.replace(scale_degree=int(st.scale_degree) + int(pts.state.scale_degree),
                        scaling_factor=float(st.scaling_factor) * float(pts.state.scaling_factor))
@@ -566,7 +566,7 @@ def hoisted_mac_sum(ct: Cipher, baby_offsets, plaintexts: Plaintext, giant_offse
         for g in range(G - 2, -1, -1):
             acc0, acc1 = ctx.rotate_raw(acc0, acc1, limbs, gk, ctx.key_for_galois(gk), out0=part[0, g],
                                         out1=part[1, g], acc=(part[0, g], part[1, g]))
-        acc0, acc1 = acc0.clone(), acc1.clone()
+        acc0, acc1 = u64_clone(acc0), u64_clone(acc1)
     del part
     st = ct.state
     deg = int(pt_state.scale_degree) if pt_state is not None else 1
@@ -683,7 +683,7 @@ def homo_add_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
     ctx.poly_op(nat.HCK_OP_ADD_SCALAR, out[0], _view(ct.cv[0], limbs), prime_idx=idx,
                 scalar=_scalar_list(enc, limbs))
     for o, x in zip(out[1:], ct.cv[1:]):
-        o.copy_(_view(x, limbs))
+        u64_copy(o, _view(x, limbs))
     return ct.cipher_like(out, state=ct.state.replace(cur_limbs=limbs))
 
 
@@ -701,7 +701,7 @@ def homo_add_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
         p = p.expand(ct.batch_size, -1, -1)
     c0 = ctx.empty(ct.batch_size, limbs, ctx.N)
     ctx.poly_op(nat.HCK_OP_ADD, c0, _view(ct.cv[0], limbs), p.contiguous(), prime_idx=idx)
-    rest = [_view(x, limbs).clone() for x in ct.cv[1:]]
+    rest = [u64_clone(_view(x, limbs)) for x in ct.cv[1:]]
     return ct.cipher_like([c0] + rest, state=ct.state.replace(cur_limbs=limbs))
 
 
@@ -740,7 +740,7 @@ def homo_relinearize(ct: Cipher, ctx: CKKSContext) -> Cipher:
     """Three components back to two: (d0, d1) + KeySwitch_{s^2 -> s}(d2) (kernel_helpers.py:146-152)."""
 
     if len(ct.cv) == 2:
-        return ct.cipher_like([x.clone() for x in ct.cv])
+        return ct.cipher_like([u64_clone(x) for x in ct.cv])
     if len(ct.cv) != 3 or ct.is_ext:
         raise ValueError("relinearize takes a three-component, non-extended ciphertext")
     limbs = _limbs(ct)
