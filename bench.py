@@ -25,6 +25,11 @@ HBM-pooled page: each append is one fused launch of eight polynomial sums into a
 ``--workload wire``: 16 ciphertexts at 24 limbs packed into one device buffer in the wire layout,
 copied to pinned host memory and unpacked again.
 
+``--workload c4``: the encrypted Llama-3-8B MLP block at 128 tokens (RMSNorm, gate/up 4096 ->
+14336, SiLU degree 63, down 14336 -> 4096, one two-pass bootstrap of the output ciphertexts), 24
+limbs, scale 2^50; its line reports seconds per block and the decrypted error against the float64
+oracle of the same arithmetic.
+
 ``--workload bootstrap``: one full-slot bootstrap (N = 2^16, 24 x 50-bit primes, dnum 3, scale
 2^50, sparse ternary secret h = 192, level budget (3, 3)) of a ciphertext at 3 limbs; its line
 reports ms per bootstrap and the precision of the refreshed slots.
@@ -71,10 +76,10 @@ def main() -> int:
     ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
                     help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
                          "(both are hoist strategies of the reference's LinearOperatorConfig)")
-    ap.add_argument("--workload", choices=("c1", "c2", "c3", "mul", "bootstrap", "kv", "wire", "stream"),
+    ap.add_argument("--workload", choices=("c1", "c2", "c3", "c4", "mul", "bootstrap", "kv", "wire", "stream"),
                     default="c2",
                     help="c2: batched key switch (headline); c1: one rotation + rescale (latency); "
-                         "c3: q_proj BSGS projection; mul: 16 ciphertext products with "
+                         "c3: q_proj BSGS projection; c4: encrypted MLP block; mul: 16 ciphertext products with "
                          "relinearisation and rescale at 24 limbs; bootstrap: one full-slot bootstrap "
                          "at 24 limbs; kv: 128 token appends into an HBM-pooled KV page; wire: 16 "
                          "ciphertexts packed into one device buffer and round-tripped through pinned "
@@ -107,6 +112,8 @@ def main() -> int:
         return run_mul(args)
     if args.workload == "bootstrap":
         return run_bootstrap(args)
+    if args.workload == "c4":
+        return run_c4(args)
     if args.workload == "kv":
         return run_kv(args)
     if args.workload == "wire":
@@ -361,25 +368,42 @@ def run_mul(args) -> int:
     return 0
 
 
-# bootstrap: the bytes of one refresh are the HBM floors of the library calls it makes, summed
+# bootstrap / c4: the bytes of one unit are the HBM floors of the library calls it makes, summed
 # from the call log of one run (limb = N x 8 bytes): key switch per item d + add + out (b, a) +
 # its key 2 beta (limbs + K); product with relinearisation 4 in + 2 out per item + the shared key;
-# MAC babies + plaintext rows + partial sums; rescale / ModRaise / weighted sums / elementwise
-# ops and automorphisms their inputs and outputs.
+# MAC babies + plaintext rows + partial sums; rescale / ModRaise / weighted sums / linear
+# combinations / elementwise ops and automorphisms their inputs and outputs.
+class _Shape:
+    __slots__ = ("shape",)
+
+    def __init__(self, shape):
+        self.shape = shape
+
+
 class _CallLog:
     NAMES = ("keyswitch", "rotate_raw", "mul_relin_raw", "relinearize_raw", "bsgs_mac", "rescale_raw",
-             "modraise", "weighted_sum", "poly_op", "automorphism")
+             "modraise", "weighted_sum", "poly_op", "automorphism", "lincomb", "rotate_ext", "moddown")
 
     def __init__(self, ctx):
         self.ctx = ctx
         self.calls = []
+
+    @classmethod
+    def _light(cls, v):
+        """Shapes instead of tensors (the log must not keep a run's intermediates alive)."""
+
+        if hasattr(v, "shape") and hasattr(v, "dtype"):
+            return _Shape(tuple(v.shape))
+        if isinstance(v, (list, tuple)):
+            return [cls._light(x) for x in v]
+        return v
 
     def __enter__(self):
         for name in self.NAMES:
             orig = getattr(self.ctx, name)
 
             def wrap(*a, _orig=orig, _name=name, **k):
-                self.calls.append((_name, a, k))
+                self.calls.append((_name, [self._light(x) for x in a], {kk: self._light(vv) for kk, vv in k.items()}))
                 return _orig(*a, **k)
 
             setattr(self.ctx, name, wrap)
@@ -432,6 +456,16 @@ class _CallLog:
                 total += int(out.shape[0]) * l * (3 if len(a) > 3 and a[3] is not None else 2)
             elif name == "automorphism":
                 total += int(a[0].shape[0]) * 2 * int(a[2])
+            elif name == "rotate_ext":
+                l, B = int(a[2]), int(a[0].shape[0])
+                total += B * (2 * l + 2 * (l + K) * (1 + (k.get("acc") is not None)) + 2 * beta(l) * (l + K))
+                ks.append(("rotation", B, l))
+            elif name == "moddown":
+                l = int(a[1])
+                total += int(a[0].shape[0]) * (2 * l + K)
+            elif name == "lincomb":
+                xs, l, outs = a[0], int(a[1]), a[2]
+                total += (sum(len(r) for r in xs) + len(outs)) * l
         return total, ks
 
 
@@ -700,6 +734,104 @@ def run_wire(args) -> int:
                      "kernel": "device_pack (headers + one strided copy per component, host time included)",
                      "ms_per_launch": round(t_pack / args.steps, 4)},
         "cpu_baseline": None}), flush=True)
+    return 0
+
+
+def run_c4(args) -> int:
+    """C4: one encrypted MLP block (holmes_amd.mlp.FeatureMajorMLPBlock) on 128 tokens x 4096
+    features (16 ciphertexts); weights N(0, 0.02^2) (a randomized Hadamard rotation of i.i.d.
+    Gaussian weights is again i.i.d. Gaussian with the same deviation, so the rotation is not
+    drawn), gamma = 1 + N(0, 0.1^2), x ~ N(0, 1)."""
+
+    import math
+
+    import torch
+
+    from holmes_amd import bootstrap as bs
+    from holmes_amd import fhe, mlp
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+    from holmes_amd.linear import LinearOperatorConfig
+
+    seed = 20261204
+    steps = int(args.steps) if args.steps != 20 else 1
+    warmup = int(args.warmup) if args.warmup != 3 else 1
+    t0 = time.perf_counter()
+    spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, scale_bits=50,
+                               secret_key_dist="SPARSE_TERNARY", hamming_weight=192, seed=seed)
+    client, ctx = fhe.generate_client_context(spec)
+    mspec = mlp.MLPBlockSpec()
+    layout = FeatureMajorPrefillLayout()
+    cfg = LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512,
+                               hoist_strategy="ext_double_hoist")
+    bspec = bs.BootstrapSpec(log_slots=15, level_budget=(3, 3))
+    rots = set(mlp.FeatureMajorMLPBlock.rotations(mspec, layout, cfg)) | set(bs.requirements(bspec, 16).rotations)
+    client.generate_rotation_keys(sorted(rots))
+    prog = bs.generate(ctx, bspec)
+    rng = np.random.default_rng(seed)
+    D, Iw = mspec.hidden_dim, mspec.intermediate_width
+    gate = rng.normal(scale=0.02, size=(Iw, D))
+    up = rng.normal(scale=0.02, size=(Iw, D))
+    down = rng.normal(scale=0.02, size=(D, Iw))
+    gamma = 1.0 + 0.1 * rng.normal(size=D)
+    block = mlp.FeatureMajorMLPBlock(ctx, gate, up, down, norm_weight=gamma, spec=mspec, layout=layout, config=cfg,
+                                     bootstrap_program=prog)
+    x = rng.normal(size=(128, D))
+    cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
+    _log(f"c4 setup {time.perf_counter() - t0:.1f} s: {len(rots)} rotation keys, {mspec.pages} feature pages")
+    for _ in range(warmup):
+        block.forward(cts)
+    with _CallLog(ctx) as log:
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        out, stages = block.forward(cts)
+        torch.cuda.synchronize()
+        s_logged = time.perf_counter() - w0
+    limbs_moved, ks = log.limbs_bytes()
+    block_bytes = limbs_moved * ctx.N * 8
+    secs = []
+    for _ in range(steps):
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        out, stages = block.forward(cts)
+        torch.cuda.synchronize()
+        secs.append(time.perf_counter() - w0)
+    s_wall = float(np.median(secs)) if secs else s_logged
+    want = layout.pack(mlp.mlp_block_numpy(x, gate, up, down, gamma, mspec))
+    err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
+    _log(f"c4: {s_wall:.3f} s per block, stages {stages}, decrypted max error {err:.3e}")
+    ks_items = sum(b for _, b, _ in ks)
+    cpu = None
+    if not args.no_cpu:
+        from oracle import oracle as O
+
+        orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+        g = ctx.galois_element(1)
+        okey = orc.make_ksk(*client.key_inputs(g))
+        xr = [np.stack([rng.integers(0, ctx.primes[i], ctx.N, dtype=np.uint64) for i in range(16)]) for _ in range(2)]
+        t = time.perf_counter()
+        orc.rotate(16, g, xr[0], xr[1], okey)
+        t_rot = time.perf_counter() - t
+        total = sum(b * t_rot * l / 16 for _, b, l in ks)
+        cpu = {"value": round(total, 1), "unit": "s", "cores": int(O.num_threads()), "kind": "port",
+               "sample": f"extrapolated from the key switches alone: one rotation at 16 limbs ({t_rot:.3f} s), scaled "
+                         f"by limbs, over the {ks_items} key-switched items of one block (MACs, encodes, "
+                         f"rescales not counted)"}
+    achieved = block_bytes / s_wall / 1e9
+    print(json.dumps({
+        "metric": "s per encrypted Llama-3-8B MLP block (C4: 128 tokens, 4096 -> 14336 -> 4096, one bootstrap)",
+        "value": round(s_wall, 4), "unit": "s", "n_gpus": 1, "steps": steps, "warmup": warmup,
+        "ms_per_step": round(s_wall * 1e3, 2), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "u64", "data": "synthetic",
+        "config": {"workload": "C4 MLP block: RMSNorm (deg-15 rsqrt), gate/up 4 pages x 4096x4096 BSGS, SiLU deg 63 "
+                               "on [-16,16], down, two-pass bootstrap of 16 cts; 24 limbs, scale 2^50, dnum 3",
+                   "decrypted_max_error": err, "error_bits": round(-math.log2(err), 2),
+                   "stage_seconds": {k: round(v, 4) for k, v in stages.items()},
+                   "key_switched_items": ks_items, "algorithmic_bytes_per_step": block_bytes},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "whole block (call-log algorithmic bytes: keys, diagonals, inputs/outputs of each call)",
+                     "ms_per_launch": round(s_wall * 1e3, 2)},
+        "cpu_baseline": cpu}), flush=True)
     return 0
 
 

@@ -472,12 +472,14 @@ class CKKSContext:
         """out[g] = sum_t w[t] * xs[g][t] over the first ``limbs`` Q primes: ``xs`` is [groups][terms]
         single polynomials ([limbs'][N] or [1][limbs'][N] views, limbs' >= limbs, any allocation),
         ``outs`` one polynomial per group, ``weights`` a [terms][limbs] uint64 GPU table of residues
-        (None: unit weights).  One launch (hck_lincomb)."""
+        (None: unit weights).  One hck_lincomb launch per 64 groups (or 256 operands)."""
 
         G = len(xs)
         if G != len(outs) or G < 1:
             raise ValueError("one output per group")
         T = len(xs[0])
+        if T > 256:
+            raise ValueError("at most 256 terms per linear combination")
         ptrs = []
         for row in xs:
             if len(row) != T:
@@ -493,9 +495,12 @@ class CKKSContext:
                     or weights.device.type != "cuda"):
                 raise ValueError(f"weights must be a contiguous [{T}][{limbs}] uint64 GPU table")
             wp = weights.data_ptr()
-        nat.check(nat.lib().hck_lincomb(self._h, int(limbs), G, T, nat.ptr_array(ptrs), wp,
-                                        nat.ptr_array([o.data_ptr() for o in outs]), _stream_ptr(self.device)),
-                  "hck_lincomb")
+        per = max(1, min(64, 256 // T))  # the kernel's pointer-list capacity per launch
+        optr = [o.data_ptr() for o in outs]
+        for g0 in range(0, G, per):
+            g1 = min(G, g0 + per)
+            nat.check(nat.lib().hck_lincomb(self._h, int(limbs), g1 - g0, T, nat.ptr_array(ptrs[g0 * T:g1 * T]), wp,
+                                            nat.ptr_array(optr[g0:g1]), _stream_ptr(self.device)), "hck_lincomb")
         return outs
 
     def moddown(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:

@@ -302,13 +302,10 @@ def homo_mul_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
     if p.shape[0] not in (1, ct.batch_size):
         raise ValueError("plaintext batch must be 1 or the ciphertext batch")
     if p.shape[0] == 1 and ct.batch_size > 1:
-        p = p.expand(ct.batch_size, -1, -1)
-    p = p.contiguous()
-    out = []
-    for x in ct.cv:
-        o = ctx.empty(x.shape[0], limbs, ctx.N)
+        p = p.expand(ct.batch_size, -1, -1)  # batch stride 0: one plaintext for every item
+    out = _alloc(ctx, len(ct.cv), int(ct.cv[0].shape[0]), limbs)
+    for o, x in zip(out, ct.cv):
         ctx.poly_op(nat.HCK_OP_MUL, o, _view(x, limbs), p, prime_idx=idx)
-        out.append(o)
     st = ct.state
     state = st.replace(
         cur_limbs=limbs,

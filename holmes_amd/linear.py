@@ -26,7 +26,7 @@ import torch
 
 from . import _native as nat
 from . import fhe
-from .context import Cipher, CipherState, CKKSContext
+from .context import Cipher, CipherState, CKKSContext, u64_cat
 
 _HOIST_STRATEGIES = {"normal", "ext_normal", "ext_double_hoist"}
 
@@ -257,8 +257,8 @@ def _stack(ciphers) -> tuple[torch.Tensor, torch.Tensor, CipherState]:
     if len(states) != 1:
         raise ValueError("linear inputs must enter at one common level and scale.")
     limbs = ciphers[0].state.cur_limbs
-    c0 = torch.cat([c.cv[0][:, :limbs] for c in ciphers], 0).contiguous()
-    c1 = torch.cat([c.cv[1][:, :limbs] for c in ciphers], 0).contiguous()
+    c0 = u64_cat([c.cv[0][:, :limbs] for c in ciphers])
+    c1 = u64_cat([c.cv[1][:, :limbs] for c in ciphers])
     return c0, c1, ciphers[0].state
 
 
@@ -294,12 +294,27 @@ class LinearOperator:
         # rotate-and-add in one pass, written over the addend
         return ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g), out0=acc[0], out1=acc[1], acc=acc)
 
+    def prepare(self, input_ciphers, dimension: int):
+        """The inputs stacked into one batch and their baby rotations (each offset one batched
+        rotation over all inputs), for every projection of the same inputs to share."""
+
+        inputs = tuple(input_ciphers)
+        ctx = self._ctx()
+        plan = self.plan(dimension)
+        x0, x1, state = _stack(inputs)
+        xc = Cipher([x0, x1], state, slots=inputs[0].slots)
+        babies = fhe.prepare_hoisted_baby_rotations(xc, plan.baby_offsets, ctx,
+                                                    strategy=str(self.config.hoist_strategy).lower(),
+                                                    baby_anchor_step=int(plan.baby_anchor_step))
+        return {"inputs": inputs, "stacked": xc, "babies": babies, "plan": plan.cache_key}
+
     def apply(self, input_ciphers, weight: LinearWeight, *, chunk_indices=None, rescale: bool = True,
-              weight_scale: float | None = None):
+              weight_scale: float | None = None, prepared: dict | None = None):
         """BSGS projection of every input; returns (outputs, stage_seconds).
 
         Weights are encoded at ``weight_scale`` (default: the prime the final rescale divides by,
-        so the output returns to the input scale)."""
+        so the output returns to the input scale).  ``prepared`` (from ``prepare`` on the same
+        inputs and dimension) reuses their baby rotations."""
 
         if self._closed:
             raise RuntimeError("linear operator is closed.")
@@ -311,17 +326,20 @@ class LinearOperator:
         ctx = self._ctx()
         plan = self.plan(weight.dimension)
         chunks = plan.chunks if chunk_indices is None else tuple(plan.chunks[int(i)] for i in chunk_indices)
-        x0, x1, state = _stack(inputs)
+        if prepared is None:
+            prepared = self.prepare(inputs, weight.dimension)
+        elif prepared["plan"] != plan.cache_key or len(prepared["inputs"]) != len(inputs) or any(
+                a is not b for a, b in zip(prepared["inputs"], inputs)):
+            raise ValueError("prepared rotations belong to other inputs or another plan")
+        xc, babies = prepared["stacked"], prepared["babies"]
+        state = xc.state
         limbs = int(state.cur_limbs)
         if rescale and limbs < 2:
             raise ValueError("rescale needs at least two limbs")
         wscale = float(ctx.rescale_divisor_at(limbs)) if weight_scale is None else float(weight_scale)
         idx = ctx.q_prime_idx(limbs)
         strategy = str(self.config.hoist_strategy).lower()
-        xc = Cipher([x0, x1], state, slots=inputs[0].slots)
-        # baby rotations, each batched over all inputs with that offset's key
-        babies = fhe.prepare_hoisted_baby_rotations(xc, plan.baby_offsets, ctx, strategy=strategy,
-                                                    baby_anchor_step=int(plan.baby_anchor_step))
+        x0 = xc.cv[0]
         total0 = total1 = None
         # encode overflow flags of every chunk, read back once after the last chunk
         flags = torch.zeros(int(plan.max_plaintext_rows), dtype=torch.int32, device=x0.device)
@@ -352,7 +370,7 @@ class LinearOperator:
                                   scaling_factor=float(state.scaling_factor) * wscale)
         slots = inputs[0].slots
         if rescale:
-            both = ctx.rescale_raw(torch.cat([total0, total1], 0), limbs)
+            both = ctx.rescale_raw(u64_cat([total0, total1]), limbs)
             n_in = total0.shape[0]
             total0, total1 = both[:n_in], both[n_in:]
             out_state = out_state.replace(cur_limbs=limbs - 1, scale_degree=int(state.scale_degree),

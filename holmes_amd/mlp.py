@@ -1,0 +1,181 @@
+"""Encrypted Llama-3 MLP block in the feature-major layout (llama3fhe/operators/linear/prefill/
+mlp.py:37-135,373-519,723-1355; norm/rmsnorm.py; nonlinear/elementwise.py).
+
+    y   = RMSNorm(x)                    (polynomial inverse square root, gamma folded into gate/up)
+    g_p = y W_gate[p]^T,  u_p = y W_up[p]^T      for every 4096-feature page p of the 14336 features
+    h_p = SiLU(g_p) * u_p               (SiLU a Chebyshev series on an interval)
+    out = sum_p h_p W_down[:, p]^T
+    out = 2^r * Bootstrap(2^-r * out)   (optional; the refresh a layer pipeline continues from)
+
+Pages follow the reference's FeatureMajorMLPLayout: the intermediate width is cut into pages of
+hidden_dim features, each page laid out like the canonical activation (16 ciphertexts for 128
+tokens), the last page zero-padded.  Every projection is a 4096 x 4096 BSGS product of this
+backend's LinearOperator; the gate and up projections of every page share the inputs' baby
+rotations.  The SiLU of all pages runs as one batch of page x cipher ciphertexts (each product of
+the Paterson-Stockmeyer evaluation one batched key switch).  The reference pairs token ciphertexts
+as x + i y and projects gate + i up in one complex product (half the projections); this block keeps
+the real pages.
+
+``mlp_block_numpy`` is the float64 oracle of the same arithmetic (the same polynomials), so the
+decrypted output measures the encryption and key-switching error only.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import fhe
+from .context import CKKSContext
+from .layouts import FeatureMajorPrefillLayout
+from .linear import LinearOperator, LinearOperatorConfig, LinearWeight, bsgs_rotations
+from .norm import rmsnorm_coefficients, rmsnorm_fhe, rmsnorm_numpy, rmsnorm_rotations
+from .polynomial import chebyshev_coefficients, eval_chebyshev
+
+__all__ = ["MLPBlockSpec", "FeatureMajorMLPBlock", "mlp_block_numpy", "silu_coefficients"]
+
+
+def silu_coefficients(degree: int = 63, interval=(-16.0, 16.0)) -> np.ndarray:
+    """Chebyshev interpolant of x sigma(x) on ``interval`` (nonlinear/elementwise.py's SiLU)."""
+
+    return chebyshev_coefficients(lambda x: x / (1.0 + np.exp(-x)), degree, interval)
+
+
+@dataclass(frozen=True)
+class MLPBlockSpec:
+    hidden_dim: int = 4096
+    intermediate_width: int = 14336
+    silu_degree: int = 63
+    silu_interval: tuple = (-16.0, 16.0)
+    rms_degree: int = 15
+    rms_interval: tuple = (0.5, 2.0)
+    eps: float = 1e-5
+    bootstrap_prescale_bits: int = 5      # |out| <= 2^5 before the refresh
+    bootstrap_iterations: int = 2
+
+    @property
+    def pages(self) -> int:
+        return -(-int(self.intermediate_width) // int(self.hidden_dim))
+
+
+def _page(weight: np.ndarray, p: int, D: int, rows: bool) -> np.ndarray:
+    """The D x D block of page p: gate/up rows p D .. (p + 1) D, down columns likewise."""
+
+    out = np.zeros((D, D), dtype=np.float64)
+    if rows:
+        blk = weight[p * D:(p + 1) * D]
+        out[:blk.shape[0]] = blk
+    else:
+        blk = weight[:, p * D:(p + 1) * D]
+        out[:, :blk.shape[1]] = blk
+    return out
+
+
+def mlp_block_numpy(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray,
+                    norm_weight: np.ndarray | None = None, spec: MLPBlockSpec = MLPBlockSpec()) -> np.ndarray:
+    """float64 oracle of the block with the same polynomials (bootstrap excluded: exact)."""
+
+    rms = rmsnorm_coefficients(spec.rms_degree, spec.rms_interval, spec.eps)
+    y = rmsnorm_numpy(x, norm_weight, rms)
+    g = y @ np.asarray(gate, dtype=np.float64).T
+    u = y @ np.asarray(up, dtype=np.float64).T
+    a, b = spec.silu_interval
+    s = np.polynomial.chebyshev.chebval((2.0 * g - (a + b)) / (b - a), silu_coefficients(spec.silu_degree,
+                                                                                        spec.silu_interval))
+    return (s * u) @ np.asarray(down, dtype=np.float64).T
+
+
+class FeatureMajorMLPBlock:
+    """The block's weights on the device (gamma folded into gate and up) and its schedule."""
+
+    def __init__(self, ctx: CKKSContext, gate: np.ndarray, up: np.ndarray, down: np.ndarray, *,
+                 norm_weight: np.ndarray | None = None, spec: MLPBlockSpec = MLPBlockSpec(),
+                 layout: FeatureMajorPrefillLayout | None = None, config: LinearOperatorConfig | None = None,
+                 bootstrap_program=None):
+        D, Iw = int(spec.hidden_dim), int(spec.intermediate_width)
+        if gate.shape != (Iw, D) or up.shape != (Iw, D) or down.shape != (D, Iw):
+            raise ValueError(f"expected gate/up [{Iw}][{D}] and down [{D}][{Iw}]")
+        self.ctx = ctx
+        self.spec = spec
+        self.layout = FeatureMajorPrefillLayout(seq_len=128, hidden_dim=D, slots=ctx.max_slots) if layout is None \
+            else layout
+        self.config = LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512,
+                                           hoist_strategy="ext_double_hoist") if config is None else config
+        self.op = LinearOperator(crypto_context=ctx, token_lanes=self.layout.tokens_per_cipher, config=self.config)
+        col = np.ones(D) if norm_weight is None else np.asarray(norm_weight, dtype=np.float64).reshape(-1)
+        gate = np.asarray(gate, dtype=np.float64) * col[None, :]
+        up = np.asarray(up, dtype=np.float64) * col[None, :]
+        self.gate = [LinearWeight(_page(gate, p, D, True), crypto_context=ctx) for p in range(spec.pages)]
+        self.up = [LinearWeight(_page(up, p, D, True), crypto_context=ctx) for p in range(spec.pages)]
+        self.down = [LinearWeight(_page(np.asarray(down, dtype=np.float64), p, D, False), crypto_context=ctx)
+                     for p in range(spec.pages)]
+        self.rms = rmsnorm_coefficients(spec.rms_degree, spec.rms_interval, spec.eps)
+        self.silu = silu_coefficients(spec.silu_degree, spec.silu_interval)
+        self.bootstrap_program = bootstrap_program
+
+    @staticmethod
+    def rotations(spec: MLPBlockSpec, layout: FeatureMajorPrefillLayout, config: LinearOperatorConfig) -> tuple:
+        """Slot rotations the block uses (the bootstrap program's come from its requirements)."""
+
+        plan = config.plan(dimension=int(spec.hidden_dim), token_lanes=layout.tokens_per_cipher)
+        return tuple(sorted(set(bsgs_rotations(plan, config.hoist_strategy)) | set(rmsnorm_rotations(layout))))
+
+    def forward(self, x_cts):
+        """Outputs (one ciphertext per input) and the seconds of each stage."""
+
+        import torch
+
+        from . import bootstrap as bs
+
+        ctx, spec = self.ctx, self.spec
+        t: dict = {}
+
+        def mark(name, t0):
+            torch.cuda.synchronize()
+            t[name] = time.perf_counter() - t0
+            return time.perf_counter()
+
+        t0 = time.perf_counter()
+        y = rmsnorm_fhe(x_cts, None, coeffs=self.rms, layout=self.layout, crypto_context=ctx).outputs
+        t0 = mark("rmsnorm", t0)
+        prep = self.op.prepare(y, spec.hidden_dim)
+        gates, ups = [], []
+        for p in range(spec.pages):
+            gates += list(self.op.project(y, self.gate[p], prepared=prep))
+            ups += list(self.op.project(y, self.up[p], prepared=prep))
+        del prep
+        t0 = mark("gate_up", t0)
+        g = fhe.pack_cipher_batch(gates)
+        s = eval_chebyshev(g, self.silu, ctx, interval=spec.silu_interval)
+        u = fhe.pack_cipher_batch(ups)
+        u = fhe.align_to(u, u.state.replace(cur_limbs=int(s.state.cur_limbs)), ctx)
+        h = fhe.rescale(fhe.homo_mul_relin(s, u, ctx), ctx)
+        del g, s, u, gates, ups
+        t0 = mark("silu_product", t0)
+        n = len(x_cts)
+        out = None
+        for p in range(spec.pages):
+            hp = [fhe.cipher_batch_item(h, p * n + i) for i in range(n)]
+            part = self.op.project(hp, self.down[p])
+            out = list(part) if out is None else [fhe.homo_add(a, b, ctx) for a, b in zip(out, part)]
+        t0 = mark("down", t0)
+        if self.bootstrap_program is not None:
+            r = int(spec.bootstrap_prescale_bits)
+            refreshed = []
+            for c in out:
+                limbs = int(c.state.cur_limbs)
+                enc = fhe.encode_scalar(2.0 ** -r, cur_limbs=limbs, scale_degree=1,
+                                        scaling_factor=float(ctx.rescale_divisor_at(limbs)), context=ctx)
+                small = fhe.rescale(fhe.homo_mul_scalar(c, enc, ctx), ctx)
+                small = small.cipher_like(small.cv, state=small.state.replace(scaling_factor=c.state.scaling_factor))
+                fresh = bs.bootstrap_with_correction(small, ctx, self.bootstrap_program,
+                                                     iterations=int(spec.bootstrap_iterations), precision_bits=12)
+                back = fhe.encode_scalar(1 << r, cur_limbs=int(fresh.state.cur_limbs), scale_degree=0,
+                                         mode="integer", context=ctx)
+                refreshed.append(fhe.homo_mul_scalar(fresh, back, ctx))
+            out = refreshed
+            t0 = mark("bootstrap", t0)
+        return tuple(out), t
