@@ -761,8 +761,7 @@ def run_c4(args) -> int:
     client, ctx = fhe.generate_client_context(spec)
     mspec = mlp.MLPBlockSpec()
     layout = FeatureMajorPrefillLayout()
-    cfg = LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512,
-                               hoist_strategy="ext_double_hoist")
+    cfg = mlp.default_config()
     bspec = bs.BootstrapSpec(log_slots=15, level_budget=(3, 3))
     rots = set(mlp.FeatureMajorMLPBlock.rotations(mspec, layout, cfg)) | set(bs.requirements(bspec, 16).rotations)
     client.generate_rotation_keys(sorted(rots))
@@ -822,7 +821,7 @@ def run_c4(args) -> int:
         "value": round(s_wall, 4), "unit": "s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(s_wall * 1e3, 2), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "u64", "data": "synthetic",
-        "config": {"workload": "C4 MLP block: RMSNorm (deg-15 rsqrt), gate/up 4 pages x 4096x4096 BSGS, SiLU deg 63 "
+        "config": {"workload": "C4 MLP block: RMSNorm (deg-15 rsqrt), gate/up 4 pages x 4096x4096 BSGS (baby 64), SiLU deg 63 "
                                "on [-16,16], down, two-pass bootstrap of 16 cts; 24 limbs, scale 2^50, dnum 3",
                    "decrypted_max_error": err, "error_bits": round(-math.log2(err), 2),
                    "stage_seconds": {k: round(v, 4) for k, v in stages.items()},

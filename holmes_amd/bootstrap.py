@@ -35,7 +35,7 @@ import numpy as np
 import torch
 
 from . import fhe
-from .context import Cipher, CKKSContext
+from .context import Cipher, CKKSContext, u64_clone
 from .polynomial import PSEvaluator as _PSEval
 from .polynomial import _baby_size, canonical_scales, chebyshev_divide  # noqa: F401
 
@@ -374,35 +374,45 @@ def _rotate_many(c0: torch.Tensor, c1: torch.Tensor, offsets, limbs: int, ctx: C
 
 
 def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: bool = True) -> Cipher:
-    """One stage on a one-item cipher, without a rescale: the baby rotations as one batched key
-    switch, the baby-step MAC of every giant row with the diagonals encoded at ``pt_scale``, the
-    giant rotations as a second batched key switch and their sum.  The slots become the stage
-    applied to the slots; the scaling factor is multiplied by ``pt_scale`` (the caller rescales,
-    possibly after further stages: a rotation's key-switch noise is then small against the still
-    unrescaled message)."""
+    """One stage on every item of ``x``, without a rescale: the baby rotations of all items as
+    one batched key switch (a Galois element per item), the baby-step MAC of every giant row with
+    the diagonals encoded at ``pt_scale`` for all items at once, the giant rotations of all items
+    as a second batched key switch, and their sums (one linear-combination launch).  The slots
+    become the stage applied to the slots; the scaling factor is multiplied by ``pt_scale`` (the
+    caller rescales, possibly after further stages: a rotation's key-switch noise is then small
+    against the still unrescaled message)."""
 
     limbs = int(x.state.cur_limbs)
-    n = ctx.max_slots
+    B = int(x.batch_size)
     c0, c1 = x.cv[0][:, :limbs].contiguous(), x.cv[1][:, :limbs].contiguous()
     nb = st.n1 - 1
-    b0, b1 = _rotate_many(c0.expand(nb, -1, -1), c1.expand(nb, -1, -1),
-                          [k1 * st.h_min for k1 in range(1, st.n1)], limbs, ctx)
+    offs = [k1 * st.h_min for k1 in range(1, st.n1) for _ in range(B)]  # offset-major, then item
+    if B == 1:
+        r0, r1 = c0.expand(nb, -1, -1), c1.expand(nb, -1, -1)  # batch stride 0: one input, every offset
+    else:
+        r0, r1 = (u64_clone(c.view(torch.int64).unsqueeze(0).expand(nb, B, limbs, ctx.N).reshape(nb * B, limbs,
+                                                                                            ctx.N).view(torch.uint64))
+                  for c in (c0, c1))
+    b0, b1 = _rotate_many(r0, r1, offs, limbs, ctx)
+    del r0, r1
     pts = _stage_plaintexts(st, limbs, pt_scale, ctx, keep)
-    res = ctx.bsgs_mac([c0] + [b0[i:i + 1] for i in range(nb)], [c1] + [b1[i:i + 1] for i in range(nb)],
-                       pts, limbs, len(st.giants))  # [2][G][1][limbs][N]
-    del b0, b1
+    res = ctx.bsgs_mac([c0] + [b0[i * B:(i + 1) * B] for i in range(nb)],
+                       [c1] + [b1[i * B:(i + 1) * B] for i in range(nb)], pts, limbs, len(st.giants))
+    del b0, b1  # res: [2][G][B][limbs][N]
     first = 1 if st.giants[0] == 0 else 0
     rot = st.giants[first:]
-    acc = fhe._alloc(ctx, 2, 1, limbs)
-    xs = [[res[c, 0, 0]] if first else [] for c in range(2)]
+    acc = fhe._alloc(ctx, 2, B, limbs)
+    xs = [[res[c, 0, b]] if first else [] for c in range(2) for b in range(B)]
     if rot:
-        g0, g1 = _rotate_many(res[0, first:, 0], res[1, first:, 0], [k2 * st.n1 * st.h_min for k2 in rot],
-                              limbs, ctx)
-        xs[0] += [g0[i] for i in range(len(rot))]
-        xs[1] += [g1[i] for i in range(len(rot))]
-    ctx.lincomb(xs, limbs, [acc[0][0], acc[1][0]])
+        G = len(rot)
+        g0, g1 = _rotate_many(res[0, first:].reshape(G * B, limbs, ctx.N), res[1, first:].reshape(G * B, limbs, ctx.N),
+                              [k2 * st.n1 * st.h_min for k2 in rot for _ in range(B)], limbs, ctx)
+        for c, gc in enumerate((g0, g1)):
+            for b in range(B):
+                xs[c * B + b] += [gc[i * B + b] for i in range(G)]
+    ctx.lincomb(xs, limbs, [acc[c][b] for c in range(2) for b in range(B)])
     s = x.state
-    return x.cipher_like(acc, batch_size=1,
+    return x.cipher_like(acc, batch_size=B,
                          state=s.replace(scale_degree=int(s.scale_degree) + 1,
                                          scaling_factor=float(s.scaling_factor) * float(pt_scale)))
 
@@ -426,15 +436,21 @@ def _rescale_times(ct: Cipher, times: int, scale: float, ctx: CKKSContext) -> Ci
     return ct.cipher_like(ct.cv, state=ct.state.replace(scaling_factor=float(scale), scale_degree=1))
 
 
+def _items(ct: Cipher, lo: int, hi: int) -> Cipher:
+    return ct.cipher_like([c[lo:hi] for c in ct.cv], batch_size=hi - lo)
+
+
 def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram) -> Cipher:
-    """Refresh ``cipher`` (one item, two components, >= 2 limbs, full slots, |slot| <= 1) to
-    ``spec.output_levels`` limbs (0: all the program leaves).  The result keeps the input's
-    scaling factor; the input is not consumed."""
+    """Refresh ``cipher`` (two components, >= 2 limbs, full slots, |slot| <= 1; a batch is refreshed
+    as one: every key switch of the pipeline covers all its items) to ``spec.output_levels`` limbs
+    (0: all the program leaves).  The result keeps the input's scaling factor; the input is not
+    consumed."""
 
     ctx = context
     spec = program.spec
-    if cipher.is_ext or len(cipher.cv) != 2 or cipher.batch_size != 1:
-        raise ValueError("bootstrap takes one two-component, non-extended ciphertext")
+    if cipher.is_ext or len(cipher.cv) != 2:
+        raise ValueError("bootstrap takes a two-component, non-extended ciphertext")
+    B = int(cipher.batch_size)
     if int(cipher.state.cur_limbs) < 2:
         raise ValueError("bootstrap needs at least two limbs (one is spent scaling the message down)")
     if int(cipher.slots) != ctx.max_slots:
@@ -467,7 +483,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram) -
     y = ev.evaluate(program.cheb)
     for _ in range(int(spec.double_angle)):
         y = ev.double_minus(y, y)
-    yr, yi = fhe.cipher_batch_item(y, 0), fhe.cipher_batch_item(y, 1)
+    yr, yi = _items(y, 0, B), _items(y, B, 2 * B)
     z = fhe.homo_add(yr, fhe.homo_mul_i(yi, ctx), ctx)
     # 6. SlotToCoeff (q_0 / (2 pi S_out) in the shares), b2 rescales, the integer 2^bits
     z = _rescale_times(apply_stages(z, program.stc, program.stc_rho, ctx, keep), b2, S_in * 2.0**-bits, ctx)

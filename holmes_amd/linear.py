@@ -218,20 +218,31 @@ def bsgs_rotations(plan: LinearPlan, strategy: str = "normal") -> tuple[int, ...
 
 
 class LinearWeight:
-    """A square weight held on the device; packs and encodes one chunk's diagonals on demand."""
+    """A square weight held on the device; packs and encodes one chunk's diagonals on demand.
+    ``imag`` (same shape) makes the weight complex, weight + i imag: its diagonals are encoded as
+    complex slots (the gate + i up projection of the paired MLP, llama3fhe/operators/linear/prefill/
+    mlp.py:461-468)."""
 
-    def __init__(self, weight: np.ndarray, *, crypto_context: CKKSContext):
+    def __init__(self, weight: np.ndarray, *, crypto_context: CKKSContext, imag: np.ndarray | None = None):
         w = np.asarray(weight)
         if w.ndim != 2 or w.shape[0] != w.shape[1]:
             raise ValueError("LinearWeight expects a square matrix.")
+        if imag is not None and np.asarray(imag).shape != w.shape:
+            raise ValueError("the imaginary part must have the weight's shape")
         self.crypto_context = crypto_context
         self.dimension = int(w.shape[0])
-        self._w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float64)).to(crypto_context.device)
+        dev = crypto_context.device
+        self._w = torch.from_numpy(np.ascontiguousarray(w, dtype=np.float64)).to(dev)
+        self._wi = None if imag is None else torch.from_numpy(np.ascontiguousarray(imag, dtype=np.float64)).to(dev)
         self._closed = False
 
     @property
     def closed(self) -> bool:
         return self._closed
+
+    @property
+    def is_complex(self) -> bool:
+        return self._wi is not None
 
     def plaintext(self, plan: LinearPlan, chunk: LinearChunk, *, limbs: int, scale: float,
                   flags: torch.Tensor | None = None) -> torch.Tensor:
@@ -241,13 +252,19 @@ class LinearWeight:
         if self._closed:
             raise RuntimeError("linear weight is closed")
         ctx = self.crypto_context
-        rows = ctx.pack_diagonals(self._w, lanes=plan.token_lanes, lane_shift=plan.lane_shift,
-                                  baby_steps=plan.baby_steps, giant_base=chunk.giant_base,
-                                  giant_count=chunk.giant_count)
-        return ctx.encode_real(rows, scale, limbs, flags=flags)
+
+        def rows(w):
+            return ctx.pack_diagonals(w, lanes=plan.token_lanes, lane_shift=plan.lane_shift,
+                                      baby_steps=plan.baby_steps, giant_base=chunk.giant_base,
+                                      giant_count=chunk.giant_count)
+
+        if self._wi is None:
+            return ctx.encode_real(rows(self._w), scale, limbs, flags=flags)
+        return ctx.encode(rows(self._w), scale, limbs, values_im=rows(self._wi), flags=flags)
 
     def close(self) -> None:
         self._w = None
+        self._wi = None
         self._closed = True
 
 

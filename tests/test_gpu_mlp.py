@@ -2,7 +2,8 @@
 24 x 50-bit limbs, scale 2^50, sparse secret): RMSNorm (degree-15 inverse square root), gate/up
 projections over two feature pages (the second half zero-padded), SiLU (degree-63 Chebyshev on
 [-16, 16]), the product, the down projection, and the two-pass bootstrap of the output -- every
-decrypted slot within 2^-16 of the float64 oracle that applies the same polynomials."""
+decrypted slot within 2^-16 of the float64 oracle that applies the same polynomials; both carriers
+(token ciphertexts paired as x + i y with one gate + i up projection per page, and real pages)."""
 
 import math
 
@@ -25,11 +26,9 @@ def env():
     mspec = mlp.MLPBlockSpec(intermediate_width=6144)
     bspec = bs.BootstrapSpec(log_slots=15, level_budget=(3, 3))
     from holmes_amd.layouts import FeatureMajorPrefillLayout
-    from holmes_amd.linear import LinearOperatorConfig
 
     layout = FeatureMajorPrefillLayout()
-    cfg = LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512,
-                               hoist_strategy="ext_double_hoist")
+    cfg = mlp.default_config()
     rots = set(mlp.FeatureMajorMLPBlock.rotations(mspec, layout, cfg)) | set(bs.requirements(bspec, 16).rotations)
     client.generate_rotation_keys(sorted(rots))
     prog = bs.generate(ctx, bspec)
@@ -43,11 +42,22 @@ def env():
     x = rng.normal(size=(128, D))
     cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
     want = layout.pack(mlp.mlp_block_numpy(x, gate, up, down, gamma, mspec))
-    return mlp, client, ctx, block, cts, want
+    real = mlp.FeatureMajorMLPBlock(ctx, gate, up, down, norm_weight=gamma, layout=layout, config=cfg,
+                                    spec=mlp.MLPBlockSpec(intermediate_width=6144, paired=False))
+    return mlp, client, ctx, block, cts, want, real
+
+
+def test_real_pages_agree(env):
+    # the separate gate / up projections on real token ciphertexts: the same block, the other carrier
+    mlp, client, ctx, block, cts, want, real = env
+    out, times = real.forward(cts)
+    err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
+    print(f"MLP block (real pages): max error 2^{math.log2(err):.1f}, stages {times}")
+    assert err < 2.0**-16
 
 
 def test_mlp_block_without_refresh(env):
-    mlp, client, ctx, block, cts, want = env
+    mlp, client, ctx, block, cts, want, real = env
     prog, block.bootstrap_program = block.bootstrap_program, None
     try:
         out, times = block.forward(cts)
@@ -60,7 +70,7 @@ def test_mlp_block_without_refresh(env):
 
 
 def test_mlp_block_with_refresh(env):
-    mlp, client, ctx, block, cts, want = env
+    mlp, client, ctx, block, cts, want, real = env
     out, times = block.forward(cts)
     assert out[0].state.cur_limbs == 8
     err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
