@@ -440,11 +440,12 @@ def _items(ct: Cipher, lo: int, hi: int) -> Cipher:
     return ct.cipher_like([c[lo:hi] for c in ct.cv], batch_size=hi - lo)
 
 
-def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram) -> Cipher:
-    """Refresh ``cipher`` (two components, >= 2 limbs, full slots, |slot| <= 1; a batch is refreshed
-    as one: every key switch of the pipeline covers all its items) to ``spec.output_levels`` limbs
-    (0: all the program leaves).  The result keeps the input's scaling factor; the input is not
-    consumed."""
+def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *, bound_bits: int = 0) -> Cipher:
+    """Refresh ``cipher`` (two components, >= 2 limbs, full slots, |slot| <= 2^bound_bits; a batch
+    is refreshed as one: every key switch of the pipeline covers all its items) to
+    ``spec.output_levels`` limbs (0: all the program leaves).  The result keeps the input's scaling
+    factor; the input is not consumed.  ``bound_bits`` moves the message 2^bound_bits further below
+    q_0 in the scale-down product and multiplies it back by the integer at the end (no level)."""
 
     ctx = context
     spec = program.spec
@@ -460,7 +461,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram) -
     limbs = int(cipher.state.cur_limbs)
     b1, b2 = len(program.cts), len(program.stc)
     # 1. message down to 2^-bits of q_0, then one limb
-    bits = max(0, int(round(math.log2(S_in / program.q0))) + int(spec.message_ratio_bits))
+    bits = max(0, int(round(math.log2(S_in / program.q0))) + int(spec.message_ratio_bits) + int(bound_bits))
     x = cipher
     if bits:
         enc = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
@@ -505,7 +506,7 @@ def _times_integer(ct: Cipher, value: int, ctx: CKKSContext) -> Cipher:
 
 
 def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *,
-                              iterations: int = 2, precision_bits: int = 12) -> Cipher:
+                              iterations: int = 2, precision_bits: int = 12, bound_bits: int = 0) -> Cipher:
     """One bootstrap, or the two-pass correction of llama3fhe/operators/nonlinear/bootstrap.py:
     626-720: first = BTS(x); the scaled error 2^p (first - x) at x's level is bootstrapped too and
     subtracted from 2^p first, then 2^-p multiplies the result back (encoded at the prime the
@@ -517,7 +518,7 @@ def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: Boo
     iterations = int(iterations)
     if iterations not in (1, 2):
         raise ValueError("bootstrap iterations must be one or two")
-    first = bootstrap(cipher, ctx, program)
+    first = bootstrap(cipher, ctx, program, bound_bits=bound_bits)
     if iterations == 1 or int(first.state.cur_limbs) <= int(cipher.state.cur_limbs):
         return first
     p = int(precision_bits)
@@ -526,7 +527,7 @@ def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: Boo
         first_scaled = _times_integer(first, scale, ctx) if p > 0 else first
         first_down = fhe.align_to(first_scaled, cipher.state, ctx)
         orig_scaled = _times_integer(cipher, scale, ctx) if p > 0 else cipher
-        error = bootstrap(fhe.homo_sub(first_down, orig_scaled, ctx), ctx, program)
+        error = bootstrap(fhe.homo_sub(first_down, orig_scaled, ctx), ctx, program, bound_bits=bound_bits)
         corrected = fhe.homo_sub(fhe.align_to(first_scaled, error.state, ctx), error, ctx)
         if p <= 0:
             return corrected

@@ -1,0 +1,866 @@
+"""Encrypted decode step of one Llama-3 layer on one GPU (config C5).
+
+One new token attends over an encrypted KV cache held in HBM-resident PairFold pages, then runs
+the MLP; the semantics are those of llama3fhe/approx/layer.py:768-906 (``poly_decode_layer_numpy``
+with the Alg2 softmax at k = 1, layer.py:325-463): polynomial RMSNorm, GQA attention with RoPE,
+softmax as a Chebyshev exp followed by one Chebyshev inverse square root round
+(p = (y / sqrt(sum y^2))^2 = exp(2 mapped) / sum exp(2 mapped)), W_O and the residual, polynomial
+RMSNorm, SwiGLU with a Chebyshev SiLU, down projection and the residual.  ``decode_layer_numpy``
+is that computation in float64 with the same polynomials; the encrypted layer matches it up to
+CKKS noise.
+
+Slot layouts (32768 complex slots):
+
+* residual stream, DecodeFM (llama3fhe/graph/decode.py:43-94): lane 0 of 8, x[d] at slot 8 d;
+* shifted lanes (llama3fhe/layouts/shifted_lane.py:1-24) for every linear: lane l of channel c
+  holds x[(c + (D / lanes) l) mod D]; a D x D block costs D / lanes diagonals;
+* KV pages: PairFold128 (llama3fhe/layouts/pairfold128.py:176-181): slot
+  16384 pair + 2 (128 f + t) + lane holds the folded pair k[f] + i k[f + 64] of KV head
+  4 g + 2 pair + lane for token t, feature f < 64; key pages store the conjugate of the RoPE'd
+  fold and value pages the plain fold, so a query page q_fold * e^(i theta) times a key page and
+  the real part gives the score, and RoPE is a diagonal product;
+* compact scores: block m = 8 p + 4 g + o (page p, group g, query offset o) of 256 slots, slot
+  16384 pair + 256 m + 2 t + lane.
+
+Every slot permutation is a masked rotation sum (rotate, multiply by a coefficient vector on the
+destination slots, add): the sparse routes of llama3fhe/operators/attention/pairfold/
+pairfold_route.py:151-182 written directly for this layout.  The QKV projection emits complex
+channels (query fold, conjugated key fold, value fold) so no real/imaginary split is needed before
+routing; W_O, gate/up and down take complex weights that carry two real matrices each.
+
+Levels come back through five one-ciphertext refreshes, each the two-pass correction of
+llama3fhe/operators/nonlinear/bootstrap.py:626-720: the softmax's row sums before the 1/sqrt and
+the residual before the MLP and the packed gate + i up before the SiLU (all three with the deep
+program, which leaves more levels), the probabilities before PV, the SwiGLU product before the
+down projection.  Masks that would cost a level after a polynomial are replaced by subtracting
+the polynomial's public value at the masked slots' known input.
+"""
+
+from __future__ import annotations
+
+import math
+import time
+from dataclasses import dataclass
+
+import numpy as np
+import torch
+
+from .polynomial import chebyshev_coefficients
+
+__all__ = ["DecodeSpec", "DecodeWeights", "DecodePolynomials", "DecodeLayer", "CipherOps", "decode_layer_numpy",
+           "decode_rotations", "rope_phase", "page_slot", "kv_head", "query_head", "pack_key_page",
+           "pack_value_page", "random_weights", "lr8", "encrypt_kv_history", "decode_bootstrap_specs",
+           "decode_key_rotations"]
+
+SLOTS = 32768
+PAIR_STRIDE = 16384
+BLOCK = 256            # slots of one feature (or score) block inside a pair half
+LANES8, SHIFT8 = 8, 512
+LANES16, SHIFT16 = 16, 128
+
+
+# ---------------------------------------------------------------------------- spec / polynomials
+@dataclass(frozen=True)
+class DecodeSpec:
+    """Shape and approximation knobs of the decode layer.  The softmax follows the Alg2 public
+    map of llama3fhe/approx/layer.py:325-390 with k = 1: mapped = (s / sqrt(d) - U) / 2 on
+    ``exp_interval``; ``rsqrt_interval`` must hold sum_t exp(2 mapped) of every query head (a
+    calibrated range, as the reference's per-layer statistics)."""
+
+    hidden_dim: int = 4096
+    query_heads: int = 32
+    kv_heads: int = 8
+    head_dim: int = 128
+    intermediate: int = 14336
+    page_size: int = 128
+    rope_theta: float = 500000.0
+    eps: float = 1e-5
+    rms_degree: int = 15
+    rms_interval: tuple = (0.5, 2.0)
+    score_shift: float = 0.0
+    exp_degree: int = 15
+    exp_interval: tuple = (-4.0, 4.0)
+    rsqrt_degree: int = 15
+    rsqrt_interval: tuple = (100.0, 4000.0)
+    silu_degree: int = 63
+    silu_interval: tuple = (-16.0, 16.0)
+    key_limbs: int = 13
+    value_limbs: int = 7
+    rowsum_bound_bits: int = 2
+    residual_bound_bits: int = 3
+    act_bound_bits: int = 4
+
+    def validate(self) -> None:
+        if (self.hidden_dim, self.query_heads, self.kv_heads, self.head_dim, self.page_size) != (4096, 32, 8, 128, 128):
+            raise ValueError("the decode layouts are built for Llama-3-8B (4096, 32/8 heads of 128, 128-token pages)")
+        if self.intermediate > 4 * self.hidden_dim:
+            raise ValueError("intermediate width above 4 blocks of 4096")
+
+
+@dataclass(frozen=True)
+class DecodePolynomials:
+    """Chebyshev series (numpy convention, argument in [-1, 1]) of the layer's approximations."""
+
+    rms: np.ndarray
+    exp: np.ndarray
+    rsqrt: np.ndarray
+    silu: np.ndarray
+
+    @classmethod
+    def fit(cls, spec: DecodeSpec) -> "DecodePolynomials":
+        eps = float(spec.eps)
+        return cls(rms=chebyshev_coefficients(lambda m: 1.0 / np.sqrt(m + eps), spec.rms_degree, spec.rms_interval),
+                   exp=chebyshev_coefficients(np.exp, spec.exp_degree, spec.exp_interval),
+                   rsqrt=chebyshev_coefficients(lambda r: 1.0 / np.sqrt(r), spec.rsqrt_degree, spec.rsqrt_interval),
+                   silu=chebyshev_coefficients(lambda x: x / (1.0 + np.exp(-x)), spec.silu_degree,
+                                               spec.silu_interval))
+
+
+def _cheb(x, coeffs, interval):
+    a, b = (float(v) for v in interval)
+    return np.polynomial.chebyshev.chebval((2.0 * np.asarray(x) - (a + b)) / (b - a), coeffs)
+
+
+@dataclass
+class DecodeWeights:
+    """Layer weights in the reference's [out, in] orientation (llama3fhe/approx/layer.py:486-491)."""
+
+    q_proj: np.ndarray
+    k_proj: np.ndarray
+    v_proj: np.ndarray
+    o_proj: np.ndarray
+    gate_proj: np.ndarray
+    up_proj: np.ndarray
+    down_proj: np.ndarray
+    input_layernorm: np.ndarray
+    post_attention_layernorm: np.ndarray
+
+
+def random_weights(spec: DecodeSpec, rng: np.random.Generator, std: float = 0.02) -> DecodeWeights:
+    D, I = spec.hidden_dim, spec.intermediate
+    kv = spec.kv_heads * spec.head_dim
+
+    def w(o, i):
+        return rng.normal(0.0, std, (o, i))
+
+    return DecodeWeights(q_proj=w(D, D), k_proj=w(kv, D), v_proj=w(kv, D), o_proj=w(D, D), gate_proj=w(I, D),
+                         up_proj=w(I, D), down_proj=w(D, I), input_layernorm=1.0 + 0.1 * rng.normal(size=D),
+                         post_attention_layernorm=1.0 + 0.1 * rng.normal(size=D))
+
+
+# ---------------------------------------------------------------------------- float64 semantics
+def rope_phase(position: int, spec: DecodeSpec) -> np.ndarray:
+    """e^(i theta_f) for the 64 folded features at ``position``, from the float32 cos / sin of
+    llama3fhe/approx/attention.py:23-38 (the reference's own rounding)."""
+
+    hd = int(spec.head_dim)
+    inv = (1.0 / (np.float32(spec.rope_theta) ** (np.arange(0, hd, 2, dtype=np.float32) / np.float32(hd))))
+    ang = (np.float32(position) * inv.astype(np.float32)).astype(np.float32)
+    return np.cos(ang).astype(np.float64) + 1j * np.sin(ang).astype(np.float64)
+
+
+def _rope(x: np.ndarray, heads: int, phase: np.ndarray) -> np.ndarray:
+    """RoPE on the rotate-half pairs (f, f + 64) as the complex product fold * e^(i theta)
+    (llama3fhe/approx/attention.py:41-59)."""
+
+    h = x.reshape(heads, 128)
+    z = (h[:, :64] + 1j * h[:, 64:]) * phase[None, :]
+    return np.concatenate([z.real, z.imag], axis=1).reshape(-1)
+
+
+def decode_layer_numpy(hidden, cache_key, cache_value, weights: DecodeWeights, spec: DecodeSpec,
+                       position: int, polys: DecodePolynomials | None = None) -> dict:
+    """One decode token in float64 (llama3fhe/approx/layer.py:768-906, Alg2 at k = 1), with this
+    layer's polynomials.  ``cache_key`` holds RoPE'd keys [tokens, 1024]; returns the output and
+    the intermediates the encrypted layer exposes."""
+
+    polys = DecodePolynomials.fit(spec) if polys is None else polys
+    x = np.asarray(hidden, dtype=np.float64).reshape(-1)
+    D = spec.hidden_dim
+
+    def rms(v, gamma):
+        m = np.mean(v * v)
+        return v * _cheb(m, polys.rms, spec.rms_interval) * np.asarray(gamma, dtype=np.float64)
+
+    xn = rms(x, weights.input_layernorm)
+    q = weights.q_proj @ xn
+    k = weights.k_proj @ xn
+    v = weights.v_proj @ xn
+    ph = rope_phase(position, spec)
+    q = _rope(q, spec.query_heads, ph)
+    k = _rope(k, spec.kv_heads, ph)
+    keys = np.vstack([np.asarray(cache_key, dtype=np.float64).reshape(-1, 1024), k[None, :]])
+    values = np.vstack([np.asarray(cache_value, dtype=np.float64).reshape(-1, 1024), v[None, :]])
+    n = keys.shape[0]
+    qh = q.reshape(32, 128)
+    kh = keys.reshape(n, 8, 128)[:, np.arange(32) // 4, :]
+    vh = values.reshape(n, 8, 128)[:, np.arange(32) // 4, :]
+    scores = np.einsum("hd,thd->ht", qh, kh)
+    mapped = scores / math.sqrt(spec.head_dim) / 2.0 - spec.score_shift / 2.0
+    y = _cheb(mapped, polys.exp, spec.exp_interval)
+    row = np.sum(y * y, axis=1, keepdims=True)
+    lam = _cheb(row, polys.rsqrt, spec.rsqrt_interval)
+    p = (y * lam) ** 2
+    o = np.einsum("ht,thd->hd", p, vh).reshape(-1)
+    h1 = x + weights.o_proj @ o
+    xn2 = rms(h1, weights.post_attention_layernorm)
+    gate = weights.gate_proj @ xn2
+    up = weights.up_proj @ xn2
+    act = _cheb(gate, polys.silu, spec.silu_interval) * up
+    out = h1 + weights.down_proj @ act
+    exact = np.exp(scores / math.sqrt(spec.head_dim))
+    exact /= exact.sum(axis=1, keepdims=True)
+    return {"output": out, "h1": h1, "q": q, "k": k, "v": v, "scores": scores, "mapped": mapped, "y": y,
+            "row_sum": row[:, 0], "probs": p, "attn": o, "gate": gate, "up": up, "act": act,
+            "softmax_vs_exact": float(np.max(np.abs(p - exact))),
+            "in_range": {"exp": bool(mapped.min() >= spec.exp_interval[0] and mapped.max() <= spec.exp_interval[1]),
+                         "rsqrt": bool(row.min() >= spec.rsqrt_interval[0] and row.max() <= spec.rsqrt_interval[1]),
+                         "silu": bool(np.abs(gate).max() <= spec.silu_interval[1])}}
+
+
+# ---------------------------------------------------------------------------- layouts
+def page_slot(pair, f, t, lane):
+    """PairFold128 page slot (llama3fhe/layouts/pairfold128.py:176-181)."""
+
+    return PAIR_STRIDE * np.asarray(pair) + 2 * (128 * np.asarray(f) + np.asarray(t)) + np.asarray(lane)
+
+
+def kv_head(g, pair, lane):
+    return 4 * np.asarray(g) + 2 * np.asarray(pair) + np.asarray(lane)
+
+
+def query_head(g, pair, lane, o):
+    return 4 * kv_head(g, pair, lane) + np.asarray(o)
+
+
+def lr8(x: np.ndarray) -> np.ndarray:
+    """DecodeFM slot vector: x[d] at slot 8 d."""
+
+    out = np.zeros(SLOTS, dtype=np.result_type(x, np.float64))
+    out[::LANES8] = np.asarray(x).reshape(-1)
+    return out
+
+
+def _grid():
+    pair, f, lane = np.meshgrid(np.arange(2), np.arange(64), np.arange(2), indexing="ij")
+    return pair.reshape(-1), f.reshape(-1), lane.reshape(-1)
+
+
+def _fold_rows(W: np.ndarray, heads: np.ndarray, f: np.ndarray, sign: float = 1.0) -> np.ndarray:
+    return W[128 * heads + f] + sign * 1j * W[128 * heads + 64 + f]
+
+
+def _pack_page(tokens: np.ndarray, g: int, conj: bool) -> np.ndarray:
+    """Page slot vector of group ``g`` for up to 128 tokens [t, 1024] (RoPE'd keys or values)."""
+
+    tokens = np.asarray(tokens, dtype=np.float64).reshape(-1, 1024)
+    out = np.zeros(SLOTS, dtype=np.complex128)
+    pair, f, lane = _grid()
+    hk = kv_head(g, pair, lane)
+    for t in range(tokens.shape[0]):
+        z = tokens[t, 128 * hk + f] + 1j * tokens[t, 128 * hk + 64 + f]
+        out[page_slot(pair, f, t, lane)] = np.conj(z) if conj else z
+    return out
+
+
+def pack_key_page(keys: np.ndarray, g: int) -> np.ndarray:
+    """Key page of group ``g``: conj(k[f] + i k[f + 64]) of RoPE'd keys."""
+
+    return _pack_page(keys, g, conj=True)
+
+
+def pack_value_page(values: np.ndarray, g: int) -> np.ndarray:
+    return _pack_page(values, g, conj=False)
+
+
+# QKV output channel c = 2048 pair + 32 f + j (slot 8 c): j < 16 queries, 16..19 keys, 20..23 values
+def _q_j(g, lane, o):
+    return 8 * g + 2 * o + lane
+
+
+def _k_j(g, lane):
+    return 16 + 2 * g + lane
+
+
+def _v_j(g, lane):
+    return 20 + 2 * g + lane
+
+
+def _z_j(g, o, lane):
+    """Attention-output index k = 1024 pair + 16 f + j (slot 16 k) of head (g, pair, lane, o)."""
+
+    return 8 * lane + 4 * g + o
+
+
+def qkv_matrix(weights: DecodeWeights) -> np.ndarray:
+    """Complex 4096 x 4096 block: channel rows (query fold, conjugated key fold, value fold) with the
+    input RMSNorm gamma folded into the columns."""
+
+    A = np.zeros((4096, 4096), dtype=np.complex128)
+    pair, f, lane = _grid()
+    for g in range(2):
+        hk = kv_head(g, pair, lane)
+        base = 2048 * pair + 32 * f
+        for o in range(4):
+            A[base + _q_j(g, lane, o)] = _fold_rows(weights.q_proj, 4 * hk + o, f)
+        A[base + _k_j(g, lane)] = _fold_rows(weights.k_proj, hk, f, sign=-1.0)
+        A[base + _v_j(g, lane)] = _fold_rows(weights.v_proj, hk, f)
+    return A * np.asarray(weights.input_layernorm, dtype=np.float64)[None, :]
+
+
+def wo_blocks(weights: DecodeWeights) -> tuple[np.ndarray, np.ndarray]:
+    """W_O as two complex 2048 x 2048 blocks over the folded attention output z (index k, slot
+    16 k): output d = 2 c + b of block b, y = Re(B_b z)."""
+
+    W = np.asarray(weights.o_proj, dtype=np.float64)
+    k = np.arange(2048)
+    pair, f, j = k // 1024, (k // 16) % 64, k % 16
+    lane, g, o = j // 8, (j // 4) % 2, j % 4
+    h = query_head(g, pair, lane, o)
+    A = W[:, 128 * h + f] - 1j * W[:, 128 * h + 64 + f]  # [4096, 2048]
+    return A[0::2].copy(), A[1::2].copy()
+
+
+def gate_up_blocks(weights: DecodeWeights) -> list[np.ndarray]:
+    """(gate + i up) / 32 in 4096-row blocks (rows past the intermediate width are zero), the post
+    attention gamma folded into the columns."""
+
+    I = weights.gate_proj.shape[0]
+    gamma = np.asarray(weights.post_attention_layernorm, dtype=np.float64)[None, :]
+    out = []
+    for b in range(4):
+        blk = np.zeros((4096, 4096), dtype=np.complex128)
+        lo, hi = 4096 * b, min(4096 * (b + 1), I)
+        if hi > lo:
+            blk[:hi - lo] = (weights.gate_proj[lo:hi] + 1j * weights.up_proj[lo:hi]) * gamma / 32.0
+        out.append(blk)
+    return out
+
+
+def down_blocks(weights: DecodeWeights) -> list[np.ndarray]:
+    """16 (D_2b - i D_(2b+1)) for the packed activations z_b = h_2b + i h_(2b+1) (h = act / 16)."""
+
+    W = np.asarray(weights.down_proj, dtype=np.float64)
+    I = W.shape[1]
+
+    def col(b):
+        blk = np.zeros((4096, 4096))
+        lo, hi = 4096 * b, min(4096 * (b + 1), I)
+        if hi > lo:
+            blk[:, :hi - lo] = W[:, lo:hi]
+        return blk
+
+    return [16.0 * (col(2 * b) - 1j * col(2 * b + 1)) for b in range(2)]
+
+
+def _mask(slots) -> np.ndarray:
+    m = np.zeros(SLOTS)
+    m[np.asarray(slots).reshape(-1)] = 1.0
+    return m
+
+
+def _pages_pad(pages: int) -> int:
+    return 1 << max(0, (int(pages) - 1).bit_length())
+
+
+def decode_rotations(pages: int = 3, baby8: int = 32, baby16: int = 16) -> tuple[int, ...]:
+    """Every slot rotation the layer uses for up to ``pages`` KV pages (the conjugation excluded)."""
+
+    rot = set()
+    rot |= {4095 * s for s in (1, 2, 4)} | {2047 * s for s in (1, 2, 4, 8)}          # SL expansions
+    rot |= {8 << k for k in range(12)}                                                # RMSNorm fold
+    rot |= {1, 2, 3, 4, 8} | {SLOTS - 8} | {SLOTS - b for b in (1, 2, 3)}            # lane folds / packing
+    rot |= {b * 8 for b in range(1, baby8)} | {s * baby8 * 8 for s in range(1, SHIFT8 // baby8)}
+    rot |= {b * 16 for b in range(1, baby16)} | {s * baby16 * 16 for s in range(1, SHIFT16 // baby16)}
+    pair, f, lane = _grid()
+    for g in range(2):
+        for ln in range(2):
+            rot.add(8 * _k_j(g, ln) - ln)
+            rot.add(8 * _v_j(g, ln) - ln)
+            for o in range(4):
+                rot.add(8 * _q_j(g, ln, o) - ln)
+                rot.add((ln - 16 * _z_j(g, o, ln)) % SLOTS)
+    rot |= {(SLOTS - (2 << k)) % SLOTS for k in range(7)} | {2 << k for k in range(7)}  # token axis
+    rot |= {BLOCK << k for k in range(6)} | {SLOTS - (BLOCK << k) for k in range(6)}    # feature axis
+    npad = _pages_pad(pages)
+    rot |= {(8 * BLOCK) << k for k in range(npad.bit_length() - 1)}
+    rot |= {SLOTS - ((8 * BLOCK) << k) for k in range(npad.bit_length() - 1)}
+    for m in range(8 * pages):
+        rot |= {(BLOCK * m) % SLOTS, (-BLOCK * m) % SLOTS}
+    rot.discard(0)
+    return tuple(sorted(int(r) % SLOTS for r in rot))
+
+
+def encrypt_kv_history(client, cache_key, cache_value, spec: DecodeSpec, scale: float):
+    """A PairFoldLayerCache of the RoPE'd history [tokens, 1024] encrypted page by page, key pages
+    at ``spec.key_limbs`` and value pages at ``spec.value_limbs`` limbs (the client side of the
+    cache the decode step extends)."""
+
+    from .kv_pages import PairFoldCipherPage, PairFoldLayerCache
+
+    ck = np.asarray(cache_key, dtype=np.float64).reshape(-1, 1024)
+    cv = np.asarray(cache_value, dtype=np.float64).reshape(-1, 1024)
+    pages = []
+    for p in range(0, ck.shape[0], spec.page_size):
+        kt, vt = ck[p:p + spec.page_size], cv[p:p + spec.page_size]
+        kg = [client.encrypt(pack_key_page(kt, g), cur_limbs=spec.key_limbs, scaling_factor=scale) for g in range(2)]
+        vg = [client.encrypt(pack_value_page(vt, g), cur_limbs=spec.value_limbs, scaling_factor=scale)
+              for g in range(2)]
+        pages.append(PairFoldCipherPage(kg, vg, kt.shape[0]))
+    return PairFoldLayerCache(pages=tuple(pages), content_tokens=int(ck.shape[0]))
+
+
+def decode_bootstrap_specs():
+    """The refresh programs: (3, 3) level budget, and the deep (2, 2) one that leaves two more
+    levels (the reference's deep_level_budget, llama3fhe/graph/common.py:657-680)."""
+
+    from .bootstrap import BootstrapSpec
+
+    return BootstrapSpec(log_slots=15, level_budget=(3, 3)), BootstrapSpec(log_slots=15, level_budget=(2, 2))
+
+
+def decode_key_rotations(pages: int, log_n: int = 16) -> tuple[int, ...]:
+    """Rotation keys of one decode step over ``pages`` pages: the layer's slot rotations, the
+    conjugation, and both refresh programs."""
+
+    from .bootstrap import requirements
+
+    rots = set(decode_rotations(pages))
+    for b in decode_bootstrap_specs():
+        rots |= set(requirements(b, log_n).rotations)
+    rots.add((1 << (log_n + 1)) - 1)
+    return tuple(sorted(rots))
+
+
+# ---------------------------------------------------------------------------- GPU operations
+class CipherOps:
+    """The ciphertext operations the layer is written in, on the GPU: every result carries exact
+    (limbs, scale) bookkeeping; products rescale; additions need equal scales at their common
+    level; ``adjust`` brings a ciphertext with spare levels to any (limbs, scale)."""
+
+    def __init__(self, ctx, program, deep_program=None):
+        from . import bootstrap as _bs
+        from . import fhe as _fhe
+        from .linear import LinearOperator, LinearOperatorConfig, LinearWeight
+
+        self.ctx, self.program = ctx, program
+        self.deep_program = program if deep_program is None else deep_program
+        self._fhe, self._bs = _fhe, _bs
+        self._LinearOperator, self._LinearOperatorConfig, self._LinearWeight = (LinearOperator,
+                                                                               LinearOperatorConfig, LinearWeight)
+        self.slots = int(ctx.max_slots)
+        self.refreshes = 0
+
+    # -- bookkeeping
+    def limbs(self, ct) -> int:
+        return int(ct.state.cur_limbs)
+
+    def scale(self, ct) -> float:
+        return float(ct.state.scaling_factor)
+
+    def batch(self, cts):
+        return self._fhe.pack_cipher_batch(list(cts))
+
+    def items(self, ct) -> list:
+        return list(self._fhe.unpack_cipher_batch(ct))
+
+    def copies(self, ct, n: int):
+        return self.batch([ct] * int(n))
+
+    # -- slot movement
+    def rotate(self, ct, r):
+        ctx = self.ctx
+        limbs = self.limbs(ct)
+        c0, c1 = ct.cv[0][:, :limbs], ct.cv[1][:, :limbs]
+        if isinstance(r, (list, tuple, np.ndarray)):
+            r = [int(v) % self.slots for v in r]
+            if ct.batch_size == 1 and len(r) > 1:
+                # one input rotated by every amount: a batch-stride-0 view, one launch
+                c0, c1 = c0.expand(len(r), -1, -1), c1.expand(len(r), -1, -1)
+            elif len(r) != ct.batch_size:
+                raise ValueError("one rotation per item")
+            nz = [i for i, v in enumerate(r) if v]
+            if len(nz) < len(r):
+                # identity items are copied; the others rotate in one launch
+                from .context import u64_copy
+
+                o0, o1 = ctx.empty(len(r), limbs, ctx.N), ctx.empty(len(r), limbs, ctx.N)
+                for i, v in enumerate(r):
+                    if not v:
+                        u64_copy(o0[i], c0[i])
+                        u64_copy(o1[i], c1[i])
+                if nz:
+                    # uint64 has no index kernels: gather and scatter through int64 views
+                    idx = torch.tensor(nz, device=c0.device)
+                    g0 = c0.contiguous().view(torch.int64).index_select(0, idx).view(torch.uint64)
+                    g1 = c1.contiguous().view(torch.int64).index_select(0, idx).view(torch.uint64)
+                    sub = self.rotate(ct.cipher_like([g0, g1], batch_size=len(nz)), [r[i] for i in nz])
+                    o0.view(torch.int64).index_copy_(0, idx, sub.cv[0].contiguous().view(torch.int64))
+                    o1.view(torch.int64).index_copy_(0, idx, sub.cv[1].contiguous().view(torch.int64))
+                return ct.cipher_like([o0, o1], batch_size=len(r))
+            gs = [ctx.galois_element(v) for v in r]
+            o0, o1 = ctx.rotate_raw(c0, c1, limbs, gs, [ctx.key_for_galois(g) for g in gs])
+            return ct.cipher_like([o0, o1], batch_size=len(gs))
+        if int(r) % self.slots == 0:
+            return ct
+        return self._fhe.homo_rotate(ct, int(r) % self.slots, ctx)
+
+    def conj(self, ct):
+        return self._fhe.homo_rotate(ct, self.ctx.M - 1, self.ctx)
+
+    def rotate_add(self, ct, r):
+        """ct + rot(ct, r) in one fused pass."""
+
+        ctx = self.ctx
+        limbs = self.limbs(ct)
+        g = ctx.galois_element(int(r) % self.slots)
+        c0, c1 = ct.cv[0][:, :limbs].contiguous(), ct.cv[1][:, :limbs].contiguous()
+        o0, o1 = ctx.rotate_raw(c0, c1, limbs, g, ctx.key_for_galois(g), acc=(c0, c1))
+        return ct.cipher_like([o0, o1])
+
+    # -- arithmetic
+    def add(self, a, b):
+        return self._fhe.homo_add(a, b, self.ctx)
+
+    def sub(self, a, b):
+        return self._fhe.homo_sub(a, b, self.ctx)
+
+    def mul_i(self, ct, negative: bool = False):
+        return self._fhe.homo_mul_i(ct, self.ctx, negative=negative)
+
+    def add_const(self, ct, c: float):
+        f = self._fhe
+        enc = f.encode_scalar(float(c), cur_limbs=self.limbs(ct), scale_degree=1, scaling_factor=self.scale(ct),
+                              context=self.ctx)
+        return f.homo_add_scalar(ct, enc, self.ctx)
+
+    def add_vec(self, ct, vec):
+        f = self._fhe
+        pt = f.encode_plaintext(np.asarray(vec), ct.state, self.slots, self.ctx)
+        return f.homo_add_pt(ct, pt, self.ctx)
+
+    def mul(self, a, b):
+        f = self._fhe
+        return f.rescale(f.homo_mul_relin(a, b, self.ctx), self.ctx)
+
+    def adjust(self, ct, limbs: int, scale: float):
+        """``ct`` at (limbs, scale): one scalar product and rescale, then dropped limbs."""
+
+        f = self._fhe
+        l = self.limbs(ct)
+        if l == int(limbs) and abs(self.scale(ct) - scale) <= 1e-12 * scale:
+            return ct
+        if l <= int(limbs):
+            raise ValueError(f"adjust needs a spare level: {l} limbs to {limbs}")
+        q = float(self.ctx.rescale_divisor_at(l))
+        enc = f.encode_scalar(1.0, cur_limbs=l, scale_degree=1, scaling_factor=scale * q / self.scale(ct),
+                              context=self.ctx)
+        out = f.rescale(f.homo_mul_scalar(ct, enc, self.ctx), self.ctx)
+        out = out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(scale), scale_degree=1))
+        if self.limbs(out) > int(limbs):
+            out = f.align_to(out, out.state.replace(cur_limbs=int(limbs)), self.ctx)
+        return out
+
+    def mac(self, terms, out_scale: float | None = None):
+        """sum_i vec_i * ct_i, rescaled: one level.  ``vec`` is a scalar, a slot vector or one row
+        per batch item; every term is encoded so its product lands on ``out_scale`` (default: the
+        first term's scale)."""
+
+        f, ctx = self._fhe, self.ctx
+        l = min(self.limbs(c) for c, _ in terms)
+        T = self.scale(terms[0][0]) if out_scale is None else float(out_scale)
+        q = float(ctx.rescale_divisor_at(l))
+        acc = None
+        for c, vec in terms:
+            if self.limbs(c) > l:
+                c = f.align_to(c, c.state.replace(cur_limbs=l), ctx)
+            pscale = T * q / self.scale(c)
+            if np.ndim(vec) == 0:
+                enc = f.encode_scalar(float(vec), cur_limbs=l, scale_degree=1, scaling_factor=pscale, context=ctx)
+                prod = f.homo_mul_scalar(c, enc, ctx)
+            else:
+                st = c.state.replace(cur_limbs=l, scale_degree=1, scaling_factor=pscale)
+                prod = f.homo_mul_pt(c, f.encode_plaintext(np.asarray(vec), st, self.slots, ctx), ctx)
+            prod = prod.cipher_like(prod.cv, state=prod.state.replace(scaling_factor=T * q))
+            acc = prod if acc is None else f.homo_add(acc, prod, ctx)
+        out = f.rescale(acc, ctx)
+        return out.cipher_like(out.cv, state=out.state.replace(scaling_factor=T, scale_degree=1))
+
+    def ideal_scale(self, limbs: int) -> float:
+        """The scale that keeps a Chebyshev evaluation's exact-scale chain from drifting: the
+        prime its first rescale drops."""
+
+        return float(self.ctx.rescale_divisor_at(int(limbs)))
+
+    def refresh_limbs(self, deep: bool = False) -> int:
+        prog = self.deep_program if deep else self.program
+        return int(prog.output_limbs) - 1
+
+    def poly(self, ct, coeffs):
+        from .polynomial import PSEvaluator
+
+        ideal = self.ideal_scale(self.limbs(ct))
+        if abs(math.log2(self.scale(ct) / ideal)) > 2.0**-12:
+            raise ValueError(f"a series input must sit at its level's prime ({ideal}), got {self.scale(ct)}")
+        coeffs = np.asarray(coeffs, dtype=np.float64)
+        ev = PSEvaluator(self.ctx, ct, self.limbs(ct), self.scale(ct), len(coeffs) - 1, self.ctx.q_primes)
+        return ev.evaluate(coeffs)
+
+    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False):
+        """Two-pass bootstrap (|slots| <= 2^bound_bits); ``deep`` uses the program that leaves more
+        levels."""
+
+        prog = self.deep_program if deep else self.program
+        self.refreshes += int(ct.batch_size)
+        return self._bs.bootstrap_with_correction(ct, self.ctx, prog, iterations=2, precision_bits=12,
+                                                  bound_bits=int(bound_bits))
+
+    def drop(self, ct, limbs: int):
+        return self._fhe.align_to(ct, ct.state.replace(cur_limbs=int(limbs)), self.ctx)
+
+    # -- linear layers
+    def linear_weight(self, matrix: np.ndarray, lanes: int, baby_steps: int):
+        D = int(matrix.shape[0])
+        cfg = self._LinearOperatorConfig(baby_steps=int(baby_steps), baby_anchor_step=-1, max_plaintext_rows=D // lanes,
+                                         hoist_strategy="ext_double_hoist", lane_shift=D // int(lanes))
+        op = self._LinearOperator(crypto_context=self.ctx, token_lanes=int(lanes), config=cfg)
+        w = self._LinearWeight(np.ascontiguousarray(matrix.real), crypto_context=self.ctx,
+                               imag=np.ascontiguousarray(matrix.imag))
+        return (op, w, D)
+
+    def linear_prepare(self, ct, handle):
+        op, _, D = handle
+        return op.prepare([ct], D)
+
+    def linear(self, ct, handle, prepared=None):
+        op, w, _ = handle
+        outs, _ = op.apply([ct], w, prepared=prepared)
+        return outs[0]
+
+
+# ---------------------------------------------------------------------------- the layer
+class DecodeLayer:
+    """One decode step over a PairFold cache of ``pages`` pages (the token's page included)."""
+
+    def __init__(self, ops, weights: DecodeWeights, spec: DecodeSpec | None = None,
+                 polys: DecodePolynomials | None = None):
+        self.spec = DecodeSpec() if spec is None else spec
+        self.spec.validate()
+        self.ops = ops
+        self.polys = DecodePolynomials.fit(self.spec) if polys is None else polys
+        sp = self.spec
+        self.qkv = ops.linear_weight(qkv_matrix(weights), LANES8, 32)
+        self.wo = [ops.linear_weight(b, LANES16, 16) for b in wo_blocks(weights)]
+        self.gate_up = [ops.linear_weight(b, LANES8, 32) for b in gate_up_blocks(weights)
+                        if np.any(b)]
+        self.down = [ops.linear_weight(b, LANES8, 32) for b in down_blocks(weights)]
+        # softmax constants: u = alpha s + beta on valid slots; y_m = gamma y; R + b_r feeds 1/sqrt
+        a_e, b_e = (float(v) for v in sp.exp_interval)
+        self.alpha = 2.0 / (math.sqrt(sp.head_dim) * 2.0 * (b_e - a_e))
+        self.beta = (-2.0 * sp.score_shift / 2.0 - (a_e + b_e)) / (b_e - a_e)
+        a_r, b_r = (float(v) for v in sp.rsqrt_interval)
+        self.gamma = math.sqrt(2.0 / (b_r - a_r))
+        self.b_r = -(a_r + b_r) / (b_r - a_r)
+        a_m, b_m = (float(v) for v in sp.rms_interval)
+        self.rms_a = 2.0 / (sp.hidden_dim * (b_m - a_m))
+        self.rms_b = -(a_m + b_m) / (b_m - a_m)
+        pair, f, lane = _grid()
+        self._dst_t0 = page_slot(pair, f, 0, lane)
+
+    # -- helpers
+    def _fold(self, ct, strides):
+        for s in strides:
+            ct = self.ops.rotate_add(ct, s)
+        return ct
+
+    def _sl8(self, ct):
+        return self._fold(ct, (4095, 8190, 16380))
+
+    # -- the step
+    def forward(self, x, cache, position: int, crypto_context=None):
+        """``x``: the DecodeFM input (one ciphertext).  ``cache``: a PairFoldLayerCache of pages at
+        (key_limbs, value_limbs); the token's key and value are appended to it.  Returns
+        (output ciphertext, stage seconds, token write)."""
+
+        from .kv_pages import PairFoldTokenWrite
+
+        ops, sp, P = self.ops, self.spec, self.polys
+        T: dict = {}
+        t0 = time.perf_counter()
+        # --- RMSNorm 1 on shifted lanes (all lanes carry the token)
+        xs = self._sl8(x)
+        s = self._fold(ops.mul(xs, xs), tuple(8 << k for k in range(12)))
+        a_m, b_m = (float(v) for v in sp.rms_interval)
+        u = ops.mac([(s, 2.0 / (sp.hidden_dim * (b_m - a_m)))], out_scale=ops.ideal_scale(ops.limbs(s) - 1))
+        u = ops.add_const(u, -(a_m + b_m) / (b_m - a_m))
+        r = ops.poly(u, P.rms)
+        xn = ops.mul(xs, r) if ops.limbs(xs) == ops.limbs(r) else ops.mul(self._drop(xs, ops.limbs(r)), r)
+        T["input_rmsnorm"] = time.perf_counter() - t0
+        # --- QKV: complex channels, lanes folded into lane 0
+        t0 = time.perf_counter()
+        uq = self._fold(ops.linear(xn, self.qkv), (1, 2, 4))
+        T["qkv_projection"] = time.perf_counter() - t0
+        # --- routes: query folds (RoPE), token key (conjugate RoPE) and value into page slots
+        t0 = time.perf_counter()
+        ph = rope_phase(position, sp)
+        pair, f, lane = _grid()
+        col = int(cache.content_tokens) % sp.page_size
+
+        def coef(values_f, ln):
+            v = np.zeros(SLOTS, dtype=np.complex128)
+            sel = lane == ln
+            v[self._dst_t0[sel]] = values_f[f[sel]]
+            return v
+
+        one = np.ones(64, dtype=np.complex128)
+        rot_cache: dict = {}
+
+        def rot_u(rr):
+            if rr not in rot_cache:
+                rot_cache[rr] = ops.rotate(uq, rr)
+            return rot_cache[rr]
+
+        kt, vt, qt = [], [], []
+        for g in range(2):
+            kt.append(ops.mac([(rot_u(8 * _k_j(g, ln) - ln), coef(np.conj(ph), ln)) for ln in range(2)]))
+            vt.append(ops.mac([(rot_u(8 * _v_j(g, ln) - ln), coef(one, ln)) for ln in range(2)]))
+            for o in range(4):
+                qt.append(ops.mac([(rot_u(8 * _q_j(g, ln, o) - ln), coef(ph, ln)) for ln in range(2)]))
+        del rot_cache
+        kv = ops.batch(kt + vt)
+        if col:
+            for b in range(7):
+                if col >> b & 1:
+                    kv = ops.rotate(kv, SLOTS - (2 << b))
+        kts, vts = ops.items(kv)[:2], ops.items(kv)[2:]
+        ks = ops.scale(cache.pages[0].key_groups[0]) if cache.pages else None
+        vs = ops.scale(cache.pages[0].value_groups[0]) if cache.pages else None
+        kts = [ops.adjust(c, sp.key_limbs, ks if ks else ops.scale(c)) for c in kts]
+        vts = [ops.adjust(c, sp.value_limbs, vs if vs else ops.scale(c)) for c in vts]
+        qb = self._fold(ops.batch(qt), tuple(SLOTS - (2 << k) for k in range(7)))
+        T["route"] = time.perf_counter() - t0
+        # --- append the token to the cache (a new page at column 0, else the four-sum)
+        t0 = time.perf_counter()
+        token = PairFoldTokenWrite(kts, vts, col)
+        cache.append(token, crypto_context=crypto_context)
+        pages = cache.pages
+        npg = len(pages)
+        occ = [int(p.occupied) for p in pages]
+        T["kv_append"] = time.perf_counter() - t0
+        # --- QK: 8 query streams x pages, fold the features, compact into one score ciphertext
+        t0 = time.perf_counter()
+        qitems = ops.items(qb)
+        kpages = ops.batch([pages[p].key_groups[g] for p in range(npg) for g in range(2) for o in range(4)])
+        qrep = ops.batch([qitems[4 * g + o] for p in range(npg) for g in range(2) for o in range(4)])
+        prod = self._fold(ops.mul(qrep, kpages), tuple(BLOCK << k for k in range(6)))
+        ms = [8 * p + 4 * g + o for p in range(npg) for g in range(2) for o in range(4)]
+        rit = ops.items(ops.rotate(prod, [(-BLOCK * m) % SLOTS for m in ms]))
+        valid = np.zeros(SLOTS)
+        terms = []
+        for i, m in enumerate(ms):
+            tt = np.arange(occ[m // 8])
+            mk = _mask(np.concatenate([PAIR_STRIDE * pr + BLOCK * m + 2 * tt + ln for pr in range(2)
+                                       for ln in range(2)]))
+            valid += mk
+            terms.append((rit[i], 0.5 * self.alpha * mk))
+        S = ops.mac(terms, out_scale=ops.ideal_scale(ops.limbs(prod) - 1))
+        S = ops.add_vec(ops.add(S, ops.conj(S)), self.beta * valid)
+        T["qk"] = time.perf_counter() - t0
+        # --- softmax: gamma exp (invalid slots hold the public value of the series at 0 and are
+        # cleared by a plaintext subtraction), row sums of squares, 1/sqrt on a refreshed copy
+        # (non-row slots again a public constant), broadcast, p = (y lambda)^2, refreshed
+        t0 = time.perf_counter()
+        ce = self.gamma * P.exp
+        ym = ops.add_vec(ops.poly(S, ce), -float(np.polynomial.chebyshev.chebval(0.0, ce)) * (1.0 - valid))
+        npad = _pages_pad(npg)
+        page_strides = tuple((8 * BLOCK) << k for k in range(npad.bit_length() - 1))
+        rs = self._fold(ops.mul(ym, ym), tuple(2 << k for k in range(7)) + page_strides)
+        rows = _mask([PAIR_STRIDE * pr + BLOCK * r + ln for pr in range(2) for r in range(8) for ln in range(2)])
+        rs = ops.refresh(ops.mac([(rs, rows)], out_scale=ops.ideal_scale(ops.refresh_limbs(deep=True))),
+                         bound_bits=sp.rowsum_bound_bits, deep=True)
+        cl = P.rsqrt / self.gamma
+        lam = ops.poly(ops.add_vec(rs, self.b_r * rows), cl)
+        lam = ops.add_vec(lam, -float(np.polynomial.chebyshev.chebval(0.0, cl)) * (1.0 - rows))
+        lam = self._fold(lam, tuple(SLOTS - (2 << k) for k in range(7)) + tuple(SLOTS - s for s in page_strides))
+        lv = min(ops.limbs(ym), ops.limbs(lam))
+        t = ops.mul(self._drop(ym, lv), self._drop(lam, lv))
+        prob = ops.refresh(ops.mul(t, t))
+        T["softmax"] = time.perf_counter() - t0
+        # --- PV: each score block broadcast over the features of its page, times the value page
+        t0 = time.perf_counter()
+        blk0 = _mask([PAIR_STRIDE * pr + j for pr in range(2) for j in range(BLOCK)])
+        xp = ops.rotate(prob, [BLOCK * m for m in ms])
+        xp = self._fold(ops.mac([(xp, blk0)]), tuple(SLOTS - (BLOCK << k) for k in range(6)))
+        vpages = ops.batch([pages[m // 8].value_groups[(m // 4) % 2] for m in ms])
+        pv = ops.items(ops.mul(xp, vpages))
+        osum = []
+        for g in range(2):
+            for o in range(4):
+                acc = None
+                for p in range(npg):
+                    c = pv[8 * p + 4 * g + o]
+                    acc = c if acc is None else ops.add(acc, c)
+                osum.append(acc)
+        ob = self._fold(ops.batch(osum), tuple(2 << k for k in range(7)))
+        T["pv"] = time.perf_counter() - t0
+        # --- attention output into z (slot 16 k), W_O on 16 shifted lanes, back to DecodeFM
+        t0 = time.perf_counter()
+        oit = ops.items(ob)
+        zt = []
+        for g in range(2):
+            for o in range(4):
+                for ln in range(2):
+                    dst = (PAIR_STRIDE * pair + BLOCK * f + 16 * _z_j(g, o, ln))[lane == 0]
+                    zt.append((ops.rotate(oit[4 * g + o], ln - 16 * _z_j(g, o, ln)), _mask(dst)))
+        z = self._fold(ops.mac(zt), (2047, 4094, 8188, 16376))
+        prep = ops.linear_prepare(z, self.wo[0])
+        ub = ops.items(self._fold(ops.batch([ops.linear(z, w, prepared=prep) for w in self.wo]), (1, 2, 4, 8)))
+        c16 = np.arange(2048) * 16
+        w = ops.mac([(ub[0], 0.5 * _mask(c16)), (ops.rotate(ub[1], SLOTS - 8), 0.5 * _mask(c16 + 8))])
+        ya = ops.add(w, ops.conj(w))
+        h1 = ops.add(ops.adjust(x, ops.limbs(ya), ops.scale(ya)), ya)
+        T["attention_output"] = time.perf_counter() - t0
+        # --- MLP: refreshed residual; RMSNorm scale and gate/up in parallel; the packed gate + i up
+        # refreshed once; SiLU; product refreshed; down on two packed activation carriers
+        t0 = time.perf_counter()
+        h1r = ops.refresh(h1, bound_bits=sp.residual_bound_bits, deep=True)
+        hs = self._sl8(h1r)
+        prep = ops.linear_prepare(hs, self.gate_up[0])
+        nb = len(self.gate_up)
+        ug = self._fold(ops.batch([ops.linear(hs, w, prepared=prep) for w in self.gate_up]), (1, 2, 4))
+        ug = ops.items(ops.rotate(ug, [(-b) % SLOTS for b in range(nb)]))
+        lanes = np.arange(SLOTS) % LANES8
+        s2 = self._fold(ops.mul(hs, hs), tuple(8 << k for k in range(12)))
+        u2 = ops.add_const(ops.mac([(s2, self.rms_a)], out_scale=ops.ideal_scale(ops.limbs(s2) - 1)), self.rms_b)
+        r2 = ops.poly(u2, P.rms)
+        # the packed gate + i up lands, after the product with the RMSNorm scale, on the scale the
+        # SiLU series needs at the refresh's output level
+        lv = min(ops.limbs(ug[0]) - 1, ops.limbs(r2))
+        want = ops.ideal_scale(ops.refresh_limbs(deep=True)) * ops.ideal_scale(lv) / ops.scale(r2)
+        uraw = ops.mac([(c, (lanes == b).astype(np.float64)) for b, c in enumerate(ug)], out_scale=want)
+        U = ops.refresh(ops.mul(self._drop(uraw, lv), self._drop(r2, lv)), deep=True)
+        Uc = ops.conj(U)
+        gate_u = ops.add(U, Uc)
+        up_u = ops.mul_i(ops.sub(U, Uc), negative=True)
+        sg = ops.poly(gate_u, P.silu)
+        hact = ops.refresh(ops.mul(sg, self._drop(up_u, ops.limbs(sg))), bound_bits=sp.act_bound_bits)
+        m0 = (lanes == 0).astype(np.float64)
+        hri = ops.items(ops.rotate(hact, [1, 2, 3]))
+        z0 = ops.mac([(hact, m0), (hri[0], 1j * m0)])
+        z1 = ops.mac([(hri[1], m0), (hri[2], 1j * m0)])
+        zz = ops.items(self._sl8(ops.batch([z0, z1])))
+        yd = None
+        for zb, wb in zip(zz, self.down):
+            yb = ops.linear(zb, wb)
+            yd = yb if yd is None else ops.add(yd, yb)
+        mm = ops.mac([(self._fold(yd, (1, 2, 4)), 0.5 * m0)])
+        ym2 = ops.add(mm, ops.conj(mm))
+        out = ops.add(ops.adjust(h1r, ops.limbs(ym2), ops.scale(ym2)), ym2)
+        T["mlp"] = time.perf_counter() - t0
+        return out, T, token
+
+    def _drop(self, ct, limbs: int):
+        ops = self.ops
+        if ops.limbs(ct) == int(limbs):
+            return ct
+        return ops.drop(ct, int(limbs))

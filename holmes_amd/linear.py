@@ -280,7 +280,11 @@ def _stack(ciphers) -> tuple[torch.Tensor, torch.Tensor, CipherState]:
 
 
 class LinearOperator:
-    """A reusable BSGS schedule over the ``token_lanes`` feature-major layout."""
+    """A reusable BSGS schedule over the ``token_lanes`` feature-major layout.  With
+    ``config.lane_shift`` the input is in the shifted-lane packing of llama3fhe/layouts/
+    shifted_lane.py:1-24 (lane l of channel c holds x[(c + lane_shift l) mod D]): the schedule has
+    ``lane_shift`` diagonals and lane l of each output channel holds the partial product over the
+    input block [lane_shift l, lane_shift (l + 1)); the caller folds the lanes."""
 
     def __init__(self, *, crypto_context, token_lanes: int, config: LinearOperatorConfig | None = None):
         self.crypto_context = crypto_context
@@ -288,8 +292,6 @@ class LinearOperator:
         if self.token_lanes <= 0:
             raise ValueError("token_lanes must be positive.")
         self.config = LinearOperatorConfig() if config is None else config
-        if int(self.config.lane_shift):
-            raise NotImplementedError("shifted-lane packing is not built in this backend yet")
         self._closed = False
 
     @property

@@ -1,0 +1,229 @@
+"""Slot-level simulator of the decode layer's ciphertext operations (CPU, no encryption).
+
+``SlotOps`` offers the operation surface of ``holmes_amd.decode.CipherOps`` on float64 complex
+slot vectors and keeps the same (limbs, scale) bookkeeping, with the prime chain of the real
+parameter set: a product drops one limb and divides the scale by the prime the rescale removes,
+additions need equal scales at their common level, a Chebyshev series consumes the levels the
+Paterson-Stockmeyer schedule consumes, a refresh returns the levels the bootstrap program leaves.
+A layout, routing, masking or level mistake in the layer therefore shows up here exactly as it
+would on the GPU, while the values stay exact (float64), so the layer's output can be held to the
+float64 semantics at round-off level.  Test infrastructure only.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from holmes_amd import bootstrap as B
+from holmes_amd.polynomial import PSEvaluator, canonical_scales
+
+SCALE_RTOL = 2.0**-20
+
+
+class _State:
+    def __init__(self, limbs: int, scale: float):
+        self.cur_limbs, self.scaling_factor, self.scale_degree = int(limbs), float(scale), 1
+
+    def replace(self, **kw):
+        s = _State(self.cur_limbs, self.scaling_factor)
+        for k, v in kw.items():
+            setattr(s, k, v)
+        return s
+
+
+class SimCt:
+    """A batch of slot vectors [B, slots] at (limbs, scale)."""
+
+    is_ext = False
+
+    def __init__(self, values, limbs: int, scale: float):
+        v = np.asarray(values, dtype=np.complex128)
+        self.values = v.reshape(1, -1) if v.ndim == 1 else v
+        self.state = _State(limbs, scale)
+        self.released = False
+
+    @property
+    def batch_size(self) -> int:
+        return int(self.values.shape[0])
+
+    @property
+    def slots(self) -> int:
+        return int(self.values.shape[1])
+
+    def deep_copy(self):
+        return SimCt(self.values.copy(), self.state.cur_limbs, self.state.scaling_factor)
+
+    def release(self):
+        self.released = True
+
+
+class SlotOps:
+    def __init__(self, primes, program, deep_program, slots: int = 32768):
+        self.primes = [int(p) for p in primes]
+        self.program, self.deep_program = program, deep_program
+        self.slots = int(slots)
+        self.refreshes = 0
+        self.log: list = []
+
+    # -- bookkeeping
+    def limbs(self, ct) -> int:
+        return int(ct.state.cur_limbs)
+
+    def scale(self, ct) -> float:
+        return float(ct.state.scaling_factor)
+
+    def _q(self, limbs: int) -> float:
+        return float(self.primes[int(limbs) - 1])
+
+    def batch(self, cts):
+        cts = list(cts)
+        l = {self.limbs(c) for c in cts}
+        s = {self.scale(c) for c in cts}
+        if len(l) != 1 or max(s) - min(s) > SCALE_RTOL * max(s):
+            raise ValueError("a batch needs one level and scale")
+        return SimCt(np.concatenate([c.values for c in cts]), l.pop(), self.scale(cts[0]))
+
+    def items(self, ct):
+        return [SimCt(ct.values[i:i + 1].copy(), self.limbs(ct), self.scale(ct)) for i in range(ct.batch_size)]
+
+    def copies(self, ct, n: int):
+        return SimCt(np.repeat(ct.values, int(n), axis=0), self.limbs(ct), self.scale(ct))
+
+    def _like(self, ct, values, limbs=None, scale=None):
+        return SimCt(values, self.limbs(ct) if limbs is None else limbs, self.scale(ct) if scale is None else scale)
+
+    # -- slot movement
+    def rotate(self, ct, r):
+        if isinstance(r, (list, tuple, np.ndarray)):
+            if len(r) != ct.batch_size and ct.batch_size != 1:
+                raise ValueError("one rotation per item")
+            v = np.stack([np.roll(ct.values[i if ct.batch_size > 1 else 0], -int(x)) for i, x in enumerate(r)])
+            return self._like(ct, v)
+        return self._like(ct, np.roll(ct.values, -int(r), axis=1))
+
+    def conj(self, ct):
+        return self._like(ct, np.conj(ct.values))
+
+    def rotate_add(self, ct, r):
+        return self._like(ct, ct.values + np.roll(ct.values, -int(r), axis=1))
+
+    # -- arithmetic
+    def _common(self, a, b):
+        if a.batch_size != b.batch_size:
+            raise ValueError("batch sizes differ")
+        return min(self.limbs(a), self.limbs(b))
+
+    def _same(self, a, b):
+        fa, fb = self.scale(a), self.scale(b)
+        if abs(fa - fb) > SCALE_RTOL * max(fa, fb):
+            raise ValueError(f"scaling factors differ ({fa} vs {fb})")
+
+    def add(self, a, b):
+        self._same(a, b)
+        return SimCt(a.values + b.values, self._common(a, b), self.scale(a))
+
+    def sub(self, a, b):
+        self._same(a, b)
+        return SimCt(a.values - b.values, self._common(a, b), self.scale(a))
+
+    def mul_i(self, ct, negative: bool = False):
+        return self._like(ct, ct.values * (-1j if negative else 1j))
+
+    def add_const(self, ct, c: float):
+        return self._like(ct, ct.values + float(c))
+
+    def add_vec(self, ct, vec):
+        return self._like(ct, ct.values + np.asarray(vec)[None, :] if np.ndim(vec) == 1 else ct.values + vec)
+
+    def mul(self, a, b):
+        l = self._common(a, b)
+        if l < 2:
+            raise ValueError("a product needs two limbs")
+        return SimCt(a.values * b.values, l - 1, self.scale(a) * self.scale(b) / self._q(l))
+
+    def drop(self, ct, limbs: int):
+        if int(limbs) > self.limbs(ct):
+            raise ValueError("cannot raise limbs")
+        return self._like(ct, ct.values, limbs=int(limbs))
+
+    def adjust(self, ct, limbs: int, scale: float):
+        l = self.limbs(ct)
+        if l == int(limbs) and abs(self.scale(ct) - scale) <= 1e-12 * scale:
+            return ct
+        if l <= int(limbs):
+            raise ValueError(f"adjust needs a spare level: {l} limbs to {limbs}")
+        return SimCt(ct.values, int(limbs), float(scale))
+
+    def mac(self, terms, out_scale: float | None = None):
+        l = min(self.limbs(c) for c, _ in terms)
+        if l < 2:
+            raise ValueError("a plaintext product needs two limbs")
+        T = self.scale(terms[0][0]) if out_scale is None else float(out_scale)
+        acc = None
+        for c, vec in terms:
+            v = c.values * (np.asarray(vec)[None, :] if np.ndim(vec) == 1 else vec)
+            acc = v if acc is None else acc + v
+        return SimCt(acc, l - 1, T)
+
+    def ideal_scale(self, limbs: int) -> float:
+        return self._q(limbs)
+
+    def refresh_limbs(self, deep: bool = False) -> int:
+        return int((self.deep_program if deep else self.program).output_limbs) - 1
+
+    def poly(self, ct, coeffs):
+        coeffs = np.asarray(coeffs, dtype=np.float64)
+        l, s = self.limbs(ct), self.scale(ct)
+        if abs(np.log2(s / self._q(l))) > 2.0**-12:
+            raise ValueError(f"a series input must sit at its level's prime ({self._q(l)}), got {s}")
+        ev = PSEvaluator(None, None, l, s, len(coeffs) - 1, self.primes, sim=True)
+        out = int(ev.evaluate(coeffs))
+        if out < 1:
+            raise ValueError("the series runs out of levels")
+        if np.max(np.abs(ct.values.real)) > 1.0 + 1e-9 or np.max(np.abs(ct.values.imag)) > 1e-9:
+            self.log.append(("poly input outside [-1, 1]", float(np.max(np.abs(ct.values)))))
+        vals = np.polynomial.chebyshev.chebval(ct.values.real, coeffs) + 0j
+        return SimCt(vals, out, canonical_scales(self.primes, l, s)[out])
+
+    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False):
+        prog = self.deep_program if deep else self.program
+        if self.limbs(ct) < 2:
+            raise ValueError("bootstrap needs at least two limbs")
+        peak = float(np.max(np.abs(ct.values)))
+        if peak > 2.0**int(bound_bits):
+            raise ValueError(f"refresh input {peak} above its bound 2^{bound_bits}")
+        self.refreshes += ct.batch_size
+        # two-pass: the program's output level less the correction's rescale
+        return SimCt(ct.values, prog.output_limbs - 1, self.scale(ct))
+
+    # -- linear layers: the shifted-lane BSGS sum (lane l of channel c covers inputs
+    #    [shift l, shift (l + 1)) of row c)
+    def linear_weight(self, matrix, lanes: int, baby_steps: int):
+        return (np.asarray(matrix, dtype=np.complex128), int(lanes))
+
+    def linear_prepare(self, ct, handle):
+        return None
+
+    def linear(self, ct, handle, prepared=None):
+        A, lanes = handle
+        D = A.shape[0]
+        shift = D // lanes
+        c = np.arange(D)[:, None]
+        j = np.arange(shift)[None, :]
+        xv = ct.values.reshape(ct.batch_size, D, lanes)
+        out = np.zeros_like(xv)
+        for l in range(lanes):
+            w = A[c, (c + j + shift * l) % D]                    # [D, shift]
+            out[:, :, l] = np.einsum("cj,bcj->bc", w, xv[:, (c + j) % D, l])
+        out = out.reshape(ct.batch_size, -1)
+        if self.limbs(ct) < 2:
+            raise ValueError("a linear layer needs two limbs")
+        return SimCt(out, self.limbs(ct) - 1, self.scale(ct))
+
+
+def make_programs(primes, L: int, scale: float):
+    """The (3, 3) and deep (2, 2) bootstrap programs of the parameter set (host planning only)."""
+
+    spec = B.BootstrapSpec(log_slots=15, level_budget=(3, 3))
+    deep = B.BootstrapSpec(log_slots=15, level_budget=(2, 2))
+    return B.plan_program(spec, primes, scale, L), B.plan_program(deep, primes, scale, L)
