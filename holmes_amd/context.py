@@ -445,6 +445,21 @@ class CKKSContext:
                                   ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_mul_relin")
         return out if stacked else (out[0], out[1])
 
+    def resident(self, table: np.ndarray) -> torch.Tensor:
+        """A small host table (residue weights, constants) on the device, uploaded once: a later
+        call with the same bytes reuses the device copy, so repeated evaluations (every bootstrap's
+        EvalMod, every step's polynomials) issue no host-to-device copy."""
+
+        a = np.ascontiguousarray(table)
+        key = (a.dtype.str, a.shape, a.tobytes())
+        cache = self.__dict__.setdefault("_resident", {})
+        t = cache.get(key)
+        if t is None:
+            if len(cache) >= 4096:
+                cache.clear()
+            t = cache[key] = torch.from_numpy(a.copy()).to(self.device)
+        return t
+
     def weighted_sum(self, x: torch.Tensor, weights: torch.Tensor, limbs: int) -> torch.Tensor:
         """out[g] = sum_j weights[g][j][l] x[j] per limb l: x [n][>= limbs][N], weights a uint64
         tensor [groups][n][limbs] of residues (moved to the device here)."""

@@ -432,6 +432,17 @@ def decode_key_rotations(pages: int, log_n: int = 16) -> tuple[int, ...]:
     return tuple(sorted(rots))
 
 
+class SlotConst:
+    """A public slot vector used again and again (masks, RoPE phases of one position): its
+    plaintext encodings are kept per (limbs, scale), so a repeated decode step encodes nothing."""
+
+    __slots__ = ("value", "cache")
+
+    def __init__(self, value):
+        self.value = np.asarray(value)
+        self.cache: dict = {}
+
+
 # ---------------------------------------------------------------------------- GPU operations
 class CipherOps:
     """The ciphertext operations the layer is written in, on the GPU: every result carries exact
@@ -450,6 +461,37 @@ class CipherOps:
                                                                                LinearOperatorConfig, LinearWeight)
         self.slots = int(ctx.max_slots)
         self.refreshes = 0
+        self._flags = torch.zeros(64, dtype=torch.int32, device=ctx.device)
+
+    def _encode(self, vec, limbs: int, scale: float):
+        """Plaintext of a slot vector at (limbs, scale); a SlotConst keeps its encodings.  The
+        overflow flags accumulate for one check in ``finish``."""
+
+        key = (int(limbs), float(scale))
+        if isinstance(vec, SlotConst):
+            hit = vec.cache.get(key)
+            if hit is not None:
+                return hit
+            v = vec.value
+        else:
+            v = np.asarray(vec)
+        ctx = self.ctx
+        re, im = ctx.slot_rows(v, self.slots)
+        poly = ctx.encode(re, float(scale), int(limbs), values_im=im, prime_idx=ctx.q_prime_idx(int(limbs)),
+                          flags=self._flags)
+        from .context import CipherState
+
+        pt = self._fhe.Plaintext(poly, CipherState(cur_limbs=int(limbs), scale_degree=1, scaling_factor=float(scale)),
+                                 slots=self.slots)
+        if isinstance(vec, SlotConst):
+            vec.cache[key] = pt
+        return pt
+
+    def finish(self) -> None:
+        """The one host synchronisation of a step: the deferred encode overflow check."""
+
+        self.ctx.check_encode_flags(self._flags)
+        self._flags.zero_()
 
     # -- bookkeeping
     def limbs(self, ct) -> int:
@@ -535,9 +577,7 @@ class CipherOps:
         return f.homo_add_scalar(ct, enc, self.ctx)
 
     def add_vec(self, ct, vec):
-        f = self._fhe
-        pt = f.encode_plaintext(np.asarray(vec), ct.state, self.slots, self.ctx)
-        return f.homo_add_pt(ct, pt, self.ctx)
+        return self._fhe.homo_add_pt(ct, self._encode(vec, self.limbs(ct), self.scale(ct)), self.ctx)
 
     def mul(self, a, b):
         f = self._fhe
@@ -575,12 +615,11 @@ class CipherOps:
             if self.limbs(c) > l:
                 c = f.align_to(c, c.state.replace(cur_limbs=l), ctx)
             pscale = T * q / self.scale(c)
-            if np.ndim(vec) == 0:
+            if not isinstance(vec, SlotConst) and np.ndim(vec) == 0:
                 enc = f.encode_scalar(float(vec), cur_limbs=l, scale_degree=1, scaling_factor=pscale, context=ctx)
                 prod = f.homo_mul_scalar(c, enc, ctx)
             else:
-                st = c.state.replace(cur_limbs=l, scale_degree=1, scaling_factor=pscale)
-                prod = f.homo_mul_pt(c, f.encode_plaintext(np.asarray(vec), st, self.slots, ctx), ctx)
+                prod = f.homo_mul_pt(c, self._encode(vec, l, pscale), ctx)
             prod = prod.cipher_like(prod.cv, state=prod.state.replace(scaling_factor=T * q))
             acc = prod if acc is None else f.homo_add(acc, prod, ctx)
         out = f.rescale(acc, ctx)
@@ -666,8 +705,18 @@ class DecodeLayer:
         self.rms_b = -(a_m + b_m) / (b_m - a_m)
         pair, f, lane = _grid()
         self._dst_t0 = page_slot(pair, f, 0, lane)
+        self._consts: dict = {}
 
     # -- helpers
+    def _const(self, key, make):
+        """A SlotConst built once per key (masks; RoPE phases per position; score masks per page
+        occupancy), so its encodings are reused by every later step."""
+
+        c = self._consts.get(key)
+        if c is None:
+            c = self._consts[key] = SlotConst(make())
+        return c
+
     def _fold(self, ct, strides):
         for s in strides:
             ct = self.ops.rotate_add(ct, s)
@@ -706,13 +755,16 @@ class DecodeLayer:
         pair, f, lane = _grid()
         col = int(cache.content_tokens) % sp.page_size
 
-        def coef(values_f, ln):
-            v = np.zeros(SLOTS, dtype=np.complex128)
-            sel = lane == ln
-            v[self._dst_t0[sel]] = values_f[f[sel]]
-            return v
+        def coef(kind, ln):
+            def make():
+                vals = {"q": ph, "k": np.conj(ph), "v": np.ones(64, dtype=np.complex128)}[kind]
+                v = np.zeros(SLOTS, dtype=np.complex128)
+                sel = lane == ln
+                v[self._dst_t0[sel]] = vals[f[sel]]
+                return v
 
-        one = np.ones(64, dtype=np.complex128)
+            return self._const(("route", kind, ln, position if kind != "v" else None), make)
+
         rot_cache: dict = {}
 
         def rot_u(rr):
@@ -722,10 +774,10 @@ class DecodeLayer:
 
         kt, vt, qt = [], [], []
         for g in range(2):
-            kt.append(ops.mac([(rot_u(8 * _k_j(g, ln) - ln), coef(np.conj(ph), ln)) for ln in range(2)]))
-            vt.append(ops.mac([(rot_u(8 * _v_j(g, ln) - ln), coef(one, ln)) for ln in range(2)]))
+            kt.append(ops.mac([(rot_u(8 * _k_j(g, ln) - ln), coef("k", ln)) for ln in range(2)]))
+            vt.append(ops.mac([(rot_u(8 * _v_j(g, ln) - ln), coef("v", ln)) for ln in range(2)]))
             for o in range(4):
-                qt.append(ops.mac([(rot_u(8 * _q_j(g, ln, o) - ln), coef(ph, ln)) for ln in range(2)]))
+                qt.append(ops.mac([(rot_u(8 * _q_j(g, ln, o) - ln), coef("q", ln)) for ln in range(2)]))
         del rot_cache
         kv = ops.batch(kt + vt)
         if col:
@@ -755,32 +807,37 @@ class DecodeLayer:
         prod = self._fold(ops.mul(qrep, kpages), tuple(BLOCK << k for k in range(6)))
         ms = [8 * p + 4 * g + o for p in range(npg) for g in range(2) for o in range(4)]
         rit = ops.items(ops.rotate(prod, [(-BLOCK * m) % SLOTS for m in ms]))
-        valid = np.zeros(SLOTS)
-        terms = []
-        for i, m in enumerate(ms):
+        okey = tuple(occ)
+
+        def block_mask(m):
             tt = np.arange(occ[m // 8])
-            mk = _mask(np.concatenate([PAIR_STRIDE * pr + BLOCK * m + 2 * tt + ln for pr in range(2)
-                                       for ln in range(2)]))
-            valid += mk
-            terms.append((rit[i], 0.5 * self.alpha * mk))
+            return _mask(np.concatenate([PAIR_STRIDE * pr + BLOCK * m + 2 * tt + ln for pr in range(2)
+                                         for ln in range(2)]))
+
+        valid = self._const(("valid", okey), lambda: sum(block_mask(m) for m in ms)).value
+        terms = [(rit[i], self._const(("score", m, okey), lambda m=m: 0.5 * self.alpha * block_mask(m)))
+                 for i, m in enumerate(ms)]
         S = ops.mac(terms, out_scale=ops.ideal_scale(ops.limbs(prod) - 1))
-        S = ops.add_vec(ops.add(S, ops.conj(S)), self.beta * valid)
+        S = ops.add_vec(ops.add(S, ops.conj(S)), self._const(("beta", okey), lambda: self.beta * valid))
         T["qk"] = time.perf_counter() - t0
         # --- softmax: gamma exp (invalid slots hold the public value of the series at 0 and are
         # cleared by a plaintext subtraction), row sums of squares, 1/sqrt on a refreshed copy
         # (non-row slots again a public constant), broadcast, p = (y lambda)^2, refreshed
         t0 = time.perf_counter()
         ce = self.gamma * P.exp
-        ym = ops.add_vec(ops.poly(S, ce), -float(np.polynomial.chebyshev.chebval(0.0, ce)) * (1.0 - valid))
+        ym = ops.add_vec(ops.poly(S, ce), self._const(("exp0", okey), lambda: -float(
+            np.polynomial.chebyshev.chebval(0.0, ce)) * (1.0 - valid)))
         npad = _pages_pad(npg)
         page_strides = tuple((8 * BLOCK) << k for k in range(npad.bit_length() - 1))
         rs = self._fold(ops.mul(ym, ym), tuple(2 << k for k in range(7)) + page_strides)
         rows = _mask([PAIR_STRIDE * pr + BLOCK * r + ln for pr in range(2) for r in range(8) for ln in range(2)])
-        rs = ops.refresh(ops.mac([(rs, rows)], out_scale=ops.ideal_scale(ops.refresh_limbs(deep=True))),
+        rs = ops.refresh(ops.mac([(rs, self._const("rows", lambda: rows))],
+                                 out_scale=ops.ideal_scale(ops.refresh_limbs(deep=True))),
                          bound_bits=sp.rowsum_bound_bits, deep=True)
         cl = P.rsqrt / self.gamma
-        lam = ops.poly(ops.add_vec(rs, self.b_r * rows), cl)
-        lam = ops.add_vec(lam, -float(np.polynomial.chebyshev.chebval(0.0, cl)) * (1.0 - rows))
+        lam = ops.poly(ops.add_vec(rs, self._const("rows_shift", lambda: self.b_r * rows)), cl)
+        lam = ops.add_vec(lam, self._const("rows_clear", lambda: -float(
+            np.polynomial.chebyshev.chebval(0.0, cl)) * (1.0 - rows)))
         lam = self._fold(lam, tuple(SLOTS - (2 << k) for k in range(7)) + tuple(SLOTS - s for s in page_strides))
         lv = min(ops.limbs(ym), ops.limbs(lam))
         t = ops.mul(self._drop(ym, lv), self._drop(lam, lv))
@@ -788,7 +845,7 @@ class DecodeLayer:
         T["softmax"] = time.perf_counter() - t0
         # --- PV: each score block broadcast over the features of its page, times the value page
         t0 = time.perf_counter()
-        blk0 = _mask([PAIR_STRIDE * pr + j for pr in range(2) for j in range(BLOCK)])
+        blk0 = self._const("block0", lambda: _mask([PAIR_STRIDE * pr + j for pr in range(2) for j in range(BLOCK)]))
         xp = ops.rotate(prob, [BLOCK * m for m in ms])
         xp = self._fold(ops.mac([(xp, blk0)]), tuple(SLOTS - (BLOCK << k) for k in range(6)))
         vpages = ops.batch([pages[m // 8].value_groups[(m // 4) % 2] for m in ms])
@@ -810,13 +867,15 @@ class DecodeLayer:
         for g in range(2):
             for o in range(4):
                 for ln in range(2):
-                    dst = (PAIR_STRIDE * pair + BLOCK * f + 16 * _z_j(g, o, ln))[lane == 0]
-                    zt.append((ops.rotate(oit[4 * g + o], ln - 16 * _z_j(g, o, ln)), _mask(dst)))
+                    jz = _z_j(g, o, ln)
+                    zt.append((ops.rotate(oit[4 * g + o], ln - 16 * jz), self._const(
+                        ("z", jz), lambda jz=jz: _mask((PAIR_STRIDE * pair + BLOCK * f + 16 * jz)[lane == 0]))))
         z = self._fold(ops.mac(zt), (2047, 4094, 8188, 16376))
         prep = ops.linear_prepare(z, self.wo[0])
         ub = ops.items(self._fold(ops.batch([ops.linear(z, w, prepared=prep) for w in self.wo]), (1, 2, 4, 8)))
         c16 = np.arange(2048) * 16
-        w = ops.mac([(ub[0], 0.5 * _mask(c16)), (ops.rotate(ub[1], SLOTS - 8), 0.5 * _mask(c16 + 8))])
+        w = ops.mac([(ub[0], self._const("wo0", lambda: 0.5 * _mask(c16))),
+                     (ops.rotate(ub[1], SLOTS - 8), self._const("wo1", lambda: 0.5 * _mask(c16 + 8)))])
         ya = ops.add(w, ops.conj(w))
         h1 = ops.add(ops.adjust(x, ops.limbs(ya), ops.scale(ya)), ya)
         T["attention_output"] = time.perf_counter() - t0
@@ -837,25 +896,28 @@ class DecodeLayer:
         # SiLU series needs at the refresh's output level
         lv = min(ops.limbs(ug[0]) - 1, ops.limbs(r2))
         want = ops.ideal_scale(ops.refresh_limbs(deep=True)) * ops.ideal_scale(lv) / ops.scale(r2)
-        uraw = ops.mac([(c, (lanes == b).astype(np.float64)) for b, c in enumerate(ug)], out_scale=want)
+        uraw = ops.mac([(c, self._const(("lane", b), lambda b=b: (lanes == b).astype(np.float64)))
+                        for b, c in enumerate(ug)], out_scale=want)
         U = ops.refresh(ops.mul(self._drop(uraw, lv), self._drop(r2, lv)), deep=True)
         Uc = ops.conj(U)
         gate_u = ops.add(U, Uc)
         up_u = ops.mul_i(ops.sub(U, Uc), negative=True)
         sg = ops.poly(gate_u, P.silu)
         hact = ops.refresh(ops.mul(sg, self._drop(up_u, ops.limbs(sg))), bound_bits=sp.act_bound_bits)
-        m0 = (lanes == 0).astype(np.float64)
+        m0 = self._const(("lane", 0), lambda: (lanes == 0).astype(np.float64))
+        m0i = self._const("lane0_i", lambda: 1j * (lanes == 0))
         hri = ops.items(ops.rotate(hact, [1, 2, 3]))
-        z0 = ops.mac([(hact, m0), (hri[0], 1j * m0)])
-        z1 = ops.mac([(hri[1], m0), (hri[2], 1j * m0)])
+        z0 = ops.mac([(hact, m0), (hri[0], m0i)])
+        z1 = ops.mac([(hri[1], m0), (hri[2], m0i)])
         zz = ops.items(self._sl8(ops.batch([z0, z1])))
         yd = None
         for zb, wb in zip(zz, self.down):
             yb = ops.linear(zb, wb)
             yd = yb if yd is None else ops.add(yd, yb)
-        mm = ops.mac([(self._fold(yd, (1, 2, 4)), 0.5 * m0)])
+        mm = ops.mac([(self._fold(yd, (1, 2, 4)), self._const("lane0_half", lambda: 0.5 * (lanes == 0)))])
         ym2 = ops.add(mm, ops.conj(mm))
         out = ops.add(ops.adjust(h1r, ops.limbs(ym2), ops.scale(ym2)), ym2)
+        ops.finish()
         T["mlp"] = time.perf_counter() - t0
         return out, T, token
 

@@ -112,7 +112,7 @@ class PSEvaluator:
         out = fhe._alloc(ctx, 2, B, limbs)
         xs = [[x.cv[c][b] for x in terms] for c in range(2) for b in range(B)]
         ctx.lincomb(xs, limbs, [out[c][b] for c in range(2) for b in range(B)],
-                    torch.from_numpy(np.ascontiguousarray(weights, dtype=np.uint64)).to(ctx.device))
+                    ctx.resident(np.asarray(weights, dtype=np.uint64)))
         return out
 
     def _residues(self, value: float, limbs: int, scaling_factor: float, integer: bool = False) -> np.ndarray:

@@ -132,7 +132,15 @@ class SlotOps:
     def add_const(self, ct, c: float):
         return self._like(ct, ct.values + float(c))
 
+    @staticmethod
+    def _val(vec):
+        return vec.value if hasattr(vec, "value") else vec
+
+    def finish(self):
+        pass
+
     def add_vec(self, ct, vec):
+        vec = self._val(vec)
         return self._like(ct, ct.values + np.asarray(vec)[None, :] if np.ndim(vec) == 1 else ct.values + vec)
 
     def mul(self, a, b):
@@ -161,6 +169,7 @@ class SlotOps:
         T = self.scale(terms[0][0]) if out_scale is None else float(out_scale)
         acc = None
         for c, vec in terms:
+            vec = self._val(vec)
             v = c.values * (np.asarray(vec)[None, :] if np.ndim(vec) == 1 else vec)
             acc = v if acc is None else acc + v
         return SimCt(acc, l - 1, T)
