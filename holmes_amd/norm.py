@@ -22,7 +22,7 @@ import numpy as np
 from . import fhe
 from .context import Cipher, CKKSContext
 from .layouts import FeatureMajorPrefillLayout
-from .polynomial import chebyshev_coefficients, eval_chebyshev
+from .polynomial import chebyshev_coefficients, entry_coefficients, eval_chebyshev, series_from_entry
 
 __all__ = ["FeatureMajorRMSNormResult", "rmsnorm_coefficients", "rmsnorm_fhe", "rmsnorm_numpy", "rmsnorm_rotations"]
 
@@ -42,10 +42,12 @@ def rmsnorm_rotations(layout: FeatureMajorPrefillLayout) -> tuple:
 
 
 def rmsnorm_coefficients(degree: int = 15, interval=(0.5, 2.0), eps: float = 1e-5) -> dict:
-    """Chebyshev interpolant of 1 / sqrt(m + eps) on ``interval`` of the mean square m."""
+    """Chebyshev interpolant of 1 / sqrt(m + eps) on ``interval`` of the mean square m, as the
+    reference's coefficient dictionary (its evaluator halves the constant term)."""
 
-    return {"coefficients": chebyshev_coefficients(lambda m: 1.0 / np.sqrt(m + eps), degree, interval),
-            "fit_interval": tuple(float(v) for v in interval), "eps": float(eps)}
+    series = chebyshev_coefficients(lambda m: 1.0 / np.sqrt(m + eps), degree, interval)
+    return {"coefficients": entry_coefficients(series), "fit_interval": tuple(float(v) for v in interval),
+            "eps": float(eps)}
 
 
 def rmsnorm_numpy(x: np.ndarray, weight: np.ndarray | None, coeffs: dict) -> np.ndarray:
@@ -54,7 +56,7 @@ def rmsnorm_numpy(x: np.ndarray, weight: np.ndarray | None, coeffs: dict) -> np.
     x = np.asarray(x, dtype=np.float64)
     lo, hi = coeffs["fit_interval"]
     m = np.mean(x * x, axis=1, keepdims=True)
-    r = np.polynomial.chebyshev.chebval((2.0 * m - (lo + hi)) / (hi - lo), coeffs["coefficients"])
+    r = np.polynomial.chebyshev.chebval((2.0 * m - (lo + hi)) / (hi - lo), series_from_entry(coeffs))
     y = x * r
     return y if weight is None else y * np.asarray(weight, dtype=np.float64)[None, :]
 
@@ -96,7 +98,7 @@ def rmsnorm_fhe(input_ciphers, weight: np.ndarray | None = None, *, coeffs: dict
     t0 = time.perf_counter()
     lo, hi = (float(v) for v in coeffs["fit_interval"])
     D = float(layout.hidden_dim)
-    r = eval_chebyshev(s, coeffs["coefficients"], ctx, interval=(D * lo, D * hi))
+    r = eval_chebyshev(s, series_from_entry(coeffs), ctx, interval=(D * lo, D * hi))
     times["rsqrt_polynomial"] = time.perf_counter() - t0
     sched["rsqrt_output_limbs"] = int(r.state.cur_limbs)
     t0 = time.perf_counter()

@@ -21,7 +21,7 @@ from . import fhe
 from .context import Cipher, CKKSContext, u64_cat
 
 __all__ = ["PSEvaluator", "canonical_scales", "chebyshev_divide", "chebyshev_coefficients", "eval_chebyshev",
-           "chebyshev_depth"]
+           "chebyshev_depth", "series_from_entry", "entry_coefficients"]
 
 
 def chebyshev_divide(coeffs: np.ndarray, M: int) -> tuple[np.ndarray, np.ndarray]:
@@ -250,6 +250,26 @@ def chebyshev_coefficients(fn, degree: int, interval=(-1.0, 1.0)) -> np.ndarray:
     if not b > a:
         raise ValueError("interval must be increasing")
     return np.polynomial.chebyshev.chebinterpolate(lambda u: fn(0.5 * (b - a) * u + 0.5 * (a + b)), int(degree))
+
+
+def series_from_entry(entry: dict) -> np.ndarray:
+    """The numpy-convention series (sum_j c_j T_j) of a reference coefficient dictionary, whose
+    evaluator halves the constant term (llama3fhe/approx/chebyshev.py:136-163: c_0 / 2 +
+    sum_(j>=1) c_j T_j)."""
+
+    c = np.array(entry["coefficients"], dtype=np.float64)
+    if len(c):
+        c[0] *= 0.5
+    return c
+
+
+def entry_coefficients(series) -> np.ndarray:
+    """Coefficients in the reference dictionary's convention for a numpy-convention series."""
+
+    c = np.array(series, dtype=np.float64)
+    if len(c):
+        c[0] *= 2.0
+    return c
 
 
 def chebyshev_depth(degree: int) -> int:
