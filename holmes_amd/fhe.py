@@ -236,6 +236,12 @@ def _binary(a: Cipher, b: Cipher, ctx: CKKSContext, op: int) -> Cipher:
     idx = ctx.q_prime_idx(limbs)
     comps = max(len(a.cv), len(b.cv))
     bufs = _alloc(ctx, comps, a.batch_size, limbs)
+    if len(a.cv) == len(b.cv) == comps > 1:
+        # components back to back in both operands: one launch over comps * batch rows
+        ja, jb = _joined(a.cv, limbs, ctx.N), _joined(b.cv, limbs, ctx.N)
+        if ja is not None and jb is not None:
+            ctx.poly_op(op, _joined(bufs, limbs, ctx.N), ja, jb, prime_idx=idx)
+            return a.cipher_like(bufs, state=a.state.replace(cur_limbs=limbs))
     out = []
     for c in range(comps):
         o = bufs[c]
@@ -304,8 +310,14 @@ def homo_mul_pt(ct: Cipher, pt: Plaintext, ctx: CKKSContext) -> Cipher:
     if p.shape[0] == 1 and ct.batch_size > 1:
         p = p.expand(ct.batch_size, -1, -1)  # batch stride 0: one plaintext for every item
     out = _alloc(ctx, len(ct.cv), int(ct.cv[0].shape[0]), limbs)
-    for o, x in zip(out, ct.cv):
-        ctx.poly_op(nat.HCK_OP_MUL, o, _view(x, limbs), p, prime_idx=idx)
+    jx = _joined(ct.cv, limbs, ctx.N) if len(ct.cv) > 1 and pt.cv[0].shape[0] == 1 else None
+    if jx is not None:
+        # one plaintext for every row of the joined components (batch stride 0)
+        pj = _view(pt.cv[0], limbs).expand(jx.shape[0], -1, -1)
+        ctx.poly_op(nat.HCK_OP_MUL, _joined(out, limbs, ctx.N), jx, pj, prime_idx=idx)
+    else:
+        for o, x in zip(out, ct.cv):
+            ctx.poly_op(nat.HCK_OP_MUL, o, _view(x, limbs), p, prime_idx=idx)
     st = ct.state
     state = st.replace(
         cur_limbs=limbs,
@@ -651,8 +663,12 @@ def homo_mul_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
     idx = ctx.q_prime_idx(limbs)
     sc = _scalar_list(enc, limbs)
     out = _alloc(ctx, len(ct.cv), int(ct.cv[0].shape[0]), limbs)
-    for o, x in zip(out, ct.cv):
-        ctx.poly_op(nat.HCK_OP_MUL_SCALAR, o, _view(x, limbs), prime_idx=idx, scalar=sc)
+    jx = _joined(ct.cv, limbs, ctx.N) if len(ct.cv) > 1 else None
+    if jx is not None:
+        ctx.poly_op(nat.HCK_OP_MUL_SCALAR, _joined(out, limbs, ctx.N), jx, prime_idx=idx, scalar=sc)
+    else:
+        for o, x in zip(out, ct.cv):
+            ctx.poly_op(nat.HCK_OP_MUL_SCALAR, o, _view(x, limbs), prime_idx=idx, scalar=sc)
     st = ct.state
     state = st.replace(cur_limbs=limbs, scale_degree=int(st.scale_degree) + enc.scale_degree,
                        scaling_factor=float(st.scaling_factor) * enc.scaling_factor)
