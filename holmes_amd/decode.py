@@ -710,12 +710,21 @@ class DecodeLayer:
     # -- helpers
     def _const(self, key, make):
         """A SlotConst built once per key (masks; RoPE phases per position; score masks per page
-        occupancy), so its encodings are reused by every later step."""
+        occupancy), so its encodings are reused by every later step.  Keys tagged with a position
+        or an occupancy keep only the latest tag: a long decode run does not accumulate them."""
 
         c = self._consts.get(key)
         if c is None:
+            tag = key[-1] if isinstance(key, tuple) and key[0] in self._TAGGED else None
+            if tag is not None:
+                stale = [k for k in self._consts
+                         if isinstance(k, tuple) and k[0] == key[0] and k[-1] is not None and k[-1] != tag]
+                for k in stale:
+                    del self._consts[k]
             c = self._consts[key] = SlotConst(make())
         return c
+
+    _TAGGED = ("route", "valid", "score", "beta", "exp0")
 
     def _fold(self, ct, strides):
         for s in strides:
@@ -797,6 +806,8 @@ class DecodeLayer:
         cache.append(token, crypto_context=crypto_context)
         pages = cache.pages
         npg = len(pages)
+        if npg > 8:
+            raise ValueError("the compact score layout holds at most 8 pages (1024 tokens)")
         occ = [int(p.occupied) for p in pages]
         T["kv_append"] = time.perf_counter() - t0
         # --- QK: 8 query streams x pages, fold the features, compact into one score ciphertext

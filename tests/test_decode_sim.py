@@ -169,3 +169,39 @@ def test_decode_layer_on_slot_simulator(history):
         prev = Dm.pack_key_page(ck[history - col:history], 0)
         assert np.allclose(k_page, prev + want, atol=1e-9)
     assert ops.limbs(last.key_groups[0]) == spec.key_limbs and ops.limbs(last.value_groups[1]) == spec.value_limbs
+
+
+def test_two_consecutive_steps_on_slot_simulator():
+    """Step two reads the page the first step opened (column 1 of the third page): its output
+    follows the float64 semantics over the grown history, and the first step's position-tagged
+    constants are gone."""
+
+    spec, w, x, ck, cv = _setup(history=256)
+    q, S = _chain()
+    prog, deep = make_programs(q, 24, S)
+    ops = SlotOps(q, prog, deep)
+    layer = Dm.DecodeLayer(ops, w, spec)
+    pages = []
+    for p in range(0, 256, 128):
+        kg = [SimCt(Dm.pack_key_page(ck[p:p + 128], g), spec.key_limbs, S) for g in range(2)]
+        vg = [SimCt(Dm.pack_value_page(cv[p:p + 128], g), spec.value_limbs, S) for g in range(2)]
+        pages.append(PairFoldCipherPage(kg, vg, 128))
+    cache = PairFoldLayerCache(pages=tuple(pages), content_tokens=256)
+
+    class _CC:
+        class fhe:
+            @staticmethod
+            def homo_add(a, b, ctx):
+                return ops.add(a, b)
+        context = None
+
+    layer.forward(SimCt(Dm.lr8(x), 24, S), cache, position=256, crypto_context=_CC)
+    first = Dm.decode_layer_numpy(x, ck, cv, w, spec, position=256)
+    x2 = np.random.default_rng(7).normal(size=spec.hidden_dim)
+    out, _, _ = layer.forward(SimCt(Dm.lr8(x2), 24, S), cache, position=257, crypto_context=_CC)
+    ref = Dm.decode_layer_numpy(x2, np.vstack([ck, first["k"]]), np.vstack([cv, first["v"]]), w, spec,
+                                position=257)
+    got = out.values[0, ::8].real
+    assert np.max(np.abs(got - ref["output"])) < 1e-9 * np.max(np.abs(ref["output"]))
+    assert cache.content_tokens == 258 and cache.pages[-1].occupied == 2
+    assert not any(isinstance(k, tuple) and k[0] == "route" and k[-1] == 256 for k in layer._consts)
