@@ -89,3 +89,28 @@ def test_linear_residues_match_oracle_composition(env):
             tot1 = ((tot1.astype(object) + a1.astype(object)) % q).astype(np.uint64)
     w0, w1 = orc.rescale(LIMBS, tot0), orc.rescale(LIMBS, tot1)
     assert np.array_equal(g0[: LIMBS - 1], w0) and np.array_equal(g1[: LIMBS - 1], w1)
+
+
+@pytest.mark.parametrize("strategy", ["normal", "ext_double_hoist"])
+def test_shifted_lane_linear_decrypts_to_matvec(env, strategy):
+    """Shifted-lane plan (lane_shift = D / lanes: 32 diagonals for D = 256) on a complex weight:
+    the lanes of every output channel sum to (W + i V) x (llama3fhe/layouts/shifted_lane.py)."""
+
+    fhe, linear, client, ctx, cfg, plan, W, X = env
+    shift = D // LANES
+    scfg = linear.LinearOperatorConfig(baby_steps=8, baby_anchor_step=-1, max_plaintext_rows=16,
+                                       hoist_strategy=strategy, lane_shift=shift)
+    splan = scfg.plan(dimension=D, token_lanes=LANES)
+    assert splan.diagonals == shift and splan.plaintext_chunks == 2
+    client.generate_rotation_keys(linear.bsgs_rotations(splan, strategy))
+    rng = np.random.default_rng(9)
+    V = rng.normal(scale=1.0 / np.sqrt(D), size=(D, D))
+    x = rng.normal(size=D)
+    s = np.arange(ctx.max_slots)
+    carrier = x[((s // LANES) + shift * (s % LANES)) % D]
+    ct = client.encrypt(carrier, cur_limbs=LIMBS)
+    op = linear.LinearOperator(crypto_context=ctx, token_lanes=LANES, config=scfg)
+    out = op.project([ct], linear.LinearWeight(W, crypto_context=ctx, imag=V))[0]
+    assert out.state.cur_limbs == LIMBS - 1
+    got = client.decrypt(out).reshape(-1, LANES).sum(axis=1)[:D]
+    assert np.max(np.abs(got - (W + 1j * V) @ x)) < 2.0**-16
