@@ -3,9 +3,10 @@
 //   k_pack_diagonals   weight rows of one BSGS chunk (llama3fhe/operators/linear/weight.py:122-154)
 //   k_sifft_cols       special inverse FFT stages with half-width 16384 .. 128 (column pass)
 //   k_sifft_rows       stages 64 .. 1 (row pass)
-//   k_encode_finish    bit-reversed gather, * 1/n, * scale, round half away from zero, residues of
-//                      every limb (Re -> coefficient k, Im -> coefficient k + n: the interleave of
-//                      bench/cmp/kernels/holmes_encode.cu:108-111), then the forward NTT.
+//   k_encode_cols      (ntt.hip) bit-reversed gather, * 1/n, * scale, round half away from zero
+//                      (Re -> coefficient k, Im -> coefficient k + n: the interleave of
+//                      bench/cmp/kernels/holmes_encode.cu:108-111), then per limb the residue and
+//                      the forward NTT's column pass; k_fwd_rows finishes the NTT.
 //
 // The special IFFT is the textbook CKKS encoder over the rotation group; the butterfly, complex
 // product and rounding are the exact IEEE operation sequence of the oracle (floating-point
@@ -177,40 +178,6 @@ __global__ __launch_bounds__(256) void k_sifft_rows(double* __restrict__ vre, do
   }
 }
 
-// Round half away from zero (llround semantics), written out: the library round() of this
-// toolchain does not send negative ties away from zero.
-__device__ __forceinline__ double round_away(double x) {
-  double r = __builtin_trunc(x);
-  const double d = x - r;  // exact
-  if (d >= 0.5) r += 1.0;
-  else if (d <= -0.5) r -= 1.0;
-  return r;
-}
-
-struct PrimeList {
-  uint8_t prime[kMaxPrimes];
-};
-
-__global__ __launch_bounds__(256) void k_encode_finish(const double* __restrict__ vre, const double* __restrict__ vim,
-                                                       double scale, int limbs, PrimeList pl, uint64_t* __restrict__ out,
-                                                       long long out_row_stride, int* __restrict__ overflow,
-                                                       DevTables T) {
-  const int k = blockIdx.x * 256 + threadIdx.x;
-  const long long row = blockIdx.y;
-  const int s = (int)(__brev((unsigned)k) >> (32 - kLogSlots));
-  const double inv_n = 1.0 / (double)kSlots;
-  const double wr = vre[row * kSlots + s] * inv_n, wi = vim[row * kSlots + s] * inv_n;
-  const double a = round_away(wr * scale), b = round_away(wi * scale);
-  if (fabs(a) >= kTwo52 || fabs(b) >= kTwo52) overflow[row] = 1;
-  uint64_t* o = out + row * out_row_stride;
-  for (int l = 0; l < limbs; ++l) {
-    const int pi = pl.prime[l];
-    const double p = T.p[pi], pinv = T.pinv[pi];
-    o[(long long)l * kN + k] = d2u(canon(a, p, pinv));
-    o[(long long)l * kN + k + kSlots] = d2u(canon(b, p, pinv));
-  }
-}
-
 }  // namespace
 }  // namespace hck
 
@@ -240,12 +207,10 @@ extern "C" int hck_encode(const hck_context* ctx, const double* values, const do
   if (limbs < 1 || limbs > hck::kMaxPrimes || !(scale > 0.0)) return HCK_ERR_ARG;
   if (rows == 0) return HCK_OK;
   if (!workspace || workspace_bytes < hck_encode_workspace_bytes(ctx, rows)) return HCK_ERR_WORKSPACE;
-  hck::PrimeList pl{};
   hck::LimbList L;
   L.n = limbs;
   for (int l = 0; l < limbs; ++l) {
     if (prime_idx[l] < 0 || prime_idx[l] >= ctx->np) return HCK_ERR_ARG;
-    pl.prime[l] = (uint8_t)prime_idx[l];
     L.off[l] = (uint16_t)l;
     L.prime[l] = (uint8_t)prime_idx[l];
   }
@@ -257,8 +222,6 @@ extern "C" int hck_encode(const hck_context* ctx, const double* values, const do
   HCK_CHECK_LAUNCH();
   hck::k_sifft_rows<<<dim3(256 / 32, rows), 256, 0, s>>>(vre, vim, ctx->d_enc_twr, ctx->d_enc_twi);
   HCK_CHECK_LAUNCH();
-  hck::k_encode_finish<<<dim3(hck::kSlots / 256, rows), 256, 0, s>>>(vre, vim, scale, limbs, pl, out, out_row_stride,
-                                                                       overflow_flags, ctx->dev);
-  HCK_CHECK_LAUNCH();
-  return hck::launch_ntt_fwd(ctx, out, hck::kU64, out, hck::kU64, rows, out_row_stride, out_row_stride, L, s);
+  // rounding, residues and the NTT's column pass in one kernel, then the row pass
+  return hck::launch_encode_ntt(ctx, vre, vim, scale, out, out_row_stride, rows, overflow_flags, L, s);
 }

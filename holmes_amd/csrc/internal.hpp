@@ -85,6 +85,11 @@ int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
 int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
+// Encode's rounding fused with the forward NTT: vre / vim are the special IFFT's [rows][N/2]
+// outputs (natural slot order); out gets rows NTT-domain polys over `list`, overflow[row] set when a
+// rounded coefficient reaches 2^52.
+int launch_encode_ntt(const hck_context* c, const double* vre, const double* vim, double scale, uint64_t* out,
+                      long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s);
 
 size_t ks_fused_bytes(const hck_context* c, int ell, int batch);
 // d and add are read through sigma_galois (galois == 1: unpermuted), or through sigma of

@@ -80,4 +80,15 @@ __device__ __forceinline__ double mulv(double a, double b, double p, double pinv
   return __builtin_fma(-q, p, h) + l;
 }
 
+// Round half away from zero (llround semantics), written out: the library round() of this
+// toolchain does not send negative ties away from zero.  trunc, one exact subtraction and two
+// comparisons: no product to contract, so the result is the same in every translation unit.
+__device__ __forceinline__ double round_away(double x) {
+  double r = __builtin_trunc(x);
+  const double d = x - r;  // exact
+  if (d >= 0.5) r += 1.0;
+  else if (d <= -0.5) r -= 1.0;
+  return r;
+}
+
 }  // namespace hck

@@ -266,6 +266,82 @@ __global__ __launch_bounds__(kThreads) void k_inv_cols(void* data, long long str
   for (int k = 0; k < 16; ++k) st<OUT>(m, (long long)(j + 16 * k) * 256 + c, x[k], p, pinv);
 }
 
+// ---------------------------------------------------------------------------- encode + cols
+// The encoder's last step fused with the column pass: the block of 16 columns of one plaintext row
+// loads each coefficient once (the special IFFT output gathered in bit-reversed order, * 1/n,
+// * scale, rounded half away from zero: coefficient n < N/2 from the real part of slot brev(n),
+// n >= N/2 from the imaginary part of slot brev(n - N/2)), then for every limb takes the residue
+// in [0, p) and runs stages 0..7 exactly as k_fwd_cols<kU64> does on stored residues, so the result
+// is bit-identical to rounding, storing every limb and transforming.  The residues of all limbs
+// never reach HBM.
+__global__ __launch_bounds__(kThreads) void k_encode_cols(const double* __restrict__ vre,
+                                                          const double* __restrict__ vim, double scale,
+                                                          double* __restrict__ out, long long out_stride,
+                                                          LimbList list, int* __restrict__ overflow,
+                                                          DevTables T) {
+  __shared__ double sh[kLds];
+  const long long row = blockIdx.y;
+  const int tid = threadIdx.x, cl = tid & 15, j = tid >> 4, c = blockIdx.x * 16 + cl;
+  const double* re = vre + row * (kN / 2);
+  const double* im = vim + row * (kN / 2);
+  double a[16];
+  bool big = false;
+  {
+#pragma clang fp contract(off)
+    const double inv_n = 1.0 / (double)(kN / 2);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const int n = (j + 16 * k) * 256 + c;
+      const int h = n >= kN / 2;
+      const int slot = (int)(__brev((unsigned)(n - h * (kN / 2))) >> (32 - (kLogN - 1)));
+      const double w = (h ? im : re)[slot] * inv_n;
+      a[k] = round_away(w * scale);
+      big |= fabs(a[k]) >= kTwo52;
+    }
+  }
+  if (big) overflow[row] = 1;
+  double* d = out + row * out_stride;
+  for (int e = 0; e < list.n; ++e) {
+    const int pi = list.prime[e];
+    const double p = T.p[pi], pinv = T.pinv[pi];
+    const double* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
+    double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = canon(a[k], p, pinv);
+#pragma unroll
+    for (int l = 0; l < 4; ++l) {
+      const int hh = 8 >> l;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k & hh) continue;
+        const double w = tw[(1 << l) + (k >> (4 - l))];
+        if (l & 1) ct<false>(x[k], x[k + hh], w, p, pinv);
+        else ct<true>(x[k], x[k + hh], w, p, pinv);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) sh[cidx(j + 16 * k, cl)] = x[k];
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = sh[cidx(16 * j + k, cl)];
+    __syncthreads();  // the next limb rewrites sh
+#pragma unroll
+    for (int l = 4; l < 8; ++l) {
+      const int hh = 128 >> l;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        if (k & hh) continue;
+        const double w = tw[(1 << l) + (j << (l - 4)) + (k >> (8 - l))];
+        if (l & 1) ct<false>(x[k], x[k + hh], w, p, pinv);
+        else ct<true>(x[k], x[k + hh], w, p, pinv);
+      }
+    }
+    double* dl = d + (long long)list.off[e] * kN;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) dl[(long long)(16 * j + k) * 256 + c] = x[k];
+  }
+}
+
 }  // namespace
 
 int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
@@ -281,6 +357,17 @@ int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
     k_fwd_rows<kU64><<<grid, kThreads, 0, s>>>(dst, dst_stride, list, c->dev);
   else
     k_fwd_rows<kF64><<<grid, kThreads, 0, s>>>(dst, dst_stride, list, c->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int launch_encode_ntt(const hck_context* c, const double* vre, const double* vim, double scale, uint64_t* out,
+                      long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s) {
+  if (list.n <= 0 || rows <= 0) return HCK_OK;
+  if (list.n > kMaxList || rows > 65535) return HCK_ERR_ARG;
+  k_encode_cols<<<dim3(16, rows), kThreads, 0, s>>>(vre, vim, scale, (double*)out, out_stride, list, overflow,
+                                                     c->dev);
+  k_fwd_rows<kU64><<<dim3(16, list.n, rows), kThreads, 0, s>>>(out, out_stride, list, c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }
