@@ -340,15 +340,50 @@ class PackedRaw:
         return np.asarray(v)
 
 
+class UnpackedRaw:
+    """A constant whose slot values a packer builds on first use: ``packer(source, slots,
+    context)`` (llama3fhe/operators/linear/weight.py:458-465), so a bundle that is never encoded
+    never packs."""
+
+    def __init__(self, source, packer):
+        self.source, self.packer = source, packer
+        self._packed: dict = {}
+
+    def values(self, slots: int, context: CKKSContext):
+        key = int(slots)
+        if key not in self._packed:
+            self._packed[key] = self.packer(self.source, int(slots), context)
+        return self._packed[key]
+
+
 class ConstantBundle:
     """Named constants encoded on demand (``bundle.plaintext(name, state, slots, context, ...)``,
-    llama3fhe/backend.py:346-356, operators/linear/weight.py:458-469).  ``cache_mode="plain"``
-    keeps each encoded plaintext for reuse; ``"none"`` encodes every call."""
+    llama3fhe/backend.py:346-356, operators/linear/weight.py:458-469), and named scalars encoded
+    as one residue table (``encoded_scalars``, llama3fhe/operators/nonlinear/polynomial.py:
+    274-291).  ``cache_mode="plain"`` keeps each encoded plaintext for reuse; ``"none"`` encodes
+    every call."""
 
-    def __init__(self, vectors: dict, cache_mode: str = "none"):
-        self.vectors = dict(vectors)
+    def __init__(self, vectors: dict | None = None, cache_mode: str = "none", scalars: dict | None = None):
+        self.vectors = dict(vectors or {})
+        self.scalars = dict(scalars or {})
         self.cache_mode = str(cache_mode)
         self._cache: dict = {}
+
+    def encoded_scalars(self, names, cur_limbs: int, scale_degree: int = 1, context: CKKSContext | None = None,
+                        scaling_factor: float | None = None, cache: bool | None = None,
+                        mode: str = "double") -> EncodedScalar:
+        """The named scalars as one EncodedScalar whose residues are [len(names)][cur_limbs]."""
+
+        names = tuple(str(n) for n in names)
+        key = ("scalars", names, int(cur_limbs), int(scale_degree), scaling_factor, str(mode))
+        hit = self._cache.get(key)
+        if hit is not None:
+            return hit
+        enc = encode_scalar(np.array([float(self.scalars[n]) for n in names]), int(cur_limbs), int(scale_degree),
+                            scaling_factor, context=context, mode=mode)
+        if (self.cache_mode in ("plain", "both")) if cache is None else bool(cache):
+            self._cache[key] = enc
+        return enc
 
     def plaintext(self, name: str, state: CipherState, slots: int, context: CKKSContext,
                   is_ext: bool = False, cache: bool | None = None) -> Plaintext:
@@ -358,6 +393,8 @@ class ConstantBundle:
         if hit is not None:
             return hit
         v = self.vectors[str(name)]
+        if isinstance(v, UnpackedRaw):
+            v = v.values(int(slots), context)
         v = v.values if isinstance(v, PackedRaw) else v
         pt = encode_plaintext(v, state, int(slots), context, is_ext=bool(is_ext))
         if keep:
