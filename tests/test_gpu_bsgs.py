@@ -58,7 +58,7 @@ def test_encode_overflow_is_reported(env):
         ctx.encode_real(torch.from_numpy(vals).cuda(), 2.0**40, 4)
 
 
-@pytest.mark.parametrize("ni,nb,G,limbs", [(16, 16, 5, 3), (3, 5, 6, 2), (1, 1, 1, 1)])
+@pytest.mark.parametrize("ni,nb,G,limbs", [(16, 16, 5, 3), (3, 5, 6, 2), (1, 1, 1, 1), (5, 64, 9, 1)])
 def test_bsgs_mac(env, ni, nb, G, limbs):
     ctx, orc = env
     rng = np.random.default_rng(ni * 100 + nb)
@@ -73,3 +73,13 @@ def test_bsgs_mac(env, ni, nb, G, limbs):
     for i in range(ni):
         want = orc.bsgs_mac(limbs, nb, G, pts, np.ascontiguousarray(babies[:, :, i]))
         assert np.array_equal(res[:, :, i], want), f"input {i}"
+
+
+def test_bsgs_mac_rejects_more_babies_than_a_launch_holds(env):
+    """65 baby steps exceed the kernel's pointer table (64): an argument error, nothing launched."""
+    from holmes_amd import _native as nat
+
+    ctx, _ = env
+    x = ctx.zeros(1, 1, ctx.N)
+    with pytest.raises(nat.NativeError):
+        ctx.bsgs_mac([x] * 65, [x] * 65, ctx.zeros(65, 1, ctx.N), 1, 1)

@@ -332,3 +332,44 @@ def test_rotate_ext_many_equals_single_rotations(env):
         ctx.rotate_raw(c0, c1, ell, gs[:2], keys)
     with pytest.raises(nat.NativeError):
         ctx.rotate_raw(c0, c1, ell, [gs[0], 4, gs[2]], keys)  # an even Galois element
+
+
+def test_batches_spanning_launches(env):
+    """66 items, more than one launch holds (64): a key switch and a rotation with a Galois
+    element per item, every item against the oracle, items 64 and 65 in the second launch."""
+    _, client, ctx, orc = env
+    ell, B = 2, 66
+    gs = [ctx.galois_element(1), ctx.galois_element(-7), ctx.M - 1]
+    pairs = [_key_pair(client, ctx, orc, g) for g in gs]
+    rng = np.random.default_rng(66)
+    d = _rand(ctx, rng, B, ell)
+    ob, oa = ctx.keyswitch(_dev(d), ell, [pairs[b % 3][0] for b in range(B)])
+    gb, ga = _host(ob), _host(oa)
+    for b in range(B):
+        wb, wa = orc.keyswitch(ell, d[b], pairs[b % 3][1])
+        assert np.array_equal(gb[b], wb) and np.array_equal(ga[b], wa), f"key switch item {b}"
+    c0, c1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
+    o0, o1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, [gs[b % 3] for b in range(B)],
+                            [pairs[b % 3][0] for b in range(B)])
+    h0, h1 = _host(o0), _host(o1)
+    for b in range(B):
+        w0, w1 = orc.rotate(ell, gs[b % 3], c0[b], c1[b], pairs[b % 3][1])
+        assert np.array_equal(h0[b], w0) and np.array_equal(h1[b], w1), f"rotation item {b}"
+
+
+def test_empty_batch_is_a_no_op(env):
+    """batch 0 returns success through the C ABI and writes nothing."""
+    from holmes_amd import _native as nat
+
+    _, client, ctx, orc = env
+    gk, _ = _key_pair(client, ctx, orc, ctx.galois_element(1))
+    d = _dev(_rand(ctx, np.random.default_rng(0), 1, 2))
+    out_b = torch.full((1, 2, ctx.N), 7, dtype=torch.int64, device="cuda").view(torch.uint64)
+    out_a = torch.full((1, 2, ctx.N), 9, dtype=torch.int64, device="cuda").view(torch.uint64)
+    L = nat.lib()
+    ws = ctx.workspace(L.hck_keyswitch_workspace_bytes(ctx.handle, 2, 1))
+    rc = L.hck_keyswitch(ctx.handle, 2, 0, d.data_ptr(), 2 * ctx.N, nat.ptr_array([gk.data_ptr()]), None, 0,
+                         out_b.data_ptr(), out_a.data_ptr(), 2 * ctx.N, ws.data_ptr(), ws.numel(), None)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert bool((out_b.view(torch.int64) == 7).all()) and bool((out_a.view(torch.int64) == 9).all())
