@@ -181,7 +181,7 @@ def rebuild_cipher(template, components: Iterable):
 
         return Cipher(components, template.state, slots=int(template.slots), is_ext=bool(getattr(template, "is_ext", False)),
                       batch_size=int(getattr(template, "batch_size", 1)))
-    except Exception:
+    except (AttributeError, TypeError, ValueError):  # a foreign cipher type without these fields
         clone = copy.copy(template)
         clone.cv = components
         return clone
