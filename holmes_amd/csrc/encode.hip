@@ -23,8 +23,7 @@
 namespace hck {
 namespace {
 
-constexpr int kSlots = kN / 2;        // 32768
-constexpr int kLogSlots = kLogN - 1;  // 15
+constexpr int kSlots = kN / 2;  // 32768
 
 struct Cx {
   double re, im;
