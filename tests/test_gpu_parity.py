@@ -373,3 +373,24 @@ def test_empty_batch_is_a_no_op(env):
     assert rc == 0
     torch.cuda.synchronize()
     assert bool((out_b.view(torch.int64) == 7).all()) and bool((out_a.view(torch.int64) == 9).all())
+
+
+def test_every_level_keyswitch_and_rescale(env):
+    """The per-level tables (ModUp digits, ModDown, rescale and ModRaise conversions, P^-1 and
+    q_last^-1 factors) at every level: a key switch at each ell = 1 .. L, a rescale and a ModRaise
+    to each ell = 2 .. L, against the oracle."""
+    _, client, ctx, orc = env
+    gk, ok = _key_pair(client, ctx, orc, ctx.galois_element(5))
+    for ell in range(1, ctx.L + 1):
+        rng = np.random.default_rng(7000 + ell)
+        d = _rand(ctx, rng, 1, ell)
+        ob, oa = ctx.keyswitch(_dev(d), ell, gk)
+        wb, wa = orc.keyswitch(ell, d[0], ok)
+        assert np.array_equal(_host(ob)[0], wb) and np.array_equal(_host(oa)[0], wa), f"key switch at {ell} limbs"
+        if ell >= 2:
+            x = _rand(ctx, rng, 2, ell)
+            got = _host(ctx.rescale_raw(_dev(x), ell))
+            for b in range(2):
+                assert np.array_equal(got[b], orc.rescale(ell, x[b])), f"rescale at {ell} limbs, item {b}"
+            y = _rand(ctx, rng, 1, 1)
+            assert np.array_equal(_host(ctx.modraise(_dev(y), ell))[0], orc.modraise(ell, y[0])), f"ModRaise to {ell}"
