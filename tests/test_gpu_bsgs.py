@@ -51,6 +51,19 @@ def test_encode_real_bit_exact(env, scale):
         assert np.array_equal(got[r], want), f"row {r}"
 
 
+def test_encode_every_limb_count(env):
+    """The fused encoder at every limb count 1 .. L (its per-limb column loop and the row pass's
+    limb list), one row each at that level's prime scale, against the oracle."""
+    ctx, orc = env
+    rng = np.random.default_rng(71)
+    for limbs in range(1, ctx.L + 1):
+        scale = float(ctx.rescale_divisor_at(limbs))
+        vals = rng.normal(scale=0.05, size=(1, ctx.max_slots))
+        got = _host(ctx.encode_real(torch.from_numpy(vals).cuda(), scale, limbs))
+        want, ok = orc.encode_real(vals[0], scale, list(range(limbs)))
+        assert ok and np.array_equal(got[0], want), f"{limbs} limbs"
+
+
 def test_encode_overflow_is_reported(env):
     ctx, _ = env
     vals = np.full((1, ctx.max_slots), 3.0e4)
