@@ -109,6 +109,19 @@ def test_mul_relin_bit_exact(env, ell):
         assert np.array_equal(h0[b], w0) and np.array_equal(h1[b], w1), b
 
 
+def test_mul_relin_every_level(env):
+    """The product with relinearisation at every level ell = 1 .. L (one item each) against the
+    oracle: every level's ModUp digits and ModDown factors under the relinearisation key."""
+    fhe, client, ctx, orc = env
+    rlk = orc.make_ksk(*client.relin_key_inputs())
+    for ell in range(1, ctx.L + 1):
+        rng = np.random.default_rng(300 + ell)
+        a0, a1, b0, b1 = (_rand(ctx, rng, 1, ell) for _ in range(4))
+        o0, o1 = ctx.mul_relin_raw(*(_dev(x) for x in (a0, a1, b0, b1)), ell, ctx.relin_key)
+        w0, w1 = orc.mul_relin(ell, a0[0], a1[0], b0[0], b1[0], rlk)
+        assert np.array_equal(_host(o0)[0], w0) and np.array_equal(_host(o1)[0], w1), f"{ell} limbs"
+
+
 def test_relinearize_of_tensor_equals_mul_relin(env):
     fhe, client, ctx, orc = env
     rng = np.random.default_rng(5)
