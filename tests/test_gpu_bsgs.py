@@ -71,7 +71,7 @@ def test_encode_overflow_is_reported(env):
         ctx.encode_real(torch.from_numpy(vals).cuda(), 2.0**40, 4)
 
 
-@pytest.mark.parametrize("ni,nb,G,limbs", [(16, 16, 5, 3), (3, 5, 6, 2), (1, 1, 1, 1), (5, 64, 9, 1)])
+@pytest.mark.parametrize("ni,nb,G,limbs", [(16, 16, 5, 3), (3, 5, 6, 2), (1, 1, 1, 1), (5, 64, 9, 1), (2, 3, 2, 24)])
 def test_bsgs_mac(env, ni, nb, G, limbs):
     ctx, orc = env
     rng = np.random.default_rng(ni * 100 + nb)
