@@ -82,6 +82,17 @@ def test_moddown_matches_oracle(env):
         assert np.array_equal(got[b], orc.moddown(LIMBS, xs[b]))
 
 
+def test_moddown_every_level(env):
+    """ModDown of an extended-basis poly at every level ell = 1 .. L against the oracle."""
+    fhe, client, ctx, x, ct = env
+    orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+    for ell in range(1, ctx.L + 1):
+        rng = np.random.default_rng(500 + ell)
+        xs = np.stack([rng.integers(0, ctx.primes[i], ctx.N, dtype=np.uint64) for i in ctx.ext_prime_idx(ell)])[None]
+        got = _h(ctx.moddown(torch.from_numpy(xs).cuda(), ell))
+        assert np.array_equal(got[0], orc.moddown(ell, xs[0])), f"{ell} limbs"
+
+
 def test_grouped_pairwise_mac_ext_decrypts(env):
     fhe, client, ctx, x, ct = env
     offs = (0, 1, 2, 3)
