@@ -100,6 +100,17 @@ def test_automorphism(env, g):
             assert np.array_equal(got[b, i], O.automorph_ntt(x[b, i], 16, g))
 
 
+def test_automorphism_power_of_two_rotations(env):
+    """sigma_g for every power-of-two rotation 2^0 .. 2^14 in both directions (the BSGS and
+    bootstrap offsets) and the conjugation, against the oracle's permutation."""
+    _, _, ctx, orc = env
+    x = _rand(ctx, np.random.default_rng(17), 1, 1)
+    gs = [ctx.galois_element(s * (1 << k)) for k in range(15) for s in (1, -1)] + [ctx.M - 1]
+    for g in gs:
+        got = _host(ctx.automorphism(_dev(x), g, 1))
+        assert np.array_equal(got[0, 0], O.automorph_ntt(x[0, 0], 16, g)), f"g = {g}"
+
+
 def test_elementwise_ops(env):
     from holmes_amd import _native as nat
 
