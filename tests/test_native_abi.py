@@ -29,6 +29,19 @@ def test_library_exports_every_declared_symbol():
     assert sorted(nat.SIGNATURES) == names
 
 
+def test_bindings_match_the_header_arity():
+    """Every ctypes signature has as many arguments as the header's prototype: a binding that
+    drifts from the header would pass shifted pointers to the kernels."""
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    text = re.sub(r"//[^\n]*", "", text)
+    decls = re.findall(r"\b(hck_[a-z0-9_]+)\s*\(([^;{)]*)\)\s*;", text)
+    assert len(decls) >= len(nat.SIGNATURES)
+    for name, params in decls:
+        p = params.strip()
+        n = 0 if p in ("", "void") else p.count(",") + 1
+        assert len(nat.SIGNATURES[name][1]) == n, f"{name}: header {n}, binding {len(nat.SIGNATURES[name][1])}"
+
+
 def test_error_strings():
     lib = nat.lib()
     assert lib.hck_error_string(0) == b"ok"
