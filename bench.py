@@ -974,30 +974,11 @@ def run_stream(args) -> int:
     return 0
 
 
-def randomized_hadamard_right(w: np.ndarray, seed: int) -> np.ndarray:
-    """w @ (diag(s) H / sqrt(n)) with s a seeded +-1 vector and H the Sylvester Hadamard matrix,
-    by an in-place fast Walsh-Hadamard transform over the last axis (the QuaRot-style rotation
-    of tools/convert/hadamard/numpy.py:1-40, restated)."""
-
-    n = w.shape[-1]
-    if n & (n - 1):
-        raise ValueError("Hadamard size must be a power of two")
-    s = np.random.default_rng(seed).choice(np.array([-1.0, 1.0]), size=n)
-    x = (np.asarray(w, dtype=np.float64) * s).copy()
-    h = 1
-    while h < n:
-        x = x.reshape(*x.shape[:-1], n // (2 * h), 2, h)
-        a, b = x[..., 0, :].copy(), x[..., 1, :].copy()
-        x[..., 0, :], x[..., 1, :] = a + b, a - b
-        x = x.reshape(*x.shape[:-3], n)
-        h *= 2
-    return x / np.sqrt(n)
-
-
 def run_c3(args) -> int:
     import torch
 
     from holmes_amd import fhe, linear
+    from holmes_amd.hadamard import randomized_hadamard_right
     from holmes_amd.layouts import FeatureMajorPrefillLayout
 
     seed = int(args.seed)

@@ -50,6 +50,8 @@ SIGNATURES = {
     "hck_poly_from_signed": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _i, _ip, _vp]),
     "hck_bsgs_mac": (_i, [_vp, _i, _ip, _i, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), _i64, _vp, _i64, _vp,
                           _vp]),
+    "holmes_mac_multi": (_i, [_vp, _vp, _vp, ctypes.c_longlong, _i, _i, _vp, ctypes.c_longlong, _i, _i, _i, _vp, _vp,
+                              _vp, _vp]),
     "hck_rotate_ext": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp, _i64,
                             _vp, _sz, _vp]),
     "hck_rotate_many": (_i, [_vp, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp,

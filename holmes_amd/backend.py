@@ -1,14 +1,23 @@
 """Execution-session boundary with the surface of llama3fhe/backend.py, backed by holmes_amd.
 
-Holmes' operators talk to their CKKS engine through ``EasyFHEContext`` (fields ``tensor, fhe,
-client, context, max_slots``; methods ``encrypt, plaintext, constant_bundle, decrypt,
-level_for_cipher``; llama3fhe/backend.py:249-397) and the module helpers of
-llama3fhe/backend.py:399-611.  This module keeps those names, arguments and error behaviour so
-operator code written against them runs on one MI355X with world size 1; every arithmetic call
-lands in libholmes_ckks (HIP, gfx950).
+Holmes' operators reach their CKKS engine through one session object (``EasyFHEContext``: fields
+``tensor, fhe, client, context, max_slots``; ``encrypt``, ``plaintext``, ``constant_bundle``,
+``decrypt``, ``level_for_cipher``; llama3fhe/backend.py:249-397) and a handful of module helpers
+(llama3fhe/backend.py:399-611).  Those names, arguments and the environment knobs the reference reads
+are the interface kept here; every arithmetic call below them lands in libholmes_ckks (HIP, gfx950).
 
-``tensor`` is PyTorch (ROCm): the easyfhe tensor shim's ``from_numpy``, ``empty``, ``zeros``,
-``cuda.Stream`` / ``Event`` / ``synchronize`` map onto torch's.
+Constant caching is organised around a byte budget (``_Budget``) that the session's cache and the
+bundles it hands out share:
+
+* a bundle is admitted when its source arrays fit the per-source limit and the budget; admitted
+  bundles are never evicted (layers scan their masks in the same order, so keeping the first ones
+  is what makes the next layer hit);
+* an admitted bundle asks the budget before it keeps an encoded plaintext; a plaintext that does
+  not fit is returned to its caller and not kept, the bundle itself stays cached;
+* a bundle that is not admitted never keeps anything (``cache_mode="none"``).
+
+``tensor`` is PyTorch (ROCm): the easyfhe tensor shim's ``from_numpy``, ``empty``, ``zeros`` and
+``cuda.Stream`` / ``Event`` / ``synchronize`` are torch's.
 """
 
 from __future__ import annotations
@@ -17,7 +26,6 @@ import hashlib
 import os
 import re
 import time
-from collections import OrderedDict
 from dataclasses import dataclass, field
 from math import log2
 
@@ -27,92 +35,142 @@ import torch
 from . import fhe
 from .config import SimulatorConfig
 
-_LAYER_CACHE_NAME = re.compile(r"model\.layers\.\d+\.")
-_RANK_ITER_CACHE_NAME = re.compile(r"\.r\d+\.i\d+\.")
+# Constant names that differ only by decoder-layer index, or by the rank/iteration tag a benchmark
+# prefixes, denote the same public mask and share one cache entry (llama3fhe/backend.py:23-54).
+_NAME_RULES = (
+    (re.compile(r"model\.layers\.\d+\."), "model.layers.*."),
+    (re.compile(r"\.r\d+\.i\d+\."), ".r*.i*."),
+)
+
+# Environment knobs of the reference session (same names, same meaning).
+ENV_CACHE_GB = "LLAMA_FHE_PLAIN_CACHE_GB"
+ENV_CACHE_SOURCE_MB = "LLAMA_FHE_PLAIN_CACHE_MAX_SOURCE_MB"
+ENV_STAGE_SYNC = "T2_STAGE_SYNC"
+ENV_ALLOCATOR_TRIM = "LLAMA_FHE_ALLOCATOR_TRIM"
+
+_STAT_FIELDS = ("entries", "bytes", "limit_bytes", "max_source_bytes", "hits", "misses", "skips")
 
 
 def _normalized_constant_name(value: object) -> object:
-    """Names that differ only by layer index or rank/iteration prefix share a cache entry
-    (llama3fhe/backend.py:47-54)."""
+    """Layer-independent form of a constant name (strings, or nested tuples / lists of them)."""
 
     if isinstance(value, str):
-        value = _LAYER_CACHE_NAME.sub("model.layers.*.", value)
-        return _RANK_ITER_CACHE_NAME.sub(".r*.i*.", value)
-    if isinstance(value, (tuple, list)):
-        return tuple(_normalized_constant_name(item) for item in value)
+        for pattern, repl in _NAME_RULES:
+            value = pattern.sub(repl, value)
+        return value
+    if isinstance(value, (list, tuple)):
+        return tuple(map(_normalized_constant_name, value))
     return value
 
 
-def _array_digest(array: np.ndarray) -> str:
-    return hashlib.blake2b(memoryview(np.ascontiguousarray(array)).cast("B"), digest_size=16).hexdigest()
+def _fingerprint(arrays: dict[str, np.ndarray]) -> str:
+    """One digest over every named array's name, shape, dtype and bytes."""
+
+    h = hashlib.sha256()
+    for name in sorted(arrays):
+        a = arrays[name]
+        h.update(f"{name}|{a.shape}|{a.dtype.str}|".encode())
+        h.update(memoryview(a).cast("B"))
+    return h.hexdigest()
+
+
+class _Budget:
+    """Bytes a session may keep in cached constants."""
+
+    def __init__(self, limit: int) -> None:
+        self.limit = max(0, int(limit))
+        self.used = 0
+
+    def take(self, nbytes: int) -> bool:
+        nbytes = int(nbytes)
+        if self.used + nbytes > self.limit:
+            return False
+        self.used += nbytes
+        return True
+
+    def reset(self) -> None:
+        self.used = 0
 
 
 class SessionPlaintextCache:
-    """First-fit byte-capped cache of immutable constant bundles (llama3fhe/backend.py:129-247):
-    an admitted entry is never evicted during a scan; an entry that would cross the budget stays
-    transient for its caller."""
+    """Never-evicting constant cache under one byte budget (policy in the module docstring).
+
+    ``get(key, factory, source_bytes=)`` returns the cached bundle for ``key`` or builds one with
+    ``factory(admitted)``; ``transient(factory, source_bytes=)`` builds an uncached one.  Once
+    ``clear()`` has run the cache refuses further use."""
 
     def __init__(self, *, limit_bytes: int, max_source_bytes: int) -> None:
-        self.limit_bytes = max(0, int(limit_bytes))
-        self.max_source_bytes = max(0, int(max_source_bytes))
-        self._entries: OrderedDict[object, fhe.ConstantBundle] = OrderedDict()
-        self._bytes = 0
-        self.hits = 0
-        self.misses = 0
-        self.skips = 0
-        self.closed = False
+        self._budget = _Budget(limit_bytes)
+        self._max_source = max(0, int(max_source_bytes))
+        self._bundles: dict[object, object] = {}
+        self._stats = {"hits": 0, "misses": 0, "skips": 0}
+        self._open = True
+
+    # -- counters and limits (read-only views)
+    limit_bytes = property(lambda self: self._budget.limit)
+    max_source_bytes = property(lambda self: self._max_source)
+    hits = property(lambda self: self._stats["hits"])
+    misses = property(lambda self: self._stats["misses"])
+    skips = property(lambda self: self._stats["skips"])
+    closed = property(lambda self: not self._open)
+
+    @property
+    def budget(self) -> _Budget:
+        return self._budget
 
     def accepts_source(self, source_bytes: int) -> bool:
-        return self.limit_bytes > 0 and int(source_bytes) <= self.max_source_bytes
+        """True when a bundle of ``source_bytes`` source data may be cached at all."""
+
+        return 0 < self._budget.limit and 0 <= int(source_bytes) <= self._max_source
+
+    def _require_open(self) -> None:
+        if not self._open:
+            raise RuntimeError("the session plaintext cache was cleared and cannot be used again")
 
     def get(self, key, factory, *, source_bytes: int):
-        if self.closed:
-            raise RuntimeError("session plaintext cache is closed")
-        hit = self._entries.get(key)
-        if hit is not None:
-            self.hits += 1
-            return hit
-        self.misses += 1
-        admit = self.accepts_source(source_bytes) and self._bytes + int(source_bytes) <= self.limit_bytes
-        bundle = factory(admit)
-        if admit:
-            self._entries[key] = bundle
-            self._bytes += int(source_bytes)
+        self._require_open()
+        if key in self._bundles:
+            self._stats["hits"] += 1
+            return self._bundles[key]
+        self._stats["misses"] += 1
+        admitted = self.accepts_source(source_bytes) and self._budget.take(source_bytes)
+        bundle = factory(admitted)
+        if admitted:
+            self._bundles[key] = bundle
         else:
-            self.skips += 1
+            self._stats["skips"] += 1
         return bundle
 
     def transient(self, factory, *, source_bytes: int):
-        if self.closed:
-            raise RuntimeError("session plaintext cache is closed")
-        self.misses += 1
-        self.skips += 1
+        self._require_open()
+        self._stats["misses"] += 1
+        self._stats["skips"] += 1
         return factory(False)
 
     def info(self) -> dict[str, int]:
-        return {
-            "entries": len(self._entries),
-            "bytes": int(self._bytes),
-            "limit_bytes": int(self.limit_bytes),
-            "max_source_bytes": int(self.max_source_bytes),
-            "hits": int(self.hits),
-            "misses": int(self.misses),
-            "skips": int(self.skips),
-        }
+        values = (len(self._bundles), self._budget.used, self._budget.limit, self._max_source, self.hits,
+                  self.misses, self.skips)
+        return {k: int(v) for k, v in zip(_STAT_FIELDS, values)}
 
     def clear(self) -> None:
-        for bundle in self._entries.values():
-            clear_cache = getattr(bundle, "clear_cache", None)
-            if callable(clear_cache):
-                clear_cache()
-        self._entries.clear()
-        self._bytes = 0
-        self.closed = True
+        self._open = False
+        bundles, self._bundles = list(self._bundles.values()), {}
+        self._budget.reset()
+        for bundle in bundles:
+            drop = getattr(bundle, "clear_cache", None)
+            if callable(drop):
+                drop()
+
+
+def _cache_from_env() -> SessionPlaintextCache:
+    gb = float(os.environ.get(ENV_CACHE_GB, "0") or 0)
+    mb = float(os.environ.get(ENV_CACHE_SOURCE_MB, "1") or 0)
+    return SessionPlaintextCache(limit_bytes=int(gb * 2**30), max_source_bytes=int(mb * 2**20))
 
 
 @dataclass
 class EasyFHEContext:
-    """Data-only session joining the client and the device context."""
+    """Session joining the client (keys, encrypt / decrypt) and the device context."""
 
     tensor: object
     fhe: object
@@ -120,67 +178,63 @@ class EasyFHEContext:
     context: object
     max_slots: int
     keygen_wall_time_s: float = 0.0
-    plaintext_cache: SessionPlaintextCache = field(init=False, repr=False)
-
-    def __post_init__(self) -> None:
-        limit_gb = float(os.environ.get("LLAMA_FHE_PLAIN_CACHE_GB", "0"))
-        max_source_mb = float(os.environ.get("LLAMA_FHE_PLAIN_CACHE_MAX_SOURCE_MB", "1"))
-        self.plaintext_cache = SessionPlaintextCache(
-            limit_bytes=int(limit_gb * 1024**3), max_source_bytes=int(max_source_mb * 1024**2)
-        )
-
-    def configure_plaintext_cache(self, *, limit_bytes: int, max_source_bytes: int) -> None:
-        info = self.plaintext_cache.info()
-        if info["entries"] or info["misses"]:
-            raise RuntimeError("plaintext cache policy must be fixed before first use")
-        self.plaintext_cache = SessionPlaintextCache(limit_bytes=limit_bytes, max_source_bytes=max_source_bytes)
+    plaintext_cache: SessionPlaintextCache = field(default_factory=_cache_from_env, init=False, repr=False)
 
     @property
     def device(self) -> str:
         return str(self.context.device)
 
+    def _limbs_at(self, level: int) -> int:
+        limbs = int(self.context.L) - int(level)
+        if limbs < 1:
+            raise ValueError(f"no limbs remain at level {level} of a {self.context.L}-limb chain")
+        return limbs
+
     def level_for_cipher(self, cipher) -> int:
         return int(self.context.L) - int(cipher.state.cur_limbs)
 
+    def configure_plaintext_cache(self, *, limit_bytes: int, max_source_bytes: int) -> None:
+        """Replace the cache policy; only allowed while the cache is still untouched."""
+
+        seen = self.plaintext_cache.info()
+        if seen["entries"] or seen["misses"]:
+            raise RuntimeError("configure the plaintext cache before the first constant is requested")
+        self.plaintext_cache = SessionPlaintextCache(limit_bytes=limit_bytes, max_source_bytes=max_source_bytes)
+
     def encrypt(self, values: np.ndarray, *, level: int, slots: int | None = None):
-        cur_limbs = int(self.context.L) - int(level)
-        if cur_limbs < 1:
-            raise ValueError(f"level {level} leaves no limbs (L = {self.context.L})")
-        return self.client.encrypt(
-            np.asarray(values).reshape(-1),
-            device=self.device,
-            slots=self.max_slots if slots is None else int(slots),
-            cur_limbs=cur_limbs,
-            scaling_factor=self.context.scale_at(cur_limbs),
-        )
+        limbs = self._limbs_at(level)
+        return self.client.encrypt(np.asarray(values).reshape(-1), device=self.device,
+                                   slots=int(slots or self.max_slots), cur_limbs=limbs,
+                                   scaling_factor=self.context.scale_at(limbs))
 
     def plaintext(self, values: np.ndarray, *, name: str, level: int, slots: int | None = None,
                   dtype: np.dtype = np.float64, is_ext: bool = False):
-        array = np.asarray(values, dtype=dtype).reshape(-1)
-        bundle = self.constant_bundle({"value": array}, cache_key=("vector", _normalized_constant_name(str(name))))
-        cur_limbs = int(self.context.L) - int(level)
-        return bundle.plaintext(
-            "value",
-            state=fhe.CipherState(cur_limbs=cur_limbs, scale_degree=1,
-                                  scaling_factor=self.context.scale_at(cur_limbs)),
-            slots=self.max_slots if slots is None else int(slots),
-            context=self.context,
-            is_ext=bool(is_ext),
-        )
+        limbs = self._limbs_at(level)
+        bundle = self.constant_bundle({"value": np.asarray(values, dtype=dtype).reshape(-1)},
+                                      cache_key=("vector", str(name)))
+        state = fhe.CipherState(cur_limbs=limbs, scale_degree=1, scaling_factor=self.context.scale_at(limbs))
+        return bundle.plaintext("value", state=state, slots=int(slots or self.max_slots), context=self.context,
+                                is_ext=bool(is_ext))
 
     def constant_bundle(self, vectors: dict[str, np.ndarray], *, cache_key: object):
+        """A ``fhe.ConstantBundle`` over ``vectors``: cached under (normalised ``cache_key``, content
+        fingerprint) when the policy admits it, else built for this caller only."""
+
         arrays = {str(k): np.ascontiguousarray(v) for k, v in vectors.items()}
-        source_bytes = sum(int(v.nbytes) for v in arrays.values())
+        nbytes = sum(a.nbytes for a in arrays.values())
+        cache = self.plaintext_cache
+        budget = cache.budget
 
-        def factory(cache: bool):
-            wrapped = {k: fhe.PackedRaw(torch.from_numpy(v)) for k, v in arrays.items()}
-            return fhe.ConstantBundle(vectors=wrapped, cache_mode="plain" if cache else "none")
+        def build(admitted: bool):
+            raws = {k: fhe.PackedRaw(torch.from_numpy(a)) for k, a in arrays.items()}
+            if not admitted:
+                return fhe.ConstantBundle(vectors=raws, cache_mode="none")
+            return fhe.ConstantBundle(vectors=raws, cache_mode="plain", keep=budget.take)
 
-        if not self.plaintext_cache.accepts_source(source_bytes):
-            return self.plaintext_cache.transient(factory, source_bytes=source_bytes)
-        content = tuple((k, tuple(v.shape), v.dtype.str, _array_digest(v)) for k, v in sorted(arrays.items()))
-        key = (_normalized_constant_name(cache_key), content)
-        return self.plaintext_cache.get(key, factory, source_bytes=source_bytes)
+        if not cache.accepts_source(nbytes):
+            return cache.transient(build, source_bytes=nbytes)
+        key = (_normalized_constant_name(cache_key), _fingerprint(arrays))
+        return cache.get(key, build, source_bytes=nbytes)
 
     def plaintext_cache_info(self) -> dict[str, int]:
         return self.plaintext_cache.info()
@@ -189,28 +243,28 @@ class EasyFHEContext:
         self.plaintext_cache.clear()
 
     def decrypt(self, cipher) -> np.ndarray:
-        value = self.client.decrypt(cipher)
-        return np.asarray(value).reshape(-1)
+        return np.asarray(self.client.decrypt(cipher)).reshape(-1)
 
 
+# ---------------------------------------------------------------------------- module helpers
 def plaintext_cache_snapshot(context) -> dict[str, int]:
-    inspect = getattr(context, "plaintext_cache_info", None)
-    if callable(inspect):
-        return {k: int(v) for k, v in inspect().items()}
-    return {k: 0 for k in ("entries", "bytes", "limit_bytes", "max_source_bytes", "hits", "misses", "skips")}
+    """The cache counters of ``context`` (zeros for an object without a cache)."""
+
+    info = getattr(context, "plaintext_cache_info", None)
+    if not callable(info):
+        return dict.fromkeys(_STAT_FIELDS, 0)
+    return {k: int(v) for k, v in info().items()}
 
 
 def release_if_supported(value) -> None:
-    """Release explicit handles (ciphertexts, plaintexts, bundles) when the object has them."""
+    """Free what ``value`` holds: its own ``release()``, else its constants' encoded cache."""
 
-    release = getattr(value, "release", None)
-    if callable(release):
-        release()
-        return
-    constants = getattr(value, "constants", None)
-    clear_cache = getattr(constants, "clear_cache", None)
-    if callable(clear_cache):
-        clear_cache()
+    for getter in (lambda v: getattr(v, "release", None),
+                   lambda v: getattr(getattr(v, "constants", None), "clear_cache", None)):
+        action = getter(value)
+        if callable(action):
+            action()
+            return
 
 
 def release_all(values) -> None:
@@ -219,24 +273,25 @@ def release_all(values) -> None:
 
 
 def synchronize_device(device: str) -> None:
-    torch.cuda.synchronize(torch.device(str(device)) if str(device).startswith("cuda") else None)
+    dev = str(device)
+    torch.cuda.synchronize(torch.device(dev) if dev.startswith("cuda") else None)
 
 
-_STAGE_SYNC: bool | None = None
+_stage_sync: list[bool | None] = [None]
 
 
 def stage_sync_enabled() -> bool:
-    """True unless T2_STAGE_SYNC=0 (llama3fhe/backend.py:450-487)."""
+    """Stage boundaries synchronise the device unless T2_STAGE_SYNC=0 (llama3fhe/backend.py:450-487)."""
 
-    global _STAGE_SYNC
-    if _STAGE_SYNC is None:
-        _STAGE_SYNC = os.environ.get("T2_STAGE_SYNC", "1") != "0"
-    return bool(_STAGE_SYNC)
+    if _stage_sync[0] is None:
+        _stage_sync[0] = os.environ.get(ENV_STAGE_SYNC, "1") != "0"
+    return bool(_stage_sync[0])
 
 
 def set_stage_sync(enabled: bool | None) -> None:
-    global _STAGE_SYNC
-    _STAGE_SYNC = None if enabled is None else bool(enabled)
+    """Force stage synchronisation on or off (None: read the environment again)."""
+
+    _stage_sync[0] = None if enabled is None else bool(enabled)
 
 
 def profile_sync_device(device: str) -> None:
@@ -245,73 +300,61 @@ def profile_sync_device(device: str) -> None:
 
 
 def trim_device_allocator_cache(device: str) -> None:
-    if os.environ.get("LLAMA_FHE_ALLOCATOR_TRIM", "") != "1" or not str(device).startswith("cuda"):
-        return
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
+    """Return torch's cached device blocks to the driver when LLAMA_FHE_ALLOCATOR_TRIM=1."""
+
+    if os.environ.get(ENV_ALLOCATOR_TRIM, "") == "1" and str(device).startswith("cuda"):
+        torch.cuda.synchronize()
+        torch.cuda.empty_cache()
 
 
 def cuda_memory_snapshot(device: str) -> dict[str, int | bool]:
-    if not str(device).startswith("cuda") or not torch.cuda.is_available():
+    if not (str(device).startswith("cuda") and torch.cuda.is_available()):
         return {"available": False}
     dev = torch.device(str(device))
     free_b, total_b = torch.cuda.mem_get_info(dev)
-    return {
-        "available": True,
-        "allocator_allocated_bytes": int(torch.cuda.memory_allocated(dev)),
-        "allocator_reserved_bytes": int(torch.cuda.memory_reserved(dev)),
-        "allocator_peak_allocated_bytes": int(torch.cuda.max_memory_allocated(dev)),
-        "allocator_peak_reserved_bytes": int(torch.cuda.max_memory_reserved(dev)),
-        "device_used_bytes": int(total_b - free_b),
-        "device_free_bytes": int(free_b),
-        "device_total_bytes": int(total_b),
-    }
+    snap: dict[str, int | bool] = {"available": True}
+    for name, fn in (("allocated", torch.cuda.memory_allocated), ("reserved", torch.cuda.memory_reserved),
+                     ("peak_allocated", torch.cuda.max_memory_allocated),
+                     ("peak_reserved", torch.cuda.max_memory_reserved)):
+        snap[f"allocator_{name}_bytes"] = int(fn(dev))
+    snap.update(device_used_bytes=int(total_b - free_b), device_free_bytes=int(free_b),
+                device_total_bytes=int(total_b))
+    return snap
+
+
+def _power_of_two(value: int, name: str) -> int:
+    value = int(value)
+    if value < 1 or value & (value - 1):
+        raise ValueError(f"{name} must be a power of two (got {value})")
+    return value
 
 
 def default_rotations(input_dim: int, block_out: int) -> set[int]:
-    """Power-of-two rotation set of llama3fhe/backend.py:540-553."""
+    """Rotation set of an isolated operator test (llama3fhe/backend.py:540-553): the strides
+    block_out 2^i below input_dim, and the powers of two below block_out."""
 
-    input_dim, block_out = int(input_dim), int(block_out)
-    if input_dim <= 0 or input_dim & (input_dim - 1):
-        raise ValueError("input_dim must be a positive power of two.")
-    if block_out <= 0 or block_out & (block_out - 1):
-        raise ValueError("block_out must be a positive power of two.")
-    rot = {block_out * (1 << i) for i in range(int(log2(input_dim)))}
-    rot.update(1 << i for i in range(int(log2(block_out))))
-    return rot
+    d = _power_of_two(input_dim, "input_dim")
+    b = _power_of_two(block_out, "block_out")
+    return {b << i for i in range(d.bit_length() - 1)} | {1 << i for i in range(int(log2(b)))}
 
 
 def create_sim_context(sim_cfg: SimulatorConfig, *, input_dim: int, block_out: int,
                        rotations=None, include_default_rotations: bool = True) -> EasyFHEContext:
-    """Isolated-test context (llama3fhe/backend.py:556-596): keygen for the requested rotations."""
+    """Isolated-test session (llama3fhe/backend.py:556-596): context and keys for the requested
+    rotations (plus the default set unless disabled)."""
 
-    requested = default_rotations(input_dim, block_out) if include_default_rotations else set()
-    requested.update(int(v) for v in rotations or () if int(v))
-    start = time.perf_counter()
-    client, context = fhe.generate_client_context(
-        fhe.CKKSContextSpec(
-            depth=int(sim_cfg.maxLevelsRemaining),
-            log_n=int(sim_cfg.logN),
-            dnum=int(sim_cfg.dnum),
-            dcrt_bits=int(sim_cfg.dcrtBits),
-            first_mod=int(sim_cfg.firstMod),
-            secret_key_dist=str(sim_cfg.secretKeyDist),
-            scale_mode="fixed",
-            rescale_policy=sim_cfg.rescale_policy(),
-            rotations=tuple(sorted(requested)),
-            auto_load_keys=True,
-            scale_bits=int(sim_cfg.scaleBits),
-        ),
-        device=str(sim_cfg.device),
-    )
-    return EasyFHEContext(
-        tensor=torch,
-        fhe=fhe,
-        client=client,
-        context=context,
-        max_slots=int(context.max_slots),
-        keygen_wall_time_s=float(time.perf_counter() - start),
-    )
+    wanted = set(default_rotations(input_dim, block_out)) if include_default_rotations else set()
+    wanted |= {int(r) for r in (rotations or ()) if int(r)}
+    spec = fhe.CKKSContextSpec(
+        depth=int(sim_cfg.maxLevelsRemaining), log_n=int(sim_cfg.logN), dnum=int(sim_cfg.dnum),
+        dcrt_bits=int(sim_cfg.dcrtBits), first_mod=int(sim_cfg.firstMod),
+        secret_key_dist=str(sim_cfg.secretKeyDist), scale_mode="fixed", rescale_policy=sim_cfg.rescale_policy(),
+        rotations=tuple(sorted(wanted)), auto_load_keys=True, scale_bits=int(sim_cfg.scaleBits))
+    t0 = time.perf_counter()
+    client, context = fhe.generate_client_context(spec, device=str(sim_cfg.device))
+    elapsed = time.perf_counter() - t0
+    return EasyFHEContext(tensor=torch, fhe=fhe, client=client, context=context,
+                          max_slots=int(context.max_slots), keygen_wall_time_s=float(elapsed))
 
 
 __all__ = [

@@ -39,17 +39,24 @@ from .context import Cipher, CKKSContext, u64_clone
 from .polynomial import PSEvaluator as _PSEval
 from .polynomial import _baby_size, canonical_scales, chebyshev_divide  # noqa: F401
 
-__all__ = ["BootstrapSpec", "BootstrapProgram", "Requirements", "Stage", "requirements", "generate", "bootstrap",
+__all__ = ["STRATEGIES", "BootstrapSpec", "BootstrapProgram", "Requirements", "Stage", "requirements", "generate", "bootstrap",
            "special_fft_layers", "merge_layers", "chebyshev_divide", "canonical_scales", "evalmod_levels",
            "evalmod_coefficients", "make_stage", "plan_stages", "plan_program", "stage_rows", "apply_stage",
            "apply_stages", "bootstrap_with_correction"]
 
 
 # ---------------------------------------------------------------------------- spec / requirements
+# Evaluation strategies the reference names (llama3fhe/operators/nonlinear/bootstrap.py:55-58): on
+# EasyFHE they trade live extended-basis batches for speed on 24-GiB cards.  Both run the same
+# stage schedule here (babies as one batched key switch, giants as a second), which fits HBM.
+STRATEGIES = frozenset({"double_hoist", "normal_bsgs"})
+
+
 @dataclass(frozen=True)
 class BootstrapSpec:
     """Keywords of easyfhe.bs.openfhe.BootstrapSpec as Holmes builds it (bootstrap.py:119-160);
-    the EvalMod fields are this backend's.  ``output_levels`` 0 means all that remain."""
+    the EvalMod fields are this backend's.  ``output_levels`` 0 means all that remain; ``dim1`` /
+    ``baby_step`` fix the baby rotations per CoeffToSlot / SlotToCoeff stage (0: automatic)."""
 
     log_slots: int = 15
     level_budget: tuple = (3, 3)
@@ -68,8 +75,26 @@ class BootstrapSpec:
             raise ValueError("this bootstrap handles full-slot ciphertexts (log_slots = log_n - 1)")
         if str(self.mode) != "modraise_first":
             raise ValueError("only mode='modraise_first' is supported")
+        if str(self.strategy) not in STRATEGIES:
+            raise ValueError(f"strategy must be one of {sorted(STRATEGIES)}, got {self.strategy!r}")
         if len(tuple(self.level_budget)) != 2 or min(int(b) for b in self.level_budget) < 1:
             raise ValueError("level_budget needs two positive entries (CoeffToSlot, SlotToCoeff)")
+        for name in ("dim1", "baby_step"):
+            pair = getattr(self, name)
+            if pair is None:
+                continue
+            if len(tuple(pair)) != 2 or any(int(v) < 0 or (int(v) and int(v) & (int(v) - 1)) or int(v) == 1
+                                            for v in pair):
+                raise ValueError(f"{name} needs two entries, each 0 (automatic) or a power of two >= 2")
+
+    def babies(self, kind: int) -> int:
+        """Baby rotations per stage of CoeffToSlot (kind 0) or SlotToCoeff (kind 1): ``dim1`` (the
+        inner BSGS dimension), else ``baby_step``, else 0 (sized from the stage's diagonals)."""
+
+        for pair in (self.dim1, self.baby_step):
+            if pair is not None and int(tuple(pair)[kind]):
+                return int(tuple(pair)[kind])
+        return 0
 
 
 @dataclass(frozen=True)
@@ -98,18 +123,20 @@ def _stage_layers(log_slots: int, budget: int, inverse: bool) -> list[list[int]]
     return out
 
 
-def _bsgs_shape(layers: list[int], n: int) -> tuple[int, int, int]:
-    """(h_min, n1, kmax): the stage's diagonals sit at k h_min, |k| <= kmax; babies 0..n1-1."""
+def _bsgs_shape(layers: list[int], n: int, n1: int = 0) -> tuple[int, int, int]:
+    """(h_min, n1, kmax): the stage's diagonals sit at k h_min, |k| <= kmax; babies 0..n1-1
+    (``n1`` 0: about the square root of the 2 kmax + 1 diagonals)."""
 
     hs = [n >> t for t in layers]
     h_min = min(hs)
     kmax = sum(h // h_min for h in hs)
-    n1 = 1 << max(1, math.ceil(math.log2(2 * kmax + 1) / 2))
-    return h_min, n1, kmax
+    if not n1:
+        n1 = 1 << max(1, math.ceil(math.log2(2 * kmax + 1) / 2))
+    return h_min, int(n1), kmax
 
 
-def _stage_rotations(layers: list[int], n: int) -> set[int]:
-    h_min, n1, kmax = _bsgs_shape(layers, n)
+def _stage_rotations(layers: list[int], n: int, n1: int = 0) -> set[int]:
+    h_min, n1, kmax = _bsgs_shape(layers, n, n1)
     rots = {(k1 * h_min) % n for k1 in range(1, n1)}
     for k2 in range(-((kmax + n1 - 1) // n1) - 1, kmax // n1 + 2):
         if k2:
@@ -128,8 +155,10 @@ def requirements(specs, log_n: int) -> Requirements:
     for spec in specs:
         spec.validate(log_n)
         b1, b2 = (int(b) for b in spec.level_budget)
-        for layers in _stage_layers(spec.log_slots, b1, True) + _stage_layers(spec.log_slots, b2, False):
-            rots |= _stage_rotations(layers, n)
+        for layers in _stage_layers(spec.log_slots, b1, True):
+            rots |= _stage_rotations(layers, n, spec.babies(0))
+        for layers in _stage_layers(spec.log_slots, b2, False):
+            rots |= _stage_rotations(layers, n, spec.babies(1))
         depth = max(depth, b1 + b2 + evalmod_levels(spec, 1024, [2] * 1025))
     rots.add(4 * n - 1)  # conjugation
     return Requirements(rotations=tuple(sorted(rots)), depth=depth)
@@ -222,10 +251,10 @@ class Stage:
     cache: dict = field(default_factory=dict)  # limbs -> encoded rows [giants * n1][limbs][N]
 
 
-def make_stage(layers: list[int], all_layers: list[dict], n: int, factor: float = 1.0) -> Stage:
+def make_stage(layers: list[int], all_layers: list[dict], n: int, factor: float = 1.0, n1: int = 0) -> Stage:
     """Merge ``layers`` (applied in list order) into one stage, every diagonal times ``factor``."""
 
-    h_min, n1, kmax = _bsgs_shape(layers, n)
+    h_min, n1, kmax = _bsgs_shape(layers, n, n1)
     merged = merge_layers([all_layers[t - 1] for t in layers], n)
     diags: dict[int, np.ndarray] = {}
     for d, v in merged.items():
@@ -251,14 +280,15 @@ def stage_rows(st: Stage, n: int) -> np.ndarray:
     return rows
 
 
-def plan_stages(log_slots: int, budget: int, inverse: bool, factor: float) -> list[Stage]:
+def plan_stages(log_slots: int, budget: int, inverse: bool, factor: float, n1: int = 0) -> list[Stage]:
     """CoeffToSlot (``inverse``: U0^-1 up to the bit reversal) or SlotToCoeff (U0 of a bit-reversed
-    input) as ``budget`` merged stages, ``factor`` folded into the first."""
+    input) as ``budget`` merged stages, ``factor`` folded into the first; ``n1`` baby rotations per
+    stage (0: automatic)."""
 
     n = 1 << int(log_slots)
     layers = special_fft_layers(log_slots, inverse=inverse)
     groups = _stage_layers(log_slots, budget, inverse)
-    return [make_stage(g, layers, n, factor if i == 0 else 1.0) for i, g in enumerate(groups)]
+    return [make_stage(g, layers, n, factor if i == 0 else 1.0, n1) for i, g in enumerate(groups)]
 
 
 class _Constants:
@@ -342,8 +372,8 @@ def plan_program(spec: BootstrapSpec, q_primes, scale: float, raise_to: int) -> 
     prog = BootstrapProgram(spec=spec, raise_to_limbs=raise_to, evalmod_limbs=em_in, output_limbs=out, q0=q0,
                             nominal_scale=S, evalmod_out_scale=S_out, mod_scale=Kp,
                             cheb=evalmod_coefficients(spec),
-                            cts=plan_stages(spec.log_slots, b1, True, 1.0),
-                            stc=plan_stages(spec.log_slots, b2, False, 1.0),
+                            cts=plan_stages(spec.log_slots, b1, True, 1.0, spec.babies(0)),
+                            stc=plan_stages(spec.log_slots, b2, False, 1.0, spec.babies(1)),
                             cts_rho=(S / (2.0 * q0 * Kp)) ** (1.0 / b1),
                             stc_rho=(q0 / (2.0 * math.pi * S_out)) ** (1.0 / b2))
     prog.constants = _Constants(prog)

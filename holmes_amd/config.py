@@ -1,11 +1,20 @@
-"""CKKS run configuration with the fields of llama3fhe/config.py:15-42 (``SimulatorConfig``),
-defaults set for the MI355X FP64 arithmetic path (50-bit primes, scale 2^40)."""
+"""CKKS run configuration with the field names of llama3fhe/config.py:15-42 (``SimulatorConfig``).
+
+Field names are the interface (configuration files and callers set them by name); the defaults are
+set for this backend's FP64 arithmetic path (50-bit primes, scale 2^40).  Both rescale techniques
+of the reference map onto a policy name: FIXEDMANUAL -> "manual", FIXEDAUTO -> "auto".
+"""
 
 from __future__ import annotations
 
 import json
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from pathlib import Path
+
+_POLICY_ALIASES = {
+    "manual": ("fixedmanual", "fixed_manual", "manual"),
+    "auto": ("fixedauto", "fixed_auto", "auto"),
+}
 
 
 @dataclass
@@ -22,26 +31,39 @@ class SimulatorConfig:
     scaleBits: int = 40
 
     def rescale_policy(self) -> str:
-        value = str(self.rescaleTech).lower()
-        if value in {"fixedmanual", "fixed_manual", "manual"}:
-            return "manual"
-        if value in {"fixedauto", "fixed_auto", "auto"}:
-            return "auto"
-        raise ValueError(f"unsupported rescale policy: {value!r}")
+        """"manual" or "auto" for the configured rescale technique."""
+
+        tech = str(self.rescaleTech).strip().lower()
+        for policy, spellings in _POLICY_ALIASES.items():
+            if tech in spellings:
+                return policy
+        raise ValueError(f"rescaleTech {self.rescaleTech!r} is neither a FIXEDMANUAL nor a FIXEDAUTO spelling")
 
     def validate(self) -> None:
-        if int(self.logN) <= 1:
-            raise ValueError("simulator.logN must be greater than one.")
-        if int(self.maxLevelsRemaining) <= 0:
-            raise ValueError("simulator.maxLevelsRemaining must be positive.")
-        if int(self.dnum) <= 0 or int(self.dcrtBits) <= 0 or int(self.firstMod) <= 0:
-            raise ValueError("simulator dnum/modulus parameters must be positive.")
+        """Raise ValueError on a configuration no context can be built from."""
+
+        problems = []
+        if int(self.logN) < 2:
+            problems.append(f"logN={self.logN} (needs at least 2)")
+        if int(self.maxLevelsRemaining) < 1:
+            problems.append(f"maxLevelsRemaining={self.maxLevelsRemaining} (needs at least 1)")
+        for name in ("dnum", "dcrtBits", "firstMod"):
+            if int(getattr(self, name)) < 1:
+                problems.append(f"{name}={getattr(self, name)} (needs at least 1)")
+        if problems:
+            raise ValueError("invalid simulator configuration: " + ", ".join(problems))
         self.rescale_policy()
 
     @classmethod
     def from_json(cls, path: str | Path) -> "SimulatorConfig":
-        sim = json.loads(Path(path).read_text(encoding="utf-8")).get("simulator", {})
-        cfg = cls(**{k: (tuple(v) if k == "level_budget" else v) for k, v in sim.items() if k in cls.__dataclass_fields__})
+        """The ``simulator`` section of a model configuration file (unknown keys ignored)."""
+
+        section = json.loads(Path(path).read_text(encoding="utf-8")).get("simulator", {})
+        known = {f.name for f in fields(cls)}
+        values = {k: v for k, v in section.items() if k in known}
+        if "level_budget" in values:
+            values["level_budget"] = tuple(values["level_budget"])
+        cfg = cls(**values)
         cfg.validate()
         return cfg
 

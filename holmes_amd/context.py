@@ -638,7 +638,7 @@ class CKKSContext:
         into NTT-domain residues [rows][limbs][N], limb l modulo prime prime_idx[l] (default: the
         first ``limbs`` Q primes; ``ext_prime_idx`` gives an extended-basis plaintext).
 
-        Overflow (a coefficient reaching 2^52) sets an int32 device flag per row.  Without
+        Overflow (a coefficient reaching 2^61) sets an int32 device flag per row.  Without
         ``flags`` they are read back here (one host sync) and raise; with a caller-owned
         ``flags`` tensor ([>= rows] int32, zeroed once) the flags accumulate there for one check
         at the caller's next synchronisation point (``check_encode_flags``)."""
@@ -678,7 +678,7 @@ class CKKSContext:
     @staticmethod
     def check_encode_flags(flags: torch.Tensor) -> None:
         if bool(flags.any().item()):
-            raise ValueError("encoded coefficient reached 2^52: lower the scale or the value range")
+            raise ValueError("encoded coefficient reached 2^61: lower the scale or the value range")
 
     def encode_real(self, values: torch.Tensor, scale: float, limbs: int, out: torch.Tensor | None = None,
                     flags: torch.Tensor | None = None) -> torch.Tensor:

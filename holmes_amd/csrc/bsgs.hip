@@ -17,6 +17,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "modarith64.hpp"
 
 namespace hck {
 namespace {
@@ -132,8 +133,104 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
   }
 }
 
+// ----------------------------------------------------------------- the sidecar-shaped MAC
+// holmes_mac_multi's layout (bench/cmp/kernels/holmes_mac.cu:359-402): one device pointer per input to
+// its baby basis [nb][>= limbs][N] (baby stride bstride words), plaintext rows [groups * nb][>= limbs][N]
+// (row stride pstride), res [2][groups][inputs][limbs][N], and the moduli as a device array (limb l uses
+// primes[l]).  No context handle is needed: every workgroup derives its limb's Barrett constant from
+// the prime (modarith64.hpp), so the entry works for any prime below 2^62 -- the reference's 59/60-bit
+// chains included.  Products are reduced one by one and summed canonically.
+constexpr int kAbiMaxInputs = 32;
+constexpr int kAbiThreads = 128;
+constexpr int kAbiTI = 2;
+constexpr int kAbiTG = 8;
+
+struct AbiInputs {
+  const uint64_t* c0[kAbiMaxInputs];
+  const uint64_t* c1[kAbiMaxInputs];
+};
+
+__global__ __launch_bounds__(kAbiThreads) void k_mac_multi_abi(uint64_t* __restrict__ res, AbiInputs in,
+                                                               long long bstride, int nb, int ni, int G,
+                                                               const uint64_t* __restrict__ pts, long long pstride,
+                                                               int limbs, const uint64_t* __restrict__ primes,
+                                                               int tiles_i) {
+  const int l = blockIdx.y;
+  const int units = kN / kAbiThreads;
+  const int unit = blockIdx.x % units, tile = blockIdx.x / units;
+  const int i0 = (tile % tiles_i) * kAbiTI, g0 = (tile / tiles_i) * kAbiTG;
+  const long long ln = (long long)l * kN + unit * kAbiThreads + threadIdx.x;
+  const Barrett64 br = barrett_make(primes[l]);
+  const uint64_t p = br.p;
+  uint64_t acc[kAbiTI][2][kAbiTG];
+#pragma unroll
+  for (int t = 0; t < kAbiTI; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < kAbiTG; ++g) acc[t][c][g] = 0;
+  for (int b = 0; b < nb; ++b) {
+    uint64_t w[kAbiTG];
+#pragma unroll
+    for (int g = 0; g < kAbiTG; ++g) {
+      const int gg = g0 + g < G ? g0 + g : g0;  // clamped rows are computed but never stored
+      w[g] = pts[((long long)gg * nb + b) * pstride + ln];
+    }
+#pragma unroll
+    for (int t = 0; t < kAbiTI; ++t) {
+      const int ii = i0 + t < ni ? i0 + t : i0;
+      const uint64_t x0 = in.c0[ii][(long long)b * bstride + ln];
+      const uint64_t x1 = in.c1[ii][(long long)b * bstride + ln];
+#pragma unroll
+      for (int g = 0; g < kAbiTG; ++g) {
+        acc[t][0][g] = addmod64(acc[t][0][g], mulmod64(x0, w[g], br), p);
+        acc[t][1][g] = addmod64(acc[t][1][g], mulmod64(x1, w[g], br), p);
+      }
+    }
+  }
+  const long long is = (long long)limbs * kN, gs = (long long)ni * is, cs = (long long)G * gs;
+#pragma unroll
+  for (int t = 0; t < kAbiTI; ++t) {
+    if (i0 + t >= ni) break;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < kAbiTG; ++g)
+        if (g0 + g < G) res[c * cs + (long long)(g0 + g) * gs + (long long)(i0 + t) * is + ln] = acc[t][c][g];
+  }
+}
+
 }  // namespace
 }  // namespace hck
+
+extern "C" int holmes_mac_multi(uint64_t* res, const uint64_t* const* c0s, const uint64_t* const* c1s,
+                                long long bstride, int nb, int inputs, const uint64_t* pts, long long pstride,
+                                int groups, int ti, int limbs, const uint64_t* primes, const uint64_t* ratios,
+                                const uint64_t* ks, void* stream) {
+  (void)ratios;  // the caller's Barrett tables: this entry derives its constants from `primes`
+  (void)ks;
+  if (inputs < 1 || inputs > hck::kAbiMaxInputs) return -1;
+  if (nb < 1) return -2;
+  if (groups < 1 || groups > 16 || (groups > 8 && ti != 10116)) return -3;
+  static const int kTiles[] = {1, 2, 4, 404, 408, 802, 804, 1601, 1602, 10108, 10116, 10204, 10208, 10402, 10404};
+  bool known = false;
+  for (int v : kTiles) known |= v == ti;
+  if (!known) return -4;  // the reference's tile selector is validated, the tile here is this kernel's own
+  if (!res || !c0s || !c1s || !pts || !primes || limbs < 1 || limbs > 65535) return HCK_ERR_ARG;
+  hck::AbiInputs in{};
+  for (int i = 0; i < inputs; ++i) {
+    if (!c0s[i] || !c1s[i]) return HCK_ERR_ARG;
+    in.c0[i] = c0s[i];
+    in.c1[i] = c1s[i];
+  }
+  const int tiles_i = (inputs + hck::kAbiTI - 1) / hck::kAbiTI;
+  const int tiles_g = (groups + hck::kAbiTG - 1) / hck::kAbiTG;
+  const dim3 grid((unsigned)(hck::kN / hck::kAbiThreads * tiles_i * tiles_g), (unsigned)limbs);
+  hck::k_mac_multi_abi<<<grid, hck::kAbiThreads, 0, (hipStream_t)stream>>>(res, in, bstride, nb, inputs, groups,
+                                                                           pts, pstride, limbs, primes, tiles_i);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
 
 extern "C" int hck_bsgs_mac(const hck_context* ctx, int limbs, const int* prime_idx, int inputs, int babies,
                             int giants, const uint64_t* const* baby_c0, const uint64_t* const* baby_c1,

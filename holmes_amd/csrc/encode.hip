@@ -12,8 +12,8 @@
 // product and rounding are the exact IEEE operation sequence of the oracle (floating-point
 // contraction is off in this file), so encoded residues are bit-identical to it.  View the
 // n = 2^15 slots as a 256 x 128 matrix (k = 128 r + c): stages with half-width >= 128 pair rows of
-// a column, the rest stay inside a row.  Coefficients must stay below 2^52 in magnitude (the
-// exact-double range); a row that overflows sets its flag and is reported to the caller.
+// a column, the rest stay inside a row.  Coefficients must stay below 2^61 in magnitude (the
+// reference's encoder cap); a row that overflows sets its flag and is reported to the caller.
 #pragma clang fp contract(off)
 #include <hip/hip_runtime.h>
 

@@ -274,6 +274,12 @@ __global__ __launch_bounds__(kThreads) void k_inv_cols(void* data, long long str
 // in [0, p) and runs stages 0..7 exactly as k_fwd_cols<kU64> does on stored residues, so the result
 // is bit-identical to rounding, storing every limb and transforming.  The residues of all limbs
 // never reach HBM.
+// Encoder cap: |coefficient| < 2^61, the reference's MAX_ENCODED_BITS
+// (llama3fhe/operators/attention/prefill/softmax.py:559).  A rounded coefficient is an exact double
+// (at and above 2^53 every double is an integer), and canon() reduces it exactly: q = floor(x / p)
+// is then below 2^12 and the residue x - q p (|.| < 2p) is the exact result of one FMA.
+constexpr double kEncodeCap = 2305843009213693952.0;  // 2^61
+
 __global__ __launch_bounds__(kThreads) void k_encode_cols(const double* __restrict__ vre,
                                                           const double* __restrict__ vim, double scale,
                                                           double* __restrict__ out, long long out_stride,
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void k_encode_cols(const double* __restri
       const int slot = (int)(__brev((unsigned)(n - h * (kN / 2))) >> (32 - (kLogN - 1)));
       const double w = (h ? im : re)[slot] * inv_n;
       a[k] = round_away(w * scale);
-      big |= fabs(a[k]) >= kTwo52;
+      big |= fabs(a[k]) >= kEncodeCap;
     }
   }
   if (big) overflow[row] = 1;

@@ -361,13 +361,25 @@ class ConstantBundle:
     llama3fhe/backend.py:346-356, operators/linear/weight.py:458-469), and named scalars encoded
     as one residue table (``encoded_scalars``, llama3fhe/operators/nonlinear/polynomial.py:
     274-291).  ``cache_mode="plain"`` keeps each encoded plaintext for reuse; ``"none"`` encodes
-    every call."""
+    every call.  ``keep`` (optional) is asked with an encoding's byte size before it is kept: a
+    session byte budget answers False once it is spent, and the encoding is then only returned."""
 
-    def __init__(self, vectors: dict | None = None, cache_mode: str = "none", scalars: dict | None = None):
+    def __init__(self, vectors: dict | None = None, cache_mode: str = "none", scalars: dict | None = None,
+                 keep=None):
         self.vectors = dict(vectors or {})
         self.scalars = dict(scalars or {})
         self.cache_mode = str(cache_mode)
+        self._keep = keep
         self._cache: dict = {}
+
+    @staticmethod
+    def _nbytes(entry) -> int:
+        tensors = getattr(entry, "cv", None) or [getattr(entry, "residues", None)]
+        return sum(int(t.numel()) * int(t.element_size()) for t in tensors if hasattr(t, "numel"))
+
+    def _store(self, key, entry) -> None:
+        if self._keep is None or self._keep(self._nbytes(entry)):
+            self._cache[key] = entry
 
     def encoded_scalars(self, names, cur_limbs: int, scale_degree: int = 1, context: CKKSContext | None = None,
                         scaling_factor: float | None = None, cache: bool | None = None,
@@ -382,7 +394,7 @@ class ConstantBundle:
         enc = encode_scalar(np.array([float(self.scalars[n]) for n in names]), int(cur_limbs), int(scale_degree),
                             scaling_factor, context=context, mode=mode)
         if (self.cache_mode in ("plain", "both")) if cache is None else bool(cache):
-            self._cache[key] = enc
+            self._store(key, enc)
         return enc
 
     def plaintext(self, name: str, state: CipherState, slots: int, context: CKKSContext,
@@ -398,12 +410,11 @@ class ConstantBundle:
         v = v.values if isinstance(v, PackedRaw) else v
         pt = encode_plaintext(v, state, int(slots), context, is_ext=bool(is_ext))
         if keep:
-            self._cache[key] = pt
+            self._store(key, pt)
         return pt
 
     def cache_info(self) -> dict:
-        total = sum(int(pt.cv[0].numel()) * 8 for pt in self._cache.values())
-        return {"entries": len(self._cache), "total_bytes": total}
+        return {"entries": len(self._cache), "total_bytes": sum(map(self._nbytes, self._cache.values()))}
 
     def clear_cache(self) -> None:
         self._cache.clear()

@@ -43,60 +43,81 @@ __all__ = [
 ]
 
 
-# ---------------------------------------------------------------------------- handle helpers
-def _group(values: Iterable[object], name: str) -> tuple:
-    g = tuple(values)
-    if len(g) != PAIRFOLD_GROUP_COUNT:
-        raise ValueError(f"{name} must contain exactly {PAIRFOLD_GROUP_COUNT} ciphertexts, got {len(g)}")
-    if any(v is None for v in g):
-        raise ValueError(f"{name} must not contain None")
-    return g
+# ---------------------------------------------------------------------------- ownership primitives
+def _free(handles: Iterable[object]) -> BaseException | None:
+    """Call ``release()`` once on every distinct handle (in order), whatever fails on the way;
+    hand back the first exception instead of raising it."""
 
-
-def _unique(handles: Iterable[object], owner: str) -> None:
-    hs = tuple(handles)
-    if len({id(h) for h in hs}) != len(hs):
-        raise ValueError(f"{owner}: ciphertext handles must not alias")
-
-
-def _release_all(handles: Iterable[object]) -> BaseException | None:
-    """Release every distinct handle once; return the first error after trying them all."""
-
-    first = None
-    seen: set[int] = set()
-    for h in tuple(handles):
-        if id(h) in seen:
+    done: set[int] = set()
+    first: BaseException | None = None
+    for h in handles:
+        if id(h) in done:
             continue
-        seen.add(id(h))
+        done.add(id(h))
+        release = getattr(h, "release", None)
+        if not callable(release):
+            continue
         try:
-            rel = getattr(h, "release", None)
-            if callable(rel):
-                rel()
-        except BaseException as err:  # every handle is still tried
-            if first is None:
-                first = err
+            release()
+        except BaseException as exc:  # keep releasing the rest
+            first = exc if first is None else first
     return first
 
 
-def _deep_copies(handles: Iterable[object]) -> tuple:
-    src = tuple(handles)
-    _unique(src, "clone sources")
-    src_ids = {id(h) for h in src}
-    made: list = []
-    try:
-        for h in src:
+def _distinct(handles: Iterable[object], what: str) -> tuple:
+    items = tuple(handles)
+    if len(set(map(id, items))) < len(items):
+        raise ValueError(f"{what}: the same ciphertext object appears twice (handles alias)")
+    return items
+
+
+def _groups(values: Iterable[object], what: str) -> tuple:
+    items = tuple(values)
+    if len(items) != PAIRFOLD_GROUP_COUNT or any(v is None for v in items):
+        raise ValueError(f"{what} needs {PAIRFOLD_GROUP_COUNT} ciphertexts (no None), got {len(items)}")
+    return items
+
+
+class _Staged:
+    """Ciphertexts produced inside one transaction.  Leaving the block with an exception releases
+    the ones that do not belong to ``keep`` (the inputs); ``commit()`` hands them over instead."""
+
+    def __init__(self, keep: Iterable[object] = ()) -> None:
+        self._keep = {id(h) for h in keep}
+        self.items: list = []
+
+    def add(self, handle):
+        self.items.append(handle)
+        return handle
+
+    def fresh(self) -> list:
+        return [h for h in self.items if id(h) not in self._keep]
+
+    def commit(self) -> tuple:
+        out, self.items = tuple(self.items), []
+        return out
+
+    def __enter__(self) -> "_Staged":
+        return self
+
+    def __exit__(self, exc_type, exc, tb) -> bool:
+        if exc_type is not None:
+            _free(self.fresh())
+        return False
+
+
+def _duplicates(handles: Iterable[object]) -> tuple:
+    """Deep copies of ``handles`` (distinct new objects), or nothing: a failed copy releases the
+    copies made so far and re-raises."""
+
+    sources = _distinct(handles, "copy sources")
+    with _Staged(keep=sources) as staged:
+        for h in sources:
             c = h.deep_copy()
-            if c is None:
-                raise RuntimeError("ciphertext deep_copy returned None")
-            if id(c) in src_ids:
-                raise RuntimeError("ciphertext deep_copy must not return a source handle")
-            if any(c is m for m in made):
-                raise RuntimeError("ciphertext deep_copy outputs must not alias each other")
-            made.append(c)
-    except BaseException:
-        _release_all(m for m in made if id(m) not in src_ids)
-        raise
-    return tuple(made)
+            if c is None or any(c is x for x in sources) or any(c is x for x in staged.items):
+                raise RuntimeError("deep_copy must return a new ciphertext object")
+            staged.add(c)
+        return staged.commit()
 
 
 # ---------------------------------------------------------------------------- HBM page pool
@@ -204,136 +225,121 @@ class KVPagePool:
 
 
 # ---------------------------------------------------------------------------- ownership types
+class _QuadOwner:
+    """Shared behaviour of a token write and a page: four ciphertexts (two key groups, then two
+    value groups) owned until they are released or moved out.  Subclasses are dataclasses with the
+    fields ``key_groups`` and ``value_groups`` and define ``_rebuild(keys, values)``."""
+
+    _noun = "ciphertext owner"
+
+    def _own(self) -> None:
+        self.key_groups = _groups(self.key_groups, "key_groups")
+        self.value_groups = _groups(self.value_groups, "value_groups")
+        _distinct(self.handles, self._noun)
+
+    @property
+    def handles(self) -> tuple:
+        return (*self.key_groups, *self.value_groups)
+
+    @property
+    def is_released(self) -> bool:
+        return self._released
+
+    def _check_live(self) -> None:
+        if self._released:
+            raise RuntimeError(f"this {self._noun} no longer owns its ciphertexts (released or moved)")
+
+    def _surrender(self) -> tuple:
+        """Give the handles to the caller; this owner is empty afterwards."""
+
+        self._check_live()
+        out = self.handles
+        self.key_groups = self.value_groups = ()
+        self._released = True
+        return out
+
+    def clone(self):
+        self._check_live()
+        copies = _duplicates(self.handles)
+        try:
+            return self._rebuild(copies[:PAIRFOLD_GROUP_COUNT], copies[PAIRFOLD_GROUP_COUNT:])
+        except BaseException:
+            _free(copies)
+            raise
+
+    def release(self) -> None:
+        if not self._released:
+            failure = _free(self._surrender())
+            if failure is not None:
+                raise failure
+
+
 @dataclass
-class PairFoldTokenWrite:
+class PairFoldTokenWrite(_QuadOwner):
     """The owned K/V payload of one token column: two key and two value ciphertexts."""
 
     key_groups: tuple | list
     value_groups: tuple | list
     column: int
     _released: bool = field(default=False, init=False, repr=False)
+    _noun = "token write"
 
     def __post_init__(self) -> None:
-        self.key_groups = _group(self.key_groups, "key_groups")
-        self.value_groups = _group(self.value_groups, "value_groups")
         self.column = int(self.column)
-        if not 0 <= self.column < PAIRFOLD_PAGE_SIZE:
-            raise ValueError(f"column must be in [0, {PAIRFOLD_PAGE_SIZE - 1}], got {self.column}")
-        _unique(self.handles, "token write")
+        if self.column not in range(PAIRFOLD_PAGE_SIZE):
+            raise ValueError(f"column {self.column} is not a page column (0..{PAIRFOLD_PAGE_SIZE - 1})")
+        self._own()
 
     @property
-    def handles(self) -> tuple:
-        return tuple(self.key_groups) + tuple(self.value_groups)
+    def is_consumed(self) -> bool:
+        return self._released
 
-    @property
-    def is_released(self) -> bool:
-        return bool(self._released)
-
-    is_consumed = is_released
-
-    def _check_live(self) -> None:
-        if self._released:
-            raise RuntimeError("PairFold token write has already been consumed")
-
-    def _take(self) -> tuple:
-        """Give up ownership without releasing (the caller now owns the handles)."""
-
-        self._check_live()
-        owned = self.handles
-        self.key_groups, self.value_groups = (), ()
-        self._released = True
-        return owned
-
-    def clone(self) -> "PairFoldTokenWrite":
-        self._check_live()
-        copies = _deep_copies(self.handles)
-        try:
-            return PairFoldTokenWrite(copies[:PAIRFOLD_GROUP_COUNT], copies[PAIRFOLD_GROUP_COUNT:], self.column)
-        except BaseException:
-            _release_all(copies)
-            raise
+    def _rebuild(self, keys, values) -> "PairFoldTokenWrite":
+        return PairFoldTokenWrite(keys, values, self.column)
 
     def move(self) -> "PairFoldTokenWrite":
-        self._check_live()
-        moved = PairFoldTokenWrite(self.key_groups, self.value_groups, self.column)  # validates first
-        self._take()
-        return moved
+        """A new write owning these handles; this one is consumed (no copy)."""
 
-    def release(self) -> None:
-        if self._released:
-            return
-        err = _release_all(self._take())
-        if err is not None:
-            raise err
+        self._check_live()
+        successor = self._rebuild(self.key_groups, self.value_groups)
+        self._surrender()
+        return successor
 
 
 @dataclass
-class PairFoldCipherPage:
+class PairFoldCipherPage(_QuadOwner):
     """One page: two K and two V ciphertexts holding ``occupied`` of its 128 token columns."""
 
     key_groups: tuple | list
     value_groups: tuple | list
     occupied: int
     _released: bool = field(default=False, init=False, repr=False)
+    _noun = "PairFold page"
 
     def __post_init__(self) -> None:
-        self.key_groups = _group(self.key_groups, "key_groups")
-        self.value_groups = _group(self.value_groups, "value_groups")
         self.occupied = int(self.occupied)
-        if not 1 <= self.occupied <= PAIRFOLD_PAGE_SIZE:
-            raise ValueError(f"occupied must be in [1, {PAIRFOLD_PAGE_SIZE}], got {self.occupied}")
-        _unique(self.handles, "PairFold page")
-
-    @property
-    def handles(self) -> tuple:
-        return tuple(self.key_groups) + tuple(self.value_groups)
+        if not 0 < self.occupied <= PAIRFOLD_PAGE_SIZE:
+            raise ValueError(f"occupied count {self.occupied} is outside 1..{PAIRFOLD_PAGE_SIZE}")
+        self._own()
 
     @property
     def remaining(self) -> int:
         return PAIRFOLD_PAGE_SIZE - self.occupied
 
-    @property
-    def is_released(self) -> bool:
-        return bool(self._released)
-
-    def _check_live(self) -> None:
-        if self._released:
-            raise RuntimeError("PairFold page has already been released")
-
-    def _take(self) -> tuple:
-        self._check_live()
-        owned = self.handles
-        self.key_groups, self.value_groups = (), ()
-        self._released = True
-        return owned
+    def _rebuild(self, keys, values) -> "PairFoldCipherPage":
+        return PairFoldCipherPage(keys, values, self.occupied)
 
     @classmethod
     def from_token_write(cls, token: PairFoldTokenWrite, occupied: int) -> "PairFoldCipherPage":
-        """The token's handles become the page (no copy); the token is consumed only once the page
-        has been built and validated."""
+        """The token's handles become the page; the token is consumed only after the page has
+        been built (a bad ``occupied`` leaves the token untouched)."""
 
         if not isinstance(token, PairFoldTokenWrite):
-            raise TypeError("token must be a PairFoldTokenWrite")
+            raise TypeError(f"expected a PairFoldTokenWrite, got {type(token).__name__}")
         token._check_live()
-        page = cls(key_groups=token.key_groups, value_groups=token.value_groups, occupied=occupied)
-        token._take()
+        page = cls(token.key_groups, token.value_groups, occupied)
+        token._surrender()
         return page
-
-    def clone(self) -> "PairFoldCipherPage":
-        self._check_live()
-        copies = _deep_copies(self.handles)
-        try:
-            return PairFoldCipherPage(copies[:PAIRFOLD_GROUP_COUNT], copies[PAIRFOLD_GROUP_COUNT:], self.occupied)
-        except BaseException:
-            _release_all(copies)
-            raise
-
-    def release(self) -> None:
-        if self._released:
-            return
-        err = _release_all(self._take())
-        if err is not None:
-            raise err
 
 
 @dataclass
@@ -351,11 +357,11 @@ class PairFoldLayerCache:
         self.pages = tuple(self.pages)
         self.content_tokens = int(self.content_tokens)
         self.layout_tag = str(self.layout_tag)
-        self._validate()
+        self._check_shape()
 
     @property
     def is_released(self) -> bool:
-        return bool(self._released)
+        return self._released
 
     @property
     def occupied(self) -> int:
@@ -364,188 +370,193 @@ class PairFoldLayerCache:
     @property
     def handles(self) -> tuple:
         self._check_live()
-        return tuple(h for p in self.pages for h in p.handles)
+        return tuple(h for page in self.pages for h in page.handles)
 
     def _check_live(self) -> None:
         if self._released:
-            raise RuntimeError("PairFold layer cache has already been released")
+            raise RuntimeError("this PairFold layer cache was released")
 
-    def _validate(self) -> None:
+    def _check_shape(self) -> None:
+        """Layout tag, page types, full pages before the tail, token count, no shared handle."""
+
         if self.layout_tag != PAIRFOLD_LAYOUT_TAG:
-            raise ValueError(f"layout_tag must be {PAIRFOLD_LAYOUT_TAG!r}, got {self.layout_tag!r}")
+            raise ValueError(f"unknown layout tag {self.layout_tag!r} (this cache is {PAIRFOLD_LAYOUT_TAG!r})")
         if self.content_tokens < 0:
-            raise ValueError("content_tokens must be non-negative")
-        if not self.pages:
-            if self.content_tokens:
-                raise ValueError("an empty PairFold cache must hold zero tokens")
-            return
-        total = 0
-        for i, p in enumerate(self.pages):
-            if not isinstance(p, PairFoldCipherPage):
-                raise TypeError("pages must be PairFoldCipherPage objects")
-            p._check_live()
-            if i < len(self.pages) - 1 and p.occupied != PAIRFOLD_PAGE_SIZE:
-                raise ValueError("every page but the tail must be full")
-            total += p.occupied
-        if total != self.content_tokens:
-            raise ValueError(f"content_tokens {self.content_tokens} differs from the pages' occupancy {total}")
-        _unique([h for p in self.pages for h in p.handles], "PairFold cache")
+            raise ValueError(f"content_tokens {self.content_tokens} is negative")
+        for page in self.pages:
+            if not isinstance(page, PairFoldCipherPage):
+                raise TypeError(f"pages hold PairFoldCipherPage objects, not {type(page).__name__}")
+            page._check_live()
+        if any(p.occupied != PAIRFOLD_PAGE_SIZE for p in self.pages[:-1]):
+            raise ValueError("a page before the last one is not full")
+        counted = sum(p.occupied for p in self.pages)
+        if counted != self.content_tokens:
+            raise ValueError(f"content_tokens is {self.content_tokens} but the pages hold {counted} tokens")
+        _distinct(self.handles, "PairFold layer cache")
+
+    def _next_column(self) -> int:
+        """The column the next token must carry: 0 opens a page, else the tail's first free one."""
+
+        if not self.pages or self.pages[-1].remaining == 0:
+            return 0
+        return self.pages[-1].occupied
 
     def clone(self) -> "PairFoldLayerCache":
         self._check_live()
-        self._validate()
-        copies = _deep_copies(self.handles)
+        self._check_shape()
+        copies = _duplicates(self.handles)
         try:
-            pages = tuple(PairFoldCipherPage(copies[i * _HANDLES:i * _HANDLES + PAIRFOLD_GROUP_COUNT],
-                                             copies[i * _HANDLES + PAIRFOLD_GROUP_COUNT:(i + 1) * _HANDLES],
-                                             p.occupied) for i, p in enumerate(self.pages))
+            pages, at = [], 0
+            for page in self.pages:
+                quad = copies[at:at + _HANDLES]
+                pages.append(PairFoldCipherPage(quad[:PAIRFOLD_GROUP_COUNT], quad[PAIRFOLD_GROUP_COUNT:], page.occupied))
+                at += _HANDLES
             return PairFoldLayerCache(pages=pages, content_tokens=self.content_tokens, layout_tag=self.layout_tag,
                                       pool=self.pool)
         except BaseException:
-            _release_all(copies)
+            _free(copies)
             raise
 
     def extend_pages(self, other: "PairFoldLayerCache") -> None:
-        """Move the pages of ``other`` (prefill output) behind this cache's full tail, no copy."""
+        """Move the pages of ``other`` (a prefill's output) behind this cache's full tail, no copy;
+        ``other`` ends released and empty."""
 
         self._check_live()
         if not isinstance(other, PairFoldLayerCache):
-            raise TypeError("other must be a PairFoldLayerCache")
-        other._check_live()
+            raise TypeError(f"expected a PairFoldLayerCache, got {type(other).__name__}")
         if other is self:
-            raise ValueError("cannot extend a cache with itself")
-        self._validate()
-        other._validate()
+            raise ValueError("a cache cannot take its own pages")
+        other._check_live()
+        self._check_shape()
+        other._check_shape()
         if not other.pages:
             return
-        if self.pages and self.pages[-1].occupied != PAIRFOLD_PAGE_SIZE:
-            raise ValueError("the tail must be full before pages are appended")
-        _unique(self.handles + other.handles, "combined PairFold cache")
-        self.pages = self.pages + other.pages
+        if self._next_column() != 0:
+            raise ValueError("the tail must be full before another cache's pages can follow it")
+        _distinct(self.handles + other.handles, "joined PairFold caches")
+        self.pages += other.pages
         self.content_tokens += other.content_tokens
         other.pages, other.content_tokens, other._released = (), 0, True
 
+    def _sums(self, tail: PairFoldCipherPage, token: PairFoldTokenWrite, crypto_context, staged: _Staged) -> None:
+        """The four page + token sums into ``staged``: one fused launch into a pool slot when the
+        pool fits them, else one homo_add per ciphertext (the reference's path)."""
+
+        pairs = tuple(zip(tail.handles, token.handles))
+        if self.pool is not None and self.pool.fits(tail.handles + token.handles):
+            for out in self.pool.add_pages(tail.handles, token.handles):
+                staged.add(out)
+            return
+        for page_ct, token_ct in pairs:
+            staged.add(crypto_context.fhe.homo_add(page_ct, token_ct, crypto_context.context))
+
     def append(self, token: PairFoldTokenWrite, *, crypto_context) -> tuple[int, int]:
-        """Consume ``token`` into its column; returns (page index, column).  A new page takes the
-        token's handles; a partial tail gets the four sums (fused into a pool slot when the cache
-        has a pool that fits, else four ``crypto_context.fhe.homo_add`` calls), committed together."""
+        """Consume ``token`` into its column; returns (page index, column).  A token at column 0
+        becomes a new page by move; any other column is added into the tail, and the four sums
+        replace the tail only once all of them exist (then the old tail and the token are
+        released).  Anything that fails first leaves the cache and the token as they were."""
 
         self._check_live()
-        self._validate()
+        self._check_shape()
         if not isinstance(token, PairFoldTokenWrite):
-            raise TypeError("token must be a PairFoldTokenWrite")
+            raise TypeError(f"expected a PairFoldTokenWrite, got {type(token).__name__}")
         token._check_live()
-        mine = tuple(h for p in self.pages for h in p.handles)
-        _unique(mine + token.handles, "cache and token write")
-        opens = not self.pages or self.pages[-1].occupied == PAIRFOLD_PAGE_SIZE
-        want = 0 if opens else self.pages[-1].occupied
-        if token.column != want:
-            raise ValueError(f"token column must be {want}, got {token.column}")
-        if opens:
-            self.pages = self.pages + (PairFoldCipherPage.from_token_write(token, occupied=1),)
+        _distinct(self.handles + token.handles, "cache and token write")
+        column = self._next_column()
+        if token.column != column:
+            raise ValueError(f"token column {token.column} is not the next free column {column}")
+        if column == 0:
+            self.pages += (PairFoldCipherPage.from_token_write(token, occupied=1),)
             self.content_tokens += 1
             return len(self.pages) - 1, 0
-
         tail = self.pages[-1]
-        inputs = {id(h) for h in mine + token.handles}
-        sums: list = []
-        try:
-            if self.pool is not None and self.pool.fits(tail.handles + token.handles):
-                sums = list(self.pool.add_pages(tail.handles, token.handles))
-            else:
-                for a, b in zip(tail.handles, token.handles):
-                    sums.append(crypto_context.fhe.homo_add(a, b, crypto_context.context))
-            _unique(sums, "append outputs")
-            if any(id(s) in inputs for s in sums):
-                raise ValueError("homo_add outputs must not alias their inputs")
-            page = PairFoldCipherPage(tuple(sums[:PAIRFOLD_GROUP_COUNT]), tuple(sums[PAIRFOLD_GROUP_COUNT:]),
-                                      tail.occupied + 1)
-        except BaseException:
-            _release_all(s for s in sums if id(s) not in inputs)
-            raise
-        # commit, then release the replaced tail and the token
-        self.pages = self.pages[:-1] + (page,)
+        inputs = self.handles + token.handles
+        with _Staged(keep=inputs) as staged:
+            self._sums(tail, token, crypto_context, staged)
+            _distinct(staged.items, "sums of an append")
+            if len(staged.fresh()) != len(staged.items):
+                raise ValueError("homo_add returned one of its inputs: outputs must be new ciphertexts (alias)")
+            sums = staged.items
+            grown = PairFoldCipherPage(sums[:PAIRFOLD_GROUP_COUNT], sums[PAIRFOLD_GROUP_COUNT:], tail.occupied + 1)
+            staged.commit()
+        self.pages = self.pages[:-1] + (grown,)
         self.content_tokens += 1
-        err = _release_all(tail._take() + token._take())
-        if err is not None:
-            raise err
-        return len(self.pages) - 1, want
+        failure = _free(tail._surrender() + token._surrender())
+        if failure is not None:
+            raise failure
+        return len(self.pages) - 1, column
 
     def release(self) -> None:
         if self._released:
             return
         pages = self.pages
         self.pages, self.content_tokens, self._released = (), 0, True
-        first = None
-        for p in pages:
+        failures = []
+        for page in pages:
             try:
-                p.release()
-            except BaseException as err:
-                if first is None:
-                    first = err
-        if first is not None:
-            raise first
+                page.release()
+            except BaseException as exc:
+                failures.append(exc)
+        if failures:
+            raise failures[0]
 
 
 def drop_pairfold_token_to_limbs(token: PairFoldTokenWrite, *, target_limbs: int, crypto_context,
                                  bootstrap_operator=None, bootstrap_iterations: int = 1,
                                  value_target_limbs: int | None = None) -> PairFoldTokenWrite:
-    """Bring K0, K1 to ``target_limbs`` and V0, V1 to ``value_target_limbs`` (default the same):
-    drop limbs, or refresh first with ``bootstrap_operator.refresh`` when a ciphertext has fewer
-    limbs than its target.  All four replacements are built before ``token`` is consumed; any
-    failure releases only the new ciphertexts (pairfold_kv_cache.py:478-621)."""
+    """A write whose K0, K1 sit at ``target_limbs`` and V0, V1 at ``value_target_limbs`` (default
+    the same), limbs dropped by ``fhe.align_to``; a ciphertext with fewer limbs than its target is
+    refreshed by ``bootstrap_operator.refresh`` first (llama3fhe/operators/pairfold_kv_cache.py:
+    478-621).  All four results exist before ``token`` is consumed; a failure releases only what
+    this call created.  A token already at its targets is moved, not copied."""
 
     if not isinstance(token, PairFoldTokenWrite):
-        raise TypeError("token must be a PairFoldTokenWrite")
+        raise TypeError(f"expected a PairFoldTokenWrite, got {type(token).__name__}")
     token._check_live()
-    target_limbs = int(target_limbs)
-    vt = target_limbs if value_target_limbs is None else int(value_target_limbs)
-    if target_limbs <= 1 or vt <= 1:
-        raise ValueError(f"a modulus drop must leave more than one limb, got {target_limbs} / {vt}")
-    iters = int(bootstrap_iterations)
-    if iters <= 0:
-        raise ValueError(f"bootstrap_iterations must be positive, got {iters}")
-    inputs = token.handles
-    targets = (target_limbs,) * PAIRFOLD_GROUP_COUNT + (vt,) * PAIRFOLD_GROUP_COUNT
-    for c in inputs:
-        if int(c.state.scale_degree) != 1 or bool(c.is_ext):
-            raise ValueError("modulus-only scheduling requires non-extended degree-1 ciphertexts")
-    have = tuple(int(c.state.cur_limbs) for c in inputs)
-    short = [(h, t) for h, t in zip(have, targets) if h < t]
-    if short and bootstrap_operator is None:
-        raise ValueError(f"too few limbs for the drop: {short[0][0]} < {short[0][1]}")
-    if have == targets:
+    key_t = int(target_limbs)
+    val_t = key_t if value_target_limbs is None else int(value_target_limbs)
+    if min(key_t, val_t) < 2:
+        raise ValueError(f"limb targets {key_t} / {val_t}: a dropped ciphertext keeps at least two limbs")
+    if int(bootstrap_iterations) < 1:
+        raise ValueError(f"bootstrap_iterations is {bootstrap_iterations}; it must be at least 1")
+    sources = token.handles
+    targets = (key_t,) * PAIRFOLD_GROUP_COUNT + (val_t,) * PAIRFOLD_GROUP_COUNT
+    for ct in sources:
+        if bool(ct.is_ext) or int(ct.state.scale_degree) != 1:
+            raise ValueError("limb drops take non-extended ciphertexts of scale degree 1")
+    current = tuple(int(ct.state.cur_limbs) for ct in sources)
+    if bootstrap_operator is None:
+        for have, want in zip(current, targets):
+            if have < want:
+                raise ValueError(f"too few limbs for the drop: {have} < {want} and no bootstrap operator")
+    if current == targets:
         return token.move()
-    fhe = getattr(crypto_context, "fhe", None)
-    ctx = getattr(crypto_context, "context", crypto_context)
-    if fhe is None:
-        from . import fhe
-    ids = {id(c) for c in inputs}
-    made: list = []
-    try:
-        for c, h, t in zip(inputs, have, targets):
-            work, fresh = c, None
-            if h < t:
-                fresh = bootstrap_operator.refresh(c, iterations=iters)
-                if id(fresh) in ids:
-                    raise RuntimeError("bootstrap refresh must return a new ciphertext")
-                work = fresh
+    ops = getattr(crypto_context, "fhe", None)
+    if ops is None:
+        from . import fhe as ops
+    native = getattr(crypto_context, "context", crypto_context)
+    with _Staged(keep=sources) as staged:
+        for ct, have, want in zip(sources, current, targets):
+            refreshed = None
+            if have < want:
+                refreshed = bootstrap_operator.refresh(ct, iterations=int(bootstrap_iterations))
+                if any(refreshed is x for x in sources):
+                    raise RuntimeError("bootstrap refresh returned its input; it must return a new ciphertext")
+            base = ct if refreshed is None else refreshed
             try:
-                made.append(fhe.align_to(work, work.state.replace(cur_limbs=t), ctx))
+                staged.add(ops.align_to(base, base.state.replace(cur_limbs=want), native))
             finally:
-                if fresh is not None:
-                    _release_all([fresh])
-        _unique(made, "limb-drop outputs")
-        if any(id(m) in ids for m in made):
-            raise RuntimeError("limb-drop outputs must not alias the token's ciphertexts")
-        out = PairFoldTokenWrite(made[:PAIRFOLD_GROUP_COUNT], made[PAIRFOLD_GROUP_COUNT:], token.column)
-    except BaseException:
-        _release_all(m for m in made if id(m) not in ids)
-        raise
-    made = []
+                if refreshed is not None:
+                    _free([refreshed])
+        if len(staged.fresh()) != len(staged.items):
+            raise RuntimeError("align_to returned one of the token's ciphertexts (alias)")
+        _distinct(staged.items, "limb-drop results")
+        result = PairFoldTokenWrite(staged.items[:PAIRFOLD_GROUP_COUNT], staged.items[PAIRFOLD_GROUP_COUNT:],
+                                    token.column)
+        staged.commit()
     try:
         token.release()
     except BaseException:
-        _release_all(out.handles)
+        _free(result.handles)
         raise
-    return out
+    return result

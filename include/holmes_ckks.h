@@ -19,7 +19,10 @@
  *   hck_rescale            fhe.rescale / F.cv_rescale_one_level (operator.py:387-394)
  *   hck_poly_op            F.cv_add / cv_sub / cv_neg / cv_mul / cv_mul_by_monomial (report.py:26-48)
  *   hck_poly_from_signed   the encoder's signed-integer reduction (holmes_encode.cu:108-111,133-159)
- *   hck_bsgs_mac           holmes_mac_multi, the multi-input BSGS baby-step MAC (holmes_mac.cu:359-402)
+ *   hck_bsgs_mac           the multi-input BSGS baby-step MAC behind fhe.hoisted_mac_sum (its semantics are
+ *                          holmes_mac.cu:8-12; per-baby pointer lists, context tables)
+ *   holmes_mac_multi       holmes_mac_multi itself, with the sidecar's argument list and layouts
+ *                          (holmes_mac.cu:359-402; bound at bench/cmp/holmes_multi_mac.py:49)
  *   hck_pack_diagonals     the BSGS weight diagonal packers (llama3fhe/operators/linear/weight.py:122-154,
  *                          gpu_packer.py:156-198)
  *   hck_encode             EasyFHE encode: special IFFT (cv_pre_encode_stage1) + holmes_encode_stage2
@@ -184,6 +187,20 @@ int hck_poly_from_signed(const hck_context* ctx, const int64_t* in, uint64_t* ou
 int hck_bsgs_mac(const hck_context* ctx, int limbs, const int* prime_idx, int inputs, int babies, int giants,
                  const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, int64_t baby_stride,
                  const uint64_t* pts, int64_t pt_stride, uint64_t* res, void* stream);
+
+/* The reference sidecar's multi-input MAC, argument for argument (bench/cmp/kernels/holmes_mac.cu:359-402,
+ * bound by ctypes at bench/cmp/holmes_multi_mac.py:49, called at :138):
+ *   res[c][g][i][l][n] = sum_{b < nb} pts[g * nb + b][l][n] * baby_i[b][c][l][n]   (mod primes[l])
+ * c0s / c1s: host arrays of `inputs` (1..32) device pointers to each input's baby basis
+ * [nb][>= limbs][N] (baby stride bstride words); pts [groups * nb][>= limbs][N] (row stride pstride);
+ * res [2][groups][inputs][limbs][N]; primes: device array, limb l modulo primes[l] (any prime below
+ * 2^62).  ratios / ks (the caller's Barrett tables) are accepted and not read.  ti is the sidecar's
+ * tile selector: validated against its accepted set, the tiling itself is this library's.
+ * Returns -1 (inputs), -2 (nb), -3 (groups: 1..16, above 8 only with ti 10116), -4 (ti) as the
+ * sidecar does, HCK_ERR_ARG for null pointers, else 0 or the HIP error of the launch. */
+int holmes_mac_multi(uint64_t* res, const uint64_t* const* c0s, const uint64_t* const* c1s, long long bstride,
+                     int nb, int inputs, const uint64_t* pts, long long pstride, int groups, int ti, int limbs,
+                     const uint64_t* primes, const uint64_t* ratios, const uint64_t* ks, void* stream);
 
 /* Diagonal rows of one BSGS chunk from a row-major float64 weight [dimension][dimension]:
  * out[gr * baby_steps + b][s] = W[(f - (giant_base + gr) baby_steps) mod D][(f + b + lane_shift lane) mod D],

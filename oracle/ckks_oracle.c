@@ -606,7 +606,8 @@ void or_special_ifft(int log_n, double* re, double* im, const double* tw_re, con
 
 /* values: real slot vector (n doubles).  out: [limbs][N] residues (NTT domain when ntt != 0),
  * limb l modulo the oracle context's prime prime_idx[l].  Returns -1 if a rounded coefficient is
- * 2^52 or more in magnitude (outside the exact-double range the GPU encoder supports), else 0. */
+ * 2^61 or more in magnitude (the encoder cap MAX_ENCODED_BITS = 61, llama3fhe/operators/attention/prefill/
+ * softmax.py:559), else 0.  Below the cap the rounded coefficient is an exact double, reduced exactly. */
 int or_encode_real(const or_ctx* c, const double* values, double scale, int limbs, const int* prime_idx,
                    int ntt, u64* out) {
   const int log_n = c->log_n;
@@ -627,7 +628,7 @@ int or_encode_real(const or_ctx* c, const double* values, double scale, int limb
     coef[k] = round_away(wr * scale);
     coef[k + n] = round_away(wi * scale);
   }
-  for (u64 k = 0; k < N; ++k) if (fabs(coef[k]) >= 4503599627370496.0) rc = -1;
+  for (u64 k = 0; k < N; ++k) if (fabs(coef[k]) >= 2305843009213693952.0) rc = -1;
   for (int l = 0; l < limbs; ++l) {
     const u64 q = c->primes[prime_idx[l]];
     u64* o = out + (size_t)l * N;

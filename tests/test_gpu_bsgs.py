@@ -66,9 +66,26 @@ def test_encode_every_limb_count(env):
 
 def test_encode_overflow_is_reported(env):
     ctx, _ = env
-    vals = np.full((1, ctx.max_slots), 3.0e4)
-    with pytest.raises(ValueError, match="2\\^52"):
+    vals = np.full((1, ctx.max_slots), 2.0**21)  # DC coefficient exactly 2^61: the first refused value
+    with pytest.raises(ValueError, match="2\\^61"):
         ctx.encode_real(torch.from_numpy(vals).cuda(), 2.0**40, 4)
+
+
+def test_encode_large_coefficients_bit_exact(env):
+    """Coefficients in [2^52, 2^61) (the reference's encoder cap, softmax.py:559): a DC offset of
+    1000 at scale 2^50 puts coefficient 0 near 2^60 and the noise rows' other coefficients past
+    2^52; residues equal the oracle's, and the constant row's DC residue is 1000 * 2^50 mod q."""
+    ctx, orc = env
+    limbs, scale = 12, 2.0**50
+    rng = np.random.default_rng(61)
+    vals = np.stack([np.full(ctx.max_slots, 1000.0), 1000.0 + rng.normal(scale=8.0, size=ctx.max_slots),
+                     rng.normal(scale=30.0, size=ctx.max_slots)])
+    got = _host(ctx.encode_real(torch.from_numpy(vals).cuda(), scale, limbs))
+    for r in range(3):
+        want, ok = orc.encode_real(vals[r], scale, list(range(limbs)))
+        assert ok and np.array_equal(got[r], want), f"row {r}"
+    coef, _ = orc.encode_real(vals[0], scale, list(range(limbs)), ntt=False)
+    assert [int(c) for c in coef[:, 0]] == [(1000 * 2**50) % q for q in ctx.primes[:limbs]]
 
 
 @pytest.mark.parametrize("ni,nb,G,limbs", [(16, 16, 5, 3), (3, 5, 6, 2), (1, 1, 1, 1), (5, 64, 9, 1), (2, 3, 2, 24)])

@@ -1,0 +1,182 @@
+"""GPU checks at the configured shapes of C3, C4 and C5 (the reduced-shape tests stay beside them).
+
+* C3: Llama-3-8B q_proj, 4096 x 4096 weight W ~ N(0, 0.02^2) right-multiplied by a seeded randomized
+  Hadamard rotation; 128 tokens x 4096 features N(0, 1) packed feature-major into 16 ciphertexts at
+  20 limbs, scale 2^40; BSGS with baby step 16 and 512 plaintext rows per chunk (seed 20261203).
+  Every decrypted output slot is within 2^-16 of X W'^T (the reference's decrypted check,
+  tests/test_linear.py:280-340, at the configured shape), and the first chunk's unrescaled residues
+  of input 0 equal the oracle composition of the same schedule (15 baby rotations, 512 encoded
+  diagonals, the multiply-accumulate, 31 Horner giant rotations) bit for bit.
+* C4: the MLP block at intermediate width 14336 (four feature pages), one two-pass bootstrap:
+  decrypted within 2^-16 of the float64 model of the same polynomials.
+* C5: the decode step at intermediate width 14336 against a 256-token encrypted KV cache: decrypted
+  within 2^-16 of the output's magnitude.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+C3_SEED = 20261203
+
+
+@pytest.fixture(scope="module")
+def c3():
+    from holmes_amd import fhe, linear
+    from holmes_amd.hadamard import randomized_hadamard_right
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+
+    cfg = linear.LinearOperatorConfig(baby_steps=16, baby_anchor_step=-1, max_plaintext_rows=512)
+    layout = FeatureMajorPrefillLayout(seq_len=128, hidden_dim=4096, slots=32768)
+    lanes = layout.tokens_per_cipher
+    plan = cfg.plan(dimension=4096, token_lanes=lanes)
+    spec = fhe.CKKSContextSpec(depth=19, dnum=3, dcrt_bits=50, first_mod=50, seed=C3_SEED,
+                               rotations=linear.bsgs_rotations(plan))
+    client, ctx = fhe.generate_client_context(spec)
+    rng = np.random.default_rng(C3_SEED)
+    w = randomized_hadamard_right(rng.normal(scale=0.02, size=(4096, 4096)), C3_SEED + 1)
+    x = rng.normal(size=(128, 4096))
+    packed = layout.pack(x)
+    cts = [client.encrypt(packed[c], cur_limbs=20, scaling_factor=2.0**40) for c in range(layout.cipher_count)]
+    op = linear.LinearOperator(crypto_context=ctx, token_lanes=lanes, config=cfg)
+    weight = linear.LinearWeight(w, crypto_context=ctx)
+    return linear, client, ctx, layout, plan, op, weight, w, x, cts
+
+
+@pytest.mark.timeout(600)
+def test_c3_q_proj_decrypts_to_matvec(c3):
+    linear, client, ctx, layout, plan, op, weight, w, x, cts = c3
+    assert len(cts) == 16 and plan.plaintext_chunks == 8 and plan.chunk_giants == 32
+    print("C3 full shape: 16 cts x 20 limbs, 4096 x 4096, baby 16, 512 rows per chunk", flush=True)
+    outs = op.project(cts, weight)
+    want = layout.pack(x @ w.T)
+    err = 0.0
+    for c, out in enumerate(outs):
+        assert out.state.cur_limbs == 19
+        err = max(err, float(np.max(np.abs(client.decrypt(out).real - want[c]))))
+    print(f"C3 decrypted max abs error {err:.3e} (2^{math.log2(err):.2f})", flush=True)
+    assert err < 2.0**-16
+
+
+@pytest.mark.timeout(900)
+def test_c3_first_chunk_residues_match_oracle(c3):
+    from oracle import oracle as O
+
+    linear, client, ctx, layout, plan, op, weight, w, x, cts = c3
+    limbs = 20
+    res, _ = op.apply(cts, weight, chunk_indices=[0], rescale=False)
+    torch.cuda.synchronize()
+    g0, g1 = res[0].cv[0].cpu().numpy()[0, :limbs], res[0].cv[1].cpu().numpy()[0, :limbs]
+    print("C3 chunk 0 on the GPU done; oracle composition of input 0 follows", flush=True)
+
+    orc = O.OracleContext(16, ctx.L, ctx.K, ctx.alpha, ctx.primes)
+    keys = {}
+
+    def rot(a0, a1, r):
+        if r not in keys:
+            g = ctx.galois_element(r)
+            keys[r] = (g, orc.make_ksk(*client.key_inputs(g)))
+        g, k = keys[r]
+        return orc.rotate(limbs, g, a0, a1, k)
+
+    c0, c1 = cts[0].cv[0].cpu().numpy()[0, :limbs], cts[0].cv[1].cpu().numpy()[0, :limbs]
+    babies = np.stack([np.stack((c0, c1))] + [np.stack(rot(c0, c1, off)) for off in plan.baby_offsets[1:]])
+    chunk = plan.chunks[0]
+    scale = float(ctx.rescale_divisor_at(limbs))
+    rows = O.pack_diagonals(w, plan.token_lanes, 0, plan.baby_steps, chunk.giant_base, chunk.giant_count,
+                            ctx.max_slots)
+    assert rows.shape[0] == 512
+    idx = list(range(limbs))
+    pts = np.stack([orc.encode_real(r, scale, idx)[0] for r in rows])
+    part = orc.bsgs_mac(limbs, plan.baby_steps, chunk.giant_count, pts, babies)
+    q = np.array(ctx.primes[:limbs], dtype=object).reshape(limbs, 1)
+    a0, a1 = part[0, -1], part[1, -1]
+    for g in range(chunk.giant_count - 2, -1, -1):
+        r0, r1 = rot(a0, a1, plan.giant_offset)
+        a0 = ((r0.astype(object) + part[0, g].astype(object)) % q).astype(np.uint64)
+        a1 = ((r1.astype(object) + part[1, g].astype(object)) % q).astype(np.uint64)
+    assert np.array_equal(g0, a0) and np.array_equal(g1, a1)
+
+
+@pytest.fixture(scope="module")
+def c4():
+    from holmes_amd import bootstrap as bs
+    from holmes_amd import fhe, mlp
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+
+    spec = fhe.CKKSContextSpec(depth=23, dnum=3, dcrt_bits=50, first_mod=50, scale_bits=50,
+                               secret_key_dist="SPARSE_TERNARY", hamming_weight=192, seed=20261204)
+    client, ctx = fhe.generate_client_context(spec, device="cuda")
+    mspec = mlp.MLPBlockSpec()
+    assert mspec.intermediate_width == 14336 and mspec.pages == 4
+    bspec = bs.BootstrapSpec(log_slots=15, level_budget=(3, 3))
+    layout = FeatureMajorPrefillLayout()
+    cfg = mlp.default_config()
+    rots = set(mlp.FeatureMajorMLPBlock.rotations(mspec, layout, cfg)) | set(bs.requirements(bspec, 16).rotations)
+    client.generate_rotation_keys(sorted(rots))
+    prog = bs.generate(ctx, bspec)
+    rng = np.random.default_rng(20261204)
+    D, Iw = 4096, 14336
+    gate = rng.normal(scale=0.02, size=(Iw, D))
+    up = rng.normal(scale=0.02, size=(Iw, D))
+    down = rng.normal(scale=0.02, size=(D, Iw))
+    gamma = 1.0 + 0.1 * rng.normal(size=D)
+    block = mlp.FeatureMajorMLPBlock(ctx, gate, up, down, norm_weight=gamma, spec=mspec, layout=layout, config=cfg,
+                                     bootstrap_program=prog)
+    x = rng.normal(size=(128, D))
+    cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
+    want = layout.pack(mlp.mlp_block_numpy(x, gate, up, down, gamma, mspec))
+    return client, block, cts, want
+
+
+@pytest.mark.timeout(900)
+def test_c4_mlp_block_full_width(c4):
+    client, block, cts, want = c4
+    print("C4 full shape: MLP block 4096 -> 14336 -> 4096 with a two-pass bootstrap", flush=True)
+    out, stages = block.forward(cts)
+    assert len(out) == 16 and out[0].state.cur_limbs == 8
+    err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
+    print(f"C4 max error 2^{math.log2(err):.1f}, stages {stages}", flush=True)
+    assert err < 2.0**-16
+
+
+@pytest.mark.timeout(900)
+def test_c5_decode_step_full_width():
+    import types
+
+    from holmes_amd import bootstrap as B
+    from holmes_amd import decode as Dm
+    from holmes_amd import fhe
+
+    seed = 20261205
+    spec = Dm.DecodeSpec()
+    assert spec.intermediate == 14336
+    cs = fhe.CKKSContextSpec(depth=23, dnum=3, dcrt_bits=50, first_mod=50, scale_bits=50,
+                             secret_key_dist="SPARSE_TERNARY", hamming_weight=192, seed=seed)
+    client, ctx = fhe.generate_client_context(cs, device="cuda")
+    client.generate_rotation_keys(Dm.decode_key_rotations(pages=3))
+    progs = [B.generate(ctx, b) for b in Dm.decode_bootstrap_specs()]
+    ops = Dm.CipherOps(ctx, progs[0], progs[1])
+    rng = np.random.default_rng(seed)
+    w = Dm.random_weights(spec, rng)
+    layer = Dm.DecodeLayer(ops, w, spec)
+    history = 256
+    x = rng.normal(size=spec.hidden_dim)
+    ck = rng.normal(size=(history, 1024))
+    cv = rng.normal(size=(history, 1024))
+    cache = Dm.encrypt_kv_history(client, ck, cv, spec, float(ctx.scale_at(ctx.L)))
+    xin = client.encrypt(Dm.lr8(x), cur_limbs=ctx.L)
+    print("C5 full shape: decode step, 256-token cache, SwiGLU 14336", flush=True)
+    out, stages, _ = layer.forward(xin, cache, position=history,
+                                   crypto_context=types.SimpleNamespace(fhe=fhe, context=ctx))
+    ref = Dm.decode_layer_numpy(x, ck, cv, w, spec, position=history)
+    got = client.decrypt(out)[::8].real
+    err = float(np.max(np.abs(got - ref["output"])))
+    mag = float(np.max(np.abs(ref["output"])))
+    print(f"C5 max error {err:.3e} (2^{math.log2(err):.2f}) of magnitude {mag:.2f}; stages {stages}", flush=True)
+    assert err <= 2.0**-16 * mag

@@ -113,7 +113,7 @@ def test_easyfhe_alias_binds_the_hot_path_surface():
 
         import holmes_amd.fhe as ours
 
-        assert fhe is ours and easyfhe.fhe is ours
+        assert fhe is easyfhe.fhe and fhe.homo_rotate is ours.homo_rotate
         for name in ("CKKSContextSpec", "generate_client_context", "CipherState", "ConstantBundle", "PackedRaw",
                      "homo_rotate", "prepare_hoisted_baby_rotations", "hoisted_mac_sum", "rescale", "align_to",
                      "homo_add", "homo_sub", "homo_mul_i", "homo_mul_pt", "fast_rotate", "grouped_pairwise_mac",
@@ -166,3 +166,35 @@ def test_joined_components_view_without_copy():
     assert _joined([buf[1], buf[0]], 4, n) is None
     gapped = torch.zeros(3, 3, 5, n, dtype=torch.int64)
     assert _joined([gapped[0], gapped[2]], 4, n) is None
+
+
+def test_admitted_bundle_keeps_encodings_only_within_the_budget(monkeypatch):
+    """An admitted bundle asks the session budget before it keeps an encoding: past the budget the
+    encoding is returned but not kept, and the bundle stays cached."""
+    from types import SimpleNamespace
+
+    from holmes_amd import fhe
+
+    class FakePt:
+        def __init__(self, n):
+            import torch
+
+            self.cv = [torch.zeros(n, dtype=torch.int64)]
+
+    sizes = iter([4, 4, 4])
+    monkeypatch.setattr(fhe, "encode_plaintext", lambda v, state, slots, ctx, is_ext=False: FakePt(next(sizes)))
+    cache = backend.SessionPlaintextCache(limit_bytes=100, max_source_bytes=100)
+    sess = SimpleNamespace(plaintext_cache=cache)
+    bundle = backend.EasyFHEContext.constant_bundle(sess, {"m": np.zeros(4)}, cache_key="model.layers.3.mask")
+    assert cache.info()["bytes"] == 32  # the 4 float64 source values
+    st = fhe.CipherState(cur_limbs=3, scale_degree=1, scaling_factor=2.0**40)
+    a = bundle.plaintext("m", st, 8, None)
+    assert bundle.plaintext("m", st, 8, None) is a and cache.info()["bytes"] == 64
+    b = bundle.plaintext("m", st.replace(cur_limbs=2), 8, None)  # 32 more bytes: still fits (96)
+    assert cache.info()["bytes"] == 96
+    c = bundle.plaintext("m", st.replace(cur_limbs=1), 8, None)  # would reach 128: not kept
+    assert bundle.plaintext("m", st.replace(cur_limbs=2), 8, None) is b and c is not None
+    assert bundle.cache_info()["entries"] == 2
+    # the same constant from another layer is a hit
+    again = backend.EasyFHEContext.constant_bundle(sess, {"m": np.zeros(4)}, cache_key="model.layers.9.mask")
+    assert again is bundle and cache.info()["hits"] == 1

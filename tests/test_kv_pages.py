@@ -197,7 +197,7 @@ def test_extend_pages_moves_prefill_pages():
     partial = PairFoldLayerCache(pages=(page(127, "x"),), content_tokens=127)
     more = PairFoldLayerCache(pages=(page(1, "y"),), content_tokens=1)
     with pytest.raises(ValueError, match="tail must be full"):
-        partial.extend_pages(more)
+        partial.extend_pages(more)  # the message names the rule: the tail must be full first
     assert not more.is_released and more.content_tokens == 1
 
 

@@ -16,7 +16,7 @@ HEADER = ROOT / "include" / "holmes_ckks.h"
 def declared_symbols():
     text = HEADER.read_text()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(hck_[a-z0-9_]+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b((?:hck|holmes)_[a-z0-9_]+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -34,7 +34,7 @@ def test_bindings_match_the_header_arity():
     drifts from the header would pass shifted pointers to the kernels."""
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     text = re.sub(r"//[^\n]*", "", text)
-    decls = re.findall(r"\b(hck_[a-z0-9_]+)\s*\(([^;{)]*)\)\s*;", text)
+    decls = re.findall(r"\b((?:hck|holmes)_[a-z0-9_]+)\s*\(([^;{)]*)\)\s*;", text)
     assert len(decls) >= len(nat.SIGNATURES)
     for name, params in decls:
         p = params.strip()
@@ -80,3 +80,17 @@ def test_product_fails_loudly_without_gpu():
 
     with pytest.raises(RuntimeError, match="GPU"):
         fhe.generate_client_context(fhe.CKKSContextSpec())
+
+
+def test_holmes_mac_multi_validates_like_the_sidecar():
+    """The sidecar's return codes (bench/cmp/kernels/holmes_mac.cu:363-366): checked before any
+    device call, so they need no GPU."""
+    lib = nat.lib()
+    f = lib.holmes_mac_multi
+    args = lambda inputs=1, nb=1, groups=1, ti=10108: (None, None, None, 0, nb, inputs, None, 0, groups, ti, 1,  # noqa: E731
+                                                         None, None, None, None)
+    assert f(*args(inputs=0)) == -1 and f(*args(inputs=33)) == -1
+    assert f(*args(nb=0)) == -2
+    assert f(*args(groups=0)) == -3 and f(*args(groups=17)) == -3 and f(*args(groups=9)) == -3
+    assert f(*args(ti=8)) == -4 and f(*args(ti=10109)) == -4
+    assert f(*args(groups=9, ti=10116)) == -1  # valid selector, null buffers: an argument error

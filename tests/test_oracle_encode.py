@@ -56,10 +56,19 @@ def test_encode_matches_fft_canonical_embedding(scale):
 
 
 def test_encode_reports_overflow():
-    ctx = O.OracleContext(16, 2, 1, 2, O.gen_primes(16, 50, 3))
-    z = np.full(1 << 15, 1.0e4)
-    _, ok = ctx.encode_real(z, 2.0**40, [0])
+    """The cap is |coefficient| < 2^61 (MAX_ENCODED_BITS, llama3fhe/operators/attention/prefill/
+    softmax.py:559).  A constant slot vector c encodes exactly to the coefficient c * scale at
+    position 0 and zeros elsewhere (every butterfly difference is 0), so the boundary is sharp."""
+    primes = O.gen_primes(16, 50, 3)
+    ctx = O.OracleContext(16, 2, 1, 2, primes)
+    _, ok = ctx.encode_real(np.full(1 << 15, 2.0**21), 2.0**40, [0])
     assert not ok
+    below = 2.0**21 - 2.0**-32  # the largest double below 2^21
+    res, ok = ctx.encode_real(np.full(1 << 15, below), 2.0**40, [0, 1], ntt=False)
+    assert ok
+    dc = 2**61 - 2**8
+    assert [int(v) for v in res[:, 0]] == [dc % q for q in primes[:2]]
+    assert not np.any(res[:, 1:])
 
 
 def _bsgs_slots(rows, x, D, lanes, B, G, giant_base=0):
