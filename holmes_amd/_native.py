@@ -11,6 +11,9 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libholmes_ckks.so"
 
+HCK_ERR_ARG = -1
+HCK_ERR_WORKSPACE = -5
+
 HCK_OP_ADD = 0
 HCK_OP_SUB = 1
 HCK_OP_MUL = 2

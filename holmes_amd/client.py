@@ -1,14 +1,18 @@
 """Client side: secret key, key generation, encrypt / decrypt.
 
-Randomness is drawn on the host from NumPy generators seeded by (spec.seed, purpose) so that a
-context is reproducible; all ring arithmetic (NTTs, products, key assembly) runs on the GPU
-through libholmes_ckks.  Holmes seeds its keys from a fixed Blake2 seed, one PRNG stream per
-rotation (llama3fhe/parallel/prefill/keys.py:49-53); this backend declares its own streams.
+Key material is drawn on the host from NumPy generators seeded by (spec.seed, purpose), so a
+context's keys are reproducible -- for benchmarks and tests only; Holmes seeds its keys from a
+fixed Blake2 seed, one PRNG stream per rotation (llama3fhe/parallel/prefill/keys.py:49-53), and
+this backend declares its own streams.  Encryption randomness (the uniform a and the error e of
+every encryption) is keyed from the operating system's entropy source (a Philox stream per
+encryption), unless the spec asks for deterministic encryption.  All ring arithmetic (NTTs,
+products, key assembly) runs on the GPU through libholmes_ckks.
 """
 
 from __future__ import annotations
 
 import hashlib
+import os
 
 import numpy as np
 import torch
@@ -21,6 +25,12 @@ from .context import Cipher, CipherState, CKKSContext
 def _rng(seed: int, *purpose) -> np.random.Generator:
     tag = hashlib.blake2b(repr((int(seed),) + tuple(purpose)).encode(), digest_size=16).digest()
     return np.random.Generator(np.random.PCG64(int.from_bytes(tag, "little")))
+
+
+def _fresh_rng() -> np.random.Generator:
+    """A generator keyed by 128 bits of OS entropy (a new key per call)."""
+
+    return np.random.Generator(np.random.Philox(key=int.from_bytes(os.urandom(16), "little")))
 
 
 def sample_ternary(rng: np.random.Generator, n: int, dist: str, h: int) -> np.ndarray:
@@ -147,7 +157,10 @@ class Client:
         ctx = self.context
         B = int(pt.shape[0])
         self._enc_counter += 1
-        rng = _rng(ctx.spec.seed, "encrypt", self._enc_counter)
+        if getattr(ctx.spec, "deterministic_encryption", False):
+            rng = _rng(ctx.spec.seed, "encrypt", self._enc_counter)
+        else:
+            rng = _fresh_rng()
         e = sample_gaussian(rng, (B, ctx.N), ctx.spec.error_sigma)
         idx = ctx.q_prime_idx(cur_limbs)
         mpe = ctx.from_signed(torch.from_numpy(e).to(ctx.device), idx)

@@ -550,7 +550,12 @@ class CKKSContext:
         self._check_poly(x, limbs, self.N)
         if limbs < 2:
             raise ValueError("rescale needs at least two limbs")
-        out = self.empty(x.shape[0], limbs - 1, self.N) if out is None else out
+        if out is None:
+            out = self.empty(x.shape[0], limbs - 1, self.N)
+        else:
+            self._check_poly(out, limbs - 1, self.N)
+            if out.shape[0] != x.shape[0]:
+                raise ValueError(f"out holds {out.shape[0]} polys for {x.shape[0]} inputs")
         L = nat.lib()
         ws = self.workspace(L.hck_rescale_workspace_bytes(self._h, limbs, x.shape[0]))
         nat.check(L.hck_rescale(self._h, limbs, x.shape[0], x.data_ptr(), _bstride(x), out.data_ptr(),

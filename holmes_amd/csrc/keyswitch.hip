@@ -167,6 +167,16 @@ extern "C" int hck_rescale(const hck_context* ctx, int level_limbs, int polys, c
   if (!ctx || !in || !out || polys < 0 || polys > 65535) return HCK_ERR_ARG;
   if (level_limbs < 2 || level_limbs > ctx->L) return HCK_ERR_ARG;
   if (polys == 0) return HCK_OK;
+  const int64_t n = hck::kN;
+  if (polys > 1 && (in_stride < level_limbs * n || out_stride < (level_limbs - 1) * n)) return HCK_ERR_ARG;
+  // The finish kernel reads in[p][i] and writes out[p][i] in the same thread: in place is safe with
+  // equal strides; any other overlap lets one poly's output overwrite input another block still reads.
+  {
+    const uint64_t* in_end = in + (int64_t)(polys - 1) * in_stride + level_limbs * n;
+    const uint64_t* out_end = out + (int64_t)(polys - 1) * out_stride + (level_limbs - 1) * n;
+    const bool overlap = in < out_end && out < in_end;
+    if (overlap && !(in == out && in_stride == out_stride)) return HCK_ERR_ARG;
+  }
   if (!workspace || workspace_bytes < hck::rescale_bytes(ctx, level_limbs, polys)) return HCK_ERR_WORKSPACE;
   return hck::rescale_fused(ctx, level_limbs, polys, in, in_stride, out, out_stride, (char*)workspace,
                             (hipStream_t)stream);

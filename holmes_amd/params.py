@@ -76,6 +76,12 @@ class CKKSContextSpec:
     seed: int = 20261201
     hamming_weight: int = 192
     error_sigma: float = 3.2
+    # Key material (secret, key-switching keys) is generated from ``seed`` so that a context is
+    # reproducible (the reference seeds its keys the same way, parallel/prefill/keys.py:49-53).
+    # Encryption randomness (a, e) comes from the OS entropy source unless this is set: two
+    # clients of one spec must not encrypt with the same (a, e).  Tests that need repeatable
+    # ciphertexts set it.
+    deterministic_encryption: bool = False
 
     @property
     def num_q(self) -> int:

@@ -1,24 +1,26 @@
 """Ciphertext wire format.
 
-The packet surface follows llama3fhe/parallel/wire.py (CipherMetadata, CipherPacket,
-cipher_metadata, validate_cipher, rebuild_cipher, pack_cipher, unpack_cipher; lines 1-383): the
-metadata records every component's full shape, dtype and device plus the state (cur_limbs,
-scale_degree, scaling_factor) and the encoding contract (slots, batch_size, is_ext); packing stages
-the components on the host as NumPy arrays (or keeps the device tensors by reference,
-``host=False``); unpacking rebuilds on a device and refuses a packet whose metadata changed.
+The packet surface keeps the names and contract of llama3fhe/parallel/wire.py (CipherMetadata,
+CipherPacket, cipher_metadata, validate_cipher, rebuild_cipher, pack_cipher, unpack_cipher;
+lines 1-383): metadata = every component's full shape, dtype and device, the state (cur_limbs,
+scale_degree, scaling_factor) and the encoding (slots, batch_size, is_ext); a packet holds host
+NumPy copies (or, ``host=False``, the device tensors themselves); unpacking places fresh tensors
+on a device and refuses a result whose metadata differs from what was sent.
 
 This backend adds one contiguous byte layout for a ciphertext, the same on the host and in HBM:
 
     header (64 bytes, little endian)
-      0  magic b"HCKW"         4  version u16        6  flags u16 (1: is_ext, 2: checksum valid)
-      8  components u16       10  limbs sent u16    12  log_n u8, 13 zero, 14 tag bytes u16
-      16 batch u32            20  slots u32          24 scale_degree u32, 4 bytes zero
+      0  magic b"HCKW"         4  version u16 (2)    6  flags u16 (1: is_ext, 2: checksum valid)
+      8  components u16       10  rows sent u16     12  cur_limbs u16     14 tag bytes u16
+      16 batch u32            20  slots u32          24 scale_degree u32   28 log_n u8, 3 zero
       32 scaling_factor f64   40  prime-chain fingerprint u64 (0: none)
       48 payload bytes u64    56  xxh64 of the payload (0 without flag 2)
     tag (utf-8, zero-padded to a multiple of 8 bytes)
-    payload: component c, item b, limb l < limbs sent: N uint64 residues, in that order
+    payload: component c, item b, row r < rows sent: N uint64 residues, in that order
 
-Only the active limbs travel (a ciphertext at 9 of 24 stored limbs sends 9).  ``device_pack``
+Only the active rows travel: cur_limbs rows of a ciphertext in the Q basis (a ciphertext at 9 of
+24 stored limbs sends 9), every stored row (cur_limbs Q limbs + the special-prime limbs) of an
+extended-basis one; the header keeps the row count and cur_limbs apart.  ``device_pack``
 assembles the layout in one HBM buffer (one strided copy per component) so a batch of ciphertexts
 crosses a link or PCIe as a single message; ``device_unpack`` rebuilds fresh component tensors
 from it.  ``serialize`` / ``deserialize`` are the host forms with the payload checksum; the
@@ -53,44 +55,55 @@ __all__ = [
     "wire_tag",
 ]
 
-_ELEMENT_BYTES = {"uint64": 8, "int64": 8, "float64": 8, "complex128": 16, "uint32": 4, "int32": 4,
-                  "float32": 4, "complex64": 8, "uint16": 2, "int16": 2, "float16": 2, "bfloat16": 2,
-                  "uint8": 1, "int8": 1, "bool": 1}
-
-
 class WireError(ValueError):
     """Malformed, corrupted or incompatible wire bytes."""
 
 
 # ---------------------------------------------------------------------------- metadata / packets
-def _components(cipher) -> tuple:
+def _itemsize(dtype) -> int | None:
+    """Bytes per element of a torch or NumPy dtype (or its string form), None if unknown."""
+
+    if dtype is None:
+        return None
+    name = str(dtype).rsplit(".", 1)[-1]
+    tdt = getattr(torch, name, None)
+    if isinstance(tdt, torch.dtype):
+        return int(tdt.itemsize)
+    try:
+        return int(np.dtype(name).itemsize)
+    except TypeError:
+        return None
+
+
+def _describe(component) -> tuple:
+    """(shape, dtype string or None, device string or None) of one component."""
+
+    shape = getattr(component, "shape", None)
+    try:
+        shape = () if shape is None else tuple(int(d) for d in shape)
+    except (TypeError, ValueError) as exc:
+        raise TypeError(f"a ciphertext component reports an unusable shape {shape!r}") from exc
+    dtype = getattr(component, "dtype", None)
+    device = getattr(component, "device", None)
+    return shape, None if dtype is None else str(dtype), (str(device) or None) if device is not None else None
+
+
+def _component_list(cipher) -> tuple:
     cv = getattr(cipher, "cv", None)
     if cv is None:
-        raise TypeError("cipher must expose a non-empty cv component sequence")
-    if hasattr(cv, "dim"):
-        cv = (cv,)
-    try:
-        cv = tuple(cv)
-    except TypeError as exc:
-        raise TypeError("cipher.cv must be iterable") from exc
-    if not cv:
-        raise ValueError("cipher.cv must not be empty")
-    return cv
-
-
-def _shape(x) -> tuple:
-    s = getattr(x, "shape", None)
-    if s is None:
-        return ()
-    try:
-        return tuple(int(e) for e in s)
-    except (TypeError, ValueError) as exc:
-        raise TypeError(f"cipher component has invalid shape {s!r}") from exc
+        raise TypeError(f"{type(cipher).__name__} has no cv component list")
+    items = (cv,) if hasattr(cv, "dim") else tuple(cv) if isinstance(cv, (list, tuple)) else None
+    if items is None:
+        raise TypeError("cipher.cv is neither a tensor nor a list / tuple of components")
+    if not items:
+        raise ValueError("cipher.cv holds no component")
+    return items
 
 
 @dataclass(frozen=True)
 class CipherMetadata:
-    """Everything but the residues; shapes include the allocated limb capacity."""
+    """A ciphertext without its residues: per-component shape (allocated limb capacity included),
+    dtype and device; the state (cur_limbs, scale_degree, scaling_factor); slots, batch, basis."""
 
     component_shapes: tuple
     component_dtypes: tuple
@@ -108,111 +121,113 @@ class CipherMetadata:
 
     @property
     def device(self) -> str | None:
-        devs = {d for d in self.component_devices if d is not None}
-        return next(iter(devs)) if len(devs) == 1 else None
+        named = set(filter(None, self.component_devices))
+        return named.pop() if len(named) == 1 else None
 
     @property
     def nbytes(self) -> int:
         total = 0
         for shape, dtype in zip(self.component_shapes, self.component_dtypes):
-            if dtype is None:
-                continue
-            eb = _ELEMENT_BYTES.get(str(dtype).removeprefix("torch."))
-            if eb is not None:
-                total += int(np.prod(shape, dtype=np.int64)) * eb if shape else eb
-        return int(total)
+            size = _itemsize(dtype)
+            if size:
+                total += size * int(np.prod(shape, dtype=np.int64))
+        return total
 
     def without_devices(self) -> tuple:
+        """Everything a transport must preserve (the device may legitimately change)."""
+
         return (self.component_shapes, self.component_dtypes, self.cur_limbs, self.scale_degree,
                 self.scaling_factor, self.slots, self.batch_size, self.is_ext)
 
 
 def cipher_metadata(cipher) -> CipherMetadata:
-    cv = _components(cipher)
+    comps = _component_list(cipher)
     state = getattr(cipher, "state", None)
-    if state is None:
-        raise TypeError("cipher must expose state metadata")
     try:
-        cur, deg = int(state.cur_limbs), int(state.scale_degree)
+        limbs, degree = int(state.cur_limbs), int(state.scale_degree)
     except (AttributeError, TypeError, ValueError) as exc:
-        raise TypeError("cipher.state must expose integer limb/scale fields") from exc
-    if cur <= 0 or deg <= 0:
-        raise ValueError(f"cipher state must be positive, got cur_limbs={cur}, scale_degree={deg}")
-    sf = getattr(state, "scaling_factor", None)
-    slots = int(getattr(cipher, "slots"))
-    batch = int(getattr(cipher, "batch_size", 1))
-    if slots <= 0 or batch <= 0:
-        raise ValueError(f"slots/batch_size must be positive, got {slots}/{batch}")
-    return CipherMetadata(
-        component_shapes=tuple(_shape(c) for c in cv),
-        component_dtypes=tuple(None if getattr(c, "dtype", None) is None else str(c.dtype) for c in cv),
-        component_devices=tuple(None if getattr(c, "device", None) is None or not str(c.device) else str(c.device)
-                                for c in cv),
-        cur_limbs=cur, scale_degree=deg, scaling_factor=None if sf is None else float(sf), slots=slots,
-        batch_size=batch, is_ext=bool(getattr(cipher, "is_ext", False)))
+        raise TypeError("cipher.state needs integer cur_limbs and scale_degree") from exc
+    slots, batch = int(getattr(cipher, "slots")), int(getattr(cipher, "batch_size", 1))
+    if min(limbs, degree, slots, batch) < 1:
+        raise ValueError(f"cur_limbs {limbs}, scale_degree {degree}, slots {slots} and batch_size {batch} "
+                         "must all be positive")
+    scale = getattr(state, "scaling_factor", None)
+    shapes, dtypes, devices = zip(*map(_describe, comps))
+    return CipherMetadata(component_shapes=tuple(shapes), component_dtypes=tuple(dtypes),
+                          component_devices=tuple(devices), cur_limbs=limbs, scale_degree=degree,
+                          scaling_factor=None if scale is None else float(scale), slots=slots, batch_size=batch,
+                          is_ext=bool(getattr(cipher, "is_ext", False)))
+
+
+def _same_device(have: str, want: str) -> bool:
+    """Equal device names, where a bare "cuda" matches any "cuda:<i>"."""
+
+    if have == want:
+        return True
+    return "cuda" in (have, want) and have.startswith("cuda") and want.startswith("cuda")
 
 
 def validate_cipher(cipher, *, expected_device: str | None = None) -> CipherMetadata:
+    """Metadata of ``cipher`` after the checks a transport relies on: one device (``expected_device``
+    when given), batch_size equal to every component's leading extent, cur_limbs within capacity."""
+
     md = cipher_metadata(cipher)
-    devs = {d for d in md.component_devices if d is not None}
-    if len(devs) > 1:
-        raise ValueError(f"cipher components span multiple devices: {sorted(devs)}")
-    if expected_device is not None and md.device is not None:
-        want, got = str(expected_device), md.device
-        if not (got == want or (want == "cuda" and got.startswith("cuda")) or (got == "cuda" and want.startswith("cuda"))):
-            raise ValueError(f"cipher device {got!r} does not match {want!r}")
+    named = sorted(set(filter(None, md.component_devices)))
+    if len(named) > 1:
+        raise ValueError(f"components live on multiple devices {named}; a packet needs one")
+    if expected_device is not None and md.device is not None and not _same_device(md.device, str(expected_device)):
+        raise ValueError(f"components are on {md.device!r}, which does not match {str(expected_device)!r}")
     for shape in md.component_shapes:
-        if shape and md.batch_size != shape[0]:
-            raise ValueError(f"cipher batch_size does not match component shape: {md.batch_size} vs {shape[0]}")
-        if len(shape) >= 2 and md.cur_limbs > shape[-2]:
-            raise ValueError(f"cipher cur_limbs={md.cur_limbs} exceeds component capacity {shape[-2]}")
+        if shape and shape[0] != md.batch_size:
+            raise ValueError(f"batch_size {md.batch_size} disagrees with a component's leading extent {shape[0]}")
+        if len(shape) > 1 and shape[-2] < md.cur_limbs:
+            raise ValueError(f"cur_limbs {md.cur_limbs} is above the component's limb capacity {shape[-2]}")
     return md
 
 
 def rebuild_cipher(template, components: Iterable):
-    """``template``'s state and encoding around ``components`` (template unchanged)."""
+    """A ciphertext with ``template``'s state and encoding around ``components`` (template kept)."""
 
-    components = list(components)
-    like = getattr(template, "cipher_like", None)
-    if callable(like):
-        return like(components)
+    comps = list(components)
+    maker = getattr(template, "cipher_like", None)
+    if callable(maker):
+        return maker(comps)
+    from .context import Cipher
+
     try:
-        from .context import Cipher
-
-        return Cipher(components, template.state, slots=int(template.slots), is_ext=bool(getattr(template, "is_ext", False)),
+        return Cipher(comps, template.state, slots=int(template.slots), is_ext=bool(getattr(template, "is_ext", False)),
                       batch_size=int(getattr(template, "batch_size", 1)))
-    except (AttributeError, TypeError, ValueError):  # a foreign cipher type without these fields
-        clone = copy.copy(template)
-        clone.cv = components
-        return clone
+    except (AttributeError, TypeError, ValueError):
+        other = copy.copy(template)  # a ciphertext type of another backend: keep its class
+        other.cv = comps
+        return other
 
 
-def _to_host(c):
-    if isinstance(c, np.ndarray):
-        return np.array(c, copy=True)
-    if callable(getattr(c, "numpy", None)):
-        h = c.cpu() if callable(getattr(c, "cpu", None)) else c
-        h = h.detach() if callable(getattr(h, "detach", None)) else h
-        return np.array(h.numpy(), copy=True)
-    return c.clone() if callable(getattr(c, "clone", None)) else c
+def _host_copy(component):
+    """A host NumPy copy of a tensor (any device), or an independent copy of anything else."""
+
+    if isinstance(component, torch.Tensor):
+        return component.detach().cpu().numpy().copy()
+    if isinstance(component, np.ndarray):
+        return component.copy()
+    return component.clone() if callable(getattr(component, "clone", None)) else component
 
 
-def _to_device(c, device: str):
-    if isinstance(c, np.ndarray):
-        t = torch.from_numpy(np.ascontiguousarray(c))
-        return t.to(device) if str(device) != "cpu" else t.clone()
-    to = getattr(c, "to", None)
-    if callable(to):
-        moved = to(str(device))
-        if moved is c and callable(getattr(c, "clone", None)):
-            moved = c.clone()
-        return moved
-    return c
+def _placed(component, device: str):
+    """``component`` as a tensor on ``device`` that shares no storage with the original."""
+
+    if isinstance(component, np.ndarray):
+        fresh = torch.from_numpy(np.ascontiguousarray(component).copy())
+        return fresh if str(device) == "cpu" else fresh.to(device)
+    if isinstance(component, torch.Tensor):
+        moved = component.to(str(device))
+        return moved.clone() if moved.data_ptr() == component.data_ptr() else moved
+    return component
 
 
 @dataclass
 class CipherPacket:
-    """A ciphertext staged for a transport: metadata, components, a routing tag, the state."""
+    """A ciphertext staged for a transport: metadata, components, a routing tag and the state."""
 
     metadata: CipherMetadata
     components: tuple
@@ -224,53 +239,56 @@ class CipherPacket:
         return self.metadata.nbytes
 
     def validate(self) -> None:
-        if len(self.components) != self.metadata.component_count:
-            raise ValueError("packet component count does not match metadata")
-        for c, shape in zip(self.components, self.metadata.component_shapes):
-            if _shape(c) != shape:
-                raise ValueError("packet component shape does not match metadata")
+        want = self.metadata.component_shapes
+        if len(self.components) != len(want):
+            raise ValueError(f"packet carries {len(self.components)} components, metadata lists {len(want)}")
+        got = tuple(_describe(c)[0] for c in self.components)
+        if got != want:
+            raise ValueError(f"packet component shape {got} does not match metadata {want}")
 
 
 def pack_cipher(cipher, *, tag: str = "", host: bool = True) -> CipherPacket:
-    """Metadata + components (host NumPy copies, or the device tensors by reference with
-    ``host=False``); ``cipher`` is not consumed."""
+    """A packet of ``cipher`` (not consumed): host NumPy copies of the components, or with
+    ``host=False`` the device tensors themselves."""
 
     md = validate_cipher(cipher)
-    comps = tuple(_to_host(c) for c in _components(cipher)) if host else tuple(_components(cipher))
-    pkt = CipherPacket(metadata=md, components=comps, tag=str(tag), state=getattr(cipher, "state", None))
-    pkt.validate()
-    return pkt
+    comps = _component_list(cipher)
+    packet = CipherPacket(metadata=md, components=tuple(map(_host_copy, comps)) if host else comps, tag=str(tag),
+                          state=getattr(cipher, "state", None))
+    packet.validate()
+    return packet
 
 
-class _Template:
-    def __init__(self, pkt: CipherPacket):
-        self.state = pkt.state
-        self.slots = int(pkt.metadata.slots)
-        self.is_ext = bool(pkt.metadata.is_ext)
-        self.batch_size = int(pkt.metadata.batch_size)
+class _PacketTemplate:
+    """What rebuild_cipher needs from a template, taken from a packet."""
+
+    def __init__(self, packet: CipherPacket) -> None:
+        md = packet.metadata
+        self.state, self.slots, self.is_ext, self.batch_size = packet.state, md.slots, md.is_ext, md.batch_size
         self.cv: list = []
 
 
 def unpack_cipher(packet: CipherPacket, *, device: str = "cuda", template=None):
-    """The cipher rebuilt on ``device`` (components never alias the sender's); refuses a packet
-    whose metadata does not survive the trip."""
+    """The packet's ciphertext on ``device`` (its components never share storage with the sender's).
+    Without a ``template`` the packet's own state is used.  A result whose metadata differs from
+    the packet's (apart from the device) is refused."""
 
     packet.validate()
-    comps = tuple(_to_device(c, str(device)) for c in packet.components)
     if template is None and packet.state is None:
-        raise ValueError("packet has no state; pass a template cipher")
-    out = rebuild_cipher(template if template is not None else _Template(packet), comps)
-    after = validate_cipher(out, expected_device=str(device))
-    if after.without_devices() != packet.metadata.without_devices():
-        raise RuntimeError(f"cipher metadata changed during transport: sent={packet.metadata.without_devices()!r} "
-                           f"got={after.without_devices()!r}")
-    return out
+        raise ValueError("the packet carries no state; pass a template ciphertext")
+    comps = [_placed(c, str(device)) for c in packet.components]
+    result = rebuild_cipher(template if template is not None else _PacketTemplate(packet), comps)
+    arrived = validate_cipher(result, expected_device=str(device)).without_devices()
+    sent = packet.metadata.without_devices()
+    if arrived != sent:
+        raise RuntimeError(f"the ciphertext arrived with other metadata than it was sent with: {sent!r} -> {arrived!r}")
+    return result
 
 
 # ---------------------------------------------------------------------------- binary layout
 _MAGIC = b"HCKW"
-_VERSION = 1
-_HDR = struct.Struct("<4sHHHHB3xIII4xdQQQ")  # 64 bytes
+_VERSION = 2
+_HDR = struct.Struct("<4sHHHHHHIIIB3xdQQQ")  # 64 bytes
 assert _HDR.size == 64
 _F_EXT, _F_SUM = 1, 2
 
@@ -295,40 +313,42 @@ def _tag_bytes(tag: str) -> bytes:
     return t + b"\0" * (-len(t) % 8)
 
 
-def _header(md: CipherMetadata, log_n: int, fingerprint: int, payload_bytes: int, checksum: int | None, tag: bytes,
-            tag_len: int) -> bytes:
+def _header(md: CipherMetadata, rows: int, log_n: int, fingerprint: int, payload_bytes: int, checksum: int | None,
+            tag: bytes, tag_len: int) -> bytes:
     if md.scaling_factor is None:
         raise ValueError("the wire format needs a scaling factor")
+    if max(rows, md.cur_limbs, md.component_count, tag_len) > 0xFFFF:
+        raise ValueError("rows, cur_limbs, components and tag length must each fit 16 bits")
     flags = (_F_EXT if md.is_ext else 0) | (_F_SUM if checksum is not None else 0)
-    h = _HDR.pack(_MAGIC, _VERSION, flags, md.component_count, md.cur_limbs, int(log_n), md.batch_size, md.slots,
-                  md.scale_degree, md.scaling_factor, int(fingerprint), int(payload_bytes), int(checksum or 0))
-    # the tag length rides in bytes 14-15 (unused by the struct's padding after log_n)
-    return h[:13] + b"\0" + struct.pack("<H", tag_len) + h[16:] + tag
+    return _HDR.pack(_MAGIC, _VERSION, flags, md.component_count, int(rows), md.cur_limbs, int(tag_len),
+                     md.batch_size, md.slots, md.scale_degree, int(log_n), md.scaling_factor, int(fingerprint),
+                     int(payload_bytes), int(checksum or 0)) + tag
 
 
 def _parse(buf: bytes) -> dict:
     if len(buf) < _HDR.size:
         raise WireError("buffer shorter than the wire header")
-    magic, ver, flags, comps, rows, log_n, batch, slots, deg, sf, fp, nbytes, chk = _HDR.unpack(
+    magic, ver, flags, comps, rows, limbs, tag_len, batch, slots, deg, log_n, sf, fp, nbytes, chk = _HDR.unpack(
         bytes(buf[:_HDR.size]))
     if magic != _MAGIC:
         raise WireError("not a ciphertext wire buffer (bad magic)")
     if ver != _VERSION:
         raise WireError(f"unsupported wire version {ver}")
-    tag_len = struct.unpack("<H", bytes(buf[14:16]))[0]
+    if not 0 < limbs <= rows or log_n > 20:
+        raise WireError(f"header holds {rows} rows for {limbs} limbs at log N {log_n}")
     n = 1 << log_n
     if nbytes != comps * batch * rows * n * 8:
         raise WireError("payload size does not match the header")
-    return dict(flags=flags, comps=comps, rows=rows, n=n, batch=batch, slots=slots, deg=deg, sf=sf, fp=fp,
-                nbytes=nbytes, chk=chk, tag_len=tag_len, tag_pad=tag_len + (-tag_len % 8))
+    return dict(flags=flags, comps=comps, rows=rows, limbs=limbs, n=n, batch=batch, slots=slots, deg=deg, sf=sf,
+                fp=fp, nbytes=nbytes, chk=chk, tag_len=tag_len, tag_pad=tag_len + (-tag_len % 8))
 
 
 def _active(cipher):
-    """(metadata, the active-limb views of the components, limbs sent)."""
+    """(metadata, the views of the rows that travel, rows sent)."""
 
     md = validate_cipher(cipher)
     rows = md.cur_limbs if not md.is_ext else int(md.component_shapes[0][-2])
-    return md, [c[:, :rows] for c in _components(cipher)], rows
+    return md, [c[:, :rows] for c in _component_list(cipher)], rows
 
 
 def serialize(cipher, *, tag: str = "", primes=None, log_n: int | None = None, checksum: bool = True) -> bytes:
@@ -349,16 +369,16 @@ def serialize(cipher, *, tag: str = "", primes=None, log_n: int | None = None, c
         pos += k
     payload = memoryview(out)[lead:]
     fp = chain_fingerprint(primes) if primes is not None else 0
-    head = _header(md, log_n, fp, len(payload), _checksum(payload) if checksum else None, tb,
+    head = _header(md, rows, log_n, fp, len(payload), _checksum(payload) if checksum else None, tb,
                    len(str(tag).encode()))
     out[:lead] = head
     return bytes(out)
 
 
-def _state_for(hdr, rows):
+def _state_for(hdr):
     from .context import CipherState
 
-    return CipherState(cur_limbs=rows, scale_degree=hdr["deg"], scaling_factor=hdr["sf"])
+    return CipherState(cur_limbs=hdr["limbs"], scale_degree=hdr["deg"], scaling_factor=hdr["sf"])
 
 
 def deserialize(buf, *, device: str = "cuda", primes=None):
@@ -378,9 +398,8 @@ def deserialize(buf, *, device: str = "cuda", primes=None):
     if h["flags"] & _F_SUM and _checksum(payload) != h["chk"]:
         raise WireError("payload checksum mismatch")
     arr = np.frombuffer(payload, dtype="<u8").reshape(h["comps"], h["batch"], h["rows"], h["n"])
-    cv = [_to_device(np.array(arr[c]), device) for c in range(h["comps"])]
-    return Cipher(cv, _state_for(h, h["rows"]), slots=h["slots"], is_ext=bool(h["flags"] & _F_EXT),
-                  batch_size=h["batch"])
+    cv = [_placed(arr[c], device) for c in range(h["comps"])]
+    return Cipher(cv, _state_for(h), slots=h["slots"], is_ext=bool(h["flags"] & _F_EXT), batch_size=h["batch"])
 
 
 def wire_tag(buf) -> str:
@@ -406,7 +425,7 @@ def device_pack(ciphers, *, tags=None, primes=None, out: torch.Tensor | None = N
         md, comps, rows = _active(ct)
         n = int(comps[0].shape[-1])
         nb = sum(int(c.numel()) for c in comps) * 8
-        hdr = _header(md, n.bit_length() - 1, fp, nb, None, _tag_bytes(tag), len(tag.encode()))
+        hdr = _header(md, rows, n.bit_length() - 1, fp, nb, None, _tag_bytes(tag), len(tag.encode()))
         parts.append((hdr, comps, nb))
         total += len(hdr) + nb
     dev = ciphers[0].cv[0].device
@@ -452,6 +471,6 @@ def device_unpack(buf: torch.Tensor, *, primes=None, count: int | None = None) -
         for _ in range(h["comps"]):
             cv.append(buf[pos:pos + step].view(torch.int64).view(shape).clone().view(torch.uint64))
             pos += step
-        out.append(Cipher(cv, _state_for(h, h["rows"]), slots=h["slots"], is_ext=bool(h["flags"] & _F_EXT),
+        out.append(Cipher(cv, _state_for(h), slots=h["slots"], is_ext=bool(h["flags"] & _F_EXT),
                           batch_size=h["batch"]))
     return out

@@ -127,3 +127,20 @@ def test_easyfhe_context_session_roundtrip():
     assert np.max(np.abs(rot.real - np.roll(v, -3))) < TOL
     backend.release_if_supported(prod)
     assert prod.cv == []
+
+
+def test_encryption_randomness_is_fresh_unless_deterministic():
+    """Two clients of one spec (same keys) must not reuse (a, e): c0 - c0' would reveal m - m'.
+    With deterministic_encryption the n-th encryptions coincide, for reproducible tests."""
+    from holmes_amd import fhe
+
+    v = np.linspace(-1.0, 1.0, 1 << 15)
+    outs = []
+    for det in (False, False, True, True):
+        client, ctx = fhe.generate_client_context(fhe.CKKSContextSpec(depth=3, dnum=2, seed=99,
+                                                                      deterministic_encryption=det))
+        ct = client.encrypt(v, cur_limbs=2)
+        assert np.max(np.abs(client.decrypt(ct).real - v)) < 2.0**-20
+        outs.append(ct.cv[1].cpu().numpy())
+    assert not np.array_equal(outs[0], outs[1])
+    assert np.array_equal(outs[2], outs[3])

@@ -264,6 +264,36 @@ def test_rescale(env, ell):
         assert np.array_equal(out[b], orc.rescale(ell, x[b]))
 
 
+def test_rescale_in_place_and_rejected_overlaps(env):
+    """In place with equal strides is exact; an out buffer that overlaps the input at another
+    stride, or strides below one poly, is an argument error (nothing launched), and a short out
+    tensor is refused on the host."""
+    from holmes_amd import _native as nat
+
+    _, _, ctx, orc = env
+    ell, polys = 6, 3
+    rng = np.random.default_rng(46)
+    x = _rand(ctx, rng, polys, ell)
+    buf = _dev(x)
+    want = [orc.rescale(ell, x[b]) for b in range(polys)]
+    got = _host(ctx.rescale_raw(buf, ell, out=buf))  # same strides: in place
+    for b in range(polys):
+        assert np.array_equal(got[b, :ell - 1], want[b])
+    L = nat.lib()
+    n = ctx.N
+    ws = ctx.workspace(L.hck_rescale_workspace_bytes(ctx.handle, ell, polys))
+    base = buf.data_ptr()
+    stream = torch.cuda.current_stream().cuda_stream
+    # out packed at (ell - 1) limbs per poly over an input with ell limbs per poly: overlapping
+    assert L.hck_rescale(ctx.handle, ell, polys, base, ell * n, base, (ell - 1) * n, ws.data_ptr(), ws.numel(),
+                         stream) == nat.HCK_ERR_ARG
+    other = ctx.empty(polys, ell, n)
+    assert L.hck_rescale(ctx.handle, ell, polys, base, (ell - 1) * n, other.data_ptr(), ell * n, ws.data_ptr(),
+                         ws.numel(), stream) == nat.HCK_ERR_ARG  # input stride below one poly
+    with pytest.raises(ValueError):
+        ctx.rescale_raw(buf, ell, out=ctx.empty(polys - 1, ell - 1, n))
+
+
 def test_batched_keyswitch_sixteen_keys(env):
     """Config C2 shape: 16 ciphertexts at 24 limbs, 16 distinct rotation keys (steps 1..16)."""
 

@@ -133,3 +133,26 @@ def test_buffer_form_holds_several_ciphertexts():
     assert wire.deserialize(one.numpy().tobytes(), device="cpu").state.cur_limbs == 3
     out = torch.empty(one.numel() + 64, dtype=torch.uint8)
     assert torch.equal(wire.device_pack(cts[0], out=out), one)
+
+
+@pytest.mark.parametrize("form", ["bytes", "buffer"])
+def test_extended_basis_ciphers_keep_rows_and_limbs_apart(form):
+    """An extended-basis ciphertext stores cur_limbs Q limbs plus the special-prime limbs: all of its
+    rows travel, and the receiver gets cur_limbs back from the header, not the row count."""
+    ct = _cipher(batch=2, rows=5, limbs=3, seed=11, is_ext=True)  # 3 Q limbs + 2 special limbs
+    if form == "bytes":
+        buf = wire.serialize(ct, primes=[97, 193])
+        assert len(buf) == 64 + 2 * 2 * 5 * N * 8
+        back = wire.deserialize(buf, device="cpu", primes=[97, 193])
+    else:
+        (back,) = wire.device_unpack(wire.device_pack(ct, primes=[97, 193]), primes=[97, 193])
+    assert back.is_ext and back.state.cur_limbs == 3 and back.batch_size == 2
+    for a, b in zip(back.cv, ct.cv):
+        assert a.shape == (2, 5, N) and torch.equal(a, b)
+
+
+def test_header_rejects_more_limbs_than_rows():
+    buf = bytearray(wire.serialize(_cipher(rows=5, limbs=3, seed=12)))
+    buf[12:14] = (4).to_bytes(2, "little")  # cur_limbs 4 > the 3 rows sent
+    with pytest.raises(wire.WireError, match="rows"):
+        wire.deserialize(bytes(buf), device="cpu")
