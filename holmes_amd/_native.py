@@ -13,6 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libholmes_ckks.so"
 
 HCK_ERR_ARG = -1
 HCK_ERR_WORKSPACE = -5
+HCK_ERR_SCRATCH = -6
 
 HCK_OP_ADD = 0
 HCK_OP_SUB = 1
@@ -55,6 +56,9 @@ SIGNATURES = {
                           _vp]),
     "holmes_mac_multi": (_i, [_vp, _vp, _vp, ctypes.c_longlong, _i, _i, _vp, ctypes.c_longlong, _i, _i, _i, _vp, _vp,
                               _vp, _vp]),
+    "hck_rotate_noalloc": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp,
+                                _i64, _vp]),
+    "hck_rotate_noalloc_limit": (_sz, [_vp, _i]),
     "hck_rotate_ext": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp, _i64,
                             _vp, _sz, _vp]),
     "hck_rotate_many": (_i, [_vp, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp,

@@ -320,6 +320,8 @@ extern "C" const char* hck_error_string(int code) {
     case HCK_ERR_PRIME: return "prime rejected (needs p < 2^50, p = 1 mod 2N, prime, distinct, within a factor 2 of the others)";
     case HCK_ERR_ALLOC: return "host allocation failed";
     case HCK_ERR_WORKSPACE: return "workspace too small";
+    case HCK_ERR_SCRATCH:
+      return "request exceeds the fixed scratch of the no-allocation entry point (HCK_NOALLOC_SCRATCH_BYTES)";
     default: return code > 0 ? hipGetErrorString((hipError_t)code) : "unknown error";
   }
 }

@@ -116,6 +116,13 @@ size_t modraise_bytes(const hck_context* c, int to, int polys);
 int modraise_fused(const hck_context* c, int to, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                    long long out_stride, char* ws, hipStream_t s);
 
+// The rotation entry points' common body (keyswitch.hip): argument checks, then the fused key switch
+// in launches of at most 64 items; `workspace` must hold ks_fused_bytes(ctx, level_limbs, min(batch, 64)).
+int rotate_impl(const hck_context* ctx, int level_limbs, int batch, uint32_t galois, const uint32_t* galois_items,
+                const uint64_t* c0, const uint64_t* c1, int64_t in_stride, const uint64_t* const* ksk,
+                const uint64_t* acc0, const uint64_t* acc1, int64_t acc_stride, uint64_t* out0, uint64_t* out1,
+                int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream, bool ext);
+
 // MI355X deals consecutive workgroups to its 8 XCDs (each with its own L2) round-robin.
 constexpr int kXcds = 8;
 

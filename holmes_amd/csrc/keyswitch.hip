@@ -47,8 +47,10 @@ namespace {
 
 bool galois_ok(uint32_t g) { return (g & 1u) != 0 && g < 2u * hck::kN; }
 
+}  // namespace
+
 // Rotation of every item b by galois (or galois_items[b]), plain or ending in the extended basis.
-int rotate_impl(const hck_context* ctx, int level_limbs, int batch, uint32_t galois, const uint32_t* galois_items,
+int hck::rotate_impl(const hck_context* ctx, int level_limbs, int batch, uint32_t galois, const uint32_t* galois_items,
                 const uint64_t* c0, const uint64_t* c1, int64_t in_stride, const uint64_t* const* ksk,
                 const uint64_t* acc0, const uint64_t* acc1, int64_t acc_stride, uint64_t* out0, uint64_t* out1,
                 int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream, bool ext) {
@@ -96,7 +98,7 @@ int rotate_impl(const hck_context* ctx, int level_limbs, int batch, uint32_t gal
   return HCK_OK;
 }
 
-}  // namespace
+using hck::rotate_impl;
 
 extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
                           const uint64_t* c0, const uint64_t* c1, int64_t in_stride,

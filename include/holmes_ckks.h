@@ -49,6 +49,10 @@ extern "C" {
 #define HCK_ERR_PRIME (-3)
 #define HCK_ERR_ALLOC (-4)
 #define HCK_ERR_WORKSPACE (-5)
+#define HCK_ERR_SCRATCH (-6)
+
+/* Bytes of the device array behind hck_rotate_noalloc (one copy per GPU, held until exit). */
+#define HCK_NOALLOC_SCRATCH_BYTES (128ull << 20)
 
 typedef struct hck_context hck_context;
 
@@ -101,6 +105,22 @@ int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galo
                const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
                int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/* hck_rotate without a workspace argument, for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference: it exists for those callers only.  Same arguments and results as hck_rotate; the
+ * key-switch workspace is a fixed device array of HCK_NOALLOC_SCRATCH_BYTES inside the library (one
+ * per GPU, resolved on the first call on that device), and nothing is allocated or freed.  A call
+ * whose launches need more (ks workspace of min(batch, 64) items at level_limbs) returns
+ * HCK_ERR_SCRATCH without launching; hck_rotate_noalloc_limit gives the largest batch that fits
+ * (2^30: any batch).  Calls that overlap on one GPU (other streams or threads) race on the array;
+ * calls on one stream are ordered.  Limit: one ciphertext up to 32 limbs at K = 8, dnum 3 (24 limbs:
+ * one ciphertext, 80 MiB). */
+int hck_rotate_noalloc(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
+                       const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                       const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                       int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride, void* stream);
+size_t hck_rotate_noalloc_limit(const hck_context* ctx, int level_limbs);
 
 /* Rotation ending in the extended basis (hoisted form; no ModDown), fhe.fast_rotate(...,
  * output_ext=True) (llama3fhe/operators/attention/prefill/input.py:1669-1687):
