@@ -73,6 +73,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
+    ap.add_argument("--ks-slices", type=int, default=0,
+                    help="c2 key-switch schedule: 0 sequential kernels, >= 2 pipelined slices of the batch")
     ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
                     help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
                          "(both are hoist strategies of the reference's LinearOperatorConfig)")
@@ -123,6 +125,7 @@ def main() -> int:
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
+    ctx.set_keyswitch_slices(args.ks_slices)
     keys = []
     for r in range(1, CTS + 1):
         g = ctx.galois_element(r)
@@ -211,6 +214,7 @@ def main() -> int:
             "batch": CTS,
             "algorithmic_bytes_per_step": step_bytes,
             "cts_per_launch": chunk,
+            "ks_slices": args.ks_slices,
         },
         "roofline": {
             "bound": "hbm",

@@ -157,6 +157,12 @@ class CKKSContext:
     def handle(self):
         return self._h
 
+    def set_keyswitch_slices(self, slices: int) -> None:
+        """Key-switch schedule for batched calls: 0 runs the five kernels in turn over the whole
+        batch (default); s >= 2 pipelines s slices (hck_context_set_ks_slices).  Same results."""
+
+        nat.check(nat.lib().hck_context_set_ks_slices(self._h, int(slices)), "hck_context_set_ks_slices")
+
     # ------------------------------------------------------------------ parameters
     def scale_at(self, cur_limbs: int) -> float:
         """Default encoding scale at a limb count (fixed scale mode)."""

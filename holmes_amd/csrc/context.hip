@@ -312,6 +312,12 @@ extern "C" int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, 
   return HCK_OK;
 }
 
+extern "C" int hck_context_set_ks_slices(hck_context* ctx, int slices) {
+  if (!ctx || slices < 0 || slices > 64) return HCK_ERR_ARG;
+  ctx->ks_slices = slices;
+  return HCK_OK;
+}
+
 extern "C" const char* hck_error_string(int code) {
   switch (code) {
     case HCK_OK: return "ok";

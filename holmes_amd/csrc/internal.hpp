@@ -49,6 +49,7 @@ struct DevTables {
 
 struct hck_context {
   int log_n, L, K, alpha, np;
+  int ks_slices = 0;  // key-switch schedule: 0 / 1 sequential kernels, >= 2 pipelined slices (ksfused.hip)
   std::vector<uint64_t> primes;
   hck::DevTables dev;
   // device allocations

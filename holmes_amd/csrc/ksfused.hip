@@ -333,11 +333,10 @@ __device__ __forceinline__ void rows_inv_to_t(double (&x)[16], double* __restric
 // limb i of a `limbs`-limb workspace poly.  1-D grid over (poly, limb, row group) tiles, decoded so
 // that the polys of one tile run on one XCD back to back (the XCDs take workgroups round-robin):
 // each row group's twiddles are then fetched into one XCD's L2, not into all eight.
-__global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
-                                                     const GalF G, int limb0, int prime0, double* __restrict__ t1,
-                                                     int limbs, int batch, DevTables T) {
-  __shared__ double S[kRowLds];
-  const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
+__device__ __forceinline__ void intt_rows_body(const uint64_t* __restrict__ d, long long d_stride, const GalF& G,
+                                               int limb0, int prime0, double* __restrict__ t1, int limbs, int batch,
+                                               const DevTables& T, int lin, double* S, int koff = 0) {
+  const int xcd = lin % kXcds, q = lin / kXcds;
   const int tile = (q / batch) * kXcds + xcd, b = q % batch;
   if (tile >= 16 * limbs) return;
   const int i = tile >> 4, rg = tile & 15;
@@ -345,8 +344,15 @@ __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict_
   const double p = T.p[pi], pinv = T.pinv[pi];
   const double* __restrict__ tw = T.tw_inv + (size_t)pi * kN;
   double x[16];
-  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), gal_of(G, b));
+  load_gal(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), gal_of(G, koff + b));
   rows_inv_to_t(x, t1 + ((long long)b * limbs + i) * kN, rg, S, tw, p, pinv);
+}
+
+__global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict__ d, long long d_stride,
+                                                     const GalF G, int limb0, int prime0, double* __restrict__ t1,
+                                                     int limbs, int batch, DevTables T) {
+  __shared__ double S[kRowLds];
+  intt_rows_body(d, d_stride, G, limb0, prime0, t1, limbs, batch, T, blockIdx.x, S);
 }
 
 // ----------------------------------------------------------------- K2 / K4: cols + conversion
@@ -363,19 +369,29 @@ __global__ __launch_bounds__(kT) void k_ks_intt_rows(const uint64_t* __restrict_
 constexpr int kRoundsFused = 3;                 // targets per thread held in registers
 constexpr int kTgtFused = 8 * kRoundsFused;     // targets a conversion group may have without SEPX
 
+// The conversion kernel's arguments: source group (z, y) at src + z src_zs + y src_ys + y src_off_y
+// limbs, destination group at dst + z dst_zs + y dst_ys, constants cc_base[y cc_y].
+struct ConvArgs {
+  const double* src;
+  long long src_zs, src_ys;
+  int src_off_y;
+  double* dst;
+  long long dst_zs, dst_ys;
+  const ConvConsts* cc_base;
+  int cc_y;
+};
+
 template <bool SEPX>
-__global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ src, long long src_zs,
-                                                     long long src_ys, int src_off_y, double* __restrict__ dst,
-                                                     long long dst_zs, long long dst_ys,
-                                                     const ConvConsts* __restrict__ cc_base, int cc_y,
-                                                     DevTables T) {
-  __shared__ double Y[16 * kYStride];
-  __shared__ double X[SEPX ? 16 * kYStride : 1];
-  __shared__ TwPair H[kSrcMax * (SEPX ? kMaxPrimes : kTgtFused)];  // H[s * nt + tg] = hmod[s][tg]
+__device__ __forceinline__ void cols_conv_body(const ConvArgs& A, int bx, int y, long long z, double* Y, double* X,
+                                               TwPair* H, const DevTables& T) {
+  const double* __restrict__ src = A.src;
+  double* __restrict__ dst = A.dst;
+  const long long src_zs = A.src_zs, src_ys = A.src_ys, dst_zs = A.dst_zs, dst_ys = A.dst_ys;
+  const int src_off_y = A.src_off_y;
+  const ConvConsts* __restrict__ cc_base = A.cc_base;
+  const int cc_y = A.cc_y;
   const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
-  const int c0 = blockIdx.x * 2;
-  const int y = blockIdx.y;
-  const long long z = blockIdx.z;
+  const int c0 = bx * 2;
   const ConvConsts& C = cc_base[y * cc_y];
   const int ns = C.ns, nt = C.nt;
   for (int q = t; q < ns * nt; q += kT) H[q] = C.hmod[q / nt][q % nt];
@@ -461,6 +477,14 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const double* __restrict__ 
       }
     }
   }
+}
+
+template <bool SEPX>
+__global__ __launch_bounds__(kT) void k_ks_cols_conv(const ConvArgs A, DevTables T) {
+  __shared__ double Y[16 * kYStride];
+  __shared__ double X[SEPX ? 16 * kYStride : 1];
+  __shared__ TwPair H[kSrcMax * (SEPX ? kMaxPrimes : kTgtFused)];  // H[s * nt + tg] = hmod[s][tg]
+  cols_conv_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, H, T);
 }
 
 // ----------------------------------------------------------------- forward row twiddles in LDS
@@ -628,8 +652,8 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
 struct TileId {
   int tile, b;
 };
-__device__ __forceinline__ TileId decode_tile(int batch) {
-  const int lin = blockIdx.x, xcd = lin % kXcds, q = lin / kXcds;
+__device__ __forceinline__ TileId decode_tile(int batch, int lin) {
+  const int xcd = lin % kXcds, q = lin / kXcds;
   return TileId{(q / batch) * kXcds + xcd, q % batch};
 }
 
@@ -640,19 +664,17 @@ __device__ __forceinline__ TileId decode_tile(int batch) {
 // extended basis: it writes (P * sigma(add) + IP_b, IP_a) over Q u P as canonical NTT-domain residues
 // to ext_b / ext_a ([ell + K] limbs per ciphertext, Q limbs first), plus the extended-basis
 // accumulators acc_b / acc_a when given (which ext_b / ext_a may alias).
-__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
-                                                   const double* __restrict__ t2, KeyPtrsF keys, int ell,
-                                                   int beta, int batch, int tiles, int e0, double* __restrict__ accp,
-                                                   const uint64_t* __restrict__ add, long long add_stride,
-                                                   uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
-                                                   const uint64_t* acc_b, const uint64_t* acc_a,
-                                                   long long acc_stride, DevTables T) {
-  __shared__ double S[kRowLds];
-  __shared__ double TW[kTwLds];
-  const TileId id = decode_tile(batch);
+__device__ __forceinline__ void rows_ip_body(const uint64_t* __restrict__ d, long long d_stride, const GalF& G,
+                                             const double* __restrict__ t2, const KeyPtrsF& keys, int ell, int beta,
+                                             int batch, int tiles, int e0, double* __restrict__ accp,
+                                             const uint64_t* __restrict__ add, long long add_stride, uint64_t* ext_b,
+                                             uint64_t* ext_a, long long ext_stride, const uint64_t* acc_b,
+                                             const uint64_t* acc_a, long long acc_stride, const DevTables& T, int lin,
+                                             double* S, double* TW, int koff = 0) {
+  const TileId id = decode_tile(batch, lin);
   if (id.tile >= tiles) return;
   const int b = id.b, e = e0 + (id.tile >> 4), rg = id.tile & 15;
-  const uint32_t g = gal_of(G, b);
+  const uint32_t g = gal_of(G, koff + b);
   const int L = T.L, K = T.K;
   const int pi = e < ell ? e : L + (e - ell);
   const double p = T.p[pi], pinv = T.pinv[pi];
@@ -663,7 +685,7 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict
     __syncthreads();
   }
   double sb[16], sa[16], x[16];
-  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T);
+  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T);
   const long long na = nat_a(rg);
   if (ext_b) {
     if (e < ell && add) {
@@ -697,6 +719,19 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict
   rows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, p, pinv);
 }
 
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
+                                                   const double* __restrict__ t2, KeyPtrsF keys, int ell,
+                                                   int beta, int batch, int tiles, int e0, double* __restrict__ accp,
+                                                   const uint64_t* __restrict__ add, long long add_stride,
+                                                   uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
+                                                   const uint64_t* acc_b, const uint64_t* acc_a,
+                                                   long long acc_stride, DevTables T) {
+  __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
+  rows_ip_body(d, d_stride, G, t2, keys, ell, beta, batch, tiles, e0, accp, add, add_stride, ext_b, ext_a, ext_stride,
+               acc_b, acc_a, acc_stride, T, blockIdx.x, S, TW);
+}
+
 // One component of the ModDown finish, its T4 tile loaded in x (map T): ip <- (ip - NTT rows(v)) * P^-1,
 // plus the addends, canonical store.  `next` (or nothing) is loaded into x once the transform is done.
 __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], const double* __restrict__ next,
@@ -728,6 +763,39 @@ __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], co
 // pass v of the ModDown conversion T4 right away, so the Q-limb inner product never goes to HBM:
 //   out_b = (IP_b - v_b) * P^-1 + sigma_g(add) (+ acc_b),   out_a = (IP_a - v_a) * P^-1 (+ acc_a),
 // canonical u64.
+__device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, long long d_stride, const GalF& G,
+                                              const double* __restrict__ t2, const KeyPtrsF& keys, int ell, int beta,
+                                              int batch, const double* __restrict__ t4,
+                                              const uint64_t* __restrict__ add, long long add_stride,
+                                              const uint64_t* __restrict__ acc_b, const uint64_t* __restrict__ acc_a,
+                                              long long acc_stride, uint64_t* __restrict__ out_b,
+                                              uint64_t* __restrict__ out_a, long long out_stride,
+                                              const LevelConsts* __restrict__ lc, const DevTables& T, int lin,
+                                              double* S, double* TW, int koff = 0) {
+  const TileId id = decode_tile(batch, lin);
+  if (id.tile >= 16 * ell) return;
+  const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
+  const uint32_t g = gal_of(G, koff + b);
+  const double p = T.p[i], pinv = T.pinv[i];
+  {
+    TwStage st;
+    tw_issue(st, T.tw_fwd + (size_t)i * kN, rg);
+    tw_store(st, TW);
+    __syncthreads();
+  }
+  const double* v_b = t4 + ((long long)b * 2 * ell + i) * kN;
+  const double* v_a = v_b + (long long)ell * kN;
+  double sb[16], sa[16], x[16];
+  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T);
+  const long long na = nat_a(rg);
+  const TwPair pinv_P = lc->p_inv[i];
+  ipq_finish(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
+             acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
+             out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
+  ipq_finish(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
+             out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
+}
+
 __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
                                                     const double* __restrict__ t2, KeyPtrsF keys, int ell, int beta,
                                                     int batch, const double* __restrict__ t4,
@@ -739,28 +807,8 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restric
                                                     DevTables T) {
   __shared__ double S[kRowLds];
   __shared__ double TW[kTwLds];
-  const TileId id = decode_tile(batch);
-  if (id.tile >= 16 * ell) return;
-  const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
-  const uint32_t g = gal_of(G, b);
-  const double p = T.p[i], pinv = T.pinv[i];
-  {
-    TwStage st;
-    tw_issue(st, T.tw_fwd + (size_t)i * kN, rg);
-    tw_store(st, TW);
-    __syncthreads();
-  }
-  const double* v_b = t4 + ((long long)b * 2 * ell + i) * kN;
-  const double* v_a = v_b + (long long)ell * kN;
-  double sb[16], sa[16], x[16];
-  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T);
-  const long long na = nat_a(rg);
-  const TwPair pinv_P = lc->p_inv[i];
-  ipq_finish(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
-             acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
-             out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
-  ipq_finish(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
-             out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
+  rows_ipq_body(d, d_stride, G, t2, keys, ell, beta, batch, t4, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
+                out_stride, lc, T, blockIdx.x, S, TW);
 }
 
 // ----------------------------------------------------------------- ModDown / rescale finish
@@ -807,6 +855,149 @@ __global__ __launch_bounds__(kT) void k_ks_rows_store(const double* __restrict__
   for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(x[k], p, pinv));
 }
 
+// ----------------------------------------------------------------- pipelined schedule
+// The five kernels above alternate between VALU-bound (K2, K4) and HBM-bound (K1, K3, K5) work, and
+// every phase of a ciphertext needs the whole previous phase of that ciphertext (a transpose through
+// the workspace).  The pipelined schedule cuts the batch into slices and runs, in launch t, phase k
+// of slice t - k for every k at once: the launch's workgroups interleave the phases (rounds of
+// per-phase groups), so the conversion kernels of one slice execute beside the inner products of
+// another on the same CUs.  Stream order between launches carries every dependency (phase k of a
+// slice ran in the previous launch); within a launch the phases touch disjoint slices.
+constexpr int kWaveLds = kRowLds + kTwLds;  // the largest phase (K3 / K5: S + TW)
+static_assert(16 * kYStride + kSrcMax * kTgtFused * 2 <= kWaveLds, "conversion phase LDS");
+
+struct WavePhase {
+  int blocks;  // workgroups of this phase in the launch (0: phase idle)
+  int group;   // workgroups per round (multiple of 8: keeps the XCD decode of the tile phases)
+  int b0;      // first item of the slice (index into keys / galois)
+  int batch;   // items of the slice
+  const uint64_t* d;
+  const uint64_t* add;
+  const uint64_t* acc_b;
+  const uint64_t* acc_a;
+  uint64_t* out_b;
+  uint64_t* out_a;
+  double* r1;
+  double* t2;
+  double* accp;
+};
+
+struct WaveArgs {
+  WavePhase ph[5];
+  int round;  // sum of the groups
+  int ell, beta;
+  long long d_stride, add_stride, acc_stride, out_stride;
+  const ConvConsts* modup;
+  const ConvConsts* moddown;
+  const LevelConsts* lc;
+  KeyPtrsF keys;
+  GalF G;
+};
+
+__global__ __launch_bounds__(kT, 2) void k_ks_wave(const WaveArgs A, DevTables T) {
+  __shared__ double smem[kWaveLds];
+  const int R = A.round, g = blockIdx.x / R;
+  int r = blockIdx.x - g * R, k = 0;
+  while (k < 4 && r >= A.ph[k].group) {
+    r -= A.ph[k].group;
+    ++k;
+  }
+  const WavePhase& P = A.ph[k];
+  const int local = g * P.group + r;
+  if (r >= P.group || local >= P.blocks) return;
+  const int ell = A.ell, beta = A.beta, K = T.K, ext_l = ell + K;
+  const long long n = kN;
+  switch (k) {
+    case 0:
+      intt_rows_body(P.d, A.d_stride, A.G, 0, 0, P.r1, ell, P.batch, T, local, smem, P.b0);
+      break;
+    case 1: {
+      const ConvArgs C{P.r1, (long long)ell * n, 0, T.alpha, P.t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                       A.modup, 1};
+      cols_conv_body<false>(C, local % 128, (local / 128) % beta, local / (128 * beta), smem, nullptr,
+                            (TwPair*)(smem + 16 * kYStride), T);
+      break;
+    }
+    case 2:
+      rows_ip_body(P.d, A.d_stride, A.G, P.t2, A.keys, ell, beta, P.batch, 16 * K, ell, P.accp, nullptr, 0, nullptr,
+                   nullptr, 0, nullptr, nullptr, 0, T, local, smem, smem + kRowLds, P.b0);
+      break;
+    case 3: {
+      const ConvArgs C{P.accp, 2LL * K * n, (long long)K * n, 0, P.r1, 2LL * ell * n, (long long)ell * n, A.moddown, 0};
+      cols_conv_body<false>(C, local % 128, (local / 128) % 2, local / 256, smem, nullptr,
+                            (TwPair*)(smem + 16 * kYStride), T);
+      break;
+    }
+    default:
+      rows_ipq_body(P.d, A.d_stride, A.G, P.t2, A.keys, ell, beta, P.batch, P.r1, P.add, A.add_stride, P.acc_b,
+                    P.acc_a, A.acc_stride, P.out_b, P.out_a, A.out_stride, A.lc, T, local, smem, smem + kRowLds,
+                    P.b0);
+      break;
+  }
+}
+
+constexpr int kWaveRounds = 32;
+
+}  // namespace
+
+namespace {
+
+// The pipelined schedule of ks_fused (see k_ks_wave); same arguments, workspace and results.
+int ks_wave(const hck_context* c, int ell, int batch, int slices, const uint64_t* d, long long d_stride, const GalF& G,
+            const KeyPtrsF& kp, const uint64_t* add, long long add_stride, const uint64_t* acc_b, const uint64_t* acc_a,
+            long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride, double* r1, double* t2,
+            double* accp, hipStream_t s) {
+  const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
+  const long long n = kN;
+  const int per = (batch + slices - 1) / slices;
+  const int ns = (batch + per - 1) / per;
+  WaveArgs A{};
+  A.ell = ell;
+  A.beta = beta;
+  A.d_stride = d_stride;
+  A.add_stride = add_stride;
+  A.acc_stride = acc_stride;
+  A.out_stride = out_stride;
+  A.modup = modup_consts(c, ell, 0);
+  A.moddown = c->d_moddown + ell;
+  A.lc = c->d_level + ell;
+  A.keys = kp;
+  A.G = G;
+  auto tiles8 = [](int tiles) { return (tiles + kXcds - 1) / kXcds * kXcds; };
+  for (int t = 0; t < ns + 4; ++t) {
+    int round = 0, rounds = 0;
+    for (int k = 0; k < 5; ++k) {
+      WavePhase& P = A.ph[k];
+      P = WavePhase{};
+      const int sl = t - k;
+      if (sl < 0 || sl >= ns) continue;
+      const int b0 = sl * per, nb = batch - b0 < per ? batch - b0 : per;
+      P.b0 = b0;
+      P.batch = nb;
+      P.d = d + (long long)b0 * d_stride;
+      P.add = add ? add + (long long)b0 * add_stride : nullptr;
+      P.acc_b = acc_b ? acc_b + (long long)b0 * acc_stride : nullptr;
+      P.acc_a = acc_a ? acc_a + (long long)b0 * acc_stride : nullptr;
+      P.out_b = out_b + (long long)b0 * out_stride;
+      P.out_a = out_a + (long long)b0 * out_stride;
+      P.r1 = r1 + (long long)b0 * 2 * ell * n;
+      P.t2 = t2 + (long long)b0 * beta * ext_l * n;
+      P.accp = accp + (long long)b0 * 2 * K * n;
+      const int blocks[5] = {tiles8(16 * ell) * nb, 128 * beta * nb, tiles8(16 * K) * nb, 256 * nb,
+                             tiles8(16 * ell) * nb};
+      P.blocks = blocks[k];
+      P.group = tiles8((P.blocks + kWaveRounds - 1) / kWaveRounds);
+      const int need = (P.blocks + P.group - 1) / P.group;
+      rounds = rounds > need ? rounds : need;
+      round += P.group;
+    }
+    A.round = round;
+    k_ks_wave<<<dim3((unsigned)(rounds * round)), kT, 0, s>>>(A, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
+
 }  // namespace
 
 // Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)], ACCP [2 K].
@@ -832,20 +1023,27 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   double* r1 = (double*)ws;
   double* t2 = r1 + (long long)batch * 2 * ell * n;
   double* accp = t2 + (long long)batch * beta * ext_l * n;
+  // Targets of digit j: ext_l minus the digit's own limbs; the last digit is the smallest.
+  const int last_digit = ell - c->alpha * (beta - 1);
+  KeyPtrsF kp{};
+  for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
+  const int slices = c->ks_slices;
+  const bool seq_conv = ext_l - last_digit <= kTgtFused && ell <= kTgtFused;  // both conversions unsplit
+  if (!ext_b && slices > 1 && batch >= 2 * slices && seq_conv) {
+    return ks_wave(c, ell, batch, slices, d, d_stride, G, kp, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
+                   out_stride, r1, t2, accp, s);
+  }
   // K1
   k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0,
                                                                                     r1, ell, batch, c->dev);
   HCK_CHECK_LAUNCH();
-  // K2: ModUp, one block per (column pair, digit, ciphertext).  Targets of digit j: ext_l minus the
-  // digit's own limbs; the last digit is the smallest.
-  const int last_digit = ell - c->alpha * (beta - 1);
+  // K2: ModUp, one block per (column pair, digit, ciphertext)
   auto cols_conv = ext_l - last_digit <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(r1, (long long)ell * n, 0, c->alpha, t2,
-                                                  (long long)beta * ext_l * n, (long long)ext_l * n,
-                                                  modup_consts(c, ell, 0), 1, c->dev);
+  cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(
+      ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+               modup_consts(c, ell, 0), 1},
+      c->dev);
   HCK_CHECK_LAUNCH();
-  KeyPtrsF kp{};
-  for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
   if (ext_b) {
     // K3 over every extended limb, ending in the extended basis
     const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
@@ -866,8 +1064,9 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
   double* t4 = r1;
   auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  md_conv<<<dim3(128, 2, batch), kT, 0, s>>>(accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n,
-                                             (long long)ell * n, c->d_moddown + ell, 0, c->dev);
+  md_conv<<<dim3(128, 2, batch), kT, 0, s>>>(
+      ConvArgs{accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n, (long long)ell * n, c->d_moddown + ell, 0},
+      c->dev);
   HCK_CHECK_LAUNCH();
   // K5: Q limbs
   {
@@ -897,8 +1096,8 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
                                                                                    tp, K, polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0,
-                                             c->d_moddown + ell, 0, c->dev);
+  md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(
+      ConvArgs{tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0, c->d_moddown + ell, 0}, c->dev);
   HCK_CHECK_LAUNCH();
   k_ks_rows_finish<<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, out, out_stride, ell,
                                                        (c->d_level + ell)->p_inv, c->dev);
@@ -922,7 +1121,8 @@ int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, 
                                                                                 ell - 1, tl, 1, polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  conv<<<dim3(128, 1, polys), kT, 0, s>>>(tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_rescale + ell, 0, c->dev);
+  conv<<<dim3(128, 1, polys), kT, 0, s>>>(ConvArgs{tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_rescale + ell, 0},
+                                          c->dev);
   HCK_CHECK_LAUNCH();
   k_ks_rows_finish<<<dim3(polys, 16, nt), kT, 0, s>>>(t4, in, in_stride, out, out_stride, nt,
                                                       (c->d_level + ell)->qlast_inv, c->dev);
@@ -945,7 +1145,8 @@ int modraise_fused(const hck_context* c, int to, int polys, const uint64_t* in, 
                                                                                 polys, c->dev);
   HCK_CHECK_LAUNCH();
   auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  conv<<<dim3(128, 1, polys), kT, 0, s>>>(tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_raise + to, 0, c->dev);
+  conv<<<dim3(128, 1, polys), kT, 0, s>>>(ConvArgs{tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_raise + to, 0},
+                                          c->dev);
   HCK_CHECK_LAUNCH();
   k_ks_rows_store<<<dim3(polys, 16, nt), kT, 0, s>>>(t4, nt, out, out_stride, 1, 1, c->dev);
   HCK_CHECK_LAUNCH();

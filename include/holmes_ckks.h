@@ -65,6 +65,11 @@ int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, int* num_p,
 /* Host copy of the root table psi^brv(k) (inverse: psi^-brv(k)) of prime `prime_idx` (N words). */
 int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uint64_t* out);
 const char* hck_error_string(int code);
+/* Key-switch schedule of batched calls: 0 or 1 (default) runs the five key-switch kernels one after
+ * another over the whole batch; s >= 2 cuts batches of at least 2 s items into s slices and runs
+ * phase k of slice t - k in launch t (every phase of the pipeline in one launch).  Results are
+ * identical; only the timing differs.  No counterpart in the reference (a scheduling knob). */
+int hck_context_set_ks_slices(hck_context* ctx, int slices);
 
 /* In-place (src == dst allowed) negacyclic NTT of `polys` x `limbs` limbs: limb l of poly b is at
  * base + b * stride + l * N and uses prime prime_idx[l] (host array).  Forward: natural-order

@@ -435,3 +435,31 @@ def test_every_level_keyswitch_and_rescale(env):
                 assert np.array_equal(got[b], orc.rescale(ell, x[b])), f"rescale at {ell} limbs, item {b}"
             y = _rand(ctx, rng, 1, 1)
             assert np.array_equal(_host(ctx.modraise(_dev(y), ell))[0], orc.modraise(ell, y[0])), f"ModRaise to {ell}"
+
+
+@pytest.mark.parametrize("slices", [2, 4])
+def test_pipelined_keyswitch_schedule_matches_oracle(env, slices):
+    """The pipelined schedule (slices of the batch, all five phases in each launch) gives the
+    residues of the sequential one: 10 items (a ragged last slice), distinct keys, per-item
+    Galois elements, accumulators, and the C2 batch of 16."""
+    _, client, ctx, orc = env
+    ell = 24
+    try:
+        ctx.set_keyswitch_slices(slices)
+        for B in (10, 16):
+            rng = np.random.default_rng(70 + slices + B)
+            c0, c1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
+            acc = _rand(ctx, rng, B, ell)
+            gs = [ctx.galois_element(r) for r in range(1, B + 1)]
+            keys = [ctx.make_switching_key(*client.key_inputs(g)) for g in gs]
+            o0, o1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, gs, keys, acc=(_dev(acc), _dev(acc)))
+            o0, o1 = _host(o0), _host(o1)
+            q = np.array(ctx.primes[:ell], dtype=object).reshape(ell, 1)
+            for b in (0, B // 2, B - 1):
+                okey = orc.make_ksk(*client.key_inputs(gs[b]))
+                w0, w1 = orc.rotate(ell, gs[b], c0[b], c1[b], okey)
+                w0 = ((w0.astype(object) + acc[b].astype(object)) % q).astype(np.uint64)
+                w1 = ((w1.astype(object) + acc[b].astype(object)) % q).astype(np.uint64)
+                assert np.array_equal(o0[b], w0) and np.array_equal(o1[b], w1), (B, b)
+    finally:
+        ctx.set_keyswitch_slices(0)
