@@ -583,6 +583,26 @@ class CipherOps:
         f = self._fhe
         return f.rescale(f.homo_mul_relin(a, b, self.ctx), self.ctx)
 
+    def mul_sum(self, a, b, sizes):
+        """Products a_i * b_i summed over consecutive groups of ``sizes`` items: the tensor products
+        of a group are added as three-component ciphertexts and relinearised once, then rescaled."""
+
+        f, ctx = self._fhe, self.ctx
+        t = f.homo_mul_no_relin(a, b, ctx)
+        limbs = self.limbs(t)
+        if sum(int(n) for n in sizes) != int(t.batch_size):
+            raise ValueError("group sizes must cover the batch")
+        G = len(sizes)
+        outs = [ctx.empty(G, limbs, ctx.N) for _ in range(3)]
+        start = 0
+        for g, n in enumerate(sizes):
+            for comp in range(3):
+                ctx.lincomb([[t.cv[comp][i, :limbs] for i in range(start, start + int(n))]], limbs,
+                            [outs[comp][g]])
+            start += int(n)
+        summed = t.cipher_like(outs, batch_size=G)
+        return f.rescale(f.homo_relinearize(summed, ctx), ctx)
+
     def adjust(self, ct, limbs: int, scale: float):
         """``ct`` at (limbs, scale): one scalar product and rescale, then dropped limbs."""
 

@@ -149,6 +149,19 @@ class SlotOps:
             raise ValueError("a product needs two limbs")
         return SimCt(a.values * b.values, l - 1, self.scale(a) * self.scale(b) / self._q(l))
 
+    def mul_sum(self, a, b, sizes):
+        l = self._common(a, b)
+        if l < 2:
+            raise ValueError("a product needs two limbs")
+        if sum(int(n) for n in sizes) != a.batch_size:
+            raise ValueError("group sizes must cover the batch")
+        prod = a.values * b.values
+        out, start = [], 0
+        for n in sizes:
+            out.append(prod[start:start + int(n)].sum(axis=0))
+            start += int(n)
+        return SimCt(np.stack(out), l - 1, self.scale(a) * self.scale(b) / self._q(l))
+
     def drop(self, ct, limbs: int):
         if int(limbs) > self.limbs(ct):
             raise ValueError("cannot raise limbs")

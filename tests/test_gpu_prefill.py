@@ -1,0 +1,47 @@
+"""GPU check of one encrypted 128-token prefill layer (holmes_amd.prefill.PrefillLayer, the
+reference's llama3fhe/graph/prefill.py:57 ``evaluate`` for the first layer: RMSNorm1, QKV, RoPE,
+causal Alg2 attention, W_O, residual, one two-pass refresh, the SwiGLU MLP block at width 14336,
+residual).  Llama-3-8B shapes with seeded random weights N(0, 0.02^2) and gammas 1 + N(0, 0.1^2),
+input N(0, 1), the 38-limb chain (depth 37, dnum 5, 50-bit primes, scale 2^50).  Every decrypted
+output slot is within 2^-16 of the float64 model of the same polynomials (prefill_layer_numpy)."""
+
+import math
+import time
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+torch = pytest.importorskip("torch")
+
+SEED = 20261206
+
+
+@pytest.mark.timeout(1100)
+def test_prefill_layer_decrypts_to_model():
+    from holmes_amd import fhe
+    from holmes_amd import prefill as P
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+
+    t0 = time.perf_counter()
+    spec = P.PrefillSpec()
+    client, ctx = fhe.generate_client_context(P.prefill_context_spec(SEED), device="cuda")
+    assert ctx.L == 38 and ctx.K == 8
+    rng = np.random.default_rng(SEED)
+    w = P.random_weights(spec, rng)
+    layer, rots = P.setup_prefill_layer(client, ctx, w, spec)
+    print(f"prefill layer setup {time.perf_counter() - t0:.1f} s, {len(rots)} rotation keys", flush=True)
+    layout = FeatureMajorPrefillLayout()
+    x = rng.normal(size=(128, 4096))
+    cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
+    out, stages = layer.forward(cts)
+    print(f"prefill layer: stages {stages}, output at {out[0].state.cur_limbs} limbs", flush=True)
+    ref = P.prefill_layer_numpy(x, w, spec)
+    want = layout.pack(ref["output"])
+    err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
+    mag = float(np.max(np.abs(ref["output"])))
+    print(f"prefill layer max error 2^{math.log2(err):.2f} of magnitude {mag:.2f}; softmax vs exact "
+          f"{ref['softmax_vs_exact']:.2e}; in range {ref['in_range']}", flush=True)
+    assert ref["in_range"]["exp"] and ref["in_range"]["rsqrt"]
+    assert err < 2.0**-16
