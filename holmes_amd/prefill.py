@@ -72,6 +72,7 @@ class PrefillSpec:
     eps: float = 1e-5
     rms_degree: int = 15
     rms_interval: tuple = (0.5, 2.0)
+    post_rms_interval: tuple = (0.5, 8.0)  # of mean(h^2) after the attention residual
     exp_degree: int = 15
     exp_interval: tuple = (-5.0, 5.0)     # of u = (S - mean_k S) / (2 sqrt(d))
     rsqrt_degree: int = 31
@@ -116,7 +117,7 @@ def prefill_mlp_spec(spec: PrefillSpec):
 
     return MLPBlockSpec(hidden_dim=spec.hidden_dim, intermediate_width=spec.intermediate,
                         silu_degree=spec.silu_degree, silu_interval=spec.silu_interval,
-                        rms_degree=spec.rms_degree, rms_interval=spec.rms_interval, eps=spec.eps)
+                        rms_degree=spec.rms_degree, rms_interval=spec.post_rms_interval, eps=spec.eps)
 
 
 def prefill_bootstrap_spec():
@@ -184,7 +185,11 @@ def prefill_layer_numpy(x: np.ndarray, w: DecodeWeights, spec: PrefillSpec,
     h = x + att["delta"]
     mspec = prefill_mlp_spec(spec)
     out = h + mlp_block_numpy(h, w.gate_proj, w.up_proj, w.down_proj, w.post_attention_layernorm, mspec)
-    return {"output": out, "h": h, "xn": xn, **att}
+    ms = np.mean(h * h, axis=1)
+    res = {"output": out, "h": h, "xn": xn, **att}
+    res["in_range"] = {**att["in_range"], "post_rms": bool(ms.min() >= spec.post_rms_interval[0]
+                                                           and ms.max() <= spec.post_rms_interval[1])}
+    return res
 
 
 # ---------------------------------------------------------------------------- weight blocks
