@@ -19,19 +19,22 @@ product with e^(i theta), and gives the real score as Re(sum_f Qz_f conj(Kz_f)):
 * projection A (complex 4096 x 4096): channel 64 h + f = Qz of query head h; channel
   2048 + 64 h + f = conj Kz of KV head h // 4 (GQA replicated), RoPE'd by e^(-i theta);
 * projection V: channel 64 h + f = Vz of KV head h // 4, the upper half zero;
-* for every key ciphertext c' and lane offset rho the K half is rotated into the lower half with
-  the lanes rotated by rho (two rotations, lane masks): lane t then holds key 8 c' + (t + rho) mod 8;
-* a product of Q_c with that carrier, folded over the 64 channels of each head (six rotations),
-  gives 2 x 8 complex scores per head; the 8 (c' <= c) x 8 offsets of query ciphertext c are packed
-  into one dense score ciphertext (key index j = 8 c' + rho at channel position j of the head: the
-  lower half for j < 64, the upper half for j >= 64), whose real part is the score; the packing
-  rotations go baby-step / giant-step over j = 8 a + b, so they need 22 keys, not 256;
+* for every key ciphertext c' and lane offset rho the K half is lane-rotated by rho (two
+  rotations, lane masks), once moved into the lower half and once kept in the upper: lane t then
+  holds key 8 c' + (t + rho) mod 8;
+* the 8 (c + 1) key indices j = 8 c' + rho of query ciphertext c are split over the two halves
+  (j < 4 (c + 1) at channel position j of the lower half, the rest at j - 4 (c + 1) of the upper),
+  so a product of Q_c (copied into both halves) with the sum of two carriers, folded over the 64
+  channels of each head (six rotations), gives the scores of two keys; they are packed into one
+  dense score ciphertext per query ciphertext, whose real part is the score, by baby-step /
+  giant-step rotations over the channel position (14 keys);
 * Alg2 on the 16 dense score ciphertexts; invalid (non-causal) positions hold score 0, so their
   exp is the public value E(0), subtracted off; row sums fold over the 128 key positions; the 16
   row-sum ciphertexts are packed into one for the inverse square root;
-* PV: each probability column is broadcast over the 64 channels and multiplied with the lane-
-  rotated value carrier; the products of a query ciphertext are summed before one
-  relinearisation; the result is complex feature-major, the input layout of W_O.
+* PV: each pair of probability columns is broadcast over the 64 channels and multiplied with the
+  lane-rotated value carriers of its two keys; the products of a query ciphertext are summed
+  before one relinearisation and the two halves added; the result is complex feature-major, the
+  input layout of W_O.
 
 ``PrefillAttention`` is written against the ciphertext-operation surface of ``decode.CipherOps``
 (GPU) and ``tests/slot_sim.SlotOps`` (float64 slots with the same level and scale bookkeeping), so
@@ -248,56 +251,66 @@ def rope_rows(spec: PrefillSpec) -> np.ndarray:
     return np.stack([np.where(d < 2048, ph[8 * c + t, d % 64], 0.0) for c in range(CTS)])
 
 
-def key_phase_masks(spec: PrefillSpec) -> list:
-    """[rho] -> ([16, slots], [16, slots]): the lane masks of the key carrier of ciphertext c' and lane
-    offset rho, times the conjugate RoPE phase of the key each slot receives (token
-    8 c' + (t + rho) mod 8, folded feature f = d mod 64)."""
+def key_phase_masks(spec: PrefillSpec, upper: bool = False) -> list:
+    """[rho] -> ([16, slots], [16, slots]): the lane masks (of one half) of the key carrier of
+    ciphertext c' and lane offset rho, times the conjugate RoPE phase of the key each slot receives
+    (token 8 c' + (t + rho) mod 8, folded feature f = d mod 64)."""
 
     d, t = _slot_grid()
     ph = np.conj(_phases(spec))
     out = []
     for rho in range(LANES):
-        lo, hi = lane_masks(rho)
+        lo, hi = lane_masks(rho, upper)
         tok = (t + rho) % LANES
         rows = np.stack([ph[8 * c + tok, d % 64] for c in range(CTS)])
         out.append((lo[None, :] * rows, hi[None, :] * rows))
     return out
 
 
-def lane_masks(rho: int) -> tuple[np.ndarray, np.ndarray]:
-    """Lower-half masks of the two rotations of a lane rotation by rho: lanes t < 8 - rho (taken
-    from the rotation by rho) and t >= 8 - rho (from the rotation by rho - 8)."""
+def lane_masks(rho: int, upper: bool = False) -> tuple[np.ndarray, np.ndarray]:
+    """Masks of one half (the lower by default) for the two rotations of a lane rotation by rho:
+    lanes t < 8 - rho (taken from the rotation by rho) and t >= 8 - rho (from the rotation by
+    rho - 8)."""
 
     d, t = _slot_grid()
-    low = d < 2048
-    return (low & (t < LANES - rho)).astype(np.float64), (low & (t >= LANES - rho)).astype(np.float64)
+    half = (d >= 2048) if upper else (d < 2048)
+    return (half & (t < LANES - rho)).astype(np.float64), (half & (t >= LANES - rho)).astype(np.float64)
 
 
-def key_position(j: int) -> int:
-    """Slot offset (channel position of head 0, lane 0) of key index j in a dense score ciphertext."""
+def split(c: int) -> int:
+    """Keys of query ciphertext c per half of its dense score ciphertext: of its 8 (c + 1) key
+    indices, j < 4 (c + 1) sit at channel position j of the lower half and the others at position
+    j - 4 (c + 1) of the upper half, so one product serves a key of each half."""
 
-    return 8 * j if j < 64 else HALF + 8 * (j - 64)
+    return 4 * (c + 1)
 
 
-def position_mask(j: int) -> np.ndarray:
-    """1 on key index j's channel position of every head and lane."""
+def key_slot(c: int, j: int) -> int:
+    """Slot offset (head 0, lane 0) of key index j in the dense score ciphertext of query c."""
 
-    d, t = _slot_grid()
-    if j < 64:
-        return ((d < 2048) & (d % 64 == j)).astype(np.float64)
-    return ((d >= 2048) & (d % 64 == j - 64)).astype(np.float64)
+    m = split(c)
+    return 8 * j if j < m else HALF + 8 * (j - m)
+
+
+def _carrier(j: int) -> tuple[int, int]:
+    """(key ciphertext c', lane offset rho) of key index j."""
+
+    return j // LANES, j % LANES
 
 
 def validity_rows() -> np.ndarray:
-    """[16, slots]: 1 where key index j (at its position) is causal for query 8 c + t."""
+    """[16, slots]: 1 where the slot of ciphertext c holds a key index j causal for query 8 c + t."""
 
     d, t = _slot_grid()
-    j = np.where(d < 2048, d % 64, 64 + d % 64)
-    cp, rho = j // 8, j % 8
+    pos = d % 64
+    upper = d >= 2048
     rows = np.zeros((CTS, SLOTS))
     for c in range(CTS):
+        m = split(c)
+        j = np.where(upper, pos + m, pos)
+        cp, rho = j // LANES, j % LANES
         key_lane = (t + rho) % LANES
-        rows[c] = ((cp < c) | ((cp == c) & (key_lane <= t))).astype(np.float64)
+        rows[c] = ((pos < m) & ((cp < c) | ((cp == c) & (key_lane <= t)))).astype(np.float64)
     return rows
 
 
@@ -318,12 +331,13 @@ def packed_count_row(power: float) -> np.ndarray:
     return np.where((d < 2048) & (c < CTS), (8.0 * c + t + 1.0) ** power, 0.0)
 
 
-def head_row_mask(t_offset: int = 0) -> np.ndarray:
+def head_row_mask(t_offset: int = 0, both: bool = False) -> np.ndarray:
     """1 on channel position 0 of every head in the lower half (slots 512 h + t), optionally shifted
-    to position ``t_offset`` (slots 512 h + 8 t_offset + t)."""
+    to position ``t_offset`` (slots 512 h + 8 t_offset + t); ``both``: in the upper half too."""
 
     d, t = _slot_grid()
-    return ((d < 2048) & (d % 64 == t_offset)).astype(np.float64)
+    half = np.ones(d.shape, dtype=bool) if both else (d < 2048)
+    return (half & (d % 64 == t_offset)).astype(np.float64)
 
 
 def attention_rotations() -> tuple[int, ...]:
@@ -335,9 +349,8 @@ def attention_rotations() -> tuple[int, ...]:
     for i in range(6):
         rots |= {LANES << i, -(LANES << i)}                            # channel folds and spreads
     for b in range(1, LANES):
-        rots |= {LANES * b, -LANES * b}                                # baby steps over key indices
-    for a in range(1, 2 * LANES):
-        rots |= {key_position(LANES * a), -key_position(LANES * a)}    # giant steps
+        rots |= {LANES * b, -LANES * b}                                # baby steps over key positions
+        rots |= {64 * b, -64 * b}                                      # giant steps
     for c in range(1, CTS):
         rots |= {LANES * c, -LANES * c}                                # row-sum packing and spread
     return tuple(sorted({r % SLOTS for r in rots} - {0}))
@@ -346,32 +359,40 @@ def attention_rotations() -> tuple[int, ...]:
 # ---------------------------------------------------------------------------- encrypted attention
 class PrefillAttention:
     """The attention core on a ciphertext-operation surface ``ops`` (decode.CipherOps or the slot
-    simulator): from the RoPE'd projection batch A (16 items) and the value batch V (16 items) to
-    the complex attention output (16 items, feature-major, the W_O input)."""
+    simulator): from the projection batch A (16 items) and the value batch V (16 items) to the
+    complex attention output (16 items, feature-major, the W_O input).
+
+    Query ciphertext c has 8 (c + 1) key indices j = 8 c' + rho (key ciphertext c' <= c, lane
+    offset rho); they are split over the two halves of every working ciphertext (``split``), so the
+    queries are copied into both halves and one product, one channel fold and one packing rotation
+    serve two keys."""
 
     def __init__(self, ops, spec: PrefillSpec | None = None, polys: PrefillPolynomials | None = None):
         self.ops = ops
         self.spec = PrefillSpec() if spec is None else spec
         self.spec.validate()
         self.polys = PrefillPolynomials.fit(self.spec) if polys is None else polys
-        self.lane = [tuple(SlotConst(m) for m in lane_masks(rho)) for rho in range(LANES)]
-        self.valid = SlotConst(validity_rows())
-        self.invalid = SlotConst(1.0 - validity_rows())
+        self.lane = {hf: [tuple(SlotConst(m) for m in lane_masks(rho, hf)) for rho in range(LANES)]
+                     for hf in (False, True)}
+        valid = validity_rows()
+        self.invalid = SlotConst(1.0 - valid)
         self.row0 = SlotConst(head_row_mask(0))
+        self.row0_both = SlotConst(head_row_mask(0, both=True))
         self.rope_q = SlotConst(rope_rows(self.spec))
-        self.key_masks = [tuple(SlotConst(m) for m in pair) for pair in key_phase_masks(self.spec)]
+        self.key_masks = {hf: [tuple(SlotConst(m) for m in pair) for pair in key_phase_masks(self.spec, hf)]
+                          for hf in (False, True)}
         d, t = _slot_grid()
         n_rows = np.stack([8.0 * c + t + 1.0 for c in range(CTS)])
-        self.valid_over_n = SlotConst(validity_rows() / n_rows)
+        self.valid_over_n = SlotConst(valid / n_rows)
         self.inv_sqrt_count = SlotConst(count_rows(-0.5))
         self.rowc = [SlotConst(head_row_mask(c)) for c in range(CTS)]
-        self.pairs = [(c, j) for c in range(CTS) for j in range(8 * (c + 1))]
-        self.pair_budget = 256
+        self.pairs = [(c, p) for c in range(CTS) for p in range(split(c))]
+        self.pair_budget = 320
         a_e, b_e = (float(v) for v in self.spec.exp_interval)
         # poly argument x = (2 u - (a + b)) / (b - a) with u = S / (2 sqrt d) and 2 Re = D + conj D = 2 S
         self.exp_alpha = 1.0 / (2.0 * math.sqrt(self.spec.head_dim)) / (b_e - a_e)
         self.exp_beta = -(a_e + b_e) / (b_e - a_e)
-        self.exp_alpha_valid = SlotConst(self.exp_alpha * validity_rows())
+        self.exp_alpha_valid = SlotConst(self.exp_alpha * valid)
         self.exp_at_zero = float(_cheb(0.0, self.polys.exp, self.spec.exp_interval))
         a_r, b_r = (float(v) for v in self.spec.rsqrt_interval)
         self.rs_alpha, self.rs_beta = 2.0 / (b_r - a_r), -(a_r + b_r) / (b_r - a_r)
@@ -379,15 +400,15 @@ class PrefillAttention:
         self.rs_shift = SlotConst(self.rs_beta * (packed_count_row(1.0) > 0))
 
     # -- carriers
-    def _lane_carriers(self, X, base: int, masks=None):
-        """Items (c', rho) for rho = 0..7 of the batch X: the half at ``base`` moved to the lower
-        half with lanes rotated by rho (lane t holds token 8 c' + (t + rho) mod 8); ``masks``
-        [rho] replaces the plain lane masks (per-item rows allowed)."""
+    def _lane_carriers(self, X, base: int, masks):
+        """Items (c', rho) for rho = 0..7 of the batch X: X rotated by ``base`` with lanes rotated
+        by rho (lane t holds token 8 c' + (t + rho) mod 8), kept on the half ``masks`` [rho] selects
+        (per-item rows allowed)."""
 
         ops = self.ops
         out = []
         for rho in range(LANES):
-            lo, hi = self.lane[rho] if masks is None else masks[rho]
+            lo, hi = masks[rho]
             if rho == 0:
                 out.append(ops.mac([(ops.rotate(X, base), lo)]))
             else:
@@ -395,16 +416,22 @@ class PrefillAttention:
         items = [ops.items(o) for o in out]             # [rho][c']
         return {(cp, rho): items[rho][cp] for cp in range(CTS) for rho in range(LANES)}
 
-    def _select(self, batch_items, keys):
-        return self.ops.batch([batch_items[k] for k in keys])
+    def _pair_carriers(self, low, up, pairs):
+        """Per pair (c, p): the carrier of key p in the lower half plus that of key p + split(c) in
+        the upper half (one batch)."""
+
+        ops = self.ops
+        lo = ops.batch([low[_carrier(p)] for _, p in pairs])
+        hi = ops.batch([up[_carrier(p + split(c))] for c, p in pairs])
+        return ops.add(lo, hi)
 
     def _query_groups(self):
-        """Consecutive query ciphertexts whose (c, j) products form one batch of at most
-        ``pair_budget`` items (the products of all 1088 pairs at once would need tens of GB)."""
+        """Consecutive query ciphertexts whose (c, p) products form one batch of at most
+        ``pair_budget`` items (the products of all pairs at once would need tens of GB)."""
 
         groups, cur, n = [], [], 0
         for c in range(CTS):
-            k = LANES * (c + 1)
+            k = split(c)
             if cur and n + k > self.pair_budget:
                 groups.append(cur)
                 cur, n = [], 0
@@ -415,44 +442,50 @@ class PrefillAttention:
 
     def _pack_keys(self, m, group):
         """Dense score ciphertexts of the query ciphertexts in ``group`` from the channel sums
-        m[(c, j)] (masked to position 0): sum_j rot(m_j, -key_position(j)) with j = 8 a + b, the
+        m[(c, p)] (masked to position 0 of both halves): sum_p rot(m_p, -8 p) with p = 8 a + b, the
         baby rotations by -8 b of the whole group in one batch, their sums over b, then the giant
-        rotations by -key_position(8 a) in one batch and the sums over a."""
+        rotations by -64 a in one batch and the sums over a."""
 
         ops = self.ops
-        pairs = [(c, j) for c in group for j in range(LANES * (c + 1))]
-        baby = ops.items(ops.rotate(ops.batch([m[p] for p in pairs]), [-LANES * (j % LANES) for _, j in pairs]))
+        pairs = [(c, p) for c in group for p in range(split(c))]
+        baby = ops.items(ops.rotate(ops.batch([m[x] for x in pairs]), [-LANES * (p % LANES) for _, p in pairs]))
         baby = dict(zip(pairs, baby))
-        giants = [(c, a) for c in group for a in range(c + 1)]
-        acc = ops.batch([baby[(c, LANES * a)] for c, a in giants])
+        giants = [(c, a) for c in group for a in range((split(c) + LANES - 1) // LANES)]
+        acc = [baby[(c, LANES * a)] for c, a in giants]
         for b in range(1, LANES):
-            acc = ops.add(acc, ops.batch([baby[(c, LANES * a + b)] for c, a in giants]))
+            sel = [i for i, (c, a) in enumerate(giants) if LANES * a + b < split(c)]
+            s = ops.add(ops.batch([acc[i] for i in sel]),
+                        ops.batch([baby[(giants[i][0], LANES * giants[i][1] + b)] for i in sel]))
+            for i, item in zip(sel, ops.items(s)):
+                acc[i] = item
         del baby
-        moved = dict(zip(giants, ops.items(ops.rotate(acc, [-key_position(LANES * a) for _, a in giants]))))
+        moved = dict(zip(giants, ops.items(ops.rotate(ops.batch(acc), [-64 * a for _, a in giants]))))
         out = {c: moved[(c, 0)] for c in group}
-        for a in range(1, max(group) + 1):
-            cs = [c for c in group if a <= c]
-            summed = ops.add(ops.batch([out[c] for c in cs]), ops.batch([moved[(c, a)] for c in cs]))
-            out.update(zip(cs, ops.items(summed)))
+        for a in range(1, LANES):
+            cs = [c for c in group if (c, a) in moved]
+            if cs:
+                summed = ops.add(ops.batch([out[c] for c in cs]), ops.batch([moved[(c, a)] for c in cs]))
+                out.update(zip(cs, ops.items(summed)))
         return out
 
     def scores(self, A):
-        """Dense score ciphertexts D_c (16 items): 2 S at key index j's position, 0 where j is not
-        computed; ``A`` the projection batch (before RoPE)."""
+        """Dense score ciphertexts D_c (16 items): 2 S at key index j's slot (``key_slot``), 0 where
+        no key is computed; ``A`` the projection batch (before RoPE)."""
 
         ops = self.ops
-        khat = self._lane_carriers(A, HALF, self.key_masks)
-        a_items = ops.items(ops.mac([(A, self.rope_q)]))
+        k_lo = self._lane_carriers(A, HALF, self.key_masks[False])    # the key half moved down
+        k_up = self._lane_carriers(A, 0, self.key_masks[True])        # ... and kept in place
+        q = ops.mac([(A, self.rope_q)])                               # RoPE'd queries, lower half
+        q = ops.items(ops.add(q, ops.rotate(q, HALF)))                # ... in both halves
         dense = {}
         for group in self._query_groups():
-            pairs = [(c, j) for c in group for j in range(LANES * (c + 1))]
-            left = ops.batch([a_items[c] for c, _ in pairs])
-            right = self._select(khat, [(j // LANES, j % LANES) for _, j in pairs])
-            prod = ops.mul(left, right)
-            del left, right
+            pairs = [(c, p) for c in group for p in range(split(c))]
+            right = self._pair_carriers(k_lo, k_up, pairs)
+            prod = ops.mul(ops.batch([q[c] for c, _ in pairs]), right)
+            del right
             for i in range(6):
                 prod = ops.rotate_add(prod, LANES << i)             # the head's 64 channels summed
-            folded = ops.items(ops.mac([(prod, self.row0)]))         # ... kept at channel position 0
+            folded = ops.items(ops.mac([(prod, self.row0_both)]))    # ... kept at channel position 0
             del prod
             dense.update(self._pack_keys(dict(zip(pairs, folded)), group))
         D = ops.batch([dense[c] for c in range(CTS)])
@@ -503,29 +536,33 @@ class PrefillAttention:
         return ops.mul(yl, yl)
 
     def pv(self, P, V):
-        """sum_k P[h][q][k] Vz(k) for every query ciphertext: complex feature-major outputs.  Column
-        j of the probabilities reaches channel position 0 by a giant rotation by key_position(8 a)
-        (the 16 ciphertexts times their a <= c, one batch) and a baby rotation by 8 b (one batch
-        of all pairs), is masked there and spread over the 64 channels."""
+        """sum_k P[h][q][k] Vz(k) for every query ciphertext: complex feature-major outputs.  The
+        probability columns of pair (c, p) (key p in the lower half, key p + split(c) in the upper)
+        reach channel position 0 by a giant rotation by 64 a (the 16 ciphertexts times their a, one
+        batch) and a baby rotation by 8 b (one batch of all pairs); they are masked there, spread
+        over the 64 channels and multiplied by the value carriers of both keys; the products of a
+        query ciphertext are summed before one relinearisation, and the upper half's sum is
+        added to the lower half's."""
 
         ops = self.ops
         if ops.limbs(V) > ops.limbs(P):
             V = ops.drop(V, ops.limbs(P))                 # the carriers only need P's level
-        vhat = self._lane_carriers(V, 0)
+        v_lo = self._lane_carriers(V, 0, self.lane[False])
+        v_up = self._lane_carriers(V, HALF, self.lane[True])
         p_items = ops.items(P)
-        giants = [(c, a) for c in range(CTS) for a in range(c + 1)]
-        g = ops.rotate(ops.batch([p_items[c] for c, _ in giants]), [key_position(LANES * a) for _, a in giants])
-        g_items = ops.items(g)
-        del g
-        src = ops.batch([g_items[i] for i in range(len(giants)) for _ in range(LANES)])
-        col = ops.rotate(src, [LANES * b for _ in giants for b in range(LANES)])
-        del src, g_items
-        col = ops.mac([(col, self.row0)])
+        giants = [(c, a) for c in range(CTS) for a in range((split(c) + LANES - 1) // LANES)]
+        at = {k: i for i, k in enumerate(giants)}
+        g_items = ops.items(ops.rotate(ops.batch([p_items[c] for c, _ in giants]), [64 * a for _, a in giants]))
+        src = ops.batch([g_items[at[(c, p // LANES)]] for c, p in self.pairs])
+        del g_items
+        col = ops.rotate(src, [LANES * (p % LANES) for _, p in self.pairs])
+        del src
+        col = ops.mac([(col, self.row0_both)])
         for i in range(6):
-            col = ops.rotate_add(col, -(LANES << i))      # the lower half: V's upper half is zero
-        right = self._select(vhat, [(j // LANES, j % LANES) for _, j in self.pairs])
-        sizes = [LANES * (c + 1) for c in range(CTS)]
-        return ops.mul_sum(col, right, sizes)
+            col = ops.rotate_add(col, -(LANES << i))      # within each half's heads
+        right = self._pair_carriers(v_lo, v_up, self.pairs)
+        sums = ops.mul_sum(col, right, [split(c) for c in range(CTS)])
+        return ops.add(sums, ops.rotate(sums, HALF))
 
     def forward(self, A, V):
         S2 = self.scores(A)

@@ -89,15 +89,22 @@ def test_slot_constants():
     lo, hi = P.lane_masks(3)
     d, t = np.arange(32768) // 8, np.arange(32768) % 8
     assert np.all((lo + hi) == (d < 2048)) and np.all(lo[(d < 2048) & (t < 5)] == 1)
+    ulo, uhi = P.lane_masks(3, upper=True)
+    assert np.all((ulo + uhi) == (d >= 2048)) and np.all(uhi[(d >= 2048) & (t >= 5)] == 1)
     valid = P.validity_rows()
-    # query 8c + t, key j = 8c' + rho -> token 8c' + (t + rho) % 8
-    s = 8 * (64 * 3 + 13) + 2                 # head 3, j = 13 (c' = 1, rho = 5), lane 2 -> key 8 + 7 = 15
-    assert valid[1, s] == 0 and valid[2, s] == 1  # query 10 (c = 1) / 18 (c = 2)
-    s = 8 * (64 * 3 + 13) + 6                 # lane 6 -> key 8 + 3 = 11, query 14
-    assert valid[1, s] == 1
-    s = 8 * (64 * 0 + 10) + 6                 # j = 10 (c' = 1, rho = 2), lane 6 -> key 8 + 0 = 8
-    assert valid[1, s] == 1
-    assert P.key_position(70) == 16384 + 48
+    # query ciphertext c keeps keys j < 4 (c + 1) at channel position j of the lower half and
+    # the others at j - 4 (c + 1) of the upper; key j = 8 c' + rho reaches lane t as token
+    # 8 c' + (t + rho) % 8
+    s = 8 * (64 * 3 + 5) + 2                  # head 3, position 5, lane 2
+    assert valid[1, s] == 1                   # c = 1: j = 5 (c' = 0) -> key 7 <= query 10
+    assert valid[1, 16384 + s] == 0           # j = 13 (c' = 1, rho = 5) -> key 15 > query 10
+    assert valid[1, 16384 + s + 4] == 1       # lane 6: key 8 + 3 = 11 <= query 14
+    assert valid[2, 16384 + s] == 0           # c = 2: j = 17 (c' = 2, rho = 1) -> key 19 > query 18
+    assert valid[2, 8 * (64 * 3 + 11) + 2] == 1   # j = 11 (c' = 1) in the lower half
+    assert valid[2, 8 * (64 * 3 + 12) + 2] == 0   # position 12 of the lower half is unused at c = 2
+    assert valid[0, 8 * 4] == 0 and valid[0, 16384 + 8 * 4] == 0   # position 4 is unused at c = 0
+    assert valid.sum() == 32 * sum(8 * c + t + 1 for c in range(16) for t in range(8))
+    assert P.key_slot(15, 70) == 16384 + 48 and P.key_slot(1, 10) == 16384 + 16 and P.key_slot(1, 7) == 56
     rots = P.attention_rotations()
     assert 16384 in rots and all(0 < r < 32768 for r in rots)
 
