@@ -17,6 +17,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 #include "modarith64.hpp"
 
 namespace hck {
@@ -244,6 +245,9 @@ extern "C" int hck_bsgs_mac(const hck_context* ctx, int limbs, const int* prime_
     if (prime_idx[l] < 0 || prime_idx[l] >= ctx->np) return HCK_ERR_ARG;
     mp.prime[l] = (uint8_t)prime_idx[l];
   }
+  if (ctx->wide)
+    return hck::wide_bsgs_mac(ctx, limbs, prime_idx, inputs, babies, giants, baby_c0, baby_c1, baby_stride, pts,
+                              pt_stride, res, (hipStream_t)stream);
   hck::BabyPtrs bp{};
   for (int b = 0; b < babies; ++b) {
     if (!baby_c0[b] || !baby_c1[b]) return HCK_ERR_ARG;

@@ -14,6 +14,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 using u64 = uint64_t;
 using u128 = unsigned __int128;
@@ -52,12 +53,19 @@ bool probable_prime(u64 n) {
   return true;
 }
 
-// A primitive 2N-th root of unity: g^((q-1)/2N) for the smallest quadratic non-residue g.
+}  // namespace
+
+namespace hck {
+// A primitive 2N-th root of unity: g^((q-1)/2N) for the smallest quadratic non-residue g (shared by
+// the FP64 and the wide tables).
 u64 primitive_root_2n(u64 q, int log_n) {
   const u64 two_n = (u64)2 << log_n;
   for (u64 g = 2;; ++g)
     if (powmod(g, (q - 1) / 2, q) == q - 1) return powmod(g, (q - 1) / two_n, q);
 }
+}  // namespace hck
+
+namespace {
 
 hck::TwPair pair_of(u64 w, u64 q) { return hck::TwPair{(double)w, (double)w / (double)q}; }
 
@@ -107,15 +115,20 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   const int np = num_q + num_p;
   const u64 two_n = (u64)2 << log_n;
   std::vector<u64> P(primes, primes + np);
+  // Every prime below 2^50: the FP64 path (modarith.hpp).  Otherwise the wide path (wide.hip), for
+  // primes in (2^31, 2^61).  Both need p = 1 mod 2N.
+  bool wide = false;
+  for (int i = 0; i < np; ++i) wide = wide || P[i] >= (1ULL << 50);
   for (int i = 0; i < np; ++i) {
-    // The FP64 path needs p < 2^50 (exactness bounds of modarith.hpp) and p = 1 mod 2N.
-    if (P[i] >= (1ULL << 50) || P[i] % two_n != 1 || !probable_prime(P[i])) return HCK_ERR_PRIME;
+    if (P[i] >= (wide ? hck::kWidePrimeLimit : (1ULL << 50)) || (wide && P[i] <= (1ULL << 31))) return HCK_ERR_PRIME;
+    if (P[i] % two_n != 1 || !probable_prime(P[i])) return HCK_ERR_PRIME;
     for (int j = 0; j < i; ++j) if (P[j] == P[i]) return HCK_ERR_PRIME;
   }
-  // Rescale reduces a [0, q_last) coefficient modulo q_i with one conditional subtraction.
-  for (int i = 0; i < np; ++i)
-    for (int j = 0; j < np; ++j)
-      if (P[i] >= 2 * P[j]) return HCK_ERR_PRIME;
+  // The FP64 rescale reduces a [0, q_last) coefficient modulo q_i with one conditional subtraction.
+  if (!wide)
+    for (int i = 0; i < np; ++i)
+      for (int j = 0; j < np; ++j)
+        if (P[i] >= 2 * P[j]) return HCK_ERR_PRIME;
 
   hck_context* c = new (std::nothrow) hck_context();
   if (!c) return HCK_ERR_ALLOC;
@@ -133,7 +146,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     const u64 q = P[i];
     hp[i] = (double)q;
     hpinv[i] = 1.0 / (double)q;
-    const u64 psi = primitive_root_2n(q, log_n), ipsi = invmod(psi, q);
+    const u64 psi = hck::primitive_root_2n(q, log_n), ipsi = invmod(psi, q);
     u64 a = 1, b = 1;
     for (size_t k = 0; k < n; ++k) {
       const size_t r = brv(k, log_n);
@@ -282,18 +295,28 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->d_primes_u64 = (const u64*)(base + o_pu);
   c->d_enc_twr = (const double*)(base + o_etr);
   c->d_enc_twi = (const double*)(base + o_eti);
+  if (wide) {
+    const int rc = hck::wide_init(c);
+    if (rc) {
+      (void)hipFree(blk);
+      delete c;
+      return rc;
+    }
+  }
   *out = c;
   return HCK_OK;
 }
 
 extern "C" void hck_context_destroy(hck_context* ctx) {
   if (!ctx) return;
+  hck::wide_free(ctx);
   if (ctx->d_block) (void)hipFree(ctx->d_block);
   delete ctx;
 }
 
 extern "C" int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uint64_t* out) {
   if (!ctx || !out || prime_idx < 0 || prime_idx >= ctx->np) return HCK_ERR_ARG;
+  if (ctx->wide) return hck::wide_twiddles(ctx, prime_idx, inverse, out);
   const size_t n = (size_t)1 << ctx->log_n;
   std::vector<double> tmp(n);
   const double* src = (inverse ? ctx->dev.tw_inv : ctx->dev.tw_fwd) + (size_t)prime_idx * n;
@@ -323,7 +346,9 @@ extern "C" const char* hck_error_string(int code) {
     case HCK_OK: return "ok";
     case HCK_ERR_ARG: return "invalid argument";
     case HCK_ERR_UNSUPPORTED: return "unsupported parameter";
-    case HCK_ERR_PRIME: return "prime rejected (needs p < 2^50, p = 1 mod 2N, prime, distinct, within a factor 2 of the others)";
+    case HCK_ERR_PRIME:
+      return "prime rejected (needs p = 1 mod 2N, prime, distinct; all below 2^50 and within a factor 2 of each other, "
+             "or any of them at or above 2^50 and all in (2^31, 2^61))";
     case HCK_ERR_ALLOC: return "host allocation failed";
     case HCK_ERR_WORKSPACE: return "workspace too small";
     case HCK_ERR_SCRATCH:

@@ -8,6 +8,8 @@
 
 namespace hck {
 
+struct WideState;  // wide.hpp: tables of a context with a prime >= 2^50
+
 constexpr int kMaxPrimes = 64;  // Q + P primes
 constexpr int kMaxAlpha = 8;    // limbs per key-switching digit (fused ModUp holds them in LDS)
 constexpr int kMaxSpecial = 8;  // P primes (fused ModDown holds them in LDS)
@@ -50,6 +52,7 @@ struct DevTables {
 struct hck_context {
   int log_n, L, K, alpha, np;
   int ks_slices = 0;  // key-switch schedule: 0 / 1 sequential kernels, >= 2 pipelined slices (ksfused.hip)
+  hck::WideState* wide = nullptr;  // set for a context with a prime >= 2^50: every kernel runs on wide.hip
   std::vector<uint64_t> primes;
   hck::DevTables dev;
   // device allocations

@@ -33,6 +33,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 namespace hck {
 namespace {
@@ -1002,6 +1003,7 @@ int ks_wave(const hck_context* c, int ell, int batch, int slices, const uint64_t
 
 // Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)], ACCP [2 K].
 size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
+  if (c->wide) return wide_ks_bytes(c, ell, batch);
   const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
   return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * c->K);
 }
@@ -1011,6 +1013,9 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
              char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
              const uint32_t* galois_items) {
+  if (c->wide)
+    return wide_ks(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
+                   out_stride, ws, s, ext_b, ext_a, ext_stride, galois_items);
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch > kMaxBatchF) return HCK_ERR_ARG;
   GalF G = gal_uniform(galois);
@@ -1080,6 +1085,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
 }
 
 size_t moddown_bytes(const hck_context* c, int ell, int polys) {
+  if (c->wide) return wide_moddown_bytes(c, ell, polys);
   return (size_t)polys * kN * 8 * (size_t)(c->K + ell);
 }
 
@@ -1087,6 +1093,7 @@ size_t moddown_bytes(const hck_context* c, int ell, int polys) {
 // out[p] = (x_Q - NTT(conv(INTT(x_P)))) * P^-1 over the ell Q primes.
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                 long long out_stride, char* ws, hipStream_t s) {
+  if (c->wide) return wide_moddown(c, ell, polys, in, in_stride, out, out_stride, ws, s);
   if (c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   const int K = c->K;
   const long long n = kN;
@@ -1105,7 +1112,10 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   return HCK_OK;
 }
 
-size_t rescale_bytes(const hck_context* c, int ell, int polys) { return (size_t)polys * kN * 8 * (size_t)ell; }
+size_t rescale_bytes(const hck_context* c, int ell, int polys) {
+  if (c->wide) return wide_rescale_bytes(c, ell, polys);
+  return (size_t)polys * kN * 8 * (size_t)ell;
+}
 
 // Rescale = ModDown with q_{ell-1} as the one special prime: INTT rows of the last limb, then the
 // cols kernel (INTT cols, centered lift, spread to the ell - 1 lower primes, NTT cols), then the
@@ -1113,6 +1123,7 @@ size_t rescale_bytes(const hck_context* c, int ell, int polys) { return (size_t)
 // spread would move them three times).
 int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                   long long out_stride, char* ws, hipStream_t s) {
+  if (c->wide) return wide_rescale(c, ell, polys, in, in_stride, out, out_stride, ws, s);
   const long long n = kN;
   const int nt = ell - 1;
   double* tl = (double*)ws;                       // [polys][1] workspace layout
@@ -1130,13 +1141,17 @@ int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, 
   return HCK_OK;
 }
 
-size_t modraise_bytes(const hck_context* c, int to, int polys) { return (size_t)polys * kN * 8 * (size_t)to; }
+size_t modraise_bytes(const hck_context* c, int to, int polys) {
+  if (c->wide) return wide_modraise_bytes(c, to, polys);
+  return (size_t)polys * kN * 8 * (size_t)to;
+}
 
 // ModRaise on the conversion kernels: INTT rows of limb 0, the cols kernel (INTT cols, centered
 // lift, spread to q_1 .. q_{to-1}, NTT cols), NTT rows with a canonical store; limb 0 itself is
 // unchanged (the lift is congruent to it modulo q_0) and copied.
 int modraise_fused(const hck_context* c, int to, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                    long long out_stride, char* ws, hipStream_t s) {
+  if (c->wide) return wide_modraise(c, to, polys, in, in_stride, out, out_stride, ws, s);
   const long long n = kN;
   const int nt = to - 1;
   double* tl = (double*)ws;                       // [polys][1] workspace layout

@@ -10,6 +10,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 namespace hck {
 namespace {
@@ -82,6 +83,7 @@ __global__ __launch_bounds__(256) void k_lincomb(const LcPtrs P, int terms, cons
 int launch_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
                   const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1,
                   uint64_t* d2, long long d_stride, hipStream_t s) {
+  if (c->wide) return wide_tensor(c, ell, batch, a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride, s);
   k_tensor<<<dim3(kN / 256, ell, batch), 256, 0, s>>>(a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride,
                                                       c->dev);
   HCK_CHECK_LAUNCH();
@@ -174,6 +176,7 @@ extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int gr
   if (!ctx || !in || !weights || !out || limbs < 1 || limbs > ctx->L || n < 1 || groups < 0 || groups > 65535)
     return HCK_ERR_ARG;
   if (groups == 0) return HCK_OK;
+  if (ctx->wide) return hck::wide_weighted_sum(ctx, limbs, n, groups, in, in_stride, weights, out, out_stride, (hipStream_t)stream);
   hck::k_weighted_sum<<<dim3(hck::kN / 256, limbs, groups), 256, 0, (hipStream_t)stream>>>(
       in, in_stride, n, weights, out, out_stride, limbs, ctx->dev);
   HCK_CHECK_LAUNCH();
@@ -194,6 +197,7 @@ extern "C" int hck_lincomb(const hck_context* ctx, int limbs, int groups, int te
     if (!out[g]) return HCK_ERR_ARG;
     P.out[g] = out[g];
   }
+  if (ctx->wide) return hck::wide_lincomb(ctx, limbs, groups, terms, x, weights, out, (hipStream_t)stream);
   hck::k_lincomb<<<dim3(hck::kN / 256, limbs, groups), 256, 0, (hipStream_t)stream>>>(P, terms, weights, limbs,
                                                                                      ctx->dev);
   HCK_CHECK_LAUNCH();

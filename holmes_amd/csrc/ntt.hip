@@ -23,6 +23,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 namespace hck {
 namespace {
@@ -352,6 +353,10 @@ __global__ __launch_bounds__(kThreads) void k_encode_cols(const double* __restri
 
 int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s) {
+  if (c->wide) {
+    if (in != kU64 || out != kU64) return HCK_ERR_UNSUPPORTED;
+    return wide_ntt(c, (const uint64_t*)src, (uint64_t*)dst, groups, src_stride, dst_stride, list, false, s);
+  }
   if (list.n <= 0 || groups <= 0) return HCK_OK;
   if (list.n > kMaxList || groups > 65535) return HCK_ERR_ARG;
   const dim3 grid(16, list.n, groups);
@@ -369,6 +374,7 @@ int launch_ntt_fwd(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
 
 int launch_encode_ntt(const hck_context* c, const double* vre, const double* vim, double scale, uint64_t* out,
                       long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s) {
+  if (c->wide) return wide_encode_ntt(c, vre, vim, scale, out, out_stride, rows, overflow, list, s);
   if (list.n <= 0 || rows <= 0) return HCK_OK;
   if (list.n > kMaxList || rows > 65535) return HCK_ERR_ARG;
   k_encode_cols<<<dim3(16, rows), kThreads, 0, s>>>(vre, vim, scale, (double*)out, out_stride, list, overflow,
@@ -380,6 +386,10 @@ int launch_encode_ntt(const hck_context* c, const double* vre, const double* vim
 
 int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt out, int groups,
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s) {
+  if (c->wide) {
+    if (in != kU64 || out != kU64) return HCK_ERR_UNSUPPORTED;
+    return wide_ntt(c, (const uint64_t*)src, (uint64_t*)dst, groups, src_stride, dst_stride, list, true, s);
+  }
   if (list.n <= 0 || groups <= 0) return HCK_OK;
   if (list.n > kMaxList || groups > 65535) return HCK_ERR_ARG;
   const dim3 grid(16, list.n, groups);

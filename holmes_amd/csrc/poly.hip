@@ -5,6 +5,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 namespace hck {
 namespace {
@@ -104,6 +105,7 @@ extern "C" int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const 
                            void* stream) {
   if (!ctx || !out || !a || !prime_idx || polys < 0 || polys > 65535) return HCK_ERR_ARG;
   if (limbs < 0 || limbs > hck::kMaxPrimes) return HCK_ERR_ARG;
+  if (op < HCK_OP_ADD || op > HCK_OP_ADD_SCALAR) return HCK_ERR_ARG;
   const bool binary = op == HCK_OP_ADD || op == HCK_OP_SUB || op == HCK_OP_MUL || op == HCK_OP_MAC;
   if (binary && !b) return HCK_ERR_ARG;
   const bool with_scalar = op == HCK_OP_MUL_SCALAR || op == HCK_OP_ADD_SCALAR;
@@ -120,6 +122,9 @@ extern "C" int hck_poly_op(const hck_context* ctx, int op, uint64_t* out, const 
     }
   }
   if (polys == 0 || limbs == 0) return HCK_OK;
+  if (ctx->wide)
+    return hck::wide_poly_op(ctx, op, out, a, b, polys, out_stride, a_stride, b_stride, limbs, prime_idx, scalar,
+                             (hipStream_t)stream);
   const dim3 grid(hck::kN / 256, limbs, polys);
   hipStream_t s = (hipStream_t)stream;
   switch (op) {

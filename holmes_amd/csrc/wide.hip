@@ -1,0 +1,979 @@
+// The wide-prime path (primes in (2^31, 2^61), any of them >= 2^50): every kernel of the library's
+// internal entry points restated on 64-bit integer words.  Residues are canonical in [0, p) in HBM
+// and between stages; products by constants (twiddles, base-conversion factors, P^-1, N^-1) use
+// Shoup's precomputed quotient, products of two variables (keys, plaintexts, ciphertext tensors)
+// Barrett's reduction (modarith64.hpp).  The algorithms are the FP64 path's -- two-pass negacyclic
+// NTT (256 x 256, LDS-staged), hybrid key switch (ModUp by the centered fast base conversion, key
+// inner product, ModDown), rescale and ModRaise by the centered lift -- and produce the same
+// residues as the CPU oracle, which is exact for any prime below 2^62.
+//
+// The kernels favour plainness over speed: the key switch runs as separate launches (INTT, one
+// conversion + NTT + inner product per digit, ModDown per component) over chunks of kWideChunk
+// items with its intermediates in the workspace.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "../../include/holmes_ckks.h"
+#include "internal.hpp"
+#include "modarith64.hpp"
+#include "wide.hpp"
+
+using u64 = uint64_t;
+using u128 = unsigned __int128;
+
+namespace hck {
+namespace {
+
+// ------------------------------------------------------------------------------------ host helpers
+u64 hmul(u64 a, u64 b, u64 q) { return (u64)((u128)a * b % q); }
+u64 hpow(u64 b, u64 e, u64 q) {
+  u64 r = 1;
+  b %= q;
+  while (e) {
+    if (e & 1) r = hmul(r, b, q);
+    b = hmul(b, b, q);
+    e >>= 1;
+  }
+  return r;
+}
+u64 hinv(u64 a, u64 q) { return hpow(a % q, q - 2, q); }
+u64 hbrv(u64 x, int bits) {
+  u64 r = 0;
+  for (int i = 0; i < bits; ++i) {
+    r = (r << 1) | (x & 1);
+    x >>= 1;
+  }
+  return r;
+}
+
+void fill_wide_conv(WideConv& cc, const std::vector<u64>& P, const std::vector<int>& src, const std::vector<int>& dst,
+                    const std::vector<int>& slot) {
+  std::memset(&cc, 0, sizeof(cc));
+  cc.ns = (int)src.size();
+  cc.nt = (int)dst.size();
+  for (int s = 0; s < cc.ns; ++s) {
+    const u64 bs = P[src[s]];
+    u64 h = 1;
+    for (int r = 0; r < cc.ns; ++r)
+      if (r != s) h = hmul(h, P[src[r]] % bs, bs);
+    cc.src_prime[s] = src[s];
+    cc.hinv[s] = hinv(h, bs);
+    cc.hinv_s[s] = shoup_companion(cc.hinv[s], bs);
+    for (int t = 0; t < cc.nt; ++t) {
+      const u64 qt = P[dst[t]];
+      u64 v = 1;
+      for (int r = 0; r < cc.ns; ++r)
+        if (r != s) v = hmul(v, P[src[r]] % qt, qt);
+      cc.hmod[s][t] = v;
+      cc.hmod_s[s][t] = shoup_companion(v, qt);
+    }
+  }
+  for (int t = 0; t < cc.nt; ++t) {
+    cc.dst_prime[t] = dst[t];
+    cc.dst_slot[t] = slot[t];
+  }
+}
+
+// ---------------------------------------------------------------------------------- device helpers
+__device__ __forceinline__ u64 wadd(u64 a, u64 b, u64 p) {
+  const u64 s = a + b;
+  return s >= p ? s - p : s;
+}
+__device__ __forceinline__ u64 wsub(u64 a, u64 b, u64 p) { return a >= b ? a - b : a + p - b; }
+// a * w mod p, canonical, for any 64-bit a (Shoup: the lazy result lies in [0, 2p)).
+__device__ __forceinline__ u64 wmulc(u64 a, u64 w, u64 ws, u64 p) {
+  const u64 r = mulshoup_lazy(a, w, ws, p);
+  return r >= p ? r - p : r;
+}
+__device__ __forceinline__ Barrett64 wbar(const WideTables& T, int pi) { return Barrett64{T.p[pi], T.mu[pi], T.w[pi]}; }
+
+// ---------------------------------------------------------------------------------------------- NTT
+// Forward transform (Cooley-Tukey, psi^brv roots, bit-reversed evaluation order out), as two passes
+// (src == dst allowed: a block reads its 16 columns or rows whole before it writes them back)
+// over the 256 x 256 view of a limb (element 256 r + c): the first eight stages act on the columns
+// (fixed c, a 256-point transform over r with root psi_rev[m + r-group]), the last eight on the rows.
+// A block holds 16 columns or 16 rows (32 KiB of LDS); 256 threads, 8 butterflies each per stage.
+constexpr int kWT = 256;
+
+__global__ __launch_bounds__(kWT) void wk_fwd_cols(const u64* src, u64* dst, long long ss,
+                                                   long long ds, LimbList list, WideTables T) {
+  __shared__ u64 sh[256 * 16];
+  const int e = blockIdx.y;
+  const long long g = blockIdx.z;
+  const int pi = list.prime[e];
+  const u64 p = T.p[pi];
+  const u64* tw = T.fwd + (size_t)pi * kN;
+  const u64* tws = T.fwd_s + (size_t)pi * kN;
+  const u64* in = src + g * ss + (long long)list.off[e] * kN;
+  u64* out = dst + g * ds + (long long)list.off[e] * kN;
+  const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int k = r + 16 * m;
+    sh[k * 16 + cl] = in[c + 256 * k];
+  }
+  __syncthreads();
+  for (int s = 0; s < 8; ++s) {
+    const int m = 1 << s, t = 128 >> s;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = r + 16 * u;
+      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
+      const int wi = m + b / t;
+      const u64 x = sh[k1 * 16 + cl];
+      const u64 y = wmulc(sh[k2 * 16 + cl], tw[wi], tws[wi], p);
+      sh[k1 * 16 + cl] = wadd(x, y, p);
+      sh[k2 * 16 + cl] = wsub(x, y, p);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int k = r + 16 * m;
+    out[c + 256 * k] = sh[k * 16 + cl];
+  }
+}
+
+__global__ __launch_bounds__(kWT) void wk_fwd_rows(u64* __restrict__ dst, long long ds, LimbList list, WideTables T) {
+  __shared__ u64 sh[16 * 256];
+  const int e = blockIdx.y;
+  const long long g = blockIdx.z;
+  const int pi = list.prime[e];
+  const u64 p = T.p[pi];
+  const u64* tw = T.fwd + (size_t)pi * kN;
+  const u64* tws = T.fwd_s + (size_t)pi * kN;
+  u64* io = dst + g * ds + (long long)list.off[e] * kN + (long long)blockIdx.x * 4096;
+  const int tid = threadIdx.x, rr = tid >> 4, lane = tid & 15, r = blockIdx.x * 16 + rr;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) sh[tid + 256 * m] = io[tid + 256 * m];
+  __syncthreads();
+  for (int s = 0; s < 8; ++s) {
+    const int t = 128 >> s, m = 256 << s;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = lane + 16 * u;
+      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
+      const int wi = m + r * (128 / t) + b / t;
+      const u64 x = sh[rr * 256 + k1];
+      const u64 y = wmulc(sh[rr * 256 + k2], tw[wi], tws[wi], p);
+      sh[rr * 256 + k1] = wadd(x, y, p);
+      sh[rr * 256 + k2] = wsub(x, y, p);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) io[tid + 256 * m] = sh[tid + 256 * m];
+}
+
+// Inverse transform (Gentleman-Sande with psi^-brv roots, then N^-1): the first eight stages act
+// on the rows, the last eight on the columns, which also apply N^-1.
+__global__ __launch_bounds__(kWT) void wk_inv_rows(const u64* src, u64* dst, long long ss,
+                                                   long long ds, LimbList list, WideTables T) {
+  __shared__ u64 sh[16 * 256];
+  const int e = blockIdx.y;
+  const long long g = blockIdx.z;
+  const int pi = list.prime[e];
+  const u64 p = T.p[pi];
+  const u64* tw = T.inv + (size_t)pi * kN;
+  const u64* tws = T.inv_s + (size_t)pi * kN;
+  const u64* in = src + g * ss + (long long)list.off[e] * kN + (long long)blockIdx.x * 4096;
+  u64* out = dst + g * ds + (long long)list.off[e] * kN + (long long)blockIdx.x * 4096;
+  const int tid = threadIdx.x, rr = tid >> 4, lane = tid & 15, r = blockIdx.x * 16 + rr;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) sh[tid + 256 * m] = in[tid + 256 * m];
+  __syncthreads();
+  for (int s = 0; s < 8; ++s) {
+    const int t = 1 << s, h = (kN / 2) >> s;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = lane + 16 * u;
+      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
+      const int wi = h + r * (128 / t) + b / t;
+      const u64 x = sh[rr * 256 + k1], y = sh[rr * 256 + k2];
+      sh[rr * 256 + k1] = wadd(x, y, p);
+      sh[rr * 256 + k2] = wmulc(wsub(x, y, p), tw[wi], tws[wi], p);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) out[tid + 256 * m] = sh[tid + 256 * m];
+}
+
+__global__ __launch_bounds__(kWT) void wk_inv_cols(u64* __restrict__ dst, long long ds, LimbList list, WideTables T) {
+  __shared__ u64 sh[256 * 16];
+  const int e = blockIdx.y;
+  const long long g = blockIdx.z;
+  const int pi = list.prime[e];
+  const u64 p = T.p[pi];
+  const u64* tw = T.inv + (size_t)pi * kN;
+  const u64* tws = T.inv_s + (size_t)pi * kN;
+  const u64 ni = T.ninv[pi], nis = T.ninv_s[pi];
+  u64* io = dst + g * ds + (long long)list.off[e] * kN;
+  const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int k = r + 16 * m;
+    sh[k * 16 + cl] = io[c + 256 * k];
+  }
+  __syncthreads();
+  for (int s = 0; s < 8; ++s) {
+    const int t = 1 << s, h = 128 >> s;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = r + 16 * u;
+      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
+      const int wi = h + b / t;
+      const u64 x = sh[k1 * 16 + cl], y = sh[k2 * 16 + cl];
+      sh[k1 * 16 + cl] = wadd(x, y, p);
+      sh[k2 * 16 + cl] = wmulc(wsub(x, y, p), tw[wi], tws[wi], p);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int k = r + 16 * m;
+    io[c + 256 * k] = wmulc(sh[k * 16 + cl], ni, nis, p);
+  }
+}
+
+// ----------------------------------------------------------------------------- base conversion
+// dst[item][slot t][k] = sum_s ybar_s * (B / b_s) mod t, ybar_s the centered representative of
+// y_s = x_s (B / b_s)^-1 mod b_s (the oracle's base_conv).  Sources are the ns consecutive limbs from
+// src_off.  Grid (N / 256, items).
+__global__ __launch_bounds__(256) void wk_conv(const u64* __restrict__ src, long long src_item, int src_off,
+                                               u64* __restrict__ dst, long long dst_item,
+                                               const WideConv* __restrict__ cc, WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const long long it = blockIdx.y;
+  const int ns = cc->ns, nt = cc->nt;
+  u64 y[kMaxAlpha];
+  bool neg[kMaxAlpha];
+#pragma unroll
+  for (int s = 0; s < kMaxAlpha; ++s) {
+    y[s] = 0;
+    neg[s] = false;
+    if (s < ns) {
+      const u64 b = T.p[cc->src_prime[s]];
+      const u64 v = wmulc(src[it * src_item + (long long)(src_off + s) * kN + k], cc->hinv[s], cc->hinv_s[s], b);
+      neg[s] = 2 * v > b;
+      y[s] = neg[s] ? b - v : v;
+    }
+  }
+  for (int t = 0; t < nt; ++t) {
+    const u64 q = T.p[cc->dst_prime[t]];
+    u64 acc = 0;
+#pragma unroll
+    for (int s = 0; s < kMaxAlpha; ++s) {
+      if (s >= ns) break;
+      const u64 prod = wmulc(y[s], cc->hmod[s][t], cc->hmod_s[s][t], q);
+      acc = neg[s] ? wsub(acc, prod, q) : wadd(acc, prod, q);
+    }
+    dst[it * dst_item + (long long)cc->dst_slot[t] * kN + k] = acc;
+  }
+}
+
+// The centered lift of one coefficient-domain limb (prime src_pi) to limbs first .. first + gridDim.y - 1
+// (limb i modulo prime i).  Grid (N / 256, targets, items).
+__global__ __launch_bounds__(256) void wk_lift(const u64* __restrict__ src, long long src_item, int src_pi,
+                                               u64* __restrict__ dst, long long dst_item, int first, WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = first + blockIdx.y;
+  const long long it = blockIdx.z;
+  const u64 ql = T.p[src_pi];
+  const Barrett64 br = wbar(T, i);
+  const u64 v = src[it * src_item + k];
+  u64 r;
+  if (2 * v > ql) {
+    const u64 m = barrett_reduce((u128)(ql - v), br);
+    r = m ? br.p - m : 0;
+  } else {
+    r = barrett_reduce((u128)v, br);
+  }
+  dst[it * dst_item + (long long)i * kN + k] = r;
+}
+
+// --------------------------------------------------------------------------------- key switch parts
+struct WKeys {
+  const u64* k[kWideChunk];
+};
+struct WGal {
+  uint32_t g[kWideChunk];
+};
+
+__device__ __forceinline__ uint32_t wbrv16(uint32_t x) { return __brev(x) >> 16; }
+
+// sigma_g of every limb of item it with g = G.g[it] (NTT domain).  Grid (N / 256, limbs, items).
+__global__ __launch_bounds__(256) void wk_automorph(const u64* __restrict__ in, long long in_item,
+                                                    u64* __restrict__ out, long long out_item, WGal G) {
+  const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+  const long long it = blockIdx.z, limb = blockIdx.y;
+  const uint32_t e = ((2u * wbrv16(k) + 1u) * G.g[it]) & (2u * kN - 1u);
+  const uint32_t src = wbrv16((e - 1u) >> 1);
+  out[it * out_item + limb * kN + k] = in[it * in_item + limb * kN + src];
+}
+
+// acc[item][comp][e] (+)= x[e] * key_j[comp][prime(e)], x the ModUp output (the digit's own limbs
+// read from the NTT-domain input d).  acc per item: [2][ell + K][N].  Grid (N / 256, ell + K, items).
+__global__ __launch_bounds__(256) void wk_ks_ip(const u64* __restrict__ ext, long long ext_item,
+                                                const u64* __restrict__ d, long long d_item, int lo, int hi, WKeys keys,
+                                                int j, int ell, int L, int K, int beta_max, u64* __restrict__ acc,
+                                                long long acc_item, int first, WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int e = blockIdx.y;
+  const long long it = blockIdx.z;
+  const int pi = e < ell ? e : L + (e - ell);
+  const Barrett64 br = wbar(T, pi);
+  const u64 x = (e >= lo && e < hi) ? d[it * d_item + (long long)e * kN + k] : ext[it * ext_item + (long long)e * kN + k];
+  const u64* key = keys.k[it];
+  const long long comp = (long long)beta_max * (L + K) * kN;
+  const long long ko = ((long long)j * (L + K) + pi) * kN + k;
+  const u64 pb = mulmod64(x, key[ko], br), pa = mulmod64(x, key[comp + ko], br);
+  u64* ab = acc + it * acc_item + (long long)e * kN + k;
+  u64* aa = ab + (long long)(ell + K) * kN;
+  if (first) {
+    *ab = pb;
+    *aa = pa;
+  } else {
+    *ab = wadd(*ab, pb, br.p);
+    *aa = wadd(*aa, pa, br.p);
+  }
+}
+
+// out[i] = (x[i] - cv[i]) P^-1 mod q_i (+ add1[i]) (+ add2[i]).  Grid (N / 256, ell, items).
+__global__ __launch_bounds__(256) void wk_ks_out(const u64* x, long long x_item, const u64* __restrict__ cv,
+                                                 long long cv_item, const u64* add1, long long add1_item,
+                                                 const u64* add2, long long add2_item, u64* out, long long out_item,
+                                                 const u64* __restrict__ fac, const u64* __restrict__ fac_s,
+                                                 WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  const long long it = blockIdx.z;
+  const u64 q = T.p[i];
+  const long long o = (long long)i * kN + k;
+  u64 v = wmulc(wsub(x[it * x_item + o], cv[it * cv_item + o], q), fac[i], fac_s[i], q);
+  if (add1) v = wadd(v, add1[it * add1_item + o], q);
+  if (add2) v = wadd(v, add2[it * add2_item + o], q);
+  out[it * out_item + o] = v;
+}
+
+// Extended-basis output: out[e] = acc[e] (+ P * s0[e] on the Q limbs) (+ add[e]).  Grid (N / 256, ell + K, items).
+__global__ __launch_bounds__(256) void wk_ks_ext_out(const u64* __restrict__ acc, long long acc_item,
+                                                     const u64* __restrict__ s0, long long s0_item, const u64* add,
+                                                     long long add_item, u64* out, long long out_item, int ell, int L,
+                                                     WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int e = blockIdx.y;
+  const long long it = blockIdx.z;
+  const int pi = e < ell ? e : L + (e - ell);
+  const u64 q = T.p[pi];
+  const long long o = (long long)e * kN + k;
+  u64 v = acc[it * acc_item + o];
+  if (s0 && e < ell) v = wadd(v, wmulc(s0[it * s0_item + o], T.pmod[pi], T.pmod_s[pi], q), q);
+  if (add) v = wadd(v, add[it * add_item + o], q);
+  out[it * out_item + o] = v;
+}
+
+// ------------------------------------------------------------------------------------ elementwise
+struct WPrimeMap {
+  uint8_t prime[kMaxPrimes];
+};
+struct WScalars {
+  u64 s[kMaxPrimes];
+  u64 ss[kMaxPrimes];
+};
+
+template <int OP>
+__global__ __launch_bounds__(256) void wk_poly_op(u64* out, const u64* a, const u64* b, long long out_stride,
+                                                  long long a_stride, long long b_stride, WPrimeMap pm, WScalars sc,
+                                                  WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int limb = blockIdx.y;
+  const int pi = pm.prime[limb];
+  const u64 p = T.p[pi];
+  const long long lo = (long long)limb * kN + k;
+  const long long z = blockIdx.z;
+  const u64 x = a[z * a_stride + lo];
+  u64 r;
+  if constexpr (OP == HCK_OP_ADD) {
+    r = wadd(x, b[z * b_stride + lo], p);
+  } else if constexpr (OP == HCK_OP_SUB) {
+    r = wsub(x, b[z * b_stride + lo], p);
+  } else if constexpr (OP == HCK_OP_NEG) {
+    r = x ? p - x : 0;
+  } else if constexpr (OP == HCK_OP_MUL) {
+    r = mulmod64(x, b[z * b_stride + lo], wbar(T, pi));
+  } else if constexpr (OP == HCK_OP_MAC) {
+    r = wadd(out[z * out_stride + lo], mulmod64(x, b[z * b_stride + lo], wbar(T, pi)), p);
+  } else if constexpr (OP == HCK_OP_MUL_SCALAR) {
+    r = wmulc(x, sc.s[limb], sc.ss[limb], p);
+  } else if constexpr (OP == HCK_OP_ADD_SCALAR) {
+    r = wadd(x, sc.s[limb], p);
+  } else {  // HCK_OP_MUL_XHALF: zeta4 on the slots k < N/2, -zeta4 above
+    const u64 m = wmulc(x, T.zeta4[pi], T.zeta4_s[pi], p);
+    r = k < kN / 2 ? m : (m ? p - m : 0);
+  }
+  out[z * out_stride + lo] = r;
+}
+
+__global__ __launch_bounds__(256) void wk_tensor(const u64* __restrict__ a0, const u64* __restrict__ a1, long long as,
+                                                 const u64* __restrict__ b0, const u64* __restrict__ b1, long long bs,
+                                                 u64* __restrict__ d0, u64* __restrict__ d1, u64* __restrict__ d2,
+                                                 long long dst, WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  const long long z = blockIdx.z;
+  const Barrett64 br = wbar(T, i);
+  const long long lo = (long long)i * kN + k;
+  const u64 x0 = a0[z * as + lo], x1 = a1[z * as + lo], y0 = b0[z * bs + lo], y1 = b1[z * bs + lo];
+  d0[z * dst + lo] = mulmod64(x0, y0, br);
+  d1[z * dst + lo] = wadd(mulmod64(x0, y1, br), mulmod64(x1, y0, br), br.p);
+  d2[z * dst + lo] = mulmod64(x1, y1, br);
+}
+
+__global__ __launch_bounds__(256) void wk_weighted_sum(const u64* __restrict__ in, long long in_stride, int n,
+                                                       const u64* __restrict__ w, u64* __restrict__ out,
+                                                       long long out_stride, int limbs, WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  const long long g = blockIdx.z;
+  const Barrett64 br = wbar(T, i);
+  const u64* wg = w + g * (long long)n * limbs + i;
+  const u64* x = in + (long long)i * kN + k;
+  u64 acc = 0;
+  for (int j = 0; j < n; ++j) acc = wadd(acc, mulmod64(x[(long long)j * in_stride], wg[(long long)j * limbs], br), br.p);
+  out[g * out_stride + (long long)i * kN + k] = acc;
+}
+
+constexpr int kWLcMaxPtrs = 256;
+constexpr int kWLcMaxGroups = 64;
+struct WLcPtrs {
+  const u64* x[kWLcMaxPtrs];
+  u64* out[kWLcMaxGroups];
+};
+
+__global__ __launch_bounds__(256) void wk_lincomb(const WLcPtrs P, int terms, const u64* __restrict__ w, int limbs,
+                                                  WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y, g = blockIdx.z;
+  const Barrett64 br = wbar(T, i);
+  const long long off = (long long)i * kN + k;
+  u64 acc = 0;
+  for (int t = 0; t < terms; ++t) {
+    const u64 x = P.x[g * terms + t][off];
+    acc = wadd(acc, w ? mulmod64(x, w[(long long)t * limbs + i], br) : x, br.p);
+  }
+  P.out[g][off] = acc;
+}
+
+constexpr int kWMaxBabies = 64;
+struct WMac {
+  const u64* c0[kWMaxBabies];
+  const u64* c1[kWMaxBabies];
+};
+
+// res[c][g][i][l][k] = sum_b pts[g B + b][l][k] * baby_b[c][i][l][k] (mod q_l).  Grid (N / 256, limbs, giants * inputs).
+__global__ __launch_bounds__(256) void wk_bsgs_mac(const WMac P, long long baby_stride, const u64* __restrict__ pts,
+                                                   long long pt_stride, u64* __restrict__ res, int inputs, int babies,
+                                                   int giants, int limbs, WPrimeMap pm, WideTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int l = blockIdx.y;
+  const int g = blockIdx.z / inputs, i = blockIdx.z % inputs;
+  const Barrett64 br = wbar(T, pm.prime[l]);
+  const long long lo = (long long)l * kN + k;
+  u64 acc0 = 0, acc1 = 0;
+  for (int b = 0; b < babies; ++b) {
+    const u64 w = pts[(long long)(g * babies + b) * pt_stride + lo];
+    acc0 = wadd(acc0, mulmod64(P.c0[b][(long long)i * baby_stride + lo], w, br), br.p);
+    acc1 = wadd(acc1, mulmod64(P.c1[b][(long long)i * baby_stride + lo], w, br), br.p);
+  }
+  const long long off = ((long long)g * inputs + i) * limbs * kN + lo;
+  res[off] = acc0;
+  res[(long long)giants * inputs * limbs * kN + off] = acc1;
+}
+
+// ---------------------------------------------------------------------------------------- encode
+constexpr double kWideEncodeCap = 2305843009213693952.0;  // 2^61, as the FP64 path
+
+// Rounded coefficients of the special IFFT's output (the FP64 path's expression, contraction off),
+// reduced modulo every listed prime (coefficient domain).  Grid (N / 256, rows).
+__global__ __launch_bounds__(256) void wk_encode_round(const double* __restrict__ vre, const double* __restrict__ vim,
+                                                       double scale, u64* __restrict__ out, long long out_stride,
+                                                       LimbList list, int* __restrict__ overflow, WideTables T) {
+  const int n = blockIdx.x * 256 + threadIdx.x;
+  const long long row = blockIdx.y;
+  const double* re = vre + row * (kN / 2);
+  const double* im = vim + row * (kN / 2);
+  double a;
+  {
+#pragma clang fp contract(off)
+    const double inv_n = 1.0 / (double)(kN / 2);
+    const int h = n >= kN / 2;
+    const int slot = (int)(__brev((unsigned)(n - h * (kN / 2))) >> (32 - (kLogN - 1)));
+    const double w = (h ? im : re)[slot] * inv_n;
+    a = round_away(w * scale);
+  }
+  const bool big = !(fabs(a) < kWideEncodeCap);
+  if (big) overflow[row] = 1;
+  const u64 mag = big ? 0 : (u64)fabs(a);
+  u64* d = out + row * out_stride;
+  for (int e = 0; e < list.n; ++e) {
+    const Barrett64 br = wbar(T, list.prime[e]);
+    const u64 r = barrett_reduce((u128)mag, br);
+    d[(long long)list.off[e] * kN + n] = (a < 0 && r) ? br.p - r : r;
+  }
+}
+
+}  // namespace
+
+// ======================================================================================= set-up
+u64 primitive_root_2n(u64 q, int log_n);  // context.hip: the root choice every table shares
+
+int wide_init(hck_context* c) {
+  const int L = c->L, K = c->K, alpha = c->alpha, bmax = c->beta_max;
+  const size_t np = (size_t)c->np, n = kN;
+  const std::vector<u64>& P = c->primes;
+  std::vector<u64> p(np), mu(np), fwd(np * n), fwd_s(np * n), inv(np * n), inv_s(np * n), ninv(np), ninv_s(np),
+      z4(np), z4_s(np), pm(np), pm_s(np), pinv(np), pinv_s(np);
+  std::vector<int> w(np);
+  for (size_t i = 0; i < np; ++i) {
+    const u64 q = P[i];
+    const Barrett64 b = barrett_make(q);
+    p[i] = q;
+    mu[i] = b.mu;
+    w[i] = b.w;
+    const u64 psi = primitive_root_2n(q, kLogN), ipsi = hinv(psi, q);
+    u64 a = 1, bb = 1;
+    for (size_t k = 0; k < n; ++k) {
+      const size_t r = hbrv(k, kLogN);
+      fwd[i * n + r] = a;
+      inv[i * n + r] = bb;
+      a = hmul(a, psi, q);
+      bb = hmul(bb, ipsi, q);
+    }
+    for (size_t k = 0; k < n; ++k) {
+      fwd_s[i * n + k] = shoup_companion(fwd[i * n + k], q);
+      inv_s[i * n + k] = shoup_companion(inv[i * n + k], q);
+    }
+    ninv[i] = hinv(n % q, q);
+    ninv_s[i] = shoup_companion(ninv[i], q);
+    z4[i] = hpow(psi, n / 2, q);
+    z4_s[i] = shoup_companion(z4[i], q);
+    u64 pp = 1;
+    for (int k = 0; k < K; ++k) pp = hmul(pp, P[L + k] % q, q);
+    pm[i] = i < (size_t)L ? pp : 0;
+    pm_s[i] = shoup_companion(pm[i], q);
+    pinv[i] = i < (size_t)L ? hinv(pp, q) : 0;
+    pinv_s[i] = shoup_companion(pinv[i], q);
+  }
+  std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1));
+  std::vector<u64> ql((size_t)(L + 1) * L, 0), ql_s((size_t)(L + 1) * L, 0);
+  for (int ell = 1; ell <= L; ++ell) {
+    const int beta = (ell + alpha - 1) / alpha;
+    for (int j = 0; j < beta; ++j) {
+      const int lo = j * alpha, hi = std::min(lo + alpha, ell);
+      std::vector<int> src, dst, slot;
+      for (int i = lo; i < hi; ++i) src.push_back(i);
+      for (int e = 0; e < ell + K; ++e) {
+        if (e >= lo && e < hi) continue;
+        dst.push_back(e < ell ? e : L + (e - ell));
+        slot.push_back(e);
+      }
+      fill_wide_conv(modup[(size_t)ell * bmax + j], P, src, dst, slot);
+    }
+    std::vector<int> src, dst, slot;
+    for (int k = 0; k < K; ++k) src.push_back(L + k);
+    for (int i = 0; i < ell; ++i) {
+      dst.push_back(i);
+      slot.push_back(i);
+    }
+    fill_wide_conv(moddown[ell], P, src, dst, slot);
+    for (int i = 0; i + 1 < ell; ++i) {
+      const u64 v = hinv(P[ell - 1] % P[i], P[i]);
+      ql[(size_t)ell * L + i] = v;
+      ql_s[(size_t)ell * L + i] = shoup_companion(v, P[i]);
+    }
+  }
+
+  auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  struct Part {
+    const void* src;
+    size_t bytes;
+    size_t off;
+  };
+  std::vector<Part> parts = {
+      {p.data(), np * 8}, {mu.data(), np * 8}, {w.data(), np * sizeof(int)},
+      {fwd.data(), fwd.size() * 8}, {fwd_s.data(), fwd_s.size() * 8}, {inv.data(), inv.size() * 8},
+      {inv_s.data(), inv_s.size() * 8}, {ninv.data(), np * 8}, {ninv_s.data(), np * 8},
+      {z4.data(), np * 8}, {z4_s.data(), np * 8}, {pm.data(), np * 8}, {pm_s.data(), np * 8},
+      {pinv.data(), np * 8}, {pinv_s.data(), np * 8},
+      {modup.data(), modup.size() * sizeof(WideConv)}, {moddown.data(), moddown.size() * sizeof(WideConv)},
+      {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8},
+  };
+  size_t off = 0;
+  for (Part& pt : parts) {
+    pt.off = off;
+    off = align(off + pt.bytes);
+  }
+  WideState* ws = new (std::nothrow) WideState();
+  if (!ws) return HCK_ERR_ALLOC;
+  hipError_t e = hipMalloc(&ws->block, off);
+  if (e != hipSuccess) {
+    delete ws;
+    return (int)e;
+  }
+  char* base = (char*)ws->block;
+  for (const Part& pt : parts) {
+    e = hipMemcpy(base + pt.off, pt.src, pt.bytes, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+      (void)hipFree(ws->block);
+      delete ws;
+      return (int)e;
+    }
+  }
+  auto at = [&](int i) { return base + parts[i].off; };
+  WideTables& T = ws->t;
+  T.p = (const u64*)at(0);
+  T.mu = (const u64*)at(1);
+  T.w = (const int*)at(2);
+  T.fwd = (const u64*)at(3);
+  T.fwd_s = (const u64*)at(4);
+  T.inv = (const u64*)at(5);
+  T.inv_s = (const u64*)at(6);
+  T.ninv = (const u64*)at(7);
+  T.ninv_s = (const u64*)at(8);
+  T.zeta4 = (const u64*)at(9);
+  T.zeta4_s = (const u64*)at(10);
+  T.pmod = (const u64*)at(11);
+  T.pmod_s = (const u64*)at(12);
+  T.pinv = (const u64*)at(13);
+  T.pinv_s = (const u64*)at(14);
+  ws->modup = (WideConv*)at(15);
+  ws->moddown = (WideConv*)at(16);
+  ws->qlast_inv = (u64*)at(17);
+  ws->qlast_inv_s = (u64*)at(18);
+  c->wide = ws;
+  return HCK_OK;
+}
+
+void wide_free(hck_context* c) {
+  if (!c->wide) return;
+  if (c->wide->block) (void)hipFree(c->wide->block);
+  delete c->wide;
+  c->wide = nullptr;
+}
+
+int wide_twiddles(const hck_context* c, int prime_idx, int inverse, uint64_t* out) {
+  const u64* src = (inverse ? c->wide->t.inv : c->wide->t.fwd) + (size_t)prime_idx * kN;
+  hipError_t e = hipMemcpy(out, src, (size_t)kN * 8, hipMemcpyDeviceToHost);
+  return e == hipSuccess ? HCK_OK : (int)e;
+}
+
+// ================================================================================== entry bodies
+int wide_ntt(const hck_context* c, const uint64_t* src, uint64_t* dst, int groups, long long src_stride,
+             long long dst_stride, const LimbList& list, bool inverse, hipStream_t s) {
+  if (list.n <= 0 || groups <= 0) return HCK_OK;
+  if (list.n > kMaxList || groups > 65535) return HCK_ERR_ARG;
+  const dim3 grid(16, list.n, groups);
+  const WideTables& T = c->wide->t;
+  if (!inverse) {
+    wk_fwd_cols<<<grid, kWT, 0, s>>>(src, dst, src_stride, dst_stride, list, T);
+    wk_fwd_rows<<<grid, kWT, 0, s>>>(dst, dst_stride, list, T);
+  } else {
+    wk_inv_rows<<<grid, kWT, 0, s>>>(src, dst, src_stride, dst_stride, list, T);
+    wk_inv_cols<<<grid, kWT, 0, s>>>(dst, dst_stride, list, T);
+  }
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int wide_encode_ntt(const hck_context* c, const double* vre, const double* vim, double scale, uint64_t* out,
+                    long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s) {
+  if (list.n <= 0 || rows <= 0) return HCK_OK;
+  if (list.n > kMaxList || rows > 65535) return HCK_ERR_ARG;
+  wk_encode_round<<<dim3(kN / 256, rows), 256, 0, s>>>(vre, vim, scale, out, out_stride, list, overflow, c->wide->t);
+  HCK_CHECK_LAUNCH();
+  return wide_ntt(c, out, out, rows, out_stride, out_stride, list, false, s);
+}
+
+namespace {
+LimbList q_list(int ell, int first = 0) {
+  LimbList l;
+  l.n = ell - first;
+  for (int i = first; i < ell; ++i) {
+    l.off[i - first] = (uint16_t)i;
+    l.prime[i - first] = (uint8_t)i;
+  }
+  return l;
+}
+}  // namespace
+
+// Per item: X (ell) + EXT (ell + K) + ACC (2 (ell + K)) + CV (ell) + SD (ell) + S0 (ell) limbs.
+size_t wide_ks_bytes(const hck_context* c, int ell, int batch) {
+  const size_t nb = (size_t)std::min(batch, kWideChunk);
+  return nb * (size_t)kN * 8 * (size_t)(7 * ell + 3 * c->K);
+}
+
+int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+            const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+            const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
+            char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
+            const uint32_t* galois_items) {
+  if (c->alpha > kMaxAlpha || ell + c->K > kMaxList) return HCK_ERR_UNSUPPORTED;
+  const WideState& W = *c->wide;
+  const WideTables& T = W.t;
+  const int K = c->K, L = c->L, alpha = c->alpha, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const long long n = kN;
+  const bool permute = galois_items != nullptr || galois != 1u;
+  const LimbList lq = q_list(ell);
+  LimbList lp;
+  lp.n = K;
+  for (int k = 0; k < K; ++k) {
+    lp.off[k] = (uint16_t)(ell + k);
+    lp.prime[k] = (uint8_t)(L + k);
+  }
+  for (int b0 = 0; b0 < batch; b0 += kWideChunk) {
+    const int nb = std::min(kWideChunk, batch - b0);
+    u64* X = (u64*)ws;
+    u64* EXT = X + (long long)nb * ell * n;
+    u64* ACC = EXT + (long long)nb * ext_l * n;
+    u64* CV = ACC + (long long)nb * 2 * ext_l * n;
+    u64* SD = CV + (long long)nb * ell * n;
+    u64* S0 = SD + (long long)nb * ell * n;
+    const u64* dd = d + (long long)b0 * d_stride;
+    long long dd_item = d_stride;
+    const u64* a0 = add ? add + (long long)b0 * add_stride : nullptr;
+    long long a0_item = add_stride;
+    if (permute) {
+      WGal G{};
+      for (int b = 0; b < nb; ++b) G.g[b] = galois_items ? galois_items[b0 + b] : galois;
+      wk_automorph<<<dim3(kN / 256, ell, nb), 256, 0, s>>>(dd, dd_item, SD, (long long)ell * n, G);
+      dd = SD;
+      dd_item = (long long)ell * n;
+      if (a0) {
+        wk_automorph<<<dim3(kN / 256, ell, nb), 256, 0, s>>>(a0, a0_item, S0, (long long)ell * n, G);
+        a0 = S0;
+        a0_item = (long long)ell * n;
+      }
+      HCK_CHECK_LAUNCH();
+    }
+    int rc = wide_ntt(c, dd, X, nb, dd_item, (long long)ell * n, lq, true, s);
+    if (rc) return rc;
+    WKeys kp{};
+    for (int b = 0; b < nb; ++b) kp.k[b] = ksk[b0 + b];
+    for (int j = 0; j < beta; ++j) {
+      const int lo = j * alpha, hi = std::min(lo + alpha, ell);
+      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(X, (long long)ell * n, lo, EXT, (long long)ext_l * n,
+                                                 W.modup + (size_t)ell * bmax + j, T);
+      HCK_CHECK_LAUNCH();
+      LimbList le;
+      le.n = 0;
+      for (int e = 0; e < ext_l; ++e) {
+        if (e >= lo && e < hi) continue;
+        le.off[le.n] = (uint16_t)e;
+        le.prime[le.n] = (uint8_t)(e < ell ? e : L + (e - ell));
+        ++le.n;
+      }
+      rc = wide_ntt(c, EXT, EXT, nb, (long long)ext_l * n, (long long)ext_l * n, le, false, s);
+      if (rc) return rc;
+      wk_ks_ip<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(EXT, (long long)ext_l * n, dd, dd_item, lo, hi, kp, j, ell, L, K,
+                                                         bmax, ACC, 2LL * ext_l * n, j == 0, T);
+      HCK_CHECK_LAUNCH();
+    }
+    if (ext_b) {
+      const long long ai = (long long)b0 * acc_stride, ei = (long long)b0 * ext_stride;
+      wk_ks_ext_out<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(ACC, 2LL * ext_l * n, a0, a0_item,
+                                                              acc_b ? acc_b + ai : nullptr, acc_stride, ext_b + ei,
+                                                              ext_stride, ell, L, T);
+      wk_ks_ext_out<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(ACC + (long long)ext_l * n, 2LL * ext_l * n, nullptr, 0,
+                                                              acc_a ? acc_a + ai : nullptr, acc_stride, ext_a + ei,
+                                                              ext_stride, ell, L, T);
+      HCK_CHECK_LAUNCH();
+      continue;
+    }
+    for (int comp = 0; comp < 2; ++comp) {
+      u64* A = ACC + (long long)comp * ext_l * n;
+      rc = wide_ntt(c, A, A, nb, 2LL * ext_l * n, 2LL * ext_l * n, lp, true, s);
+      if (rc) return rc;
+      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(A, 2LL * ext_l * n, ell, CV, (long long)ell * n, W.moddown + ell, T);
+      HCK_CHECK_LAUNCH();
+      rc = wide_ntt(c, CV, CV, nb, (long long)ell * n, (long long)ell * n, lq, false, s);
+      if (rc) return rc;
+      const u64* accin = comp == 0 ? acc_b : acc_a;
+      u64* o = (comp == 0 ? out_b : out_a) + (long long)b0 * out_stride;
+      wk_ks_out<<<dim3(kN / 256, ell, nb), 256, 0, s>>>(
+          A, 2LL * ext_l * n, CV, (long long)ell * n, comp == 0 ? a0 : nullptr, a0_item,
+          accin ? accin + (long long)b0 * acc_stride : nullptr, acc_stride, o, out_stride, T.pinv, T.pinv_s, T);
+      HCK_CHECK_LAUNCH();
+    }
+  }
+  return HCK_OK;
+}
+
+size_t wide_moddown_bytes(const hck_context* c, int ell, int polys) {
+  return (size_t)polys * kN * 8 * (size_t)(c->K + ell);
+}
+
+int wide_moddown(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                 long long out_stride, char* ws, hipStream_t s) {
+  const WideState& W = *c->wide;
+  const int K = c->K, L = c->L;
+  const long long n = kN;
+  u64* TP = (u64*)ws;
+  u64* CV = TP + (long long)polys * K * n;
+  LimbList lp;
+  lp.n = K;
+  for (int k = 0; k < K; ++k) {
+    lp.off[k] = (uint16_t)k;
+    lp.prime[k] = (uint8_t)(L + k);
+  }
+  int rc = wide_ntt(c, in + (long long)ell * n, TP, polys, in_stride, (long long)K * n, lp, true, s);
+  if (rc) return rc;
+  wk_conv<<<dim3(kN / 256, polys), 256, 0, s>>>(TP, (long long)K * n, 0, CV, (long long)ell * n, W.moddown + ell, W.t);
+  HCK_CHECK_LAUNCH();
+  rc = wide_ntt(c, CV, CV, polys, (long long)ell * n, (long long)ell * n, q_list(ell), false, s);
+  if (rc) return rc;
+  wk_ks_out<<<dim3(kN / 256, ell, polys), 256, 0, s>>>(in, in_stride, CV, (long long)ell * n, nullptr, 0, nullptr, 0,
+                                                       out, out_stride, W.t.pinv, W.t.pinv_s, W.t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+size_t wide_rescale_bytes(const hck_context* c, int ell, int polys) {
+  (void)c;
+  return (size_t)polys * kN * 8 * (size_t)ell;
+}
+
+int wide_rescale(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                 long long out_stride, char* ws, hipStream_t s) {
+  const WideState& W = *c->wide;
+  const long long n = kN;
+  const int nt = ell - 1;
+  u64* TL = (u64*)ws;
+  u64* TT = TL + (long long)polys * n;
+  LimbList l1;
+  l1.n = 1;
+  l1.off[0] = 0;
+  l1.prime[0] = (uint8_t)(ell - 1);
+  int rc = wide_ntt(c, in + (long long)(ell - 1) * n, TL, polys, in_stride, n, l1, true, s);
+  if (rc) return rc;
+  wk_lift<<<dim3(kN / 256, nt, polys), 256, 0, s>>>(TL, n, ell - 1, TT, (long long)nt * n, 0, W.t);
+  HCK_CHECK_LAUNCH();
+  rc = wide_ntt(c, TT, TT, polys, (long long)nt * n, (long long)nt * n, q_list(nt), false, s);
+  if (rc) return rc;
+  const size_t lv = (size_t)ell * c->L;
+  wk_ks_out<<<dim3(kN / 256, nt, polys), 256, 0, s>>>(in, in_stride, TT, (long long)nt * n, nullptr, 0, nullptr, 0, out,
+                                                      out_stride, W.qlast_inv + lv, W.qlast_inv_s + lv, W.t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+size_t wide_modraise_bytes(const hck_context* c, int to, int polys) {
+  (void)c;
+  (void)to;
+  return (size_t)polys * kN * 8;
+}
+
+int wide_modraise(const hck_context* c, int to, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                  long long out_stride, char* ws, hipStream_t s) {
+  const long long n = kN;
+  u64* TL = (u64*)ws;
+  LimbList l0;
+  l0.n = 1;
+  l0.off[0] = 0;
+  l0.prime[0] = 0;
+  int rc = wide_ntt(c, in, TL, polys, in_stride, n, l0, true, s);
+  if (rc) return rc;
+  // a single poly may come with any item stride (0 included): its pitch is then the row itself
+  const long long os = polys > 1 ? out_stride : (long long)to * n;
+  wk_lift<<<dim3(kN / 256, to - 1, polys), 256, 0, s>>>(TL, n, 0, out, os, 1, c->wide->t);
+  HCK_CHECK_LAUNCH();
+  rc = wide_ntt(c, out, out, polys, os, os, q_list(to, 1), false, s);
+  if (rc) return rc;
+  const size_t row = (size_t)n * 8;
+  const size_t dp = polys > 1 ? (size_t)out_stride * 8 : row, sp = polys > 1 ? (size_t)in_stride * 8 : row;
+  hipError_t e = hipMemcpy2DAsync(out, dp, in, sp, row, polys, hipMemcpyDeviceToDevice, s);
+  return e == hipSuccess ? HCK_OK : (int)e;
+}
+
+int wide_poly_op(const hck_context* c, int op, uint64_t* out, const uint64_t* a, const uint64_t* b, int polys,
+                 long long out_stride, long long a_stride, long long b_stride, int limbs, const int* prime_idx,
+                 const uint64_t* scalar, hipStream_t s) {
+  WPrimeMap pm{};
+  WScalars sc{};
+  const bool with_scalar = op == HCK_OP_MUL_SCALAR || op == HCK_OP_ADD_SCALAR;
+  for (int i = 0; i < limbs; ++i) {
+    pm.prime[i] = (uint8_t)prime_idx[i];
+    if (with_scalar) {
+      const u64 q = c->primes[prime_idx[i]];
+      sc.s[i] = scalar[i];
+      sc.ss[i] = shoup_companion(scalar[i], q);
+    }
+  }
+  const dim3 grid(kN / 256, limbs, polys);
+  const WideTables& T = c->wide->t;
+  switch (op) {
+    case HCK_OP_ADD: wk_poly_op<HCK_OP_ADD><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_SUB: wk_poly_op<HCK_OP_SUB><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_MUL: wk_poly_op<HCK_OP_MUL><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_NEG: wk_poly_op<HCK_OP_NEG><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_MUL_SCALAR: wk_poly_op<HCK_OP_MUL_SCALAR><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_MUL_XHALF: wk_poly_op<HCK_OP_MUL_XHALF><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_MAC: wk_poly_op<HCK_OP_MAC><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    case HCK_OP_ADD_SCALAR: wk_poly_op<HCK_OP_ADD_SCALAR><<<grid, 256, 0, s>>>(out, a, b, out_stride, a_stride, b_stride, pm, sc, T); break;
+    default: return HCK_ERR_ARG;
+  }
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int wide_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
+                const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1, uint64_t* d2,
+                long long d_stride, hipStream_t s) {
+  wk_tensor<<<dim3(kN / 256, ell, batch), 256, 0, s>>>(a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride,
+                                                       c->wide->t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int wide_weighted_sum(const hck_context* c, int limbs, int n, int groups, const uint64_t* in, long long in_stride,
+                      const uint64_t* w, uint64_t* out, long long out_stride, hipStream_t s) {
+  wk_weighted_sum<<<dim3(kN / 256, limbs, groups), 256, 0, s>>>(in, in_stride, n, w, out, out_stride, limbs,
+                                                                c->wide->t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int wide_lincomb(const hck_context* c, int limbs, int groups, int terms, const uint64_t* const* x, const uint64_t* w,
+                 uint64_t* const* out, hipStream_t s) {
+  if (groups > kWLcMaxGroups || (long long)groups * terms > kWLcMaxPtrs) return HCK_ERR_ARG;
+  WLcPtrs P{};
+  for (int j = 0; j < groups * terms; ++j) P.x[j] = x[j];
+  for (int g = 0; g < groups; ++g) P.out[g] = out[g];
+  wk_lincomb<<<dim3(kN / 256, limbs, groups), 256, 0, s>>>(P, terms, w, limbs, c->wide->t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int wide_bsgs_mac(const hck_context* c, int limbs, const int* prime_idx, int inputs, int babies, int giants,
+                  const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, long long baby_stride,
+                  const uint64_t* pts, long long pt_stride, uint64_t* res, hipStream_t s) {
+  if (babies > kWMaxBabies || (long long)giants * inputs > 65535) return HCK_ERR_ARG;
+  WMac P{};
+  for (int b = 0; b < babies; ++b) {
+    if (!baby_c0[b] || !baby_c1[b]) return HCK_ERR_ARG;
+    P.c0[b] = baby_c0[b];
+    P.c1[b] = baby_c1[b];
+  }
+  WPrimeMap pm{};
+  for (int l = 0; l < limbs; ++l) pm.prime[l] = (uint8_t)prime_idx[l];
+  wk_bsgs_mac<<<dim3(kN / 256, limbs, giants * inputs), 256, 0, s>>>(P, baby_stride, pts, pt_stride, res, inputs,
+                                                                     babies, giants, limbs, pm, c->wide->t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+}  // namespace hck

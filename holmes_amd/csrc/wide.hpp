@@ -1,0 +1,98 @@
+// The wide-prime path: contexts whose primes reach 2^50 (up to 2^61), such as the reference's
+// production chain (assets/feature_major.json: 38 Q limbs of 59/60 bits, dnum 5).  The FP64 arithmetic of
+// modarith.hpp is exact only below 2^50, so these contexts run every kernel on 64-bit integer words
+// (modarith64.hpp: Shoup products for constants, Barrett for products of two variables) and keep
+// residues canonical in [0, p) between stages.  One implementation per width: a context is either
+// FP64 (every prime below 2^50) or wide, and the library's internal entry points (NTT, key switch,
+// ModDown, rescale, ModRaise, encode, elementwise, tensor, MAC) dispatch on hck_context::wide.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <vector>
+
+#include "internal.hpp"
+
+namespace hck {
+
+constexpr uint64_t kWidePrimeLimit = 1ULL << 61;  // lazy sums below 4p stay inside 64 bits
+constexpr int kWideChunk = 8;                      // items per key-switch launch sequence
+
+// Fast base conversion constants (sources b_s -> targets t) with Shoup companions.
+struct WideConv {
+  int ns, nt;
+  int src_prime[kMaxAlpha];
+  int dst_prime[kMaxPrimes];
+  int dst_slot[kMaxPrimes];
+  uint64_t hinv[kMaxAlpha], hinv_s[kMaxAlpha];        // (B / b_s)^-1 mod b_s
+  uint64_t hmod[kMaxAlpha][kMaxPrimes];               // (B / b_s) mod t
+  uint64_t hmod_s[kMaxAlpha][kMaxPrimes];
+};
+
+struct WideTables {
+  const uint64_t* p;       // [np]
+  const uint64_t* mu;      // [np] Barrett factors floor(2^(2w) / p)
+  const int* w;            // [np] bit lengths
+  const uint64_t* fwd;     // [np][N] psi^brv(k)
+  const uint64_t* fwd_s;   // Shoup companions
+  const uint64_t* inv;     // [np][N] psi^-brv(k)
+  const uint64_t* inv_s;
+  const uint64_t* ninv;    // [np] N^-1
+  const uint64_t* ninv_s;
+  const uint64_t* zeta4;   // [np] psi^(N/2)
+  const uint64_t* zeta4_s;
+  const uint64_t* pmod;    // [np] P mod q_i (0 for the special primes)
+  const uint64_t* pmod_s;
+  const uint64_t* pinv;    // [np] P^-1 mod q_i (Q primes)
+  const uint64_t* pinv_s;
+};
+
+struct WideState {
+  WideTables t{};
+  void* block = nullptr;         // one allocation for every table
+  WideConv* modup = nullptr;     // [(L + 1) * beta_max]
+  WideConv* moddown = nullptr;   // [L + 1]: P primes -> q_0 .. q_{ell-1}
+  uint64_t* qlast_inv = nullptr; // [(L + 1) * L]: level ell, prime i: q_{ell-1}^-1 mod q_i
+  uint64_t* qlast_inv_s = nullptr;
+};
+
+// Context set-up and release (context.hip calls these for a context with a prime >= 2^50).
+int wide_init(hck_context* c);
+void wide_free(hck_context* c);
+int wide_twiddles(const hck_context* c, int prime_idx, int inverse, uint64_t* out);
+
+// The internal entry points' wide bodies (same arguments and semantics as the FP64 ones).
+int wide_ntt(const hck_context* c, const uint64_t* src, uint64_t* dst, int groups, long long src_stride,
+             long long dst_stride, const LimbList& list, bool inverse, hipStream_t s);
+int wide_encode_ntt(const hck_context* c, const double* vre, const double* vim, double scale, uint64_t* out,
+                    long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s);
+size_t wide_ks_bytes(const hck_context* c, int ell, int batch);
+int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+            const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+            const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
+            char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
+            const uint32_t* galois_items);
+size_t wide_moddown_bytes(const hck_context* c, int ell, int polys);
+int wide_moddown(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                 long long out_stride, char* ws, hipStream_t s);
+size_t wide_rescale_bytes(const hck_context* c, int ell, int polys);
+int wide_rescale(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                 long long out_stride, char* ws, hipStream_t s);
+size_t wide_modraise_bytes(const hck_context* c, int to, int polys);
+int wide_modraise(const hck_context* c, int to, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
+                  long long out_stride, char* ws, hipStream_t s);
+int wide_poly_op(const hck_context* c, int op, uint64_t* out, const uint64_t* a, const uint64_t* b, int polys,
+                 long long out_stride, long long a_stride, long long b_stride, int limbs, const int* prime_idx,
+                 const uint64_t* scalar, hipStream_t s);
+int wide_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
+                const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1, uint64_t* d2,
+                long long d_stride, hipStream_t s);
+int wide_weighted_sum(const hck_context* c, int limbs, int n, int groups, const uint64_t* in, long long in_stride,
+                      const uint64_t* w, uint64_t* out, long long out_stride, hipStream_t s);
+int wide_lincomb(const hck_context* c, int limbs, int groups, int terms, const uint64_t* const* x,
+                 const uint64_t* w, uint64_t* const* out, hipStream_t s);
+int wide_bsgs_mac(const hck_context* c, int limbs, const int* prime_idx, int inputs, int babies, int giants,
+                  const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, long long baby_stride,
+                  const uint64_t* pts, long long pt_stride, uint64_t* res, hipStream_t s);
+
+}  // namespace hck

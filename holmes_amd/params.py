@@ -114,11 +114,10 @@ class CKKSContextSpec:
         if self.num_q < 2 or int(self.dnum) < 1:
             raise ValueError("need depth >= 1 and dnum >= 1")
         for bits in (self.dcrt_bits, self.first_mod, self.special_bits or self.dcrt_bits):
-            if int(bits) > 50:
-                raise ValueError(
-                    "the FP64-exact modular arithmetic needs primes below 2^50 "
-                    f"(got {bits}-bit primes)"
-                )
+            # primes below 2^50 run on the FP64-exact arithmetic; wider ones (the reference's 59/60-bit
+            # chains) on the 64-bit integer path, which takes primes up to 2^61
+            if not 32 <= int(bits) <= 60:
+                raise ValueError(f"prime sizes from 32 to 60 bits are supported (got {bits}-bit primes)")
         if str(self.secret_key_dist).upper() not in ("UNIFORM_TERNARY", "SPARSE_TERNARY"):
             raise ValueError(f"unsupported secret key distribution {self.secret_key_dist!r}")
         if str(self.scale_mode) != "fixed":

@@ -58,8 +58,17 @@ def test_spec_prime_chain_follows_oracle_rule():
     assert p == O.gen_primes(16, 50, 8)
     assert q == O.gen_primes(16, 50, 24, exclude=p)
     assert ntt_primes(16, 50, 3) == O.gen_primes(16, 50, 3)
-    with pytest.raises(ValueError):
-        CKKSContextSpec(dcrt_bits=59).validate()
+    # the reference's production chain (assets/feature_major.json): 60-bit q_0 and specials, 59-bit rest
+    wide = CKKSContextSpec(depth=37, dnum=5, dcrt_bits=59, first_mod=60)
+    wide.validate()
+    q, p = wide.prime_chain()
+    assert len(q) == 38 and len(p) == 8 and wide.alpha == 8
+    assert p == O.gen_primes(16, 60, 8) and q[:1] == O.gen_primes(16, 60, 1, exclude=p)
+    assert q[1:] == O.gen_primes(16, 59, 37, exclude=p + q[:1])
+    assert [x.bit_length() for x in q[:2]] == [60, 59] and all(x.bit_length() == 60 for x in p)
+    for bits in (61, 31):
+        with pytest.raises(ValueError):
+            CKKSContextSpec(dcrt_bits=bits).validate()
 
 
 @pytest.mark.parametrize("slots", [32768, 4096])
