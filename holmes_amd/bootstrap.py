@@ -1,4 +1,4 @@
-"""CKKS bootstrapping of full-slot ciphertexts on the GPU kernels (the ``easyfhe.bs.openfhe``
+"""CKKS bootstrapping of full-slot and sparse-slot ciphertexts on the GPU kernels (the ``easyfhe.bs.openfhe``
 surface Holmes drives: ``BootstrapSpec``, ``generate(context, spec)``, ``bootstrap(cipher, context,
 program)``, ``requirements(specs, log_n).rotations``; llama3fhe/operators/nonlinear/
 bootstrap.py:119-160,260-348,626-640).
@@ -19,6 +19,20 @@ Pipeline ("modraise_first"), every step a sequence of this package's HIP-backed 
    [-1, 1], then d double-angle steps cos(2a) = 2 cos^2(a) - 1: sin(2 pi t) = sin(2 pi m / q_0).
 6. Recombine R + i J and SlotToCoeff: U0 (the forward butterflies, bit-reversed input) times
    q_0 / (2 pi S) in the plaintexts, then the integer 2^r; the output decrypts to the input message.
+
+Sparse slots (``log_slots`` k < log_n - 1, n = 2^k): the message is periodic with period n, i.e. its
+polynomial lies in the subring Z[Y], Y = X^(N / 2n).  After ModRaise, log2(N / 2n) rotate-and-adds
+by n, 2n, ..., N/4 slots (the trace onto the subring) multiply the message by R = N / 2n and keep
+only the subring part of q_0 I; the polynomial then has 2n coefficients in Y, its slots are the size-n
+special DFT of them (Y evaluates to exp(2 pi i 5^j / 4n) at the j-th point), so CoeffToSlot and
+SlotToCoeff are the size-n butterflies on the period-n slot vector (every diagonal tiled over the
+N/2 slots, every rotation taken modulo n) and 1 / R joins the CoeffToSlot constant
+(the reference's sparse_specs, llama3fhe/operators/nonlinear/bootstrap.py:112-142).  The pipeline's
+own noise (EvalMod's rescales above all) is not periodic: left alone it would sit on the polynomial's
+coefficients outside the subring, where no later sparse refresh can see it (a two-pass correction
+would not converge).  So the output is traced once more, at its low level: the trace projects onto
+the subring exactly, and its gain R = 2^j replaces j of the message-ratio bits in the final integer
+product (2^(bits - j)), so the trace's own key-switch noise meets the full-size message.
 
 Scales: every plaintext and scalar multiplied in is encoded at exactly the prime the following
 rescale drops, so the working scale never drifts; after ModRaise the ciphertext is read at the
@@ -71,14 +85,16 @@ class BootstrapSpec:
     cheb_degree: int = 48
 
     def validate(self, log_n: int) -> None:
-        if int(self.log_slots) != int(log_n) - 1:
-            raise ValueError("this bootstrap handles full-slot ciphertexts (log_slots = log_n - 1)")
+        if not 1 <= int(self.log_slots) <= int(log_n) - 1:
+            raise ValueError(f"log_slots must lie in [1, {int(log_n) - 1}], got {self.log_slots}")
         if str(self.mode) != "modraise_first":
             raise ValueError("only mode='modraise_first' is supported")
         if str(self.strategy) not in STRATEGIES:
             raise ValueError(f"strategy must be one of {sorted(STRATEGIES)}, got {self.strategy!r}")
         if len(tuple(self.level_budget)) != 2 or min(int(b) for b in self.level_budget) < 1:
             raise ValueError("level_budget needs two positive entries (CoeffToSlot, SlotToCoeff)")
+        if max(int(b) for b in self.level_budget) > int(self.log_slots):
+            raise ValueError(f"a level budget above log_slots ({self.log_slots}) leaves empty stages")
         for name in ("dim1", "baby_step"):
             pair = getattr(self, name)
             if pair is None:
@@ -86,6 +102,22 @@ class BootstrapSpec:
             if len(tuple(pair)) != 2 or any(int(v) < 0 or (int(v) and int(v) & (int(v) - 1)) or int(v) == 1
                                             for v in pair):
                 raise ValueError(f"{name} needs two entries, each 0 (automatic) or a power of two >= 2")
+
+    @property
+    def slots(self) -> int:
+        return 1 << int(self.log_slots)
+
+    def sparse_extra_bits(self, log_n: int) -> int:
+        """Extra scale-down bits of a sparse program: its 2n coefficients are sqrt(R) times those of
+        a full-slot message of the same slot size (R = N / 2n), so the sine's cubic error grows by R
+        at the same message ratio; ceil(log2(R) / 2) more bits bring it back, for sqrt(R) in noise."""
+
+        return -(-(int(log_n) - 1 - int(self.log_slots)) // 2)
+
+    def trace_rotations(self, log_n: int) -> tuple[int, ...]:
+        """Slot rotations of the trace onto the period-n subring (empty at full slots)."""
+
+        return tuple(self.slots << i for i in range(int(log_n) - 1 - int(self.log_slots)))
 
     def babies(self, kind: int) -> int:
         """Baby rotations per stage of CoeffToSlot (kind 0) or SlotToCoeff (kind 1): ``dim1`` (the
@@ -149,18 +181,19 @@ def requirements(specs, log_n: int) -> Requirements:
     """Rotation amounts (slot rotations, plus the conjugation 2N - 1) and depth of the programs."""
 
     specs = (specs,) if isinstance(specs, BootstrapSpec) else tuple(specs)
-    n = 1 << (int(log_n) - 1)
     rots: set[int] = set()
     depth = 0
     for spec in specs:
         spec.validate(log_n)
+        n = spec.slots
+        rots |= set(spec.trace_rotations(log_n))
         b1, b2 = (int(b) for b in spec.level_budget)
         for layers in _stage_layers(spec.log_slots, b1, True):
             rots |= _stage_rotations(layers, n, spec.babies(0))
         for layers in _stage_layers(spec.log_slots, b2, False):
             rots |= _stage_rotations(layers, n, spec.babies(1))
         depth = max(depth, b1 + b2 + evalmod_levels(spec, 1024, [2] * 1025))
-    rots.add(4 * n - 1)  # conjugation
+    rots.add((1 << (int(log_n) + 1)) - 1)  # conjugation
     return Requirements(rotations=tuple(sorted(rots)), depth=depth)
 
 
@@ -249,6 +282,7 @@ class Stage:
     giants: list            # giant indices k2: 0 (when present) first, then ascending
     diags: dict             # k -> slot vector (complex128, length n)
     cache: dict = field(default_factory=dict)  # limbs -> encoded rows [giants * n1][limbs][N]
+    n: int = 0              # slots of the transform (the period; 0: unset, the full slot count)
 
 
 def make_stage(layers: list[int], all_layers: list[dict], n: int, factor: float = 1.0, n1: int = 0) -> Stage:
@@ -263,7 +297,7 @@ def make_stage(layers: list[int], all_layers: list[dict], n: int, factor: float 
             raise AssertionError("merged diagonal off the stage's grid")
         diags[s // h_min] = v * factor
     giants = sorted({k // n1 for k in diags}, key=lambda k2: (k2 != 0, k2))  # the unrotated row first
-    return Stage(layers=list(layers), h_min=h_min, n1=n1, giants=giants, diags=diags)
+    return Stage(layers=list(layers), h_min=h_min, n1=n1, giants=giants, diags=diags, n=int(n))
 
 
 def stage_rows(st: Stage, n: int) -> np.ndarray:
@@ -348,12 +382,12 @@ def generate(context: CKKSContext, spec: BootstrapSpec) -> BootstrapProgram:
                          "generate them from requirements(spec, log_n).rotations")
     if ctx.relin_key is None:
         raise ValueError("bootstrap needs the relinearisation key")
-    return plan_program(spec, ctx.q_primes, float(ctx.scale_at(ctx.L)), ctx.L)
+    return plan_program(spec, ctx.q_primes, float(ctx.scale_at(ctx.L)), ctx.L, int(ctx.logN))
 
 
-def plan_program(spec: BootstrapSpec, q_primes, scale: float, raise_to: int) -> BootstrapProgram:
+def plan_program(spec: BootstrapSpec, q_primes, scale: float, raise_to: int, log_n: int = 16) -> BootstrapProgram:
     """The host half of ``generate``: level schedule, stage diagonals and interpolant for a chain
-    of Q primes, the nominal scale S and the ModRaise target."""
+    of Q primes, the nominal scale S and the ModRaise target (ring degree 2^log_n)."""
 
     b1, b2 = (int(b) for b in spec.level_budget)
     raise_to = int(raise_to)
@@ -369,12 +403,13 @@ def plan_program(spec: BootstrapSpec, q_primes, scale: float, raise_to: int) -> 
     S = float(scale)
     S_out = canonical_scales(primes, em_in, S)[em_out]
     Kp = float(int(spec.mod_bound) + 1)
+    trace_gain = float(1 << (int(log_n) - 1 - int(spec.log_slots)))  # R = N / 2n of the subring trace
     prog = BootstrapProgram(spec=spec, raise_to_limbs=raise_to, evalmod_limbs=em_in, output_limbs=out, q0=q0,
                             nominal_scale=S, evalmod_out_scale=S_out, mod_scale=Kp,
                             cheb=evalmod_coefficients(spec),
                             cts=plan_stages(spec.log_slots, b1, True, 1.0, spec.babies(0)),
                             stc=plan_stages(spec.log_slots, b2, False, 1.0, spec.babies(1)),
-                            cts_rho=(S / (2.0 * q0 * Kp)) ** (1.0 / b1),
+                            cts_rho=(S / (2.0 * q0 * Kp * trace_gain)) ** (1.0 / b1),
                             stc_rho=(q0 / (2.0 * math.pi * S_out)) ** (1.0 / b2))
     prog.constants = _Constants(prog)
     return prog
@@ -386,7 +421,10 @@ def _stage_plaintexts(st: Stage, limbs: int, pt_scale: float, ctx: CKKSContext, 
     pts = st.cache.get(key)
     if pts is not None:
         return pts
-    rows = stage_rows(st, ctx.max_slots)
+    n = int(st.n) or ctx.max_slots
+    rows = stage_rows(st, n)
+    if n < ctx.max_slots:
+        rows = np.tile(rows, (1, ctx.max_slots // n))  # the period-n diagonals over every slot
     re = torch.from_numpy(np.ascontiguousarray(rows.real)).to(ctx.device)
     im = torch.from_numpy(np.ascontiguousarray(rows.imag)).to(ctx.device)
     pts = ctx.encode(re, float(pt_scale), int(limbs), values_im=im)
@@ -395,12 +433,33 @@ def _stage_plaintexts(st: Stage, limbs: int, pt_scale: float, ctx: CKKSContext, 
     return pts
 
 
-def _rotate_many(c0: torch.Tensor, c1: torch.Tensor, offsets, limbs: int, ctx: CKKSContext):
+def _rotate_many(c0: torch.Tensor, c1: torch.Tensor, offsets, limbs: int, ctx: CKKSContext, n: int = 0):
     """Item i of (c0, c1) ([items][limbs][N]; batch stride 0: one input) rotated by offsets[i],
-    each with its own key, in one batched key switch with a Galois element per item."""
+    each with its own key, in one batched key switch with a Galois element per item.  Offsets are
+    taken modulo n (the period of the slot vectors; 0: the full slot count); an offset that is a
+    multiple of n is the identity and its item is copied."""
 
-    gs = [ctx.galois_element(int(off) % ctx.max_slots) for off in offsets]
-    return ctx.rotate_raw(c0, c1, limbs, gs, [ctx.key_for_galois(g) for g in gs])
+    n = int(n) or ctx.max_slots
+    offs = [int(off) % n for off in offsets]
+    if all(offs):
+        gs = [ctx.galois_element(o) for o in offs]
+        return ctx.rotate_raw(c0, c1, limbs, gs, [ctx.key_for_galois(g) for g in gs])
+    B = len(offs)
+    o0, o1 = ctx.empty(B, limbs, ctx.N), ctx.empty(B, limbs, ctx.N)
+    nz = [i for i, o in enumerate(offs) if o]
+    for i, o in enumerate(offs):
+        if not o:
+            o0[i].view(torch.int64).copy_(c0[i, :limbs].view(torch.int64))
+            o1[i].view(torch.int64).copy_(c1[i, :limbs].view(torch.int64))
+    if nz:
+        idx = torch.tensor(nz, device=c0.device)
+        g0 = c0[:, :limbs].contiguous().view(torch.int64).index_select(0, idx).view(torch.uint64)
+        g1 = c1[:, :limbs].contiguous().view(torch.int64).index_select(0, idx).view(torch.uint64)
+        gs = [ctx.galois_element(offs[i]) for i in nz]
+        r0, r1 = ctx.rotate_raw(g0, g1, limbs, gs, [ctx.key_for_galois(g) for g in gs])
+        o0.view(torch.int64).index_copy_(0, idx, r0.view(torch.int64))
+        o1.view(torch.int64).index_copy_(0, idx, r1.view(torch.int64))
+    return o0, o1
 
 
 def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: bool = True) -> Cipher:
@@ -414,16 +473,17 @@ def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: b
 
     limbs = int(x.state.cur_limbs)
     B = int(x.batch_size)
+    n = int(st.n) or ctx.max_slots  # rotations act on period-n slot vectors modulo n
     c0, c1 = x.cv[0][:, :limbs].contiguous(), x.cv[1][:, :limbs].contiguous()
     nb = st.n1 - 1
-    offs = [k1 * st.h_min for k1 in range(1, st.n1) for _ in range(B)]  # offset-major, then item
+    offs = [(k1 * st.h_min) % n for k1 in range(1, st.n1) for _ in range(B)]  # offset-major, then item
     if B == 1:
         r0, r1 = c0.expand(nb, -1, -1), c1.expand(nb, -1, -1)  # batch stride 0: one input, every offset
     else:
         r0, r1 = (u64_clone(c.view(torch.int64).unsqueeze(0).expand(nb, B, limbs, ctx.N).reshape(nb * B, limbs,
                                                                                             ctx.N).view(torch.uint64))
                   for c in (c0, c1))
-    b0, b1 = _rotate_many(r0, r1, offs, limbs, ctx)
+    b0, b1 = _rotate_many(r0, r1, offs, limbs, ctx, n)
     del r0, r1
     pts = _stage_plaintexts(st, limbs, pt_scale, ctx, keep)
     res = ctx.bsgs_mac([c0] + [b0[i * B:(i + 1) * B] for i in range(nb)],
@@ -436,7 +496,7 @@ def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: b
     if rot:
         G = len(rot)
         g0, g1 = _rotate_many(res[0, first:].reshape(G * B, limbs, ctx.N), res[1, first:].reshape(G * B, limbs, ctx.N),
-                              [k2 * st.n1 * st.h_min for k2 in rot for _ in range(B)], limbs, ctx)
+                              [(k2 * st.n1 * st.h_min) % n for k2 in rot for _ in range(B)], limbs, ctx, n)
         for c, gc in enumerate((g0, g1)):
             for b in range(B):
                 xs[c * B + b] += [gc[i * B + b] for i in range(G)]
@@ -466,12 +526,26 @@ def _rescale_times(ct: Cipher, times: int, scale: float, ctx: CKKSContext) -> Ci
     return ct.cipher_like(ct.cv, state=ct.state.replace(scaling_factor=float(scale), scale_degree=1))
 
 
+def _trace(ct: Cipher, spec: BootstrapSpec, ctx: CKKSContext) -> Cipher:
+    """sum of sigma(ct) over the automorphisms fixing the period-n subring: log2(N / 2n) fused
+    rotate-and-adds by n, 2n, ..., N/4 slots (nothing at full slots).  It multiplies the subring part
+    of the polynomial by R = N / 2n and removes the rest."""
+
+    for r in spec.trace_rotations(ctx.logN):
+        lim = int(ct.state.cur_limbs)
+        c0, c1 = (c[:, :lim].contiguous() for c in ct.cv)
+        g = ctx.galois_element(int(r))
+        t0, t1 = ctx.rotate_raw(c0, c1, lim, g, ctx.key_for_galois(g), acc=(c0, c1))
+        ct = ct.cipher_like([t0, t1])
+    return ct
+
+
 def _items(ct: Cipher, lo: int, hi: int) -> Cipher:
     return ct.cipher_like([c[lo:hi] for c in ct.cv], batch_size=hi - lo)
 
 
 def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *, bound_bits: int = 0) -> Cipher:
-    """Refresh ``cipher`` (two components, >= 2 limbs, full slots, |slot| <= 2^bound_bits; a batch
+    """Refresh ``cipher`` (two components, >= 2 limbs, 2^log_slots slots, |slot| <= 2^bound_bits; a batch
     is refreshed as one: every key switch of the pipeline covers all its items) to
     ``spec.output_levels`` limbs (0: all the program leaves).  The result keeps the input's scaling
     factor; the input is not consumed.  ``bound_bits`` moves the message 2^bound_bits further below
@@ -484,14 +558,17 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
     B = int(cipher.batch_size)
     if int(cipher.state.cur_limbs) < 2:
         raise ValueError("bootstrap needs at least two limbs (one is spent scaling the message down)")
-    if int(cipher.slots) != ctx.max_slots:
-        raise ValueError("bootstrap handles full-slot ciphertexts")
+    if int(cipher.slots) != spec.slots:
+        raise ValueError(f"this program refreshes ciphertexts of {spec.slots} slots, not {cipher.slots} "
+                         "(a periodic full-slot message is viewed at its period first)")
     keep = program.constants is None or program.constants.mode != "none"
     S_in = float(cipher.state.scaling_factor)
     limbs = int(cipher.state.cur_limbs)
     b1, b2 = len(program.cts), len(program.stc)
     # 1. message down to 2^-bits of q_0, then one limb
-    bits = max(0, int(round(math.log2(S_in / program.q0))) + int(spec.message_ratio_bits) + int(bound_bits))
+    bits = max(0, int(round(math.log2(S_in / program.q0))) + int(spec.message_ratio_bits) + int(bound_bits)
+               + spec.sparse_extra_bits(ctx.logN))
+    bits = max(bits, len(spec.trace_rotations(ctx.logN)))  # the output trace's gain is paid from these
     x = cipher
     if bits:
         enc = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
@@ -502,6 +579,8 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
     S = program.nominal_scale
     ct = x.cipher_like(raised, state=x.state.replace(cur_limbs=program.raise_to_limbs, scale_degree=1,
                                                      scaling_factor=S))
+    # 2b. sparse slots: the trace onto the period-n subring (the gain R is in the CoeffToSlot constant)
+    ct = _trace(ct, spec, ctx)
     # 3. CoeffToSlot at the raised level: (M_lo + i M_hi) / (2 q_0 K') up to the shares rho
     ct = apply_stages(ct, program.cts, program.cts_rho, ctx, keep)
     # 4. real and imaginary parts before the rescales (t / K' with t = M / q_0), then b1 rescales
@@ -518,8 +597,11 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
     z = fhe.homo_add(yr, fhe.homo_mul_i(yi, ctx), ctx)
     # 6. SlotToCoeff (q_0 / (2 pi S_out) in the shares), b2 rescales, the integer 2^bits
     z = _rescale_times(apply_stages(z, program.stc, program.stc_rho, ctx, keep), b2, S_in * 2.0**-bits, ctx)
-    if bits:
-        z = fhe.homo_mul_scalar(z, fhe.encode_scalar(1 << bits, cur_limbs=int(z.state.cur_limbs), scale_degree=0,
+    # 6b. sparse slots: project the output onto the subring; its gain R = 2^j is part of the 2^bits
+    z = _trace(z, spec, ctx)
+    up = bits - len(spec.trace_rotations(ctx.logN))
+    if up:
+        z = fhe.homo_mul_scalar(z, fhe.encode_scalar(1 << up, cur_limbs=int(z.state.cur_limbs), scale_degree=0,
                                                      mode="integer", context=ctx), ctx)
     # the decryption is now S_in * (encoding of the input slots)
     z = z.cipher_like(z.cv, state=z.state.replace(scaling_factor=S_in, scale_degree=1))

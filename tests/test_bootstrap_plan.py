@@ -126,11 +126,16 @@ def test_requirements_cover_every_stage_rotation():
     assert req.depth == 3 + 2 + B.evalmod_levels(spec, 40, [2] * 41)
 
 
-def test_full_slot_spec_is_required():
-    with pytest.raises(ValueError):
-        B.requirements(B.BootstrapSpec(log_slots=14), 16)
-    with pytest.raises(ValueError):
-        B.requirements(B.BootstrapSpec(mode="slots_first"), 16)
+def test_spec_validation_and_sparse_rotations():
+    for bad in (B.BootstrapSpec(log_slots=0), B.BootstrapSpec(log_slots=16), B.BootstrapSpec(mode="slots_first"),
+                B.BootstrapSpec(log_slots=2, level_budget=(3, 2))):
+        with pytest.raises(ValueError):
+            B.requirements(bad, 16)
+    sparse = B.BootstrapSpec(log_slots=12, level_budget=(2, 2))
+    assert sparse.trace_rotations(16) == (4096, 8192, 16384)
+    rots = set(B.requirements(sparse, 16).rotations)
+    assert {4096, 8192, 16384, (1 << 17) - 1} <= rots and all(r < 4096 for r in rots - {4096, 8192, 16384, (1 << 17) - 1})
+    assert B.BootstrapSpec().trace_rotations(16) == ()
 
 
 def test_chebyshev_division_identity():
@@ -171,12 +176,18 @@ def test_evalmod_levels_match_schedule():
 
 
 def _simulate(prog, v, q0, I, S_in, log_n, bits):
-    """The bootstrap on slot values: what the GPU path computes, less the encryption noise."""
+    """The bootstrap on slot values: what the GPU path computes, less the encryption noise.  A
+    sparse program (v of 2^log_slots < N / 2 slots) traces the raised slot vector onto its period
+    and then works on one period, as the GPU's tiled diagonals and rotations modulo n do."""
 
     S = prog.nominal_scale
-    m = encoding.encode_real_coeffs(v, S_in * 2.0**-bits, log_n)     # message at one limb
+    n = len(v)
+    m = encoding.encode_real_coeffs(v, S_in * 2.0**-bits, log_n, n)  # message at one limb
     M = m + float(q0) * I                                             # after ModRaise
     z = encoding.decode(M, S, log_n)
+    for r in prog.spec.trace_rotations(log_n):
+        z = z + _rot(z, r)
+    z = z[:n]
     for st in prog.cts:
         z = _bsgs(st, z)
     z = z * prog.cts_rho ** len(prog.cts)
@@ -201,7 +212,7 @@ def test_numeric_pipeline_returns_the_input(seed):
     spec = B.BootstrapSpec(log_slots=log_n - 1, level_budget=(3, 3))
     rng = np.random.default_rng(seed)
     primes = [2**50 - 2**27 * k + 1 for k in range(1, 31)]
-    prog = B.plan_program(spec, primes, 2.0**50, 30)
+    prog = B.plan_program(spec, primes, 2.0**50, 30, log_n)
     n = 1 << (log_n - 1)
     v = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)) / math.sqrt(2)
     I = rng.integers(-spec.mod_bound + 1, spec.mod_bound, 1 << log_n).astype(np.float64)
@@ -216,7 +227,7 @@ def test_numeric_pipeline_catches_a_wrong_constant():
     log_n = 8
     spec = B.BootstrapSpec(log_slots=log_n - 1, level_budget=(2, 2))
     primes = [2**50 - 2**27 * k + 1 for k in range(1, 31)]
-    prog = B.plan_program(spec, primes, 2.0**50, 30)
+    prog = B.plan_program(spec, primes, 2.0**50, 30, log_n)
     rng = np.random.default_rng(5)
     n = 1 << (log_n - 1)
     v = rng.uniform(-1, 1, n) + 0j
@@ -226,3 +237,34 @@ def test_numeric_pipeline_catches_a_wrong_constant():
     prog.stc[0].diags = {k: d * (1 + 2.0**-10) for k, d in prog.stc[0].diags.items()}
     bad = _simulate(prog, v, primes[0], I, 2.0**50, log_n, 12)
     assert np.max(np.abs(bad - v)) > 2.0**-12
+
+
+@pytest.mark.parametrize("log_slots,budget", [(6, (2, 2)), (3, (2, 3)), (1, (1, 1))])
+def test_numeric_sparse_pipeline_returns_the_input(log_slots, budget):
+    """Sparse slots: the message is periodic with period n = 2^log_slots; q_0 I is a full-ring
+    polynomial (only the trace makes it sparse), and the pipeline must return the n slots."""
+
+    log_n = 10
+    spec = B.BootstrapSpec(log_slots=log_slots, level_budget=budget)
+    primes = [2**50 - 2**27 * k + 1 for k in range(1, 31)]
+    prog = B.plan_program(spec, primes, 2.0**50, 30, log_n)
+    rng = np.random.default_rng(log_slots)
+    n = 1 << log_slots
+    v = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)) / math.sqrt(2)
+    I = rng.integers(-spec.mod_bound + 1, spec.mod_bound, 1 << log_n).astype(np.float64)
+    bits = int(round(math.log2(2.0**50 / primes[0]))) + spec.message_ratio_bits + spec.sparse_extra_bits(log_n)
+    got = _simulate(prog, v, primes[0], I, 2.0**50, log_n, bits)
+    assert np.max(np.abs(got - v)) < 2.0**-20
+    # without the extra scale-down bits the sine's cubic error grows with R = N / 2n (the 2n
+    # coefficients of a sparse message are sqrt(R) times those of a full one of the same slot size)
+    R = 1 << (log_n - 1 - log_slots)
+    plain = _simulate(prog, v, primes[0], I, 2.0**50, log_n, bits - spec.sparse_extra_bits(log_n))
+    if R >= 64:
+        assert np.max(np.abs(plain - v)) > 2.0**-20
+    # without the trace's gain in the constant the result is off by R = N / 2n
+    prog.cts_rho *= (1 << (log_n - 1 - log_slots)) ** (1.0 / len(prog.cts))
+    try:
+        bad = _simulate(prog, v, primes[0], I, 2.0**50, log_n, bits)
+    except AssertionError:
+        return  # the EvalMod input left [-1, 1]: caught
+    assert np.max(np.abs(bad - v)) > 2.0**-8
