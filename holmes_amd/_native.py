@@ -66,6 +66,8 @@ SIGNATURES = {
                              _i64, _vp, _sz, _vp]),
     "hck_rotate_ext_many": (_i, [_vp, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp,
                                  _i64, _vp, _sz, _vp]),
+    "hck_rotate_ext_sum": (_i, [_vp, _i, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp,
+                                _vp, _i64, _vp, _sz, _vp]),
     "hck_moddown_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_moddown": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_pack_diagonals": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),

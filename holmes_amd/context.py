@@ -395,6 +395,51 @@ class CKKSContext:
                      _stream_ptr(self.device)), name)
         return out0, out1
 
+    def rotate_ext_sum(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois, keys, out0: torch.Tensor,
+                       out1: torch.Tensor, acc: tuple[torch.Tensor, torch.Tensor] | None = None):
+        """Grouped extended-basis rotations: c0 / c1 are [group][outputs][limbs][N] (any strides with
+        a uniform item step), member m rotated by ``galois[m]`` with ``keys[m]``;
+        out[o] = acc[o] + sum_m (P sigma_m(c0[m][o]) + IP(sigma_m(c1[m][o]))) as [outputs][limbs + K][N]
+        (the outputs may be the ``acc`` tensors).  Equals ``len(galois)`` accumulating ``rotate_ext``
+        calls bit for bit."""
+
+        G, B = int(c0.shape[0]), int(c0.shape[1])
+        if tuple(c1.shape[:2]) != (G, B) or len(galois) != G or len(keys) != G:
+            raise ValueError("one Galois element and one key per member, matching c0 / c1")
+        items = []
+        for c in (c0, c1):
+            flat = c.reshape(G * B, *c.shape[2:]) if c.is_contiguous() else None
+            if flat is None or flat.data_ptr() != c.data_ptr():
+                raise ValueError("grouped rotations need contiguous [group][outputs] inputs")
+            self._check_poly(flat, limbs, self.N)
+            items.append(flat)
+        for k in keys:
+            self._check_key(k)
+        ext = limbs + self.K
+        for o in (out0, out1):
+            self._check_poly(o, ext, self.N)
+            if o.shape[0] != B:
+                raise ValueError("outputs need one row per output")
+        a0 = a1 = None
+        a_stride = 0
+        if acc is not None:
+            a0, a1 = acc
+            for a in (a0, a1):
+                self._check_poly(a, ext, self.N)
+                if a.shape[0] != B:
+                    raise ValueError("accumulators need one row per output")
+            a_stride = _bstride(a0)
+        L = nat.lib()
+        ws = self.workspace(L.hck_keyswitch_workspace_bytes(self._h, limbs, G * B))
+        nat.check(L.hck_rotate_ext_sum(self._h, limbs, B, G, nat.u32_array(galois), items[0].data_ptr(),
+                                       items[1].data_ptr(), _bstride(items[0]),
+                                       nat.ptr_array([k.data_ptr() for k in keys]),
+                                       a0.data_ptr() if a0 is not None else None,
+                                       a1.data_ptr() if a1 is not None else None, a_stride,
+                                       out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
+                                       _stream_ptr(self.device)), "hck_rotate_ext_sum")
+        return out0, out1
+
     def _pair(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, what: str) -> int:
         self._check_poly(c0, limbs, self.N)
         self._check_poly(c1, limbs, self.N)

@@ -105,6 +105,13 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
              char* ws, hipStream_t s, uint64_t* ext_b = nullptr, uint64_t* ext_a = nullptr,
              long long ext_stride = 0, const uint32_t* galois_items = nullptr);
+// Grouped extended-basis rotations: item b = m * outputs + o (d / add at b * stride, Galois element
+// galois_items[b], key ksk[b]) is member m of output o; ext[o] = acc[o] + sum_m (P sigma(add) +
+// IP_b(sigma(d)), IP_a(sigma(d))).  outputs * group <= 64; workspace ks_fused_bytes(c, ell, outputs * group).
+int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const uint64_t* d, long long d_stride,
+                 const uint32_t* galois_items, const uint64_t* const* ksk, const uint64_t* add, long long add_stride,
+                 const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride, uint64_t* ext_b,
+                 uint64_t* ext_a, long long ext_stride, char* ws, hipStream_t s);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

@@ -138,6 +138,34 @@ extern "C" int hck_rotate_ext_many(const hck_context* ctx, int level_limbs, int 
                      out0, out1, out_stride, workspace, workspace_bytes, stream, true);
 }
 
+extern "C" int hck_rotate_ext_sum(const hck_context* ctx, int level_limbs, int outputs, int group,
+                                  const uint32_t* galois, const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                                  const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
+                                  int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (!ctx || !galois || !c0 || !c1 || !ksk || !out0 || !out1) return HCK_ERR_ARG;
+  if (level_limbs < 1 || level_limbs > ctx->L || outputs < 0 || group < 1) return HCK_ERR_ARG;
+  if ((long long)outputs * group > hck::kMaxBatch) return HCK_ERR_ARG;
+  if ((acc0 == nullptr) != (acc1 == nullptr) || out0 == out1) return HCK_ERR_ARG;
+  if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1) return HCK_ERR_ARG;
+  const int64_t ext_limb_words = (int64_t)(level_limbs + ctx->K) * hck::kN;
+  if (outputs > 1 && (out_stride < ext_limb_words || (acc0 && acc_stride < ext_limb_words))) return HCK_ERR_ARG;
+  for (int m = 0; m < group; ++m)
+    if (!galois_ok(galois[m]) || !ksk[m]) return HCK_ERR_ARG;
+  if (outputs == 0) return HCK_OK;
+  const int batch = outputs * group;
+  if (!workspace || workspace_bytes < hck::ks_fused_bytes(ctx, level_limbs, batch)) return HCK_ERR_WORKSPACE;
+  uint32_t gi[hck::kMaxBatch];
+  const uint64_t* keys[hck::kMaxBatch];
+  for (int m = 0; m < group; ++m)
+    for (int o = 0; o < outputs; ++o) {
+      gi[m * outputs + o] = galois[m];
+      keys[m * outputs + o] = ksk[m];
+    }
+  return hck::ks_fused_sum(ctx, level_limbs, outputs, group, c1, in_stride, gi, keys, c0, in_stride, acc0, acc1,
+                           acc_stride, out0, out1, out_stride, (char*)workspace, (hipStream_t)stream);
+}
+
 extern "C" size_t hck_moddown_workspace_bytes(const hck_context* ctx, int level_limbs, int polys) {
   if (!ctx || level_limbs < 1 || level_limbs > ctx->L || polys < 0) return 0;
   const int chunk = polys < 65535 ? polys : 65535;

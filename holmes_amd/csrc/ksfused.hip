@@ -585,13 +585,14 @@ __device__ __forceinline__ void rows_fwd_lds(double (&x)[16], double* S, const d
 // tile load is issued as soon as the previous transform has left its result in S, behind that
 // digit's key loads, so the tile lands while the inner product runs.  After the last digit, `after`
 // (a workspace limb, or null) is loaded into x for the caller.  TW must hold the forward twiddles
-// (visible).  Returns |sb|, |sa| <= p/2 + 1.
+// (visible).  With ``zero`` false the products are added to sb / sa (|sb|, |sa| <= p/2 + 1 on entry:
+// the grouped kernel's running sums).  Returns |sb|, |sa| <= p/2 + 1.
 __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], double (&x)[16],
                                         const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
                                         const double* __restrict__ t2, const uint64_t* __restrict__ key, int b,
                                         int e, int pi, int rg, int ell, int beta, double* S, const double* TW,
                                         const double* __restrict__ after, double p, double pinv,
-                                        const DevTables& T) {
+                                        const DevTables& T, bool zero = true) {
   const int L = T.L, K = T.K, alpha = T.alpha;
   const int ext_l = ell + K;
   const int beta_max = (L + alpha - 1) / alpha;
@@ -608,8 +609,10 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
   const int nt2 = beta - (own >= 0 ? 1 : 0);
   auto t2digit = [&](int n) { return (own >= 0 && n >= own) ? n + 1 : n; };
   uint64_t kb[16], ka[16];
+  if (zero) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
+    for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
+  }
   if (own >= 0) {
     load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
     load_keys(kb, ka, own);
@@ -637,7 +640,7 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
       sb[k] += mulv(v, u2d(kb[k]), p, pinv);  // |v| <= 3.9p: |term| <= 2p
       sa[k] += mulv(v, u2d(ka[k]), p, pinv);
     }
-    if (n % 3 == 2) {  // <= p/2 + 3 * 2p (+ 0.9p for the own digit) < 8p <= 2^53 between reductions
+    if (n % 3 == 2) {  // <= p/2 + 1 + 3 * 2p (+ 0.9p for the own digit) < 8p <= 2^53 between reductions
 #pragma unroll
       for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
     }
@@ -795,6 +798,63 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
              out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
   ipq_finish(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
              out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
+}
+
+// K3 for grouped extended-basis rotations: output o (one tile of it per workgroup) is
+//   acc[o] + sum_m (P * sigma_m(add[b]) + IP_b(sigma_m(d[b])), IP_a(sigma_m(d[b])))   over b = m * outputs + o,
+// the members m < group each with their own Galois element and key (the giant steps of one BSGS
+// chunk for every input: the running sum stays in registers, so the extended accumulator is read
+// and written once per group instead of once per member).  All outputs of a tile are dealt to one
+// XCD, so a member's key tile is fetched from HBM once and shared from L2.  ext may alias acc.
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip_sum(const uint64_t* __restrict__ d, long long d_stride,
+                                                       const GalF G, const double* __restrict__ t2, KeyPtrsF keys,
+                                                       int ell, int beta, int outputs, int group, int tiles,
+                                                       const uint64_t* __restrict__ add, long long add_stride,
+                                                       uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
+                                                       const uint64_t* acc_b, const uint64_t* acc_a,
+                                                       long long acc_stride, DevTables T) {
+  __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
+  const TileId id = decode_tile(outputs, blockIdx.x);
+  if (id.tile >= tiles) return;
+  const int o = id.b, e = id.tile >> 4, rg = id.tile & 15;
+  const int L = T.L;
+  const int pi = e < ell ? e : L + (e - ell);
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  {
+    TwStage st;
+    tw_issue(st, T.tw_fwd + (size_t)pi * kN, rg);
+    tw_store(st, TW);
+    __syncthreads();
+  }
+  const long long na = nat_a(rg);
+  double sb[16], sa[16], x[16];
+  for (int m = 0; m < group; ++m) {
+    const int b = m * outputs + o;
+    const uint32_t g = gal_of(G, b);
+    tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T, m == 0);
+    if (e < ell && add) {
+      double ad[16];
+      load_gal(ad, add + (long long)b * add_stride + (long long)e * kN, na, g);
+      const TwPair pm = T.pmodq[pi];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sb[k] = reduce(sb[k] + mulc(ad[k], pm, p), p, pinv);  // back to p/2 + 1
+    }
+  }
+  if (acc_b) {
+    double ab[16], aa[16];
+    load_gal(ab, acc_b + (long long)o * acc_stride + (long long)e * kN, na, 1u);
+    load_gal(aa, acc_a + (long long)o * acc_stride + (long long)e * kN, na, 1u);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { sb[k] += ab[k]; sa[k] += aa[k]; }  // |sb| <= 1.5 p + 1
+  }
+  uint64_t* ob = ext_b + (long long)o * ext_stride + (long long)e * kN + na;
+  uint64_t* oa = ext_a + (long long)o * ext_stride + (long long)e * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    ob[16 * k] = d2u(canon(sb[k], p, pinv));
+    oa[16 * k] = d2u(canon(sa[k], p, pinv));
+  }
 }
 
 __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
@@ -1081,6 +1141,62 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
                                                              out_a, out_stride, c->d_level + ell, c->dev);
     HCK_CHECK_LAUNCH();
   }
+  return HCK_OK;
+}
+
+// Grouped extended-basis rotations (k_ks_rows_ip_sum): item b = m * outputs + o of d / add (Galois
+// element galois_items[b], key ksk[b]) is member m of output o.  K1 and K2 run over every item, as
+// in ks_fused; the workspace is ks_fused_bytes(c, ell, outputs * group).
+int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const uint64_t* d, long long d_stride,
+                 const uint32_t* galois_items, const uint64_t* const* ksk, const uint64_t* add, long long add_stride,
+                 const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride, uint64_t* ext_b,
+                 uint64_t* ext_a, long long ext_stride, char* ws, hipStream_t s) {
+  const int batch = outputs * group;
+  if (outputs < 1 || group < 1 || batch > kMaxBatchF) return HCK_ERR_ARG;
+  if (c->wide) {
+    // one member at a time, each accumulated into the extended outputs (same residues)
+    for (int m = 0; m < group; ++m) {
+      const uint64_t* keys[kMaxBatchF];
+      uint32_t gals[kMaxBatchF];
+      for (int o = 0; o < outputs; ++o) {
+        keys[o] = ksk[m * outputs + o];
+        gals[o] = galois_items[m * outputs + o];
+      }
+      const long long off = (long long)m * outputs;
+      const int rc = wide_ks(c, ell, outputs, d + off * d_stride, d_stride, 1u, keys,
+                             add ? add + off * add_stride : nullptr, add_stride, m ? ext_b : acc_b, m ? ext_a : acc_a,
+                             m ? ext_stride : acc_stride, nullptr, nullptr, 0, ws, s, ext_b, ext_a, ext_stride, gals);
+      if (rc) return rc;
+    }
+    return HCK_OK;
+  }
+  if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
+  GalF G{};
+  G.per_item = 1;
+  KeyPtrsF kp{};
+  for (int b = 0; b < batch; ++b) {
+    G.g[b] = galois_items[b];
+    kp.k[b] = ksk[b];
+  }
+  const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
+  const long long n = kN;
+  double* r1 = (double*)ws;
+  double* t2 = r1 + (long long)batch * 2 * ell * n;
+  const int last_digit = ell - c->alpha * (beta - 1);
+  k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0,
+                                                                                    r1, ell, batch, c->dev);
+  HCK_CHECK_LAUNCH();
+  auto cols_conv = ext_l - last_digit <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(
+      ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+               modup_consts(c, ell, 0), 1},
+      c->dev);
+  HCK_CHECK_LAUNCH();
+  const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
+  k_ks_rows_ip_sum<<<dim3(groups * kXcds * outputs), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, outputs, group,
+                                                                tiles, add, add_stride, ext_b, ext_a, ext_stride,
+                                                                acc_b, acc_a, acc_stride, c->dev);
+  HCK_CHECK_LAUNCH();
   return HCK_OK;
 }
 

@@ -578,6 +578,9 @@ def prepare_hoisted_baby_rotations(ct: Cipher, offsets, ctx: CKKSContext, strate
     return tuple(out)
 
 
+GIANT_GROUP = 4  # giant steps per grouped extended-basis launch (hck_rotate_ext_sum); 1: one per launch
+
+
 def hoisted_mac_sum(ct: Cipher, baby_offsets, plaintexts: Plaintext, giant_offset: int, giant_count: int,
                     ctx: CKKSContext, strategy: str = "normal", baby_anchor_step: int = -1,
                     baby_rotations=None) -> Cipher:
@@ -611,11 +614,20 @@ def hoisted_mac_sum(ct: Cipher, baby_offsets, plaintexts: Plaintext, giant_offse
     if strategy == "ext_double_hoist" and G > 1:
         ext0 = _lift_ext(part[0, 0], limbs, ctx)
         ext1 = _lift_ext(part[1, 0], limbs, ctx)
-        for g in range(1, G):
-            # each partial rotated by its own giant multiple, summed in the extended basis
-            gg = _galois(g * int(giant_offset), ctx)
-            ctx.rotate_ext(part[0, g], part[1, g], limbs, gg, ctx.key_for_galois(gg), out0=ext0, out1=ext1,
-                           acc=(ext0, ext1))
+        B = int(part.shape[2])
+        step = max(1, min(GIANT_GROUP, 64 // B))  # giants per grouped launch (<= 64 items)
+        for g0 in range(1, G, step):
+            # each partial rotated by its own giant multiple, summed in the extended basis; a group of
+            # giants keeps its running sum on chip and touches the accumulator once
+            gs = list(range(g0, min(G, g0 + step)))
+            gals = [_galois(g * int(giant_offset), ctx) for g in gs]
+            keys = [ctx.key_for_galois(gg) for gg in gals]
+            if len(gs) == 1:
+                ctx.rotate_ext(part[0, gs[0]], part[1, gs[0]], limbs, gals[0], keys[0], out0=ext0, out1=ext1,
+                               acc=(ext0, ext1))
+            else:
+                ctx.rotate_ext_sum(part[0, gs[0]:gs[-1] + 1], part[1, gs[0]:gs[-1] + 1], limbs, gals, keys,
+                                   ext0, ext1, acc=(ext0, ext1))
         acc0, acc1 = ctx.moddown(ext0, limbs), ctx.moddown(ext1, limbs)
     else:
         acc0, acc1 = part[0, G - 1], part[1, G - 1]

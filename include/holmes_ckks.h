@@ -141,6 +141,21 @@ int hck_rotate_ext(const hck_context* ctx, int level_limbs, int batch, uint32_t 
                    int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/* Grouped extended-basis rotations, the giant steps of a double-hoisted BSGS chunk taken `group` at
+ * a time: for o < outputs,
+ *   out[o] = acc[o] + sum_{m < group} (P sigma_m(c0[m][o]) + IP_b(sigma_m(c1[m][o])), IP_a(sigma_m(c1[m][o])))
+ * over the level_limbs Q primes then the K special primes, item (m, o) at c0 / c1 + (m * outputs + o) *
+ * in_stride, member m rotated by galois[m] with key ksk[m] (host arrays of `group`).  The running sum
+ * stays on chip, so the extended accumulator is read and written once per call instead of once per
+ * member (fhe.hoisted_mac_sum, "ext_double_hoist", llama3fhe/operators/linear/config.py:353-360).
+ * outputs * group <= 64; out may alias acc (not c0 / c1); strides as hck_rotate_ext.  Identical
+ * residues to `group` hck_rotate_ext calls accumulating in turn.  Workspace:
+ * hck_rotate_workspace_bytes(ctx, level_limbs, outputs * group). */
+int hck_rotate_ext_sum(const hck_context* ctx, int level_limbs, int outputs, int group, const uint32_t* galois,
+                       const uint64_t* c0, const uint64_t* c1, int64_t in_stride, const uint64_t* const* ksk,
+                       const uint64_t* acc0, const uint64_t* acc1, int64_t acc_stride, uint64_t* out0,
+                       uint64_t* out1, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
 /* hck_rotate / hck_rotate_ext with a Galois element per item (galois[b], host array of `batch`):
  * one launch sequence for rotations by different amounts, each with its own key -- the batched
  * giant step of bench/cmp/holmes_multi_mac.py:180-186 (fhe.homo_rotate_batch) and the baby and

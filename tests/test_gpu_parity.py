@@ -463,3 +463,35 @@ def test_pipelined_keyswitch_schedule_matches_oracle(env, slices):
                 assert np.array_equal(o0[b], w0) and np.array_equal(o1[b], w1), (B, b)
     finally:
         ctx.set_keyswitch_slices(0)
+
+
+@pytest.mark.parametrize("ell,outputs,group", [(20, 5, 3), (9, 16, 4), (24, 1, 2)])
+def test_grouped_ext_rotations_equal_sequential(env, ell, outputs, group):
+    """hck_rotate_ext_sum (a group of giant steps summed on chip, one accumulator pass) against
+    `group` accumulating hck_rotate_ext calls, and its ModDown against the oracle's rotations."""
+    _, client, ctx, orc = env
+    rots = [1, -17, 4096, 333][:group]
+    gs = [ctx.galois_element(r) for r in rots]
+    pairs = [_key_pair(client, ctx, orc, g) for g in gs]
+    rng = np.random.default_rng(1000 * ell + outputs)
+    c0 = _rand(ctx, rng, group * outputs, ell).reshape(group, outputs, ell, ctx.N)
+    c1 = _rand(ctx, rng, group * outputs, ell).reshape(group, outputs, ell, ctx.N)
+    idx = ctx.ext_prime_idx(ell)
+    a0, a1 = _rand(ctx, rng, outputs, len(idx), idx), _rand(ctx, rng, outputs, len(idx), idx)
+    s0, s1 = _dev(a0), _dev(a1)
+    for m in range(group):
+        ctx.rotate_ext(_dev(c0[m]), _dev(c1[m]), ell, gs[m], pairs[m][0], out0=s0, out1=s1, acc=(s0, s1))
+    g0, g1 = _dev(a0), _dev(a1)
+    ctx.rotate_ext_sum(_dev(c0), _dev(c1), ell, gs, [p[0] for p in pairs], g0, g1, acc=(g0, g1))
+    assert np.array_equal(_host(g0), _host(s0)) and np.array_equal(_host(g1), _host(s1))
+    # no accumulator: the first member starts the sum (ModDown of a sum rounds once, so it is pinned
+    # through the sequential rotate_ext, whose ModDown equals the oracle's rotation bit for bit)
+    e0, e1 = ctx.empty(outputs, len(idx), ctx.N), ctx.empty(outputs, len(idx), ctx.N)
+    ctx.rotate_ext_sum(_dev(c0), _dev(c1), ell, gs, [p[0] for p in pairs], e0, e1)
+    r0, r1 = ctx.rotate_ext(_dev(c0[0]), _dev(c1[0]), ell, gs[0], pairs[0][0])
+    for m in range(1, group):
+        ctx.rotate_ext(_dev(c0[m]), _dev(c1[m]), ell, gs[m], pairs[m][0], out0=r0, out1=r1, acc=(r0, r1))
+    assert np.array_equal(_host(e0), _host(r0)) and np.array_equal(_host(e1), _host(r1))
+    w0, w1 = orc.rotate(ell, gs[0], c0[0, 0], c1[0, 0], pairs[0][1])
+    one0, one1 = ctx.rotate_ext(_dev(c0[0, :1]), _dev(c1[0, :1]), ell, gs[0], pairs[0][0])
+    assert np.array_equal(_host(ctx.moddown(one0, ell))[0], w0)

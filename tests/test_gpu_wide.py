@@ -202,3 +202,8 @@ def test_encrypt_rotate_decrypt(env):
     err2 = float(np.max(np.abs(client.decrypt(sq).real - np.roll(x, -3) ** 2)))
     print(f"wide product + rescale: decrypted error 2^{math.log2(err2):.1f}", flush=True)
     assert err2 < 2.0**-30
+
+
+@pytest.mark.parametrize("ell,outputs,group", [(19, 5, 3)])
+def test_grouped_ext_rotations(env, ell, outputs, group):
+    G.test_grouped_ext_rotations_equal_sequential(env, ell, outputs, group)
