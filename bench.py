@@ -31,10 +31,11 @@ limbs, scale 2^50; its line reports seconds per block and the decrypted error ag
 oracle of the same arithmetic.
 
 ``--workload layer``: one encrypted Llama-3-8B prefill layer at 128 tokens (the metric's "s per
-encrypted layer"): RMSNorm1, complex QKV projections, RoPE, causal Alg2 attention over 32 heads,
-W_O, residual, one two-pass refresh, the SwiGLU MLP block at width 14336, residual; 38 limbs of
-50-bit primes, dnum 5, scale 2^50; its line reports seconds per layer and the decrypted error
-against the float64 model of the same polynomials.
+encrypted layer"), steady state as the reference times its layer 10: input refresh, RMSNorm1,
+complex QKV projections, RoPE, causal Alg2 attention over 32 heads (series inputs refreshed), W_O,
+residual, refresh, the SwiGLU MLP block at width 14336, residual; 38 limbs of 50-bit primes, dnum 5,
+scale 2^50; its line reports seconds per layer (and the model's first layer beside it) and the
+decrypted error against the float64 model of the same polynomials.
 
 ``--workload c2wide``: the C2 shape (16 ciphertexts, 16 distinct rotation keys) on the reference's
 production chain (assets/feature_major.json: 38 Q limbs of 60/59-bit primes, dnum 5, 8 special
@@ -1042,10 +1043,14 @@ def run_c5(args) -> int:
 
 def run_layer(args) -> int:
     """N1: one encrypted Llama-3-8B prefill layer (holmes_amd.prefill.PrefillLayer) on 128 tokens x
-    4096 features (16 ciphertexts at 38 limbs): weights N(0, 0.02^2), gammas 1 + N(0, 0.1^2),
-    x ~ N(0, 1).  Keys, the refresh program and the weight objects are built before the timed
-    region; every weight diagonal is encoded inside it (per projection chunk, as the reference
-    encodes per call), while the attention's slot constants keep their encodings across steps."""
+    4096 features (16 ciphertexts, 38-limb chain): weights N(0, 0.02^2), gammas 1 + N(0, 0.1^2),
+    x ~ N(0, 1).  ``value`` is the steady-state layer, as the reference times its layer 10
+    (bench/t2_layer.py): the input arrives at 4 limbs (the previous layer's output level) and is
+    refreshed first, and the softmax's series inputs are refreshed; the model's first layer (fresh
+    input at 38 limbs, one refresh) is timed beside it.  Keys, the refresh program and the weight
+    objects are built before the timed region; every weight diagonal is encoded inside it (per
+    projection chunk, as the reference encodes per call), while the attention's slot constants keep
+    their encodings across steps."""
 
     import math
 
@@ -1063,35 +1068,45 @@ def run_layer(args) -> int:
     client, ctx = fhe.generate_client_context(P.prefill_context_spec(seed))
     rng = np.random.default_rng(seed)
     w = P.random_weights(spec, rng)
-    layer, rots = P.setup_prefill_layer(client, ctx, w, spec)
+    first, rots = P.setup_prefill_layer(client, ctx, w, spec)
+    steady = P.PrefillLayer(ctx, w, spec, program=first.program, config=first.config, steady=True)
     layout = FeatureMajorPrefillLayout()
     x = rng.normal(size=(128, spec.hidden_dim))
-    cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
+    packed = layout.pack(x)
+    cts_first = [client.encrypt(row, cur_limbs=ctx.L) for row in packed]
+    cts_steady = [client.encrypt(row, cur_limbs=4) for row in packed]
     _log(f"layer setup {time.perf_counter() - t0:.1f} s: {len(rots)} rotation keys, {ctx.L} limbs, dnum {ctx.dnum}")
-    for _ in range(warmup):
-        layer.forward(cts)
+
+    def timed(layer, cts, label):
+        for _ in range(warmup):
+            layer.forward(cts)
+        secs, all_stages = [], []
+        for _ in range(steps):
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            out, stages = layer.forward(cts)
+            torch.cuda.synchronize()
+            secs.append(time.perf_counter() - w0)
+            all_stages.append(stages)
+            _log(f"{label} step {len(secs)}: {secs[-1]:.3f} s")
+        med = float(np.median(secs))
+        return out, med, {k: float(np.median([st[k] for st in all_stages])) for k in all_stages[0]}
+
+    out_f, s_first, stages_f = timed(first, cts_first, "first layer")
+    out, s_wall, stages = timed(steady, cts_steady, "steady layer")
     with _CallLog(ctx) as log:
         torch.cuda.synchronize()
-        out, stages = layer.forward(cts)
+        steady.forward(cts_steady)
         torch.cuda.synchronize()
     limbs_moved, ks = log.limbs_bytes()
     layer_bytes = limbs_moved * ctx.N * 8
-    secs, all_stages = [], []
-    for _ in range(steps):
-        torch.cuda.synchronize()
-        w0 = time.perf_counter()
-        out, stages = layer.forward(cts)
-        torch.cuda.synchronize()
-        secs.append(time.perf_counter() - w0)
-        all_stages.append(stages)
-        _log(f"layer step {len(secs)}: {secs[-1]:.3f} s")
-    s_wall = float(np.median(secs))
-    stages = {k: float(np.median([st[k] for st in all_stages])) for k in all_stages[0]}
     ref = P.prefill_layer_numpy(x, w, spec)
     want = layout.pack(ref["output"])
     err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
+    err_f = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out_f))
     mag = float(np.max(np.abs(ref["output"])))
-    _log(f"layer: {s_wall:.3f} s per layer, stages {stages}, decrypted max error {err:.3e} of magnitude {mag:.2f}")
+    _log(f"steady layer: {s_wall:.3f} s, stages {stages}, error {err:.3e}; first layer {s_first:.3f} s, "
+         f"error {err_f:.3e}; magnitude {mag:.2f}")
     ks_items = sum(b for _, b, _ in ks)
     cpu = None
     if not args.no_cpu:
@@ -1107,22 +1122,25 @@ def run_layer(args) -> int:
         total = sum(b * t_rot * l / 16 for _, b, l in ks)
         cpu = {"value": round(total, 1), "unit": "s", "cores": int(O.num_threads()), "kind": "port",
                "sample": f"extrapolated from the key switches alone: one rotation at 16 limbs of the 38-limb chain "
-                         f"({t_rot:.3f} s), scaled by limbs, over the {ks_items} key-switched items of one layer "
-                         f"(MACs, encodes, rescales not counted)"}
+                         f"({t_rot:.3f} s), scaled by limbs, over the {ks_items} key-switched items of one "
+                         f"steady-state layer (MACs, encodes, rescales not counted)"}
     achieved = layer_bytes / s_wall / 1e9
     print(json.dumps({
         "metric": "s per encrypted Llama-3-8B layer (128-tok prefill, 1 GPU)",
         "value": round(s_wall, 4), "unit": "s", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(s_wall * 1e3, 2), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
         "dtype": "u64", "data": "synthetic",
-        "config": {"workload": "N1 prefill layer, 128 tokens: RMSNorm1 (deg-15 rsqrt), complex QKV (2 x 4096x4096 BSGS), "
-                               "RoPE, causal Alg2 attention 32/8/128 (exp deg 15, rsqrt deg 31), W_O, residual, "
-                               "two-pass refresh of 16 cts, SwiGLU 4096->14336->4096 (SiLU deg 63), residual; "
-                               "38 limbs, scale 2^50, dnum 5",
+        "config": {"workload": "N1 prefill layer, steady state, 128 tokens: input refresh, RMSNorm1 (deg-15 rsqrt), "
+                               "complex QKV (2 x 4096x4096 BSGS), RoPE, causal Alg2 attention 32/8/128 (exp deg 15 "
+                               "and rsqrt deg 31 on refreshed inputs), W_O, residual, refresh, SwiGLU "
+                               "4096->14336->4096 (SiLU deg 63), residual; every refresh two-pass; 38 limbs, "
+                               "scale 2^50, dnum 5",
                    "decrypted_max_error": err, "output_magnitude": mag, "error_bits": round(-math.log2(err), 2),
                    "softmax_vs_exact": ref["softmax_vs_exact"], "in_range": ref["in_range"],
-                   "rotation_keys": len(rots),
+                   "rotation_keys": len(rots), "refreshed_items_per_layer": steady.ops.refreshes // (warmup + steps + 1),
                    "stage_seconds": {k: round(v, 4) for k, v in stages.items()},
+                   "first_layer_seconds": round(s_first, 4), "first_layer_error": err_f,
+                   "first_layer_stage_seconds": {k: round(v, 4) for k, v in stages_f.items()},
                    "key_switched_items": ks_items, "algorithmic_bytes_per_step": layer_bytes},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,

@@ -59,6 +59,7 @@ __all__ = ["PrefillSpec", "PrefillPolynomials", "PrefillAttention", "PrefillLaye
 
 LANES = 8
 CTS = 16
+PV_INPUT_LIMBS = 5  # PV (mask + product) -> 3, W_O -> 2, residual, then the refresh
 HALF = 16384
 SLOTS = 32768
 
@@ -367,8 +368,14 @@ class PrefillAttention:
     queries are copied into both halves and one product, one channel fold and one packing rotation
     serve two keys."""
 
-    def __init__(self, ops, spec: PrefillSpec | None = None, polys: PrefillPolynomials | None = None):
+    def __init__(self, ops, spec: PrefillSpec | None = None, polys: PrefillPolynomials | None = None, *,
+                 refresh_series_inputs: bool = False):
         self.ops = ops
+        # refresh the exp series' input (16 ciphertexts, |x| <= 1) and the inverse square root's (one
+        # packed ciphertext) before evaluating them: the steady-state layer, whose attention starts
+        # from a refreshed layer input rather than a fresh encryption at the top of the chain
+        # (the reference's refresh_softmax_exp_inputs, llama3fhe/graph/prefill.py:134-221)
+        self.refresh_series_inputs = bool(refresh_series_inputs)
         self.spec = PrefillSpec() if spec is None else spec
         self.spec.validate()
         self.polys = PrefillPolynomials.fit(self.spec) if polys is None else polys
@@ -522,6 +529,7 @@ class PrefillAttention:
         # the affine map lands on the prime of the next level: the series input's exact scale
         x = ops.mac([(S2, self.exp_alpha_valid)], out_scale=ops.ideal_scale(ops.limbs(S2) - 1))
         x = ops.add_const(x, self.exp_beta) if self.exp_beta else x
+        x = self._refreshed_series_input(x)
         y = ops.poly(x, self.polys.exp)
         # invalid positions hold x = beta: remove the public E(0) there (no level)
         y = ops.add_vec(y, SlotConst(-self.exp_at_zero * self.invalid.value))
@@ -529,11 +537,23 @@ class PrefillAttention:
         packed = ops.mac([(ops.rotate(rows[c], -8 * c), self.rowc[c]) for c in range(CTS)])
         z = ops.mac([(packed, self.rs_in)], out_scale=ops.ideal_scale(ops.limbs(packed) - 1))
         z = ops.add_vec(z, self.rs_shift)                # slots outside the packed rows stay at 0
+        z = self._refreshed_series_input(z)
         lam = ops.poly(z, self.polys.rsqrt)             # rsqrt(R / n) at (h, c, t)
         spread = ops.rotate(ops.copies(lam, CTS), [8 * c for c in range(CTS)])
         lam_c = self._spread_keys(ops.mac([(spread, self.inv_sqrt_count)]))   # 1 / sqrt(R) everywhere
         yl = ops.mul(y, lam_c)
         return ops.mul(yl, yl)
+
+    def _refreshed_series_input(self, x):
+        """With refresh_series_inputs: a two-pass refresh of a series input (|x| <= 1), then one
+        scalar product that puts it back on its level's prime (the series' exact-scale chain)."""
+
+        if not self.refresh_series_inputs:
+            return x
+        ops = self.ops
+        x = ops.refresh(x, bound_bits=0)
+        lim = ops.limbs(x) - 1
+        return ops.adjust(x, lim, ops.ideal_scale(lim))
 
     def pv(self, P, V):
         """sum_k P[h][q][k] Vz(k) for every query ciphertext: complex feature-major outputs.  The
@@ -545,6 +565,10 @@ class PrefillAttention:
         added to the lower half's."""
 
         ops = self.ops
+        if ops.limbs(P) > PV_INPUT_LIMBS:
+            # the column mask, the product, W_O and the residual need no more: the rest of the
+            # layer's work runs on fewer limbs (the residual is refreshed after it)
+            P = ops.drop(P, PV_INPUT_LIMBS)
         if ops.limbs(V) > ops.limbs(P):
             V = ops.drop(V, ops.limbs(P))                 # the carriers only need P's level
         v_lo = self._lane_carriers(V, 0, self.lane[False])
@@ -615,10 +639,16 @@ def prefill_key_rotations(spec: PrefillSpec, config, mlp_spec, bootstrap_spec, l
 class PrefillLayer:
     """One encrypted prefill layer on the GPU: RMSNorm1, projections A and V (one baby-rotation set
     for both), RoPE, the attention core, W_O, the residual, one two-pass refresh of the residual,
-    the MLP block and the second residual."""
+    the MLP block and the second residual.
+
+    ``steady``: the layer as it runs inside the model (the reference's layer_idx > 0 schedule,
+    llama3fhe/graph/prefill.py:217-221,392-459): its input is the previous layer's output at a low
+    level, so it is refreshed first (two passes, as one batch), and the attention refreshes the exp
+    series' input (16 ciphertexts) and the inverse square root's (one packed ciphertext).  Without
+    it the layer is the model's first, fed by a fresh encryption at the top of the chain."""
 
     def __init__(self, ctx, weights: DecodeWeights, spec: PrefillSpec | None = None, *, program, config=None,
-                 mlp_spec=None):
+                 mlp_spec=None, steady: bool = False):
         from .decode import CipherOps
         from .layouts import FeatureMajorPrefillLayout
         from .linear import LinearOperator, LinearWeight
@@ -632,7 +662,8 @@ class PrefillLayer:
         self.config = default_config() if config is None else config
         self.ops = CipherOps(ctx, program)
         self.program = program
-        self.attn = PrefillAttention(self.ops, self.spec)
+        self.steady = bool(steady)
+        self.attn = PrefillAttention(self.ops, self.spec, refresh_series_inputs=self.steady)
         self.rms = rmsnorm_coefficients(self.spec.rms_degree, self.spec.rms_interval, self.spec.eps)
         self.op = LinearOperator(crypto_context=ctx, token_lanes=LANES, config=self.config)
         gamma = np.asarray(weights.input_layernorm, dtype=np.float64)
@@ -667,6 +698,9 @@ class PrefillLayer:
             t0 = now
 
         x_cts = tuple(x_cts)
+        if self.steady:
+            x_cts = tuple(ops.items(ops.refresh(ops.batch(x_cts), bound_bits=5)))
+            mark("refresh_input")
         xn = rmsnorm_fhe(x_cts, None, coeffs=self.rms, layout=self.layout, crypto_context=ctx).outputs
         mark("rmsnorm1")
         prepared = self.op.prepare(xn, self.spec.hidden_dim)
@@ -695,9 +729,10 @@ class PrefillLayer:
         return tuple(ops.items(out)), t
 
 
-def setup_prefill_layer(client, ctx, weights: DecodeWeights, spec: PrefillSpec | None = None, config=None):
+def setup_prefill_layer(client, ctx, weights: DecodeWeights, spec: PrefillSpec | None = None, config=None,
+                        steady: bool = False):
     """Every rotation key of the layer and its refresh program, then the layer (``client`` holds
-    the secret key; the layer itself only sees ``ctx``)."""
+    the secret key; the layer itself only sees ``ctx``); ``steady`` as for ``PrefillLayer``."""
 
     from .bootstrap import generate
     from .mlp import default_config
@@ -708,4 +743,4 @@ def setup_prefill_layer(client, ctx, weights: DecodeWeights, spec: PrefillSpec |
     rots = prefill_key_rotations(spec, config, prefill_mlp_spec(spec), bspec, int(ctx.logN))
     client.generate_rotation_keys(rots)
     program = generate(ctx, bspec)
-    return PrefillLayer(ctx, weights, spec, program=program, config=config), rots
+    return PrefillLayer(ctx, weights, spec, program=program, config=config, steady=steady), rots

@@ -3,7 +3,9 @@ reference's llama3fhe/graph/prefill.py:57 ``evaluate`` for the first layer: RMSN
 causal Alg2 attention, W_O, residual, one two-pass refresh, the SwiGLU MLP block at width 14336,
 residual).  Llama-3-8B shapes with seeded random weights N(0, 0.02^2) and gammas 1 + N(0, 0.1^2),
 input N(0, 1), the 38-limb chain (depth 37, dnum 5, 50-bit primes, scale 2^50).  Every decrypted
-output slot is within 2^-16 of the float64 model of the same polynomials (prefill_layer_numpy)."""
+output slot is within 2^-16 of the float64 model of the same polynomials (prefill_layer_numpy), for
+the model's first layer (fresh input at 38 limbs) and for a steady-state layer (input at 4 limbs,
+refreshed first; the softmax's series inputs refreshed).""" 
 
 import math
 import time
@@ -18,8 +20,8 @@ torch = pytest.importorskip("torch")
 SEED = 20261206
 
 
-@pytest.mark.timeout(1100)
-def test_prefill_layer_decrypts_to_model():
+@pytest.fixture(scope="module")
+def layer_env():
     from holmes_amd import fhe
     from holmes_amd import prefill as P
     from holmes_amd.layouts import FeatureMajorPrefillLayout
@@ -34,14 +36,38 @@ def test_prefill_layer_decrypts_to_model():
     print(f"prefill layer setup {time.perf_counter() - t0:.1f} s, {len(rots)} rotation keys", flush=True)
     layout = FeatureMajorPrefillLayout()
     x = rng.normal(size=(128, 4096))
-    cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
-    out, stages = layer.forward(cts)
-    print(f"prefill layer: stages {stages}, output at {out[0].state.cur_limbs} limbs", flush=True)
     ref = P.prefill_layer_numpy(x, w, spec)
+    assert all(ref["in_range"].values()), ref["in_range"]
+    return P, client, ctx, spec, w, layer, layout, x, ref
+
+
+def _check(client, out, layout, ref, what):
     want = layout.pack(ref["output"])
     err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
     mag = float(np.max(np.abs(ref["output"])))
-    print(f"prefill layer max error 2^{math.log2(err):.2f} of magnitude {mag:.2f}; softmax vs exact "
-          f"{ref['softmax_vs_exact']:.2e}; in range {ref['in_range']}", flush=True)
-    assert all(ref["in_range"].values()), ref["in_range"]
+    print(f"{what}: max error 2^{math.log2(err):.2f} of magnitude {mag:.2f}; softmax vs exact "
+          f"{ref['softmax_vs_exact']:.2e}", flush=True)
     assert err < 2.0**-16
+
+
+@pytest.mark.timeout(1100)
+def test_prefill_layer_decrypts_to_model(layer_env):
+    P, client, ctx, spec, w, layer, layout, x, ref = layer_env
+    cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
+    out, stages = layer.forward(cts)
+    print(f"prefill layer: stages {stages}, output at {out[0].state.cur_limbs} limbs", flush=True)
+    _check(client, out, layout, ref, "first layer")
+
+
+@pytest.mark.timeout(1100)
+def test_steady_state_layer_decrypts_to_model(layer_env):
+    """The layer as it runs inside the model: its input arrives at 4 limbs (the previous layer's
+    output level) and is refreshed first; the exp and inverse-square-root inputs are refreshed too."""
+    P, client, ctx, spec, w, layer, layout, x, ref = layer_env
+    steady = P.PrefillLayer(ctx, w, spec, program=layer.program, config=layer.config, steady=True)
+    cts = [client.encrypt(row, cur_limbs=4) for row in layout.pack(x)]
+    out, stages = steady.forward(cts)
+    print(f"steady layer: stages {stages}, output at {out[0].state.cur_limbs} limbs, "
+          f"{steady.ops.refreshes} refreshed items", flush=True)
+    assert out[0].state.cur_limbs >= 3
+    _check(client, out, layout, ref, "steady layer")

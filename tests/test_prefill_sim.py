@@ -132,4 +132,29 @@ def test_attention_dataflow_on_the_slot_simulator(env):
     print(f"attention sim: max error {err:.3e} of magnitude {mag:.3f}; output at {ops.limbs(out)} limbs; "
           f"probabilities at {ops.limbs(mid['probs'])}; log {ops.log[:3]}")
     assert err < 1e-9 * mag
-    assert ops.limbs(out) >= 4  # W_O and the residual still fit
+    assert ops.limbs(out) >= 3  # W_O (one level) leaves the residual two limbs for its refresh
+
+
+def test_steady_state_attention_on_the_slot_simulator(env):
+    """The steady-state layer's attention: A and V at the level a refreshed layer input leaves after
+    RMSNorm1 and the projections (refresh output 21 -> RMSNorm 14 -> projections 13), the exp and
+    inverse-square-root inputs refreshed; the output must still leave levels for W_O and the residual."""
+    spec, w, x, xn = env
+    cs = P.prefill_context_spec()
+    q_primes, _ = cs.prime_chain()
+    scale = 2.0**50
+    ops = SlotOps(q_primes, *make_programs(q_primes, len(q_primes), scale))
+    start = ops.refresh_limbs() - 8
+    attn = P.PrefillAttention(ops, spec, refresh_series_inputs=True)
+    A, V = P.attention_input_numpy(xn, spec, w)
+    out, mid = attn.forward(SimCt(A, start, scale), SimCt(V, start, scale))
+    model = P.attention_numpy(xn, w, spec)
+    oz = model["attn"].reshape(128, 32, 128)
+    oz = np.hstack([(oz[:, :, :64] + 1j * oz[:, :, 64:]).reshape(128, 2048), np.zeros((128, 2048))])
+    lay = FeatureMajorPrefillLayout()
+    want = np.asarray(lay.pack(oz.real)) + 1j * np.asarray(lay.pack(oz.imag))
+    err = np.max(np.abs(out.values[:, :16384] - want[:, :16384]))
+    print(f"steady attention sim: A at {start} limbs, output at {ops.limbs(out)} limbs, {ops.refreshes} refreshed "
+          f"items, error {err:.2e}")
+    assert err < 1e-9 * np.max(np.abs(want))
+    assert ops.limbs(out) >= 3 and ops.refreshes == 17
