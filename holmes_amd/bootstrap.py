@@ -544,15 +544,32 @@ def _items(ct: Cipher, lo: int, hi: int) -> Cipher:
     return ct.cipher_like([c[lo:hi] for c in ct.cv], batch_size=hi - lo)
 
 
-def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *, bound_bits: int = 0) -> Cipher:
+def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *, bound_bits: int = 0,
+              timings: dict | None = None) -> Cipher:
     """Refresh ``cipher`` (two components, >= 2 limbs, 2^log_slots slots, |slot| <= 2^bound_bits; a batch
     is refreshed as one: every key switch of the pipeline covers all its items) to
     ``spec.output_levels`` limbs (0: all the program leaves).  The result keeps the input's scaling
     factor; the input is not consumed.  ``bound_bits`` moves the message 2^bound_bits further below
-    q_0 in the scale-down product and multiplies it back by the integer at the end (no level)."""
+    q_0 in the scale-down product and multiplies it back by the integer at the end (no level).
+    ``timings``: a dict that receives the seconds of each step (the device is synchronised between
+    steps, so only for measurement)."""
 
     ctx = context
     spec = program.spec
+    clock = [None]
+
+    def mark(name):
+        if timings is None:
+            return
+        import time as _time
+
+        torch.cuda.synchronize()
+        now = _time.perf_counter()
+        if clock[0] is not None:
+            timings[name] = timings.get(name, 0.0) + now - clock[0]
+        clock[0] = now
+
+    mark("start")
     if cipher.is_ext or len(cipher.cv) != 2:
         raise ValueError("bootstrap takes a two-component, non-extended ciphertext")
     B = int(cipher.batch_size)
@@ -581,6 +598,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
                                                      scaling_factor=S))
     # 2b. sparse slots: the trace onto the period-n subring (the gain R is in the CoeffToSlot constant)
     ct = _trace(ct, spec, ctx)
+    mark("scale_down_modraise")
     # 3. CoeffToSlot at the raised level: (M_lo + i M_hi) / (2 q_0 K') up to the shares rho
     ct = apply_stages(ct, program.cts, program.cts_rho, ctx, keep)
     # 4. real and imaginary parts before the rescales (t / K' with t = M / q_0), then b1 rescales
@@ -588,6 +606,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
     re = fhe.homo_add(ct, conj, ctx)
     im = fhe.homo_mul_i(fhe.homo_sub(ct, conj, ctx), ctx, negative=True)
     both = _rescale_times(fhe.pack_cipher_batch([re, im]), b1, S, ctx)
+    mark("coeff_to_slot")
     # 5. EvalMod: sin(2 pi t) = cos(2 pi (K' u - 1/4)) by the interpolant and double angles
     ev = _PSEval(ctx, both, program.evalmod_limbs, S, int(spec.cheb_degree), ctx.q_primes)
     y = ev.evaluate(program.cheb)
@@ -595,6 +614,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
         y = ev.double_minus(y, y)
     yr, yi = _items(y, 0, B), _items(y, B, 2 * B)
     z = fhe.homo_add(yr, fhe.homo_mul_i(yi, ctx), ctx)
+    mark("eval_mod")
     # 6. SlotToCoeff (q_0 / (2 pi S_out) in the shares), b2 rescales, the integer 2^bits
     z = _rescale_times(apply_stages(z, program.stc, program.stc_rho, ctx, keep), b2, S_in * 2.0**-bits, ctx)
     # 6b. sparse slots: project the output onto the subring; its gain R = 2^j is part of the 2^bits
@@ -608,6 +628,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
     target = int(spec.output_levels) or program.output_limbs
     if int(z.state.cur_limbs) > target:
         z = fhe.align_to(z, z.state.replace(cur_limbs=target), ctx)
+    mark("slot_to_coeff")
     return z
 
 
