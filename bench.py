@@ -1045,8 +1045,9 @@ def run_layer(args) -> int:
     """N1: one encrypted Llama-3-8B prefill layer (holmes_amd.prefill.PrefillLayer) on 128 tokens x
     4096 features (16 ciphertexts, 38-limb chain): weights N(0, 0.02^2), gammas 1 + N(0, 0.1^2),
     x ~ N(0, 1).  ``value`` is the steady-state layer, as the reference times its layer 10
-    (bench/t2_layer.py): the input arrives at 4 limbs (the previous layer's output level) and is
-    refreshed first, and the softmax's series inputs are refreshed; the model's first layer (fresh
+    (bench/t2_layer.py): the input arrives at the previous layer's output level and is refreshed
+    first, and the softmax's series inputs are refreshed (each refresh raised only as far as its
+    consumer needs); the model's first layer (fresh
     input at 38 limbs, one refresh) is timed beside it.  Keys, the refresh program and the weight
     objects are built before the timed region; every weight diagonal is encoded inside it (per
     projection chunk, as the reference encodes per call), while the attention's slot constants keep
@@ -1069,12 +1070,13 @@ def run_layer(args) -> int:
     rng = np.random.default_rng(seed)
     w = P.random_weights(spec, rng)
     first, rots = P.setup_prefill_layer(client, ctx, w, spec)
-    steady = P.PrefillLayer(ctx, w, spec, program=first.program, config=first.config, steady=True)
+    steady = P.PrefillLayer(ctx, w, spec, program=first.program, config=first.config, steady=True,
+                            programs=first.programs)
     layout = FeatureMajorPrefillLayout()
     x = rng.normal(size=(128, spec.hidden_dim))
     packed = layout.pack(x)
     cts_first = [client.encrypt(row, cur_limbs=ctx.L) for row in packed]
-    cts_steady = [client.encrypt(row, cur_limbs=4) for row in packed]
+    cts_steady = [client.encrypt(row, cur_limbs=P.LAYER_OUTPUT_LIMBS) for row in packed]
     _log(f"layer setup {time.perf_counter() - t0:.1f} s: {len(rots)} rotation keys, {ctx.L} limbs, dnum {ctx.dnum}")
 
     def timed(layer, cts, label):

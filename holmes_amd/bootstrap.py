@@ -79,6 +79,7 @@ class BootstrapSpec:
     mode: str = "modraise_first"
     dim1: tuple | None = None
     baby_step: tuple | None = None
+    raise_limbs: int = 0         # ModRaise target (0: the context's top); fewer leave fewer levels, cost less
     message_ratio_bits: int = 8  # message <= 2^-8 q_0 at one limb: sine error <= 2^-13.3 relative
     mod_bound: int = 24          # |I| <= mod_bound on every coefficient (sparse secret)
     double_angle: int = 3
@@ -87,6 +88,8 @@ class BootstrapSpec:
     def validate(self, log_n: int) -> None:
         if not 1 <= int(self.log_slots) <= int(log_n) - 1:
             raise ValueError(f"log_slots must lie in [1, {int(log_n) - 1}], got {self.log_slots}")
+        if int(self.raise_limbs) < 0 or int(self.raise_limbs) == 1:
+            raise ValueError("raise_limbs must be 0 (the top of the chain) or at least 2")
         if str(self.mode) != "modraise_first":
             raise ValueError("only mode='modraise_first' is supported")
         if str(self.strategy) not in STRATEGIES:
@@ -382,7 +385,25 @@ def generate(context: CKKSContext, spec: BootstrapSpec) -> BootstrapProgram:
                          "generate them from requirements(spec, log_n).rotations")
     if ctx.relin_key is None:
         raise ValueError("bootstrap needs the relinearisation key")
-    return plan_program(spec, ctx.q_primes, float(ctx.scale_at(ctx.L)), ctx.L, int(ctx.logN))
+    raise_to = min(ctx.L, int(spec.raise_limbs)) if int(spec.raise_limbs) else ctx.L
+    return plan_program(spec, ctx.q_primes, float(ctx.scale_at(ctx.L)), raise_to, int(ctx.logN))
+
+
+def raise_for_output(spec: BootstrapSpec, q_primes, limbs_needed: int, *, two_pass: bool = True,
+                     log_n: int = 16) -> int:
+    """The fewest ModRaise limbs whose program leaves ``limbs_needed`` limbs after the refresh (one
+    fewer with the two-pass correction's final rescale); the whole chain if none leaves enough."""
+
+    L = len(q_primes)
+    need = int(limbs_needed) + (1 if two_pass else 0)
+    for raise_to in range(2, L + 1):
+        try:
+            out = plan_program(spec, q_primes, 2.0**50, raise_to, log_n).output_limbs
+        except ValueError:
+            continue
+        if out >= need:
+            return raise_to
+    return L
 
 
 def plan_program(spec: BootstrapSpec, q_primes, scale: float, raise_to: int, log_n: int = 16) -> BootstrapProgram:

@@ -461,6 +461,7 @@ class CipherOps:
                                                                                LinearOperatorConfig, LinearWeight)
         self.slots = int(ctx.max_slots)
         self.refreshes = 0
+        self.refresh_levels: list = []   # (input limbs, output limbs) of each refresh
         self._flags = torch.zeros(64, dtype=torch.int32, device=ctx.device)
 
     def _encode(self, vec, limbs: int, scale: float):
@@ -665,14 +666,16 @@ class CipherOps:
         ev = PSEvaluator(self.ctx, ct, self.limbs(ct), self.scale(ct), len(coeffs) - 1, self.ctx.q_primes)
         return ev.evaluate(coeffs)
 
-    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False):
+    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False, program=None):
         """Two-pass bootstrap (|slots| <= 2^bound_bits); ``deep`` uses the program that leaves more
-        levels."""
+        levels, ``program`` any other."""
 
-        prog = self.deep_program if deep else self.program
+        prog = program if program is not None else (self.deep_program if deep else self.program)
         self.refreshes += int(ct.batch_size)
-        return self._bs.bootstrap_with_correction(ct, self.ctx, prog, iterations=2, precision_bits=12,
-                                                  bound_bits=int(bound_bits))
+        out = self._bs.bootstrap_with_correction(ct, self.ctx, prog, iterations=2, precision_bits=12,
+                                                 bound_bits=int(bound_bits))
+        self.refresh_levels.append((self.limbs(ct), self.limbs(out)))
+        return out
 
     def drop(self, ct, limbs: int):
         return self._fhe.align_to(ct, ct.state.replace(cur_limbs=int(limbs)), self.ctx)

@@ -124,12 +124,33 @@ def prefill_mlp_spec(spec: PrefillSpec):
                         rms_degree=spec.rms_degree, rms_interval=spec.post_rms_interval, eps=spec.eps)
 
 
-def prefill_bootstrap_spec():
-    """The refresh of the attention residual: full slots, level budget (3, 3)."""
+def prefill_bootstrap_spec(raise_limbs: int = 0):
+    """The layer's refreshes: full slots, level budget (3, 3), ModRaise to ``raise_limbs`` (0: the
+    top of the chain)."""
 
     from .bootstrap import BootstrapSpec
 
-    return BootstrapSpec(log_slots=15, level_budget=(3, 3))
+    return BootstrapSpec(log_slots=15, level_budget=(3, 3), raise_limbs=int(raise_limbs))
+
+
+# Limbs each refresh of the layer must leave (after the two-pass correction): the residual before
+# the MLP block (its 19 levels, then at least 2 for the next layer's input refresh), the steady
+# layer's input (RMSNorm1 8 + projections 1, then scores 3, mean 2 and the exp series' affine map 1
+# before its own refresh, which needs 2), the exp series' input (its adjust 1, the series 5, then
+# y^2 / pack / affine 3 before the inverse square root's refresh, and y down to p at 5 limbs for PV),
+# and the inverse square root's input (adjust 1, series 6, spread 1, y lambda 1, p 1, PV at 5).
+REFRESH_LIMBS = {"residual": 21, "input": 17, "exp": 13, "rsqrt": 15}
+MLP_LEVELS = 19                  # levels FeatureMajorMLPBlock takes at prefill_mlp_spec (RMSNorm2 to down_proj)
+LAYER_OUTPUT_LIMBS = REFRESH_LIMBS["residual"] - MLP_LEVELS   # the next layer's input level
+
+
+def refresh_raise_limbs(q_primes) -> dict:
+    """ModRaise target of each refresh of the layer: the fewest limbs that leave ``REFRESH_LIMBS``."""
+
+    from .bootstrap import raise_for_output
+
+    spec = prefill_bootstrap_spec()
+    return {k: raise_for_output(spec, q_primes, v) for k, v in REFRESH_LIMBS.items()}
 
 
 # ---------------------------------------------------------------------------- float64 semantics
@@ -369,13 +390,14 @@ class PrefillAttention:
     serve two keys."""
 
     def __init__(self, ops, spec: PrefillSpec | None = None, polys: PrefillPolynomials | None = None, *,
-                 refresh_series_inputs: bool = False):
+                 refresh_series_inputs: bool = False, series_programs: dict | None = None):
         self.ops = ops
         # refresh the exp series' input (16 ciphertexts, |x| <= 1) and the inverse square root's (one
         # packed ciphertext) before evaluating them: the steady-state layer, whose attention starts
         # from a refreshed layer input rather than a fresh encryption at the top of the chain
         # (the reference's refresh_softmax_exp_inputs, llama3fhe/graph/prefill.py:134-221)
         self.refresh_series_inputs = bool(refresh_series_inputs)
+        self.series_programs = dict(series_programs or {})  # "exp" / "rsqrt" -> program (default: ops')
         self.spec = PrefillSpec() if spec is None else spec
         self.spec.validate()
         self.polys = PrefillPolynomials.fit(self.spec) if polys is None else polys
@@ -529,7 +551,7 @@ class PrefillAttention:
         # the affine map lands on the prime of the next level: the series input's exact scale
         x = ops.mac([(S2, self.exp_alpha_valid)], out_scale=ops.ideal_scale(ops.limbs(S2) - 1))
         x = ops.add_const(x, self.exp_beta) if self.exp_beta else x
-        x = self._refreshed_series_input(x)
+        x = self._refreshed_series_input(x, "exp")
         y = ops.poly(x, self.polys.exp)
         # invalid positions hold x = beta: remove the public E(0) there (no level)
         y = ops.add_vec(y, SlotConst(-self.exp_at_zero * self.invalid.value))
@@ -537,21 +559,21 @@ class PrefillAttention:
         packed = ops.mac([(ops.rotate(rows[c], -8 * c), self.rowc[c]) for c in range(CTS)])
         z = ops.mac([(packed, self.rs_in)], out_scale=ops.ideal_scale(ops.limbs(packed) - 1))
         z = ops.add_vec(z, self.rs_shift)                # slots outside the packed rows stay at 0
-        z = self._refreshed_series_input(z)
+        z = self._refreshed_series_input(z, "rsqrt")
         lam = ops.poly(z, self.polys.rsqrt)             # rsqrt(R / n) at (h, c, t)
         spread = ops.rotate(ops.copies(lam, CTS), [8 * c for c in range(CTS)])
         lam_c = self._spread_keys(ops.mac([(spread, self.inv_sqrt_count)]))   # 1 / sqrt(R) everywhere
         yl = ops.mul(y, lam_c)
         return ops.mul(yl, yl)
 
-    def _refreshed_series_input(self, x):
+    def _refreshed_series_input(self, x, which: str):
         """With refresh_series_inputs: a two-pass refresh of a series input (|x| <= 1), then one
         scalar product that puts it back on its level's prime (the series' exact-scale chain)."""
 
         if not self.refresh_series_inputs:
             return x
         ops = self.ops
-        x = ops.refresh(x, bound_bits=0)
+        x = ops.refresh(x, bound_bits=0, program=self.series_programs.get(which))
         lim = ops.limbs(x) - 1
         return ops.adjust(x, lim, ops.ideal_scale(lim))
 
@@ -648,7 +670,7 @@ class PrefillLayer:
     it the layer is the model's first, fed by a fresh encryption at the top of the chain."""
 
     def __init__(self, ctx, weights: DecodeWeights, spec: PrefillSpec | None = None, *, program, config=None,
-                 mlp_spec=None, steady: bool = False):
+                 mlp_spec=None, steady: bool = False, programs: dict | None = None):
         from .decode import CipherOps
         from .layouts import FeatureMajorPrefillLayout
         from .linear import LinearOperator, LinearWeight
@@ -663,7 +685,12 @@ class PrefillLayer:
         self.ops = CipherOps(ctx, program)
         self.program = program
         self.steady = bool(steady)
-        self.attn = PrefillAttention(self.ops, self.spec, refresh_series_inputs=self.steady)
+        self.levels: dict = {}   # limbs at the stage boundaries of the last forward
+        # refresh programs per site ("residual", "input", "exp", "rsqrt"); missing ones use ``program``
+        self.programs = dict(programs or {})
+        self.attn = PrefillAttention(self.ops, self.spec, refresh_series_inputs=self.steady,
+                                     series_programs={k: self.programs[k] for k in ("exp", "rsqrt")
+                                                      if k in self.programs})
         self.rms = rmsnorm_coefficients(self.spec.rms_degree, self.spec.rms_interval, self.spec.eps)
         self.op = LinearOperator(crypto_context=ctx, token_lanes=LANES, config=self.config)
         gamma = np.asarray(weights.input_layernorm, dtype=np.float64)
@@ -699,7 +726,7 @@ class PrefillLayer:
 
         x_cts = tuple(x_cts)
         if self.steady:
-            x_cts = tuple(ops.items(ops.refresh(ops.batch(x_cts), bound_bits=5)))
+            x_cts = tuple(ops.items(ops.refresh(ops.batch(x_cts), bound_bits=5, program=self.programs.get("input"))))
             mark("refresh_input")
         xn = rmsnorm_fhe(x_cts, None, coeffs=self.rms, layout=self.layout, crypto_context=ctx).outputs
         mark("rmsnorm1")
@@ -709,7 +736,9 @@ class PrefillLayer:
         del prepared
         mark("qkv_projection")
         A, V = ops.batch(a_out), ops.batch(v_out)
+        self.levels = {"input": ops.limbs(x_cts[0]), "rmsnorm1": ops.limbs(xn[0]), "A": ops.limbs(A)}
         out, _ = self.attn.forward(A, V)
+        self.levels["attention"] = ops.limbs(out)
         mark("attention")
         proj, _ = self.op.apply(ops.items(out), self.w_o)
         delta = ops.batch(proj)
@@ -718,12 +747,14 @@ class PrefillLayer:
         x = ops.adjust(x, ops.limbs(delta), ops.scale(delta))
         h = ops.add(x, delta)
         mark("w_o_residual")
-        h = ops.refresh(h, bound_bits=5)
+        self.levels["residual"] = ops.limbs(h)
+        h = ops.refresh(h, bound_bits=5, program=self.programs.get("residual"))
         mark("refresh")
         m_out, _ = self.mlp.forward(ops.items(h))
         m = ops.batch(m_out)
         h2 = ops.adjust(h, ops.limbs(m), ops.scale(m))
         out = ops.add(h2, m)
+        self.levels["output"] = ops.limbs(out)
         ops.finish()
         mark("mlp_residual")
         return tuple(ops.items(out)), t
@@ -743,4 +774,5 @@ def setup_prefill_layer(client, ctx, weights: DecodeWeights, spec: PrefillSpec |
     rots = prefill_key_rotations(spec, config, prefill_mlp_spec(spec), bspec, int(ctx.logN))
     client.generate_rotation_keys(rots)
     program = generate(ctx, bspec)
-    return PrefillLayer(ctx, weights, spec, program=program, config=config, steady=steady), rots
+    programs = {k: generate(ctx, prefill_bootstrap_spec(r)) for k, r in refresh_raise_limbs(ctx.q_primes).items()}
+    return PrefillLayer(ctx, weights, spec, program=program, config=config, steady=steady, programs=programs), rots

@@ -63,6 +63,7 @@ class SlotOps:
         self.program, self.deep_program = program, deep_program
         self.slots = int(slots)
         self.refreshes = 0
+        self.refresh_levels: list = []
         self.log: list = []
 
     # -- bookkeeping
@@ -207,14 +208,15 @@ class SlotOps:
         vals = np.polynomial.chebyshev.chebval(ct.values.real, coeffs) + 0j
         return SimCt(vals, out, canonical_scales(self.primes, l, s)[out])
 
-    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False):
-        prog = self.deep_program if deep else self.program
+    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False, program=None):
+        prog = program if program is not None else (self.deep_program if deep else self.program)
         if self.limbs(ct) < 2:
             raise ValueError("bootstrap needs at least two limbs")
         peak = float(np.max(np.abs(ct.values)))
         if peak > 2.0**int(bound_bits):
             raise ValueError(f"refresh input {peak} above its bound 2^{bound_bits}")
         self.refreshes += ct.batch_size
+        self.refresh_levels.append((self.limbs(ct), prog.output_limbs - 1))
         # two-pass: the program's output level less the correction's rescale
         return SimCt(ct.values, prog.output_limbs - 1, self.scale(ct))
 

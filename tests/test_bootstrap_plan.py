@@ -268,3 +268,31 @@ def test_numeric_sparse_pipeline_returns_the_input(log_slots, budget):
     except AssertionError:
         return  # the EvalMod input left [-1, 1]: caught
     assert np.max(np.abs(bad - v)) > 2.0**-8
+
+
+def test_raise_target_is_the_fewest_limbs_that_leave_the_output():
+    """raise_for_output: the program raised to the returned limb count leaves the requested limbs
+    (plus one for the two-pass correction), one limb fewer does not, and the lower-raised program
+    still returns its input on the numeric pipeline (its scales come from the shorter chain)."""
+
+    log_n = 10
+    spec = B.BootstrapSpec(log_slots=log_n - 1, level_budget=(3, 3))
+    primes = [2**50 - 2**27 * k + 1 for k in range(1, 31)]
+    top = B.plan_program(spec, primes, 2.0**50, 30, log_n).output_limbs
+    for need in (3, 8, top - 1):
+        r = B.raise_for_output(spec, primes, need, log_n=log_n)
+        assert B.plan_program(spec, primes, 2.0**50, r, log_n).output_limbs >= need + 1
+        assert B.plan_program(spec, primes, 2.0**50, r - 1, log_n).output_limbs < need + 1
+        assert B.raise_for_output(spec, primes, need, two_pass=False, log_n=log_n) == r - 1
+    assert B.raise_for_output(spec, primes, top + 5, log_n=log_n) == 30
+    r = B.raise_for_output(spec, primes, 4, log_n=log_n)
+    prog = B.plan_program(spec, primes, 2.0**50, r, log_n)
+    rng = np.random.default_rng(9)
+    n = 1 << (log_n - 1)
+    v = (rng.uniform(-1, 1, n) + 1j * rng.uniform(-1, 1, n)) / math.sqrt(2)
+    I = rng.integers(-spec.mod_bound + 1, spec.mod_bound, 1 << log_n).astype(np.float64)
+    bits = int(round(math.log2(2.0**50 / primes[0]))) + spec.message_ratio_bits
+    assert np.max(np.abs(_simulate(prog, v, primes[0], I, 2.0**50, log_n, bits) - v)) < 2.0**-20
+    for bad in (-1, 1):
+        with pytest.raises(ValueError, match="raise_limbs"):
+            B.BootstrapSpec(raise_limbs=bad).validate(16)

@@ -55,19 +55,26 @@ def test_prefill_layer_decrypts_to_model(layer_env):
     P, client, ctx, spec, w, layer, layout, x, ref = layer_env
     cts = [client.encrypt(row, cur_limbs=ctx.L) for row in layout.pack(x)]
     out, stages = layer.forward(cts)
-    print(f"prefill layer: stages {stages}, output at {out[0].state.cur_limbs} limbs", flush=True)
+    print(f"prefill layer: stages {stages}, levels {layer.levels}, refreshes {layer.ops.refresh_levels}",
+          flush=True)
+    assert out[0].state.cur_limbs == P.LAYER_OUTPUT_LIMBS
     _check(client, out, layout, ref, "first layer")
 
 
 @pytest.mark.timeout(1100)
 def test_steady_state_layer_decrypts_to_model(layer_env):
-    """The layer as it runs inside the model: its input arrives at 4 limbs (the previous layer's
-    output level) and is refreshed first; the exp and inverse-square-root inputs are refreshed too."""
+    """The layer as it runs inside the model: its input arrives at the previous layer's output level
+    and is refreshed first; the exp and inverse-square-root inputs are refreshed too, each refresh
+    through the program raised only as far as its consumer needs."""
     P, client, ctx, spec, w, layer, layout, x, ref = layer_env
-    steady = P.PrefillLayer(ctx, w, spec, program=layer.program, config=layer.config, steady=True)
-    cts = [client.encrypt(row, cur_limbs=4) for row in layout.pack(x)]
-    out, stages = steady.forward(cts)
+    steady = P.PrefillLayer(ctx, w, spec, program=layer.program, config=layer.config, steady=True,
+                            programs=layer.programs)
+    cts = [client.encrypt(row, cur_limbs=P.LAYER_OUTPUT_LIMBS) for row in layout.pack(x)]
+    try:
+        out, stages = steady.forward(cts)
+    finally:
+        print(f"steady layer levels {steady.levels}, refreshes {steady.ops.refresh_levels}", flush=True)
     print(f"steady layer: stages {stages}, output at {out[0].state.cur_limbs} limbs, "
           f"{steady.ops.refreshes} refreshed items", flush=True)
-    assert out[0].state.cur_limbs >= 3
+    assert out[0].state.cur_limbs == P.LAYER_OUTPUT_LIMBS
     _check(client, out, layout, ref, "steady layer")

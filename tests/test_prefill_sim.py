@@ -136,16 +136,22 @@ def test_attention_dataflow_on_the_slot_simulator(env):
 
 
 def test_steady_state_attention_on_the_slot_simulator(env):
-    """The steady-state layer's attention: A and V at the level a refreshed layer input leaves after
-    RMSNorm1 and the projections (refresh output 21 -> RMSNorm 14 -> projections 13), the exp and
-    inverse-square-root inputs refreshed; the output must still leave levels for W_O and the residual."""
+    """The steady-state layer's attention with the layer's own refresh programs (each raised only as
+    far as its consumer needs): A and V at the level the refreshed layer input leaves after RMSNorm1
+    and the projections, the exp and inverse-square-root inputs refreshed; the output must still
+    leave levels for W_O and the residual."""
     spec, w, x, xn = env
     cs = P.prefill_context_spec()
     q_primes, _ = cs.prime_chain()
     scale = 2.0**50
     ops = SlotOps(q_primes, *make_programs(q_primes, len(q_primes), scale))
-    start = ops.refresh_limbs() - 8
-    attn = P.PrefillAttention(ops, spec, refresh_series_inputs=True)
+    from holmes_amd import bootstrap as B
+
+    raises = P.refresh_raise_limbs(q_primes)
+    progs = {k: B.plan_program(P.prefill_bootstrap_spec(r), q_primes, scale, r) for k, r in raises.items()}
+    assert all(progs[k].output_limbs - 1 >= v for k, v in P.REFRESH_LIMBS.items()), raises
+    start = progs["input"].output_limbs - 1 - 9                # refreshed input -> RMSNorm1 (8) -> projections (1)
+    attn = P.PrefillAttention(ops, spec, refresh_series_inputs=True, series_programs=progs)
     A, V = P.attention_input_numpy(xn, spec, w)
     out, mid = attn.forward(SimCt(A, start, scale), SimCt(V, start, scale))
     model = P.attention_numpy(xn, w, spec)
