@@ -86,6 +86,8 @@ def main() -> int:
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
     ap.add_argument("--ks-slices", type=int, default=0,
                     help="c2 key-switch schedule: 0 sequential kernels, >= 2 pipelined slices of the batch")
+    ap.add_argument("--conv-engine", choices=("mfma", "valu"), default="mfma",
+                    help="c2 ModUp / ModDown conversion sums: int8 matrix cores or FP64 VALU (same results)")
     ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
                     help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
                          "(both are hoist strategies of the reference's LinearOperatorConfig)")
@@ -142,6 +144,7 @@ def main() -> int:
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
     ctx.set_keyswitch_slices(args.ks_slices)
+    ctx.set_conversion_engine(args.conv_engine)
     keys = []
     for r in range(1, CTS + 1):
         g = ctx.galois_element(r)
@@ -231,6 +234,7 @@ def main() -> int:
             "algorithmic_bytes_per_step": step_bytes,
             "cts_per_launch": chunk,
             "ks_slices": args.ks_slices,
+            "conv_engine": args.conv_engine,
         },
         "roofline": {
             "bound": "hbm",

@@ -163,6 +163,15 @@ class CKKSContext:
 
         nat.check(nat.lib().hck_context_set_ks_slices(self._h, int(slices)), "hck_context_set_ks_slices")
 
+    def set_conversion_engine(self, engine: str) -> None:
+        """Engine of the key switch's ModUp / ModDown conversion sums: "mfma" (default, int8 matrix
+        cores on balanced base-256 digits) or "valu" (FP64 multiply-accumulates).  Same results."""
+
+        codes = {"valu": 0, "mfma": 1}
+        if engine not in codes:
+            raise ValueError(f"conversion engine must be one of {sorted(codes)}, got {engine!r}")
+        nat.check(nat.lib().hck_context_set_conv_engine(self._h, codes[engine]), "hck_context_set_conv_engine")
+
     # ------------------------------------------------------------------ parameters
     def scale_at(self, cur_limbs: int) -> float:
         """Default encoding scale at a limb count (fixed scale mode)."""

@@ -100,6 +100,36 @@ void fill_conv(hck::ConvConsts& cc, const std::vector<u64>& P, const std::vector
     }
   }
   for (int t = 0; t < cc.nt; ++t) { cc.dst_prime[t] = dst[t]; cc.dst_slot[t] = dst_slot[t]; }
+  cc.dig_off = -1;
+}
+
+// The matrix-core table of a conversion (layout at ConvConsts::dig_off), appended to `out`.  A
+// source residue y (centered, |y| < 2^49) splits into balanced digits y = sum_a d_a 256^a, a < 7;
+// then y hmod[s][t] = sum_a d_a K_{s,a,t} (mod t) with K_{s,a,t} = hmod[s][t] 256^a mod t, and
+// each centered K splits the same way into digits e_c: the conversion sum becomes
+// sum_c 256^c sum_{s,a} d_{s,a} e_{s,a,t,c}, exact int8 products summed in int32.
+bool append_conv_digits(hck::ConvConsts& cc, const std::vector<u64>& P, std::vector<uint8_t>& out) {
+  constexpr int D = hck::kConvDigits;
+  cc.dig_off = (long long)out.size();
+  const size_t base = out.size();
+  out.resize(base + (size_t)cc.nt * D * 64, 0);
+  for (int t = 0; t < cc.nt; ++t) {
+    const u64 qt = P[cc.dst_prime[t]];
+    for (int s = 0; s < cc.ns; ++s) {
+      u64 k = (u64)cc.hmod[s][t].w;  // exact: a residue below 2^50
+      for (int a = 0; a < D; ++a) {
+        long long v = (long long)k - (k > qt / 2 ? (long long)qt : 0);
+        for (int c = 0; c < D; ++c) {
+          const int d = (int)(int8_t)(uint8_t)(v & 0xFF);  // balanced digit in [-128, 127]
+          out[base + (((size_t)t * D + c) * 8 + s) * 8 + a] = (uint8_t)(int8_t)d;
+          v = (v - d) / 256;
+        }
+        if (v != 0) return false;  // cannot happen for |K| < 2^49 (seven digits reach 2^55)
+        k = mulmod(k, 256 % qt, qt);
+      }
+    }
+  }
+  return true;
 }
 
 }  // namespace
@@ -231,8 +261,17 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     }
   }
 
+  // matrix-core digit tables of every ModUp and ModDown conversion
+  std::vector<uint8_t> digits;
+  bool digits_ok = true;
+  for (hck::ConvConsts& cc : c->h_modup)   // (a wide context converts on wide.hip)
+    if (cc.nt > 0 && !wide) digits_ok = digits_ok && append_conv_digits(cc, P, digits);
+  for (hck::ConvConsts& cc : c->h_moddown)
+    if (cc.nt > 0 && !wide) digits_ok = digits_ok && append_conv_digits(cc, P, digits);
+  if (!digits_ok) { delete c; return HCK_ERR_UNSUPPORTED; }
+
   // one device block: [p | pinv | fwd | inv | ninv | ninv_w1 | zeta4 | pmodq | modup | moddown | level |
-  // rescale | raise | primes | encoder roots]
+  // rescale | raise | primes | encoder roots | conversion digits]
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   size_t off = 0;
   const size_t o_p = off; off = align(off + np * sizeof(double));
@@ -251,6 +290,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   const size_t o_pu = off; off = align(off + np * sizeof(u64));
   const size_t o_etr = off; off = align(off + nslots * sizeof(double));
   const size_t o_eti = off; off = align(off + nslots * sizeof(double));
+  const size_t o_dig = off; off = align(off + digits.size());
   void* blk = nullptr;
   hipError_t e = hipMalloc(&blk, off);
   if (e != hipSuccess) { delete c; return (int)e; }
@@ -272,6 +312,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       {o_pu, P.data(), np * sizeof(u64)},
       {o_etr, etr.data(), nslots * sizeof(double)},
       {o_eti, eti.data(), nslots * sizeof(double)},
+      {o_dig, digits.data(), digits.size()},
   };
   for (const Up& u : ups) {
     e = hipMemcpy(base + u.o, u.src, u.bytes, hipMemcpyHostToDevice);
@@ -287,6 +328,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->dev.ninv_w1 = (const hck::TwPair*)(base + o_nw1);
   c->dev.zeta4 = (const hck::TwPair*)(base + o_z4);
   c->dev.pmodq = (const hck::TwPair*)(base + o_pmq);
+  c->dev.conv_dig = (const uint8_t*)(base + o_dig);
   c->d_modup = (hck::ConvConsts*)(base + o_mu);
   c->d_moddown = (hck::ConvConsts*)(base + o_md);
   c->d_level = (hck::LevelConsts*)(base + o_lv);
@@ -338,6 +380,12 @@ extern "C" int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, 
 extern "C" int hck_context_set_ks_slices(hck_context* ctx, int slices) {
   if (!ctx || slices < 0 || slices > 64) return HCK_ERR_ARG;
   ctx->ks_slices = slices;
+  return HCK_OK;
+}
+
+extern "C" int hck_context_set_conv_engine(hck_context* ctx, int engine) {
+  if (!ctx || engine < 0 || engine > 1) return HCK_ERR_ARG;
+  ctx->conv_engine = engine;
   return HCK_OK;
 }
 

@@ -27,7 +27,12 @@ struct ConvConsts {
   TwPair inv_n0[kMaxAlpha];
   TwPair inv_n1[kMaxAlpha];
   TwPair hmod[kMaxAlpha][kMaxPrimes];
+  // Byte offset of this conversion's matrix-core table in DevTables::conv_dig (-1: none):
+  // [t][c][s][a] = balanced base-256 digit c of (hmod[s][t] * 256^a mod t), centered, for
+  // s < 8, a < 8 (zero for s >= ns and for a = 7), c < kConvDigits.
+  long long dig_off;
 };
+constexpr int kConvDigits = 7;  // balanced base-256 digits of a centered residue (|x| < 2^49)
 
 // Per-level ModDown / rescale constants.
 struct LevelConsts {
@@ -45,6 +50,7 @@ struct DevTables {
   const TwPair* ninv_w1;// [np]: N^-1 * psi_rev_inv[1] (last inverse stage folded with N^-1)
   const TwPair* zeta4;  // [np]: psi^(N/2), a primitive 4th root of unity (multiplication by X^(N/2))
   const TwPair* pmodq;  // [np]: P = prod of the special primes, mod each prime (0 for the special ones)
+  const uint8_t* conv_dig;  // digit tables of the ModUp / ModDown conversions (ConvConsts::dig_off)
 };
 
 }  // namespace hck
@@ -52,6 +58,7 @@ struct DevTables {
 struct hck_context {
   int log_n, L, K, alpha, np;
   int ks_slices = 0;  // key-switch schedule: 0 / 1 sequential kernels, >= 2 pipelined slices (ksfused.hip)
+  int conv_engine = 1;  // ModUp / ModDown conversion sums: 1 int8 matrix cores, 0 FP64 VALU (same results)
   hck::WideState* wide = nullptr;  // set for a context with a prime >= 2^50: every kernel runs on wide.hip
   std::vector<uint64_t> primes;
   hck::DevTables dev;

@@ -488,6 +488,162 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const ConvArgs A, DevTables
   cols_conv_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, H, T);
 }
 
+// ----------------------------------------------------------------- K2 / K4 on the matrix cores
+// The same transform as cols_conv_body, with the conversion sums on the int8 matrix cores.
+// Phase 1 is unchanged except that each centered source residue y (|y| < 2^49) is stored as the
+// 64-bit word of its balanced base-256 digits d_0..d_6 (byte a = d_a as int8, byte 7 zero).  The
+// table ConvConsts::dig_off holds, per target t, the digits e_c of K_{s,a,t} = hmod[s][t] 256^a mod
+// t (centered), so that out_t = sum_c 256^c C_c (mod t) with C_c = sum_{s,a} d_{s,a} e_{s,a,t,c}:
+// for every 16 coefficients one v_mfma_i32_16x16x64_i8 per digit c computes C_c for 16 target rows
+// (K = 8 sources x 8 digit bytes), |C_c| <= 56 * 128^2 < 2^20.
+// Phase 2 mapping: wave w takes column w >> 1 and half w & 1 of its targets; quarter-wave g (the
+// 16 lanes that form a column slot) owns kMItems targets, MFMA rows 4 g + r.  A lane's MFMA
+// operand rows / columns are its lane index mod 16: the constants of row j, the digits of the
+// coefficient 16 k + j of tile k; its output rows 4 g + r at column j, i.e. rows j + 16 k of its
+// quarter's targets over the 16 tiles: the NTT cols pass's layout A, so the sums go straight into
+// the forward transform.  (Operand layout measured: lane l supplies A row l % 16 and B column
+// l % 16 with K bytes 16 (l / 16) .. +15; D row 4 (l / 16) + r, column l % 16 in register r.)
+typedef int v4i __attribute__((ext_vector_type(4)));
+constexpr int kMItems = 3;               // targets per quarter-wave per pass
+constexpr int kMPass = 8 * kMItems;      // targets of one column per pass (two waves x 4 quarters)
+
+// Balanced base-256 digits of an integer-valued y, |y| < 2^49: v = y + M lies in [0, 2^56) for
+// M = 0x0080808080808080, and byte a of v, minus 128, is digit a (byte 7 stays 0); subtracting
+// 128 from each byte is the XOR with M.  y + 1.5 2^52 puts y, offset, in the mantissa.
+__device__ __forceinline__ uint64_t digit_word(double y) {
+  constexpr uint64_t M = 0x0080808080808080ULL;
+  const double t = y + 6755399441055744.0;  // bits(t) = 0x4338000000000000 + y
+  return ((uint64_t)__double_as_longlong(t) + (M - 0x4338000000000000ULL)) ^ M;
+}
+
+// sum_c C_c 256^c mod p into [-p/2 - 1, p/2 + 1] (|C_c| < 2^20): lo = C_0..C_3 part (|lo| < 2^45),
+// hi = C_4..C_6 part (|hi| < 2^37), value lo + 2^32 hi.  hi 2^32 is exact; q = rint(hi 2^32 / p)
+// leaves |hi 2^32 - q p| <= 1.5 p (exact FMA), the sum with lo stays below 2^52, and reduce()
+// centers it.
+// The pairs a = C_0 + 256 C_1, b = C_2 + 256 C_3, d = C_4 + 256 C_5 and C_6 (each |.| < 2^29).
+__device__ __forceinline__ double mconv_fold(int a, int b, int d, int c6, double p, double pinv) {
+  const double lo = __builtin_fma(65536.0, (double)b, (double)a);
+  const double hi = __builtin_fma(65536.0, (double)c6, (double)d);
+  const double q = __builtin_rint(hi * (4294967296.0 * pinv));
+  const double r = __builtin_fma(-q, p, hi * 4294967296.0) + lo;
+  return reduce(r, p, pinv);
+}
+
+template <bool SEPX>
+__device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y, long long z, double* Y, double* X,
+                                                const DevTables& T) {
+  const double* __restrict__ src = A.src;
+  double* __restrict__ dst = A.dst;
+  const ConvConsts& C = A.cc_base[y * A.cc_y];
+  const int ns = C.ns, nt = C.nt;
+  const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
+  const int c0 = bx * 2;
+  uint64_t* D = reinterpret_cast<uint64_t*>(Y);
+  // phase 1: slot sigma = (source sigma >> 1, column sigma & 1), as in cols_conv_body
+  {
+    const int s = sigma >> 1, cl = sigma & 1;
+    const bool act = s < ns;
+    const int sp = C.src_prime[act ? s : 0];
+    const double p = T.p[sp], pinv = T.pinv[sp];
+    const double* __restrict__ tw = T.tw_inv + (size_t)sp * kN;
+    double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = 0.0;
+    if (act) {
+      const double* col = src + z * A.src_zs + y * A.src_ys + (long long)(y * A.src_off_y + s) * kN +
+                          (long long)(c0 + cl) * 16;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = col[4096 * k + j];
+      col_inv_hi(x, j, tw, p, pinv);
+    }
+    double* R = Y + sigma * kYStride;
+    col_b_to_a(x, R, j);
+    if (act) col_inv_lo(x, tw, C.inv_n0[s], C.inv_n1[s], p, pinv);
+    // centered lift as in cols_conv_body, then the digit word (an idle source stores zero digits)
+#pragma unroll
+    for (int k = 0; k < 16; ++k) D[sigma * kYStride + j + 16 * k] = act ? digit_word(reduce(x[k], p, pinv)) : 0ULL;
+  }
+  __syncthreads();
+  // phase 2
+  const int w = t >> 6, g = (t >> 4) & 3;
+  const int cl = w >> 1, h = w & 1;
+  const uint8_t* __restrict__ dig = T.conv_dig + C.dig_off;
+  const uint64_t* B0 = D + (4 * g + cl) * kYStride + j;      // source 2 g, column cl
+  const uint64_t* B1 = D + (4 * g + 2 + cl) * kYStride + j;  // source 2 g + 1
+  double* RX = (SEPX ? X : Y) + sigma * kYStride;
+  double* dbase = dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
+  for (int base = 0; base < nt; base += kMPass) {
+    // constants of MFMA row j: target of quarter j >> 2, item j & 3
+    const int ta = base + (4 * h + (j >> 2)) * kMItems + (j & 3);
+    const bool arow = (j & 3) < kMItems && ta < nt;
+    v4i av[kConvDigits];
+#pragma unroll
+    for (int c = 0; c < kConvDigits; ++c)
+      av[c] = arow ? *reinterpret_cast<const v4i*>(dig + ((size_t)ta * kConvDigits + c) * 64 + 16 * g) : v4i{0, 0, 0, 0};
+    int to[kMItems];
+    double p[kMItems], pinv[kMItems];
+#pragma unroll
+    for (int r = 0; r < kMItems; ++r) {
+      to[r] = base + (4 * h + g) * kMItems + r;
+      const int tp = C.dst_prime[to[r] < nt ? to[r] : 0];
+      p[r] = T.p[tp];
+      pinv[r] = T.pinv[tp];
+    }
+    double x[kMItems][16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint64_t w0 = B0[16 * k], w1 = B1[16 * k];
+      const v4i bv = {(int)(uint32_t)w0, (int)(uint32_t)(w0 >> 32), (int)(uint32_t)w1, (int)(uint32_t)(w1 >> 32)};
+      v4i acc[kConvDigits];
+#pragma unroll
+      for (int c = 0; c < kConvDigits; ++c)
+        acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[c], bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < kMItems; ++r) {
+        x[r][k] = mconv_fold(acc[0][r] + (int)((uint32_t)acc[1][r] << 8), acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
+                             acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], p[r], pinv[r]);
+        // the fold happens here, in its tile: sunk to its use in the transform, every tile's
+        // accumulators would stay live at once
+        asm volatile("" : "+v"(x[r][k]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!SEPX) __syncthreads();  // every wave is done reading D before its runs become exchange buffers
+#pragma unroll
+    for (int r = 0; r < kMItems; ++r) {
+      const bool act = to[r] < nt;
+      const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? to[r] : 0] * kN;
+      if (act) col_fwd_lo<true>(x[r], tw, p[r], pinv[r]);
+      col_a_to_b(x[r], RX, j);
+      if (act) {
+        col_fwd_hi(x[r], j, tw, p[r], pinv[r]);
+        double* col = dbase + (long long)C.dst_slot[to[r]] * kN;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) col[4096 * k + j] = x[r][k];
+      }
+    }
+  }
+}
+
+template <bool SEPX>
+__global__ __launch_bounds__(kT, 2) void k_ks_cols_mconv(const ConvArgs A, DevTables T) {
+  __shared__ double Y[16 * kYStride];
+  __shared__ double X[SEPX ? 16 * kYStride : 1];
+  cols_mconv_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, T);
+}
+
+// Launches a ModUp / ModDown conversion (grid (128, groups, items)) on the engine the context
+// selects; nt_max is the largest target count over the groups.
+void launch_conv(const hck_context* c, const ConvArgs& A, dim3 grid, int nt_max, hipStream_t s) {
+  if (c->conv_engine == 1) {
+    auto k = nt_max <= kMPass ? k_ks_cols_mconv<false> : k_ks_cols_mconv<true>;
+    k<<<grid, kT, 0, s>>>(A, c->dev);
+  } else {
+    auto k = nt_max <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+    k<<<grid, kT, 0, s>>>(A, c->dev);
+  }
+}
+
 // ----------------------------------------------------------------- forward row twiddles in LDS
 // The tile kernels keep the forward twiddles of their 16 rows in LDS, so that no global load sits
 // between a tile's data loads and its transform (loads retire in order: a twiddle load issued
@@ -1103,11 +1259,10 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
                                                                                     r1, ell, batch, c->dev);
   HCK_CHECK_LAUNCH();
   // K2: ModUp, one block per (column pair, digit, ciphertext)
-  auto cols_conv = ext_l - last_digit <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(
-      ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
-               modup_consts(c, ell, 0), 1},
-      c->dev);
+  launch_conv(c,
+              ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                       modup_consts(c, ell, 0), 1},
+              dim3(128, beta, batch), ext_l - last_digit, s);
   HCK_CHECK_LAUNCH();
   if (ext_b) {
     // K3 over every extended limb, ending in the extended basis
@@ -1128,10 +1283,10 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   }
   // K4: ModDown conversion, one block per (column pair, component, ciphertext); T4 reuses R1
   double* t4 = r1;
-  auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  md_conv<<<dim3(128, 2, batch), kT, 0, s>>>(
-      ConvArgs{accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n, (long long)ell * n, c->d_moddown + ell, 0},
-      c->dev);
+  launch_conv(c,
+              ConvArgs{accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n, (long long)ell * n,
+                       c->d_moddown + ell, 0},
+              dim3(128, 2, batch), ell, s);
   HCK_CHECK_LAUNCH();
   // K5: Q limbs
   {
@@ -1186,11 +1341,10 @@ int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const ui
   k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0,
                                                                                     r1, ell, batch, c->dev);
   HCK_CHECK_LAUNCH();
-  auto cols_conv = ext_l - last_digit <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  cols_conv<<<dim3(128, beta, batch), kT, 0, s>>>(
-      ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
-               modup_consts(c, ell, 0), 1},
-      c->dev);
+  launch_conv(c,
+              ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                       modup_consts(c, ell, 0), 1},
+              dim3(128, beta, batch), ext_l - last_digit, s);
   HCK_CHECK_LAUNCH();
   const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
   k_ks_rows_ip_sum<<<dim3(groups * kXcds * outputs), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, outputs, group,
@@ -1218,9 +1372,8 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
   k_ks_intt_rows<<<dim3(((16 * K + kXcds - 1) / kXcds) * kXcds * polys), kT, 0, s>>>(in, in_stride, gal_uniform(1u), ell, c->L,
                                                                                    tp, K, polys, c->dev);
   HCK_CHECK_LAUNCH();
-  auto md_conv = ell <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
-  md_conv<<<dim3(128, 1, polys), kT, 0, s>>>(
-      ConvArgs{tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0, c->d_moddown + ell, 0}, c->dev);
+  launch_conv(c, ConvArgs{tp, (long long)K * n, 0, 0, t4, (long long)ell * n, 0, c->d_moddown + ell, 0},
+              dim3(128, 1, polys), ell, s);
   HCK_CHECK_LAUNCH();
   k_ks_rows_finish<<<dim3(polys, 16, ell), kT, 0, s>>>(t4, in, in_stride, out, out_stride, ell,
                                                        (c->d_level + ell)->p_inv, c->dev);

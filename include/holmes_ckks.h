@@ -71,6 +71,12 @@ const char* hck_error_string(int code);
  * identical; only the timing differs.  No counterpart in the reference (a scheduling knob). */
 int hck_context_set_ks_slices(hck_context* ctx, int slices);
 
+/* Engine of the ModUp / ModDown base-conversion sums inside every key switch: 1 (default) the int8
+ * matrix cores (each residue split into balanced base-256 digits, exact int32 sums), 0 FP64 VALU
+ * multiply-accumulates.  Results are identical; only the timing differs.  No counterpart in the
+ * reference (a scheduling knob). */
+int hck_context_set_conv_engine(hck_context* ctx, int engine);
+
 /* In-place (src == dst allowed) negacyclic NTT of `polys` x `limbs` limbs: limb l of poly b is at
  * base + b * stride + l * N and uses prime prime_idx[l] (host array).  Forward: natural-order
  * coefficients in, bit-reversed evaluation order out (out[k] = a(psi^(2 brv(k) + 1))). */

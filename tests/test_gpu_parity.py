@@ -198,6 +198,37 @@ def test_keyswitch(env, ell):
         assert np.array_equal(ga[b], wa), f"a component, item {b}"
 
 
+@pytest.mark.parametrize("ell", [24, 9, 1])
+def test_conversion_engines_agree(env, ell):
+    """The ModUp / ModDown conversion sums on the int8 matrix cores (the default) and on FP64 VALU
+    give bit-identical key switches and extended-basis ModDowns, equal to the oracle's."""
+    _, client, ctx, orc = env
+    g = ctx.galois_element(5)
+    gk, ok = _key_pair(client, ctx, orc, g)
+    rng = np.random.default_rng(900 + ell)
+    d = _rand(ctx, rng, 3, ell)
+    d[0, 0, :4] = [0, 1, ctx.primes[0] - 1, (ctx.primes[0] - 1) // 2]
+    idx = ctx.ext_prime_idx(ell)
+    x = _rand(ctx, rng, 2, len(idx), idx)
+    got = {}
+    try:
+        for engine in ("valu", "mfma"):
+            ctx.set_conversion_engine(engine)
+            ob, oa = ctx.keyswitch(_dev(d), ell, gk)
+            got[engine] = (_host(ob), _host(oa), _host(ctx.moddown(_dev(x), ell)))
+    finally:
+        ctx.set_conversion_engine("mfma")
+    for a, b in zip(got["valu"], got["mfma"]):
+        assert np.array_equal(a, b)
+    for b in range(3):
+        wb, wa = orc.keyswitch(ell, d[b], ok)
+        assert np.array_equal(got["mfma"][0][b], wb) and np.array_equal(got["mfma"][1][b], wa), b
+    for b in range(2):
+        assert np.array_equal(got["mfma"][2][b], orc.moddown(ell, x[b])), b
+    with pytest.raises(ValueError):
+        ctx.set_conversion_engine("fp32")
+
+
 def test_rotate_matches_oracle(env):
     _, client, ctx, orc = env
     ell = 24
