@@ -57,10 +57,11 @@ import time
 import numpy as np
 
 BYTES_PER_CT = (12 + 96 + 24) * 2**20  # 138,412,032
-# HBM bytes one C2 step actually moves (all five kernels), from two rocprofv3 --pmc runs of this
-# workload: FETCH_SIZE (x 2.0, the factor the stream workload's known 192 MiB read calibrates) +
-# WRITE_SIZE (x 1.0): 2 x 1,662,281 KiB + 1,703,936 KiB (= 3246.6 MiB read + 1664.0 MiB written).
-C2_TRAFFIC_BYTES = 5_149_181_760
+# HBM bytes one C2 step actually moves (all five kernels) come from two rocprofv3 --pmc runs of
+# this workload (FETCH_SIZE x 2.0, the factor the stream workload's known read calibrates, plus
+# WRITE_SIZE x 1.0), recorded with the SHA-256 of the kernel sources they were measured on; the
+# line reports them only while the sources still match.
+C2_TRAFFIC_RECORD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "keyswitch_c2_traffic.json")
 CTS = 16
 LIMBS = 24
 HBM_PEAK_GBS = 8000.0
@@ -186,6 +187,10 @@ def main() -> int:
     value = step_bytes / (ms_wall * 1e-3) / 1e9
     achieved = step_bytes / (ms_events * 1e-3) / 1e9
     _log(f"{args.steps} steps: {ms_wall:.3f} ms/step wall, {ms_events:.3f} ms/step events")
+    traffic, traffic_rec = c2_traffic()
+    if traffic is None:
+        _log("roofline.traffic: no PMC record for these kernel sources (null)" if traffic_rec is None else
+             "roofline.traffic: the PMC record was measured on other kernel sources (null)")
 
     cpu = None
     if not args.no_cpu:
@@ -235,6 +240,8 @@ def main() -> int:
             "cts_per_launch": chunk,
             "ks_slices": args.ks_slices,
             "conv_engine": args.conv_engine,
+            "traffic_record": None if traffic is None else {k: traffic_rec[k] for k in ("fetch_kib", "write_kib",
+                                                                                       "fetch_scale", "measured")},
         },
         "roofline": {
             "bound": "hbm",
@@ -242,7 +249,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": C2_TRAFFIC_BYTES,
+            "traffic": traffic,
             "kernel": "hck_keyswitch (whole ModUp -> inner product -> ModDown launch sequence per step)",
             "ms_per_launch": round(ms_events, 4),
         },
@@ -1043,6 +1050,34 @@ def run_c5(args) -> int:
                      "ms_per_launch": round(s_wall * 1e3, 2)},
         "cpu_baseline": cpu}), flush=True)
     return 0
+
+
+def kernel_sources_sha256() -> str:
+    """SHA-256 over the library's kernel sources (name and bytes of every csrc file, sorted)."""
+
+    import hashlib
+
+    root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "holmes_amd", "csrc")
+    h = hashlib.sha256()
+    for name in sorted(os.listdir(root)):
+        if name.endswith((".hip", ".hpp", ".h")):
+            h.update(name.encode())
+            with open(os.path.join(root, name), "rb") as f:
+                h.update(f.read())
+    return h.hexdigest()
+
+
+def c2_traffic():
+    """(bytes per step, record) from the traffic record if it was measured on these sources."""
+
+    try:
+        with open(C2_TRAFFIC_RECORD) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None, None
+    if rec.get("sources_sha256") != kernel_sources_sha256():
+        return None, rec
+    return int(rec["traffic_bytes"]), rec
 
 
 def run_layer(args) -> int:
