@@ -253,7 +253,7 @@ def main() -> int:
             "kernel": "hck_keyswitch (whole ModUp -> inner product -> ModDown launch sequence per step)",
             "ms_per_launch": round(ms_events, 4),
         },
-        "cpu_baseline": cpu,
+        "cpu_baseline": _cpu_annotated(cpu),
     }
     print(json.dumps(line), flush=True)
     return 0
@@ -332,7 +332,7 @@ def run_c2wide(args) -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "hck_keyswitch on the wide path (whole launch sequence per step)",
                      "ms_per_launch": round(ms_events, 4)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -400,7 +400,7 @@ def run_c1(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "rotation (5 fused key-switch kernels) + rescale", "ms_per_launch": round(ms, 4)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -474,7 +474,7 @@ def run_mul(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "tensor + 5 key-switch kernels + rescale per step", "ms_per_launch": round(ms, 4)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -658,7 +658,7 @@ def run_bootstrap(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole bootstrap (key switches, MACs, rescales, elementwise)", "ms_per_launch": round(ms, 3)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -765,7 +765,7 @@ def run_kv(args) -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_lincomb (8 groups x 2 terms per append)", "ms_per_launch": round(k_ms, 5)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -940,7 +940,7 @@ def run_c4(args) -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole block (call-log algorithmic bytes: keys, diagonals, inputs/outputs of each call)",
                      "ms_per_launch": round(s_wall * 1e3, 2)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -1048,8 +1048,29 @@ def run_c5(args) -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole step (call-log algorithmic bytes: keys, diagonals, inputs/outputs of each call)",
                      "ms_per_launch": round(s_wall * 1e3, 2)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
+
+
+def _cpu_model() -> str:
+    """The host CPU's model name (/proc/cpuinfo) and its logical CPU count."""
+
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return f"{name} ({os.cpu_count()} logical CPUs visible)"
+
+
+def _cpu_annotated(cpu):
+    """A cpu_baseline dict with the host CPU model added (None stays None)."""
+
+    return None if cpu is None else {**cpu, "cpu_model": _cpu_model()}
 
 
 def kernel_sources_sha256() -> str:
@@ -1187,7 +1208,7 @@ def run_layer(args) -> int:
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole layer (call-log algorithmic bytes: keys, diagonals, inputs/outputs of each call)",
                      "ms_per_launch": round(s_wall * 1e3, 2)},
-        "cpu_baseline": cpu}), flush=True)
+        "cpu_baseline": _cpu_annotated(cpu)}), flush=True)
     return 0
 
 
@@ -1317,7 +1338,7 @@ def run_c3(args) -> int:
             "kernel": "whole projection (babies, pack + encode, MAC, Horner giant key switches, rescale)",
             "ms_per_launch": round(s_events * 1e3, 3),
         },
-        "cpu_baseline": cpu,
+        "cpu_baseline": _cpu_annotated(cpu),
     }
     print(json.dumps(line), flush=True)
     return 0

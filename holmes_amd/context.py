@@ -578,6 +578,22 @@ class CKKSContext:
                                             nat.ptr_array(optr[g0:g1]), _stream_ptr(self.device)), "hck_lincomb")
         return outs
 
+    def lincomb_ptrs(self, in_ptrs, limbs: int, out_ptrs, terms: int) -> None:
+        """``lincomb`` with unit weights on raw device addresses: ``in_ptrs`` holds ``terms``
+        addresses per group (group-major), ``out_ptrs`` one per group, each a [>= limbs][N] uint64
+        polynomial with contiguous limbs on this context's device.  The caller has checked the
+        tensors behind the addresses (the KV page pool does, once per component)."""
+
+        G = len(out_ptrs)
+        if G < 1 or len(in_ptrs) != G * terms or terms < 1 or terms > 256:
+            raise ValueError("lincomb_ptrs: one output per group and `terms` inputs per output (<= 256)")
+        per = max(1, min(64, 256 // terms))
+        lib, stream = nat.lib(), _stream_ptr(self.device)
+        for g0 in range(0, G, per):
+            g1 = min(G, g0 + per)
+            nat.check(lib.hck_lincomb(self._h, int(limbs), g1 - g0, terms, nat.ptr_array(in_ptrs[g0 * terms:g1 * terms]),
+                                      None, nat.ptr_array(out_ptrs[g0:g1]), stream), "hck_lincomb")
+
     def moddown(self, x: torch.Tensor, limbs: int, out: torch.Tensor | None = None) -> torch.Tensor:
         """Extended-basis polys [polys][limbs + K][N] -> [polys][limbs][N] (divide by P, round)."""
 

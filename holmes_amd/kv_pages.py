@@ -157,6 +157,14 @@ class KVPagePool:
                                device=ctx.device)
         self._free = list(range(self.capacity - 1, -1, -1))
         self._refs = [0] * self.capacity
+        # per slot: the component views and the device address of every (handle, component, item)
+        # polynomial, computed once so that an append does no tensor indexing
+        poly = self.limbs * ctx.N * 8
+        base = self.buf.data_ptr()
+        self._views = [[(self.buf[s, h, 0], self.buf[s, h, 1]) for h in range(_HANDLES)] for s in range(self.capacity)]
+        self._addr = [[base + (((s * _HANDLES + h) * 2 + c) * self.batch + b) * poly
+                       for h in range(_HANDLES) for c in range(2) for b in range(self.batch)]
+                      for s in range(self.capacity)]
 
     @property
     def nbytes(self) -> int:
@@ -183,9 +191,26 @@ class KVPagePool:
             self._free.append(s)
 
     def _ciphers(self, s: int, template: Cipher) -> tuple:
-        return tuple(PooledCipher([self.buf[s, h, 0], self.buf[s, h, 1]], template.state.replace(cur_limbs=self.limbs),
-                                  slots=template.slots, batch_size=self.batch, pool=self, slot=s)
-                     for h in range(_HANDLES))
+        state = template.state.replace(cur_limbs=self.limbs)
+        return tuple(PooledCipher(list(self._views[s][h]), state, slots=template.slots, batch_size=self.batch, pool=self,
+                                  slot=s) for h in range(_HANDLES))
+
+    def _item_addresses(self, handles) -> list:
+        """Device address of every (handle, component, item) polynomial of ``handles``, in the pool's
+        slot order, after one check per component tensor: uint64 on the pool's device, [batch][>=
+        limbs][N] with contiguous limbs."""
+
+        N, dev = self.ctx.N, self.buf.device
+        out = []
+        for h in handles:
+            for t in h.cv:
+                if (t.dtype != torch.uint64 or t.device != dev or t.dim() != 3 or t.shape[0] != self.batch
+                        or t.shape[1] < self.limbs or t.shape[2] != N or t.stride(2) != 1 or t.stride(1) != N):
+                    raise ValueError("page ciphertext components must be [batch][>= limbs][N] uint64 tensors with "
+                                     "contiguous limbs on the pool's device")
+                p0, sb = t.data_ptr(), t.stride(0) * 8
+                out.extend(p0 + b * sb for b in range(self.batch))
+        return out
 
     def fits(self, handles) -> bool:
         """True when every handle is a two-component ciphertext of this backend at the pool's level
@@ -208,15 +233,11 @@ class KVPagePool:
             if int(a.state.scale_degree) != int(b.state.scale_degree) or not fhe._same_scale(
                     float(a.state.scaling_factor), float(b.state.scaling_factor)):
                 raise ValueError("page and token differ in scale")
+        lp, rp = self._item_addresses(left), self._item_addresses(right)
         s = self._alloc()
         try:
-            xs, outs = [], []
-            for h in range(_HANDLES):
-                for c in range(2):
-                    for b in range(self.batch):
-                        xs.append([left[h].cv[c][b], right[h].cv[c][b]])
-                        outs.append(self.buf[s, h, c, b])
-            self.ctx.lincomb(xs, self.limbs, outs)
+            ins = [a for pair in zip(lp, rp) for a in pair]
+            self.ctx.lincomb_ptrs(ins, self.limbs, self._addr[s], 2)
         except BaseException:
             self._refs[s] = 0
             self._free.append(s)
