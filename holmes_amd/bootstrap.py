@@ -483,6 +483,31 @@ def _rotate_many(c0: torch.Tensor, c1: torch.Tensor, offsets, limbs: int, ctx: C
     return o0, o1
 
 
+# Batches of at least this many items rotate a stage's giant partials in the extended basis (one
+# ModDown per item for all giants); smaller ones close every giant rotation with its own ModDown.
+# Every batch size takes one path, so that a batch refreshes bit-identically to its items alone.
+EXT_GIANTS_MIN_BATCH = 1
+
+
+def _ext_giant_sum(res: torch.Tensor, first: int, g_offs, B: int, limbs: int, ctx: CKKSContext) -> list:
+    """sum_k rot(res[:, first + k], g_offs[k]) (+ res[:, 0] when ``first``) for every item: the
+    partials rotated in the extended basis, summed there a group of giants per launch (the running
+    sum stays on chip), then one ModDown per component (fhe.hoisted_mac_sum's double hoisting)."""
+
+    if first:
+        ext0, ext1 = fhe._lift_ext(res[0, 0], limbs, ctx), fhe._lift_ext(res[1, 0], limbs, ctx)
+    else:
+        ext0, ext1 = ctx.zeros(B, limbs + ctx.K, ctx.N), ctx.zeros(B, limbs + ctx.K, ctx.N)
+    step = max(1, min(fhe.GIANT_GROUP, 64 // B))
+    for i0 in range(0, len(g_offs), step):
+        i1 = min(len(g_offs), i0 + step)
+        gals = [ctx.galois_element(o) for o in g_offs[i0:i1]]
+        keys = [ctx.key_for_galois(g) for g in gals]
+        lo, hi = first + i0, first + i1
+        ctx.rotate_ext_sum(res[0, lo:hi], res[1, lo:hi], limbs, gals, keys, ext0, ext1, acc=(ext0, ext1))
+    return [ctx.moddown(ext0, limbs), ctx.moddown(ext1, limbs)]
+
+
 def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: bool = True) -> Cipher:
     """One stage on every item of ``x``, without a rescale: the baby rotations of all items as
     one batched key switch (a Galois element per item), the baby-step MAC of every giant row with
@@ -512,6 +537,13 @@ def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: b
     del b0, b1  # res: [2][G][B][limbs][N]
     first = 1 if st.giants[0] == 0 else 0
     rot = st.giants[first:]
+    g_offs = [(k2 * st.n1 * st.h_min) % n for k2 in rot]
+    if rot and B >= EXT_GIANTS_MIN_BATCH and all(g_offs):
+        acc = _ext_giant_sum(res, first, g_offs, B, limbs, ctx)
+        s = x.state
+        return x.cipher_like(acc, batch_size=B,
+                             state=s.replace(scale_degree=int(s.scale_degree) + 1,
+                                             scaling_factor=float(s.scaling_factor) * float(pt_scale)))
     acc = fhe._alloc(ctx, 2, B, limbs)
     xs = [[res[c, 0, b]] if first else [] for c in range(2) for b in range(B)]
     if rot:
