@@ -69,6 +69,11 @@ SIGNATURES = {
                                  _i64, _vp, _sz, _vp]),
     "hck_rotate_ext_sum": (_i, [_vp, _i, _i, _i, _u32p, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp,
                                 _vp, _i64, _vp, _sz, _vp]),
+    "hck_rotate_hoist_digits_bytes": (_sz, [_vp, _i, _i]),
+    "hck_rotate_hoist_workspace_bytes": (_sz, [_vp, _i, _i, _i]),
+    "hck_rotate_hoist_prepare": (_i, [_vp, _i, _i, _vp, _i64, _vp, _vp, _sz, _vp]),
+    "hck_rotate_hoisted": (_i, [_vp, _i, _i, _i, _u32p, _vp, _vp, _i64, _vp, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp,
+                                _sz, _vp]),
     "hck_moddown_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_moddown": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_pack_diagonals": (_i, [_vp, _vp, _i, _i, _i, _i, _i, _i, _vp, _vp]),

@@ -523,14 +523,20 @@ def apply_stage(x: Cipher, st: Stage, ctx: CKKSContext, pt_scale: float, keep: b
     c0, c1 = x.cv[0][:, :limbs].contiguous(), x.cv[1][:, :limbs].contiguous()
     nb = st.n1 - 1
     offs = [(k1 * st.h_min) % n for k1 in range(1, st.n1) for _ in range(B)]  # offset-major, then item
-    if B == 1:
-        r0, r1 = c0.expand(nb, -1, -1), c1.expand(nb, -1, -1)  # batch stride 0: one input, every offset
+    if ctx.supports_hoisting and all(offs):
+        # one ModUp per item, every baby rotation read from its hoisted digits (item i: input i % B)
+        digits = ctx.hoist_digits(c1, limbs)
+        gals = [ctx.galois_element(o) for o in offs]
+        b0, b1 = ctx.rotate_hoisted(c0, c1, limbs, digits, gals, [ctx.key_for_galois(g) for g in gals])
+        del digits
     else:
-        r0, r1 = (u64_clone(c.view(torch.int64).unsqueeze(0).expand(nb, B, limbs, ctx.N).reshape(nb * B, limbs,
-                                                                                            ctx.N).view(torch.uint64))
-                  for c in (c0, c1))
-    b0, b1 = _rotate_many(r0, r1, offs, limbs, ctx, n)
-    del r0, r1
+        if B == 1:
+            r0, r1 = c0.expand(nb, -1, -1), c1.expand(nb, -1, -1)  # batch stride 0: one input, every offset
+        else:
+            r0, r1 = (u64_clone(c.view(torch.int64).unsqueeze(0).expand(nb, B, limbs, ctx.N).reshape(
+                nb * B, limbs, ctx.N).view(torch.uint64)) for c in (c0, c1))
+        b0, b1 = _rotate_many(r0, r1, offs, limbs, ctx, n)
+        del r0, r1
     pts = _stage_plaintexts(st, limbs, pt_scale, ctx, keep)
     res = ctx.bsgs_mac([c0] + [b0[i * B:(i + 1) * B] for i in range(nb)],
                        [c1] + [b1[i * B:(i + 1) * B] for i in range(nb)], pts, limbs, len(st.giants))

@@ -137,6 +137,8 @@ class CKKSContext:
                 "hck_context_create",
             )
         self._h = h
+        # hoisted rotations (hck_rotate_hoisted) run on the FP64 path: every prime below 2^50
+        self.supports_hoisting = max(self.primes) < (1 << 50)
         self._ws: torch.Tensor | None = None
         self.rotation_keys: dict[int, torch.Tensor] = {}
         self.relin_key: torch.Tensor | None = None
@@ -342,6 +344,60 @@ class CKKSContext:
                      a1.data_ptr() if a1 is not None else None, a_stride,
                      out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
                      _stream_ptr(self.device)), name)
+        return out0, out1
+
+    def hoist_digits(self, c1: torch.Tensor, limbs: int) -> torch.Tensor:
+        """The extended ModUp digits of every c1 ([inputs][limbs][N]) in the full NTT domain, as
+        [inputs][beta][limbs + K][N] uint64 (hck_rotate_hoist_prepare): computed once, they serve
+        any number of ``rotate_hoisted`` calls on these inputs."""
+
+        self._check_poly(c1, limbs, self.N)
+        B = int(c1.shape[0])
+        L = nat.lib()
+        beta = -(-int(limbs) // self.alpha)
+        digits = torch.empty((B, beta, int(limbs) + self.K, self.N), dtype=torch.uint64, device=self.device)
+        if digits.numel() * 8 != L.hck_rotate_hoist_digits_bytes(self._h, limbs, B):
+            raise RuntimeError("hoisted digit layout disagrees with the library")
+        ws = self.workspace(L.hck_rotate_hoist_workspace_bytes(self._h, limbs, B, 0))
+        nat.check(L.hck_rotate_hoist_prepare(self._h, limbs, B, c1.data_ptr(), _bstride(c1), digits.data_ptr(),
+                                             ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                  "hck_rotate_hoist_prepare")
+        return digits
+
+    def rotate_hoisted(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, digits: torch.Tensor, galois, keys,
+                       out0: torch.Tensor | None = None, out1: torch.Tensor | None = None):
+        """Item i < len(galois): input i % inputs of (c0, c1) rotated by galois[i] with keys[i], from
+        the digits ``hoist_digits(c1, limbs)`` (hck_rotate_hoisted); bit-identical to ``rotate_raw``
+        with a Galois element per item on the repeated inputs."""
+
+        self._check_poly(c0, limbs, self.N)
+        self._check_poly(c1, limbs, self.N)
+        if _bstride(c0) != _bstride(c1) or c0.shape[0] != c1.shape[0]:
+            raise ValueError("c0 and c1 need the same inputs and batch stride")
+        B = int(c0.shape[0])
+        beta = -(-int(limbs) // self.alpha)
+        if (digits.dtype != torch.uint64 or tuple(digits.shape) != (B, beta, int(limbs) + self.K, self.N)
+                or not digits.is_contiguous()):
+            raise ValueError("digits must come from hoist_digits of these inputs at this level")
+        items = len(galois)
+        if len(keys) != items:
+            raise ValueError("one key per rotated item")
+        for k in keys:
+            self._check_key(k)
+        out0 = self.empty(items, limbs, self.N) if out0 is None else out0
+        out1 = self.empty(items, limbs, self.N) if out1 is None else out1
+        for o in (out0, out1):
+            self._check_poly(o, limbs, self.N)
+            if o.shape[0] != items:
+                raise ValueError("outputs need one row per rotated item")
+        if _bstride(out0) != _bstride(out1):
+            raise ValueError("out0 and out1 need the same batch stride")
+        L = nat.lib()
+        ws = self.workspace(L.hck_rotate_hoist_workspace_bytes(self._h, limbs, B, items))
+        nat.check(L.hck_rotate_hoisted(self._h, limbs, B, items, nat.u32_array(galois), c0.data_ptr(), c1.data_ptr(),
+                                       _bstride(c0), digits.data_ptr(), nat.ptr_array([k.data_ptr() for k in keys]),
+                                       out0.data_ptr(), out1.data_ptr(), _bstride(out0), ws.data_ptr(), ws.numel(),
+                                       _stream_ptr(self.device)), "hck_rotate_hoisted")
         return out0, out1
 
     @staticmethod

@@ -119,6 +119,18 @@ int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const ui
                  const uint32_t* galois_items, const uint64_t* const* ksk, const uint64_t* add, long long add_stride,
                  const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride, uint64_t* ext_b,
                  uint64_t* ext_a, long long ext_stride, char* ws, hipStream_t s);
+// Hoisted rotations: ks_hoist materialises the extended digits of `inputs` polys d in the full NTT
+// domain ([inputs][beta][ell + K] canonical limbs, workspace ks_hoist_bytes); ks_hoisted rotates
+// input i % inputs by galois[i] with ksk[i] for every item i < items from them (workspace
+// ks_hoisted_bytes), bit-identical to ks_fused.  FP64 contexts only (HCK_ERR_UNSUPPORTED on a wide one).
+size_t ks_hoist_bytes(const hck_context* c, int ell, int inputs);
+int ks_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
+             char* ws, hipStream_t s);
+size_t ks_hoisted_bytes(const hck_context* c, int ell, int items);
+int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint32_t* galois,
+               const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
+               const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
+               hipStream_t s);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

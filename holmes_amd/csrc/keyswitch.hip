@@ -166,6 +166,48 @@ extern "C" int hck_rotate_ext_sum(const hck_context* ctx, int level_limbs, int o
                            acc_stride, out0, out1, out_stride, (char*)workspace, (hipStream_t)stream);
 }
 
+extern "C" size_t hck_rotate_hoist_digits_bytes(const hck_context* ctx, int level_limbs, int inputs) {
+  if (!ctx || level_limbs < 1 || level_limbs > ctx->L || inputs < 0) return 0;
+  const size_t beta = (size_t)(level_limbs + ctx->alpha - 1) / ctx->alpha;
+  return (size_t)inputs * beta * (size_t)(level_limbs + ctx->K) * hck::kN * 8;
+}
+
+extern "C" size_t hck_rotate_hoist_workspace_bytes(const hck_context* ctx, int level_limbs, int inputs, int items) {
+  if (!ctx || level_limbs < 1 || level_limbs > ctx->L || inputs < 0 || items < 0) return 0;
+  const size_t a = hck::ks_hoist_bytes(ctx, level_limbs, inputs), b = hck::ks_hoisted_bytes(ctx, level_limbs, items);
+  return a > b ? a : b;
+}
+
+extern "C" int hck_rotate_hoist_prepare(const hck_context* ctx, int level_limbs, int inputs, const uint64_t* c1,
+                                        int64_t in_stride, uint64_t* digits, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  if (!ctx || !c1 || !digits || level_limbs < 1 || level_limbs > ctx->L || inputs < 0) return HCK_ERR_ARG;
+  if (ctx->wide) return HCK_ERR_UNSUPPORTED;
+  if (inputs > 1 && in_stride < (int64_t)level_limbs * hck::kN) return HCK_ERR_ARG;
+  if (inputs == 0) return HCK_OK;
+  if (!workspace || workspace_bytes < hck::ks_hoist_bytes(ctx, level_limbs, inputs)) return HCK_ERR_WORKSPACE;
+  return hck::ks_hoist(ctx, level_limbs, inputs, c1, in_stride, digits, (char*)workspace, (hipStream_t)stream);
+}
+
+extern "C" int hck_rotate_hoisted(const hck_context* ctx, int level_limbs, int inputs, int items,
+                                  const uint32_t* galois, const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                                  const uint64_t* digits, const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1,
+                                  int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!ctx || !galois || !c0 || !c1 || !digits || !ksk || !out0 || !out1) return HCK_ERR_ARG;
+  if (level_limbs < 1 || level_limbs > ctx->L || inputs < 1 || items < 0) return HCK_ERR_ARG;
+  if (ctx->wide) return HCK_ERR_UNSUPPORTED;
+  const int64_t limb_words = (int64_t)level_limbs * hck::kN;
+  if (inputs > 1 && in_stride < limb_words) return HCK_ERR_ARG;
+  if (items > 1 && out_stride < limb_words) return HCK_ERR_ARG;
+  if (out0 == out1 || out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1) return HCK_ERR_ARG;
+  for (int i = 0; i < items; ++i)
+    if (!galois_ok(galois[i]) || !ksk[i]) return HCK_ERR_ARG;
+  if (items == 0) return HCK_OK;
+  if (!workspace || workspace_bytes < hck::ks_hoisted_bytes(ctx, level_limbs, items)) return HCK_ERR_WORKSPACE;
+  return hck::ks_hoisted(ctx, level_limbs, inputs, items, galois, ksk, c0, c1, in_stride, digits, out0, out1,
+                         out_stride, (char*)workspace, (hipStream_t)stream);
+}
+
 extern "C" size_t hck_moddown_workspace_bytes(const hck_context* ctx, int level_limbs, int polys) {
   if (!ctx || level_limbs < 1 || level_limbs > ctx->L || polys < 0) return 0;
   const int chunk = polys < 65535 ? polys : 65535;

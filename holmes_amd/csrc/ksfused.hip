@@ -743,18 +743,31 @@ __device__ __forceinline__ void rows_fwd_lds(double (&x)[16], double* S, const d
 // (a workspace limb, or null) is loaded into x for the caller.  TW must hold the forward twiddles
 // (visible).  With ``zero`` false the products are added to sb / sa (|sb|, |sa| <= p/2 + 1 on entry:
 // the grouped kernel's running sums).  Returns |sb|, |sa| <= p/2 + 1.
+// Hoisted digits (HoistSrc::digits non-null): the extended digits of every input were materialised
+// once in the full NTT domain (natural layout, canonical u64, [input][beta][ell + K] limbs, the own
+// digit's limbs unused), and item b rotates input (src0 + b) mod inputs: each digit is then read
+// through sigma_g like d itself, with no row transform (ModUp commutes with sigma_g).
+struct HoistSrc {
+  const uint64_t* digits;
+  int inputs, src0;
+};
+template <bool HOIST>
+__device__ __forceinline__ int hoist_input(const HoistSrc& H, int b) { return HOIST ? (H.src0 + b) % H.inputs : b; }
+
+template <bool HOIST = false>
 __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], double (&x)[16],
                                         const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
                                         const double* __restrict__ t2, const uint64_t* __restrict__ key, int b,
                                         int e, int pi, int rg, int ell, int beta, double* S, const double* TW,
                                         const double* __restrict__ after, double p, double pinv,
-                                        const DevTables& T, bool zero = true) {
+                                        const DevTables& T, bool zero = true, HoistSrc H = HoistSrc{nullptr, 1, 0}) {
   const int L = T.L, K = T.K, alpha = T.alpha;
   const int ext_l = ell + K;
   const int beta_max = (L + alpha - 1) / alpha;
   const long long comp_stride = (long long)beta_max * (L + K) * kN;
   const int own = e < ell ? e / alpha : -1;
   const long long na = nat_a(rg);
+  const int src = hoist_input<HOIST>(H, b);
   const double* t2b = t2 + ((long long)b * beta * ext_l + e) * kN;  // digit j at t2b + j * ext_l * kN
   auto load_keys = [&](uint64_t (&kb)[16], uint64_t (&ka)[16], int jd) {
     const uint64_t* kp = key + ((long long)jd * (L + K) + pi) * kN + na;
@@ -770,13 +783,35 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
     for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
   }
   if (own >= 0) {
-    load_gal(x, d + (long long)b * d_stride + (long long)e * kN, na, g);
+    load_gal(x, d + (long long)src * d_stride + (long long)e * kN, na, g);
     load_keys(kb, ka, own);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
       sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);  // |x| < p: |term| <= 0.9p
       sa[k] += mulv(x[k], u2d(ka[k]), p, pinv);
     }
+  }
+  if constexpr (HOIST) {
+    // canonical digits read through sigma_g: |term| <= 0.9p; a reduction every three digits keeps
+    // the sums below p/2 + 1 + 0.9p + 3 * 0.9p < 8p <= 2^53
+    for (int n = 0; n < nt2; ++n) {
+      const int jd = t2digit(n);
+      load_gal(x, H.digits + ((long long)(src * beta + jd) * ext_l + e) * kN, na, g);
+      load_keys(kb, ka, jd);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);
+        sa[k] += mulv(x[k], u2d(ka[k]), p, pinv);
+      }
+      if (n % 3 == 2) {
+#pragma unroll
+        for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+      }
+    }
+    if (after) load_t(x, after, rg);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+    return;
   }
   {
     const double* first = nt2 > 0 ? t2b + (long long)t2digit(0) * ext_l * kN : after;
@@ -824,13 +859,14 @@ __device__ __forceinline__ TileId decode_tile(int batch, int lin) {
 // extended basis: it writes (P * sigma(add) + IP_b, IP_a) over Q u P as canonical NTT-domain residues
 // to ext_b / ext_a ([ell + K] limbs per ciphertext, Q limbs first), plus the extended-basis
 // accumulators acc_b / acc_a when given (which ext_b / ext_a may alias).
+template <bool HOIST = false>
 __device__ __forceinline__ void rows_ip_body(const uint64_t* __restrict__ d, long long d_stride, const GalF& G,
                                              const double* __restrict__ t2, const KeyPtrsF& keys, int ell, int beta,
                                              int batch, int tiles, int e0, double* __restrict__ accp,
                                              const uint64_t* __restrict__ add, long long add_stride, uint64_t* ext_b,
                                              uint64_t* ext_a, long long ext_stride, const uint64_t* acc_b,
                                              const uint64_t* acc_a, long long acc_stride, const DevTables& T, int lin,
-                                             double* S, double* TW, int koff = 0) {
+                                             double* S, double* TW, int koff = 0, HoistSrc H = HoistSrc{nullptr, 1, 0}) {
   const TileId id = decode_tile(batch, lin);
   if (id.tile >= tiles) return;
   const int b = id.b, e = e0 + (id.tile >> 4), rg = id.tile & 15;
@@ -845,12 +881,13 @@ __device__ __forceinline__ void rows_ip_body(const uint64_t* __restrict__ d, lon
     __syncthreads();
   }
   double sb[16], sa[16], x[16];
-  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T);
+  tile_ip<HOIST>(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T,
+                 true, H);
   const long long na = nat_a(rg);
   if (ext_b) {
     if (e < ell && add) {
       double ad[16];
-      load_gal(ad, add + (long long)b * add_stride + (long long)e * kN, na, g);
+      load_gal(ad, add + (long long)hoist_input<HOIST>(H, b) * add_stride + (long long)e * kN, na, g);
       const TwPair pm = T.pmodq[pi];
 #pragma unroll
       for (int k = 0; k < 16; ++k) sb[k] += mulc(ad[k], pm, p);  // |sb| <= 1.5 p
@@ -892,6 +929,17 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict
                acc_b, acc_a, acc_stride, T, blockIdx.x, S, TW);
 }
 
+// K3 of hoisted rotations (P limbs only): the digits come from HoistSrc, item b rotates input
+// (H.src0 + b) mod H.inputs.
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ip_h(const uint64_t* __restrict__ d, long long d_stride,
+                                                     const GalF G, KeyPtrsF keys, int ell, int beta, int batch,
+                                                     double* __restrict__ accp, DevTables T, HoistSrc H) {
+  __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
+  rows_ip_body<true>(d, d_stride, G, nullptr, keys, ell, beta, batch, 16 * T.K, ell, accp, nullptr, 0, nullptr,
+                     nullptr, 0, nullptr, nullptr, 0, T, blockIdx.x, S, TW, 0, H);
+}
+
 // One component of the ModDown finish, its T4 tile loaded in x (map T): ip <- (ip - NTT rows(v)) * P^-1,
 // plus the addends, canonical store.  `next` (or nothing) is loaded into x once the transform is done.
 __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], const double* __restrict__ next,
@@ -923,6 +971,7 @@ __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], co
 // pass v of the ModDown conversion T4 right away, so the Q-limb inner product never goes to HBM:
 //   out_b = (IP_b - v_b) * P^-1 + sigma_g(add) (+ acc_b),   out_a = (IP_a - v_a) * P^-1 (+ acc_a),
 // canonical u64.
+template <bool HOIST = false>
 __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, long long d_stride, const GalF& G,
                                               const double* __restrict__ t2, const KeyPtrsF& keys, int ell, int beta,
                                               int batch, const double* __restrict__ t4,
@@ -931,7 +980,8 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
                                               long long acc_stride, uint64_t* __restrict__ out_b,
                                               uint64_t* __restrict__ out_a, long long out_stride,
                                               const LevelConsts* __restrict__ lc, const DevTables& T, int lin,
-                                              double* S, double* TW, int koff = 0) {
+                                              double* S, double* TW, int koff = 0,
+                                              HoistSrc H = HoistSrc{nullptr, 1, 0}) {
   const TileId id = decode_tile(batch, lin);
   if (id.tile >= 16 * ell) return;
   const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
@@ -946,10 +996,11 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
   const double* v_b = t4 + ((long long)b * 2 * ell + i) * kN;
   const double* v_a = v_b + (long long)ell * kN;
   double sb[16], sa[16], x[16];
-  tile_ip(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T);
+  tile_ip<HOIST>(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T, true,
+                 H);
   const long long na = nat_a(rg);
   const TwPair pinv_P = lc->p_inv[i];
-  ipq_finish(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
+  ipq_finish(sb, x, v_a, add ? add + (long long)hoist_input<HOIST>(H, b) * add_stride + (long long)i * kN : nullptr, g,
              acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
              out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
   ipq_finish(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
@@ -1026,6 +1077,39 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restric
   __shared__ double TW[kTwLds];
   rows_ipq_body(d, d_stride, G, t2, keys, ell, beta, batch, t4, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
                 out_stride, lc, T, blockIdx.x, S, TW);
+}
+
+// K5 of hoisted rotations: as k_ks_rows_ipq with the digits and inputs of HoistSrc.
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq_h(const uint64_t* __restrict__ d, long long d_stride,
+                                                      const GalF G, KeyPtrsF keys, int ell, int beta, int batch,
+                                                      const double* __restrict__ t4, const uint64_t* __restrict__ add,
+                                                      long long add_stride, uint64_t* __restrict__ out_b,
+                                                      uint64_t* __restrict__ out_a, long long out_stride,
+                                                      const LevelConsts* __restrict__ lc, DevTables T, HoistSrc H) {
+  __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
+  rows_ipq_body<true>(d, d_stride, G, nullptr, keys, ell, beta, batch, t4, add, add_stride, nullptr, nullptr, 0, out_b,
+                      out_a, out_stride, lc, T, blockIdx.x, S, TW, 0, H);
+}
+
+// The hoisted digits: the NTT rows pass of every ModUp output tile of T2, stored canonical in the
+// natural layout at digits[b][j][e] (the own digit's limbs of digit j are skipped: d itself serves
+// them).  Grid (16 (ell + K), beta, batch).
+__global__ __launch_bounds__(kT) void k_ks_hoist_store(const double* __restrict__ t2, int ell, int beta,
+                                                       uint64_t* __restrict__ digits, DevTables T) {
+  __shared__ double S[kRowLds];
+  const int e = blockIdx.x >> 4, rg = blockIdx.x & 15, j = blockIdx.y, b = blockIdx.z;
+  if (e < ell && e / T.alpha == j) return;
+  const int ext_l = ell + T.K;
+  const int pi = e < ell ? e : T.L + (e - ell);
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  const long long off = ((long long)(b * beta + j) * ext_l + e) * kN;
+  double x[16];
+  load_t(x, t2 + off, rg);
+  rows_fwd_t(x, rg, S, T.tw_fwd + (size_t)pi * kN, p, pinv);
+  uint64_t* o = digits + off + nat_a(rg);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(x[k], p, pinv));
 }
 
 // ----------------------------------------------------------------- ModDown / rescale finish
@@ -1351,6 +1435,94 @@ int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const ui
                                                                 tiles, add, add_stride, ext_b, ext_a, ext_stride,
                                                                 acc_b, acc_a, acc_stride, c->dev);
   HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+// ----------------------------------------------------------------- hoisted rotations
+// ks_hoist: the extended digits of `inputs` polynomials d (NTT domain, no automorphism) in the full
+// NTT domain, canonical u64 [inputs][beta][ell + K] limbs (the own digit's limbs of each digit are
+// left unwritten); workspace T1 + T2 as in ks_fused.
+size_t ks_hoist_bytes(const hck_context* c, int ell, int inputs) {
+  const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
+  const size_t per = inputs < kMaxBatchF ? inputs : kMaxBatchF;
+  return per * kN * 8 * (ell + beta * ext_l);
+}
+
+int ks_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
+             char* ws, hipStream_t s) {
+  if (c->wide) return HCK_ERR_UNSUPPORTED;
+  if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
+  const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
+  const long long n = kN;
+  const int per = inputs < kMaxBatchF ? inputs : kMaxBatchF;
+  double* t1 = (double*)ws;
+  double* t2 = t1 + (long long)per * ell * n;
+  const int last_digit = ell - c->alpha * (beta - 1);
+  for (int b0 = 0; b0 < inputs; b0 += kMaxBatchF) {
+    const int nb = inputs - b0 < kMaxBatchF ? inputs - b0 : kMaxBatchF;
+    k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * nb), kT, 0, s>>>(
+        d + (long long)b0 * d_stride, d_stride, gal_uniform(1u), 0, 0, t1, ell, nb, c->dev);
+    HCK_CHECK_LAUNCH();
+    launch_conv(c,
+                ConvArgs{t1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                         modup_consts(c, ell, 0), 1},
+                dim3(128, beta, nb), ext_l - last_digit, s);
+    HCK_CHECK_LAUNCH();
+    k_ks_hoist_store<<<dim3(16 * ext_l, beta, nb), kT, 0, s>>>(t2, ell, beta,
+                                                                digits + (long long)b0 * beta * ext_l * n, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
+
+// ks_hoisted: item i (< items) = rotation of input i % inputs by galois[i] with key ksk[i], from its
+// hoisted digits: (sigma(c0) + KS_b(sigma(c1)), KS_a(sigma(c1))) over ell limbs, bit-identical to
+// ks_fused with that Galois element (ModUp commutes with sigma).  Workspace T4 + ACCP per item of
+// a launch (at most kMaxBatchF items each).
+size_t ks_hoisted_bytes(const hck_context* c, int ell, int items) {
+  const int per = items < kMaxBatchF ? items : kMaxBatchF;
+  return (size_t)per * kN * 8 * (2 * ell + 2 * c->K);
+}
+
+int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint32_t* galois,
+               const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
+               const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
+               hipStream_t s) {
+  if (c->wide) return HCK_ERR_UNSUPPORTED;
+  if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
+  const int K = c->K, beta = beta_of(c, ell);
+  const long long n = kN;
+  for (int i0 = 0; i0 < items; i0 += kMaxBatchF) {
+    const int nb = items - i0 < kMaxBatchF ? items - i0 : kMaxBatchF;
+    GalF G{};
+    G.per_item = 1;
+    KeyPtrsF kp{};
+    for (int b = 0; b < nb; ++b) {
+      G.g[b] = galois[i0 + b];
+      kp.k[b] = ksk[i0 + b];
+    }
+    const HoistSrc H{digits, inputs, i0 % inputs};
+    double* t4 = (double*)ws;
+    double* accp = t4 + (long long)nb * 2 * ell * n;
+    {
+      const int tiles = 16 * K, groups = (tiles + kXcds - 1) / kXcds;
+      k_ks_rows_ip_h<<<dim3(groups * kXcds * nb), kT, 0, s>>>(c1, in_stride, G, kp, ell, beta, nb, accp, c->dev, H);
+      HCK_CHECK_LAUNCH();
+    }
+    launch_conv(c,
+                ConvArgs{accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n, (long long)ell * n,
+                         c->d_moddown + ell, 0},
+                dim3(128, 2, nb), ell, s);
+    HCK_CHECK_LAUNCH();
+    {
+      const int tiles = 16 * ell, groups = (tiles + kXcds - 1) / kXcds;
+      k_ks_rows_ipq_h<<<dim3(groups * kXcds * nb), kT, 0, s>>>(c1, in_stride, G, kp, ell, beta, nb, t4, c0, in_stride,
+                                                             out_b + (long long)i0 * out_stride,
+                                                             out_a + (long long)i0 * out_stride, out_stride,
+                                                             c->d_level + ell, c->dev, H);
+      HCK_CHECK_LAUNCH();
+    }
+  }
   return HCK_OK;
 }
 

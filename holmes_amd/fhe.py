@@ -548,8 +548,9 @@ def _has_key(ctx: CKKSContext, offset: int) -> bool:
 def prepare_hoisted_baby_rotations(ct: Cipher, offsets, ctx: CKKSContext, strategy: str = "normal",
                                    baby_anchor_step: int = -1) -> tuple:
     """The baby basis of a BSGS product: one cipher per offset (the input batch rotated by it),
-    offset 0 sharing the input's tensors.  An offset without its own key is reached from the
-    largest smaller offset already built whose difference has a key (the anchor blocks of
+    offset 0 sharing the input's tensors.  The offsets with their own keys come from one hoisted
+    ModUp per input (``CKKSContext.rotate_hoisted``); an offset without its own key is reached from
+    the largest smaller offset already built whose difference has a key (the anchor blocks of
     llama3fhe/operators/linear/config.py:235-268)."""
 
     if ct.is_ext:
@@ -560,9 +561,22 @@ def prepare_hoisted_baby_rotations(ct: Cipher, offsets, ctx: CKKSContext, strate
         # the MAC needs one batch stride across the basis: drop the stored limbs above the level
         c0, c1 = c0.contiguous(), c1.contiguous()
     built: dict[int, tuple] = {}
+    offsets = [int(o) for o in offsets]
+    direct = [o for o in dict.fromkeys(offsets) if o % ctx.max_slots and _has_key(ctx, o)]
+    if ctx.supports_hoisting and len(direct) > 1:
+        # one ModUp per input; every offset with its own key read from the hoisted digits
+        B = int(c0.shape[0])
+        gals = [_galois(o, ctx) for o in direct for _ in range(B)]
+        digits = ctx.hoist_digits(c1, limbs)
+        h0, h1 = ctx.rotate_hoisted(c0, c1, limbs, digits, gals, [ctx.key_for_galois(g) for g in gals])
+        del digits
+        for i, o in enumerate(direct):
+            built[o] = (h0[i * B:(i + 1) * B], h1[i * B:(i + 1) * B])
     out = []
-    for off in [int(o) for o in offsets]:
-        if off % ctx.max_slots == 0:
+    for off in offsets:
+        if off in built:
+            pair = built[off]
+        elif off % ctx.max_slots == 0:
             pair = (c0, c1)
         elif _has_key(ctx, off):
             g = _galois(off, ctx)

@@ -162,6 +162,29 @@ int hck_rotate_ext_sum(const hck_context* ctx, int level_limbs, int outputs, int
                        const uint64_t* acc0, const uint64_t* acc1, int64_t acc_stride, uint64_t* out0,
                        uint64_t* out1, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Hoisted rotations of several inputs by several amounts, the hoisted baby steps of a BSGS product
+ * (fhe.prepare_hoisted_baby_rotations, llama3fhe/operators/linear/operator.py:113-119) and of a
+ * bootstrap's linear transforms ("double_hoist", llama3fhe/operators/nonlinear/bootstrap.py:
+ * 119-160).  hck_rotate_hoist_prepare runs the ModUp of c1 of each of `inputs` ciphertexts once and
+ * stores its extended digits in the full NTT domain: `digits` (device, hck_rotate_hoist_digits_bytes
+ * bytes) holds [inputs][ceil(level_limbs / alpha)][level_limbs + K] limbs.  hck_rotate_hoisted
+ * then rotates input i % inputs by galois[i] with key ksk[i] for every item i < items (host arrays):
+ * out[i] = (sigma(c0) + KS_b(sigma(c1)), KS_a(sigma(c1))) over level_limbs limbs, reading the
+ * digits through sigma (ModUp commutes with the automorphism), so each rotation skips the INTT,
+ * the conversion and the digits' NTT.  Bit-identical to hck_rotate_many.  c0 / c1 at
+ * input * in_stride, out at i * out_stride.  Workspace hck_rotate_hoist_workspace_bytes(ctx,
+ * level_limbs, inputs, items) serves both calls.  HCK_ERR_UNSUPPORTED on a context with a prime at
+ * or above 2^50. */
+size_t hck_rotate_hoist_digits_bytes(const hck_context* ctx, int level_limbs, int inputs);
+size_t hck_rotate_hoist_workspace_bytes(const hck_context* ctx, int level_limbs, int inputs, int items);
+int hck_rotate_hoist_prepare(const hck_context* ctx, int level_limbs, int inputs, const uint64_t* c1,
+                             int64_t in_stride, uint64_t* digits, void* workspace, size_t workspace_bytes,
+                             void* stream);
+int hck_rotate_hoisted(const hck_context* ctx, int level_limbs, int inputs, int items, const uint32_t* galois,
+                       const uint64_t* c0, const uint64_t* c1, int64_t in_stride, const uint64_t* digits,
+                       const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* hck_rotate / hck_rotate_ext with a Galois element per item (galois[b], host array of `batch`):
  * one launch sequence for rotations by different amounts, each with its own key -- the batched
  * giant step of bench/cmp/holmes_multi_mac.py:180-186 (fhe.homo_rotate_batch) and the baby and

@@ -229,6 +229,30 @@ def test_conversion_engines_agree(env, ell):
         ctx.set_conversion_engine("fp32")
 
 
+@pytest.mark.parametrize("ell,inputs,per", [(24, 3, 5), (9, 2, 3), (1, 1, 4)])
+def test_hoisted_rotations_equal_rotate_many(env, ell, inputs, per):
+    """Rotations from hoisted ModUp digits (one ModUp per input, read through sigma) equal the
+    per-item key switch bit for bit, item i = input i % inputs, and one of them equals the oracle."""
+    _, client, ctx, orc = env
+    rng = np.random.default_rng(1100 + ell)
+    c0, c1 = _rand(ctx, rng, inputs, ell), _rand(ctx, rng, inputs, ell)
+    c1[0, 0, :3] = [0, 1, ctx.primes[0] - 1]
+    steps = [1, -3, 64, 4097, (1 << 15) - 1, 7][:per]
+    gals = [ctx.galois_element(r) for r in steps for _ in range(inputs)]  # offset-major, then input
+    pairs = {g: _key_pair(client, ctx, orc, g) for g in set(gals)}
+    keys = [pairs[g][0] for g in gals]
+    d0, d1 = _dev(c0), _dev(c1)
+    digits = ctx.hoist_digits(d1, ell)
+    h0, h1 = ctx.rotate_hoisted(d0, d1, ell, digits, gals, keys)
+    idx = torch.tensor([i % inputs for i in range(len(gals))], device=d0.device)
+    r0, r1 = (x.view(torch.int64).index_select(0, idx).view(torch.uint64) for x in (d0, d1))
+    w0, w1 = ctx.rotate_raw(r0, r1, ell, gals, keys)
+    assert torch.equal(h0, w0) and torch.equal(h1, w1)
+    g = gals[1]
+    o0, o1 = orc.rotate(ell, g, c0[1 % inputs], c1[1 % inputs], pairs[g][1])
+    assert np.array_equal(_host(h0)[1], o0) and np.array_equal(_host(h1)[1], o1)
+
+
 def test_rotate_matches_oracle(env):
     _, client, ctx, orc = env
     ell = 24
