@@ -548,6 +548,30 @@ class CipherOps:
             return ct
         return self._fhe.homo_rotate(ct, int(r) % self.slots, ctx)
 
+    def rotate_offsets(self, ct, offsets) -> list:
+        """The batch ``ct`` rotated by each offset, one batch per offset: one ModUp per item and
+        every rotation read from its hoisted digits (``CKKSContext.rotate_hoisted``); offset 0 is
+        ``ct`` itself."""
+
+        ctx = self.ctx
+        limbs = self.limbs(ct)
+        B = int(ct.batch_size)
+        offs = [int(o) % self.slots for o in offsets]
+        nz = [o for o in dict.fromkeys(offs) if o]
+        done = {}
+        if nz and ctx.supports_hoisting:
+            c0, c1 = (c[:, :limbs].contiguous() for c in ct.cv)
+            gals = [ctx.galois_element(o) for o in nz for _ in range(B)]
+            digits = ctx.hoist_digits(c1, limbs)
+            h0, h1 = ctx.rotate_hoisted(c0, c1, limbs, digits, gals, [ctx.key_for_galois(g) for g in gals])
+            del digits
+            for i, o in enumerate(nz):
+                done[o] = ct.cipher_like([h0[i * B:(i + 1) * B], h1[i * B:(i + 1) * B]], batch_size=B)
+        else:
+            for o in nz:
+                done[o] = self.rotate(ct, o)
+        return [done[o] if o else ct for o in offs]
+
     def conj(self, ct):
         return self._fhe.homo_rotate(ct, self.ctx.M - 1, self.ctx)
 

@@ -429,21 +429,28 @@ class PrefillAttention:
         self.rs_shift = SlotConst(self.rs_beta * (packed_count_row(1.0) > 0))
 
     # -- carriers
-    def _lane_carriers(self, X, base: int, masks):
-        """Items (c', rho) for rho = 0..7 of the batch X: X rotated by ``base`` with lanes rotated
-        by rho (lane t holds token 8 c' + (t + rho) mod 8), kept on the half ``masks`` [rho] selects
-        (per-item rows allowed)."""
+    def _lane_carriers(self, X, *sets):
+        """For each (base, masks) of ``sets``: items (c', rho) for rho = 0..7 of the batch X, X rotated
+        by ``base`` with lanes rotated by rho (lane t holds token 8 c' + (t + rho) mod 8), kept on the
+        half ``masks`` [rho] selects (per-item rows allowed).  Every rotation of X comes from one
+        hoisted ModUp per item (15 offsets per set)."""
 
         ops = self.ops
-        out = []
-        for rho in range(LANES):
-            lo, hi = masks[rho]
-            if rho == 0:
-                out.append(ops.mac([(ops.rotate(X, base), lo)]))
-            else:
-                out.append(ops.mac([(ops.rotate(X, base + rho), lo), (ops.rotate(X, base + rho - LANES), hi)]))
-        items = [ops.items(o) for o in out]             # [rho][c']
-        return {(cp, rho): items[rho][cp] for cp in range(CTS) for rho in range(LANES)}
+        offs = [o for base, _ in sets for o in [base] + [b for rho in range(1, LANES)
+                                                          for b in (base + rho, base + rho - LANES)]]
+        rot = dict(zip(offs, ops.rotate_offsets(X, offs)))
+        result = []
+        for base, masks in sets:
+            out = []
+            for rho in range(LANES):
+                lo, hi = masks[rho]
+                if rho == 0:
+                    out.append(ops.mac([(rot[base], lo)]))
+                else:
+                    out.append(ops.mac([(rot[base + rho], lo), (rot[base + rho - LANES], hi)]))
+            items = [ops.items(o) for o in out]             # [rho][c']
+            result.append({(cp, rho): items[rho][cp] for cp in range(CTS) for rho in range(LANES)})
+        return result
 
     def _pair_carriers(self, low, up, pairs):
         """Per pair (c, p): the carrier of key p in the lower half plus that of key p + split(c) in
@@ -502,8 +509,8 @@ class PrefillAttention:
         no key is computed; ``A`` the projection batch (before RoPE)."""
 
         ops = self.ops
-        k_lo = self._lane_carriers(A, HALF, self.key_masks[False])    # the key half moved down
-        k_up = self._lane_carriers(A, 0, self.key_masks[True])        # ... and kept in place
+        # the key half moved down, and kept in place
+        k_lo, k_up = self._lane_carriers(A, (HALF, self.key_masks[False]), (0, self.key_masks[True]))
         q = ops.mac([(A, self.rope_q)])                               # RoPE'd queries, lower half
         q = ops.items(ops.add(q, ops.rotate(q, HALF)))                # ... in both halves
         dense = {}
@@ -555,13 +562,14 @@ class PrefillAttention:
         y = ops.poly(x, self.polys.exp)
         # invalid positions hold x = beta: remove the public E(0) there (no level)
         y = ops.add_vec(y, SlotConst(-self.exp_at_zero * self.invalid.value))
-        rows = ops.items(self._fold_keys(ops.mul(y, y)))                 # R at (h, 0, t)
-        packed = ops.mac([(ops.rotate(rows[c], -8 * c), self.rowc[c]) for c in range(CTS)])
+        rows = self._fold_keys(ops.mul(y, y))                            # R at (h, 0, t)
+        rows = ops.items(ops.rotate(rows, [-8 * c for c in range(CTS)]))  # one launch, a rotation per item
+        packed = ops.mac([(rows[c], self.rowc[c]) for c in range(CTS)])
         z = ops.mac([(packed, self.rs_in)], out_scale=ops.ideal_scale(ops.limbs(packed) - 1))
         z = ops.add_vec(z, self.rs_shift)                # slots outside the packed rows stay at 0
         z = self._refreshed_series_input(z, "rsqrt")
         lam = ops.poly(z, self.polys.rsqrt)             # rsqrt(R / n) at (h, c, t)
-        spread = ops.rotate(ops.copies(lam, CTS), [8 * c for c in range(CTS)])
+        spread = ops.batch(ops.rotate_offsets(lam, [8 * c for c in range(CTS)]))
         lam_c = self._spread_keys(ops.mac([(spread, self.inv_sqrt_count)]))   # 1 / sqrt(R) everywhere
         yl = ops.mul(y, lam_c)
         return ops.mul(yl, yl)
@@ -593,8 +601,7 @@ class PrefillAttention:
             P = ops.drop(P, PV_INPUT_LIMBS)
         if ops.limbs(V) > ops.limbs(P):
             V = ops.drop(V, ops.limbs(P))                 # the carriers only need P's level
-        v_lo = self._lane_carriers(V, 0, self.lane[False])
-        v_up = self._lane_carriers(V, HALF, self.lane[True])
+        v_lo, v_up = self._lane_carriers(V, (0, self.lane[False]), (HALF, self.lane[True]))
         p_items = ops.items(P)
         giants = [(c, a) for c in range(CTS) for a in range((split(c) + LANES - 1) // LANES)]
         at = {k: i for i, k in enumerate(giants)}

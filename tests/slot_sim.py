@@ -102,6 +102,9 @@ class SlotOps:
             return self._like(ct, v)
         return self._like(ct, np.roll(ct.values, -int(r), axis=1))
 
+    def rotate_offsets(self, ct, offsets) -> list:
+        return [self.rotate(ct, int(o)) for o in offsets]
+
     def conj(self, ct):
         return self._like(ct, np.conj(ct.values))
 
