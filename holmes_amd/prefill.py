@@ -392,6 +392,7 @@ class PrefillAttention:
     def __init__(self, ops, spec: PrefillSpec | None = None, polys: PrefillPolynomials | None = None, *,
                  refresh_series_inputs: bool = False, series_programs: dict | None = None):
         self.ops = ops
+        self._mark = lambda name: None  # stage timing callback of the running forward
         # refresh the exp series' input (16 ciphertexts, |x| <= 1) and the inverse square root's (one
         # packed ciphertext) before evaluating them: the steady-state layer, whose attention starts
         # from a refreshed layer input rather than a fresh encryption at the top of the chain
@@ -581,7 +582,9 @@ class PrefillAttention:
         if not self.refresh_series_inputs:
             return x
         ops = self.ops
+        self._mark("attention_softmax")
         x = ops.refresh(x, bound_bits=0, program=self.series_programs.get(which))
+        self._mark(f"attention_{which}_refresh")
         lim = ops.limbs(x) - 1
         return ops.adjust(x, lim, ops.ideal_scale(lim))
 
@@ -617,10 +620,21 @@ class PrefillAttention:
         sums = ops.mul_sum(col, right, [split(c) for c in range(CTS)])
         return ops.add(sums, ops.rotate(sums, HALF))
 
-    def forward(self, A, V):
-        S2 = self.scores(A)
-        P = self.softmax(S2)
-        return self.pv(P, V), {"scores": S2, "probs": P}
+    def forward(self, A, V, mark=None):
+        """Attention output and its intermediates; ``mark(name)`` (optional) is called after the
+        scores, around each series-input refresh, and after the softmax and PV (stage timing)."""
+
+        self._mark = mark if mark is not None else (lambda name: None)
+        try:
+            S2 = self.scores(A)
+            self._mark("attention_scores")
+            P = self.softmax(S2)
+            self._mark("attention_softmax")
+            out = self.pv(P, V)
+            self._mark("attention_pv")
+        finally:
+            self._mark = lambda name: None
+        return out, {"scores": S2, "probs": P}
 
 
 def attention_input_numpy(xn: np.ndarray, spec: PrefillSpec, w: DecodeWeights) -> tuple[np.ndarray, np.ndarray]:
@@ -728,7 +742,7 @@ class PrefillLayer:
             nonlocal t0
             torch.cuda.synchronize()
             now = time.perf_counter()
-            t[name] = now - t0
+            t[name] = t.get(name, 0.0) + now - t0
             t0 = now
 
         x_cts = tuple(x_cts)
@@ -744,9 +758,9 @@ class PrefillLayer:
         mark("qkv_projection")
         A, V = ops.batch(a_out), ops.batch(v_out)
         self.levels = {"input": ops.limbs(x_cts[0]), "rmsnorm1": ops.limbs(xn[0]), "A": ops.limbs(A)}
-        out, _ = self.attn.forward(A, V)
+        out, _ = self.attn.forward(A, V, mark=mark)
         self.levels["attention"] = ops.limbs(out)
-        mark("attention")
+        t["attention"] = sum(v for k, v in t.items() if k.startswith("attention_"))
         proj, _ = self.op.apply(ops.items(out), self.w_o)
         delta = ops.batch(proj)
         delta = ops.add(delta, ops.conj(delta))
