@@ -84,6 +84,8 @@ SIGNATURES = {
     "hck_relinearize": (_i, [_vp, _i, _i, _vp, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "hck_mul_relin_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_mul_relin": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "hck_mul_relin_rescale_workspace_bytes": (_sz, [_vp, _i, _i]),
+    "hck_mul_relin_rescale": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "hck_weighted_sum": (_i, [_vp, _i, _i, _i, _vp, _i64, _vp, _vp, _i64, _vp]),
     "hck_lincomb": (_i, [_vp, _i, _i, _i, ctypes.POINTER(_vp), _vp, ctypes.POINTER(_vp), _vp]),
     "hck_modraise_workspace_bytes": (_sz, [_vp, _i, _i]),

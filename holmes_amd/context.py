@@ -561,6 +561,27 @@ class CKKSContext:
                                   ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_mul_relin")
         return out if stacked else (out[0], out[1])
 
+    def mul_relin_rescale_raw(self, a0, a1, b0, b1, limbs: int, key: torch.Tensor, stacked: bool = False):
+        """mul_relin_raw followed by the rescale, in one native call (the same residues): outputs at
+        ``limbs - 1`` limbs."""
+
+        self._check_key(key)
+        if limbs < 2:
+            raise ValueError("a rescaled product needs at least two limbs")
+        sa = self._pair(a0, a1, limbs, "mul lhs")
+        sb = self._pair(b0, b1, limbs, "mul rhs")
+        B = a0.shape[0]
+        if b0.shape[0] != B:
+            raise ValueError("mul operands need the same batch")
+        out = self.empty(2, B, limbs - 1, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_mul_relin_rescale_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_mul_relin_rescale(self._h, limbs, B, a0.data_ptr(), a1.data_ptr(), sa, b0.data_ptr(),
+                                          b1.data_ptr(), sb, key.data_ptr(), out[0].data_ptr(), out[1].data_ptr(),
+                                          (limbs - 1) * self.N, ws.data_ptr(), ws.numel(),
+                                          _stream_ptr(self.device)), "hck_mul_relin_rescale")
+        return out if stacked else (out[0], out[1])
+
     def resident(self, table: np.ndarray) -> torch.Tensor:
         """A small host table (residue weights, constants) on the device, uploaded once: a later
         call with the same bytes reuses the device copy, so repeated evaluations (every bootstrap's

@@ -226,6 +226,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->h_level.assign((size_t)(num_q + 1), hck::LevelConsts{});
   c->h_rescale.assign((size_t)(num_q + 1), hck::ConvConsts{});
   c->h_raise.assign((size_t)(num_q + 1), hck::ConvConsts{});
+  c->h_mdrs.assign((size_t)(num_q + 1), hck::ConvConsts{});
   for (int ell = 1; ell <= num_q; ++ell) {
     const int beta = (ell + alpha - 1) / alpha;
     for (int j = 0; j < beta; ++j) {
@@ -251,6 +252,30 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       std::vector<int> usrc{0}, udst, uslot;
       for (int i = 1; i < ell; ++i) { udst.push_back(i); uslot.push_back(i - 1); }
       fill_conv(c->h_raise[ell], P, usrc, udst, uslot, ninv_u, ninv_w1_u);
+      // ModDown fused with the rescale: the moddown sums of targets q_0 .. q_{ell-2} times P^-1,
+      // q_{ell-1} as the extra target nt, and P^-1 folded into the Z limb's inverse transform
+      std::vector<int> fdst(dst.begin(), dst.end() - 1), fslot(slot.begin(), slot.end() - 1);
+      hck::ConvConsts& fc = c->h_mdrs[ell];
+      fill_conv(fc, P, src, fdst, fslot, ninv_u, ninv_w1_u);
+      auto p_inv_mod = [&](u64 q) {
+        u64 pm = 1;
+        for (int k = 0; k < num_p; ++k) pm = mulmod(pm, P[num_q + k] % q, q);
+        return invmod(pm, q);
+      };
+      for (int t = 0; t <= fc.nt; ++t) {
+        const int qi = t < fc.nt ? fdst[t] : ell - 1;
+        const u64 q = P[qi], pinv_q = p_inv_mod(q);
+        for (int s = 0; s < fc.ns; ++s) {
+          u64 v = 1;
+          for (int r = 0; r < fc.ns; ++r) if (r != s) v = mulmod(v, P[src[r]] % q, q);
+          fc.hmod[s][t] = pair_of(mulmod(v, pinv_q, q), q);
+        }
+      }
+      fc.dst_prime[fc.nt] = ell - 1;
+      fc.dst_slot[fc.nt] = ell - 1;
+      const u64 ql = P[ell - 1], pinv_l = p_inv_mod(ql);
+      fc.z_n0 = pair_of(mulmod(ninv_u[ell - 1], pinv_l, ql), ql);
+      fc.z_n1 = pair_of(mulmod(ninv_w1_u[ell - 1], pinv_l, ql), ql);
     }
     hck::LevelConsts& lc = c->h_level[ell];
     for (int i = 0; i < ell; ++i) {
@@ -268,10 +293,12 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
     if (cc.nt > 0 && !wide) digits_ok = digits_ok && append_conv_digits(cc, P, digits);
   for (hck::ConvConsts& cc : c->h_moddown)
     if (cc.nt > 0 && !wide) digits_ok = digits_ok && append_conv_digits(cc, P, digits);
+  for (hck::ConvConsts& cc : c->h_mdrs)
+    if (cc.nt > 0 && !wide) digits_ok = digits_ok && append_conv_digits(cc, P, digits);
   if (!digits_ok) { delete c; return HCK_ERR_UNSUPPORTED; }
 
   // one device block: [p | pinv | fwd | inv | ninv | ninv_w1 | zeta4 | pmodq | modup | moddown | level |
-  // rescale | raise | primes | encoder roots | conversion digits]
+  // rescale | raise | moddown-rescale | primes | encoder roots | conversion digits]
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   size_t off = 0;
   const size_t o_p = off; off = align(off + np * sizeof(double));
@@ -287,6 +314,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   const size_t o_lv = off; off = align(off + c->h_level.size() * sizeof(hck::LevelConsts));
   const size_t o_rs = off; off = align(off + c->h_rescale.size() * sizeof(hck::ConvConsts));
   const size_t o_ra = off; off = align(off + c->h_raise.size() * sizeof(hck::ConvConsts));
+  const size_t o_mr = off; off = align(off + c->h_mdrs.size() * sizeof(hck::ConvConsts));
   const size_t o_pu = off; off = align(off + np * sizeof(u64));
   const size_t o_etr = off; off = align(off + nslots * sizeof(double));
   const size_t o_eti = off; off = align(off + nslots * sizeof(double));
@@ -309,6 +337,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
       {o_lv, c->h_level.data(), c->h_level.size() * sizeof(hck::LevelConsts)},
       {o_rs, c->h_rescale.data(), c->h_rescale.size() * sizeof(hck::ConvConsts)},
       {o_ra, c->h_raise.data(), c->h_raise.size() * sizeof(hck::ConvConsts)},
+      {o_mr, c->h_mdrs.data(), c->h_mdrs.size() * sizeof(hck::ConvConsts)},
       {o_pu, P.data(), np * sizeof(u64)},
       {o_etr, etr.data(), nslots * sizeof(double)},
       {o_eti, eti.data(), nslots * sizeof(double)},
@@ -334,6 +363,7 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   c->d_level = (hck::LevelConsts*)(base + o_lv);
   c->d_rescale = (hck::ConvConsts*)(base + o_rs);
   c->d_raise = (hck::ConvConsts*)(base + o_ra);
+  c->d_mdrs = (hck::ConvConsts*)(base + o_mr);
   c->d_primes_u64 = (const u64*)(base + o_pu);
   c->d_enc_twr = (const double*)(base + o_etr);
   c->d_enc_twi = (const double*)(base + o_eti);

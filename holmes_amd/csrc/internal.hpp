@@ -31,6 +31,11 @@ struct ConvConsts {
   // [t][c][s][a] = balanced base-256 digit c of (hmod[s][t] * 256^a mod t), centered, for
   // s < 8, a < 8 (zero for s >= ns and for a = 7), c < kConvDigits.
   long long dig_off;
+  // ModDown fused with the rescale (d_mdrs): the sources are the P primes, the stored targets
+  // q_0 .. q_{ell-2} with hmod[s][t] = (P / p_s mod q_t) P^-1, and q_{ell-1} rides along as
+  // target nt (hmod[s][nt], dst_prime[nt]); the extra source limb Z (the q_{ell-1} limb of
+  // P * d + IP) leaves its inverse transform multiplied by P^-1 through z_n0 / z_n1.
+  TwPair z_n0, z_n1;
 };
 constexpr int kConvDigits = 7;  // balanced base-256 digits of a centered residue (|x| < 2^49)
 
@@ -68,11 +73,12 @@ struct hck_context {
   hck::ConvConsts* d_moddown = nullptr; // [L + 1]
   hck::ConvConsts* d_rescale = nullptr; // [L + 1]: level ell converts limb ell - 1 to limbs 0 .. ell - 2
   hck::ConvConsts* d_raise = nullptr;   // [L + 1]: target count t converts limb 0 to limbs 1 .. t - 1
+  hck::ConvConsts* d_mdrs = nullptr;    // [L + 1]: ModDown fused with the rescale from ell to ell - 1 limbs
   hck::LevelConsts* d_level = nullptr;  // [L + 1]
   const uint64_t* d_primes_u64 = nullptr; // [np]
   const double* d_enc_twr = nullptr;      // [N/2]: special-IFFT roots, stage h at [h-1, 2h-1)
   const double* d_enc_twi = nullptr;
-  std::vector<hck::ConvConsts> h_modup, h_moddown, h_rescale, h_raise;
+  std::vector<hck::ConvConsts> h_modup, h_moddown, h_rescale, h_raise, h_mdrs;
   std::vector<hck::LevelConsts> h_level;
   int beta_max;
 };
@@ -131,6 +137,14 @@ int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint3
                const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
                const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
                hipStream_t s);
+// Relinearisation fused with the rescale: out = rescale((acc_b, acc_a) + KeySwitch(d)) at ell - 1
+// limbs, bit-identical to ks_fused followed by rescale_fused; the q_{ell-1} limb joins the ModDown
+// sources (see ConvConsts::z_n0).  Matrix-core conversion engine, FP64 contexts, ell >= 2 only
+// (HCK_ERR_UNSUPPORTED otherwise).  Workspace ks_rs_bytes.
+size_t ks_rs_bytes(const hck_context* c, int ell, int batch);
+int ks_relin_rescale(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
+                     const uint64_t* const* ksk, const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride,
+                     uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws, hipStream_t s);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

@@ -380,6 +380,7 @@ struct ConvArgs {
   long long dst_zs, dst_ys;
   const ConvConsts* cc_base;
   int cc_y;
+  const double* zsrc;  // the ModDown-rescale's extra source limb (group (z, y) at zsrc + z src_zs + y src_ys)
 };
 
 template <bool SEPX>
@@ -529,6 +530,16 @@ __device__ __forceinline__ double mconv_fold(int a, int b, int d, int c6, double
   return reduce(r, p, pinv);
 }
 
+// mconv_fold with an integer addend r (|r| < 2^49) in the low part: |lo + r| < 2^50, and the
+// fold's final sum stays below 2^52.
+__device__ __forceinline__ double mconv_fold_add(int a, int b, int d, int c6, double r, double p, double pinv) {
+  const double lo = __builtin_fma(65536.0, (double)b, (double)a) + r;
+  const double hi = __builtin_fma(65536.0, (double)c6, (double)d);
+  const double q = __builtin_rint(hi * (4294967296.0 * pinv));
+  const double v = __builtin_fma(-q, p, hi * 4294967296.0) + lo;
+  return reduce(v, p, pinv);
+}
+
 template <bool SEPX>
 __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y, long long z, double* Y, double* X,
                                                 const DevTables& T) {
@@ -630,6 +641,153 @@ __global__ __launch_bounds__(kT, 2) void k_ks_cols_mconv(const ConvArgs A, DevTa
   __shared__ double Y[16 * kYStride];
   __shared__ double X[SEPX ? 16 * kYStride : 1];
   cols_mconv_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, T);
+}
+
+// ----------------------------------------------------------------- K4 of the ModDown fused with the rescale
+// cols_mconv_body with one more source limb, Z = the q_{ell-1} limb of P * acc + IP (ConvConsts
+// of d_mdrs).  After phase 1, slots 0 and 1 run Z's INTT cols (P^-1 folded into its last stage, via
+// two extra LDS runs); phase 1c forms, for every coefficient of the two columns, the rescale's
+// centered residue r = [Z P^-1 - sum_s y_s hmod[s][nt]]_{q_{ell-1}}, i.e. the q_{ell-1} limb of the
+// ModDown output in the coefficient domain; phase 2 adds r to every stored target's conversion sum
+// (whose tables carry P^-1) before the NTT cols.  With the finish of k_ks_rows_ipq_rs this yields
+//   out_i = ((IP_i - NTT(conv_i)) P^-1 + acc_i - NTT(r)) q_{ell-1}^-1,
+// the ModDown followed by the rescale, exactly.
+__device__ __forceinline__ double undigit(uint64_t w) {
+  constexpr uint64_t M = 0x0080808080808080ULL;
+  return __longlong_as_double((long long)((w ^ M) - M + 0x4338000000000000ULL)) - 6755399441055744.0;
+}
+
+template <bool SEPX>
+__device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, int y, long long z, double* Y, double* X,
+                                                   double* Z, const DevTables& T) {
+  const double* __restrict__ src = A.src;
+  double* __restrict__ dst = A.dst;
+  const ConvConsts& C = A.cc_base[y * A.cc_y];
+  const int ns = C.ns, nt = C.nt;
+  const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
+  const int c0 = bx * 2;
+  uint64_t* D = reinterpret_cast<uint64_t*>(Y);
+  // phase 1: the P sources, as in cols_mconv_body
+  {
+    const int s = sigma >> 1, cl = sigma & 1;
+    const bool act = s < ns;
+    const int sp = C.src_prime[act ? s : 0];
+    const double p = T.p[sp], pinv = T.pinv[sp];
+    const double* __restrict__ tw = T.tw_inv + (size_t)sp * kN;
+    double x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = 0.0;
+    if (act) {
+      const double* col = src + z * A.src_zs + y * A.src_ys + (long long)s * kN + (long long)(c0 + cl) * 16;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = col[4096 * k + j];
+      col_inv_hi(x, j, tw, p, pinv);
+    }
+    double* R = Y + sigma * kYStride;
+    col_b_to_a(x, R, j);
+    if (act) col_inv_lo(x, tw, C.inv_n0[s], C.inv_n1[s], p, pinv);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) D[sigma * kYStride + j + 16 * k] = act ? digit_word(reduce(x[k], p, pinv)) : 0ULL;
+    // phase 1b: Z's columns on slots 0 and 1 (one wave), Z P^-1 centered into run cl of Z
+    if (sigma < 2) {
+      const int zp = C.dst_prime[nt];
+      const double pz = T.p[zp], pzinv = T.pinv[zp];
+      const double* __restrict__ twz = T.tw_inv + (size_t)zp * kN;
+      const double* col = A.zsrc + z * A.src_zs + y * A.src_ys + (long long)(c0 + cl) * 16;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = col[4096 * k + j];
+      col_inv_hi(x, j, twz, pz, pzinv);
+      double* RZ = Z + cl * kYStride;
+      col_b_to_a(x, RZ, j);
+      col_inv_lo(x, twz, C.z_n0, C.z_n1, pz, pzinv);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) RZ[j + 16 * k] = reduce(x[k], pz, pzinv);
+    }
+  }
+  __syncthreads();
+  // phase 1c: r for the 512 coefficients of the two columns, two per thread
+  {
+    const int zp = C.dst_prime[nt];
+    const double pz = T.p[zp], pzinv = T.pinv[zp];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int q = t + 256 * u, cl = q >> 8, pos = q & 255;
+      double acc = 0.0;
+      for (int s = 0; s < ns; ++s)  // |y_s| < 2^49: |term| <= p, the sum within 8 p
+        acc += mulc(undigit(D[(2 * s + cl) * kYStride + pos]), C.hmod[s][nt], pz);
+      // |Z - acc| <= p + 2 once acc is reduced: reduce() returns the exact centered residue
+      const double v = Z[cl * kYStride + pos] - reduce(acc, pz, pzinv);
+      Z[cl * kYStride + pos] = reduce(v, pz, pzinv);
+    }
+  }
+  __syncthreads();
+  // phase 2: as cols_mconv_body, r added to every conversion sum
+  const int w = t >> 6, g = (t >> 4) & 3;
+  const int cl = w >> 1, h = w & 1;
+  const uint8_t* __restrict__ dig = T.conv_dig + C.dig_off;
+  const uint64_t* B0 = D + (4 * g + cl) * kYStride + j;      // source 2 g, column cl
+  const uint64_t* B1 = D + (4 * g + 2 + cl) * kYStride + j;  // source 2 g + 1
+  const double* RZ = Z + cl * kYStride + j;
+  double* RX = (SEPX ? X : Y) + sigma * kYStride;
+  double* dbase = dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
+  for (int base = 0; base < nt; base += kMPass) {
+    const int ta = base + (4 * h + (j >> 2)) * kMItems + (j & 3);
+    const bool arow = (j & 3) < kMItems && ta < nt;
+    v4i av[kConvDigits];
+#pragma unroll
+    for (int c = 0; c < kConvDigits; ++c)
+      av[c] = arow ? *reinterpret_cast<const v4i*>(dig + ((size_t)ta * kConvDigits + c) * 64 + 16 * g) : v4i{0, 0, 0, 0};
+    int to[kMItems];
+    double p[kMItems], pinv[kMItems];
+#pragma unroll
+    for (int r = 0; r < kMItems; ++r) {
+      to[r] = base + (4 * h + g) * kMItems + r;
+      const int tp = C.dst_prime[to[r] < nt ? to[r] : 0];
+      p[r] = T.p[tp];
+      pinv[r] = T.pinv[tp];
+    }
+    double x[kMItems][16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const uint64_t w0 = B0[16 * k], w1 = B1[16 * k];
+      const double rz = RZ[16 * k];
+      const v4i bv = {(int)(uint32_t)w0, (int)(uint32_t)(w0 >> 32), (int)(uint32_t)w1, (int)(uint32_t)(w1 >> 32)};
+      v4i acc[kConvDigits];
+#pragma unroll
+      for (int c = 0; c < kConvDigits; ++c)
+        acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[c], bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < kMItems; ++r) {
+        x[r][k] = mconv_fold_add(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
+                                 acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
+                                 acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], rz, p[r], pinv[r]);
+        asm volatile("" : "+v"(x[r][k]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!SEPX) __syncthreads();
+#pragma unroll
+    for (int r = 0; r < kMItems; ++r) {
+      const bool act = to[r] < nt;
+      const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? to[r] : 0] * kN;
+      if (act) col_fwd_lo<true>(x[r], tw, p[r], pinv[r]);
+      col_a_to_b(x[r], RX, j);
+      if (act) {
+        col_fwd_hi(x[r], j, tw, p[r], pinv[r]);
+        double* col = dbase + (long long)C.dst_slot[to[r]] * kN;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) col[4096 * k + j] = x[r][k];
+      }
+    }
+  }
+}
+
+template <bool SEPX>
+__global__ __launch_bounds__(kT, 2) void k_ks_cols_mconv_rs(const ConvArgs A, DevTables T) {
+  __shared__ double Y[16 * kYStride];
+  __shared__ double X[SEPX ? 16 * kYStride : 1];
+  __shared__ double Z[2 * kYStride];
+  cols_mconv_rs_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, Z, T);
 }
 
 // Launches a ModUp / ModDown conversion (grid (128, groups, items)) on the engine the context
@@ -908,12 +1066,26 @@ __device__ __forceinline__ void rows_ip_body(const uint64_t* __restrict__ d, lon
     }
     return;
   }
-  // P limb: INTT rows of both components, stored to the workspace for the ModDown cols kernel
+  // P limb: INTT rows of both components, stored to the workspace for the ModDown cols kernel.
+  // ACCP holds tiles / 16 limbs per component from e0 on: the K special limbs, or (ModDown fused
+  // with the rescale, e0 = ell - 1) the q_{ell-1} limb first, as Z = P * acc + IP.
+  const int k1 = tiles >> 4;
+  if (e < ell && acc_b) {
+    double ab[16], aa[16];
+    load_gal(ab, acc_b + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+    load_gal(aa, acc_a + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+    const TwPair pm = T.pmodq[pi];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      sb[k] = reduce(sb[k] + mulc(ab[k], pm, p), p, pinv);
+      sa[k] = reduce(sa[k] + mulc(aa[k], pm, p), p, pinv);
+    }
+  }
   const double* __restrict__ twi = T.tw_inv + (size_t)pi * kN;
-  double* o = accp + ((long long)b * 2 * K + (e - ell)) * kN;
+  double* o = accp + ((long long)b * 2 * k1 + (e - e0)) * kN;
   __syncthreads();  // the inner product's reads of S are done before the exchanges rewrite it
   rows_inv_to_t(sb, o, rg, S, twi, p, pinv);
-  rows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, p, pinv);
+  rows_inv_to_t(sa, o + (long long)k1 * kN, rg, S, twi, p, pinv);
 }
 
 __global__ __launch_bounds__(kT, 2) void k_ks_rows_ip(const uint64_t* __restrict__ d, long long d_stride, const GalF G,
@@ -966,12 +1138,28 @@ __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], co
   for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
 }
 
+// ipq_finish of the ModDown fused with the rescale: ip <- (ip P^-1 - NTT rows(v) + acc) q_{ell-1}^-1.
+__device__ __forceinline__ void ipq_finish_rs(double (&ip)[16], double (&x)[16], const double* __restrict__ next,
+                                              const uint64_t* __restrict__ acc_limb, uint64_t* __restrict__ o,
+                                              long long na, int rg, double* S, const double* TW, TwPair pinv_P,
+                                              TwPair ql_inv, double p, double pinv) {
+  rows_fwd_lds(x, S, TW, p, pinv);
+  if (next) load_t(x, next, rg);
+  double ad[16];
+  load_gal(ad, acc_limb, na, 1u);
+#pragma unroll
+  for (int k = 0; k < 16; ++k)  // |ip P^-1| <= p, |v| <= 3.9 p, acc < p: |.| <= 6 p
+    ip[k] = mulc(mulc(ip[k], pinv_P, p) - S[s_out(k)] + ad[k], ql_inv, p);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
+}
+
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
 // Tile = (row group, Q limb i): the inner product of limb i (as in K3) is combined with the NTT rows
 // pass v of the ModDown conversion T4 right away, so the Q-limb inner product never goes to HBM:
 //   out_b = (IP_b - v_b) * P^-1 + sigma_g(add) (+ acc_b),   out_a = (IP_a - v_a) * P^-1 (+ acc_a),
 // canonical u64.
-template <bool HOIST = false>
+template <bool HOIST = false, bool RS = false>
 __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, long long d_stride, const GalF& G,
                                               const double* __restrict__ t2, const KeyPtrsF& keys, int ell, int beta,
                                               int batch, const double* __restrict__ t4,
@@ -982,8 +1170,9 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
                                               const LevelConsts* __restrict__ lc, const DevTables& T, int lin,
                                               double* S, double* TW, int koff = 0,
                                               HoistSrc H = HoistSrc{nullptr, 1, 0}) {
+  const int nq = RS ? ell - 1 : ell;  // output limbs (the rescale drops q_{ell-1})
   const TileId id = decode_tile(batch, lin);
-  if (id.tile >= 16 * ell) return;
+  if (id.tile >= 16 * nq) return;
   const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
   const uint32_t g = gal_of(G, koff + b);
   const double p = T.p[i], pinv = T.pinv[i];
@@ -993,13 +1182,22 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
     tw_store(st, TW);
     __syncthreads();
   }
-  const double* v_b = t4 + ((long long)b * 2 * ell + i) * kN;
-  const double* v_a = v_b + (long long)ell * kN;
+  const double* v_b = t4 + ((long long)b * 2 * nq + i) * kN;
+  const double* v_a = v_b + (long long)nq * kN;
   double sb[16], sa[16], x[16];
   tile_ip<HOIST>(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T, true,
                  H);
   const long long na = nat_a(rg);
   const TwPair pinv_P = lc->p_inv[i];
+  if constexpr (RS) {
+    // out = (IP P^-1 - v + acc) q_{ell-1}^-1, v = NTT rows of (conv P^-1 + r)
+    const TwPair ql_inv = lc->qlast_inv[i];
+    ipq_finish_rs(sb, x, v_a, acc_b + (long long)b * acc_stride + (long long)i * kN,
+                  out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv);
+    ipq_finish_rs(sa, x, nullptr, acc_a + (long long)b * acc_stride + (long long)i * kN,
+                  out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv);
+    return;
+  }
   ipq_finish(sb, x, v_a, add ? add + (long long)hoist_input<HOIST>(H, b) * add_stride + (long long)i * kN : nullptr, g,
              acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
              out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, p, pinv);
@@ -1077,6 +1275,22 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq(const uint64_t* __restric
   __shared__ double TW[kTwLds];
   rows_ipq_body(d, d_stride, G, t2, keys, ell, beta, batch, t4, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
                 out_stride, lc, T, blockIdx.x, S, TW);
+}
+
+// K5 of the relinearisation fused with the rescale: Q limbs 0 .. ell - 2 (ipq_finish_rs).
+__global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq_rs(const uint64_t* __restrict__ d, long long d_stride,
+                                                       const GalF G, const double* __restrict__ t2, KeyPtrsF keys,
+                                                       int ell, int beta,
+                                                       int batch, const double* __restrict__ t4,
+                                                       const uint64_t* __restrict__ acc_b,
+                                                       const uint64_t* __restrict__ acc_a, long long acc_stride,
+                                                       uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
+                                                       long long out_stride, const LevelConsts* __restrict__ lc,
+                                                       DevTables T) {
+  __shared__ double S[kRowLds];
+  __shared__ double TW[kTwLds];
+  rows_ipq_body<false, true>(d, d_stride, G, t2, keys, ell, beta, batch, t4, nullptr, 0, acc_b, acc_a,
+                             acc_stride, out_b, out_a, out_stride, lc, T, blockIdx.x, S, TW);
 }
 
 // K5 of hoisted rotations: as k_ks_rows_ipq with the digits and inputs of HoistSrc.
@@ -1378,6 +1592,63 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
     k_ks_rows_ipq<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, t4,
                                                              add, add_stride, acc_b, acc_a, acc_stride, out_b,
                                                              out_a, out_stride, c->d_level + ell, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
+
+size_t ks_rs_bytes(const hck_context* c, int ell, int batch) {
+  const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
+  return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * (c->K + 1));
+}
+
+int ks_relin_rescale(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
+                     const uint64_t* const* ksk, const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride,
+                     uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws, hipStream_t s) {
+  if (c->wide || c->conv_engine != 1 || ell < 2) return HCK_ERR_UNSUPPORTED;
+  if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
+  if (batch < 1 || batch > kMaxBatchF || !acc_b || !acc_a) return HCK_ERR_ARG;
+  const GalF G = gal_uniform(1u);
+  const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K, nq = ell - 1;
+  const long long n = kN;
+  double* r1 = (double*)ws;
+  double* t2 = r1 + (long long)batch * 2 * ell * n;
+  double* accp = t2 + (long long)batch * beta * ext_l * n;  // [batch][2][K + 1]: q_{ell-1}, then P
+  const int last_digit = ell - c->alpha * (beta - 1);
+  KeyPtrsF kp{};
+  for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
+  // K1, K2 as in ks_fused
+  k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0,
+                                                                                    r1, ell, batch, c->dev);
+  HCK_CHECK_LAUNCH();
+  launch_conv(c,
+              ConvArgs{r1, (long long)ell * n, 0, c->alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                       modup_consts(c, ell, 0), 1},
+              dim3(128, beta, batch), ext_l - last_digit, s);
+  HCK_CHECK_LAUNCH();
+  // K3 over q_{ell-1} and the K special limbs
+  {
+    const int tiles = 16 * (K + 1), groups = (tiles + kXcds - 1) / kXcds;
+    k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, tiles,
+                                                            ell - 1, accp, nullptr, 0, nullptr, nullptr, 0, acc_b,
+                                                            acc_a, acc_stride, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
+  // K4: ModDown + rescale conversion to the ell - 1 lower limbs; T4 reuses R1
+  double* t4 = r1;
+  {
+    const ConvArgs A{accp + n, 2LL * (K + 1) * n, (long long)(K + 1) * n, 0, t4, 2LL * nq * n, (long long)nq * n,
+                     c->d_mdrs + ell, 0, accp};
+    if (nq <= kMPass) k_ks_cols_mconv_rs<false><<<dim3(128, 2, batch), kT, 0, s>>>(A, c->dev);
+    else k_ks_cols_mconv_rs<true><<<dim3(128, 2, batch), kT, 0, s>>>(A, c->dev);
+    HCK_CHECK_LAUNCH();
+  }
+  // K5: Q limbs 0 .. ell - 2
+  {
+    const int tiles = 16 * nq, groups = (tiles + kXcds - 1) / kXcds;
+    k_ks_rows_ipq_rs<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, t4,
+                                                                acc_b, acc_a, acc_stride, out_b, out_a, out_stride,
+                                                                c->d_level + ell, c->dev);
     HCK_CHECK_LAUNCH();
   }
   return HCK_OK;

@@ -170,6 +170,72 @@ extern "C" int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch,
   return HCK_OK;
 }
 
+// The product rescaled: on the matrix-core conversion engine the relinearisation's ModDown and the
+// rescale share one pass (ks_relin_rescale); otherwise hck_mul_relin into the workspace, then the
+// rescale.  Both give the same residues.
+static bool relin_rescale_fused(const hck_context* ctx, int ell) {
+  return !ctx->wide && ctx->conv_engine == 1 && ell >= 2 && ctx->alpha <= hck::kMaxAlpha && ctx->K <= hck::kMaxSpecial;
+}
+
+extern "C" size_t hck_mul_relin_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch) {
+  if (!hck::valid_level(ctx, level_limbs) || level_limbs < 2 || batch < 0) return 0;
+  const int chunk = batch < hck::kMaxBatchM ? batch : hck::kMaxBatchM;
+  const size_t poly = (size_t)level_limbs * hck::kN * 8;
+  if (relin_rescale_fused(ctx, level_limbs)) return hck::ks_rs_bytes(ctx, level_limbs, chunk) + 3 * chunk * poly;
+  const size_t ks = hck::ks_fused_bytes(ctx, level_limbs, chunk), rs = hck::rescale_bytes(ctx, level_limbs, 2 * chunk);
+  return (ks > rs ? ks : rs) + 5 * chunk * poly;
+}
+
+extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                                     const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
+                                     int64_t b_stride, const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1,
+                                     int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!hck::valid_level(ctx, level_limbs) || level_limbs < 2 || batch < 0) return HCK_ERR_ARG;
+  if (!a0 || !a1 || !b0 || !b1 || !relin_ksk || !out0 || !out1 || out0 == out1) return HCK_ERR_ARG;
+  if (batch == 0) return HCK_OK;
+  if (!workspace || workspace_bytes < hck_mul_relin_rescale_workspace_bytes(ctx, level_limbs, batch))
+    return HCK_ERR_WORKSPACE;
+  const int ell = level_limbs;
+  const bool fused = relin_rescale_fused(ctx, ell);
+  const int chunk = batch < hck::kMaxBatchM ? batch : hck::kMaxBatchM;
+  const long long poly = (long long)ell * hck::kN;
+  const size_t ks_bytes = fused ? hck::ks_rs_bytes(ctx, ell, chunk) : [&] {
+    const size_t ks = hck::ks_fused_bytes(ctx, ell, chunk), rs = hck::rescale_bytes(ctx, ell, 2 * chunk);
+    return ks > rs ? ks : rs;
+  }();
+  char* ks_ws = (char*)workspace;
+  uint64_t* d = (uint64_t*)(ks_ws + ks_bytes);  // [3][chunk][ell][N], then (unfused) [2][chunk][ell][N]
+  const uint64_t* keys[hck::kMaxBatchM];
+  for (int b = 0; b < chunk; ++b) keys[b] = relin_ksk;
+  hipStream_t s = (hipStream_t)stream;
+  for (int i0 = 0; i0 < batch; i0 += chunk) {
+    const int nb = batch - i0 < chunk ? batch - i0 : chunk;
+    uint64_t* d0 = d;
+    uint64_t* d1 = d + (long long)chunk * poly;
+    uint64_t* d2 = d + 2LL * chunk * poly;
+    int rc = hck::launch_tensor(ctx, ell, nb, a0 + (long long)i0 * a_stride, a1 + (long long)i0 * a_stride, a_stride,
+                                b0 + (long long)i0 * b_stride, b1 + (long long)i0 * b_stride, b_stride, d0, d1, d2,
+                                poly, s);
+    if (rc) return rc;
+    const long long oi = (long long)i0 * out_stride;
+    if (fused) {
+      rc = hck::ks_relin_rescale(ctx, ell, nb, d2, poly, keys, d0, d1, poly, out0 + oi, out1 + oi, out_stride, ks_ws,
+                                 s);
+      if (rc) return rc;
+      continue;
+    }
+    uint64_t* mid = d + 3LL * chunk * poly;  // [2][nb][ell][N]: the relinearised product
+    rc = hck::ks_fused(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, mid, mid + (long long)nb * poly,
+                       poly, ks_ws, s);
+    if (rc) return rc;
+    rc = hck::rescale_fused(ctx, ell, nb, mid, poly, out0 + oi, out_stride, ks_ws, s);
+    if (rc) return rc;
+    rc = hck::rescale_fused(ctx, ell, nb, mid + (long long)nb * poly, poly, out1 + oi, out_stride, ks_ws, s);
+    if (rc) return rc;
+  }
+  return HCK_OK;
+}
+
 extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int groups, const uint64_t* in,
                                 int64_t in_stride, const uint64_t* weights, uint64_t* out, int64_t out_stride,
                                 void* stream) {

@@ -606,7 +606,7 @@ class CipherOps:
 
     def mul(self, a, b):
         f = self._fhe
-        return f.rescale(f.homo_mul_relin(a, b, self.ctx), self.ctx)
+        return f.homo_mul_relin_rescale(a, b, self.ctx)
 
     def mul_sum(self, a, b, sizes):
         """Products a_i * b_i summed over consecutive groups of ``sizes`` items: the tensor products

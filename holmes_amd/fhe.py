@@ -53,6 +53,7 @@ __all__ = [
     "homo_mul_no_relin",
     "homo_relinearize",
     "homo_mul_relin",
+    "homo_mul_relin_rescale",
     "homo_mul_relin_rescale_postop",
     "grouped_scalar_weighted_acc",
     "cipher_batch_item",
@@ -845,15 +846,27 @@ def homo_mul_relin(a: Cipher, b: Cipher, ctx: CKKSContext) -> Cipher:
     return a.cipher_like([both[0], both[1]], state=_product_state(a, b, limbs))
 
 
+def homo_mul_relin_rescale(a: Cipher, b: Cipher, ctx: CKKSContext) -> Cipher:
+    """rescale(homo_mul_relin(a, b)) in one native call (hck_mul_relin_rescale: the relinearisation's
+    ModDown and the rescale share one conversion pass), the same residues and state."""
+
+    limbs, (a0, a1), (b0, b1) = _mul_operands(a, b)
+    if limbs < 2:
+        raise ValueError("rescale needs a non-extended ciphertext with at least two limbs")
+    both = ctx.mul_relin_rescale_raw(a0, a1, b0, b1, limbs, _relin_key(ctx), stacked=True)
+    st = _product_state(a, b, limbs)
+    state = st.replace(cur_limbs=limbs - 1, scale_degree=max(1, int(st.scale_degree) - 1),
+                       scaling_factor=float(st.scaling_factor) / float(ctx.rescale_divisor_at(limbs)))
+    return a.cipher_like([both[0], both[1]], state=state)
+
+
 def homo_mul_relin_rescale_postop(lhs: Cipher, rhs: Cipher, ctx: CKKSContext, apply_double: bool = False,
                                   sub: Cipher | None = None, scalar: EncodedScalar | None = None) -> Cipher:
     """rescale(lhs * rhs) (relinearised), then x 2 when ``apply_double``, minus ``sub`` (dropped to
     the result's level), plus the encoded ``scalar``: the Chebyshev step T_{a+b} = 2 T_a T_b -
     T_{|a-b|} (llama3fhe/operators/nonlinear/polynomial.py:140-190)."""
 
-    prod = homo_mul_relin(lhs, rhs, ctx)
-    out = rescale(prod, ctx)
-    prod.release()
+    out = homo_mul_relin_rescale(lhs, rhs, ctx)
     if apply_double:
         doubled = homo_add(out, out, ctx)
         out.release()

@@ -177,7 +177,7 @@ class FeatureMajorMLPBlock:
         ctx, spec = self.ctx, self.spec
         s = eval_chebyshev(g, self.silu, ctx, interval=spec.silu_interval)
         u = fhe.align_to(u, u.state.replace(cur_limbs=int(s.state.cur_limbs)), ctx)
-        return fhe.rescale(fhe.homo_mul_relin(s, u, ctx), ctx)
+        return fhe.homo_mul_relin_rescale(s, u, ctx)
 
     def _paired(self, y, mark):
         """The reference's paired carrier: one complex gate + i up projection per page."""

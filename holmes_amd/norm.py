@@ -90,7 +90,7 @@ def rmsnorm_fhe(input_ciphers, weight: np.ndarray | None = None, *, coeffs: dict
     sched: dict = {}
     t0 = time.perf_counter()
     x = fhe.pack_cipher_batch(cts)
-    sq = fhe.rescale(fhe.homo_mul_relin(x, x, ctx), ctx)
+    sq = fhe.homo_mul_relin_rescale(x, x, ctx)
     times["square"] = time.perf_counter() - t0
     t0 = time.perf_counter()
     s = _fold(sq, layout, ctx)
@@ -103,7 +103,7 @@ def rmsnorm_fhe(input_ciphers, weight: np.ndarray | None = None, *, coeffs: dict
     sched["rsqrt_output_limbs"] = int(r.state.cur_limbs)
     t0 = time.perf_counter()
     xr = fhe.align_to(x, x.state.replace(cur_limbs=int(r.state.cur_limbs)), ctx)
-    y = fhe.rescale(fhe.homo_mul_relin(xr, r, ctx), ctx)
+    y = fhe.homo_mul_relin_rescale(xr, r, ctx)
     if weight is not None:
         w = np.asarray(weight, dtype=np.float64).reshape(-1)
         if w.shape != (int(layout.hidden_dim),):

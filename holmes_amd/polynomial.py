@@ -145,7 +145,7 @@ class PSEvaluator:
         a, b = self.adjust(a, l), self.adjust(b, l)
         if self.sim:
             return l - 1
-        return self._fix(fhe.rescale(fhe.homo_mul_relin(a, b, self.ctx), self.ctx), l - 1)
+        return self._fix(fhe.homo_mul_relin_rescale(a, b, self.ctx), l - 1)
 
     def add(self, a, b):
         l = min(self.lv(a), self.lv(b))
@@ -164,8 +164,8 @@ class PSEvaluator:
         return x
 
     def mul_many(self, pairs) -> list:
-        """Products of several operand pairs as one batched product + relinearisation and one
-        rescale, every operand first brought to the lowest level among them."""
+        """Products of several operand pairs (relinearised and rescaled), every operand first brought
+        to the lowest level among them; small batches go as one batched call."""
 
         if len(pairs) == 1 or self.sim:
             return [self.mul(a, b) for a, b in pairs]
@@ -174,15 +174,17 @@ class PSEvaluator:
             raise ValueError("EvalMod ran out of levels")
         ops = [(self.adjust(a, l), self.adjust(b, l)) for a, b in pairs]
         B = ops[0][0].batch_size
+        if B >= 16:  # a launch sequence per pair is already large: no operand copies
+            return [self._fix(fhe.homo_mul_relin_rescale(a, b, self.ctx), l - 1) for a, b in ops]
         side = [[u64_cat([pr[k].cv[c][:, :l] for pr in ops]) for c in range(2)] for k in range(2)]
-        both = self.ctx.mul_relin_raw(side[0][0], side[0][1], side[1][0], side[1][1], l, self.ctx.relin_key,
-                                      stacked=True)
+        both = self.ctx.mul_relin_rescale_raw(side[0][0], side[0][1], side[1][0], side[1][1], l, self.ctx.relin_key,
+                                              stacked=True)
         x0 = ops[0][0]
         n = len(ops) * B
-        prod = x0.cipher_like([both[0], both[1]], batch_size=n,
-                              state=x0.state.replace(cur_limbs=l, scale_degree=2,
-                                                     scaling_factor=self.canon[l] * self.canon[l]))
-        r = self._fix(fhe.rescale(prod, self.ctx), l - 1)
+        r = self._fix(x0.cipher_like([both[0], both[1]], batch_size=n,
+                                     state=x0.state.replace(cur_limbs=l - 1, scale_degree=1,
+                                                            scaling_factor=self.canon[l] * self.canon[l]
+                                                            / float(self.ctx.rescale_divisor_at(l)))), l - 1)
         return [r.cipher_like([c[i * B:(i + 1) * B] for c in r.cv], batch_size=B) for i in range(len(ops))]
 
     def _finish_double(self, p, sub=None):

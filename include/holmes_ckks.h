@@ -31,6 +31,8 @@
  *                          fhe.homo_mul_no_relin / homo_relinearize / homo_mul_relin
  *                          (llama3fhe/operators/attention/prefill/qk.py:460-464,
  *                          attention/kernel_helpers.py:146-152, nonlinear/polynomial.py:140-190)
+ *   hck_mul_relin_rescale  the multiply-relinearise-rescale of fhe.homo_mul_relin_rescale_postop
+ *                          (nonlinear/polynomial.py:140-150)
  *   hck_weighted_sum       fhe.grouped_scalar_weighted_acc (nonlinear/polynomial.py:256-300)
  */
 #ifndef HOLMES_CKKS_H
@@ -311,6 +313,18 @@ int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch, const uint
                   int64_t a_stride, const uint64_t* b0, const uint64_t* b1, int64_t b_stride,
                   const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride, void* workspace,
                   size_t workspace_bytes, void* stream);
+
+/* Ciphertext x ciphertext product, relinearised and rescaled: outputs at level_limbs - 1 limbs
+ * (level_limbs >= 2), the residues of hck_mul_relin followed by hck_rescale, bit for bit.  The
+ * multiply-relinearise-rescale core of EasyFHE's fhe.homo_mul_relin_rescale_postop
+ * (llama3fhe/operators/nonlinear/polynomial.py:140-150), its post-ops left to the caller.  On the
+ * matrix-core conversion engine the ModDown and the rescale share one conversion pass (the
+ * q_{level-1} limb joins the P limbs as a source); otherwise it runs the two steps. */
+size_t hck_mul_relin_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
+int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                          const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
+                          int64_t b_stride, const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1,
+                          int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
 
 /* Grouped scalar-weighted sum over one component of n inputs (item stride in_stride, [limbs][N]
  * each): out[g] = sum_j weights[g][j][l] * in[j] (mod q_l); weights is a device array

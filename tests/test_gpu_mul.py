@@ -122,6 +122,38 @@ def test_mul_relin_every_level(env):
         assert np.array_equal(_host(o0)[0], w0) and np.array_equal(_host(o1)[0], w1), f"{ell} limbs"
 
 
+@pytest.mark.parametrize("engine", ["mfma", "valu"])
+def test_mul_relin_rescale_equals_product_then_rescale(env, engine):
+    """hck_mul_relin_rescale (the ModDown fused with the rescale on the matrix-core engine, the two
+    steps on the FP64 one) gives the residues of hck_mul_relin followed by hck_rescale at every
+    level, batch 3, and the oracle's product-then-rescale at three levels."""
+    _, _, ctx, _ = env
+    ctx.set_conversion_engine(engine)
+    try:
+        check_mul_relin_rescale(env, range(2, ctx.L + 1), (2, 9, ctx.L))
+    finally:
+        ctx.set_conversion_engine("mfma")
+
+
+def check_mul_relin_rescale(env, levels, oracle_levels, batch=3):
+    fhe, client, ctx, orc = env
+    rlk = orc.make_ksk(*client.relin_key_inputs())
+    for ell in levels:
+        rng = np.random.default_rng(700 + ell)
+        a0, a1, b0, b1 = (_dev(_rand(ctx, rng, batch, ell)) for _ in range(4))
+        f0, f1 = ctx.mul_relin_rescale_raw(a0, a1, b0, b1, ell, ctx.relin_key)
+        p0, p1 = ctx.mul_relin_raw(a0, a1, b0, b1, ell, ctx.relin_key)
+        w0, w1 = ctx.rescale_raw(p0, ell), ctx.rescale_raw(p1, ell)
+        assert f0.shape == (batch, ell - 1, ctx.N)
+        assert torch.equal(f0, w0) and torch.equal(f1, w1), f"{ell} limbs"
+        if ell in oracle_levels:
+            h0, h1 = _host(f0), _host(f1)
+            for b in range(batch):
+                m0, m1 = orc.mul_relin(ell, *(_host(x)[b] for x in (a0, a1, b0, b1)), rlk)
+                assert np.array_equal(h0[b], orc.rescale(ell, m0)), (ell, b)
+                assert np.array_equal(h1[b], orc.rescale(ell, m1)), (ell, b)
+
+
 def test_relinearize_of_tensor_equals_mul_relin(env):
     fhe, client, ctx, orc = env
     rng = np.random.default_rng(5)

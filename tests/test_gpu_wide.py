@@ -161,6 +161,11 @@ def test_mul_relin(env, ell):
     M.test_mul_relin_bit_exact(env, ell)
 
 
+@pytest.mark.parametrize("ell", [38, 2])
+def test_mul_relin_rescale(env, ell):
+    M.check_mul_relin_rescale(env, [ell], [ell], batch=2)
+
+
 def test_lincomb(env):
     M.test_lincomb_matches_oracle(env)
 
