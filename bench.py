@@ -600,7 +600,8 @@ class _CallLog:
 def run_bootstrap(args) -> int:
     """Full-slot bootstrap of one ciphertext at 3 limbs (holmes_amd.bootstrap, the
     easyfhe.bs.openfhe surface): ModRaise, CoeffToSlot (3 merged BSGS stages), EvalMod (degree-48
-    Chebyshev + 3 double angles on the real and imaginary parts), SlotToCoeff (3 stages)."""
+    Chebyshev + 3 double angles on the real and imaginary parts), SlotToCoeff (3 stages).
+    ``graph_replay_ms`` times the same bootstrap replayed as one HIP graph (``RefreshGraph``)."""
 
     import math
 
@@ -641,6 +642,18 @@ def run_bootstrap(args) -> int:
     ms_wall = (time.perf_counter() - w0) * 1e3 / args.steps
     ms = ev0.elapsed_time(ev1) / args.steps
     err = float(np.max(np.abs(client.decrypt(out) - v)))
+    # the same bootstrap replayed as one HIP graph (RefreshGraph), reported beside the eager value
+    graph = B.RefreshGraph(ctx, prog, ct, iterations=1)
+    for _ in range(args.warmup):
+        gout = graph(ct)
+    torch.cuda.synchronize()
+    g0 = time.perf_counter()
+    for _ in range(args.steps):
+        gout = graph(ct)
+    torch.cuda.synchronize()
+    ms_graph = (time.perf_counter() - g0) * 1e3 / args.steps
+    if any(not torch.equal(a, b) for a, b in zip(gout.cv, out.cv)):
+        raise RuntimeError("the graph replay differs from the eager bootstrap")
     ks_items = sum(b for _, b, _ in ks)
     cpu = None
     if not args.no_cpu:
@@ -672,7 +685,7 @@ def run_bootstrap(args) -> int:
                                "%d double angles, message ratio 2^-%d, sparse ternary h=192"
                                % (prog.output_limbs, bspec.cheb_degree, bspec.double_angle, bspec.message_ratio_bits),
                    "max_error_bits": round(-math.log2(err), 2), "key_switched_items": ks_items,
-                   "algorithmic_bytes_per_step": bs_bytes},
+                   "algorithmic_bytes_per_step": bs_bytes, "graph_replay_ms": round(ms_graph, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "whole bootstrap (key switches, MACs, rescales, elementwise)", "ms_per_launch": round(ms, 3)},

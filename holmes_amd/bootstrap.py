@@ -56,7 +56,7 @@ from .polynomial import _baby_size, canonical_scales, chebyshev_divide  # noqa: 
 __all__ = ["STRATEGIES", "BootstrapSpec", "BootstrapProgram", "Requirements", "Stage", "requirements", "generate", "bootstrap",
            "special_fft_layers", "merge_layers", "chebyshev_divide", "canonical_scales", "evalmod_levels",
            "evalmod_coefficients", "make_stage", "plan_stages", "plan_program", "stage_rows", "apply_stage",
-           "apply_stages", "bootstrap_with_correction"]
+           "apply_stages", "bootstrap_with_correction", "RefreshGraph"]
 
 
 # ---------------------------------------------------------------------------- spec / requirements
@@ -730,3 +730,56 @@ def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: Boo
         return out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(cipher.state.scaling_factor)))
     except ValueError:
         return first
+
+
+# ---------------------------------------------------------------------------- graph replay
+class RefreshGraph:
+    """``bootstrap_with_correction`` of one input shape (batch, limbs, scale) captured once as a HIP
+    graph and replayed.  A refresh of one or two ciphertexts is some 330 launches per pass with host
+    work between them; replayed, they reach the GPU as one graph launch.
+
+    The graph reads its input from a static buffer (``__call__`` copies the ciphertext in on the
+    current stream) and writes the same output tensors on every replay (``__call__`` returns
+    copies).  Capture needs warm caches, so the constructor first runs the refresh once eagerly.
+    Every device tensor the captured kernels read outside the graph's own memory pool -- the
+    context's workspace, its resident tables and keys, the program's encoded stage diagonals -- is
+    referenced here, so that no cache eviction frees it while the graph exists; a graph is bound to
+    the context and program it was captured with."""
+
+    def __init__(self, ctx: CKKSContext, program: BootstrapProgram, like: Cipher, *, iterations: int = 2,
+                 precision_bits: int = 12, bound_bits: int = 0):
+        if like.is_ext or len(like.cv) != 2:
+            raise ValueError("a refresh graph takes a two-component, non-extended ciphertext")
+        self.ctx, self.program = ctx, program
+        self.batch, self.limbs = int(like.batch_size), int(like.state.cur_limbs)
+        self.state = like.state
+        self._kw = dict(iterations=int(iterations), precision_bits=int(precision_bits), bound_bits=int(bound_bits))
+        self._in = [ctx.empty(self.batch, self.limbs, ctx.N) for _ in range(2)]
+        self._load(like)
+        src = like.cipher_like(list(self._in), batch_size=self.batch, state=like.state)
+        bootstrap_with_correction(src, ctx, program, **self._kw)  # warms every cache the refresh reads
+        torch.cuda.synchronize()
+        self._graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self._graph):
+            self._out = bootstrap_with_correction(src, ctx, program, **self._kw)
+        torch.cuda.synchronize()
+        self._pins = (ctx._ws, list(ctx.__dict__.get("_resident", {}).values()), list(ctx.rotation_keys.values()),
+                      ctx.relin_key, [list(st.cache.values()) for st in program.cts + program.stc])
+
+    def _load(self, ct: Cipher) -> None:
+        for dst, src in zip(self._in, ct.cv):
+            dst.view(torch.int64).copy_(src[:, :self.limbs].view(torch.int64))
+
+    def __call__(self, ct: Cipher) -> Cipher:
+        st = ct.state
+        if (ct.is_ext or len(ct.cv) != 2 or int(ct.batch_size) != self.batch or int(st.cur_limbs) != self.limbs
+                or int(st.scale_degree) != int(self.state.scale_degree)
+                or float(st.scaling_factor) != float(self.state.scaling_factor)):
+            raise ValueError(f"this refresh graph takes {self.batch} ciphertexts at {self.limbs} limbs and scale "
+                             f"{self.state.scaling_factor}")
+        self._load(ct)
+        self._graph.replay()
+        out = [self.ctx.empty(*c.shape) for c in self._out.cv]
+        for o, c in zip(out, self._out.cv):
+            o.view(torch.int64).copy_(c.view(torch.int64))
+        return self._out.cipher_like(out, batch_size=self.batch, state=self._out.state)

@@ -182,6 +182,27 @@ def test_two_pass_correction(env):
     assert e2 < 2.0**-20 and e2 < e1 / 64
 
 
+@pytest.mark.parametrize("iterations", [2, 1])
+def test_refresh_graph_replays_equal_eager(env, iterations):
+    """A refresh captured as one HIP graph: every replay, with eager refreshes and other kernels
+    between the replays, gives the eager result bit for bit, for two different inputs in turn."""
+    B, fhe, client, ctx, prog = env
+    rng = np.random.default_rng(40 + iterations)
+    cts = [client.encrypt(_slots(rng, ctx.max_slots), cur_limbs=3) for _ in range(2)]
+    graph = B.RefreshGraph(ctx, prog, cts[0], iterations=iterations)
+    for rep in range(3):
+        for ct in cts:
+            got = graph(ct)
+            want = B.bootstrap_with_correction(ct, ctx, prog, iterations=iterations)
+            fhe.homo_add(want, want, ctx)  # other eager work between replays
+            torch.cuda.synchronize()
+            assert got.state.cur_limbs == want.state.cur_limbs
+            for a, b in zip(got.cv, want.cv):
+                assert torch.equal(a[:, :want.state.cur_limbs], b[:, :want.state.cur_limbs]), rep
+    with pytest.raises(ValueError):
+        graph(client.encrypt(_slots(rng, ctx.max_slots), cur_limbs=4))
+
+
 def test_batched_bootstrap_equals_single_ones(env):
     # every kernel of the pipeline works per item, so a batch refreshes bit-identically
     B, fhe, client, ctx, prog = env
