@@ -50,6 +50,9 @@ SIGNATURES = {
     "hck_rotate_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_rotate": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _vp, _i64,
                         _vp, _sz, _vp]),
+    "hck_rotate_rescale_workspace_bytes": (_sz, [_vp, _i, _i]),
+    "hck_rotate_rescale": (_i, [_vp, _i, _i, _u32, _vp, _vp, _i64, ctypes.POINTER(_vp), _vp, _vp, _i64, _vp, _sz,
+                                _vp]),
     "hck_rescale_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_rescale": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
     "hck_poly_op": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i64, _i64, _i64, _i, _ip, _u64p, _vp]),

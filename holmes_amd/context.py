@@ -346,6 +346,32 @@ class CKKSContext:
                      _stream_ptr(self.device)), name)
         return out0, out1
 
+    def rotate_rescale_raw(self, c0: torch.Tensor, c1: torch.Tensor, limbs: int, galois: int, keys):
+        """``rotate_raw`` by one Galois element followed by the rescale, in one native call (the same
+        residues): outputs [batch][limbs - 1][N]."""
+
+        self._check_poly(c0, limbs, self.N)
+        self._check_poly(c1, limbs, self.N)
+        if limbs < 2:
+            raise ValueError("a rescaled rotation needs at least two limbs")
+        if _bstride(c0) != _bstride(c1):
+            raise ValueError("c0 and c1 need the same batch stride")
+        B = c0.shape[0]
+        if isinstance(keys, torch.Tensor):
+            keys = [keys] * B
+        if len(keys) != B:
+            raise ValueError("one key per batch item")
+        for k in keys:
+            self._check_key(k)
+        out0, out1 = self.empty(B, limbs - 1, self.N), self.empty(B, limbs - 1, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_rotate_rescale_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_rotate_rescale(self._h, limbs, B, int(galois), c0.data_ptr(), c1.data_ptr(), _bstride(c0),
+                                       nat.ptr_array([k.data_ptr() for k in keys]), out0.data_ptr(), out1.data_ptr(),
+                                       (limbs - 1) * self.N, ws.data_ptr(), ws.numel(), _stream_ptr(self.device)),
+                  "hck_rotate_rescale")
+        return out0, out1
+
     def hoist_digits(self, c1: torch.Tensor, limbs: int) -> torch.Tensor:
         """The extended ModUp digits of every c1 ([inputs][limbs][N]) in the full NTT domain, as
         [inputs][beta][limbs + K][N] uint64 (hck_rotate_hoist_prepare): computed once, they serve

@@ -137,14 +137,16 @@ int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint3
                const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
                const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
                hipStream_t s);
-// Relinearisation fused with the rescale: out = rescale((acc_b, acc_a) + KeySwitch(d)) at ell - 1
-// limbs, bit-identical to ks_fused followed by rescale_fused; the q_{ell-1} limb joins the ModDown
-// sources (see ConvConsts::z_n0).  Matrix-core conversion engine, FP64 contexts, ell >= 2 only
-// (HCK_ERR_UNSUPPORTED otherwise).  Workspace ks_rs_bytes.
+// ks_fused followed by rescale_fused in one pass: out = rescale((sigma(add) + acc_b, acc_a) +
+// KeySwitch(sigma(d))) at ell - 1 limbs, bit-identical to the two steps; the q_{ell-1} limb joins
+// the ModDown sources (see ConvConsts::z_n0).  add and the acc pair are nullable (relinearisation:
+// acc = (d0, d1); rotation: add = c0).  Matrix-core conversion engine, FP64 contexts, ell >= 2
+// only (HCK_ERR_UNSUPPORTED otherwise).  Workspace ks_rs_bytes.
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch);
-int ks_relin_rescale(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
-                     const uint64_t* const* ksk, const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride,
-                     uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws, hipStream_t s);
+int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+                const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+                const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
+                char* ws, hipStream_t s);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

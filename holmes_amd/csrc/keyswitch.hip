@@ -109,6 +109,65 @@ extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, ui
                      out0, out1, out_stride, workspace, workspace_bytes, stream, false);
 }
 
+// Rotation followed by the rescale: on the matrix-core conversion engine one pass (ks_rescaled, the
+// rotation's ModDown and the rescale share the conversion), otherwise the rotation into the
+// workspace and then the rescale.  Both give the same residues.
+static bool rotate_rescale_fused(const hck_context* ctx, int ell) {
+  return !ctx->wide && ctx->conv_engine == 1 && ell >= 2;
+}
+
+static size_t rotate_rescale_ks_bytes(const hck_context* ctx, int ell, int chunk) {
+  if (rotate_rescale_fused(ctx, ell)) return hck::ks_rs_bytes(ctx, ell, chunk);
+  const size_t ks = hck::ks_fused_bytes(ctx, ell, chunk), rs = hck::rescale_bytes(ctx, ell, chunk);
+  return ks > rs ? ks : rs;
+}
+
+extern "C" size_t hck_rotate_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch) {
+  if (!ctx || level_limbs < 2 || level_limbs > ctx->L || batch < 0) return 0;
+  const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
+  const size_t mid = rotate_rescale_fused(ctx, level_limbs) ? 0 : (size_t)2 * chunk * level_limbs * hck::kN * 8;
+  return rotate_rescale_ks_bytes(ctx, level_limbs, chunk) + mid;
+}
+
+extern "C" int hck_rotate_rescale(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
+                                  const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
+                                  const uint64_t* const* ksk, uint64_t* out0, uint64_t* out1, int64_t out_stride,
+                                  void* workspace, size_t workspace_bytes, void* stream) {
+  if (!ctx || !c0 || !c1 || !ksk || !out0 || !out1 || batch < 0) return HCK_ERR_ARG;
+  if (level_limbs < 2 || level_limbs > ctx->L || !galois_ok(galois)) return HCK_ERR_ARG;
+  if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1 || out0 == out1) return HCK_ERR_ARG;
+  if (batch == 0) return HCK_OK;
+  for (int b = 0; b < batch; ++b) if (!ksk[b]) return HCK_ERR_ARG;
+  if (!workspace || workspace_bytes < hck_rotate_rescale_workspace_bytes(ctx, level_limbs, batch))
+    return HCK_ERR_WORKSPACE;
+  const int ell = level_limbs;
+  const int chunk = batch < hck::kMaxBatch ? batch : hck::kMaxBatch;
+  const bool fused = rotate_rescale_fused(ctx, ell);
+  char* ks_ws = (char*)workspace;
+  uint64_t* mid = (uint64_t*)(ks_ws + rotate_rescale_ks_bytes(ctx, ell, chunk));  // [2][chunk][ell][N] (unfused)
+  const long long poly = (long long)ell * hck::kN;
+  hipStream_t s = (hipStream_t)stream;
+  for (int b0 = 0; b0 < batch; b0 += chunk) {
+    const int nb = batch - b0 < chunk ? batch - b0 : chunk;
+    const long long ii = (long long)b0 * in_stride, oi = (long long)b0 * out_stride;
+    int rc;
+    if (fused) {
+      rc = hck::ks_rescaled(ctx, ell, nb, c1 + ii, in_stride, galois, ksk + b0, c0 + ii, in_stride, nullptr, nullptr,
+                            0, out0 + oi, out1 + oi, out_stride, ks_ws, s);
+      if (rc) return rc;
+      continue;
+    }
+    rc = hck::ks_fused(ctx, ell, nb, c1 + ii, in_stride, galois, ksk + b0, c0 + ii, in_stride, nullptr, nullptr, 0,
+                       mid, mid + (long long)nb * poly, poly, ks_ws, s);
+    if (rc) return rc;
+    rc = hck::rescale_fused(ctx, ell, nb, mid, poly, out0 + oi, out_stride, ks_ws, s);
+    if (rc) return rc;
+    rc = hck::rescale_fused(ctx, ell, nb, mid + (long long)nb * poly, poly, out1 + oi, out_stride, ks_ws, s);
+    if (rc) return rc;
+  }
+  return HCK_OK;
+}
+
 extern "C" int hck_rotate_many(const hck_context* ctx, int level_limbs, int batch, const uint32_t* galois,
                                const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
                                const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,

@@ -1070,16 +1070,24 @@ __device__ __forceinline__ void rows_ip_body(const uint64_t* __restrict__ d, lon
   // ACCP holds tiles / 16 limbs per component from e0 on: the K special limbs, or (ModDown fused
   // with the rescale, e0 = ell - 1) the q_{ell-1} limb first, as Z = P * acc + IP.
   const int k1 = tiles >> 4;
-  if (e < ell && acc_b) {
-    double ab[16], aa[16];
-    load_gal(ab, acc_b + (long long)b * acc_stride + (long long)e * kN, na, 1u);
-    load_gal(aa, acc_a + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+  if (e < ell && (add || acc_b)) {  // Z = IP + P (sigma(add) + acc): |sb| <= p/2 + 1 + 3 p before the reduction
     const TwPair pm = T.pmodq[pi];
+    double t[16];
+    if (add) {
+      load_gal(t, add + (long long)hoist_input<HOIST>(H, b) * add_stride + (long long)e * kN, na, g);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      sb[k] = reduce(sb[k] + mulc(ab[k], pm, p), p, pinv);
-      sa[k] = reduce(sa[k] + mulc(aa[k], pm, p), p, pinv);
+      for (int k = 0; k < 16; ++k) sb[k] += mulc(t[k], pm, p);
     }
+    if (acc_b) {
+      load_gal(t, acc_b + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sb[k] += mulc(t[k], pm, p);
+      load_gal(t, acc_a + (long long)b * acc_stride + (long long)e * kN, na, 1u);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sa[k] += mulc(t[k], pm, p);
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
   }
   const double* __restrict__ twi = T.tw_inv + (size_t)pi * kN;
   double* o = accp + ((long long)b * 2 * k1 + (e - e0)) * kN;
@@ -1138,20 +1146,30 @@ __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], co
   for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
 }
 
-// ipq_finish of the ModDown fused with the rescale: ip <- (ip P^-1 - NTT rows(v) + acc) q_{ell-1}^-1.
+// ipq_finish of the ModDown fused with the rescale:
+//   ip <- (ip P^-1 - NTT rows(v) + sigma_g(add) + acc) q_{ell-1}^-1   (add, acc nullable).
 __device__ __forceinline__ void ipq_finish_rs(double (&ip)[16], double (&x)[16], const double* __restrict__ next,
+                                              const uint64_t* __restrict__ add_limb, uint32_t g,
                                               const uint64_t* __restrict__ acc_limb, uint64_t* __restrict__ o,
                                               long long na, int rg, double* S, const double* TW, TwPair pinv_P,
                                               TwPair ql_inv, double p, double pinv) {
   rows_fwd_lds(x, S, TW, p, pinv);
   if (next) load_t(x, next, rg);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) ip[k] = mulc(ip[k], pinv_P, p) - S[s_out(k)];  // |.| <= p + 3.9 p
   double ad[16];
-  load_gal(ad, acc_limb, na, 1u);
+  if (add_limb) {
+    load_gal(ad, add_limb, na, g);
 #pragma unroll
-  for (int k = 0; k < 16; ++k)  // |ip P^-1| <= p, |v| <= 3.9 p, acc < p: |.| <= 6 p
-    ip[k] = mulc(mulc(ip[k], pinv_P, p) - S[s_out(k)] + ad[k], ql_inv, p);
+    for (int k = 0; k < 16; ++k) ip[k] += ad[k];
+  }
+  if (acc_limb) {
+    load_gal(ad, acc_limb, na, 1u);
 #pragma unroll
-  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
+    for (int k = 0; k < 16; ++k) ip[k] += ad[k];  // |.| <= 6.9 p
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(ip[k], ql_inv, p), p, pinv));
 }
 
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
@@ -1190,11 +1208,12 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
   const long long na = nat_a(rg);
   const TwPair pinv_P = lc->p_inv[i];
   if constexpr (RS) {
-    // out = (IP P^-1 - v + acc) q_{ell-1}^-1, v = NTT rows of (conv P^-1 + r)
+    // out = (IP P^-1 - v + sigma(add) + acc) q_{ell-1}^-1, v = NTT rows of (conv P^-1 + r)
     const TwPair ql_inv = lc->qlast_inv[i];
-    ipq_finish_rs(sb, x, v_a, acc_b + (long long)b * acc_stride + (long long)i * kN,
+    ipq_finish_rs(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
+                  acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
                   out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv);
-    ipq_finish_rs(sa, x, nullptr, acc_a + (long long)b * acc_stride + (long long)i * kN,
+    ipq_finish_rs(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
                   out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv);
     return;
   }
@@ -1282,6 +1301,7 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq_rs(const uint64_t* __rest
                                                        const GalF G, const double* __restrict__ t2, KeyPtrsF keys,
                                                        int ell, int beta,
                                                        int batch, const double* __restrict__ t4,
+                                                       const uint64_t* __restrict__ add, long long add_stride,
                                                        const uint64_t* __restrict__ acc_b,
                                                        const uint64_t* __restrict__ acc_a, long long acc_stride,
                                                        uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
@@ -1289,7 +1309,7 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq_rs(const uint64_t* __rest
                                                        DevTables T) {
   __shared__ double S[kRowLds];
   __shared__ double TW[kTwLds];
-  rows_ipq_body<false, true>(d, d_stride, G, t2, keys, ell, beta, batch, t4, nullptr, 0, acc_b, acc_a,
+  rows_ipq_body<false, true>(d, d_stride, G, t2, keys, ell, beta, batch, t4, add, add_stride, acc_b, acc_a,
                              acc_stride, out_b, out_a, out_stride, lc, T, blockIdx.x, S, TW);
 }
 
@@ -1602,13 +1622,14 @@ size_t ks_rs_bytes(const hck_context* c, int ell, int batch) {
   return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * (c->K + 1));
 }
 
-int ks_relin_rescale(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
-                     const uint64_t* const* ksk, const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride,
-                     uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws, hipStream_t s) {
+int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+                const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+                const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
+                char* ws, hipStream_t s) {
   if (c->wide || c->conv_engine != 1 || ell < 2) return HCK_ERR_UNSUPPORTED;
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
-  if (batch < 1 || batch > kMaxBatchF || !acc_b || !acc_a) return HCK_ERR_ARG;
-  const GalF G = gal_uniform(1u);
+  if (batch < 1 || batch > kMaxBatchF || (acc_b == nullptr) != (acc_a == nullptr)) return HCK_ERR_ARG;
+  const GalF G = gal_uniform(galois);
   const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K, nq = ell - 1;
   const long long n = kN;
   double* r1 = (double*)ws;
@@ -1630,7 +1651,7 @@ int ks_relin_rescale(const hck_context* c, int ell, int batch, const uint64_t* d
   {
     const int tiles = 16 * (K + 1), groups = (tiles + kXcds - 1) / kXcds;
     k_ks_rows_ip<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, tiles,
-                                                            ell - 1, accp, nullptr, 0, nullptr, nullptr, 0, acc_b,
+                                                            ell - 1, accp, add, add_stride, nullptr, nullptr, 0, acc_b,
                                                             acc_a, acc_stride, c->dev);
     HCK_CHECK_LAUNCH();
   }
@@ -1647,8 +1668,8 @@ int ks_relin_rescale(const hck_context* c, int ell, int batch, const uint64_t* d
   {
     const int tiles = 16 * nq, groups = (tiles + kXcds - 1) / kXcds;
     k_ks_rows_ipq_rs<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, t4,
-                                                                acc_b, acc_a, acc_stride, out_b, out_a, out_stride,
-                                                                c->d_level + ell, c->dev);
+                                                                add, add_stride, acc_b, acc_a, acc_stride, out_b,
+                                                                out_a, out_stride, c->d_level + ell, c->dev);
     HCK_CHECK_LAUNCH();
   }
   return HCK_OK;

@@ -171,7 +171,7 @@ extern "C" int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch,
 }
 
 // The product rescaled: on the matrix-core conversion engine the relinearisation's ModDown and the
-// rescale share one pass (ks_relin_rescale); otherwise hck_mul_relin into the workspace, then the
+// rescale share one pass (ks_rescaled); otherwise hck_mul_relin into the workspace, then the
 // rescale.  Both give the same residues.
 static bool relin_rescale_fused(const hck_context* ctx, int ell) {
   return !ctx->wide && ctx->conv_engine == 1 && ell >= 2 && ctx->alpha <= hck::kMaxAlpha && ctx->K <= hck::kMaxSpecial;
@@ -219,8 +219,8 @@ extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, in
     if (rc) return rc;
     const long long oi = (long long)i0 * out_stride;
     if (fused) {
-      rc = hck::ks_relin_rescale(ctx, ell, nb, d2, poly, keys, d0, d1, poly, out0 + oi, out1 + oi, out_stride, ks_ws,
-                                 s);
+      rc = hck::ks_rescaled(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, out0 + oi, out1 + oi,
+                            out_stride, ks_ws, s);
       if (rc) return rc;
       continue;
     }

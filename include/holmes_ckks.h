@@ -31,6 +31,7 @@
  *                          fhe.homo_mul_no_relin / homo_relinearize / homo_mul_relin
  *                          (llama3fhe/operators/attention/prefill/qk.py:460-464,
  *                          attention/kernel_helpers.py:146-152, nonlinear/polynomial.py:140-190)
+ *   hck_rotate_rescale     fhe.homo_rotate followed by fhe.rescale (operator.py:446-453, 387-394)
  *   hck_mul_relin_rescale  the multiply-relinearise-rescale of fhe.homo_mul_relin_rescale_postop
  *                          (nonlinear/polynomial.py:140-150)
  *   hck_weighted_sum       fhe.grouped_scalar_weighted_acc (nonlinear/polynomial.py:256-300)
@@ -118,6 +119,15 @@ int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galo
                const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
                int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                void* workspace, size_t workspace_bytes, void* stream);
+
+/* Rotation followed by the rescale (C1's unit: INTT, automorphism, key switch, NTT, rescale):
+ * outputs at level_limbs - 1 limbs (level_limbs >= 2), the residues of hck_rotate followed by
+ * hck_rescale, bit for bit; fhe.homo_rotate then fhe.rescale (operator.py:446-453, 387-394).  On
+ * the matrix-core conversion engine the ModDown and the rescale share one conversion pass. */
+size_t hck_rotate_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
+int hck_rotate_rescale(const hck_context* ctx, int level_limbs, int batch, uint32_t galois, const uint64_t* c0,
+                       const uint64_t* c1, int64_t in_stride, const uint64_t* const* ksk, uint64_t* out0,
+                       uint64_t* out1, int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
 
 /* hck_rotate without a workspace argument, for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No counterpart in the

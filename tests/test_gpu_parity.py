@@ -269,6 +269,39 @@ def test_rotate_matches_oracle(env):
     assert np.array_equal(_host(r0)[0], orc.rescale(ell, w0))
 
 
+@pytest.mark.parametrize("engine", ["mfma", "valu"])
+def test_rotate_rescale_equals_rotation_then_rescale(env, engine):
+    """hck_rotate_rescale (one pass on the matrix-core engine, two steps on the FP64 one) gives the
+    residues of hck_rotate followed by hck_rescale at every level (batch 3, one rotation amount),
+    and the oracle's rotation-then-rescale at 24, 9 and 2 limbs (config C1's unit)."""
+    _, client, ctx, orc = env
+    ctx.set_conversion_engine(engine)
+    try:
+        check_rotate_rescale((None, client, ctx, orc), range(2, ctx.L + 1), (2, 9, ctx.L))
+    finally:
+        ctx.set_conversion_engine("mfma")
+
+
+def check_rotate_rescale(env, levels, oracle_levels, batch=3, rot=1):
+    _, client, ctx, orc = env
+    g = ctx.galois_element(rot)
+    gk, ok = _key_pair(client, ctx, orc, g)
+    for ell in levels:
+        rng = np.random.default_rng(900 + ell)
+        c0, c1 = _dev(_rand(ctx, rng, batch, ell)), _dev(_rand(ctx, rng, batch, ell))
+        f0, f1 = ctx.rotate_rescale_raw(c0, c1, ell, g, gk)
+        o0, o1 = ctx.rotate_raw(c0, c1, ell, g, gk)
+        w0, w1 = ctx.rescale_raw(o0, ell), ctx.rescale_raw(o1, ell)
+        assert f0.shape == (batch, ell - 1, ctx.N)
+        assert torch.equal(f0, w0) and torch.equal(f1, w1), f"{ell} limbs"
+        if ell in oracle_levels:
+            h0, h1, hc0, hc1 = _host(f0), _host(f1), _host(c0), _host(c1)
+            for b in range(batch):
+                r0, r1 = orc.rotate(ell, g, hc0[b], hc1[b], ok)
+                assert np.array_equal(h0[b], orc.rescale(ell, r0)), (ell, b)
+                assert np.array_equal(h1[b], orc.rescale(ell, r1)), (ell, b)
+
+
 @pytest.mark.parametrize("ell,rot", [(20, 128), (9, -3), (3, 4096)])
 def test_rotate_accumulate_batch_matches_oracle(env, ell, rot):
     """Batched rotation with a shared key and the fused addends: out = rot(c) + acc, written over

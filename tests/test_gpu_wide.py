@@ -162,6 +162,11 @@ def test_mul_relin(env, ell):
 
 
 @pytest.mark.parametrize("ell", [38, 2])
+def test_rotate_rescale(env, ell):
+    G.check_rotate_rescale(env, [ell], [ell], batch=2, rot=5)
+
+
+@pytest.mark.parametrize("ell", [38, 2])
 def test_mul_relin_rescale(env, ell):
     M.check_mul_relin_rescale(env, [ell], [ell], batch=2)
 
