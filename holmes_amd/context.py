@@ -681,6 +681,47 @@ class CKKSContext:
                                             nat.ptr_array(optr[g0:g1]), _stream_ptr(self.device)), "hck_lincomb")
         return outs
 
+    def lincomb_rescale(self, xs, limbs: int, outs, weights: torch.Tensor, add=None, add_groups=()) -> None:
+        """outs[g] = rescale(sum_t w[t] * xs[g][t]) from ``limbs`` to ``limbs - 1`` limbs, plus the
+        residues ``add`` (``limbs - 1`` canonical values) on the groups listed in ``add_groups``
+        (hck_lincomb_rescale: the combination is never stored).  ``xs`` as for ``lincomb`` (at least
+        ``limbs`` limbs each), ``outs`` [limbs - 1][N] polynomials, ``weights`` a [terms][limbs]
+        uint64 GPU table."""
+
+        G = len(xs)
+        if G != len(outs) or G < 1:
+            raise ValueError("one output per group")
+        if limbs < 2:
+            raise ValueError("a rescaled combination needs at least two limbs")
+        T = len(xs[0])
+        if T > 256:
+            raise ValueError("at most 256 terms per linear combination")
+        ptrs = []
+        for row in xs:
+            if len(row) != T:
+                raise ValueError("every group needs the same number of terms")
+            for t in row:
+                self._check_single(t, limbs, "lincomb input")
+                ptrs.append(t.data_ptr())
+        for o in outs:
+            self._check_single(o, limbs - 1, "lincomb output")
+        if (weights.dtype != torch.uint64 or tuple(weights.shape) != (T, limbs) or not weights.is_contiguous()
+                or weights.device.type != "cuda"):
+            raise ValueError(f"weights must be a contiguous [{T}][{limbs}] uint64 GPU table")
+        addv = None if add is None else nat.u64_array([int(v) for v in list(add)[:limbs - 1]])
+        groups_with_add = {int(g) for g in add_groups}
+        per = max(1, min(64, 256 // T))
+        optr = [o.data_ptr() for o in outs]
+        L = nat.lib()
+        stream = _stream_ptr(self.device)
+        for g0 in range(0, G, per):
+            g1 = min(G, g0 + per)
+            mask = sum(1 << (g - g0) for g in range(g0, g1) if g in groups_with_add)
+            ws = self.workspace(L.hck_lincomb_rescale_workspace_bytes(self._h, limbs, g1 - g0))
+            nat.check(L.hck_lincomb_rescale(self._h, int(limbs), g1 - g0, T, nat.ptr_array(ptrs[g0 * T:g1 * T]),
+                                            weights.data_ptr(), nat.ptr_array(optr[g0:g1]), addv, mask,
+                                            ws.data_ptr(), ws.numel(), stream), "hck_lincomb_rescale")
+
     def lincomb_ptrs(self, in_ptrs, limbs: int, out_ptrs, terms: int) -> None:
         """``lincomb`` with unit weights on raw device addresses: ``in_ptrs`` holds ``terms``
         addresses per group (group-major), ``out_ptrs`` one per group, each a [>= limbs][N] uint64

@@ -156,6 +156,16 @@ int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, lo
 size_t rescale_bytes(const hck_context* c, int ell, int polys);
 int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                   long long out_stride, char* ws, hipStream_t s);
+// out[g] = rescale(sum_t w[t][.] x[g * terms + t]) from ell to ell - 1 limbs, plus the residues
+// add[i] on the groups whose bit is set in add_mask (add nullable); w a device [terms][ell] table.
+// groups <= 64, groups * terms <= 256.  FP64 contexts (HCK_ERR_UNSUPPORTED on a wide one).
+// Workspace lincomb_rescale_bytes.
+constexpr int kLcRsPtrs = 256;
+constexpr int kLcRsGroups = 64;
+size_t lincomb_rescale_bytes(const hck_context* c, int ell, int groups);
+int lincomb_rescale(const hck_context* c, int ell, int groups, int terms, const uint64_t* const* x,
+                    const uint64_t* w, uint64_t* const* out, const uint64_t* add, uint64_t add_mask, char* ws,
+                    hipStream_t s);
 // ModRaise of polys from one limb (q_0) to `to` limbs: the centered lift of limb 0's coefficients,
 // reduced modulo q_1 .. q_{to-1} and transformed; limb 0 is copied.  Workspace: polys * to limbs.
 size_t modraise_bytes(const hck_context* c, int to, int polys);

@@ -1874,6 +1874,103 @@ int rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, 
   return HCK_OK;
 }
 
+// ----------------------------------------------------------------- linear combination + rescale
+// out[g] = rescale(sum_t w[t] x[g][t]) (+ the residues add[] on the groups of add_mask), the
+// Paterson-Stockmeyer step "c0 + sum c_j T_j, rescaled": the combination is formed in the two
+// kernels that read it (the last limb's INTT rows, and the finish over the other limbs), so it is
+// never stored.  The residues equal hck_lincomb followed by hck_rescale and a scalar add.
+struct LcRsArgs {
+  const uint64_t* x[kLcRsPtrs];  // group-major: x[g * terms + t], limb i at x + i N
+  uint64_t* out[kLcRsGroups];    // limb i < ell - 1 at out + i N
+  uint64_t add[kMaxPrimes];      // per output limb
+};
+
+// the combination of limb `limb` of group g's terms for row group rg, natural layout (reduced to
+// within p/2 + 1): weights w[t][limb] ([terms][ell]), reduced every 7 terms (|acc| < 8 p)
+__device__ __forceinline__ void lc_tile(double (&acc)[16], const LcRsArgs& A, int g, int terms,
+                                        const uint64_t* __restrict__ w, int ell, int limb, long long na, double p,
+                                        double pinv) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0.0;
+  for (int t = 0; t < terms; ++t) {
+    const uint64_t* xl = A.x[g * terms + t] + (long long)limb * kN + na;
+    const double wt = u2d(w[(long long)t * ell + limb]);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] += mulv(u2d(xl[16 * k]), wt, p, pinv);  // |term| <= 0.875 p
+    if (t % 7 == 6) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[k] = reduce(acc[k], p, pinv);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = reduce(acc[k], p, pinv);
+}
+
+// INTT rows of the combination's last limb (ell - 1) of every group, to the workspace layout.
+// Grid (16, groups).
+__global__ __launch_bounds__(kT) void k_lc_intt_last(const LcRsArgs A, int terms, const uint64_t* __restrict__ w,
+                                                     int ell, double* __restrict__ tl, DevTables T) {
+  __shared__ double S[kRowLds];
+  const int rg = blockIdx.x, g = blockIdx.y, pi = ell - 1;
+  const double p = T.p[pi], pinv = T.pinv[pi];
+  double x[16];
+  lc_tile(x, A, g, terms, w, ell, pi, nat_a(rg), p, pinv);
+  // lc_tile reads the natural layout; rows_inv_to_t takes the values in map N, which nat_a indexes
+  rows_inv_to_t(x, tl + (long long)g * kN, rg, S, T.tw_inv + (size_t)pi * kN, p, pinv);
+}
+
+// The finish: out[g][i] = (sum_t w[t][i] x[g][t][i] - NTT rows(T4[g][i])) q_{ell-1}^-1 (+ add[i]).
+// Grid (groups, 16, ell - 1).
+__global__ __launch_bounds__(kT) void k_lc_finish(const LcRsArgs A, int terms, const uint64_t* __restrict__ w,
+                                                  int ell, const double* __restrict__ t4, uint64_t add_mask,
+                                                  const TwPair* __restrict__ ql_inv, DevTables T) {
+  __shared__ double S[kRowLds];
+  const int g = blockIdx.x, rg = blockIdx.y, i = blockIdx.z, nt = ell - 1;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const long long na = nat_a(rg);
+  double a[16], x[16];
+  load_t(x, t4 + ((long long)g * nt + i) * kN, rg);
+  lc_tile(a, A, g, terms, w, ell, i, na, p, pinv);
+  rows_fwd_t(x, rg, S, T.tw_fwd + (size_t)i * kN, p, pinv);
+  const TwPair qi = ql_inv[i];
+  const double ad = ((add_mask >> g) & 1ull) ? u2d(A.add[i]) : 0.0;
+  uint64_t* o = A.out[g] + (long long)i * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(a[k] - x[k], qi, p) + ad, p, pinv));  // |a - x| <= 4.9 p
+}
+
+size_t lincomb_rescale_bytes(const hck_context* c, int ell, int groups) {
+  (void)c;
+  return (size_t)groups * kN * 8 * (size_t)ell;
+}
+
+int lincomb_rescale(const hck_context* c, int ell, int groups, int terms, const uint64_t* const* x,
+                    const uint64_t* w, uint64_t* const* out, const uint64_t* add, uint64_t add_mask, char* ws,
+                    hipStream_t s) {
+  if (c->wide) return HCK_ERR_UNSUPPORTED;
+  if (ell < 2 || groups < 1 || groups > kLcRsGroups || terms < 1 || groups * terms > kLcRsPtrs || !w)
+    return HCK_ERR_ARG;
+  LcRsArgs A{};
+  for (int j = 0; j < groups * terms; ++j) A.x[j] = x[j];
+  for (int g = 0; g < groups; ++g) A.out[g] = out[g];
+  for (int i = 0; i < ell - 1; ++i) A.add[i] = add ? add[i] : 0;
+  if (!add) add_mask = 0;
+  const long long n = kN;
+  double* tl = (double*)ws;                    // [groups][1] workspace layout
+  double* t4 = tl + (long long)groups * n;     // [groups][ell - 1] workspace layout
+  k_lc_intt_last<<<dim3(16, groups), kT, 0, s>>>(A, terms, w, ell, tl, c->dev);
+  HCK_CHECK_LAUNCH();
+  const int nt = ell - 1;
+  auto conv = nt <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
+  conv<<<dim3(128, 1, groups), kT, 0, s>>>(ConvArgs{tl, n, 0, 0, t4, (long long)nt * n, 0, c->d_rescale + ell, 0},
+                                           c->dev);
+  HCK_CHECK_LAUNCH();
+  k_lc_finish<<<dim3(groups, 16, nt), kT, 0, s>>>(A, terms, w, ell, t4, add_mask, (c->d_level + ell)->qlast_inv,
+                                                  c->dev);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
 size_t modraise_bytes(const hck_context* c, int to, int polys) {
   if (c->wide) return wide_modraise_bytes(c, to, polys);
   return (size_t)polys * kN * 8 * (size_t)to;

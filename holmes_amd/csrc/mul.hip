@@ -249,6 +249,52 @@ extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int gr
   return HCK_OK;
 }
 
+extern "C" size_t hck_lincomb_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int groups) {
+  if (!ctx || level_limbs < 2 || level_limbs > ctx->L || groups < 0) return 0;
+  if (!ctx->wide) return hck::lincomb_rescale_bytes(ctx, level_limbs, groups);
+  // the wide path runs the two steps: the combination [groups][ell][N], then one rescale at a time
+  return (size_t)groups * level_limbs * hck::kN * 8 + hck::rescale_bytes(ctx, level_limbs, 1);
+}
+
+extern "C" int hck_lincomb_rescale(const hck_context* ctx, int level_limbs, int groups, int terms,
+                                   const uint64_t* const* x, const uint64_t* weights, uint64_t* const* out,
+                                   const uint64_t* add, uint64_t add_mask, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  const int ell = level_limbs;
+  if (!ctx || !x || !out || !weights || ell < 2 || ell > ctx->L || groups < 0 || terms < 1) return HCK_ERR_ARG;
+  if (groups > hck::kLcRsGroups || (long long)groups * terms > hck::kLcRsPtrs) return HCK_ERR_ARG;
+  if (groups == 0) return HCK_OK;
+  for (int j = 0; j < groups * terms; ++j)
+    if (!x[j]) return HCK_ERR_ARG;
+  for (int g = 0; g < groups; ++g)
+    if (!out[g]) return HCK_ERR_ARG;
+  if (add)
+    for (int i = 0; i < ell - 1; ++i)
+      if (add[i] >= ctx->primes[i]) return HCK_ERR_ARG;
+  if (!workspace || workspace_bytes < hck_lincomb_rescale_workspace_bytes(ctx, ell, groups)) return HCK_ERR_WORKSPACE;
+  hipStream_t s = (hipStream_t)stream;
+  if (!ctx->wide)
+    return hck::lincomb_rescale(ctx, ell, groups, terms, x, weights, out, add, add_mask, (char*)workspace, s);
+  const long long poly = (long long)ell * hck::kN;
+  uint64_t* tmp = (uint64_t*)workspace;
+  char* rs_ws = (char*)(tmp + groups * poly);
+  uint64_t* tptr[hck::kLcRsGroups];
+  for (int g = 0; g < groups; ++g) tptr[g] = tmp + g * poly;
+  int rc = hck_lincomb(ctx, ell, groups, terms, x, weights, tptr, stream);
+  if (rc) return rc;
+  int prime_idx[hck::kMaxPrimes];
+  for (int i = 0; i < ell - 1; ++i) prime_idx[i] = i;
+  for (int g = 0; g < groups; ++g) {
+    rc = hck::rescale_fused(ctx, ell, 1, tptr[g], poly, out[g], (long long)(ell - 1) * hck::kN, rs_ws, s);
+    if (rc) return rc;
+    if (add && ((add_mask >> g) & 1ull)) {
+      rc = hck_poly_op(ctx, HCK_OP_ADD_SCALAR, out[g], out[g], nullptr, 1, 0, 0, 0, ell - 1, prime_idx, add, stream);
+      if (rc) return rc;
+    }
+  }
+  return HCK_OK;
+}
+
 extern "C" int hck_lincomb(const hck_context* ctx, int limbs, int groups, int terms, const uint64_t* const* x,
                            const uint64_t* weights, uint64_t* const* out, void* stream) {
   if (!ctx || !x || !out || limbs < 1 || limbs > ctx->L || groups < 0 || terms < 1) return HCK_ERR_ARG;

@@ -115,6 +115,21 @@ class PSEvaluator:
                     ctx.resident(np.asarray(weights, dtype=np.uint64)))
         return out
 
+    def _combine_rescale(self, terms, limbs: int, weights: np.ndarray, c0: float = 0.0) -> list:
+        """rescale(sum_t weights[t] * terms[t]) at ``limbs - 1`` limbs, plus c0 (encoded at that level's
+        canonical scale) on the c0 component: one hck_lincomb_rescale, the combination never stored."""
+
+        ctx = self.ctx
+        B = terms[0].batch_size
+        l = limbs - 1
+        out = fhe._alloc(ctx, 2, B, l)
+        xs = [[x.cv[c][b] for x in terms] for c in range(2) for b in range(B)]
+        add = None if c0 == 0.0 else [int(v) for v in self._residues(float(c0), l, self.canon[l])]
+        ctx.lincomb_rescale(xs, limbs, [out[c][b] for c in range(2) for b in range(B)],
+                            ctx.resident(np.asarray(weights, dtype=np.uint64)), add=add,
+                            add_groups=range(B) if add is not None else ())
+        return out
+
     def _residues(self, value: float, limbs: int, scaling_factor: float, integer: bool = False) -> np.ndarray:
         return fhe._scalar_residues(value, limbs, scaling_factor, integer, self.ctx)[0]
 
@@ -131,10 +146,10 @@ class PSEvaluator:
         if hit is not None and hit[0] is x:
             return hit[1]
         ratio = self.canon[l] * float(self.primes[l]) / self.canon[lx]
-        out = self._combine([x], l + 1, self._residues(1.0, l + 1, ratio)[None])
-        t = x.cipher_like(out, state=x.state.replace(cur_limbs=l + 1, scale_degree=2,
-                                                     scaling_factor=self.canon[l] * float(self.primes[l])))
-        y = self._fix(fhe.rescale(t, self.ctx), l)
+        out = self._combine_rescale([x], l + 1, self._residues(1.0, l + 1, ratio)[None])
+        y = self._fix(x.cipher_like(out, state=x.state.replace(
+            cur_limbs=l, scale_degree=1,
+            scaling_factor=self.canon[l] * float(self.primes[l]) / float(self.ctx.rescale_divisor_at(l + 1)))), l)
         self._adj[key] = (x, y)
         return y
 
@@ -206,7 +221,7 @@ class PSEvaluator:
     def lincomb(self, terms, c0: float, cap: int | None):
         """c0 + sum c_j x_j over ``terms`` = [(c_j, x_j)], rescaled once, at min(level) - 1 or ``cap``:
         each coefficient is encoded at the ratio that lands its term on the target scale, and the
-        terms are read at their own levels by one hck_lincomb launch."""
+        terms are read at their own levels by one hck_lincomb_rescale (c0 added in its last kernel)."""
 
         l = min(self.lv(x) for _, x in terms) - 1
         if cap is not None:
@@ -218,9 +233,9 @@ class PSEvaluator:
         target = self.canon[l] * float(self.primes[l])
         w = np.stack([self._residues(float(c), l + 1, target / self.canon[self.lv(x)]) for c, x in terms])
         x0 = terms[0][1]
-        acc = x0.cipher_like(self._combine([x for _, x in terms], l + 1, w),
-                             state=x0.state.replace(cur_limbs=l + 1, scale_degree=2, scaling_factor=target))
-        return self._add_const_inplace(self._fix(fhe.rescale(acc, self.ctx), l), c0)
+        out = self._combine_rescale([x for _, x in terms], l + 1, w, c0)
+        return self._fix(x0.cipher_like(out, state=x0.state.replace(
+            cur_limbs=l, scale_degree=1, scaling_factor=target / float(self.ctx.rescale_divisor_at(l + 1)))), l)
 
     # -- the series
     def evaluate(self, coeffs, cap: int | None = None):

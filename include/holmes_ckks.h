@@ -35,6 +35,8 @@
  *   hck_mul_relin_rescale  the multiply-relinearise-rescale of fhe.homo_mul_relin_rescale_postop
  *                          (nonlinear/polynomial.py:140-150)
  *   hck_weighted_sum       fhe.grouped_scalar_weighted_acc (nonlinear/polynomial.py:256-300)
+ *   hck_lincomb_rescale    the evaluator's weighted sum of basis terms followed by its rescale
+ *                          (nonlinear/polynomial.py:256-300)
  */
 #ifndef HOLMES_CKKS_H
 #define HOLMES_CKKS_H
@@ -353,6 +355,18 @@ int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int groups, const
  * llama3fhe/operators/pairfold_kv_cache.py:400-450) in one launch. */
 int hck_lincomb(const hck_context* ctx, int limbs, int groups, int terms, const uint64_t* const* x,
                 const uint64_t* weights, uint64_t* const* out, void* stream);
+
+/* A linear combination followed by the rescale: out[g] = rescale(sum_t w[t] * x[g * terms + t])
+ * from level_limbs to level_limbs - 1 limbs, plus the residues add[i] (level_limbs - 1 of them,
+ * canonical; add may be NULL) on the groups whose bit is set in add_mask; weights a device
+ * [terms][level_limbs] table.  groups <= 64, groups * terms <= 256; outputs must not be inputs.
+ * The residues of hck_lincomb, hck_rescale and an HCK_OP_ADD_SCALAR, without storing the
+ * combination: the Paterson-Stockmeyer step "c0 + sum c_j T_j, rescaled" of the reference's
+ * evaluator (llama3fhe/operators/nonlinear/polynomial.py:256-300 followed by its rescale). */
+size_t hck_lincomb_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int groups);
+int hck_lincomb_rescale(const hck_context* ctx, int level_limbs, int groups, int terms, const uint64_t* const* x,
+                        const uint64_t* weights, uint64_t* const* out, const uint64_t* add, uint64_t add_mask,
+                        void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

@@ -310,3 +310,39 @@ def test_lincomb_matches_oracle(env):
         assert np.array_equal(got[limbs:], first[g][limbs:])  # limbs above the count untouched
     with pytest.raises(ValueError):
         ctx.lincomb(srcs, limbs, outs[:2])
+
+
+@pytest.mark.parametrize("limbs,G,T", [(6, 3, 9), (24, 64, 4), (2, 5, 1)])
+def test_lincomb_rescale_matches_oracle(env, limbs, G, T):
+    check_lincomb_rescale(env, limbs, G, T)
+
+
+def check_lincomb_rescale(env, limbs, G, T):
+    """hck_lincomb_rescale: operands at different levels in separate allocations, weighted, a scalar
+    added on every other group; equal to hck_lincomb + hck_rescale + the scalar add on the GPU, and
+    to the oracle's weighted sum followed by its rescale."""
+    fhe, client, ctx, orc = env
+    from holmes_amd import _native as nat
+
+    rng = np.random.default_rng(1000 + limbs + G)
+    srcs = [[_dev(_rand(ctx, rng, 1, limbs + int(rng.integers(0, 3)))[0]) for _ in range(T)] for _ in range(G)]
+    w = np.stack([[rng.integers(0, ctx.primes[i], dtype=np.uint64) for i in range(limbs)] for _ in range(T)])
+    wd = torch.from_numpy(w).cuda()
+    add = [int(rng.integers(0, ctx.primes[i])) for i in range(limbs - 1)]
+    groups = range(0, G, 2)
+    outs = [ctx.empty(limbs - 1, ctx.N) for _ in range(G)]
+    ctx.lincomb_rescale(srcs, limbs, outs, wd, add=add, add_groups=groups)
+    acc = [ctx.empty(limbs, ctx.N) for _ in range(G)]
+    ctx.lincomb(srcs, limbs, acc, wd)
+    for g in range(G):
+        want = ctx.rescale_raw(acc[g][None], limbs)
+        if g in groups:
+            ctx.poly_op(nat.HCK_OP_ADD_SCALAR, want, want, prime_idx=ctx.q_prime_idx(limbs - 1), scalar=add)
+        assert torch.equal(outs[g], want[0]), f"group {g}"
+    for g in (0, G - 1):
+        x = np.stack([_host(t)[:limbs] for t in srcs[g]])
+        r = orc.rescale(limbs, orc.weighted_sum(limbs, x, w[None])[0])
+        if g in groups:
+            q = np.array(ctx.primes[:limbs - 1], dtype=object).reshape(-1, 1)
+            r = ((r.astype(object) + np.array(add, dtype=object).reshape(-1, 1)) % q).astype(np.uint64)
+        assert np.array_equal(_host(outs[g]), r), f"oracle group {g}"

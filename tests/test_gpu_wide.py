@@ -175,6 +175,11 @@ def test_lincomb(env):
     M.test_lincomb_matches_oracle(env)
 
 
+@pytest.mark.parametrize("limbs,G,T", [(38, 3, 5), (2, 2, 1)])
+def test_lincomb_rescale(env, limbs, G, T):
+    M.check_lincomb_rescale(env, limbs, G, T)
+
+
 @pytest.mark.parametrize("ni,nb,G_,limbs", [(3, 5, 6, 2), (2, 3, 2, 38), (5, 64, 2, 1)])
 def test_bsgs_mac(env, ni, nb, G_, limbs):
     _, _, ctx, orc = env
