@@ -512,8 +512,8 @@ class _Shape:
 
 class _CallLog:
     NAMES = ("keyswitch", "rotate_raw", "mul_relin_raw", "mul_relin_rescale_raw", "relinearize_raw", "bsgs_mac",
-             "rescale_raw", "modraise", "weighted_sum", "poly_op", "automorphism", "lincomb", "rotate_ext",
-             "rotate_ext_sum", "hoist_digits", "rotate_hoisted", "moddown")
+             "rescale_raw", "modraise", "weighted_sum", "poly_op", "automorphism", "lincomb", "lincomb_rescale",
+             "rotate_ext", "rotate_ext_sum", "hoist_digits", "rotate_hoisted", "rotate_rescale_raw", "moddown")
 
     def __init__(self, ctx):
         self.ctx = ctx
@@ -613,6 +613,13 @@ class _CallLog:
             elif name == "lincomb":
                 xs, l, outs = a[0], int(a[1]), a[2]
                 total += (sum(len(r) for r in xs) + len(outs)) * l
+            elif name == "lincomb_rescale":  # the terms in, the rescaled sums out
+                xs, l, outs = a[0], int(a[1]), a[2]
+                total += sum(len(r) for r in xs) * l + len(outs) * (l - 1)
+            elif name == "rotate_rescale_raw":
+                l, B = int(a[2]), int(a[0].shape[0])
+                total += B * (2 * l + 2 * (l - 1) + 2 * beta(l) * (l + K))
+                ks.append(("rotation", B, l))
         return total, ks
 
 
