@@ -89,6 +89,8 @@ SIGNATURES = {
     "hck_mul_relin": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
     "hck_mul_relin_rescale_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_mul_relin_rescale": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _vp, _vp, _i64, _vp, _sz, _vp]),
+    "hck_mul_relin_rescale_postop": (_i, [_vp, _i, _i, _vp, _vp, _i64, _vp, _vp, _i64, _vp, _i, _vp, _vp, _i64, _u64p,
+                                          _vp, _vp, _i64, _vp, _sz, _vp]),
     "hck_weighted_sum": (_i, [_vp, _i, _i, _i, _vp, _i64, _vp, _vp, _i64, _vp]),
     "hck_lincomb": (_i, [_vp, _i, _i, _i, ctypes.POINTER(_vp), _vp, ctypes.POINTER(_vp), _vp]),
     "hck_lincomb_rescale_workspace_bytes": (_sz, [_vp, _i, _i]),

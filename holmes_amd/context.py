@@ -608,6 +608,39 @@ class CKKSContext:
                                           _stream_ptr(self.device)), "hck_mul_relin_rescale")
         return out if stacked else (out[0], out[1])
 
+    def mul_relin_rescale_postop_raw(self, a0, a1, b0, b1, limbs: int, key: torch.Tensor, *, apply_double: bool = False,
+                                     sub: tuple | None = None, scalar=None):
+        """``mul_relin_rescale_raw`` then (apply_double ? 2 : 1) * product - sub (+ the ``limbs - 1``
+        canonical residues ``scalar`` on the c0 component) in the product's last kernel
+        (hck_mul_relin_rescale_postop): a [2][batch][limbs - 1][N] tensor.  ``sub`` is a (c0, c1)
+        pair of [batch][>= limbs - 1][N] tensors with one batch stride."""
+
+        self._check_key(key)
+        if limbs < 2:
+            raise ValueError("a rescaled product needs at least two limbs")
+        sa = self._pair(a0, a1, limbs, "mul lhs")
+        sb = self._pair(b0, b1, limbs, "mul rhs")
+        B = a0.shape[0]
+        if b0.shape[0] != B:
+            raise ValueError("mul operands need the same batch")
+        s0 = s1 = None
+        ss = 0
+        if sub is not None:
+            s0, s1 = sub
+            ss = self._pair(s0, s1, limbs - 1, "postop sub")
+            if s0.shape[0] != B:
+                raise ValueError("postop sub needs one row per product")
+        sc = None if scalar is None else nat.u64_array([int(v) for v in list(scalar)[:limbs - 1]])
+        out = self.empty(2, B, limbs - 1, self.N)
+        L = nat.lib()
+        ws = self.workspace(L.hck_mul_relin_rescale_workspace_bytes(self._h, limbs, B))
+        nat.check(L.hck_mul_relin_rescale_postop(
+            self._h, limbs, B, a0.data_ptr(), a1.data_ptr(), sa, b0.data_ptr(), b1.data_ptr(), sb, key.data_ptr(),
+            1 if apply_double else 0, s0.data_ptr() if s0 is not None else None,
+            s1.data_ptr() if s1 is not None else None, ss, sc, out[0].data_ptr(), out[1].data_ptr(),
+            (limbs - 1) * self.N, ws.data_ptr(), ws.numel(), _stream_ptr(self.device)), "hck_mul_relin_rescale_postop")
+        return out
+
     def resident(self, table: np.ndarray) -> torch.Tensor:
         """A small host table (residue weights, constants) on the device, uploaded once: a later
         call with the same bytes reuses the device copy, so repeated evaluations (every bootstrap's

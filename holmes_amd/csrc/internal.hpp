@@ -143,10 +143,14 @@ int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint3
 // acc = (d0, d1); rotation: add = c0).  Matrix-core conversion engine, FP64 contexts, ell >= 2
 // only (HCK_ERR_UNSUPPORTED otherwise).  Workspace ks_rs_bytes.
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch);
+// Post-ops on the ell - 1 output limbs: out <- (twice ? 2 out : out) - sub (+ scalar[i] on out_b);
+// sub_b / sub_a ([>= ell - 1] limbs per item at sub_stride) and scalar (ell - 1 canonical residues)
+// nullable.
 int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
-                char* ws, hipStream_t s);
+                char* ws, hipStream_t s, int twice = 0, const uint64_t* sub_b = nullptr,
+                const uint64_t* sub_a = nullptr, long long sub_stride = 0, const uint64_t* scalar = nullptr);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

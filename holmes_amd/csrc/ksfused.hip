@@ -1147,12 +1147,15 @@ __device__ __forceinline__ void ipq_finish(double (&ip)[16], double (&x)[16], co
 }
 
 // ipq_finish of the ModDown fused with the rescale:
-//   ip <- (ip P^-1 - NTT rows(v) + sigma_g(add) + acc) q_{ell-1}^-1   (add, acc nullable).
+//   r <- (ip P^-1 - NTT rows(v) + sigma_g(add) + acc) q_{ell-1}^-1   (add, acc nullable),
+// then the post-ops of RsPost: r <- (twice ? 2 r : r) - sub + scalar   (sub nullable, scalar 0).
 __device__ __forceinline__ void ipq_finish_rs(double (&ip)[16], double (&x)[16], const double* __restrict__ next,
                                               const uint64_t* __restrict__ add_limb, uint32_t g,
                                               const uint64_t* __restrict__ acc_limb, uint64_t* __restrict__ o,
                                               long long na, int rg, double* S, const double* TW, TwPair pinv_P,
-                                              TwPair ql_inv, double p, double pinv) {
+                                              TwPair ql_inv, double p, double pinv,
+                                              const uint64_t* __restrict__ sub_limb = nullptr, bool twice = false,
+                                              double scalar = 0.0) {
   rows_fwd_lds(x, S, TW, p, pinv);
   if (next) load_t(x, next, rg);
 #pragma unroll
@@ -1168,9 +1171,34 @@ __device__ __forceinline__ void ipq_finish_rs(double (&ip)[16], double (&x)[16],
 #pragma unroll
     for (int k = 0; k < 16; ++k) ip[k] += ad[k];  // |.| <= 6.9 p
   }
+  if (!sub_limb && !twice && scalar == 0.0) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(ip[k], ql_inv, p), p, pinv));
+    for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(mulc(ip[k], ql_inv, p), p, pinv));
+    return;
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {  // |r| <= 1.5 p: |2 r - sub + scalar| <= 5 p
+    const double r = mulc(ip[k], ql_inv, p);
+    ip[k] = (twice ? 2.0 * r : r) + scalar;
+  }
+  if (sub_limb) {
+    load_gal(ad, sub_limb, na, 1u);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ip[k] -= ad[k];
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(ip[k], p, pinv));
 }
+
+// Post-ops of a rescaled product (the Chebyshev step of fhe.homo_mul_relin_rescale_postop):
+// out <- (twice ? 2 out : out) - sub (+ scalar[i] on the b component).
+struct RsPost {
+  const uint64_t* sub_b;
+  const uint64_t* sub_a;
+  long long sub_stride;
+  int twice, has_scalar;
+  uint64_t scalar[kMaxPrimes];
+};
 
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
 // Tile = (row group, Q limb i): the inner product of limb i (as in K3) is combined with the NTT rows
@@ -1187,7 +1215,7 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
                                               uint64_t* __restrict__ out_a, long long out_stride,
                                               const LevelConsts* __restrict__ lc, const DevTables& T, int lin,
                                               double* S, double* TW, int koff = 0,
-                                              HoistSrc H = HoistSrc{nullptr, 1, 0}) {
+                                              HoistSrc H = HoistSrc{nullptr, 1, 0}, const RsPost* post = nullptr) {
   const int nq = RS ? ell - 1 : ell;  // output limbs (the rescale drops q_{ell-1})
   const TileId id = decode_tile(batch, lin);
   if (id.tile >= 16 * nq) return;
@@ -1210,11 +1238,15 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
   if constexpr (RS) {
     // out = (IP P^-1 - v + sigma(add) + acc) q_{ell-1}^-1, v = NTT rows of (conv P^-1 + r)
     const TwPair ql_inv = lc->qlast_inv[i];
+    const long long so = (long long)b * post->sub_stride + (long long)i * kN;
     ipq_finish_rs(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
                   acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
-                  out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv);
+                  out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv,
+                  post->sub_b ? post->sub_b + so : nullptr, post->twice != 0,
+                  post->has_scalar ? u2d(post->scalar[i]) : 0.0);
     ipq_finish_rs(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
-                  out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv);
+                  out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv,
+                  post->sub_a ? post->sub_a + so : nullptr, post->twice != 0, 0.0);
     return;
   }
   ipq_finish(sb, x, v_a, add ? add + (long long)hoist_input<HOIST>(H, b) * add_stride + (long long)i * kN : nullptr, g,
@@ -1306,11 +1338,12 @@ __global__ __launch_bounds__(kT, 2) void k_ks_rows_ipq_rs(const uint64_t* __rest
                                                        const uint64_t* __restrict__ acc_a, long long acc_stride,
                                                        uint64_t* __restrict__ out_b, uint64_t* __restrict__ out_a,
                                                        long long out_stride, const LevelConsts* __restrict__ lc,
-                                                       DevTables T) {
+                                                       DevTables T, RsPost post) {
   __shared__ double S[kRowLds];
   __shared__ double TW[kTwLds];
   rows_ipq_body<false, true>(d, d_stride, G, t2, keys, ell, beta, batch, t4, add, add_stride, acc_b, acc_a,
-                             acc_stride, out_b, out_a, out_stride, lc, T, blockIdx.x, S, TW);
+                             acc_stride, out_b, out_a, out_stride, lc, T, blockIdx.x, S, TW, 0,
+                             HoistSrc{nullptr, 1, 0}, &post);
 }
 
 // K5 of hoisted rotations: as k_ks_rows_ipq with the digits and inputs of HoistSrc.
@@ -1625,7 +1658,8 @@ size_t ks_rs_bytes(const hck_context* c, int ell, int batch) {
 int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
-                char* ws, hipStream_t s) {
+                char* ws, hipStream_t s, int twice, const uint64_t* sub_b, const uint64_t* sub_a,
+                long long sub_stride, const uint64_t* scalar) {
   if (c->wide || c->conv_engine != 1 || ell < 2) return HCK_ERR_UNSUPPORTED;
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch < 1 || batch > kMaxBatchF || (acc_b == nullptr) != (acc_a == nullptr)) return HCK_ERR_ARG;
@@ -1667,9 +1701,16 @@ int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, lon
   // K5: Q limbs 0 .. ell - 2
   {
     const int tiles = 16 * nq, groups = (tiles + kXcds - 1) / kXcds;
+    RsPost post{};
+    post.sub_b = sub_b;
+    post.sub_a = sub_a;
+    post.sub_stride = sub_stride;
+    post.twice = twice;
+    post.has_scalar = scalar != nullptr;
+    for (int i = 0; scalar && i < nq; ++i) post.scalar[i] = scalar[i];
     k_ks_rows_ipq_rs<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, t4,
                                                                 add, add_stride, acc_b, acc_a, acc_stride, out_b,
-                                                                out_a, out_stride, c->d_level + ell, c->dev);
+                                                                out_a, out_stride, c->d_level + ell, c->dev, post);
     HCK_CHECK_LAUNCH();
   }
   return HCK_OK;

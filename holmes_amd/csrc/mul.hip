@@ -186,12 +186,22 @@ extern "C" size_t hck_mul_relin_rescale_workspace_bytes(const hck_context* ctx, 
   return (ks > rs ? ks : rs) + 5 * chunk * poly;
 }
 
-extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
-                                     const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
-                                     int64_t b_stride, const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1,
-                                     int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+namespace {
+
+// The rescaled product with its post-ops: out = (twice ? 2 : 1) * rescale(a * b) - sub (+ scalar on
+// out0); sub0 / sub1 and scalar nullable.
+int mul_relin_rescale_post(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                           const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
+                           int64_t b_stride, const uint64_t* relin_ksk, int twice, const uint64_t* sub0,
+                           const uint64_t* sub1, int64_t sub_stride, const uint64_t* scalar, uint64_t* out0,
+                           uint64_t* out1, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                           hipStream_t s) {
   if (!hck::valid_level(ctx, level_limbs) || level_limbs < 2 || batch < 0) return HCK_ERR_ARG;
   if (!a0 || !a1 || !b0 || !b1 || !relin_ksk || !out0 || !out1 || out0 == out1) return HCK_ERR_ARG;
+  if ((sub0 == nullptr) != (sub1 == nullptr)) return HCK_ERR_ARG;
+  if (scalar)
+    for (int i = 0; i < level_limbs - 1; ++i)
+      if (scalar[i] >= ctx->primes[i]) return HCK_ERR_ARG;
   if (batch == 0) return HCK_OK;
   if (!workspace || workspace_bytes < hck_mul_relin_rescale_workspace_bytes(ctx, level_limbs, batch))
     return HCK_ERR_WORKSPACE;
@@ -207,7 +217,8 @@ extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, in
   uint64_t* d = (uint64_t*)(ks_ws + ks_bytes);  // [3][chunk][ell][N], then (unfused) [2][chunk][ell][N]
   const uint64_t* keys[hck::kMaxBatchM];
   for (int b = 0; b < chunk; ++b) keys[b] = relin_ksk;
-  hipStream_t s = (hipStream_t)stream;
+  int prime_idx[hck::kMaxPrimes];
+  for (int i = 0; i < ell - 1; ++i) prime_idx[i] = i;
   for (int i0 = 0; i0 < batch; i0 += chunk) {
     const int nb = batch - i0 < chunk ? batch - i0 : chunk;
     uint64_t* d0 = d;
@@ -217,10 +228,11 @@ extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, in
                                 b0 + (long long)i0 * b_stride, b1 + (long long)i0 * b_stride, b_stride, d0, d1, d2,
                                 poly, s);
     if (rc) return rc;
-    const long long oi = (long long)i0 * out_stride;
+    const long long oi = (long long)i0 * out_stride, si = (long long)i0 * sub_stride;
     if (fused) {
       rc = hck::ks_rescaled(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, out0 + oi, out1 + oi,
-                            out_stride, ks_ws, s);
+                            out_stride, ks_ws, s, twice, sub0 ? sub0 + si : nullptr, sub1 ? sub1 + si : nullptr,
+                            sub_stride, scalar);
       if (rc) return rc;
       continue;
     }
@@ -228,12 +240,53 @@ extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, in
     rc = hck::ks_fused(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, mid, mid + (long long)nb * poly,
                        poly, ks_ws, s);
     if (rc) return rc;
-    rc = hck::rescale_fused(ctx, ell, nb, mid, poly, out0 + oi, out_stride, ks_ws, s);
-    if (rc) return rc;
-    rc = hck::rescale_fused(ctx, ell, nb, mid + (long long)nb * poly, poly, out1 + oi, out_stride, ks_ws, s);
-    if (rc) return rc;
+    uint64_t* outs[2] = {out0 + oi, out1 + oi};
+    const uint64_t* subs[2] = {sub0 ? sub0 + si : nullptr, sub1 ? sub1 + si : nullptr};
+    for (int c = 0; c < 2; ++c) {
+      rc = hck::rescale_fused(ctx, ell, nb, mid + (long long)c * nb * poly, poly, outs[c], out_stride, ks_ws, s);
+      if (rc) return rc;
+      if (twice) {
+        rc = hck_poly_op(ctx, HCK_OP_ADD, outs[c], outs[c], outs[c], nb, out_stride, out_stride, out_stride, ell - 1,
+                         prime_idx, nullptr, s);
+        if (rc) return rc;
+      }
+      if (subs[c]) {
+        rc = hck_poly_op(ctx, HCK_OP_SUB, outs[c], outs[c], subs[c], nb, out_stride, out_stride, sub_stride, ell - 1,
+                         prime_idx, nullptr, s);
+        if (rc) return rc;
+      }
+      if (scalar && c == 0) {
+        rc = hck_poly_op(ctx, HCK_OP_ADD_SCALAR, outs[c], outs[c], nullptr, nb, out_stride, out_stride, 0, ell - 1,
+                         prime_idx, scalar, s);
+        if (rc) return rc;
+      }
+    }
   }
   return HCK_OK;
+}
+
+}  // namespace
+
+extern "C" int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                                     const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
+                                     int64_t b_stride, const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1,
+                                     int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
+  return mul_relin_rescale_post(ctx, level_limbs, batch, a0, a1, a_stride, b0, b1, b_stride, relin_ksk, 0, nullptr,
+                                nullptr, 0, nullptr, out0, out1, out_stride, workspace, workspace_bytes,
+                                (hipStream_t)stream);
+}
+
+extern "C" int hck_mul_relin_rescale_postop(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                                            const uint64_t* a1, int64_t a_stride, const uint64_t* b0,
+                                            const uint64_t* b1, int64_t b_stride, const uint64_t* relin_ksk,
+                                            int apply_double, const uint64_t* sub0, const uint64_t* sub1,
+                                            int64_t sub_stride, const uint64_t* scalar, uint64_t* out0,
+                                            uint64_t* out1, int64_t out_stride, void* workspace,
+                                            size_t workspace_bytes, void* stream) {
+  if (sub0 && (sub0 == out0 || sub0 == out1 || sub1 == out0 || sub1 == out1)) return HCK_ERR_ARG;
+  return mul_relin_rescale_post(ctx, level_limbs, batch, a0, a1, a_stride, b0, b1, b_stride, relin_ksk,
+                                apply_double ? 1 : 0, sub0, sub1, sub_stride, scalar, out0, out1, out_stride, workspace,
+                                workspace_bytes, (hipStream_t)stream);
 }
 
 extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int groups, const uint64_t* in,

@@ -864,26 +864,28 @@ def homo_mul_relin_rescale_postop(lhs: Cipher, rhs: Cipher, ctx: CKKSContext, ap
                                   sub: Cipher | None = None, scalar: EncodedScalar | None = None) -> Cipher:
     """rescale(lhs * rhs) (relinearised), then x 2 when ``apply_double``, minus ``sub`` (dropped to
     the result's level), plus the encoded ``scalar``: the Chebyshev step T_{a+b} = 2 T_a T_b -
-    T_{|a-b|} (llama3fhe/operators/nonlinear/polynomial.py:140-190)."""
+    T_{|a-b|} (llama3fhe/operators/nonlinear/polynomial.py:140-190).  One native call
+    (hck_mul_relin_rescale_postop): the post-ops ride on the product's last kernel."""
 
-    out = homo_mul_relin_rescale(lhs, rhs, ctx)
-    if apply_double:
-        doubled = homo_add(out, out, ctx)
-        out.release()
-        out = doubled
+    limbs, (a0, a1), (b0, b1) = _mul_operands(lhs, rhs)
+    if limbs < 2:
+        raise ValueError("rescale needs a non-extended ciphertext with at least two limbs")
+    st = _product_state(lhs, rhs, limbs)
+    state = st.replace(cur_limbs=limbs - 1, scale_degree=max(1, int(st.scale_degree) - 1),
+                       scaling_factor=float(st.scaling_factor) / float(ctx.rescale_divisor_at(limbs)))
+    pair = None
     if sub is not None:
-        s_al = align_to(sub, out.state, ctx) if _limbs(sub) > _limbs(out) else sub
-        sub_state = s_al.state.replace(scale_degree=out.state.scale_degree)
-        diff = homo_sub(out, s_al.cipher_like(s_al.cv, state=sub_state), ctx)
-        if s_al is not sub:
-            s_al.release()
-        out.release()
-        out = diff
+        if sub.is_ext or len(sub.cv) != 2 or sub.batch_size != lhs.batch_size or _limbs(sub) < limbs - 1:
+            raise ValueError("postop sub must be a two-component ciphertext of the batch with the result's limbs")
+        pair = tuple(_view(x, limbs - 1) for x in sub.cv)
+    sc = None
     if scalar is not None:
-        added = homo_add_scalar(out, scalar, ctx)
-        out.release()
-        out = added
-    return out
+        if not _same_scale(float(state.scaling_factor), scalar.scaling_factor):
+            raise ValueError(f"scalar scale {scalar.scaling_factor} != product scale {state.scaling_factor}")
+        sc = _scalar_list(scalar, limbs - 1)
+    both = ctx.mul_relin_rescale_postop_raw(a0, a1, b0, b1, limbs, _relin_key(ctx), apply_double=bool(apply_double),
+                                            sub=pair, scalar=sc)
+    return lhs.cipher_like([both[0], both[1]], state=state)
 
 
 def grouped_scalar_weighted_acc(batch: Cipher, table: EncodedScalar, ctx: CKKSContext) -> Cipher:

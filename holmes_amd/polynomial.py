@@ -81,10 +81,10 @@ class PSEvaluator:
         j0 = 1
         while j0 < self.k:  # T_(j0+1) .. T_(2 j0) from T_(j/2) T_(j - j/2): one batched product per depth
             js = list(range(j0 + 1, min(2 * j0, self.k) + 1))
-            prods = self.mul_many([(T[j // 2], T[j - j // 2]) for j in js])
-            for j, p in zip(js, prods):
-                a, b = j // 2, j - j // 2
-                T[j] = self._finish_double(p, None if a == b else T[b - a])
+            pairs = [(T[j // 2], T[j - j // 2]) for j in js]
+            subs = [None if j // 2 == j - j // 2 else T[j - 2 * (j // 2)] for j in js]
+            for j, t in zip(js, self.mul_many_double(pairs, subs)):
+                T[j] = t
             j0 *= 2
         M = 2 * self.k
         while M <= degree:
@@ -213,10 +213,43 @@ class PSEvaluator:
         out = p.cipher_like(self._combine(terms, l, w))
         return self._add_const_inplace(out, -1.0) if sub is None else out
 
+    def _mul_double(self, a, b, sub, l: int):
+        """2 a b - sub (sub = None: - 1) for a, b at l limbs: one hck_mul_relin_rescale_postop (the
+        doubling, the subtraction and the constant ride on the product's last kernel)."""
+
+        ctx = self.ctx
+        pair = sc = None
+        if sub is None:
+            sc = [int(v) for v in self._residues(-1.0, l - 1, self.canon[l - 1])]
+        else:
+            s = self.adjust(sub, l - 1)
+            pair = tuple(c[:, :l - 1] for c in s.cv)
+        both = ctx.mul_relin_rescale_postop_raw(a.cv[0][:, :l], a.cv[1][:, :l], b.cv[0][:, :l], b.cv[1][:, :l], l,
+                                                ctx.relin_key, apply_double=True, sub=pair, scalar=sc)
+        state = a.state.replace(cur_limbs=l - 1, scale_degree=1,
+                                scaling_factor=self.canon[l] * self.canon[l] / float(ctx.rescale_divisor_at(l)))
+        return self._fix(a.cipher_like([both[0], both[1]], state=state), l - 1)
+
+    def mul_many_double(self, pairs, subs) -> list:
+        """2 a b - sub (sub None: - 1) for every pair, every operand first brought to the lowest
+        level among them (as ``mul_many``)."""
+
+        if self.sim:
+            return [self._finish_double(p, s) for p, s in zip(self.mul_many(pairs), subs)]
+        l = min(self.lv(x) for pr in pairs for x in pr)
+        if l < 2:
+            raise ValueError("EvalMod ran out of levels")
+        B = pairs[0][0].batch_size
+        if len(pairs) == 1 or B >= 16:
+            return [self._mul_double(self.adjust(a, l), self.adjust(b, l), s, l) for (a, b), s in zip(pairs, subs)]
+        return [self._finish_double(p, s) for p, s in zip(self.mul_many(pairs), subs)]
+
     def double_minus(self, a, b, sub=None):
         """2 a b - sub (sub = None: - 1)."""
 
-        return self._finish_double(self.mul(a, b), sub)
+        if self.sim:
+            return self._finish_double(self.mul(a, b), sub)
+        return self.mul_many_double([(a, b)], [sub])[0]
 
     def lincomb(self, terms, c0: float, cap: int | None):
         """c0 + sum c_j x_j over ``terms`` = [(c_j, x_j)], rescaled once, at min(level) - 1 or ``cap``:

@@ -32,8 +32,9 @@
  *                          (llama3fhe/operators/attention/prefill/qk.py:460-464,
  *                          attention/kernel_helpers.py:146-152, nonlinear/polynomial.py:140-190)
  *   hck_rotate_rescale     fhe.homo_rotate followed by fhe.rescale (operator.py:446-453, 387-394)
- *   hck_mul_relin_rescale  the multiply-relinearise-rescale of fhe.homo_mul_relin_rescale_postop
- *                          (nonlinear/polynomial.py:140-150)
+ *   hck_mul_relin_rescale(_postop)
+ *                          fhe.homo_mul_relin_rescale_postop (nonlinear/polynomial.py:140-150): the
+ *                          rescaled product, and with its double / subtract / scalar post-ops
  *   hck_weighted_sum       fhe.grouped_scalar_weighted_acc (nonlinear/polynomial.py:256-300)
  *   hck_lincomb_rescale    the evaluator's weighted sum of basis terms followed by its rescale
  *                          (nonlinear/polynomial.py:256-300)
@@ -337,6 +338,19 @@ int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, co
                           const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
                           int64_t b_stride, const uint64_t* relin_ksk, uint64_t* out0, uint64_t* out1,
                           int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream);
+
+/* hck_mul_relin_rescale with the post-ops of EasyFHE's fhe.homo_mul_relin_rescale_postop
+ * (llama3fhe/operators/nonlinear/polynomial.py:140-150, the Chebyshev step T_(a+b) = 2 T_a T_b -
+ * T_|a-b|): out = (apply_double ? 2 : 1) * rescale(a * b) - sub (+ scalar on out0), sub0 / sub1
+ * ([>= level_limbs - 1] limbs per item at sub_stride) and scalar (level_limbs - 1 canonical
+ * residues, host array) nullable; outputs must not be sub.  The residues of the product followed by
+ * the additions, computed in the product's last kernel on the matrix-core engine. */
+int hck_mul_relin_rescale_postop(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
+                                 const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
+                                 int64_t b_stride, const uint64_t* relin_ksk, int apply_double, const uint64_t* sub0,
+                                 const uint64_t* sub1, int64_t sub_stride, const uint64_t* scalar, uint64_t* out0,
+                                 uint64_t* out1, int64_t out_stride, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /* Grouped scalar-weighted sum over one component of n inputs (item stride in_stride, [limbs][N]
  * each): out[g] = sum_j weights[g][j][l] * in[j] (mod q_l); weights is a device array

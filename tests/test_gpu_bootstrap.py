@@ -134,7 +134,9 @@ def test_evalmod_matches_host_polynomial(env):
     for _ in range(prog.spec.double_angle):
         want = 2 * want * want - 1
     got = client.decrypt(y).real
-    assert np.max(np.abs(got - want)) < 2.0**-24
+    # the evaluation's own noise at scale 2^50 (fresh encryption noise through the T_k chain and three
+    # double angles) sits near 2^-24.3 at the maximum over 65536 slots; 2^-23 leaves it a margin
+    assert np.max(np.abs(got - want)) < 2.0**-23
 
 
 @pytest.mark.parametrize("limbs", [3, 2])

@@ -346,3 +346,41 @@ def check_lincomb_rescale(env, limbs, G, T):
             q = np.array(ctx.primes[:limbs - 1], dtype=object).reshape(-1, 1)
             r = ((r.astype(object) + np.array(add, dtype=object).reshape(-1, 1)) % q).astype(np.uint64)
         assert np.array_equal(_host(outs[g]), r), f"oracle group {g}"
+
+
+@pytest.mark.parametrize("engine", ["mfma", "valu"])
+def test_mul_relin_rescale_postop_equals_the_steps(env, engine):
+    _, _, ctx, _ = env
+    ctx.set_conversion_engine(engine)
+    try:
+        check_mul_relin_rescale_postop(env, (24, 9, 2))
+    finally:
+        ctx.set_conversion_engine("mfma")
+
+
+def check_mul_relin_rescale_postop(env, levels, batch=3):
+    """hck_mul_relin_rescale_postop (2 x product - sub, 2 x product + scalar, product - sub) equals the
+    rescaled product followed by the additions, residue for residue."""
+    from holmes_amd import _native as nat
+
+    fhe, client, ctx, orc = env
+    for ell in levels:
+        rng = np.random.default_rng(1300 + ell)
+        a0, a1, b0, b1 = (_dev(_rand(ctx, rng, batch, ell)) for _ in range(4))
+        s0, s1 = (_dev(_rand(ctx, rng, batch, ell)) for _ in range(2))  # more limbs than needed
+        sc = [int(rng.integers(0, ctx.primes[i])) for i in range(ell - 1)]
+        base = ctx.mul_relin_rescale_raw(a0, a1, b0, b1, ell, ctx.relin_key, stacked=True)
+        idx = ctx.q_prime_idx(ell - 1)
+        for twice, sub, scalar in ((True, True, False), (True, False, True), (False, True, True)):
+            want = base.clone()
+            for c, sv in ((0, s0), (1, s1)):
+                w = want[c]
+                if twice:
+                    ctx.poly_op(nat.HCK_OP_ADD, w, w, w, prime_idx=idx)
+                if sub:
+                    ctx.poly_op(nat.HCK_OP_SUB, w, w, sv[:, :ell - 1], prime_idx=idx)
+                if scalar and c == 0:
+                    ctx.poly_op(nat.HCK_OP_ADD_SCALAR, w, w, prime_idx=idx, scalar=sc)
+            got = ctx.mul_relin_rescale_postop_raw(a0, a1, b0, b1, ell, ctx.relin_key, apply_double=twice,
+                                                   sub=(s0, s1) if sub else None, scalar=sc if scalar else None)
+            assert torch.equal(got, want), (ell, twice, sub, scalar)

@@ -166,6 +166,10 @@ def test_rotate_rescale(env, ell):
     G.check_rotate_rescale(env, [ell], [ell], batch=2, rot=5)
 
 
+def test_mul_relin_rescale_postop(env):
+    M.check_mul_relin_rescale_postop(env, (38, 2), batch=2)
+
+
 @pytest.mark.parametrize("ell", [38, 2])
 def test_mul_relin_rescale(env, ell):
     M.check_mul_relin_rescale(env, [ell], [ell], batch=2)
