@@ -649,7 +649,7 @@ def bootstrap(cipher: Cipher, context: CKKSContext, program: BootstrapProgram, *
     if bits:
         enc = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
                                 scaling_factor=float(ctx.rescale_divisor_at(limbs)) * 2.0**-bits, context=ctx)
-        x = fhe.rescale(fhe.homo_mul_scalar(x, enc, ctx), ctx)
+        x = fhe.homo_mul_scalar_rescale(x, enc, ctx)
     # 2. ModRaise: decrypts to M = m + q_0 I over the raised modulus; read at the nominal scale S
     raised = [ctx.modraise(c[:, :1].contiguous(), program.raise_to_limbs) for c in x.cv]
     S = program.nominal_scale
@@ -726,7 +726,7 @@ def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: Boo
         limbs = int(corrected.state.cur_limbs)
         back = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
                                  scaling_factor=float(ctx.rescale_divisor_at(limbs)) * 2.0**-p, context=ctx)
-        out = fhe.rescale(fhe.homo_mul_scalar(corrected, back, ctx), ctx)
+        out = fhe.homo_mul_scalar_rescale(corrected, back, ctx)
         return out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(cipher.state.scaling_factor)))
     except ValueError:
         return first

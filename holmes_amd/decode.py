@@ -649,7 +649,7 @@ class CipherOps:
         q = float(self.ctx.rescale_divisor_at(l))
         enc = f.encode_scalar(1.0, cur_limbs=l, scale_degree=1, scaling_factor=scale * q / self.scale(ct),
                               context=self.ctx)
-        out = f.rescale(f.homo_mul_scalar(ct, enc, self.ctx), self.ctx)
+        out = f.homo_mul_scalar_rescale(ct, enc, self.ctx)
         out = out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(scale), scale_degree=1))
         if self.limbs(out) > int(limbs):
             out = f.align_to(out, out.state.replace(cur_limbs=int(limbs)), self.ctx)

@@ -751,12 +751,22 @@ def homo_mul_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
 
 
 def homo_mul_scalar_rescale(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:
-    """homo_mul_scalar followed by rescale (softmax.py:720-729, norm/refresh.py:21-31)."""
+    """homo_mul_scalar followed by rescale (softmax.py:720-729, norm/refresh.py:21-31), as one
+    hck_lincomb_rescale of a single term: the product is never stored; the same residues."""
 
-    tmp = homo_mul_scalar(ct, enc, ctx)
-    out = rescale(tmp, ctx)
-    tmp.release()
-    return out
+    limbs = min(_limbs(ct), enc.cur_limbs)
+    if ct.is_ext or limbs < 2:
+        raise ValueError("rescale needs a non-extended ciphertext with at least two limbs")
+    B = int(ct.cv[0].shape[0])
+    w = ctx.resident(np.asarray(_scalar_list(enc, limbs), dtype=np.uint64).reshape(1, limbs))
+    out = _alloc(ctx, len(ct.cv), B, limbs - 1)
+    ctx.lincomb_rescale([[x[b]] for x in ct.cv for b in range(B)], limbs, [o[b] for o in out for b in range(B)], w)
+    st = ct.state
+    sd = int(st.scale_degree) + enc.scale_degree
+    state = st.replace(cur_limbs=limbs - 1, scale_degree=max(1, sd - 1),
+                       scaling_factor=float(st.scaling_factor) * enc.scaling_factor
+                       / float(ctx.rescale_divisor_at(limbs)))
+    return ct.cipher_like(out, state=state)
 
 
 def homo_add_scalar(ct: Cipher, enc: EncodedScalar, ctx: CKKSContext) -> Cipher:

@@ -261,7 +261,7 @@ class FeatureMajorMLPBlock:
             limbs = int(c.state.cur_limbs)
             enc = fhe.encode_scalar(2.0 ** -r, cur_limbs=limbs, scale_degree=1,
                                     scaling_factor=float(ctx.rescale_divisor_at(limbs)), context=ctx)
-            small = fhe.rescale(fhe.homo_mul_scalar(c, enc, ctx), ctx)
+            small = fhe.homo_mul_scalar_rescale(c, enc, ctx)
             small = small.cipher_like(small.cv, state=small.state.replace(scaling_factor=c.state.scaling_factor))
             fresh = bs.bootstrap_with_correction(small, ctx, self.bootstrap_program,
                                                  iterations=int(spec.bootstrap_iterations), precision_bits=12)

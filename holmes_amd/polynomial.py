@@ -341,7 +341,7 @@ def eval_chebyshev(ct: Cipher, coeffs, ctx: CKKSContext, interval=(-1.0, 1.0)) -
     alpha, beta = 2.0 / (b - a), -(a + b) / (b - a)
     q = float(ctx.rescale_divisor_at(limbs))
     enc = fhe.encode_scalar(alpha, cur_limbs=limbs, scale_degree=1, scaling_factor=q, context=ctx)
-    u = fhe.rescale(fhe.homo_mul_scalar(ct, enc, ctx), ctx)
+    u = fhe.homo_mul_scalar_rescale(ct, enc, ctx)
     S = float(ct.state.scaling_factor)
     u = u.cipher_like(u.cv, state=u.state.replace(scaling_factor=S, scale_degree=1))
     if beta != 0.0:

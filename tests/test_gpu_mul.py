@@ -218,6 +218,8 @@ def test_scalar_ops(fixed_env):
     r = fhe.homo_mul_scalar_rescale(ct, half, ctx)
     assert r.state.cur_limbs == 5
     assert np.max(np.abs(client.decrypt(r).real - 0.5 * x)) < TOL
+    steps = fhe.rescale(fhe.homo_mul_scalar(ct, half, ctx), ctx)  # the fused call gives the steps' residues
+    assert r.state == steps.state and all(torch.equal(a, b) for a, b in zip(r.cv, steps.cv))
     shift = fhe.encode_scalar(0.375, cur_limbs=6, scale_degree=1, scaling_factor=ct.state.scaling_factor,
                               context=ctx)
     assert np.max(np.abs(client.decrypt(fhe.homo_add_scalar(ct, shift, ctx)).real - (x + 0.375))) < TOL
