@@ -511,7 +511,8 @@ class _Shape:
 
 
 class _CallLog:
-    NAMES = ("keyswitch", "rotate_raw", "mul_relin_raw", "mul_relin_rescale_raw", "relinearize_raw", "bsgs_mac",
+    NAMES = ("keyswitch", "rotate_raw", "mul_relin_raw", "mul_relin_rescale_raw", "mul_relin_rescale_postop_raw",
+             "relinearize_raw", "bsgs_mac",
              "rescale_raw", "modraise", "weighted_sum", "poly_op", "automorphism", "lincomb", "lincomb_rescale",
              "rotate_ext", "rotate_ext_sum", "hoist_digits", "rotate_hoisted", "rotate_rescale_raw", "moddown")
 
@@ -569,6 +570,10 @@ class _CallLog:
             elif name == "mul_relin_rescale_raw":
                 l, B = int(a[4]), int(a[0].shape[0])
                 total += B * (4 * l + 2 * (l - 1)) + 2 * beta(l) * (l + K)
+                ks.append(("product", B, l))
+            elif name == "mul_relin_rescale_postop_raw":  # + the subtrahend when given
+                l, B = int(a[4]), int(a[0].shape[0])
+                total += B * (4 * l + 2 * (l - 1) * (1 + (k.get("sub") is not None))) + 2 * beta(l) * (l + K)
                 ks.append(("product", B, l))
             elif name == "hoist_digits":  # c1 in, the extended digits out
                 l, B = int(a[1]), int(a[0].shape[0])
