@@ -145,12 +145,15 @@ int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint3
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch);
 // Post-ops on the ell - 1 output limbs: out <- (twice ? 2 out : out) - sub (+ scalar[i] on out_b);
 // sub_b / sub_a ([>= ell - 1] limbs per item at sub_stride) and scalar (ell - 1 canonical residues)
-// nullable.
+// nullable.  prod_ab = {a0, a1, b0, b1} (nullable): the accumulators of limbs < ell - 1 are the
+// tensor terms a0 b0 and a0 b1 + a1 b0, formed in the last kernel (acc_b / acc_a then only serve
+// the q_{ell-1} limb).
 int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
                 char* ws, hipStream_t s, int twice = 0, const uint64_t* sub_b = nullptr,
-                const uint64_t* sub_a = nullptr, long long sub_stride = 0, const uint64_t* scalar = nullptr);
+                const uint64_t* sub_a = nullptr, long long sub_stride = 0, const uint64_t* scalar = nullptr,
+                const uint64_t* const* prod_ab = nullptr, long long a_stride = 0, long long b_stride = 0);
 // ModDown of extended-basis polys ([ell + K] canonical limbs each) to ell limbs.
 size_t moddown_bytes(const hck_context* c, int ell, int polys);
 int moddown_ext(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,

@@ -1155,12 +1155,28 @@ __device__ __forceinline__ void ipq_finish_rs(double (&ip)[16], double (&x)[16],
                                               long long na, int rg, double* S, const double* TW, TwPair pinv_P,
                                               TwPair ql_inv, double p, double pinv,
                                               const uint64_t* __restrict__ sub_limb = nullptr, bool twice = false,
-                                              double scalar = 0.0) {
+                                              double scalar = 0.0, const uint64_t* __restrict__ px1 = nullptr,
+                                              const uint64_t* __restrict__ py1 = nullptr,
+                                              const uint64_t* __restrict__ px2 = nullptr,
+                                              const uint64_t* __restrict__ py2 = nullptr) {
   rows_fwd_lds(x, S, TW, p, pinv);
   if (next) load_t(x, next, rg);
 #pragma unroll
   for (int k = 0; k < 16; ++k) ip[k] = mulc(ip[k], pinv_P, p) - S[s_out(k)];  // |.| <= p + 3.9 p
   double ad[16];
+  if (px1) {  // the tensor term formed here: x1 y1 (+ x2 y2), each product within 0.875 p
+    double t[16];
+    load_gal(ad, px1, na, 1u);
+    load_gal(t, py1, na, 1u);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ip[k] += mulv(ad[k], t[k], p, pinv);
+    if (px2) {
+      load_gal(ad, px2, na, 1u);
+      load_gal(t, py2, na, 1u);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) ip[k] += mulv(ad[k], t[k], p, pinv);
+    }
+  }
   if (add_limb) {
     load_gal(ad, add_limb, na, g);
 #pragma unroll
@@ -1198,6 +1214,10 @@ struct RsPost {
   long long sub_stride;
   int twice, has_scalar;
   uint64_t scalar[kMaxPrimes];
+  // the product's degree-0/1 terms formed in the finish instead of read as accumulators:
+  // acc_b = a0 b0, acc_a = a0 b1 + a1 b0 on limbs < ell - 1 (a*, b* nullable)
+  const uint64_t *a0, *a1, *b0, *b1;
+  long long a_stride, b_stride;
 };
 
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
@@ -1239,14 +1259,20 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
     // out = (IP P^-1 - v + sigma(add) + acc) q_{ell-1}^-1, v = NTT rows of (conv P^-1 + r)
     const TwPair ql_inv = lc->qlast_inv[i];
     const long long so = (long long)b * post->sub_stride + (long long)i * kN;
+    const bool prod = post->a0 != nullptr;
+    const long long ao = (long long)b * post->a_stride + (long long)i * kN;
+    const long long bo = (long long)b * post->b_stride + (long long)i * kN;
     ipq_finish_rs(sb, x, v_a, add ? add + (long long)b * add_stride + (long long)i * kN : nullptr, g,
-                  acc_b ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
+                  acc_b && !prod ? acc_b + (long long)b * acc_stride + (long long)i * kN : nullptr,
                   out_b + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv,
                   post->sub_b ? post->sub_b + so : nullptr, post->twice != 0,
-                  post->has_scalar ? u2d(post->scalar[i]) : 0.0);
-    ipq_finish_rs(sa, x, nullptr, nullptr, 1u, acc_a ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
+                  post->has_scalar ? u2d(post->scalar[i]) : 0.0, prod ? post->a0 + ao : nullptr,
+                  prod ? post->b0 + bo : nullptr);
+    ipq_finish_rs(sa, x, nullptr, nullptr, 1u,
+                  acc_a && !prod ? acc_a + (long long)b * acc_stride + (long long)i * kN : nullptr,
                   out_a + (long long)b * out_stride + (long long)i * kN + na, na, rg, S, TW, pinv_P, ql_inv, p, pinv,
-                  post->sub_a ? post->sub_a + so : nullptr, post->twice != 0, 0.0);
+                  post->sub_a ? post->sub_a + so : nullptr, post->twice != 0, 0.0, prod ? post->a0 + ao : nullptr,
+                  prod ? post->b1 + bo : nullptr, prod ? post->a1 + ao : nullptr, prod ? post->b0 + bo : nullptr);
     return;
   }
   ipq_finish(sb, x, v_a, add ? add + (long long)hoist_input<HOIST>(H, b) * add_stride + (long long)i * kN : nullptr, g,
@@ -1659,7 +1685,8 @@ int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, lon
                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
                 char* ws, hipStream_t s, int twice, const uint64_t* sub_b, const uint64_t* sub_a,
-                long long sub_stride, const uint64_t* scalar) {
+                long long sub_stride, const uint64_t* scalar, const uint64_t* const* prod_ab, long long a_stride,
+                long long b_stride) {
   if (c->wide || c->conv_engine != 1 || ell < 2) return HCK_ERR_UNSUPPORTED;
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch < 1 || batch > kMaxBatchF || (acc_b == nullptr) != (acc_a == nullptr)) return HCK_ERR_ARG;
@@ -1708,6 +1735,14 @@ int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, lon
     post.twice = twice;
     post.has_scalar = scalar != nullptr;
     for (int i = 0; scalar && i < nq; ++i) post.scalar[i] = scalar[i];
+    if (prod_ab) {
+      post.a0 = prod_ab[0];
+      post.a1 = prod_ab[1];
+      post.b0 = prod_ab[2];
+      post.b1 = prod_ab[3];
+      post.a_stride = a_stride;
+      post.b_stride = b_stride;
+    }
     k_ks_rows_ipq_rs<<<dim3(groups * kXcds * batch), kT, 0, s>>>(d, d_stride, G, t2, kp, ell, beta, batch, t4,
                                                                 add, add_stride, acc_b, acc_a, acc_stride, out_b,
                                                                 out_a, out_stride, c->d_level + ell, c->dev, post);

@@ -36,6 +36,28 @@ __global__ __launch_bounds__(256) void k_tensor(const uint64_t* __restrict__ a0,
   d2[z * d_stride + lo] = d2u(canon(mulv(x1, y1, p, pinv), p, pinv));
 }
 
+// The tensor terms the fused rescaled product reads from memory: d2 = a1 b1 on every limb, d0 and d1
+// on the last limb only (the finish forms them for the other limbs from a and b).
+// Grid (N / 256, limbs, batch).
+__global__ __launch_bounds__(256) void k_tensor_d2(const uint64_t* __restrict__ a0, const uint64_t* __restrict__ a1,
+                                                   long long a_stride, const uint64_t* __restrict__ b0,
+                                                   const uint64_t* __restrict__ b1, long long b_stride,
+                                                   uint64_t* __restrict__ d0, uint64_t* __restrict__ d1,
+                                                   uint64_t* __restrict__ d2, long long d_stride, int ell, DevTables T) {
+  const int k = blockIdx.x * 256 + threadIdx.x;
+  const int i = blockIdx.y;
+  const long long z = blockIdx.z;
+  const double p = T.p[i], pinv = T.pinv[i];
+  const long long lo = (long long)i * kN + k;
+  const double x1 = u2d(a1[z * a_stride + lo]), y1 = u2d(b1[z * b_stride + lo]);
+  d2[z * d_stride + lo] = d2u(canon(mulv(x1, y1, p, pinv), p, pinv));
+  if (i == ell - 1) {
+    const double x0 = u2d(a0[z * a_stride + lo]), y0 = u2d(b0[z * b_stride + lo]);
+    d0[z * d_stride + lo] = d2u(canon(mulv(x0, y0, p, pinv), p, pinv));
+    d1[z * d_stride + lo] = d2u(canon(mulv(x0, y1, p, pinv) + mulv(x1, y0, p, pinv), p, pinv));
+  }
+}
+
 // out[g][l][k] = sum_j w[g][j][l] * in[j][l][k] (mod q_l), canonical.  Grid (N / 256, limbs, groups).
 __global__ __launch_bounds__(256) void k_weighted_sum(const uint64_t* __restrict__ in, long long in_stride, int n,
                                                       const uint64_t* __restrict__ w, uint64_t* __restrict__ out,
@@ -224,18 +246,23 @@ int mul_relin_rescale_post(const hck_context* ctx, int level_limbs, int batch, c
     uint64_t* d0 = d;
     uint64_t* d1 = d + (long long)chunk * poly;
     uint64_t* d2 = d + 2LL * chunk * poly;
-    int rc = hck::launch_tensor(ctx, ell, nb, a0 + (long long)i0 * a_stride, a1 + (long long)i0 * a_stride, a_stride,
-                                b0 + (long long)i0 * b_stride, b1 + (long long)i0 * b_stride, b_stride, d0, d1, d2,
-                                poly, s);
-    if (rc) return rc;
+    const long long ai = (long long)i0 * a_stride, bi = (long long)i0 * b_stride;
     const long long oi = (long long)i0 * out_stride, si = (long long)i0 * sub_stride;
+    int rc;
     if (fused) {
+      // d2 everywhere and d0 / d1 on the last limb; the finish forms d0 / d1 of the other limbs
+      hck::k_tensor_d2<<<dim3(hck::kN / 256, ell, nb), 256, 0, s>>>(a0 + ai, a1 + ai, a_stride, b0 + bi, b1 + bi,
+                                                                   b_stride, d0, d1, d2, poly, ell, ctx->dev);
+      HCK_CHECK_LAUNCH();
+      const uint64_t* ab[4] = {a0 + ai, a1 + ai, b0 + bi, b1 + bi};
       rc = hck::ks_rescaled(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, out0 + oi, out1 + oi,
                             out_stride, ks_ws, s, twice, sub0 ? sub0 + si : nullptr, sub1 ? sub1 + si : nullptr,
-                            sub_stride, scalar);
+                            sub_stride, scalar, ab, a_stride, b_stride);
       if (rc) return rc;
       continue;
     }
+    rc = hck::launch_tensor(ctx, ell, nb, a0 + ai, a1 + ai, a_stride, b0 + bi, b1 + bi, b_stride, d0, d1, d2, poly, s);
+    if (rc) return rc;
     uint64_t* mid = d + 3LL * chunk * poly;  // [2][nb][ell][N]: the relinearised product
     rc = hck::ks_fused(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, mid, mid + (long long)nb * poly,
                        poly, ks_ws, s);
