@@ -1601,11 +1601,60 @@ size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
   return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * c->K);
 }
 
+namespace {
+
+int ks_fused_one(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
+                 long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
+                 long long ext_stride, const uint32_t* galois_items);
+
+}  // namespace
+
+// The multi-stream schedule (hck_context_set_ks_streams): slice t of ks_slice_items items runs the
+// whole key switch on ks_stream[t % ks_streams] over its own part of the workspace (the workspace is
+// linear in the item count, so slice t starts at ks_fused_bytes(b0) bytes).  The library streams
+// wait for everything queued on s so far, and s waits for every slice before anything after the call.
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
              char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
              const uint32_t* galois_items) {
+  const int m = c->ks_slice_items, ns = c->ks_streams;
+  if (c->wide || ns < 2 || m < 1 || batch <= m)
+    return ks_fused_one(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b,
+                        out_a, out_stride, ws, s, ext_b, ext_a, ext_stride, galois_items);
+  const int slices = (batch + m - 1) / m, used = slices < ns ? slices : ns;
+  hipError_t e = hipEventRecord(c->ks_fork, s);
+  for (int i = 0; e == hipSuccess && i < used; ++i) e = hipStreamWaitEvent(c->ks_stream[i], c->ks_fork, 0);
+  if (e != hipSuccess) return (int)e;
+  int rc = HCK_OK;
+  for (int t = 0; t < slices && rc == HCK_OK; ++t) {
+    const int b0 = t * m, nb = batch - b0 < m ? batch - b0 : m;
+    const auto at = [b0](long long stride) { return (long long)b0 * stride; };
+    rc = ks_fused_one(c, ell, nb, d + at(d_stride), d_stride, galois, ksk + b0, add ? add + at(add_stride) : nullptr,
+                      add_stride, acc_b ? acc_b + at(acc_stride) : nullptr, acc_a ? acc_a + at(acc_stride) : nullptr,
+                      acc_stride, out_b ? out_b + at(out_stride) : nullptr, out_a ? out_a + at(out_stride) : nullptr,
+                      out_stride, ws + ks_fused_bytes(c, ell, b0), c->ks_stream[t % ns],
+                      ext_b ? ext_b + at(ext_stride) : nullptr, ext_a ? ext_a + at(ext_stride) : nullptr, ext_stride,
+                      galois_items ? galois_items + b0 : nullptr);
+  }
+  // join every stream that received work, also after a failed launch (s must not run ahead of it)
+  for (int i = 0; i < used; ++i) {
+    hipError_t ej = hipEventRecord(c->ks_join[i], c->ks_stream[i]);
+    if (ej == hipSuccess) ej = hipStreamWaitEvent(s, c->ks_join[i], 0);
+    if (ej != hipSuccess && rc == HCK_OK) rc = (int)ej;
+  }
+  return rc;
+}
+
+namespace {
+
+int ks_fused_one(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
+                 long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
+                 long long ext_stride, const uint32_t* galois_items) {
   if (c->wide)
     return wide_ks(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
                    out_stride, ws, s, ext_b, ext_a, ext_stride, galois_items);
@@ -1675,6 +1724,8 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
   }
   return HCK_OK;
 }
+
+}  // namespace
 
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch) {
   const size_t beta = beta_of(c, ell), ext_l = ell + c->K;

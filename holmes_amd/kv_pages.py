@@ -549,7 +549,7 @@ def drop_pairfold_token_to_limbs(token: PairFoldTokenWrite, *, target_limbs: int
     if bootstrap_operator is None:
         for have, want in zip(current, targets):
             if have < want:
-                raise ValueError(f"too few limbs for the drop: {have} < {want} and no bootstrap operator")
+                raise ValueError(f"a page at {have} limbs needs a refresh to reach {want}, and no refresh operator was given")
     if current == targets:
         return token.move()
     ops = getattr(crypto_context, "fhe", None)

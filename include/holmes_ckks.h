@@ -77,6 +77,17 @@ const char* hck_error_string(int code);
  * identical; only the timing differs.  No counterpart in the reference (a scheduling knob). */
 int hck_context_set_ks_slices(hck_context* ctx, int slices);
 
+/* Multi-stream key-switch schedule: with streams >= 2 and slice_items >= 1, a batched key switch of
+ * more than slice_items items runs in slices of slice_items items, slice t on library stream
+ * t % streams (at most 4, default priority), forked from the caller's stream by an event and joined
+ * back into it before the call returns; each slice uses its own part of the caller's workspace.  A
+ * slice's intermediates are then read back while they are still in the last-level cache, and the
+ * conversion kernels of one slice can share the CUs with the inner-product kernels of another.
+ * streams < 2 or slice_items = 0 restores one stream (default).  Results are identical; only the
+ * timing differs.  Not for concurrent use of one context from several host threads.  No counterpart
+ * in the reference (a scheduling knob). */
+int hck_context_set_ks_streams(hck_context* ctx, int streams, int slice_items);
+
 /* Engine of the ModUp / ModDown base-conversion sums inside every key switch: 1 (default) the int8
  * matrix cores (each residue split into balanced base-256 digits, exact int32 sums), 0 FP64 VALU
  * multiply-accumulates.  Results are identical; only the timing differs.  No counterpart in the

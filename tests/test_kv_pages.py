@@ -266,7 +266,7 @@ def test_limb_drop_is_transactional():
     dropped = drop_pairfold_token_to_limbs(same_level, target_limbs=4, value_target_limbs=3, crypto_context=ctx)
     assert [h.state.cur_limbs for h in dropped.handles] == [4, 4, 3, 3]
     assert all(h.releases == 1 for h in hs) and dropped.column == 4
-    with pytest.raises(ValueError, match="too few limbs"):
+    with pytest.raises(ValueError, match="needs a refresh to reach"):
         drop_pairfold_token_to_limbs(dropped, target_limbs=5, crypto_context=ctx)
     assert not dropped.is_consumed
     with pytest.raises(ValueError):
