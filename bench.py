@@ -107,7 +107,13 @@ def main() -> int:
                          "host memory; stream: the "
                          "residue negation kernel over 16 x 24 limbs, a plain read-once/write-once "
                          "stream of known size (HBM ceiling and counter calibration)")
+    ap.add_argument("--write-traffic-record", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="no GPU: sum the last C2 step's five key-switch dispatches in the counter CSVs of "
+                         "two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of `bench.py --steps 2 "
+                         "--warmup 0 --no-cpu` and write the traffic record for the current kernel sources")
     args = ap.parse_args()
+    if args.write_traffic_record:
+        return write_traffic_record(*args.write_traffic_record)
     if args.gpus != 1:
         print(
             "bench.py measures one GPU: this build has no multi-GPU path (each GPU box has one "
@@ -1154,6 +1160,39 @@ def kernel_sources_sha256() -> str:
             with open(os.path.join(root, name), "rb") as f:
                 h.update(f.read())
     return h.hexdigest()
+
+
+def write_traffic_record(fetch_dir: str, write_dir: str) -> int:
+    """The C2 traffic record from two PMC runs: per counter, the last five key-switch dispatches
+    (one C2 step: INTT rows, ModUp, P-limb rows, ModDown, Q-limb rows) are summed (KiB); FETCH_SIZE
+    is scaled by 2.0 and WRITE_SIZE by 1.0, the factors a plain stream kernel of known size reads
+    (profiles/stream_calibration.md)."""
+
+    import csv
+    import datetime
+    import glob
+
+    def last_step_kib(d: str) -> float:
+        per_dispatch: dict[int, float] = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    if "k_ks_" in r["Kernel_Name"]:
+                        i = int(r["Dispatch_Id"])
+                        per_dispatch[i] = per_dispatch.get(i, 0.0) + float(r["Counter_Value"])
+        if len(per_dispatch) < 5:
+            raise SystemExit(f"{d}: fewer than five key-switch dispatches in the counter CSVs")
+        return sum(v for _, v in sorted(per_dispatch.items())[-5:])
+
+    fetch, write = last_step_kib(fetch_dir), last_step_kib(write_dir)
+    rec = {"sources_sha256": kernel_sources_sha256(), "fetch_kib": round(fetch, 1), "write_kib": round(write, 1),
+           "fetch_scale": 2.0, "write_scale": 1.0, "traffic_bytes": int(round((2.0 * fetch + write) * 1024)),
+           "measured": f"{datetime.date.today().isoformat()} rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on "
+                       "bench.py --steps 2 --warmup 0 --no-cpu"}
+    with open(C2_TRAFFIC_RECORD, "w") as f:
+        json.dump(rec, f, indent=1)
+    print(json.dumps(rec))
+    return 0
 
 
 def c2_traffic():
