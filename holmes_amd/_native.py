@@ -14,6 +14,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libholmes_ckks.so"
 HCK_ERR_ARG = -1
 HCK_ERR_WORKSPACE = -5
 HCK_ERR_SCRATCH = -6
+HCK_NOALLOC_SCRATCH_BYTES = 128 << 20   # include/holmes_ckks.h: the array behind hck_rotate_noalloc
 
 HCK_OP_ADD = 0
 HCK_OP_SUB = 1

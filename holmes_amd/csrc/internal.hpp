@@ -201,6 +201,15 @@ inline const ConvConsts* modup_consts(const hck_context* c, int ell, int j) {
   return c->d_modup + (size_t)ell * c->beta_max + j;
 }
 inline int prime_of_ext(const hck_context* c, int ell, int e) { return e < ell ? e : c->L + (e - ell); }
+// Whether two batches of n items (item i of p at p + i * p_stride, p_len words long; likewise q)
+// share any word.  Strides are non-negative; a stride of 0 repeats one item.
+inline bool batches_overlap(const uint64_t* p, int64_t p_stride, int64_t p_len, const uint64_t* q, int64_t q_stride,
+                            int64_t q_len, int n) {
+  if (n <= 0 || !p || !q) return false;
+  const uint64_t* p_end = p + (int64_t)(n - 1) * p_stride + p_len;
+  const uint64_t* q_end = q + (int64_t)(n - 1) * q_stride + q_len;
+  return p < q_end && q < p_end;
+}
 }  // namespace hck
 
 #define HCK_CHECK_LAUNCH()                         \

@@ -221,6 +221,19 @@ int mul_relin_rescale_post(const hck_context* ctx, int level_limbs, int batch, c
   if (!hck::valid_level(ctx, level_limbs) || level_limbs < 2 || batch < 0) return HCK_ERR_ARG;
   if (!a0 || !a1 || !b0 || !b1 || !relin_ksk || !out0 || !out1 || out0 == out1) return HCK_ERR_ARG;
   if ((sub0 == nullptr) != (sub1 == nullptr)) return HCK_ERR_ARG;
+  {
+    // The outputs may not overlap the operands or each other: the matrix-core engine's finish
+    // re-reads a0, a1, b0, b1 after it has stored the first output component, and tiles of
+    // different items are in flight together.
+    const int64_t in_len = (int64_t)level_limbs * hck::kN, out_len = (int64_t)(level_limbs - 1) * hck::kN;
+    const uint64_t* outs[2] = {out0, out1};
+    const uint64_t* ins[4] = {a0, a1, b0, b1};
+    const int64_t in_stride[4] = {a_stride, a_stride, b_stride, b_stride};
+    for (const uint64_t* o : outs)
+      for (int k = 0; k < 4; ++k)
+        if (hck::batches_overlap(o, out_stride, out_len, ins[k], in_stride[k], in_len, batch)) return HCK_ERR_ARG;
+    if (hck::batches_overlap(out0, out_stride, out_len, out1, out_stride, out_len, batch)) return HCK_ERR_ARG;
+  }
   if (scalar)
     for (int i = 0; i < level_limbs - 1; ++i)
       if (scalar[i] >= ctx->primes[i]) return HCK_ERR_ARG;
@@ -348,6 +361,12 @@ extern "C" int hck_lincomb_rescale(const hck_context* ctx, int level_limbs, int 
     if (!x[j]) return HCK_ERR_ARG;
   for (int g = 0; g < groups; ++g)
     if (!out[g]) return HCK_ERR_ARG;
+  // outputs must not be inputs: the fused path forms the combination and its rescale in one pass,
+  // so an output written over any group's input would be read back by another tile
+  for (int g = 0; g < groups; ++g)
+    for (int j = 0; j < groups * terms; ++j)
+      if (hck::batches_overlap(out[g], 0, (int64_t)(ell - 1) * hck::kN, x[j], 0, (int64_t)ell * hck::kN, 1))
+        return HCK_ERR_ARG;
   if (add)
     for (int i = 0; i < ell - 1; ++i)
       if (add[i] >= ctx->primes[i]) return HCK_ERR_ARG;

@@ -45,14 +45,20 @@ int scratch_address(void** out) {
   return HCK_OK;
 }
 
+// Items per launch that fit the scratch array at this level (at most 64, the key switch's own launch
+// size); 0 when not even one item fits.
+int items_per_launch(const hck_context* ctx, int level_limbs) {
+  int n = 64;
+  while (n > 0 && hck::ks_fused_bytes(ctx, level_limbs, n) > kScratchBytes) --n;
+  return n;
+}
+
 }  // namespace
 
 extern "C" size_t hck_rotate_noalloc_limit(const hck_context* ctx, int level_limbs) {
-  // largest batch whose launches (<= 64 items each) fit the scratch array at this level
+  // any batch runs (in launches of as many items as fit) once one item fits the array
   if (!ctx || level_limbs < 1 || level_limbs > ctx->L) return 0;
-  const size_t one = hck::ks_fused_bytes(ctx, level_limbs, 1);
-  const size_t fit = one ? kScratchBytes / one : 0;
-  return fit >= 64 ? (size_t)1 << 30 : fit;  // 64 items fit: any batch (it runs in 64-item launches)
+  return items_per_launch(ctx, level_limbs) > 0 ? (size_t)1 << 30 : 0;
 }
 
 extern "C" int hck_rotate_noalloc(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
@@ -61,14 +67,27 @@ extern "C" int hck_rotate_noalloc(const hck_context* ctx, int level_limbs, int b
                                   int64_t acc_stride, uint64_t* out0, uint64_t* out1, int64_t out_stride,
                                   void* stream) {
   if (!ctx || batch < 0 || level_limbs < 1 || level_limbs > ctx->L) return HCK_ERR_ARG;
-  const int chunk = batch < 64 ? batch : 64;
-  const size_t need = hck::ks_fused_bytes(ctx, level_limbs, chunk);
-  if (need > kScratchBytes) return HCK_ERR_SCRATCH;
+  const int per = items_per_launch(ctx, level_limbs);
+  if (per < 1) return HCK_ERR_SCRATCH;
+  if (batch == 0)
+    return hck::rotate_impl(ctx, level_limbs, 0, galois, nullptr, c0, c1, in_stride, ksk, acc0, acc1, acc_stride,
+                            out0, out1, out_stride, nullptr, 0, stream, false);
+  // every per-item argument is checked before the first launch, so an error launches nothing
+  if (!ksk) return HCK_ERR_ARG;
+  for (int b = 0; b < batch; ++b)
+    if (!ksk[b]) return HCK_ERR_ARG;
   void* ws = nullptr;
-  if (batch > 0) {
-    const int rc = scratch_address(&ws);
+  const int rc0 = scratch_address(&ws);
+  if (rc0) return rc0;
+  // launches of `per` items, in order on one stream, each reusing the whole array
+  for (int i0 = 0; i0 < batch; i0 += per) {
+    const int nb = batch - i0 < per ? batch - i0 : per;
+    const int64_t ii = (int64_t)i0 * in_stride, ai = (int64_t)i0 * acc_stride, oi = (int64_t)i0 * out_stride;
+    const int rc = hck::rotate_impl(ctx, level_limbs, nb, galois, nullptr, c0 ? c0 + ii : nullptr,
+                                    c1 ? c1 + ii : nullptr, in_stride, ksk + i0, acc0 ? acc0 + ai : nullptr,
+                                    acc1 ? acc1 + ai : nullptr, acc_stride, out0 ? out0 + oi : nullptr,
+                                    out1 ? out1 + oi : nullptr, out_stride, ws, kScratchBytes, stream, false);
     if (rc) return rc;
   }
-  return hck::rotate_impl(ctx, level_limbs, batch, galois, nullptr, c0, c1, in_stride, ksk, acc0, acc1, acc_stride,
-                          out0, out1, out_stride, ws, kScratchBytes, stream, false);
+  return HCK_OK;
 }

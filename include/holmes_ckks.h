@@ -147,12 +147,13 @@ int hck_rotate_rescale(const hck_context* ctx, int level_limbs, int batch, uint3
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  No counterpart in the
  * reference: it exists for those callers only.  Same arguments and results as hck_rotate; the
  * key-switch workspace is a fixed device array of HCK_NOALLOC_SCRATCH_BYTES inside the library (one
- * per GPU, resolved on the first call on that device), and nothing is allocated or freed.  A call
- * whose launches need more (ks workspace of min(batch, 64) items at level_limbs) returns
- * HCK_ERR_SCRATCH without launching; hck_rotate_noalloc_limit gives the largest batch that fits
- * (2^30: any batch).  Calls that overlap on one GPU (other streams or threads) race on the array;
- * calls on one stream are ordered.  Limit: one ciphertext up to 32 limbs at K = 8, dnum 3 (24 limbs:
- * one ciphertext, 80 MiB). */
+ * per GPU, resolved on the first call on that device), and nothing is allocated or freed.  The batch
+ * runs in launches of as many items as the array holds at level_limbs (at most 64), one after
+ * another on the stream; a level at which not even one item's key-switch workspace fits returns
+ * HCK_ERR_SCRATCH without launching.  hck_rotate_noalloc_limit gives the largest batch that runs:
+ * 2^30 (any batch) or 0.  Calls that overlap on one GPU (other streams or threads) race on the array;
+ * calls on one stream are ordered.  Limit: a ciphertext of up to 32 limbs at K = 8, dnum 3 (24 limbs:
+ * 80 MiB per item, so one item per launch). */
 int hck_rotate_noalloc(const hck_context* ctx, int level_limbs, int batch, uint32_t galois,
                        const uint64_t* c0, const uint64_t* c1, int64_t in_stride,
                        const uint64_t* const* ksk, const uint64_t* acc0, const uint64_t* acc1,
@@ -343,7 +344,9 @@ int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch, const uint
  * multiply-relinearise-rescale core of EasyFHE's fhe.homo_mul_relin_rescale_postop
  * (llama3fhe/operators/nonlinear/polynomial.py:140-150), its post-ops left to the caller.  On the
  * matrix-core conversion engine the ModDown and the rescale share one conversion pass (the
- * q_{level-1} limb joins the P limbs as a source); otherwise it runs the two steps. */
+ * q_{level-1} limb joins the P limbs as a source); otherwise it runs the two steps.  The outputs
+ * must not overlap a0, a1, b0, b1 or each other (HCK_ERR_ARG): the fused engine re-reads the
+ * operands after its first store. */
 size_t hck_mul_relin_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
 int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
                           const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
@@ -354,7 +357,8 @@ int hck_mul_relin_rescale(const hck_context* ctx, int level_limbs, int batch, co
  * (llama3fhe/operators/nonlinear/polynomial.py:140-150, the Chebyshev step T_(a+b) = 2 T_a T_b -
  * T_|a-b|): out = (apply_double ? 2 : 1) * rescale(a * b) - sub (+ scalar on out0), sub0 / sub1
  * ([>= level_limbs - 1] limbs per item at sub_stride) and scalar (level_limbs - 1 canonical
- * residues, host array) nullable; outputs must not be sub.  The residues of the product followed by
+ * residues, host array) nullable; outputs must not be sub, nor overlap the operands or each other
+ * (HCK_ERR_ARG).  The residues of the product followed by
  * the additions, computed in the product's last kernel on the matrix-core engine. */
 int hck_mul_relin_rescale_postop(const hck_context* ctx, int level_limbs, int batch, const uint64_t* a0,
                                  const uint64_t* a1, int64_t a_stride, const uint64_t* b0, const uint64_t* b1,
@@ -384,8 +388,8 @@ int hck_lincomb(const hck_context* ctx, int limbs, int groups, int terms, const 
 /* A linear combination followed by the rescale: out[g] = rescale(sum_t w[t] * x[g * terms + t])
  * from level_limbs to level_limbs - 1 limbs, plus the residues add[i] (level_limbs - 1 of them,
  * canonical; add may be NULL) on the groups whose bit is set in add_mask; weights a device
- * [terms][level_limbs] table.  groups <= 64, groups * terms <= 256; outputs must not be inputs.
- * The residues of hck_lincomb, hck_rescale and an HCK_OP_ADD_SCALAR, without storing the
+ * [terms][level_limbs] table.  groups <= 64, groups * terms <= 256; an output that overlaps any
+ * input of any group is refused (HCK_ERR_ARG).  The residues of hck_lincomb, hck_rescale and an HCK_OP_ADD_SCALAR, without storing the
  * combination: the Paterson-Stockmeyer step "c0 + sum c_j T_j, rescaled" of the reference's
  * evaluator (llama3fhe/operators/nonlinear/polynomial.py:256-300 followed by its rescale). */
 size_t hck_lincomb_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int groups);

@@ -179,4 +179,4 @@ def test_c5_decode_step_full_width():
     err = float(np.max(np.abs(got - ref["output"])))
     mag = float(np.max(np.abs(ref["output"])))
     print(f"C5 max error {err:.3e} (2^{math.log2(err):.2f}) of magnitude {mag:.2f}; stages {stages}", flush=True)
-    assert err <= 2.0**-16 * mag
+    assert err < 2.0**-16  # absolute, in decoded units (the slot scale), as for C4 and the prefill layer

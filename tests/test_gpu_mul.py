@@ -288,6 +288,58 @@ def test_product_arguments_are_checked(env):
     assert rc == -1
 
 
+@pytest.mark.parametrize("engine", ["mfma", "valu"])
+def test_aliased_products_are_refused(env, engine):
+    """hck_mul_relin_rescale(_postop) refuses outputs that overlap an operand (in place on a0, a1,
+    b0 or b1, or a view shifted by one limb) on both conversion engines, and
+    hck_lincomb_rescale refuses an output that is any group's input: both before launching."""
+    fhe, client, ctx, orc = env
+    from holmes_amd import _native as nat
+
+    lib = nat.lib()
+    ctx.set_conversion_engine(engine)
+    try:
+        limbs, B, N = 4, 2, ctx.N
+        a = ctx.empty(2, B, limbs, N)
+        b = ctx.empty(2, B, limbs, N)
+        fresh = ctx.empty(2, B, limbs - 1, N)
+        ws = ctx.workspace(lib.hck_mul_relin_rescale_workspace_bytes(ctx.handle, limbs, B))
+        st = limbs * N
+        stream = torch.cuda.current_stream().cuda_stream
+
+        def call(o0, o1, ostride):
+            return lib.hck_mul_relin_rescale(ctx.handle, limbs, B, a[0].data_ptr(), a[1].data_ptr(), st,
+                                             b[0].data_ptr(), b[1].data_ptr(), st, ctx.relin_key.data_ptr(),
+                                             o0, o1, ostride, ws.data_ptr(), ws.numel(), stream)
+
+        for target in (a[0], a[1], b[0], b[1]):
+            assert call(target.data_ptr(), fresh[1].data_ptr(), st) == nat.HCK_ERR_ARG
+            assert call(fresh[0].data_ptr(), target.data_ptr(), st) == nat.HCK_ERR_ARG
+        assert call(a[0, 0, 1].data_ptr(), fresh[1].data_ptr(), st) == nat.HCK_ERR_ARG  # shifted by one limb
+        assert call(fresh[0].data_ptr(), fresh[0, 0, 1].data_ptr(), (limbs - 1) * N) == nat.HCK_ERR_ARG
+        rc = lib.hck_mul_relin_rescale_postop(ctx.handle, limbs, B, a[0].data_ptr(), a[1].data_ptr(), st,
+                                              b[0].data_ptr(), b[1].data_ptr(), st, ctx.relin_key.data_ptr(), 1,
+                                              None, None, 0, None, b[1].data_ptr(), fresh[1].data_ptr(), st,
+                                              ws.data_ptr(), ws.numel(), stream)
+        assert rc == nat.HCK_ERR_ARG
+        x = [ctx.empty(limbs, N) for _ in range(4)]
+        w = torch.zeros(2, limbs, dtype=torch.uint64, device="cuda")
+        lws = ctx.workspace(lib.hck_lincomb_rescale_workspace_bytes(ctx.handle, limbs, 2))
+        outs = [ctx.empty(limbs - 1, N), x[2]]  # group 1 writes over group 1's first input
+        rc = lib.hck_lincomb_rescale(ctx.handle, limbs, 2, 2, nat.ptr_array([t.data_ptr() for t in x]), w.data_ptr(),
+                                     nat.ptr_array([o.data_ptr() for o in outs]), None, 0, lws.data_ptr(),
+                                     lws.numel(), stream)
+        assert rc == nat.HCK_ERR_ARG
+        outs = [x[3], ctx.empty(limbs - 1, N)]  # group 0 writes over group 1's input
+        rc = lib.hck_lincomb_rescale(ctx.handle, limbs, 2, 2, nat.ptr_array([t.data_ptr() for t in x]), w.data_ptr(),
+                                     nat.ptr_array([o.data_ptr() for o in outs]), None, 0, lws.data_ptr(),
+                                     lws.numel(), stream)
+        assert rc == nat.HCK_ERR_ARG
+        torch.cuda.synchronize()
+    finally:
+        ctx.set_conversion_engine("mfma")
+
+
 def test_lincomb_matches_oracle(env):
     """Pointer-list linear combinations (hck_lincomb): operands at different levels in separate
     allocations, weighted (against the oracle's weighted sum per group) and unit weights (against
