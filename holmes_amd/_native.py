@@ -40,6 +40,7 @@ SIGNATURES = {
     "hck_context_destroy": (None, [_vp]),
     "hck_context_info": (_i, [_vp, _ip, _ip, _ip, _ip]),
     "hck_context_twiddles": (_i, [_vp, _i, _i, _u64p]),
+    "hck_context_root_tables": (_i, [_vp, _vp, _vp]),
     "hck_error_string": (ctypes.c_char_p, [_i]),
     "hck_context_set_ks_slices": (_i, [_vp, _i]),
     "hck_context_set_ks_streams": (_i, [_vp, _i, _i]),
@@ -100,6 +101,9 @@ SIGNATURES = {
                                  ctypes.c_uint64, _vp, _sz, _vp]),
     "hck_modraise_workspace_bytes": (_sz, [_vp, _i, _i]),
     "hck_modraise": (_i, [_vp, _i, _i, _vp, _i64, _vp, _i64, _vp, _sz, _vp]),
+    # the reference sidecar's encode entry (argtypes of bench/cmp/holmes_fast_stage2.py:37)
+    "holmes_encode_stage2": (_i, [_vp, _vp, ctypes.c_longlong, _i, ctypes.c_double, _i, _vp, _vp, _vp, _vp, _vp, _vp,
+                                  _vp, _i, _i, _i]),
 }
 
 _lib = None

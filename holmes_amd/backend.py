@@ -349,7 +349,7 @@ def create_sim_context(sim_cfg: SimulatorConfig, *, input_dim: int, block_out: i
         depth=int(sim_cfg.maxLevelsRemaining), log_n=int(sim_cfg.logN), dnum=int(sim_cfg.dnum),
         dcrt_bits=int(sim_cfg.dcrtBits), first_mod=int(sim_cfg.firstMod),
         secret_key_dist=str(sim_cfg.secretKeyDist), scale_mode="fixed", rescale_policy=sim_cfg.rescale_policy(),
-        rotations=tuple(sorted(wanted)), auto_load_keys=True, scale_bits=int(sim_cfg.scaleBits))
+        rotations=tuple(sorted(wanted)), auto_load_keys=True, scale_bits=sim_cfg.scale_bits())
     t0 = time.perf_counter()
     client, context = fhe.generate_client_context(spec, device=str(sim_cfg.device))
     elapsed = time.perf_counter() - t0

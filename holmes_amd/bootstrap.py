@@ -704,12 +704,18 @@ def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: Boo
     subtracted from 2^p first, then 2^-p multiplies the result back (encoded at the prime the
     rescale drops, so the scale is the input's exactly).  The second pass's own error is divided
     by 2^p.  A ValueError in the second pass (too few levels) returns the first result, as the
-    reference does."""
+    reference does.
+
+    ``iterations=3`` (this build's extension; the reference stops at two) adds one more pass at the
+    same output level: the remaining error out - x, scaled by 2^(2p), is bootstrapped, brought back
+    by 2^(-2p) (one scalar product and rescale of the correction term only, so the scalar's rounding
+    touches a term 2^(2p) below the message), and subtracted.  A refresh whose output error a later
+    series amplifies (an inverse square root near its interval's lower end) uses it."""
 
     ctx = context
     iterations = int(iterations)
-    if iterations not in (1, 2):
-        raise ValueError("bootstrap iterations must be one or two")
+    if iterations not in (1, 2, 3):
+        raise ValueError("bootstrap iterations must be one, two or three")
     first = bootstrap(cipher, ctx, program, bound_bits=bound_bits)
     if iterations == 1 or int(first.state.cur_limbs) <= int(cipher.state.cur_limbs):
         return first
@@ -727,9 +733,27 @@ def bootstrap_with_correction(cipher: Cipher, context: CKKSContext, program: Boo
         back = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
                                  scaling_factor=float(ctx.rescale_divisor_at(limbs)) * 2.0**-p, context=ctx)
         out = fhe.homo_mul_scalar_rescale(corrected, back, ctx)
-        return out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(cipher.state.scaling_factor)))
+        out = out.cipher_like(out.cv, state=out.state.replace(scaling_factor=float(cipher.state.scaling_factor)))
     except ValueError:
         return first
+    if iterations == 2:
+        return out
+    try:
+        scale2 = 1 << (2 * p)
+        rest = fhe.homo_sub(_times_integer(fhe.align_to(out, cipher.state, ctx), scale2, ctx),
+                            _times_integer(cipher, scale2, ctx), ctx)
+        error = bootstrap(rest, ctx, program, bound_bits=bound_bits)
+        limbs = int(error.state.cur_limbs)
+        back = fhe.encode_scalar(1.0, cur_limbs=limbs, scale_degree=1,
+                                 scaling_factor=float(ctx.rescale_divisor_at(limbs)) * 2.0**(-2 * p), context=ctx)
+        term = fhe.homo_mul_scalar_rescale(error, back, ctx)
+        term = term.cipher_like(term.cv, state=term.state.replace(scaling_factor=float(cipher.state.scaling_factor)))
+        lv = min(int(out.state.cur_limbs), int(term.state.cur_limbs))
+        out = fhe.align_to(out, out.state.replace(cur_limbs=lv), ctx)
+        term = fhe.align_to(term, term.state.replace(cur_limbs=lv), ctx)
+        return fhe.homo_sub(out, term, ctx)
+    except ValueError:
+        return out
 
 
 # ---------------------------------------------------------------------------- graph replay

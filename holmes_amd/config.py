@@ -1,8 +1,9 @@
-"""CKKS run configuration with the field names of llama3fhe/config.py:15-42 (``SimulatorConfig``).
-
-Field names are the interface (configuration files and callers set them by name); the defaults are
-set for this backend's FP64 arithmetic path (50-bit primes, scale 2^40).  Both rescale techniques
-of the reference map onto a policy name: FIXEDMANUAL -> "manual", FIXEDAUTO -> "auto".
+"""CKKS run configuration with the field names and defaults of llama3fhe/config.py:15-42
+(``SimulatorConfig``): depth 37, 59-bit primes with a 60-bit first modulus, dnum 3 -- a
+default-constructed configuration builds the reference's chain (on this backend's 64-bit integer
+path).  ``scaleBits`` is this backend's addition: the fixed scale 2^scaleBits, 0 meaning 2^dcrtBits
+(the reference's fixed scale follows dcrtBits).  Both rescale techniques of the reference map onto
+a policy name: FIXEDMANUAL -> "manual", FIXEDAUTO -> "auto".
 """
 
 from __future__ import annotations
@@ -20,15 +21,20 @@ _POLICY_ALIASES = {
 @dataclass
 class SimulatorConfig:
     logN: int = 16
-    maxLevelsRemaining: int = 23
+    maxLevelsRemaining: int = 37
     level_budget: tuple[int, int] = (4, 4)
     dnum: int = 3
-    dcrtBits: int = 50
-    firstMod: int = 50
+    dcrtBits: int = 59
+    firstMod: int = 60
     secretKeyDist: str = "SPARSE_TERNARY"
     rescaleTech: str = "FIXEDMANUAL"
     device: str = "cuda"
-    scaleBits: int = 40
+    scaleBits: int = 0
+
+    def scale_bits(self) -> int:
+        """log2 of the fixed scale: scaleBits, or dcrtBits when scaleBits is 0."""
+
+        return int(self.scaleBits) if int(self.scaleBits) else int(self.dcrtBits)
 
     def rescale_policy(self) -> str:
         """"manual" or "auto" for the configured rescale technique."""

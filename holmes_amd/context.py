@@ -106,8 +106,73 @@ def _stream_ptr(device) -> int:
     return int(torch.cuda.current_stream(device).cuda_stream)
 
 
+# EasyFHE's Encode.cu constant MAX_64BIT_VALUE: the encode sidecar stores a negative coefficient c
+# as MAX + c and subtracts MAX mod p after the reduction (bench/cmp/kernels/holmes_encode.cu:15,133-159).
+_MAX64 = 9223372036854775295
+
+
+class ResidueTable(list):
+    """A table of residues or moduli as Python ints (host arithmetic indexes and slices it like a
+    list) with a device copy: ``data_ptr()`` is the address of a uint64 tensor of the same values on
+    the context's device, which is how the reference's ctypes bindings pass EasyFHE's context
+    tables (``ctx.primes.data_ptr()``, bench/cmp/holmes_multi_mac.py:139)."""
+
+    def __init__(self, values, device):
+        super().__init__(int(v) for v in values)
+        self._device = device
+        self._tensor = None
+
+    @property
+    def tensor(self) -> torch.Tensor:
+        if self._tensor is None:
+            self._tensor = torch.tensor(np.array(list(self), dtype=np.uint64), device=self._device)
+        return self._tensor
+
+    def data_ptr(self) -> int:
+        return int(self.tensor.data_ptr())
+
+
+class _PerLimbTables:
+    """``table[limbs]``: a device uint64 tensor over q_0 .. q_(limbs-1) followed by the K special
+    primes, built once per limb count -- the shape of EasyFHE's ``QplusP_map`` family
+    (bench/cmp/holmes_fast_stage2.py:74-77)."""
+
+    def __init__(self, ctx: "CKKSContext", value_of):
+        self._ctx, self._value_of, self._cache = ctx, value_of, {}
+
+    def __getitem__(self, limbs: int) -> torch.Tensor:
+        limbs = int(limbs)
+        if not 1 <= limbs <= self._ctx.L:
+            raise KeyError(f"limb count {limbs} outside [1, {self._ctx.L}]")
+        hit = self._cache.get(limbs)
+        if hit is None:
+            primes = list(self._ctx.q_primes[:limbs]) + list(self._ctx.p_primes)
+            vals = np.array([self._value_of(int(p)) for p in primes], dtype=np.uint64)
+            hit = self._cache[limbs] = torch.tensor(vals, device=self._ctx.device)
+        return hit
+
+
+def barrett_k(p: int) -> int:
+    """The Barrett shift of EasyFHE's tables: floor(log2 p) + 63 (bench/cmp/kernels/holmes_mac.cu:56-58)."""
+
+    return int(p).bit_length() - 1 + 63
+
+
+def barrett_ratio(p: int) -> int:
+    """floor(2^k / p) with k = barrett_k(p), below 2^64 (bench/cmp/kernels/holmes_mac.cu:56-58)."""
+
+    return (1 << barrett_k(p)) // int(p)
+
+
 class CKKSContext:
-    """Prime chain + device tables (libholmes_ckks context) + evaluation keys in HBM."""
+    """Prime chain + device tables (libholmes_ckks context) + evaluation keys in HBM.
+
+    Besides the host lists the library needs, the context carries EasyFHE's native-context tables
+    as device uint64 tensors, with the reference's definitions, so code that binds them by address
+    runs unchanged: ``primes`` (Q then P; a ResidueTable, so ``primes.data_ptr()``), ``barret_ratio``
+    and ``barret_k`` (per prime), ``PModq`` (P mod q_i), ``QplusP_map`` /
+    ``QmaxdiffplusPmaxdiff_map`` / ``QbarretRatioplusPbarretRatio_map`` / ``QbarretKplusPbarretK_map``
+    (per limb count) and ``power_of_roots`` / ``power_of_roots_shoup`` ([L + K][N])."""
 
     def __init__(self, spec: CKKSContextSpec, device: str = "cuda"):
         spec.validate()
@@ -121,7 +186,7 @@ class CKKSContext:
         self.max_slots = self.N // 2
         q, p = spec.prime_chain()
         self.q_primes, self.p_primes = q, p
-        self.primes = q + p
+        self.primes = ResidueTable(q + p, self.device)
         self.L = len(q)
         self.K = len(p)
         self.alpha = spec.alpha
@@ -142,6 +207,71 @@ class CKKSContext:
         self._ws: torch.Tensor | None = None
         self.rotation_keys: dict[int, torch.Tensor] = {}
         self.relin_key: torch.Tensor | None = None
+
+    # ------------------------------------------------------------------ EasyFHE's native tables
+    @property
+    def barret_ratio(self) -> torch.Tensor:
+        return self._table("barret_ratio", lambda: [barrett_ratio(p) for p in self.primes])
+
+    @property
+    def barret_k(self) -> torch.Tensor:
+        return self._table("barret_k", lambda: [barrett_k(p) for p in self.primes])
+
+    @property
+    def PModq(self) -> torch.Tensor:  # noqa: N802 -- EasyFHE's attribute name
+        P = 1
+        for p in self.p_primes:
+            P *= int(p)
+        return self._table("PModq", lambda: [P % int(q) for q in self.q_primes])
+
+    @property
+    def QplusP_map(self) -> _PerLimbTables:  # noqa: N802
+        return self._limb_tables("QplusP_map", lambda p: p)
+
+    @property
+    def QmaxdiffplusPmaxdiff_map(self) -> _PerLimbTables:  # noqa: N802
+        return self._limb_tables("QmaxdiffplusPmaxdiff_map", lambda p: _MAX64 % p)
+
+    @property
+    def QbarretRatioplusPbarretRatio_map(self) -> _PerLimbTables:  # noqa: N802
+        return self._limb_tables("QbarretRatioplusPbarretRatio_map", barrett_ratio)
+
+    @property
+    def QbarretKplusPbarretK_map(self) -> _PerLimbTables:  # noqa: N802
+        return self._limb_tables("QbarretKplusPbarretK_map", barrett_k)
+
+    @property
+    def power_of_roots(self) -> torch.Tensor:
+        return self._root_tables()[0]
+
+    @property
+    def power_of_roots_shoup(self) -> torch.Tensor:
+        return self._root_tables()[1]
+
+    def _table(self, name: str, values) -> torch.Tensor:
+        cache = self.__dict__.setdefault("_native_tables", {})
+        if name not in cache:
+            cache[name] = torch.tensor(np.array(values(), dtype=np.uint64), device=self.device)
+        return cache[name]
+
+    def _limb_tables(self, name: str, value_of) -> _PerLimbTables:
+        cache = self.__dict__.setdefault("_native_tables", {})
+        if name not in cache:
+            cache[name] = _PerLimbTables(self, value_of)
+        return cache[name]
+
+    def _root_tables(self) -> tuple[torch.Tensor, torch.Tensor]:
+        """psi^brv(k) and its Shoup companions floor(w 2^64 / p), [L + K][N] each (hck_context_root_tables)."""
+
+        cache = self.__dict__.setdefault("_native_tables", {})
+        if "roots" not in cache:
+            roots = torch.empty(len(self.primes), self.N, dtype=torch.uint64, device=self.device)
+            shoup = torch.empty_like(roots)
+            with torch.cuda.device(self.device):
+                nat.check(nat.lib().hck_context_root_tables(self._h, roots.data_ptr(), shoup.data_ptr()),
+                          "hck_context_root_tables")
+            cache["roots"] = (roots, shoup)
+        return cache["roots"]
 
     # ------------------------------------------------------------------ lifetime
     def close(self) -> None:

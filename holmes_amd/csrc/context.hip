@@ -14,6 +14,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "modarith64.hpp"
 #include "wide.hpp"
 
 using u64 = uint64_t;
@@ -409,6 +410,21 @@ extern "C" int hck_context_twiddles(const hck_context* ctx, int prime_idx, int i
   if (e != hipSuccess) return (int)e;
   for (size_t k = 0; k < n; ++k) out[k] = (uint64_t)tmp[k];
   return HCK_OK;
+}
+
+extern "C" int hck_context_root_tables(const hck_context* ctx, uint64_t* roots, uint64_t* roots_shoup) {
+  if (!ctx || !roots || !roots_shoup) return HCK_ERR_ARG;
+  const size_t n = (size_t)1 << ctx->log_n, total = (size_t)ctx->np * n;
+  std::vector<uint64_t> w(total), ws(total);
+  for (int i = 0; i < ctx->np; ++i) {
+    const int rc = hck_context_twiddles(ctx, i, 0, w.data() + (size_t)i * n);
+    if (rc) return rc;
+    const uint64_t p = ctx->primes[i];
+    for (size_t k = 0; k < n; ++k) ws[(size_t)i * n + k] = hck::shoup_companion(w[(size_t)i * n + k], p);
+  }
+  hipError_t e = hipMemcpy(roots, w.data(), total * 8, hipMemcpyHostToDevice);
+  if (e == hipSuccess) e = hipMemcpy(roots_shoup, ws.data(), total * 8, hipMemcpyHostToDevice);
+  return e == hipSuccess ? HCK_OK : (int)e;
 }
 
 extern "C" int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, int* num_p, int* alpha) {

@@ -19,6 +19,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 namespace hck {
 namespace {
@@ -223,4 +224,21 @@ extern "C" int hck_encode(const hck_context* ctx, const double* values, const do
   HCK_CHECK_LAUNCH();
   // rounding, residues and the NTT's column pass in one kernel, then the row pass
   return hck::launch_encode_ntt(ctx, vre, vim, scale, out, out_row_stride, rows, overflow_flags, L, s);
+}
+
+// The reference's encode sidecar entry point with its argument list (bench/cmp/kernels/
+// holmes_encode.cu:240-285, bound by bench/cmp/holmes_fast_stage2.py:37).  The per-limb Barrett
+// tables (diffs, ratios, ks) and the launch-shape knobs (limbs_per_block, parts bit 2) belong to the
+// sidecar's own kernels and are accepted but not read: residues are reduced exactly by `primes`.
+extern "C" int holmes_encode_stage2(void* out, const void* in, long long in_stride, int rows, double sf, int limbs,
+                                    const void* primes, const void* diffs, const void* ratios, const void* ks,
+                                    const void* roots, const void* roots_shoup, void* stream, int rows_per_launch,
+                                    int parts, int limbs_per_block) {
+  (void)diffs;
+  (void)ratios;
+  (void)ks;
+  (void)limbs_per_block;
+  return hck::encode_stage2((uint64_t*)out, (const double*)in, in_stride, rows, sf, limbs, (const uint64_t*)primes,
+                            (const uint64_t*)roots, (const uint64_t*)roots_shoup, rows_per_launch, parts,
+                            (hipStream_t)stream);
 }

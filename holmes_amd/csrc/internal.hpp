@@ -111,7 +111,7 @@ int launch_ntt_inv(const hck_context* c, const void* src, Fmt in, void* dst, Fmt
                    long long src_stride, long long dst_stride, const LimbList& list, hipStream_t s);
 // Encode's rounding fused with the forward NTT: vre / vim are the special IFFT's [rows][N/2]
 // outputs (natural slot order); out gets rows NTT-domain polys over `list`, overflow[row] set when a
-// rounded coefficient reaches 2^52.
+// rounded coefficient reaches 2^61.
 int launch_encode_ntt(const hck_context* c, const double* vre, const double* vim, double scale, uint64_t* out,
                       long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s);
 

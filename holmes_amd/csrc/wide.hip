@@ -527,7 +527,91 @@ __global__ __launch_bounds__(256) void wk_encode_round(const double* __restrict_
   }
 }
 
+// ------------------------------------------------------------------- the encode sidecar's stage 2
+// Rows of the special IFFT's output as interleaved doubles (slot j: Re at 2 j, Im at 2 j + 1);
+// coefficient n < N/2 is Re of slot n, n >= N/2 is Im of slot n - N/2 (bench/cmp/kernels/
+// holmes_encode.cu:108-111), times sf, rounded half away from zero, reduced exactly by each limb's
+// prime, then the forward NTT's column pass with the caller's root table (psi^brv(k) and Shoup
+// companions, limb e at e * N).  A coefficient of magnitude 2^63 or more encodes as 0.  Grid
+// (16, limbs, rows): 16 columns of one limb of one row per block; wk_fwd_rows finishes the NTT.
+__global__ __launch_bounds__(kWT) void wk_stage2_cols(const double* __restrict__ in, long long in_stride, double sf,
+                                                      u64* __restrict__ out, int limbs, const u64* __restrict__ primes,
+                                                      const u64* __restrict__ roots, const u64* __restrict__ roots_s) {
+  __shared__ u64 sh[256 * 16];
+  const int e = blockIdx.y;
+  const long long row = blockIdx.z;
+  const u64 p = primes[e];
+  const u64* tw = roots + (size_t)e * kN;
+  const u64* tws = roots_s + (size_t)e * kN;
+  const double* src = in + row * in_stride;
+  u64* o = out + (row * limbs + e) * (long long)kN;
+  const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int k = r + 16 * m;
+    const int n = c + 256 * k;
+    const double v = src[n < kN / 2 ? 2 * n : 2 * (n - kN / 2) + 1];
+    double a;
+    {
+#pragma clang fp contract(off)
+      a = round_away(v * sf);
+    }
+    const u64 mag = fabs(a) < 9223372036854775808.0 ? (u64)fabs(a) % p : 0;
+    sh[k * 16 + cl] = (a < 0 && mag) ? p - mag : mag;
+  }
+  __syncthreads();
+  for (int st = 0; st < 8; ++st) {
+    const int m = 1 << st, t = 128 >> st;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int b = r + 16 * u;
+      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
+      const int wi = m + b / t;
+      const u64 x = sh[k1 * 16 + cl];
+      const u64 y = wmulc(sh[k2 * 16 + cl], tw[wi], tws[wi], p);
+      sh[k1 * 16 + cl] = wadd(x, y, p);
+      sh[k2 * 16 + cl] = wsub(x, y, p);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    const int k = r + 16 * m;
+    o[c + 256 * k] = sh[k * 16 + cl];
+  }
+}
+
 }  // namespace
+
+int encode_stage2(uint64_t* out, const double* in, long long in_stride, int rows, double sf, int limbs,
+                  const uint64_t* primes, const uint64_t* roots, const uint64_t* roots_shoup, int rows_per_launch,
+                  int parts, hipStream_t s) {
+  if (rows <= 0 || limbs <= 0) return HCK_OK;
+  if (!out || !in || !primes || !roots || !roots_shoup || limbs > kMaxList) return HCK_ERR_ARG;
+  if (rows > 1 && in_stride < kN) return HCK_ERR_ARG;
+  // the row pass reads the caller's tables through the wide kernels' table view
+  WideTables T{};
+  T.p = primes;
+  T.fwd = roots;
+  T.fwd_s = roots_shoup;
+  LimbList list;
+  list.n = limbs;
+  for (int e = 0; e < limbs; ++e) {
+    list.off[e] = (uint16_t)e;
+    list.prime[e] = (uint8_t)e;
+  }
+  const int step = rows_per_launch > 0 && rows_per_launch < 65535 ? rows_per_launch : 65535;
+  for (int r0 = 0; r0 < rows; r0 += step) {
+    const int nr = rows - r0 < step ? rows - r0 : step;
+    u64* o = out + (long long)r0 * limbs * kN;
+    if (parts & 1)
+      wk_stage2_cols<<<dim3(16, limbs, nr), kWT, 0, s>>>(in + (long long)r0 * in_stride, in_stride, sf, o, limbs,
+                                                         primes, roots, roots_shoup);
+    if (parts & 2) wk_fwd_rows<<<dim3(16, limbs, nr), kWT, 0, s>>>(o, (long long)limbs * kN, list, T);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
 
 // ======================================================================================= set-up
 u64 primitive_root_2n(u64 q, int log_n);  // context.hip: the root choice every table shares

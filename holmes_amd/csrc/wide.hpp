@@ -95,4 +95,10 @@ int wide_bsgs_mac(const hck_context* c, int limbs, const int* prime_idx, int inp
                   const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, long long baby_stride,
                   const uint64_t* pts, long long pt_stride, uint64_t* res, hipStream_t s);
 
+// holmes_encode_stage2's body: the caller's tables (primes [limbs], roots / roots_shoup [>= limbs][N]),
+// any prime below 2^61; parts bit 0 runs the rounding + column pass, bit 1 the row pass.
+int encode_stage2(uint64_t* out, const double* in, long long in_stride, int rows, double sf, int limbs,
+                  const uint64_t* primes, const uint64_t* roots, const uint64_t* roots_shoup, int rows_per_launch,
+                  int parts, hipStream_t s);
+
 }  // namespace hck

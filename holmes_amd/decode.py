@@ -105,12 +105,13 @@ class DecodeSpec:
 
 @dataclass(frozen=True)
 class DecodePolynomials:
-    """Chebyshev series (numpy convention, argument in [-1, 1]) of the layer's approximations."""
+    """Chebyshev series (numpy convention, argument in [-1, 1]) of the layer's approximations, or
+    (``exact``) the functions themselves."""
 
-    rms: np.ndarray
-    exp: np.ndarray
-    rsqrt: np.ndarray
-    silu: np.ndarray
+    rms: object
+    exp: object
+    rsqrt: object
+    silu: object
 
     @classmethod
     def fit(cls, spec: DecodeSpec) -> "DecodePolynomials":
@@ -121,8 +122,22 @@ class DecodePolynomials:
                    silu=chebyshev_coefficients(lambda x: x / (1.0 + np.exp(-x)), spec.silu_degree,
                                                spec.silu_interval))
 
+    @classmethod
+    def exact(cls, spec: DecodeSpec) -> "DecodePolynomials":
+        """The functions the series approximate, in their place: the float64 model then computes a
+        textbook Llama-3 layer (the softmax map makes (y lambda)^2 = exp(s / sqrt(d)) / sum)."""
+
+        eps = float(spec.eps)
+        return cls(rms=lambda m: 1.0 / np.sqrt(m + eps), exp=np.exp, rsqrt=lambda r: 1.0 / np.sqrt(r),
+                   silu=lambda x: x / (1.0 + np.exp(-x)))
+
 
 def _cheb(x, coeffs, interval):
+    """The series on ``interval`` at x; a callable in place of the coefficients is the exact function
+    it approximates, evaluated at x itself (the float64 models' exact mode)."""
+
+    if callable(coeffs):
+        return coeffs(np.asarray(x, dtype=np.float64))
     a, b = (float(v) for v in interval)
     return np.polynomial.chebyshev.chebval((2.0 * np.asarray(x) - (a + b)) / (b - a), coeffs)
 
@@ -705,23 +720,23 @@ class CipherOps:
         ev = PSEvaluator(self.ctx, ct, self.limbs(ct), self.scale(ct), len(coeffs) - 1, self.ctx.q_primes)
         return ev.evaluate(coeffs)
 
-    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False, program=None):
+    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False, program=None, iterations: int = 2):
         """Two-pass bootstrap (|slots| <= 2^bound_bits); ``deep`` uses the program that leaves more
-        levels, ``program`` any other."""
+        levels, ``program`` any other; ``iterations`` 3 adds the third correction pass."""
 
         prog = program if program is not None else (self.deep_program if deep else self.program)
         self.refreshes += int(ct.batch_size)
         if self.graph_refresh and int(ct.batch_size) <= self.GRAPH_REFRESH_MAX_BATCH:
             st = ct.state
             key = (id(prog), int(ct.batch_size), int(st.cur_limbs), int(st.scale_degree), float(st.scaling_factor),
-                   int(bound_bits))
+                   int(bound_bits), int(iterations))
             hit = self._graphs.get(key)
             if hit is None or hit[0] is not prog:
-                hit = self._graphs[key] = (prog, self._bs.RefreshGraph(self.ctx, prog, ct, iterations=2,
+                hit = self._graphs[key] = (prog, self._bs.RefreshGraph(self.ctx, prog, ct, iterations=int(iterations),
                                                                        precision_bits=12, bound_bits=int(bound_bits)))
             out = hit[1](ct)
         else:
-            out = self._bs.bootstrap_with_correction(ct, self.ctx, prog, iterations=2, precision_bits=12,
+            out = self._bs.bootstrap_with_correction(ct, self.ctx, prog, iterations=int(iterations), precision_bits=12,
                                                      bound_bits=int(bound_bits))
         self.refresh_levels.append((self.limbs(ct), self.limbs(out)))
         return out

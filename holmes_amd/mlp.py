@@ -95,16 +95,27 @@ def _page(weight: np.ndarray, p: int, D: int, rows: bool) -> np.ndarray:
 
 
 def mlp_block_numpy(x: np.ndarray, gate: np.ndarray, up: np.ndarray, down: np.ndarray,
-                    norm_weight: np.ndarray | None = None, spec: MLPBlockSpec = MLPBlockSpec()) -> np.ndarray:
-    """float64 oracle of the block with the same polynomials (bootstrap excluded: exact)."""
+                    norm_weight: np.ndarray | None = None, spec: MLPBlockSpec = MLPBlockSpec(), *,
+                    exact: bool = False, functions: dict | None = None) -> np.ndarray:
+    """float64 oracle of the block with the same polynomials (bootstrap excluded: exact);
+    ``exact`` puts 1 / sqrt(m + eps) and x sigma(x) in place of the series (a textbook SwiGLU),
+    ``functions`` ({"rms": f, "silu": g}) any other function in place of either series."""
 
-    rms = rmsnorm_coefficients(spec.rms_degree, spec.rms_interval, spec.eps)
+    eps = float(spec.eps)
+    fn = dict(functions or {})
+    if exact:
+        fn.setdefault("rms", lambda m: 1.0 / np.sqrt(m + eps))
+        fn.setdefault("silu", lambda v: v / (1.0 + np.exp(-v)))
+    rms = {"function": fn["rms"]} if "rms" in fn else rmsnorm_coefficients(spec.rms_degree, spec.rms_interval, eps)
     y = rmsnorm_numpy(x, norm_weight, rms)
     g = y @ np.asarray(gate, dtype=np.float64).T
     u = y @ np.asarray(up, dtype=np.float64).T
-    a, b = spec.silu_interval
-    s = np.polynomial.chebyshev.chebval((2.0 * g - (a + b)) / (b - a), silu_coefficients(spec.silu_degree,
-                                                                                        spec.silu_interval))
+    if "silu" in fn:
+        s = fn["silu"](g)
+    else:
+        a, b = spec.silu_interval
+        s = np.polynomial.chebyshev.chebval((2.0 * g - (a + b)) / (b - a), silu_coefficients(spec.silu_degree,
+                                                                                            spec.silu_interval))
     return (s * u) @ np.asarray(down, dtype=np.float64).T
 
 

@@ -51,12 +51,16 @@ def rmsnorm_coefficients(degree: int = 15, interval=(0.5, 2.0), eps: float = 1e-
 
 
 def rmsnorm_numpy(x: np.ndarray, weight: np.ndarray | None, coeffs: dict) -> np.ndarray:
-    """The same computation in float64 with the same polynomial (the decrypted-output oracle)."""
+    """The same computation in float64 with the same polynomial (the decrypted-output oracle); a
+    ``{"function": f}`` dictionary evaluates f(mean square) instead (exact mode)."""
 
     x = np.asarray(x, dtype=np.float64)
-    lo, hi = coeffs["fit_interval"]
     m = np.mean(x * x, axis=1, keepdims=True)
-    r = np.polynomial.chebyshev.chebval((2.0 * m - (lo + hi)) / (hi - lo), series_from_entry(coeffs))
+    if "function" in coeffs:   # exact mode: the function the series approximates
+        r = coeffs["function"](m)
+    else:
+        lo, hi = coeffs["fit_interval"]
+        r = np.polynomial.chebyshev.chebval((2.0 * m - (lo + hi)) / (hi - lo), series_from_entry(coeffs))
     y = x * r
     return y if weight is None else y * np.asarray(weight, dtype=np.float64)[None, :]
 

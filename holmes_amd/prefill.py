@@ -84,11 +84,17 @@ class PrefillSpec:
     silu_degree: int = 63
     silu_interval: tuple = (-16.0, 16.0)
     # refresh input bounds |slot| <= 2^bits (a two-pass refresh leaves about 2^(bits - 25)): the
-    # steady layer's input is a previous layer's output (|out| near 14 on the synthetic workload);
+    # steady layer's input is a previous layer's output (|out| below 14.3 on the synthetic workload);
     # the residual h before the MLP block stays below 7.7 there, and the block multiplies its
     # refresh error about tenfold, so its bound is the tighter one
-    input_bound_bits: int = 5
+    input_bound_bits: int = 4
     residual_bound_bits: int = 4
+    # correction passes of the steady layer's series-input refreshes: the inverse square root's
+    # input z maps R / n in [0.9, 128] onto [-1, 1], so near R / n = 1 an error in z moves lambda^2
+    # (hence every probability) about 64 times as much; a third pass takes that refresh's error from
+    # 2^-25 to below 2^-27
+    exp_refresh_iterations: int = 2
+    rsqrt_refresh_iterations: int = 3
 
     def validate(self) -> None:
         if (self.hidden_dim, self.query_heads, self.kv_heads, self.head_dim, self.seq_len) != (4096, 32, 8, 128, 128):
@@ -97,10 +103,10 @@ class PrefillSpec:
 
 @dataclass
 class PrefillPolynomials:
-    """Chebyshev series (numpy convention, argument in [-1, 1])."""
+    """Chebyshev series (numpy convention, argument in [-1, 1]), or the exact functions."""
 
-    exp: np.ndarray
-    rsqrt: np.ndarray
+    exp: object
+    rsqrt: object
 
     @classmethod
     def fit(cls, spec: PrefillSpec) -> "PrefillPolynomials":
@@ -203,19 +209,33 @@ def attention_numpy(xn: np.ndarray, w: DecodeWeights, spec: PrefillSpec,
 
 
 def prefill_layer_numpy(x: np.ndarray, w: DecodeWeights, spec: PrefillSpec,
-                        polys: PrefillPolynomials | None = None) -> dict:
-    """The whole layer in float64 with the layer's polynomials (the refresh is exact here)."""
+                        polys: PrefillPolynomials | None = None, *, exact: bool = False,
+                        functions: dict | None = None) -> dict:
+    """The whole layer in float64 with the layer's polynomials (the refresh is exact here);
+    ``exact`` puts the functions themselves in place of every series (RMSNorm's 1 / sqrt, exp,
+    the inverse square root, SiLU): a textbook Llama-3 layer.  ``functions`` replaces any of them
+    by name ("rms" for both RMSNorms, "exp", "rsqrt", "silu") with another function."""
 
     from .mlp import mlp_block_numpy
     from .norm import rmsnorm_coefficients, rmsnorm_numpy
 
     x = np.asarray(x, dtype=np.float64)
-    rms = rmsnorm_coefficients(spec.rms_degree, spec.rms_interval, spec.eps)
+    eps = float(spec.eps)
+    fn = dict(functions or {})
+    if exact:
+        fn.setdefault("rms", lambda m: 1.0 / np.sqrt(m + eps))
+        fn.setdefault("exp", np.exp)
+        fn.setdefault("rsqrt", lambda r: 1.0 / np.sqrt(r))
+        fn.setdefault("silu", lambda v: v / (1.0 + np.exp(-v)))
+    polys = PrefillPolynomials.fit(spec) if polys is None else polys
+    polys = PrefillPolynomials(exp=fn.get("exp", polys.exp), rsqrt=fn.get("rsqrt", polys.rsqrt))
+    rms = {"function": fn["rms"]} if "rms" in fn else rmsnorm_coefficients(spec.rms_degree, spec.rms_interval, eps)
     xn = rmsnorm_numpy(x, w.input_layernorm, rms)
     att = attention_numpy(xn, w, spec, polys)
     h = x + att["delta"]
     mspec = prefill_mlp_spec(spec)
-    out = h + mlp_block_numpy(h, w.gate_proj, w.up_proj, w.down_proj, w.post_attention_layernorm, mspec)
+    out = h + mlp_block_numpy(h, w.gate_proj, w.up_proj, w.down_proj, w.post_attention_layernorm, mspec,
+                              functions={k: fn[k] for k in ("rms", "silu") if k in fn})
     ms = np.mean(h * h, axis=1)
     res = {"output": out, "h": h, "xn": xn, **att}
     res["in_range"] = {**att["in_range"], "post_rms": bool(ms.min() >= spec.post_rms_interval[0]
@@ -404,6 +424,7 @@ class PrefillAttention:
         # from a refreshed layer input rather than a fresh encryption at the top of the chain
         # (the reference's refresh_softmax_exp_inputs, llama3fhe/graph/prefill.py:134-221)
         self.refresh_series_inputs = bool(refresh_series_inputs)
+        self._taps = None
         self.series_programs = dict(series_programs or {})  # "exp" / "rsqrt" -> program (default: ops')
         self.spec = PrefillSpec() if spec is None else spec
         self.spec.validate()
@@ -589,7 +610,9 @@ class PrefillAttention:
             return x
         ops = self.ops
         self._mark("attention_softmax")
-        x = ops.refresh(x, bound_bits=0, program=self.series_programs.get(which))
+        self._tap(f"{which}_in", x)
+        passes = self.spec.rsqrt_refresh_iterations if which == "rsqrt" else self.spec.exp_refresh_iterations
+        x = self._tap(which, ops.refresh(x, bound_bits=0, program=self.series_programs.get(which), iterations=passes))
         self._mark(f"attention_{which}_refresh")
         lim = ops.limbs(x) - 1
         return ops.adjust(x, lim, ops.ideal_scale(lim))
@@ -626,11 +649,18 @@ class PrefillAttention:
         sums = ops.mul_sum(col, right, [split(c) for c in range(CTS)])
         return ops.add(sums, ops.rotate(sums, HALF))
 
-    def forward(self, A, V, mark=None):
+    def _tap(self, name, ct):
+        if self._taps is not None:
+            self._taps[name] = ct
+        return ct
+
+    def forward(self, A, V, mark=None, taps: dict | None = None):
         """Attention output and its intermediates; ``mark(name)`` (optional) is called after the
-        scores, around each series-input refresh, and after the softmax and PV (stage timing)."""
+        scores, around each series-input refresh, and after the softmax and PV (stage timing);
+        ``taps`` (optional) receives each series refresh's input and output."""
 
         self._mark = mark if mark is not None else (lambda name: None)
+        self._taps = taps
         try:
             S2 = self.scores(A)
             self._mark("attention_scores")
@@ -640,6 +670,7 @@ class PrefillAttention:
             self._mark("attention_pv")
         finally:
             self._mark = lambda name: None
+            self._taps = None
         return out, {"scores": S2, "probs": P}
 
 
@@ -732,8 +763,10 @@ class PrefillLayer:
                                         norm_weight=weights.post_attention_layernorm, spec=self.mlp_spec,
                                         layout=self.layout, config=self.config, bootstrap_program=None)
 
-    def forward(self, x_cts):
-        """Layer output (16 ciphertexts) and the seconds of each stage."""
+    def forward(self, x_cts, taps: dict | None = None):
+        """Layer output (16 ciphertexts) and the seconds of each stage.  ``taps``, when given,
+        receives named intermediates (each refresh's input and output among them), so the error
+        each stage adds can be measured by decryption."""
 
         import torch
 
@@ -751,10 +784,16 @@ class PrefillLayer:
             t[name] = t.get(name, 0.0) + now - t0
             t0 = now
 
+        def tap(name, ct):
+            if taps is not None:
+                taps[name] = ct
+            return ct
+
         x_cts = tuple(x_cts)
         if self.steady:
-            x_cts = tuple(ops.items(ops.refresh(ops.batch(x_cts), bound_bits=self.spec.input_bound_bits,
-                                                program=self.programs.get("input"))))
+            xb = tap("input_in", ops.batch(x_cts))
+            x_cts = tuple(ops.items(tap("input", ops.refresh(xb, bound_bits=self.spec.input_bound_bits,
+                                                             program=self.programs.get("input")))))
             mark("refresh_input")
         xn = rmsnorm_fhe(x_cts, None, coeffs=self.rms, layout=self.layout, crypto_context=ctx).outputs
         mark("rmsnorm1")
@@ -765,7 +804,7 @@ class PrefillLayer:
         mark("qkv_projection")
         A, V = ops.batch(a_out), ops.batch(v_out)
         self.levels = {"input": ops.limbs(x_cts[0]), "rmsnorm1": ops.limbs(xn[0]), "A": ops.limbs(A)}
-        out, _ = self.attn.forward(A, V, mark=mark)
+        out, _ = self.attn.forward(A, V, mark=mark, taps=taps)
         self.levels["attention"] = ops.limbs(out)
         t["attention"] = sum(v for k, v in t.items() if k.startswith("attention_"))
         proj, _ = self.op.apply(ops.items(out), self.w_o)
@@ -776,12 +815,14 @@ class PrefillLayer:
         h = ops.add(x, delta)
         mark("w_o_residual")
         self.levels["residual"] = ops.limbs(h)
-        h = ops.refresh(h, bound_bits=self.spec.residual_bound_bits, program=self.programs.get("residual"))
+        tap("residual_in", h)
+        h = tap("residual", ops.refresh(h, bound_bits=self.spec.residual_bound_bits,
+                                        program=self.programs.get("residual")))
         mark("refresh")
         m_out, _ = self.mlp.forward(ops.items(h))
-        m = ops.batch(m_out)
+        m = tap("mlp", ops.batch(m_out))
         h2 = ops.adjust(h, ops.limbs(m), ops.scale(m))
-        out = ops.add(h2, m)
+        out = tap("output", ops.add(h2, m))
         self.levels["output"] = ops.limbs(out)
         ops.finish()
         mark("mlp_residual")

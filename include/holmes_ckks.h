@@ -27,6 +27,8 @@
  *                          gpu_packer.py:156-198)
  *   hck_encode             EasyFHE encode: special IFFT (cv_pre_encode_stage1) + holmes_encode_stage2
  *                          (round, reduce, NTT; holmes_encode.cu:240-285)
+ *   holmes_encode_stage2   holmes_encode_stage2 itself, with the sidecar's argument list
+ *                          (holmes_encode.cu:240-285; bound at bench/cmp/holmes_fast_stage2.py:37)
  *   hck_tensor / hck_relinearize / hck_mul_relin
  *                          fhe.homo_mul_no_relin / homo_relinearize / homo_mul_relin
  *                          (llama3fhe/operators/attention/prefill/qk.py:460-464,
@@ -70,6 +72,12 @@ void hck_context_destroy(hck_context* ctx);
 int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, int* num_p, int* alpha);
 /* Host copy of the root table psi^brv(k) (inverse: psi^-brv(k)) of prime `prime_idx` (N words). */
 int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uint64_t* out);
+/* The forward root tables of every prime of the context (Q primes, then P) written to the caller's
+ * device buffers, [num_q + num_p][N] uint64 each: roots[i][k] = psi_i^brv(k) and
+ * roots_shoup[i][k] = floor(roots[i][k] * 2^64 / p_i).  EasyFHE's context.power_of_roots /
+ * power_of_roots_shoup, the tables the encode sidecar is called with
+ * (bench/cmp/holmes_fast_stage2.py:74-82).  Synchronous (set-up, not the hot path). */
+int hck_context_root_tables(const hck_context* ctx, uint64_t* roots, uint64_t* roots_shoup);
 const char* hck_error_string(int code);
 /* Key-switch schedule of batched calls: 0 or 1 (default) runs the five key-switch kernels one after
  * another over the whole batch; s >= 2 cuts batches of at least 2 s items into s slices and runs
@@ -308,12 +316,31 @@ int hck_pack_diagonals(const hck_context* ctx, const double* weight, int dimensi
 /* Encode `rows` slot vectors at `scale` into NTT-domain residues out[row][l] (row stride
  * out_row_stride words, limb l modulo prime prime_idx[l]; Q then P primes gives an
  * extended-basis plaintext).  values / values_im: float64 [rows][N/2] real and imaginary parts
- * (values_im NULL: real input).  A coefficient of magnitude >= 2^52 sets overflow_flags[row]
- * (device int array, caller-zeroed). */
+ * (values_im NULL: real input).  A coefficient of magnitude >= 2^61 (the reference's encoder cap
+ * MAX_ENCODED_BITS) sets overflow_flags[row] (device int array, caller-zeroed). */
 size_t hck_encode_workspace_bytes(const hck_context* ctx, int rows);
 int hck_encode(const hck_context* ctx, const double* values, const double* values_im, int rows, double scale,
                int limbs, const int* prime_idx, uint64_t* out, int64_t out_row_stride, void* workspace,
                size_t workspace_bytes, int* overflow_flags, void* stream);
+
+/* The reference's encode sidecar, holmes_encode_stage2, with its argument list and return
+ * convention (bench/cmp/kernels/holmes_encode.cu:240-285; bound with the argtypes of
+ * bench/cmp/holmes_fast_stage2.py:37 and called as at :71-85).  out[rows][limbs][N] <- the forward
+ * NTT of round(in * sf) mod primes[l]: `in` holds each row's special-IFFT output as interleaved
+ * doubles (slot j: Re at 2 j, Im at 2 j + 1; row stride in_stride doubles), coefficient n < N/2
+ * takes Re of slot n and n >= N/2 Im of slot n - N/2, rounded half away from zero (llround).
+ * primes: device [limbs] (context.QplusP_map[limbs]); roots / roots_shoup: device [>= limbs][N]
+ * (context.power_of_roots(_shoup), hck_context_root_tables).  Any prime below 2^61.  diffs, ratios,
+ * ks (the sidecar's Barrett tables) and limbs_per_block are accepted and not read: residues are
+ * reduced exactly by primes[l].  rows_per_launch > 0 runs the rows in batches of that many; parts
+ * bit 0 runs the rounding and the NTT's column pass, bit 1 its row pass (3: the encode), bit 2 is
+ * ignored (one stream).  Coefficients must stay below 2^63 in magnitude (the encoder cap is 2^61);
+ * larger ones encode as 0.  Returns 0, HCK_ERR_ARG, or a hipError_t; rows <= 0 or limbs <= 0 is a
+ * no-op, as in the sidecar. */
+int holmes_encode_stage2(void* out, const void* in, long long in_stride, int rows, double sf, int limbs,
+                         const void* primes, const void* diffs, const void* ratios, const void* ks,
+                         const void* roots, const void* roots_shoup, void* stream, int rows_per_launch, int parts,
+                         int limbs_per_block);
 
 /* Tensor product of `batch` ciphertext pairs at level_limbs limbs (a = (a0, a1), b = (b0, b1), item
  * strides a_stride / b_stride): d0 = a0 b0, d1 = a0 b1 + a1 b0, d2 = a1 b1 — the three-component

@@ -643,6 +643,29 @@ int or_encode_real(const or_ctx* c, const double* values, double scale, int limb
   return rc;
 }
 
+/* Stage 1 alone, as the encode sidecar receives it (bench/cmp/kernels/holmes_encode.cu:108-111):
+ * out[2 k] = Re(w_k), out[2 k + 1] = Im(w_k), w_k = v[brv(k)] / n after the special IFFT of the
+ * real slot vector `values` -- the same IEEE sequence as or_encode_real, so rounding out * scale
+ * coefficient by coefficient gives that function's coefficients. */
+void or_encode_stage1(const or_ctx* c, const double* values, double* out) {
+  const int log_n = c->log_n;
+  const u64 n = c->n >> 1;
+  double* re = (double*)malloc(sizeof(double) * n);
+  double* im = (double*)calloc(n, sizeof(double));
+  double* twr = (double*)malloc(sizeof(double) * n);
+  double* twi = (double*)malloc(sizeof(double) * n);
+  memcpy(re, values, sizeof(double) * n);
+  or_encode_twiddles(log_n, twr, twi);
+  or_special_ifft(log_n, re, im, twr, twi);
+  const double inv_n = 1.0 / (double)n;
+  for (u64 k = 0; k < n; ++k) {
+    const u64 s = bitrev(k, log_n - 1);
+    out[2 * k] = re[s] * inv_n;
+    out[2 * k + 1] = im[s] * inv_n;
+  }
+  free(re); free(im); free(twr); free(twi);
+}
+
 /* Diagonal packing of the BSGS weight rows (llama3fhe/operators/linear/weight.py:122-154):
  * row (g, b) of a chunk, g = giant_base + gr, gr < giant_count, b < baby_steps:
  *   row[s] = W[(f - g B) mod D][(f + b + lane_shift * lane) mod D],  f = s / lanes, lane = s % lanes. */

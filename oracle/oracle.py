@@ -69,6 +69,7 @@ def lib():
         "or_encode_twiddles": (None, [i, _f64p, _f64p]),
         "or_special_ifft": (None, [i, _f64p, _f64p, _f64p, _f64p]),
         "or_encode_real": (i, [_vp, _f64p, ctypes.c_double, i, _i32p, i, _u64p]),
+        "or_encode_stage1": (None, [_vp, _f64p, _f64p]),
         "or_pack_diagonals": (None, [_f64p, i, i, i, i, i, i, i, _f64p]),
     }
     for name, (res, args) in sig.items():
@@ -249,6 +250,15 @@ class OracleContext:
         out = np.zeros((idx.size, self.n), dtype=np.uint64)
         rc = lib().or_encode_real(self._h, _p(values), float(scale), int(idx.size), _p(idx), int(bool(ntt)), _p(out))
         return out, rc == 0
+
+    def encode_stage1(self, values: np.ndarray) -> np.ndarray:
+        """The special IFFT's output w (interleaved Re, Im per slot; N doubles) that encode_real
+        rounds: the encode sidecar's stage-2 input (bench/cmp/kernels/holmes_encode.cu:108-111)."""
+
+        values = np.ascontiguousarray(values, dtype=np.float64)
+        out = np.empty(1 << self.log_n, dtype=np.float64)
+        lib().or_encode_stage1(self._h, _p(values), _p(out))
+        return out
 
     def tensor(self, limbs: int, a0, a1, b0, b1):
         """(a0 b0, a0 b1 + a1 b0, a1 b1) over the first ``limbs`` Q primes ([limbs][N] each)."""

@@ -211,7 +211,7 @@ class SlotOps:
         vals = np.polynomial.chebyshev.chebval(ct.values.real, coeffs) + 0j
         return SimCt(vals, out, canonical_scales(self.primes, l, s)[out])
 
-    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False, program=None):
+    def refresh(self, ct, *, bound_bits: int = 0, deep: bool = False, program=None, iterations: int = 2):
         prog = program if program is not None else (self.deep_program if deep else self.program)
         if self.limbs(ct) < 2:
             raise ValueError("bootstrap needs at least two limbs")

@@ -11,7 +11,8 @@ dnum 3, scale 2^50, sparse ternary secret of Hamming weight 192):
   its scaling factor and its slots within 2^-12 (measured: 2^-13.4 max, 2^-15 rms for random
   slots; the limit is EvalMod's rescale noise at scale 2^50, about 2^-29 after the double angles,
   against a message of 2^-8 q_0), a constant vector (one large coefficient: the sine's worst case)
-  likewise, and the two-pass correction of the reference within 2^-20.
+  likewise, the two-pass correction of the reference within 2^-20, and this build's third pass
+  below 2^-26.
 The oracle is not used here: the bootstrap is built from kernels whose bit-exact parity the other
 GPU tests check, so these tests check its mathematics through decryption.
 """
@@ -182,6 +183,23 @@ def test_two_pass_correction(env):
     e2 = float(np.max(np.abs(client.decrypt(two) - v)))
     print(f"one pass 2^{math.log2(e1):.1f}, two passes 2^{math.log2(e2):.1f}")
     assert e2 < 2.0**-20 and e2 < e1 / 64
+
+
+def test_three_pass_correction(env):
+    """The third correction pass (this build's extension) leaves the two-pass output level and the
+    input's scale, and cuts the error below the two-pass error."""
+    B, fhe, client, ctx, prog = env
+    rng = np.random.default_rng(22)
+    v = _slots(rng, ctx.max_slots)
+    ct = client.encrypt(v, cur_limbs=3)
+    two = B.bootstrap_with_correction(ct, ctx, prog, iterations=2, precision_bits=12)
+    three = B.bootstrap_with_correction(ct, ctx, prog, iterations=3, precision_bits=12)
+    assert three.state.cur_limbs == two.state.cur_limbs == prog.output_limbs - 1
+    assert three.state.scaling_factor == ct.state.scaling_factor
+    e2 = float(np.max(np.abs(client.decrypt(two) - v)))
+    e3 = float(np.max(np.abs(client.decrypt(three) - v)))
+    print(f"two passes 2^{math.log2(e2):.1f}, three passes 2^{math.log2(e3):.1f}")
+    assert e3 < 2.0**-26 and e3 < e2 / 4
 
 
 @pytest.mark.parametrize("iterations", [2, 1])

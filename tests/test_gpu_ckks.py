@@ -110,7 +110,7 @@ def test_easyfhe_context_session_roundtrip():
     from holmes_amd import backend
     from holmes_amd.config import SimulatorConfig
 
-    cfg = SimulatorConfig(maxLevelsRemaining=5, dnum=2)
+    cfg = SimulatorConfig(maxLevelsRemaining=5, dnum=2, dcrtBits=50, firstMod=50, scaleBits=40)
     sess = backend.create_sim_context(cfg, input_dim=16, block_out=8, rotations=(3,))
     assert sess.max_slots == 32768 and sess.context.L == 6
     rng = np.random.default_rng(11)

@@ -92,11 +92,43 @@ def test_holmes_mac_multi_matches_the_context_mac():
     c0s = ptr_t(*[base[0][0, i].data_ptr() for i in range(inputs)])
     c1s = ptr_t(*[base[1][0, i].data_ptr() for i in range(inputs)])
     res = torch.zeros((2, groups, inputs, limbs, N), dtype=torch.uint64, device=dev)
-    primes = torch.tensor(ctx.primes[:limbs], dtype=torch.uint64, device=dev)
     lib = _bound()
+    # the reference's own call (bench/cmp/holmes_multi_mac.py:138-140): the context's device tables
+    # by address, ctx.primes.data_ptr(), ctx.barret_ratio.data_ptr(), ctx.barret_k.data_ptr()
     code = lib.holmes_mac_multi(res.data_ptr(), c0s, c1s, inputs * limbs * N, nb, inputs, pts.data_ptr(), limbs * N,
-                                groups, 10116, limbs, primes.data_ptr(), None, None,
-                                torch.cuda.current_stream().cuda_stream)
+                                groups, 10116, limbs, ctx.primes.data_ptr(), ctx.barret_ratio.data_ptr(),
+                                ctx.barret_k.data_ptr(), torch.cuda.current_stream().cuda_stream)
     assert code == 0
     torch.cuda.synchronize()
     assert torch.equal(res.view(torch.int64).cpu(), ref.view(torch.int64).cpu())
+
+
+def test_native_context_tables():
+    """EasyFHE's context tables with the reference's definitions: primes (Q then P) on the device,
+    barret_k = floor(log2 p) + 63, barret_ratio = floor(2^k / p) (bench/cmp/kernels/holmes_mac.cu:56-58),
+    PModq = P mod q_i; the Barrett pair reduces products exactly, as the sidecar's barrett128 does."""
+
+    from holmes_amd import fhe
+
+    for dcrt, first in ((50, 50), (59, 60)):
+        _, ctx = fhe.generate_client_context(fhe.CKKSContextSpec(depth=5, dnum=2, dcrt_bits=dcrt, first_mod=first,
+                                                                 seed=4))
+        primes = [int(p) for p in ctx.primes]
+        assert torch.tensor(primes, dtype=torch.uint64).tolist() == ctx.primes.tensor.cpu().tolist()
+        ratio = [int(v) for v in ctx.barret_ratio.cpu().tolist()]
+        k = [int(v) for v in ctx.barret_k.cpu().tolist()]
+        P = 1
+        for p in ctx.p_primes:
+            P *= int(p)
+        assert [int(v) for v in ctx.PModq.cpu().tolist()] == [P % int(q) for q in ctx.q_primes]
+        rng = np.random.default_rng(dcrt)
+        for p, r, kk in zip(primes, ratio, k):
+            assert kk == p.bit_length() - 1 + 63 and r == (1 << kk) // p and r < (1 << 64)
+            for _ in range(50):
+                a, b = (int(x) % p for x in rng.integers(0, 1 << 62, size=2, dtype=np.uint64))
+                x = a * b
+                est = (x * r) >> kk            # barrett128's quotient estimate
+                rem = x - est * p
+                while rem >= p:
+                    rem -= p
+                assert rem == x % p and 0 <= x - est * p < 3 * p

@@ -3,7 +3,8 @@ reference's llama3fhe/graph/prefill.py:57 ``evaluate`` for the first layer: RMSN
 causal Alg2 attention, W_O, residual, one two-pass refresh, the SwiGLU MLP block at width 14336,
 residual).  Llama-3-8B shapes with seeded random weights N(0, 0.02^2) and gammas 1 + N(0, 0.1^2),
 input N(0, 1), the 38-limb chain (depth 37, dnum 5, 50-bit primes, scale 2^50).  Every decrypted
-output slot is within 2^-16 of the float64 model of the same polynomials (prefill_layer_numpy), for
+output slot is within 2^-17 (the 2^-16 bar with a bit of margin) of the float64 model of the same
+polynomials (prefill_layer_numpy), for
 the model's first layer (fresh input at 38 limbs) and for a steady-state layer (input at 4 limbs,
 refreshed first; the softmax's series inputs refreshed).""" 
 
@@ -47,7 +48,7 @@ def _check(client, out, layout, ref, what):
     mag = float(np.max(np.abs(ref["output"])))
     print(f"{what}: max error 2^{math.log2(err):.2f} of magnitude {mag:.2f}; softmax vs exact "
           f"{ref['softmax_vs_exact']:.2e}", flush=True)
-    assert err < 2.0**-16
+    assert err < 2.0**-17  # the 2^-16 bar with a bit of margin (measured 2^-18.2 steady, 2^-19 first)
 
 
 @pytest.mark.timeout(1100)

@@ -47,6 +47,9 @@ def test_simulator_config_validation():
     cfg = SimulatorConfig()
     cfg.validate()
     assert cfg.rescale_policy() == "manual"
+    # the reference's defaults (llama3fhe/config.py:18-22): depth 37, 59-bit primes, 60-bit first modulus
+    assert (cfg.maxLevelsRemaining, cfg.dnum, cfg.dcrtBits, cfg.firstMod) == (37, 3, 59, 60)
+    assert cfg.scale_bits() == 59 and SimulatorConfig(scaleBits=40).scale_bits() == 40
     with pytest.raises(ValueError):
         SimulatorConfig(rescaleTech="BOGUS").rescale_policy()
 

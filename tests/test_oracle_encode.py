@@ -55,6 +55,31 @@ def test_encode_matches_fft_canonical_embedding(scale):
     assert np.array_equal(res_ntt, ctx.ntt_fwd_limbs(res, [0, 1, 2]))
 
 
+def test_stage1_is_the_encoders_rounding_input():
+    """encode_stage1 (the encode sidecar's stage-2 input, interleaved Re / Im) rounded half away
+    from zero and reduced gives encode_real's coefficient-domain residues: coefficient k < n from
+    Re w_k, k >= n from Im w_(k-n) (bench/cmp/kernels/holmes_encode.cu:108-111); and it is the
+    canonical embedding's inverse, so it matches the independent NumPy encoder before rounding."""
+
+    ps = O.gen_primes(16, 59, 2)
+    ctx = O.OracleContext(16, 2, 0, 1, ps)
+    rng = np.random.default_rng(8)
+    z = rng.normal(size=1 << 15)
+    scale = 2.0**45
+    w = ctx.encode_stage1(z)
+    x = w * scale
+    r = np.trunc(x)
+    d = x - r
+    coef = r + (d >= 0.5) - (d <= -0.5)
+    coef = np.array([int(c) for c in np.concatenate([coef[0::2], coef[1::2]])], dtype=object)
+    res, ok = ctx.encode_real(z, scale, [0, 1], ntt=False)
+    assert ok
+    for l, q in enumerate(ps):
+        assert np.array_equal(res[l].astype(object), coef % q)
+    m = encoding.encode(z, scale, 16)  # the NumPy encoder, independently rounded
+    assert np.max(np.abs(np.asarray(m, dtype=np.float64) - coef.astype(np.float64))) <= 1.0
+
+
 def test_encode_reports_overflow():
     """The cap is |coefficient| < 2^61 (MAX_ENCODED_BITS, llama3fhe/operators/attention/prefill/
     softmax.py:559).  A constant slot vector c encodes exactly to the coefficient c * scale at
