@@ -1,6 +1,8 @@
 """Benchmark on one MI355X.
 
-Default (``--workload c2``, the headline line): batched hybrid key switching.
+Default (``--workload c2``, the headline line): batched hybrid key switching, with the steady
+prefill layer's seconds and decrypted error (the metric's first half, as ``--workload layer``
+measures it) in the line's ``layer`` object (``--no-layer`` skips it).
 
 Workload (one "step"): 16 ciphertext polynomials d at 24 limbs of 50-bit primes, N = 2^16, each
 key-switched with its own rotation key (rotations 1..16), dnum 3 (8-limb digits), 8 special
@@ -83,6 +85,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-layer", action="store_true",
+                    help="c2: skip the steady prefill layer measured beside the key switch (the metric's first half)")
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
     ap.add_argument("--ks-slices", type=int, default=0,
@@ -267,6 +271,12 @@ def main() -> int:
         },
         "cpu_baseline": _cpu_annotated(cpu),
     }
+    if not args.no_layer:
+        # the metric's first half beside the key-switch half, measured in the same run
+        del d, out_b, out_a, keys
+        ctx.rotation_keys.clear()
+        torch.cuda.empty_cache()
+        line["layer"] = c2_layer_figures()
     print(json.dumps(line), flush=True)
     return 0
 
@@ -1208,6 +1218,83 @@ def c2_traffic():
     return int(rec["traffic_bytes"]), rec
 
 
+def _layer_setup(seed: int = 20261206) -> dict:
+    """The N1 workload: the 38-limb context, every rotation key and refresh program of the layer,
+    the first-layer and steady-state PrefillLayer objects, and the encrypted input (128 tokens x
+    4096 features N(0, 1), 16 ciphertexts) at the top of the chain and at the steady input level."""
+
+    from holmes_amd import fhe
+    from holmes_amd import prefill as P
+    from holmes_amd.layouts import FeatureMajorPrefillLayout
+
+    t0 = time.perf_counter()
+    spec = P.PrefillSpec()
+    client, ctx = fhe.generate_client_context(P.prefill_context_spec(seed))
+    rng = np.random.default_rng(seed)
+    w = P.random_weights(spec, rng)
+    first, rots = P.setup_prefill_layer(client, ctx, w, spec)
+    steady = P.PrefillLayer(ctx, w, spec, program=first.program, config=first.config, steady=True,
+                            programs=first.programs)
+    layout = FeatureMajorPrefillLayout()
+    x = rng.normal(size=(128, spec.hidden_dim))
+    packed = layout.pack(x)
+    cts_first = [client.encrypt(row, cur_limbs=ctx.L) for row in packed]
+    cts_steady = [client.encrypt(row, cur_limbs=P.LAYER_OUTPUT_LIMBS) for row in packed]
+    _log(f"layer setup {time.perf_counter() - t0:.1f} s: {len(rots)} rotation keys, {ctx.L} limbs, dnum {ctx.dnum}")
+    return {"P": P, "ctx": ctx, "client": client, "rng": rng, "spec": spec, "w": w, "x": x, "layout": layout,
+            "first": first, "steady": steady, "rots": rots, "cts_first": cts_first, "cts_steady": cts_steady}
+
+
+def _time_layer(layer, cts, label: str, steps: int, warmup: int):
+    """(last output, median seconds, median stage seconds) over ``steps`` forwards after ``warmup``."""
+
+    import torch
+
+    for _ in range(warmup):
+        layer.forward(cts)
+    secs, all_stages = [], []
+    out = None
+    for _ in range(steps):
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        out, stages = layer.forward(cts)
+        torch.cuda.synchronize()
+        secs.append(time.perf_counter() - w0)
+        all_stages.append(stages)
+        _log(f"{label} step {len(secs)}: {secs[-1]:.3f} s")
+    med = float(np.median(secs))
+    return out, med, {k: float(np.median([st[k] for st in all_stages])) for k in all_stages[0]}
+
+
+def _layer_error(L: dict, out, ref=None):
+    """(float64 model, max decrypted error over every slot, output magnitude) of a layer output."""
+
+    P, client, layout = L["P"], L["client"], L["layout"]
+    if ref is None:
+        ref = P.prefill_layer_numpy(L["x"], L["w"], L["spec"])
+    want = layout.pack(ref["output"])
+    err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
+    return ref, err, float(np.max(np.abs(ref["output"])))
+
+
+def c2_layer_figures(steps: int = 2, warmup: int = 1) -> dict:
+    """The metric's other half for the default line: the steady-state N1 layer's seconds (median of
+    ``steps`` after ``warmup``) and its decrypted error against the float64 model."""
+
+    import math
+
+    L = _layer_setup()
+    out, s_wall, stages = _time_layer(L["steady"], L["cts_steady"], "steady layer", steps, warmup)
+    _, err, mag = _layer_error(L, out)
+    _log(f"steady layer: {s_wall:.3f} s, error {err:.3e} (2^{math.log2(err):.2f}), magnitude {mag:.2f}")
+    return {"metric": "s per encrypted Llama-3-8B layer (128-tok prefill, 1 GPU)",
+            "value": round(s_wall, 4), "unit": "s", "steps": steps, "warmup": warmup,
+            "workload": "N1 prefill layer, steady state (as --workload layer): 128 tokens, 38 limbs of 50-bit "
+                        "primes, dnum 5, scale 2^50; input, residual and series inputs refreshed",
+            "decrypted_max_error": err, "error_bits": round(-math.log2(err), 2), "output_magnitude": round(mag, 4),
+            "stage_seconds": {k: round(v, 4) for k, v in stages.items()}}
+
+
 def run_layer(args) -> int:
     """N1: one encrypted Llama-3-8B prefill layer (holmes_amd.prefill.PrefillLayer) on 128 tokens x
     4096 features (16 ciphertexts, 38-limb chain): weights N(0, 0.02^2), gammas 1 + N(0, 0.1^2),
@@ -1224,56 +1311,22 @@ def run_layer(args) -> int:
 
     import torch
 
-    from holmes_amd import fhe
-    from holmes_amd import prefill as P
-    from holmes_amd.layouts import FeatureMajorPrefillLayout
-
-    seed = 20261206
     steps = int(args.steps) if args.steps != 20 else 3
     warmup = int(args.warmup) if args.warmup != 3 else 1
-    t0 = time.perf_counter()
-    spec = P.PrefillSpec()
-    client, ctx = fhe.generate_client_context(P.prefill_context_spec(seed))
-    rng = np.random.default_rng(seed)
-    w = P.random_weights(spec, rng)
-    first, rots = P.setup_prefill_layer(client, ctx, w, spec)
-    steady = P.PrefillLayer(ctx, w, spec, program=first.program, config=first.config, steady=True,
-                            programs=first.programs)
-    layout = FeatureMajorPrefillLayout()
-    x = rng.normal(size=(128, spec.hidden_dim))
-    packed = layout.pack(x)
-    cts_first = [client.encrypt(row, cur_limbs=ctx.L) for row in packed]
-    cts_steady = [client.encrypt(row, cur_limbs=P.LAYER_OUTPUT_LIMBS) for row in packed]
-    _log(f"layer setup {time.perf_counter() - t0:.1f} s: {len(rots)} rotation keys, {ctx.L} limbs, dnum {ctx.dnum}")
-
-    def timed(layer, cts, label):
-        for _ in range(warmup):
-            layer.forward(cts)
-        secs, all_stages = [], []
-        for _ in range(steps):
-            torch.cuda.synchronize()
-            w0 = time.perf_counter()
-            out, stages = layer.forward(cts)
-            torch.cuda.synchronize()
-            secs.append(time.perf_counter() - w0)
-            all_stages.append(stages)
-            _log(f"{label} step {len(secs)}: {secs[-1]:.3f} s")
-        med = float(np.median(secs))
-        return out, med, {k: float(np.median([st[k] for st in all_stages])) for k in all_stages[0]}
-
-    out_f, s_first, stages_f = timed(first, cts_first, "first layer")
-    out, s_wall, stages = timed(steady, cts_steady, "steady layer")
+    L = _layer_setup()
+    P, ctx, client, rng = L["P"], L["ctx"], L["client"], L["rng"]
+    first, steady, spec, w, x = L["first"], L["steady"], L["spec"], L["w"], L["x"]
+    rots, cts_steady = L["rots"], L["cts_steady"]
+    out_f, s_first, stages_f = _time_layer(first, L["cts_first"], "first layer", steps, warmup)
+    out, s_wall, stages = _time_layer(steady, cts_steady, "steady layer", steps, warmup)
     with _CallLog(ctx) as log:
         torch.cuda.synchronize()
         steady.forward(cts_steady)
         torch.cuda.synchronize()
     limbs_moved, ks = log.limbs_bytes()
     layer_bytes = limbs_moved * ctx.N * 8
-    ref = P.prefill_layer_numpy(x, w, spec)
-    want = layout.pack(ref["output"])
-    err = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out))
-    err_f = max(float(np.max(np.abs(client.decrypt(o).real - want[i]))) for i, o in enumerate(out_f))
-    mag = float(np.max(np.abs(ref["output"])))
+    ref, err, mag = _layer_error(L, out)
+    _, err_f, _ = _layer_error(L, out_f, ref)
     _log(f"steady layer: {s_wall:.3f} s, stages {stages}, error {err:.3e}; first layer {s_first:.3f} s, "
          f"error {err_f:.3e}; magnitude {mag:.2f}")
     ks_items = sum(b for _, b, _ in ks)
@@ -1302,8 +1355,8 @@ def run_layer(args) -> int:
         "config": {"workload": "N1 prefill layer, steady state, 128 tokens: input refresh, RMSNorm1 (deg-15 rsqrt), "
                                "complex QKV (2 x 4096x4096 BSGS), RoPE, causal Alg2 attention 32/8/128 (exp deg 15 "
                                "and rsqrt deg 31 on refreshed inputs), W_O, residual, refresh, SwiGLU "
-                               "4096->14336->4096 (SiLU deg 63), residual; every refresh two-pass; 38 limbs, "
-                               "scale 2^50, dnum 5",
+                               "4096->14336->4096 (SiLU deg 63), residual; refreshes two-pass, the inverse "
+                               "square root's input three-pass; 38 limbs, scale 2^50, dnum 5",
                    "decrypted_max_error": err, "output_magnitude": mag, "error_bits": round(-math.log2(err), 2),
                    "softmax_vs_exact": ref["softmax_vs_exact"], "in_range": ref["in_range"],
                    "rotation_keys": len(rots), "refreshed_items_per_layer": steady.ops.refreshes // (warmup + steps + 1),

@@ -16,9 +16,20 @@ from oracle import oracle as O
 from tests.helpers import centered, crt
 
 
-def _ctx(log_n, L, K, alpha, bits=50):
-    ps = O.gen_primes(log_n, bits, L + K)
-    P, Q = ps[:K], ps[K:]
+# Both chain widths the GPU tests run on: 50-bit primes (the FP64 path) and the reference's
+# production shape (assets/feature_major.json:3-14): a 60-bit first modulus, 59-bit Q primes, 60-bit
+# special primes (the wide path).  Every pin below runs on both.
+pytestmark = pytest.mark.parametrize("chain", ["50", "60/59"])
+
+
+def _ctx(log_n, L, K, alpha, chain="50"):
+    if chain == "50":
+        ps = O.gen_primes(log_n, 50, L + K)
+        P, Q = ps[:K], ps[K:]
+    else:
+        P = O.gen_primes(log_n, 60, K)
+        q0 = O.gen_primes(log_n, 60, 1, exclude=P)
+        Q = q0 + O.gen_primes(log_n, 59, L - 1)
     return O.OracleContext(log_n, L, K, alpha, Q + P)
 
 
@@ -28,8 +39,8 @@ def _rand_ntt(ctx, rng, limbs, prime_idx=None):
 
 
 @pytest.mark.parametrize("ell,digit", [(6, 0), (6, 2), (5, 2), (4, 1)])
-def test_modup_is_approximate_crt_lift(ell, digit):
-    ctx = _ctx(4, 6, 2, 2)
+def test_modup_is_approximate_crt_lift(ell, digit, chain):
+    ctx = _ctx(4, 6, 2, 2, chain=chain)
     rng = np.random.default_rng(ell * 10 + digit)
     d = _rand_ntt(ctx, rng, ell)
     ext = ctx.modup(ell, digit, d)
@@ -59,8 +70,8 @@ def test_modup_is_approximate_crt_lift(ell, digit):
 
 
 @pytest.mark.parametrize("ell", [6, 3])
-def test_moddown_is_rounded_division_by_P(ell):
-    ctx = _ctx(4, 6, 3, 2)
+def test_moddown_is_rounded_division_by_P(ell, chain):
+    ctx = _ctx(4, 6, 3, 2, chain=chain)
     rng = np.random.default_rng(ell)
     ext_idx = list(range(ell)) + [ctx.L + k for k in range(ctx.K)]
     x = _rand_ntt(ctx, rng, len(ext_idx), ext_idx)
@@ -91,8 +102,8 @@ def test_moddown_is_rounded_division_by_P(ell):
 
 
 @pytest.mark.parametrize("ell", [2, 5])
-def test_rescale_is_exact_rounding(ell):
-    ctx = _ctx(4, 5, 1, 2)
+def test_rescale_is_exact_rounding(ell, chain):
+    ctx = _ctx(4, 5, 1, 2, chain=chain)
     rng = np.random.default_rng(100 + ell)
     x = _rand_ntt(ctx, rng, ell)
     out = ctx.rescale(ell, x)
@@ -127,11 +138,11 @@ def _poly_ntt(ctx, coeffs, prime_idx):
 
 
 @pytest.mark.parametrize("ell", [6, 5, 3])
-def test_keyswitch_decrypt_invariant(ell):
+def test_keyswitch_decrypt_invariant(ell, chain):
     """b + a s - d s' is small mod Q_ell: key generation and key switch agree with the algebra."""
 
     log_n, L, K, alpha = 10, 6, 2, 2
-    ctx = _ctx(log_n, L, K, alpha)
+    ctx = _ctx(log_n, L, K, alpha, chain=chain)
     rng = np.random.default_rng(5 + ell)
     n = ctx.n
     s = _ternary(rng, n)
@@ -163,11 +174,11 @@ def test_keyswitch_decrypt_invariant(ell):
     assert worst < 2**20, worst
 
 
-def test_keyswitch_key_is_gadget_of_secret():
+def test_keyswitch_key_is_gadget_of_secret(chain):
     """b_j + a_j s - e_j = P T_j s' with T_j = 1 on digit j, 0 on other Q primes and on P."""
 
     log_n, L, K, alpha = 5, 5, 2, 2
-    ctx = _ctx(log_n, L, K, alpha)
+    ctx = _ctx(log_n, L, K, alpha, chain=chain)
     rng = np.random.default_rng(3)
     n = ctx.n
     s, sf = _ternary(rng, n), _ternary(rng, n)
@@ -190,8 +201,8 @@ def test_keyswitch_key_is_gadget_of_secret():
             assert lhs == rhs
 
 
-def test_bsgs_mac_matches_big_integer_sum():
-    ctx = _ctx(4, 3, 1, 3)
+def test_bsgs_mac_matches_big_integer_sum(chain):
+    ctx = _ctx(4, 3, 1, 3, chain=chain)
     rng = np.random.default_rng(9)
     limbs, nb, G = 3, 4, 2
     pt = np.stack([_rand_ntt(ctx, rng, limbs) for _ in range(G * nb)])
@@ -207,10 +218,10 @@ def test_bsgs_mac_matches_big_integer_sum():
 
 
 @pytest.mark.parametrize("to", [2, 5])
-def test_modraise_is_the_centered_lift(to):
+def test_modraise_is_the_centered_lift(to, chain):
     # every output limb holds the centered representative of limb 0's coefficient (|x| < q_0 / 2)
     # reduced modulo its own prime; limb 0 is unchanged
-    ctx = _ctx(4, 5, 1, 2)
+    ctx = _ctx(4, 5, 1, 2, chain=chain)
     rng = np.random.default_rng(200 + to)
     x = _rand_ntt(ctx, rng, 1)
     out = ctx.modraise(to, x[0])

@@ -16,9 +16,20 @@ from oracle import oracle as O
 from tests.helpers import centered, crt, negacyclic_mul
 
 
-def _ctx(log_n, L, K, alpha, bits=50):
-    ps = O.gen_primes(log_n, bits, L + K)
-    P, Q = ps[:K], ps[K:]
+# Both chain widths the GPU tests run on: 50-bit primes (the FP64 path) and the reference's
+# production shape (assets/feature_major.json:3-14): a 60-bit first modulus, 59-bit Q primes, 60-bit
+# special primes (the wide path).  Every pin below runs on both.
+pytestmark = pytest.mark.parametrize("chain", ["50", "60/59"])
+
+
+def _ctx(log_n, L, K, alpha, chain="50"):
+    if chain == "50":
+        ps = O.gen_primes(log_n, 50, L + K)
+        P, Q = ps[:K], ps[K:]
+    else:
+        P = O.gen_primes(log_n, 60, K)
+        q0 = O.gen_primes(log_n, 60, 1, exclude=P)
+        Q = q0 + O.gen_primes(log_n, 59, L - 1)
     return O.OracleContext(log_n, L, K, alpha, Q + P)
 
 
@@ -45,8 +56,8 @@ def negacyclic_square_py(s):
     return out
 
 
-def test_tensor_is_the_ntt_of_the_negacyclic_products():
-    ctx = _ctx(5, 3, 1, 3)
+def test_tensor_is_the_ntt_of_the_negacyclic_products(chain):
+    ctx = _ctx(5, 3, 1, 3, chain=chain)
     rng = np.random.default_rng(7)
     limbs = 3
     idx = list(range(limbs))
@@ -65,9 +76,9 @@ def test_tensor_is_the_ntt_of_the_negacyclic_products():
         assert [int(v) for v in got[2][i]] == want2
 
 
-def test_tensor_is_not_symmetric_in_the_wrong_way():
+def test_tensor_is_not_symmetric_in_the_wrong_way(chain):
     # swapping the roles of (a0, a1) and (b0, b1) keeps d0, d1, d2; swapping a0 with a1 does not
-    ctx = _ctx(4, 2, 1, 2)
+    ctx = _ctx(4, 2, 1, 2, chain=chain)
     rng = np.random.default_rng(3)
     v = [_rand_coeffs(ctx, rng, 2) for _ in range(4)]
     base = ctx.tensor(2, *v)
@@ -79,9 +90,9 @@ def test_tensor_is_not_symmetric_in_the_wrong_way():
 
 
 @pytest.mark.parametrize("ell", [4, 3, 1])
-def test_relinearize_keeps_the_decryption(ell):
+def test_relinearize_keeps_the_decryption(ell, chain):
     log_n, L, K, alpha = 4, 4, 2, 2
-    ctx = _ctx(log_n, L, K, alpha)
+    ctx = _ctx(log_n, L, K, alpha, chain=chain)
     rng = np.random.default_rng(100 + ell)
     n = ctx.n
     s = rng.integers(-1, 2, n).astype(np.int64)
@@ -117,10 +128,10 @@ def test_relinearize_keeps_the_decryption(ell):
         assert abs(noise) < 2**20, noise
 
 
-def test_secret_square_schoolbook_against_ntt():
+def test_secret_square_schoolbook_against_ntt(chain):
     # the negacyclic square of a ternary secret, computed through the oracle's NTT over one prime,
     # equals the schoolbook integer square (its coefficients are far below q / 2)
-    ctx = _ctx(6, 1, 1, 1)
+    ctx = _ctx(6, 1, 1, 1, chain=chain)
     rng = np.random.default_rng(11)
     s = rng.integers(-1, 2, ctx.n).astype(np.int64)
     q = ctx.primes[0]
@@ -130,8 +141,8 @@ def test_secret_square_schoolbook_against_ntt():
     assert got == negacyclic_square_py([int(v) for v in s])
 
 
-def test_weighted_sum_matches_big_integer_sums():
-    ctx = _ctx(4, 3, 1, 3)
+def test_weighted_sum_matches_big_integer_sums(chain):
+    ctx = _ctx(4, 3, 1, 3, chain=chain)
     rng = np.random.default_rng(5)
     limbs, n, G = 3, 5, 2
     x = np.stack([_rand_coeffs(ctx, rng, limbs) for _ in range(n)])

@@ -2,7 +2,8 @@
 
 Each check comes from mathematics, not from the oracle's formulas: primality by an independent
 Miller-Rabin base set, psi by its order, the NTT by the O(N^2) evaluation sum, the convolution
-theorem against schoolbook negacyclic products, automorphisms by polynomial substitution.
+theorem against schoolbook negacyclic products, automorphisms by polynomial substitution.  Every
+pin runs on 50-bit primes and on the reference's 59/60-bit widths (assets/feature_major.json:9-11).
 """
 
 import numpy as np
@@ -12,7 +13,7 @@ from oracle import oracle as O
 from tests.helpers import bitrev, is_prime_py, negacyclic_mul, small_primes
 
 
-@pytest.mark.parametrize("log_n,bits", [(4, 30), (10, 50), (16, 50)])
+@pytest.mark.parametrize("log_n,bits", [(4, 30), (10, 50), (16, 50), (16, 59), (16, 60)])
 def test_prime_chain_rule(log_n, bits):
     ps = O.gen_primes(log_n, bits, 6)
     assert ps == small_primes(log_n, bits, 6)
@@ -27,9 +28,10 @@ def test_prime_chain_rule(log_n, bits):
     assert O.gen_primes(log_n, bits, 3, exclude=ps[:2]) == ps[2:5]
 
 
+@pytest.mark.parametrize("bits", [50, 59, 60])
 @pytest.mark.parametrize("log_n", [3, 10, 16])
-def test_psi_is_primitive_2n_root(log_n):
-    for q in O.gen_primes(log_n, 50, 3):
+def test_psi_is_primitive_2n_root(log_n, bits):
+    for q in O.gen_primes(log_n, bits, 3):
         psi = O.find_psi(q, log_n)
         n = 1 << log_n
         assert pow(psi, n, q) == q - 1  # psi^N = -1 => order exactly 2N
@@ -38,10 +40,11 @@ def test_psi_is_primitive_2n_root(log_n):
         assert psi == pow(g, (q - 1) // (2 * n), q)
 
 
-@pytest.mark.parametrize("log_n", [3, 5, 8])
-def test_ntt_equals_brute_force_evaluation(log_n):
+@pytest.mark.parametrize("bits", [50, 59, 60])
+@pytest.mark.parametrize("log_n", [3, 5, 8, 10])
+def test_ntt_equals_brute_force_evaluation(log_n, bits):
     n = 1 << log_n
-    q = O.gen_primes(log_n, 50, 1)[0]
+    q = O.gen_primes(log_n, bits, 1)[0]
     psi = O.find_psi(q, log_n)
     fwd, inv = O.make_tables(q, psi, log_n)
     assert all(int(fwd[k]) == pow(psi, bitrev(k, log_n), q) for k in range(n))
@@ -56,10 +59,11 @@ def test_ntt_equals_brute_force_evaluation(log_n):
     assert np.array_equal(O.ntt_inv(out, log_n, q, inv), a)
 
 
-def test_ntt_edge_values():
+@pytest.mark.parametrize("bits", [50, 59, 60])
+def test_ntt_edge_values(bits):
     log_n = 16
     n = 1 << log_n
-    q = O.gen_primes(log_n, 50, 1)[0]
+    q = O.gen_primes(log_n, bits, 1)[0]
     fwd, inv = O.make_tables(q, O.find_psi(q, log_n), log_n)
     for a in (np.zeros(n, np.uint64), np.full(n, q - 1, np.uint64)):
         assert np.array_equal(O.ntt_inv(O.ntt_fwd(a, log_n, q, fwd), log_n, q, inv), a)
@@ -69,10 +73,11 @@ def test_ntt_edge_values():
     assert np.all(O.ntt_fwd(d, log_n, q, fwd) == 1)
 
 
+@pytest.mark.parametrize("bits", [50, 59, 60])
 @pytest.mark.parametrize("log_n", [4, 7])
-def test_convolution_theorem(log_n):
+def test_convolution_theorem(log_n, bits):
     n = 1 << log_n
-    q = O.gen_primes(log_n, 50, 1)[0]
+    q = O.gen_primes(log_n, bits, 1)[0]
     fwd, inv = O.make_tables(q, O.find_psi(q, log_n), log_n)
     rng = np.random.default_rng(11)
     a = rng.integers(0, q, n, dtype=np.uint64)
@@ -83,11 +88,12 @@ def test_convolution_theorem(log_n):
     assert [int(v) for v in c] == negacyclic_mul([int(v) for v in a], [int(v) for v in b], q)
 
 
+@pytest.mark.parametrize("bits", [50, 60])
 @pytest.mark.parametrize("g", [5, 25, 5**7 % 256, 255])
-def test_automorphism_coeff_and_ntt(g):
+def test_automorphism_coeff_and_ntt(g, bits):
     log_n = 7
     n = 1 << log_n
-    q = O.gen_primes(log_n, 50, 1)[0]
+    q = O.gen_primes(log_n, bits, 1)[0]
     fwd, inv = O.make_tables(q, O.find_psi(q, log_n), log_n)
     rng = np.random.default_rng(g)
     a = rng.integers(0, q, n, dtype=np.uint64)
