@@ -114,7 +114,7 @@ def main() -> int:
     ap.add_argument("--write-traffic-record", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                     help="no GPU: sum the last C2 step's five key-switch dispatches in the counter CSVs of "
                          "two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of `bench.py --steps 2 "
-                         "--warmup 0 --no-cpu` and write the traffic record for the current kernel sources")
+                         "--warmup 0 --no-cpu --no-layer` and write the traffic record for the current kernel sources")
     args = ap.parse_args()
     if args.write_traffic_record:
         return write_traffic_record(*args.write_traffic_record)
@@ -1198,7 +1198,7 @@ def write_traffic_record(fetch_dir: str, write_dir: str) -> int:
     rec = {"sources_sha256": kernel_sources_sha256(), "fetch_kib": round(fetch, 1), "write_kib": round(write, 1),
            "fetch_scale": 2.0, "write_scale": 1.0, "traffic_bytes": int(round((2.0 * fetch + write) * 1024)),
            "measured": f"{datetime.date.today().isoformat()} rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE on "
-                       "bench.py --steps 2 --warmup 0 --no-cpu"}
+                       "bench.py --steps 2 --warmup 0 --no-cpu --no-layer"}
     with open(C2_TRAFFIC_RECORD, "w") as f:
         json.dump(rec, f, indent=1)
     print(json.dumps(rec))

@@ -202,8 +202,8 @@ class CKKSContext:
                 "hck_context_create",
             )
         self._h = h
-        # hoisted rotations (hck_rotate_hoisted) run on the FP64 path: every prime below 2^50
-        self.supports_hoisting = max(self.primes) < (1 << 50)
+        # hoisted rotations (hck_rotate_hoisted) run on both prime widths
+        self.supports_hoisting = True
         self._ws: torch.Tensor | None = None
         self.rotation_keys: dict[int, torch.Tensor] = {}
         self.relin_key: torch.Tensor | None = None

@@ -135,7 +135,7 @@ int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const ui
 // Hoisted rotations: ks_hoist materialises the extended digits of `inputs` polys d in the full NTT
 // domain ([inputs][beta][ell + K] canonical limbs, workspace ks_hoist_bytes); ks_hoisted rotates
 // input i % inputs by galois[i] with ksk[i] for every item i < items from them (workspace
-// ks_hoisted_bytes), bit-identical to ks_fused.  FP64 contexts only (HCK_ERR_UNSUPPORTED on a wide one).
+// ks_hoisted_bytes), bit-identical to ks_fused.  A wide context runs wide_hoist / wide_hoisted.
 size_t ks_hoist_bytes(const hck_context* c, int ell, int inputs);
 int ks_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
              char* ws, hipStream_t s);

@@ -241,7 +241,6 @@ extern "C" int hck_rotate_hoist_prepare(const hck_context* ctx, int level_limbs,
                                         int64_t in_stride, uint64_t* digits, void* workspace, size_t workspace_bytes,
                                         void* stream) {
   if (!ctx || !c1 || !digits || level_limbs < 1 || level_limbs > ctx->L || inputs < 0) return HCK_ERR_ARG;
-  if (ctx->wide) return HCK_ERR_UNSUPPORTED;
   if (inputs > 1 && in_stride < (int64_t)level_limbs * hck::kN) return HCK_ERR_ARG;
   if (inputs == 0) return HCK_OK;
   if (!workspace || workspace_bytes < hck::ks_hoist_bytes(ctx, level_limbs, inputs)) return HCK_ERR_WORKSPACE;
@@ -254,7 +253,6 @@ extern "C" int hck_rotate_hoisted(const hck_context* ctx, int level_limbs, int i
                                   int64_t out_stride, void* workspace, size_t workspace_bytes, void* stream) {
   if (!ctx || !galois || !c0 || !c1 || !digits || !ksk || !out0 || !out1) return HCK_ERR_ARG;
   if (level_limbs < 1 || level_limbs > ctx->L || inputs < 1 || items < 0) return HCK_ERR_ARG;
-  if (ctx->wide) return HCK_ERR_UNSUPPORTED;
   const int64_t limb_words = (int64_t)level_limbs * hck::kN;
   if (inputs > 1 && in_stride < limb_words) return HCK_ERR_ARG;
   if (items > 1 && out_stride < limb_words) return HCK_ERR_ARG;

@@ -1862,6 +1862,7 @@ int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const ui
 // NTT domain, canonical u64 [inputs][beta][ell + K] limbs (the own digit's limbs of each digit are
 // left unwritten); workspace T1 + T2 as in ks_fused.
 size_t ks_hoist_bytes(const hck_context* c, int ell, int inputs) {
+  if (c->wide) return wide_hoist_bytes(c, ell, inputs);
   const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
   const size_t per = inputs < kMaxBatchF ? inputs : kMaxBatchF;
   return per * kN * 8 * (ell + beta * ext_l);
@@ -1869,7 +1870,7 @@ size_t ks_hoist_bytes(const hck_context* c, int ell, int inputs) {
 
 int ks_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
              char* ws, hipStream_t s) {
-  if (c->wide) return HCK_ERR_UNSUPPORTED;
+  if (c->wide) return wide_hoist(c, ell, inputs, d, d_stride, digits, ws, s);
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
   const long long n = kN;
@@ -1899,6 +1900,7 @@ int ks_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long 
 // ks_fused with that Galois element (ModUp commutes with sigma).  Workspace T4 + ACCP per item of
 // a launch (at most kMaxBatchF items each).
 size_t ks_hoisted_bytes(const hck_context* c, int ell, int items) {
+  if (c->wide) return wide_hoisted_bytes(c, ell, items);
   const int per = items < kMaxBatchF ? items : kMaxBatchF;
   return (size_t)per * kN * 8 * (2 * ell + 2 * c->K);
 }
@@ -1907,7 +1909,9 @@ int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint3
                const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
                const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
                hipStream_t s) {
-  if (c->wide) return HCK_ERR_UNSUPPORTED;
+  if (c->wide)
+    return wide_hoisted(c, ell, inputs, items, galois, ksk, c0, c1, in_stride, digits, out_b, out_a, out_stride, ws,
+                        s);
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   const int K = c->K, beta = beta_of(c, ell);
   const long long n = kN;

@@ -377,6 +377,49 @@ __global__ __launch_bounds__(256) void wk_ks_ext_out(const u64* __restrict__ acc
   out[it * out_item + o] = v;
 }
 
+// Hoisted rotations.  Item it of a launch is input (first + it) % inputs rotated by G.g[it]; its
+// extended digits (the ModUp of c1, NTT domain, [inputs][beta][ell + K][N], the digit's own limbs
+// included) are read through sigma_g, which commutes with ModUp (the centered lift is odd-symmetric):
+// acc[item][comp][e] = sum_j sigma(digit_j)[e] * key_j[comp][prime(e)].  Grid (N / 256, ell + K, items).
+__global__ __launch_bounds__(256) void wk_ks_ip_h(const u64* __restrict__ digits, int inputs, int first, WGal G,
+                                                  WKeys keys, int beta, int ell, int L, int K, int beta_max,
+                                                  u64* __restrict__ acc, long long acc_item, WideTables T) {
+  const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+  const int e = blockIdx.y;
+  const long long it = blockIdx.z;
+  const int ext_l = ell + K;
+  const long long in = (first + it) % inputs;
+  const uint32_t g = G.g[it];
+  const uint32_t ex = ((2u * wbrv16(k) + 1u) * g) & (2u * kN - 1u);
+  const uint32_t src = wbrv16((ex - 1u) >> 1);
+  const int pi = e < ell ? e : L + (e - ell);
+  const Barrett64 br = wbar(T, pi);
+  const u64* key = keys.k[it];
+  const long long comp = (long long)beta_max * (L + K) * kN;
+  const u64* dg = digits + (in * beta * ext_l + e) * (long long)kN + src;
+  u64 ab = 0, aa = 0;
+  for (int j = 0; j < beta; ++j) {
+    const u64 x = dg[(long long)j * ext_l * kN];
+    const long long ko = ((long long)j * (L + K) + pi) * kN + k;
+    ab = wadd(ab, mulmod64(x, key[ko], br), br.p);
+    aa = wadd(aa, mulmod64(x, key[comp + ko], br), br.p);
+  }
+  u64* o = acc + it * acc_item + (long long)e * kN + k;
+  o[0] = ab;
+  o[(long long)ext_l * kN] = aa;
+}
+
+// sigma of every limb of input (first + it) % inputs by G.g[it].  Grid (N / 256, limbs, items).
+__global__ __launch_bounds__(256) void wk_automorph_h(const u64* __restrict__ in, long long in_item, int inputs,
+                                                      int first, u64* __restrict__ out, long long out_item, WGal G) {
+  const uint32_t k = blockIdx.x * 256 + threadIdx.x;
+  const long long it = blockIdx.z, limb = blockIdx.y;
+  const long long src_item = (first + it) % inputs;
+  const uint32_t e = ((2u * wbrv16(k) + 1u) * G.g[it]) & (2u * kN - 1u);
+  const uint32_t src = wbrv16((e - 1u) >> 1);
+  out[it * out_item + limb * kN + k] = in[src_item * in_item + limb * kN + src];
+}
+
 // ------------------------------------------------------------------------------------ elementwise
 struct WPrimeMap {
   uint8_t prime[kMaxPrimes];
@@ -891,6 +934,106 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
       wk_ks_out<<<dim3(kN / 256, ell, nb), 256, 0, s>>>(
           A, 2LL * ext_l * n, CV, (long long)ell * n, comp == 0 ? a0 : nullptr, a0_item,
           accin ? accin + (long long)b0 * acc_stride : nullptr, acc_stride, o, out_stride, T.pinv, T.pinv_s, T);
+      HCK_CHECK_LAUNCH();
+    }
+  }
+  return HCK_OK;
+}
+
+size_t wide_hoist_bytes(const hck_context* c, int ell, int inputs) {
+  return (size_t)std::min(inputs, kWideChunk) * kN * 8 * (size_t)ell;
+}
+
+int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
+               char* ws, hipStream_t s) {
+  if (c->alpha > kMaxAlpha || ell + c->K > kMaxList) return HCK_ERR_UNSUPPORTED;
+  const WideState& W = *c->wide;
+  const WideTables& T = W.t;
+  const int K = c->K, L = c->L, alpha = c->alpha, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const long long n = kN, dig_item = (long long)beta * ext_l * n;
+  const LimbList lq = q_list(ell);
+  for (int b0 = 0; b0 < inputs; b0 += kWideChunk) {
+    const int nb = std::min(kWideChunk, inputs - b0);
+    u64* X = (u64*)ws;
+    const u64* dd = d + (long long)b0 * d_stride;
+    int rc = wide_ntt(c, dd, X, nb, d_stride, (long long)ell * n, lq, true, s);
+    if (rc) return rc;
+    for (int j = 0; j < beta; ++j) {
+      const int lo = j * alpha, hi = std::min(lo + alpha, ell);
+      u64* EXT = digits + (long long)b0 * dig_item + (long long)j * ext_l * n;
+      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(X, (long long)ell * n, lo, EXT, dig_item,
+                                                 W.modup + (size_t)ell * bmax + j, T);
+      HCK_CHECK_LAUNCH();
+      LimbList le;
+      le.n = 0;
+      for (int e = 0; e < ext_l; ++e) {
+        if (e >= lo && e < hi) continue;
+        le.off[le.n] = (uint16_t)e;
+        le.prime[le.n] = (uint8_t)(e < ell ? e : L + (e - ell));
+        ++le.n;
+      }
+      rc = wide_ntt(c, EXT, EXT, nb, dig_item, dig_item, le, false, s);
+      if (rc) return rc;
+      // the digit's own limbs are the input's NTT-domain limbs themselves
+      hipError_t e = hipMemcpy2DAsync(EXT + (long long)lo * n, (size_t)dig_item * 8, dd + (long long)lo * n,
+                                      (size_t)d_stride * 8, (size_t)(hi - lo) * n * 8, (size_t)nb,
+                                      hipMemcpyDeviceToDevice, s);
+      if (e != hipSuccess) return (int)e;
+    }
+  }
+  return HCK_OK;
+}
+
+size_t wide_hoisted_bytes(const hck_context* c, int ell, int items) {
+  // ACC [2][ell + K] + CV [ell] + sigma(c0) [ell] per item of a launch
+  return (size_t)std::min(items, kWideChunk) * kN * 8 * (size_t)(2 * (ell + c->K) + 2 * ell);
+}
+
+int wide_hoisted(const hck_context* c, int ell, int inputs, int items, const uint32_t* galois,
+                 const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
+                 const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
+                 hipStream_t s) {
+  (void)c1;  // its ModUp is in `digits`
+  if (c->alpha > kMaxAlpha || ell + c->K > kMaxList) return HCK_ERR_UNSUPPORTED;
+  const WideState& W = *c->wide;
+  const WideTables& T = W.t;
+  const int K = c->K, L = c->L, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const long long n = kN;
+  const LimbList lq = q_list(ell);
+  LimbList lp;
+  lp.n = K;
+  for (int k = 0; k < K; ++k) {
+    lp.off[k] = (uint16_t)(ell + k);
+    lp.prime[k] = (uint8_t)(L + k);
+  }
+  for (int i0 = 0; i0 < items; i0 += kWideChunk) {
+    const int nb = std::min(kWideChunk, items - i0);
+    u64* ACC = (u64*)ws;
+    u64* CV = ACC + (long long)nb * 2 * ext_l * n;
+    u64* S0 = CV + (long long)nb * ell * n;
+    WGal G{};
+    WKeys kp{};
+    for (int b = 0; b < nb; ++b) {
+      G.g[b] = galois[i0 + b];
+      kp.k[b] = ksk[i0 + b];
+    }
+    const int first = i0 % inputs;
+    wk_ks_ip_h<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(digits, inputs, first, G, kp, beta, ell, L, K, bmax, ACC,
+                                                         2LL * ext_l * n, T);
+    wk_automorph_h<<<dim3(kN / 256, ell, nb), 256, 0, s>>>(c0, in_stride, inputs, first, S0, (long long)ell * n, G);
+    HCK_CHECK_LAUNCH();
+    for (int comp = 0; comp < 2; ++comp) {
+      u64* A = ACC + (long long)comp * ext_l * n;
+      int rc = wide_ntt(c, A, A, nb, 2LL * ext_l * n, 2LL * ext_l * n, lp, true, s);
+      if (rc) return rc;
+      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(A, 2LL * ext_l * n, ell, CV, (long long)ell * n, W.moddown + ell, T);
+      HCK_CHECK_LAUNCH();
+      rc = wide_ntt(c, CV, CV, nb, (long long)ell * n, (long long)ell * n, lq, false, s);
+      if (rc) return rc;
+      u64* o = (comp == 0 ? out_b : out_a) + (long long)i0 * out_stride;
+      wk_ks_out<<<dim3(kN / 256, ell, nb), 256, 0, s>>>(A, 2LL * ext_l * n, CV, (long long)ell * n,
+                                                        comp == 0 ? S0 : nullptr, (long long)ell * n, nullptr, 0, o,
+                                                        out_stride, T.pinv, T.pinv_s, T);
       HCK_CHECK_LAUNCH();
     }
   }

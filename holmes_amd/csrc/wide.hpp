@@ -72,6 +72,14 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
             const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
             char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
             const uint32_t* galois_items);
+size_t wide_hoist_bytes(const hck_context* c, int ell, int inputs);
+int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
+               char* ws, hipStream_t s);
+size_t wide_hoisted_bytes(const hck_context* c, int ell, int items);
+int wide_hoisted(const hck_context* c, int ell, int inputs, int items, const uint32_t* galois,
+                 const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
+                 const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
+                 hipStream_t s);
 size_t wide_moddown_bytes(const hck_context* c, int ell, int polys);
 int wide_moddown(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                  long long out_stride, char* ws, hipStream_t s);

@@ -583,6 +583,7 @@ class PrefillAttention:
         mean = self._fold_keys(ops.mac([(S2, self.valid_over_n)]))       # 2 mean at position 0
         mean = self._spread_keys(ops.mac([(mean, self.row0)]))           # at every key position
         S2 = ops.sub(ops.adjust(S2, ops.limbs(mean), ops.scale(mean)), mean)
+        self._mark("attention_mean")
         # the affine map lands on the prime of the next level: the series input's exact scale
         x = ops.mac([(S2, self.exp_alpha_valid)], out_scale=ops.ideal_scale(ops.limbs(S2) - 1))
         x = ops.add_const(x, self.exp_beta) if self.exp_beta else x

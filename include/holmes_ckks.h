@@ -208,8 +208,8 @@ int hck_rotate_ext_sum(const hck_context* ctx, int level_limbs, int outputs, int
  * digits through sigma (ModUp commutes with the automorphism), so each rotation skips the INTT,
  * the conversion and the digits' NTT.  Bit-identical to hck_rotate_many.  c0 / c1 at
  * input * in_stride, out at i * out_stride.  Workspace hck_rotate_hoist_workspace_bytes(ctx,
- * level_limbs, inputs, items) serves both calls.  HCK_ERR_UNSUPPORTED on a context with a prime at
- * or above 2^50. */
+ * level_limbs, inputs, items) serves both calls.  Both prime widths (the wide path reads the
+ * digits through sigma in its inner-product kernel). */
 size_t hck_rotate_hoist_digits_bytes(const hck_context* ctx, int level_limbs, int inputs);
 size_t hck_rotate_hoist_workspace_bytes(const hck_context* ctx, int level_limbs, int inputs, int items);
 int hck_rotate_hoist_prepare(const hck_context* ctx, int level_limbs, int inputs, const uint64_t* c1,

@@ -2,7 +2,8 @@
 (assets/feature_major.json: N = 2^16, 38 Q limbs -- q_0 of 60 bits, the other 37 of 59 bits -- dnum
 5, 8 special primes of 60 bits), every kernel through the C ABI bit-exact against the CPU oracle
 (exact 128-bit arithmetic for any prime below 2^62): NTT, automorphism, elementwise ops, key
-generation, key switch at 38, 19 and 8 limbs, rotation with and without addends, the extended-basis
+generation, key switch at 38, 19 and 8 limbs, rotation with and without addends, hoisted rotations,
+the extended-basis
 rotation and ModDown, rescale, ModRaise, tensor and relinearisation, the BSGS MAC and the encoder
 for coefficients up to 2^61.  Several checks are the FP64 path's own test bodies, run here on the
 wide context."""
@@ -105,6 +106,13 @@ def test_rotate_and_rescale(env):
 @pytest.mark.parametrize("ell,rot", [(19, 128), (3, -3)])
 def test_rotate_accumulate_batch(env, ell, rot):
     G.test_rotate_accumulate_batch_matches_oracle(env, ell, rot)
+
+
+@pytest.mark.parametrize("ell,inputs,per", [(38, 3, 4), (11, 2, 3), (1, 1, 2)])
+def test_hoisted_rotations(env, ell, inputs, per):
+    """Hoisted rotations on the wide path (one ModUp per input, the digits read through sigma in
+    the inner product): bit-identical to the per-item key switch and to the oracle."""
+    G.test_hoisted_rotations_equal_rotate_many(env, ell, inputs, per)
 
 
 @pytest.mark.parametrize("ell", [38, 7])
