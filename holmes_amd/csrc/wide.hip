@@ -96,12 +96,53 @@ __device__ __forceinline__ Barrett64 wbar(const WideTables& T, int pi) { return 
 // (src == dst allowed: a block reads its 16 columns or rows whole before it writes them back)
 // over the 256 x 256 view of a limb (element 256 r + c): the first eight stages act on the columns
 // (fixed c, a 256-point transform over r with root psi_rev[m + r-group]), the last eight on the rows.
-// A block holds 16 columns or 16 rows (32 KiB of LDS); 256 threads, 8 butterflies each per stage.
+// A block holds 16 columns or 16 rows; 256 threads.  Each pass runs its eight stages as two
+// radix-16 rounds in registers (16 words per thread) with one LDS exchange between them: in the
+// first round a thread holds the 16 elements 16 apart, in the second the 16 consecutive ones.
 constexpr int kWT = 256;
+constexpr int kWPad = 17;  // LDS row stride of the column kernels (words)
+
+__device__ __forceinline__ int wpad(int k) { return k + (k >> 4); }  // row kernels' LDS index
+
+// Four Cooley-Tukey stages over x[0..15] at distances 8, 4, 2, 1: stage s pairs (u, u + (8 >> s))
+// with root index base(s) + (group(s, u)), the caller's closure.
+template <typename Root>
+__device__ __forceinline__ void wfwd16(u64 (&x)[16], const u64* tw, const u64* tws, u64 p, Root root) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d = 8 >> s;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u & d) continue;
+      const int wi = root(s, u);
+      const u64 y = wmulc(x[u + d], tw[wi], tws[wi], p);
+      const u64 a = x[u];
+      x[u] = wadd(a, y, p);
+      x[u + d] = wsub(a, y, p);
+    }
+  }
+}
+
+// Four Gentleman-Sande stages over x[0..15] at distances 1, 2, 4, 8: (a, b) -> (a + b, (a - b) w).
+template <typename Root>
+__device__ __forceinline__ void winv16(u64 (&x)[16], const u64* tw, const u64* tws, u64 p, Root root) {
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d = 1 << s;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u & d) continue;
+      const int wi = root(s, u);
+      const u64 a = x[u], b = x[u + d];
+      x[u] = wadd(a, b, p);
+      x[u + d] = wmulc(wsub(a, b, p), tw[wi], tws[wi], p);
+    }
+  }
+}
 
 __global__ __launch_bounds__(kWT) void wk_fwd_cols(const u64* src, u64* dst, long long ss,
                                                    long long ds, LimbList list, WideTables T) {
-  __shared__ u64 sh[256 * 16];
+  __shared__ u64 sh[256 * kWPad];
   const int e = blockIdx.y;
   const long long g = blockIdx.z;
   const int pi = list.prime[e];
@@ -111,35 +152,25 @@ __global__ __launch_bounds__(kWT) void wk_fwd_cols(const u64* src, u64* dst, lon
   const u64* in = src + g * ss + (long long)list.off[e] * kN;
   u64* out = dst + g * ds + (long long)list.off[e] * kN;
   const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
+  u64 x[16];
+  // rows r + 16 u of column c: stages 0..3 (row distances 128 .. 16), root (1 << s) + (u >> (4 - s))
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int k = r + 16 * m;
-    sh[k * 16 + cl] = in[c + 256 * k];
-  }
+  for (int u = 0; u < 16; ++u) x[u] = in[c + 256 * (r + 16 * u)];
+  wfwd16(x, tw, tws, p, [](int s, int u) { return (1 << s) + (u >> (4 - s)); });
+#pragma unroll
+  for (int u = 0; u < 16; ++u) sh[(r + 16 * u) * kWPad + cl] = x[u];
   __syncthreads();
-  for (int s = 0; s < 8; ++s) {
-    const int m = 1 << s, t = 128 >> s;
+  // rows 16 q + m (q = r): stages 4..7 (row distances 8 .. 1), root (16 << s) + ((16 q + m) >> (4 - s))
+  const int q = r;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int b = r + 16 * u;
-      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
-      const int wi = m + b / t;
-      const u64 x = sh[k1 * 16 + cl];
-      const u64 y = wmulc(sh[k2 * 16 + cl], tw[wi], tws[wi], p);
-      sh[k1 * 16 + cl] = wadd(x, y, p);
-      sh[k2 * 16 + cl] = wsub(x, y, p);
-    }
-    __syncthreads();
-  }
+  for (int m = 0; m < 16; ++m) x[m] = sh[(16 * q + m) * kWPad + cl];
+  wfwd16(x, tw, tws, p, [q](int s, int m) { return (16 << s) + ((16 * q + m) >> (4 - s)); });
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int k = r + 16 * m;
-    out[c + 256 * k] = sh[k * 16 + cl];
-  }
+  for (int m = 0; m < 16; ++m) out[c + 256 * (16 * q + m)] = x[m];
 }
 
 __global__ __launch_bounds__(kWT) void wk_fwd_rows(u64* __restrict__ dst, long long ds, LimbList list, WideTables T) {
-  __shared__ u64 sh[16 * 256];
+  __shared__ u64 sh[16 * 272];
   const int e = blockIdx.y;
   const long long g = blockIdx.z;
   const int pi = list.prime[e];
@@ -148,32 +179,34 @@ __global__ __launch_bounds__(kWT) void wk_fwd_rows(u64* __restrict__ dst, long l
   const u64* tws = T.fwd_s + (size_t)pi * kN;
   u64* io = dst + g * ds + (long long)list.off[e] * kN + (long long)blockIdx.x * 4096;
   const int tid = threadIdx.x, rr = tid >> 4, lane = tid & 15, r = blockIdx.x * 16 + rr;
+  u64* row = sh + rr * 272;
+  u64 x[16];
+  // elements lane + 16 u of row r: stages 8..11 (distances 128 .. 16),
+  // root (256 << s) + r (1 << s) + (u >> (4 - s))
 #pragma unroll
-  for (int m = 0; m < 16; ++m) sh[tid + 256 * m] = io[tid + 256 * m];
+  for (int u = 0; u < 16; ++u) x[u] = io[rr * 256 + lane + 16 * u];
+  wfwd16(x, tw, tws, p, [r](int s, int u) { return (256 << s) + (r << s) + (u >> (4 - s)); });
+#pragma unroll
+  for (int u = 0; u < 16; ++u) row[wpad(lane + 16 * u)] = x[u];
   __syncthreads();
-  for (int s = 0; s < 8; ++s) {
-    const int t = 128 >> s, m = 256 << s;
+  // elements 16 q + m (q = lane): stages 12..15 (distances 8 .. 1),
+  // root (4096 << s) + r (16 << s) + ((16 q + m) >> (4 - s))
+  const int q = lane;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int b = lane + 16 * u;
-      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
-      const int wi = m + r * (128 / t) + b / t;
-      const u64 x = sh[rr * 256 + k1];
-      const u64 y = wmulc(sh[rr * 256 + k2], tw[wi], tws[wi], p);
-      sh[rr * 256 + k1] = wadd(x, y, p);
-      sh[rr * 256 + k2] = wsub(x, y, p);
-    }
-    __syncthreads();
-  }
+  for (int m = 0; m < 16; ++m) x[m] = row[wpad(16 * q + m)];
+  wfwd16(x, tw, tws, p, [r, q](int s, int m) { return (4096 << s) + (r << (4 + s)) + ((16 * q + m) >> (4 - s)); });
 #pragma unroll
-  for (int m = 0; m < 16; ++m) io[tid + 256 * m] = sh[tid + 256 * m];
+  for (int m = 0; m < 16; ++m) row[wpad(16 * q + m)] = x[m];
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 16; ++u) io[rr * 256 + lane + 16 * u] = row[wpad(lane + 16 * u)];
 }
 
 // Inverse transform (Gentleman-Sande with psi^-brv roots, then N^-1): the first eight stages act
 // on the rows, the last eight on the columns, which also apply N^-1.
 __global__ __launch_bounds__(kWT) void wk_inv_rows(const u64* src, u64* dst, long long ss,
                                                    long long ds, LimbList list, WideTables T) {
-  __shared__ u64 sh[16 * 256];
+  __shared__ u64 sh[16 * 272];
   const int e = blockIdx.y;
   const long long g = blockIdx.z;
   const int pi = list.prime[e];
@@ -183,28 +216,30 @@ __global__ __launch_bounds__(kWT) void wk_inv_rows(const u64* src, u64* dst, lon
   const u64* in = src + g * ss + (long long)list.off[e] * kN + (long long)blockIdx.x * 4096;
   u64* out = dst + g * ds + (long long)list.off[e] * kN + (long long)blockIdx.x * 4096;
   const int tid = threadIdx.x, rr = tid >> 4, lane = tid & 15, r = blockIdx.x * 16 + rr;
+  u64* row = sh + rr * 272;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) sh[tid + 256 * m] = in[tid + 256 * m];
+  for (int u = 0; u < 16; ++u) row[wpad(lane + 16 * u)] = in[rr * 256 + lane + 16 * u];
   __syncthreads();
-  for (int s = 0; s < 8; ++s) {
-    const int t = 1 << s, h = (kN / 2) >> s;
+  u64 x[16];
+  // elements 16 q + m (q = lane): stages 0..3 (distances 1 .. 8),
+  // root (32768 >> s) + r (128 >> s) + ((16 q + m) >> (s + 1))
+  const int q = lane;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int b = lane + 16 * u;
-      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
-      const int wi = h + r * (128 / t) + b / t;
-      const u64 x = sh[rr * 256 + k1], y = sh[rr * 256 + k2];
-      sh[rr * 256 + k1] = wadd(x, y, p);
-      sh[rr * 256 + k2] = wmulc(wsub(x, y, p), tw[wi], tws[wi], p);
-    }
-    __syncthreads();
-  }
+  for (int m = 0; m < 16; ++m) x[m] = row[wpad(16 * q + m)];
+  winv16(x, tw, tws, p, [r, q](int s, int m) { return (32768 >> s) + r * (128 >> s) + ((16 * q + m) >> (s + 1)); });
 #pragma unroll
-  for (int m = 0; m < 16; ++m) out[tid + 256 * m] = sh[tid + 256 * m];
+  for (int m = 0; m < 16; ++m) row[wpad(16 * q + m)] = x[m];
+  __syncthreads();
+  // elements lane + 16 u: stages 4..7 (distances 16 .. 128), root (2048 >> s) + r (8 >> s) + (u >> (s + 1))
+#pragma unroll
+  for (int u = 0; u < 16; ++u) x[u] = row[wpad(lane + 16 * u)];
+  winv16(x, tw, tws, p, [r](int s, int u) { return (2048 >> s) + r * (8 >> s) + (u >> (s + 1)); });
+#pragma unroll
+  for (int u = 0; u < 16; ++u) out[rr * 256 + lane + 16 * u] = x[u];
 }
 
 __global__ __launch_bounds__(kWT) void wk_inv_cols(u64* __restrict__ dst, long long ds, LimbList list, WideTables T) {
-  __shared__ u64 sh[256 * 16];
+  __shared__ u64 sh[256 * kWPad];
   const int e = blockIdx.y;
   const long long g = blockIdx.z;
   const int pi = list.prime[e];
@@ -214,30 +249,21 @@ __global__ __launch_bounds__(kWT) void wk_inv_cols(u64* __restrict__ dst, long l
   const u64 ni = T.ninv[pi], nis = T.ninv_s[pi];
   u64* io = dst + g * ds + (long long)list.off[e] * kN;
   const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
+  u64 x[16];
+  // rows 16 q + m of column c (q = r): stages 8..11 (row distances 1 .. 8), root (128 >> s) + ((16 q + m) >> (s + 1))
+  const int q = r;
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int k = r + 16 * m;
-    sh[k * 16 + cl] = io[c + 256 * k];
-  }
+  for (int m = 0; m < 16; ++m) x[m] = io[c + 256 * (16 * q + m)];
+  winv16(x, tw, tws, p, [q](int s, int m) { return (128 >> s) + ((16 * q + m) >> (s + 1)); });
+#pragma unroll
+  for (int m = 0; m < 16; ++m) sh[(16 * q + m) * kWPad + cl] = x[m];
   __syncthreads();
-  for (int s = 0; s < 8; ++s) {
-    const int t = 1 << s, h = 128 >> s;
+  // rows r + 16 u: stages 12..15 (row distances 16 .. 128), root (8 >> s) + (u >> (s + 1)); then N^-1
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int b = r + 16 * u;
-      const int k1 = (b / t) * 2 * t + (b % t), k2 = k1 + t;
-      const int wi = h + b / t;
-      const u64 x = sh[k1 * 16 + cl], y = sh[k2 * 16 + cl];
-      sh[k1 * 16 + cl] = wadd(x, y, p);
-      sh[k2 * 16 + cl] = wmulc(wsub(x, y, p), tw[wi], tws[wi], p);
-    }
-    __syncthreads();
-  }
+  for (int u = 0; u < 16; ++u) x[u] = sh[(r + 16 * u) * kWPad + cl];
+  winv16(x, tw, tws, p, [](int s, int u) { return (8 >> s) + (u >> (s + 1)); });
 #pragma unroll
-  for (int m = 0; m < 16; ++m) {
-    const int k = r + 16 * m;
-    io[c + 256 * k] = wmulc(sh[k * 16 + cl], ni, nis, p);
-  }
+  for (int u = 0; u < 16; ++u) io[c + 256 * (r + 16 * u)] = wmulc(x[u], ni, nis, p);
 }
 
 // ----------------------------------------------------------------------------- base conversion
@@ -316,31 +342,33 @@ __global__ __launch_bounds__(256) void wk_automorph(const u64* __restrict__ in, 
   out[it * out_item + limb * kN + k] = in[it * in_item + limb * kN + src];
 }
 
-// acc[item][comp][e] (+)= x[e] * key_j[comp][prime(e)], x the ModUp output (the digit's own limbs
-// read from the NTT-domain input d).  acc per item: [2][ell + K][N].  Grid (N / 256, ell + K, items).
+// acc[item][comp][e] = sum_j x_j[e] * key_j[comp][prime(e)] over every digit j in one pass, x_j the
+// ModUp output of digit j ([beta][ell + K] per item; the digit's own limbs read from the NTT-domain
+// input d).  acc per item: [2][ell + K][N].  Grid (N / 256, ell + K, items).
 __global__ __launch_bounds__(256) void wk_ks_ip(const u64* __restrict__ ext, long long ext_item,
-                                                const u64* __restrict__ d, long long d_item, int lo, int hi, WKeys keys,
-                                                int j, int ell, int L, int K, int beta_max, u64* __restrict__ acc,
-                                                long long acc_item, int first, WideTables T) {
+                                                const u64* __restrict__ d, long long d_item, int alpha, int beta,
+                                                WKeys keys, int ell, int L, int K, int beta_max, u64* __restrict__ acc,
+                                                long long acc_item, WideTables T) {
   const int k = blockIdx.x * 256 + threadIdx.x;
   const int e = blockIdx.y;
   const long long it = blockIdx.z;
+  const int ext_l = ell + K;
   const int pi = e < ell ? e : L + (e - ell);
   const Barrett64 br = wbar(T, pi);
-  const u64 x = (e >= lo && e < hi) ? d[it * d_item + (long long)e * kN + k] : ext[it * ext_item + (long long)e * kN + k];
   const u64* key = keys.k[it];
   const long long comp = (long long)beta_max * (L + K) * kN;
-  const long long ko = ((long long)j * (L + K) + pi) * kN + k;
-  const u64 pb = mulmod64(x, key[ko], br), pa = mulmod64(x, key[comp + ko], br);
-  u64* ab = acc + it * acc_item + (long long)e * kN + k;
-  u64* aa = ab + (long long)(ell + K) * kN;
-  if (first) {
-    *ab = pb;
-    *aa = pa;
-  } else {
-    *ab = wadd(*ab, pb, br.p);
-    *aa = wadd(*aa, pa, br.p);
+  const int own = e < ell ? e / alpha : -1;  // the digit whose own limb e is
+  u64 ab = 0, aa = 0;
+  for (int j = 0; j < beta; ++j) {
+    const u64 x = j == own ? d[it * d_item + (long long)e * kN + k]
+                           : ext[it * ext_item + ((long long)j * ext_l + e) * kN + k];
+    const long long ko = ((long long)j * (L + K) + pi) * kN + k;
+    ab = wadd(ab, mulmod64(x, key[ko], br), br.p);
+    aa = wadd(aa, mulmod64(x, key[comp + ko], br), br.p);
   }
+  u64* o = acc + it * acc_item + (long long)e * kN + k;
+  o[0] = ab;
+  o[(long long)ext_l * kN] = aa;
 }
 
 // out[i] = (x[i] - cv[i]) P^-1 mod q_i (+ add1[i]) (+ add2[i]).  Grid (N / 256, ell, items).
@@ -840,8 +868,9 @@ LimbList q_list(int ell, int first = 0) {
 
 // Per item: X (ell) + EXT (ell + K) + ACC (2 (ell + K)) + CV (ell) + SD (ell) + S0 (ell) limbs.
 size_t wide_ks_bytes(const hck_context* c, int ell, int batch) {
-  const size_t nb = (size_t)std::min(batch, kWideChunk);
-  return nb * (size_t)kN * 8 * (size_t)(7 * ell + 3 * c->K);
+  // per item: X [ell], EXT [beta][ell + K], ACC [2][ell + K], CV, SD, S0 [ell] each
+  const size_t nb = (size_t)std::min(batch, kWideChunk), ext_l = (size_t)(ell + c->K);
+  return nb * (size_t)kN * 8 * (4 * (size_t)ell + ((size_t)beta_of(c, ell) + 2) * ext_l);
 }
 
 int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
@@ -865,8 +894,9 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
   for (int b0 = 0; b0 < batch; b0 += kWideChunk) {
     const int nb = std::min(kWideChunk, batch - b0);
     u64* X = (u64*)ws;
-    u64* EXT = X + (long long)nb * ell * n;
-    u64* ACC = EXT + (long long)nb * ext_l * n;
+    u64* EXT = X + (long long)nb * ell * n;                  // [nb][beta][ext_l]
+    const long long ext_item = (long long)beta * ext_l * n;
+    u64* ACC = EXT + (long long)nb * ext_item;
     u64* CV = ACC + (long long)nb * 2 * ext_l * n;
     u64* SD = CV + (long long)nb * ell * n;
     u64* S0 = SD + (long long)nb * ell * n;
@@ -891,9 +921,12 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
     if (rc) return rc;
     WKeys kp{};
     for (int b = 0; b < nb; ++b) kp.k[b] = ksk[b0 + b];
+    // every digit's ModUp into its own slab, then one inner product over all of them: the
+    // accumulators are written once instead of read and written per digit
     for (int j = 0; j < beta; ++j) {
       const int lo = j * alpha, hi = std::min(lo + alpha, ell);
-      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(X, (long long)ell * n, lo, EXT, (long long)ext_l * n,
+      u64* EXTj = EXT + (long long)j * ext_l * n;
+      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(X, (long long)ell * n, lo, EXTj, ext_item,
                                                  W.modup + (size_t)ell * bmax + j, T);
       HCK_CHECK_LAUNCH();
       LimbList le;
@@ -904,12 +937,12 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
         le.prime[le.n] = (uint8_t)(e < ell ? e : L + (e - ell));
         ++le.n;
       }
-      rc = wide_ntt(c, EXT, EXT, nb, (long long)ext_l * n, (long long)ext_l * n, le, false, s);
+      rc = wide_ntt(c, EXTj, EXTj, nb, ext_item, ext_item, le, false, s);
       if (rc) return rc;
-      wk_ks_ip<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(EXT, (long long)ext_l * n, dd, dd_item, lo, hi, kp, j, ell, L, K,
-                                                         bmax, ACC, 2LL * ext_l * n, j == 0, T);
-      HCK_CHECK_LAUNCH();
     }
+    wk_ks_ip<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(EXT, ext_item, dd, dd_item, alpha, beta, kp, ell, L, K, bmax, ACC,
+                                                       2LL * ext_l * n, T);
+    HCK_CHECK_LAUNCH();
     if (ext_b) {
       const long long ai = (long long)b0 * acc_stride, ei = (long long)b0 * ext_stride;
       wk_ks_ext_out<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(ACC, 2LL * ext_l * n, a0, a0_item,

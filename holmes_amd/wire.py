@@ -29,7 +29,6 @@ prime-chain fingerprint makes a receiver with another context refuse the bytes.
 
 from __future__ import annotations
 
-import copy
 import hashlib
 import struct
 from dataclasses import dataclass
@@ -186,21 +185,21 @@ def validate_cipher(cipher, *, expected_device: str | None = None) -> CipherMeta
 
 
 def rebuild_cipher(template, components: Iterable):
-    """A ciphertext with ``template``'s state and encoding around ``components`` (template kept)."""
+    """A ciphertext around ``components`` with ``template``'s state and encoding.  A template with
+    ``cipher_like`` (any ciphertext of this backend) builds it; otherwise the template only has to
+    carry ``state``, ``slots``, ``is_ext`` and ``batch_size`` -- a packet's metadata does -- and a
+    Cipher of this backend is made from them."""
 
     comps = list(components)
-    maker = getattr(template, "cipher_like", None)
-    if callable(maker):
-        return maker(comps)
+    if callable(getattr(template, "cipher_like", None)):
+        return template.cipher_like(comps)
     from .context import Cipher
 
-    try:
-        return Cipher(comps, template.state, slots=int(template.slots), is_ext=bool(getattr(template, "is_ext", False)),
-                      batch_size=int(getattr(template, "batch_size", 1)))
-    except (AttributeError, TypeError, ValueError):
-        other = copy.copy(template)  # a ciphertext type of another backend: keep its class
-        other.cv = comps
-        return other
+    missing = [k for k in ("state", "slots") if getattr(template, k, None) is None]
+    if missing:
+        raise TypeError(f"a rebuild template needs {', '.join(missing)} (or a cipher_like method)")
+    return Cipher(comps, template.state, slots=int(template.slots), is_ext=bool(getattr(template, "is_ext", False)),
+                  batch_size=int(getattr(template, "batch_size", 1)))
 
 
 def _host_copy(component):
@@ -259,15 +258,6 @@ def pack_cipher(cipher, *, tag: str = "", host: bool = True) -> CipherPacket:
     return packet
 
 
-class _PacketTemplate:
-    """What rebuild_cipher needs from a template, taken from a packet."""
-
-    def __init__(self, packet: CipherPacket) -> None:
-        md = packet.metadata
-        self.state, self.slots, self.is_ext, self.batch_size = packet.state, md.slots, md.is_ext, md.batch_size
-        self.cv: list = []
-
-
 def unpack_cipher(packet: CipherPacket, *, device: str = "cuda", template=None):
     """The packet's ciphertext on ``device`` (its components never share storage with the sender's).
     Without a ``template`` the packet's own state is used.  A result whose metadata differs from
@@ -277,7 +267,12 @@ def unpack_cipher(packet: CipherPacket, *, device: str = "cuda", template=None):
     if template is None and packet.state is None:
         raise ValueError("the packet carries no state; pass a template ciphertext")
     comps = [_placed(c, str(device)) for c in packet.components]
-    result = rebuild_cipher(template if template is not None else _PacketTemplate(packet), comps)
+    if template is None:
+        from types import SimpleNamespace
+
+        md = packet.metadata
+        template = SimpleNamespace(state=packet.state, slots=md.slots, is_ext=md.is_ext, batch_size=md.batch_size)
+    result = rebuild_cipher(template, comps)
     arrived = validate_cipher(result, expected_device=str(device)).without_devices()
     sent = packet.metadata.without_devices()
     if arrived != sent:
