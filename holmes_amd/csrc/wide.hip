@@ -70,9 +70,14 @@ void fill_wide_conv(WideConv& cc, const std::vector<u64>& P, const std::vector<i
         if (r != s) v = hmul(v, P[src[r]] % qt, qt);
       cc.hmod[s][t] = v;
       cc.hmod_s[s][t] = shoup_companion(v, qt);
+      cc.hmod_m[s][t] = (u64)(((u128)v << 64) % qt);
     }
   }
   for (int t = 0; t < cc.nt; ++t) {
+    const u64 qt = P[dst[t]];
+    u64 inv = qt;  // Newton's iteration for qt^-1 mod 2^64: each step doubles the correct low bits
+    for (int i = 0; i < 6; ++i) inv *= 2 - qt * inv;
+    cc.tneg_inv[t] = 0 - inv;
     cc.dst_prime[t] = dst[t];
     cc.dst_slot[t] = slot[t];
   }
@@ -269,7 +274,11 @@ __global__ __launch_bounds__(kWT) void wk_inv_cols(u64* __restrict__ dst, long l
 // ----------------------------------------------------------------------------- base conversion
 // dst[item][slot t][k] = sum_s ybar_s * (B / b_s) mod t, ybar_s the centered representative of
 // y_s = x_s (B / b_s)^-1 mod b_s (the oracle's base_conv).  Sources are the ns consecutive limbs from
-// src_off.  Grid (N / 256, items).
+// src_off.  The sum is taken lazily: with |ybar_s| < b_s / 2 < 2^60 and the constants in Montgomery
+// form f = (B / b_s) 2^64 mod t (negated, t - f, for a negative ybar_s), every term is a positive
+// 128-bit product and the whole sum stays below 2^63 t (ns <= 8), so one Montgomery reduction
+// (x + m t) / 2^64, m = x (-t^-1) mod 2^64, lands it in [0, 2t) with the 2^64 factor removed.
+// Grid (N / 256, items).
 __global__ __launch_bounds__(256) void wk_conv(const u64* __restrict__ src, long long src_item, int src_off,
                                                u64* __restrict__ dst, long long dst_item,
                                                const WideConv* __restrict__ cc, WideTables T) {
@@ -291,14 +300,17 @@ __global__ __launch_bounds__(256) void wk_conv(const u64* __restrict__ src, long
   }
   for (int t = 0; t < nt; ++t) {
     const u64 q = T.p[cc->dst_prime[t]];
-    u64 acc = 0;
+    u128 x = 0;
 #pragma unroll
     for (int s = 0; s < kMaxAlpha; ++s) {
       if (s >= ns) break;
-      const u64 prod = wmulc(y[s], cc->hmod[s][t], cc->hmod_s[s][t], q);
-      acc = neg[s] ? wsub(acc, prod, q) : wadd(acc, prod, q);
+      const u64 f = cc->hmod_m[s][t];
+      x += (u128)y[s] * (neg[s] ? q - f : f);
     }
-    dst[it * dst_item + (long long)cc->dst_slot[t] * kN + k] = acc;
+    const u64 m = (u64)x * cc->tneg_inv[t];
+    u64 r = (u64)((x + (u128)m * q) >> 64);
+    r = r >= q ? r - q : r;
+    dst[it * dst_item + (long long)cc->dst_slot[t] * kN + k] = r;
   }
 }
 

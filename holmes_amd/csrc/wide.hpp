@@ -27,6 +27,8 @@ struct WideConv {
   uint64_t hinv[kMaxAlpha], hinv_s[kMaxAlpha];        // (B / b_s)^-1 mod b_s
   uint64_t hmod[kMaxAlpha][kMaxPrimes];               // (B / b_s) mod t
   uint64_t hmod_s[kMaxAlpha][kMaxPrimes];
+  uint64_t hmod_m[kMaxAlpha][kMaxPrimes];             // (B / b_s) 2^64 mod t (Montgomery form)
+  uint64_t tneg_inv[kMaxPrimes];                      // -t^-1 mod 2^64
 };
 
 struct WideTables {
