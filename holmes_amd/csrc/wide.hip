@@ -354,33 +354,71 @@ __global__ __launch_bounds__(256) void wk_automorph(const u64* __restrict__ in, 
   out[it * out_item + limb * kN + k] = in[it * in_item + limb * kN + src];
 }
 
-// acc[item][comp][e] = sum_j x_j[e] * key_j[comp][prime(e)] over every digit j in one pass, x_j the
-// ModUp output of digit j ([beta][ell + K] per item; the digit's own limbs read from the NTT-domain
-// input d).  acc per item: [2][ell + K][N].  Grid (N / 256, ell + K, items).
-__global__ __launch_bounds__(256) void wk_ks_ip(const u64* __restrict__ ext, long long ext_item,
-                                                const u64* __restrict__ d, long long d_item, int alpha, int beta,
-                                                WKeys keys, int ell, int L, int K, int beta_max, u64* __restrict__ acc,
-                                                long long acc_item, WideTables T) {
-  const int k = blockIdx.x * 256 + threadIdx.x;
+// The inner product fused with the forward NTT's row pass: for every digit j, the block takes the
+// column-pass output of digit j on its 16 rows of limb e (the digit's own limb: the NTT-domain input
+// d as it is), finishes the transform in registers (the wk_fwd_rows body), and multiplies by both
+// key halves, accumulating over the digits on chip; acc[item][comp][e] is written once.
+// Grid (16, ell + K, items).
+__global__ __launch_bounds__(kWT) void wk_ks_ip_rows(const u64* __restrict__ ext, long long ext_item,
+                                                     const u64* __restrict__ d, long long d_item, int alpha,
+                                                     int beta, WKeys keys, int ell, int L, int K, int beta_max,
+                                                     u64* __restrict__ acc, long long acc_item, WideTables T) {
+  __shared__ u64 sh[16 * 272];
   const int e = blockIdx.y;
   const long long it = blockIdx.z;
   const int ext_l = ell + K;
   const int pi = e < ell ? e : L + (e - ell);
+  const u64 p = T.p[pi];
   const Barrett64 br = wbar(T, pi);
+  const u64* tw = T.fwd + (size_t)pi * kN;
+  const u64* tws = T.fwd_s + (size_t)pi * kN;
+  const int tid = threadIdx.x, rr = tid >> 4, lane = tid & 15, r = blockIdx.x * 16 + rr;
+  const long long base = (long long)blockIdx.x * 4096 + rr * 256 + lane;  // element lane + 16 u of row r
   const u64* key = keys.k[it];
   const long long comp = (long long)beta_max * (L + K) * kN;
-  const int own = e < ell ? e / alpha : -1;  // the digit whose own limb e is
-  u64 ab = 0, aa = 0;
+  const int own = e < ell ? e / alpha : -1;
+  u64* row = sh + rr * 272;
+  u64 ab[16], aa[16], x[16];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) ab[u] = aa[u] = 0;
   for (int j = 0; j < beta; ++j) {
-    const u64 x = j == own ? d[it * d_item + (long long)e * kN + k]
-                           : ext[it * ext_item + ((long long)j * ext_l + e) * kN + k];
-    const long long ko = ((long long)j * (L + K) + pi) * kN + k;
-    ab = wadd(ab, mulmod64(x, key[ko], br), br.p);
-    aa = wadd(aa, mulmod64(x, key[comp + ko], br), br.p);
+    if (j == own) {
+      const u64* src = d + it * d_item + (long long)e * kN + base;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = src[16 * u];
+    } else {
+      const u64* src = ext + it * ext_item + ((long long)j * ext_l + e) * kN + base;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = src[16 * u];
+      wfwd16(x, tw, tws, p, [r](int s, int u) { return (256 << s) + (r << s) + (u >> (4 - s)); });
+#pragma unroll
+      for (int u = 0; u < 16; ++u) row[wpad(lane + 16 * u)] = x[u];
+      __syncthreads();
+      const int q = lane;
+#pragma unroll
+      for (int m = 0; m < 16; ++m) x[m] = row[wpad(16 * q + m)];
+      wfwd16(x, tw, tws, p,
+             [r, q](int s, int m) { return (4096 << s) + (r << (4 + s)) + ((16 * q + m) >> (4 - s)); });
+#pragma unroll
+      for (int m = 0; m < 16; ++m) row[wpad(16 * q + m)] = x[m];
+      __syncthreads();
+#pragma unroll
+      for (int u = 0; u < 16; ++u) x[u] = row[wpad(lane + 16 * u)];
+      __syncthreads();  // the LDS rows are rewritten by the next digit
+    }
+    const u64* kb = key + ((long long)j * (L + K) + pi) * kN + base;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      ab[u] = wadd(ab[u], mulmod64(x[u], kb[16 * u], br), p);
+      aa[u] = wadd(aa[u], mulmod64(x[u], kb[comp + 16 * u], br), p);
+    }
   }
-  u64* o = acc + it * acc_item + (long long)e * kN + k;
-  o[0] = ab;
-  o[(long long)ext_l * kN] = aa;
+  u64* o = acc + it * acc_item + (long long)e * kN + base;
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    o[16 * u] = ab[u];
+    o[(long long)ext_l * kN + 16 * u] = aa[u];
+  }
 }
 
 // out[i] = (x[i] - cv[i]) P^-1 mod q_i (+ add1[i]) (+ add2[i]).  Grid (N / 256, ell, items).
@@ -949,11 +987,12 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
         le.prime[le.n] = (uint8_t)(e < ell ? e : L + (e - ell));
         ++le.n;
       }
-      rc = wide_ntt(c, EXTj, EXTj, nb, ext_item, ext_item, le, false, s);
-      if (rc) return rc;
+      // the column pass only: the inner product finishes each digit's transform on chip
+      wk_fwd_cols<<<dim3(16, le.n, nb), kWT, 0, s>>>(EXTj, EXTj, ext_item, ext_item, le, T);
+      HCK_CHECK_LAUNCH();
     }
-    wk_ks_ip<<<dim3(kN / 256, ext_l, nb), 256, 0, s>>>(EXT, ext_item, dd, dd_item, alpha, beta, kp, ell, L, K, bmax, ACC,
-                                                       2LL * ext_l * n, T);
+    wk_ks_ip_rows<<<dim3(16, ext_l, nb), kWT, 0, s>>>(EXT, ext_item, dd, dd_item, alpha, beta, kp, ell, L, K, bmax,
+                                                      ACC, 2LL * ext_l * n, T);
     HCK_CHECK_LAUNCH();
     if (ext_b) {
       const long long ai = (long long)b0 * acc_stride, ei = (long long)b0 * ext_stride;
