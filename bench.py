@@ -97,6 +97,9 @@ def main() -> int:
     ap.add_argument("--ks-slice-items", type=int, default=0, help="items per slice of the multi-stream schedule")
     ap.add_argument("--conv-engine", choices=("mfma", "valu"), default="mfma",
                     help="c2 ModUp / ModDown conversion sums: int8 matrix cores or FP64 VALU (same results)")
+    ap.add_argument("--chain", choices=("50", "reference"), default="50",
+                    help="layer: the 38-limb chain on 50-bit primes (FP64 kernels) or the reference's own "
+                         "60/59-bit primes (assets/feature_major.json; 64-bit integer kernels)")
     ap.add_argument("--strategy", choices=("normal", "ext_double_hoist"), default="ext_double_hoist",
                     help="c3 giant steps: Horner chain (normal) or double hoisting in the extended basis "
                          "(both are hoist strategies of the reference's LinearOperatorConfig)")
@@ -1218,18 +1221,20 @@ def c2_traffic():
     return int(rec["traffic_bytes"]), rec
 
 
-def _layer_setup(seed: int = 20261206) -> dict:
-    """The N1 workload: the 38-limb context, every rotation key and refresh program of the layer,
-    the first-layer and steady-state PrefillLayer objects, and the encrypted input (128 tokens x
-    4096 features N(0, 1), 16 ciphertexts) at the top of the chain and at the steady input level."""
+def _layer_setup(seed: int = 20261206, chain: str = "50") -> dict:
+    """The N1 workload: the 38-limb context (``chain``: 50-bit primes, or the reference's 60/59-bit
+    ones with its refresh schedule, prefill.reference_chain_spec), every rotation key and refresh
+    program of the layer, the first-layer and steady-state PrefillLayer objects, and the encrypted
+    input (128 tokens x 4096 features N(0, 1), 16 ciphertexts) at the top of the chain and at the
+    steady input level."""
 
     from holmes_amd import fhe
     from holmes_amd import prefill as P
     from holmes_amd.layouts import FeatureMajorPrefillLayout
 
     t0 = time.perf_counter()
-    spec = P.PrefillSpec()
-    client, ctx = fhe.generate_client_context(P.prefill_context_spec(seed))
+    spec = P.PrefillSpec() if chain == "50" else P.reference_chain_spec()
+    client, ctx = fhe.generate_client_context(P.prefill_context_spec(seed, chain=chain))
     rng = np.random.default_rng(seed)
     w = P.random_weights(spec, rng)
     first, rots = P.setup_prefill_layer(client, ctx, w, spec)
@@ -1313,7 +1318,7 @@ def run_layer(args) -> int:
 
     steps = int(args.steps) if args.steps != 20 else 3
     warmup = int(args.warmup) if args.warmup != 3 else 1
-    L = _layer_setup()
+    L = _layer_setup(chain=args.chain)
     P, ctx, client, rng = L["P"], L["ctx"], L["client"], L["rng"]
     first, steady, spec, w, x = L["first"], L["steady"], L["spec"], L["w"], L["x"]
     rots, cts_steady = L["rots"], L["cts_steady"]
@@ -1355,8 +1360,13 @@ def run_layer(args) -> int:
         "config": {"workload": "N1 prefill layer, steady state, 128 tokens: input refresh, RMSNorm1 (deg-15 rsqrt), "
                                "complex QKV (2 x 4096x4096 BSGS), RoPE, causal Alg2 attention 32/8/128 (exp deg 15 "
                                "and rsqrt deg 31 on refreshed inputs), W_O, residual, refresh, SwiGLU "
-                               "4096->14336->4096 (SiLU deg 63), residual; refreshes two-pass, the inverse "
-                               "square root's input three-pass; 38 limbs, scale 2^50, dnum 5",
+                               "4096->14336->4096 (SiLU deg 63), residual; refresh passes: input "
+                               f"{spec.input_refresh_iterations}, exp input {spec.exp_refresh_iterations}, inverse "
+                               f"square root input {spec.rsqrt_refresh_iterations}, residual "
+                               f"{spec.residual_refresh_iterations}; 38 limbs of "
+                               + ("50-bit primes, scale 2^50" if args.chain == "50" else
+                                  "the reference's 60/59-bit primes, scale 2^59") + ", dnum 5",
+                   "chain": args.chain,
                    "decrypted_max_error": err, "output_magnitude": mag, "error_bits": round(-math.log2(err), 2),
                    "softmax_vs_exact": ref["softmax_vs_exact"], "in_range": ref["in_range"],
                    "rotation_keys": len(rots), "refreshed_items_per_layer": steady.ops.refreshes // (warmup + steps + 1),

@@ -392,13 +392,15 @@ def generate(context: CKKSContext, spec: BootstrapSpec) -> BootstrapProgram:
 def raise_for_output(spec: BootstrapSpec, q_primes, limbs_needed: int, *, two_pass: bool = True,
                      log_n: int = 16) -> int:
     """The fewest ModRaise limbs whose program leaves ``limbs_needed`` limbs after the refresh (one
-    fewer with the two-pass correction's final rescale); the whole chain if none leaves enough."""
+    fewer with the two-pass correction's final rescale); the whole chain if none leaves enough.
+    The level schedule is planned at the chain's own scale (the power of two nearest its primes)."""
 
     L = len(q_primes)
     need = int(limbs_needed) + (1 if two_pass else 0)
+    scale = 2.0 ** round(math.log2(float(q_primes[min(1, L - 1)])))
     for raise_to in range(2, L + 1):
         try:
-            out = plan_program(spec, q_primes, 2.0**50, raise_to, log_n).output_limbs
+            out = plan_program(spec, q_primes, scale, raise_to, log_n).output_limbs
         except ValueError:
             continue
         if out >= need:

@@ -679,7 +679,7 @@ class EncodedScalar:
         self.scaling_factor = float(scaling_factor)
 
 
-def _scaled_int(value, scaling_factor: float, integer: bool) -> int:
+def _scaled_int(value, scaling_factor: float, integer: bool, limit: int = 1 << MAX_ENCODED_BITS) -> int:
     if integer:
         if float(value) != int(value):
             raise ValueError(f"integer mode needs an integral value, got {value!r}")
@@ -689,17 +689,30 @@ def _scaled_int(value, scaling_factor: float, integer: bool) -> int:
         if not np.isfinite(x):
             raise ValueError("scalar * scale is not finite")
         m = int(np.sign(x) * np.floor(abs(x) + 0.5))  # round half away from zero, as the encoder
-    if abs(m) >= 1 << MAX_ENCODED_BITS:
-        raise ValueError(f"encoded scalar {value!r} x {scaling_factor} exceeds 2^{MAX_ENCODED_BITS}")
+    if abs(m) >= limit:
+        raise ValueError(f"encoded scalar {value!r} x {scaling_factor} exceeds the limit 2^{limit.bit_length() - 1}")
     return m
+
+
+def _scalar_limit(primes) -> int:
+    """A scalar is one integer reduced exactly modulo each prime, so it is not bound by the
+    polynomial encoder's 2^61: it may reach a quarter of the level's modulus (its residues then
+    name it with a factor-2 margin), and 2^61 at any level.  The reference chain's 59-bit scales
+    need this for the Chebyshev evaluator's coefficients (|c| * 2^59 above 2^61)."""
+
+    Q = 1
+    for q in primes:
+        Q *= int(q)
+    return max(1 << MAX_ENCODED_BITS, Q >> 2)
 
 
 def _scalar_residues(values, cur_limbs: int, scaling_factor: float, integer: bool, ctx: CKKSContext) -> np.ndarray:
     vals = np.atleast_1d(np.asarray(values, dtype=np.float64 if not integer else object))
     primes = ctx.q_primes[: int(cur_limbs)]
+    limit = _scalar_limit(primes)
     out = np.empty(vals.shape + (len(primes),), dtype=np.uint64)
     for pos in np.ndindex(vals.shape):
-        m = _scaled_int(vals[pos], scaling_factor, integer)
+        m = _scaled_int(vals[pos], scaling_factor, integer, limit)
         out[pos] = [m % q for q in primes]
     return out
 

@@ -53,6 +53,7 @@ import numpy as np
 from .decode import DecodeWeights, SlotConst, _cheb, random_weights, rope_phase
 
 __all__ = ["PrefillSpec", "PrefillPolynomials", "PrefillAttention", "PrefillLayer", "prefill_layer_numpy",
+           "reference_chain_spec",
            "attention_numpy", "qk_matrix", "v_matrix", "wo_matrix", "random_weights", "attention_rotations",
            "prefill_key_rotations", "prefill_context_spec", "prefill_mlp_spec", "prefill_bootstrap_spec",
            "setup_prefill_layer"]
@@ -95,6 +96,8 @@ class PrefillSpec:
     # 2^-25 to below 2^-27
     exp_refresh_iterations: int = 2
     rsqrt_refresh_iterations: int = 3
+    input_refresh_iterations: int = 2
+    residual_refresh_iterations: int = 2
 
     def validate(self) -> None:
         if (self.hidden_dim, self.query_heads, self.kv_heads, self.head_dim, self.seq_len) != (4096, 32, 8, 128, 128):
@@ -116,14 +119,32 @@ class PrefillPolynomials:
                    rsqrt=chebyshev_coefficients(lambda r: 1.0 / np.sqrt(r), spec.rsqrt_degree, spec.rsqrt_interval))
 
 
-def prefill_context_spec(seed: int = 20261206):
+def prefill_context_spec(seed: int = 20261206, chain: str = "50"):
     """Depth 37 (38 Q limbs), dnum 5 (8-limb digits), 8 special primes: the reference's production
-    structure (assets/feature_major.json) on 50-bit primes, scale 2^50."""
+    structure (assets/feature_major.json).  ``chain="50"``: on 50-bit primes, scale 2^50 (the FP64
+    kernels); ``chain="reference"``: the reference's own primes, a 60-bit first modulus and 59-bit Q
+    primes (dcrtBits 59, firstMod 60), scale 2^59 (the 64-bit integer kernels)."""
 
     from .fhe import CKKSContextSpec
 
+    if chain == "reference":
+        return CKKSContextSpec(depth=37, dnum=5, dcrt_bits=59, first_mod=60, scale_bits=59,
+                               secret_key_dist="SPARSE_TERNARY", hamming_weight=192, seed=seed)
+    if chain != "50":
+        raise ValueError(f"chain must be '50' or 'reference', got {chain!r}")
     return CKKSContextSpec(depth=37, dnum=5, dcrt_bits=50, first_mod=50, scale_bits=50,
                            secret_key_dist="SPARSE_TERNARY", hamming_weight=192, seed=seed)
+
+
+def reference_chain_spec() -> PrefillSpec:
+    """The layer's refresh schedule on the reference's 60/59-bit chain, whose one-pass bootstrap
+    reaches 2^-22 (2^-13 on 50-bit primes): the exp series' input refreshed in one pass, as the
+    reference refreshes its softmax checkpoint (llama3fhe/schedule.py:38-43,
+    softmax_main_bootstrap_iterations = 1); the inverse square root's input in two (one pass there
+    would reach the probabilities multiplied some 64-fold); the layer input and the residual in two
+    (measured: one pass at both gives 2^-15.1 against the 2^-16 bar, two give 2^-17.7)."""
+
+    return PrefillSpec(exp_refresh_iterations=1, rsqrt_refresh_iterations=2)
 
 
 def prefill_mlp_spec(spec: PrefillSpec):
@@ -794,7 +815,8 @@ class PrefillLayer:
         if self.steady:
             xb = tap("input_in", ops.batch(x_cts))
             x_cts = tuple(ops.items(tap("input", ops.refresh(xb, bound_bits=self.spec.input_bound_bits,
-                                                             program=self.programs.get("input")))))
+                                                             program=self.programs.get("input"),
+                                                             iterations=self.spec.input_refresh_iterations))))
             mark("refresh_input")
         xn = rmsnorm_fhe(x_cts, None, coeffs=self.rms, layout=self.layout, crypto_context=ctx).outputs
         mark("rmsnorm1")
@@ -818,7 +840,8 @@ class PrefillLayer:
         self.levels["residual"] = ops.limbs(h)
         tap("residual_in", h)
         h = tap("residual", ops.refresh(h, bound_bits=self.spec.residual_bound_bits,
-                                        program=self.programs.get("residual")))
+                                        program=self.programs.get("residual"),
+                                        iterations=self.spec.residual_refresh_iterations))
         mark("refresh")
         m_out, _ = self.mlp.forward(ops.items(h))
         m = tap("mlp", ops.batch(m_out))

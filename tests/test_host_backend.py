@@ -155,6 +155,11 @@ def test_scalar_encoding_residues_and_rounding():
         fhe._scaled_int(2.5, 1.0, True)  # integer mode needs an integral value
     with pytest.raises(ValueError):
         fhe._scaled_int(1.0, 2.0**61, False)  # beyond the 2^61 encoding cap
+    # a scalar (one exactly reduced integer) may exceed 2^61 up to a quarter of the level's modulus
+    big = fhe._scalar_residues(4.0, 2, 2.0**60, False, ctx)
+    assert [int(v) for v in big[0]] == [2**62 % q for q in primes[:2]]
+    with pytest.raises(ValueError):
+        fhe._scalar_residues(1.0, 1, 2.0**62, False, ctx)  # one limb: 2^61 stays the limit
     tab = fhe._scalar_residues(np.array([1.0, -1.0]), 3, 4.0, False, ctx)
     assert tab.shape == (2, 3) and int(tab[1, 0]) == primes[0] - 4
 
