@@ -936,9 +936,9 @@ def run_wire(args) -> int:
 
 def run_c4(args) -> int:
     """C4: one encrypted MLP block (holmes_amd.mlp.FeatureMajorMLPBlock) on 128 tokens x 4096
-    features (16 ciphertexts); weights N(0, 0.02^2) (a randomized Hadamard rotation of i.i.d.
-    Gaussian weights is again i.i.d. Gaussian with the same deviation, so the rotation is not
-    drawn), gamma = 1 + N(0, 0.1^2), x ~ N(0, 1)."""
+    features (16 ciphertexts); weights N(0, 0.02^2) rotated as a converted checkpoint's are (gate /
+    up by a seeded randomized Hadamard on the 4096 axis, down by H_28 (x) H_512 on the 14336 axis,
+    holmes_amd.hadamard.rotate_mlp_weights), gamma = 1 + N(0, 0.1^2), x ~ N(0, 1)."""
 
     import math
 
@@ -946,6 +946,7 @@ def run_c4(args) -> int:
 
     from holmes_amd import bootstrap as bs
     from holmes_amd import fhe, mlp
+    from holmes_amd.hadamard import rotate_mlp_weights
     from holmes_amd.layouts import FeatureMajorPrefillLayout
     from holmes_amd.linear import LinearOperatorConfig
 
@@ -965,9 +966,8 @@ def run_c4(args) -> int:
     prog = bs.generate(ctx, bspec)
     rng = np.random.default_rng(seed)
     D, Iw = mspec.hidden_dim, mspec.intermediate_width
-    gate = rng.normal(scale=0.02, size=(Iw, D))
-    up = rng.normal(scale=0.02, size=(Iw, D))
-    down = rng.normal(scale=0.02, size=(D, Iw))
+    gate, up, down = rotate_mlp_weights(rng.normal(scale=0.02, size=(Iw, D)), rng.normal(scale=0.02, size=(Iw, D)),
+                                        rng.normal(scale=0.02, size=(D, Iw)), seed + 1)
     gamma = 1.0 + 0.1 * rng.normal(size=D)
     block = mlp.FeatureMajorMLPBlock(ctx, gate, up, down, norm_weight=gamma, spec=mspec, layout=layout, config=cfg,
                                      bootstrap_program=prog)

@@ -7,8 +7,9 @@
   tests/test_linear.py:280-340, at the configured shape), and the first chunk's unrescaled residues
   of input 0 equal the oracle composition of the same schedule (15 baby rotations, 512 encoded
   diagonals, the multiply-accumulate, 31 Horner giant rotations) bit for bit.
-* C4: the MLP block at intermediate width 14336 (four feature pages), one two-pass bootstrap:
-  decrypted within 2^-16 of the float64 model of the same polynomials.
+* C4: the MLP block at intermediate width 14336 (four feature pages), one two-pass bootstrap, weights
+  rotated as a converted checkpoint's (gate / up by a randomized Hadamard on 4096, down by
+  H_28 (x) H_512 on 14336): decrypted within 2^-16 of the float64 model of the same polynomials.
 * C5: the decode step at intermediate width 14336 against a 256-token encrypted KV cache: decrypted
   within 2^-16 of the output's magnitude.
 """
@@ -107,6 +108,7 @@ def test_c3_first_chunk_residues_match_oracle(c3):
 def c4():
     from holmes_amd import bootstrap as bs
     from holmes_amd import fhe, mlp
+    from holmes_amd.hadamard import rotate_mlp_weights
     from holmes_amd.layouts import FeatureMajorPrefillLayout
 
     spec = fhe.CKKSContextSpec(depth=23, dnum=3, dcrt_bits=50, first_mod=50, scale_bits=50,
@@ -122,9 +124,8 @@ def c4():
     prog = bs.generate(ctx, bspec)
     rng = np.random.default_rng(20261204)
     D, Iw = 4096, 14336
-    gate = rng.normal(scale=0.02, size=(Iw, D))
-    up = rng.normal(scale=0.02, size=(Iw, D))
-    down = rng.normal(scale=0.02, size=(D, Iw))
+    gate, up, down = rotate_mlp_weights(rng.normal(scale=0.02, size=(Iw, D)), rng.normal(scale=0.02, size=(Iw, D)),
+                                        rng.normal(scale=0.02, size=(D, Iw)), 20261205)
     gamma = 1.0 + 0.1 * rng.normal(size=D)
     block = mlp.FeatureMajorMLPBlock(ctx, gate, up, down, norm_weight=gamma, spec=mspec, layout=layout, config=cfg,
                                      bootstrap_program=prog)
