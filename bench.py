@@ -89,12 +89,6 @@ def main() -> int:
                     help="c2: skip the steady prefill layer measured beside the key switch (the metric's first half)")
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
-    ap.add_argument("--ks-slices", type=int, default=0,
-                    help="c2 key-switch schedule: 0 sequential kernels, >= 2 pipelined slices of the batch")
-    ap.add_argument("--ks-streams", type=int, default=0,
-                    help="c2 multi-stream schedule: slices of --ks-slice-items items on this many library "
-                         "streams (0 or 1: one stream)")
-    ap.add_argument("--ks-slice-items", type=int, default=0, help="items per slice of the multi-stream schedule")
     ap.add_argument("--conv-engine", choices=("mfma", "valu"), default="mfma",
                     help="c2 ModUp / ModDown conversion sums: int8 matrix cores or FP64 VALU (same results)")
     ap.add_argument("--chain", choices=("50", "reference"), default="50",
@@ -161,8 +155,6 @@ def main() -> int:
     spec = fhe.CKKSContextSpec(depth=LIMBS - 1, dnum=3, dcrt_bits=50, first_mod=50, seed=args.seed)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
-    ctx.set_keyswitch_slices(args.ks_slices)
-    ctx.set_keyswitch_streams(args.ks_streams, args.ks_slice_items)
     ctx.set_conversion_engine(args.conv_engine)
     keys = []
     for r in range(1, CTS + 1):
@@ -256,8 +248,6 @@ def main() -> int:
             "batch": CTS,
             "algorithmic_bytes_per_step": step_bytes,
             "cts_per_launch": chunk,
-            "ks_slices": args.ks_slices,
-            "ks_streams": [args.ks_streams, args.ks_slice_items],
             "conv_engine": args.conv_engine,
             "traffic_record": None if traffic is None else {k: traffic_rec[k] for k in ("fetch_kib", "write_kib",
                                                                                        "fetch_scale", "measured")},

@@ -42,8 +42,6 @@ SIGNATURES = {
     "hck_context_twiddles": (_i, [_vp, _i, _i, _u64p]),
     "hck_context_root_tables": (_i, [_vp, _vp, _vp]),
     "hck_error_string": (ctypes.c_char_p, [_i]),
-    "hck_context_set_ks_slices": (_i, [_vp, _i]),
-    "hck_context_set_ks_streams": (_i, [_vp, _i, _i]),
     "hck_context_set_conv_engine": (_i, [_vp, _i]),
     "hck_ntt_forward": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _i, _ip, _vp]),
     "hck_ntt_inverse": (_i, [_vp, _vp, _vp, _i, _i64, _i64, _i, _ip, _vp]),

@@ -289,21 +289,6 @@ class CKKSContext:
     def handle(self):
         return self._h
 
-    def set_keyswitch_slices(self, slices: int) -> None:
-        """Key-switch schedule for batched calls: 0 runs the five kernels in turn over the whole
-        batch (default); s >= 2 pipelines s slices (hck_context_set_ks_slices).  Same results."""
-
-        nat.check(nat.lib().hck_context_set_ks_slices(self._h, int(slices)), "hck_context_set_ks_slices")
-
-    def set_keyswitch_streams(self, streams: int, slice_items: int) -> None:
-        """Multi-stream key-switch schedule: batches of more than ``slice_items`` items run in slices
-        of that many, slice t on library stream t % ``streams`` (2 to 4), forked from and joined back
-        into the current stream (hck_context_set_ks_streams).  ``streams`` < 2 restores one stream.
-        Same results."""
-
-        nat.check(nat.lib().hck_context_set_ks_streams(self._h, int(streams), int(slice_items)),
-                  "hck_context_set_ks_streams")
-
     def set_conversion_engine(self, engine: str) -> None:
         """Engine of the key switch's ModUp / ModDown conversion sums: "mfma" (default, int8 matrix
         cores on balanced base-256 digits) or "valu" (FP64 multiply-accumulates).  Same results."""

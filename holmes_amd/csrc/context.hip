@@ -380,21 +380,8 @@ extern "C" int hck_context_create(hck_context** out, int log_n, int num_q, int n
   return HCK_OK;
 }
 
-static void ks_streams_release(hck_context* ctx) {
-  for (int i = 0; i < hck_context::kMaxKsStreams; ++i) {
-    if (ctx->ks_stream[i]) (void)hipStreamDestroy(ctx->ks_stream[i]);
-    if (ctx->ks_join[i]) (void)hipEventDestroy(ctx->ks_join[i]);
-    ctx->ks_stream[i] = nullptr;
-    ctx->ks_join[i] = nullptr;
-  }
-  if (ctx->ks_fork) (void)hipEventDestroy(ctx->ks_fork);
-  ctx->ks_fork = nullptr;
-  ctx->ks_streams = ctx->ks_slice_items = 0;
-}
-
 extern "C" void hck_context_destroy(hck_context* ctx) {
   if (!ctx) return;
-  ks_streams_release(ctx);
   hck::wide_free(ctx);
   if (ctx->d_block) (void)hipFree(ctx->d_block);
   delete ctx;
@@ -433,33 +420,6 @@ extern "C" int hck_context_info(const hck_context* ctx, int* log_n, int* num_q, 
   if (num_q) *num_q = ctx->L;
   if (num_p) *num_p = ctx->K;
   if (alpha) *alpha = ctx->alpha;
-  return HCK_OK;
-}
-
-extern "C" int hck_context_set_ks_slices(hck_context* ctx, int slices) {
-  if (!ctx || slices < 0 || slices > 64) return HCK_ERR_ARG;
-  ctx->ks_slices = slices;
-  return HCK_OK;
-}
-
-extern "C" int hck_context_set_ks_streams(hck_context* ctx, int streams, int slice_items) {
-  if (!ctx || streams < 0 || streams > hck_context::kMaxKsStreams || slice_items < 0 || slice_items > 64)
-    return HCK_ERR_ARG;
-  ks_streams_release(ctx);
-  if (streams < 2 || slice_items < 1) return HCK_OK;
-  // Every stream at the default priority; non-blocking so the legacy null stream does not serialise
-  // them.  Events carry no timing (fork / join only).
-  hipError_t e = hipEventCreateWithFlags(&ctx->ks_fork, hipEventDisableTiming);
-  for (int i = 0; e == hipSuccess && i < streams; ++i) {
-    e = hipStreamCreateWithFlags(&ctx->ks_stream[i], hipStreamNonBlocking);
-    if (e == hipSuccess) e = hipEventCreateWithFlags(&ctx->ks_join[i], hipEventDisableTiming);
-  }
-  if (e != hipSuccess) {
-    ks_streams_release(ctx);
-    return (int)e;
-  }
-  ctx->ks_streams = streams;
-  ctx->ks_slice_items = slice_items;
   return HCK_OK;
 }
 

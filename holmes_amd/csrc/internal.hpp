@@ -62,15 +62,7 @@ struct DevTables {
 
 struct hck_context {
   int log_n, L, K, alpha, np;
-  int ks_slices = 0;  // key-switch schedule: 0 / 1 sequential kernels, >= 2 pipelined slices (ksfused.hip)
   int conv_engine = 1;  // ModUp / ModDown conversion sums: 1 int8 matrix cores, 0 FP64 VALU (same results)
-  // Multi-stream key-switch schedule (ksfused.hip): batches of more than ks_slice_items items are cut
-  // into slices of that many, slice t runs its five kernels on ks_stream[t % ks_streams] (library
-  // streams at the default priority), forked from and joined back into the caller's stream.
-  static constexpr int kMaxKsStreams = 4;
-  int ks_streams = 0, ks_slice_items = 0;
-  hipStream_t ks_stream[kMaxKsStreams] = {};
-  hipEvent_t ks_fork = nullptr, ks_join[kMaxKsStreams] = {};
   hck::WideState* wide = nullptr;  // set for a context with a prime >= 2^50: every kernel runs on wide.hip
   std::vector<uint64_t> primes;
   hck::DevTables dev;

@@ -1449,149 +1449,6 @@ __global__ __launch_bounds__(kT) void k_ks_rows_store(const double* __restrict__
   for (int k = 0; k < 16; ++k) o[16 * k] = d2u(canon(x[k], p, pinv));
 }
 
-// ----------------------------------------------------------------- pipelined schedule
-// The five kernels above alternate between VALU-bound (K2, K4) and HBM-bound (K1, K3, K5) work, and
-// every phase of a ciphertext needs the whole previous phase of that ciphertext (a transpose through
-// the workspace).  The pipelined schedule cuts the batch into slices and runs, in launch t, phase k
-// of slice t - k for every k at once: the launch's workgroups interleave the phases (rounds of
-// per-phase groups), so the conversion kernels of one slice execute beside the inner products of
-// another on the same CUs.  Stream order between launches carries every dependency (phase k of a
-// slice ran in the previous launch); within a launch the phases touch disjoint slices.
-constexpr int kWaveLds = kRowLds + kTwLds;  // the largest phase (K3 / K5: S + TW)
-static_assert(16 * kYStride + kSrcMax * kTgtFused * 2 <= kWaveLds, "conversion phase LDS");
-
-struct WavePhase {
-  int blocks;  // workgroups of this phase in the launch (0: phase idle)
-  int group;   // workgroups per round (multiple of 8: keeps the XCD decode of the tile phases)
-  int b0;      // first item of the slice (index into keys / galois)
-  int batch;   // items of the slice
-  const uint64_t* d;
-  const uint64_t* add;
-  const uint64_t* acc_b;
-  const uint64_t* acc_a;
-  uint64_t* out_b;
-  uint64_t* out_a;
-  double* r1;
-  double* t2;
-  double* accp;
-};
-
-struct WaveArgs {
-  WavePhase ph[5];
-  int round;  // sum of the groups
-  int ell, beta;
-  long long d_stride, add_stride, acc_stride, out_stride;
-  const ConvConsts* modup;
-  const ConvConsts* moddown;
-  const LevelConsts* lc;
-  KeyPtrsF keys;
-  GalF G;
-};
-
-__global__ __launch_bounds__(kT, 2) void k_ks_wave(const WaveArgs A, DevTables T) {
-  __shared__ double smem[kWaveLds];
-  const int R = A.round, g = blockIdx.x / R;
-  int r = blockIdx.x - g * R, k = 0;
-  while (k < 4 && r >= A.ph[k].group) {
-    r -= A.ph[k].group;
-    ++k;
-  }
-  const WavePhase& P = A.ph[k];
-  const int local = g * P.group + r;
-  if (r >= P.group || local >= P.blocks) return;
-  const int ell = A.ell, beta = A.beta, K = T.K, ext_l = ell + K;
-  const long long n = kN;
-  switch (k) {
-    case 0:
-      intt_rows_body(P.d, A.d_stride, A.G, 0, 0, P.r1, ell, P.batch, T, local, smem, P.b0);
-      break;
-    case 1: {
-      const ConvArgs C{P.r1, (long long)ell * n, 0, T.alpha, P.t2, (long long)beta * ext_l * n, (long long)ext_l * n,
-                       A.modup, 1};
-      cols_conv_body<false>(C, local % 128, (local / 128) % beta, local / (128 * beta), smem, nullptr,
-                            (TwPair*)(smem + 16 * kYStride), T);
-      break;
-    }
-    case 2:
-      rows_ip_body(P.d, A.d_stride, A.G, P.t2, A.keys, ell, beta, P.batch, 16 * K, ell, P.accp, nullptr, 0, nullptr,
-                   nullptr, 0, nullptr, nullptr, 0, T, local, smem, smem + kRowLds, P.b0);
-      break;
-    case 3: {
-      const ConvArgs C{P.accp, 2LL * K * n, (long long)K * n, 0, P.r1, 2LL * ell * n, (long long)ell * n, A.moddown, 0};
-      cols_conv_body<false>(C, local % 128, (local / 128) % 2, local / 256, smem, nullptr,
-                            (TwPair*)(smem + 16 * kYStride), T);
-      break;
-    }
-    default:
-      rows_ipq_body(P.d, A.d_stride, A.G, P.t2, A.keys, ell, beta, P.batch, P.r1, P.add, A.add_stride, P.acc_b,
-                    P.acc_a, A.acc_stride, P.out_b, P.out_a, A.out_stride, A.lc, T, local, smem, smem + kRowLds,
-                    P.b0);
-      break;
-  }
-}
-
-constexpr int kWaveRounds = 32;
-
-}  // namespace
-
-namespace {
-
-// The pipelined schedule of ks_fused (see k_ks_wave); same arguments, workspace and results.
-int ks_wave(const hck_context* c, int ell, int batch, int slices, const uint64_t* d, long long d_stride, const GalF& G,
-            const KeyPtrsF& kp, const uint64_t* add, long long add_stride, const uint64_t* acc_b, const uint64_t* acc_a,
-            long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride, double* r1, double* t2,
-            double* accp, hipStream_t s) {
-  const int K = c->K, beta = beta_of(c, ell), ext_l = ell + K;
-  const long long n = kN;
-  const int per = (batch + slices - 1) / slices;
-  const int ns = (batch + per - 1) / per;
-  WaveArgs A{};
-  A.ell = ell;
-  A.beta = beta;
-  A.d_stride = d_stride;
-  A.add_stride = add_stride;
-  A.acc_stride = acc_stride;
-  A.out_stride = out_stride;
-  A.modup = modup_consts(c, ell, 0);
-  A.moddown = c->d_moddown + ell;
-  A.lc = c->d_level + ell;
-  A.keys = kp;
-  A.G = G;
-  auto tiles8 = [](int tiles) { return (tiles + kXcds - 1) / kXcds * kXcds; };
-  for (int t = 0; t < ns + 4; ++t) {
-    int round = 0, rounds = 0;
-    for (int k = 0; k < 5; ++k) {
-      WavePhase& P = A.ph[k];
-      P = WavePhase{};
-      const int sl = t - k;
-      if (sl < 0 || sl >= ns) continue;
-      const int b0 = sl * per, nb = batch - b0 < per ? batch - b0 : per;
-      P.b0 = b0;
-      P.batch = nb;
-      P.d = d + (long long)b0 * d_stride;
-      P.add = add ? add + (long long)b0 * add_stride : nullptr;
-      P.acc_b = acc_b ? acc_b + (long long)b0 * acc_stride : nullptr;
-      P.acc_a = acc_a ? acc_a + (long long)b0 * acc_stride : nullptr;
-      P.out_b = out_b + (long long)b0 * out_stride;
-      P.out_a = out_a + (long long)b0 * out_stride;
-      P.r1 = r1 + (long long)b0 * 2 * ell * n;
-      P.t2 = t2 + (long long)b0 * beta * ext_l * n;
-      P.accp = accp + (long long)b0 * 2 * K * n;
-      const int blocks[5] = {tiles8(16 * ell) * nb, 128 * beta * nb, tiles8(16 * K) * nb, 256 * nb,
-                             tiles8(16 * ell) * nb};
-      P.blocks = blocks[k];
-      P.group = tiles8((P.blocks + kWaveRounds - 1) / kWaveRounds);
-      const int need = (P.blocks + P.group - 1) / P.group;
-      rounds = rounds > need ? rounds : need;
-      round += P.group;
-    }
-    A.round = round;
-    k_ks_wave<<<dim3((unsigned)(rounds * round)), kT, 0, s>>>(A, c->dev);
-    HCK_CHECK_LAUNCH();
-  }
-  return HCK_OK;
-}
-
 }  // namespace
 
 // Workspace (doubles, per ciphertext): R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)], ACCP [2 K].
@@ -1601,60 +1458,11 @@ size_t ks_fused_bytes(const hck_context* c, int ell, int batch) {
   return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * c->K);
 }
 
-namespace {
-
-int ks_fused_one(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
-                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
-                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
-                 long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
-                 long long ext_stride, const uint32_t* galois_items);
-
-}  // namespace
-
-// The multi-stream schedule (hck_context_set_ks_streams): slice t of ks_slice_items items runs the
-// whole key switch on ks_stream[t % ks_streams] over its own part of the workspace (the workspace is
-// linear in the item count, so slice t starts at ks_fused_bytes(b0) bytes).  The library streams
-// wait for everything queued on s so far, and s waits for every slice before anything after the call.
 int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
              const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
              const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
              char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
              const uint32_t* galois_items) {
-  const int m = c->ks_slice_items, ns = c->ks_streams;
-  if (c->wide || ns < 2 || m < 1 || batch <= m)
-    return ks_fused_one(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b,
-                        out_a, out_stride, ws, s, ext_b, ext_a, ext_stride, galois_items);
-  const int slices = (batch + m - 1) / m, used = slices < ns ? slices : ns;
-  hipError_t e = hipEventRecord(c->ks_fork, s);
-  for (int i = 0; e == hipSuccess && i < used; ++i) e = hipStreamWaitEvent(c->ks_stream[i], c->ks_fork, 0);
-  if (e != hipSuccess) return (int)e;
-  int rc = HCK_OK;
-  for (int t = 0; t < slices && rc == HCK_OK; ++t) {
-    const int b0 = t * m, nb = batch - b0 < m ? batch - b0 : m;
-    const auto at = [b0](long long stride) { return (long long)b0 * stride; };
-    rc = ks_fused_one(c, ell, nb, d + at(d_stride), d_stride, galois, ksk + b0, add ? add + at(add_stride) : nullptr,
-                      add_stride, acc_b ? acc_b + at(acc_stride) : nullptr, acc_a ? acc_a + at(acc_stride) : nullptr,
-                      acc_stride, out_b ? out_b + at(out_stride) : nullptr, out_a ? out_a + at(out_stride) : nullptr,
-                      out_stride, ws + ks_fused_bytes(c, ell, b0), c->ks_stream[t % ns],
-                      ext_b ? ext_b + at(ext_stride) : nullptr, ext_a ? ext_a + at(ext_stride) : nullptr, ext_stride,
-                      galois_items ? galois_items + b0 : nullptr);
-  }
-  // join every stream that received work, also after a failed launch (s must not run ahead of it)
-  for (int i = 0; i < used; ++i) {
-    hipError_t ej = hipEventRecord(c->ks_join[i], c->ks_stream[i]);
-    if (ej == hipSuccess) ej = hipStreamWaitEvent(s, c->ks_join[i], 0);
-    if (ej != hipSuccess && rc == HCK_OK) rc = (int)ej;
-  }
-  return rc;
-}
-
-namespace {
-
-int ks_fused_one(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
-                 const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
-                 const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
-                 long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
-                 long long ext_stride, const uint32_t* galois_items) {
   if (c->wide)
     return wide_ks(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
                    out_stride, ws, s, ext_b, ext_a, ext_stride, galois_items);
@@ -1674,12 +1482,6 @@ int ks_fused_one(const hck_context* c, int ell, int batch, const uint64_t* d, lo
   const int last_digit = ell - c->alpha * (beta - 1);
   KeyPtrsF kp{};
   for (int b = 0; b < batch; ++b) kp.k[b] = ksk[b];
-  const int slices = c->ks_slices;
-  const bool seq_conv = ext_l - last_digit <= kTgtFused && ell <= kTgtFused;  // both conversions unsplit
-  if (!ext_b && slices > 1 && batch >= 2 * slices && seq_conv) {
-    return ks_wave(c, ell, batch, slices, d, d_stride, G, kp, add, add_stride, acc_b, acc_a, acc_stride, out_b, out_a,
-                   out_stride, r1, t2, accp, s);
-  }
   // K1
   k_ks_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0,
                                                                                     r1, ell, batch, c->dev);
@@ -1724,8 +1526,6 @@ int ks_fused_one(const hck_context* c, int ell, int batch, const uint64_t* d, lo
   }
   return HCK_OK;
 }
-
-}  // namespace
 
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch) {
   const size_t beta = beta_of(c, ell), ext_l = ell + c->K;

@@ -79,23 +79,6 @@ int hck_context_twiddles(const hck_context* ctx, int prime_idx, int inverse, uin
  * (bench/cmp/holmes_fast_stage2.py:74-82).  Synchronous (set-up, not the hot path). */
 int hck_context_root_tables(const hck_context* ctx, uint64_t* roots, uint64_t* roots_shoup);
 const char* hck_error_string(int code);
-/* Key-switch schedule of batched calls: 0 or 1 (default) runs the five key-switch kernels one after
- * another over the whole batch; s >= 2 cuts batches of at least 2 s items into s slices and runs
- * phase k of slice t - k in launch t (every phase of the pipeline in one launch).  Results are
- * identical; only the timing differs.  No counterpart in the reference (a scheduling knob). */
-int hck_context_set_ks_slices(hck_context* ctx, int slices);
-
-/* Multi-stream key-switch schedule: with streams >= 2 and slice_items >= 1, a batched key switch of
- * more than slice_items items runs in slices of slice_items items, slice t on library stream
- * t % streams (at most 4, default priority), forked from the caller's stream by an event and joined
- * back into it before the call returns; each slice uses its own part of the caller's workspace.  A
- * slice's intermediates are then read back while they are still in the last-level cache, and the
- * conversion kernels of one slice can share the CUs with the inner-product kernels of another.
- * streams < 2 or slice_items = 0 restores one stream (default).  Results are identical; only the
- * timing differs.  Not for concurrent use of one context from several host threads.  No counterpart
- * in the reference (a scheduling knob). */
-int hck_context_set_ks_streams(hck_context* ctx, int streams, int slice_items);
-
 /* Engine of the ModUp / ModDown base-conversion sums inside every key switch: 1 (default) the int8
  * matrix cores (each residue split into balanced base-256 digits, exact int32 sums), 0 FP64 VALU
  * multiply-accumulates.  Results are identical; only the timing differs.  No counterpart in the

@@ -438,24 +438,3 @@ def check_mul_relin_rescale_postop(env, levels, batch=3):
             got = ctx.mul_relin_rescale_postop_raw(a0, a1, b0, b1, ell, ctx.relin_key, apply_double=twice,
                                                    sub=(s0, s1) if sub else None, scalar=sc if scalar else None)
             assert torch.equal(got, want), (ell, twice, sub, scalar)
-
-
-def test_products_under_multistream_schedule(env):
-    """Products with relinearisation (hck_mul_relin, and the FP64-engine hck_mul_relin_rescale whose
-    relinearisation runs the plain key switch) under the multi-stream key-switch schedule (slices of
-    2 items on 2 library streams; 7 items, a ragged last slice) give the one-stream residues."""
-    _, _, ctx, _ = env
-    ell, batch = 12, 7
-    rng = np.random.default_rng(4242)
-    a0, a1, b0, b1 = (_dev(_rand(ctx, rng, batch, ell)) for _ in range(4))
-    ref = ctx.mul_relin_raw(a0, a1, b0, b1, ell, ctx.relin_key, stacked=True)
-    ctx.set_conversion_engine("valu")
-    try:
-        ref_rs = ctx.mul_relin_rescale_raw(a0, a1, b0, b1, ell, ctx.relin_key, stacked=True)
-        ctx.set_keyswitch_streams(2, 2)
-        for _ in range(2):
-            assert torch.equal(ctx.mul_relin_raw(a0, a1, b0, b1, ell, ctx.relin_key, stacked=True), ref)
-            assert torch.equal(ctx.mul_relin_rescale_raw(a0, a1, b0, b1, ell, ctx.relin_key, stacked=True), ref_rs)
-    finally:
-        ctx.set_keyswitch_streams(0, 0)
-        ctx.set_conversion_engine("mfma")

@@ -525,69 +525,6 @@ def test_every_level_keyswitch_and_rescale(env):
             assert np.array_equal(_host(ctx.modraise(_dev(y), ell))[0], orc.modraise(ell, y[0])), f"ModRaise to {ell}"
 
 
-@pytest.mark.parametrize("slices", [2, 4])
-def test_pipelined_keyswitch_schedule_matches_oracle(env, slices):
-    """The pipelined schedule (slices of the batch, all five phases in each launch) gives the
-    residues of the sequential one: 10 items (a ragged last slice), distinct keys, per-item
-    Galois elements, accumulators, and the C2 batch of 16."""
-    _, client, ctx, orc = env
-    ell = 24
-    try:
-        ctx.set_keyswitch_slices(slices)
-        for B in (10, 16):
-            rng = np.random.default_rng(70 + slices + B)
-            c0, c1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
-            acc = _rand(ctx, rng, B, ell)
-            gs = [ctx.galois_element(r) for r in range(1, B + 1)]
-            keys = [ctx.make_switching_key(*client.key_inputs(g)) for g in gs]
-            o0, o1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, gs, keys, acc=(_dev(acc), _dev(acc)))
-            o0, o1 = _host(o0), _host(o1)
-            q = np.array(ctx.primes[:ell], dtype=object).reshape(ell, 1)
-            for b in (0, B // 2, B - 1):
-                okey = orc.make_ksk(*client.key_inputs(gs[b]))
-                w0, w1 = orc.rotate(ell, gs[b], c0[b], c1[b], okey)
-                w0 = ((w0.astype(object) + acc[b].astype(object)) % q).astype(np.uint64)
-                w1 = ((w1.astype(object) + acc[b].astype(object)) % q).astype(np.uint64)
-                assert np.array_equal(o0[b], w0) and np.array_equal(o1[b], w1), (B, b)
-    finally:
-        ctx.set_keyswitch_slices(0)
-
-
-@pytest.mark.parametrize("streams,items", [(2, 1), (2, 3), (4, 2)])
-def test_multistream_keyswitch_schedule_matches_oracle(env, streams, items):
-    """The multi-stream schedule (slices of `items` items on `streams` library streams, forked from
-    and joined into the current stream) gives the residues of the one-stream schedule: 10 items (a
-    ragged last slice when items = 3), distinct keys, per-item Galois elements, accumulators, the
-    extended-basis output, and oracle spot checks."""
-    _, client, ctx, orc = env
-    ell, B = 24, 10
-    rng = np.random.default_rng(90 + 10 * streams + items)
-    c0, c1 = _rand(ctx, rng, B, ell), _rand(ctx, rng, B, ell)
-    acc = _rand(ctx, rng, B, ell)
-    gs = [ctx.galois_element(r) for r in range(1, B + 1)]
-    keys = [ctx.make_switching_key(*client.key_inputs(g)) for g in gs]
-    ref0, ref1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, gs, keys, acc=(_dev(acc), _dev(acc)))
-    ref0, ref1 = _host(ref0), _host(ref1)
-    x0, x1 = ctx.rotate_ext(_dev(c0), _dev(c1), ell, gs, keys)
-    x0, x1 = _host(x0), _host(x1)
-    try:
-        ctx.set_keyswitch_streams(streams, items)
-        for rep in range(2):
-            o0, o1 = ctx.rotate_raw(_dev(c0), _dev(c1), ell, gs, keys, acc=(_dev(acc), _dev(acc)))
-            e0, e1 = ctx.rotate_ext(_dev(c0), _dev(c1), ell, gs, keys)
-            assert np.array_equal(_host(o0), ref0) and np.array_equal(_host(o1), ref1), rep
-            assert np.array_equal(_host(e0), x0) and np.array_equal(_host(e1), x1), rep
-    finally:
-        ctx.set_keyswitch_streams(0, 0)
-    q = np.array(ctx.primes[:ell], dtype=object).reshape(ell, 1)
-    for b in (0, B - 1):
-        okey = orc.make_ksk(*client.key_inputs(gs[b]))
-        w0, w1 = orc.rotate(ell, gs[b], c0[b], c1[b], okey)
-        w0 = ((w0.astype(object) + acc[b].astype(object)) % q).astype(np.uint64)
-        w1 = ((w1.astype(object) + acc[b].astype(object)) % q).astype(np.uint64)
-        assert np.array_equal(ref0[b], w0) and np.array_equal(ref1[b], w1), b
-
-
 @pytest.mark.parametrize("ell,outputs,group", [(20, 5, 3), (9, 16, 4), (24, 1, 2)])
 def test_grouped_ext_rotations_equal_sequential(env, ell, outputs, group):
     """hck_rotate_ext_sum (a group of giant steps summed on chip, one accumulator pass) against
