@@ -90,7 +90,7 @@ def main() -> int:
     ap.add_argument("--seed", type=int, default=20261202)
     ap.add_argument("--chunk", type=int, default=CTS, help="ciphertexts per key-switch launch sequence")
     ap.add_argument("--conv-engine", choices=("mfma", "valu"), default="mfma",
-                    help="c2 ModUp / ModDown conversion sums: int8 matrix cores or FP64 VALU (same results)")
+                    help="c2 / c2wide ModUp / ModDown conversion sums: int8 matrix cores or the VALU (same results)")
     ap.add_argument("--chain", choices=("50", "reference"), default="50",
                     help="layer: the 38-limb chain on 50-bit primes (FP64 kernels) or the reference's own "
                          "60/59-bit primes (assets/feature_major.json; 64-bit integer kernels)")
@@ -288,6 +288,7 @@ def run_c2wide(args) -> int:
     spec = fhe.CKKSContextSpec(depth=ell - 1, dnum=5, dcrt_bits=59, first_mod=60, scale_bits=59, seed=args.seed)
     t0 = time.perf_counter()
     client, ctx = fhe.generate_client_context(spec)
+    ctx.set_conversion_engine(args.conv_engine)
     keys = []
     for r in range(1, CTS + 1):
         g = ctx.galois_element(r)

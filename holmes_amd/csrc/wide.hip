@@ -314,6 +314,98 @@ __global__ __launch_bounds__(256) void wk_conv(const u64* __restrict__ src, long
   }
 }
 
+// The same conversion on the int8 matrix cores.  Each source residue is centered (ybar_s, |ybar_s| <
+// b_s / 2 < 2^60) and written as the 64-bit word of its eight balanced base-256 digits d_{s,a}
+// (byte a = d_{s,a} + 128 of ybar_s + 0x80..80; the XOR turns each byte into d_{s,a} as int8).  With
+// the digits e_{s,a,t,c} of K_{s,a,t} = (B / b_s) 256^a mod t (fill_wide_digits), one
+// v_mfma_i32_16x16x64_i8 per output digit c gives C_c = sum_{s,a} d_{s,a} e_{s,a,t,c} for 16 targets x 16
+// coefficients (K = 8 sources x 8 digit bytes; |C_c| <= 64 * 128^2 = 2^20), and
+//   sum_c 256^c C_c = sum_{s,a} d_{s,a} K_{s,a,t} == sum_s ybar_s (B / b_s)  (mod t),
+// the conversion's sum.  The fold pairs the byte positions, estimates the quotient by t in FP64
+// (fold_inv = fl(1 / t)) and takes the remainder exactly in wrapping 64-bit arithmetic, then one
+// correction into [0, t): the residue wk_conv returns.  Operand layout (measured): lane l supplies A row l % 16 and B column l % 16 with K bytes
+// 16 (l / 16) .. +15 and receives D rows 4 (l / 16) + r, column l % 16 in register r.  Lane (q, j)
+// therefore feeds sources 2q and 2q + 1 of coefficient j of its wave's tile of 16 coefficients and
+// folds targets 16 G + 4q + r of that coefficient.  Grid (N / (64 TPW), items): each of the four
+// waves takes TPW consecutive tiles, whose source words it requests together (the kernel is bound
+// by the memory requests in flight, not by its arithmetic).
+typedef int wv4i __attribute__((ext_vector_type(4)));
+constexpr int kWmGroups = (kMaxPrimes + 15) / 16;
+constexpr u64 kDigitBias = 0x8080808080808080ULL;
+
+__device__ __forceinline__ u64 wfold(const wv4i (&a)[8], int r, u64 t, double tinv) {
+  // byte-position pairs (|.| < 2^29), x = p0 + p1 2^16 + p2 2^32 + p3 2^48 with |x| < 2^76.01
+  const int p0 = a[0][r] + a[1][r] * 256, p1 = a[2][r] + a[3][r] * 256;
+  const int p2 = a[4][r] + a[5][r] * 256, p3 = a[6][r] + a[7][r] * 256;
+  // the quotient from a double estimate of x (absolute error < 2^25, so |x / t - qq| < 0.5 + 2^-20 for
+  // t > 2^46), the remainder x - qq t exactly in wrapping 64-bit arithmetic: it lies in (-t, t)
+  const double xd = __builtin_fma(__builtin_fma(__builtin_fma((double)p3, 65536.0, (double)p2), 65536.0, (double)p1),
+                                  65536.0, (double)p0);
+  const long long qq = (long long)__builtin_rint(xd * tinv);
+  const u64 xl = (u64)(long long)p0 + ((u64)(long long)p1 << 16) + ((u64)(long long)p2 << 32) +
+                 ((u64)(long long)p3 << 48);
+  long long v = (long long)(xl - (u64)qq * t);
+  if (v < 0) v += (long long)t;
+  return (u64)v;
+}
+
+template <int TPW>
+__global__ __launch_bounds__(256) void wk_mconv(const u64* __restrict__ src, long long src_item, int src_off,
+                                                u64* __restrict__ dst, long long dst_item,
+                                                const WideConv* __restrict__ cc, const wv4i* __restrict__ dig,
+                                                WideTables T) {
+  __shared__ wv4i A[kWmGroups * 8 * 64];
+  const int ns = cc->ns, nt = cc->nt, groups = (nt + 15) >> 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, q = lane >> 4, j = lane & 15;
+  const long long it = blockIdx.y;
+  const int tile0 = (blockIdx.x * 4 + wave) * TPW;
+  // every source word of the wave's tiles is requested before anything waits on memory
+  u64 raw[TPW][2], b[2], hv[2], hs[2];
+  bool act[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int sidx = 2 * q + h;
+    act[h] = sidx < ns;
+    const int si = act[h] ? sidx : 0;
+    const u64* sp = src + it * src_item + (long long)(src_off + si) * kN;
+#pragma unroll
+    for (int tt = 0; tt < TPW; ++tt) raw[tt][h] = act[h] ? sp[(tile0 + tt) * 16 + j] : 0;
+    b[h] = T.p[cc->src_prime[si]];
+    hv[h] = cc->hinv[si];
+    hs[h] = cc->hinv_s[si];
+  }
+  const wv4i* __restrict__ tab = dig + cc->dig_off;
+  for (int i = threadIdx.x; i < groups * 512; i += 256) A[i] = tab[i];
+  __syncthreads();
+#pragma unroll
+  for (int tt = 0; tt < TPW; ++tt) {
+    const int k = (tile0 + tt) * 16 + j;
+    u64 w[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      w[h] = 0;
+      if (act[h]) {
+        const u64 v = wmulc(raw[tt][h], hv[h], hs[h], b[h]);
+        const long long y = 2 * v > b[h] ? (long long)v - (long long)b[h] : (long long)v;
+        w[h] = ((u64)y + kDigitBias) ^ kDigitBias;
+      }
+    }
+    const wv4i bv = {(int)(uint32_t)w[0], (int)(uint32_t)(w[0] >> 32), (int)(uint32_t)w[1], (int)(uint32_t)(w[1] >> 32)};
+    for (int G = 0; G < groups; ++G) {
+      wv4i acc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c)
+        acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(A[(G * 8 + c) * 64 + lane], bv, wv4i{0, 0, 0, 0}, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = 16 * G + 4 * q + r;
+        if (t < nt)
+          dst[it * dst_item + (long long)cc->dst_slot[t] * kN + k] = wfold(acc, r, T.p[cc->dst_prime[t]], cc->fold_inv[t]);
+      }
+    }
+  }
+}
+
 // The centered lift of one coefficient-domain limb (prime src_pi) to limbs first .. first + gridDim.y - 1
 // (limb i modulo prime i).  Grid (N / 256, targets, items).
 __global__ __launch_bounds__(256) void wk_lift(const u64* __restrict__ src, long long src_item, int src_pi,
@@ -737,6 +829,44 @@ int encode_stage2(uint64_t* out, const double* in, long long in_stride, int rows
 // ======================================================================================= set-up
 u64 primitive_root_2n(u64 q, int log_n);  // context.hip: the root choice every table shares
 
+// Balanced base-256 digits of 0 <= v < 2^62: v = sum_c e_c 256^c with every e_c in [-128, 127].
+void balanced_digits(u64 v, int8_t (&e)[8]) {
+  long long x = (long long)v;
+  for (int c = 0; c < 8; ++c) {
+    int d = (int)(x & 255);
+    if (d >= 128) d -= 256;
+    e[c] = (int8_t)d;
+    x = (x - d) / 256;  // exact: x - d is a multiple of 256
+  }
+}
+
+// The matrix-core operands of one conversion (wk_mconv): for target group G (targets 16 G .. 16 G + 15),
+// output digit c and lane l, the 16 bytes lane l supplies as the A operand of
+// v_mfma_i32_16x16x64_i8 -- row l % 16 (target 16 G + l % 16), K bytes 16 (l / 16) .. +15, i.e.
+// source s = 2 (l / 16) + m / 8 and digit position a = m % 8 for byte m: digit c of
+// K_{s,a,t} = (B / b_s) 256^a mod t (zero for t >= nt or s >= ns).  Also sets fold_inv.
+void fill_wide_digits(WideConv& cc, const std::vector<u64>& P, std::vector<int8_t>& tab) {
+  const int groups = (cc.nt + 15) / 16;
+  cc.dig_off = (long long)(tab.size() / 16);
+  const size_t base = tab.size();
+  tab.resize(base + (size_t)groups * 8 * 64 * 16, 0);
+  for (int t = 0; t < cc.nt; ++t) {
+    const u64 qt = P[cc.dst_prime[t]];
+    cc.fold_inv[t] = 1.0 / (double)qt;
+    const int G = t / 16, i = t % 16;
+    for (int sidx = 0; sidx < cc.ns; ++sidx) {
+      u64 k = cc.hmod[sidx][t];
+      for (int a = 0; a < 8; ++a) {
+        int8_t e[8];
+        balanced_digits(k, e);
+        const int qd = sidx / 2, m = 8 * (sidx % 2) + a, l = 16 * qd + i;
+        for (int c = 0; c < 8; ++c) tab[base + (((size_t)G * 8 + c) * 64 + l) * 16 + m] = e[c];
+        k = hmul(k, 256 % qt, qt);
+      }
+    }
+  }
+}
+
 int wide_init(hck_context* c) {
   const int L = c->L, K = c->K, alpha = c->alpha, bmax = c->beta_max;
   const size_t np = (size_t)c->np, n = kN;
@@ -803,6 +933,18 @@ int wide_init(hck_context* c) {
     }
   }
 
+  // The matrix-core conversion's fold needs every target prime above 2^46 (|byte-position sum| < 2^45).
+  bool mconv = true;
+  for (size_t i = 0; i < np; ++i) mconv = mconv && P[i] > (1ULL << 46);
+  std::vector<int8_t> dig;
+  if (mconv) {
+    for (int ell = 1; ell <= L; ++ell) {
+      const int beta = (ell + alpha - 1) / alpha;
+      for (int j = 0; j < beta; ++j) fill_wide_digits(modup[(size_t)ell * bmax + j], P, dig);
+      fill_wide_digits(moddown[ell], P, dig);
+    }
+  }
+
   auto align = [](size_t x) { return (x + 255) & ~(size_t)255; };
   struct Part {
     const void* src;
@@ -816,7 +958,7 @@ int wide_init(hck_context* c) {
       {z4.data(), np * 8}, {z4_s.data(), np * 8}, {pm.data(), np * 8}, {pm_s.data(), np * 8},
       {pinv.data(), np * 8}, {pinv_s.data(), np * 8},
       {modup.data(), modup.size() * sizeof(WideConv)}, {moddown.data(), moddown.size() * sizeof(WideConv)},
-      {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8},
+      {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8}, {dig.data(), dig.size()},
   };
   size_t off = 0;
   for (Part& pt : parts) {
@@ -832,6 +974,7 @@ int wide_init(hck_context* c) {
   }
   char* base = (char*)ws->block;
   for (const Part& pt : parts) {
+    if (pt.bytes == 0) continue;
     e = hipMemcpy(base + pt.off, pt.src, pt.bytes, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
       (void)hipFree(ws->block);
@@ -860,6 +1003,7 @@ int wide_init(hck_context* c) {
   ws->moddown = (WideConv*)at(16);
   ws->qlast_inv = (u64*)at(17);
   ws->qlast_inv_s = (u64*)at(18);
+  ws->conv_dig = mconv ? (const void*)at(19) : nullptr;
   c->wide = ws;
   return HCK_OK;
 }
@@ -913,6 +1057,25 @@ LimbList q_list(int ell, int first = 0) {
     l.prime[i - first] = (uint8_t)i;
   }
   return l;
+}
+}  // namespace
+
+namespace {
+// The base conversion of nb items: on the matrix cores (the context's default engine) when the
+// context has its digit tables, else on the VALU (wk_conv); identical residues.
+void launch_wconv(const hck_context* c, const u64* src, long long src_item, int src_off, u64* dst,
+                  long long dst_item, const WideConv* cc, int nb, hipStream_t s) {
+  const WideState& W = *c->wide;
+  if (c->conv_engine == 1 && W.conv_dig) {
+    if (nb >= 4)
+      wk_mconv<4><<<dim3(kN / 256, nb), 256, 0, s>>>(src, src_item, src_off, dst, dst_item, cc,
+                                                      (const wv4i*)W.conv_dig, W.t);
+    else
+      wk_mconv<1><<<dim3(kN / 64, nb), 256, 0, s>>>(src, src_item, src_off, dst, dst_item, cc,
+                                                     (const wv4i*)W.conv_dig, W.t);
+  } else {
+    wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(src, src_item, src_off, dst, dst_item, cc, W.t);
+  }
 }
 }  // namespace
 
@@ -976,8 +1139,7 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
     for (int j = 0; j < beta; ++j) {
       const int lo = j * alpha, hi = std::min(lo + alpha, ell);
       u64* EXTj = EXT + (long long)j * ext_l * n;
-      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(X, (long long)ell * n, lo, EXTj, ext_item,
-                                                 W.modup + (size_t)ell * bmax + j, T);
+      launch_wconv(c, X, (long long)ell * n, lo, EXTj, ext_item, W.modup + (size_t)ell * bmax + j, nb, s);
       HCK_CHECK_LAUNCH();
       LimbList le;
       le.n = 0;
@@ -1009,7 +1171,7 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
       u64* A = ACC + (long long)comp * ext_l * n;
       rc = wide_ntt(c, A, A, nb, 2LL * ext_l * n, 2LL * ext_l * n, lp, true, s);
       if (rc) return rc;
-      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(A, 2LL * ext_l * n, ell, CV, (long long)ell * n, W.moddown + ell, T);
+      launch_wconv(c, A, 2LL * ext_l * n, ell, CV, (long long)ell * n, W.moddown + ell, nb, s);
       HCK_CHECK_LAUNCH();
       rc = wide_ntt(c, CV, CV, nb, (long long)ell * n, (long long)ell * n, lq, false, s);
       if (rc) return rc;
@@ -1045,8 +1207,7 @@ int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, lon
     for (int j = 0; j < beta; ++j) {
       const int lo = j * alpha, hi = std::min(lo + alpha, ell);
       u64* EXT = digits + (long long)b0 * dig_item + (long long)j * ext_l * n;
-      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(X, (long long)ell * n, lo, EXT, dig_item,
-                                                 W.modup + (size_t)ell * bmax + j, T);
+      launch_wconv(c, X, (long long)ell * n, lo, EXT, dig_item, W.modup + (size_t)ell * bmax + j, nb, s);
       HCK_CHECK_LAUNCH();
       LimbList le;
       le.n = 0;
@@ -1110,7 +1271,7 @@ int wide_hoisted(const hck_context* c, int ell, int inputs, int items, const uin
       u64* A = ACC + (long long)comp * ext_l * n;
       int rc = wide_ntt(c, A, A, nb, 2LL * ext_l * n, 2LL * ext_l * n, lp, true, s);
       if (rc) return rc;
-      wk_conv<<<dim3(kN / 256, nb), 256, 0, s>>>(A, 2LL * ext_l * n, ell, CV, (long long)ell * n, W.moddown + ell, T);
+      launch_wconv(c, A, 2LL * ext_l * n, ell, CV, (long long)ell * n, W.moddown + ell, nb, s);
       HCK_CHECK_LAUNCH();
       rc = wide_ntt(c, CV, CV, nb, (long long)ell * n, (long long)ell * n, lq, false, s);
       if (rc) return rc;
@@ -1143,7 +1304,7 @@ int wide_moddown(const hck_context* c, int ell, int polys, const uint64_t* in, l
   }
   int rc = wide_ntt(c, in + (long long)ell * n, TP, polys, in_stride, (long long)K * n, lp, true, s);
   if (rc) return rc;
-  wk_conv<<<dim3(kN / 256, polys), 256, 0, s>>>(TP, (long long)K * n, 0, CV, (long long)ell * n, W.moddown + ell, W.t);
+  launch_wconv(c, TP, (long long)K * n, 0, CV, (long long)ell * n, W.moddown + ell, polys, s);
   HCK_CHECK_LAUNCH();
   rc = wide_ntt(c, CV, CV, polys, (long long)ell * n, (long long)ell * n, q_list(ell), false, s);
   if (rc) return rc;

@@ -29,6 +29,10 @@ struct WideConv {
   uint64_t hmod_s[kMaxAlpha][kMaxPrimes];
   uint64_t hmod_m[kMaxAlpha][kMaxPrimes];             // (B / b_s) 2^64 mod t (Montgomery form)
   uint64_t tneg_inv[kMaxPrimes];                      // -t^-1 mod 2^64
+  // The matrix-core form (wk_mconv): fold_inv[t] = fl(1 / t), the fold's quotient estimate, and the
+  // offset (in 16-byte operand units) of this conversion's digit table in WideState::conv_dig.
+  double fold_inv[kMaxPrimes];
+  long long dig_off;
 };
 
 struct WideTables {
@@ -56,6 +60,9 @@ struct WideState {
   WideConv* moddown = nullptr;   // [L + 1]: P primes -> q_0 .. q_{ell-1}
   uint64_t* qlast_inv = nullptr; // [(L + 1) * L]: level ell, prime i: q_{ell-1}^-1 mod q_i
   uint64_t* qlast_inv_s = nullptr;
+  // int8 operands of the matrix-core base conversion (every modup / moddown table, at dig_off), or
+  // null when a prime of the context lies below 2^46 (the fold's bound); then wk_conv runs.
+  const void* conv_dig = nullptr;
 };
 
 // Context set-up and release (context.hip calls these for a context with a prime >= 2^50).

@@ -2,7 +2,7 @@
 (assets/feature_major.json: N = 2^16, 38 Q limbs -- q_0 of 60 bits, the other 37 of 59 bits -- dnum
 5, 8 special primes of 60 bits), every kernel through the C ABI bit-exact against the CPU oracle
 (exact 128-bit arithmetic for any prime below 2^62): NTT, automorphism, elementwise ops, key
-generation, key switch at 38, 19 and 8 limbs, rotation with and without addends, hoisted rotations,
+generation, key switch at 38, 19 and 8 limbs (base conversion on either engine), rotation with and without addends, hoisted rotations,
 the extended-basis
 rotation and ModDown, rescale, ModRaise, tensor and relinearisation, the BSGS MAC and the encoder
 for coefficients up to 2^61.  Several checks are the FP64 path's own test bodies, run here on the
@@ -87,6 +87,14 @@ def test_switching_key_generation(env):
 def test_keyswitch(env, ell):
     print(f"wide key switch at {ell} limbs", flush=True)
     G.test_keyswitch(env, ell)
+
+
+@pytest.mark.parametrize("ell", [38, 9, 1])
+def test_conversion_engines_agree(env, ell):
+    """The wide base conversion on the int8 matrix cores (the default: eight balanced base-256 digits
+    per source, a 128-bit-free fold) and on the VALU (64-bit products, one Montgomery reduction) give
+    bit-identical key switches and ModDowns, equal to the oracle's."""
+    G.test_conversion_engines_agree(env, ell)
 
 
 def test_rotate_and_rescale(env):
