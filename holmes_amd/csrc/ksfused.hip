@@ -280,6 +280,19 @@ __device__ __forceinline__ void load_gal(double (&x)[16], const uint64_t* __rest
   }
 }
 
+// load_gal without the conversion: the raw words, so that a caller can issue the loads early and
+// convert them where they are used (a conversion right behind the loads would wait for them there).
+__device__ __forceinline__ void load_gal_raw(uint64_t (&r)[16], const uint64_t* __restrict__ limb, long long na,
+                                             uint32_t g) {
+  if (g == 1u) {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) r[k] = limb[na + 16 * k];
+  } else {
+#pragma unroll
+    for (int k = 0; k < 16; ++k) r[k] = limb[gal_src(na + 16 * k, g)];
+  }
+}
+
 // Natural-layout access in layout A under map N: thread (rb, j) owns words j + 16k of row g + 16 rb;
 // 16 consecutive lanes touch 128 consecutive bytes.
 __device__ __forceinline__ long long nat_a(int g) {
@@ -601,14 +614,19 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
       pinv[r] = T.pinv[tp];
     }
     double x[kMItems][16];
+    // the next tile's digit words are read while this tile's sums are folded
+    uint64_t w0 = B0[0], w1 = B1[0];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const uint64_t w0 = B0[16 * k], w1 = B1[16 * k];
       const v4i bv = {(int)(uint32_t)w0, (int)(uint32_t)(w0 >> 32), (int)(uint32_t)w1, (int)(uint32_t)(w1 >> 32)};
       v4i acc[kConvDigits];
 #pragma unroll
       for (int c = 0; c < kConvDigits; ++c)
         acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[c], bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+      if (k < 15) {
+        w0 = B0[16 * (k + 1)];
+        w1 = B1[16 * (k + 1)];
+      }
 #pragma unroll
       for (int r = 0; r < kMItems; ++r) {
         x[r][k] = mconv_fold(acc[0][r] + (int)((uint32_t)acc[1][r] << 8), acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
@@ -747,15 +765,19 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
       pinv[r] = T.pinv[tp];
     }
     double x[kMItems][16];
+    uint64_t w0 = B0[0], w1 = B1[0];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const uint64_t w0 = B0[16 * k], w1 = B1[16 * k];
       const double rz = RZ[16 * k];
       const v4i bv = {(int)(uint32_t)w0, (int)(uint32_t)(w0 >> 32), (int)(uint32_t)w1, (int)(uint32_t)(w1 >> 32)};
       v4i acc[kConvDigits];
 #pragma unroll
       for (int c = 0; c < kConvDigits; ++c)
         acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[c], bv, v4i{0, 0, 0, 0}, 0, 0, 0);
+      if (k < 15) {
+        w0 = B0[16 * (k + 1)];
+        w1 = B1[16 * (k + 1)];
+      }
 #pragma unroll
       for (int r = 0; r < kMItems; ++r) {
         x[r][k] = mconv_fold_add(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
@@ -912,54 +934,104 @@ struct HoistSrc {
 template <bool HOIST>
 __device__ __forceinline__ int hoist_input(const HoistSrc& H, int b) { return HOIST ? (H.src0 + b) % H.inputs : b; }
 
-template <bool HOIST = false>
-__device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], double (&x)[16],
-                                        const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
-                                        const double* __restrict__ t2, const uint64_t* __restrict__ key, int b,
-                                        int e, int pi, int rg, int ell, int beta, double* S, const double* TW,
-                                        const double* __restrict__ after, double p, double pinv,
-                                        const DevTables& T, bool zero = true, HoistSrc H = HoistSrc{nullptr, 1, 0}) {
-  const int L = T.L, K = T.K, alpha = T.alpha;
-  const int ext_l = ell + K;
-  const int beta_max = (L + alpha - 1) / alpha;
-  const long long comp_stride = (long long)beta_max * (L + K) * kN;
-  const int own = e < ell ? e / alpha : -1;
-  const long long na = nat_a(rg);
-  const int src = hoist_input<HOIST>(H, b);
-  const double* t2b = t2 + ((long long)b * beta * ext_l + e) * kN;  // digit j at t2b + j * ext_l * kN
-  auto load_keys = [&](uint64_t (&kb)[16], uint64_t (&ka)[16], int jd) {
+// Where tile_ip reads its operands: the own digit's limb e (d through sigma_g), the keys of digit jd,
+// the ModUp output tile of T2 digit jd (or, hoisted, the materialised digit).
+struct IpSrc {
+  const uint64_t* d;
+  long long d_stride;
+  const double* t2b;      // T2 digit j at t2b + j * ext_l * kN
+  const uint64_t* key;
+  long long comp_stride;  // the key's a component follows its b component at this distance
+  int L, K, ext_l, beta, own, nt2, pi, src;
+  long long na;
+  __device__ __forceinline__ int t2digit(int n) const { return (own >= 0 && n >= own) ? n + 1 : n; }
+  __device__ __forceinline__ void keys(uint64_t (&kb)[16], uint64_t (&ka)[16], int jd) const {
     const uint64_t* kp = key + ((long long)jd * (L + K) + pi) * kN + na;
 #pragma unroll
     for (int k = 0; k < 16; ++k) { kb[k] = kp[16 * k]; ka[k] = kp[comp_stride + 16 * k]; }
-  };
-  // the T2 digits: every digit but the own one, ascending
-  const int nt2 = beta - (own >= 0 ? 1 : 0);
-  auto t2digit = [&](int n) { return (own >= 0 && n >= own) ? n + 1 : n; };
-  uint64_t kb[16], ka[16];
+  }
+};
+
+template <bool HOIST>
+__device__ __forceinline__ IpSrc ip_src(const uint64_t* __restrict__ d, long long d_stride,
+                                        const double* __restrict__ t2, const uint64_t* __restrict__ key, int b, int e,
+                                        int pi, int rg, int ell, int beta, const DevTables& T, const HoistSrc& H) {
+  IpSrc I;
+  I.d = d;
+  I.d_stride = d_stride;
+  I.key = key;
+  I.L = T.L;
+  I.K = T.K;
+  I.ext_l = ell + T.K;
+  I.beta = beta;
+  const int beta_max = (T.L + T.alpha - 1) / T.alpha;
+  I.comp_stride = (long long)beta_max * (T.L + T.K) * kN;
+  I.own = e < ell ? e / T.alpha : -1;
+  I.nt2 = beta - (I.own >= 0 ? 1 : 0);
+  I.pi = pi;
+  I.na = nat_a(rg);
+  I.src = hoist_input<HOIST>(H, b);
+  I.t2b = t2 ? t2 + ((long long)b * beta * I.ext_l + e) * kN : nullptr;
+  return I;
+}
+
+// The loads of tile_ip's first step: the own digit (raw words into xr) and its keys; without an own
+// digit the first T2 tile (x only), or, hoisted, the first materialised digit (xr) and its keys.  The
+// tile kernels issue them before their twiddle staging, so that the data is in flight across the
+// staging barrier, and call tile_ip_body with ``pre`` set.  OWN_ALWAYS: the caller's limb is a Q
+// limb (an own digit exists), so no other load path joins the own digit's (a join would make the
+// compiler wait for the staged twiddles before these loads).
+template <bool HOIST, bool OWN_ALWAYS = false>
+__device__ __forceinline__ void tile_ip_first(uint64_t (&xr)[16], double (&x)[16], uint64_t (&kb)[16],
+                                              uint64_t (&ka)[16], const IpSrc& I, int e, int rg, uint32_t g,
+                                              const HoistSrc& H, const double* __restrict__ after) {
+  if (OWN_ALWAYS || I.own >= 0) {
+    load_gal_raw(xr, I.d + (long long)I.src * I.d_stride + (long long)e * kN, I.na, g);
+    I.keys(kb, ka, I.own);
+  } else if constexpr (HOIST) {
+    if (I.nt2 > 0) {
+      const int jd = I.t2digit(0);
+      load_gal_raw(xr, H.digits + ((long long)(I.src * I.beta + jd) * I.ext_l + e) * kN, I.na, g);
+      I.keys(kb, ka, jd);
+    }
+  } else {
+    const double* first = I.nt2 > 0 ? I.t2b + (long long)I.t2digit(0) * I.ext_l * kN : after;
+    if (first) load_t(x, first, rg);
+  }
+}
+
+template <bool HOIST, bool OWN_ALWAYS = false>
+__device__ __forceinline__ void tile_ip_body(double (&sb)[16], double (&sa)[16], double (&x)[16], uint64_t (&xr)[16],
+                                             uint64_t (&kb)[16], uint64_t (&ka)[16], const IpSrc& I, int e, int rg,
+                                             uint32_t g, double* S, const double* TW, const double* __restrict__ after,
+                                             double p, double pinv, bool zero, const HoistSrc& H, bool pre) {
   if (zero) {
 #pragma unroll
     for (int k = 0; k < 16; ++k) { sb[k] = 0.0; sa[k] = 0.0; }
   }
-  if (own >= 0) {
-    load_gal(x, d + (long long)src * d_stride + (long long)e * kN, na, g);
-    load_keys(kb, ka, own);
+  if (OWN_ALWAYS || I.own >= 0) {
+    if (!pre) tile_ip_first<HOIST, OWN_ALWAYS>(xr, x, kb, ka, I, e, rg, g, H, after);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);  // |x| < p: |term| <= 0.9p
-      sa[k] += mulv(x[k], u2d(ka[k]), p, pinv);
+      const double v = u2d(xr[k]);
+      sb[k] += mulv(v, u2d(kb[k]), p, pinv);  // |v| < p: |term| <= 0.9p
+      sa[k] += mulv(v, u2d(ka[k]), p, pinv);
     }
   }
   if constexpr (HOIST) {
     // canonical digits read through sigma_g: |term| <= 0.9p; a reduction every three digits keeps
     // the sums below p/2 + 1 + 0.9p + 3 * 0.9p < 8p <= 2^53
-    for (int n = 0; n < nt2; ++n) {
-      const int jd = t2digit(n);
-      load_gal(x, H.digits + ((long long)(src * beta + jd) * ext_l + e) * kN, na, g);
-      load_keys(kb, ka, jd);
+    for (int n = 0; n < I.nt2; ++n) {
+      const int jd = I.t2digit(n);
+      if (n > 0 || OWN_ALWAYS || I.own >= 0 || !pre) {
+        load_gal_raw(xr, H.digits + ((long long)(I.src * I.beta + jd) * I.ext_l + e) * kN, I.na, g);
+        I.keys(kb, ka, jd);
+      }
 #pragma unroll
       for (int k = 0; k < 16; ++k) {
-        sb[k] += mulv(x[k], u2d(kb[k]), p, pinv);
-        sa[k] += mulv(x[k], u2d(ka[k]), p, pinv);
+        const double v = u2d(xr[k]);
+        sb[k] += mulv(v, u2d(kb[k]), p, pinv);
+        sa[k] += mulv(v, u2d(ka[k]), p, pinv);
       }
       if (n % 3 == 2) {
 #pragma unroll
@@ -971,17 +1043,17 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
     for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
     return;
   }
-  {
-    const double* first = nt2 > 0 ? t2b + (long long)t2digit(0) * ext_l * kN : after;
+  if (OWN_ALWAYS || I.own >= 0 || !pre) {
+    const double* first = I.nt2 > 0 ? I.t2b + (long long)I.t2digit(0) * I.ext_l * kN : after;
     if (first) load_t(x, first, rg);
   }
-  for (int n = 0; n < nt2; ++n) {
+  for (int n = 0; n < I.nt2; ++n) {
     rows_fwd_lds(x, S, TW, p, pinv);
     // the keys, then the next tile: the inner product waits for the keys only, the tile lands
     // behind it.  (Keys issued before the transform would overlap it too, but with the tile, both
     // accumulators and the transform live they do not fit in 256 VGPRs.)
-    load_keys(kb, ka, t2digit(n));
-    const double* next = n + 1 < nt2 ? t2b + (long long)t2digit(n + 1) * ext_l * kN : after;
+    I.keys(kb, ka, I.t2digit(n));
+    const double* next = n + 1 < I.nt2 ? I.t2b + (long long)I.t2digit(n + 1) * I.ext_l * kN : after;
     if (next) load_t(x, next, rg);
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -996,6 +1068,18 @@ __device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], doub
   }
 #pragma unroll
   for (int k = 0; k < 16; ++k) { sb[k] = reduce(sb[k], p, pinv); sa[k] = reduce(sa[k], p, pinv); }
+}
+
+template <bool HOIST = false>
+__device__ __forceinline__ void tile_ip(double (&sb)[16], double (&sa)[16], double (&x)[16],
+                                        const uint64_t* __restrict__ d, long long d_stride, uint32_t g,
+                                        const double* __restrict__ t2, const uint64_t* __restrict__ key, int b,
+                                        int e, int pi, int rg, int ell, int beta, double* S, const double* TW,
+                                        const double* __restrict__ after, double p, double pinv,
+                                        const DevTables& T, bool zero = true, HoistSrc H = HoistSrc{nullptr, 1, 0}) {
+  uint64_t xr[16], kb[16], ka[16];
+  const IpSrc I = ip_src<HOIST>(d, d_stride, t2, key, b, e, pi, rg, ell, beta, T, H);
+  tile_ip_body<HOIST>(sb, sa, x, xr, kb, ka, I, e, rg, g, S, TW, after, p, pinv, zero, H, false);
 }
 
 // Grids of the tile kernels: one linear id per (ciphertext, tile).  Workgroups are dealt to the 8
@@ -1032,15 +1116,17 @@ __device__ __forceinline__ void rows_ip_body(const uint64_t* __restrict__ d, lon
   const int L = T.L, K = T.K;
   const int pi = e < ell ? e : L + (e - ell);
   const double p = T.p[pi], pinv = T.pinv[pi];
+  double sb[16], sa[16], x[16];
+  uint64_t xr[16], kb[16], ka[16];
+  const IpSrc I = ip_src<HOIST>(d, d_stride, t2, keys.k[koff + b], b, e, pi, rg, ell, beta, T, H);
   {
     TwStage st;
     tw_issue(st, T.tw_fwd + (size_t)pi * kN, rg);
+    tile_ip_first<HOIST>(xr, x, kb, ka, I, e, rg, g, H, nullptr);  // in flight across the staging barrier
     tw_store(st, TW);
     __syncthreads();
   }
-  double sb[16], sa[16], x[16];
-  tile_ip<HOIST>(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, e, pi, rg, ell, beta, S, TW, nullptr, p, pinv, T,
-                 true, H);
+  tile_ip_body<HOIST>(sb, sa, x, xr, kb, ka, I, e, rg, g, S, TW, nullptr, p, pinv, true, H, true);
   const long long na = nat_a(rg);
   if (ext_b) {
     if (e < ell && add) {
@@ -1242,17 +1328,19 @@ __device__ __forceinline__ void rows_ipq_body(const uint64_t* __restrict__ d, lo
   const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
   const uint32_t g = gal_of(G, koff + b);
   const double p = T.p[i], pinv = T.pinv[i];
-  {
-    TwStage st;
-    tw_issue(st, T.tw_fwd + (size_t)i * kN, rg);
-    tw_store(st, TW);
-    __syncthreads();
-  }
   const double* v_b = t4 + ((long long)b * 2 * nq + i) * kN;
   const double* v_a = v_b + (long long)nq * kN;
   double sb[16], sa[16], x[16];
-  tile_ip<HOIST>(sb, sa, x, d, d_stride, g, t2, keys.k[koff + b], b, i, i, rg, ell, beta, S, TW, v_b, p, pinv, T, true,
-                 H);
+  uint64_t xr[16], kb[16], ka[16];
+  const IpSrc I = ip_src<HOIST>(d, d_stride, t2, keys.k[koff + b], b, i, i, rg, ell, beta, T, H);
+  {
+    TwStage st;
+    tw_issue(st, T.tw_fwd + (size_t)i * kN, rg);
+    tile_ip_first<HOIST, true>(xr, x, kb, ka, I, i, rg, g, H, v_b);  // in flight across the staging barrier
+    tw_store(st, TW);
+    __syncthreads();
+  }
+  tile_ip_body<HOIST, true>(sb, sa, x, xr, kb, ka, I, i, rg, g, S, TW, v_b, p, pinv, true, H, true);
   const long long na = nat_a(rg);
   const TwPair pinv_P = lc->p_inv[i];
   if constexpr (RS) {
