@@ -21,7 +21,7 @@ LIB = OUT_DIR / "libholmes_ckks.so"
 ARCH = os.environ.get("HOLMES_AMD_ARCH", "gfx950")
 
 SOURCES = ["context.hip", "ntt.hip", "poly.hip", "keyswitch.hip", "ksfused.hip", "bsgs.hip", "encode.hip",
-           "mul.hip", "noalloc.hip", "wide.hip"]
+           "mul.hip", "noalloc.hip", "wide.hip", "wide_fused.hip"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 FLAGS = [

@@ -21,6 +21,7 @@
 #include "internal.hpp"
 #include "modarith64.hpp"
 #include "wide.hpp"
+#include "wide_dev.hpp"
 
 using u64 = uint64_t;
 using u128 = unsigned __int128;
@@ -82,19 +83,6 @@ void fill_wide_conv(WideConv& cc, const std::vector<u64>& P, const std::vector<i
     cc.dst_slot[t] = slot[t];
   }
 }
-
-// ---------------------------------------------------------------------------------- device helpers
-__device__ __forceinline__ u64 wadd(u64 a, u64 b, u64 p) {
-  const u64 s = a + b;
-  return s >= p ? s - p : s;
-}
-__device__ __forceinline__ u64 wsub(u64 a, u64 b, u64 p) { return a >= b ? a - b : a + p - b; }
-// a * w mod p, canonical, for any 64-bit a (Shoup: the lazy result lies in [0, 2p)).
-__device__ __forceinline__ u64 wmulc(u64 a, u64 w, u64 ws, u64 p) {
-  const u64 r = mulshoup_lazy(a, w, ws, p);
-  return r >= p ? r - p : r;
-}
-__device__ __forceinline__ Barrett64 wbar(const WideTables& T, int pi) { return Barrett64{T.p[pi], T.mu[pi], T.w[pi]}; }
 
 // ---------------------------------------------------------------------------------------------- NTT
 // Forward transform (Cooley-Tukey, psi^brv roots, bit-reversed evaluation order out), as two passes
@@ -329,25 +317,7 @@ __global__ __launch_bounds__(256) void wk_conv(const u64* __restrict__ src, long
 // folds targets 16 G + 4q + r of that coefficient.  Grid (N / (64 TPW), items): each of the four
 // waves takes TPW consecutive tiles, whose source words it requests together (the kernel is bound
 // by the memory requests in flight, not by its arithmetic).
-typedef int wv4i __attribute__((ext_vector_type(4)));
 constexpr int kWmGroups = (kMaxPrimes + 15) / 16;
-constexpr u64 kDigitBias = 0x8080808080808080ULL;
-
-__device__ __forceinline__ u64 wfold(const wv4i (&a)[8], int r, u64 t, double tinv) {
-  // byte-position pairs (|.| < 2^29), x = p0 + p1 2^16 + p2 2^32 + p3 2^48 with |x| < 2^76.01
-  const int p0 = a[0][r] + a[1][r] * 256, p1 = a[2][r] + a[3][r] * 256;
-  const int p2 = a[4][r] + a[5][r] * 256, p3 = a[6][r] + a[7][r] * 256;
-  // the quotient from a double estimate of x (absolute error < 2^25, so |x / t - qq| < 0.5 + 2^-20 for
-  // t > 2^46), the remainder x - qq t exactly in wrapping 64-bit arithmetic: it lies in (-t, t)
-  const double xd = __builtin_fma(__builtin_fma(__builtin_fma((double)p3, 65536.0, (double)p2), 65536.0, (double)p1),
-                                  65536.0, (double)p0);
-  const long long qq = (long long)__builtin_rint(xd * tinv);
-  const u64 xl = (u64)(long long)p0 + ((u64)(long long)p1 << 16) + ((u64)(long long)p2 << 32) +
-                 ((u64)(long long)p3 << 48);
-  long long v = (long long)(xl - (u64)qq * t);
-  if (v < 0) v += (long long)t;
-  return (u64)v;
-}
 
 template <int TPW>
 __global__ __launch_bounds__(256) void wk_mconv(const u64* __restrict__ src, long long src_item, int src_off,
@@ -385,9 +355,7 @@ __global__ __launch_bounds__(256) void wk_mconv(const u64* __restrict__ src, lon
     for (int h = 0; h < 2; ++h) {
       w[h] = 0;
       if (act[h]) {
-        const u64 v = wmulc(raw[tt][h], hv[h], hs[h], b[h]);
-        const long long y = 2 * v > b[h] ? (long long)v - (long long)b[h] : (long long)v;
-        w[h] = ((u64)y + kDigitBias) ^ kDigitBias;
+        w[h] = wdigits(wmulc(raw[tt][h], hv[h], hs[h], b[h]), b[h]);
       }
     }
     const wv4i bv = {(int)(uint32_t)w[0], (int)(uint32_t)(w[0] >> 32), (int)(uint32_t)w[1], (int)(uint32_t)(w[1] >> 32)};
@@ -872,7 +840,7 @@ int wide_init(hck_context* c) {
   const size_t np = (size_t)c->np, n = kN;
   const std::vector<u64>& P = c->primes;
   std::vector<u64> p(np), mu(np), fwd(np * n), fwd_s(np * n), inv(np * n), inv_s(np * n), ninv(np), ninv_s(np),
-      z4(np), z4_s(np), pm(np), pm_s(np), pinv(np), pinv_s(np);
+      z4(np), z4_s(np), pm(np), pm_s(np), pinv(np), pinv_s(np), mneg(np), r64(np), r64_s(np);
   std::vector<int> w(np);
   for (size_t i = 0; i < np; ++i) {
     const u64 q = P[i];
@@ -903,6 +871,11 @@ int wide_init(hck_context* c) {
     pm_s[i] = shoup_companion(pm[i], q);
     pinv[i] = i < (size_t)L ? hinv(pp, q) : 0;
     pinv_s[i] = shoup_companion(pinv[i], q);
+    u64 qi = q;  // Newton's iteration for q^-1 mod 2^64: each step doubles the correct low bits
+    for (int it = 0; it < 6; ++it) qi *= 2 - q * qi;
+    mneg[i] = 0 - qi;
+    r64[i] = (u64)(((u128)1 << 64) % q);
+    r64_s[i] = shoup_companion(r64[i], q);
   }
   std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1));
   std::vector<u64> ql((size_t)(L + 1) * L, 0), ql_s((size_t)(L + 1) * L, 0);
@@ -933,6 +906,21 @@ int wide_init(hck_context* c) {
     }
   }
 
+  // the fused key switch's source constants: hinv with the inverse transform's last stage folded in
+  auto fold_inverse = [&](WideConv& cc) {
+    for (int s = 0; s < cc.ns; ++s) {
+      const int sp = cc.src_prime[s];
+      const u64 b = P[sp];
+      const u64 n0 = hmul(ninv[sp], cc.hinv[s], b), n1 = hmul(n0, inv[(size_t)sp * n + 1], b);
+      cc.inv_n0[s] = n0;
+      cc.inv_n0_s[s] = shoup_companion(n0, b);
+      cc.inv_n1[s] = n1;
+      cc.inv_n1_s[s] = shoup_companion(n1, b);
+    }
+  };
+  for (WideConv& cc : modup) fold_inverse(cc);
+  for (WideConv& cc : moddown) fold_inverse(cc);
+
   // The matrix-core conversion's fold needs every target prime above 2^46 (|byte-position sum| < 2^45).
   bool mconv = true;
   for (size_t i = 0; i < np; ++i) mconv = mconv && P[i] > (1ULL << 46);
@@ -959,6 +947,7 @@ int wide_init(hck_context* c) {
       {pinv.data(), np * 8}, {pinv_s.data(), np * 8},
       {modup.data(), modup.size() * sizeof(WideConv)}, {moddown.data(), moddown.size() * sizeof(WideConv)},
       {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8}, {dig.data(), dig.size()},
+      {mneg.data(), np * 8}, {r64.data(), np * 8}, {r64_s.data(), np * 8},
   };
   size_t off = 0;
   for (Part& pt : parts) {
@@ -1004,6 +993,9 @@ int wide_init(hck_context* c) {
   ws->qlast_inv = (u64*)at(17);
   ws->qlast_inv_s = (u64*)at(18);
   ws->conv_dig = mconv ? (const void*)at(19) : nullptr;
+  T.mneg = (const u64*)at(20);
+  T.r64 = (const u64*)at(21);
+  T.r64_s = (const u64*)at(22);
   c->wide = ws;
   return HCK_OK;
 }
@@ -1081,6 +1073,7 @@ void launch_wconv(const hck_context* c, const u64* src, long long src_item, int 
 
 // Per item: X (ell) + EXT (ell + K) + ACC (2 (ell + K)) + CV (ell) + SD (ell) + S0 (ell) limbs.
 size_t wide_ks_bytes(const hck_context* c, int ell, int batch) {
+  if (wide_fused_ok(c)) return wide_fused_bytes(c, ell, batch);
   // per item: X [ell], EXT [beta][ell + K], ACC [2][ell + K], CV, SD, S0 [ell] each
   const size_t nb = (size_t)std::min(batch, kWideChunk), ext_l = (size_t)(ell + c->K);
   return nb * (size_t)kN * 8 * (4 * (size_t)ell + ((size_t)beta_of(c, ell) + 2) * ext_l);
@@ -1091,6 +1084,9 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
             const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
             char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
             const uint32_t* galois_items) {
+  if (wide_fused_ok(c))
+    return wide_ks_fused(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b,
+                         out_a, out_stride, ws, s, ext_b, ext_a, ext_stride, galois_items);
   if (c->alpha > kMaxAlpha || ell + c->K > kMaxList) return HCK_ERR_UNSUPPORTED;
   const WideState& W = *c->wide;
   const WideTables& T = W.t;

@@ -29,6 +29,9 @@ struct WideConv {
   uint64_t hmod_s[kMaxAlpha][kMaxPrimes];
   uint64_t hmod_m[kMaxAlpha][kMaxPrimes];             // (B / b_s) 2^64 mod t (Montgomery form)
   uint64_t tneg_inv[kMaxPrimes];                      // -t^-1 mod 2^64
+  // The fused key switch (wide_fused.hip) runs the sources' inverse column pass in the same kernel and
+  // folds hinv into its last stage: inv_n0 = N^-1 hinv, inv_n1 = N^-1 psi_rev_inv[1] hinv (mod b_s).
+  uint64_t inv_n0[kMaxAlpha], inv_n0_s[kMaxAlpha], inv_n1[kMaxAlpha], inv_n1_s[kMaxAlpha];
   // The matrix-core form (wk_mconv): fold_inv[t] = fl(1 / t), the fold's quotient estimate, and the
   // offset (in 16-byte operand units) of this conversion's digit table in WideState::conv_dig.
   double fold_inv[kMaxPrimes];
@@ -51,6 +54,9 @@ struct WideTables {
   const uint64_t* pmod_s;
   const uint64_t* pinv;    // [np] P^-1 mod q_i (Q primes)
   const uint64_t* pinv_s;
+  const uint64_t* mneg;    // [np] -p^-1 mod 2^64 (Montgomery products of the fused key switch)
+  const uint64_t* r64;     // [np] 2^64 mod p, which undoes a Montgomery product's 2^-64
+  const uint64_t* r64_s;
 };
 
 struct WideState {
@@ -81,6 +87,15 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
             const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a, long long out_stride,
             char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a, long long ext_stride,
             const uint32_t* galois_items);
+// The fused key switch (wide_fused.hip): five kernels with the FP64 path's schedule, on contexts whose
+// conversions run on the matrix cores (wide_fused_ok); wide_ks and wide_ks_bytes dispatch to it.
+bool wide_fused_ok(const hck_context* c);
+size_t wide_fused_bytes(const hck_context* c, int ell, int batch);
+int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+                  const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+                  const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
+                  long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
+                  long long ext_stride, const uint32_t* galois_items);
 size_t wide_hoist_bytes(const hck_context* c, int ell, int inputs);
 int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
                char* ws, hipStream_t s);

@@ -1,0 +1,622 @@
+// Fused hybrid key switch on 64-bit words: the wide-prime path's counterpart of ksfused.hip.
+//
+// The same five-kernel schedule and workspace tile layout (tile_layout.hpp) as the FP64 kernels,
+// with residues held as 64-bit words (primes below 2^61: the reference's 60/59-bit production chain).
+// Arithmetic (every bound below needs 4p < 2^63):
+//  * transforms run lazily (Harvey): forward butterflies take and return words below 4p, inverse
+//    ones below 2p; products by twiddles and conversion factors use Shoup's companions, whose lazy
+//    result lies below 2p for any 64-bit input.  Workspace words keep these lazy ranges;
+//  * key products are Montgomery products x k 2^-64 (below 2p for x < 4p, k < p), summed lazily
+//    below 2p and multiplied by 2^64 mod p (Shoup, canonical result) once per output;
+//  * the base-conversion sums run on the int8 matrix cores with the wide digit tables (wide_dev.hpp:
+//    wdigits takes a canonical residue, wfold returns one).
+// Outputs are canonical.
+//
+//   K1 wf_intt_rows   sigma_g(d) (natural) --INTT rows-->                              T1 (workspace)
+//   K2 wf_cols_mconv  T1 --INTT cols (N^-1 hinv folded)--> digits --ModUp sums (MFMA)--> NTT cols --> T2
+//   K3 wf_rows_ip     P limbs: T2 --NTT rows--> x_j;  acc = sum_j x_j key_j --INTT rows--> ACCP
+//                     (or every extended limb, ending in the extended basis)
+//   K4 wf_cols_mconv  ACCP --INTT cols--> ModDown sums P -> Q --NTT cols--> T4
+//   K5 wf_rows_ipq    Q limbs: acc as in K3 (d itself for the digit's own limb); T4 --NTT rows--> v;
+//                     out = (acc - v) P^-1 (+ sigma_g(add)) (+ acc_in)
+//
+// Every intermediate is an exact residue, so the outputs equal those of the separate-launch wide
+// kernels and of the CPU oracle (same centered fast base conversion).  Algorithm: EasyFHE's key switch
+// for fhe.homo_rotate (F.cv_modup, F.cv_innerproduct_*, F.cv_moddown; bench/cmp/report.py:26-30).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "../../include/holmes_ckks.h"
+#include "internal.hpp"
+#include "tile_layout.hpp"
+#include "wide_dev.hpp"
+
+namespace hck {
+namespace {
+
+using u64 = uint64_t;
+
+constexpr int kT = 256;         // threads per workgroup
+constexpr int kItems = 64;      // ciphertexts per launch (key pointers passed by value)
+constexpr int kYStride = 272;   // LDS stride of one (source, column) run of 256 words
+constexpr int kMItems = 3;      // targets per quarter-wave per conversion pass
+constexpr int kMPass = 8 * kMItems;
+
+struct WKeysF {
+  const u64* k[kItems];
+};
+struct WGalF {
+  int per_item;
+  uint32_t uniform;
+  uint32_t g[kItems];
+};
+__device__ __forceinline__ uint32_t gal_of(const WGalF& G, int b) { return G.per_item ? G.g[b] : G.uniform; }
+
+// Cooley-Tukey (u, v) -> (u + w v, u - w v), inputs and outputs below 4p; Gentleman-Sande
+// (u, v) -> (u + v, (u - v) w), inputs and outputs below 2p.  p2 = 2p.
+__device__ __forceinline__ void w_ct(u64& u, u64& v, u64 w, u64 ws, u64 p, u64 p2) {
+  const u64 a = u >= p2 ? u - p2 : u;
+  const u64 y = mulshoup_lazy(v, w, ws, p);
+  u = a + y;
+  v = a - y + p2;
+}
+__device__ __forceinline__ void w_gs(u64& u, u64& v, u64 w, u64 ws, u64 p, u64 p2) {
+  const u64 a = u, b = v, s = a + b;
+  u = s >= p2 ? s - p2 : s;
+  v = mulshoup_lazy(a - b + p2, w, ws, p);
+}
+__device__ __forceinline__ u64 wcanon2(u64 x, u64 p) { return x >= p ? x - p : x; }         // x < 2p
+__device__ __forceinline__ u64 wcanon4(u64 x, u64 p) { return wcanon2(x >= 2 * p ? x - 2 * p : x, p); }  // x < 4p
+
+// x k 2^-64 mod p below 2p, for x k < 2^64 p (Montgomery; mneg = -p^-1 mod 2^64): t + m p is a
+// multiple of 2^64 for m = t mneg, and its low words add up to 2^64 exactly when t's low word is not 0.
+__device__ __forceinline__ u64 wmont(u64 x, u64 k, u64 p, u64 mneg) {
+  const u128_t t = (u128_t)x * k;
+  const u64 tl = (u64)t, th = (u64)(t >> 64);
+  const u64 m = tl * mneg;
+  return th + (u64)(((u128_t)m * p) >> 64) + (tl != 0 ? 1 : 0);
+}
+
+// ----------------------------------------------------------------- column transforms (16-thread slots)
+// Root indices as in ksfused.hip: stage l of a column pairs rows 128 >> l apart; layout A holds rows
+// j + 16k (group k >> (4 - l)), layout B rows 16j + k (group (j << (l - 4)) + (k >> (8 - l))).
+__device__ __forceinline__ void wcol_fwd_lo(u64 (&x)[16], const u64* __restrict__ tw, const u64* __restrict__ tws,
+                                            u64 p) {
+#pragma unroll
+  for (int l = 0; l < 4; ++l) {
+    const int h = 8 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const int wi = (1 << l) + (k >> (4 - l));
+      w_ct(x[k], x[k + h], tw[wi], tws[wi], p, 2 * p);
+    }
+  }
+}
+
+__device__ __forceinline__ void wcol_fwd_hi(u64 (&x)[16], int j, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+#pragma unroll
+  for (int l = 4; l < 8; ++l) {
+    const int h = 128 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const int wi = (1 << l) + (j << (l - 4)) + (k >> (8 - l));
+      w_ct(x[k], x[k + h], tw[wi], tws[wi], p, 2 * p);
+    }
+  }
+}
+
+__device__ __forceinline__ void wcol_inv_hi(u64 (&x)[16], int j, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+#pragma unroll
+  for (int l = 7; l >= 4; --l) {
+    const int h = 128 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const int wi = (1 << l) + (j << (l - 4)) + (k >> (8 - l));
+      w_gs(x[k], x[k + h], tw[wi], tws[wi], p, 2 * p);
+    }
+  }
+}
+
+// inverse stages 3..1 on layout A, then stage 0 with its root, N^-1 and the conversion's hinv folded:
+// n0 = N^-1 hinv, n1 = N^-1 psi_rev_inv[1] hinv (WideConv::inv_n0 / inv_n1); inputs below 2p
+__device__ __forceinline__ void wcol_inv_lo(u64 (&x)[16], const u64* __restrict__ tw, const u64* __restrict__ tws,
+                                            u64 n0, u64 n0s, u64 n1, u64 n1s, u64 p) {
+#pragma unroll
+  for (int l = 3; l >= 1; --l) {
+    const int h = 8 >> l;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      const int wi = (1 << l) + (k >> (4 - l));
+      w_gs(x[k], x[k + h], tw[wi], tws[wi], p, 2 * p);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) {  // canonical results (the conversion's digits need them)
+    const u64 a = x[k], b = x[k + 8];
+    x[k] = wcanon2(mulshoup_lazy(a + b, n0, n0s, p), p);
+    x[k + 8] = wcanon2(mulshoup_lazy(a - b + 2 * p, n1, n1s, p), p);
+  }
+}
+
+// ----------------------------------------------------------------- row transforms (256 threads)
+// stage l of row b: layout A (words j + 16k) groups (b << (l - 8)) + (k >> (12 - l)); layout B
+// (words 16j + k) groups (b << (l - 8)) + (j << (l - 12)) + (k >> (16 - l)).
+// Each stage addresses its roots from one per-stage base (tw + base, constant offsets), so that the
+// stages' root addresses cost a few registers when the compiler hoists them out of a digit loop.
+__device__ __forceinline__ void wrow_fwd_lo(u64 (&x)[16], int b, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+#pragma unroll
+  for (int l = 8; l < 12; ++l) {
+    const int h = 2048 >> l;
+    const int base = (1 << l) + (b << (l - 8));
+    const u64* __restrict__ t = tw + base;
+    const u64* __restrict__ ts = tws + base;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      w_ct(x[k], x[k + h], t[k >> (12 - l)], ts[k >> (12 - l)], p, 2 * p);
+    }
+  }
+}
+
+__device__ __forceinline__ void wrow_fwd_hi(u64 (&x)[16], int b, int j, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+#pragma unroll
+  for (int l = 12; l < 16; ++l) {
+    const int h = 32768 >> l;
+    const int base = (1 << l) + (b << (l - 8)) + (j << (l - 12));
+    const u64* __restrict__ t = tw + base;
+    const u64* __restrict__ ts = tws + base;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      w_ct(x[k], x[k + h], t[k >> (16 - l)], ts[k >> (16 - l)], p, 2 * p);
+    }
+  }
+}
+
+__device__ __forceinline__ void wrow_inv_hi(u64 (&x)[16], int b, int j, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+#pragma unroll
+  for (int l = 15; l >= 12; --l) {
+    const int h = 32768 >> l;
+    const int base = (1 << l) + (b << (l - 8)) + (j << (l - 12));
+    const u64* __restrict__ t = tw + base;
+    const u64* __restrict__ ts = tws + base;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      w_gs(x[k], x[k + h], t[k >> (16 - l)], ts[k >> (16 - l)], p, 2 * p);
+    }
+  }
+}
+
+__device__ __forceinline__ void wrow_inv_lo(u64 (&x)[16], int b, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+#pragma unroll
+  for (int l = 11; l >= 8; --l) {
+    const int h = 2048 >> l;
+    const int base = (1 << l) + (b << (l - 8));
+    const u64* __restrict__ t = tw + base;
+    const u64* __restrict__ ts = tws + base;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if (k & h) continue;
+      w_gs(x[k], x[k + h], t[k >> (12 - l)], ts[k >> (12 - l)], p, 2 * p);
+    }
+  }
+}
+
+// NTT rows pass of row group g, x as load_t returns it (map T, layout A); returns layout A under map N
+// (the thread's natural words nat_a(g) + 16k).
+__device__ __forceinline__ void wrows_fwd_t(u64 (&x)[16], int g, u64* S, const u64* __restrict__ tw,
+                                            const u64* __restrict__ tws, u64 p) {
+  const RowMap mt = map_t(), mn = map_n();
+  wrow_fwd_lo(x, g + 16 * mt.rb, tw, tws, p);
+  row_xchg<true, false>(x, S, mt, mn);
+  wrow_fwd_hi(x, g + 16 * mn.rb, mn.j, tw, tws, p);
+  row_xchg<false, true>(x, S, mn, mn);
+}
+
+// INTT rows pass of row group g held in layout A under map N; stores the result to the workspace.
+__device__ __forceinline__ void wrows_inv_to_t(u64 (&x)[16], u64* __restrict__ dst_t, int g, u64* S,
+                                               const u64* __restrict__ tw, const u64* __restrict__ tws, u64 p) {
+  const RowMap mt = map_t(), mn = map_n();
+  row_xchg<true, false>(x, S, mn, mn);
+  wrow_inv_hi(x, g + 16 * mn.rb, mn.j, tw, tws, p);
+  row_xchg<false, true>(x, S, mn, mt);
+  wrow_inv_lo(x, g + 16 * mt.rb, tw, tws, p);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) dst_t[ws_a(g, k)] = x[k];
+}
+
+// ----------------------------------------------------------------- K1: INTT rows of d
+__global__ __launch_bounds__(kT) void wf_intt_rows(const u64* __restrict__ d, long long d_stride, const WGalF G,
+                                                   u64* __restrict__ t1, int limbs, int batch, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const TileId id = decode_tile(batch, blockIdx.x);
+  if (id.tile >= 16 * limbs) return;
+  const int i = id.tile >> 4, rg = id.tile & 15, b = id.b;
+  const u64 p = T.p[i];
+  u64 x[16];
+  load_gal_raw(x, d + (long long)b * d_stride + (long long)i * kN, nat_a(rg), gal_of(G, b));
+  wrows_inv_to_t(x, t1 + ((long long)b * limbs + i) * kN, rg, S, T.inv + (size_t)i * kN, T.inv_s + (size_t)i * kN, p);
+}
+
+// ----------------------------------------------------------------- K2 / K4: cols + conversion
+// Block: columns (c0, c0 + 1) of conversion group y (a ModUp digit, or a ModDown component) of item z;
+// 16 slots of 16 threads.  Phase 1: slot sigma = (source sigma >> 1, column sigma & 1) runs the INTT
+// column stages of its source column and leaves the centered residue's digit word in run sigma of D.
+// Phase 2 (as ksfused.hip's cols_mconv_body): wave w takes column w >> 1 and half w & 1 of each pass's
+// 8 mi targets; quarter g owns mi (<= kMItems) of them, MFMA rows 4g + r; a lane supplies A row j (the
+// digit bytes of sources 2g, 2g + 1 for target ta(j)) and B column j (the digit words of coefficient
+// j + 16k), and receives rows 4g + r at column j: rows j + 16k of its targets over the 16 tiles, the
+// forward column pass's layout A.  SEPX keeps separate exchange runs (X) so that D serves every pass.
+struct WConvArgs {
+  const u64* src;
+  long long src_zs, src_ys;
+  int src_off_y;
+  u64* dst;
+  long long dst_zs, dst_ys;
+  const WideConv* cc_base;
+  int cc_y;
+};
+
+template <bool SEPX>
+__global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTables T, const wv4i* __restrict__ dig) {
+  __shared__ u64 D[16 * kYStride];
+  __shared__ u64 X[SEPX ? 16 * kYStride : 1];
+  const int y = blockIdx.y;
+  const long long z = blockIdx.z;
+  const WideConv& C = A.cc_base[y * A.cc_y];
+  const int ns = C.ns, nt = C.nt;
+  const int t = threadIdx.x, sigma = t >> 4, j = t & 15;
+  const int c0 = blockIdx.x * 2;
+  // phase 1
+  {
+    const int s = sigma >> 1, cl = sigma & 1;
+    const bool act = s < ns;
+    const int sp = C.src_prime[act ? s : 0];
+    const u64 p = T.p[sp];
+    const u64* __restrict__ tw = T.inv + (size_t)sp * kN;
+    const u64* __restrict__ tws = T.inv_s + (size_t)sp * kN;
+    u64 x[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = 0;
+    if (act) {
+      const u64* col = A.src + z * A.src_zs + y * A.src_ys + (long long)(y * A.src_off_y + s) * kN +
+                       (long long)(c0 + cl) * 16;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) x[k] = col[4096 * k + j];  // rows 16 j + k: wpos = 4096 k + 16 c + j
+      wcol_inv_hi(x, j, tw, tws, p);
+    }
+    u64* R = D + sigma * kYStride;
+    col_b_to_a(x, R, j);
+    if (act) wcol_inv_lo(x, tw, tws, C.inv_n0[s], C.inv_n0_s[s], C.inv_n1[s], C.inv_n1_s[s], p);
+    // an idle source stores zero digits
+#pragma unroll
+    for (int k = 0; k < 16; ++k) R[j + 16 * k] = act ? wdigits(x[k], p) : 0ULL;
+  }
+  __syncthreads();
+  // phase 2
+  const int w = t >> 6, g = (t >> 4) & 3;
+  const int cl = w >> 1, h = w & 1;
+  const u64* B0 = D + (4 * g + cl) * kYStride + j;      // source 2 g, column cl
+  const u64* B1 = D + (4 * g + 2 + cl) * kYStride + j;  // source 2 g + 1
+  u64* RX = (SEPX ? X : D) + sigma * kYStride;
+  u64* dbase = A.dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
+  const wv4i* __restrict__ tab = dig + C.dig_off;
+  for (int base = 0; base < nt;) {
+    // mi targets per quarter in this pass (at most kMItems): the last pass spreads what is left over
+    // every quarter, so that no wave idles while another folds three targets
+    const int mi = min(kMItems, (nt - base + 7) / 8);
+    // constants of MFMA row j: target of quarter j >> 2, item j & 3
+    const int ta = base + (4 * h + (j >> 2)) * mi + (j & 3);
+    const bool arow = (j & 3) < mi && ta < nt;
+    wv4i av[8];
+#pragma unroll
+    for (int c = 0; c < 8; ++c) av[c] = arow ? tab[((ta >> 4) * 8 + c) * 64 + 16 * g + (ta & 15)] : wv4i{0, 0, 0, 0};
+    int to[kMItems], tp[kMItems], ts[kMItems];
+    u64 pr[kMItems];
+    double tinv[kMItems];
+#pragma unroll
+    for (int r = 0; r < kMItems; ++r) {
+      to[r] = r < mi ? base + (4 * h + g) * mi + r : nt;
+      const int tt = to[r] < nt ? to[r] : 0;
+      tp[r] = C.dst_prime[tt];
+      ts[r] = C.dst_slot[tt];
+      pr[r] = T.p[tp[r]];
+      tinv[r] = C.fold_inv[tt];
+    }
+    u64 x[kMItems][16];
+    uint64_t w0 = B0[0], w1 = B1[0];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const wv4i bv = {(int)(uint32_t)w0, (int)(uint32_t)(w0 >> 32), (int)(uint32_t)w1, (int)(uint32_t)(w1 >> 32)};
+      wv4i acc[8];
+#pragma unroll
+      for (int c = 0; c < 8; ++c) acc[c] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[c], bv, wv4i{0, 0, 0, 0}, 0, 0, 0);
+      if (k < 15) {  // the next tile's digit words are read while this tile's sums are folded
+        w0 = B0[16 * (k + 1)];
+        w1 = B1[16 * (k + 1)];
+      }
+#pragma unroll
+      for (int r = 0; r < kMItems; ++r) {
+        x[r][k] = r < mi ? wfold(acc, r, pr[r], tinv[r]) : 0;
+        asm volatile("" : "+v"(x[r][k]));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (!SEPX) __syncthreads();  // every wave is done reading D before its runs become exchange buffers
+#pragma unroll
+    for (int r = 0; r < kMItems; ++r) {
+      if (r >= mi) break;  // uniform over the block
+      const bool act = to[r] < nt;
+      const u64* __restrict__ tw = T.fwd + (size_t)tp[r] * kN;
+      const u64* __restrict__ tws = T.fwd_s + (size_t)tp[r] * kN;
+      if (act) wcol_fwd_lo(x[r], tw, tws, pr[r]);
+      col_a_to_b(x[r], RX, j);
+      if (act) {
+        wcol_fwd_hi(x[r], j, tw, tws, pr[r]);
+        u64* col = dbase + (long long)ts[r] * kN;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) col[4096 * k + j] = x[r][k];
+      }
+    }
+    base += 8 * mi;
+  }
+}
+
+// ----------------------------------------------------------------- inner product of one tile
+// sb / sa = sum_j x_j key_j[comp] mod p over the digits j of item b, extended limb e (prime pi), row
+// group rg: x_j the NTT rows pass of T2 digit j (below 4p), or, for the digit that holds limb e, d
+// itself read through sigma_g.  Montgomery products summed below 2p, then one product by 2^64 mod p:
+// canonical results.
+struct WIp {
+  const u64* d;
+  long long d_stride;
+  const u64* t2;
+  const u64* key;
+  int ell, beta, L, K, alpha, beta_max;
+};
+
+__device__ __forceinline__ void wtile_ip(u64 (&sb)[16], u64 (&sa)[16], u64 (&x)[16], const WIp& I, int b, int e,
+                                         int pi, int rg, uint32_t g, u64* S, const u64* __restrict__ tw,
+                                         const u64* __restrict__ tws, const WideTables& T) {
+  const u64 p = T.p[pi], p2 = 2 * p, mneg = T.mneg[pi];
+  const int ext_l = I.ell + I.K;
+  const long long comp = (long long)I.beta_max * (I.L + I.K) * kN;
+  const int own = e < I.ell ? e / I.alpha : -1;
+  const long long na = nat_a(rg);
+  const u64* t2b = I.t2 + ((long long)b * I.beta * ext_l + e) * kN;
+  // one key component at a time: the 16 words of the other are not live across the products
+  auto mac = [&](u64 (&acc)[16], const u64* __restrict__ kp) {
+    u64 kw[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) kw[k] = kp[16 * k];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const u64 v = acc[k] + wmont(x[k], kw[k], p, mneg);  // below 4p
+      acc[k] = v >= p2 ? v - p2 : v;
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sb[k] = sa[k] = 0;
+  for (int jd = 0; jd < I.beta; ++jd) {
+    if (jd == own) {
+      load_gal_raw(x, I.d + (long long)b * I.d_stride + (long long)e * kN, na, g);
+    } else {
+      load_t(x, t2b + (long long)jd * ext_l * kN, rg);
+      wrows_fwd_t(x, rg, S, tw, tws, p);
+    }
+    const u64* kp = I.key + ((long long)jd * (I.L + I.K) + pi) * kN + na;
+    mac(sb, kp);
+    mac(sa, kp + comp);
+  }
+  const u64 r = T.r64[pi], rs = T.r64_s[pi];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    sb[k] = wmulc(sb[k], r, rs, p);
+    sa[k] = wmulc(sa[k], r, rs, p);
+  }
+}
+
+// ----------------------------------------------------------------- K3: inner product, P limbs / ext
+// Tile = (row group, extended limb e0 + tile / 16).  Without ext_b the kernel covers the K special
+// limbs (e0 = ell) and runs the inner product's INTT rows pass into ACCP ([item][2][K], workspace
+// layout) for the ModDown conversion.  With ext_b it covers every extended limb (e0 = 0) and ends the
+// key switch in the extended basis: (P sigma(add) + IP_b, IP_a) (+ acc) over Q u P, natural layout.
+__global__ __launch_bounds__(kT, 2) void wf_rows_ip(const WIp I, const WGalF G, WKeysF keys, int batch, int tiles,
+                                                    int e0, u64* __restrict__ accp, const u64* __restrict__ add,
+                                                    long long add_stride, u64* ext_b, u64* ext_a, long long ext_stride,
+                                                    const u64* acc_b, const u64* acc_a, long long acc_stride,
+                                                    WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const TileId id = decode_tile(batch, blockIdx.x);
+  if (id.tile >= tiles) return;
+  const int b = id.b, e = e0 + (id.tile >> 4), rg = id.tile & 15;
+  const uint32_t g = gal_of(G, b);
+  const int pi = e < I.ell ? e : I.L + (e - I.ell);
+  const u64 p = T.p[pi];
+  WIp Ib = I;
+  Ib.key = keys.k[b];
+  u64 sb[16], sa[16], x[16];
+  wtile_ip(sb, sa, x, Ib, b, e, pi, rg, g, S, T.fwd + (size_t)pi * kN, T.fwd_s + (size_t)pi * kN, T);
+  const long long na = nat_a(rg);
+  if (ext_b) {
+    if (e < I.ell && add) {
+      load_gal_raw(x, add + (long long)b * add_stride + (long long)e * kN, na, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sb[k] = wadd(sb[k], wmulc(x[k], T.pmod[pi], T.pmod_s[pi], p), p);
+    }
+    if (acc_b) {
+      // read before the store below by the same thread: ext may alias acc
+      const u64* ab = acc_b + (long long)b * acc_stride + (long long)e * kN + na;
+      const u64* aa = acc_a + (long long)b * acc_stride + (long long)e * kN + na;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        sb[k] = wadd(sb[k], ab[16 * k], p);
+        sa[k] = wadd(sa[k], aa[16 * k], p);
+      }
+    }
+    u64* ob = ext_b + (long long)b * ext_stride + (long long)e * kN + na;
+    u64* oa = ext_a + (long long)b * ext_stride + (long long)e * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      ob[16 * k] = sb[k];
+      oa[16 * k] = sa[k];
+    }
+    return;
+  }
+  const int K = I.K;
+  u64* o = accp + ((long long)b * 2 * K + (e - e0)) * kN;
+  const u64* twi = T.inv + (size_t)pi * kN;
+  const u64* twis = T.inv_s + (size_t)pi * kN;
+  wrows_inv_to_t(sb, o, rg, S, twi, twis, p);
+  wrows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, twis, p);
+}
+
+// ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
+// out_b = (IP_b - v_b) P^-1 + sigma_g(add) (+ acc_b),  out_a = (IP_a - v_a) P^-1 (+ acc_a),
+// v = the NTT rows pass of the ModDown conversion T4 ([item][2][ell], workspace layout; below 4p).
+__global__ __launch_bounds__(kT, 2) void wf_rows_ipq(const WIp I, const WGalF G, WKeysF keys, int batch,
+                                                     const u64* __restrict__ t4, const u64* __restrict__ add,
+                                                     long long add_stride, const u64* __restrict__ acc_b,
+                                                     const u64* __restrict__ acc_a, long long acc_stride,
+                                                     u64* __restrict__ out_b, u64* __restrict__ out_a,
+                                                     long long out_stride, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  __shared__ u64 Park[16 * kT];  // sa while sb is finished (keeps both out of the registers at once)
+  const int ell = I.ell;
+  const TileId id = decode_tile(batch, blockIdx.x);
+  if (id.tile >= 16 * ell) return;
+  const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
+  const uint32_t g = gal_of(G, b);
+  const u64 p = T.p[i];
+  const u64* tw = T.fwd + (size_t)i * kN;
+  const u64* tws = T.fwd_s + (size_t)i * kN;
+  WIp Ib = I;
+  Ib.key = keys.k[b];
+  u64 sb[16], sa[16], x[16];
+  wtile_ip(sb, sa, x, Ib, b, i, i, rg, g, S, tw, tws, T);
+  const long long na = nat_a(rg);
+  const u64 pv = T.pinv[i], pvs = T.pinv_s[i];
+  auto finish = [&](u64 (&s)[16], int comp, const u64* addend, const u64* ac, u64* out) {
+    load_t(x, t4 + ((long long)b * 2 * ell + (long long)comp * ell + i) * kN, rg);
+    wrows_fwd_t(x, rg, S, tw, tws, p);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s[k] = wcanon2(mulshoup_lazy(s[k] + 4 * p - x[k], pv, pvs, p), p);  // v < 4p
+    if (addend) {
+      load_gal_raw(x, addend + (long long)b * add_stride + (long long)i * kN, na, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k] = wadd(s[k], x[k], p);
+    }
+    if (ac) {
+      const u64* a = ac + (long long)b * acc_stride + (long long)i * kN + na;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k] = wadd(s[k], a[16 * k], p);
+    }
+    u64* o = out + (long long)b * out_stride + (long long)i * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o[16 * k] = s[k];
+  };
+#pragma unroll
+  for (int k = 0; k < 16; ++k) Park[k * kT + threadIdx.x] = sa[k];
+  finish(sb, 0, add, acc_b, out_b);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sa[k] = Park[k * kT + threadIdx.x];
+  finish(sa, 1, nullptr, acc_a, out_a);
+}
+
+void launch_wconv_fused(const WConvArgs& A, int nt_max, dim3 grid, const WideState& W, hipStream_t s) {
+  auto k = nt_max <= kMPass ? wf_cols_mconv<false> : wf_cols_mconv<true>;
+  k<<<grid, kT, 0, s>>>(A, W.t, (const wv4i*)W.conv_dig);
+}
+
+}  // namespace
+
+bool wide_fused_ok(const hck_context* c) {
+  return c->wide && c->conv_engine == 1 && c->wide->conv_dig && c->alpha <= kMaxAlpha && c->K <= kMaxSpecial;
+}
+
+size_t wide_fused_bytes(const hck_context* c, int ell, int batch) {
+  const size_t nb = (size_t)std::min(batch, kItems), beta = beta_of(c, ell), ext_l = (size_t)(ell + c->K);
+  return nb * kN * 8 * (2 * (size_t)ell + beta * ext_l + 2 * (size_t)c->K);
+}
+
+int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride, uint32_t galois,
+                  const uint64_t* const* ksk, const uint64_t* add, long long add_stride, const uint64_t* acc_b,
+                  const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
+                  long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
+                  long long ext_stride, const uint32_t* galois_items) {
+  if (!wide_fused_ok(c)) return HCK_ERR_UNSUPPORTED;
+  const WideState& W = *c->wide;
+  const int K = c->K, L = c->L, alpha = c->alpha, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const long long n = kN;
+  const int last_digit = ell - alpha * (beta - 1);
+  for (int b0 = 0; b0 < batch; b0 += kItems) {
+    const int nb = std::min(kItems, batch - b0);
+    WGalF G{};
+    G.per_item = galois_items ? 1 : 0;
+    G.uniform = galois;
+    if (galois_items)
+      for (int b = 0; b < nb; ++b) G.g[b] = galois_items[b0 + b];
+    WKeysF kp{};
+    for (int b = 0; b < nb; ++b) kp.k[b] = ksk[b0 + b];
+    const uint64_t* dd = d + (long long)b0 * d_stride;
+    const uint64_t* a0 = add ? add + (long long)b0 * add_stride : nullptr;
+    u64* r1 = (u64*)ws;  // T1 [nb][ell], later T4 [nb][2][ell]
+    u64* t2 = r1 + (long long)nb * 2 * ell * n;
+    u64* accp = t2 + (long long)nb * beta * ext_l * n;
+    const WIp I{dd, d_stride, t2, nullptr, ell, beta, L, K, alpha, bmax};
+    // K1
+    wf_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * nb), kT, 0, s>>>(dd, d_stride, G, r1, ell, nb, W.t);
+    HCK_CHECK_LAUNCH();
+    // K2: ModUp, one block per (column pair, digit, item)
+    launch_wconv_fused(WConvArgs{r1, (long long)ell * n, 0, alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                                 W.modup + (size_t)ell * bmax, 1},
+                       ext_l - last_digit, dim3(128, beta, nb), W, s);
+    HCK_CHECK_LAUNCH();
+    if (ext_b) {
+      const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
+      const long long ai = (long long)b0 * acc_stride, ei = (long long)b0 * ext_stride;
+      wf_rows_ip<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, tiles, 0, nullptr, a0, add_stride, ext_b + ei,
+                                                          ext_a + ei, ext_stride, acc_b ? acc_b + ai : nullptr,
+                                                          acc_a ? acc_a + ai : nullptr, acc_stride, W.t);
+      HCK_CHECK_LAUNCH();
+      continue;
+    }
+    // K3 over the K special limbs
+    {
+      const int tiles = 16 * K, groups = (tiles + kXcds - 1) / kXcds;
+      wf_rows_ip<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, tiles, ell, accp, nullptr, 0, nullptr, nullptr,
+                                                          0, nullptr, nullptr, 0, W.t);
+      HCK_CHECK_LAUNCH();
+    }
+    // K4: ModDown conversion, one block per (column pair, component, item); T4 reuses R1
+    u64* t4 = r1;
+    launch_wconv_fused(WConvArgs{accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n, (long long)ell * n,
+                                 W.moddown + ell, 0},
+                       ell, dim3(128, 2, nb), W, s);
+    HCK_CHECK_LAUNCH();
+    // K5: Q limbs
+    {
+      const int tiles = 16 * ell, groups = (tiles + kXcds - 1) / kXcds;
+      const long long ai = (long long)b0 * acc_stride, oi = (long long)b0 * out_stride;
+      wf_rows_ipq<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, t4, a0, add_stride,
+                                                           acc_b ? acc_b + ai : nullptr, acc_a ? acc_a + ai : nullptr,
+                                                           acc_stride, out_b + oi, out_a + oi, out_stride, W.t);
+      HCK_CHECK_LAUNCH();
+    }
+  }
+  return HCK_OK;
+}
+
+}  // namespace hck
