@@ -531,20 +531,21 @@ __global__ __launch_bounds__(256) void wk_ks_ip_h(const u64* __restrict__ digits
   const uint32_t ex = ((2u * wbrv16(k) + 1u) * g) & (2u * kN - 1u);
   const uint32_t src = wbrv16((ex - 1u) >> 1);
   const int pi = e < ell ? e : L + (e - ell);
-  const Barrett64 br = wbar(T, pi);
+  const u64 p = T.p[pi], p2 = 2 * p, mneg = T.mneg[pi];
   const u64* key = keys.k[it];
   const long long comp = (long long)beta_max * (L + K) * kN;
   const u64* dg = digits + (in * beta * ext_l + e) * (long long)kN + src;
-  u64 ab = 0, aa = 0;
+  u64 ab = 0, aa = 0;  // Montgomery products summed below 2p, then one product by 2^64 mod p
   for (int j = 0; j < beta; ++j) {
     const u64 x = dg[(long long)j * ext_l * kN];
     const long long ko = ((long long)j * (L + K) + pi) * kN + k;
-    ab = wadd(ab, mulmod64(x, key[ko], br), br.p);
-    aa = wadd(aa, mulmod64(x, key[comp + ko], br), br.p);
+    const u64 vb = ab + wmont(x, key[ko], p, mneg), va = aa + wmont(x, key[comp + ko], p, mneg);
+    ab = vb >= p2 ? vb - p2 : vb;
+    aa = va >= p2 ? va - p2 : va;
   }
   u64* o = acc + it * acc_item + (long long)e * kN + k;
-  o[0] = ab;
-  o[(long long)ext_l * kN] = aa;
+  o[0] = wmulc(ab, T.r64[pi], T.r64_s[pi], p);
+  o[(long long)ext_l * kN] = wmulc(aa, T.r64[pi], T.r64_s[pi], p);
 }
 
 // sigma of every limb of input (first + it) % inputs by G.g[it].  Grid (N / 256, limbs, items).
@@ -656,24 +657,88 @@ struct WMac {
   const u64* c1[kWMaxBabies];
 };
 
-// res[c][g][i][l][k] = sum_b pts[g B + b][l][k] * baby_b[c][i][l][k] (mod q_l).  Grid (N / 256, limbs, giants * inputs).
-__global__ __launch_bounds__(256) void wk_bsgs_mac(const WMac P, long long baby_stride, const u64* __restrict__ pts,
-                                                   long long pt_stride, u64* __restrict__ res, int inputs, int babies,
-                                                   int giants, int limbs, WPrimeMap pm, WideTables T) {
-  const int k = blockIdx.x * 256 + threadIdx.x;
-  const int l = blockIdx.y;
-  const int g = blockIdx.z / inputs, i = blockIdx.z % inputs;
-  const Barrett64 br = wbar(T, pm.prime[l]);
-  const long long lo = (long long)l * kN + k;
-  u64 acc0 = 0, acc1 = 0;
-  for (int b = 0; b < babies; ++b) {
-    const u64 w = pts[(long long)(g * babies + b) * pt_stride + lo];
-    acc0 = wadd(acc0, mulmod64(P.c0[b][(long long)i * baby_stride + lo], w, br), br.p);
-    acc1 = wadd(acc1, mulmod64(P.c1[b][(long long)i * baby_stride + lo], w, br), br.p);
+// res[c][g][i][l][k] = sum_b pts[g B + b][l][k] * baby_b[c][i][l][k] (mod q_l), the FP64 MAC's tiling
+// (bsgs.hip: k_bsgs_mac): a thread owns one coefficient of one limb and a kWTI x kWTG tile of (input,
+// giant) accumulators for both components; per baby step it reads kWTG plaintext words and 2 kWTI baby
+// words for 2 kWTI kWTG products (the next step's words are in flight while the current one computes).
+// Products are Montgomery products (canonical operands: below 2p each), summed below 2p, and brought
+// back by one product with 2^64 mod p: canonical results.  All tiles of one (limb, 128-coefficient)
+// unit are dealt to one XCD, so the unit's plaintext and baby words come from HBM once.
+constexpr int kWMacThreads = 128;
+constexpr int kWTI = 4;
+constexpr int kWTG = 4;
+
+struct WMacOps {
+  u64 w[kWTG], x0[kWTI], x1[kWTI];
+};
+
+__device__ __forceinline__ void wmac_load(WMacOps& o, const WMac& P, int b, int babies, int G, int ni, int g0,
+                                          int i0, const u64* __restrict__ pts, long long pt_stride,
+                                          long long baby_stride, long long ln) {
+#pragma unroll
+  for (int g = 0; g < kWTG; ++g) {
+    const int gg = g0 + g < G ? g0 + g : g0;  // clamped rows are computed but never stored
+    o.w[g] = pts[((long long)gg * babies + b) * pt_stride + ln];
   }
-  const long long off = ((long long)g * inputs + i) * limbs * kN + lo;
-  res[off] = acc0;
-  res[(long long)giants * inputs * limbs * kN + off] = acc1;
+#pragma unroll
+  for (int t = 0; t < kWTI; ++t) {
+    const int ii = i0 + t < ni ? i0 + t : i0;
+    o.x0[t] = P.c0[b][(long long)ii * baby_stride + ln];
+    o.x1[t] = P.c1[b][(long long)ii * baby_stride + ln];
+  }
+}
+
+__global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long long baby_stride,
+                                                            const u64* __restrict__ pts, long long pt_stride,
+                                                            u64* __restrict__ res, int inputs, int babies, int giants,
+                                                            int limbs, WPrimeMap pm, int units_per_limb, int tiles_i,
+                                                            int tiles_g, int total_units, WideTables T) {
+  const int tiles = tiles_i * tiles_g;
+  const int lin = blockIdx.x;
+  const int xcd = lin % kXcds, q = lin / kXcds;
+  const int unit = (q / tiles) * kXcds + xcd;
+  const int tile = q % tiles;
+  if (unit >= total_units) return;
+  const int l = unit / units_per_limb;
+  const int n = (unit % units_per_limb) * kWMacThreads + threadIdx.x;
+  const int i0 = (tile % tiles_i) * kWTI, g0 = (tile / tiles_i) * kWTG;
+  const int pi = pm.prime[l];
+  const u64 p = T.p[pi], p2 = 2 * p, mneg = T.mneg[pi];
+  const long long ln = (long long)l * kN + n;
+  u64 acc[kWTI][2][kWTG];
+#pragma unroll
+  for (int t = 0; t < kWTI; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < kWTG; ++g) acc[t][c][g] = 0;
+  WMacOps cur, nxt;
+  wmac_load(cur, P, 0, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+  for (int b = 0; b < babies; ++b) {
+    if (b + 1 < babies) wmac_load(nxt, P, b + 1, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+#pragma unroll
+    for (int t = 0; t < kWTI; ++t)
+#pragma unroll
+      for (int g = 0; g < kWTG; ++g) {
+        const u64 v0 = acc[t][0][g] + wmont(cur.x0[t], cur.w[g], p, mneg);
+        const u64 v1 = acc[t][1][g] + wmont(cur.x1[t], cur.w[g], p, mneg);
+        acc[t][0][g] = v0 >= p2 ? v0 - p2 : v0;
+        acc[t][1][g] = v1 >= p2 ? v1 - p2 : v1;
+      }
+    cur = nxt;
+  }
+  const u64 r = T.r64[pi], rs = T.r64_s[pi];
+  const long long is = (long long)limbs * kN, gs = (long long)inputs * is, cs = (long long)giants * gs;
+#pragma unroll
+  for (int t = 0; t < kWTI; ++t) {
+    if (i0 + t >= inputs) break;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < kWTG; ++g)
+        if (g0 + g < giants)
+          res[c * cs + (long long)(g0 + g) * gs + (long long)(i0 + t) * is + ln] = wmulc(acc[t][c][g], r, rs, p);
+  }
 }
 
 // ---------------------------------------------------------------------------------------- encode
@@ -1429,7 +1494,7 @@ int wide_lincomb(const hck_context* c, int limbs, int groups, int terms, const u
 int wide_bsgs_mac(const hck_context* c, int limbs, const int* prime_idx, int inputs, int babies, int giants,
                   const uint64_t* const* baby_c0, const uint64_t* const* baby_c1, long long baby_stride,
                   const uint64_t* pts, long long pt_stride, uint64_t* res, hipStream_t s) {
-  if (babies > kWMaxBabies || (long long)giants * inputs > 65535) return HCK_ERR_ARG;
+  if (babies > kWMaxBabies) return HCK_ERR_ARG;
   WMac P{};
   for (int b = 0; b < babies; ++b) {
     if (!baby_c0[b] || !baby_c1[b]) return HCK_ERR_ARG;
@@ -1438,8 +1503,15 @@ int wide_bsgs_mac(const hck_context* c, int limbs, const int* prime_idx, int inp
   }
   WPrimeMap pm{};
   for (int l = 0; l < limbs; ++l) pm.prime[l] = (uint8_t)prime_idx[l];
-  wk_bsgs_mac<<<dim3(kN / 256, limbs, giants * inputs), 256, 0, s>>>(P, baby_stride, pts, pt_stride, res, inputs,
-                                                                     babies, giants, limbs, pm, c->wide->t);
+  const int units_per_limb = kN / kWMacThreads;
+  const int total_units = limbs * units_per_limb;
+  const int tiles_i = (inputs + kWTI - 1) / kWTI, tiles_g = (giants + kWTG - 1) / kWTG;
+  const long long units_padded = ((long long)total_units + kXcds - 1) / kXcds * kXcds;
+  const long long blocks = units_padded * tiles_i * tiles_g;
+  if (blocks > 0x7fffffffLL) return HCK_ERR_ARG;
+  wk_bsgs_mac<<<dim3((unsigned)blocks), kWMacThreads, 0, s>>>(P, baby_stride, pts, pt_stride, res, inputs, babies,
+                                                             giants, limbs, pm, units_per_limb, tiles_i, tiles_g,
+                                                             total_units, c->wide->t);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }

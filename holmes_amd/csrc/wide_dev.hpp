@@ -21,6 +21,16 @@ __device__ __forceinline__ uint64_t wmulc(uint64_t a, uint64_t w, uint64_t ws, u
 }
 __device__ __forceinline__ Barrett64 wbar(const WideTables& T, int pi) { return Barrett64{T.p[pi], T.mu[pi], T.w[pi]}; }
 
+// x k 2^-64 mod p below 2p, for x k < 2^64 p (Montgomery; mneg = -p^-1 mod 2^64): t + m p is a
+// multiple of 2^64 for m = t mneg, and its low words add up to 2^64 exactly when t's low word is not 0.
+// Sums of such products are brought back by one product with 2^64 mod p (WideTables::r64).
+__device__ __forceinline__ uint64_t wmont(uint64_t x, uint64_t k, uint64_t p, uint64_t mneg) {
+  const u128_t t = (u128_t)x * k;
+  const uint64_t tl = (uint64_t)t, th = (uint64_t)(t >> 64);
+  const uint64_t m = tl * mneg;
+  return th + (uint64_t)(((u128_t)m * p) >> 64) + (tl != 0 ? 1 : 0);
+}
+
 // The int8 matrix-core base conversion's operands and fold (wide.hip: wk_mconv, wide_fused.hip).
 // Each source residue is centered (|ybar| < b / 2 < 2^60) and written as the 64-bit word of its eight
 // balanced base-256 digits (byte a = d_a + 128 of ybar + 0x80..80; the XOR turns each byte into d_a as

@@ -69,15 +69,6 @@ __device__ __forceinline__ void w_gs(u64& u, u64& v, u64 w, u64 ws, u64 p, u64 p
 __device__ __forceinline__ u64 wcanon2(u64 x, u64 p) { return x >= p ? x - p : x; }         // x < 2p
 __device__ __forceinline__ u64 wcanon4(u64 x, u64 p) { return wcanon2(x >= 2 * p ? x - 2 * p : x, p); }  // x < 4p
 
-// x k 2^-64 mod p below 2p, for x k < 2^64 p (Montgomery; mneg = -p^-1 mod 2^64): t + m p is a
-// multiple of 2^64 for m = t mneg, and its low words add up to 2^64 exactly when t's low word is not 0.
-__device__ __forceinline__ u64 wmont(u64 x, u64 k, u64 p, u64 mneg) {
-  const u128_t t = (u128_t)x * k;
-  const u64 tl = (u64)t, th = (u64)(t >> 64);
-  const u64 m = tl * mneg;
-  return th + (u64)(((u128_t)m * p) >> 64) + (tl != 0 ? 1 : 0);
-}
-
 // ----------------------------------------------------------------- column transforms (16-thread slots)
 // Root indices as in ksfused.hip: stage l of a column pairs rows 128 >> l apart; layout A holds rows
 // j + 16k (group k >> (4 - l)), layout B rows 16j + k (group (j << (l - 4)) + (k >> (8 - l))).
