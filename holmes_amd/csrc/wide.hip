@@ -133,6 +133,44 @@ __device__ __forceinline__ void winv16(u64 (&x)[16], const u64* tw, const u64* t
   }
 }
 
+// The same stages on lazy words (Harvey): forward butterflies take and return words below 4p, inverse
+// ones below 2p (Shoup's lazy products lie below 2p for any 64-bit input; 4p < 2^63).  The NTT kernels
+// below run on them and canonicalise what they store, so that their outputs stay canonical.
+template <typename Root>
+__device__ __forceinline__ void wfwd16_lazy(u64 (&x)[16], const u64* tw, const u64* tws, u64 p, Root root) {
+  const u64 p2 = 2 * p;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d = 8 >> s;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u & d) continue;
+      const int wi = root(s, u);
+      const u64 a = x[u] >= p2 ? x[u] - p2 : x[u];
+      const u64 y = mulshoup_lazy(x[u + d], tw[wi], tws[wi], p);
+      x[u] = a + y;
+      x[u + d] = a - y + p2;
+    }
+  }
+}
+
+template <typename Root>
+__device__ __forceinline__ void winv16_lazy(u64 (&x)[16], const u64* tw, const u64* tws, u64 p, Root root) {
+  const u64 p2 = 2 * p;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int d = 1 << s;
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      if (u & d) continue;
+      const int wi = root(s, u);
+      const u64 a = x[u], b = x[u + d], t = a + b;
+      x[u] = t >= p2 ? t - p2 : t;
+      x[u + d] = mulshoup_lazy(a - b + p2, tw[wi], tws[wi], p);
+    }
+  }
+}
+
 __global__ __launch_bounds__(kWT) void wk_fwd_cols(const u64* src, u64* dst, long long ss,
                                                    long long ds, LimbList list, WideTables T) {
   __shared__ u64 sh[256 * kWPad];
@@ -149,7 +187,7 @@ __global__ __launch_bounds__(kWT) void wk_fwd_cols(const u64* src, u64* dst, lon
   // rows r + 16 u of column c: stages 0..3 (row distances 128 .. 16), root (1 << s) + (u >> (4 - s))
 #pragma unroll
   for (int u = 0; u < 16; ++u) x[u] = in[c + 256 * (r + 16 * u)];
-  wfwd16(x, tw, tws, p, [](int s, int u) { return (1 << s) + (u >> (4 - s)); });
+  wfwd16_lazy(x, tw, tws, p, [](int s, int u) { return (1 << s) + (u >> (4 - s)); });
 #pragma unroll
   for (int u = 0; u < 16; ++u) sh[(r + 16 * u) * kWPad + cl] = x[u];
   __syncthreads();
@@ -157,9 +195,9 @@ __global__ __launch_bounds__(kWT) void wk_fwd_cols(const u64* src, u64* dst, lon
   const int q = r;
 #pragma unroll
   for (int m = 0; m < 16; ++m) x[m] = sh[(16 * q + m) * kWPad + cl];
-  wfwd16(x, tw, tws, p, [q](int s, int m) { return (16 << s) + ((16 * q + m) >> (4 - s)); });
+  wfwd16_lazy(x, tw, tws, p, [q](int s, int m) { return (16 << s) + ((16 * q + m) >> (4 - s)); });
 #pragma unroll
-  for (int m = 0; m < 16; ++m) out[c + 256 * (16 * q + m)] = x[m];
+  for (int m = 0; m < 16; ++m) out[c + 256 * (16 * q + m)] = wcanon4(x[m], p);
 }
 
 __global__ __launch_bounds__(kWT) void wk_fwd_rows(u64* __restrict__ dst, long long ds, LimbList list, WideTables T) {
@@ -178,7 +216,7 @@ __global__ __launch_bounds__(kWT) void wk_fwd_rows(u64* __restrict__ dst, long l
   // root (256 << s) + r (1 << s) + (u >> (4 - s))
 #pragma unroll
   for (int u = 0; u < 16; ++u) x[u] = io[rr * 256 + lane + 16 * u];
-  wfwd16(x, tw, tws, p, [r](int s, int u) { return (256 << s) + (r << s) + (u >> (4 - s)); });
+  wfwd16_lazy(x, tw, tws, p, [r](int s, int u) { return (256 << s) + (r << s) + (u >> (4 - s)); });
 #pragma unroll
   for (int u = 0; u < 16; ++u) row[wpad(lane + 16 * u)] = x[u];
   __syncthreads();
@@ -187,9 +225,9 @@ __global__ __launch_bounds__(kWT) void wk_fwd_rows(u64* __restrict__ dst, long l
   const int q = lane;
 #pragma unroll
   for (int m = 0; m < 16; ++m) x[m] = row[wpad(16 * q + m)];
-  wfwd16(x, tw, tws, p, [r, q](int s, int m) { return (4096 << s) + (r << (4 + s)) + ((16 * q + m) >> (4 - s)); });
+  wfwd16_lazy(x, tw, tws, p, [r, q](int s, int m) { return (4096 << s) + (r << (4 + s)) + ((16 * q + m) >> (4 - s)); });
 #pragma unroll
-  for (int m = 0; m < 16; ++m) row[wpad(16 * q + m)] = x[m];
+  for (int m = 0; m < 16; ++m) row[wpad(16 * q + m)] = wcanon4(x[m], p);
   __syncthreads();
 #pragma unroll
   for (int u = 0; u < 16; ++u) io[rr * 256 + lane + 16 * u] = row[wpad(lane + 16 * u)];
@@ -219,16 +257,16 @@ __global__ __launch_bounds__(kWT) void wk_inv_rows(const u64* src, u64* dst, lon
   const int q = lane;
 #pragma unroll
   for (int m = 0; m < 16; ++m) x[m] = row[wpad(16 * q + m)];
-  winv16(x, tw, tws, p, [r, q](int s, int m) { return (32768 >> s) + r * (128 >> s) + ((16 * q + m) >> (s + 1)); });
+  winv16_lazy(x, tw, tws, p, [r, q](int s, int m) { return (32768 >> s) + r * (128 >> s) + ((16 * q + m) >> (s + 1)); });
 #pragma unroll
   for (int m = 0; m < 16; ++m) row[wpad(16 * q + m)] = x[m];
   __syncthreads();
   // elements lane + 16 u: stages 4..7 (distances 16 .. 128), root (2048 >> s) + r (8 >> s) + (u >> (s + 1))
 #pragma unroll
   for (int u = 0; u < 16; ++u) x[u] = row[wpad(lane + 16 * u)];
-  winv16(x, tw, tws, p, [r](int s, int u) { return (2048 >> s) + r * (8 >> s) + (u >> (s + 1)); });
+  winv16_lazy(x, tw, tws, p, [r](int s, int u) { return (2048 >> s) + r * (8 >> s) + (u >> (s + 1)); });
 #pragma unroll
-  for (int u = 0; u < 16; ++u) out[rr * 256 + lane + 16 * u] = x[u];
+  for (int u = 0; u < 16; ++u) out[rr * 256 + lane + 16 * u] = wcanon2(x[u], p);
 }
 
 __global__ __launch_bounds__(kWT) void wk_inv_cols(u64* __restrict__ dst, long long ds, LimbList list, WideTables T) {
@@ -247,14 +285,14 @@ __global__ __launch_bounds__(kWT) void wk_inv_cols(u64* __restrict__ dst, long l
   const int q = r;
 #pragma unroll
   for (int m = 0; m < 16; ++m) x[m] = io[c + 256 * (16 * q + m)];
-  winv16(x, tw, tws, p, [q](int s, int m) { return (128 >> s) + ((16 * q + m) >> (s + 1)); });
+  winv16_lazy(x, tw, tws, p, [q](int s, int m) { return (128 >> s) + ((16 * q + m) >> (s + 1)); });
 #pragma unroll
   for (int m = 0; m < 16; ++m) sh[(16 * q + m) * kWPad + cl] = x[m];
   __syncthreads();
   // rows r + 16 u: stages 12..15 (row distances 16 .. 128), root (8 >> s) + (u >> (s + 1)); then N^-1
 #pragma unroll
   for (int u = 0; u < 16; ++u) x[u] = sh[(r + 16 * u) * kWPad + cl];
-  winv16(x, tw, tws, p, [](int s, int u) { return (8 >> s) + (u >> (s + 1)); });
+  winv16_lazy(x, tw, tws, p, [](int s, int u) { return (8 >> s) + (u >> (s + 1)); });
 #pragma unroll
   for (int u = 0; u < 16; ++u) io[c + 256 * (r + 16 * u)] = wmulc(x[u], ni, nis, p);
 }

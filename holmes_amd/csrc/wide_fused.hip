@@ -66,8 +66,6 @@ __device__ __forceinline__ void w_gs(u64& u, u64& v, u64 w, u64 ws, u64 p, u64 p
   u = s >= p2 ? s - p2 : s;
   v = mulshoup_lazy(a - b + p2, w, ws, p);
 }
-__device__ __forceinline__ u64 wcanon2(u64 x, u64 p) { return x >= p ? x - p : x; }         // x < 2p
-__device__ __forceinline__ u64 wcanon4(u64 x, u64 p) { return wcanon2(x >= 2 * p ? x - 2 * p : x, p); }  // x < 4p
 
 // ----------------------------------------------------------------- column transforms (16-thread slots)
 // Root indices as in ksfused.hip: stage l of a column pairs rows 128 >> l apart; layout A holds rows
