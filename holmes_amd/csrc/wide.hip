@@ -980,7 +980,7 @@ int wide_init(hck_context* c) {
     r64[i] = (u64)(((u128)1 << 64) % q);
     r64_s[i] = shoup_companion(r64[i], q);
   }
-  std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1));
+  std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1)), rescale((size_t)(L + 1));
   std::vector<u64> ql((size_t)(L + 1) * L, 0), ql_s((size_t)(L + 1) * L, 0);
   for (int ell = 1; ell <= L; ++ell) {
     const int beta = (ell + alpha - 1) / alpha;
@@ -1002,6 +1002,14 @@ int wide_init(hck_context* c) {
       slot.push_back(i);
     }
     fill_wide_conv(moddown[ell], P, src, dst, slot);
+    if (ell >= 2) {  // the centered lift of q_{ell-1}: a one-source conversion (hinv = 1, factors 1)
+      std::vector<int> rs_src = {ell - 1}, rs_dst, rs_slot;
+      for (int i = 0; i + 1 < ell; ++i) {
+        rs_dst.push_back(i);
+        rs_slot.push_back(i);
+      }
+      fill_wide_conv(rescale[ell], P, rs_src, rs_dst, rs_slot);
+    }
     for (int i = 0; i + 1 < ell; ++i) {
       const u64 v = hinv(P[ell - 1] % P[i], P[i]);
       ql[(size_t)ell * L + i] = v;
@@ -1023,6 +1031,7 @@ int wide_init(hck_context* c) {
   };
   for (WideConv& cc : modup) fold_inverse(cc);
   for (WideConv& cc : moddown) fold_inverse(cc);
+  for (WideConv& cc : rescale) fold_inverse(cc);
 
   // The matrix-core conversion's fold needs every target prime above 2^46 (|byte-position sum| < 2^45).
   bool mconv = true;
@@ -1033,6 +1042,7 @@ int wide_init(hck_context* c) {
       const int beta = (ell + alpha - 1) / alpha;
       for (int j = 0; j < beta; ++j) fill_wide_digits(modup[(size_t)ell * bmax + j], P, dig);
       fill_wide_digits(moddown[ell], P, dig);
+      if (ell >= 2) fill_wide_digits(rescale[ell], P, dig);
     }
   }
 
@@ -1051,6 +1061,7 @@ int wide_init(hck_context* c) {
       {modup.data(), modup.size() * sizeof(WideConv)}, {moddown.data(), moddown.size() * sizeof(WideConv)},
       {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8}, {dig.data(), dig.size()},
       {mneg.data(), np * 8}, {r64.data(), np * 8}, {r64_s.data(), np * 8},
+      {rescale.data(), rescale.size() * sizeof(WideConv)},
   };
   size_t off = 0;
   for (Part& pt : parts) {
@@ -1099,6 +1110,7 @@ int wide_init(hck_context* c) {
   T.mneg = (const u64*)at(20);
   T.r64 = (const u64*)at(21);
   T.r64_s = (const u64*)at(22);
+  ws->rescale = (WideConv*)at(23);
   c->wide = ws;
   return HCK_OK;
 }
@@ -1286,11 +1298,13 @@ int wide_ks(const hck_context* c, int ell, int batch, const uint64_t* d, long lo
 }
 
 size_t wide_hoist_bytes(const hck_context* c, int ell, int inputs) {
+  if (wide_fused_ok(c)) return wide_fused_hoist_bytes(c, ell, inputs);
   return (size_t)std::min(inputs, kWideChunk) * kN * 8 * (size_t)ell;
 }
 
 int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
                char* ws, hipStream_t s) {
+  if (wide_fused_ok(c)) return wide_hoist_fused(c, ell, inputs, d, d_stride, digits, ws, s);
   if (c->alpha > kMaxAlpha || ell + c->K > kMaxList) return HCK_ERR_UNSUPPORTED;
   const WideState& W = *c->wide;
   const WideTables& T = W.t;
@@ -1329,6 +1343,7 @@ int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, lon
 }
 
 size_t wide_hoisted_bytes(const hck_context* c, int ell, int items) {
+  if (wide_fused_ok(c)) return wide_fused_hoisted_bytes(c, ell, items);
   // ACC [2][ell + K] + CV [ell] + sigma(c0) [ell] per item of a launch
   return (size_t)std::min(items, kWideChunk) * kN * 8 * (size_t)(2 * (ell + c->K) + 2 * ell);
 }
@@ -1337,6 +1352,8 @@ int wide_hoisted(const hck_context* c, int ell, int inputs, int items, const uin
                  const uint64_t* const* ksk, const uint64_t* c0, const uint64_t* c1, long long in_stride,
                  const uint64_t* digits, uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws,
                  hipStream_t s) {
+  if (wide_fused_ok(c))
+    return wide_hoisted_fused(c, ell, inputs, items, galois, ksk, c0, in_stride, digits, out_b, out_a, out_stride, ws, s);
   (void)c1;  // its ModUp is in `digits`
   if (c->alpha > kMaxAlpha || ell + c->K > kMaxList) return HCK_ERR_UNSUPPORTED;
   const WideState& W = *c->wide;
@@ -1385,11 +1402,13 @@ int wide_hoisted(const hck_context* c, int ell, int inputs, int items, const uin
 }
 
 size_t wide_moddown_bytes(const hck_context* c, int ell, int polys) {
+  if (wide_fused_ok(c)) return wide_fused_moddown_bytes(c, ell, polys);
   return (size_t)polys * kN * 8 * (size_t)(c->K + ell);
 }
 
 int wide_moddown(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                  long long out_stride, char* ws, hipStream_t s) {
+  if (wide_fused_ok(c)) return wide_moddown_fused(c, ell, polys, in, in_stride, out, out_stride, ws, s);
   const WideState& W = *c->wide;
   const int K = c->K, L = c->L;
   const long long n = kN;
@@ -1414,12 +1433,13 @@ int wide_moddown(const hck_context* c, int ell, int polys, const uint64_t* in, l
 }
 
 size_t wide_rescale_bytes(const hck_context* c, int ell, int polys) {
-  (void)c;
+  if (wide_fused_ok(c)) return wide_fused_rescale_bytes(c, ell, polys);
   return (size_t)polys * kN * 8 * (size_t)ell;
 }
 
 int wide_rescale(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride, uint64_t* out,
                  long long out_stride, char* ws, hipStream_t s) {
+  if (wide_fused_ok(c) && ell >= 2) return wide_rescale_fused(c, ell, polys, in, in_stride, out, out_stride, ws, s);
   const WideState& W = *c->wide;
   const long long n = kN;
   const int nt = ell - 1;

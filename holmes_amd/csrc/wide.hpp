@@ -64,6 +64,7 @@ struct WideState {
   void* block = nullptr;         // one allocation for every table
   WideConv* modup = nullptr;     // [(L + 1) * beta_max]
   WideConv* moddown = nullptr;   // [L + 1]: P primes -> q_0 .. q_{ell-1}
+  WideConv* rescale = nullptr;   // [L + 1]: level ell lifts q_{ell-1} to q_0 .. q_{ell-2} (the fused rescale)
   uint64_t* qlast_inv = nullptr; // [(L + 1) * L]: level ell, prime i: q_{ell-1}^-1 mod q_i
   uint64_t* qlast_inv_s = nullptr;
   // int8 operands of the matrix-core base conversion (every modup / moddown table, at dig_off), or
@@ -96,6 +97,19 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
                   const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
                   long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
                   long long ext_stride, const uint32_t* galois_items);
+size_t wide_fused_rescale_bytes(const hck_context* c, int ell, int polys);
+int wide_rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
+                       uint64_t* out, long long out_stride, char* ws, hipStream_t s);
+size_t wide_fused_moddown_bytes(const hck_context* c, int ell, int polys);
+int wide_moddown_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
+                       uint64_t* out, long long out_stride, char* ws, hipStream_t s);
+size_t wide_fused_hoist_bytes(const hck_context* c, int ell, int inputs);
+int wide_hoist_fused(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride,
+                     uint64_t* digits, char* ws, hipStream_t s);
+size_t wide_fused_hoisted_bytes(const hck_context* c, int ell, int items);
+int wide_hoisted_fused(const hck_context* c, int ell, int inputs, int items, const uint32_t* galois,
+                       const uint64_t* const* ksk, const uint64_t* c0, long long in_stride, const uint64_t* digits,
+                       uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws, hipStream_t s);
 size_t wide_hoist_bytes(const hck_context* c, int ell, int inputs);
 int wide_hoist(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride, uint64_t* digits,
                char* ws, hipStream_t s);

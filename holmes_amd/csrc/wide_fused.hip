@@ -227,16 +227,20 @@ __device__ __forceinline__ void wrows_inv_to_t(u64 (&x)[16], u64* __restrict__ d
 }
 
 // ----------------------------------------------------------------- K1: INTT rows of d
+// Limb i (< limbs) of item b reads input limb limb0 + i under prime prime0 + i and writes workspace limb
+// i of a `limbs`-limb item.
 __global__ __launch_bounds__(kT) void wf_intt_rows(const u64* __restrict__ d, long long d_stride, const WGalF G,
-                                                   u64* __restrict__ t1, int limbs, int batch, WideTables T) {
+                                                   int limb0, int prime0, u64* __restrict__ t1, int limbs, int batch,
+                                                   WideTables T) {
   __shared__ u64 S[kRowLds];
   const TileId id = decode_tile(batch, blockIdx.x);
   if (id.tile >= 16 * limbs) return;
-  const int i = id.tile >> 4, rg = id.tile & 15, b = id.b;
-  const u64 p = T.p[i];
+  const int i = id.tile >> 4, rg = id.tile & 15, b = id.b, pi = prime0 + i;
+  const u64 p = T.p[pi];
   u64 x[16];
-  load_gal_raw(x, d + (long long)b * d_stride + (long long)i * kN, nat_a(rg), gal_of(G, b));
-  wrows_inv_to_t(x, t1 + ((long long)b * limbs + i) * kN, rg, S, T.inv + (size_t)i * kN, T.inv_s + (size_t)i * kN, p);
+  load_gal_raw(x, d + (long long)b * d_stride + (long long)(limb0 + i) * kN, nat_a(rg), gal_of(G, b));
+  wrows_inv_to_t(x, t1 + ((long long)b * limbs + i) * kN, rg, S, T.inv + (size_t)pi * kN, T.inv_s + (size_t)pi * kN,
+                 p);
 }
 
 // ----------------------------------------------------------------- K2 / K4: cols + conversion
@@ -524,6 +528,156 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ipq(const WIp I, const WGalF G,
   finish(sa, 1, nullptr, acc_a, out_a);
 }
 
+// ----------------------------------------------------------------- ModDown / rescale finish
+// Poly pl = blockIdx.x, limb i = blockIdx.z: v = NTT rows of T4[pl][i] (below 4p); out = (x - v) inv
+// with x canonical (natural layout): inv = P^-1 (ModDown of an extended-basis input) or
+// q_{ell-1}^-1 (rescale).  Grid (polys, 16, limbs).
+__global__ __launch_bounds__(kT) void wf_rows_finish(const u64* __restrict__ t4, const u64* __restrict__ xq,
+                                                     long long xq_stride, u64* __restrict__ out, long long out_stride,
+                                                     int limbs, const u64* __restrict__ inv,
+                                                     const u64* __restrict__ inv_s, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const int pl = blockIdx.x, rg = blockIdx.y, i = blockIdx.z;
+  const u64 p = T.p[i];
+  const long long na = nat_a(rg);
+  u64 x[16], a[16];
+  load_t(x, t4 + ((long long)pl * limbs + i) * kN, rg);
+  load_gal_raw(a, xq + (long long)pl * xq_stride + (long long)i * kN, na, 1u);
+  wrows_fwd_t(x, rg, S, T.fwd + (size_t)i * kN, T.fwd_s + (size_t)i * kN, p);
+  const u64 w = inv[i], ws = inv_s[i];
+  u64* o = out + (long long)pl * out_stride + (long long)i * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = wcanon2(mulshoup_lazy(a[k] + 4 * p - x[k], w, ws, p), p);
+}
+
+// ----------------------------------------------------------------- hoisted rotations
+// The hoisted digits: digits[input][j][e] = the NTT-domain ModUp of digit j on extended limb e
+// (canonical, natural layout; the digit's own limbs are the input's limbs).  Grid (16 (ell + K), beta,
+// inputs): the row pass of each T2 tile, or a copy of the own limb.
+__global__ __launch_bounds__(kT) void wf_hoist_store(const u64* __restrict__ t2, const u64* __restrict__ d,
+                                                     long long d_stride, int ell, int beta, int alpha, int L, int K,
+                                                     u64* __restrict__ digits, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const int e = blockIdx.x >> 4, rg = blockIdx.x & 15, j = blockIdx.y, b = blockIdx.z;
+  const int ext_l = ell + K;
+  const long long na = nat_a(rg);
+  const long long off = ((long long)(b * beta + j) * ext_l + e) * kN;
+  u64 x[16];
+  if (e < ell && e / alpha == j) {
+    load_gal_raw(x, d + (long long)b * d_stride + (long long)e * kN, na, 1u);
+  } else {
+    const int pi = e < ell ? e : L + (e - ell);
+    const u64 p = T.p[pi];
+    load_t(x, t2 + off, rg);
+    wrows_fwd_t(x, rg, S, T.fwd + (size_t)pi * kN, T.fwd_s + (size_t)pi * kN, p);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) x[k] = wcanon4(x[k], p);
+  }
+  u64* o = digits + off + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = x[k];
+}
+
+// Item b rotates input (src0 + b) % inputs by its Galois element: the inner product reads every digit
+// through sigma_g (ModUp commutes with sigma_g), with no row transform.  Montgomery products summed
+// below 2p, then one product by 2^64 mod p: canonical.
+struct WHoist {
+  const u64* digits;
+  int inputs, src0;
+};
+__device__ __forceinline__ void wtile_ip_h(u64 (&sb)[16], u64 (&sa)[16], u64 (&x)[16], const WHoist& H,
+                                           const u64* __restrict__ key, int beta, int ell, int L, int K, int beta_max,
+                                           int b, int e, int pi, int rg, uint32_t g, const WideTables& T) {
+  const u64 p = T.p[pi], p2 = 2 * p, mneg = T.mneg[pi];
+  const int ext_l = ell + K, src = (H.src0 + b) % H.inputs;
+  const long long comp = (long long)beta_max * (L + K) * kN;
+  const long long na = nat_a(rg);
+  auto mac = [&](u64 (&acc)[16], const u64* __restrict__ kp) {
+    u64 kw[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) kw[k] = kp[16 * k];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const u64 v = acc[k] + wmont(x[k], kw[k], p, mneg);
+      acc[k] = v >= p2 ? v - p2 : v;
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sb[k] = sa[k] = 0;
+  for (int jd = 0; jd < beta; ++jd) {
+    load_gal_raw(x, H.digits + ((long long)(src * beta + jd) * ext_l + e) * kN, na, g);
+    const u64* kp = key + ((long long)jd * (L + K) + pi) * kN + na;
+    mac(sb, kp);
+    mac(sa, kp + comp);
+  }
+  const u64 r = T.r64[pi], rs = T.r64_s[pi];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    sb[k] = wmulc(sb[k], r, rs, p);
+    sa[k] = wmulc(sa[k], r, rs, p);
+  }
+}
+
+// P limbs of hoisted rotations: the inner product's INTT rows pass into ACCP ([item][2][K]).
+__global__ __launch_bounds__(kT, 2) void wf_rows_ip_h(const WGalF G, WKeysF keys, int ell, int beta, int L, int K,
+                                                      int beta_max, int batch, u64* __restrict__ accp, WHoist H,
+                                                      WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const TileId id = decode_tile(batch, blockIdx.x);
+  if (id.tile >= 16 * K) return;
+  const int b = id.b, e = ell + (id.tile >> 4), rg = id.tile & 15, pi = L + (e - ell);
+  const u64 p = T.p[pi];
+  u64 sb[16], sa[16], x[16];
+  wtile_ip_h(sb, sa, x, H, keys.k[b], beta, ell, L, K, beta_max, b, e, pi, rg, gal_of(G, b), T);
+  u64* o = accp + ((long long)b * 2 * K + (e - ell)) * kN;
+  const u64* twi = T.inv + (size_t)pi * kN;
+  const u64* twis = T.inv_s + (size_t)pi * kN;
+  wrows_inv_to_t(sb, o, rg, S, twi, twis, p);
+  wrows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, twis, p);
+}
+
+// Q limbs of hoisted rotations: out_b = (IP_b - v_b) P^-1 + sigma_g(c0 of the input), out_a = (IP_a - v_a) P^-1.
+__global__ __launch_bounds__(kT, 2) void wf_rows_ipq_h(const WGalF G, WKeysF keys, int ell, int beta, int L, int K,
+                                                       int beta_max, int batch, const u64* __restrict__ t4,
+                                                       const u64* __restrict__ c0, long long c0_stride,
+                                                       u64* __restrict__ out_b, u64* __restrict__ out_a,
+                                                       long long out_stride, WHoist H, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  __shared__ u64 Park[16 * kT];
+  const TileId id = decode_tile(batch, blockIdx.x);
+  if (id.tile >= 16 * ell) return;
+  const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
+  const uint32_t g = gal_of(G, b);
+  const u64 p = T.p[i];
+  const u64* tw = T.fwd + (size_t)i * kN;
+  const u64* tws = T.fwd_s + (size_t)i * kN;
+  u64 sb[16], sa[16], x[16];
+  wtile_ip_h(sb, sa, x, H, keys.k[b], beta, ell, L, K, beta_max, b, i, i, rg, g, T);
+  const long long na = nat_a(rg);
+  const u64 pv = T.pinv[i], pvs = T.pinv_s[i];
+  const int src = (H.src0 + b) % H.inputs;
+  auto finish = [&](u64 (&s)[16], int comp, const u64* addend, u64* out) {
+    load_t(x, t4 + ((long long)b * 2 * ell + (long long)comp * ell + i) * kN, rg);
+    wrows_fwd_t(x, rg, S, tw, tws, p);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s[k] = wcanon2(mulshoup_lazy(s[k] + 4 * p - x[k], pv, pvs, p), p);
+    if (addend) {
+      load_gal_raw(x, addend + (long long)src * c0_stride + (long long)i * kN, na, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k] = wadd(s[k], x[k], p);
+    }
+    u64* o = out + (long long)b * out_stride + (long long)i * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o[16 * k] = s[k];
+  };
+#pragma unroll
+  for (int k = 0; k < 16; ++k) Park[k * kT + threadIdx.x] = sa[k];
+  finish(sb, 0, c0, out_b);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sa[k] = Park[k * kT + threadIdx.x];
+  finish(sa, 1, nullptr, out_a);
+}
+
 void launch_wconv_fused(const WConvArgs& A, int nt_max, dim3 grid, const WideState& W, hipStream_t s) {
   auto k = nt_max <= kMPass ? wf_cols_mconv<false> : wf_cols_mconv<true>;
   k<<<grid, kT, 0, s>>>(A, W.t, (const wv4i*)W.conv_dig);
@@ -566,7 +720,8 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
     u64* accp = t2 + (long long)nb * beta * ext_l * n;
     const WIp I{dd, d_stride, t2, nullptr, ell, beta, L, K, alpha, bmax};
     // K1
-    wf_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * nb), kT, 0, s>>>(dd, d_stride, G, r1, ell, nb, W.t);
+    wf_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * nb), kT, 0, s>>>(dd, d_stride, G, 0, 0, r1, ell, nb,
+                                                                                  W.t);
     HCK_CHECK_LAUNCH();
     // K2: ModUp, one block per (column pair, digit, item)
     launch_wconv_fused(WConvArgs{r1, (long long)ell * n, 0, alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
@@ -602,6 +757,152 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
       wf_rows_ipq<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, t4, a0, add_stride,
                                                            acc_b ? acc_b + ai : nullptr, acc_a ? acc_a + ai : nullptr,
                                                            acc_stride, out_b + oi, out_a + oi, out_stride, W.t);
+      HCK_CHECK_LAUNCH();
+    }
+  }
+  return HCK_OK;
+}
+
+size_t wide_fused_rescale_bytes(const hck_context* c, int ell, int polys) {
+  (void)c;
+  return (size_t)polys * kN * 8 * (size_t)ell;  // TL [1] + T4 [ell - 1] per poly
+}
+
+// Rescale by q_{ell-1}: INTT rows of the last limb, the lift to the ell - 1 lower primes in the
+// conversion kernel (INTT cols, centered residue, NTT cols), then the finish with q_{ell-1}^-1.
+int wide_rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
+                       uint64_t* out, long long out_stride, char* ws, hipStream_t s) {
+  const WideState& W = *c->wide;
+  const long long n = kN;
+  const int nt = ell - 1;
+  u64* tl = (u64*)ws;                   // [polys][1]
+  u64* t4 = tl + (long long)polys * n;  // [polys][ell - 1]
+  WGalF G{};
+  G.uniform = 1u;
+  for (int p0 = 0; p0 < polys; p0 += 65535) {
+    const int np = std::min(65535, polys - p0);
+    wf_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * np), kT, 0, s>>>(
+        in + (long long)p0 * in_stride, in_stride, G, ell - 1, ell - 1, tl + (long long)p0 * n, 1, np, W.t);
+    HCK_CHECK_LAUNCH();
+    launch_wconv_fused(WConvArgs{tl + (long long)p0 * n, n, 0, 0, t4 + (long long)p0 * nt * n, (long long)nt * n, 0,
+                                 W.rescale + ell, 0},
+                       nt, dim3(128, 1, np), W, s);
+    HCK_CHECK_LAUNCH();
+    const size_t lv = (size_t)ell * c->L;
+    wf_rows_finish<<<dim3(np, 16, nt), kT, 0, s>>>(t4 + (long long)p0 * nt * n, in + (long long)p0 * in_stride,
+                                                   in_stride, out + (long long)p0 * out_stride, out_stride, nt,
+                                                   W.qlast_inv + lv, W.qlast_inv_s + lv, W.t);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
+
+size_t wide_fused_moddown_bytes(const hck_context* c, int ell, int polys) {
+  return (size_t)polys * kN * 8 * (size_t)(c->K + ell);  // TP [K] + T4 [ell] per poly
+}
+
+// ModDown of extended-basis polys ([ell + K] canonical limbs, Q first): INTT rows of the P limbs, the
+// conversion P -> Q (INTT cols, sums, NTT cols), then the finish with P^-1.
+int wide_moddown_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
+                       uint64_t* out, long long out_stride, char* ws, hipStream_t s) {
+  const WideState& W = *c->wide;
+  const int K = c->K;
+  const long long n = kN;
+  u64* tp = (u64*)ws;                        // [polys][K]
+  u64* t4 = tp + (long long)polys * K * n;  // [polys][ell]
+  WGalF G{};
+  G.uniform = 1u;
+  for (int p0 = 0; p0 < polys; p0 += 65535) {
+    const int np = std::min(65535, polys - p0);
+    wf_intt_rows<<<dim3(((16 * K + kXcds - 1) / kXcds) * kXcds * np), kT, 0, s>>>(
+        in + (long long)p0 * in_stride, in_stride, G, ell, c->L, tp + (long long)p0 * K * n, K, np, W.t);
+    HCK_CHECK_LAUNCH();
+    launch_wconv_fused(WConvArgs{tp + (long long)p0 * K * n, (long long)K * n, 0, 0, t4 + (long long)p0 * ell * n,
+                                 (long long)ell * n, 0, W.moddown + ell, 0},
+                       ell, dim3(128, 1, np), W, s);
+    HCK_CHECK_LAUNCH();
+    wf_rows_finish<<<dim3(np, 16, ell), kT, 0, s>>>(t4 + (long long)p0 * ell * n, in + (long long)p0 * in_stride,
+                                                    in_stride, out + (long long)p0 * out_stride, out_stride, ell,
+                                                    W.t.pinv, W.t.pinv_s, W.t);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
+
+size_t wide_fused_hoist_bytes(const hck_context* c, int ell, int inputs) {
+  const size_t nb = (size_t)std::min(inputs, kItems), beta = beta_of(c, ell), ext_l = (size_t)(ell + c->K);
+  return nb * kN * 8 * ((size_t)ell + beta * ext_l);  // T1 [ell] + T2 [beta][ell + K] per input
+}
+
+// The hoisted digits of every input (wf_hoist_store's format): INTT rows, the ModUp conversion, then
+// the row pass of every T2 tile stored canonical in the natural layout.
+int wide_hoist_fused(const hck_context* c, int ell, int inputs, const uint64_t* d, long long d_stride,
+                     uint64_t* digits, char* ws, hipStream_t s) {
+  const WideState& W = *c->wide;
+  const int K = c->K, alpha = c->alpha, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const long long n = kN;
+  const int last_digit = ell - alpha * (beta - 1);
+  const int per = std::min(inputs, kItems);
+  u64* t1 = (u64*)ws;
+  u64* t2 = t1 + (long long)per * ell * n;
+  WGalF G{};
+  G.uniform = 1u;
+  for (int b0 = 0; b0 < inputs; b0 += kItems) {
+    const int nb = std::min(kItems, inputs - b0);
+    const uint64_t* dd = d + (long long)b0 * d_stride;
+    wf_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * nb), kT, 0, s>>>(dd, d_stride, G, 0, 0, t1, ell, nb,
+                                                                                  W.t);
+    HCK_CHECK_LAUNCH();
+    launch_wconv_fused(WConvArgs{t1, (long long)ell * n, 0, alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                                 W.modup + (size_t)ell * bmax, 1},
+                       ext_l - last_digit, dim3(128, beta, nb), W, s);
+    HCK_CHECK_LAUNCH();
+    wf_hoist_store<<<dim3(16 * ext_l, beta, nb), kT, 0, s>>>(t2, dd, d_stride, ell, beta, alpha, c->L, K,
+                                                             digits + (long long)b0 * beta * ext_l * n, W.t);
+    HCK_CHECK_LAUNCH();
+  }
+  return HCK_OK;
+}
+
+size_t wide_fused_hoisted_bytes(const hck_context* c, int ell, int items) {
+  const size_t nb = (size_t)std::min(items, kItems);
+  return nb * kN * 8 * (2 * (size_t)ell + 2 * (size_t)c->K);  // T4 [2][ell] + ACCP [2][K] per item
+}
+
+// Item i (< items) = rotation of input i % inputs by galois[i] with key ksk[i], from its hoisted digits:
+// (sigma(c0) + KS_b(sigma(c1)), KS_a(sigma(c1))), the residues of wide_ks_fused with that element.
+int wide_hoisted_fused(const hck_context* c, int ell, int inputs, int items, const uint32_t* galois,
+                       const uint64_t* const* ksk, const uint64_t* c0, long long in_stride, const uint64_t* digits,
+                       uint64_t* out_b, uint64_t* out_a, long long out_stride, char* ws, hipStream_t s) {
+  const WideState& W = *c->wide;
+  const int K = c->K, L = c->L, beta = beta_of(c, ell), bmax = c->beta_max;
+  const long long n = kN;
+  for (int i0 = 0; i0 < items; i0 += kItems) {
+    const int nb = std::min(kItems, items - i0);
+    WGalF G{};
+    G.per_item = 1;
+    WKeysF kp{};
+    for (int b = 0; b < nb; ++b) {
+      G.g[b] = galois[i0 + b];
+      kp.k[b] = ksk[i0 + b];
+    }
+    const WHoist H{digits, inputs, i0 % inputs};
+    u64* t4 = (u64*)ws;
+    u64* accp = t4 + (long long)nb * 2 * ell * n;
+    {
+      const int tiles = 16 * K, groups = (tiles + kXcds - 1) / kXcds;
+      wf_rows_ip_h<<<dim3(groups * kXcds * nb), kT, 0, s>>>(G, kp, ell, beta, L, K, bmax, nb, accp, H, W.t);
+      HCK_CHECK_LAUNCH();
+    }
+    launch_wconv_fused(WConvArgs{accp, 2LL * K * n, (long long)K * n, 0, t4, 2LL * ell * n, (long long)ell * n,
+                                 W.moddown + ell, 0},
+                       ell, dim3(128, 2, nb), W, s);
+    HCK_CHECK_LAUNCH();
+    {
+      const int tiles = 16 * ell, groups = (tiles + kXcds - 1) / kXcds;
+      wf_rows_ipq_h<<<dim3(groups * kXcds * nb), kT, 0, s>>>(G, kp, ell, beta, L, K, bmax, nb, t4, c0, in_stride,
+                                                             out_b + (long long)i0 * out_stride,
+                                                             out_a + (long long)i0 * out_stride, out_stride, H, W.t);
       HCK_CHECK_LAUNCH();
     }
   }
