@@ -699,12 +699,15 @@ struct WMac {
 // (bsgs.hip: k_bsgs_mac): a thread owns one coefficient of one limb and a kWTI x kWTG tile of (input,
 // giant) accumulators for both components; per baby step it reads kWTG plaintext words and 2 kWTI baby
 // words for 2 kWTI kWTG products (the next step's words are in flight while the current one computes).
-// Products are Montgomery products (canonical operands: below 2p each), summed below 2p, and brought
-// back by one product with 2^64 mod p: canonical results.  All tiles of one (limb, 128-coefficient)
-// unit are dealt to one XCD, so the unit's plaintext and baby words come from HBM once.
+// The products of canonical operands (below p^2) are summed exactly in 128 bits; every kFoldEvery baby
+// steps (kFoldEvery p^2 < p 2^64 for p < 2^61) a sum is folded back to its canonical residue by one
+// Montgomery reduction and one product with 2^64 mod p, and the last fold gives the result.  All tiles
+// of one (limb, 128-coefficient) unit are dealt to one XCD, so the unit's plaintext and baby words come
+// from HBM once.
 constexpr int kWMacThreads = 128;
 constexpr int kWTI = 4;
 constexpr int kWTG = 4;
+constexpr int kFoldEvery = 8;
 
 struct WMacOps {
   u64 w[kWTG], x0[kWTI], x1[kWTI];
@@ -726,6 +729,14 @@ __device__ __forceinline__ void wmac_load(WMacOps& o, const WMac& P, int b, int 
   }
 }
 
+// t mod p for t < p 2^64: Montgomery's reduction (t 2^-64, below 2p), then the product with 2^64 mod p.
+__device__ __forceinline__ u64 wfold128(u128 t, u64 p, u64 mneg, u64 r, u64 rs) {
+  const u64 tl = (u64)t, th = (u64)(t >> 64);
+  const u64 m = tl * mneg;
+  const u64 u = th + (u64)(((u128)m * p) >> 64) + (tl != 0 ? 1 : 0);
+  return wmulc(u, r, rs, p);
+}
+
 __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long long baby_stride,
                                                             const u64* __restrict__ pts, long long pt_stride,
                                                             u64* __restrict__ res, int inputs, int babies, int giants,
@@ -741,9 +752,9 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
   const int n = (unit % units_per_limb) * kWMacThreads + threadIdx.x;
   const int i0 = (tile % tiles_i) * kWTI, g0 = (tile / tiles_i) * kWTG;
   const int pi = pm.prime[l];
-  const u64 p = T.p[pi], p2 = 2 * p, mneg = T.mneg[pi];
+  const u64 p = T.p[pi], mneg = T.mneg[pi], r = T.r64[pi], rs = T.r64_s[pi];
   const long long ln = (long long)l * kN + n;
-  u64 acc[kWTI][2][kWTG];
+  u128 acc[kWTI][2][kWTG];
 #pragma unroll
   for (int t = 0; t < kWTI; ++t)
 #pragma unroll
@@ -758,14 +769,19 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
     for (int t = 0; t < kWTI; ++t)
 #pragma unroll
       for (int g = 0; g < kWTG; ++g) {
-        const u64 v0 = acc[t][0][g] + wmont(cur.x0[t], cur.w[g], p, mneg);
-        const u64 v1 = acc[t][1][g] + wmont(cur.x1[t], cur.w[g], p, mneg);
-        acc[t][0][g] = v0 >= p2 ? v0 - p2 : v0;
-        acc[t][1][g] = v1 >= p2 ? v1 - p2 : v1;
+        acc[t][0][g] += (u128)cur.x0[t] * cur.w[g];
+        acc[t][1][g] += (u128)cur.x1[t] * cur.w[g];
       }
+    if (b % kFoldEvery == kFoldEvery - 1 && b + 1 < babies) {  // the folded residue restarts the sum
+#pragma unroll
+      for (int t = 0; t < kWTI; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int g = 0; g < kWTG; ++g) acc[t][c][g] = wfold128(acc[t][c][g], p, mneg, r, rs);
+    }
     cur = nxt;
   }
-  const u64 r = T.r64[pi], rs = T.r64_s[pi];
   const long long is = (long long)limbs * kN, gs = (long long)inputs * is, cs = (long long)giants * gs;
 #pragma unroll
   for (int t = 0; t < kWTI; ++t) {
@@ -775,7 +791,8 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
 #pragma unroll
       for (int g = 0; g < kWTG; ++g)
         if (g0 + g < giants)
-          res[c * cs + (long long)(g0 + g) * gs + (long long)(i0 + t) * is + ln] = wmulc(acc[t][c][g], r, rs, p);
+          res[c * cs + (long long)(g0 + g) * gs + (long long)(i0 + t) * is + ln] =
+              wfold128(acc[t][c][g], p, mneg, r, rs);
   }
 }
 
