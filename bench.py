@@ -1151,18 +1151,23 @@ def _cpu_annotated(cpu):
     return None if cpu is None else {**cpu, "cpu_model": _cpu_model()}
 
 
+# The sources the C2 step's kernels are built from: the FP64 key-switch kernels and their entry
+# point, the tile layout, the arithmetic and the context tables they read.  The traffic record holds
+# only while these match (a change to the wide-prime kernels does not move C2's bytes).
+C2_KERNEL_SOURCES = ("context.hip", "internal.hpp", "keyswitch.hip", "ksfused.hip", "modarith.hpp", "tile_layout.hpp")
+
+
 def kernel_sources_sha256() -> str:
-    """SHA-256 over the library's kernel sources (name and bytes of every csrc file, sorted)."""
+    """SHA-256 over the C2 kernels' sources (name and bytes of each file of C2_KERNEL_SOURCES)."""
 
     import hashlib
 
     root = os.path.join(os.path.dirname(os.path.abspath(__file__)), "holmes_amd", "csrc")
     h = hashlib.sha256()
-    for name in sorted(os.listdir(root)):
-        if name.endswith((".hip", ".hpp", ".h")):
-            h.update(name.encode())
-            with open(os.path.join(root, name), "rb") as f:
-                h.update(f.read())
+    for name in sorted(C2_KERNEL_SOURCES):
+        h.update(name.encode())
+        with open(os.path.join(root, name), "rb") as f:
+            h.update(f.read())
     return h.hexdigest()
 
 
