@@ -550,6 +550,34 @@ __global__ __launch_bounds__(kT) void wf_rows_finish(const u64* __restrict__ t4,
   for (int k = 0; k < 16; ++k) o[16 * k] = wcanon2(mulshoup_lazy(a[k] + 4 * p - x[k], w, ws, p), p);
 }
 
+// wf_rows_finish with one output pointer per polynomial (the groups of a weighted sum with its
+// rescale) and a canonical residue added on the polynomials of add_mask.
+struct WGroupOut {
+  u64* out[kLcRsGroups];
+  u64 add[kMaxPrimes];
+  unsigned long long add_mask;
+};
+
+__global__ __launch_bounds__(kT) void wf_rows_finish_groups(const u64* __restrict__ t4, const u64* __restrict__ xq,
+                                                            long long xq_stride, const WGroupOut O, int limbs,
+                                                            const u64* __restrict__ inv,
+                                                            const u64* __restrict__ inv_s, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const int pl = blockIdx.x, rg = blockIdx.y, i = blockIdx.z;
+  const u64 p = T.p[i];
+  const long long na = nat_a(rg);
+  u64 x[16], a[16];
+  load_t(x, t4 + ((long long)pl * limbs + i) * kN, rg);
+  load_gal_raw(a, xq + (long long)pl * xq_stride + (long long)i * kN, na, 1u);
+  wrows_fwd_t(x, rg, S, T.fwd + (size_t)i * kN, T.fwd_s + (size_t)i * kN, p);
+  const u64 w = inv[i], ws = inv_s[i];
+  const bool add = (O.add_mask >> pl) & 1ull;  // uniform
+  const u64 av = add ? O.add[i] : 0;
+  u64* o = O.out[pl] + (long long)i * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) o[16 * k] = wadd(wcanon2(mulshoup_lazy(a[k] + 4 * p - x[k], w, ws, p), p), av, p);
+}
+
 // ----------------------------------------------------------------- hoisted rotations
 // The hoisted digits: digits[input][j][e] = the NTT-domain ModUp of digit j on extended limb e
 // (canonical, natural layout; the digit's own limbs are the input's limbs).  Grid (16 (ell + K), beta,
@@ -794,6 +822,37 @@ int wide_rescale_fused(const hck_context* c, int ell, int polys, const uint64_t*
                                                    W.qlast_inv + lv, W.qlast_inv_s + lv, W.t);
     HCK_CHECK_LAUNCH();
   }
+  return HCK_OK;
+}
+
+// wide_rescale_fused over the groups of a weighted sum: in [groups][ell] contiguous (stride in_stride),
+// group g rescaled into out[g] ([ell - 1] limbs), add[i] added on the groups of add_mask.  One launch
+// sequence for all groups; the residues are those of one rescale per group.
+int wide_rescale_groups(const hck_context* c, int ell, int groups, const uint64_t* in, long long in_stride,
+                        uint64_t* const* out, const uint64_t* add, uint64_t add_mask, char* ws, hipStream_t s) {
+  if (groups < 1) return HCK_OK;
+  if (groups > kLcRsGroups || ell < 2) return HCK_ERR_ARG;
+  const WideState& W = *c->wide;
+  const long long n = kN;
+  const int nt = ell - 1;
+  u64* tl = (u64*)ws;                    // [groups][1]
+  u64* t4 = tl + (long long)groups * n;  // [groups][ell - 1]
+  WGalF G{};
+  G.uniform = 1u;
+  WGroupOut O{};
+  for (int g = 0; g < groups; ++g) O.out[g] = out[g];
+  if (add)
+    for (int i = 0; i < nt; ++i) O.add[i] = add[i];
+  O.add_mask = add ? add_mask : 0ull;
+  wf_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * groups), kT, 0, s>>>(in, in_stride, G, ell - 1, ell - 1,
+                                                                                tl, 1, groups, W.t);
+  HCK_CHECK_LAUNCH();
+  launch_wconv_fused(WConvArgs{tl, n, 0, 0, t4, (long long)nt * n, 0, W.rescale + ell, 0}, nt, dim3(128, 1, groups), W, s);
+  HCK_CHECK_LAUNCH();
+  const size_t lv = (size_t)ell * c->L;
+  wf_rows_finish_groups<<<dim3(groups, 16, nt), kT, 0, s>>>(t4, in, in_stride, O, nt, W.qlast_inv + lv,
+                                                            W.qlast_inv_s + lv, W.t);
+  HCK_CHECK_LAUNCH();
   return HCK_OK;
 }
 

@@ -195,7 +195,7 @@ def test_lincomb(env):
     M.test_lincomb_matches_oracle(env)
 
 
-@pytest.mark.parametrize("limbs,G,T", [(38, 3, 5), (2, 2, 1)])
+@pytest.mark.parametrize("limbs,G,T", [(38, 3, 5), (2, 2, 1), (24, 64, 1)])
 def test_lincomb_rescale(env, limbs, G, T):
     M.check_lincomb_rescale(env, limbs, G, T)
 
