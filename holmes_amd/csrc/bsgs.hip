@@ -91,11 +91,8 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int g = 0; g < kTG; ++g) acc[t][c][g] = 0.0;
-  // two-stage software pipeline: baby step b + 1's loads are in flight while b computes
-  MacOps cur, nxt;
-  mac_load(cur, babies, 0, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
-  for (int b = 0; b < nb; ++b) {
-    if (b + 1 < nb) mac_load(nxt, babies, b + 1, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
+  // one baby step's products from its loaded words; every 8 steps the sums are reduced
+  auto step = [&](const MacOps& cur, int b) {
     double w[kTG], wp[kTG];
 #pragma unroll
     for (int g = 0; g < kTG; ++g) {
@@ -119,8 +116,26 @@ __global__ __launch_bounds__(kMacThreads) void k_bsgs_mac(uint64_t* __restrict__
 #pragma unroll
           for (int g = 0; g < kTG; ++g) acc[t][c][g] = reduce(acc[t][c][g], p, pinv);
     }
-    cur = nxt;
+  };
+  // two-stage software pipeline on two register sets: baby step b + 1's words load into one set while
+  // step b computes from the other (the last pair reloads its own words, unused), so the wait before
+  // a step's products covers only that step's own loads.
+  MacOps o0, o1;
+  mac_load(o0, babies, 0, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
+  int b = 0;
+  for (; b + 1 < nb; b += 2) {
+    mac_load(o1, babies, b + 1, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
+    // the loads stay ahead of the products they overlap: neither the compiler's IR passes (the
+    // memory clobber) nor the scheduler (the barrier) move them below
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step(o0, b);
+    mac_load(o0, babies, b + 2 < nb ? b + 2 : b + 1, nb, G, ni, g0, i0, pts, pt_stride, baby_stride, ln);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step(o1, b + 1);
   }
+  if (b < nb) step(o0, b);  // odd count: the last step's words are in o0
   const long long is = (long long)limbs * kN, gs = (long long)ni * is, cs = (long long)G * gs;
 #pragma unroll
   for (int t = 0; t < kTI; ++t) {
