@@ -761,10 +761,8 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
     for (int c = 0; c < 2; ++c)
 #pragma unroll
       for (int g = 0; g < kWTG; ++g) acc[t][c][g] = 0;
-  WMacOps cur, nxt;
-  wmac_load(cur, P, 0, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
-  for (int b = 0; b < babies; ++b) {
-    if (b + 1 < babies) wmac_load(nxt, P, b + 1, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+  // one baby step's products; every kFoldEvery steps the sums are folded
+  auto step = [&](const WMacOps& cur, int b) {
 #pragma unroll
     for (int t = 0; t < kWTI; ++t)
 #pragma unroll
@@ -780,8 +778,25 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
 #pragma unroll
           for (int g = 0; g < kWTG; ++g) acc[t][c][g] = wfold128(acc[t][c][g], p, mneg, r, rs);
     }
-    cur = nxt;
+  };
+  // two-stage software pipeline on two register sets: step b + 1's words load into one set while step
+  // b computes from the other (the last pair reloads its own words, unused); the memory clobber and
+  // the scheduling barrier keep each set's loads ahead of the products they overlap, so a step waits
+  // only for its own loads
+  WMacOps o0, o1;
+  wmac_load(o0, P, 0, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+  int b = 0;
+  for (; b + 1 < babies; b += 2) {
+    wmac_load(o1, P, b + 1, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step(o0, b);
+    wmac_load(o0, P, b + 2 < babies ? b + 2 : b + 1, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step(o1, b + 1);
   }
+  if (b < babies) step(o0, b);  // odd count: the last step's words are in o0
   const long long is = (long long)limbs * kN, gs = (long long)inputs * is, cs = (long long)giants * gs;
 #pragma unroll
   for (int t = 0; t < kWTI; ++t) {
