@@ -1143,6 +1143,8 @@ int wide_init(hck_context* c) {
   T.r64 = (const u64*)at(21);
   T.r64_s = (const u64*)at(22);
   ws->rescale = (WideConv*)at(23);
+  ws->primes_below_2_60 = true;
+  for (int i = 0; i < c->np; ++i) ws->primes_below_2_60 = ws->primes_below_2_60 && c->primes[i] < (1ULL << 60);
   c->wide = ws;
   return HCK_OK;
 }

@@ -70,6 +70,8 @@ struct WideState {
   // int8 operands of the matrix-core base conversion (every modup / moddown table, at dig_off), or
   // null when a prime of the context lies below 2^46 (the fold's bound); then wk_conv runs.
   const void* conv_dig = nullptr;
+  // every prime below 2^60: the fused kernels' forward passes keep their words below 16p (wide_fused.hip)
+  bool primes_below_2_60 = false;
 };
 
 // Context set-up and release (context.hip calls these for a context with a prime >= 2^50).

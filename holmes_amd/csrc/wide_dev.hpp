@@ -23,6 +23,7 @@ __device__ __forceinline__ Barrett64 wbar(const WideTables& T, int pi) { return 
 // canonical representative of a lazy word below 2p / below 4p
 __device__ __forceinline__ uint64_t wcanon2(uint64_t x, uint64_t p) { return x >= p ? x - p : x; }
 __device__ __forceinline__ uint64_t wcanon4(uint64_t x, uint64_t p) { return wcanon2(x >= 2 * p ? x - 2 * p : x, p); }
+__device__ __forceinline__ uint64_t wcanon8(uint64_t x, uint64_t p) { return wcanon4(x >= 4 * p ? x - 4 * p : x, p); }
 
 // x k 2^-64 mod p below 2p, for x k < 2^64 p (Montgomery; mneg = -p^-1 mod 2^64): t + m p is a
 // multiple of 2^64 for m = t mneg, and its low words add up to 2^64 exactly when t's low word is not 0.

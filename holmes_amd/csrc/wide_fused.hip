@@ -1,12 +1,15 @@
 // Fused hybrid key switch on 64-bit words: the wide-prime path's counterpart of ksfused.hip.
 //
 // The same five-kernel schedule and workspace tile layout (tile_layout.hpp) as the FP64 kernels,
-// with residues held as 64-bit words (primes below 2^61: the reference's 60/59-bit production chain).
-// Arithmetic (every bound below needs 4p < 2^63):
-//  * transforms run lazily (Harvey): forward butterflies take and return words below 4p, inverse
-//    ones below 2p; products by twiddles and conversion factors use Shoup's companions, whose lazy
-//    result lies below 2p for any 64-bit input.  Workspace words keep these lazy ranges;
-//  * key products are Montgomery products x k 2^-64 (below 2p for x < 4p, k < p), summed lazily
+// with residues held as 64-bit words (every prime below 2^60, wide_fused_ok: the reference's 60/59-bit
+// production chain).
+// Arithmetic (every bound below needs 16p <= 2^64):
+//  * transforms run lazily: a forward pass of four stages takes words below 8p, adds 2p per stage
+//    (w_ct, no reduction) and subtracts 8p once at its end, so its outputs lie below 8p; inverse
+//    (Harvey) butterflies take and return words below 2p; products by twiddles and conversion factors
+//    use Shoup's companions, whose lazy result lies below 2p for any 64-bit input.  Workspace words
+//    keep these lazy ranges;
+//  * key products are Montgomery products x k 2^-64 (below 1.5p for x < 8p, k < p), summed lazily
 //    below 2p and multiplied by 2^64 mod p (Shoup, canonical result) once per output;
 //  * the base-conversion sums run on the int8 matrix cores with the wide digit tables (wide_dev.hpp:
 //    wdigits takes a canonical residue, wfold returns one).
@@ -53,13 +56,21 @@ struct WGalF {
 };
 __device__ __forceinline__ uint32_t gal_of(const WGalF& G, int b) { return G.per_item ? G.g[b] : G.uniform; }
 
-// Cooley-Tukey (u, v) -> (u + w v, u - w v), inputs and outputs below 4p; Gentleman-Sande
-// (u, v) -> (u + v, (u - v) w), inputs and outputs below 2p.  p2 = 2p.
+// Cooley-Tukey (u, v) -> (u + w v, u - w v) without a reduction: w v lies below 2p (Shoup, for any
+// 64-bit v), so each stage raises the bound by 2p.  A forward pass of four stages takes words below 8p
+// to words below 16p (<= 2^64 for p < 2^60: wide_fused_ok) and subtracts 8p once at its end
+// (w_fwd_end), so every forward pass's outputs, and the transform's, lie below 8p.
+// Gentleman-Sande (u, v) -> (u + v, (u - v) w), inputs and outputs below 2p.  p2 = 2p.
 __device__ __forceinline__ void w_ct(u64& u, u64& v, u64 w, u64 ws, u64 p, u64 p2) {
-  const u64 a = u >= p2 ? u - p2 : u;
+  const u64 a = u;
   const u64 y = mulshoup_lazy(v, w, ws, p);
   u = a + y;
   v = a - y + p2;
+}
+__device__ __forceinline__ void w_fwd_end(u64 (&x)[16], u64 p) {
+  const u64 p8 = 8 * p;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = x[k] >= p8 ? x[k] - p8 : x[k];
 }
 __device__ __forceinline__ void w_gs(u64& u, u64& v, u64 w, u64 ws, u64 p, u64 p2) {
   const u64 a = u, b = v, s = a + b;
@@ -82,6 +93,7 @@ __device__ __forceinline__ void wcol_fwd_lo(u64 (&x)[16], const u64* __restrict_
       w_ct(x[k], x[k + h], tw[wi], tws[wi], p, 2 * p);
     }
   }
+  w_fwd_end(x, p);
 }
 
 __device__ __forceinline__ void wcol_fwd_hi(u64 (&x)[16], int j, const u64* __restrict__ tw,
@@ -96,6 +108,7 @@ __device__ __forceinline__ void wcol_fwd_hi(u64 (&x)[16], int j, const u64* __re
       w_ct(x[k], x[k + h], tw[wi], tws[wi], p, 2 * p);
     }
   }
+  w_fwd_end(x, p);
 }
 
 __device__ __forceinline__ void wcol_inv_hi(u64 (&x)[16], int j, const u64* __restrict__ tw,
@@ -153,6 +166,7 @@ __device__ __forceinline__ void wrow_fwd_lo(u64 (&x)[16], int b, const u64* __re
       w_ct(x[k], x[k + h], t[k >> (12 - l)], ts[k >> (12 - l)], p, 2 * p);
     }
   }
+  w_fwd_end(x, p);
 }
 
 __device__ __forceinline__ void wrow_fwd_hi(u64 (&x)[16], int b, int j, const u64* __restrict__ tw,
@@ -169,6 +183,7 @@ __device__ __forceinline__ void wrow_fwd_hi(u64 (&x)[16], int b, int j, const u6
       w_ct(x[k], x[k + h], t[k >> (16 - l)], ts[k >> (16 - l)], p, 2 * p);
     }
   }
+  w_fwd_end(x, p);
 }
 
 __device__ __forceinline__ void wrow_inv_hi(u64 (&x)[16], int b, int j, const u64* __restrict__ tw,
@@ -369,7 +384,7 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
 
 // ----------------------------------------------------------------- inner product of one tile
 // sb / sa = sum_j x_j key_j[comp] mod p over the digits j of item b, extended limb e (prime pi), row
-// group rg: x_j the NTT rows pass of T2 digit j (below 4p), or, for the digit that holds limb e, d
+// group rg: x_j the NTT rows pass of T2 digit j (below 8p), or, for the digit that holds limb e, d
 // itself read through sigma_g.  Montgomery products summed below 2p, then one product by 2^64 mod p:
 // canonical results.
 struct WIp {
@@ -396,7 +411,7 @@ __device__ __forceinline__ void wtile_ip(u64 (&sb)[16], u64 (&sa)[16], u64 (&x)[
     for (int k = 0; k < 16; ++k) kw[k] = kp[16 * k];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
-      const u64 v = acc[k] + wmont(x[k], kw[k], p, mneg);  // below 4p
+      const u64 v = acc[k] + wmont(x[k], kw[k], p, mneg);  // below 3.5p
       acc[k] = v >= p2 ? v - p2 : v;
     }
   };
@@ -478,7 +493,7 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ip(const WIp I, const WGalF G, 
 
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
 // out_b = (IP_b - v_b) P^-1 + sigma_g(add) (+ acc_b),  out_a = (IP_a - v_a) P^-1 (+ acc_a),
-// v = the NTT rows pass of the ModDown conversion T4 ([item][2][ell], workspace layout; below 4p).
+// v = the NTT rows pass of the ModDown conversion T4 ([item][2][ell], workspace layout; below 8p).
 __global__ __launch_bounds__(kT, 2) void wf_rows_ipq(const WIp I, const WGalF G, WKeysF keys, int batch,
                                                      const u64* __restrict__ t4, const u64* __restrict__ add,
                                                      long long add_stride, const u64* __restrict__ acc_b,
@@ -505,7 +520,7 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ipq(const WIp I, const WGalF G,
     load_t(x, t4 + ((long long)b * 2 * ell + (long long)comp * ell + i) * kN, rg);
     wrows_fwd_t(x, rg, S, tw, tws, p);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) s[k] = wcanon2(mulshoup_lazy(s[k] + 4 * p - x[k], pv, pvs, p), p);  // v < 4p
+    for (int k = 0; k < 16; ++k) s[k] = wcanon2(mulshoup_lazy(s[k] + 8 * p - x[k], pv, pvs, p), p);  // v < 8p
     if (addend) {
       load_gal_raw(x, addend + (long long)b * add_stride + (long long)i * kN, na, g);
 #pragma unroll
@@ -529,7 +544,7 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ipq(const WIp I, const WGalF G,
 }
 
 // ----------------------------------------------------------------- ModDown / rescale finish
-// Poly pl = blockIdx.x, limb i = blockIdx.z: v = NTT rows of T4[pl][i] (below 4p); out = (x - v) inv
+// Poly pl = blockIdx.x, limb i = blockIdx.z: v = NTT rows of T4[pl][i] (below 8p); out = (x - v) inv
 // with x canonical (natural layout): inv = P^-1 (ModDown of an extended-basis input) or
 // q_{ell-1}^-1 (rescale).  Grid (polys, 16, limbs).
 __global__ __launch_bounds__(kT) void wf_rows_finish(const u64* __restrict__ t4, const u64* __restrict__ xq,
@@ -547,7 +562,7 @@ __global__ __launch_bounds__(kT) void wf_rows_finish(const u64* __restrict__ t4,
   const u64 w = inv[i], ws = inv_s[i];
   u64* o = out + (long long)pl * out_stride + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) o[16 * k] = wcanon2(mulshoup_lazy(a[k] + 4 * p - x[k], w, ws, p), p);
+  for (int k = 0; k < 16; ++k) o[16 * k] = wcanon2(mulshoup_lazy(a[k] + 8 * p - x[k], w, ws, p), p);
 }
 
 // wf_rows_finish with one output pointer per polynomial (the groups of a weighted sum with its
@@ -575,7 +590,7 @@ __global__ __launch_bounds__(kT) void wf_rows_finish_groups(const u64* __restric
   const u64 av = add ? O.add[i] : 0;
   u64* o = O.out[pl] + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) o[16 * k] = wadd(wcanon2(mulshoup_lazy(a[k] + 4 * p - x[k], w, ws, p), p), av, p);
+  for (int k = 0; k < 16; ++k) o[16 * k] = wadd(wcanon2(mulshoup_lazy(a[k] + 8 * p - x[k], w, ws, p), p), av, p);
 }
 
 // ----------------------------------------------------------------- hoisted rotations
@@ -599,7 +614,7 @@ __global__ __launch_bounds__(kT) void wf_hoist_store(const u64* __restrict__ t2,
     load_t(x, t2 + off, rg);
     wrows_fwd_t(x, rg, S, T.fwd + (size_t)pi * kN, T.fwd_s + (size_t)pi * kN, p);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) x[k] = wcanon4(x[k], p);
+    for (int k = 0; k < 16; ++k) x[k] = wcanon8(x[k], p);
   }
   u64* o = digits + off + na;
 #pragma unroll
@@ -688,7 +703,7 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ipq_h(const WGalF G, WKeysF key
     load_t(x, t4 + ((long long)b * 2 * ell + (long long)comp * ell + i) * kN, rg);
     wrows_fwd_t(x, rg, S, tw, tws, p);
 #pragma unroll
-    for (int k = 0; k < 16; ++k) s[k] = wcanon2(mulshoup_lazy(s[k] + 4 * p - x[k], pv, pvs, p), p);
+    for (int k = 0; k < 16; ++k) s[k] = wcanon2(mulshoup_lazy(s[k] + 8 * p - x[k], pv, pvs, p), p);
     if (addend) {
       load_gal_raw(x, addend + (long long)src * c0_stride + (long long)i * kN, na, g);
 #pragma unroll
@@ -714,7 +729,8 @@ void launch_wconv_fused(const WConvArgs& A, int nt_max, dim3 grid, const WideSta
 }  // namespace
 
 bool wide_fused_ok(const hck_context* c) {
-  return c->wide && c->conv_engine == 1 && c->wide->conv_dig && c->alpha <= kMaxAlpha && c->K <= kMaxSpecial;
+  return c->wide && c->conv_engine == 1 && c->wide->conv_dig && c->wide->primes_below_2_60 && c->alpha <= kMaxAlpha &&
+         c->K <= kMaxSpecial;
 }
 
 size_t wide_fused_bytes(const hck_context* c, int ell, int batch) {
