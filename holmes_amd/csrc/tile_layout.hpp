@@ -113,10 +113,17 @@ __device__ __forceinline__ long long ws_a(int g, int k) {
 // 16 live 64-bit addresses.
 constexpr int kBufWord3 = 0x00020000;  // raw buffer, 32-bit data format (gfx9 family)
 
+// src_t is a tile's base and the same on every lane of a wave (every caller derives it from the
+// workgroup's item and tile only); it is passed through readfirstlane so that the descriptor is
+// built in scalar registers even where the compiler cannot prove the address uniform (otherwise it
+// wraps each load in a loop over the distinct descriptors of the wave).
 template <typename E>
 __device__ __forceinline__ void load_t(E (&x)[16], const E* __restrict__ src_t, int g) {
   static_assert(sizeof(E) == 8, "workspace words are 64-bit");
-  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)src_t, 0, kN * 8, kBufWord3);
+  const uint64_t a = (uint64_t)src_t;
+  const uint64_t au = (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)a) |
+                      ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(a >> 32)) << 32);
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc((void*)au, 0, kN * 8, kBufWord3);
   const int off = (int)ws_a(g, 0) * 8;
 #pragma unroll
   for (int k = 0; k < 16; ++k)
