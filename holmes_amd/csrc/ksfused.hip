@@ -491,10 +491,13 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
   const uint64_t* B1 = D + (4 * g + 2 + cl) * kYStride + j;  // source 2 g + 1
   double* RX = (SEPX ? X : Y) + sigma * kYStride;
   double* dbase = dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
-  for (int base = 0; base < nt; base += kMPass) {
+  for (int base = 0; base < nt;) {
+    // mi targets per quarter in this pass (at most kMItems): the last pass spreads what is left over
+    // every quarter, so that no wave idles while another transforms three targets
+    const int mi = min(kMItems, (nt - base + 7) / 8);
     // constants of MFMA row j: target of quarter j >> 2, item j & 3
-    const int ta = base + (4 * h + (j >> 2)) * kMItems + (j & 3);
-    const bool arow = (j & 3) < kMItems && ta < nt;
+    const int ta = base + (4 * h + (j >> 2)) * mi + (j & 3);
+    const bool arow = (j & 3) < mi && ta < nt;
     v4i av[kConvDigits];
 #pragma unroll
     for (int c = 0; c < kConvDigits; ++c)
@@ -503,7 +506,7 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
     double p[kMItems], pinv[kMItems];
 #pragma unroll
     for (int r = 0; r < kMItems; ++r) {
-      to[r] = base + (4 * h + g) * kMItems + r;
+      to[r] = r < mi ? base + (4 * h + g) * mi + r : nt;
       const int tp = C.dst_prime[to[r] < nt ? to[r] : 0];
       p[r] = T.p[tp];
       pinv[r] = T.pinv[tp];
@@ -524,8 +527,10 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
       }
 #pragma unroll
       for (int r = 0; r < kMItems; ++r) {
-        x[r][k] = mconv_fold(acc[0][r] + (int)((uint32_t)acc[1][r] << 8), acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
-                             acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], p[r], pinv[r]);
+        x[r][k] = r < mi ? mconv_fold(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
+                                      acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
+                                      acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], p[r], pinv[r])
+                         : 0.0;
         // the fold happens here, in its tile: sunk to its use in the transform, every tile's
         // accumulators would stay live at once
         asm volatile("" : "+v"(x[r][k]));
@@ -535,6 +540,7 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
     if (!SEPX) __syncthreads();  // every wave is done reading D before its runs become exchange buffers
 #pragma unroll
     for (int r = 0; r < kMItems; ++r) {
+      if (r >= mi) break;  // uniform over the block
       const bool act = to[r] < nt;
       const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? to[r] : 0] * kN;
       if (act) col_fwd_lo<true>(x[r], tw, p[r], pinv[r]);
@@ -546,6 +552,7 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
         for (int k = 0; k < 16; ++k) col[4096 * k + j] = x[r][k];
       }
     }
+    base += 8 * mi;
   }
 }
 
@@ -643,9 +650,10 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
   const double* RZ = Z + cl * kYStride + j;
   double* RX = (SEPX ? X : Y) + sigma * kYStride;
   double* dbase = dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
-  for (int base = 0; base < nt; base += kMPass) {
-    const int ta = base + (4 * h + (j >> 2)) * kMItems + (j & 3);
-    const bool arow = (j & 3) < kMItems && ta < nt;
+  for (int base = 0; base < nt;) {
+    const int mi = min(kMItems, (nt - base + 7) / 8);  // as in cols_mconv_body
+    const int ta = base + (4 * h + (j >> 2)) * mi + (j & 3);
+    const bool arow = (j & 3) < mi && ta < nt;
     v4i av[kConvDigits];
 #pragma unroll
     for (int c = 0; c < kConvDigits; ++c)
@@ -654,7 +662,7 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
     double p[kMItems], pinv[kMItems];
 #pragma unroll
     for (int r = 0; r < kMItems; ++r) {
-      to[r] = base + (4 * h + g) * kMItems + r;
+      to[r] = r < mi ? base + (4 * h + g) * mi + r : nt;
       const int tp = C.dst_prime[to[r] < nt ? to[r] : 0];
       p[r] = T.p[tp];
       pinv[r] = T.pinv[tp];
@@ -675,9 +683,10 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
       }
 #pragma unroll
       for (int r = 0; r < kMItems; ++r) {
-        x[r][k] = mconv_fold_add(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
-                                 acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
-                                 acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], rz, p[r], pinv[r]);
+        x[r][k] = r < mi ? mconv_fold_add(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
+                                          acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
+                                          acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], rz, p[r], pinv[r])
+                         : 0.0;
         asm volatile("" : "+v"(x[r][k]));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -685,6 +694,7 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
     if (!SEPX) __syncthreads();
 #pragma unroll
     for (int r = 0; r < kMItems; ++r) {
+      if (r >= mi) break;  // uniform over the block
       const bool act = to[r] < nt;
       const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? to[r] : 0] * kN;
       if (act) col_fwd_lo<true>(x[r], tw, p[r], pinv[r]);
@@ -696,6 +706,7 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
         for (int k = 0; k < 16; ++k) col[4096 * k + j] = x[r][k];
       }
     }
+    base += 8 * mi;
   }
 }
 
