@@ -189,10 +189,15 @@ def rescale(ct: Cipher, ctx: CKKSContext) -> Cipher:
     if ct.is_ext or limbs < 2:
         raise ValueError("rescale needs a non-extended ciphertext with at least two limbs")
     both = _joined(ct.cv, limbs, ctx.N)
-    if both is None:
-        both = u64_cat([_view(c, limbs) for c in ct.cv])
-    out = ctx.rescale_raw(both, limbs)
     B = ct.batch_size
+    if both is not None:
+        out = ctx.rescale_raw(both, limbs)
+    else:
+        # components in separate buffers: each rescaled into its half of one output (no copy of
+        # the input into a joint buffer first)
+        out = ctx.empty(len(ct.cv) * B, limbs - 1, ctx.N)
+        for i, c in enumerate(ct.cv):
+            ctx.rescale_raw(_view(c, limbs), limbs, out=out[i * B:(i + 1) * B])
     parts = [out[i * B:(i + 1) * B] for i in range(len(ct.cv))]
     st = ct.state
     state = st.replace(
