@@ -345,11 +345,10 @@ extern "C" int hck_weighted_sum(const hck_context* ctx, int limbs, int n, int gr
 extern "C" size_t hck_lincomb_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int groups) {
   if (!ctx || level_limbs < 2 || level_limbs > ctx->L || groups < 0) return 0;
   if (!ctx->wide) return hck::lincomb_rescale_bytes(ctx, level_limbs, groups);
-  // the wide path runs the two steps: the combination [groups][ell][N], then the rescale of every
-  // group in one launch sequence (one rescale at a time without the fused wide kernels)
-  const size_t rs = hck::wide_fused_ok(ctx) ? hck::wide_fused_rescale_bytes(ctx, level_limbs, groups)
-                                            : hck::rescale_bytes(ctx, level_limbs, 1);
-  return (size_t)groups * level_limbs * hck::kN * 8 + rs;
+  // the fused wide kernels form the sums where they are used; the separate-launch ones run the two
+  // steps: the combination [groups][ell][N], then one rescale at a time
+  if (hck::wide_fused_ok(ctx)) return hck::wide_fused_rescale_bytes(ctx, level_limbs, groups);
+  return (size_t)groups * level_limbs * hck::kN * 8 + hck::rescale_bytes(ctx, level_limbs, 1);
 }
 
 extern "C" int hck_lincomb_rescale(const hck_context* ctx, int level_limbs, int groups, int terms,
@@ -377,6 +376,8 @@ extern "C" int hck_lincomb_rescale(const hck_context* ctx, int level_limbs, int 
   hipStream_t s = (hipStream_t)stream;
   if (!ctx->wide)
     return hck::lincomb_rescale(ctx, ell, groups, terms, x, weights, out, add, add_mask, (char*)workspace, s);
+  if (hck::wide_fused_ok(ctx))
+    return hck::wide_lincomb_rescale_fused(ctx, ell, groups, terms, x, weights, out, add, add_mask, (char*)workspace, s);
   const long long poly = (long long)ell * hck::kN;
   uint64_t* tmp = (uint64_t*)workspace;
   char* rs_ws = (char*)(tmp + groups * poly);
@@ -384,7 +385,6 @@ extern "C" int hck_lincomb_rescale(const hck_context* ctx, int level_limbs, int 
   for (int g = 0; g < groups; ++g) tptr[g] = tmp + g * poly;
   int rc = hck_lincomb(ctx, ell, groups, terms, x, weights, tptr, stream);
   if (rc) return rc;
-  if (hck::wide_fused_ok(ctx)) return hck::wide_rescale_groups(ctx, ell, groups, tmp, poly, out, add, add_mask, rs_ws, s);
   int prime_idx[hck::kMaxPrimes];
   for (int i = 0; i < ell - 1; ++i) prime_idx[i] = i;
   for (int g = 0; g < groups; ++g) {

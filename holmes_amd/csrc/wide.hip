@@ -729,13 +729,6 @@ __device__ __forceinline__ void wmac_load(WMacOps& o, const WMac& P, int b, int 
   }
 }
 
-// t mod p for t < p 2^64: Montgomery's reduction (t 2^-64, below 2p), then the product with 2^64 mod p.
-__device__ __forceinline__ u64 wfold128(u128 t, u64 p, u64 mneg, u64 r, u64 rs) {
-  const u64 tl = (u64)t, th = (u64)(t >> 64);
-  const u64 m = tl * mneg;
-  const u64 u = th + (u64)(((u128)m * p) >> 64) + (tl != 0 ? 1 : 0);
-  return wmulc(u, r, rs, p);
-}
 
 __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long long baby_stride,
                                                             const u64* __restrict__ pts, long long pt_stride,

@@ -102,10 +102,11 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
 size_t wide_fused_rescale_bytes(const hck_context* c, int ell, int polys);
 int wide_rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
                        uint64_t* out, long long out_stride, char* ws, hipStream_t s);
-// wide_rescale_fused of the groups of a weighted sum, each into its own output, with the optional
-// scalar addend (hck_lincomb_rescale); workspace wide_fused_rescale_bytes(c, ell, groups).
-int wide_rescale_groups(const hck_context* c, int ell, int groups, const uint64_t* in, long long in_stride,
-                        uint64_t* const* out, const uint64_t* add, uint64_t add_mask, char* ws, hipStream_t s);
+// hck_lincomb_rescale on the fused kernels: out[g] = rescale(sum_t w[t] x[g][t]) (+ add on the groups of
+// add_mask) without storing the combination; workspace wide_fused_rescale_bytes(c, ell, groups).
+int wide_lincomb_rescale_fused(const hck_context* c, int ell, int groups, int terms, const uint64_t* const* x,
+                               const uint64_t* w, uint64_t* const* out, const uint64_t* add, uint64_t add_mask,
+                               char* ws, hipStream_t s);
 size_t wide_fused_moddown_bytes(const hck_context* c, int ell, int polys);
 int wide_moddown_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
                        uint64_t* out, long long out_stride, char* ws, hipStream_t s);

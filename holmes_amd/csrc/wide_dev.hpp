@@ -35,6 +35,15 @@ __device__ __forceinline__ uint64_t wmont(uint64_t x, uint64_t k, uint64_t p, ui
   return th + (uint64_t)(((u128_t)m * p) >> 64) + (tl != 0 ? 1 : 0);
 }
 
+// t mod p for t < p 2^64: Montgomery's reduction (t 2^-64, below 2p), then the product with 2^64 mod p
+// (r = 2^64 mod p, rs its Shoup companion); canonical result.
+__device__ __forceinline__ uint64_t wfold128(u128_t t, uint64_t p, uint64_t mneg, uint64_t r, uint64_t rs) {
+  const uint64_t tl = (uint64_t)t, th = (uint64_t)(t >> 64);
+  const uint64_t m = tl * mneg;
+  const uint64_t u = th + (uint64_t)(((u128_t)m * p) >> 64) + (tl != 0 ? 1 : 0);
+  return wmulc(u, r, rs, p);
+}
+
 // The int8 matrix-core base conversion's operands and fold (wide.hip: wk_mconv, wide_fused.hip).
 // Each source residue is centered (|ybar| < b / 2 < 2^60) and written as the 64-bit word of its eight
 // balanced base-256 digits (byte a = d_a + 128 of ybar + 0x80..80; the XOR turns each byte into d_a as

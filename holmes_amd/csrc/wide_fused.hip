@@ -565,32 +565,72 @@ __global__ __launch_bounds__(kT) void wf_rows_finish(const u64* __restrict__ t4,
   for (int k = 0; k < 16; ++k) o[16 * k] = wcanon2(mulshoup_lazy(a[k] + 8 * p - x[k], w, ws, p), p);
 }
 
-// wf_rows_finish with one output pointer per polynomial (the groups of a weighted sum with its
-// rescale) and a canonical residue added on the polynomials of add_mask.
-struct WGroupOut {
+// ----------------------------------------------------------------- weighted sums with their rescale
+// out[g] = rescale(sum_t w[t] x[g][t]) (+ add on the groups of add_mask), the combination never
+// stored (hck_lincomb_rescale): wf_lc_intt_last forms the sum of the last limb and runs its INTT rows,
+// the conversion lifts it to the lower primes, and wf_lc_finish forms each lower limb's sum again and
+// finishes it with the NTT rows of the lift.  The sums are exact 128-bit sums of products of canonical
+// words (each below p^2), folded once every kLcFold terms (a folded residue plus kLcFold - 1 products
+// stays below p 2^64 for p < 2^60).
+struct WLcRsArgs {
+  const u64* x[kLcRsPtrs];  // group-major: x[g * terms + t]
   u64* out[kLcRsGroups];
   u64 add[kMaxPrimes];
   unsigned long long add_mask;
 };
+constexpr int kLcFold = 15;
 
-__global__ __launch_bounds__(kT) void wf_rows_finish_groups(const u64* __restrict__ t4, const u64* __restrict__ xq,
-                                                            long long xq_stride, const WGroupOut O, int limbs,
-                                                            const u64* __restrict__ inv,
-                                                            const u64* __restrict__ inv_s, WideTables T) {
+// sum_t w[t][i] x[g][t] at limb i (prime pi) of row group rg's natural words na + 16 k, canonical
+__device__ __forceinline__ void wlc_tile(u64 (&x)[16], const WLcRsArgs& A, int g, int terms,
+                                         const u64* __restrict__ w, int wlimbs, int i, int pi, long long na,
+                                         const WideTables& T) {
+  const u64 p = T.p[pi], mneg = T.mneg[pi], r = T.r64[pi], rs = T.r64_s[pi];
+  u128_t acc[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) acc[k] = 0;
+  for (int t = 0; t < terms; ++t) {
+    const u64* xs = A.x[g * terms + t] + (long long)i * kN + na;
+    const u64 wt = w[(long long)t * wlimbs + i];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[k] += (u128_t)xs[16 * k] * wt;
+    if (t % kLcFold == kLcFold - 1 && t + 1 < terms) {  // uniform
+#pragma unroll
+      for (int k = 0; k < 16; ++k) acc[k] = wfold128(acc[k], p, mneg, r, rs);
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 16; ++k) x[k] = wfold128(acc[k], p, mneg, r, rs);
+}
+
+// Grid (16, groups): the last limb's sum, its INTT rows into the workspace layout
+__global__ __launch_bounds__(kT) void wf_lc_intt_last(const WLcRsArgs A, int terms, const u64* __restrict__ w, int ell,
+                                                      u64* __restrict__ tl, WideTables T) {
   __shared__ u64 S[kRowLds];
-  const int pl = blockIdx.x, rg = blockIdx.y, i = blockIdx.z;
+  const int rg = blockIdx.x, g = blockIdx.y, pi = ell - 1;
+  u64 x[16];
+  wlc_tile(x, A, g, terms, w, ell, pi, pi, nat_a(rg), T);
+  wrows_inv_to_t(x, tl + (long long)g * kN, rg, S, T.inv + (size_t)pi * kN, T.inv_s + (size_t)pi * kN, T.p[pi]);
+}
+
+// Grid (groups, 16, ell - 1): out[g][i] = (sum_t w[t][i] x[g][t][i] - NTT rows(T4[g][i])) q_{ell-1}^-1
+// (+ add[i]); the NTT rows pass leaves v below 8p
+__global__ __launch_bounds__(kT) void wf_lc_finish(const WLcRsArgs A, int terms, const u64* __restrict__ w, int ell,
+                                                   const u64* __restrict__ t4, const u64* __restrict__ inv,
+                                                   const u64* __restrict__ inv_s, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const int g = blockIdx.x, rg = blockIdx.y, i = blockIdx.z, nt = ell - 1;
   const u64 p = T.p[i];
   const long long na = nat_a(rg);
   u64 x[16], a[16];
-  load_t(x, t4 + ((long long)pl * limbs + i) * kN, rg);
-  load_gal_raw(a, xq + (long long)pl * xq_stride + (long long)i * kN, na, 1u);
+  load_t(x, t4 + ((long long)g * nt + i) * kN, rg);
+  wlc_tile(a, A, g, terms, w, ell, i, i, na, T);
   wrows_fwd_t(x, rg, S, T.fwd + (size_t)i * kN, T.fwd_s + (size_t)i * kN, p);
-  const u64 w = inv[i], ws = inv_s[i];
-  const bool add = (O.add_mask >> pl) & 1ull;  // uniform
-  const u64 av = add ? O.add[i] : 0;
-  u64* o = O.out[pl] + (long long)i * kN + na;
+  const u64 wv = inv[i], wvs = inv_s[i];
+  const bool add = (A.add_mask >> g) & 1ull;  // uniform
+  const u64 av = add ? A.add[i] : 0;
+  u64* o = A.out[g] + (long long)i * kN + na;
 #pragma unroll
-  for (int k = 0; k < 16; ++k) o[16 * k] = wadd(wcanon2(mulshoup_lazy(a[k] + 8 * p - x[k], w, ws, p), p), av, p);
+  for (int k = 0; k < 16; ++k) o[16 * k] = wadd(wcanon2(mulshoup_lazy(a[k] + 8 * p - x[k], wv, wvs, p), p), av, p);
 }
 
 // ----------------------------------------------------------------- hoisted rotations
@@ -841,33 +881,30 @@ int wide_rescale_fused(const hck_context* c, int ell, int polys, const uint64_t*
   return HCK_OK;
 }
 
-// wide_rescale_fused over the groups of a weighted sum: in [groups][ell] contiguous (stride in_stride),
-// group g rescaled into out[g] ([ell - 1] limbs), add[i] added on the groups of add_mask.  One launch
-// sequence for all groups; the residues are those of one rescale per group.
-int wide_rescale_groups(const hck_context* c, int ell, int groups, const uint64_t* in, long long in_stride,
-                        uint64_t* const* out, const uint64_t* add, uint64_t add_mask, char* ws, hipStream_t s) {
+// hck_lincomb_rescale on the fused kernels (the weighted sums are formed where they are used);
+// workspace wide_fused_rescale_bytes(c, ell, groups)
+int wide_lincomb_rescale_fused(const hck_context* c, int ell, int groups, int terms, const uint64_t* const* x,
+                               const uint64_t* w, uint64_t* const* out, const uint64_t* add, uint64_t add_mask,
+                               char* ws, hipStream_t s) {
   if (groups < 1) return HCK_OK;
-  if (groups > kLcRsGroups || ell < 2) return HCK_ERR_ARG;
+  if (ell < 2 || groups > kLcRsGroups || terms < 1 || (long long)groups * terms > kLcRsPtrs || !w) return HCK_ERR_ARG;
   const WideState& W = *c->wide;
   const long long n = kN;
   const int nt = ell - 1;
   u64* tl = (u64*)ws;                    // [groups][1]
   u64* t4 = tl + (long long)groups * n;  // [groups][ell - 1]
-  WGalF G{};
-  G.uniform = 1u;
-  WGroupOut O{};
-  for (int g = 0; g < groups; ++g) O.out[g] = out[g];
+  WLcRsArgs A{};
+  for (int j = 0; j < groups * terms; ++j) A.x[j] = x[j];
+  for (int g = 0; g < groups; ++g) A.out[g] = out[g];
   if (add)
-    for (int i = 0; i < nt; ++i) O.add[i] = add[i];
-  O.add_mask = add ? add_mask : 0ull;
-  wf_intt_rows<<<dim3(((16 + kXcds - 1) / kXcds) * kXcds * groups), kT, 0, s>>>(in, in_stride, G, ell - 1, ell - 1,
-                                                                                tl, 1, groups, W.t);
+    for (int i = 0; i < nt; ++i) A.add[i] = add[i];
+  A.add_mask = add ? add_mask : 0ull;
+  wf_lc_intt_last<<<dim3(16, groups), kT, 0, s>>>(A, terms, w, ell, tl, W.t);
   HCK_CHECK_LAUNCH();
   launch_wconv_fused(WConvArgs{tl, n, 0, 0, t4, (long long)nt * n, 0, W.rescale + ell, 0}, nt, dim3(128, 1, groups), W, s);
   HCK_CHECK_LAUNCH();
   const size_t lv = (size_t)ell * c->L;
-  wf_rows_finish_groups<<<dim3(groups, 16, nt), kT, 0, s>>>(t4, in, in_stride, O, nt, W.qlast_inv + lv,
-                                                            W.qlast_inv_s + lv, W.t);
+  wf_lc_finish<<<dim3(groups, 16, nt), kT, 0, s>>>(A, terms, w, ell, t4, W.qlast_inv + lv, W.qlast_inv_s + lv, W.t);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }
