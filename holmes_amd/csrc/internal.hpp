@@ -139,8 +139,9 @@ int ks_hoisted(const hck_context* c, int ell, int inputs, int items, const uint3
 // ks_fused followed by rescale_fused in one pass: out = rescale((sigma(add) + acc_b, acc_a) +
 // KeySwitch(sigma(d))) at ell - 1 limbs, bit-identical to the two steps; the q_{ell-1} limb joins
 // the ModDown sources (see ConvConsts::z_n0).  add and the acc pair are nullable (relinearisation:
-// acc = (d0, d1); rotation: add = c0).  Matrix-core conversion engine, FP64 contexts, ell >= 2
-// only (HCK_ERR_UNSUPPORTED otherwise).  Workspace ks_rs_bytes.
+// acc = (d0, d1); rotation: add = c0).  Matrix-core conversion engine and ell >= 2 only: FP64
+// contexts, or wide ones with wide_fused_ok (wide_ks_rescaled; HCK_ERR_UNSUPPORTED otherwise).
+// Workspace ks_rs_bytes.
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch);
 // Post-ops on the ell - 1 output limbs: out <- (twice ? 2 out : out) - sub (+ scalar[i] on out_b);
 // sub_b / sub_a ([>= ell - 1] limbs per item at sub_stride) and scalar (ell - 1 canonical residues)

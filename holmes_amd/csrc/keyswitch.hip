@@ -3,6 +3,7 @@
 
 #include "../../include/holmes_ckks.h"
 #include "internal.hpp"
+#include "wide.hpp"
 
 namespace hck {
 namespace {
@@ -113,7 +114,7 @@ extern "C" int hck_rotate(const hck_context* ctx, int level_limbs, int batch, ui
 // rotation's ModDown and the rescale share the conversion), otherwise the rotation into the
 // workspace and then the rescale.  Both give the same residues.
 static bool rotate_rescale_fused(const hck_context* ctx, int ell) {
-  return !ctx->wide && ctx->conv_engine == 1 && ell >= 2;
+  return ell >= 2 && (ctx->wide ? hck::wide_fused_ok(ctx) : ctx->conv_engine == 1);
 }
 
 static size_t rotate_rescale_ks_bytes(const hck_context* ctx, int ell, int chunk) {

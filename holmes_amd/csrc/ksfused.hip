@@ -1510,6 +1510,7 @@ int ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, long l
 }
 
 size_t ks_rs_bytes(const hck_context* c, int ell, int batch) {
+  if (c->wide) return wide_fused_rs_bytes(c, ell, batch);
   const size_t beta = beta_of(c, ell), ext_l = ell + c->K;
   return (size_t)batch * kN * 8 * (2 * ell + beta * ext_l + 2 * (c->K + 1));
 }
@@ -1520,7 +1521,11 @@ int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, lon
                 char* ws, hipStream_t s, int twice, const uint64_t* sub_b, const uint64_t* sub_a,
                 long long sub_stride, const uint64_t* scalar, const uint64_t* const* prod_ab, long long a_stride,
                 long long b_stride) {
-  if (c->wide || c->conv_engine != 1 || ell < 2) return HCK_ERR_UNSUPPORTED;
+  if (c->wide)
+    return wide_ks_rescaled(c, ell, batch, d, d_stride, galois, ksk, add, add_stride, acc_b, acc_a, acc_stride, out_b,
+                            out_a, out_stride, ws, s, twice, sub_b, sub_a, sub_stride, scalar, prod_ab, a_stride,
+                            b_stride);
+  if (c->conv_engine != 1 || ell < 2) return HCK_ERR_UNSUPPORTED;
   if (c->alpha > kSrcMax || c->K > kSrcMax) return HCK_ERR_UNSUPPORTED;
   if (batch < 1 || batch > kMaxBatchF || (acc_b == nullptr) != (acc_a == nullptr)) return HCK_ERR_ARG;
   const GalF G = gal_uniform(galois);

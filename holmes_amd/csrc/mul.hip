@@ -196,7 +196,8 @@ extern "C" int hck_mul_relin(const hck_context* ctx, int level_limbs, int batch,
 // rescale share one pass (ks_rescaled); otherwise hck_mul_relin into the workspace, then the
 // rescale.  Both give the same residues.
 static bool relin_rescale_fused(const hck_context* ctx, int ell) {
-  return !ctx->wide && ctx->conv_engine == 1 && ell >= 2 && ctx->alpha <= hck::kMaxAlpha && ctx->K <= hck::kMaxSpecial;
+  if (ctx->wide) return ell >= 2 && hck::wide_fused_ok(ctx);
+  return ctx->conv_engine == 1 && ell >= 2 && ctx->alpha <= hck::kMaxAlpha && ctx->K <= hck::kMaxSpecial;
 }
 
 extern "C" size_t hck_mul_relin_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch) {
@@ -264,9 +265,15 @@ int mul_relin_rescale_post(const hck_context* ctx, int level_limbs, int batch, c
     int rc;
     if (fused) {
       // d2 everywhere and d0 / d1 on the last limb; the finish forms d0 / d1 of the other limbs
-      hck::k_tensor_d2<<<dim3(hck::kN / 256, ell, nb), 256, 0, s>>>(a0 + ai, a1 + ai, a_stride, b0 + bi, b1 + bi,
-                                                                   b_stride, d0, d1, d2, poly, ell, ctx->dev);
-      HCK_CHECK_LAUNCH();
+      if (ctx->wide) {
+        rc = hck::wide_tensor_d2(ctx, ell, nb, a0 + ai, a1 + ai, a_stride, b0 + bi, b1 + bi, b_stride, d0, d1, d2, poly,
+                                 s);
+        if (rc) return rc;
+      } else {
+        hck::k_tensor_d2<<<dim3(hck::kN / 256, ell, nb), 256, 0, s>>>(a0 + ai, a1 + ai, a_stride, b0 + bi, b1 + bi,
+                                                                     b_stride, d0, d1, d2, poly, ell, ctx->dev);
+        HCK_CHECK_LAUNCH();
+      }
       const uint64_t* ab[4] = {a0 + ai, a1 + ai, b0 + bi, b1 + bi};
       rc = hck::ks_rescaled(ctx, ell, nb, d2, poly, 1u, keys, nullptr, 0, d0, d1, poly, out0 + oi, out1 + oi,
                             out_stride, ks_ws, s, twice, sub0 ? sub0 + si : nullptr, sub1 ? sub1 + si : nullptr,

@@ -642,16 +642,18 @@ __global__ __launch_bounds__(256) void wk_poly_op(u64* out, const u64* a, const 
 __global__ __launch_bounds__(256) void wk_tensor(const u64* __restrict__ a0, const u64* __restrict__ a1, long long as,
                                                  const u64* __restrict__ b0, const u64* __restrict__ b1, long long bs,
                                                  u64* __restrict__ d0, u64* __restrict__ d1, u64* __restrict__ d2,
-                                                 long long dst, WideTables T) {
+                                                 long long dst, int d01_from, WideTables T) {
   const int k = blockIdx.x * 256 + threadIdx.x;
   const int i = blockIdx.y;
   const long long z = blockIdx.z;
   const Barrett64 br = wbar(T, i);
   const long long lo = (long long)i * kN + k;
-  const u64 x0 = a0[z * as + lo], x1 = a1[z * as + lo], y0 = b0[z * bs + lo], y1 = b1[z * bs + lo];
+  const u64 x1 = a1[z * as + lo], y1 = b1[z * bs + lo];
+  d2[z * dst + lo] = mulmod64(x1, y1, br);
+  if (i < d01_from) return;  // d0 / d1 only on limbs d01_from.. (uniform over the block)
+  const u64 x0 = a0[z * as + lo], y0 = b0[z * bs + lo];
   d0[z * dst + lo] = mulmod64(x0, y0, br);
   d1[z * dst + lo] = wadd(mulmod64(x0, y1, br), mulmod64(x1, y0, br), br.p);
-  d2[z * dst + lo] = mulmod64(x1, y1, br);
 }
 
 __global__ __launch_bounds__(256) void wk_weighted_sum(const u64* __restrict__ in, long long in_stride, int n,
@@ -1005,7 +1007,8 @@ int wide_init(hck_context* c) {
     r64[i] = (u64)(((u128)1 << 64) % q);
     r64_s[i] = shoup_companion(r64[i], q);
   }
-  std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1)), rescale((size_t)(L + 1));
+  std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1)), rescale((size_t)(L + 1)),
+      mdrs((size_t)(L + 1));
   std::vector<u64> ql((size_t)(L + 1) * L, 0), ql_s((size_t)(L + 1) * L, 0);
   for (int ell = 1; ell <= L; ++ell) {
     const int beta = (ell + alpha - 1) / alpha;
@@ -1034,6 +1037,30 @@ int wide_init(hck_context* c) {
         rs_slot.push_back(i);
       }
       fill_wide_conv(rescale[ell], P, rs_src, rs_dst, rs_slot);
+      // ModDown fused with the rescale: the ModDown sums of q_0 .. q_{ell-2} times P^-1, q_{ell-1} as
+      // the extra target nt (its factors times P^-1 as well), P^-1 folded into Z's inverse transform
+      WideConv& fc = mdrs[ell];
+      fill_wide_conv(fc, P, src, rs_dst, rs_slot);
+      for (int t = 0; t <= fc.nt; ++t) {
+        const int qi = t < fc.nt ? rs_dst[t] : ell - 1;
+        const u64 q = P[qi];
+        for (int sidx = 0; sidx < fc.ns; ++sidx) {
+          u64 v = pinv[qi];
+          for (int r = 0; r < fc.ns; ++r)
+            if (r != sidx) v = hmul(v, P[src[r]] % q, q);
+          fc.hmod[sidx][t] = v;
+          fc.hmod_s[sidx][t] = shoup_companion(v, q);
+          fc.hmod_m[sidx][t] = (u64)(((u128)v << 64) % q);
+        }
+      }
+      fc.dst_prime[fc.nt] = ell - 1;
+      fc.dst_slot[fc.nt] = ell - 1;
+      const u64 ql = P[ell - 1], z0 = hmul(ninv[ell - 1], pinv[ell - 1], ql);
+      const u64 z1 = hmul(z0, inv[(size_t)(ell - 1) * n + 1], ql);
+      fc.z_n0 = z0;
+      fc.z_n0_s = shoup_companion(z0, ql);
+      fc.z_n1 = z1;
+      fc.z_n1_s = shoup_companion(z1, ql);
     }
     for (int i = 0; i + 1 < ell; ++i) {
       const u64 v = hinv(P[ell - 1] % P[i], P[i]);
@@ -1057,6 +1084,7 @@ int wide_init(hck_context* c) {
   for (WideConv& cc : modup) fold_inverse(cc);
   for (WideConv& cc : moddown) fold_inverse(cc);
   for (WideConv& cc : rescale) fold_inverse(cc);
+  for (WideConv& cc : mdrs) fold_inverse(cc);
 
   // The matrix-core conversion's fold needs every target prime above 2^46 (|byte-position sum| < 2^45).
   bool mconv = true;
@@ -1068,6 +1096,7 @@ int wide_init(hck_context* c) {
       for (int j = 0; j < beta; ++j) fill_wide_digits(modup[(size_t)ell * bmax + j], P, dig);
       fill_wide_digits(moddown[ell], P, dig);
       if (ell >= 2) fill_wide_digits(rescale[ell], P, dig);
+      if (ell >= 2) fill_wide_digits(mdrs[ell], P, dig);
     }
   }
 
@@ -1086,7 +1115,7 @@ int wide_init(hck_context* c) {
       {modup.data(), modup.size() * sizeof(WideConv)}, {moddown.data(), moddown.size() * sizeof(WideConv)},
       {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8}, {dig.data(), dig.size()},
       {mneg.data(), np * 8}, {r64.data(), np * 8}, {r64_s.data(), np * 8},
-      {rescale.data(), rescale.size() * sizeof(WideConv)},
+      {rescale.data(), rescale.size() * sizeof(WideConv)}, {mdrs.data(), mdrs.size() * sizeof(WideConv)},
   };
   size_t off = 0;
   for (Part& pt : parts) {
@@ -1136,6 +1165,7 @@ int wide_init(hck_context* c) {
   T.r64 = (const u64*)at(21);
   T.r64_s = (const u64*)at(22);
   ws->rescale = (WideConv*)at(23);
+  ws->mdrs = (WideConv*)at(24);
   ws->primes_below_2_60 = true;
   for (int i = 0; i < c->np; ++i) ws->primes_below_2_60 = ws->primes_below_2_60 && c->primes[i] < (1ULL << 60);
   c->wide = ws;
@@ -1551,8 +1581,17 @@ int wide_poly_op(const hck_context* c, int op, uint64_t* out, const uint64_t* a,
 int wide_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
                 const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1, uint64_t* d2,
                 long long d_stride, hipStream_t s) {
-  wk_tensor<<<dim3(kN / 256, ell, batch), 256, 0, s>>>(a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride,
+  wk_tensor<<<dim3(kN / 256, ell, batch), 256, 0, s>>>(a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride, 0,
                                                        c->wide->t);
+  HCK_CHECK_LAUNCH();
+  return HCK_OK;
+}
+
+int wide_tensor_d2(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1,
+                   long long a_stride, const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0,
+                   uint64_t* d1, uint64_t* d2, long long d_stride, hipStream_t s) {
+  wk_tensor<<<dim3(kN / 256, ell, batch), 256, 0, s>>>(a0, a1, a_stride, b0, b1, b_stride, d0, d1, d2, d_stride,
+                                                       ell - 1, c->wide->t);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
 }

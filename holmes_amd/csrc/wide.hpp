@@ -36,6 +36,12 @@ struct WideConv {
   // offset (in 16-byte operand units) of this conversion's digit table in WideState::conv_dig.
   double fold_inv[kMaxPrimes];
   long long dig_off;
+  // ModDown fused with the rescale (WideState::mdrs): sources the P primes, stored targets
+  // q_0 .. q_{ell-2} with hmod[s][t] = (P / p_s mod q_t) P^-1; q_{ell-1} rides along as target nt
+  // (hmod[s][nt], dst_prime[nt], no digit table), and the extra source limb Z (the q_{ell-1} limb of
+  // P * acc + IP) leaves its inverse transform multiplied by P^-1: z_n0 = N^-1 P^-1,
+  // z_n1 = N^-1 psi_rev_inv[1] P^-1 (mod q_{ell-1}).
+  uint64_t z_n0, z_n0_s, z_n1, z_n1_s;
 };
 
 struct WideTables {
@@ -65,6 +71,7 @@ struct WideState {
   WideConv* modup = nullptr;     // [(L + 1) * beta_max]
   WideConv* moddown = nullptr;   // [L + 1]: P primes -> q_0 .. q_{ell-1}
   WideConv* rescale = nullptr;   // [L + 1]: level ell lifts q_{ell-1} to q_0 .. q_{ell-2} (the fused rescale)
+  WideConv* mdrs = nullptr;      // [L + 1]: level ell's ModDown fused with the rescale (ell >= 2)
   uint64_t* qlast_inv = nullptr; // [(L + 1) * L]: level ell, prime i: q_{ell-1}^-1 mod q_i
   uint64_t* qlast_inv_s = nullptr;
   // int8 operands of the matrix-core base conversion (every modup / moddown table, at dig_off), or
@@ -99,6 +106,15 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
                   const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
                   long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
                   long long ext_stride, const uint32_t* galois_items);
+// ks_rescaled's wide body (same arguments and semantics): the key switch's ModDown and the rescale by
+// q_{ell-1} in one conversion, on contexts with wide_fused_ok; workspace wide_fused_rs_bytes.
+size_t wide_fused_rs_bytes(const hck_context* c, int ell, int batch);
+int wide_ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
+                     uint32_t galois, const uint64_t* const* ksk, const uint64_t* add, long long add_stride,
+                     const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride, uint64_t* out_b,
+                     uint64_t* out_a, long long out_stride, char* ws, hipStream_t s, int twice,
+                     const uint64_t* sub_b, const uint64_t* sub_a, long long sub_stride, const uint64_t* scalar,
+                     const uint64_t* const* prod_ab, long long a_stride, long long b_stride);
 size_t wide_fused_rescale_bytes(const hck_context* c, int ell, int polys);
 int wide_rescale_fused(const hck_context* c, int ell, int polys, const uint64_t* in, long long in_stride,
                        uint64_t* out, long long out_stride, char* ws, hipStream_t s);
@@ -140,6 +156,11 @@ int wide_poly_op(const hck_context* c, int op, uint64_t* out, const uint64_t* a,
 int wide_tensor(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1, long long a_stride,
                 const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0, uint64_t* d1, uint64_t* d2,
                 long long d_stride, hipStream_t s);
+// The tensor terms a rescaled product reads (ks_rescaled with prod_ab): d2 = a1 b1 on every limb,
+// d0 = a0 b0 and d1 = a0 b1 + a1 b0 on the last limb only.
+int wide_tensor_d2(const hck_context* c, int ell, int batch, const uint64_t* a0, const uint64_t* a1,
+                   long long a_stride, const uint64_t* b0, const uint64_t* b1, long long b_stride, uint64_t* d0,
+                   uint64_t* d1, uint64_t* d2, long long d_stride, hipStream_t s);
 int wide_weighted_sum(const hck_context* c, int limbs, int n, int groups, const uint64_t* in, long long in_stride,
                       const uint64_t* w, uint64_t* out, long long out_stride, hipStream_t s);
 int wide_lincomb(const hck_context* c, int limbs, int groups, int terms, const uint64_t* const* x,

@@ -73,4 +73,21 @@ __device__ __forceinline__ uint64_t wfold(const wv4i (&a)[8], int r, uint64_t t,
   return (uint64_t)v;
 }
 
+// wfold of the conversion sum plus a signed term z (|z| < 2^60): the sum x + z, |x + z| < 2^76.02, is
+// estimated in double with an absolute error below 2^26, so the quotient estimate still leaves the
+// remainder in (-t, t) for t > 2^46.
+__device__ __forceinline__ uint64_t wfold_add(const wv4i (&a)[8], int r, uint64_t t, double tinv, long long z) {
+  const int p0 = a[0][r] + a[1][r] * 256, p1 = a[2][r] + a[3][r] * 256;
+  const int p2 = a[4][r] + a[5][r] * 256, p3 = a[6][r] + a[7][r] * 256;
+  const double xd = __builtin_fma(__builtin_fma(__builtin_fma((double)p3, 65536.0, (double)p2), 65536.0, (double)p1),
+                                  65536.0, (double)p0) +
+                    (double)z;
+  const long long qq = (long long)__builtin_rint(xd * tinv);
+  const uint64_t xl = (uint64_t)(long long)p0 + ((uint64_t)(long long)p1 << 16) + ((uint64_t)(long long)p2 << 32) +
+                      ((uint64_t)(long long)p3 << 48) + (uint64_t)z;
+  long long v = (long long)(xl - (uint64_t)qq * t);
+  if (v < 0) v += (long long)t;
+  return (uint64_t)v;
+}
+
 }  // namespace hck

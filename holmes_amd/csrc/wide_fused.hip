@@ -275,12 +275,21 @@ struct WConvArgs {
   long long dst_zs, dst_ys;
   const WideConv* cc_base;
   int cc_y;
+  const u64* zsrc;  // RS: the extra source limb Z, group (z, y) at zsrc + z src_zs + y src_ys
 };
 
-template <bool SEPX>
+// RS (the ModDown fused with the rescale, WideState::mdrs): after phase 1, slots 0 and 1 also run the
+// INTT cols of Z, the q_{ell-1} limb of P * acc + IP (P^-1 folded into its last stage); phase 1c
+// forms, for every coefficient of the two columns, the centered residue
+// r = [Z P^-1 - sum_s ybar_s hmod[s][nt]]_{q_{ell-1}}, the q_{ell-1} limb of the ModDown output in
+// the coefficient domain; phase 2 adds r to every stored target's sum (whose factors carry P^-1).
+// With the finish of wf_rows_ipq_rs this gives ((IP - NTT(conv)) P^-1 + acc - NTT(r)) q_{ell-1}^-1,
+// the ModDown followed by the rescale, exactly.
+template <bool SEPX, bool RS = false>
 __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTables T, const wv4i* __restrict__ dig) {
   __shared__ u64 D[16 * kYStride];
   __shared__ u64 X[SEPX ? 16 * kYStride : 1];
+  __shared__ long long Z[RS ? 2 * kYStride : 1];
   const int y = blockIdx.y;
   const long long z = blockIdx.z;
   const WideConv& C = A.cc_base[y * A.cc_y];
@@ -311,8 +320,41 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
     // an idle source stores zero digits
 #pragma unroll
     for (int k = 0; k < 16; ++k) R[j + 16 * k] = act ? wdigits(x[k], p) : 0ULL;
+    if constexpr (RS) {
+      if (sigma < 2) {  // phase 1b (one wave): Z P^-1 of column cl, canonical, into run cl of Z
+        const int zp = C.dst_prime[nt];
+        const u64 pz = T.p[zp];
+        const u64* __restrict__ twz = T.inv + (size_t)zp * kN;
+        const u64* __restrict__ twzs = T.inv_s + (size_t)zp * kN;
+        const u64* col = A.zsrc + z * A.src_zs + y * A.src_ys + (long long)(c0 + cl) * 16;
+#pragma unroll
+        for (int k = 0; k < 16; ++k) x[k] = col[4096 * k + j];
+        wcol_inv_hi(x, j, twz, twzs, pz);
+        u64* RZ = reinterpret_cast<u64*>(Z) + cl * kYStride;
+        col_b_to_a(x, RZ, j);
+        wcol_inv_lo(x, twz, twzs, C.z_n0, C.z_n0_s, C.z_n1, C.z_n1_s, pz);
+#pragma unroll
+        for (int k = 0; k < 16; ++k) RZ[j + 16 * k] = x[k];
+      }
+    }
   }
   __syncthreads();
+  if constexpr (RS) {  // phase 1c: r for the 512 coefficients of the two columns, two per thread
+    const u64 pz = T.p[C.dst_prime[nt]];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int q = t + 256 * u, cl = q >> 8, pos = q & 255;
+      u64 acc = 0;
+      for (int s = 0; s < ns; ++s) {  // ybar_s hmod[s][nt] with the sign of the centered digit word
+        const long long yb = (long long)((D[(2 * s + cl) * kYStride + pos] ^ kDigitBias) - kDigitBias);
+        const u64 m = wmulc(yb < 0 ? 0ULL - (u64)yb : (u64)yb, C.hmod[s][nt], C.hmod_s[s][nt], pz);
+        acc = yb < 0 ? wsub(acc, m, pz) : wadd(acc, m, pz);
+      }
+      const u64 v = wsub((u64)Z[cl * kYStride + pos], acc, pz);
+      Z[cl * kYStride + pos] = 2 * v > pz ? (long long)v - (long long)pz : (long long)v;
+    }
+    __syncthreads();
+  }
   // phase 2
   const int w = t >> 6, g = (t >> 4) & 3;
   const int cl = w >> 1, h = w & 1;
@@ -355,9 +397,11 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
         w0 = B0[16 * (k + 1)];
         w1 = B1[16 * (k + 1)];
       }
+      const long long rz = RS ? Z[cl * kYStride + j + 16 * k] : 0;  // row j + 16k of column cl
 #pragma unroll
       for (int r = 0; r < kMItems; ++r) {
-        x[r][k] = r < mi ? wfold(acc, r, pr[r], tinv[r]) : 0;
+        if constexpr (RS) x[r][k] = r < mi ? wfold_add(acc, r, pr[r], tinv[r], rz) : 0;
+        else x[r][k] = r < mi ? wfold(acc, r, pr[r], tinv[r]) : 0;
         asm volatile("" : "+v"(x[r][k]));
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -483,12 +527,31 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ip(const WIp I, const WGalF G, 
     }
     return;
   }
-  const int K = I.K;
-  u64* o = accp + ((long long)b * 2 * K + (e - e0)) * kN;
+  // ACCP holds tiles / 16 limbs per component from e0 on: the K special limbs, or (ModDown fused with
+  // the rescale, e0 = ell - 1) the q_{ell-1} limb first, as Z = IP + P (sigma(add) + acc)
+  const int k1 = tiles >> 4;
+  if (e < I.ell) {
+    const u64 pm = T.pmod[pi], pms = T.pmod_s[pi];
+    if (add) {
+      load_gal_raw(x, add + (long long)b * add_stride + (long long)e * kN, na, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) sb[k] = wadd(sb[k], wmulc(x[k], pm, pms, p), p);
+    }
+    if (acc_b) {
+      const u64* ab = acc_b + (long long)b * acc_stride + (long long)e * kN + na;
+      const u64* aa = acc_a + (long long)b * acc_stride + (long long)e * kN + na;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        sb[k] = wadd(sb[k], wmulc(ab[16 * k], pm, pms, p), p);
+        sa[k] = wadd(sa[k], wmulc(aa[16 * k], pm, pms, p), p);
+      }
+    }
+  }
+  u64* o = accp + ((long long)b * 2 * k1 + (e - e0)) * kN;
   const u64* twi = T.inv + (size_t)pi * kN;
   const u64* twis = T.inv_s + (size_t)pi * kN;
   wrows_inv_to_t(sb, o, rg, S, twi, twis, p);
-  wrows_inv_to_t(sa, o + (long long)K * kN, rg, S, twi, twis, p);
+  wrows_inv_to_t(sa, o + (long long)k1 * kN, rg, S, twi, twis, p);
 }
 
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
@@ -541,6 +604,96 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ipq(const WIp I, const WGalF G,
 #pragma unroll
   for (int k = 0; k < 16; ++k) sa[k] = Park[k * kT + threadIdx.x];
   finish(sa, 1, nullptr, acc_a, out_a);
+}
+
+// ----------------------------------------------------------------- K5 of the ModDown fused with the rescale
+// Q limbs i < ell - 1: out = (IP P^-1 - v + sigma_g(add) + acc) q_{ell-1}^-1, v the NTT rows pass of
+// T4 = conv P^-1 + r ([item][2][ell - 1], workspace layout; below 8p), then the post-ops
+// out <- (twice ? 2 out : out) - sub (+ scalar[i] on out_b).  With a0 .. b1 set the accumulators are
+// the tensor terms a0 b0 and a0 b1 + a1 b0, formed here.
+struct WRsPost {
+  const u64 *sub_b, *sub_a;
+  long long sub_stride;
+  int twice, has_scalar;
+  u64 scalar[kMaxPrimes];
+  const u64 *a0, *a1, *b0, *b1;
+  long long a_stride, b_stride;
+  const u64 *ql, *ql_s;  // q_{ell-1}^-1 mod q_i and its companion at this level
+};
+
+__global__ __launch_bounds__(kT, 2) void wf_rows_ipq_rs(const WIp I, const WGalF G, WKeysF keys, int batch,
+                                                        const u64* __restrict__ t4, const u64* __restrict__ add,
+                                                        long long add_stride, const u64* __restrict__ acc_b,
+                                                        const u64* __restrict__ acc_a, long long acc_stride,
+                                                        u64* __restrict__ out_b, u64* __restrict__ out_a,
+                                                        long long out_stride, const WRsPost post, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  __shared__ u64 Park[16 * kT];  // sa while sb is finished
+  const int nq = I.ell - 1;
+  const TileId id = decode_tile(batch, blockIdx.x);
+  if (id.tile >= 16 * nq) return;
+  const int b = id.b, i = id.tile >> 4, rg = id.tile & 15;
+  const uint32_t g = gal_of(G, b);
+  const u64 p = T.p[i], mneg = T.mneg[i];
+  const u64* tw = T.fwd + (size_t)i * kN;
+  const u64* tws = T.fwd_s + (size_t)i * kN;
+  WIp Ib = I;
+  Ib.key = keys.k[b];
+  u64 sb[16], sa[16], x[16];
+  wtile_ip(sb, sa, x, Ib, b, i, i, rg, g, S, tw, tws, T);
+  const long long na = nat_a(rg);
+  const u64 pv = T.pinv[i], pvs = T.pinv_s[i], ql = post.ql[i], qls = post.ql_s[i];
+  const u64 r64 = T.r64[i], r64s = T.r64_s[i];
+  const bool prod = post.a0 != nullptr;
+  const long long ao = (long long)b * post.a_stride + (long long)i * kN + na;
+  const long long bo = (long long)b * post.b_stride + (long long)i * kN + na;
+  const long long so = (long long)b * post.sub_stride + (long long)i * kN + na;
+  // x1 y1 (+ x2 y2): Montgomery products of canonical words (each below 2p), one product by 2^64 mod p
+  auto finish = [&](u64 (&s)[16], int comp, const u64* addend, const u64* ac, const u64* sub, u64 scal,
+                    const u64* x1, const u64* y1, const u64* x2, const u64* y2, u64* out) {
+    load_t(x, t4 + ((long long)b * 2 * nq + (long long)comp * nq + i) * kN, rg);
+    wrows_fwd_t(x, rg, S, tw, tws, p);
+#pragma unroll
+    for (int k = 0; k < 16; ++k) s[k] = wmulc(s[k], pv, pvs, p) + 8 * p - x[k];  // below 9p
+    if (x1) {
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        u64 m = wmont(x1[16 * k], y1[16 * k], p, mneg);
+        if (x2) m += wmont(x2[16 * k], y2[16 * k], p, mneg);
+        s[k] += wmulc(m, r64, r64s, p);  // below 10p
+      }
+    }
+    if (addend) {
+      load_gal_raw(x, addend + (long long)b * add_stride + (long long)i * kN, na, g);
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k] += x[k];
+    }
+    if (ac) {
+      const u64* a = ac + (long long)b * acc_stride + (long long)i * kN + na;
+#pragma unroll
+      for (int k = 0; k < 16; ++k) s[k] += a[16 * k];  // below 12p <= 2^64 (p < 2^60)
+    }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      u64 r = wcanon2(mulshoup_lazy(s[k], ql, qls, p), p);
+      if (post.twice) r = wadd(r, r, p);
+      if (sub) r = wsub(r, sub[16 * k], p);
+      s[k] = wadd(r, scal, p);
+    }
+    u64* o = out + (long long)b * out_stride + (long long)i * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) o[16 * k] = s[k];
+  };
+#pragma unroll
+  for (int k = 0; k < 16; ++k) Park[k * kT + threadIdx.x] = sa[k];
+  finish(sb, 0, add, prod ? nullptr : acc_b, post.sub_b ? post.sub_b + so : nullptr,
+         post.has_scalar ? post.scalar[i] : 0, prod ? post.a0 + ao : nullptr, prod ? post.b0 + bo : nullptr, nullptr,
+         nullptr, out_b);
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sa[k] = Park[k * kT + threadIdx.x];
+  finish(sa, 1, nullptr, prod ? nullptr : acc_a, post.sub_a ? post.sub_a + so : nullptr, 0,
+         prod ? post.a0 + ao : nullptr, prod ? post.b1 + bo : nullptr, prod ? post.a1 + ao : nullptr,
+         prod ? post.b0 + bo : nullptr, out_a);
 }
 
 // ----------------------------------------------------------------- ModDown / rescale finish
@@ -766,6 +919,11 @@ void launch_wconv_fused(const WConvArgs& A, int nt_max, dim3 grid, const WideSta
   k<<<grid, kT, 0, s>>>(A, W.t, (const wv4i*)W.conv_dig);
 }
 
+void launch_wconv_rs(const WConvArgs& A, int nt_max, dim3 grid, const WideState& W, hipStream_t s) {
+  auto k = nt_max <= kMPass ? wf_cols_mconv<false, true> : wf_cols_mconv<true, true>;
+  k<<<grid, kT, 0, s>>>(A, W.t, (const wv4i*)W.conv_dig);
+}
+
 }  // namespace
 
 bool wide_fused_ok(const hck_context* c) {
@@ -841,6 +999,93 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
       wf_rows_ipq<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, t4, a0, add_stride,
                                                            acc_b ? acc_b + ai : nullptr, acc_a ? acc_a + ai : nullptr,
                                                            acc_stride, out_b + oi, out_a + oi, out_stride, W.t);
+      HCK_CHECK_LAUNCH();
+    }
+  }
+  return HCK_OK;
+}
+
+// Workspace per item: R1 = T1 / T4 [2 ell limbs], T2 [beta (ell + K)], ACCP [2 (K + 1)].
+size_t wide_fused_rs_bytes(const hck_context* c, int ell, int batch) {
+  const size_t nb = (size_t)std::min(batch, kItems), beta = beta_of(c, ell), ext_l = (size_t)(ell + c->K);
+  return nb * kN * 8 * (2 * (size_t)ell + beta * ext_l + 2 * (size_t)(c->K + 1));
+}
+
+// The key switch with its ModDown fused with the rescale (ks_rescaled on the wide path): K1, K2 as in
+// wide_ks_fused; K3 over q_{ell-1} and the special limbs (Z and the P limbs into ACCP); K4 the
+// ModDown-rescale conversion to q_0 .. q_{ell-2} (T4); K5 the Q limbs below ell - 1 with the post-ops.
+int wide_ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, long long d_stride,
+                     uint32_t galois, const uint64_t* const* ksk, const uint64_t* add, long long add_stride,
+                     const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride, uint64_t* out_b,
+                     uint64_t* out_a, long long out_stride, char* ws, hipStream_t s, int twice,
+                     const uint64_t* sub_b, const uint64_t* sub_a, long long sub_stride, const uint64_t* scalar,
+                     const uint64_t* const* prod_ab, long long a_stride, long long b_stride) {
+  if (!wide_fused_ok(c) || ell < 2) return HCK_ERR_UNSUPPORTED;
+  if (batch < 1 || (acc_b == nullptr) != (acc_a == nullptr) || (sub_b == nullptr) != (sub_a == nullptr))
+    return HCK_ERR_ARG;
+  const WideState& W = *c->wide;
+  const int K = c->K, L = c->L, alpha = c->alpha, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const int nq = ell - 1;
+  const long long n = kN;
+  const int last_digit = ell - alpha * (beta - 1);
+  WRsPost post{};
+  post.twice = twice;
+  post.has_scalar = scalar != nullptr;
+  for (int i = 0; scalar && i < nq; ++i) post.scalar[i] = scalar[i];
+  post.ql = W.qlast_inv + (size_t)ell * L;
+  post.ql_s = W.qlast_inv_s + (size_t)ell * L;
+  for (int b0 = 0; b0 < batch; b0 += kItems) {
+    const int nb = std::min(kItems, batch - b0);
+    WGalF G{};
+    G.uniform = galois;
+    WKeysF kp{};
+    for (int b = 0; b < nb; ++b) kp.k[b] = ksk[b0 + b];
+    const uint64_t* dd = d + (long long)b0 * d_stride;
+    const uint64_t* a0 = add ? add + (long long)b0 * add_stride : nullptr;
+    const long long ai = (long long)b0 * acc_stride, oi = (long long)b0 * out_stride;
+    const uint64_t* ab = acc_b ? acc_b + ai : nullptr;
+    const uint64_t* aa = acc_a ? acc_a + ai : nullptr;
+    post.sub_b = sub_b ? sub_b + (long long)b0 * sub_stride : nullptr;
+    post.sub_a = sub_a ? sub_a + (long long)b0 * sub_stride : nullptr;
+    post.sub_stride = sub_stride;
+    if (prod_ab) {
+      post.a0 = prod_ab[0] + (long long)b0 * a_stride;
+      post.a1 = prod_ab[1] + (long long)b0 * a_stride;
+      post.b0 = prod_ab[2] + (long long)b0 * b_stride;
+      post.b1 = prod_ab[3] + (long long)b0 * b_stride;
+      post.a_stride = a_stride;
+      post.b_stride = b_stride;
+    }
+    u64* r1 = (u64*)ws;  // T1 [nb][ell], later T4 [nb][2][ell - 1]
+    u64* t2 = r1 + (long long)nb * 2 * ell * n;
+    u64* accp = t2 + (long long)nb * beta * ext_l * n;  // [nb][2][K + 1]: q_{ell-1}, then P
+    const WIp I{dd, d_stride, t2, nullptr, ell, beta, L, K, alpha, bmax};
+    // K1, K2 as in wide_ks_fused
+    wf_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * nb), kT, 0, s>>>(dd, d_stride, G, 0, 0, r1, ell, nb,
+                                                                                  W.t);
+    HCK_CHECK_LAUNCH();
+    launch_wconv_fused(WConvArgs{r1, (long long)ell * n, 0, alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                                 W.modup + (size_t)ell * bmax, 1},
+                       ext_l - last_digit, dim3(128, beta, nb), W, s);
+    HCK_CHECK_LAUNCH();
+    // K3 over q_{ell-1} and the K special limbs
+    {
+      const int tiles = 16 * (K + 1), groups = (tiles + kXcds - 1) / kXcds;
+      wf_rows_ip<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, tiles, ell - 1, accp, a0, add_stride, nullptr,
+                                                          nullptr, 0, ab, aa, acc_stride, W.t);
+      HCK_CHECK_LAUNCH();
+    }
+    // K4: the ModDown-rescale conversion, one block per (column pair, component, item); T4 reuses R1
+    u64* t4 = r1;
+    launch_wconv_rs(WConvArgs{accp + n, 2LL * (K + 1) * n, (long long)(K + 1) * n, 0, t4, 2LL * nq * n, (long long)nq * n,
+                              W.mdrs + ell, 0, accp},
+                    nq, dim3(128, 2, nb), W, s);
+    HCK_CHECK_LAUNCH();
+    // K5: Q limbs 0 .. ell - 2
+    {
+      const int tiles = 16 * nq, groups = (tiles + kXcds - 1) / kXcds;
+      wf_rows_ipq_rs<<<dim3(groups * kXcds * nb), kT, 0, s>>>(I, G, kp, nb, t4, a0, add_stride, ab, aa, acc_stride,
+                                                              out_b + oi, out_a + oi, out_stride, post, W.t);
       HCK_CHECK_LAUNCH();
     }
   }

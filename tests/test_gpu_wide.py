@@ -4,7 +4,8 @@
 (exact 128-bit arithmetic for any prime below 2^62): NTT, automorphism, elementwise ops, key
 generation, key switch at 38, 19 and 8 limbs (base conversion on either engine), rotation with and without addends, hoisted rotations,
 the extended-basis
-rotation and ModDown, rescale, ModRaise, tensor and relinearisation, the BSGS MAC and the encoder
+rotation and ModDown, rescale, ModRaise, tensor and relinearisation, the rotation and the product
+with their ModDown fused into the rescale (against the unfused pair and the oracle), the BSGS MAC and the encoder
 for coefficients up to 2^61.  Several checks are the FP64 path's own test bodies, run here on the
 wide context."""
 
@@ -177,16 +178,16 @@ def test_mul_relin(env, ell):
     M.test_mul_relin_bit_exact(env, ell)
 
 
-@pytest.mark.parametrize("ell", [38, 2])
+@pytest.mark.parametrize("ell", [38, 25, 2])
 def test_rotate_rescale(env, ell):
     G.check_rotate_rescale(env, [ell], [ell], batch=2, rot=5)
 
 
 def test_mul_relin_rescale_postop(env):
-    M.check_mul_relin_rescale_postop(env, (38, 2), batch=2)
+    M.check_mul_relin_rescale_postop(env, (38, 26, 2), batch=2)
 
 
-@pytest.mark.parametrize("ell", [38, 2])
+@pytest.mark.parametrize("ell", [38, 25, 2])
 def test_mul_relin_rescale(env, ell):
     M.check_mul_relin_rescale(env, [ell], [ell], batch=2)
 
