@@ -137,6 +137,15 @@ extern "C" int hck_rotate_rescale(const hck_context* ctx, int level_limbs, int b
   if (!ctx || !c0 || !c1 || !ksk || !out0 || !out1 || batch < 0) return HCK_ERR_ARG;
   if (level_limbs < 2 || level_limbs > ctx->L || !galois_ok(galois)) return HCK_ERR_ARG;
   if (out0 == c0 || out0 == c1 || out1 == c0 || out1 == c1 || out0 == out1) return HCK_ERR_ARG;
+  {
+    // no partial overlaps either: the fused pass reads c0 through the automorphism (any position of
+    // a limb) while tiles of other limbs and items store the outputs
+    const int64_t in_len = (int64_t)level_limbs * hck::kN, out_len = (int64_t)(level_limbs - 1) * hck::kN;
+    for (const uint64_t* o : {out0, out1})
+      for (const uint64_t* c : {c0, c1})
+        if (hck::batches_overlap(o, out_stride, out_len, c, in_stride, in_len, batch)) return HCK_ERR_ARG;
+    if (hck::batches_overlap(out0, out_stride, out_len, out1, out_stride, out_len, batch)) return HCK_ERR_ARG;
+  }
   if (batch == 0) return HCK_OK;
   for (int b = 0; b < batch; ++b) if (!ksk[b]) return HCK_ERR_ARG;
   if (!workspace || workspace_bytes < hck_rotate_rescale_workspace_bytes(ctx, level_limbs, batch))

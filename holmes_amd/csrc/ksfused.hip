@@ -1598,6 +1598,9 @@ int ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const ui
                  uint64_t* ext_a, long long ext_stride, char* ws, hipStream_t s) {
   const int batch = outputs * group;
   if (outputs < 1 || group < 1 || batch > kMaxBatchF) return HCK_ERR_ARG;
+  if (c->wide && wide_fused_ok(c))
+    return wide_ks_fused_sum(c, ell, outputs, group, d, d_stride, galois_items, ksk, add, add_stride, acc_b, acc_a,
+                             acc_stride, ext_b, ext_a, ext_stride, ws, s);
   if (c->wide) {
     // one member at a time, each accumulated into the extended outputs (same residues)
     for (int m = 0; m < group; ++m) {

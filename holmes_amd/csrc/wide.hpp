@@ -106,6 +106,11 @@ int wide_ks_fused(const hck_context* c, int ell, int batch, const uint64_t* d, l
                   const uint64_t* acc_a, long long acc_stride, uint64_t* out_b, uint64_t* out_a,
                   long long out_stride, char* ws, hipStream_t s, uint64_t* ext_b, uint64_t* ext_a,
                   long long ext_stride, const uint32_t* galois_items);
+// ks_fused_sum's wide body on the fused kernels (same arguments; outputs * group <= 64).
+int wide_ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const uint64_t* d, long long d_stride,
+                      const uint32_t* galois_items, const uint64_t* const* ksk, const uint64_t* add,
+                      long long add_stride, const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride,
+                      uint64_t* ext_b, uint64_t* ext_a, long long ext_stride, char* ws, hipStream_t s);
 // ks_rescaled's wide body (same arguments and semantics): the key switch's ModDown and the rescale by
 // q_{ell-1} in one conversion, on contexts with wide_fused_ok; workspace wide_fused_rs_bytes.
 size_t wide_fused_rs_bytes(const hck_context* c, int ell, int batch);

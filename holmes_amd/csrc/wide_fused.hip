@@ -439,6 +439,9 @@ struct WIp {
   int ell, beta, L, K, alpha, beta_max;
 };
 
+// FINISH = false leaves the sums in the Montgomery domain (x k 2^-64, below 2p) and INIT = false adds to
+// them: the grouped kernel runs several items' inner products into one pair of sums.
+template <bool INIT = true, bool FINISH = true>
 __device__ __forceinline__ void wtile_ip(u64 (&sb)[16], u64 (&sa)[16], u64 (&x)[16], const WIp& I, int b, int e,
                                          int pi, int rg, uint32_t g, u64* S, const u64* __restrict__ tw,
                                          const u64* __restrict__ tws, const WideTables& T) {
@@ -459,8 +462,10 @@ __device__ __forceinline__ void wtile_ip(u64 (&sb)[16], u64 (&sa)[16], u64 (&x)[
       acc[k] = v >= p2 ? v - p2 : v;
     }
   };
+  if constexpr (INIT) {
 #pragma unroll
-  for (int k = 0; k < 16; ++k) sb[k] = sa[k] = 0;
+    for (int k = 0; k < 16; ++k) sb[k] = sa[k] = 0;
+  }
   for (int jd = 0; jd < I.beta; ++jd) {
     if (jd == own) {
       load_gal_raw(x, I.d + (long long)b * I.d_stride + (long long)e * kN, na, g);
@@ -472,6 +477,7 @@ __device__ __forceinline__ void wtile_ip(u64 (&sb)[16], u64 (&sa)[16], u64 (&x)[
     mac(sb, kp);
     mac(sa, kp + comp);
   }
+  if constexpr (!FINISH) return;
   const u64 r = T.r64[pi], rs = T.r64_s[pi];
 #pragma unroll
   for (int k = 0; k < 16; ++k) {
@@ -552,6 +558,69 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ip(const WIp I, const WGalF G, 
   const u64* twis = T.inv_s + (size_t)pi * kN;
   wrows_inv_to_t(sb, o, rg, S, twi, twis, p);
   wrows_inv_to_t(sa, o + (long long)k1 * kN, rg, S, twi, twis, p);
+}
+
+// ----------------------------------------------------------------- K3 of grouped extended-basis rotations
+// Output o (one tile of it per workgroup) is
+//   acc[o] + sum_m (P sigma_m(add[b]) + IP_b(sigma_m(d[b])), IP_a(sigma_m(d[b])))   over b = m * outputs + o,
+// each member with its own Galois element and key: the members' products and P sigma(add) (as the
+// Montgomery product by P mod p) run into one pair of lazy sums, scaled by 2^64 mod p once, so the
+// extended accumulator is read and written once per output.  Natural layout; ext may alias acc.
+__global__ __launch_bounds__(kT, 2) void wf_rows_ip_sum(const WIp I, const WGalF G, WKeysF keys, int outputs, int group,
+                                                        int tiles, const u64* __restrict__ add, long long add_stride,
+                                                        u64* ext_b, u64* ext_a, long long ext_stride, const u64* acc_b,
+                                                        const u64* acc_a, long long acc_stride, WideTables T) {
+  __shared__ u64 S[kRowLds];
+  const TileId id = decode_tile(outputs, blockIdx.x);
+  if (id.tile >= tiles) return;
+  const int o = id.b, e = id.tile >> 4, rg = id.tile & 15;
+  const int pi = e < I.ell ? e : I.L + (e - I.ell);
+  const u64 p = T.p[pi], p2 = 2 * p, mneg = T.mneg[pi];
+  const u64* tw = T.fwd + (size_t)pi * kN;
+  const u64* tws = T.fwd_s + (size_t)pi * kN;
+  const long long na = nat_a(rg);
+  u64 sb[16], sa[16], x[16];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) sb[k] = sa[k] = 0;
+  for (int m = 0; m < group; ++m) {
+    const int b = m * outputs + o;
+    const uint32_t g = gal_of(G, b);
+    WIp Ib = I;
+    Ib.key = keys.k[b];
+    wtile_ip<false, false>(sb, sa, x, Ib, b, e, pi, rg, g, S, tw, tws, T);
+    if (e < I.ell && add) {
+      load_gal_raw(x, add + (long long)b * add_stride + (long long)e * kN, na, g);
+      const u64 pm = T.pmod[pi];
+#pragma unroll
+      for (int k = 0; k < 16; ++k) {
+        const u64 v = sb[k] + wmont(x[k], pm, p, mneg);  // below 3.5p
+        sb[k] = v >= p2 ? v - p2 : v;
+      }
+    }
+  }
+  const u64 r = T.r64[pi], rs = T.r64_s[pi];
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    sb[k] = wmulc(sb[k], r, rs, p);
+    sa[k] = wmulc(sa[k], r, rs, p);
+  }
+  if (acc_b) {
+    // read before the store below by the same thread: ext may alias acc
+    const u64* ab = acc_b + (long long)o * acc_stride + (long long)e * kN + na;
+    const u64* aa = acc_a + (long long)o * acc_stride + (long long)e * kN + na;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      sb[k] = wadd(sb[k], ab[16 * k], p);
+      sa[k] = wadd(sa[k], aa[16 * k], p);
+    }
+  }
+  u64* ob = ext_b + (long long)o * ext_stride + (long long)e * kN + na;
+  u64* oa = ext_a + (long long)o * ext_stride + (long long)e * kN + na;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    ob[16 * k] = sb[k];
+    oa[16 * k] = sa[k];
+  }
 }
 
 // ----------------------------------------------------------------- K5: Q limbs: inner product + ModDown
@@ -1089,6 +1158,44 @@ int wide_ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d
       HCK_CHECK_LAUNCH();
     }
   }
+  return HCK_OK;
+}
+
+// Grouped extended-basis rotations (ks_fused_sum on the wide path): item b = m * outputs + o of d / add
+// (Galois element galois_items[b], key ksk[b]) is member m of output o; K1 and K2 run over every item,
+// as in wide_ks_fused, then wf_rows_ip_sum; workspace wide_fused_bytes(c, ell, outputs * group).
+int wide_ks_fused_sum(const hck_context* c, int ell, int outputs, int group, const uint64_t* d, long long d_stride,
+                      const uint32_t* galois_items, const uint64_t* const* ksk, const uint64_t* add,
+                      long long add_stride, const uint64_t* acc_b, const uint64_t* acc_a, long long acc_stride,
+                      uint64_t* ext_b, uint64_t* ext_a, long long ext_stride, char* ws, hipStream_t s) {
+  const int batch = outputs * group;
+  if (!wide_fused_ok(c)) return HCK_ERR_UNSUPPORTED;
+  if (outputs < 1 || group < 1 || batch > kItems || (acc_b == nullptr) != (acc_a == nullptr)) return HCK_ERR_ARG;
+  const WideState& W = *c->wide;
+  const int K = c->K, L = c->L, alpha = c->alpha, beta = beta_of(c, ell), ext_l = ell + K, bmax = c->beta_max;
+  const long long n = kN;
+  const int last_digit = ell - alpha * (beta - 1);
+  WGalF G{};
+  G.per_item = 1;
+  WKeysF kp{};
+  for (int b = 0; b < batch; ++b) {
+    G.g[b] = galois_items[b];
+    kp.k[b] = ksk[b];
+  }
+  u64* r1 = (u64*)ws;  // T1 [batch][ell]
+  u64* t2 = r1 + (long long)batch * 2 * ell * n;
+  const WIp I{d, d_stride, t2, nullptr, ell, beta, L, K, alpha, bmax};
+  wf_intt_rows<<<dim3(((16 * ell + kXcds - 1) / kXcds) * kXcds * batch), kT, 0, s>>>(d, d_stride, G, 0, 0, r1, ell,
+                                                                                    batch, W.t);
+  HCK_CHECK_LAUNCH();
+  launch_wconv_fused(WConvArgs{r1, (long long)ell * n, 0, alpha, t2, (long long)beta * ext_l * n, (long long)ext_l * n,
+                               W.modup + (size_t)ell * bmax, 1},
+                     ext_l - last_digit, dim3(128, beta, batch), W, s);
+  HCK_CHECK_LAUNCH();
+  const int tiles = 16 * ext_l, groups = (tiles + kXcds - 1) / kXcds;
+  wf_rows_ip_sum<<<dim3(groups * kXcds * outputs), kT, 0, s>>>(I, G, kp, outputs, group, tiles, add, add_stride, ext_b,
+                                                               ext_a, ext_stride, acc_b, acc_a, acc_stride, W.t);
+  HCK_CHECK_LAUNCH();
   return HCK_OK;
 }
 

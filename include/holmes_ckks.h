@@ -128,7 +128,8 @@ int hck_rotate(const hck_context* ctx, int level_limbs, int batch, uint32_t galo
 /* Rotation followed by the rescale (C1's unit: INTT, automorphism, key switch, NTT, rescale):
  * outputs at level_limbs - 1 limbs (level_limbs >= 2), the residues of hck_rotate followed by
  * hck_rescale, bit for bit; fhe.homo_rotate then fhe.rescale (operator.py:446-453, 387-394).  On
- * the matrix-core conversion engine the ModDown and the rescale share one conversion pass. */
+ * the matrix-core conversion engine the ModDown and the rescale share one conversion pass.  The
+ * outputs may not overlap c0, c1 or each other (HCK_ERR_ARG). */
 size_t hck_rotate_rescale_workspace_bytes(const hck_context* ctx, int level_limbs, int batch);
 int hck_rotate_rescale(const hck_context* ctx, int level_limbs, int batch, uint32_t galois, const uint64_t* c0,
                        const uint64_t* c1, int64_t in_stride, const uint64_t* const* ksk, uint64_t* out0,

@@ -382,6 +382,35 @@ def test_rescale_in_place_and_rejected_overlaps(env):
         ctx.rescale_raw(buf, ell, out=ctx.empty(polys - 1, ell - 1, n))
 
 
+def test_rotate_rescale_rejects_overlapping_outputs(env):
+    """hck_rotate_rescale refuses outputs that share words with c0, c1 or each other at any offset
+    (the fused pass reads c0 through the automorphism while other tiles store): HCK_ERR_ARG, nothing
+    launched."""
+    from holmes_amd import _native as nat
+
+    _, client, ctx, orc = env
+    ell, n = 4, ctx.N
+    g = ctx.galois_element(3)
+    gk, _ = _key_pair(client, ctx, orc, g)
+    rng = np.random.default_rng(47)
+    c0, c1 = _dev(_rand(ctx, rng, 1, ell)), _dev(_rand(ctx, rng, 1, ell))
+    free0, free1 = ctx.empty(1, ell - 1, n), ctx.empty(1, ell - 1, n)
+    L = nat.lib()
+    ws = ctx.workspace(L.hck_rotate_rescale_workspace_bytes(ctx.handle, ell, 1))
+    keys = nat.ptr_array([gk.data_ptr()])
+    stream = torch.cuda.current_stream().cuda_stream
+
+    def call(o0, o1):
+        return L.hck_rotate_rescale(ctx.handle, ell, 1, g, c0.data_ptr(), c1.data_ptr(), ell * n, keys, o0, o1,
+                                    (ell - 1) * n, ws.data_ptr(), ws.numel(), stream)
+
+    assert call(c0.data_ptr() + 8 * n, free1.data_ptr()) == nat.HCK_ERR_ARG  # out0 one limb into c0
+    assert call(free0.data_ptr(), c1.data_ptr() + 8 * n) == nat.HCK_ERR_ARG  # out1 one limb into c1
+    assert call(free0.data_ptr(), free0.data_ptr() + 8 * n) == nat.HCK_ERR_ARG  # out1 inside out0
+    assert call(free0.data_ptr(), free1.data_ptr()) == 0
+    torch.cuda.synchronize()
+
+
 def test_batched_keyswitch_sixteen_keys(env):
     """Config C2 shape: 16 ciphertexts at 24 limbs, 16 distinct rotation keys (steps 1..16)."""
 

@@ -240,6 +240,6 @@ def test_encrypt_rotate_decrypt(env):
     assert err2 < 2.0**-30
 
 
-@pytest.mark.parametrize("ell,outputs,group", [(19, 5, 3)])
+@pytest.mark.parametrize("ell,outputs,group", [(19, 5, 3), (38, 4, 4), (3, 1, 2)])
 def test_grouped_ext_rotations(env, ell, outputs, group):
     G.test_grouped_ext_rotations_equal_sequential(env, ell, outputs, group)
