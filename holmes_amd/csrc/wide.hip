@@ -809,32 +809,63 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
 // ---------------------------------------------------------------------------------------- encode
 constexpr double kWideEncodeCap = 2305843009213693952.0;  // 2^61, as the FP64 path
 
-// Rounded coefficients of the special IFFT's output (the FP64 path's expression, contraction off),
-// reduced modulo every listed prime (coefficient domain).  Grid (N / 256, rows).
-__global__ __launch_bounds__(256) void wk_encode_round(const double* __restrict__ vre, const double* __restrict__ vim,
-                                                       double scale, u64* __restrict__ out, long long out_stride,
-                                                       LimbList list, int* __restrict__ overflow, WideTables T) {
-  const int n = blockIdx.x * 256 + threadIdx.x;
+// The rounding of the special IFFT's output (the FP64 path's expression, contraction off) fused with
+// the forward transform's column pass: the block rounds the 16 columns' 4096 coefficients once, then
+// for every listed limb reduces them modulo its prime and runs the column stages (as wk_fwd_cols);
+// wk_fwd_rows finishes the transform.  Grid (16, rows).
+__global__ __launch_bounds__(kWT) void wk_encode_cols(const double* __restrict__ vre, const double* __restrict__ vim,
+                                                      double scale, u64* __restrict__ out, long long out_stride,
+                                                      LimbList list, int* __restrict__ overflow, WideTables T) {
+  __shared__ u64 sh[256 * kWPad];
   const long long row = blockIdx.y;
+  const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
   const double* re = vre + row * (kN / 2);
   const double* im = vim + row * (kN / 2);
-  double a;
+  u64 mag[16];
+  unsigned neg = 0;
+  bool big = false;
   {
 #pragma clang fp contract(off)
     const double inv_n = 1.0 / (double)(kN / 2);
-    const int h = n >= kN / 2;
-    const int slot = (int)(__brev((unsigned)(n - h * (kN / 2))) >> (32 - (kLogN - 1)));
-    const double w = (h ? im : re)[slot] * inv_n;
-    a = round_away(w * scale);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const int n = c + 256 * (r + 16 * u);
+      const int h = n >= kN / 2;
+      const int slot = (int)(__brev((unsigned)(n - h * (kN / 2))) >> (32 - (kLogN - 1)));
+      const double w = (h ? im : re)[slot] * inv_n;
+      const double a = round_away(w * scale);
+      const bool b = !(fabs(a) < kWideEncodeCap);
+      big |= b;
+      mag[u] = b ? 0 : (u64)fabs(a);
+      neg |= (a < 0 ? 1u : 0u) << u;
+    }
   }
-  const bool big = !(fabs(a) < kWideEncodeCap);
   if (big) overflow[row] = 1;
-  const u64 mag = big ? 0 : (u64)fabs(a);
   u64* d = out + row * out_stride;
   for (int e = 0; e < list.n; ++e) {
-    const Barrett64 br = wbar(T, list.prime[e]);
-    const u64 r = barrett_reduce((u128)mag, br);
-    d[(long long)list.off[e] * kN + n] = (a < 0 && r) ? br.p - r : r;
+    const int pi = list.prime[e];
+    const Barrett64 br = wbar(T, pi);
+    const u64 p = br.p;
+    const u64* tw = T.fwd + (size_t)pi * kN;
+    const u64* tws = T.fwd_s + (size_t)pi * kN;
+    u64 x[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const u64 v = barrett_reduce((u128)mag[u], br);
+      x[u] = ((neg >> u) & 1u) && v ? p - v : v;
+    }
+    wfwd16_lazy(x, tw, tws, p, [](int s, int u) { return (1 << s) + (u >> (4 - s)); });
+#pragma unroll
+    for (int u = 0; u < 16; ++u) sh[(r + 16 * u) * kWPad + cl] = x[u];
+    __syncthreads();
+    const int q = r;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) x[m] = sh[(16 * q + m) * kWPad + cl];
+    wfwd16_lazy(x, tw, tws, p, [q](int s, int m) { return (16 << s) + ((16 * q + m) >> (4 - s)); });
+    u64* o = d + (long long)list.off[e] * kN;
+#pragma unroll
+    for (int m = 0; m < 16; ++m) o[c + 256 * (16 * q + m)] = wcanon4(x[m], p);
+    __syncthreads();  // every thread has read sh before the next limb writes it
   }
 }
 
@@ -1207,9 +1238,10 @@ int wide_encode_ntt(const hck_context* c, const double* vre, const double* vim, 
                     long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s) {
   if (list.n <= 0 || rows <= 0) return HCK_OK;
   if (list.n > kMaxList || rows > 65535) return HCK_ERR_ARG;
-  wk_encode_round<<<dim3(kN / 256, rows), 256, 0, s>>>(vre, vim, scale, out, out_stride, list, overflow, c->wide->t);
+  wk_encode_cols<<<dim3(16, rows), kWT, 0, s>>>(vre, vim, scale, out, out_stride, list, overflow, c->wide->t);
+  wk_fwd_rows<<<dim3(16, list.n, rows), kWT, 0, s>>>(out, out_stride, list, c->wide->t);
   HCK_CHECK_LAUNCH();
-  return wide_ntt(c, out, out, rows, out_stride, out_stride, list, false, s);
+  return HCK_OK;
 }
 
 namespace {
