@@ -806,6 +806,141 @@ __global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac(const WMac P, long l
   }
 }
 
+// The MAC on contexts whose primes all lie below 2^60: each canonical word is split into 30-bit halves
+// (x = x1 2^30 + x0), and a product's three partial products go into three 64-bit sums without carries,
+//   S0 += x0 w0,   S1 += x0 w1 + x1 w0,   S2 += x1 w1   (each partial product below 2^60, the middle pair
+// below 2^61), so a product costs four 32 x 32 -> 64 multiply-adds.  Every kSFold baby steps the sums are
+// normalised: the bits of S0 above 2^30 move into S1, those of S1 into S2, and S2 2^60 comes back as
+// one Shoup product by 2^60 mod p (below 2p) added to S0; the invariant S0 < 2^30 + 2p, S1 < 2^30,
+// S2 = 0 keeps kSFold more steps inside 64 bits (2^30 + 2^61 + 7 2^60 and 2^30 + 7 2^61 + 2^34 below
+// 2^64).  The result is the canonical residue of S0 + S1 2^30 (below 2^62), the value sum_b x_b w_b
+// mod p exactly, as the 128-bit MAC gives it.  Tiles of kSTI inputs x kSTG giants per thread.
+constexpr int kSTI = 2;
+constexpr int kSTG = 4;
+constexpr int kSFold = 7;
+constexpr u64 kM30 = (1ULL << 30) - 1;
+
+struct WSplitOps {
+  u64 w[kSTG], x0[kSTI], x1[kSTI];
+};
+
+__device__ __forceinline__ void wmac30_load(WSplitOps& o, const WMac& P, int b, int babies, int G, int ni, int g0,
+                                            int i0, const u64* __restrict__ pts, long long pt_stride,
+                                            long long baby_stride, long long ln) {
+#pragma unroll
+  for (int g = 0; g < kSTG; ++g) {
+    const int gg = g0 + g < G ? g0 + g : g0;  // clamped rows are computed but never stored
+    o.w[g] = pts[((long long)gg * babies + b) * pt_stride + ln];
+  }
+#pragma unroll
+  for (int t = 0; t < kSTI; ++t) {
+    const int ii = i0 + t < ni ? i0 + t : i0;
+    o.x0[t] = P.c0[b][(long long)ii * baby_stride + ln];
+    o.x1[t] = P.c1[b][(long long)ii * baby_stride + ln];
+  }
+}
+
+__global__ __launch_bounds__(kWMacThreads) void wk_bsgs_mac30(const WMac P, long long baby_stride,
+                                                              const u64* __restrict__ pts, long long pt_stride,
+                                                              u64* __restrict__ res, int inputs, int babies,
+                                                              int giants, int limbs, WPrimeMap pm, int units_per_limb,
+                                                              int tiles_i, int tiles_g, int total_units, WideTables T) {
+  const int tiles = tiles_i * tiles_g;
+  const int lin = blockIdx.x;
+  const int xcd = lin % kXcds, q = lin / kXcds;
+  const int unit = (q / tiles) * kXcds + xcd;
+  const int tile = q % tiles;
+  if (unit >= total_units) return;
+  const int l = unit / units_per_limb;
+  const int n = (unit % units_per_limb) * kWMacThreads + threadIdx.x;
+  const int i0 = (tile % tiles_i) * kSTI, g0 = (tile / tiles_i) * kSTG;
+  const int pi = pm.prime[l];
+  const u64 p = T.p[pi], c60 = T.r60[pi], c60s = T.r60_s[pi];
+  const long long ln = (long long)l * kN + n;
+  u64 s0[kSTI][2][kSTG], s1[kSTI][2][kSTG], s2[kSTI][2][kSTG];
+#pragma unroll
+  for (int t = 0; t < kSTI; ++t)
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < kSTG; ++g) s0[t][c][g] = s1[t][c][g] = s2[t][c][g] = 0;
+  auto step = [&](const WSplitOps& o, int b) {
+    uint32_t wl[kSTG], wh[kSTG];
+#pragma unroll
+    for (int g = 0; g < kSTG; ++g) {
+      wl[g] = (uint32_t)o.w[g] & (uint32_t)kM30;
+      wh[g] = (uint32_t)(o.w[g] >> 30);
+    }
+#pragma unroll
+    for (int t = 0; t < kSTI; ++t)
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u64 x = c ? o.x1[t] : o.x0[t];
+        const uint32_t xl = (uint32_t)x & (uint32_t)kM30, xh = (uint32_t)(x >> 30);
+#pragma unroll
+        for (int g = 0; g < kSTG; ++g) {
+          s0[t][c][g] += (u64)xl * wl[g];
+          s1[t][c][g] += (u64)xl * wh[g];
+          s1[t][c][g] += (u64)xh * wl[g];
+          s2[t][c][g] += (u64)xh * wh[g];
+        }
+      }
+    if (b % kSFold == kSFold - 1 && b + 1 < babies) {  // uniform
+#pragma unroll
+      for (int t = 0; t < kSTI; ++t)
+#pragma unroll
+        for (int c = 0; c < 2; ++c)
+#pragma unroll
+          for (int g = 0; g < kSTG; ++g) {
+            u64 a = s0[t][c][g], m = s1[t][c][g], h = s2[t][c][g];
+            m += a >> 30;
+            a &= kM30;
+            h += m >> 30;
+            m &= kM30;
+            s0[t][c][g] = a + mulshoup_lazy(h, c60, c60s, p);
+            s1[t][c][g] = m;
+            s2[t][c][g] = 0;
+          }
+    }
+  };
+  // the two-register-set pipeline of wk_bsgs_mac
+  WSplitOps o0, o1;
+  wmac30_load(o0, P, 0, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+  int b = 0;
+  for (; b + 1 < babies; b += 2) {
+    wmac30_load(o1, P, b + 1, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride, ln);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step(o0, b);
+    wmac30_load(o0, P, b + 2 < babies ? b + 2 : b + 1, babies, giants, inputs, g0, i0, pts, pt_stride, baby_stride,
+                ln);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step(o1, b + 1);
+  }
+  if (b < babies) step(o0, b);
+  const u64 mneg = T.mneg[pi], r = T.r64[pi], rs = T.r64_s[pi];
+  const long long is = (long long)limbs * kN, gs = (long long)inputs * is, cs = (long long)giants * gs;
+#pragma unroll
+  for (int t = 0; t < kSTI; ++t) {
+    if (i0 + t >= inputs) break;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < kSTG; ++g)
+        if (g0 + g < giants) {
+          // the last block's sums, normalised as above, then S0 + S1 2^30 + S2 2^60 reduced exactly
+          u64 a = s0[t][c][g], m = s1[t][c][g], h = s2[t][c][g];
+          m += a >> 30;
+          a &= kM30;
+          h += m >> 30;
+          m &= kM30;
+          const u64 v = a + (m << 30) + mulshoup_lazy(h, c60, c60s, p);  // below 2^61 + 2^30
+          res[c * cs + (long long)(g0 + g) * gs + (long long)(i0 + t) * is + ln] = wfold128((u128)v, p, mneg, r, rs);
+        }
+  }
+}
+
 // ---------------------------------------------------------------------------------------- encode
 constexpr double kWideEncodeCap = 2305843009213693952.0;  // 2^61, as the FP64 path
 
@@ -1001,7 +1136,7 @@ int wide_init(hck_context* c) {
   const size_t np = (size_t)c->np, n = kN;
   const std::vector<u64>& P = c->primes;
   std::vector<u64> p(np), mu(np), fwd(np * n), fwd_s(np * n), inv(np * n), inv_s(np * n), ninv(np), ninv_s(np),
-      z4(np), z4_s(np), pm(np), pm_s(np), pinv(np), pinv_s(np), mneg(np), r64(np), r64_s(np);
+      z4(np), z4_s(np), pm(np), pm_s(np), pinv(np), pinv_s(np), mneg(np), r64(np), r64_s(np), r60(np), r60_s(np);
   std::vector<int> w(np);
   for (size_t i = 0; i < np; ++i) {
     const u64 q = P[i];
@@ -1037,6 +1172,8 @@ int wide_init(hck_context* c) {
     mneg[i] = 0 - qi;
     r64[i] = (u64)(((u128)1 << 64) % q);
     r64_s[i] = shoup_companion(r64[i], q);
+    r60[i] = (1ULL << 60) % q;
+    r60_s[i] = shoup_companion(r60[i], q);
   }
   std::vector<WideConv> modup((size_t)(L + 1) * bmax), moddown((size_t)(L + 1)), rescale((size_t)(L + 1)),
       mdrs((size_t)(L + 1));
@@ -1147,6 +1284,7 @@ int wide_init(hck_context* c) {
       {ql.data(), ql.size() * 8}, {ql_s.data(), ql_s.size() * 8}, {dig.data(), dig.size()},
       {mneg.data(), np * 8}, {r64.data(), np * 8}, {r64_s.data(), np * 8},
       {rescale.data(), rescale.size() * sizeof(WideConv)}, {mdrs.data(), mdrs.size() * sizeof(WideConv)},
+      {r60.data(), np * 8}, {r60_s.data(), np * 8},
   };
   size_t off = 0;
   for (Part& pt : parts) {
@@ -1197,6 +1335,8 @@ int wide_init(hck_context* c) {
   T.r64_s = (const u64*)at(22);
   ws->rescale = (WideConv*)at(23);
   ws->mdrs = (WideConv*)at(24);
+  T.r60 = (const u64*)at(25);
+  T.r60_s = (const u64*)at(26);
   ws->primes_below_2_60 = true;
   for (int i = 0; i < c->np; ++i) ws->primes_below_2_60 = ws->primes_below_2_60 && c->primes[i] < (1ULL << 60);
   c->wide = ws;
@@ -1661,8 +1801,20 @@ int wide_bsgs_mac(const hck_context* c, int limbs, const int* prime_idx, int inp
   for (int l = 0; l < limbs; ++l) pm.prime[l] = (uint8_t)prime_idx[l];
   const int units_per_limb = kN / kWMacThreads;
   const int total_units = limbs * units_per_limb;
-  const int tiles_i = (inputs + kWTI - 1) / kWTI, tiles_g = (giants + kWTG - 1) / kWTG;
   const long long units_padded = ((long long)total_units + kXcds - 1) / kXcds * kXcds;
+  bool split = true;  // the split MAC needs every prime of the launch below 2^60
+  for (int l = 0; l < limbs; ++l) split = split && c->primes[prime_idx[l]] < (1ULL << 60);
+  if (split) {
+    const int tiles_i = (inputs + kSTI - 1) / kSTI, tiles_g = (giants + kSTG - 1) / kSTG;
+    const long long blocks = units_padded * tiles_i * tiles_g;
+    if (blocks > 0x7fffffffLL) return HCK_ERR_ARG;
+    wk_bsgs_mac30<<<dim3((unsigned)blocks), kWMacThreads, 0, s>>>(P, baby_stride, pts, pt_stride, res, inputs, babies,
+                                                                 giants, limbs, pm, units_per_limb, tiles_i, tiles_g,
+                                                                 total_units, c->wide->t);
+    HCK_CHECK_LAUNCH();
+    return HCK_OK;
+  }
+  const int tiles_i = (inputs + kWTI - 1) / kWTI, tiles_g = (giants + kWTG - 1) / kWTG;
   const long long blocks = units_padded * tiles_i * tiles_g;
   if (blocks > 0x7fffffffLL) return HCK_ERR_ARG;
   wk_bsgs_mac<<<dim3((unsigned)blocks), kWMacThreads, 0, s>>>(P, baby_stride, pts, pt_stride, res, inputs, babies,

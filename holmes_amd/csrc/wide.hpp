@@ -63,6 +63,8 @@ struct WideTables {
   const uint64_t* mneg;    // [np] -p^-1 mod 2^64 (Montgomery products of the fused key switch)
   const uint64_t* r64;     // [np] 2^64 mod p, which undoes a Montgomery product's 2^-64
   const uint64_t* r64_s;
+  const uint64_t* r60;     // [np] 2^60 mod p (the split MAC's top partial sum), with its companion
+  const uint64_t* r60_s;
 };
 
 struct WideState {

@@ -201,7 +201,7 @@ def test_lincomb_rescale(env, limbs, G, T):
     M.check_lincomb_rescale(env, limbs, G, T)
 
 
-@pytest.mark.parametrize("ni,nb,G_,limbs", [(3, 5, 6, 2), (2, 3, 2, 38), (5, 64, 2, 1)])
+@pytest.mark.parametrize("ni,nb,G_,limbs", [(3, 5, 6, 2), (2, 3, 2, 38), (5, 64, 2, 1), (4, 15, 9, 3), (2, 14, 4, 2)])
 def test_bsgs_mac(env, ni, nb, G_, limbs):
     _, _, ctx, orc = env
     B.test_bsgs_mac((ctx, orc), ni, nb, G_, limbs)
