@@ -194,6 +194,13 @@ inline const ConvConsts* modup_consts(const hck_context* c, int ell, int j) {
   return c->d_modup + (size_t)ell * c->beta_max + j;
 }
 inline int prime_of_ext(const hck_context* c, int ell, int e) { return e < ell ? e : c->L + (e - ell); }
+// Limbs per workgroup of the encoders' rounding + column kernels (grid (16, limb chunks, rows)):
+// enough chunks for about 2048 workgroups.
+inline int encode_limbs_per_block(int limbs, int rows) {
+  int chunks = (2048 + 16 * rows - 1) / (16 * rows);
+  chunks = chunks < 1 ? 1 : (chunks > limbs ? limbs : chunks);
+  return (limbs + chunks - 1) / chunks;
+}
 // Whether two batches of n items (item i of p at p + i * p_stride, p_len words long; likewise q)
 // share any word.  Strides are non-negative; a stride of 0 repeats one item.
 inline bool batches_overlap(const uint64_t* p, int64_t p_stride, int64_t p_len, const uint64_t* q, int64_t q_stride,

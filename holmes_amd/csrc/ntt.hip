@@ -271,10 +271,11 @@ __global__ __launch_bounds__(kThreads) void k_inv_cols(void* data, long long str
 // The encoder's last step fused with the column pass: the block of 16 columns of one plaintext row
 // loads each coefficient once (the special IFFT output gathered in bit-reversed order, * 1/n,
 // * scale, rounded half away from zero: coefficient n < N/2 from the real part of slot brev(n),
-// n >= N/2 from the imaginary part of slot brev(n - N/2)), then for every limb takes the residue
-// in [0, p) and runs stages 0..7 exactly as k_fwd_cols<kU64> does on stored residues, so the result
-// is bit-identical to rounding, storing every limb and transforming.  The residues of all limbs
-// never reach HBM.
+// n >= N/2 from the imaginary part of slot brev(n - N/2)), then for each of its limbs (lpb of them
+// from blockIdx.y lpb: a launch of few rows still fills the chip) takes the residue in [0, p) and
+// runs stages 0..7 exactly as k_fwd_cols<kU64> does on stored residues, so the result is
+// bit-identical to rounding, storing every limb and transforming.  The residues of all limbs never
+// reach HBM.  Grid (16, limb chunks, rows).
 // Encoder cap: |coefficient| < 2^61, the reference's MAX_ENCODED_BITS
 // (llama3fhe/operators/attention/prefill/softmax.py:559).  A rounded coefficient is an exact double
 // (at and above 2^53 every double is an integer), and canon() reduces it exactly: q = floor(x / p)
@@ -284,10 +285,10 @@ constexpr double kEncodeCap = 2305843009213693952.0;  // 2^61
 __global__ __launch_bounds__(kThreads) void k_encode_cols(const double* __restrict__ vre,
                                                           const double* __restrict__ vim, double scale,
                                                           double* __restrict__ out, long long out_stride,
-                                                          LimbList list, int* __restrict__ overflow,
+                                                          LimbList list, int lpb, int* __restrict__ overflow,
                                                           DevTables T) {
   __shared__ double sh[kLds];
-  const long long row = blockIdx.y;
+  const long long row = blockIdx.z;
   const int tid = threadIdx.x, cl = tid & 15, j = tid >> 4, c = blockIdx.x * 16 + cl;
   const double* re = vre + row * (kN / 2);
   const double* im = vim + row * (kN / 2);
@@ -308,7 +309,8 @@ __global__ __launch_bounds__(kThreads) void k_encode_cols(const double* __restri
   }
   if (big) overflow[row] = 1;
   double* d = out + row * out_stride;
-  for (int e = 0; e < list.n; ++e) {
+  const int e_end = min(list.n, ((int)blockIdx.y + 1) * lpb);  // this block: limbs [blockIdx.y lpb, e_end)
+  for (int e = (int)blockIdx.y * lpb; e < e_end; ++e) {
     const int pi = list.prime[e];
     const double p = T.p[pi], pinv = T.pinv[pi];
     const double* __restrict__ tw = T.tw_fwd + (size_t)pi * kN;
@@ -377,8 +379,11 @@ int launch_encode_ntt(const hck_context* c, const double* vre, const double* vim
   if (c->wide) return wide_encode_ntt(c, vre, vim, scale, out, out_stride, rows, overflow, list, s);
   if (list.n <= 0 || rows <= 0) return HCK_OK;
   if (list.n > kMaxList || rows > 65535) return HCK_ERR_ARG;
-  k_encode_cols<<<dim3(16, rows), kThreads, 0, s>>>(vre, vim, scale, (double*)out, out_stride, list, overflow,
-                                                     c->dev);
+  // limbs split over blockIdx.y so that a launch of few rows still fills the chip (each block rounds
+  // its coefficients again: the IFFT output is read from L2)
+  const int lpb = encode_limbs_per_block(list.n, rows);
+  k_encode_cols<<<dim3(16, (list.n + lpb - 1) / lpb, rows), kThreads, 0, s>>>(vre, vim, scale, (double*)out,
+                                                                            out_stride, list, lpb, overflow, c->dev);
   k_fwd_rows<kU64><<<dim3(16, list.n, rows), kThreads, 0, s>>>(out, out_stride, list, c->dev);
   HCK_CHECK_LAUNCH();
   return HCK_OK;

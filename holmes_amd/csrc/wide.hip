@@ -946,13 +946,14 @@ constexpr double kWideEncodeCap = 2305843009213693952.0;  // 2^61, as the FP64 p
 
 // The rounding of the special IFFT's output (the FP64 path's expression, contraction off) fused with
 // the forward transform's column pass: the block rounds the 16 columns' 4096 coefficients once, then
-// for every listed limb reduces them modulo its prime and runs the column stages (as wk_fwd_cols);
-// wk_fwd_rows finishes the transform.  Grid (16, rows).
+// for each of its listed limbs reduces them modulo the limb's prime and runs the column stages (as
+// wk_fwd_cols); wk_fwd_rows finishes the transform.  Grid (16, limb chunks of lpb, rows).
 __global__ __launch_bounds__(kWT) void wk_encode_cols(const double* __restrict__ vre, const double* __restrict__ vim,
                                                       double scale, u64* __restrict__ out, long long out_stride,
-                                                      LimbList list, int* __restrict__ overflow, WideTables T) {
+                                                      LimbList list, int lpb, int* __restrict__ overflow,
+                                                      WideTables T) {
   __shared__ u64 sh[256 * kWPad];
-  const long long row = blockIdx.y;
+  const long long row = blockIdx.z;
   const int tid = threadIdx.x, cl = tid & 15, r = tid >> 4, c = blockIdx.x * 16 + cl;
   const double* re = vre + row * (kN / 2);
   const double* im = vim + row * (kN / 2);
@@ -977,7 +978,8 @@ __global__ __launch_bounds__(kWT) void wk_encode_cols(const double* __restrict__
   }
   if (big) overflow[row] = 1;
   u64* d = out + row * out_stride;
-  for (int e = 0; e < list.n; ++e) {
+  const int e_end = min(list.n, ((int)blockIdx.y + 1) * lpb);  // this block: limbs [blockIdx.y lpb, e_end)
+  for (int e = (int)blockIdx.y * lpb; e < e_end; ++e) {
     const int pi = list.prime[e];
     const Barrett64 br = wbar(T, pi);
     const u64 p = br.p;
@@ -1378,7 +1380,9 @@ int wide_encode_ntt(const hck_context* c, const double* vre, const double* vim, 
                     long long out_stride, int rows, int* overflow, const LimbList& list, hipStream_t s) {
   if (list.n <= 0 || rows <= 0) return HCK_OK;
   if (list.n > kMaxList || rows > 65535) return HCK_ERR_ARG;
-  wk_encode_cols<<<dim3(16, rows), kWT, 0, s>>>(vre, vim, scale, out, out_stride, list, overflow, c->wide->t);
+  const int lpb = encode_limbs_per_block(list.n, rows);
+  wk_encode_cols<<<dim3(16, (list.n + lpb - 1) / lpb, rows), kWT, 0, s>>>(vre, vim, scale, out, out_stride, list, lpb,
+                                                                         overflow, c->wide->t);
   wk_fwd_rows<<<dim3(16, list.n, rows), kWT, 0, s>>>(out, out_stride, list, c->wide->t);
   HCK_CHECK_LAUNCH();
   return HCK_OK;
