@@ -207,6 +207,48 @@ def test_bsgs_mac(env, ni, nb, G_, limbs):
     B.test_bsgs_mac((ctx, orc), ni, nb, G_, limbs)
 
 
+def test_bsgs_mac_on_primes_above_2_60():
+    """A context whose primes lie in [2^60, 2^61) (reachable through the C ABI; the Python spec stops
+    at 60 bits) runs the 128-bit MAC, since the split MAC needs every prime below 2^60: bit-exact
+    against the oracle over several folds, odd counts and clamped tiles."""
+    import ctypes
+
+    from holmes_amd import _native as nat
+    from holmes_amd.params import ntt_primes
+
+    primes = ntt_primes(16, 61, 3)  # two Q primes, one special prime
+    assert all(p >= 1 << 60 for p in primes)
+    L = nat.lib()
+    h = ctypes.c_void_p()
+    nat.check(L.hck_context_create(ctypes.byref(h), 16, 2, 1, 1, nat.u64_array(primes)), "hck_context_create")
+    try:
+        orc = O.OracleContext(16, 2, 1, 1, primes)
+        ni, nb, G, limbs = 3, 11, 5, 2
+        n = 1 << 16
+        rng = np.random.default_rng(61)
+        q = np.array(primes[:limbs], dtype=np.uint64).reshape(1, limbs, 1)
+        pts = rng.integers(0, 2**62, size=(G * nb, limbs, n), dtype=np.uint64) % q
+        babies = rng.integers(0, 2**62, size=(nb, 2, ni, limbs, n), dtype=np.uint64) % q.reshape(1, 1, 1, limbs, 1)
+        pts[0, 0, :3] = primes[0] - 1
+        babies[0, :, 0, 0, :3] = primes[0] - 1
+        bt = torch.from_numpy(babies).cuda()
+        pt = torch.from_numpy(pts).cuda()
+        res = torch.empty((2, G, ni, limbs, n), dtype=torch.uint64, device="cuda")
+        c0 = [bt[b, 0] for b in range(nb)]
+        c1 = [bt[b, 1] for b in range(nb)]
+        rc = L.hck_bsgs_mac(h, limbs, nat.int_array([0, 1]), ni, nb, G, nat.ptr_array([t.data_ptr() for t in c0]),
+                            nat.ptr_array([t.data_ptr() for t in c1]), limbs * n, pt.data_ptr(), limbs * n,
+                            res.data_ptr(), torch.cuda.current_stream().cuda_stream)
+        assert rc == 0
+        got = _host(res)
+        for i in range(ni):
+            want = orc.bsgs_mac(limbs, nb, G, pts, np.ascontiguousarray(babies[:, :, i]))
+            assert np.array_equal(got[:, :, i], want), f"input {i}"
+    finally:
+        torch.cuda.synchronize()
+        L.hck_context_destroy(h)
+
+
 @pytest.mark.parametrize("scale", [2.0**40, None])
 def test_encode(env, scale):
     _, _, ctx, orc = env
