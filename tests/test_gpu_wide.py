@@ -192,6 +192,20 @@ def test_mul_relin_rescale(env, ell):
     M.check_mul_relin_rescale(env, [ell], [ell], batch=2)
 
 
+def test_unfused_fallbacks_on_the_valu_engine(env):
+    """With the VALU conversion engine the wide context has no fused kernels (wide_fused_ok is false,
+    as on a chain with a prime at or above 2^60): the rotation and the product with their rescale run
+    as two steps and grouped giant steps one member at a time.  Same residues as the oracle."""
+    fhe, client, ctx, orc = env
+    ctx.set_conversion_engine("valu")
+    try:
+        G.check_rotate_rescale(env, [38, 2], [38, 2], batch=2, rot=3)
+        M.check_mul_relin_rescale(env, [9, 2], [9, 2], batch=2)
+        G.test_grouped_ext_rotations_equal_sequential(env, 9, 3, 2)
+    finally:
+        ctx.set_conversion_engine("mfma")
+
+
 def test_lincomb(env):
     M.test_lincomb_matches_oracle(env)
 
