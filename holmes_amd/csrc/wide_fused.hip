@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kT) void wf_intt_rows(const u64* __restrict__ d, lo
 // 16 slots of 16 threads.  Phase 1: slot sigma = (source sigma >> 1, column sigma & 1) runs the INTT
 // column stages of its source column and leaves the centered residue's digit word in run sigma of D.
 // Phase 2 (as ksfused.hip's cols_mconv_body): wave w takes column w >> 1 and half w & 1 of each pass's
-// 8 mi targets; quarter g owns mi (<= kMItems) of them, MFMA rows 4g + r; a lane supplies A row j (the
+// 8 mi targets; quarter g owns mi (<= MI) of them, MFMA rows 4g + r; a lane supplies A row j (the
 // digit bytes of sources 2g, 2g + 1 for target ta(j)) and B column j (the digit words of coefficient
 // j + 16k), and receives rows 4g + r at column j: rows j + 16k of its targets over the 16 tiles, the
 // forward column pass's layout A.  SEPX keeps separate exchange runs (X) so that D serves every pass.
@@ -285,7 +285,9 @@ struct WConvArgs {
 // the coefficient domain; phase 2 adds r to every stored target's sum (whose factors carry P^-1).
 // With the finish of wf_rows_ipq_rs this gives ((IP - NTT(conv)) P^-1 + acc - NTT(r)) q_{ell-1}^-1,
 // the ModDown followed by the rescale, exactly.
-template <bool SEPX, bool RS = false>
+// MI: targets per quarter-wave per pass (kMItems, or 2 for conversions of at most 16 targets: 154
+// instead of 206 VGPRs, three waves per SIMD).
+template <bool SEPX, bool RS = false, int MI = kMItems>
 __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTables T, const wv4i* __restrict__ dig) {
   __shared__ u64 D[16 * kYStride];
   __shared__ u64 X[SEPX ? 16 * kYStride : 1];
@@ -364,20 +366,20 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
   u64* dbase = A.dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
   const wv4i* __restrict__ tab = dig + C.dig_off;
   for (int base = 0; base < nt;) {
-    // mi targets per quarter in this pass (at most kMItems): the last pass spreads what is left over
+    // mi targets per quarter in this pass (at most MI): the last pass spreads what is left over
     // every quarter, so that no wave idles while another folds three targets
-    const int mi = min(kMItems, (nt - base + 7) / 8);
+    const int mi = min(MI, (nt - base + 7) / 8);
     // constants of MFMA row j: target of quarter j >> 2, item j & 3
     const int ta = base + (4 * h + (j >> 2)) * mi + (j & 3);
     const bool arow = (j & 3) < mi && ta < nt;
     wv4i av[8];
 #pragma unroll
     for (int c = 0; c < 8; ++c) av[c] = arow ? tab[((ta >> 4) * 8 + c) * 64 + 16 * g + (ta & 15)] : wv4i{0, 0, 0, 0};
-    int to[kMItems], tp[kMItems], ts[kMItems];
-    u64 pr[kMItems];
-    double tinv[kMItems];
+    int to[MI], tp[MI], ts[MI];
+    u64 pr[MI];
+    double tinv[MI];
 #pragma unroll
-    for (int r = 0; r < kMItems; ++r) {
+    for (int r = 0; r < MI; ++r) {
       to[r] = r < mi ? base + (4 * h + g) * mi + r : nt;
       const int tt = to[r] < nt ? to[r] : 0;
       tp[r] = C.dst_prime[tt];
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
       pr[r] = T.p[tp[r]];
       tinv[r] = C.fold_inv[tt];
     }
-    u64 x[kMItems][16];
+    u64 x[MI][16];
     uint64_t w0 = B0[0], w1 = B1[0];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -399,7 +401,7 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
       }
       const long long rz = RS ? Z[cl * kYStride + j + 16 * k] : 0;  // row j + 16k of column cl
 #pragma unroll
-      for (int r = 0; r < kMItems; ++r) {
+      for (int r = 0; r < MI; ++r) {
         if constexpr (RS) x[r][k] = r < mi ? wfold_add(acc, r, pr[r], tinv[r], rz) : 0;
         else x[r][k] = r < mi ? wfold(acc, r, pr[r], tinv[r]) : 0;
         asm volatile("" : "+v"(x[r][k]));
@@ -408,7 +410,7 @@ __global__ __launch_bounds__(kT, 2) void wf_cols_mconv(const WConvArgs A, WideTa
     }
     if (!SEPX) __syncthreads();  // every wave is done reading D before its runs become exchange buffers
 #pragma unroll
-    for (int r = 0; r < kMItems; ++r) {
+    for (int r = 0; r < MI; ++r) {
       if (r >= mi) break;  // uniform over the block
       const bool act = to[r] < nt;
       const u64* __restrict__ tw = T.fwd + (size_t)tp[r] * kN;
@@ -984,12 +986,13 @@ __global__ __launch_bounds__(kT, 2) void wf_rows_ipq_h(const WGalF G, WKeysF key
 }
 
 void launch_wconv_fused(const WConvArgs& A, int nt_max, dim3 grid, const WideState& W, hipStream_t s) {
-  auto k = nt_max <= kMPass ? wf_cols_mconv<false> : wf_cols_mconv<true>;
+  auto k = nt_max <= 16 ? wf_cols_mconv<false, false, 2> : nt_max <= kMPass ? wf_cols_mconv<false> : wf_cols_mconv<true>;
   k<<<grid, kT, 0, s>>>(A, W.t, (const wv4i*)W.conv_dig);
 }
 
 void launch_wconv_rs(const WConvArgs& A, int nt_max, dim3 grid, const WideState& W, hipStream_t s) {
-  auto k = nt_max <= kMPass ? wf_cols_mconv<false, true> : wf_cols_mconv<true, true>;
+  auto k = nt_max <= 16 ? wf_cols_mconv<false, true, 2>
+                        : nt_max <= kMPass ? wf_cols_mconv<false, true> : wf_cols_mconv<true, true>;
   k<<<grid, kT, 0, s>>>(A, W.t, (const wv4i*)W.conv_dig);
 }
 
