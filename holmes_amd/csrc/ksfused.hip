@@ -406,7 +406,7 @@ __global__ __launch_bounds__(kT) void k_ks_cols_conv(const ConvArgs A, DevTables
 // for every 16 coefficients one v_mfma_i32_16x16x64_i8 per digit c computes C_c for 16 target rows
 // (K = 8 sources x 8 digit bytes), |C_c| <= 56 * 128^2 < 2^20.
 // Phase 2 mapping: wave w takes column w >> 1 and half w & 1 of its targets; quarter-wave g (the
-// 16 lanes that form a column slot) owns kMItems targets, MFMA rows 4 g + r.  A lane's MFMA
+// 16 lanes that form a column slot) owns MI (kMItems) targets, MFMA rows 4 g + r.  A lane's MFMA
 // operand rows / columns are its lane index mod 16: the constants of row j, the digits of the
 // coefficient 16 k + j of tile k; its output rows 4 g + r at column j, i.e. rows j + 16 k of its
 // quarter's targets over the 16 tiles: the NTT cols pass's layout A, so the sums go straight into
@@ -448,7 +448,7 @@ __device__ __forceinline__ double mconv_fold_add(int a, int b, int d, int c6, do
   return reduce(v, p, pinv);
 }
 
-template <bool SEPX>
+template <bool SEPX, int MI = kMItems>
 __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y, long long z, double* Y, double* X,
                                                 const DevTables& T) {
   const double* __restrict__ src = A.src;
@@ -492,9 +492,9 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
   double* RX = (SEPX ? X : Y) + sigma * kYStride;
   double* dbase = dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
   for (int base = 0; base < nt;) {
-    // mi targets per quarter in this pass (at most kMItems): the last pass spreads what is left over
+    // mi targets per quarter in this pass (at most MI): the last pass spreads what is left over
     // every quarter, so that no wave idles while another transforms three targets
-    const int mi = min(kMItems, (nt - base + 7) / 8);
+    const int mi = min(MI, (nt - base + 7) / 8);
     // constants of MFMA row j: target of quarter j >> 2, item j & 3
     const int ta = base + (4 * h + (j >> 2)) * mi + (j & 3);
     const bool arow = (j & 3) < mi && ta < nt;
@@ -502,16 +502,16 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
 #pragma unroll
     for (int c = 0; c < kConvDigits; ++c)
       av[c] = arow ? *reinterpret_cast<const v4i*>(dig + ((size_t)ta * kConvDigits + c) * 64 + 16 * g) : v4i{0, 0, 0, 0};
-    int to[kMItems];
-    double p[kMItems], pinv[kMItems];
+    int to[MI];
+    double p[MI], pinv[MI];
 #pragma unroll
-    for (int r = 0; r < kMItems; ++r) {
+    for (int r = 0; r < MI; ++r) {
       to[r] = r < mi ? base + (4 * h + g) * mi + r : nt;
       const int tp = C.dst_prime[to[r] < nt ? to[r] : 0];
       p[r] = T.p[tp];
       pinv[r] = T.pinv[tp];
     }
-    double x[kMItems][16];
+    double x[MI][16];
     // the next tile's digit words are read while this tile's sums are folded
     uint64_t w0 = B0[0], w1 = B1[0];
 #pragma unroll
@@ -526,7 +526,7 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
         w1 = B1[16 * (k + 1)];
       }
 #pragma unroll
-      for (int r = 0; r < kMItems; ++r) {
+      for (int r = 0; r < MI; ++r) {
         x[r][k] = r < mi ? mconv_fold(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
                                       acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
                                       acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], p[r], pinv[r])
@@ -539,7 +539,7 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
     }
     if (!SEPX) __syncthreads();  // every wave is done reading D before its runs become exchange buffers
 #pragma unroll
-    for (int r = 0; r < kMItems; ++r) {
+    for (int r = 0; r < MI; ++r) {
       if (r >= mi) break;  // uniform over the block
       const bool act = to[r] < nt;
       const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? to[r] : 0] * kN;
@@ -556,11 +556,13 @@ __device__ __forceinline__ void cols_mconv_body(const ConvArgs& A, int bx, int y
   }
 }
 
-template <bool SEPX>
+// MI: targets per quarter-wave per pass (kMItems, or 2 for conversions of at most 16 targets: fewer
+// registers, three waves per SIMD).
+template <bool SEPX, int MI = kMItems>
 __global__ __launch_bounds__(kT, 2) void k_ks_cols_mconv(const ConvArgs A, DevTables T) {
   __shared__ double Y[16 * kYStride];
   __shared__ double X[SEPX ? 16 * kYStride : 1];
-  cols_mconv_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, T);
+  cols_mconv_body<SEPX, MI>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, T);
 }
 
 // ----------------------------------------------------------------- K4 of the ModDown fused with the rescale
@@ -577,7 +579,7 @@ __device__ __forceinline__ double undigit(uint64_t w) {
   return __longlong_as_double((long long)((w ^ M) - M + 0x4338000000000000ULL)) - 6755399441055744.0;
 }
 
-template <bool SEPX>
+template <bool SEPX, int MI = kMItems>
 __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, int y, long long z, double* Y, double* X,
                                                    double* Z, const DevTables& T) {
   const double* __restrict__ src = A.src;
@@ -651,23 +653,23 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
   double* RX = (SEPX ? X : Y) + sigma * kYStride;
   double* dbase = dst + z * A.dst_zs + y * A.dst_ys + (long long)(c0 + cl) * 16;
   for (int base = 0; base < nt;) {
-    const int mi = min(kMItems, (nt - base + 7) / 8);  // as in cols_mconv_body
+    const int mi = min(MI, (nt - base + 7) / 8);  // as in cols_mconv_body
     const int ta = base + (4 * h + (j >> 2)) * mi + (j & 3);
     const bool arow = (j & 3) < mi && ta < nt;
     v4i av[kConvDigits];
 #pragma unroll
     for (int c = 0; c < kConvDigits; ++c)
       av[c] = arow ? *reinterpret_cast<const v4i*>(dig + ((size_t)ta * kConvDigits + c) * 64 + 16 * g) : v4i{0, 0, 0, 0};
-    int to[kMItems];
-    double p[kMItems], pinv[kMItems];
+    int to[MI];
+    double p[MI], pinv[MI];
 #pragma unroll
-    for (int r = 0; r < kMItems; ++r) {
+    for (int r = 0; r < MI; ++r) {
       to[r] = r < mi ? base + (4 * h + g) * mi + r : nt;
       const int tp = C.dst_prime[to[r] < nt ? to[r] : 0];
       p[r] = T.p[tp];
       pinv[r] = T.pinv[tp];
     }
-    double x[kMItems][16];
+    double x[MI][16];
     uint64_t w0 = B0[0], w1 = B1[0];
 #pragma unroll
     for (int k = 0; k < 16; ++k) {
@@ -682,7 +684,7 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
         w1 = B1[16 * (k + 1)];
       }
 #pragma unroll
-      for (int r = 0; r < kMItems; ++r) {
+      for (int r = 0; r < MI; ++r) {
         x[r][k] = r < mi ? mconv_fold_add(acc[0][r] + (int)((uint32_t)acc[1][r] << 8),
                                           acc[2][r] + (int)((uint32_t)acc[3][r] << 8),
                                           acc[4][r] + (int)((uint32_t)acc[5][r] << 8), acc[6][r], rz, p[r], pinv[r])
@@ -693,7 +695,7 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
     }
     if (!SEPX) __syncthreads();
 #pragma unroll
-    for (int r = 0; r < kMItems; ++r) {
+    for (int r = 0; r < MI; ++r) {
       if (r >= mi) break;  // uniform over the block
       const bool act = to[r] < nt;
       const double* __restrict__ tw = T.tw_fwd + (size_t)C.dst_prime[act ? to[r] : 0] * kN;
@@ -710,19 +712,19 @@ __device__ __forceinline__ void cols_mconv_rs_body(const ConvArgs& A, int bx, in
   }
 }
 
-template <bool SEPX>
+template <bool SEPX, int MI = kMItems>
 __global__ __launch_bounds__(kT, 2) void k_ks_cols_mconv_rs(const ConvArgs A, DevTables T) {
   __shared__ double Y[16 * kYStride];
   __shared__ double X[SEPX ? 16 * kYStride : 1];
   __shared__ double Z[2 * kYStride];
-  cols_mconv_rs_body<SEPX>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, Z, T);
+  cols_mconv_rs_body<SEPX, MI>(A, blockIdx.x, blockIdx.y, blockIdx.z, Y, X, Z, T);
 }
 
 // Launches a ModUp / ModDown conversion (grid (128, groups, items)) on the engine the context
 // selects; nt_max is the largest target count over the groups.
 void launch_conv(const hck_context* c, const ConvArgs& A, dim3 grid, int nt_max, hipStream_t s) {
   if (c->conv_engine == 1) {
-    auto k = nt_max <= kMPass ? k_ks_cols_mconv<false> : k_ks_cols_mconv<true>;
+    auto k = nt_max <= 16 ? k_ks_cols_mconv<false, 2> : nt_max <= kMPass ? k_ks_cols_mconv<false> : k_ks_cols_mconv<true>;
     k<<<grid, kT, 0, s>>>(A, c->dev);
   } else {
     auto k = nt_max <= kTgtFused ? k_ks_cols_conv<false> : k_ks_cols_conv<true>;
@@ -1559,7 +1561,8 @@ int ks_rescaled(const hck_context* c, int ell, int batch, const uint64_t* d, lon
   {
     const ConvArgs A{accp + n, 2LL * (K + 1) * n, (long long)(K + 1) * n, 0, t4, 2LL * nq * n, (long long)nq * n,
                      c->d_mdrs + ell, 0, accp};
-    if (nq <= kMPass) k_ks_cols_mconv_rs<false><<<dim3(128, 2, batch), kT, 0, s>>>(A, c->dev);
+    if (nq <= 16) k_ks_cols_mconv_rs<false, 2><<<dim3(128, 2, batch), kT, 0, s>>>(A, c->dev);
+    else if (nq <= kMPass) k_ks_cols_mconv_rs<false><<<dim3(128, 2, batch), kT, 0, s>>>(A, c->dev);
     else k_ks_cols_mconv_rs<true><<<dim3(128, 2, batch), kT, 0, s>>>(A, c->dev);
     HCK_CHECK_LAUNCH();
   }
